@@ -1,0 +1,152 @@
+"""Loader for libaero_hip.so and the ctypes prototypes of every symbol in
+include/aero_hip.h.
+
+There is no CPU fallback anywhere in this package: if the library is missing,
+or no GPU is visible, every op raises (AeroHipUnavailable or the reference's
+*Unavailable classes, which derive from it).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_uint8, c_uint32, c_void_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("AERO_HIP_LIB", os.path.join(HERE, "libaero_hip.so"))
+
+
+class AeroHipUnavailable(RuntimeError):
+    """libaero_hip.so is not built or no MI355X is visible."""
+
+
+class AeroHipError(RuntimeError):
+    """A libaero_hip entry point refused its arguments or hit a HIP error."""
+
+
+fp = POINTER(c_float)
+ip = POINTER(c_int32)
+u8p = POINTER(c_uint8)
+vp = c_void_p
+
+# name -> (restype, argtypes), exactly the prototypes of include/aero_hip.h
+PROTOTYPES = {
+    # reference-compatible host ABI
+    "aero_tensor_silu": (c_int, [fp, c_int64]),
+    "aero_tensor_gelu": (c_int, [fp, c_int64]),
+    "aero_tensor_mul": (c_int, [fp, fp, c_int64]),
+    "aero_tensor_swiglu": (c_int, [fp, fp, c_int64]),
+    "aero_tensor_rmsnorm": (c_int, [fp, fp, fp, c_int64, c_float]),
+    "aero_tensor_l2norm": (c_int, [fp, fp, fp, c_int64, c_float, c_int]),
+    "aero_tensor_rmsnorm_rows": (c_int, [fp, c_int64, c_int64, c_float]),
+    "aero_rope_tables": (c_int64, [c_int64, ip, c_int64, c_float, c_int64, fp, c_int64,
+                                   fp, fp]),
+    "aero_apply_rope": (None, [fp, c_int64, c_int64, c_int64, fp, fp, ip, c_int]),
+    "aero_rmsnorm_rows": (None, [fp, fp, fp, c_int64, c_int64, c_float]),
+    "aero_l2norm_rows": (None, [fp, fp, fp, c_int64, c_int64, c_float]),
+    "aero_gelu": (None, [fp, c_int64]),
+    "aero_silu": (None, [fp, c_int64]),
+    "aero_swiglu": (None, [fp, fp, c_int64]),
+    "aero_dtype_block_bytes": (c_int64, [c_int]),
+    "aero_dtype_block_values": (c_int64, [c_int]),
+    "aero_hardware_threads": (c_int, []),
+    "aero_dequant_ref": (c_int, [c_int, u8p, c_int64, fp, c_int64]),
+    "aero_dequant_threaded": (c_int, [c_int, u8p, c_int64, fp, c_int64, c_int]),
+    # device-pointer fused ops
+    "aero_hip_rmsnorm": (c_int, [vp, vp, vp, c_int64, c_int64, c_float, c_int, vp]),
+    "aero_hip_gated_rmsnorm_silu": (c_int, [vp, vp, vp, c_int64, vp, c_int64, c_int64,
+                                            c_int64, c_float, vp]),
+    "aero_hip_act_mul": (c_int, [c_int, vp, vp, vp, c_int64, vp]),
+    "aero_hip_rope_inv_freq": (c_int64, [c_int64, c_int64, c_float, fp, c_int64, fp]),
+    "aero_hip_rope_tables": (c_int, [vp, c_int64, vp, c_int64, vp, vp, vp]),
+    "aero_hip_qk_norm_rope": (c_int, [vp, vp, c_int64, vp, vp, c_int64, vp, vp, c_float,
+                                      c_int, c_int64, c_int64, c_int64, c_int, vp, vp, vp,
+                                      vp, c_int64, vp]),
+    "aero_hip_embed_gather": (c_int, [c_int, vp, c_int64, c_int64, c_int64, vp, c_int64,
+                                      c_float, vp, vp, vp]),
+    "aero_hip_dequant": (c_int, [c_int, vp, c_int64, vp, c_int64, vp]),
+    "aero_hip_copy_f32": (c_int, [vp, vp, c_int64, vp]),
+    # runtime
+    "aero_hip_last_error": (c_char_p, []),
+    "aero_hip_version": (c_char_p, []),
+    "aero_hip_device_count": (c_int, []),
+    "aero_hip_set_device": (c_int, [c_int]),
+    "aero_hip_malloc": (vp, [c_int64]),
+    "aero_hip_free": (c_int, [vp]),
+    "aero_hip_memcpy_htod": (c_int, [vp, vp, c_int64]),
+    "aero_hip_memcpy_dtoh": (c_int, [vp, vp, c_int64]),
+    "aero_hip_memcpy_dtod": (c_int, [vp, vp, c_int64, vp]),
+    "aero_hip_memset": (c_int, [vp, c_int, c_int64]),
+    "aero_hip_stream_create": (vp, []),
+    "aero_hip_stream_destroy": (c_int, [vp]),
+    "aero_hip_stream_synchronize": (c_int, [vp]),
+    "aero_hip_device_synchronize": (c_int, []),
+    "aero_hip_event_create": (vp, []),
+    "aero_hip_event_destroy": (c_int, [vp]),
+    "aero_hip_event_record": (c_int, [vp, vp]),
+    "aero_hip_event_synchronize": (c_int, [vp]),
+    "aero_hip_event_elapsed_ms": (c_float, [vp, vp]),
+    "aero_hip_time_next_kernel": (c_int, [vp, vp]),
+}
+
+_lib = None
+_load_error: str | None = None
+
+
+def load(path: str | None = None):
+    """Load libaero_hip.so once and declare every prototype. Returns None and
+    records the reason when the file is missing or lacks a symbol."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if _load_error is not None and path is None:
+        return None
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        _load_error = f"{p} not found; build it with `python -m aero_amd.build`"
+        return None
+    try:
+        L = ctypes.CDLL(p)
+        for name, (res, args) in PROTOTYPES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+    except (OSError, AttributeError) as e:
+        _load_error = f"{p}: {e}"
+        return None
+    _lib = L
+    return _lib
+
+
+def unavailable_reason() -> str:
+    load()
+    if _lib is None:
+        return _load_error or "libaero_hip not loaded"
+    if _lib.aero_hip_device_count() <= 0:
+        return "no HIP device visible"
+    return ""
+
+
+def available() -> bool:
+    """Library loaded and at least one GPU visible."""
+    return unavailable_reason() == ""
+
+
+def lib(exc: type = AeroHipUnavailable):
+    """The loaded library with a usable GPU, or raise `exc`."""
+    L = load()
+    if L is None or L.aero_hip_device_count() <= 0:
+        raise exc(unavailable_reason())
+    return L
+
+
+def last_error() -> str:
+    L = load()
+    if L is None:
+        return ""
+    return (L.aero_hip_last_error() or b"").decode(errors="replace")
+
+
+def check(ok, what: str):
+    """Raise AeroHipError with the library's reason when an entry point refused."""
+    if not ok:
+        raise AeroHipError(f"{what}: {last_error()}")

@@ -1,0 +1,89 @@
+// Internal helpers shared by the libaero_hip translation units: error state,
+// launch wrapper with optional per-kernel device timing, wave-level
+// reductions and exact fp16 decoding. gfx950 only (wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
+
+#include <cstdint>
+#include <cstdio>
+
+namespace aero {
+
+// ---------------------------------------------------------------- errors
+// Thread-local "why was this refused" string returned by aero_hip_last_error.
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+bool hip_ok(hipError_t e, const char* what);
+
+// ---------------------------------------------------------------- timing
+// Per-thread arming set by aero_hip_time_next_kernel; consumed by launch().
+struct TimingSlot {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+TimingSlot& timing_slot();
+
+// Launch `kernel` on `stream`. When per-kernel timing is armed the launch
+// goes through hipExtLaunchKernelGGL so the events carry the kernel's own
+// begin/end timestamps. Returns false (with the error set) on failure.
+template <typename... KArgs, typename... Args>
+bool launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block,
+            uint32_t shmem, hipStream_t stream, Args... args) {
+    TimingSlot& ts = timing_slot();
+    if (ts.start != nullptr) {
+        hipEvent_t a = ts.start, b = ts.stop;
+        ts.start = ts.stop = nullptr;
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, a, b, 0,
+                              static_cast<KArgs>(args)...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream,
+                           static_cast<KArgs>(args)...);
+    }
+    return hip_ok(hipGetLastError(), name);
+}
+
+inline bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ------------------------------------------------------- device helpers
+// Sum across aligned groups of W lanes (W a power of two, W <= 64) with an
+// xor butterfly. Every lane of a group ends with the identical bit pattern
+// (fp add is commutative), so every lane derives the same scale factor.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Exact IEEE half -> single from the raw 16 bits, subnormals included
+// (v_cvt_f32_f16 would also be exact; the integer form keeps the result
+// independent of the wave's fp16 denormal mode).
+__host__ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 31u;
+    uint32_t m = h & 1023u;
+    uint32_t bits;
+    if (e == 31u) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else if (e != 0u) {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    } else if (m == 0u) {
+        bits = sign;
+    } else {
+        // subnormal: m * 2^-24 with m < 1024; normalise so bit 10 is set
+#if defined(__HIP_DEVICE_COMPILE__)
+        const int lz = __clz(m) - 21;  // leading zeros within 11 bits
+#else
+        const int lz = __builtin_clz(m) - 21;
+#endif
+        m <<= lz;
+        bits = sign | ((uint32_t)(113 - lz) << 23) | ((m & 1023u) << 13);
+    }
+    return __builtin_bit_cast(float, bits);
+}
+
+}  // namespace aero

@@ -1,0 +1,355 @@
+// Reference-compatible host-pointer ABI of libaero_hip.so.
+//
+// Each entry point keeps the name, signature and status convention of the
+// reference symbol it replaces (src/tensor.cpp:205-304, src/transformer.cpp:
+// 223-284, src/kernels.cpp:560-603): buffers are host memory and the call is
+// synchronous. Inputs are staged into a per-device HBM arena (grown on
+// demand, reused across calls, freed at exit), the same device kernels as
+// the aero_hip_* entry points run on a library-owned stream, and the result
+// is copied back before returning. Calls from several threads serialise on
+// the arena lock. Bad arguments are refused before any device work. The
+// `void` entry points clear the error string on entry; after a refusal or a
+// HIP error they return with aero_hip_last_error() saying why, so a caller
+// detects failure by a non-empty error string.
+#include "common.hpp"
+#include "aero_hip.h"
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+namespace aero {
+
+bool norm_rows(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
+               float eps, int flags, hipStream_t stream);
+bool act_mul(int kind, const float* g, const float* u, float* out, int64_t n,
+             hipStream_t s);
+int64_t rope_inv_freq_host(int64_t head_dim, int64_t n_dims, float base,
+                           const float* ff, int64_t n_ff, float* inv_out);
+bool rope_tables_dev(const int32_t* pos, int64_t n_pos, const float* inv, int64_t half,
+                     float* c, float* s, hipStream_t stream);
+bool dequant_dev(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
+                 int64_t n_values, hipStream_t s);
+int64_t dtype_block_bytes(int t);
+int64_t dtype_block_values(int t);
+
+namespace {
+
+struct Arena {
+    std::mutex mu;
+    void* buf = nullptr;
+    size_t cap = 0;
+    hipStream_t stream = nullptr;
+};
+
+constexpr int kMaxDevices = 64;
+Arena g_arena[kMaxDevices];
+
+// Holds the current device's arena for the duration of one host call and
+// carves 256-byte aligned sub-buffers out of it.
+class Staging {
+public:
+    Staging() {
+        int dev = 0;
+        ok_ = hip_ok(hipGetDevice(&dev), "hipGetDevice");
+        if (ok_ && (dev < 0 || dev >= kMaxDevices)) {
+            set_error("device index %d out of range", dev);
+            ok_ = false;
+        }
+        a_ = &g_arena[ok_ ? dev : 0];
+        lock_ = std::unique_lock<std::mutex>(a_->mu);
+        if (ok_ && a_->stream == nullptr)
+            ok_ = hip_ok(hipStreamCreate(&a_->stream), "hipStreamCreate");
+    }
+    bool ok() const { return ok_; }
+    hipStream_t stream() const { return a_->stream; }
+
+    // Reserve sizes[i] bytes for each i; pointers land in out[i].
+    bool reserve(std::initializer_list<size_t> sizes, void** out) {
+        if (!ok_) return false;
+        size_t total = 0;
+        for (size_t s : sizes) total += (s + 255) & ~size_t(255);
+        if (total == 0) total = 256;
+        if (total > a_->cap) {
+            if (a_->buf != nullptr) {
+                (void)hipStreamSynchronize(a_->stream);
+                (void)hipFree(a_->buf);
+                a_->buf = nullptr;
+                a_->cap = 0;
+            }
+            if (!hip_ok(hipMalloc(&a_->buf, total), "hipMalloc(staging)")) return false;
+            a_->cap = total;
+        }
+        char* p = static_cast<char*>(a_->buf);
+        int i = 0;
+        for (size_t s : sizes) {
+            out[i++] = p;
+            p += (s + 255) & ~size_t(255);
+        }
+        return true;
+    }
+
+    bool h2d(void* d, const void* h, size_t n) {
+        return n == 0 || hip_ok(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, a_->stream),
+                                "hipMemcpyAsync H2D");
+    }
+    bool d2h(void* h, const void* d, size_t n) {
+        return n == 0 || hip_ok(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, a_->stream),
+                                "hipMemcpyAsync D2H");
+    }
+    bool finish() { return hip_ok(hipStreamSynchronize(a_->stream), "hipStreamSynchronize"); }
+
+private:
+    Arena* a_ = nullptr;
+    std::unique_lock<std::mutex> lock_;
+    bool ok_ = false;
+};
+
+// out = f(in) for an n-float buffer (optionally with a second input).
+bool host_act(int kind, float* g, const float* u, int64_t n) {
+    Staging st;
+    void* p[2];
+    const size_t bytes = (size_t)n * sizeof(float);
+    if (!st.reserve({bytes, u ? bytes : 0}, p)) return false;
+    float* dg = static_cast<float*>(p[0]);
+    float* du = u ? static_cast<float*>(p[1]) : nullptr;
+    return st.h2d(dg, g, bytes) && (!u || st.h2d(du, u, bytes)) &&
+           act_mul(kind, dg, du, dg, n, st.stream()) && st.d2h(g, dg, bytes) && st.finish();
+}
+
+bool host_norm(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
+               float eps, int flags) {
+    Staging st;
+    void* p[2];
+    const size_t bytes = (size_t)(rows * cols) * sizeof(float);
+    const size_t wbytes = w ? (size_t)cols * sizeof(float) : 0;
+    if (!st.reserve({bytes, wbytes}, p)) return false;
+    float* dx = static_cast<float*>(p[0]);
+    float* dw = w ? static_cast<float*>(p[1]) : nullptr;
+    return st.h2d(dx, x, bytes) && (!w || st.h2d(dw, w, wbytes)) &&
+           norm_rows(dx, dw, dx, rows, cols, eps, flags, st.stream()) &&
+           st.d2h(out, dx, bytes) && st.finish();
+}
+
+}  // namespace
+
+bool qk_norm_rope_public(float* q, float* q_out, int64_t hq, float* k, float* k_out,
+                         int64_t hk, const float* qw, const float* kw, float eps,
+                         int flags, int64_t n_tok, int64_t D, int64_t n_rot, int mode,
+                         const int32_t* pos, const float* inv, const float* ct,
+                         const float* stb, int64_t n_tab, hipStream_t s) {
+    return aero_hip_qk_norm_rope(q, q_out, hq, k, k_out, hk, qw, kw, eps, flags, n_tok, D,
+                                 n_rot, mode, pos, inv, ct, stb, n_tab, s) == 1;
+}
+
+}  // namespace aero
+
+using aero::set_error;
+
+extern "C" {
+
+// ------------------------------------------------------ src/tensor.cpp ABI
+int aero_tensor_silu(float* v, int64_t n) {
+    if (!v || n <= 0) { set_error("aero_tensor_silu: null or n <= 0"); return 0; }
+    return aero::host_act(AERO_ACT_SILU, v, nullptr, n) ? 1 : 0;
+}
+
+int aero_tensor_gelu(float* v, int64_t n) {
+    if (!v || n <= 0) { set_error("aero_tensor_gelu: null or n <= 0"); return 0; }
+    return aero::host_act(AERO_ACT_GELU, v, nullptr, n) ? 1 : 0;
+}
+
+int aero_tensor_mul(float* a, const float* b, int64_t n) {
+    if (!a || !b || n <= 0) { set_error("aero_tensor_mul: null or n <= 0"); return 0; }
+    return aero::host_act(AERO_ACT_IDENTITY, a, b, n) ? 1 : 0;
+}
+
+int aero_tensor_swiglu(float* gate, const float* up, int64_t n) {
+    if (!gate || !up || n <= 0) { set_error("aero_tensor_swiglu: null or n <= 0"); return 0; }
+    return aero::host_act(AERO_ACT_SILU, gate, up, n) ? 1 : 0;
+}
+
+int aero_tensor_rmsnorm(const float* x, const float* weight, float* out, int64_t n,
+                        float eps) {
+    if (!x || !weight || !out || n <= 0) {
+        set_error("aero_tensor_rmsnorm: null or n <= 0");
+        return 0;
+    }
+    return aero::host_norm(x, weight, out, 1, n, eps, 0) ? 1 : 0;
+}
+
+int aero_tensor_l2norm(const float* x, const float* weight, float* out, int64_t n,
+                       float eps, int weighted) {
+    if (!x || !out || n <= 0 || (weighted && !weight)) {
+        set_error("aero_tensor_l2norm: null, n <= 0 or weighted without weight");
+        return 0;
+    }
+    return aero::host_norm(x, weighted ? weight : nullptr, out, 1, n, eps, AERO_NORM_L2)
+               ? 1 : 0;
+}
+
+int aero_tensor_rmsnorm_rows(float* t, int64_t rows, int64_t cols, float eps) {
+    if (!t || rows <= 0 || cols <= 0) {
+        set_error("aero_tensor_rmsnorm_rows: null or non-positive dims");
+        return 0;
+    }
+    return aero::host_norm(t, nullptr, t, rows, cols, eps, 0) ? 1 : 0;
+}
+
+// ------------------------------------------------- src/transformer.cpp ABI
+int64_t aero_rope_tables(int64_t head_dim, const int32_t* positions, int64_t n_pos,
+                         float base, int64_t n_dims, const float* freq_factors,
+                         int64_t n_ff, float* cos_out, float* sin_out) {
+    if (head_dim <= 0 || n_pos < 0 || positions == nullptr) {
+        set_error("aero_rope_tables: head_dim <= 0, n_pos < 0 or null positions");
+        return -1;
+    }
+    std::vector<float> inv((size_t)head_dim / 2 + 1);
+    const int64_t n = aero::rope_inv_freq_host(head_dim, n_dims, base, freq_factors, n_ff,
+                                               inv.data());
+    if (n < 0) {
+        set_error("aero_rope_tables: freq_factors shorter than n_rot/2");
+        return -1;
+    }
+    const int64_t half = n / 2;
+    if (half <= 0 || n_pos == 0) return n;
+    if (cos_out == nullptr || sin_out == nullptr) {
+        set_error("aero_rope_tables: null output");
+        return -1;
+    }
+    aero::Staging st;
+    void* p[4];
+    const size_t tb = (size_t)(n_pos * half) * sizeof(float);
+    if (!st.reserve({(size_t)n_pos * 4, (size_t)half * 4, tb, tb}, p)) return -1;
+    const bool ok = st.h2d(p[0], positions, (size_t)n_pos * 4) &&
+                    st.h2d(p[1], inv.data(), (size_t)half * 4) &&
+                    aero::rope_tables_dev(static_cast<int32_t*>(p[0]), n_pos,
+                                          static_cast<float*>(p[1]), half,
+                                          static_cast<float*>(p[2]),
+                                          static_cast<float*>(p[3]), st.stream()) &&
+                    st.d2h(cos_out, p[2], tb) && st.d2h(sin_out, p[3], tb) && st.finish();
+    return ok ? n : -1;
+}
+
+void aero_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
+                     const float* cos_tab, const float* sin_tab, const int32_t* positions,
+                     int mode) {
+    aero::clear_error();
+    const int64_t half = n_rot / 2;
+    if (half <= 0 || head_dim <= 0 || n_rows <= 0) return;
+    if (!x || !cos_tab || !sin_tab || n_rot > head_dim) {
+        set_error("aero_apply_rope: null buffer or n_rot > head_dim");
+        return;
+    }
+    // The table must cover every position read (POSITION-indexed).
+    int64_t n_tab = n_rows;
+    if (positions != nullptr) {
+        int64_t mx = -1;
+        for (int64_t r = 0; r < n_rows; ++r) {
+            if (positions[r] < 0) {
+                set_error("aero_apply_rope: negative position %d at row %lld",
+                          positions[r], (long long)r);
+                return;
+            }
+            mx = std::max<int64_t>(mx, positions[r]);
+        }
+        n_tab = mx + 1;
+    }
+    aero::Staging st;
+    void* p[4];
+    const size_t xb = (size_t)(n_rows * head_dim) * 4;
+    const size_t tb = (size_t)(n_tab * half) * 4;
+    if (!st.reserve({xb, tb, tb, positions ? (size_t)n_rows * 4 : 0}, p)) return;
+    float* dx = static_cast<float*>(p[0]);
+    int32_t* dpos = positions ? static_cast<int32_t*>(p[3]) : nullptr;
+    const int m = mode == 0 ? AERO_ROPE_NEOX : AERO_ROPE_INTERLEAVED;
+    (void)(st.h2d(dx, x, xb) && st.h2d(p[1], cos_tab, tb) && st.h2d(p[2], sin_tab, tb) &&
+           (!positions || st.h2d(dpos, positions, (size_t)n_rows * 4)) &&
+           aero::qk_norm_rope_public(dx, nullptr, 1, nullptr, nullptr, 0, nullptr, nullptr,
+                                     0.0f, 0, n_rows, head_dim, 2 * half, m, dpos, nullptr,
+                                     static_cast<float*>(p[1]), static_cast<float*>(p[2]),
+                                     n_tab, st.stream()) &&
+           st.d2h(x, dx, xb) && st.finish());
+}
+
+void aero_rmsnorm_rows(const float* x, const float* weight, float* out, int64_t n_rows,
+                       int64_t n_cols, float eps) {
+    aero::clear_error();
+    if (!x || !out || n_rows <= 0 || n_cols <= 0) {
+        set_error("aero_rmsnorm_rows: null or non-positive dims");
+        return;
+    }
+    (void)aero::host_norm(x, weight, out, n_rows, n_cols, eps, 0);
+}
+
+void aero_l2norm_rows(const float* x, const float* weight, float* out, int64_t n_rows,
+                      int64_t n_cols, float eps) {
+    aero::clear_error();
+    if (!x || !out || n_rows <= 0 || n_cols <= 0) {
+        set_error("aero_l2norm_rows: null or non-positive dims");
+        return;
+    }
+    (void)aero::host_norm(x, weight, out, n_rows, n_cols, eps, AERO_NORM_L2);
+}
+
+void aero_gelu(float* v, int64_t n) {
+    aero::clear_error();
+    if (!v || n <= 0) return;
+    (void)aero::host_act(AERO_ACT_GELU, v, nullptr, n);
+}
+
+void aero_silu(float* v, int64_t n) {
+    aero::clear_error();
+    if (!v || n <= 0) return;
+    (void)aero::host_act(AERO_ACT_SILU, v, nullptr, n);
+}
+
+void aero_swiglu(float* gate, const float* up, int64_t n) {
+    aero::clear_error();
+    if (!gate || !up || n <= 0) return;
+    (void)aero::host_act(AERO_ACT_SILU, gate, up, n);
+}
+
+// ------------------------------------------------------ src/kernels.cpp ABI
+int aero_hardware_threads(void) {
+    const unsigned hc = std::thread::hardware_concurrency();
+    return (int)std::min(hc == 0 ? 1u : hc, 8u);
+}
+
+int aero_dequant_ref(int t, const uint8_t* raw, int64_t raw_len, float* out,
+                     int64_t n_values) {
+    const int64_t bv = aero::dtype_block_values(t), bb = aero::dtype_block_bytes(t);
+    const bool known = t == AERO_DTYPE_F32 || t == AERO_DTYPE_F16 || t == AERO_DTYPE_BF16 ||
+                       t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q6_K;
+    if (!known || bv <= 0 || !raw || !out || n_values < 0) {
+        set_error("aero_dequant_ref: dtype %d not supported on the GPU path or bad args", t);
+        return 0;
+    }
+    const int64_t nblocks = n_values / bv;
+    if (raw_len < nblocks * bb) {
+        set_error("aero_dequant_ref: raw_len %lld < %lld", (long long)raw_len,
+                  (long long)(nblocks * bb));
+        return 0;
+    }
+    if (nblocks == 0) return 1;
+    aero::Staging st;
+    void* p[2];
+    const size_t rbytes = (size_t)(nblocks * bb);
+    const size_t obytes = (size_t)(nblocks * bv) * 4;
+    if (!st.reserve({rbytes, obytes}, p)) return 0;
+    const bool ok = st.h2d(p[0], raw, rbytes) &&
+                    aero::dequant_dev(t, static_cast<uint8_t*>(p[0]), (int64_t)rbytes,
+                                      static_cast<float*>(p[1]), n_values, st.stream()) &&
+                    st.d2h(out, p[1], obytes) && st.finish();
+    return ok ? 1 : 0;
+}
+
+int aero_dequant_threaded(int t, const uint8_t* raw, int64_t raw_len, float* out,
+                          int64_t n_values, int threads) {
+    (void)threads;
+    return aero_dequant_ref(t, raw, raw_len, out, n_values);
+}
+
+}  // extern "C"

@@ -1,0 +1,282 @@
+// Row norms on gfx950: RMSNorm (plain, Gemma (1+w), weightless), the L2
+// variant, and the gated-DeltaNet norm(x)*silu(z).
+//
+// One kernel template covers all of them. A row (or a `group`-long slice of
+// a row) is owned by TPR consecutive lanes; each lane keeps V float4 of the
+// row in VGPRs, so x (and z) are read from HBM exactly once with 128-bit
+// coalesced loads. The sum of squares is reduced with a wave64 xor butterfly
+// and, when a row spans several waves, one LDS step. The output is written
+// once with 128-bit stores. HBM bytes per row: 4*(2*cols) (+4*cols for z);
+// the weight vector is re-read from L2, not HBM.
+//
+// Arithmetic follows the reference operation by operation with contraction
+// disabled: inv = 1/sqrtf(ss/n + eps), out = (x*inv)*w (src/tensor.cpp:
+// 128-134); L2: inv = 1/max(sqrtf(ss), eps) (src/tensor.cpp:136-154); gated:
+// out = ((x/denom)*w)*(z/(1+expf(-z))) (src/ssm.cpp:17,327-343). Only the
+// summation order of ss differs (tree instead of serial).
+#include "common.hpp"
+#include "aero_hip.h"
+
+#pragma clang fp contract(off)
+
+namespace aero {
+namespace {
+
+struct NormParams {
+    const float* x;
+    const float* z;      // gated only
+    const float* w;      // may be null (ones)
+    float* out;          // may alias x
+    int64_t rows;        // number of normalised slices
+    int cols;            // slice length
+    int gpr;             // slices per original row (weight offset)
+    int w_len;           // weight period
+    float eps;
+    int flags;
+};
+
+__device__ __forceinline__ float silu_div(float v) { return v / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float norm_scale(float ss, const NormParams& p) {
+    if (p.flags & AERO_NORM_L2) {
+        const float nrm = sqrtf(ss);
+        return 1.0f / (nrm > p.eps ? nrm : p.eps);
+    }
+    return 1.0f / sqrtf(ss / (float)p.cols + p.eps);
+}
+
+__device__ __forceinline__ float apply_w(float v, const float* w, int idx, int flags) {
+    if (w == nullptr) return v;
+    const float wc = (flags & AERO_NORM_UNIT_OFFSET) ? 1.0f + w[idx] : w[idx];
+    return v * wc;
+}
+
+template <int TPR, int V, bool GATED>
+__global__ __launch_bounds__(TPR > 256 ? TPR : 256)
+void norm_vec_kernel(NormParams p) {
+    constexpr int BS = TPR > 256 ? TPR : 256;
+    constexpr int RPB = BS / TPR;
+    const int tid = threadIdx.x;
+    const int lr = tid / TPR;
+    const int t = tid % TPR;
+    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
+    const bool ok = row < p.rows;
+    const int nv = p.cols >> 2;
+    const int64_t base = ok ? row * (int64_t)p.cols : 0;
+    const float4* xr = reinterpret_cast<const float4*>(p.x + base);
+    const float4* zr = reinterpret_cast<const float4*>(GATED ? p.z + base : p.x);
+
+    float4 xv[V];
+    float4 zv[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = i * TPR + t;
+        if (ok && c < nv) {
+            xv[i] = xr[c];
+            if (GATED) zv[i] = zr[c];
+        } else {
+            xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (GATED) zv[i] = xv[i];
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        ss += xv[i].x * xv[i].x;
+        ss += xv[i].y * xv[i].y;
+        ss += xv[i].z * xv[i].z;
+        ss += xv[i].w * xv[i].w;
+    }
+    if constexpr (TPR <= 64) {
+        ss = group_sum<TPR>(ss);
+    } else {
+        constexpr int WPR = TPR / 64;  // waves per row
+        __shared__ float part[BS / 64];
+        ss = group_sum<64>(ss);
+        if ((tid & 63) == 0) part[tid >> 6] = ss;
+        __syncthreads();
+        const int w0 = lr * WPR;
+        ss = part[w0];
+#pragma unroll
+        for (int k = 1; k < WPR; ++k) ss += part[w0 + k];
+    }
+    if (!ok) return;
+
+    float4* orow = reinterpret_cast<float4*>(p.out + base);
+    if constexpr (GATED) {
+        const float denom = sqrtf(ss / (float)p.cols + p.eps);
+        const int col0 = (int)(row % p.gpr) * p.cols;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int c = i * TPR + t;
+            if (c >= nv) continue;
+            const int wi = (col0 + 4 * c) % p.w_len;
+            const float4 wv = *reinterpret_cast<const float4*>(p.w + wi);
+            float4 o;
+            o.x = ((xv[i].x / denom) * wv.x) * silu_div(zv[i].x);
+            o.y = ((xv[i].y / denom) * wv.y) * silu_div(zv[i].y);
+            o.z = ((xv[i].z / denom) * wv.z) * silu_div(zv[i].z);
+            o.w = ((xv[i].w / denom) * wv.w) * silu_div(zv[i].w);
+            orow[c] = o;
+        }
+    } else {
+        const float inv = norm_scale(ss, p);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int c = i * TPR + t;
+            if (c >= nv) continue;
+            float4 o = make_float4(xv[i].x * inv, xv[i].y * inv, xv[i].z * inv,
+                                   xv[i].w * inv);
+            if (p.w != nullptr) {
+                float4 wv = reinterpret_cast<const float4*>(p.w)[c];
+                if (p.flags & AERO_NORM_UNIT_OFFSET) {
+                    wv.x = 1.0f + wv.x; wv.y = 1.0f + wv.y;
+                    wv.z = 1.0f + wv.z; wv.w = 1.0f + wv.w;
+                }
+                o.x = o.x * wv.x; o.y = o.y * wv.y; o.z = o.z * wv.z; o.w = o.w * wv.w;
+            }
+            orow[c] = o;
+        }
+    }
+}
+
+// Any shape / alignment: one 256-thread block per slice, two passes over the
+// slice (the second pass hits L2). Same arithmetic as the vector kernel.
+template <bool GATED>
+__global__ __launch_bounds__(256) void norm_scalar_kernel(NormParams p) {
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t base = row * (int64_t)p.cols;
+    const float* xr = p.x + base;
+    float ss = 0.0f;
+    for (int c = tid; c < p.cols; c += 256) ss += xr[c] * xr[c];
+    __shared__ float part[4];
+    ss = group_sum<64>(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    ss = ((part[0] + part[1]) + part[2]) + part[3];
+    float* o = p.out + base;
+    if constexpr (GATED) {
+        const float denom = sqrtf(ss / (float)p.cols + p.eps);
+        const float* zr = p.z + base;
+        const int64_t col0 = (row % p.gpr) * (int64_t)p.cols;
+        for (int c = tid; c < p.cols; c += 256) {
+            const float wn = p.w[(col0 + c) % p.w_len];
+            o[c] = ((xr[c] / denom) * wn) * silu_div(zr[c]);
+        }
+    } else {
+        const float inv = norm_scale(ss, p);
+        for (int c = tid; c < p.cols; c += 256)
+            o[c] = apply_w(xr[c] * inv, p.w, c, p.flags);
+    }
+}
+
+using NormKernel = void (*)(NormParams);
+
+template <bool GATED, int TPR>
+NormKernel pick_v(int v) {
+    switch (v) {
+    case 1: return norm_vec_kernel<TPR, 1, GATED>;
+    case 2: return norm_vec_kernel<TPR, 2, GATED>;
+    case 3: return norm_vec_kernel<TPR, 3, GATED>;
+    case 4: return norm_vec_kernel<TPR, 4, GATED>;
+    case 5: return norm_vec_kernel<TPR, 5, GATED>;
+    case 6: return norm_vec_kernel<TPR, 6, GATED>;
+    case 7: return norm_vec_kernel<TPR, 7, GATED>;
+    case 8: return norm_vec_kernel<TPR, 8, GATED>;
+    default: return nullptr;
+    }
+}
+
+template <bool GATED>
+NormKernel pick(int tpr, int v) {
+    switch (tpr) {
+    case 8: return pick_v<GATED, 8>(v);
+    case 16: return pick_v<GATED, 16>(v);
+    case 32: return pick_v<GATED, 32>(v);
+    case 64: return pick_v<GATED, 64>(v);
+    case 128: return pick_v<GATED, 128>(v);
+    case 256: return pick_v<GATED, 256>(v);
+    case 512: return pick_v<GATED, 512>(v);
+    case 1024: return pick_v<GATED, 1024>(v);
+    default: return nullptr;
+    }
+}
+
+// Lanes per slice: the smallest power of two (8..1024) that keeps each lane
+// at <= 4 float4, so a lane has four 128-bit loads (eight when gated) in
+// flight; V then covers the rest (<= 8).
+void choose_shape(int nv, int* tpr, int* v) {
+    int t = 8;
+    while (t < 1024 && t * 4 < nv) t *= 2;
+    *tpr = t;
+    *v = (nv + t - 1) / t;
+}
+
+bool run_norm(NormParams p, bool gated, hipStream_t stream) {
+    if (p.rows == 0) return true;
+    const bool vec = (p.cols % 4 == 0) && aligned16(p.x) && aligned16(p.out) &&
+                     (p.w == nullptr || aligned16(p.w)) &&
+                     (!gated || (aligned16(p.z) && p.w_len % 4 == 0));
+    int tpr = 0, v = 0;
+    if (vec) choose_shape(p.cols / 4, &tpr, &v);
+    if (vec && v <= 8) {
+        const int bs = tpr > 256 ? tpr : 256;
+        const int rpb = bs / tpr;
+        const int64_t blocks = (p.rows + rpb - 1) / rpb;
+        NormKernel k = gated ? pick<true>(tpr, v) : pick<false>(tpr, v);
+        return launch("norm_vec_kernel", k, dim3((unsigned)blocks), dim3(bs), 0,
+                      stream, p);
+    }
+    NormKernel k = gated ? norm_scalar_kernel<true> : norm_scalar_kernel<false>;
+    return launch("norm_scalar_kernel", k, dim3((unsigned)p.rows), dim3(256), 0,
+                  stream, p);
+}
+
+}  // namespace
+
+// Used by the host-pointer ABI (dropin.hip).
+bool norm_rows(const float* x, const float* w, float* out, int64_t rows,
+               int64_t cols, float eps, int flags, hipStream_t stream) {
+    if (x == nullptr || out == nullptr || rows < 0 || cols <= 0 ||
+        cols > (int64_t)0x7fffffff || rows > (int64_t)0x7fffffff) {
+        set_error("rmsnorm: bad arguments (rows=%lld cols=%lld)", (long long)rows,
+                  (long long)cols);
+        return false;
+    }
+    NormParams p{x, nullptr, w, out, rows, (int)cols, 1, (int)cols, eps, flags};
+    return run_norm(p, false, stream);
+}
+
+}  // namespace aero
+
+extern "C" {
+
+int aero_hip_rmsnorm(const float* x, const float* w, float* out, int64_t rows,
+                     int64_t cols, float eps, int flags, void* stream) {
+    return aero::norm_rows(x, w, out, rows, cols, eps, flags, (hipStream_t)stream)
+               ? 1 : 0;
+}
+
+int aero_hip_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
+                                int64_t w_len, float* out, int64_t rows,
+                                int64_t inner, int64_t group, float eps,
+                                void* stream) {
+    if (!x || !z || !w || !out || rows < 0 || inner <= 0 || group <= 0 ||
+        w_len <= 0 || inner % group != 0 || inner > (int64_t)0x7fffffff) {
+        aero::set_error("gated_rmsnorm_silu: bad arguments (rows=%lld inner=%lld "
+                        "group=%lld w_len=%lld)", (long long)rows, (long long)inner,
+                        (long long)group, (long long)w_len);
+        return 0;
+    }
+    const int64_t slices = rows * (inner / group);
+    if (slices > (int64_t)0x7fffffff) {
+        aero::set_error("gated_rmsnorm_silu: too many slices (%lld)", (long long)slices);
+        return 0;
+    }
+    aero::NormParams p{x, z, w, out, slices, (int)group, (int)(inner / group),
+                       (int)w_len, eps, 0};
+    return aero::run_norm(p, true, (hipStream_t)stream) ? 1 : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,170 @@
+"""HBM buffers, streams and events over libaero_hip's runtime helpers.
+
+No PyTorch: a DeviceArray is a hipMalloc'd buffer with a numpy-style shape and
+dtype, created from or copied back to a numpy array. `ptr` is the raw device
+address passed to the aero_hip_* entry points.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+
+
+class DeviceArray:
+    """A contiguous array in HBM. Owns its allocation unless created as a view."""
+
+    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owner", "_base")
+
+    def __init__(self, shape, dtype=np.float32, *, _ptr=None, _owner=True, _base=None):
+        self.shape = tuple(int(d) for d in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        n = 1
+        for d in self.shape:
+            if d < 0:
+                raise ValueError(f"negative dimension in {self.shape}")
+            n *= d
+        self.nbytes = n * self.dtype.itemsize
+        self._base = _base
+        if _ptr is not None:
+            self.ptr = _ptr
+            self._owner = _owner
+            return
+        L = _lib.lib()
+        p = L.aero_hip_malloc(max(self.nbytes, 256))
+        if not p:
+            raise MemoryError(f"hipMalloc of {self.nbytes} bytes failed: {_lib.last_error()}")
+        self.ptr = p
+        self._owner = True
+
+    # ------------------------------------------------------------ creation
+    @classmethod
+    def empty(cls, shape, dtype=np.float32) -> "DeviceArray":
+        return cls(shape, dtype)
+
+    @classmethod
+    def from_numpy(cls, a) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        d.copy_from(a)
+        return d
+
+    def view(self, shape=None, dtype=None, offset_bytes: int = 0) -> "DeviceArray":
+        """A non-owning view at `offset_bytes` into this buffer."""
+        shape = self.shape if shape is None else shape
+        dtype = self.dtype if dtype is None else dtype
+        v = DeviceArray(shape, dtype, _ptr=self.ptr + offset_bytes, _owner=False, _base=self)
+        if offset_bytes < 0 or offset_bytes + v.nbytes > self.nbytes:
+            raise ValueError("view outside the parent buffer")
+        return v
+
+    # ------------------------------------------------------------ transfer
+    def copy_from(self, a) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes != self.nbytes:
+            raise ValueError(f"size mismatch: host {a.nbytes} B vs device {self.nbytes} B")
+        _lib.check(_lib.lib().aero_hip_memcpy_htod(self.ptr, a.ctypes.data, a.nbytes),
+                   "memcpy H2D")
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        _lib.check(_lib.lib().aero_hip_memcpy_dtoh(out.ctypes.data, self.ptr, self.nbytes),
+                   "memcpy D2H")
+        return out
+
+    @property
+    def size(self) -> int:
+        return self.nbytes // self.dtype.itemsize
+
+    def free(self) -> None:
+        if self._owner and self.ptr:
+            L = _lib.load()
+            if L is not None:
+                L.aero_hip_free(self.ptr)
+        self.ptr = 0
+        self._owner = False
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __repr__(self):
+        return f"DeviceArray(shape={self.shape}, dtype={self.dtype}, ptr=0x{self.ptr or 0:x})"
+
+
+def as_ptr(x):
+    """Device address of a DeviceArray, None for None; ints pass through."""
+    if x is None:
+        return None
+    if isinstance(x, DeviceArray):
+        return x.ptr
+    if isinstance(x, int):
+        return x
+    raise TypeError(f"expected a DeviceArray, got {type(x).__name__}")
+
+
+class Stream:
+    """A HIP stream at default priority (NULL handle = the null stream)."""
+
+    def __init__(self, null: bool = False):
+        self.handle = None if null else _lib.lib().aero_hip_stream_create()
+        if not null and not self.handle:
+            raise _lib.AeroHipError(f"stream create: {_lib.last_error()}")
+
+    def synchronize(self) -> None:
+        _lib.check(_lib.lib().aero_hip_stream_synchronize(self.handle), "stream sync")
+
+    def destroy(self) -> None:
+        if self.handle:
+            _lib.lib().aero_hip_stream_destroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        self.handle = _lib.lib().aero_hip_event_create()
+        if not self.handle:
+            raise _lib.AeroHipError(f"event create: {_lib.last_error()}")
+
+    def record(self, stream: Stream | None = None) -> None:
+        _lib.check(_lib.lib().aero_hip_event_record(self.handle, stream.handle if stream else None),
+                   "event record")
+
+    def synchronize(self) -> None:
+        _lib.check(_lib.lib().aero_hip_event_synchronize(self.handle), "event sync")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = _lib.lib().aero_hip_event_elapsed_ms(self.handle, end.handle)
+        if ms < 0:
+            raise _lib.AeroHipError(f"event elapsed: {_lib.last_error()}")
+        return float(ms)
+
+    def destroy(self) -> None:
+        if self.handle:
+            _lib.lib().aero_hip_event_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def time_next_kernel(start: Event, stop: Event) -> None:
+    """The next kernel launched by an aero_hip_* op on this thread records its
+    own device begin/end timestamps into start/stop."""
+    _lib.check(_lib.lib().aero_hip_time_next_kernel(start.handle, stop.handle), "time_next_kernel")
+
+
+def synchronize() -> None:
+    _lib.check(_lib.lib().aero_hip_device_synchronize(), "device sync")
+
+
+def device_count() -> int:
+    L = _lib.load()
+    return 0 if L is None else int(L.aero_hip_device_count())

@@ -1,0 +1,188 @@
+"""Device-resident fused ops: the aero_hip_* entry points over DeviceArrays.
+
+Every function checks on the host that each buffer is large enough for the
+shape it is given before anything is launched, then enqueues one kernel on
+`stream` (None = the null stream) and returns without waiting. These are the
+ops a model loop calls with activations already in HBM; the reference-shaped
+numpy wrappers live in tensor_native / transformer_native / native.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import _lib
+from .device import DeviceArray, Stream, as_ptr
+
+NORM_UNIT_OFFSET = 1
+NORM_L2 = 2
+
+ACT_SILU = 0
+ACT_GELU = 1
+ACT_GELU_TANH = 2
+ACT_IDENTITY = 3
+ACTS = {"silu": ACT_SILU, "swiglu": ACT_SILU, "gelu": ACT_GELU, "geglu": ACT_GELU,
+        "gelu_erf": ACT_GELU, "gelu_tanh": ACT_GELU_TANH, "geglu_tanh": ACT_GELU_TANH,
+        "identity": ACT_IDENTITY, "mul": ACT_IDENTITY}
+
+ROPE_NEOX = 0
+ROPE_INTERLEAVED = 1
+
+DTYPE_F32, DTYPE_F16, DTYPE_Q8_0, DTYPE_Q4_K, DTYPE_Q6_K, DTYPE_BF16 = 0, 1, 8, 12, 14, 30
+_BLOCK = {DTYPE_F32: (1, 4), DTYPE_F16: (1, 2), DTYPE_BF16: (1, 2), DTYPE_Q8_0: (32, 34),
+          DTYPE_Q4_K: (256, 144), DTYPE_Q6_K: (256, 210)}
+
+
+def _s(stream: Stream | None):
+    return None if stream is None else stream.handle
+
+
+def _need(arr, nelem: int, dtype, name: str):
+    if arr is None:
+        return
+    if not isinstance(arr, DeviceArray):
+        raise TypeError(f"{name}: expected a DeviceArray, got {type(arr).__name__}")
+    if arr.dtype != np.dtype(dtype):
+        raise TypeError(f"{name}: dtype {arr.dtype}, expected {np.dtype(dtype)}")
+    if arr.size < nelem:
+        raise ValueError(f"{name}: holds {arr.size} elements, needs {nelem}")
+
+
+def rmsnorm(x: DeviceArray, w: DeviceArray | None, out: DeviceArray, rows: int, cols: int,
+            eps: float, unit_offset: bool = False, l2: bool = False,
+            stream: Stream | None = None) -> None:
+    """out[r] = x[r]/sqrt(mean(x[r]^2)+eps) * (w or 1+w); L2 form with l2=True."""
+    _need(x, rows * cols, np.float32, "x")
+    _need(out, rows * cols, np.float32, "out")
+    _need(w, cols, np.float32, "w")
+    flags = (NORM_UNIT_OFFSET if unit_offset else 0) | (NORM_L2 if l2 else 0)
+    L = _lib.lib()
+    _lib.check(L.aero_hip_rmsnorm(x.ptr, as_ptr(w), out.ptr, rows, cols, float(eps), flags,
+                                  _s(stream)), "rmsnorm")
+
+
+def gated_rmsnorm_silu(x: DeviceArray, z: DeviceArray, w: DeviceArray, out: DeviceArray,
+                       rows: int, inner: int, eps: float, group: int | None = None,
+                       stream: Stream | None = None) -> None:
+    """out = rmsnorm_group(x) * tile(w) * silu(z); group=None is the whole row."""
+    group = inner if group is None else int(group)
+    _need(x, rows * inner, np.float32, "x")
+    _need(z, rows * inner, np.float32, "z")
+    _need(out, rows * inner, np.float32, "out")
+    _need(w, 1, np.float32, "w")
+    _lib.check(_lib.lib().aero_hip_gated_rmsnorm_silu(x.ptr, z.ptr, w.ptr, w.size, out.ptr,
+                                                      rows, inner, group, float(eps),
+                                                      _s(stream)), "gated_rmsnorm_silu")
+
+
+def act_mul(kind, gate: DeviceArray, up: DeviceArray | None, out: DeviceArray,
+            n: int | None = None, stream: Stream | None = None) -> None:
+    """out = act(gate) * up (up None: out = act(gate)). kind: int or name."""
+    k = ACTS[kind] if isinstance(kind, str) else int(kind)
+    n = gate.size if n is None else int(n)
+    _need(gate, n, np.float32, "gate")
+    _need(up, n, np.float32, "up")
+    _need(out, n, np.float32, "out")
+    _lib.check(_lib.lib().aero_hip_act_mul(k, gate.ptr, as_ptr(up), out.ptr, n, _s(stream)),
+               "act_mul")
+
+
+def rope_inv_freq(head_dim: int, n_dims: int | None, base: float, freq_factors=None):
+    """(n_rot, inv[n_rot/2]) on the host, bit-identical to the reference's."""
+    import ctypes
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32).reshape(-1)
+    inv = np.zeros(max(head_dim // 2, 1), dtype=np.float32)
+    n = _lib.load().aero_hip_rope_inv_freq(
+        head_dim, -1 if n_dims is None else int(n_dims), float(base),
+        None if ff is None else ff.ctypes.data_as(_lib.fp), 0 if ff is None else ff.size,
+        inv.ctypes.data_as(_lib.fp))
+    if n < 0:
+        raise ValueError(f"rope_inv_freq refused: {_lib.last_error()}")
+    return int(n), inv[: n // 2].copy()
+
+
+def rope_tables(pos: DeviceArray, inv: DeviceArray, cos_out: DeviceArray, sin_out: DeviceArray,
+                stream: Stream | None = None) -> None:
+    half = inv.size
+    _need(pos, pos.size, np.int32, "pos")
+    _need(cos_out, pos.size * half, np.float32, "cos")
+    _need(sin_out, pos.size * half, np.float32, "sin")
+    _lib.check(_lib.lib().aero_hip_rope_tables(pos.ptr, pos.size, inv.ptr, half, cos_out.ptr,
+                                               sin_out.ptr, _s(stream)), "rope_tables")
+
+
+def qk_norm_rope(q: DeviceArray, n_q_heads: int, n_tok: int, head_dim: int, n_rot: int,
+                 *, k: DeviceArray | None = None, n_k_heads: int = 0,
+                 q_out: DeviceArray | None = None, k_out: DeviceArray | None = None,
+                 q_norm_w: DeviceArray | None = None, k_norm_w: DeviceArray | None = None,
+                 eps: float = 1e-6, unit_offset: bool = False, mode: int = ROPE_NEOX,
+                 pos: DeviceArray | None = None, inv_freq: DeviceArray | None = None,
+                 cos_tab: DeviceArray | None = None, sin_tab: DeviceArray | None = None,
+                 stream: Stream | None = None) -> None:
+    """Per-head RMSNorm (optional) then RoPE on q [n_tok, Hq, D] and k [n_tok, Hk, D].
+    Angles from inv_freq (computed) or a position-indexed cos/sin table."""
+    half = n_rot // 2
+    _need(q, n_tok * n_q_heads * head_dim, np.float32, "q")
+    _need(q_out, n_tok * n_q_heads * head_dim, np.float32, "q_out")
+    if n_k_heads:
+        _need(k, n_tok * n_k_heads * head_dim, np.float32, "k")
+        _need(k_out, n_tok * n_k_heads * head_dim, np.float32, "k_out")
+        if k is None:
+            raise ValueError("k is required when n_k_heads > 0")
+    _need(q_norm_w, head_dim, np.float32, "q_norm_w")
+    _need(k_norm_w, head_dim, np.float32, "k_norm_w")
+    _need(pos, n_tok, np.int32, "pos")
+    _need(inv_freq, half, np.float32, "inv_freq")
+    n_tab = 0
+    if cos_tab is not None or sin_tab is not None:
+        if cos_tab is None or sin_tab is None or half == 0:
+            raise ValueError("a table needs both cos_tab and sin_tab")
+        n_tab = min(cos_tab.size, sin_tab.size) // half
+        _need(cos_tab, n_tab * half, np.float32, "cos_tab")
+        _need(sin_tab, n_tab * half, np.float32, "sin_tab")
+    flags = NORM_UNIT_OFFSET if unit_offset else 0
+    _lib.check(_lib.lib().aero_hip_qk_norm_rope(
+        q.ptr, as_ptr(q_out), n_q_heads, as_ptr(k), as_ptr(k_out), n_k_heads,
+        as_ptr(q_norm_w), as_ptr(k_norm_w), float(eps), flags, n_tok, head_dim, n_rot,
+        int(mode), as_ptr(pos), as_ptr(inv_freq), as_ptr(cos_tab), as_ptr(sin_tab), n_tab,
+        _s(stream)), "qk_norm_rope")
+
+
+def row_bytes(dtype: int, n_embd: int) -> int:
+    bv, bb = _BLOCK[dtype]
+    if n_embd % bv:
+        raise ValueError(f"n_embd {n_embd} is not a multiple of the block size {bv}")
+    return (n_embd // bv) * bb
+
+
+def embed_gather(dtype: int, table: DeviceArray, vocab: int, n_embd: int, ids: DeviceArray,
+                 out: DeviceArray, scale: float = 0.0, bad_count: DeviceArray | None = None,
+                 n_ids: int | None = None, stream: Stream | None = None) -> None:
+    """out[i] = dequant(table row ids[i]) (* scale when scale > 0)."""
+    n_ids = ids.size if n_ids is None else int(n_ids)
+    rb = row_bytes(dtype, n_embd)
+    if table.nbytes < vocab * rb:
+        raise ValueError(f"table holds {table.nbytes} B, needs {vocab * rb}")
+    _need(ids, n_ids, np.int32, "ids")
+    _need(out, n_ids * n_embd, np.float32, "out")
+    _need(bad_count, 1, np.uint32, "bad_count")
+    _lib.check(_lib.lib().aero_hip_embed_gather(int(dtype), table.ptr, table.nbytes, vocab,
+                                                n_embd, ids.ptr, n_ids, float(scale), out.ptr,
+                                                as_ptr(bad_count), _s(stream)), "embed_gather")
+
+
+def dequant(dtype: int, raw: DeviceArray, out: DeviceArray, n_values: int,
+            stream: Stream | None = None) -> None:
+    bv, bb = _BLOCK[dtype]
+    if raw.nbytes < (n_values // bv) * bb:
+        raise ValueError("raw buffer too short")
+    _need(out, (n_values // bv) * bv, np.float32, "out")
+    _lib.check(_lib.lib().aero_hip_dequant(int(dtype), raw.ptr, raw.nbytes, out.ptr, n_values,
+                                           _s(stream)), "dequant")
+
+
+def copy_f32(src: DeviceArray, dst: DeviceArray, n: int | None = None,
+             stream: Stream | None = None) -> None:
+    n = src.size if n is None else int(n)
+    _need(src, n, np.float32, "src")
+    _need(dst, n, np.float32, "dst")
+    _lib.check(_lib.lib().aero_hip_copy_f32(src.ptr, dst.ptr, n, _s(stream)), "copy_f32")

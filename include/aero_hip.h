@@ -1,0 +1,241 @@
+/* aero_hip.h -- C ABI of libaero_hip.so, the MI355X (gfx950) implementation of
+ * Aero's fused per-layer elementwise path: RMSNorm (plain, (1+w), per-head
+ * QK-norm, gated norm*silu), act*mul (SwiGLU, GeGLU erf/tanh), RoPE (NeoX and
+ * interleaved, full and partial, computed angle or pre-computed table) and
+ * GGUF embedding row gather with Q8_0 / Q4_K / Q6_K dequant.
+ *
+ * Three groups of entry points:
+ *
+ *  1. Reference-compatible host-pointer symbols. Same names, signatures and
+ *     status conventions as the reference's C ABI, so the reference's ctypes
+ *     bindings can load this library in place of libaero_tensor /
+ *     libaero_transformer / libaero_kernels for these ops. Buffers are host
+ *     memory; each call stages them through HBM, runs the kernel, copies the
+ *     result back and returns when it is complete (synchronous, like the
+ *     reference). Citations name the reference function each one replaces.
+ *
+ *  2. Device-pointer entry points (aero_hip_*). All buffers are HBM pointers;
+ *     work is enqueued on `stream` (NULL = the null stream) and the call
+ *     returns without waiting. They return 1 on success and 0 on refusal
+ *     (bad shape, misaligned pointer, HIP error); aero_hip_last_error()
+ *     then describes why. Nothing is allocated; the caller owns every buffer.
+ *
+ *  3. Runtime helpers (device memory, streams, events, per-kernel timing)
+ *     so that a host without PyTorch can drive the device path.
+ *
+ * Layouts are row-major fp32 unless stated. Pointers must be 16-byte aligned
+ * where a vectorised kernel applies (any hipMalloc pointer is); unaligned or
+ * odd-sized inputs take a scalar kernel with the same arithmetic.
+ */
+#ifndef AERO_HIP_H
+#define AERO_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------
+ * 1. Reference-compatible host-pointer ABI
+ * ---------------------------------------------------------------------- */
+
+/* src/tensor.cpp:234-238 aero_tensor_silu: v[i] *= sigmoid(v[i]), in place.
+ * 1 = ok, 0 = refused (null or n <= 0). */
+int aero_tensor_silu(float* v, int64_t n);
+/* src/tensor.cpp:240-244 aero_tensor_gelu: erf-form GELU (A&S 7.1.26), in place. */
+int aero_tensor_gelu(float* v, int64_t n);
+/* src/tensor.cpp:252-257 aero_tensor_mul: a[i] *= b[i]. */
+int aero_tensor_mul(float* a, const float* b, int64_t n);
+/* src/tensor.cpp:259-264 aero_tensor_swiglu: gate[i] = silu(gate[i])*up[i]. */
+int aero_tensor_swiglu(float* gate, const float* up, int64_t n);
+/* src/tensor.cpp:266-275 aero_tensor_rmsnorm: out = x/sqrt(mean(x^2)+eps)*w. */
+int aero_tensor_rmsnorm(const float* x, const float* weight, float* out,
+                        int64_t n, float eps);
+/* src/tensor.cpp:277-288 aero_tensor_l2norm: out = x/max(||x||,eps)*w
+ * (weighted = 1) or weightless (weighted = 0, weight may be NULL). */
+int aero_tensor_l2norm(const float* x, const float* weight, float* out,
+                       int64_t n, float eps, int weighted);
+/* src/tensor.cpp:290-296 aero_tensor_rmsnorm_rows: weightless per-row RMS
+ * over a rows x cols block, in place. */
+int aero_tensor_rmsnorm_rows(float* t, int64_t rows, int64_t cols, float eps);
+
+/* src/transformer.cpp:227-233 aero_rope_tables: cos/sin [n_pos, n_rot/2],
+ * ROW-indexed (row t = positions[t]). Returns n_rot, or -1 when head_dim <= 0,
+ * n_pos < 0, positions == NULL or freq_factors is shorter than n_rot/2
+ * (and -1 on a HIP failure, which the reference cannot have). */
+int64_t aero_rope_tables(int64_t head_dim, const int32_t* positions,
+                         int64_t n_pos, float base, int64_t n_dims,
+                         const float* freq_factors, int64_t n_ff,
+                         float* cos_out, float* sin_out);
+/* src/transformer.cpp:235-240 aero_apply_rope: rotate x [n_rows, head_dim]
+ * in place; row r reads table row positions[r] (or r when NULL). mode 0 =
+ * NeoX, otherwise interleaved. Rows with a negative position are refused as
+ * a whole (nothing is written; aero_hip_last_error says why). */
+void aero_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
+                     const float* cos_tab, const float* sin_tab,
+                     const int32_t* positions, int mode);
+/* src/transformer.cpp:242-245 aero_rmsnorm_rows: out (may alias x) =
+ * per-row RMSNorm; weight NULL = ones. */
+void aero_rmsnorm_rows(const float* x, const float* weight, float* out,
+                       int64_t n_rows, int64_t n_cols, float eps);
+/* src/transformer.cpp:247-250 aero_l2norm_rows. */
+void aero_l2norm_rows(const float* x, const float* weight, float* out,
+                      int64_t n_rows, int64_t n_cols, float eps);
+/* src/transformer.cpp:252-253 aero_gelu / aero_silu (in place, void). */
+void aero_gelu(float* v, int64_t n);
+void aero_silu(float* v, int64_t n);
+/* src/transformer.cpp:255-257 aero_swiglu (in place on gate, void). */
+void aero_swiglu(float* gate, const float* up, int64_t n);
+
+/* src/kernels.cpp:560-565 block geometry of a ggml type id; 0 if unknown. */
+int64_t aero_dtype_block_bytes(int t);
+int64_t aero_dtype_block_values(int t);
+/* src/kernels.cpp:566 aero_hardware_threads: min(host cores, 8). Kept for the
+ * reference binding's auto-thread rule; the GPU path ignores it. */
+int aero_hardware_threads(void);
+/* src/kernels.cpp:568-584 aero_dequant_ref: dequantise floor(n/bv) blocks of
+ * type t (F32, F16, BF16, Q8_0, Q4_K, Q6_K). Refuses (0) a raw_len shorter
+ * than the blocks need, or any other type. */
+int aero_dequant_ref(int t, const uint8_t* raw, int64_t raw_len, float* out,
+                     int64_t n_values);
+/* src/kernels.cpp:587-603 aero_dequant_threaded: same result; `threads` is
+ * accepted for signature compatibility and ignored. */
+int aero_dequant_threaded(int t, const uint8_t* raw, int64_t raw_len,
+                          float* out, int64_t n_values, int threads);
+
+/* ------------------------------------------------------------------------
+ * 2. Device-pointer fused ops (HBM pointers, asynchronous on `stream`)
+ * ---------------------------------------------------------------------- */
+
+#define AERO_NORM_UNIT_OFFSET 1 /* weight is applied as (1 + w) (Gemma)      */
+#define AERO_NORM_L2          2 /* divisor max(||x||, eps) instead of RMS     */
+
+/* Per-row RMSNorm: out[r] = x[r] * (1/sqrt(mean(x[r]^2)+eps)) * w.
+ * Replaces src/tensor.cpp:128-134 / src/transformer.cpp:98-104 (rows) and,
+ * with rows = T*H and cols = head_dim, the per-head QK-norm of
+ * src/attention_layer.cpp:89-108. w may be NULL (ones); out may alias x. */
+int aero_hip_rmsnorm(const float* x, const float* w, float* out, int64_t rows,
+                     int64_t cols, float eps, int flags, void* stream);
+
+/* Gated RMSNorm * silu (src/ssm.cpp:327-343): x, z, out are [rows, inner];
+ * for each group-long slice: denom = sqrt(mean(x^2)+eps),
+ * out = ((x/denom) * w[col % w_len]) * z/(1+exp(-z)). group = inner is the
+ * reference's whole-row RMS; group must divide inner. out may alias x. */
+int aero_hip_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
+                                int64_t w_len, float* out, int64_t rows,
+                                int64_t inner, int64_t group, float eps,
+                                void* stream);
+
+#define AERO_ACT_SILU      0 /* g*sigmoid(g)           src/tensor.cpp:104-106,120-125 */
+#define AERO_ACT_GELU      1 /* erf GELU, A&S 7.1.26   src/tensor.cpp:52-59,108-114   */
+#define AERO_ACT_GELU_TANH 2 /* tanh-approximate GELU (no reference function)        */
+#define AERO_ACT_IDENTITY  3 /* plain product (mul_)   src/tensor.cpp:116-118         */
+
+/* out[i] = act(gate[i]) * up[i] (up == NULL: out = act(gate)). n elements.
+ * out may alias gate or up. Replaces swiglu_ / gelu_+mul_ / silu_ / mul_. */
+int aero_hip_act_mul(int kind, const float* gate, const float* up, float* out,
+                     int64_t n, void* stream);
+
+/* Host-side arithmetic only (no device work): the per-pair inverse
+ * frequencies of src/transformer.cpp:34-47, inv[p] = 1/powf(base,
+ * (float)p*2/(float)n) (/ ff[p]), written to host inv_out[n/2]. Returns n
+ * (the rotated width, even) or -1. Computing them on the host with the same
+ * expression keeps (float)pos*inv bit-identical to the reference's angle. */
+int64_t aero_hip_rope_inv_freq(int64_t head_dim, int64_t n_dims, float base,
+                               const float* freq_factors, int64_t n_ff,
+                               float* inv_out);
+
+/* Device rope_tables: cos/sin[t*half + p] = cos/sin((float)pos[t]*inv[p]).
+ * pos [n_pos] int32, inv [half] (from aero_hip_rope_inv_freq). */
+int aero_hip_rope_tables(const int32_t* pos, int64_t n_pos, const float* inv,
+                         int64_t half, float* cos_out, float* sin_out,
+                         void* stream);
+
+#define AERO_ROPE_NEOX        0 /* pairs (x[p], x[p+n_rot/2]) */
+#define AERO_ROPE_INTERLEAVED 1 /* pairs (x[2p], x[2p+1])      */
+
+/* Fused per-head RMSNorm -> RoPE on q [n_tok, n_q_heads, head_dim] and
+ * (optionally) k [n_tok, n_k_heads, head_dim], one pass per head row.
+ * Reproduces src/attention_layer.cpp:89-156: optional RMSNorm over the head
+ * (q_norm_w / k_norm_w [head_dim], NULL = no norm for that tensor;
+ * norm_flags as for aero_hip_rmsnorm), then RoPE on the first n_rot
+ * channels at the token's position (every head of a token shares it):
+ *   - angle source: inv_freq [n_rot/2] (angle = (float)pos*inv[p], fp32,
+ *     accurate sincos) or a POSITION-indexed table cos_tab/sin_tab
+ *     [n_tab, n_rot/2] (exactly one of the two must be given);
+ *   - pos [n_tok] int32 (NULL = token index); a token whose position falls
+ *     outside [0, n_tab) of a table is left unchanged;
+ *   - channels >= n_rot pass through (normalised when a norm is applied).
+ * q_out / k_out NULL = in place. n_k_heads may be 0 with k == NULL. */
+int aero_hip_qk_norm_rope(float* q, float* q_out, int64_t n_q_heads,
+                          float* k, float* k_out, int64_t n_k_heads,
+                          const float* q_norm_w, const float* k_norm_w,
+                          float eps, int norm_flags, int64_t n_tok,
+                          int64_t head_dim, int64_t n_rot, int mode,
+                          const int32_t* pos, const float* inv_freq,
+                          const float* cos_tab, const float* sin_tab,
+                          int64_t n_tab, void* stream);
+
+/* ggml type ids accepted by the gather / dequant entry points */
+#define AERO_DTYPE_F32  0
+#define AERO_DTYPE_F16  1
+#define AERO_DTYPE_Q8_0 8
+#define AERO_DTYPE_Q4_K 12
+#define AERO_DTYPE_Q6_K 14
+#define AERO_DTYPE_BF16 30
+
+/* Token-embedding row gather + dequant (src/model.cpp:297-316 with
+ * dequant_ref, src/kernels.cpp:315-458): out[i, :] = dequant(table row
+ * ids[i]) (* scale when scale > 0, a separate fp32 multiply as the reference's
+ * second pass). table holds vocab rows of (n_embd/bv)*bb bytes (table_bytes
+ * >= that, base 4-byte aligned); types Q8_0, Q4_K, Q6_K. An id outside
+ * [0, vocab) yields a zero row and, when bad_count != NULL, adds 1 to
+ * *bad_count (device uint32; the caller clears it). */
+int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
+                          int64_t vocab, int64_t n_embd, const int32_t* ids,
+                          int64_t n_ids, float scale, float* out,
+                          uint32_t* bad_count, void* stream);
+
+/* Whole-buffer dequant (the device form of aero_dequant_ref): floor(n/bv)
+ * blocks of raw -> out. Types F32, F16, BF16, Q8_0, Q4_K, Q6_K. */
+int aero_hip_dequant(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
+                     int64_t n_values, void* stream);
+
+/* Plain fp32 copy kernel (dst = src, n elements): the known-size reference
+ * workload used to calibrate HBM byte counters. */
+int aero_hip_copy_f32(const float* src, float* dst, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------
+ * 3. Runtime helpers
+ * ---------------------------------------------------------------------- */
+const char* aero_hip_last_error(void);  /* thread-local, "" when none       */
+const char* aero_hip_version(void);
+int   aero_hip_device_count(void);      /* 0 when no GPU / no driver        */
+int   aero_hip_set_device(int device);
+void* aero_hip_malloc(int64_t bytes);   /* NULL on failure                  */
+int   aero_hip_free(void* p);
+int   aero_hip_memcpy_htod(void* dst, const void* src, int64_t bytes);
+int   aero_hip_memcpy_dtoh(void* dst, const void* src, int64_t bytes);
+int   aero_hip_memcpy_dtod(void* dst, const void* src, int64_t bytes,
+                           void* stream);
+int   aero_hip_memset(void* dst, int value, int64_t bytes);  /* synchronous */
+void* aero_hip_stream_create(void);     /* default priority                 */
+int   aero_hip_stream_destroy(void* stream);
+int   aero_hip_stream_synchronize(void* stream);
+int   aero_hip_device_synchronize(void);
+void* aero_hip_event_create(void);
+int   aero_hip_event_destroy(void* ev);
+int   aero_hip_event_record(void* ev, void* stream);
+int   aero_hip_event_synchronize(void* ev);
+/* Milliseconds between two recorded events; negative on error. */
+float aero_hip_event_elapsed_ms(void* start, void* stop);
+/* Arm per-kernel timing: the next kernel this thread launches through any
+ * aero_hip_* op records `start` when it begins and `stop` when it ends on the
+ * device (hipExtLaunchKernel), then the arming is cleared. */
+int   aero_hip_time_next_kernel(void* start, void* stop);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AERO_HIP_H */

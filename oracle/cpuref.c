@@ -1,0 +1,224 @@
+/* oracle/cpuref.c -- fp32 part of the CPU restatement (norms, activations,
+ * RoPE, gated norm).
+ *
+ * TEST INFRASTRUCTURE: the checker for the HIP path, and the "port" CPU
+ * baseline. Built with gcc -O2 -ffp-contract=off and no -ffast-math, as the
+ * reference builds its fp32 libraries (Makefile:74-76,144-154), so every
+ * multiply and add rounds separately and summation is serial in fp32.
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *   cr_rmsnorm_rows    float64 closed form x/sqrt(mean(x^2)+eps)*w; "ones in ->
+ *                      weight out" (tests/test_tensor.cpp:98-104); weight=NULL
+ *                      bit-identical to ones (tests/test_transformer_cpp.cpp:
+ *                      289-294); compiled reference src/transformer.cpp when
+ *                      it builds (bit-exact).
+ *   cr_l2norm_rows     float64 closed form with the max(norm, eps) floor; the
+ *                      sub-eps floor case of tests/test_tensor_native.py:
+ *                      154-181; compiled reference (bit-exact).
+ *   cr_gated_rmsnorm_silu  float64 closed form of src/ssm.cpp:327-343;
+ *                      invariants (z -> +inf with w = 1 gives unit RMS over the
+ *                      group; group = inner has no per-head effect). The
+ *                      reference only reaches this arithmetic inside
+ *                      aero_ssm_forward_q, so there is no compiled cross-check.
+ *   cr_act / cr_act_mul  math.erf / math.tanh / exp closed forms in float64;
+ *                      spot values of tests/test_tensor_native.py:118-132;
+ *                      compiled reference (bit-exact for silu/gelu/swiglu/mul).
+ *                      gelu_tanh has no reference function: closed form only.
+ *   cr_rope_*          compiled reference (bit-exact); relative-position
+ *                      invariance, norm preservation, tail pass-through and
+ *                      freq_factor 1e30 => cos 1, sin 0
+ *                      (tests/test_transformer_cpp.cpp:137-257); float64
+ *                      closed form of the angle.
+ */
+#include "cpuref.h"
+
+#include <math.h>
+#include <stddef.h>
+
+/* ------------------------------------------------------------------ norms */
+
+/* src/tensor.cpp:128-134 (rmsnorm) applied per row as src/transformer.cpp:
+ * 98-104 does. ss accumulates serially in fp32, inv = 1/sqrt(ss/n + eps), and
+ * out = (x*inv)*w. unit_offset = 1 is the Gemma-style (1+w) composition:
+ * w' = 1 + w in fp32, then the same expression (the reference has no such
+ * function; this is rms_norm(x, np.float32(1) + w)). out may alias x. */
+void cr_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows,
+                     int64_t cols, float eps, int unit_offset) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float* o = out + r * cols;
+        float ss = 0.0f;
+        for (int64_t c = 0; c < cols; ++c) ss += xr[c] * xr[c];
+        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+        for (int64_t c = 0; c < cols; ++c) {
+            const float v = xr[c] * inv;
+            if (w == NULL) {
+                o[c] = v * 1.0f;
+            } else {
+                const float wc = unit_offset ? 1.0f + w[c] : w[c];
+                o[c] = v * wc;
+            }
+        }
+    }
+}
+
+/* src/tensor.cpp:136-154 (l2norm) per row as src/transformer.cpp:106-113:
+ * denominator max(||x||, eps), weighted iff w != NULL. */
+void cr_l2norm_rows(const float* x, const float* w, float* out, int64_t rows,
+                    int64_t cols, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float* o = out + r * cols;
+        float ss = 0.0f;
+        for (int64_t c = 0; c < cols; ++c) ss += xr[c] * xr[c];
+        const float nrm = sqrtf(ss);
+        const float inv = 1.0f / (nrm > eps ? nrm : eps);
+        for (int64_t c = 0; c < cols; ++c)
+            o[c] = xr[c] * inv * (w ? w[c] : 1.0f);
+    }
+}
+
+/* silu in the division form of src/ssm.cpp:17. */
+static float silu_div(float v) { return v / (1.0f + expf(-v)); }
+
+/* Gated RMSNorm * silu, src/ssm.cpp:327-343 (numpy twin engine/ssm.py:
+ * 346-348). For each `group`-long slice of a row: ss over the slice,
+ * denom = sqrt(ss/group + eps), out = ((x/denom) * w[col % w_len]) * silu(z),
+ * where col is the column inside the `inner`-long row. group = inner is the
+ * reference (whole-row RMS, F4 in the survey); a smaller group that divides
+ * inner is the per-head reading. */
+void cr_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
+                           int64_t w_len, float* out, int64_t rows,
+                           int64_t inner, int64_t group, float eps) {
+    const int64_t gpr = inner / group;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t g = 0; g < gpr; ++g) {
+            const int64_t off = r * inner + g * group;
+            const float* xr = x + off;
+            const float* zr = z + off;
+            float* o = out + off;
+            float ss = 0.0f;
+            for (int64_t c = 0; c < group; ++c) ss += xr[c] * xr[c];
+            ss /= (float)group;
+            const float denom = sqrtf(ss + eps);
+            for (int64_t c = 0; c < group; ++c) {
+                const float wn = w[(g * group + c) % w_len];
+                o[c] = (xr[c] / denom) * wn * silu_div(zr[c]);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------ activations */
+
+/* src/tensor.cpp:47 */
+static float sigmoid_recip(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+/* Abramowitz & Stegun 7.1.26 erf (published constants), evaluated in the
+ * order of src/tensor.cpp:52-59. */
+static float erf_as(float v) {
+    const float s = copysignf(1.0f, v);
+    const float a = fabsf(v);
+    const float t = 1.0f / (1.0f + 0.3275911f * a);
+    const float p = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t
+                      - 0.284496736f) * t + 0.254829592f) * t;
+    return s * (1.0f - p * expf(-a * a));
+}
+
+static float act1(int kind, float v) {
+    switch (kind) {
+    case 0: /* src/tensor.cpp:104-106: v *= sigmoid(v) */
+        return v * sigmoid_recip(v);
+    case 1: /* src/tensor.cpp:108-114 */
+        return 0.5f * v * (1.0f + erf_as(v * 0.7071067811865476f));
+    case 2: /* tanh-approximate GELU: no reference function; closed form */
+        return 0.5f * v *
+               (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+    default:
+        return v;
+    }
+}
+
+void cr_act(int kind, float* v, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) v[i] = act1(kind, v[i]);
+}
+
+/* out = act(gate) * up. kind 0 is swiglu_ (src/tensor.cpp:120-125,
+ * (g*sigmoid(g))*u); kind 1 is gelu_ then mul_ (src/tensor.cpp:108-118, as
+ * src/model.cpp:224-225 calls them); kind 3 is mul_ alone. */
+void cr_act_mul(int kind, const float* gate, const float* up, float* out,
+                int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float a = act1(kind, gate[i]);
+        out[i] = up ? a * up[i] : a;
+    }
+}
+
+/* ------------------------------------------------------------------- RoPE */
+
+/* The per-pair inverse frequency of src/transformer.cpp:34-47:
+ * n = head dim or min(n_dims, head_dim), rounded down to even;
+ * inv[p] = 1/powf(base, (float)p*2/(float)n), divided by ff[p] when given.
+ * Returns n (the rotated width) or -1 on the reference's refusals. */
+int64_t cr_rope_inv_freq(int64_t head_dim, int64_t n_dims, float base,
+                         const float* ff, int64_t n_ff, float* inv_out) {
+    if (head_dim <= 0) return -1;
+    int64_t n = (n_dims <= 0) ? head_dim : (n_dims < head_dim ? n_dims : head_dim);
+    n -= n % 2;
+    const int64_t half = n / 2;
+    if (half <= 0) return n;
+    if (ff != NULL && n_ff < half) return -1;
+    for (int64_t p = 0; p < half; ++p) {
+        const float e = (float)((float)p * 2.0f / (float)n);
+        float inv = 1.0f / powf(base, e);
+        if (ff != NULL) inv /= ff[p];
+        inv_out[p] = inv;
+    }
+    return n;
+}
+
+/* src/transformer.cpp:27-61. ROW-indexed: row t holds (float)pos[t]*inv[p]. */
+int64_t cr_rope_tables(int64_t head_dim, const int32_t* pos, int64_t n_pos,
+                       float base, int64_t n_dims, const float* ff,
+                       int64_t n_ff, float* cos_out, float* sin_out) {
+    if (head_dim <= 0 || n_pos < 0 || pos == NULL) return -1;
+    float inv[4096];
+    int64_t n = (n_dims <= 0) ? head_dim : (n_dims < head_dim ? n_dims : head_dim);
+    n -= n % 2;
+    if (n / 2 > 4096) return -1;
+    const int64_t got = cr_rope_inv_freq(head_dim, n_dims, base, ff, n_ff, inv);
+    if (got < 0) return -1;
+    const int64_t half = got / 2;
+    for (int64_t t = 0; t < n_pos; ++t) {
+        for (int64_t p = 0; p < half; ++p) {
+            const float ang = (float)pos[t] * inv[p];
+            cos_out[t * half + p] = cosf(ang);
+            sin_out[t * half + p] = sinf(ang);
+        }
+    }
+    return got;
+}
+
+/* src/transformer.cpp:63-96. In place; row r reads table row pos[r] (or r):
+ * POSITION-indexed. mode 0 = NeoX (x[p], x[p+half]); anything else pairs
+ * (x[2p], x[2p+1]). Channels >= 2*half are untouched. */
+void cr_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
+                   const float* cos_tab, const float* sin_tab,
+                   const int32_t* pos, int mode) {
+    const int64_t half = n_rot / 2;
+    if (half <= 0 || head_dim <= 0) return;
+    for (int64_t r = 0; r < n_rows; ++r) {
+        float* xr = x + r * head_dim;
+        const int64_t pi = pos ? (int64_t)pos[r] : r;
+        const float* c = cos_tab + pi * half;
+        const float* s = sin_tab + pi * half;
+        for (int64_t p = 0; p < half; ++p) {
+            const int64_t i0 = (mode == 0) ? p : 2 * p;
+            const int64_t i1 = (mode == 0) ? p + half : 2 * p + 1;
+            const float x0 = xr[i0];
+            const float x1 = xr[i1];
+            xr[i0] = x0 * c[p] - x1 * s[p];
+            xr[i1] = x0 * s[p] + x1 * c[p];
+        }
+    }
+}

@@ -1,0 +1,66 @@
+/* oracle/cpuref.h -- CPU restatement of Aero's fused per-layer elementwise path.
+ *
+ * TEST INFRASTRUCTURE. This library is the checker, never the product: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The GPU path in aero_amd/ never calls it and has no CPU fallback.
+ *
+ * Every function restates the reference algorithm in plain C, in the
+ * reference's fp32 operation order, and cites the file:line it follows
+ * (paths relative to the BattleCrusader/aero tree). See cpuref.c for how each
+ * function's parity is pinned.
+ */
+#ifndef AERO_CPUREF_H
+#define AERO_CPUREF_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (include/aero/kernels.hpp:40-49) */
+enum {
+    CR_F32 = 0, CR_F16 = 1, CR_Q8_0 = 8, CR_Q4_K = 12, CR_Q5_K = 13,
+    CR_Q6_K = 14, CR_IQ4_XS = 23, CR_BF16 = 30
+};
+
+/* ---- quant (cpuref_quant.c) ------------------------------------------- */
+float   cr_f16_to_f32(uint16_t h);
+void    cr_f16_to_f32_n(const uint16_t* h, float* out, int64_t n);
+int64_t cr_block_bytes(int type);
+int64_t cr_block_values(int type);
+int     cr_dequant(int type, const uint8_t* raw, int64_t raw_len, float* out,
+                   int64_t n_values);
+int     cr_dequant_threaded(int type, const uint8_t* raw, int64_t raw_len,
+                            float* out, int64_t n_values, int threads);
+int     cr_embed_gather(int type, const uint8_t* table, int64_t vocab,
+                        int64_t n_embd, const int32_t* ids, int64_t n_ids,
+                        float scale, float* out);
+
+/* ---- fp32 path (cpuref.c) --------------------------------------------- */
+void cr_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows,
+                     int64_t cols, float eps, int unit_offset);
+void cr_l2norm_rows(const float* x, const float* w, float* out, int64_t rows,
+                    int64_t cols, float eps);
+void cr_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
+                           int64_t w_len, float* out, int64_t rows,
+                           int64_t inner, int64_t group, float eps);
+
+/* act kinds: 0 silu, 1 gelu (erf, A&S 7.1.26), 2 gelu (tanh), 3 identity */
+void cr_act(int kind, float* v, int64_t n);
+void cr_act_mul(int kind, const float* gate, const float* up, float* out,
+                int64_t n);
+
+int64_t cr_rope_inv_freq(int64_t head_dim, int64_t n_dims, float base,
+                         const float* ff, int64_t n_ff, float* inv_out);
+int64_t cr_rope_tables(int64_t head_dim, const int32_t* pos, int64_t n_pos,
+                       float base, int64_t n_dims, const float* ff,
+                       int64_t n_ff, float* cos_out, float* sin_out);
+void    cr_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
+                      const float* cos_tab, const float* sin_tab,
+                      const int32_t* pos, int mode);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,242 @@
+"""ctypes binding of the oracle's C restatement (libaero_cpuref.so).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). Every function takes and
+returns numpy arrays; the C side follows the reference file:line cited in
+oracle/cpuref.c and oracle/cpuref_quant.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_uint8, c_uint16
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libaero_cpuref.so")
+
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, BF16 = 0, 1, 8, 12, 13, 14, 23, 30
+ACT_SILU, ACT_GELU, ACT_GELU_TANH, ACT_IDENTITY = 0, 1, 2, 3
+ROPE_NEOX, ROPE_INTERLEAVED = 0, 1
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle not built: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        fp, ip, up = POINTER(c_float), POINTER(c_int32), POINTER(c_uint8)
+        L.cr_f16_to_f32.argtypes = [c_uint16]
+        L.cr_f16_to_f32.restype = c_float
+        L.cr_f16_to_f32_n.argtypes = [POINTER(c_uint16), fp, c_int64]
+        L.cr_f16_to_f32_n.restype = None
+        L.cr_block_bytes.argtypes = [c_int]
+        L.cr_block_bytes.restype = c_int64
+        L.cr_block_values.argtypes = [c_int]
+        L.cr_block_values.restype = c_int64
+        L.cr_dequant.argtypes = [c_int, up, c_int64, fp, c_int64]
+        L.cr_dequant.restype = c_int
+        L.cr_dequant_threaded.argtypes = [c_int, up, c_int64, fp, c_int64, c_int]
+        L.cr_dequant_threaded.restype = c_int
+        L.cr_embed_gather.argtypes = [c_int, up, c_int64, c_int64, ip, c_int64,
+                                      c_float, fp]
+        L.cr_embed_gather.restype = c_int
+        L.cr_rmsnorm_rows.argtypes = [fp, fp, fp, c_int64, c_int64, c_float, c_int]
+        L.cr_rmsnorm_rows.restype = None
+        L.cr_l2norm_rows.argtypes = [fp, fp, fp, c_int64, c_int64, c_float]
+        L.cr_l2norm_rows.restype = None
+        L.cr_gated_rmsnorm_silu.argtypes = [fp, fp, fp, c_int64, fp, c_int64,
+                                            c_int64, c_int64, c_float]
+        L.cr_gated_rmsnorm_silu.restype = None
+        L.cr_act.argtypes = [c_int, fp, c_int64]
+        L.cr_act.restype = None
+        L.cr_act_mul.argtypes = [c_int, fp, fp, fp, c_int64]
+        L.cr_act_mul.restype = None
+        L.cr_rope_inv_freq.argtypes = [c_int64, c_int64, c_float, fp, c_int64, fp]
+        L.cr_rope_inv_freq.restype = c_int64
+        L.cr_rope_tables.argtypes = [c_int64, ip, c_int64, c_float, c_int64, fp,
+                                     c_int64, fp, fp]
+        L.cr_rope_tables.restype = c_int64
+        L.cr_apply_rope.argtypes = [fp, c_int64, c_int64, c_int64, fp, fp, ip, c_int]
+        L.cr_apply_rope.restype = None
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    if a is None:
+        return ctypes.cast(None, POINTER(c_float))
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(POINTER(c_float))
+
+
+def _i(a):
+    if a is None:
+        return ctypes.cast(None, POINTER(c_int32))
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(POINTER(c_int32))
+
+
+def _u8(a):
+    assert a.dtype == np.uint8 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(POINTER(c_uint8))
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().cr_f16_to_f32(int(h)))
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    """Vector form (no Python-float round trip, so NaN payloads survive)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16).reshape(-1)
+    out = np.empty(h.size, dtype=np.float32)
+    lib().cr_f16_to_f32_n(h.ctypes.data_as(POINTER(c_uint16)), _f(out), h.size)
+    return out
+
+
+def block_bytes(t: int) -> int:
+    return int(lib().cr_block_bytes(t))
+
+
+def block_values(t: int) -> int:
+    return int(lib().cr_block_values(t))
+
+
+def dequant(t: int, raw: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    out = np.zeros(n, dtype=np.float32)
+    if threads > 1:
+        ok = lib().cr_dequant_threaded(t, _u8(raw), raw.size, _f(out), n, threads)
+    else:
+        ok = lib().cr_dequant(t, _u8(raw), raw.size, _f(out), n)
+    if not ok:
+        raise ValueError("oracle dequant refused")
+    return out
+
+
+def embed_gather(t: int, table: np.ndarray, vocab: int, n_embd: int, ids,
+                 scale: float = 0.0) -> np.ndarray:
+    table = np.ascontiguousarray(table, dtype=np.uint8).reshape(-1)
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+    out = np.zeros((ids.size, n_embd), dtype=np.float32)
+    if not lib().cr_embed_gather(t, _u8(table), vocab, n_embd, _i(ids), ids.size,
+                                 float(scale), _f(out)):
+        raise ValueError("oracle embed_gather refused")
+    return out
+
+
+def rmsnorm_rows(x, w, eps: float, unit_offset: bool = False) -> np.ndarray:
+    x = f32(x)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    out = np.empty_like(x)
+    w = None if w is None else f32(w)
+    lib().cr_rmsnorm_rows(_f(x), _f(w), _f(out), rows, cols, float(eps),
+                          1 if unit_offset else 0)
+    return out
+
+
+def l2norm_rows(x, w, eps: float) -> np.ndarray:
+    x = f32(x)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    out = np.empty_like(x)
+    w = None if w is None else f32(w)
+    lib().cr_l2norm_rows(_f(x), _f(w), _f(out), rows, cols, float(eps))
+    return out
+
+
+def gated_rmsnorm_silu(x, z, w, eps: float, group: int | None = None) -> np.ndarray:
+    x, z, w = f32(x), f32(z), f32(w)
+    inner = x.shape[-1]
+    rows = x.size // inner
+    group = inner if group is None else int(group)
+    out = np.empty_like(x)
+    lib().cr_gated_rmsnorm_silu(_f(x), _f(z), _f(w), w.size, _f(out), rows, inner,
+                                group, float(eps))
+    return out
+
+
+def act(kind: int, x) -> np.ndarray:
+    out = np.array(f32(x), copy=True)
+    lib().cr_act(kind, _f(out), out.size)
+    return out
+
+
+def act_mul(kind: int, gate, up) -> np.ndarray:
+    gate = f32(gate)
+    up = None if up is None else f32(up)
+    out = np.empty_like(gate)
+    lib().cr_act_mul(kind, _f(gate), _f(up), _f(out), gate.size)
+    return out
+
+
+def rope_inv_freq(head_dim: int, n_dims, base: float, ff=None):
+    ffa = None if ff is None else f32(ff).reshape(-1)
+    inv = np.zeros(4096, dtype=np.float32)
+    n = lib().cr_rope_inv_freq(head_dim, -1 if n_dims is None else int(n_dims),
+                               float(base), _f(ffa), 0 if ffa is None else ffa.size,
+                               _f(inv))
+    if n < 0:
+        raise ValueError("oracle rope_inv_freq refused")
+    return int(n), inv[: n // 2].copy()
+
+
+def rope_tables(head_dim: int, positions, base: float, n_dims=None, ff=None):
+    pos = np.ascontiguousarray(positions, dtype=np.int32).reshape(-1)
+    n = head_dim if n_dims is None else min(int(n_dims), head_dim)
+    n -= n % 2
+    half = n // 2
+    ffa = None if ff is None else f32(ff).reshape(-1)
+    cos = np.zeros(max(pos.size * half, 1), dtype=np.float32)
+    sin = np.zeros(max(pos.size * half, 1), dtype=np.float32)
+    got = lib().cr_rope_tables(head_dim, _i(pos), pos.size, float(base),
+                               -1 if n_dims is None else int(n_dims), _f(ffa),
+                               0 if ffa is None else ffa.size, _f(cos), _f(sin))
+    if got < 0:
+        raise ValueError("oracle rope_tables refused")
+    h = got // 2
+    return cos[: pos.size * h].reshape(pos.size, h), sin[: pos.size * h].reshape(pos.size, h)
+
+
+def apply_rope(x, cos, sin, positions=None, mode: int = ROPE_NEOX,
+               n_rot: int | None = None) -> np.ndarray:
+    """Rotated copy of x (..., head_dim); table rows are read by positions[row]."""
+    out = np.array(f32(x), copy=True)
+    head_dim = out.shape[-1]
+    rows = out.size // head_dim
+    cos, sin = f32(cos), f32(sin)
+    n_rot = 2 * cos.shape[1] if n_rot is None else n_rot
+    pos = None if positions is None else np.ascontiguousarray(positions, np.int32)
+    lib().cr_apply_rope(_f(out), rows, head_dim, n_rot, _f(cos), _f(sin), _i(pos), mode)
+    return out
+
+
+def qk_norm_rope(x, n_tok: int, n_head: int, head_dim: int, n_rot: int, pos,
+                 base: float, mode: int = ROPE_NEOX, norm_w=None, eps: float = 1e-6,
+                 unit_offset: bool = False, ff=None, cos_tab=None, sin_tab=None):
+    """The composition the fused kernel reproduces (src/attention_layer.cpp:89-156):
+    optional per-(token, head) RMSNorm over head_dim, then RoPE on the first
+    n_rot channels at the token's position. Angles come from a table built by
+    rope_tables over the token positions (row t <-> token t), or, when cos_tab /
+    sin_tab are given, from that POSITION-indexed table."""
+    x = f32(x).reshape(n_tok, n_head, head_dim)
+    pos = np.ascontiguousarray(pos, dtype=np.int32).reshape(-1)
+    if norm_w is not None:
+        x = rmsnorm_rows(x, norm_w, eps, unit_offset)
+    if n_rot < 2:
+        return np.array(x, copy=True)
+    if cos_tab is None:
+        c, s = rope_tables(n_rot, pos, base, n_rot, ff)
+        rowpos = np.repeat(np.arange(n_tok, dtype=np.int32), n_head)
+    else:
+        c, s = cos_tab, sin_tab
+        rowpos = np.repeat(pos, n_head)
+    return apply_rope(x, c, s, rowpos, mode, n_rot=n_rot)

@@ -1,0 +1,162 @@
+"""ctypes binding of the reference's own hot-path C++ built into oracle/_ref/.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). `make -C oracle ref`
+compiles src/kernels.cpp and src/transformer.cpp + src/tensor.cpp of the
+reference tree into oracle/_ref/; those libraries export the reference's C ABI
+(src/kernels.cpp:560-603, src/tensor.cpp:205-304, src/transformer.cpp:
+223-284). This module loads them when present and returns None otherwise, so
+callers skip the cross-check rather than fail.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_uint8
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF_DIR = os.path.join(HERE, "_ref")
+KERNELS = os.path.join(REF_DIR, "libref_kernels.so")
+TRANSFORMER = os.path.join(REF_DIR, "libref_transformer.so")
+
+_k = None
+_t = None
+
+
+def kernels():
+    global _k
+    if _k is None and os.path.exists(KERNELS):
+        L = ctypes.CDLL(KERNELS)
+        L.aero_dequant_ref.argtypes = [c_int, POINTER(c_uint8), c_int64,
+                                       POINTER(c_float), c_int64]
+        L.aero_dequant_ref.restype = c_int
+        L.aero_dequant_threaded.argtypes = [c_int, POINTER(c_uint8), c_int64,
+                                            POINTER(c_float), c_int64, c_int]
+        L.aero_dequant_threaded.restype = c_int
+        _k = L
+    return _k
+
+
+def transformer():
+    global _t
+    if _t is None and os.path.exists(TRANSFORMER):
+        L = ctypes.CDLL(TRANSFORMER)
+        fp, ip = POINTER(c_float), POINTER(c_int32)
+        L.aero_rope_tables.argtypes = [c_int64, ip, c_int64, c_float, c_int64, fp,
+                                       c_int64, fp, fp]
+        L.aero_rope_tables.restype = c_int64
+        L.aero_apply_rope.argtypes = [fp, c_int64, c_int64, c_int64, fp, fp, ip, c_int]
+        L.aero_apply_rope.restype = None
+        L.aero_rmsnorm_rows.argtypes = [fp, fp, fp, c_int64, c_int64, c_float]
+        L.aero_rmsnorm_rows.restype = None
+        L.aero_l2norm_rows.argtypes = [fp, fp, fp, c_int64, c_int64, c_float]
+        L.aero_l2norm_rows.restype = None
+        for name in ("aero_gelu", "aero_silu"):
+            getattr(L, name).argtypes = [fp, c_int64]
+            getattr(L, name).restype = None
+        L.aero_swiglu.argtypes = [fp, fp, c_int64]
+        L.aero_swiglu.restype = None
+        L.aero_tensor_mul.argtypes = [fp, fp, c_int64]
+        L.aero_tensor_mul.restype = c_int
+        _t = L
+    return _t
+
+
+def available() -> bool:
+    return kernels() is not None and transformer() is not None
+
+
+def _f(a):
+    if a is None:
+        return ctypes.cast(None, POINTER(c_float))
+    return a.ctypes.data_as(POINTER(c_float))
+
+
+def _i(a):
+    if a is None:
+        return ctypes.cast(None, POINTER(c_int32))
+    return a.ctypes.data_as(POINTER(c_int32))
+
+
+def dequant(t: int, raw: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    out = np.zeros(n, dtype=np.float32)
+    p = raw.ctypes.data_as(POINTER(c_uint8))
+    if threads > 1:
+        ok = kernels().aero_dequant_threaded(t, p, raw.size, _f(out), n, threads)
+    else:
+        ok = kernels().aero_dequant_ref(t, p, raw.size, _f(out), n)
+    if not ok:
+        raise ValueError("reference dequant refused")
+    return out
+
+
+def rmsnorm_rows(x, w, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cols = x.shape[-1]
+    out = np.empty_like(x)
+    w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    transformer().aero_rmsnorm_rows(_f(x), _f(w), _f(out), x.size // cols, cols,
+                                    float(eps))
+    return out
+
+
+def l2norm_rows(x, w, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cols = x.shape[-1]
+    out = np.empty_like(x)
+    w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    transformer().aero_l2norm_rows(_f(x), _f(w), _f(out), x.size // cols, cols,
+                                   float(eps))
+    return out
+
+
+def act(name: str, x) -> np.ndarray:
+    out = np.array(np.ascontiguousarray(x, dtype=np.float32), copy=True)
+    getattr(transformer(), "aero_" + name)(_f(out), out.size)
+    return out
+
+
+def swiglu(g, u) -> np.ndarray:
+    out = np.array(np.ascontiguousarray(g, dtype=np.float32), copy=True)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    transformer().aero_swiglu(_f(out), _f(u), out.size)
+    return out
+
+
+def mul(a, b) -> np.ndarray:
+    out = np.array(np.ascontiguousarray(a, dtype=np.float32), copy=True)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    transformer().aero_tensor_mul(_f(out), _f(b), out.size)
+    return out
+
+
+def rope_tables(head_dim: int, positions, base: float, n_dims=None, ff=None):
+    pos = np.ascontiguousarray(positions, dtype=np.int32).reshape(-1)
+    n = head_dim if n_dims is None else min(int(n_dims), head_dim)
+    n -= n % 2
+    half = n // 2
+    ffa = None if ff is None else np.ascontiguousarray(ff, dtype=np.float32)
+    cos = np.zeros(max(pos.size * half, 1), dtype=np.float32)
+    sin = np.zeros(max(pos.size * half, 1), dtype=np.float32)
+    got = transformer().aero_rope_tables(head_dim, _i(pos), pos.size, float(base),
+                                         -1 if n_dims is None else int(n_dims),
+                                         _f(ffa), 0 if ffa is None else ffa.size,
+                                         _f(cos), _f(sin))
+    if got < 0:
+        raise ValueError("reference rope_tables refused")
+    h = got // 2
+    return cos[: pos.size * h].reshape(pos.size, h), sin[: pos.size * h].reshape(pos.size, h)
+
+
+def apply_rope(x, cos, sin, positions=None, mode: int = 0, n_rot=None) -> np.ndarray:
+    out = np.array(np.ascontiguousarray(x, dtype=np.float32), copy=True)
+    head_dim = out.shape[-1]
+    cos = np.ascontiguousarray(cos, dtype=np.float32)
+    sin = np.ascontiguousarray(sin, dtype=np.float32)
+    n_rot = 2 * cos.shape[1] if n_rot is None else n_rot
+    pos = None if positions is None else np.ascontiguousarray(positions, np.int32)
+    transformer().aero_apply_rope(_f(out), out.size // head_dim, head_dim, n_rot,
+                                  _f(cos), _f(sin), _i(pos), mode)
+    return out
