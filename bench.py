@@ -1,0 +1,421 @@
+"""Benchmark of the fused per-layer elementwise path on one MI355X.
+
+A step is one pass of the path over one batch at the Llama-3-8B 512-token
+prefill shape: Q4_K token-embedding gather (512 rows of 4096), RMSNorm
+(512 x 4096), NeoX RoPE on q (512 x 32 x 128) and k (512 x 8 x 128) at
+positions 0..511, and SwiGLU on gate/up (512 x 14336). Inputs are synthetic
+(seeded), resident in HBM before timing starts, and rotated over --sets
+buffer sets (> 1 GiB together) so no launch reads data the 256 MiB Infinity
+Cache still holds from the previous use of its set.
+
+`value` is the whole step's algorithmic HBM bytes / wall time per step
+(GB/s). `roofline` is the dominant kernel (SwiGLU, 88 MB per launch): its
+algorithmic bytes / its mean device duration, measured with HIP events
+recorded by the kernel's own dispatch (hipExtLaunchKernel) during the timed
+steps. `cpu_baseline` is the same step on the host: the reference's own C++
+(built into oracle/_ref) when present, else the oracle's restatement,
+single-threaded like the reference, over a bounded sample.
+
+    python bench.py [--steps K] [--warmup W] [--sets S] [--cpu-seconds T]
+    python bench.py --all-shapes        # per-op table over every layer shape
+    python bench.py --only OP --steps K # one kernel only (for counter runs)
+    python bench.py --copy-calibration  # a plain copy of known size
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "fused-op HBM GB/s (% of MI355X peak) + rows/s vs CPU ref, Llama-3-8B shapes"
+OPS = ("embed_gather", "rmsnorm", "rope_qk", "swiglu")
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--sets", type=int, default=10)
+    p.add_argument("--shape", default=None)
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--all-shapes", action="store_true")
+    p.add_argument("--only", choices=OPS + ("rope_qk_norm", "gated_norm"), default=None)
+    p.add_argument("--copy-calibration", action="store_true")
+    return p.parse_args(argv)
+
+
+# ---------------------------------------------------------------- GPU side
+class StepBuffers:
+    """One buffer set of a step, in HBM."""
+
+    def __init__(self, s, d_table, rng):
+        from aero_amd import workloads as W
+        from aero_amd.device import DeviceArray as DA
+
+        R = s.n_tok
+        self.ids = DA.from_numpy(rng.integers(0, s.vocab, R).astype(np.int32))
+        self.emb_out = DA.empty((R, s.hidden))
+        self.x = DA.from_numpy(rng.standard_normal((R, s.hidden), dtype=np.float32))
+        self.h = DA.empty((R, s.hidden))
+        self.q = DA.from_numpy(rng.standard_normal((R, s.hq, s.head_dim), dtype=np.float32))
+        self.k = DA.from_numpy(rng.standard_normal((R, s.hk, s.head_dim), dtype=np.float32))
+        self.gate = DA.from_numpy(rng.standard_normal((R, s.ffn), dtype=np.float32))
+        self.up = DA.from_numpy(rng.standard_normal((R, s.ffn), dtype=np.float32))
+        self.act_out = DA.empty((R, s.ffn))
+        if s.gated:
+            n_v, dd = s.gated
+            self.gx = DA.from_numpy(rng.standard_normal((R, n_v * dd), dtype=np.float32))
+            self.gz = DA.from_numpy(rng.standard_normal((R, n_v * dd), dtype=np.float32))
+            self.gout = DA.empty((R, n_v * dd))
+        self.table = d_table
+
+
+class Path:
+    """The ops of one shape, bound to device constants."""
+
+    def __init__(self, name, sets, seed=0):
+        from aero_amd import ops
+        from aero_amd import workloads as W
+        from aero_amd.device import DeviceArray as DA
+
+        self.ops, self.W = ops, W
+        s = W.SHAPES[name]
+        self.s = s
+        rng = np.random.default_rng(seed)
+        bv, bb = W.BLOCK[s.emb_type]
+        self.table_host = W.make_table(s.emb_type, s.vocab * (s.hidden // bv), rng)
+        self.table = DA.from_numpy(self.table_host)
+        w = rng.standard_normal(s.hidden, dtype=np.float32) * np.float32(0.1)
+        self.w = DA.from_numpy(w if s.unit_offset else np.float32(1) + w)
+        self.pos_host = W.positions(s, rng)
+        self.pos = DA.from_numpy(self.pos_host)
+        n_rot, inv = ops.rope_inv_freq(s.n_rot, s.n_rot, s.theta)
+        self.inv = DA.from_numpy(inv)
+        self.tab = None
+        if s.rope_table:
+            # the dense position-indexed table, built on the device
+            dense = DA.from_numpy(np.arange(s.rope_table, dtype=np.int32))
+            half = s.n_rot // 2
+            self.tab = (DA.empty((s.rope_table, half)), DA.empty((s.rope_table, half)))
+            ops.rope_tables(dense, self.inv, self.tab[0], self.tab[1])
+        self.qk_w = None
+        if s.qk_norm:
+            self.qk_w = (DA.from_numpy(np.float32(0) + rng.standard_normal(s.head_dim,
+                                                                           dtype=np.float32) * 0.1),
+                         DA.from_numpy(rng.standard_normal(s.head_dim, dtype=np.float32) * 0.1))
+        if s.gated:
+            self.gw = DA.from_numpy(np.float32(1) + rng.standard_normal(s.gated[1],
+                                                                        dtype=np.float32) * 0.1)
+        self.sets = [StepBuffers(s, self.table, rng) for _ in range(sets)]
+        self.scale = float(np.float32(np.sqrt(s.hidden))) if s.emb_scale else 0.0
+
+    def bytes(self):
+        W, s = self.W, self.s
+        b = {
+            "embed_gather": W.bytes_embed(s.n_tok, s.hidden, s.emb_type),
+            "rmsnorm": W.bytes_rmsnorm(s.n_tok, s.hidden),
+            "rope_qk": W.bytes_rope(s.n_tok, s.hq + s.hk, s.head_dim, s.n_rot, s.qk_norm,
+                                    True, bool(s.rope_table)) + (4 * s.head_dim if s.qk_norm
+                                                                 else 0),
+            "swiglu": W.bytes_act(s.n_tok, s.ffn),
+        }
+        if s.gated:
+            b["gated_norm"] = W.bytes_gated(s.n_tok, s.gated[0] * s.gated[1], s.gated[1])
+        return b
+
+    def rows(self):
+        s = self.s
+        r = {"embed_gather": s.n_tok, "rmsnorm": s.n_tok, "rope_qk": s.n_tok * (s.hq + s.hk),
+             "swiglu": s.n_tok}
+        if s.gated:
+            r["gated_norm"] = s.n_tok
+        return r
+
+    def run(self, op, i, stream=None):
+        ops, s, b = self.ops, self.s, self.sets[i % len(self.sets)]
+        if op == "embed_gather":
+            ops.embed_gather(s.emb_type, b.table, s.vocab, s.hidden, b.ids, b.emb_out,
+                             scale=self.scale, stream=stream)
+        elif op == "rmsnorm":
+            ops.rmsnorm(b.x, self.w, b.h, s.n_tok, s.hidden, s.eps, unit_offset=s.unit_offset,
+                        stream=stream)
+        elif op == "rope_qk":
+            kw = {"cos_tab": self.tab[0], "sin_tab": self.tab[1]} if self.tab else {
+                "inv_freq": self.inv}
+            ops.qk_norm_rope(b.q, s.hq, s.n_tok, s.head_dim, s.n_rot, k=b.k, n_k_heads=s.hk,
+                             q_norm_w=self.qk_w[0] if self.qk_w else None,
+                             k_norm_w=self.qk_w[1] if self.qk_w else None, eps=s.eps,
+                             unit_offset=s.unit_offset, pos=self.pos, stream=stream, **kw)
+        elif op == "swiglu":
+            ops.act_mul(s.act, b.gate, b.up, b.act_out, stream=stream)
+        elif op == "gated_norm":
+            ops.gated_rmsnorm_silu(b.gx, b.gz, self.gw, b.gout, s.n_tok,
+                                   s.gated[0] * s.gated[1], s.eps, stream=stream)
+        else:
+            raise ValueError(op)
+
+    def step_ops(self):
+        return list(OPS) + (["gated_norm"] if self.s.gated else [])
+
+
+def timed_steps(path, steps, warmup, per_kernel=True, only=None):
+    """Run warmup + steps; returns (ms per step, {op: [kernel ms ...]})."""
+    from aero_amd.device import Event, Stream, synchronize, time_next_kernel
+
+    stream = Stream()
+    ops_list = [only] if only else path.step_ops()
+    for i in range(warmup):
+        for op in ops_list:
+            path.run(op, i, stream)
+    stream.synchronize()
+    evs = {op: [(Event(), Event()) for _ in range(steps)] for op in ops_list} if per_kernel else {}
+    t0 = time.perf_counter()
+    for i in range(steps):
+        for op in ops_list:
+            if per_kernel:
+                a, b = evs[op][i]
+                time_next_kernel(a, b)
+            path.run(op, warmup + i, stream)
+    stream.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    synchronize()
+    ker = {op: [a.elapsed_ms(b) for a, b in evs[op]] for op in evs}
+    stream.destroy()
+    return wall, ker
+
+
+# ---------------------------------------------------------------- CPU side
+def cpu_baseline(path, seconds):
+    """The same step on the host, single-threaded, timed per op around the
+    reference's own C entry points (oracle/_ref) or the oracle's."""
+    import ctypes
+    from ctypes import POINTER, c_float, c_int32, c_uint8
+
+    from oracle import cpuref, refbind
+
+    s, W = path.s, path.W
+    use_ref = refbind.available()
+    K = refbind.kernels() if use_ref else None
+    T = refbind.transformer() if use_ref else None
+    C = cpuref.lib()
+    fp = lambda a: a.ctypes.data_as(POINTER(c_float))  # noqa: E731
+    ip = lambda a: a.ctypes.data_as(POINTER(c_int32))  # noqa: E731
+    rng = np.random.default_rng(1)
+    R = s.n_tok
+    bv, bb = W.BLOCK[s.emb_type]
+    rb = (s.hidden // bv) * bb
+    table = path.table_host
+    ids = rng.integers(0, s.vocab, R).astype(np.int32)
+    emb = np.empty((R, s.hidden), np.float32)
+    x = rng.standard_normal((R, s.hidden), dtype=np.float32)
+    w = (np.float32(1) + rng.standard_normal(s.hidden, dtype=np.float32) * np.float32(0.1))
+    h = np.empty_like(x)
+    q0 = rng.standard_normal((R, s.hq, s.head_dim), dtype=np.float32)
+    k0 = rng.standard_normal((R, s.hk, s.head_dim), dtype=np.float32)
+    half = s.n_rot // 2
+    pos = path.pos_host.astype(np.int32)
+    # a dense 0..max_pos table, as the reference's attention layer builds it
+    # (src/attention_layer.cpp:127-135), read by position in apply_rope
+    allpos = np.arange(int(pos.max()) + 1, dtype=np.int32)
+    n_tab = allpos.size
+    cos = np.empty((n_tab, half), np.float32)
+    sin = np.empty((n_tab, half), np.float32)
+    qpos = np.repeat(pos, s.hq).astype(np.int32)
+    kpos = np.repeat(pos, s.hk).astype(np.int32)
+    g0 = rng.standard_normal((R, s.ffn), dtype=np.float32)
+    up = rng.standard_normal((R, s.ffn), dtype=np.float32)
+    tbase = table.ctypes.data
+
+    def embed():
+        for i in range(R):
+            src = ctypes.cast(tbase + int(ids[i]) * rb, POINTER(c_uint8))
+            dst = ctypes.cast(emb.ctypes.data + i * s.hidden * 4, POINTER(c_float))
+            if use_ref:
+                K.aero_dequant_ref(s.emb_type, src, rb, dst, s.hidden)
+            else:
+                C.cr_dequant(s.emb_type, src, rb, dst, s.hidden)
+
+    def norm():
+        if use_ref:
+            T.aero_rmsnorm_rows(fp(x), fp(w), fp(h), R, s.hidden, s.eps)
+        else:
+            C.cr_rmsnorm_rows(fp(x), fp(w), fp(h), R, s.hidden, s.eps, 0)
+
+    def rope(q, k):
+        # the table is rebuilt per call, as the reference's attention layer does
+        if use_ref:
+            T.aero_rope_tables(s.n_rot, ip(allpos), n_tab, s.theta, s.n_rot, None, 0, fp(cos),
+                               fp(sin))
+            T.aero_apply_rope(fp(q), R * s.hq, s.head_dim, s.n_rot, fp(cos), fp(sin), ip(qpos), 0)
+            T.aero_apply_rope(fp(k), R * s.hk, s.head_dim, s.n_rot, fp(cos), fp(sin), ip(kpos), 0)
+        else:
+            C.cr_rope_tables(s.n_rot, ip(allpos), n_tab, s.theta, s.n_rot, None, 0, fp(cos),
+                             fp(sin))
+            C.cr_apply_rope(fp(q), R * s.hq, s.head_dim, s.n_rot, fp(cos), fp(sin), ip(qpos), 0)
+            C.cr_apply_rope(fp(k), R * s.hk, s.head_dim, s.n_rot, fp(cos), fp(sin), ip(kpos), 0)
+
+    def swiglu(g):
+        if use_ref:
+            T.aero_swiglu(fp(g), fp(up), g.size)
+        else:
+            C.cr_act_mul(0, fp(g), fp(up), fp(g), g.size)
+
+    times = {op: [] for op in OPS}
+    t_end = time.perf_counter() + seconds
+    reps = 0
+    while reps < 3 or time.perf_counter() < t_end:
+        q, k, g = q0.copy(), k0.copy(), g0.copy()   # fresh inputs, outside the timing
+        for op, fn in (("embed_gather", embed), ("rmsnorm", norm),
+                       ("rope_qk", lambda: rope(q, k)), ("swiglu", lambda: swiglu(g))):
+            t0 = time.perf_counter_ns()
+            fn()
+            times[op].append((time.perf_counter_ns() - t0) * 1e-6)
+        reps += 1
+    med = {op: statistics.median(v) for op, v in times.items()}
+    return med, reps, ("reference" if use_ref else "port")
+
+
+# ---------------------------------------------------------------- reports
+def traffic_from_profiles(kernel_tag):
+    """HBM bytes per launch of the dominant kernel from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "swiglu_llama3_8b_prefill_counters.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def main(argv=None):
+    a = parse_args(argv)
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
+              "(every op is row-independent: see DESIGN.md for how it shards).",
+              file=sys.stderr)
+        return 2
+    from aero_amd import _lib, workloads as W
+
+    if not _lib.available():
+        print(f"HIP path unavailable: {_lib.unavailable_reason()}", file=sys.stderr)
+        return 1
+    if a.copy_calibration:
+        return copy_calibration(a)
+    if a.all_shapes:
+        return all_shapes(a)
+
+    name = a.shape or W.HEADLINE
+    path = Path(name, a.sets)
+    if a.only:
+        wall, ker = timed_steps(path, a.steps, a.warmup, True, a.only)
+        b = path.bytes()[a.only]
+        mean = statistics.mean(ker[a.only])
+        print(json.dumps({"op": a.only, "shape": name, "kernel_us": round(mean * 1e3, 3),
+                          "GB/s": round(b / (mean * 1e-3) / 1e9, 1), "bytes": b}))
+        return 0
+    wall, ker = timed_steps(path, a.steps, a.warmup, True)
+    bts = path.bytes()
+    rows = path.rows()
+    total = sum(bts[op] for op in path.step_ops())
+    value = total / (wall * 1e-3) / 1e9
+    per_op = {}
+    for op in path.step_ops():
+        m = statistics.mean(ker[op])
+        per_op[op] = {"kernel_us": round(m * 1e3, 3), "kernel_us_median": round(
+            statistics.median(ker[op]) * 1e3, 3), "bytes": bts[op],
+            "GB/s": round(bts[op] / (m * 1e-3) / 1e9, 1),
+            "frac": round(bts[op] / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "rows_per_s": round(rows[op] / (m * 1e-3), 1)}
+    dom = "swiglu"
+    ach = per_op[dom]["GB/s"]
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(wall, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{name}: Q4_K embedding gather + RMSNorm + NeoX RoPE (q, k) "
+                               f"+ SwiGLU, one layer's elementwise path",
+                   "tokens": path.s.n_tok, "hidden": path.s.hidden, "heads": [path.s.hq,
+                                                                              path.s.hk],
+                   "head_dim": path.s.head_dim, "ffn": path.s.ffn, "buffer_sets": a.sets},
+        "rows_per_s": round(path.s.n_tok / (wall * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
+                     "kernel": "act_vec_kernel<silu> (SwiGLU 512x14336)",
+                     "bytes_per_launch": bts[dom]},
+        "ops": per_op,
+    }
+    if not a.no_cpu:
+        med, reps, kind = cpu_baseline(path, a.cpu_seconds)
+        cpu_ms = sum(med.values())
+        out["cpu_baseline"] = {
+            "value": round(total / (cpu_ms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": kind, "rows_per_s": round(path.s.n_tok / (cpu_ms * 1e-3), 1),
+            "ms_per_step": round(cpu_ms, 3),
+            "ops_ms": {k: round(v, 3) for k, v in med.items()},
+            "sample": f"the full step ({path.s.n_tok} tokens) repeated {reps} times "
+                      f"(~{a.cpu_seconds:.0f} s), median per op, single thread, "
+                      f"os.cpu_count()={os.cpu_count()}"}
+        out["speedup_vs_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out))
+    return 0
+
+
+def all_shapes(a):
+    """Per-op kernel time, GB/s and fraction of peak for every layer shape."""
+    from aero_amd import workloads as W
+
+    res = {}
+    for name in W.SHAPES:
+        sets = a.sets if W.SHAPES[name].n_tok <= 4096 else 2
+        path = Path(name, sets)
+        wall, ker = timed_steps(path, max(20, a.steps // 4), 5, True)
+        bts, rows = path.bytes(), path.rows()
+        res[name] = {}
+        for op in path.step_ops():
+            m = statistics.mean(ker[op])
+            res[name][op] = {"kernel_us": round(m * 1e3, 3), "bytes": bts[op],
+                             "GB/s": round(bts[op] / (m * 1e-3) / 1e9, 1),
+                             "frac": round(bts[op] / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "rows_per_s": round(rows[op] / (m * 1e-3), 1)}
+        print(json.dumps({"shape": name, "ops": res[name]}), flush=True)
+        del path
+    return 0
+
+
+def copy_calibration(a):
+    """A plain fp32 copy of 256 MiB, for scaling FETCH_SIZE / WRITE_SIZE."""
+    from aero_amd import ops
+    from aero_amd.device import DeviceArray as DA, Event, synchronize, time_next_kernel
+
+    n = 64 * 1024 * 1024
+    bufs = [(DA.empty(n), DA.empty(n)) for _ in range(4)]
+    ts = []
+    for i in range(a.warmup + a.steps):
+        src, dst = bufs[i % 4]
+        e0, e1 = Event(), Event()
+        time_next_kernel(e0, e1)
+        ops.copy_f32(src, dst)
+        if i >= a.warmup:
+            ts.append((e0, e1))
+    synchronize()
+    m = statistics.mean(x.elapsed_ms(y) for x, y in ts)
+    print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n,
+                      "kernel_us": round(m * 1e3, 2),
+                      "GB/s": round(8 * n / (m * 1e-3) / 1e9, 1)}))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
