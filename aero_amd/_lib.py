@@ -86,6 +86,12 @@ PROTOTYPES = {
     "aero_hip_event_synchronize": (c_int, [vp]),
     "aero_hip_event_elapsed_ms": (c_float, [vp, vp]),
     "aero_hip_time_next_kernel": (c_int, [vp, vp]),
+    "aero_hip_plan_create": (vp, []),
+    "aero_hip_plan_begin": (c_int, [vp]),
+    "aero_hip_plan_end": (c_int, [vp]),
+    "aero_hip_plan_size": (c_int64, [vp]),
+    "aero_hip_plan_launch": (c_int, [vp, vp, POINTER(vp), POINTER(vp)]),
+    "aero_hip_plan_destroy": (c_int, [vp]),
 }
 
 _lib = None
@@ -131,11 +137,18 @@ def available() -> bool:
     return unavailable_reason() == ""
 
 
+_ready = None
+
+
 def lib(exc: type = AeroHipUnavailable):
     """The loaded library with a usable GPU, or raise `exc`."""
+    global _ready
+    if _ready is not None:
+        return _ready
     L = load()
     if L is None or L.aero_hip_device_count() <= 0:
         raise exc(unavailable_reason())
+    _ready = L
     return L
 
 

@@ -8,6 +8,8 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <functional>
+#include <vector>
 
 namespace aero {
 
@@ -25,12 +27,40 @@ struct TimingSlot {
 };
 TimingSlot& timing_slot();
 
-// Launch `kernel` on `stream`. When per-kernel timing is armed the launch
-// goes through hipExtLaunchKernelGGL so the events carry the kernel's own
-// begin/end timestamps. Returns false (with the error set) on failure.
+// ------------------------------------------------------------------ plans
+// A plan is a recorded list of launches replayed by aero_hip_plan_launch.
+// While a plan records on this thread, launch() appends a closure holding the
+// kernel, its launch shape and its arguments by value instead of launching,
+// so the host-side checks and kernel choice of every op run once, at record
+// time, and a replay is a tight loop of hipLaunchKernel calls.
+struct PlanEntry {
+    const char* name;
+    std::function<void(hipStream_t, hipEvent_t, hipEvent_t)> run;
+};
+struct Plan {
+    std::vector<PlanEntry> entries;
+};
+Plan*& recording_plan();
+
+// Launch `kernel` on `stream` (or record it into the plan this thread is
+// recording). When per-kernel timing is armed the launch goes through
+// hipExtLaunchKernelGGL so the events carry the kernel's own begin/end
+// timestamps. Returns false (with the error set) on failure.
 template <typename... KArgs, typename... Args>
 bool launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block,
             uint32_t shmem, hipStream_t stream, Args... args) {
+    if (Plan* plan = recording_plan()) {
+        plan->entries.push_back(
+            {name, [=](hipStream_t s, hipEvent_t a, hipEvent_t b) {
+                 if (a != nullptr)
+                     hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, a, b, 0,
+                                           static_cast<KArgs>(args)...);
+                 else
+                     hipLaunchKernelGGL(kernel, grid, block, shmem, s,
+                                        static_cast<KArgs>(args)...);
+             }});
+        return true;
+    }
     TimingSlot& ts = timing_slot();
     if (ts.start != nullptr) {
         hipEvent_t a = ts.start, b = ts.stop;
@@ -44,8 +74,33 @@ bool launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block,
     return hip_ok(hipGetLastError(), name);
 }
 
+// Device-to-device copy that is recorded like a launch while a plan records.
+bool async_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
+
+// ------------------------------------------------------------------ tuning
+// Launch-shape knobs (block sizes, lanes per row, rows per lane). Defaults
+// are the measured best; AERO_HIP_TUNE="key=value,..." overrides them for
+// sweeps. Read once per process.
+int tune(const char* key, int dflt);
+
 inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ------------------------------------------------- streaming loads/stores
+// Data read once or written once (activations) moves with the nontemporal
+// hint, so it streams through the caches without evicting what is reused
+// (weights, tables, the cos/sin of a token). Measured on MI355X: +10-15%
+// HBM throughput for the streaming kernels at 88-400 MB per launch.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld_stream(const float* p) {
+    const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream(float* p, float4 v) {
+    const v4f t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<v4f*>(p));
 }
 
 // ------------------------------------------------------- device helpers

@@ -4,7 +4,8 @@
 // One kernel template covers all of them. A row (or a `group`-long slice of
 // a row) is owned by TPR consecutive lanes; each lane keeps V float4 of the
 // row in VGPRs, so x (and z) are read from HBM exactly once with 128-bit
-// coalesced loads. The sum of squares is reduced with a wave64 xor butterfly
+// coalesced loads (nontemporal: each element is used once). The sum of
+// squares is reduced with a wave64 xor butterfly
 // and, when a row spans several waves, one LDS step. The output is written
 // once with 128-bit stores. HBM bytes per row: 4*(2*cols) (+4*cols for z);
 // the weight vector is re-read from L2, not HBM.
@@ -63,8 +64,8 @@ void norm_vec_kernel(NormParams p) {
     const bool ok = row < p.rows;
     const int nv = p.cols >> 2;
     const int64_t base = ok ? row * (int64_t)p.cols : 0;
-    const float4* xr = reinterpret_cast<const float4*>(p.x + base);
-    const float4* zr = reinterpret_cast<const float4*>(GATED ? p.z + base : p.x);
+    const float* xr = p.x + base;
+    const float* zr = GATED ? p.z + base : p.x;
 
     float4 xv[V];
     float4 zv[V];
@@ -72,8 +73,8 @@ void norm_vec_kernel(NormParams p) {
     for (int i = 0; i < V; ++i) {
         const int c = i * TPR + t;
         if (ok && c < nv) {
-            xv[i] = xr[c];
-            if (GATED) zv[i] = zr[c];
+            xv[i] = ld_stream(xr + 4 * c);
+            if (GATED) zv[i] = ld_stream(zr + 4 * c);
         } else {
             xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (GATED) zv[i] = xv[i];
@@ -102,7 +103,7 @@ void norm_vec_kernel(NormParams p) {
     }
     if (!ok) return;
 
-    float4* orow = reinterpret_cast<float4*>(p.out + base);
+    float* orow = p.out + base;
     if constexpr (GATED) {
         const float denom = sqrtf(ss / (float)p.cols + p.eps);
         const int col0 = (int)(row % p.gpr) * p.cols;
@@ -117,7 +118,7 @@ void norm_vec_kernel(NormParams p) {
             o.y = ((xv[i].y / denom) * wv.y) * silu_div(zv[i].y);
             o.z = ((xv[i].z / denom) * wv.z) * silu_div(zv[i].z);
             o.w = ((xv[i].w / denom) * wv.w) * silu_div(zv[i].w);
-            orow[c] = o;
+            st_stream(orow + 4 * c, o);
         }
     } else {
         const float inv = norm_scale(ss, p);
@@ -135,7 +136,7 @@ void norm_vec_kernel(NormParams p) {
                 }
                 o.x = o.x * wv.x; o.y = o.y * wv.y; o.z = o.z * wv.z; o.w = o.w * wv.w;
             }
-            orow[c] = o;
+            st_stream(orow + 4 * c, o);
         }
     }
 }
@@ -207,8 +208,9 @@ NormKernel pick(int tpr, int v) {
 // at <= 4 float4, so a lane has four 128-bit loads (eight when gated) in
 // flight; V then covers the rest (<= 8).
 void choose_shape(int nv, int* tpr, int* v) {
+    const int vmax = tune("norm_vmax", 4);
     int t = 8;
-    while (t < 1024 && t * 4 < nv) t *= 2;
+    while (t < 1024 && t * vmax < nv) t *= 2;
     *tpr = t;
     *v = (nv + t - 1) / t;
 }

@@ -136,9 +136,9 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
     const int64_t row = gb / p.nbr;
     const int64_t b = gb % p.nbr;
     const int64_t tok = p.ids ? (int64_t)p.ids[row] : row;
-    float4* o = reinterpret_cast<float4*>(p.out + gb * Q::BV) + l;
+    float* o = p.out + gb * Q::BV + 4 * l;
     if (tok < 0 || tok >= p.vocab) {
-        *o = make_float4(0.f, 0.f, 0.f, 0.f);
+        st_stream(o, make_float4(0.f, 0.f, 0.f, 0.f));
         if (p.bad != nullptr && b == 0 && l == 0) atomicAdd(p.bad, 1u);
         return;
     }
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
     if (p.scale > 0.0f) {
         v.x = v.x * p.scale; v.y = v.y * p.scale; v.z = v.z * p.scale; v.w = v.w * p.scale;
     }
-    *o = v;
+    st_stream(o, v);
 }
 
 // F16 / BF16 element-wise decode for whole-buffer dequant.
@@ -239,10 +239,7 @@ bool dequant_dev(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
         return false;
     }
     if (nblocks == 0) return true;
-    if (dtype == AERO_DTYPE_F32)
-        return hip_ok(hipMemcpyAsync(out, raw, (size_t)(nblocks * 4),
-                                     hipMemcpyDeviceToDevice, s),
-                      "dequant F32 copy");
+    if (dtype == AERO_DTYPE_F32) return async_copy(out, raw, (size_t)(nblocks * 4), s);
     if (dtype == AERO_DTYPE_F16 || dtype == AERO_DTYPE_BF16) {
         if (reinterpret_cast<uintptr_t>(raw) & 1u) {
             set_error("dequant: fp16 input must be 2-byte aligned");

@@ -60,9 +60,6 @@ constexpr int kRopeBlock = 256;
 __device__ __forceinline__ float4 ld4(const float* p) {
     return *reinterpret_cast<const float4*>(p);
 }
-__device__ __forceinline__ void st4(float* p, float4 v) {
-    *reinterpret_cast<float4*>(p) = v;
-}
 
 __device__ __forceinline__ float4 wmul(float4 v, float inv, const float* w, int flags) {
     float4 o = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
@@ -132,8 +129,8 @@ void rope_vec_kernel(RopeParams p) {
             dst[i] = (isq ? p.q_out : p.k_out) + roff;
             wrow[i] = isq ? p.q_w : p.k_w;
             if (valid[i]) {
-                A[i] = ld4(src + a0);
-                B[i] = ld4(src + b0);
+                A[i] = ld_stream(src + a0);
+                B[i] = ld_stream(src + b0);
             }
         }
     }
@@ -187,8 +184,8 @@ void rope_vec_kernel(RopeParams p) {
                 rot2(B[i].z, B[i].w, c4.w, s4.w);
             }
         }
-        st4(dst[i] + a0, A[i]);
-        st4(dst[i] + b0, B[i]);
+        st_stream(dst[i] + a0, A[i]);
+        st_stream(dst[i] + b0, B[i]);
     }
 }
 
@@ -308,11 +305,14 @@ bool qk_norm_rope(RopeParams p, hipStream_t stream) {
     if (vec) {
         const int S = kRopeBlock / L;
         const int need = (NH + S - 1) / S;
-        int rps = need < 8 ? need : 8;
+        const int rps_max = tune("rope_rps_max", 8);
+        const int64_t min_wg = tune("rope_min_wg", 1024);
+        int rps = need < rps_max ? need : rps_max;
+        if (rps < 1) rps = 1;
         int n_hg = 1;
         for (;; --rps) {
             n_hg = (NH + S * rps - 1) / (S * rps);
-            if (rps == 1 || p.n_tok * n_hg >= 1024) break;
+            if (rps == 1 || p.n_tok * n_hg >= min_wg) break;
         }
         p.n_hg = n_hg;
         p.hpw = (NH + n_hg - 1) / n_hg;

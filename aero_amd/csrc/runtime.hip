@@ -5,14 +5,58 @@
 #include "aero_hip.h"
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstring>
+#include <map>
+#include <new>
+#include <mutex>
+#include <string>
 
 namespace aero {
 
 namespace {
 thread_local char g_err[512] = {0};
 thread_local TimingSlot g_timing;
+thread_local Plan* g_recording = nullptr;
 }  // namespace
+
+Plan*& recording_plan() { return g_recording; }
+
+bool async_copy(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (Plan* plan = recording_plan()) {
+        plan->entries.push_back({"copy", [=](hipStream_t s, hipEvent_t a, hipEvent_t b) {
+                                     if (a != nullptr) (void)hipEventRecord(a, s);
+                                     (void)hipMemcpyAsync(dst, src, bytes,
+                                                          hipMemcpyDeviceToDevice, s);
+                                     if (b != nullptr) (void)hipEventRecord(b, s);
+                                 }});
+        return true;
+    }
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream),
+                  "hipMemcpyAsync D2D");
+}
+
+int tune(const char* key, int dflt) {
+    static std::once_flag once;
+    static std::map<std::string, int> knobs;
+    std::call_once(once, [] {
+        const char* env = std::getenv("AERO_HIP_TUNE");
+        if (env == nullptr) return;
+        std::string all(env);
+        size_t i = 0;
+        while (i < all.size()) {
+            size_t j = all.find(',', i);
+            if (j == std::string::npos) j = all.size();
+            const std::string kv = all.substr(i, j - i);
+            const size_t eq = kv.find('=');
+            if (eq != std::string::npos)
+                knobs[kv.substr(0, eq)] = std::atoi(kv.c_str() + eq + 1);
+            i = j + 1;
+        }
+    });
+    auto it = knobs.find(key);
+    return it == knobs.end() ? dflt : it->second;
+}
 
 void set_error(const char* fmt, ...) {
     va_list ap;
@@ -171,6 +215,51 @@ float aero_hip_event_elapsed_ms(void* start, void* stop) {
                 "hipEventElapsedTime"))
         return -1.0f;
     return ms;
+}
+
+void* aero_hip_plan_create(void) { return new (std::nothrow) aero::Plan(); }
+
+int aero_hip_plan_destroy(void* plan) {
+    if (plan == nullptr) return 1;
+    if (aero::recording_plan() == plan) aero::recording_plan() = nullptr;
+    delete static_cast<aero::Plan*>(plan);
+    return 1;
+}
+
+int aero_hip_plan_begin(void* plan) {
+    if (plan == nullptr || aero::recording_plan() != nullptr) {
+        set_error("plan_begin: null plan or a plan is already recording on this thread");
+        return 0;
+    }
+    aero::recording_plan() = static_cast<aero::Plan*>(plan);
+    return 1;
+}
+
+int aero_hip_plan_end(void* plan) {
+    if (plan == nullptr || aero::recording_plan() != plan) {
+        set_error("plan_end: this plan is not recording on this thread");
+        return 0;
+    }
+    aero::recording_plan() = nullptr;
+    return 1;
+}
+
+int64_t aero_hip_plan_size(void* plan) {
+    return plan == nullptr ? 0 : (int64_t)static_cast<aero::Plan*>(plan)->entries.size();
+}
+
+int aero_hip_plan_launch(void* plan, void* stream, void** starts, void** stops) {
+    if (plan == nullptr || aero::recording_plan() != nullptr) {
+        set_error("plan_launch: null plan, or called while a plan records");
+        return 0;
+    }
+    auto& entries = static_cast<aero::Plan*>(plan)->entries;
+    for (size_t i = 0; i < entries.size(); ++i) {
+        hipEvent_t a = starts ? (hipEvent_t)starts[i] : nullptr;
+        hipEvent_t b = stops ? (hipEvent_t)stops[i] : nullptr;
+        entries[i].run((hipStream_t)stream, a, b);
+    }
+    return hip_ok(hipGetLastError(), "plan_launch") ? 1 : 0;
 }
 
 int aero_hip_time_next_kernel(void* start, void* stop) {

@@ -155,6 +155,62 @@ class Event:
             pass
 
 
+class Plan:
+    """A recorded sequence of aero_hip_* device ops, replayed with one call.
+
+        plan = Plan()
+        with plan:                       # ops are checked and recorded, not run
+            ops.rmsnorm(x, w, h, R, N, eps)
+            ops.act_mul("silu", g, u, o)
+        plan.launch(stream)              # issues the recorded kernels in order
+
+    The buffers an op was recorded with must outlive the plan; the plan keeps
+    Python references to nothing, so the caller holds them.
+    """
+
+    def __init__(self):
+        self.handle = _lib.lib().aero_hip_plan_create()
+        if not self.handle:
+            raise MemoryError("plan create failed")
+
+    def __enter__(self):
+        _lib.check(_lib.lib().aero_hip_plan_begin(self.handle), "plan_begin")
+        return self
+
+    def __exit__(self, *exc):
+        _lib.check(_lib.lib().aero_hip_plan_end(self.handle), "plan_end")
+        return False
+
+    def __len__(self) -> int:
+        return int(_lib.lib().aero_hip_plan_size(self.handle))
+
+    def event_arrays(self, starts, stops):
+        """ctypes arrays of event handles for launch(), one pair per kernel."""
+        n = len(self)
+        if len(starts) != n or len(stops) != n:
+            raise ValueError(f"need {n} start and stop events")
+        arr = ctypes.c_void_p * n
+        return arr(*[e.handle for e in starts]), arr(*[e.handle for e in stops])
+
+    def launch(self, stream: "Stream | None" = None, events=None) -> None:
+        a, b = (None, None) if events is None else events
+        _lib.check(_lib.lib().aero_hip_plan_launch(self.handle, stream.handle if stream else None,
+                                                   a, b), "plan_launch")
+
+    def destroy(self) -> None:
+        if self.handle:
+            L = _lib.load()
+            if L is not None:
+                L.aero_hip_plan_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
 def time_next_kernel(start: Event, stop: Event) -> None:
     """The next kernel launched by an aero_hip_* op on this thread records its
     own device begin/end timestamps into start/stop."""

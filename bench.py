@@ -8,11 +8,14 @@ positions 0..511, and SwiGLU on gate/up (512 x 14336). Inputs are synthetic
 buffer sets (> 1 GiB together) so no launch reads data the 256 MiB Infinity
 Cache still holds from the previous use of its set.
 
-`value` is the whole step's algorithmic HBM bytes / wall time per step
-(GB/s). `roofline` is the dominant kernel (SwiGLU, 88 MB per launch): its
-algorithmic bytes / its mean device duration, measured with HIP events
-recorded by the kernel's own dispatch (hipExtLaunchKernel) during the timed
-steps. `cpu_baseline` is the same step on the host: the reference's own C++
+A step replays a recorded plan (aero_hip_plan_launch: the four kernels
+issued from C, one host call per step). `value` is the whole step's
+algorithmic HBM bytes / wall time per step over the timed region (GB/s).
+`roofline` is the dominant kernel (SwiGLU, 88 MB per launch): its algorithmic
+bytes / its mean device duration, measured with HIP events recorded by the
+kernel's own dispatch (hipExtLaunchKernel) over a second region of the same
+run that replays the same plans with an event pair per kernel (events per
+kernel serialise the host side, so that region times kernels, not steps). `cpu_baseline` is the same step on the host: the reference's own C++
 (built into oracle/_ref) when present, else the oracle's restatement,
 single-threaded like the reference, over a bounded sample.
 
@@ -51,6 +54,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--all-shapes", action="store_true")
+    p.add_argument("--shapes", default=None, help="comma list for --all-shapes")
     p.add_argument("--only", choices=OPS + ("rope_qk_norm", "gated_norm"), default=None)
     p.add_argument("--copy-calibration", action="store_true")
     return p.parse_args(argv)
@@ -170,30 +174,89 @@ class Path:
         return list(OPS) + (["gated_norm"] if self.s.gated else [])
 
 
-def timed_steps(path, steps, warmup, per_kernel=True, only=None):
-    """Run warmup + steps; returns (ms per step, {op: [kernel ms ...]})."""
-    from aero_amd.device import Event, Stream, synchronize, time_next_kernel
+def build_plans(path, only=None):
+    """One recorded plan per buffer set: the step's ops in order."""
+    from aero_amd.device import Plan
+
+    ops_list = [only] if only else path.step_ops()
+    plans = []
+    for i in range(len(path.sets)):
+        p = Plan()
+        with p:
+            for op in ops_list:
+                path.run(op, i)
+        plans.append(p)
+    return plans, ops_list
+
+
+def kernel_kinds(path, ops_list):
+    """Op name of each kernel a step records (an op may record two)."""
+    from aero_amd.device import Plan
+
+    kinds = []
+    for op in ops_list:
+        probe = Plan()
+        with probe:
+            path.run(op, 0)
+        kinds += [op] * len(probe)
+        probe.destroy()
+    return kinds
+
+
+def timed_steps(path, steps, warmup, only=None):
+    """The timed region: `warmup` untimed step replays, then exactly `steps`
+    replays (one plan launch, one C call each) bracketed by a stream
+    synchronize on both sides. Returns wall ms per step."""
+    from aero_amd.device import Stream
 
     stream = Stream()
-    ops_list = [only] if only else path.step_ops()
+    plans, _ = build_plans(path, only)
     for i in range(warmup):
-        for op in ops_list:
-            path.run(op, i, stream)
+        plans[i % len(plans)].launch(stream)
     stream.synchronize()
-    evs = {op: [(Event(), Event()) for _ in range(steps)] for op in ops_list} if per_kernel else {}
     t0 = time.perf_counter()
     for i in range(steps):
-        for op in ops_list:
-            if per_kernel:
-                a, b = evs[op][i]
-                time_next_kernel(a, b)
-            path.run(op, warmup + i, stream)
+        plans[(warmup + i) % len(plans)].launch(stream)
     stream.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    synchronize()
-    ker = {op: [a.elapsed_ms(b) for a, b in evs[op]] for op in evs}
     stream.destroy()
-    return wall, ker
+    for p in plans:
+        p.destroy()
+    return wall
+
+
+def kernel_times(path, steps, warmup, only=None):
+    """The kernel-timing region: the same replays with every kernel recording
+    its own device begin/end (hipExtLaunchKernel events on the stream it runs
+    on). Recording events per kernel serialises the host side, so this region
+    gives kernel durations, not step throughput. Returns {op: [ms per step]}."""
+    from aero_amd.device import Event, Stream, synchronize
+
+    stream = Stream()
+    plans, ops_list = build_plans(path, only)
+    kinds = kernel_kinds(path, ops_list)
+    n_k = len(plans[0])
+    assert len(kinds) == n_k
+    for i in range(warmup):
+        plans[i % len(plans)].launch(stream)
+    stream.synchronize()
+    evs = [([Event() for _ in range(n_k)], [Event() for _ in range(n_k)]) for _ in range(steps)]
+    arrs = [plans[0].event_arrays(a, b) for a, b in evs]
+    for i in range(steps):
+        plans[(warmup + i) % len(plans)].launch(stream, arrs[i])
+    stream.synchronize()
+    synchronize()
+    ker = {op: [] for op in ops_list}
+    for a, b in evs:
+        per = {}
+        for k in range(n_k):
+            per[kinds[k]] = per.get(kinds[k], 0.0) + a[k].elapsed_ms(b[k])
+        for op, ms in per.items():
+            ker[op].append(ms)
+    stream.destroy()
+    for p in plans:
+        p.destroy()
+    return ker
 
 
 # ---------------------------------------------------------------- CPU side
@@ -318,13 +381,14 @@ def main(argv=None):
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
     if a.only:
-        wall, ker = timed_steps(path, a.steps, a.warmup, True, a.only)
+        ker = kernel_times(path, a.steps, a.warmup, a.only)
         b = path.bytes()[a.only]
         mean = statistics.mean(ker[a.only])
         print(json.dumps({"op": a.only, "shape": name, "kernel_us": round(mean * 1e3, 3),
                           "GB/s": round(b / (mean * 1e-3) / 1e9, 1), "bytes": b}))
         return 0
-    wall, ker = timed_steps(path, a.steps, a.warmup, True)
+    wall = timed_steps(path, a.steps, a.warmup)
+    ker = kernel_times(path, a.steps, a.warmup)
     bts = path.bytes()
     rows = path.rows()
     total = sum(bts[op] for op in path.step_ops())
@@ -377,10 +441,11 @@ def all_shapes(a):
     from aero_amd import workloads as W
 
     res = {}
-    for name in W.SHAPES:
+    names = a.shapes.split(",") if a.shapes else list(W.SHAPES)
+    for name in names:
         sets = a.sets if W.SHAPES[name].n_tok <= 4096 else 2
         path = Path(name, sets)
-        wall, ker = timed_steps(path, max(20, a.steps // 4), 5, True)
+        ker = kernel_times(path, max(20, a.steps // 4), 5)
         bts, rows = path.bytes(), path.rows()
         res[name] = {}
         for op in path.step_ops():

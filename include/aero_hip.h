@@ -230,6 +230,21 @@ int   aero_hip_event_record(void* ev, void* stream);
 int   aero_hip_event_synchronize(void* ev);
 /* Milliseconds between two recorded events; negative on error. */
 float aero_hip_event_elapsed_ms(void* start, void* stop);
+/* Plans: record a sequence of aero_hip_* device ops once, replay it many
+ * times. Between plan_begin and plan_end on one thread, every aero_hip_*
+ * device op is checked and resolved to its kernel and launch shape as usual
+ * but recorded (with its pointer and size arguments) instead of launched;
+ * plan_launch then issues the recorded kernels in order on `stream` with no
+ * per-op host work. starts / stops (nullable) are arrays of plan_size()
+ * events: entry i then records the device begin/end of its own kernel.
+ * The recorded buffers must stay allocated while the plan is used. */
+void*   aero_hip_plan_create(void);
+int     aero_hip_plan_begin(void* plan);
+int     aero_hip_plan_end(void* plan);
+int64_t aero_hip_plan_size(void* plan);
+int     aero_hip_plan_launch(void* plan, void* stream, void** starts, void** stops);
+int     aero_hip_plan_destroy(void* plan);
+
 /* Arm per-kernel timing: the next kernel this thread launches through any
  * aero_hip_* op records `start` when it begins and `stop` when it ends on the
  * device (hipExtLaunchKernel), then the arming is cleared. */

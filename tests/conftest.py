@@ -21,6 +21,14 @@ def golden(name: str):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path)")
+    # A fresh checkout has no built libraries: build what is missing (the GPU
+    # box receives them prebuilt and never compiles here).
+    import subprocess
+    if not os.path.exists(os.path.join(ROOT, "oracle", "libaero_cpuref.so")):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    if not os.path.exists(os.path.join(ROOT, "aero_amd", "libaero_hip.so")):
+        from aero_amd import build
+        build.build()
 
 
 def rel_to_scale(got, ref) -> float:

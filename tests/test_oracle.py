@@ -1,0 +1,344 @@
+"""CPU: pin the oracle (oracle/cpuref*.c) before trusting it as the checker.
+
+Every function is checked against at least one of: the reference's own C++
+outputs (golden vectors from oracle/_ref, committed, and the live build when
+present), the known-answer blocks of the reference's tests, float64 closed
+forms, and the invariants the reference's tests assert. The last section
+plants plausible mistakes in a numpy restatement and shows the same checks
+reject them, so a check that passes is a check that could have failed.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import bits_equal, golden, rel_to_scale
+from oracle import cpuref as O
+from oracle import refbind as R
+
+ref_built = pytest.mark.skipif(not R.available(), reason="oracle/_ref not built here")
+
+
+# ---------------------------------------------------------------- fp16 / quant
+def test_f16_exhaustive():
+    h = np.arange(65536, dtype=np.uint16)
+    assert np.array_equal(O.f16_bits_to_f32(h).view(np.uint32),
+                          h.view(np.float16).astype(np.float32).view(np.uint32))
+
+
+KATS = [("q4k_nibbles", O.Q4_K), ("q4k_pack_dmin0", O.Q4_K), ("q4k_pack_dmin1", O.Q4_K),
+        ("q6k_zero", O.Q6_K), ("q6k_ones", O.Q6_K), ("q6k_lownib", O.Q6_K),
+        ("q8_0_ramp", O.Q8_0)]
+
+
+@pytest.mark.parametrize("name,t", KATS)
+def test_quant_kat(name, t):
+    k = golden("kat_quant.npz")
+    want = k[name + "_want"]
+    assert bits_equal(O.dequant(t, k[name + "_raw"], want.size), want)
+
+
+def test_q4k_dmin_with_zero_mins_is_noop():
+    k = golden("kat_quant.npz")
+    assert bits_equal(O.dequant(O.Q4_K, k["q4k_nibbles_dmin2_raw"], 256), k["q4k_nibbles_want"])
+
+
+def test_block_geometry():
+    for t, bb, bv in ((O.Q8_0, 34, 32), (O.Q4_K, 144, 256), (O.Q6_K, 210, 256), (O.F16, 2, 1),
+                      (O.F32, 4, 1), (O.BF16, 2, 1)):
+        assert O.block_bytes(t) == bb and O.block_values(t) == bv
+
+
+def test_dequant_refusals():
+    with pytest.raises(ValueError):
+        O.dequant(O.Q4_K, np.zeros(143, np.uint8), 256)      # short buffer
+    with pytest.raises(ValueError):
+        O.dequant(O.Q5_K, np.zeros(176, np.uint8), 256)      # not a path type
+    assert O.dequant(O.Q8_0, np.zeros(34, np.uint8), 31).sum() == 0  # floor(n/bv) = 0 blocks
+
+
+def test_threaded_dequant_bit_identical():
+    rng = np.random.default_rng(3)
+    from aero_amd import workloads as W
+    for t in (O.Q8_0, O.Q4_K, O.Q6_K):
+        raw = W.make_table(t, 333, rng)
+        n = 333 * O.block_values(t)
+        a = O.dequant(t, raw, n)
+        for th in (2, 3, 8, 16):
+            assert bits_equal(O.dequant(t, raw, n, threads=th), a)
+
+
+# ---------------------------------------------------------------- golden vectors
+def test_golden_norms_and_acts():
+    g = golden("ref_vectors.npz")
+    assert bits_equal(O.rmsnorm_rows(g["norm_x"], g["norm_w"], 1e-6), g["rms_out"])
+    assert bits_equal(O.rmsnorm_rows(g["norm_x"], None, 1e-6), g["rms_out_noweight"])
+    assert bits_equal(O.l2norm_rows(g["norm_x"], g["norm_w"], 1e-6), g["l2_out"])
+    assert bits_equal(O.rmsnorm_rows(g["rms4096_x"], g["rms4096_w"], 1e-5), g["rms4096_out"])
+    z, up = g["act_z"], g["act_up"]
+    assert bits_equal(O.act(O.ACT_SILU, z), g["silu_out"])
+    assert bits_equal(O.act(O.ACT_GELU, z), g["gelu_out"])
+    assert bits_equal(O.act_mul(O.ACT_SILU, z, up), g["swiglu_out"])
+    assert bits_equal(O.act_mul(O.ACT_IDENTITY, z, up), g["mul_out"])
+
+
+def test_golden_rope():
+    g = golden("ref_vectors.npz")
+    pos = g["rope_pos"]
+    ff = np.concatenate([np.ones(16, np.float32), np.full(16, 1e30, np.float32)])
+    for tag, hd, nd, base, f in (("full128", 128, None, 500000.0, None),
+                                 ("partial64of256", 256, 64, 1e7, None),
+                                 ("ff64", 64, None, 10000.0, ff)):
+        c, s = O.rope_tables(hd, pos, base, nd, f)
+        assert bits_equal(c, g[f"tab_{tag}_cos"]) and bits_equal(s, g[f"tab_{tag}_sin"]), tag
+    x, c, s, rp = g["apply_x"], g["apply_cos"], g["apply_sin"], g["apply_pos"]
+    assert bits_equal(O.apply_rope(x, c, s, rp, 0), g["apply_neox"])
+    assert bits_equal(O.apply_rope(x, c, s, rp, 1), g["apply_inter"])
+    assert bits_equal(O.apply_rope(x, g["apply_cos8"], g["apply_sin8"], rp, 0),
+                      g["apply_partial8"])
+
+
+def test_golden_dequant():
+    g = golden("ref_vectors.npz")
+    for t in (8, 12, 14):
+        want = g[f"deq{t}_out"]
+        assert bits_equal(O.dequant(t, g[f"deq{t}_raw"], want.size), want)
+
+
+# ------------------------------------------------------ live reference build
+@ref_built
+def test_live_reference_fp32_path():
+    rng = np.random.default_rng(99)
+    for rows, cols in ((1, 1), (3, 7), (17, 896), (5, 4096), (2, 8193)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        w = rng.standard_normal(cols).astype(np.float32)
+        assert bits_equal(O.rmsnorm_rows(x, w, 1e-5), R.rmsnorm_rows(x, w, 1e-5))
+        assert bits_equal(O.l2norm_rows(x, None, 1e-6), R.l2norm_rows(x, None, 1e-6))
+    z = (rng.standard_normal(9999) * 6).astype(np.float32)
+    u = rng.standard_normal(9999).astype(np.float32)
+    assert bits_equal(O.act(0, z), R.act("silu", z))
+    assert bits_equal(O.act(1, z), R.act("gelu", z))
+    assert bits_equal(O.act_mul(0, z, u), R.swiglu(z, u))
+    for hd, nd, base in ((128, None, 5e5), (256, 64, 1e7), (64, None, 1e6), (80, 48, 1e4)):
+        pos = rng.integers(0, 65536, 50).astype(np.int32)
+        a, b = O.rope_tables(hd, pos, base, nd), R.rope_tables(hd, pos, base, nd)
+        assert bits_equal(a[0], b[0]) and bits_equal(a[1], b[1])
+        xr = rng.standard_normal((50, hd)).astype(np.float32)
+        rows = np.arange(50, dtype=np.int32)
+        for mode in (0, 1):
+            assert bits_equal(O.apply_rope(xr, a[0], a[1], rows, mode),
+                              R.apply_rope(xr, a[0], a[1], rows, mode))
+
+
+@ref_built
+def test_live_reference_dequant():
+    from aero_amd import workloads as W
+    rng = np.random.default_rng(98)
+    for t in (O.Q8_0, O.Q4_K, O.Q6_K):
+        raw = W.make_table(t, 257, rng)
+        n = 257 * O.block_values(t)
+        assert bits_equal(O.dequant(t, raw, n), R.dequant(t, raw, n))
+    raw = rng.integers(0, 256, 2000, dtype=np.uint8)
+    for t in (O.F16, O.BF16, O.F32):
+        n = 2000 // O.block_bytes(t)
+        a, b = O.dequant(t, raw, n), R.dequant(t, raw, n)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------------- closed forms
+def test_rmsnorm_closed_form():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((9, 2560)) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(2560)).astype(np.float32)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    assert rel_to_scale(O.rmsnorm_rows(x, w, 1e-6), want) < 1e-6
+    # Gemma (1+w) is the composition with w' = 1 + w in fp32
+    assert bits_equal(O.rmsnorm_rows(x, w - 1, 1e-6, unit_offset=True),
+                      O.rmsnorm_rows(x, np.float32(1) + (w - np.float32(1)), 1e-6))
+    # weight None == ones, bit for bit; ones in -> weight out
+    assert bits_equal(O.rmsnorm_rows(x, None, 1e-6), O.rmsnorm_rows(x, np.ones(2560, np.float32), 1e-6))
+    assert np.allclose(O.rmsnorm_rows(np.ones((2, 2560), np.float32), w, 1e-6), w, rtol=1e-5)
+
+
+def test_l2norm_closed_form_and_floor():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((4, 64)).astype(np.float32)
+    x64 = x.astype(np.float64)
+    want = x64 / np.maximum(np.linalg.norm(x64, axis=1, keepdims=True), 1e-6)
+    assert rel_to_scale(O.l2norm_rows(x, None, 1e-6), want) < 1e-6
+    tiny = np.full((1, 64), 1e-9, np.float32)
+    got = np.linalg.norm(O.l2norm_rows(tiny, None, 1e-6).astype(np.float64))
+    assert abs(got - 8e-9 / 1e-6) / (8e-9 / 1e-6) < 1e-3
+
+
+def test_gated_norm_closed_form_and_invariants():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((6, 4096)).astype(np.float32)
+    z = rng.standard_normal((6, 4096)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    for group in (4096, 128):
+        xg = x64.reshape(6, -1, group)
+        nrm = xg / np.sqrt((xg ** 2).mean(axis=2, keepdims=True) + 1e-6)
+        want = nrm.reshape(6, 4096) * np.tile(w, 32) * (z64 / (1 + np.exp(-z64)))
+        assert rel_to_scale(O.gated_rmsnorm_silu(x, z, w, 1e-6, group), want) < 1e-6
+    big = np.full_like(z, 60.0)
+    out = O.gated_rmsnorm_silu(x, big, np.ones(128, np.float32), 1e-6).astype(np.float64) / 60
+    assert np.allclose(np.sqrt((out ** 2).mean(axis=1)), 1.0, atol=1e-5)
+
+
+def test_activation_closed_forms():
+    z = np.linspace(-8, 8, 4001, dtype=np.float32)
+    z64 = z.astype(np.float64)
+    gelu = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in z64])
+    tanh = 0.5 * z64 * (1 + np.tanh(math.sqrt(2 / math.pi) * (z64 + 0.044715 * z64 ** 3)))
+    assert np.abs(O.act(O.ACT_GELU, z) - gelu).max() < 2e-6
+    assert rel_to_scale(O.act(O.ACT_GELU_TANH, z), tanh) < 1e-6
+    assert rel_to_scale(O.act(O.ACT_SILU, z), z64 / (1 + np.exp(-z64))) < 1e-6
+    # the erf form is not the tanh form (tests/test_tensor_native.py:118-126)
+    assert np.abs(O.act(O.ACT_GELU, z) - tanh).max() > 1e-4
+
+
+def test_rope_closed_form():
+    pos = np.array([0, 1, 37, 511, 4095, 16383, 32767], np.int32)
+    for hd, nd, base in ((128, None, 5e5), (256, 64, 1e7)):
+        n, inv = O.rope_inv_freq(hd, nd, base)
+        inv64 = 1.0 / (np.float64(base) ** (np.arange(n // 2) * 2.0 / n))
+        assert np.abs(inv / inv64 - 1).max() < 1e-6
+        c, s = O.rope_tables(hd, pos, base, nd)
+        ang = (pos.astype(np.float32)[:, None] * inv[None, :]).astype(np.float64)  # fp32 angle
+        assert np.abs(c - np.cos(ang)).max() < 1e-6 and np.abs(s - np.sin(ang)).max() < 1e-6
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 64)).astype(np.float32)
+    c, s = O.rope_tables(64, np.arange(5), 1e4)
+    rows = np.arange(5, dtype=np.int32)
+    x64, c64, s64 = x.astype(np.float64), c.astype(np.float64), s.astype(np.float64)
+    want = x64.copy()
+    want[:, :32] = x64[:, :32] * c64 - x64[:, 32:] * s64
+    want[:, 32:] = x64[:, :32] * s64 + x64[:, 32:] * c64
+    assert rel_to_scale(O.apply_rope(x, c, s, rows, 0), want) < 1e-6
+
+
+def test_rope_properties():
+    rng = np.random.default_rng(9)
+    D = 16
+    q0, k0 = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    c, s = O.rope_tables(D, np.arange(32), 1e4)
+
+    def score(qp, kp, mode):
+        q = O.apply_rope(q0[None], c, s, np.array([qp], np.int32), mode)[0]
+        k = O.apply_rope(k0[None], c, s, np.array([kp], np.int32), mode)[0]
+        return float(np.dot(q.astype(np.float64), k))
+
+    for mode in (0, 1):
+        base = score(0, 5, mode)
+        assert max(abs(score(t, t + 5, mode) - base) for t in range(1, 21)) < 1e-4
+        assert abs(score(5, 0, mode) - base) > 1e-3   # not symmetric
+        r = O.apply_rope(q0[None], c, s, np.array([7], np.int32), mode)[0]
+        assert abs(np.linalg.norm(r) - np.linalg.norm(q0)) < 1e-5
+    c8, s8 = O.rope_tables(D, np.arange(32), 1e4, 8)
+    r = O.apply_rope(q0[None], c8, s8, np.array([5], np.int32), 0)[0]
+    assert bits_equal(r[8:], q0[8:]) and not np.allclose(r[:8], q0[:8])
+    ff = np.concatenate([np.ones(4, np.float32), np.full(4, 1e30, np.float32)])
+    cf, sf = O.rope_tables(D, np.arange(1, 6), 1e4, None, ff)
+    # tests/test_transformer_cpp.cpp:137-158: cos -> 1, sin -> 0 within 1e-5
+    assert np.abs(cf[:, 4:] - 1).max() < 1e-5 and np.abs(sf[:, 4:]).max() < 1e-5
+    with pytest.raises(ValueError):
+        O.rope_tables(D, np.arange(3), 1e4, None, np.ones(3, np.float32))
+
+
+def test_embed_gather_rows_and_refusals():
+    from aero_amd import workloads as W
+    rng = np.random.default_rng(10)
+    for t in (O.Q8_0, O.Q4_K, O.Q6_K):
+        bv, bb = W.BLOCK[t]
+        table = W.make_table(t, 40 * 2, rng)
+        ids = rng.integers(0, 40, 25).astype(np.int32)
+        got = O.embed_gather(t, table, 40, 2 * bv, ids)
+        for i, tok in enumerate(ids):
+            assert bits_equal(got[i], O.dequant(t, table[tok * 2 * bb:(tok + 1) * 2 * bb], 2 * bv))
+        scaled = O.embed_gather(t, table, 40, 2 * bv, ids, scale=float(np.float32(math.sqrt(2560))))
+        assert bits_equal(scaled, got * np.float32(math.sqrt(2560)))
+        with pytest.raises(ValueError):
+            O.embed_gather(t, table, 40, 2 * bv, np.array([40], np.int32))
+        with pytest.raises(ValueError):
+            O.embed_gather(t, table, 40, 2 * bv, np.array([-1], np.int32))
+        with pytest.raises(ValueError):
+            O.embed_gather(t, table, 40, bv + 1, ids)
+
+
+# ------------------------------------------------------------ planted mistakes
+def _f16(b):
+    return b.view(np.float16).astype(np.float32)
+
+
+def np_q4k(raw, swap_nibbles=False, naive_scales=False):
+    """numpy restatement of Q4_K with optional planted mistakes."""
+    a = raw.reshape(-1, 144)
+    d, dmin = _f16(a[:, 0:2].copy()).reshape(-1), _f16(a[:, 2:4].copy()).reshape(-1)
+    sc, qs = a[:, 4:16].astype(np.int32), a[:, 16:].astype(np.int32)
+    out = np.empty((a.shape[0], 256), np.float32)
+
+    def sm(k):
+        if k < 4 or naive_scales:
+            return sc[:, k % 8] & 63, sc[:, (k + 4) % 12] & 63
+        return (sc[:, k + 4] & 15) | ((sc[:, k - 4] >> 6) << 4), (sc[:, k + 4] >> 4) | ((sc[:, k] >> 6) << 4)
+
+    for j in range(4):
+        s1, m1 = sm(2 * j)
+        s2, m2 = sm(2 * j + 1)
+        lo, hi = qs[:, 32 * j:32 * j + 32] & 15, qs[:, 32 * j:32 * j + 32] >> 4
+        if swap_nibbles:
+            lo, hi = hi, lo
+        out[:, 64 * j:64 * j + 32] = (d * s1.astype(np.float32))[:, None] * lo - (dmin * m1.astype(np.float32))[:, None]
+        out[:, 64 * j + 32:64 * j + 64] = (d * s2.astype(np.float32))[:, None] * hi - (dmin * m2.astype(np.float32))[:, None]
+    return out.reshape(-1)
+
+
+def np_q6k(raw, qh_shift_off=0):
+    a = raw.reshape(-1, 210)
+    ql, qh = a[:, :128].astype(np.int32), a[:, 128:192].astype(np.int32)
+    sc = a[:, 192:208].view(np.int8).astype(np.float32)
+    d = _f16(a[:, 208:210].copy()).reshape(-1)
+    out = np.empty((a.shape[0], 256), np.float32)
+    for h in range(2):
+        for l in range(32):
+            lo, hi, hb = ql[:, 64 * h + l], ql[:, 64 * h + l + 32], qh[:, 32 * h + l]
+            qv = [(lo & 15) | (((hb >> (0 + qh_shift_off)) & 3) << 4),
+                  (hi & 15) | (((hb >> (2 + qh_shift_off)) & 3) << 4),
+                  (lo >> 4) | (((hb >> 4) & 3) << 4), (hi >> 4) | (((hb >> 6) & 3) << 4)]
+            for k in range(4):
+                out[:, 128 * h + l + 32 * k] = d * sc[:, 8 * h + l // 16 + 2 * k] * (qv[k] - 32).astype(np.float32)
+    return out.reshape(-1)
+
+
+def test_planted_quant_mistakes_are_caught():
+    k = golden("kat_quant.npz")
+    g = golden("ref_vectors.npz")
+    raw = k["q4k_pack_dmin1_raw"]
+    want = k["q4k_pack_dmin1_want"]
+    assert bits_equal(np_q4k(raw), want)                      # the restatement passes
+    assert not bits_equal(np_q4k(raw, swap_nibbles=True), want)
+    assert not bits_equal(np_q4k(g["deq12_raw"], naive_scales=True), g["deq12_out"])
+    assert bits_equal(np_q6k(g["deq14_raw"]), g["deq14_out"])
+    assert not bits_equal(np_q6k(g["deq14_raw"], qh_shift_off=1), g["deq14_out"])
+
+
+def test_planted_fp32_mistakes_are_caught():
+    g = golden("ref_vectors.npz")
+    x, w = g["norm_x"].astype(np.float64), g["norm_w"].astype(np.float64)
+    sum_not_mean = x / np.sqrt((x ** 2).sum(axis=1, keepdims=True) + 1e-6) * w
+    assert rel_to_scale(sum_not_mean, g["rms_out"]) > 1e-2
+    xr, c, s, rp = g["apply_x"], g["apply_cos"], g["apply_sin"], g["apply_pos"]
+    # NeoX read with interleaved pairing (the wrong mode) is rejected
+    assert not bits_equal(O.apply_rope(xr, c, s, rp, 1), g["apply_neox"])
+    # partial rotary with the head_dim exponent instead of n_rot's (F5) is rejected
+    pos = g["rope_pos"]
+    c_wrong = np.cos(pos.astype(np.float64)[:, None] /
+                     (1e7 ** (np.arange(32) * 2.0 / 256)))
+    assert np.abs(c_wrong - g["tab_partial64of256_cos"]).max() > 1e-2
+    # tanh GELU where the erf form is required is rejected
+    z = g["act_z"].astype(np.float64)
+    tanh = 0.5 * z * (1 + np.tanh(math.sqrt(2 / math.pi) * (z + 0.044715 * z ** 3)))
+    assert np.abs(tanh - g["gelu_out"]).max() > 1e-4
