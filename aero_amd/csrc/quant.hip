@@ -51,14 +51,53 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) {
 }
 
 template <int TYPE> struct QType;
-template <> struct QType<AERO_DTYPE_Q8_0> { static constexpr int BV = 32, BB = 34, LPB = 8; };
-template <> struct QType<AERO_DTYPE_Q4_K> { static constexpr int BV = 256, BB = 144, LPB = 64; };
-template <> struct QType<AERO_DTYPE_Q6_K> { static constexpr int BV = 256, BB = 210, LPB = 64; };
+template <> struct QType<AERO_DTYPE_Q4_K> { static constexpr int BV = 256, BB = 144; };
+template <> struct QType<AERO_DTYPE_Q6_K> { static constexpr int BV = 256, BB = 210; };
 
-// Values 4l..4l+3 of one Q8_0 block.
-__device__ __forceinline__ float4 dec_q8_0(const uint8_t* blk, int l) {
-    const float d = half_bits_to_float(ld_u16(blk));
-    const uint32_t q = ld_u32_a2(blk + 2 + 4 * l);
+// A "unit" is 256 consecutive output values. For Q4_K / Q6_K a unit is one
+// block and lane l of a wave produces values 4l..4l+3 of it. For Q8_0 a unit
+// is eight consecutive blocks of the flattened (row, block) sequence (rows of
+// any block count): lane l produces values 4(l%8).. of block l/8. Each wave
+// takes NB consecutive units, issues the loads of all of them first (raw
+// words into registers), then decodes and stores, so a wave has NB units of
+// loads in flight and writes NB KiB.
+
+// Raw words one lane needs for its four values of one unit.
+struct RawQ8 { uint32_t d, q0, q1; };        // fp16 d, quant bytes as 2 x 16 bit
+struct RawQ4 { uint32_t dd, s0, s1, s2, q; }; // d|dmin, 12 scale bytes, 4 quant bytes
+struct RawQ6 { uint32_t ql0, ql1, qh0, qh1, sc, d; };
+
+// Q8_0 lanes work per block: lane l covers values 4(l%8).. of its block.
+__device__ __forceinline__ void load_raw(const uint8_t* blk, int l, RawQ8& r) {
+    const int k = l & 7;
+    r.d = ld_u16(blk);
+    r.q0 = ld_u16(blk + 2 + 4 * k);
+    r.q1 = ld_u16(blk + 4 + 4 * k);
+}
+__device__ __forceinline__ void load_raw(const uint8_t* blk, int l, RawQ4& r) {
+    const int j = l >> 4, i0 = (l & 7) * 4;
+    r.dd = ld_u32(blk);
+    r.s0 = ld_u32(blk + 4);
+    r.s1 = ld_u32(blk + 8);
+    r.s2 = ld_u32(blk + 12);
+    r.q = ld_u32(blk + 16 + 32 * j + i0);
+}
+__device__ __forceinline__ void load_raw(const uint8_t* blk, int l, RawQ6& r) {
+    const int h = l >> 5, k = (l >> 3) & 3, lq = (l & 7) * 4;
+    const uint8_t* ql = blk + 64 * h + lq + 32 * (k & 1);
+    const uint8_t* qh = blk + 128 + 32 * h + lq;
+    r.ql0 = ld_u16(ql);
+    r.ql1 = ld_u16(ql + 2);
+    r.qh0 = ld_u16(qh);
+    r.qh1 = ld_u16(qh + 2);
+    r.sc = blk[192 + 8 * h + (lq >> 4) + 2 * k];
+    r.d = ld_u16(blk + 208);
+}
+
+// Q8_0, src/kernels.cpp:364-373: y = d*q.
+__device__ __forceinline__ float4 decode(const RawQ8& r, int) {
+    const float d = half_bits_to_float(r.d);
+    const uint32_t q = r.q0 | (r.q1 << 16);
     float4 v;
     v.x = d * (float)(int8_t)byte_of(q, 0);
     v.y = d * (float)(int8_t)byte_of(q, 1);
@@ -67,19 +106,18 @@ __device__ __forceinline__ float4 dec_q8_0(const uint8_t* blk, int l) {
     return v;
 }
 
-// Values 4l..4l+3 of one Q4_K block: group j = l/16 covers values 64j..64j+63,
-// low nibbles first (sub-block 2j) then high nibbles (sub-block 2j+1).
-__device__ __forceinline__ float4 dec_q4_k(const uint8_t* blk, int l) {
-    const uint32_t dd = ld_u32(blk);
-    const float d = half_bits_to_float(dd & 0xFFFFu);
-    const float dmin = half_bits_to_float(dd >> 16);
-    const uint32_t s0 = ld_u32(blk + 4), s1 = ld_u32(blk + 8), s2 = ld_u32(blk + 12);
+// Q4_K, src/kernels.cpp:65-73,337-363: group j = l/16 covers values
+// 64j..64j+63, low nibbles (sub-block 2j) then high nibbles (2j+1);
+// y = (d*sc)*q - (dmin*m).
+__device__ __forceinline__ float4 decode(const RawQ4& r, int l) {
+    const float d = half_bits_to_float(r.dd & 0xFFFFu);
+    const float dmin = half_bits_to_float(r.dd >> 16);
     const int j = l >> 4;
     const int hi = (l >> 3) & 1;
-    const int i0 = (l & 7) * 4;
     const int k = 2 * j + hi;
-    // byte idx of the 12-byte scale field, selected without a private array
-    auto sb = [&](int idx) {
+    // byte idx of the 12-byte scale field, selected from registers
+    const uint32_t s0 = r.s0, s1 = r.s1, s2 = r.s2;
+    auto sb = [s0, s1, s2](int idx) {
         const uint32_t w = idx < 4 ? s0 : (idx < 8 ? s1 : s2);
         return byte_of(w, idx & 3);
     };
@@ -93,27 +131,22 @@ __device__ __forceinline__ float4 dec_q4_k(const uint8_t* blk, int l) {
     }
     const float f = d * (float)sc;
     const float g = dmin * (float)mn;
-    const uint32_t q = ld_u32(blk + 16 + 32 * j + i0);
     const int sh = hi ? 4 : 0;
     float4 v;
-    v.x = f * (float)((byte_of(q, 0) >> sh) & 15u) - g;
-    v.y = f * (float)((byte_of(q, 1) >> sh) & 15u) - g;
-    v.z = f * (float)((byte_of(q, 2) >> sh) & 15u) - g;
-    v.w = f * (float)((byte_of(q, 3) >> sh) & 15u) - g;
+    v.x = f * (float)((byte_of(r.q, 0) >> sh) & 15u) - g;
+    v.y = f * (float)((byte_of(r.q, 1) >> sh) & 15u) - g;
+    v.z = f * (float)((byte_of(r.q, 2) >> sh) & 15u) - g;
+    v.w = f * (float)((byte_of(r.q, 3) >> sh) & 15u) - g;
     return v;
 }
 
-// Values 4l..4l+3 of one Q6_K block: half h = l/32, quarter k = (l/8)%4
-// (values 128h + 32k + lq .. +3, lq = 4*(l%8)).
-__device__ __forceinline__ float4 dec_q6_k(const uint8_t* blk, int l) {
-    const int h = l >> 5;
+// Q6_K, src/kernels.cpp:427-458: half h = l/32, quarter k = (l/8)%4 (values
+// 128h + 32k + lq .. +3, lq = 4*(l%8)); y = (d*sc)*(q-32).
+__device__ __forceinline__ float4 decode(const RawQ6& r, int l) {
     const int k = (l >> 3) & 3;
-    const int lq = (l & 7) * 4;
-    const uint32_t ql = ld_u32_a2(blk + 64 * h + lq + 32 * (k & 1));
-    const uint32_t qh = ld_u32_a2(blk + 128 + 32 * h + lq);
-    const int sc = (int8_t)blk[192 + 8 * h + (lq >> 4) + 2 * k];
-    const float d = half_bits_to_float(ld_u16(blk + 208));
-    const float f = d * (float)sc;
+    const uint32_t ql = r.ql0 | (r.ql1 << 16);
+    const uint32_t qh = r.qh0 | (r.qh1 << 16);
+    const float f = half_bits_to_float(r.d) * (float)(int8_t)r.sc;
     const int shl = (k >= 2) ? 4 : 0;
     const int shh = 2 * k;
     float qv[4];
@@ -126,31 +159,46 @@ __device__ __forceinline__ float4 dec_q6_k(const uint8_t* blk, int l) {
     return make_float4(qv[0], qv[1], qv[2], qv[3]);
 }
 
-template <int TYPE>
+template <int TYPE, typename RAW, int NB>
 __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
     using Q = QType<TYPE>;
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t gb = g / Q::LPB;
-    const int l = (int)(g % Q::LPB);
-    if (gb >= p.n_rows * p.nbr) return;
-    const int64_t row = gb / p.nbr;
-    const int64_t b = gb % p.nbr;
-    const int64_t tok = p.ids ? (int64_t)p.ids[row] : row;
-    float* o = p.out + gb * Q::BV + 4 * l;
-    if (tok < 0 || tok >= p.vocab) {
-        st_stream(o, make_float4(0.f, 0.f, 0.f, 0.f));
-        if (p.bad != nullptr && b == 0 && l == 0) atomicAdd(p.bad, 1u);
-        return;
+    static_assert(Q::BV == 256, "one block per unit");
+    const int l = threadIdx.x & 63;
+    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t upr = p.nbr;            // units per row
+    const int64_t n_units = p.n_rows * upr;
+    RAW raw[NB];
+    bool ok[NB];
+    int64_t unit[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        unit[i] = wave * NB + i;
+        ok[i] = false;
+        if (unit[i] < n_units) {
+            const int64_t row = unit[i] / upr;
+            const int64_t u = unit[i] % upr;
+            const int64_t tok = p.ids ? (int64_t)p.ids[row] : row;
+            if (tok >= 0 && tok < p.vocab) {
+                ok[i] = true;
+                load_raw(p.table + tok * p.rb + u * Q::BB, l, raw[i]);
+            } else if (p.bad != nullptr && u == 0 && l == 0) {
+                atomicAdd(p.bad, 1u);
+            }
+        }
     }
-    const uint8_t* blk = p.table + tok * p.rb + b * Q::BB;
-    float4 v;
-    if constexpr (TYPE == AERO_DTYPE_Q8_0) v = dec_q8_0(blk, l);
-    else if constexpr (TYPE == AERO_DTYPE_Q4_K) v = dec_q4_k(blk, l);
-    else v = dec_q6_k(blk, l);
-    if (p.scale > 0.0f) {
-        v.x = v.x * p.scale; v.y = v.y * p.scale; v.z = v.z * p.scale; v.w = v.w * p.scale;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (unit[i] >= n_units) continue;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ok[i]) {
+            v = decode(raw[i], l);
+            if (p.scale > 0.0f) {
+                v.x = v.x * p.scale; v.y = v.y * p.scale;
+                v.z = v.z * p.scale; v.w = v.w * p.scale;
+            }
+        }
+        st_stream(p.out + unit[i] * 256 + 4 * l, v);
     }
-    st_stream(o, v);
 }
 
 // F16 / BF16 element-wise decode for whole-buffer dequant.
@@ -189,25 +237,82 @@ bool is_block_quant(int t) {
     return t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q6_K;
 }
 
-bool run_gather(int dtype, GatherParams p, hipStream_t s) {
-    const int64_t nb = p.n_rows * p.nbr;
-    if (nb == 0) return true;
-    const int lpb = dtype == AERO_DTYPE_Q8_0 ? 8 : 64;
-    const int64_t blocks = (nb * lpb + 255) / 256;
+template <int NB>
+__global__ __launch_bounds__(256) void gather_q8_0_kernel(GatherParams p) {
+    const int l = threadIdx.x & 63;
+    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t n_blocks = p.n_rows * p.nbr;
+    RawQ8 raw[NB];
+    bool ok[NB];
+    int64_t gb[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        gb[i] = (wave * NB + i) * 8 + (l >> 3);
+        ok[i] = false;
+        if (gb[i] < n_blocks) {
+            const int64_t row = gb[i] / p.nbr;
+            const int64_t b = gb[i] % p.nbr;
+            const int64_t tok = p.ids ? (int64_t)p.ids[row] : row;
+            if (tok >= 0 && tok < p.vocab) {
+                ok[i] = true;
+                load_raw(p.table + tok * p.rb + b * 34, l, raw[i]);
+            } else if (p.bad != nullptr && b == 0 && (l & 7) == 0) {
+                atomicAdd(p.bad, 1u);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (gb[i] >= n_blocks) continue;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ok[i]) {
+            v = decode(raw[i], l);
+            if (p.scale > 0.0f) {
+                v.x = v.x * p.scale; v.y = v.y * p.scale;
+                v.z = v.z * p.scale; v.w = v.w * p.scale;
+            }
+        }
+        st_stream(p.out + gb[i] * 32 + 4 * (l & 7), v);
+    }
+}
+
+template <int TYPE, typename RAW>
+bool launch_gather(const char* name, GatherParams p, int64_t n_units, hipStream_t s) {
+    // Small gathers want many short waves (latency), large ones want more
+    // bytes in flight per wave: measured crossover ~128K units on MI355X.
+    const int nb = tune("gather_nb", n_units >= 131072 ? 2 : 1);
+    const int per_wave = nb >= 4 ? 4 : (nb >= 2 ? 2 : 1);
+    const int64_t waves = (n_units + per_wave - 1) / per_wave;
+    const int64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7fffffff) {
         set_error("gather: grid too large");
         return false;
     }
+    if constexpr (TYPE == AERO_DTYPE_Q8_0) {
+        switch (per_wave) {
+        case 4: return launch(name, gather_q8_0_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        case 2: return launch(name, gather_q8_0_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        default: return launch(name, gather_q8_0_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        }
+    } else {
+        switch (per_wave) {
+        case 4: return launch(name, gather_kernel<TYPE, RAW, 4>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        case 2: return launch(name, gather_kernel<TYPE, RAW, 2>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        default: return launch(name, gather_kernel<TYPE, RAW, 1>, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        }
+    }
+}
+
+bool run_gather(int dtype, GatherParams p, hipStream_t s) {
+    const int64_t nb = p.n_rows * p.nbr;
+    if (nb == 0) return true;
     switch (dtype) {
-    case AERO_DTYPE_Q8_0:
-        return launch("gather_kernel<Q8_0>", gather_kernel<AERO_DTYPE_Q8_0>,
-                      dim3((unsigned)blocks), dim3(256), 0, s, p);
+    case AERO_DTYPE_Q8_0:  // units of 8 blocks of the flattened sequence
+        return launch_gather<AERO_DTYPE_Q8_0, RawQ8>("gather_q8_0_kernel", p, (nb + 7) / 8, s);
     case AERO_DTYPE_Q4_K:
-        return launch("gather_kernel<Q4_K>", gather_kernel<AERO_DTYPE_Q4_K>,
-                      dim3((unsigned)blocks), dim3(256), 0, s, p);
+        return launch_gather<AERO_DTYPE_Q4_K, RawQ4>("gather_kernel<Q4_K>", p, nb, s);
     case AERO_DTYPE_Q6_K:
-        return launch("gather_kernel<Q6_K>", gather_kernel<AERO_DTYPE_Q6_K>,
-                      dim3((unsigned)blocks), dim3(256), 0, s, p);
+        return launch_gather<AERO_DTYPE_Q6_K, RawQ6>("gather_kernel<Q6_K>", p, nb, s);
     default:
         set_error("gather: unsupported dtype %d", dtype);
         return false;

@@ -57,6 +57,10 @@ def parse_args(argv=None):
     p.add_argument("--shapes", default=None, help="comma list for --all-shapes")
     p.add_argument("--only", choices=OPS + ("rope_qk_norm", "gated_norm"), default=None)
     p.add_argument("--copy-calibration", action="store_true")
+    p.add_argument("--host-abi", action="store_true",
+                   help="PCIe-inclusive rate of the reference-compatible host ABI")
+    p.add_argument("--launch-floor", action="store_true",
+                   help="device duration of a one-block launch")
     return p.parse_args(argv)
 
 
@@ -375,6 +379,10 @@ def main(argv=None):
         return 1
     if a.copy_calibration:
         return copy_calibration(a)
+    if a.host_abi:
+        return host_abi(a)
+    if a.launch_floor:
+        return launch_floor(a)
     if a.all_shapes:
         return all_shapes(a)
 
@@ -479,6 +487,65 @@ def copy_calibration(a):
     print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n,
                       "kernel_us": round(m * 1e3, 2),
                       "GB/s": round(8 * n / (m * 1e-3) / 1e9, 1)}))
+    return 0
+
+
+def host_abi(a):
+    """The reference-compatible host-pointer entry points at the 512-token
+    shape: algorithmic bytes / wall time of the whole call, PCIe included."""
+    from aero_amd import native as NK, tensor_native as TN, transformer_native as N
+    from aero_amd import workloads as W
+
+    s = W.SHAPES[W.HEADLINE]
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((s.n_tok, s.hidden), dtype=np.float32)
+    w = np.float32(1) + rng.standard_normal(s.hidden, dtype=np.float32) * np.float32(0.1)
+    g = rng.standard_normal((s.n_tok, s.ffn), dtype=np.float32)
+    u = rng.standard_normal((s.n_tok, s.ffn), dtype=np.float32)
+    q = rng.standard_normal((s.n_tok * s.hq, s.head_dim), dtype=np.float32)
+    c, si = N.rope_tables(s.head_dim, np.arange(s.n_tok), s.theta)
+    qpos = np.repeat(np.arange(s.n_tok), s.hq).astype(np.int32)
+    raw = W.make_table(s.emb_type, s.n_tok * (s.hidden // 256), rng).tobytes()
+    cases = [
+        ("transformer_native.rmsnorm_rows", lambda: N.rmsnorm_rows(x, w, s.eps),
+         W.bytes_rmsnorm(s.n_tok, s.hidden)),
+        ("tensor_native.swiglu", lambda: TN.swiglu(g.copy(), u), W.bytes_act(s.n_tok, s.ffn)),
+        ("transformer_native.apply_rope(q)", lambda: N.apply_rope(q, c, si, qpos),
+         8 * q.size),
+        ("native.dequant(Q4_K, 512 rows)", lambda: NK.dequant(s.emb_type, raw, (s.n_tok, s.hidden)),
+         W.bytes_embed(s.n_tok, s.hidden, s.emb_type)),
+    ]
+    out = {}
+    for name, fn, b in cases:
+        fn()
+        ts = []
+        for _ in range(max(3, a.steps // 20)):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        m = statistics.median(ts)
+        out[name] = {"ms": round(m * 1e3, 3), "GB/s_incl_pcie": round(b / m / 1e9, 2)}
+    print(json.dumps({"host_abi_llama3_8b_prefill": out}))
+    return 0
+
+
+def launch_floor(a):
+    """Device duration of a one-block launch (act_mul on 4 floats)."""
+    from aero_amd import ops
+    from aero_amd.device import DeviceArray as DA, Event, synchronize, time_next_kernel
+
+    g, u, o = DA.empty(4), DA.empty(4), DA.empty(4)
+    pairs = []
+    for i in range(a.warmup + a.steps):
+        e0, e1 = Event(), Event()
+        time_next_kernel(e0, e1)
+        ops.act_mul("silu", g, u, o)
+        if i >= a.warmup:
+            pairs.append((e0, e1))
+    synchronize()
+    ts = sorted(x.elapsed_ms(y) * 1e3 for x, y in pairs)
+    print(json.dumps({"one_block_kernel_us_median": round(ts[len(ts) // 2], 3),
+                      "min_us": round(ts[0], 3)}))
     return 0
 
 

@@ -198,3 +198,21 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "8"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_per_op_selector(monkeypatch):
+    from aero_amd import select
+    monkeypatch.setenv("AERO_GPU_OPS", "rmsnorm, rope")
+    assert select.enabled("rmsnorm") and select.enabled("rope") and not select.enabled("act")
+    assert select.enabled("act", override=True) and not select.enabled("rope", override=False)
+    monkeypatch.setenv("AERO_GPU_OPS", "all")
+    assert all(select.enabled(op) for op in select.OPS)
+    monkeypatch.setenv("AERO_GPU_OPS", "none")
+    assert not any(select.enabled(op) for op in select.OPS)
+    monkeypatch.delenv("AERO_GPU_OPS")
+    assert not select.enabled("embed")
+    monkeypatch.setenv("AERO_GPU_OPS", "rmsnrom")
+    with pytest.raises(ValueError):
+        select.enabled("rmsnorm")
+    with pytest.raises(ValueError):
+        select.enabled("softmax")
