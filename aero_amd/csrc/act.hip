@@ -74,10 +74,13 @@ void act_vec_kernel(const float* g, const float* u, float* out, int64_t n4) {
             if constexpr (UP) uv[i] = ld_stream(u + 4 * idx);
         }
     }
+    const int64_t first = (int64_t)blockIdx.x * (BS * U);
+    const StreamOut o(out + 4 * first, (n4 - first) * 16);
 #pragma unroll
     for (int i = 0; i < U; ++i) {
         const int64_t idx = base + (int64_t)i * BS;
-        if (idx < n4) st_stream(out + 4 * idx, act4<KIND, UP>(gv[i], UP ? uv[i] : gv[i]));
+        if (idx < n4)
+            o.store((uint32_t)((idx - first) * 16), act4<KIND, UP>(gv[i], UP ? uv[i] : gv[i]));
     }
 }
 

@@ -98,10 +98,35 @@ __device__ __forceinline__ float4 ld_stream(const float* p) {
     const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
     return make_float4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ void st_stream(float* p, float4 v) {
-    const v4f t = {v.x, v.y, v.z, v.w};
-    __builtin_nontemporal_store(t, reinterpret_cast<v4f*>(p));
-}
+
+// Output stores through a buffer descriptor: the hardware drops any store
+// at or past `bytes` from the base, so a wrong offset cannot write outside
+// the output. The descriptor is built from a base the caller guarantees is
+// the same for every lane of the wave (it is read from lane 0); offsets are
+// 32-bit bytes from that base. The cache policy is NT (streaming), which on
+// MI355X measured equal to nontemporal global stores and faster than
+// device-scope SC1 stores for the gathers (1.7x at 16384 rows).
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9)
+constexpr int kStorePolicy = 2;  // cache-policy operand (gfx950: 1 SC0, 2 NT, 16 SC1)
+
+struct StreamOut {
+    __amdgpu_buffer_rsrc_t rsrc;
+    __device__ __forceinline__ StreamOut(float* wave_uniform_base, int64_t bytes) {
+        const uint64_t a = reinterpret_cast<uint64_t>(wave_uniform_base);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+        const int64_t cl = bytes < 0 ? 0 : (bytes > 0xFFFFFFFFll ? 0xFFFFFFFFll : bytes);
+        const uint32_t n = __builtin_amdgcn_readfirstlane((uint32_t)cl);
+        rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0, (int)n, kBufferDword3);
+    }
+    __device__ __forceinline__ void store(uint32_t byte_off, float4 v) const {
+        const v4u d = {__builtin_bit_cast(uint32_t, v.x), __builtin_bit_cast(uint32_t, v.y),
+                       __builtin_bit_cast(uint32_t, v.z), __builtin_bit_cast(uint32_t, v.w)};
+        __builtin_amdgcn_raw_buffer_store_b128(d, rsrc, (int)byte_off, 0, kStorePolicy);
+    }
+};
 
 // ------------------------------------------------------- device helpers
 // Sum across aligned groups of W lanes (W a power of two, W <= 64) with an

@@ -101,9 +101,12 @@ void norm_vec_kernel(NormParams p) {
 #pragma unroll
         for (int k = 1; k < WPR; ++k) ss += part[w0 + k];
     }
+    // every lane of the block shares the descriptor based at its first row
+    const int64_t row0 = (int64_t)blockIdx.x * RPB;
+    const StreamOut os(p.out + row0 * p.cols, (p.rows - row0) * (int64_t)p.cols * 4);
+    const uint32_t obase = (uint32_t)(lr * p.cols) * 4u;
     if (!ok) return;
 
-    float* orow = p.out + base;
     if constexpr (GATED) {
         const float denom = sqrtf(ss / (float)p.cols + p.eps);
         const int col0 = (int)(row % p.gpr) * p.cols;
@@ -118,7 +121,7 @@ void norm_vec_kernel(NormParams p) {
             o.y = ((xv[i].y / denom) * wv.y) * silu_div(zv[i].y);
             o.z = ((xv[i].z / denom) * wv.z) * silu_div(zv[i].z);
             o.w = ((xv[i].w / denom) * wv.w) * silu_div(zv[i].w);
-            st_stream(orow + 4 * c, o);
+            os.store(obase + 16u * c, o);
         }
     } else {
         const float inv = norm_scale(ss, p);
@@ -136,7 +139,7 @@ void norm_vec_kernel(NormParams p) {
                 }
                 o.x = o.x * wv.x; o.y = o.y * wv.y; o.z = o.z * wv.z; o.w = o.w * wv.w;
             }
-            st_stream(orow + 4 * c, o);
+            os.store(obase + 16u * c, o);
         }
     }
 }

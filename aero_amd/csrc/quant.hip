@@ -186,6 +186,8 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
             }
         }
     }
+    const int64_t u0 = wave * NB;  // first unit of the wave
+    const StreamOut o(p.out + u0 * 256, (n_units - u0) * 1024);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         if (unit[i] >= n_units) continue;
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
                 v.z = v.z * p.scale; v.w = v.w * p.scale;
             }
         }
-        st_stream(p.out + unit[i] * 256 + 4 * l, v);
+        o.store((uint32_t)(((unit[i] - u0) * 256 + 4 * l) * 4), v);
     }
 }
 
@@ -261,6 +263,8 @@ __global__ __launch_bounds__(256) void gather_q8_0_kernel(GatherParams p) {
             }
         }
     }
+    const int64_t gb0 = wave * NB * 8;  // first block of the wave
+    const StreamOut o(p.out + gb0 * 32, (n_blocks - gb0) * 128);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         if (gb[i] >= n_blocks) continue;
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(256) void gather_q8_0_kernel(GatherParams p) {
                 v.z = v.z * p.scale; v.w = v.w * p.scale;
             }
         }
-        st_stream(p.out + gb[i] * 32 + 4 * (l & 7), v);
+        o.store((uint32_t)(((gb[i] - gb0) * 32 + 4 * (l & 7)) * 4), v);
     }
 }
 

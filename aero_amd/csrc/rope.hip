@@ -111,8 +111,9 @@ void rope_vec_kernel(RopeParams p) {
     }
 
     float4 A[RPS], B[RPS];
-    float* dst[RPS];
     const float* wrow[RPS];
+    int rowoff[RPS];   // element offset of the row inside its token's q or k block
+    bool isq_row[RPS];
     bool valid[RPS];
 #pragma unroll
     for (int i = 0; i < RPS; ++i) {
@@ -120,13 +121,15 @@ void rope_vec_kernel(RopeParams p) {
         valid[i] = active && h < h1;
         A[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         B[i] = A[i];
-        dst[i] = nullptr;
         wrow[i] = nullptr;
+        rowoff[i] = 0;
+        isq_row[i] = true;
         if (h < h1) {
             const bool isq = h < p.hq;
-            const int64_t roff = (t * (isq ? p.hq : p.hk) + (isq ? h : h - p.hq)) * (int64_t)p.D;
+            isq_row[i] = isq;
+            rowoff[i] = (isq ? h : h - p.hq) * p.D;
+            const int64_t roff = t * (int64_t)(isq ? p.hq : p.hk) * p.D + rowoff[i];
             const float* src = (isq ? p.q : p.k) + roff;
-            dst[i] = (isq ? p.q_out : p.k_out) + roff;
             wrow[i] = isq ? p.q_w : p.k_w;
             if (valid[i]) {
                 A[i] = ld_stream(src + a0);
@@ -149,6 +152,11 @@ void rope_vec_kernel(RopeParams p) {
         reinterpret_cast<float*>(cs_s)[tid] = sn;
     }
     __syncthreads();
+
+    // this token's q rows and k rows, each a contiguous block of heads x D
+    const StreamOut oq(p.q_out + t * (int64_t)p.hq * p.D, (int64_t)p.hq * p.D * 4);
+    const StreamOut ok_(p.hk > 0 ? p.k_out + t * (int64_t)p.hk * p.D : p.q_out,
+                        (int64_t)p.hk * p.D * 4);
 
     float4 c4 = make_float4(1.f, 1.f, 1.f, 1.f), s4 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (rot) {
@@ -184,8 +192,15 @@ void rope_vec_kernel(RopeParams p) {
                 rot2(B[i].z, B[i].w, c4.w, s4.w);
             }
         }
-        st_stream(dst[i] + a0, A[i]);
-        st_stream(dst[i] + b0, B[i]);
+        const uint32_t off = (uint32_t)(rowoff[i] + a0) * 4u;
+        const uint32_t offb = (uint32_t)(rowoff[i] + b0) * 4u;
+        if (isq_row[i]) {
+            oq.store(off, A[i]);
+            oq.store(offb, B[i]);
+        } else {
+            ok_.store(off, A[i]);
+            ok_.store(offb, B[i]);
+        }
     }
 }
 

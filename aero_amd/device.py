@@ -68,6 +68,15 @@ class DeviceArray:
         _lib.check(_lib.lib().aero_hip_memcpy_htod(self.ptr, a.ctypes.data, a.nbytes),
                    "memcpy H2D")
 
+    def clone(self) -> "DeviceArray":
+        """A new allocation holding a device-to-device copy of this one
+        (complete when this returns)."""
+        d = DeviceArray(self.shape, self.dtype)
+        L = _lib.lib()
+        _lib.check(L.aero_hip_memcpy_dtod(d.ptr, self.ptr, self.nbytes, None), "memcpy D2D")
+        _lib.check(L.aero_hip_stream_synchronize(None), "stream synchronize")
+        return d
+
     def numpy(self) -> np.ndarray:
         out = np.empty(self.shape, dtype=self.dtype)
         _lib.check(_lib.lib().aero_hip_memcpy_dtoh(out.ctypes.data, self.ptr, self.nbytes),

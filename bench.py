@@ -15,7 +15,11 @@ algorithmic HBM bytes / wall time per step over the timed region (GB/s).
 bytes / its mean device duration, measured with HIP events recorded by the
 kernel's own dispatch (hipExtLaunchKernel) over a second region of the same
 run that replays the same plans with an event pair per kernel (events per
-kernel serialise the host side, so that region times kernels, not steps). `cpu_baseline` is the same step on the host: the reference's own C++
+kernel serialise the host side, so that region times kernels, not steps).
+Each entry of `ops` gives that per-dispatch figure (`kernel_us`, `frac`) and
+a sustained one (`sustained_us`, `sustained_frac`): the op alone, launched
+back to back over its own > 1 GiB rotation of buffers, timed by one event
+pair around the whole region. `cpu_baseline` is the same step on the host: the reference's own C++
 (built into oracle/_ref) when present, else the oracle's restatement,
 single-threaded like the reference, over a bounded sample.
 
@@ -40,6 +44,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+SUSTAINED_ROTATION = 5 << 28  # bytes one rotation of buffer sets moves (1.25 GiB)
+SUSTAINED_REPS = 8            # rotations timed per op
 METRIC = "fused-op HBM GB/s (% of MI355X peak) + rows/s vs CPU ref, Llama-3-8B shapes"
 OPS = ("embed_gather", "rmsnorm", "rope_qk", "swiglu")
 
@@ -69,25 +75,50 @@ class StepBuffers:
     """One buffer set of a step, in HBM."""
 
     def __init__(self, s, d_table, rng):
-        from aero_amd import workloads as W
         from aero_amd.device import DeviceArray as DA
 
         R = s.n_tok
+
+        def normal(*shape):
+            return DA.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+
         self.ids = DA.from_numpy(rng.integers(0, s.vocab, R).astype(np.int32))
         self.emb_out = DA.empty((R, s.hidden))
-        self.x = DA.from_numpy(rng.standard_normal((R, s.hidden), dtype=np.float32))
+        self.x = normal(R, s.hidden)
         self.h = DA.empty((R, s.hidden))
-        self.q = DA.from_numpy(rng.standard_normal((R, s.hq, s.head_dim), dtype=np.float32))
-        self.k = DA.from_numpy(rng.standard_normal((R, s.hk, s.head_dim), dtype=np.float32))
-        self.gate = DA.from_numpy(rng.standard_normal((R, s.ffn), dtype=np.float32))
-        self.up = DA.from_numpy(rng.standard_normal((R, s.ffn), dtype=np.float32))
+        self.q = normal(R, s.hq, s.head_dim)
+        self.k = normal(R, s.hk, s.head_dim)
+        self.gate = normal(R, s.ffn)
+        self.up = normal(R, s.ffn)
         self.act_out = DA.empty((R, s.ffn))
         if s.gated:
             n_v, dd = s.gated
-            self.gx = DA.from_numpy(rng.standard_normal((R, n_v * dd), dtype=np.float32))
-            self.gz = DA.from_numpy(rng.standard_normal((R, n_v * dd), dtype=np.float32))
+            self.gx = normal(R, n_v * dd)
+            self.gz = normal(R, n_v * dd)
             self.gout = DA.empty((R, n_v * dd))
         self.table = d_table
+
+    INPUTS = {"embed_gather": (("ids",), ("emb_out",)), "rmsnorm": (("x",), ("h",)),
+              "rope_qk": (("q", "k"), ()), "swiglu": (("gate", "up"), ("act_out",)),
+              "gated_norm": (("gx", "gz"), ("gout",))}
+
+    @classmethod
+    def copy_for(cls, src, op, rng, vocab):
+        """A new set of `op`'s buffers: device copies of `src`'s activations,
+        fresh token ids (so no two sets read the same table rows), fresh
+        outputs."""
+        from aero_amd.device import DeviceArray as DA
+
+        b = cls.__new__(cls)
+        ins, outs = cls.INPUTS[op]
+        for n in ins:
+            a = getattr(src, n)
+            setattr(b, n, DA.from_numpy(rng.integers(0, vocab, a.shape).astype(np.int32))
+                    if n == "ids" else a.clone())
+        for n in outs:
+            setattr(b, n, DA.empty(getattr(src, n).shape))
+        b.table = src.table
+        return b
 
 
 class Path:
@@ -263,6 +294,59 @@ def kernel_times(path, steps, warmup, only=None):
     return ker
 
 
+def sustained_times(path, ops_list, reps):
+    """Back-to-back launches of one op: a plan issues the op once on each of
+    its own buffer sets (together > 1 GiB, or 256 sets for ops under 5 MB,
+    so the 256 MiB Infinity Cache holds no set of a large op from its
+    previous use) and is replayed `reps` times between
+    one event pair on the stream. Returns {op: mean µs per launch}. No event
+    is recorded per kernel, so this is the op's cost inside a busy stream."""
+    from aero_amd.device import Event, Plan, Stream
+
+    out = {}
+    rng = np.random.default_rng(1)
+    step_sets = path.sets
+    for op in ops_list:
+        n = min(256, max(4, -(-SUSTAINED_ROTATION // max(1, path.bytes()[op]))))
+        path.sets = [StepBuffers.copy_for(step_sets[i % len(step_sets)], op, rng, path.s.vocab)
+                     for i in range(n)]
+        plan = Plan()
+        with plan:
+            for i in range(n):
+                path.run(op, i)
+        per_plan = len(plan) // n
+        stream = Stream()
+        for _ in range(2):
+            plan.launch(stream)
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(reps):
+            plan.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        out[op] = e0.elapsed_ms(e1) * 1e3 / (reps * n)
+        assert per_plan >= 1
+        plan.destroy()
+        stream.destroy()
+        path.sets = None  # frees this op's sets before the next op allocates
+    path.sets = step_sets
+    return out
+
+
+def op_entry(b, rows, us_event, us_sustained):
+    """Per-op figures: per-dispatch (events on each kernel) and sustained
+    (back-to-back launches)."""
+    e = {"kernel_us": round(us_event, 3), "bytes": b,
+         "GB/s": round(b / (us_event * 1e-6) / 1e9, 1),
+         "frac": round(b / (us_event * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+         "rows_per_s": round(rows / (us_event * 1e-6), 1)}
+    if us_sustained is not None:
+        g = b / (us_sustained * 1e-6) / 1e9
+        e.update({"sustained_us": round(us_sustained, 3), "sustained_GB/s": round(g, 1),
+                  "sustained_frac": round(g / HBM_PEAK_GBS, 4)})
+    return e
+
+
 # ---------------------------------------------------------------- CPU side
 def cpu_baseline(path, seconds):
     """The same step on the host, single-threaded, timed per op around the
@@ -397,18 +481,15 @@ def main(argv=None):
         return 0
     wall = timed_steps(path, a.steps, a.warmup)
     ker = kernel_times(path, a.steps, a.warmup)
+    sus = sustained_times(path, path.step_ops(), SUSTAINED_REPS)
     bts = path.bytes()
     rows = path.rows()
     total = sum(bts[op] for op in path.step_ops())
     value = total / (wall * 1e-3) / 1e9
     per_op = {}
     for op in path.step_ops():
-        m = statistics.mean(ker[op])
-        per_op[op] = {"kernel_us": round(m * 1e3, 3), "kernel_us_median": round(
-            statistics.median(ker[op]) * 1e3, 3), "bytes": bts[op],
-            "GB/s": round(bts[op] / (m * 1e-3) / 1e9, 1),
-            "frac": round(bts[op] / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "rows_per_s": round(rows[op] / (m * 1e-3), 1)}
+        per_op[op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3, sus[op])
+        per_op[op]["kernel_us_median"] = round(statistics.median(ker[op]) * 1e3, 3)
     dom = "swiglu"
     ach = per_op[dom]["GB/s"]
     out = {
@@ -454,14 +535,12 @@ def all_shapes(a):
         sets = a.sets if W.SHAPES[name].n_tok <= 4096 else 2
         path = Path(name, sets)
         ker = kernel_times(path, max(20, a.steps // 4), 5)
+        sus = sustained_times(path, path.step_ops(), SUSTAINED_REPS)
         bts, rows = path.bytes(), path.rows()
         res[name] = {}
         for op in path.step_ops():
-            m = statistics.mean(ker[op])
-            res[name][op] = {"kernel_us": round(m * 1e3, 3), "bytes": bts[op],
-                             "GB/s": round(bts[op] / (m * 1e-3) / 1e9, 1),
-                             "frac": round(bts[op] / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                             "rows_per_s": round(rows[op] / (m * 1e-3), 1)}
+            res[name][op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3,
+                                     sus[op])
         print(json.dumps({"shape": name, "ops": res[name]}), flush=True)
         del path
     return 0
