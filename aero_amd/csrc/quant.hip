@@ -1,14 +1,14 @@
 // GGUF token-embedding row gather with Q8_0 / Q4_K / Q6_K dequant on gfx950,
 // and the same kernels as a whole-buffer dequant.
 //
-// Work is split by quant block: a Q4_K or Q6_K block (256 values) is one
-// wave, each lane producing one float4 of consecutive outputs; a Q8_0 block
-// (32 values) is eight lanes. A lane reads only the bytes its four values
-// need (a 32-bit word of quants plus the block header, which every lane of
-// the block shares through L1), unpacks the 6-bit / 4-bit scales in
-// registers and writes one 128-bit store, so a wave writes 1 KiB of
-// contiguous output. HBM bytes per gathered row: (n_embd/bv)*bb read +
-// 4*n_embd written.
+// One wave (a 64-thread workgroup) takes a run of U*256 consecutive values of
+// one output row. It reads the row's token id once, loads the run's quant
+// blocks (contiguous in the table) with coalesced 32-bit loads, one per lane
+// per 256 bytes, stages them in LDS, and then each lane decodes four values
+// per 256-value step from LDS (block header plus the quant bytes of its four
+// values, unpacking 6-bit / 4-bit scales in registers) and writes one
+// 128-bit store, so each step of a wave writes 1 KiB of contiguous output.
+// HBM bytes per gathered row: (n_embd/bv)*bb read + 4*n_embd written.
 //
 // Arithmetic is the reference's, operation by operation with contraction
 // off, so results are bit-identical: Q8_0 d*q (src/kernels.cpp:364-373);
@@ -50,17 +50,12 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) {
     return (w >> (8 * k)) & 0xFFu;
 }
 
-template <int TYPE> struct QType;
-template <> struct QType<AERO_DTYPE_Q4_K> { static constexpr int BV = 256, BB = 144; };
-template <> struct QType<AERO_DTYPE_Q6_K> { static constexpr int BV = 256, BB = 210; };
-
-// A "unit" is 256 consecutive output values. For Q4_K / Q6_K a unit is one
-// block and lane l of a wave produces values 4l..4l+3 of it. For Q8_0 a unit
-// is eight consecutive blocks of the flattened (row, block) sequence (rows of
-// any block count): lane l produces values 4(l%8).. of block l/8. Each wave
-// takes NB consecutive units, issues the loads of all of them first (raw
-// words into registers), then decodes and stores, so a wave has NB units of
-// loads in flight and writes NB KiB.
+// In each 256-value step of a run, lane l produces values 4l..4l+3: for
+// Q4_K / Q6_K of the step's one block, for Q8_0 values 4(l%8).. of the
+// step's block l/8. load_raw reads the words a lane needs from the run staged
+// in LDS: Q8_0 and Q6_K blocks start at even byte offsets and are read in
+// 16-bit pieces, Q4_K blocks start at multiples of 4 (144-byte blocks in a
+// 4-byte aligned table).
 
 // Raw words one lane needs for its four values of one unit.
 struct RawQ8 { uint32_t d, q0, q1; };        // fp16 d, quant bytes as 2 x 16 bit
@@ -159,50 +154,6 @@ __device__ __forceinline__ float4 decode(const RawQ6& r, int l) {
     return make_float4(qv[0], qv[1], qv[2], qv[3]);
 }
 
-template <int TYPE, typename RAW, int NB>
-__global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
-    using Q = QType<TYPE>;
-    static_assert(Q::BV == 256, "one block per unit");
-    const int l = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t upr = p.nbr;            // units per row
-    const int64_t n_units = p.n_rows * upr;
-    RAW raw[NB];
-    bool ok[NB];
-    int64_t unit[NB];
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        unit[i] = wave * NB + i;
-        ok[i] = false;
-        if (unit[i] < n_units) {
-            const int64_t row = unit[i] / upr;
-            const int64_t u = unit[i] % upr;
-            const int64_t tok = p.ids ? (int64_t)p.ids[row] : row;
-            if (tok >= 0 && tok < p.vocab) {
-                ok[i] = true;
-                load_raw(p.table + tok * p.rb + u * Q::BB, l, raw[i]);
-            } else if (p.bad != nullptr && u == 0 && l == 0) {
-                atomicAdd(p.bad, 1u);
-            }
-        }
-    }
-    const int64_t u0 = wave * NB;  // first unit of the wave
-    const StreamOut o(p.out + u0 * 256, (n_units - u0) * 1024);
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        if (unit[i] >= n_units) continue;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (ok[i]) {
-            v = decode(raw[i], l);
-            if (p.scale > 0.0f) {
-                v.x = v.x * p.scale; v.y = v.y * p.scale;
-                v.z = v.z * p.scale; v.w = v.w * p.scale;
-            }
-        }
-        o.store((uint32_t)(((unit[i] - u0) * 256 + 4 * l) * 4), v);
-    }
-}
-
 // F16 / BF16 element-wise decode for whole-buffer dequant.
 template <bool BF>
 __global__ __launch_bounds__(256)
@@ -239,84 +190,118 @@ bool is_block_quant(int t) {
     return t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q6_K;
 }
 
-template <int NB>
-__global__ __launch_bounds__(256) void gather_q8_0_kernel(GatherParams p) {
-    const int l = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t n_blocks = p.n_rows * p.nbr;
-    RawQ8 raw[NB];
-    bool ok[NB];
-    int64_t gb[NB];
+template <int TYPE> struct QT;
+template <> struct QT<AERO_DTYPE_Q8_0> { static constexpr int BV = 32, BB = 34; using Raw = RawQ8; };
+template <> struct QT<AERO_DTYPE_Q4_K> { static constexpr int BV = 256, BB = 144; using Raw = RawQ4; };
+template <> struct QT<AERO_DTYPE_Q6_K> { static constexpr int BV = 256, BB = 210; using Raw = RawQ6; };
+
+// Wave w covers values [c*U*256, min((c+1)*U*256, n_embd)) of output row
+// r = w / cpr (c = w % cpr). Every branch on r, the token or the run length
+// is uniform across the wave.
+template <int TYPE, int U>
+__global__ __launch_bounds__(64) void gather_rows_kernel(GatherParams p, int cpr) {
+    using Q = QT<TYPE>;
+    constexpr int BPS = 256 / Q::BV;                   // blocks per 256-value step
+    constexpr int MAX_DW = (U * BPS * Q::BB + 3 + 3) / 4;  // + up to 3 bytes of misalignment
+    constexpr int PER = (MAX_DW + 63) / 64;
+    __shared__ __align__(16) uint32_t stage[PER * 64];
+
+    const int l = threadIdx.x;
+    const int row = (int)blockIdx.x / cpr;
+    const int c = (int)blockIdx.x - row * cpr;
+    const int64_t n_embd = p.nbr * Q::BV;
+    const int64_t v_begin = (int64_t)c * (U * 256);
+    const int nv = (int)min((int64_t)(U * 256), n_embd - v_begin);  // values in this run
+    const StreamOut o(p.out + (int64_t)row * n_embd + v_begin, (int64_t)nv * 4);
+
+    const int64_t tok = p.ids ? (int64_t)p.ids[row] : (int64_t)row;
+    if (tok < 0 || tok >= p.vocab) {
+        if (p.bad != nullptr && c == 0 && l == 0) atomicAdd(p.bad, 1u);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        gb[i] = (wave * NB + i) * 8 + (l >> 3);
-        ok[i] = false;
-        if (gb[i] < n_blocks) {
-            const int64_t row = gb[i] / p.nbr;
-            const int64_t b = gb[i] % p.nbr;
-            const int64_t tok = p.ids ? (int64_t)p.ids[row] : row;
-            if (tok >= 0 && tok < p.vocab) {
-                ok[i] = true;
-                load_raw(p.table + tok * p.rb + b * 34, l, raw[i]);
-            } else if (p.bad != nullptr && b == 0 && (l & 7) == 0) {
-                atomicAdd(p.bad, 1u);
-            }
-        }
+        for (int st = 0; st < U; ++st)
+            if (st * 256 + 4 * l < nv)
+                o.store((uint32_t)(st * 256 + 4 * l) * 4u, make_float4(0.f, 0.f, 0.f, 0.f));
+        return;
     }
-    const int64_t gb0 = wave * NB * 8;  // first block of the wave
-    const StreamOut o(p.out + gb0 * 32, (n_blocks - gb0) * 128);
+
+    // The run's blocks are contiguous: load the 4-byte words that cover them.
+    // The first word is aligned down, so the loads stay inside the words that
+    // hold the run's bytes (no access beyond the table's last word).
+    const uint8_t* g = p.table + tok * p.rb + (v_begin / Q::BV) * Q::BB;
+    const int off = (int)(reinterpret_cast<uintptr_t>(g) & 3u);
+    const uint32_t* g4 = reinterpret_cast<const uint32_t*>(g - off);
+    const int n_dw = (off + (nv / Q::BV) * Q::BB + 3) >> 2;
+    // Indices past the run re-read its last word, so every load is issued
+    // unconditionally and all of them are in flight together.
+    uint32_t w[PER];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        if (gb[i] >= n_blocks) continue;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (ok[i]) {
-            v = decode(raw[i], l);
-            if (p.scale > 0.0f) {
-                v.x = v.x * p.scale; v.y = v.y * p.scale;
-                v.z = v.z * p.scale; v.w = v.w * p.scale;
-            }
+    for (int i = 0; i < PER; ++i) w[i] = g4[min(l + 64 * i, n_dw - 1)];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) stage[l + 64 * i] = w[i];
+    __syncthreads();
+
+    const uint8_t* run = reinterpret_cast<const uint8_t*>(stage) + off;
+#pragma unroll
+    for (int st = 0; st < U; ++st) {
+        const int v0 = st * 256 + 4 * l;
+        if (v0 >= nv) break;
+        typename Q::Raw raw;
+        load_raw(run + (v0 / Q::BV) * Q::BB, l, raw);
+        float4 v = decode(raw, l);
+        if (p.scale > 0.0f) {
+            v.x = v.x * p.scale; v.y = v.y * p.scale;
+            v.z = v.z * p.scale; v.w = v.w * p.scale;
         }
-        o.store((uint32_t)(((gb[i] - gb0) * 32 + 4 * (l & 7)) * 4), v);
+        o.store((uint32_t)v0 * 4u, v);
     }
 }
 
-template <int TYPE, typename RAW>
-bool launch_gather(const char* name, GatherParams p, int64_t n_units, hipStream_t s) {
-    // Small gathers want many short waves (latency), large ones want more
-    // bytes in flight per wave: measured crossover ~128K units on MI355X.
-    const int nb = tune("gather_nb", n_units >= 131072 ? 2 : 1);
-    const int per_wave = nb >= 4 ? 4 : (nb >= 2 ? 2 : 1);
-    const int64_t waves = (n_units + per_wave - 1) / per_wave;
-    const int64_t blocks = (waves + 3) / 4;
-    if (blocks > 0x7fffffff) {
-        set_error("gather: grid too large");
+template <int TYPE>
+bool launch_rows(const char* name, GatherParams p, hipStream_t s) {
+    const int64_t n_embd = p.nbr * QT<TYPE>::BV;
+    const int64_t steps_per_row = (n_embd + 255) / 256;
+    // Run length, from a sweep of 1..16 on MI355X over the layer shapes:
+    // up to 64K steps, the shortest run that brings the grid down to 4096
+    // waves, widened to a whole row when it would leave a short last run in
+    // each row; beyond that, runs of 4 steps (16K x 8192 Q4_K: 98 us at 4,
+    // 110 us at 16, 135 us at 2).
+    const int64_t total = p.n_rows * steps_per_row;
+    int u = 4;
+    if (total <= 65536) {
+        u = 1;
+        while (u < 16 && p.n_rows * ((steps_per_row + u - 1) / u) > 4096) u *= 2;
+        if (steps_per_row % u != 0 && u < steps_per_row) {
+            int whole = 1;
+            while (whole < steps_per_row) whole *= 2;
+            if (whole <= 16) u = whole;
+        }
+    }
+    u = tune("gather_u", u);
+    const int64_t cpr = (steps_per_row + u - 1) / u;
+    const int64_t waves = p.n_rows * cpr;
+    if (waves > 0x7fffffff || cpr > 0x7fffffff) {
+        set_error("gather: grid too large (%lld waves)", (long long)waves);
         return false;
     }
-    if constexpr (TYPE == AERO_DTYPE_Q8_0) {
-        switch (per_wave) {
-        case 4: return launch(name, gather_q8_0_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, p);
-        case 2: return launch(name, gather_q8_0_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, p);
-        default: return launch(name, gather_q8_0_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, p);
-        }
-    } else {
-        switch (per_wave) {
-        case 4: return launch(name, gather_kernel<TYPE, RAW, 4>, dim3((unsigned)blocks), dim3(256), 0, s, p);
-        case 2: return launch(name, gather_kernel<TYPE, RAW, 2>, dim3((unsigned)blocks), dim3(256), 0, s, p);
-        default: return launch(name, gather_kernel<TYPE, RAW, 1>, dim3((unsigned)blocks), dim3(256), 0, s, p);
-        }
+    const dim3 grid((unsigned)waves), block(64);
+    switch (u) {
+    case 16: return launch(name, gather_rows_kernel<TYPE, 16>, grid, block, 0, s, p, (int)cpr);
+    case 8: return launch(name, gather_rows_kernel<TYPE, 8>, grid, block, 0, s, p, (int)cpr);
+    case 4: return launch(name, gather_rows_kernel<TYPE, 4>, grid, block, 0, s, p, (int)cpr);
+    case 2: return launch(name, gather_rows_kernel<TYPE, 2>, grid, block, 0, s, p, (int)cpr);
+    case 1: return launch(name, gather_rows_kernel<TYPE, 1>, grid, block, 0, s, p, (int)cpr);
+    default:
+        set_error("gather: run length %d not in {1,2,4,8,16}", u);
+        return false;
     }
 }
 
 bool run_gather(int dtype, GatherParams p, hipStream_t s) {
-    const int64_t nb = p.n_rows * p.nbr;
-    if (nb == 0) return true;
+    if (p.n_rows * p.nbr == 0) return true;
     switch (dtype) {
-    case AERO_DTYPE_Q8_0:  // units of 8 blocks of the flattened sequence
-        return launch_gather<AERO_DTYPE_Q8_0, RawQ8>("gather_q8_0_kernel", p, (nb + 7) / 8, s);
-    case AERO_DTYPE_Q4_K:
-        return launch_gather<AERO_DTYPE_Q4_K, RawQ4>("gather_kernel<Q4_K>", p, nb, s);
-    case AERO_DTYPE_Q6_K:
-        return launch_gather<AERO_DTYPE_Q6_K, RawQ6>("gather_kernel<Q6_K>", p, nb, s);
+    case AERO_DTYPE_Q8_0: return launch_rows<AERO_DTYPE_Q8_0>("gather_rows_kernel<Q8_0>", p, s);
+    case AERO_DTYPE_Q4_K: return launch_rows<AERO_DTYPE_Q4_K>("gather_rows_kernel<Q4_K>", p, s);
+    case AERO_DTYPE_Q6_K: return launch_rows<AERO_DTYPE_Q6_K>("gather_rows_kernel<Q6_K>", p, s);
     default:
         set_error("gather: unsupported dtype %d", dtype);
         return false;

@@ -25,6 +25,7 @@ single-threaded like the reference, over a bounded sample.
 
     python bench.py [--steps K] [--warmup W] [--sets S] [--cpu-seconds T]
     python bench.py --all-shapes        # per-op table over every layer shape
+    python bench.py --all-shapes --only OP   # one op over every layer shape
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
 """
@@ -61,7 +62,7 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--all-shapes", action="store_true")
     p.add_argument("--shapes", default=None, help="comma list for --all-shapes")
-    p.add_argument("--only", choices=OPS + ("rope_qk_norm", "gated_norm"), default=None)
+    p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
     p.add_argument("--copy-calibration", action="store_true")
     p.add_argument("--host-abi", action="store_true",
                    help="PCIe-inclusive rate of the reference-compatible host ABI")
@@ -440,9 +441,9 @@ def cpu_baseline(path, seconds):
 
 # ---------------------------------------------------------------- reports
 def traffic_from_profiles(kernel_tag):
-    """HBM bytes per launch of the dominant kernel from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
-    path = os.path.join(ROOT, "profiles", "swiglu_llama3_8b_prefill_counters.md")
+    """HBM bytes per launch of the dominant kernel (SwiGLU) from the committed
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "llama3_8b_prefill_counters.md")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read())
@@ -534,11 +535,14 @@ def all_shapes(a):
     for name in names:
         sets = a.sets if W.SHAPES[name].n_tok <= 4096 else 2
         path = Path(name, sets)
-        ker = kernel_times(path, max(20, a.steps // 4), 5)
-        sus = sustained_times(path, path.step_ops(), SUSTAINED_REPS)
+        ops_list = [a.only] if a.only else path.step_ops()
+        if a.only == "gated_norm" and not path.s.gated:
+            continue
+        ker = kernel_times(path, max(20, a.steps // 4), 5, a.only)
+        sus = sustained_times(path, ops_list, SUSTAINED_REPS)
         bts, rows = path.bytes(), path.rows()
         res[name] = {}
-        for op in path.step_ops():
+        for op in ops_list:
             res[name][op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3,
                                      sus[op])
         print(json.dumps({"shape": name, "ops": res[name]}), flush=True)

@@ -67,6 +67,35 @@ def test_gather_brute_force_rows(hip, oracle, t):
         assert bits_equal(got[i], row)
 
 
+@pytest.mark.parametrize("t,n_embd,rows", [
+    (W.Q8_0, 32 * 45, 32768),    # 2-byte aligned odd rows, runs of 4 steps, ragged tail
+    (W.Q6_K, 256 * 5, 40000),    # 2-byte aligned odd rows, runs of 4 steps, one-block tail
+    (W.Q4_K, 256 * 48, 8192),    # runs of 8 steps
+    (W.Q8_0, 32 * 7, 3),         # a row shorter than one 256-value step
+])
+def test_gather_run_lengths(hip, oracle, t, n_embd, rows):
+    """Long gathers take multi-step runs per wave; row lengths that are not a
+    whole number of runs, and rows that start 2 bytes past a 4-byte boundary,
+    still select and decode every value exactly. Some ids are out of range."""
+    rng = np.random.default_rng(n_embd + rows)
+    bv, bb = W.BLOCK[t]
+    vocab = 997
+    table = W.make_table(t, vocab * (n_embd // bv), rng)
+    ids = rng.integers(0, vocab, rows).astype(np.int32)
+    ids[::1009] = -5
+    ids[7::2003] = vocab
+    n_bad = int(((ids < 0) | (ids >= vocab)).sum())
+    print(f"gather runs type={t} n_embd={n_embd} rows={rows} bad={n_bad}", flush=True)
+    bad = DA.from_numpy(np.zeros(1, np.uint32))
+    e = {"type": t, "table": table, "vocab": vocab, "n_embd": n_embd, "ids": ids, "scale": 0.0}
+    got = gpu_gather(e, bad=bad)
+    assert int(bad.numpy()[0]) == n_bad
+    ok = (ids >= 0) & (ids < vocab)
+    assert not got[~ok].any()
+    want = oracle.embed_gather(t, table, vocab, n_embd, ids[ok])
+    assert bits_equal(got[ok], want)
+
+
 def test_dequant_types(hip, oracle):
     rng = np.random.default_rng(31)
     cases = [(W.F32, 4, 1), (W.F16, 2, 1), (W.BF16, 2, 1), (W.Q8_0, 34, 32), (W.Q4_K, 144, 256),
