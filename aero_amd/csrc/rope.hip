@@ -3,22 +3,27 @@
 // the token's position).
 //
 // Layout: q [n_tok, hq, D] and k [n_tok, hk, D]; a token's hq + hk head rows
-// share its position. A workgroup takes one token and a range of its heads.
-// Its first `half` lanes produce the token's cos/sin pairs once (fp32 angle
-// (float)pos*inv[p] then sincos, or a gather from a position-indexed table)
-// into LDS, so the transcendental work is per token, not per head row.
+// share its position. A workgroup takes a tile of TW consecutive tokens and
+// a group of their heads (TW x heads rows). Its lanes first produce the cos/sin
+// pairs of the tile's tokens (fp32 angle (float)pos*inv[p] then sincos, or a
+// gather from a position-indexed table) into LDS, so the transcendental work
+// is per token, not per head row.
 //
 // Each head row is owned by L lanes (L = D/8 when the whole row is touched,
-// n_rot/8 otherwise); every lane holds two float4 chunks:
-//   NeoX rotation lane j:        x[4j..4j+3]   and x[half+4j..half+4j+3]
-//   interleaved rotation lane j: x[8j..8j+3]   and x[8j+4..8j+7]
-//   pass-through lane j:         x[n_rot+8m .. n_rot+8m+7], m = j - n_rot/8
-// so both members of every rotated pair sit in the same lane and no shuffle
-// is needed for the rotation; the norm's sum of squares is an xor butterfly
-// over the L lanes. All loads of a lane's rows are issued before the LDS
-// barrier, and each element is read once and written once: HBM bytes per
-// head row 8*D (4*D read + 4*D written; 8*n_rot for an in-place partial
-// rotation without norm, which touches only the rotated channels).
+// n_rot/8 rounded up to a power of two otherwise), each holding two float4
+// chunks (chunk c = x[4c..4c+3]) chosen so that every load instruction of a
+// wave reads contiguous 16-byte chunks and both members of every rotated pair
+// sit in the same lane (no shuffle for the rotation):
+//   NeoX, rotating lane j < n_rot/8:   chunks j and j + n_rot/8 (x[p], x[p+half])
+//   NeoX, pass-through lane j:         chunks n_rot/4 + m and n_rot/4 + m + (L - n_rot/8),
+//                                      m = j - n_rot/8
+//   interleaved lane j:                chunks j and j + span (span = L, or n_rot/8
+//                                      in place), each rotated iff below n_rot
+// The norm's sum of squares is an xor butterfly over the L lanes. A lane owns
+// up to RPS rows of the tile; all their loads are issued before the LDS
+// barrier, and each element is read once and written once: HBM bytes per head
+// row 8*D (4*D read + 4*D written; 8*n_rot for an in-place partial rotation
+// without norm, which touches only the rotated channels).
 //
 // Arithmetic with contraction off, in the reference's order:
 // norm (x*inv)*w with inv = 1/sqrtf(ss/D + eps) (src/tensor.cpp:128-134);
@@ -51,11 +56,20 @@ struct RopeParams {
     const float* stab;
     int64_t n_tab;
     int hpw;      // heads per workgroup
-    int n_hg;     // workgroups per token
+    int n_hg;     // head groups per token tile
+    int tw;       // tokens per tile
     int do_tail;  // lanes beyond n_rot/8 carry the pass-through channels
 };
 
 constexpr int kRopeBlock = 256;
+constexpr int kRopeLds = kRopeBlock;  // cos (and sin) floats of one tile: TW * n_rot/2
+constexpr int kRopeMaxTw = 64;  // tokens per tile
+// Read-only stand-in for an absent positions array.
+// Global (not constant) memory on purpose: a select between them and a kernel
+// argument pointer then stays a global load (a constant-space address would
+// turn it into a flat load, which the compiler can only wait for with the
+// whole vector-memory counter).
+__device__ int32_t kZeroInt[1] = {0};
 
 __device__ __forceinline__ float4 ld4(const float* p) {
     return *reinterpret_cast<const float4*>(p);
@@ -77,95 +91,117 @@ __device__ __forceinline__ void rot2(float& x0, float& x1, float c, float s) {
     x1 = a * s + b * c;
 }
 
-template <int L, int RPS>
+// TABLE: angles from the position-indexed cos/sin table (else computed from
+// p.inv); one path per instantiation keeps the load counts exact.
+template <int L, int RPS, bool TABLE>
 __global__ __launch_bounds__(kRopeBlock)
 void rope_vec_kernel(RopeParams p) {
     constexpr int S = kRopeBlock / L;
-    __shared__ float4 cs_c[64];
-    __shared__ float4 cs_s[64];
+    __shared__ __align__(16) float cs_c[kRopeLds];
+    __shared__ __align__(16) float cs_s[kRopeLds];
+    static_assert(kRopeLds <= kRopeBlock, "one cos/sin entry per lane");
+    __shared__ int tok_ok[kRopeMaxTw];
 
     const int tid = threadIdx.x;
-    const int64_t t = blockIdx.x / p.n_hg;
-    const int hg = blockIdx.x % p.n_hg;
+    const int tile = (int)(blockIdx.x / p.n_hg);
+    const int hg = (int)(blockIdx.x - (unsigned)tile * p.n_hg);
+    const int64_t t0 = (int64_t)tile * p.tw;
+    const int tw = (int)min((int64_t)p.tw, p.n_tok - t0);
     const int NH = p.hq + p.hk;
     const int h0 = hg * p.hpw;
-    const int h1 = min(h0 + p.hpw, NH);
+    const int hn = min(h0 + p.hpw, NH) - h0;
+    const int rows = tw * hn;
     const int s = tid / L;
     const int j = tid % L;
     const int half = p.n_rot >> 1;
     const int r8 = p.n_rot >> 3;
 
-    const int64_t pt = p.pos ? (int64_t)p.pos[t] : t;
-    if (p.inv == nullptr && (pt < 0 || pt >= p.n_tab)) return;  // uniform per block
-
-    // element offsets of this lane's two chunks inside a head row
-    const bool rot = j < r8;
-    const bool active = rot || (p.do_tail && j < (p.D >> 3));
-    int a0, b0;
-    if (rot) {
-        a0 = p.mode == AERO_ROPE_NEOX ? 4 * j : 8 * j;
-        b0 = p.mode == AERO_ROPE_NEOX ? half + 4 * j : 8 * j + 4;
+    int cA, cB;
+    bool rotA, rotB;
+    if (p.mode == AERO_ROPE_NEOX) {
+        if (j < r8) {
+            cA = j; cB = j + r8; rotA = rotB = true;
+        } else {
+            cA = 2 * r8 + (j - r8); cB = cA + (L - r8); rotA = rotB = false;
+        }
     } else {
-        a0 = p.n_rot + 8 * (j - r8);
-        b0 = a0 + 4;
+        const int span = p.do_tail ? L : r8;
+        cA = j; cB = j + span;
+        rotA = cA < 2 * r8; rotB = cB < 2 * r8;
     }
+    const bool active = p.do_tail || j < r8;
+    const int a0 = 4 * cA, b0 = 4 * cB;
 
+    // The position (and inverse frequency) of this lane's cos/sin entry is
+    // loaded first, from a clamped index, and used only after the row loads
+    // are issued: the vector-memory counter retires in order, so the angle is
+    // computed while the rows are in flight. Without positions the load reads
+    // a one-element stand-in with stride 0, so no branch separates the load
+    // from its use.
+    const int n_fill = tw * half;  // <= kRopeBlock: one entry per lane
+    const int fidx = min(tid, n_fill > 0 ? n_fill - 1 : 0);
+    const int hdiv = half > 0 ? half : 1;
+    const int fti = fidx / hdiv;
+    const int fq = fidx - fti * hdiv;
+    const int32_t* pos_base = p.pos != nullptr ? p.pos + t0 : kZeroInt;
+    const int pos_step = p.pos != nullptr ? 1 : 0;
+    const int fpos = pos_base[fti * pos_step];
+    const float finv = TABLE ? 0.0f : p.inv[fq];
+    const int my_pos = pos_base[min(tid, tw - 1) * pos_step];  // token `tid` of the tile
+
+    // Row loads are unconditional too (a lane past the tile's rows re-reads
+    // its last row, an idle lane reads chunk 0), so the compiler knows how
+    // many loads follow the position loads; invalid values are masked later.
     float4 A[RPS], B[RPS];
-    const float* wrow[RPS];
-    int rowoff[RPS];   // element offset of the row inside its token's q or k block
-    bool isq_row[RPS];
-    bool valid[RPS];
 #pragma unroll
     for (int i = 0; i < RPS; ++i) {
-        const int h = h0 + s + S * i;
-        valid[i] = active && h < h1;
-        A[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        B[i] = A[i];
-        wrow[i] = nullptr;
-        rowoff[i] = 0;
-        isq_row[i] = true;
-        if (h < h1) {
-            const bool isq = h < p.hq;
-            isq_row[i] = isq;
-            rowoff[i] = (isq ? h : h - p.hq) * p.D;
-            const int64_t roff = t * (int64_t)(isq ? p.hq : p.hk) * p.D + rowoff[i];
-            const float* src = (isq ? p.q : p.k) + roff;
-            wrow[i] = isq ? p.q_w : p.k_w;
-            if (valid[i]) {
-                A[i] = ld_stream(src + a0);
-                B[i] = ld_stream(src + b0);
-            }
-        }
+        const int r = min(s + S * i, rows - 1);
+        const int ti = p.tw == 1 ? 0 : r / hn;
+        const int h = h0 + (r - ti * hn);
+        const bool isq = h < p.hq;
+        const int64_t roff = ((t0 + ti) * (isq ? p.hq : p.hk) + (isq ? h : h - p.hq)) *
+                             (int64_t)p.D;
+        const float* src = (isq ? p.q : p.k) + roff;
+        A[i] = ld_stream(src + (active ? a0 : 0));
+        B[i] = ld_stream(src + (active ? b0 : 0));
     }
 
-    // the token's cos/sin for pairs 0..half-1, once per workgroup
-    if (tid < half) {
-        float c, sn;
-        if (p.inv != nullptr) {
-            const float ang = (float)pt * p.inv[tid];
+    // cos/sin of pairs 0..half-1 for each token of the tile (lanes past the
+    // tile's entries compute a copy of the last one and do not store it)
+    if (tid < tw) {  // a token outside its table is left untouched
+        const int64_t pt = p.pos != nullptr ? (int64_t)my_pos : t0 + tid;
+        tok_ok[tid] = !TABLE || (pt >= 0 && pt < p.n_tab);
+    }
+    if (n_fill > 0) {
+        const int64_t pt = p.pos != nullptr ? (int64_t)fpos : t0 + fti;
+        float c = 1.0f, sn = 0.0f;
+        if (!TABLE) {
+            const float ang = (float)pt * finv;
             sincosf(ang, &sn, &c);
-        } else {
-            c = p.ctab[pt * half + tid];
-            sn = p.stab[pt * half + tid];
+        } else if (p.n_tab > 0) {  // clamped read; out-of-table tokens are skipped
+            const int64_t pc = pt < 0 ? 0 : (pt >= p.n_tab ? p.n_tab - 1 : pt);
+            c = p.ctab[pc * half + fq];
+            sn = p.stab[pc * half + fq];
         }
-        reinterpret_cast<float*>(cs_c)[tid] = c;
-        reinterpret_cast<float*>(cs_s)[tid] = sn;
+        if (tid < n_fill) {
+            cs_c[tid] = c;
+            cs_s[tid] = sn;
+        }
     }
     __syncthreads();
 
-    // this token's q rows and k rows, each a contiguous block of heads x D
-    const StreamOut oq(p.q_out + t * (int64_t)p.hq * p.D, (int64_t)p.hq * p.D * 4);
-    const StreamOut ok_(p.hk > 0 ? p.k_out + t * (int64_t)p.hk * p.D : p.q_out,
-                        (int64_t)p.hk * p.D * 4);
-
-    float4 c4 = make_float4(1.f, 1.f, 1.f, 1.f), s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (rot) {
-        c4 = cs_c[j];
-        s4 = cs_s[j];
-    }
+    // the tile's q rows and k rows, each a contiguous block of tokens x heads x D
+    const StreamOut oq(p.q_out + t0 * p.hq * (int64_t)p.D, (int64_t)tw * p.hq * p.D * 4);
+    const StreamOut ok_(p.hk > 0 ? p.k_out + t0 * p.hk * (int64_t)p.D : p.q_out,
+                        (int64_t)tw * p.hk * p.D * 4);
 
 #pragma unroll
     for (int i = 0; i < RPS; ++i) {
+        const int r = s + S * i;
+        if (!active || r >= rows) {
+            A[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            B[i] = A[i];
+        }
         // sum of squares over the whole head row (all L lanes of the slot)
         float ss = 0.0f;
         ss += A[i].x * A[i].x; ss += A[i].y * A[i].y;
@@ -173,32 +209,51 @@ void rope_vec_kernel(RopeParams p) {
         ss += B[i].x * B[i].x; ss += B[i].y * B[i].y;
         ss += B[i].z * B[i].z; ss += B[i].w * B[i].w;
         ss = group_sum<L>(ss);
-        if (!valid[i]) continue;
-        if (wrow[i] != nullptr) {
+        if (!active || r >= rows) continue;
+        const int ti = p.tw == 1 ? 0 : r / hn;
+        const int h = h0 + (r - ti * hn);
+        const bool isq = h < p.hq;
+        if (!tok_ok[ti]) continue;
+        const float* w = isq ? p.q_w : p.k_w;
+        if (w != nullptr) {
             const float inv = 1.0f / sqrtf(ss / (float)p.D + p.eps);
-            A[i] = wmul(A[i], inv, wrow[i] + a0, p.norm_flags);
-            B[i] = wmul(B[i], inv, wrow[i] + b0, p.norm_flags);
+            A[i] = wmul(A[i], inv, w + a0, p.norm_flags);
+            B[i] = wmul(B[i], inv, w + b0, p.norm_flags);
         }
-        if (rot) {
-            if (p.mode == AERO_ROPE_NEOX) {
+        const float* cc = cs_c + ti * half;
+        const float* sc = cs_s + ti * half;
+        if (p.mode == AERO_ROPE_NEOX) {
+            if (rotA) {
+                const float4 c4 = *reinterpret_cast<const float4*>(cc + 4 * j);
+                const float4 s4 = *reinterpret_cast<const float4*>(sc + 4 * j);
                 rot2(A[i].x, B[i].x, c4.x, s4.x);
                 rot2(A[i].y, B[i].y, c4.y, s4.y);
                 rot2(A[i].z, B[i].z, c4.z, s4.z);
                 rot2(A[i].w, B[i].w, c4.w, s4.w);
-            } else {
-                rot2(A[i].x, A[i].y, c4.x, s4.x);
-                rot2(A[i].z, A[i].w, c4.y, s4.y);
-                rot2(B[i].x, B[i].y, c4.z, s4.z);
-                rot2(B[i].z, B[i].w, c4.w, s4.w);
+            }
+        } else {
+            if (rotA) {
+                const float2 c2 = *reinterpret_cast<const float2*>(cc + 2 * cA);
+                const float2 s2 = *reinterpret_cast<const float2*>(sc + 2 * cA);
+                rot2(A[i].x, A[i].y, c2.x, s2.x);
+                rot2(A[i].z, A[i].w, c2.y, s2.y);
+            }
+            if (rotB) {
+                const float2 c2 = *reinterpret_cast<const float2*>(cc + 2 * cB);
+                const float2 s2 = *reinterpret_cast<const float2*>(sc + 2 * cB);
+                rot2(B[i].x, B[i].y, c2.x, s2.x);
+                rot2(B[i].z, B[i].w, c2.y, s2.y);
             }
         }
-        const uint32_t off = (uint32_t)(rowoff[i] + a0) * 4u;
-        const uint32_t offb = (uint32_t)(rowoff[i] + b0) * 4u;
-        if (isq_row[i]) {
-            oq.store(off, A[i]);
+        const uint32_t row_off =
+            (uint32_t)((ti * (isq ? p.hq : p.hk) + (isq ? h : h - p.hq)) * p.D);
+        const uint32_t offa = (row_off + (uint32_t)a0) * 4u;
+        const uint32_t offb = (row_off + (uint32_t)b0) * 4u;
+        if (isq) {
+            oq.store(offa, A[i]);
             oq.store(offb, B[i]);
         } else {
-            ok_.store(off, A[i]);
+            ok_.store(offa, A[i]);
             ok_.store(offb, B[i]);
         }
     }
@@ -264,31 +319,36 @@ void rope_tables_kernel(const int32_t* pos, int64_t n_pos, const float* inv,
 
 using RopeKernel = void (*)(RopeParams);
 
-template <int L>
+template <int L, bool TABLE>
 RopeKernel pick_rps(int rps) {
     switch (rps) {
-    case 1: return rope_vec_kernel<L, 1>;
-    case 2: return rope_vec_kernel<L, 2>;
-    case 3: return rope_vec_kernel<L, 3>;
-    case 4: return rope_vec_kernel<L, 4>;
-    case 5: return rope_vec_kernel<L, 5>;
-    case 6: return rope_vec_kernel<L, 6>;
-    case 7: return rope_vec_kernel<L, 7>;
-    case 8: return rope_vec_kernel<L, 8>;
+    case 1: return rope_vec_kernel<L, 1, TABLE>;
+    case 2: return rope_vec_kernel<L, 2, TABLE>;
+    case 3: return rope_vec_kernel<L, 3, TABLE>;
+    case 4: return rope_vec_kernel<L, 4, TABLE>;
+    case 5: return rope_vec_kernel<L, 5, TABLE>;
+    case 6: return rope_vec_kernel<L, 6, TABLE>;
+    case 7: return rope_vec_kernel<L, 7, TABLE>;
+    case 8: return rope_vec_kernel<L, 8, TABLE>;
     default: return nullptr;
     }
 }
 
-RopeKernel pick_rope(int L, int rps) {
+template <bool TABLE>
+RopeKernel pick_l(int L, int rps) {
     switch (L) {
-    case 2: return pick_rps<2>(rps);
-    case 4: return pick_rps<4>(rps);
-    case 8: return pick_rps<8>(rps);
-    case 16: return pick_rps<16>(rps);
-    case 32: return pick_rps<32>(rps);
-    case 64: return pick_rps<64>(rps);
+    case 2: return pick_rps<2, TABLE>(rps);
+    case 4: return pick_rps<4, TABLE>(rps);
+    case 8: return pick_rps<8, TABLE>(rps);
+    case 16: return pick_rps<16, TABLE>(rps);
+    case 32: return pick_rps<32, TABLE>(rps);
+    case 64: return pick_rps<64, TABLE>(rps);
     default: return nullptr;
     }
+}
+
+RopeKernel pick_rope(int L, int rps, bool table) {
+    return table ? pick_l<true>(L, rps) : pick_l<false>(L, rps);
 }
 
 int next_pow2(int v) {
@@ -318,31 +378,55 @@ bool qk_norm_rope(RopeParams p, hipStream_t stream) {
     }
     const int64_t blocks_cap = 0x7fffffff;
     if (vec) {
+        // Heads of one token are split into groups only when they exceed
+        // rps_max rows per lane, or to reach min_wg workgroups on short inputs.
         const int S = kRopeBlock / L;
-        const int need = (NH + S - 1) / S;
-        const int rps_max = tune("rope_rps_max", 8);
+        const int rps_max = std::min(8, std::max(1, tune("rope_rps_max", 8)));
         const int64_t min_wg = tune("rope_min_wg", 1024);
-        int rps = need < rps_max ? need : rps_max;
-        if (rps < 1) rps = 1;
-        int n_hg = 1;
-        for (;; --rps) {
-            n_hg = (NH + S * rps - 1) / (S * rps);
-            if (rps == 1 || p.n_tok * n_hg >= min_wg) break;
-        }
-        p.n_hg = n_hg;
+        const int half = p.n_rot / 2;
+        int n_hg = (NH + S * rps_max - 1) / (S * rps_max);
+        while (p.n_tok * n_hg < min_wg && (NH + n_hg - 1) / n_hg > S) ++n_hg;
         p.hpw = (NH + n_hg - 1) / n_hg;
-        rps = (p.hpw + S - 1) / S;
-        if (rps > 8) {  // more heads than 8 slots per lane group: add groups
-            p.n_hg = (NH + S * 8 - 1) / (S * 8);
-            p.hpw = (NH + p.n_hg - 1) / p.n_hg;
-            rps = (p.hpw + S - 1) / S;
+        p.n_hg = (NH + p.hpw - 1) / p.hpw;
+        // Tiles of several tokens only pay when one token per workgroup already
+        // gives several rounds of workgroups (>= 4096): then tiles grow while a
+        // workgroup moves < 64 KB and the grid keeps >= 512 workgroups. Swept
+        // on MI355X over 1/2/4/8 tokens: 4096 x 18 heads, in-place 64/256
+        // partial rotation 10.1 -> 8.6 us at 8 tokens; every other layer shape
+        // equal or slower with tiles.
+        const int64_t row_bytes = 8 * (int64_t)(p.do_tail ? p.D : p.n_rot);
+        int tw = 1;
+        if (p.n_tok * p.n_hg >= 4096)
+            while (2 * tw <= kRopeMaxTw && 2 * tw * (half > 0 ? half : 1) <= kRopeLds &&
+                   (2 * tw * p.hpw + S - 1) / S <= rps_max &&
+                   (int64_t)tw * p.hpw * row_bytes < 65536 &&
+                   ((p.n_tok + 2 * tw - 1) / (2 * tw)) * p.n_hg >= 512)
+                tw *= 2;
+        // an override is clamped to what fits: LDS, 8 rows per lane, 64 tokens
+        int t = tune("rope_tw", tw);
+        while (t > 1 && (t > kRopeMaxTw || t * half > kRopeLds || (t * p.hpw + S - 1) / S > 8))
+            t /= 2;
+        p.tw = t < 1 ? 1 : t;
+        const int64_t hmax = p.hq > p.hk ? p.hq : p.hk;
+        if ((int64_t)p.tw * hmax * p.D * 4 >= ((int64_t)1 << 31)) vec = false;
+    }
+    if (vec) {
+        const int S = kRopeBlock / L;
+        const int rps = (p.tw * p.hpw + S - 1) / S;
+        const int half = p.n_rot / 2;
+        if (rps < 1 || rps > 8 || p.tw < 1 || p.tw > kRopeMaxTw || p.tw * half > kRopeLds) {
+            set_error("qk_norm_rope: tile of %d tokens does not fit", p.tw);
+            return false;
         }
-        const int64_t blocks = p.n_tok * p.n_hg;
+        const int64_t blocks = ((p.n_tok + p.tw - 1) / p.tw) * p.n_hg;
         if (blocks > blocks_cap) {
             set_error("qk_norm_rope: grid too large");
             return false;
         }
-        return launch("rope_vec_kernel", pick_rope(L, rps), dim3((unsigned)blocks),
+        // without inv_freq: a table, or nothing rotates (n_rot < 2, no table,
+        // every token valid), which the table kernel handles without reads
+        const bool table = p.inv == nullptr;
+        return launch("rope_vec_kernel", pick_rope(L, rps, table), dim3((unsigned)blocks),
                       dim3(kRopeBlock), 0, stream, p);
     }
     const int64_t blocks = p.n_tok * NH;
@@ -460,8 +544,11 @@ int aero_hip_qk_norm_rope(float* q, float* q_out, int64_t n_q_heads, float* k,
     p.ctab = cos_tab;
     p.stab = sin_tab;
     p.n_tab = have_tab ? n_tab : 0;
-    if (p.n_rot < 2 && p.inv == nullptr && !have_tab) {
-        // nothing rotates: keep the norm/copy path (it never reads a table)
+    if (p.n_rot < 2) {
+        // nothing rotates: the norm/copy path reads no angle source, and every
+        // token counts as inside the (absent) table
+        p.inv = nullptr;
+        p.ctab = p.stab = nullptr;
         p.n_tab = (int64_t)1 << 62;
         p.pos = nullptr;
     }

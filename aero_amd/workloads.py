@@ -25,7 +25,7 @@ Shapes:
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 
@@ -54,6 +54,7 @@ class Shape:
     rope_table: int = 0     # rows of a dense pre-computed table, 0 = computed angle
     emb_scale: bool = False
     gated: tuple = ()       # (n_v, d) of the gated norm, when the shape has one
+    rope_mode: int = 0      # 0 NeoX, 1 interleaved
     extra: dict = field(default_factory=dict)
 
 
@@ -76,6 +77,31 @@ SHAPES = {
 
 # the shape the headline metric is quoted on
 HEADLINE = "llama3_8b_prefill"
+
+
+def _l8b(name, **kw):
+    return replace(SHAPES[HEADLINE], name=name, **kw)
+
+
+# Every op variant of the path at the Llama-3-8B 512-token geometry
+# (R=512, N=4096, 32/8 heads x 128, FFN 14336): name -> (shape, op).
+VARIANTS = {
+    "rmsnorm": (SHAPES[HEADLINE], "rmsnorm"),
+    "rmsnorm_unit_offset": (_l8b("rmsnorm_unit_offset", unit_offset=True), "rmsnorm"),
+    "gated_norm_32x128": (_l8b("gated_norm_32x128", gated=(32, 128)), "gated_norm"),
+    "rope_neox": (SHAPES[HEADLINE], "rope_qk"),
+    "rope_interleaved": (_l8b("rope_interleaved", rope_mode=1), "rope_qk"),
+    "rope_partial64_in_place": (_l8b("rope_partial64_in_place", n_rot=64), "rope_qk"),
+    "rope_table": (_l8b("rope_table", rope_table=512), "rope_qk"),
+    "qk_norm_rope": (_l8b("qk_norm_rope", qk_norm=True), "rope_qk"),
+    "swiglu": (SHAPES[HEADLINE], "swiglu"),
+    "geglu_erf": (_l8b("geglu_erf", act="gelu"), "swiglu"),
+    "geglu_tanh": (_l8b("geglu_tanh", act="gelu_tanh"), "swiglu"),
+    "gather_q4_k": (SHAPES[HEADLINE], "embed_gather"),
+    "gather_q8_0": (_l8b("gather_q8_0", emb_type=Q8_0), "embed_gather"),
+    "gather_q6_k_scaled": (_l8b("gather_q6_k_scaled", emb_type=Q6_K, emb_scale=True),
+                           "embed_gather"),
+}
 
 
 def positions(s: Shape, rng) -> np.ndarray:

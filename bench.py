@@ -11,21 +11,24 @@ Cache still holds from the previous use of its set.
 A step replays a recorded plan (aero_hip_plan_launch: the four kernels
 issued from C, one host call per step). `value` is the whole step's
 algorithmic HBM bytes / wall time per step over the timed region (GB/s).
-`roofline` is the dominant kernel (SwiGLU, 88 MB per launch): its algorithmic
-bytes / its mean device duration, measured with HIP events recorded by the
-kernel's own dispatch (hipExtLaunchKernel) over a second region of the same
-run that replays the same plans with an event pair per kernel (events per
-kernel serialise the host side, so that region times kernels, not steps).
-Each entry of `ops` gives that per-dispatch figure (`kernel_us`, `frac`) and
-a sustained one (`sustained_us`, `sustained_frac`): the op alone, launched
-back to back over its own > 1 GiB rotation of buffers, timed by one event
-pair around the whole region. `cpu_baseline` is the same step on the host: the reference's own C++
+Each entry of `ops` gives two device timings of the op: per dispatch
+(`kernel_us`, `frac`: a second region of the same run replays the same plans
+with an event pair recorded by each kernel's own dispatch, hipExtLaunchKernel;
+events per kernel serialise the host side, so that region times kernels, not
+steps) and sustained (`sustained_us`, `sustained_frac`: the op alone, launched
+back to back on one stream over its own > 1 GiB rotation of buffers, with one
+HIP event pair on that stream around the whole region; mean duration =
+region / launches). `roofline` is the dominant kernel (SwiGLU, 88 MB per
+launch): algorithmic bytes / its sustained mean launch duration (the
+per-dispatch figure is kept beside it; a rare slow dispatch moves that mean
+by several percent). `cpu_baseline` is the same step on the host: the reference's own C++
 (built into oracle/_ref) when present, else the oracle's restatement,
 single-threaded like the reference, over a bounded sample.
 
     python bench.py [--steps K] [--warmup W] [--sets S] [--cpu-seconds T]
     python bench.py --all-shapes        # per-op table over every layer shape
     python bench.py --all-shapes --only OP   # one op over every layer shape
+    python bench.py --variants          # every op variant at the 512-token shape
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
 """
@@ -61,7 +64,9 @@ def parse_args(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--all-shapes", action="store_true")
-    p.add_argument("--shapes", default=None, help="comma list for --all-shapes")
+    p.add_argument("--shapes", default=None, help="comma list for --all-shapes / --variants")
+    p.add_argument("--variants", action="store_true",
+                   help="every op variant at the Llama-3-8B 512-token geometry")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
     p.add_argument("--copy-calibration", action="store_true")
     p.add_argument("--host-abi", action="store_true",
@@ -75,7 +80,7 @@ def parse_args(argv=None):
 class StepBuffers:
     """One buffer set of a step, in HBM."""
 
-    def __init__(self, s, d_table, rng):
+    def __init__(self, s, d_table, rng, only=None):
         from aero_amd.device import DeviceArray as DA
 
         R = s.n_tok
@@ -83,16 +88,23 @@ class StepBuffers:
         def normal(*shape):
             return DA.from_numpy(rng.standard_normal(shape, dtype=np.float32))
 
-        self.ids = DA.from_numpy(rng.integers(0, s.vocab, R).astype(np.int32))
-        self.emb_out = DA.empty((R, s.hidden))
-        self.x = normal(R, s.hidden)
-        self.h = DA.empty((R, s.hidden))
-        self.q = normal(R, s.hq, s.head_dim)
-        self.k = normal(R, s.hk, s.head_dim)
-        self.gate = normal(R, s.ffn)
-        self.up = normal(R, s.ffn)
-        self.act_out = DA.empty((R, s.ffn))
-        if s.gated:
+        def want(op):
+            return only is None or only == op
+
+        if want("embed_gather"):
+            self.ids = DA.from_numpy(rng.integers(0, s.vocab, R).astype(np.int32))
+            self.emb_out = DA.empty((R, s.hidden))
+        if want("rmsnorm"):
+            self.x = normal(R, s.hidden)
+            self.h = DA.empty((R, s.hidden))
+        if want("rope_qk"):
+            self.q = normal(R, s.hq, s.head_dim)
+            self.k = normal(R, s.hk, s.head_dim)
+        if want("swiglu"):
+            self.gate = normal(R, s.ffn)
+            self.up = normal(R, s.ffn)
+            self.act_out = DA.empty((R, s.ffn))
+        if s.gated and want("gated_norm"):
             n_v, dd = s.gated
             self.gx = normal(R, n_v * dd)
             self.gz = normal(R, n_v * dd)
@@ -125,18 +137,21 @@ class StepBuffers:
 class Path:
     """The ops of one shape, bound to device constants."""
 
-    def __init__(self, name, sets, seed=0):
+    def __init__(self, name, sets, seed=0, shape=None, only=None):
         from aero_amd import ops
         from aero_amd import workloads as W
         from aero_amd.device import DeviceArray as DA
 
         self.ops, self.W = ops, W
-        s = W.SHAPES[name]
+        s = shape if shape is not None else W.SHAPES[name]
         self.s = s
+        self.only = only
         rng = np.random.default_rng(seed)
         bv, bb = W.BLOCK[s.emb_type]
-        self.table_host = W.make_table(s.emb_type, s.vocab * (s.hidden // bv), rng)
-        self.table = DA.from_numpy(self.table_host)
+        self.table = self.table_host = None
+        if only in (None, "embed_gather"):
+            self.table_host = W.make_table(s.emb_type, s.vocab * (s.hidden // bv), rng)
+            self.table = DA.from_numpy(self.table_host)
         w = rng.standard_normal(s.hidden, dtype=np.float32) * np.float32(0.1)
         self.w = DA.from_numpy(w if s.unit_offset else np.float32(1) + w)
         self.pos_host = W.positions(s, rng)
@@ -158,7 +173,7 @@ class Path:
         if s.gated:
             self.gw = DA.from_numpy(np.float32(1) + rng.standard_normal(s.gated[1],
                                                                         dtype=np.float32) * 0.1)
-        self.sets = [StepBuffers(s, self.table, rng) for _ in range(sets)]
+        self.sets = [StepBuffers(s, self.table, rng, only) for _ in range(sets)]
         self.scale = float(np.float32(np.sqrt(s.hidden))) if s.emb_scale else 0.0
 
     def bytes(self):
@@ -197,7 +212,8 @@ class Path:
             ops.qk_norm_rope(b.q, s.hq, s.n_tok, s.head_dim, s.n_rot, k=b.k, n_k_heads=s.hk,
                              q_norm_w=self.qk_w[0] if self.qk_w else None,
                              k_norm_w=self.qk_w[1] if self.qk_w else None, eps=s.eps,
-                             unit_offset=s.unit_offset, pos=self.pos, stream=stream, **kw)
+                             unit_offset=s.unit_offset, mode=s.rope_mode, pos=self.pos,
+                             stream=stream, **kw)
         elif op == "swiglu":
             ops.act_mul(s.act, b.gate, b.up, b.act_out, stream=stream)
         elif op == "gated_norm":
@@ -207,6 +223,8 @@ class Path:
             raise ValueError(op)
 
     def step_ops(self):
+        if self.only:
+            return [self.only]
         return list(OPS) + (["gated_norm"] if self.s.gated else [])
 
 
@@ -470,6 +488,8 @@ def main(argv=None):
         return launch_floor(a)
     if a.all_shapes:
         return all_shapes(a)
+    if a.variants:
+        return variants(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -492,7 +512,7 @@ def main(argv=None):
         per_op[op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3, sus[op])
         per_op[op]["kernel_us_median"] = round(statistics.median(ker[op]) * 1e3, 3)
     dom = "swiglu"
-    ach = per_op[dom]["GB/s"]
+    ach = per_op[dom]["sustained_GB/s"]
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(wall, 5),
@@ -507,7 +527,8 @@ def main(argv=None):
         "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                      "kernel": "act_vec_kernel<silu> (SwiGLU 512x14336)",
-                     "bytes_per_launch": bts[dom]},
+                     "bytes_per_launch": bts[dom], "launch_us": per_op[dom]["sustained_us"],
+                     "per_dispatch_GB/s": per_op[dom]["GB/s"]},
         "ops": per_op,
     }
     if not a.no_cpu:
@@ -546,6 +567,23 @@ def all_shapes(a):
             res[name][op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3,
                                      sus[op])
         print(json.dumps({"shape": name, "ops": res[name]}), flush=True)
+        del path
+    return 0
+
+
+def variants(a):
+    """Every op variant at the Llama-3-8B 512-token geometry: per-dispatch and
+    sustained time, GB/s and fraction of peak, one JSON line per variant."""
+    from aero_amd import workloads as W
+
+    names = a.shapes.split(",") if a.shapes else list(W.VARIANTS)
+    for name in names:
+        shape, op = W.VARIANTS[name]
+        path = Path(name, a.sets, shape=shape, only=op)
+        ker = kernel_times(path, max(20, a.steps // 4), 5, op)
+        sus = sustained_times(path, [op], SUSTAINED_REPS)
+        e = op_entry(path.bytes()[op], path.rows()[op], statistics.mean(ker[op]) * 1e3, sus[op])
+        print(json.dumps({"variant": name, "op": op, **e}), flush=True)
         del path
     return 0
 

@@ -119,6 +119,45 @@ def test_rope_variants(hip, oracle, D, n_rot, mode, norm, oop):
     assert rel_to_scale(gk, wk) <= RTOL
 
 
+@pytest.mark.parametrize("mode,n_rot,norm,oop,table", [
+    (0, 64, False, False, False), (1, 64, True, False, False), (0, 32, True, False, False),
+    (1, 16, False, True, False), (0, 16, False, False, False), (1, 32, False, False, True),
+    (0, 64, True, False, True)])
+def test_rope_token_tiles(hip, oracle, mode, n_rot, norm, oop, table):
+    """Long inputs are processed in tiles of several tokens per workgroup (the
+    cos/sin of each token of the tile in LDS): 16411 tokens leave a ragged last
+    tile; with a table, tokens whose position is outside it sit inside tiles
+    and must be left untouched while their neighbours are rotated."""
+    rng = np.random.default_rng(1000 + 10 * n_rot + mode)
+    T, H, HK, D = 16411, 5, 1, 64
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    k = rng.standard_normal((T, HK, D)).astype(np.float32)
+    pos = rng.integers(0, 4096, T).astype(np.int32)
+    tab = None
+    bad = np.zeros(T, bool)
+    if table:
+        tab = oracle.rope_tables(n_rot, np.arange(4000, dtype=np.int32), 1e4)
+        bad = pos >= 4000
+        pos[::997] = -3
+        bad[::997] = True
+    qw = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    kw = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    print(f"rope tiles T={T} mode={mode} n_rot={n_rot} norm={norm} oop={oop} table={table} "
+          f"bad={int(bad.sum())}", flush=True)
+    gq, gk = gpu_rope(q, pos, D, n_rot, k=k, theta=1e4, mode=mode, q_w=qw, k_w=kw,
+                      out_of_place=oop, table=tab)
+    ok = ~bad
+    wq = oracle_rope(oracle, q[ok], pos[ok], D, n_rot, 1e4, mode, qw, table=tab)
+    wk = oracle_rope(oracle, k[ok], pos[ok], D, n_rot, 1e4, mode, kw, table=tab)
+    if table and not norm:  # same cos/sin, same operations: bit-exact
+        assert bits_equal(gq[ok], wq) and bits_equal(gk[ok], wk)
+    else:  # computed angles, or the norm's tree sum of squares
+        assert rel_to_scale(gq[ok], wq) <= RTOL
+        assert rel_to_scale(gk[ok], wk) <= RTOL
+    if table and not oop:
+        assert bits_equal(gq[bad], q[bad]) and bits_equal(gk[bad], k[bad])
+
+
 @pytest.mark.parametrize("D,n_rot", [(80, 80), (80, 32), (6, 4), (10, 6), (24, 12), (64, 63)])
 def test_rope_generic_kernel(hip, oracle, D, n_rot):
     """Shapes outside the vector kernel (D or n_rot not a multiple of 8, or
