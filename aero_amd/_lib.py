@@ -51,6 +51,8 @@ PROTOTYPES = {
     "aero_hardware_threads": (c_int, []),
     "aero_dequant_ref": (c_int, [c_int, u8p, c_int64, fp, c_int64]),
     "aero_dequant_threaded": (c_int, [c_int, u8p, c_int64, fp, c_int64, c_int]),
+    "aero_matvec": (c_int, [c_int, u8p, fp, fp, c_int64, c_int64, c_int]),
+    "aero_matmul": (c_int, [c_int, u8p, fp, fp, c_int64, c_int64, c_int64, c_int]),
     # device-pointer fused ops
     "aero_hip_rmsnorm": (c_int, [vp, vp, vp, c_int64, c_int64, c_float, c_int, vp]),
     "aero_hip_gated_rmsnorm_silu": (c_int, [vp, vp, vp, c_int64, vp, c_int64, c_int64,
@@ -64,6 +66,7 @@ PROTOTYPES = {
     "aero_hip_embed_gather": (c_int, [c_int, vp, c_int64, c_int64, c_int64, vp, c_int64,
                                       c_float, vp, vp, vp]),
     "aero_hip_dequant": (c_int, [c_int, vp, c_int64, vp, c_int64, vp]),
+    "aero_hip_matvec": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp]),
     "aero_hip_copy_f32": (c_int, [vp, vp, c_int64, vp]),
     # runtime
     "aero_hip_last_error": (c_char_p, []),

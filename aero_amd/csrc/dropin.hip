@@ -34,6 +34,8 @@ bool dequant_dev(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
                  int64_t n_values, hipStream_t s);
 int64_t dtype_block_bytes(int t);
 int64_t dtype_block_values(int t);
+bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
+              int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s);
 
 namespace {
 
@@ -322,7 +324,8 @@ int aero_dequant_ref(int t, const uint8_t* raw, int64_t raw_len, float* out,
                      int64_t n_values) {
     const int64_t bv = aero::dtype_block_values(t), bb = aero::dtype_block_bytes(t);
     const bool known = t == AERO_DTYPE_F32 || t == AERO_DTYPE_F16 || t == AERO_DTYPE_BF16 ||
-                       t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q6_K;
+                       t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q5_K ||
+                       t == AERO_DTYPE_Q6_K || t == AERO_DTYPE_IQ4_XS;
     if (!known || bv <= 0 || !raw || !out || n_values < 0) {
         set_error("aero_dequant_ref: dtype %d not supported on the GPU path or bad args", t);
         return 0;
@@ -344,6 +347,53 @@ int aero_dequant_ref(int t, const uint8_t* raw, int64_t raw_len, float* out,
                                       static_cast<float*>(p[1]), n_values, st.stream()) &&
                     st.d2h(out, p[1], obytes) && st.finish();
     return ok ? 1 : 0;
+}
+
+// src/kernels.cpp:497-538 through :605-615: refuse what the reference refuses
+// (a type without a block dot, n_cols % bv), stage W and X, one GEMV launch
+// per call.
+static int host_gemv(int t, const uint8_t* w, const float* X, float* Y, int64_t n_tok,
+                     int64_t n_rows, int64_t n_cols) {
+    aero::clear_error();
+    const bool quant = t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q5_K ||
+                       t == AERO_DTYPE_Q6_K || t == AERO_DTYPE_IQ4_XS;
+    const int64_t bv = aero::dtype_block_values(t), bb = aero::dtype_block_bytes(t);
+    if (!quant || n_cols < 0 || n_cols % bv != 0 || n_rows < 0 || n_tok < 0) {
+        set_error("aero_matvec: dtype %d / n_cols %lld refused", t, (long long)n_cols);
+        return 0;
+    }
+    if (n_rows == 0 || n_tok == 0) return 1;
+    if (w == nullptr || X == nullptr || Y == nullptr) {
+        set_error("aero_matvec: null pointer");
+        return 0;
+    }
+    if (n_cols == 0) {  // empty dot products, as the reference's loop leaves them
+        std::memset(Y, 0, (size_t)(n_tok * n_rows) * sizeof(float));
+        return 1;
+    }
+    const size_t wbytes = (size_t)(n_rows * (n_cols / bv) * bb);
+    const size_t xbytes = (size_t)(n_tok * n_cols) * 4, ybytes = (size_t)(n_tok * n_rows) * 4;
+    aero::Staging st;
+    void* p[3];
+    if (!st.reserve({wbytes, xbytes, ybytes}, p)) return 0;
+    const bool ok = st.h2d(p[0], w, wbytes) && st.h2d(p[1], X, xbytes) &&
+                    aero::gemv_dev(t, static_cast<uint8_t*>(p[0]), (int64_t)wbytes,
+                                   static_cast<float*>(p[1]), static_cast<float*>(p[2]), n_rows,
+                                   n_cols, n_tok, st.stream()) &&
+                    st.d2h(Y, p[2], ybytes) && st.finish();
+    return ok ? 1 : 0;
+}
+
+int aero_matvec(int t, const uint8_t* w, const float* x, float* y, int64_t n_rows,
+                int64_t n_cols, int threads) {
+    (void)threads;
+    return host_gemv(t, w, x, y, 1, n_rows, n_cols);
+}
+
+int aero_matmul(int t, const uint8_t* w, const float* X, float* Y, int64_t n_tokens,
+                int64_t n_rows, int64_t n_cols, int threads) {
+    (void)threads;
+    return host_gemv(t, w, X, Y, n_tokens, n_rows, n_cols);
 }
 
 int aero_dequant_threaded(int t, const uint8_t* raw, int64_t raw_len, float* out,

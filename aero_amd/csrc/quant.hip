@@ -1,5 +1,5 @@
-// GGUF token-embedding row gather with Q8_0 / Q4_K / Q6_K dequant on gfx950,
-// and the same kernels as a whole-buffer dequant.
+// GGUF token-embedding row gather with Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_XS
+// dequant on gfx950, and the same kernel as a whole-buffer dequant.
 //
 // One wave (a 64-thread workgroup) takes a run of U*256 consecutive values of
 // one output row. It reads the row's token id once, loads the run's quant
@@ -10,14 +10,10 @@
 // 128-bit store, so each step of a wave writes 1 KiB of contiguous output.
 // HBM bytes per gathered row: (n_embd/bv)*bb read + 4*n_embd written.
 //
-// Arithmetic is the reference's, operation by operation with contraction
-// off, so results are bit-identical: Q8_0 d*q (src/kernels.cpp:364-373);
-// Q4_K (d*sc)*q - (dmin*m) with the 6-bit unpacking of src/kernels.cpp:65-73,
-// 337-363; Q6_K (d*sc)*(q-32) (src/kernels.cpp:427-458). fp16 scales are
-// decoded exactly (subnormals included). The optional embedding scale is a
-// separate multiply, as the reference's second pass (src/model.cpp:315-316).
-#include "common.hpp"
-#include "aero_hip.h"
+// Values are the reference's dequant bit for bit (quant_blocks.hpp). The
+// optional embedding scale is a separate multiply, as the reference's second
+// pass (src/model.cpp:315-316).
+#include "quant_blocks.hpp"
 
 #pragma clang fp contract(off)
 
@@ -36,124 +32,6 @@ struct GatherParams {
     uint32_t* bad;       // optional count of out-of-range ids
 };
 
-__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
-    return *reinterpret_cast<const uint16_t*>(p);
-}
-// 4 bytes at a 2-byte aligned address, little endian
-__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
-    return ld_u16(p) | (ld_u16(p + 2) << 16);
-}
-__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
-    return *reinterpret_cast<const uint32_t*>(p);
-}
-__device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) {
-    return (w >> (8 * k)) & 0xFFu;
-}
-
-// In each 256-value step of a run, lane l produces values 4l..4l+3: for
-// Q4_K / Q6_K of the step's one block, for Q8_0 values 4(l%8).. of the
-// step's block l/8. load_raw reads the words a lane needs from the run staged
-// in LDS: Q8_0 and Q6_K blocks start at even byte offsets and are read in
-// 16-bit pieces, Q4_K blocks start at multiples of 4 (144-byte blocks in a
-// 4-byte aligned table).
-
-// Raw words one lane needs for its four values of one unit.
-struct RawQ8 { uint32_t d, q0, q1; };        // fp16 d, quant bytes as 2 x 16 bit
-struct RawQ4 { uint32_t dd, s0, s1, s2, q; }; // d|dmin, 12 scale bytes, 4 quant bytes
-struct RawQ6 { uint32_t ql0, ql1, qh0, qh1, sc, d; };
-
-// Q8_0 lanes work per block: lane l covers values 4(l%8).. of its block.
-__device__ __forceinline__ void load_raw(const uint8_t* blk, int l, RawQ8& r) {
-    const int k = l & 7;
-    r.d = ld_u16(blk);
-    r.q0 = ld_u16(blk + 2 + 4 * k);
-    r.q1 = ld_u16(blk + 4 + 4 * k);
-}
-__device__ __forceinline__ void load_raw(const uint8_t* blk, int l, RawQ4& r) {
-    const int j = l >> 4, i0 = (l & 7) * 4;
-    r.dd = ld_u32(blk);
-    r.s0 = ld_u32(blk + 4);
-    r.s1 = ld_u32(blk + 8);
-    r.s2 = ld_u32(blk + 12);
-    r.q = ld_u32(blk + 16 + 32 * j + i0);
-}
-__device__ __forceinline__ void load_raw(const uint8_t* blk, int l, RawQ6& r) {
-    const int h = l >> 5, k = (l >> 3) & 3, lq = (l & 7) * 4;
-    const uint8_t* ql = blk + 64 * h + lq + 32 * (k & 1);
-    const uint8_t* qh = blk + 128 + 32 * h + lq;
-    r.ql0 = ld_u16(ql);
-    r.ql1 = ld_u16(ql + 2);
-    r.qh0 = ld_u16(qh);
-    r.qh1 = ld_u16(qh + 2);
-    r.sc = blk[192 + 8 * h + (lq >> 4) + 2 * k];
-    r.d = ld_u16(blk + 208);
-}
-
-// Q8_0, src/kernels.cpp:364-373: y = d*q.
-__device__ __forceinline__ float4 decode(const RawQ8& r, int) {
-    const float d = half_bits_to_float(r.d);
-    const uint32_t q = r.q0 | (r.q1 << 16);
-    float4 v;
-    v.x = d * (float)(int8_t)byte_of(q, 0);
-    v.y = d * (float)(int8_t)byte_of(q, 1);
-    v.z = d * (float)(int8_t)byte_of(q, 2);
-    v.w = d * (float)(int8_t)byte_of(q, 3);
-    return v;
-}
-
-// Q4_K, src/kernels.cpp:65-73,337-363: group j = l/16 covers values
-// 64j..64j+63, low nibbles (sub-block 2j) then high nibbles (2j+1);
-// y = (d*sc)*q - (dmin*m).
-__device__ __forceinline__ float4 decode(const RawQ4& r, int l) {
-    const float d = half_bits_to_float(r.dd & 0xFFFFu);
-    const float dmin = half_bits_to_float(r.dd >> 16);
-    const int j = l >> 4;
-    const int hi = (l >> 3) & 1;
-    const int k = 2 * j + hi;
-    // byte idx of the 12-byte scale field, selected from registers
-    const uint32_t s0 = r.s0, s1 = r.s1, s2 = r.s2;
-    auto sb = [s0, s1, s2](int idx) {
-        const uint32_t w = idx < 4 ? s0 : (idx < 8 ? s1 : s2);
-        return byte_of(w, idx & 3);
-    };
-    uint32_t sc, mn;
-    if (k < 4) {
-        sc = sb(k) & 63u;
-        mn = sb(k + 4) & 63u;
-    } else {
-        sc = (sb(k + 4) & 15u) | ((sb(k - 4) >> 6) << 4);
-        mn = (sb(k + 4) >> 4) | ((sb(k) >> 6) << 4);
-    }
-    const float f = d * (float)sc;
-    const float g = dmin * (float)mn;
-    const int sh = hi ? 4 : 0;
-    float4 v;
-    v.x = f * (float)((byte_of(r.q, 0) >> sh) & 15u) - g;
-    v.y = f * (float)((byte_of(r.q, 1) >> sh) & 15u) - g;
-    v.z = f * (float)((byte_of(r.q, 2) >> sh) & 15u) - g;
-    v.w = f * (float)((byte_of(r.q, 3) >> sh) & 15u) - g;
-    return v;
-}
-
-// Q6_K, src/kernels.cpp:427-458: half h = l/32, quarter k = (l/8)%4 (values
-// 128h + 32k + lq .. +3, lq = 4*(l%8)); y = (d*sc)*(q-32).
-__device__ __forceinline__ float4 decode(const RawQ6& r, int l) {
-    const int k = (l >> 3) & 3;
-    const uint32_t ql = r.ql0 | (r.ql1 << 16);
-    const uint32_t qh = r.qh0 | (r.qh1 << 16);
-    const float f = half_bits_to_float(r.d) * (float)(int8_t)r.sc;
-    const int shl = (k >= 2) ? 4 : 0;
-    const int shh = 2 * k;
-    float qv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int q = (int)(((byte_of(ql, e) >> shl) & 15u) |
-                            (((byte_of(qh, e) >> shh) & 3u) << 4));
-        qv[e] = f * (float)(q - 32);
-    }
-    return make_float4(qv[0], qv[1], qv[2], qv[3]);
-}
-
 // F16 / BF16 element-wise decode for whole-buffer dequant.
 template <bool BF>
 __global__ __launch_bounds__(256)
@@ -168,7 +46,8 @@ int block_values(int t) {
     switch (t) {
     case AERO_DTYPE_F32: case AERO_DTYPE_F16: case AERO_DTYPE_BF16: return 1;
     case AERO_DTYPE_Q8_0: return 32;
-    case AERO_DTYPE_Q4_K: case 13: case AERO_DTYPE_Q6_K: case 23: return 256;
+    case AERO_DTYPE_Q4_K: case AERO_DTYPE_Q5_K: case AERO_DTYPE_Q6_K:
+    case AERO_DTYPE_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -179,21 +58,18 @@ int block_bytes(int t) {
     case AERO_DTYPE_F16: case AERO_DTYPE_BF16: return 2;
     case AERO_DTYPE_Q8_0: return 34;
     case AERO_DTYPE_Q4_K: return 144;
-    case 13: return 176;
+    case AERO_DTYPE_Q5_K: return 176;
     case AERO_DTYPE_Q6_K: return 210;
-    case 23: return 136;
+    case AERO_DTYPE_IQ4_XS: return 136;
     default: return 0;
     }
 }
 
 bool is_block_quant(int t) {
-    return t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q6_K;
+    return t == AERO_DTYPE_Q8_0 || t == AERO_DTYPE_Q4_K || t == AERO_DTYPE_Q5_K ||
+           t == AERO_DTYPE_Q6_K || t == AERO_DTYPE_IQ4_XS;
 }
 
-template <int TYPE> struct QT;
-template <> struct QT<AERO_DTYPE_Q8_0> { static constexpr int BV = 32, BB = 34; using Raw = RawQ8; };
-template <> struct QT<AERO_DTYPE_Q4_K> { static constexpr int BV = 256, BB = 144; using Raw = RawQ4; };
-template <> struct QT<AERO_DTYPE_Q6_K> { static constexpr int BV = 256, BB = 210; using Raw = RawQ6; };
 
 // Wave w covers values [c*U*256, min((c+1)*U*256, n_embd)) of output row
 // r = w / cpr (c = w % cpr). Every branch on r, the token or the run length
@@ -302,6 +178,9 @@ bool run_gather(int dtype, GatherParams p, hipStream_t s) {
     case AERO_DTYPE_Q8_0: return launch_rows<AERO_DTYPE_Q8_0>("gather_rows_kernel<Q8_0>", p, s);
     case AERO_DTYPE_Q4_K: return launch_rows<AERO_DTYPE_Q4_K>("gather_rows_kernel<Q4_K>", p, s);
     case AERO_DTYPE_Q6_K: return launch_rows<AERO_DTYPE_Q6_K>("gather_rows_kernel<Q6_K>", p, s);
+    case AERO_DTYPE_Q5_K: return launch_rows<AERO_DTYPE_Q5_K>("gather_rows_kernel<Q5_K>", p, s);
+    case AERO_DTYPE_IQ4_XS:
+        return launch_rows<AERO_DTYPE_IQ4_XS>("gather_rows_kernel<IQ4_XS>", p, s);
     default:
         set_error("gather: unsupported dtype %d", dtype);
         return false;
@@ -364,7 +243,8 @@ bool embed_gather(int dtype, const uint8_t* table, int64_t table_bytes, int64_t 
                   int64_t n_embd, const int32_t* ids, int64_t n_ids, float scale,
                   float* out, uint32_t* bad, hipStream_t s) {
     if (!is_block_quant(dtype)) {
-        set_error("embed_gather: dtype %d not supported (Q8_0, Q4_K, Q6_K)", dtype);
+        set_error("embed_gather: dtype %d not supported (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS)",
+                  dtype);
         return false;
     }
     const int64_t bv = block_values(dtype), bb = block_bytes(dtype);

@@ -1,18 +1,18 @@
-"""GPU drop-in for the dequant half of the reference's engine/native.py
-(libaero_kernels).
+"""GPU drop-in for the reference's engine/native.py (libaero_kernels):
+dequant and the quantised matvec / matmul.
 
-Same constants, names, arguments and exceptions as engine/native.py:22-229:
+Same constants, names, arguments and exceptions as engine/native.py:22-285:
 DTYPE_*, NATIVE_TYPES, KernelsUnavailable, available(), unavailable_reason(),
 block_bytes(), block_values(), hardware_threads(), hw_threads(), _u8(),
-_raw_nbytes() and dequant(dtype, raw, shape, threads=0) -> a new float32
-array of `shape`. raw may be bytes, bytearray or memoryview (or a uint8
+_raw_nbytes(), dequant(dtype, raw, shape, threads=0) -> a new float32 array
+of `shape`, matvec(dtype, w_bytes, x) -> W @ x and matmul(dtype, w_bytes, X)
+-> X @ W^T. raw / w_bytes may be bytes, bytearray or memoryview (or a uint8
 ndarray); a short buffer or an unsupported type raises ValueError before any
-device work.
+device work. The host forms upload their inputs per call; a loop that keeps
+weights in HBM uses aero_amd.ops.matvec.
 
-NATIVE_TYPES is the set this GPU path dequantises: Q8_0, Q4_K, Q6_K (the
-reference's set also holds Q5_K and IQ4_XS, which its callers then dequantise
-with their own numpy path, engine/gguf.py:258-261). matvec / matmul (the
-fused quantised GEMV) are not part of this path and raise NotImplementedError.
+NATIVE_TYPES is the reference's set (engine/native.py:33-34): Q8_0, Q4_K,
+Q5_K, Q6_K, IQ4_XS, all dequantised on the GPU.
 """
 from __future__ import annotations
 
@@ -31,7 +31,8 @@ DTYPE_Q6_K = 14
 DTYPE_IQ4_XS = 23
 DTYPE_BF16 = 30
 
-NATIVE_TYPES = frozenset({DTYPE_Q8_0, DTYPE_Q4_K, DTYPE_Q6_K})
+NATIVE_TYPES = frozenset({DTYPE_Q8_0, DTYPE_Q4_K, DTYPE_Q5_K, DTYPE_Q6_K,
+                          DTYPE_IQ4_XS})
 
 _BLOCK_VALUES = {DTYPE_F32: 1, DTYPE_F16: 1, DTYPE_Q8_0: 32, DTYPE_Q4_K: 256,
                  DTYPE_Q5_K: 256, DTYPE_Q6_K: 256, DTYPE_IQ4_XS: 256, DTYPE_BF16: 1}
@@ -102,6 +103,11 @@ def _u8(arr):
     raise TypeError(f"expected bytes-like, got {type(arr).__name__}")
 
 
+def _raw_len(raw) -> int:
+    """len() of the weight buffer, as the reference sizes it (bytes)."""
+    return int(raw.nbytes) if isinstance(raw, np.ndarray) else len(raw)
+
+
 def _raw_nbytes(raw, dtype: int, n_values: int) -> int:
     """Bytes the caller actually passed (never more)."""
     if isinstance(raw, np.ndarray):
@@ -146,13 +152,56 @@ def dequant(dtype: int, raw, shape, threads: int = 0):
     return out.reshape(shape)
 
 
-def _not_here(name):
-    def f(*a, **k):
-        raise NotImplementedError(
-            f"{name} (fused quantised GEMV) is not part of the GPU elementwise path")
-    f.__name__ = name
-    return f
+def matvec(dtype: int, w_bytes, x, threads: int = 1):
+    """y = W @ x (engine/native.py:232-255). `w_bytes` is the raw quantised
+    tensor, `x` a float32 array; n_rows = values in w_bytes // x.size. W is
+    uploaded per call (the reference's signature holds no device handle);
+    `threads` is ignored."""
+    lib = _require()
+    if dtype not in NATIVE_TYPES:
+        raise ValueError(f"dtype {dtype} has no native kernel")
+    wb = _u8(w_bytes)
+    keep = None
+    if isinstance(wb, tuple):
+        wb, keep = wb
+    xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n_cols = xv.size
+    bv = block_values(dtype)
+    n_rows = (_raw_len(w_bytes) // block_bytes(dtype)) * bv // n_cols if n_cols else 0
+    y = np.zeros(n_rows, dtype=np.float32)
+    ok = lib.aero_matvec(int(dtype), wb, xv.ctypes.data_as(POINTER(c_float)),
+                         y.ctypes.data_as(POINTER(c_float)), c_int64(n_rows), c_int64(n_cols),
+                         c_int(threads))
+    del keep
+    if not ok:
+        raise ValueError(
+            f"native matvec refused dtype={dtype} n_rows={n_rows} n_cols={n_cols}: "
+            f"{_lib.last_error()}")
+    return y
 
 
-matvec = _not_here("matvec")
-matmul = _not_here("matmul")
+def matmul(dtype: int, w_bytes, X, threads: int = 1):
+    """Y = X @ W^T (engine/native.py:258-285): X (T, n_cols) -> Y (T, n_rows)."""
+    lib = _require()
+    if dtype not in NATIVE_TYPES:
+        raise ValueError(f"dtype {dtype} has no native kernel")
+    wb = _u8(w_bytes)
+    keep = None
+    if isinstance(wb, tuple):
+        wb, keep = wb
+    Xv = np.ascontiguousarray(X, dtype=np.float32)
+    if Xv.ndim == 1:
+        Xv = Xv[None, :]
+    T, n_cols = Xv.shape
+    bv = block_values(dtype)
+    n_rows = (_raw_len(w_bytes) // block_bytes(dtype)) * bv // n_cols if n_cols else 0
+    Y = np.zeros((T, n_rows), dtype=np.float32)
+    ok = lib.aero_matmul(int(dtype), wb, Xv.ctypes.data_as(POINTER(c_float)),
+                         Y.ctypes.data_as(POINTER(c_float)), c_int64(T), c_int64(n_rows),
+                         c_int64(n_cols), c_int(threads))
+    del keep
+    if not ok:
+        raise ValueError(
+            f"native matmul refused dtype={dtype} T={T} n_rows={n_rows} n_cols={n_cols}: "
+            f"{_lib.last_error()}")
+    return Y

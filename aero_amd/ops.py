@@ -28,8 +28,10 @@ ROPE_NEOX = 0
 ROPE_INTERLEAVED = 1
 
 DTYPE_F32, DTYPE_F16, DTYPE_Q8_0, DTYPE_Q4_K, DTYPE_Q6_K, DTYPE_BF16 = 0, 1, 8, 12, 14, 30
+DTYPE_Q5_K, DTYPE_IQ4_XS = 13, 23
 _BLOCK = {DTYPE_F32: (1, 4), DTYPE_F16: (1, 2), DTYPE_BF16: (1, 2), DTYPE_Q8_0: (32, 34),
-          DTYPE_Q4_K: (256, 144), DTYPE_Q6_K: (256, 210)}
+          DTYPE_Q4_K: (256, 144), DTYPE_Q5_K: (256, 176), DTYPE_Q6_K: (256, 210),
+          DTYPE_IQ4_XS: (256, 136)}
 
 
 def _s(stream: Stream | None):
@@ -178,6 +180,23 @@ def dequant(dtype: int, raw: DeviceArray, out: DeviceArray, n_values: int,
     _need(out, (n_values // bv) * bv, np.float32, "out")
     _lib.check(_lib.lib().aero_hip_dequant(int(dtype), raw.ptr, raw.nbytes, out.ptr, n_values,
                                            _s(stream)), "dequant")
+
+
+def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: int,
+           n_cols: int, n_tok: int = 1, stream: Stream | None = None) -> None:
+    """y[t, r] = sum_c W[r, c] * x[t, c] for t < n_tok: W n_rows rows of quant
+    blocks (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS), x [n_tok, n_cols], y [n_tok, n_rows]."""
+    if dtype not in _BLOCK or _BLOCK[dtype][0] == 1:
+        raise ValueError(f"dtype {dtype} has no quantised GEMV")
+    bv, bb = _BLOCK[dtype]
+    if n_cols <= 0 or n_cols % bv:
+        raise ValueError(f"n_cols {n_cols} must be a positive multiple of {bv}")
+    if w.nbytes < n_rows * (n_cols // bv) * bb:
+        raise ValueError("weight buffer too short")
+    _need(x, n_tok * n_cols, np.float32, "x")
+    _need(y, n_tok * n_rows, np.float32, "y")
+    _lib.check(_lib.lib().aero_hip_matvec(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows,
+                                          n_cols, n_tok, _s(stream)), "matvec")
 
 
 def copy_f32(src: DeviceArray, dst: DeviceArray, n: int | None = None,

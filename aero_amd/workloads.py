@@ -29,8 +29,9 @@ from dataclasses import dataclass, field, replace
 
 import numpy as np
 
-F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, BF16 = 0, 1, 8, 12, 13, 14, 23, 30
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
+         IQ4_XS: (256, 136)}
 
 
 @dataclass(frozen=True)
@@ -191,6 +192,18 @@ def make_table(t: int, n_blocks: int, rng) -> np.ndarray:
         blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
         d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.01))
         blk[:, 208:210] = _f16_bytes(d)
+        return blk.reshape(-1)
+    if t == Q5_K:
+        # as Q4_K: random bytes (scales, qh, qs), d, dmin = fp16(|N(0, 0.01)|)
+        blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
+        dd = np.abs(rng.standard_normal((n_blocks, 2), dtype=np.float32) * np.float32(0.01))
+        blk[:, 0:4] = np.ascontiguousarray(dd.astype(np.float16)).view(np.uint8).reshape(-1, 4)
+        return blk.reshape(-1)
+    if t == IQ4_XS:
+        # random scale and quant bytes, d = fp16(|N(0, 0.001)|) (x codebook up to 127)
+        blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
+        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.001))
+        blk[:, 0:2] = _f16_bytes(d)
         return blk.reshape(-1)
     raise ValueError(t)
 

@@ -95,7 +95,7 @@ int64_t aero_dtype_block_values(int t);
  * reference binding's auto-thread rule; the GPU path ignores it. */
 int aero_hardware_threads(void);
 /* src/kernels.cpp:568-584 aero_dequant_ref: dequantise floor(n/bv) blocks of
- * type t (F32, F16, BF16, Q8_0, Q4_K, Q6_K). Refuses (0) a raw_len shorter
+ * type t (F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS). Refuses (0) a raw_len shorter
  * than the blocks need, or any other type. */
 int aero_dequant_ref(int t, const uint8_t* raw, int64_t raw_len, float* out,
                      int64_t n_values);
@@ -103,6 +103,16 @@ int aero_dequant_ref(int t, const uint8_t* raw, int64_t raw_len, float* out,
  * accepted for signature compatibility and ignored. */
 int aero_dequant_threaded(int t, const uint8_t* raw, int64_t raw_len,
                           float* out, int64_t n_values, int threads);
+/* src/kernels.cpp:605-609 aero_matvec: y = W @ x, W n_rows rows of quant
+ * blocks of type t (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS). 1 = done; 0 = refused
+ * (another type, n_cols % block size, a null pointer). W is uploaded per call;
+ * `threads` is ignored. */
+int aero_matvec(int t, const uint8_t* w, const float* x, float* y, int64_t n_rows,
+                int64_t n_cols, int threads);
+/* src/kernels.cpp:611-615 aero_matmul: Y[t*n_rows + r] = row r of W dotted
+ * with token t of X, for n_tokens tokens. Same refusals as aero_matvec. */
+int aero_matmul(int t, const uint8_t* w, const float* X, float* Y, int64_t n_tokens,
+                int64_t n_rows, int64_t n_cols, int threads);
 
 /* ------------------------------------------------------------------------
  * 2. Device-pointer fused ops (HBM pointers, asynchronous on `stream`)
@@ -182,14 +192,16 @@ int aero_hip_qk_norm_rope(float* q, float* q_out, int64_t n_q_heads,
 #define AERO_DTYPE_F16  1
 #define AERO_DTYPE_Q8_0 8
 #define AERO_DTYPE_Q4_K 12
+#define AERO_DTYPE_Q5_K 13
 #define AERO_DTYPE_Q6_K 14
+#define AERO_DTYPE_IQ4_XS 23
 #define AERO_DTYPE_BF16 30
 
 /* Token-embedding row gather + dequant (src/model.cpp:297-316 with
  * dequant_ref, src/kernels.cpp:315-458): out[i, :] = dequant(table row
  * ids[i]) (* scale when scale > 0, a separate fp32 multiply as the reference's
  * second pass). table holds vocab rows of (n_embd/bv)*bb bytes (table_bytes
- * >= that, base 4-byte aligned); types Q8_0, Q4_K, Q6_K. An id outside
+ * >= that, base 4-byte aligned); types Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS. An id outside
  * [0, vocab) yields a zero row and, when bad_count != NULL, adds 1 to
  * *bad_count (device uint32; the caller clears it). */
 int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
@@ -198,9 +210,20 @@ int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
                           uint32_t* bad_count, void* stream);
 
 /* Whole-buffer dequant (the device form of aero_dequant_ref): floor(n/bv)
- * blocks of raw -> out. Types F32, F16, BF16, Q8_0, Q4_K, Q6_K. */
+ * blocks of raw -> out. Types F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS. */
 int aero_hip_dequant(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
                      int64_t n_values, void* stream);
+
+/* Quantised GEMV / small-batch GEMM, the device form of the reference's
+ * matvec / matmul (src/kernels.cpp:497-538, block dots :78-250):
+ * y[t*n_rows + r] = sum_c W[r, c] * x[t*n_cols + c] for t < n_tok, W =
+ * n_rows rows of (n_cols/bv)*bb bytes of type dtype (Q8_0, Q4_K, Q5_K, Q6_K,
+ * IQ4_XS; w_bytes >= that, base 4-byte aligned), x fp32 16-byte aligned.
+ * n_cols must be a multiple of the block size. Sums run in a different order
+ * from the reference's serial loop (equal to ~1e-6 of the output scale). */
+int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
+                    float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
+                    void* stream);
 
 /* Plain fp32 copy kernel (dst = src, n elements): the known-size reference
  * workload used to calibrate HBM byte counters. */

@@ -33,6 +33,10 @@ int     cr_dequant(int type, const uint8_t* raw, int64_t raw_len, float* out,
                    int64_t n_values);
 int     cr_dequant_threaded(int type, const uint8_t* raw, int64_t raw_len,
                             float* out, int64_t n_values, int threads);
+int     cr_matvec(int type, const uint8_t* w, const float* x, float* y,
+                  int64_t n_rows, int64_t n_cols);
+int     cr_matmul(int type, const uint8_t* w, const float* X, float* Y,
+                  int64_t n_tok, int64_t n_rows, int64_t n_cols);
 int     cr_embed_gather(int type, const uint8_t* table, int64_t vocab,
                         int64_t n_embd, const int32_t* ids, int64_t n_ids,
                         float scale, float* out);

@@ -41,6 +41,10 @@ def lib():
         L.cr_dequant.restype = c_int
         L.cr_dequant_threaded.argtypes = [c_int, up, c_int64, fp, c_int64, c_int]
         L.cr_dequant_threaded.restype = c_int
+        L.cr_matvec.argtypes = [c_int, up, fp, fp, c_int64, c_int64]
+        L.cr_matvec.restype = c_int
+        L.cr_matmul.argtypes = [c_int, up, fp, fp, c_int64, c_int64, c_int64]
+        L.cr_matmul.restype = c_int
         L.cr_embed_gather.argtypes = [c_int, up, c_int64, c_int64, ip, c_int64,
                                       c_float, fp]
         L.cr_embed_gather.restype = c_int
@@ -119,6 +123,27 @@ def dequant(t: int, raw: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
     if not ok:
         raise ValueError("oracle dequant refused")
     return out
+
+
+def matvec(t: int, w: np.ndarray, x, n_rows: int) -> np.ndarray:
+    """y = W @ x with W [n_rows, x.size] in quant blocks (src/kernels.cpp:497-515)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    x = f32(x).reshape(-1)
+    y = np.zeros(n_rows, dtype=np.float32)
+    if not lib().cr_matvec(t, _u8(w), _f(x), _f(y), n_rows, x.size):
+        raise ValueError("oracle matvec refused")
+    return y
+
+
+def matmul(t: int, w: np.ndarray, X, n_rows: int) -> np.ndarray:
+    """Y = X @ W^T, X [T, n_cols] (src/kernels.cpp:517-538)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    X = f32(X)
+    T, n_cols = X.shape
+    Y = np.zeros((T, n_rows), dtype=np.float32)
+    if not lib().cr_matmul(t, _u8(w), _f(X), _f(Y), T, n_rows, n_cols):
+        raise ValueError("oracle matmul refused")
+    return Y
 
 
 def embed_gather(t: int, table: np.ndarray, vocab: int, n_embd: int, ids,

@@ -18,6 +18,14 @@
  *                   mn 8..1, d/dmin in {0,1}); compiled reference (bit-exact).
  *   Q6_K            tests/test_quant.py:96-124 (all-zero -> -32, all-one ->
  *                   31, low-nibble pattern -> -17/-32); compiled reference.
+ *   Q5_K, IQ4_XS    compiled reference (bit-exact) on random blocks; Q5_K
+ *                   with qh = 0 equals Q4_K of the same bytes, with qh all
+ *                   ones adds 16*(d*sc) to every value; IQ4_XS with one
+ *                   nibble value per block reproduces the codebook times dl.
+ *   cr_matvec,      the compiled reference's aero_matvec/aero_matmul (within
+ *   cr_matmul       1e-6 of scale: its -ffast-math may reorder sums) and the
+ *                   float64 product dequant(W) @ x; matmul rows == matvec
+ *                   (tests/test_kernels.cpp:289-314).
  *   cr_embed_gather brute-force row selection on tiny tables; refusals of
  *                   src/model.cpp:297-316.
  */
@@ -152,6 +160,61 @@ static void deq_q6_k(const uint8_t* blk, float* o) {
     }
 }
 
+/* Q5_K, src/kernels.cpp:374-404: 176 bytes = d, dmin (fp16), 12 scale bytes
+ * (the Q4_K 6-bit packing), qh[32], qs[128]. As Q4_K, plus a fifth bit: value
+ * i of group j takes bit 2j (low nibbles) or 2j+1 (high nibbles) of qh[i];
+ * y = (d*sc)*(nibble | bit<<4) - (dmin*m). */
+static void deq_q5_k(const uint8_t* blk, float* o) {
+    const float d = cr_f16_to_f32(rd16(blk));
+    const float dmin = cr_f16_to_f32(rd16(blk + 2));
+    const uint8_t* sc = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    for (int j = 0; j < 4; ++j) {
+        int s1, m1, s2, m2;
+        q4k_scale_min(2 * j, sc, &s1, &m1);
+        q4k_scale_min(2 * j + 1, sc, &s2, &m2);
+        const float f1 = d * (float)s1, g1 = dmin * (float)m1;
+        const float f2 = d * (float)s2, g2 = dmin * (float)m2;
+        for (int i = 0; i < 32; ++i) {
+            const uint8_t b = qs[32 * j + i];
+            const int h1 = (qh[i] >> (2 * j)) & 1;
+            const int h2 = (qh[i] >> (2 * j + 1)) & 1;
+            o[64 * j + i] = f1 * (float)((b & 15) | (h1 << 4)) - g1;
+            o[64 * j + 32 + i] = f2 * (float)((b >> 4) | (h2 << 4)) - g2;
+        }
+    }
+}
+
+/* IQ4_XS codebook (src/kernels.cpp:212-215): the GGML IQ4_NL non-linear
+ * 4-bit levels, a file-format constant. */
+static const float kIq4nl[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                 1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+
+/* 6-bit scale of IQ4_XS sub-block ib: low 4 bits from scales_l (two per
+ * byte), high 2 bits from the 16-bit scales_h (src/kernels.cpp:405-425). */
+static int iq4xs_scale(const uint8_t* blk, int ib) {
+    const unsigned sh = (unsigned)rd16(blk + 2);
+    const uint8_t* sl = blk + 4;
+    return ((sl[ib >> 1] >> (4 * (ib & 1))) & 15) | (int)(((sh >> (2 * ib)) & 3u) << 4);
+}
+
+/* IQ4_XS: 136 bytes = fp16 d, scales_h (2), scales_l (4), qs[128]. Sub-block
+ * ib of 32 values: dl = d*(ls-32); values j < 16 are the low nibbles of
+ * qs[16ib + j], values 16..31 the high nibbles; y = dl*codebook[nibble]. */
+static void deq_iq4_xs(const uint8_t* blk, float* o) {
+    const float d = cr_f16_to_f32(rd16(blk));
+    const uint8_t* qs = blk + 8;
+    for (int ib = 0; ib < 8; ++ib) {
+        const float dl = d * (float)(iq4xs_scale(blk, ib) - 32);
+        const uint8_t* q = qs + 16 * ib;
+        for (int j = 0; j < 16; ++j) {
+            o[32 * ib + j] = dl * kIq4nl[q[j] & 15];
+            o[32 * ib + 16 + j] = dl * kIq4nl[q[j] >> 4];
+        }
+    }
+}
+
 static int deq_blocks(int type, const uint8_t* raw, float* out, int64_t b0,
                       int64_t b1) {
     const int64_t bb = cr_block_bytes(type), bv = cr_block_values(type);
@@ -162,6 +225,8 @@ static int deq_blocks(int type, const uint8_t* raw, float* out, int64_t b0,
         case CR_Q8_0: deq_q8_0(blk, o); break;
         case CR_Q4_K: deq_q4_k(blk, o); break;
         case CR_Q6_K: deq_q6_k(blk, o); break;
+        case CR_Q5_K: deq_q5_k(blk, o); break;
+        case CR_IQ4_XS: deq_iq4_xs(blk, o); break;
         case CR_F16: o[0] = cr_f16_to_f32(rd16(blk)); break;
         case CR_BF16: o[0] = bf16_to_f32(rd16(blk)); break;
         case CR_F32: memcpy(o, blk, 4); break;
@@ -171,9 +236,13 @@ static int deq_blocks(int type, const uint8_t* raw, float* out, int64_t b0,
     return 1;
 }
 
+static int is_block_quant(int type) {
+    return type == CR_Q8_0 || type == CR_Q4_K || type == CR_Q5_K || type == CR_Q6_K ||
+           type == CR_IQ4_XS;
+}
+
 static int supported(int type) {
-    return type == CR_F32 || type == CR_F16 || type == CR_BF16 ||
-           type == CR_Q8_0 || type == CR_Q4_K || type == CR_Q6_K;
+    return type == CR_F32 || type == CR_F16 || type == CR_BF16 || is_block_quant(type);
 }
 
 /* dequant_ref, src/kernels.cpp:315-323: refuse a short buffer, then
@@ -241,4 +310,134 @@ int cr_embed_gather(int type, const uint8_t* table, int64_t vocab,
     if (scale > 0.0f)
         for (int64_t i = 0; i < n_ids * n_embd; ++i) out[i] *= scale;
     return 1;
+}
+
+/* ------------------------------------------------------------ block dots
+ * One block of a quantised weight row dotted with the matching x values,
+ * in the reference's accumulation order (src/kernels.cpp:78-250). */
+
+/* src/kernels.cpp:78-84: d * sum(q*x). */
+static float dot_q8_0(const uint8_t* blk, const float* x) {
+    const float d = cr_f16_to_f32(rd16(blk));
+    const int8_t* q = (const int8_t*)(blk + 2);
+    float acc = 0.0f;
+    for (int i = 0; i < 32; ++i) acc += (float)q[i] * x[i];
+    return d * acc;
+}
+
+/* Q4_K (src/kernels.cpp:123-156) and Q5_K (:90-121, fifth bit from qh):
+ * per group j, qx = sum(q*x) and sx = sum(x) over each 32-value half;
+ * acc += (d*sc)*qx - (dmin*m)*sx. */
+static float dot_q45_k(const uint8_t* blk, const float* x, int five) {
+    const float d = cr_f16_to_f32(rd16(blk));
+    const float dmin = cr_f16_to_f32(rd16(blk + 2));
+    const uint8_t* sc = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + (five ? 48 : 16);
+    float acc = 0.0f;
+    for (int j = 0; j < 4; ++j) {
+        int s1, m1, s2, m2;
+        q4k_scale_min(2 * j, sc, &s1, &m1);
+        q4k_scale_min(2 * j + 1, sc, &s2, &m2);
+        float qx1 = 0.0f, sx1 = 0.0f, qx2 = 0.0f, sx2 = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const uint8_t b = qs[32 * j + i];
+            const float xlo = x[64 * j + i], xhi = x[64 * j + 32 + i];
+            const int h1 = five ? (qh[i] >> (2 * j)) & 1 : 0;
+            const int h2 = five ? (qh[i] >> (2 * j + 1)) & 1 : 0;
+            qx1 += (float)((b & 15) | (h1 << 4)) * xlo;
+            sx1 += xlo;
+            qx2 += (float)((b >> 4) | (h2 << 4)) * xhi;
+            sx2 += xhi;
+        }
+        acc += (d * (float)s1) * qx1 - (dmin * (float)m1) * sx1;
+        acc += (d * (float)s2) * qx2 - (dmin * (float)m2) * sx2;
+    }
+    return acc;
+}
+
+/* src/kernels.cpp:170-200: acc += d*sc*(q-32)*x, four values per (h, l). */
+static float dot_q6_k(const uint8_t* blk, const float* x) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const float d = cr_f16_to_f32(rd16(blk + 208));
+    float acc = 0.0f;
+    for (int h = 0; h < 2; ++h) {
+        for (int l = 0; l < 32; ++l) {
+            const int lo = ql[64 * h + l], hi = ql[64 * h + l + 32], hb = qh[32 * h + l];
+            const int is = l >> 4;
+            const float v0 = (float)(((lo & 15) | ((hb & 3) << 4)) - 32);
+            const float v1 = (float)(((hi & 15) | (((hb >> 2) & 3) << 4)) - 32);
+            const float v2 = (float)(((lo >> 4) | (((hb >> 4) & 3) << 4)) - 32);
+            const float v3 = (float)(((hi >> 4) | (((hb >> 6) & 3) << 4)) - 32);
+            const float* xb = x + 128 * h + l;
+            acc += d * (float)sc[8 * h + is] * v0 * xb[0];
+            acc += d * (float)sc[8 * h + is + 2] * v1 * xb[32];
+            acc += d * (float)sc[8 * h + is + 4] * v2 * xb[64];
+            acc += d * (float)sc[8 * h + is + 6] * v3 * xb[96];
+        }
+    }
+    return acc;
+}
+
+/* src/kernels.cpp:217-238: per sub-block, dl * sum(codebook[q]*x). */
+static float dot_iq4_xs(const uint8_t* blk, const float* x) {
+    const float d = cr_f16_to_f32(rd16(blk));
+    const uint8_t* qs = blk + 8;
+    float acc = 0.0f;
+    for (int ib = 0; ib < 8; ++ib) {
+        const float dl = d * (float)(iq4xs_scale(blk, ib) - 32);
+        const uint8_t* q = qs + 16 * ib;
+        const float* xb = x + 32 * ib;
+        float sub = 0.0f;
+        for (int j = 0; j < 16; ++j) {
+            sub += kIq4nl[q[j] & 15] * xb[j];
+            sub += kIq4nl[q[j] >> 4] * xb[j + 16];
+        }
+        acc += dl * sub;
+    }
+    return acc;
+}
+
+static float block_dot(int type, const uint8_t* blk, const float* x) {
+    switch (type) {
+    case CR_Q8_0: return dot_q8_0(blk, x);
+    case CR_Q4_K: return dot_q45_k(blk, x, 0);
+    case CR_Q5_K: return dot_q45_k(blk, x, 1);
+    case CR_Q6_K: return dot_q6_k(blk, x);
+    case CR_IQ4_XS: return dot_iq4_xs(blk, x);
+    default: return 0.0f;
+    }
+}
+
+/* matvec, src/kernels.cpp:497-515: y[r] = sum over blocks in order of the
+ * block dot of row r; refuses non-quantised types and n_cols % bv. */
+int cr_matvec(int type, const uint8_t* w, const float* x, float* y, int64_t n_rows,
+              int64_t n_cols) {
+    if (!is_block_quant(type) || w == NULL || x == NULL || y == NULL) return 0;
+    const int64_t bv = cr_block_values(type), bb = cr_block_bytes(type);
+    if (n_cols % bv != 0) return 0;
+    const int64_t rb = (n_cols / bv) * bb;
+    for (int64_t r = 0; r < n_rows; ++r) {
+        float acc = 0.0f;
+        for (int64_t c = 0; c < n_cols; c += bv) acc += block_dot(type, w + r * rb + (c / bv) * bb, x + c);
+        y[r] = acc;
+    }
+    return 1;
+}
+
+/* matmul, src/kernels.cpp:517-538: Y[t, r] = matvec of token t. */
+int cr_matmul(int type, const uint8_t* w, const float* X, float* Y, int64_t n_tok,
+              int64_t n_rows, int64_t n_cols) {
+    if (!is_block_quant(type) || X == NULL || Y == NULL) return 0;
+    float* tmp = (float*)malloc((size_t)(n_rows > 0 ? n_rows : 1) * sizeof(float));
+    if (tmp == NULL) return 0;
+    int ok = 1;
+    for (int64_t t = 0; t < n_tok && ok; ++t) {
+        ok = cr_matvec(type, w, X + t * n_cols, tmp, n_rows, n_cols);
+        for (int64_t r = 0; ok && r < n_rows; ++r) Y[t * n_rows + r] = tmp[r];
+    }
+    free(tmp);
+    return ok;
 }

@@ -34,6 +34,12 @@ def kernels():
         L.aero_dequant_threaded.argtypes = [c_int, POINTER(c_uint8), c_int64,
                                             POINTER(c_float), c_int64, c_int]
         L.aero_dequant_threaded.restype = c_int
+        L.aero_matvec.argtypes = [c_int, POINTER(c_uint8), POINTER(c_float),
+                                  POINTER(c_float), c_int64, c_int64, c_int]
+        L.aero_matvec.restype = c_int
+        L.aero_matmul.argtypes = [c_int, POINTER(c_uint8), POINTER(c_float),
+                                  POINTER(c_float), c_int64, c_int64, c_int64, c_int]
+        L.aero_matmul.restype = c_int
         _k = L
     return _k
 
@@ -90,6 +96,27 @@ def dequant(t: int, raw: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
     if not ok:
         raise ValueError("reference dequant refused")
     return out
+
+
+def matvec(t: int, w: np.ndarray, x, n_rows: int, threads: int = 1) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    y = np.zeros(n_rows, dtype=np.float32)
+    if not kernels().aero_matvec(t, w.ctypes.data_as(POINTER(c_uint8)), _f(x), _f(y),
+                                 n_rows, x.size, threads):
+        raise ValueError("reference matvec refused")
+    return y
+
+
+def matmul(t: int, w: np.ndarray, X, n_rows: int, threads: int = 1) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    T, n_cols = X.shape
+    Y = np.zeros((T, n_rows), dtype=np.float32)
+    if not kernels().aero_matmul(t, w.ctypes.data_as(POINTER(c_uint8)), _f(X), _f(Y), T,
+                                 n_rows, n_cols, threads):
+        raise ValueError("reference matmul refused")
+    return Y
 
 
 def rmsnorm_rows(x, w, eps: float) -> np.ndarray:

@@ -18,8 +18,9 @@ where the reference tree exists):
 2. ref_vectors.npz -- inputs and outputs of the reference's own C++ (built
    into oracle/_ref/ from src/kernels.cpp, src/transformer.cpp and
    src/tensor.cpp) on small seeded inputs: row norms, activations, RoPE tables
-   and rotation, and Q8_0 / Q4_K / Q6_K dequant. These pin the oracle and the
-   GPU path where the reference build is absent (the GPU box).
+   and rotation, Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_XS dequant, and matvec /
+   matmul over each of those block types. These pin the oracle and the GPU
+   path where the reference build is absent (the GPU box).
 """
 from __future__ import annotations
 
@@ -167,6 +168,20 @@ def ref_vectors() -> dict:
         bv = 32 if t == 8 else 256
         v[f"deq{t}_raw"] = raw
         v[f"deq{t}_out"] = R.dequant(t, raw, nb * bv)
+    # Q5_K and IQ4_XS dequant; matvec and matmul of every block type
+    from aero_amd import workloads as W
+    for t in (W.Q5_K, W.IQ4_XS):
+        raw = W.make_table(t, 12, rng)
+        v[f"deq{t}_raw"] = raw
+        v[f"deq{t}_out"] = R.dequant(t, raw, 12 * 256)
+    for t in (W.Q8_0, W.Q4_K, W.Q5_K, W.Q6_K, W.IQ4_XS):
+        n_rows, n_cols = 24, 512
+        bv, bb = W.BLOCK[t]
+        w = W.make_table(t, n_rows * n_cols // bv, rng)
+        X = rng.standard_normal((3, n_cols)).astype(np.float32)
+        v[f"mv{t}_w"], v[f"mv{t}_x"] = w, X
+        v[f"mv{t}_y"] = R.matvec(t, w, X[0], n_rows)
+        v[f"mm{t}_y"] = R.matmul(t, w, X, n_rows)
     return v
 
 

@@ -99,6 +99,12 @@ def test_refusals_happen_before_device_work():
     assert L.aero_tensor_l2norm(None, None, None, 4, 1e-6, 1) == 0
     assert L.aero_rope_tables(0, None, 0, 1e4, -1, None, 0, None, None) == -1
     assert L.aero_dequant_ref(23, None, 0, None, 256) == 0
+    assert L.aero_hip_matvec(0, 4, 1 << 20, 16, 16, 4, 256, 1, None) == 0          # F32
+    assert L.aero_hip_matvec(12, 4, 1 << 20, 16, 16, 4, 255, 1, None) == 0         # 255 % 256
+    assert L.aero_hip_matvec(12, 4, 100, 16, 16, 4, 256, 1, None) == 0             # short W
+    assert "w_bytes" in _lib.last_error()
+    assert L.aero_matvec(0, None, None, None, 4, 16, 1) == 0
+    assert L.aero_matmul(14, None, None, None, 2, 4, 255, 1) == 0
     assert L.aero_hip_plan_begin(None) == 0
     assert L.aero_hip_time_next_kernel(1, None) == 0
 
@@ -172,8 +178,12 @@ def test_reference_python_surface():
     assert params(TN.mul) == [("a", inspect._empty), ("b", inspect._empty)]
     assert params(native.dequant) == [("dtype", inspect._empty), ("raw", inspect._empty),
                                       ("shape", inspect._empty), ("threads", 0)]
+    assert params(native.matvec) == [("dtype", inspect._empty), ("w_bytes", inspect._empty),
+                                     ("x", inspect._empty), ("threads", 1)]
+    assert params(native.matmul) == [("dtype", inspect._empty), ("w_bytes", inspect._empty),
+                                     ("X", inspect._empty), ("threads", 1)]
     assert (native.DTYPE_Q8_0, native.DTYPE_Q4_K, native.DTYPE_Q6_K) == (8, 12, 14)
-    assert native.NATIVE_TYPES == {8, 12, 14}
+    assert native.NATIVE_TYPES == {8, 12, 13, 14, 23}
     with pytest.raises(TypeError):
         TN._p([1.0, 2.0])
     with pytest.raises(TypeError):

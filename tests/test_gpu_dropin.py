@@ -144,7 +144,8 @@ def f16(v: float) -> bytes:
     return struct.pack("<e", v)
 
 
-@pytest.mark.parametrize("type_id,bb,bv", [(8, 34, 32), (12, 144, 256), (14, 210, 256)])
+@pytest.mark.parametrize("type_id,bb,bv", [(8, 34, 32), (12, 144, 256), (13, 176, 256),
+                                            (14, 210, 256), (23, 136, 256)])
 def test_native_dequant(hip, oracle, type_id, bb, bv):
     rng = np.random.default_rng(4)
     assert type_id in NK.NATIVE_TYPES
@@ -158,7 +159,7 @@ def test_native_dequant(hip, oracle, type_id, bb, bv):
             buf[off + 208:off + 210] = f16(0.02 * (b + 1))
         else:
             buf[off:off + 2] = f16(0.02 * (b + 1))
-            if type_id == 12:
+            if type_id in (12, 13):
                 buf[off + 2:off + 4] = f16(0.01 * (b + 1))
     raw = bytes(buf)
     want = oracle.dequant(type_id, np.frombuffer(raw, np.uint8), NB * bv)
@@ -173,6 +174,6 @@ def test_native_dequant(hip, oracle, type_id, bb, bv):
 
 def test_native_dequant_refuses_other_types(hip):
     with pytest.raises(ValueError):
-        NK.dequant(NK.DTYPE_Q5_K, bytes(176), (256,))
+        NK.dequant(2, bytes(18), (32,))          # Q4_0: not a native type
     with pytest.raises(TypeError):
         NK.dequant(NK.DTYPE_Q8_0, [1, 2, 3], (32,))

@@ -51,7 +51,7 @@ def test_gather_edge_ids_and_bad_count(hip, oracle):
     assert bits_equal(got[ok], want)
 
 
-@pytest.mark.parametrize("t", [W.Q8_0, W.Q4_K, W.Q6_K])
+@pytest.mark.parametrize("t", [W.Q8_0, W.Q4_K, W.Q5_K, W.Q6_K, W.IQ4_XS])
 def test_gather_brute_force_rows(hip, oracle, t):
     """Row selection: each output row equals the dequant of exactly that table row."""
     rng = np.random.default_rng(t)
@@ -71,6 +71,8 @@ def test_gather_brute_force_rows(hip, oracle, t):
     (W.Q8_0, 32 * 45, 32768),    # 2-byte aligned odd rows, runs of 4 steps, ragged tail
     (W.Q6_K, 256 * 5, 40000),    # 2-byte aligned odd rows, runs of 4 steps, one-block tail
     (W.Q4_K, 256 * 48, 8192),    # runs of 8 steps
+    (W.Q5_K, 256 * 16, 16384),   # runs of 4 steps (over 64K steps)
+    (W.IQ4_XS, 256 * 10, 3000),  # whole-row runs of 16 steps
     (W.Q8_0, 32 * 7, 3),         # a row shorter than one 256-value step
 ])
 def test_gather_run_lengths(hip, oracle, t, n_embd, rows):
@@ -99,7 +101,7 @@ def test_gather_run_lengths(hip, oracle, t, n_embd, rows):
 def test_dequant_types(hip, oracle):
     rng = np.random.default_rng(31)
     cases = [(W.F32, 4, 1), (W.F16, 2, 1), (W.BF16, 2, 1), (W.Q8_0, 34, 32), (W.Q4_K, 144, 256),
-             (W.Q6_K, 210, 256)]
+             (W.Q5_K, 176, 256), (W.Q6_K, 210, 256), (W.IQ4_XS, 136, 256)]
     for t, bb, bv in cases:
         nb = 1001
         if t in W.BLOCK:
@@ -152,7 +154,7 @@ def test_dequant_kat(hip):
 
 def test_dequant_golden(hip):
     g = golden("ref_vectors.npz")
-    for t, bv in ((8, 32), (12, 256), (14, 256)):
+    for t, bv in ((8, 32), (12, 256), (13, 256), (14, 256), (23, 256)):
         raw = g[f"deq{t}_raw"]
         want = g[f"deq{t}_out"]
         out = DA.empty(want.size)

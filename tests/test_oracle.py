@@ -53,7 +53,9 @@ def test_dequant_refusals():
     with pytest.raises(ValueError):
         O.dequant(O.Q4_K, np.zeros(143, np.uint8), 256)      # short buffer
     with pytest.raises(ValueError):
-        O.dequant(O.Q5_K, np.zeros(176, np.uint8), 256)      # not a path type
+        O.dequant(O.IQ4_XS, np.zeros(135, np.uint8), 256)    # short buffer
+    with pytest.raises(ValueError):
+        O.dequant(2, np.zeros(18, np.uint8), 32)             # Q4_0: no dequantiser
     assert O.dequant(O.Q8_0, np.zeros(34, np.uint8), 31).sum() == 0  # floor(n/bv) = 0 blocks
 
 
@@ -100,9 +102,31 @@ def test_golden_rope():
 
 def test_golden_dequant():
     g = golden("ref_vectors.npz")
-    for t in (8, 12, 14):
+    for t in (8, 12, 13, 14, 23):
         want = g[f"deq{t}_out"]
         assert bits_equal(O.dequant(t, g[f"deq{t}_raw"], want.size), want)
+
+
+def scale_err(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def test_golden_matvec_matmul():
+    """The reference's own matvec / matmul outputs (src/kernels.cpp:497-538).
+    The reference is built with -ffast-math, so its sums may be reassociated:
+    within 1e-6 of the output scale (bit-exact for four of the five types)."""
+    g = golden("ref_vectors.npz")
+    for t in (8, 12, 13, 14, 23):
+        w, X = g[f"mv{t}_w"], g[f"mv{t}_x"]
+        n_rows = g[f"mv{t}_y"].size
+        y = O.matvec(t, w, X[0], n_rows)
+        assert scale_err(y, g[f"mv{t}_y"]) <= 1e-6, t
+        Y = O.matmul(t, w, X, n_rows)
+        assert scale_err(Y, g[f"mm{t}_y"]) <= 1e-6, t
+        # every token row of matmul is that token's matvec (tests/test_kernels.cpp:289-314)
+        for i in range(X.shape[0]):
+            assert bits_equal(Y[i], O.matvec(t, w, X[i], n_rows))
 
 
 # ------------------------------------------------------ live reference build
@@ -134,7 +158,7 @@ def test_live_reference_fp32_path():
 def test_live_reference_dequant():
     from aero_amd import workloads as W
     rng = np.random.default_rng(98)
-    for t in (O.Q8_0, O.Q4_K, O.Q6_K):
+    for t in (O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_XS):
         raw = W.make_table(t, 257, rng)
         n = 257 * O.block_values(t)
         assert bits_equal(O.dequant(t, raw, n), R.dequant(t, raw, n))
@@ -143,6 +167,70 @@ def test_live_reference_dequant():
         n = 2000 // O.block_bytes(t)
         a, b = O.dequant(t, raw, n), R.dequant(t, raw, n)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@ref_built
+def test_live_reference_matvec():
+    from aero_amd import workloads as W
+    rng = np.random.default_rng(97)
+    for t in (O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_XS):
+        bv = O.block_values(t)
+        for n_rows, n_cols in ((1, bv), (37, 4 * 256), (5, 4096)):
+            w = W.make_table(t, n_rows * n_cols // bv, rng)
+            X = rng.standard_normal((2, n_cols)).astype(np.float32)
+            assert scale_err(O.matvec(t, w, X[0], n_rows), R.matvec(t, w, X[0], n_rows)) <= 1e-6
+            assert scale_err(O.matmul(t, w, X, n_rows), R.matmul(t, w, X, n_rows)) <= 1e-6
+
+
+def test_q5k_iq4xs_closed_forms():
+    """Q5_K with qh = 0 is Q4_K of the same fields; each qh bit adds 16 to its
+    quant; IQ4_XS with one nibble value per block is dl * codebook[value]."""
+    from aero_amd import workloads as W
+    rng = np.random.default_rng(96)
+    q4 = W.make_table(O.Q4_K, 8, rng).reshape(8, 144)
+    q5 = np.zeros((8, 176), np.uint8)
+    q5[:, :16], q5[:, 48:] = q4[:, :16], q4[:, 16:]
+    assert bits_equal(O.dequant(O.Q5_K, q5, 8 * 256), O.dequant(O.Q4_K, q4, 8 * 256))
+    q5[:, 16:48] = 0xFF
+    d = _f16(q5[:, 0:2].copy()).astype(np.float64).reshape(-1, 1)
+    dmin = _f16(q5[:, 2:4].copy()).astype(np.float64).reshape(-1, 1)
+    got = O.dequant(O.Q5_K, q5, 8 * 256).reshape(8, 256).astype(np.float64)
+    base = O.dequant(O.Q4_K, q4, 8 * 256).reshape(8, 256).astype(np.float64)
+    # every value gains 16 * d * sc of its sub-block: (got - base) / d is 16*sc, an integer
+    steps = (got - base) / d
+    assert np.allclose(steps, np.round(steps), atol=1e-3) and (np.round(steps) % 16 == 0).all()
+    del dmin
+    codebook = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89,
+                         113], np.float32)
+    for k in range(16):
+        blk = np.zeros(136, np.uint8)
+        blk[0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+        blk[2:4] = [0b10010011, 0b01101100]           # scales_h: 2 bits per sub-block
+        blk[4:8] = [0x21, 0x43, 0x65, 0x87]           # scales_l: 4 bits per sub-block
+        blk[8:] = k | (k << 4)
+        out = O.dequant(O.IQ4_XS, blk, 256).reshape(8, 32)
+        sh = int(blk[2]) | (int(blk[3]) << 8)
+        for ib in range(8):
+            ls = ((int(blk[4 + ib // 2]) >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+            dl = np.float32(0.25) * np.float32(ls - 32)
+            assert bits_equal(out[ib], np.full(32, dl * codebook[k], np.float32)), (k, ib)
+
+
+def test_matvec_is_dequant_times_x():
+    """y = dequant(W) @ x, evaluated in float64 (the definition of matvec)."""
+    from aero_amd import workloads as W
+    rng = np.random.default_rng(95)
+    for t in (O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_XS):
+        n_rows, n_cols = 19, 2048
+        bv = O.block_values(t)
+        w = W.make_table(t, n_rows * n_cols // bv, rng)
+        x = rng.standard_normal(n_cols).astype(np.float32)
+        Wf = O.dequant(t, w, n_rows * n_cols).astype(np.float64).reshape(n_rows, n_cols)
+        assert scale_err(O.matvec(t, w, x, n_rows), Wf @ x.astype(np.float64)) <= 1e-6, t
+    with pytest.raises(ValueError):
+        O.matvec(O.Q4_K, np.zeros(144, np.uint8), np.zeros(255, np.float32), 1)   # n_cols % 256
+    with pytest.raises(ValueError):
+        O.matvec(O.F32, np.zeros(64, np.uint8), np.zeros(16, np.float32), 1)     # not a block type
 
 
 # ------------------------------------------------------------- closed forms
@@ -313,6 +401,37 @@ def np_q6k(raw, qh_shift_off=0):
     return out.reshape(-1)
 
 
+def np_iq4xs(raw, swap_scale_bits=False):
+    """numpy restatement of IQ4_XS dequant, with an optional planted mistake."""
+    cb = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+                  np.float32)
+    a = raw.reshape(-1, 136)
+    d = _f16(a[:, 0:2].copy()).reshape(-1)
+    sh = a[:, 2].astype(np.int32) | (a[:, 3].astype(np.int32) << 8)
+    out = np.empty((a.shape[0], 256), np.float32)
+    for ib in range(8):
+        lo = (a[:, 4 + ib // 2].astype(np.int32) >> (4 * (ib % 2))) & 15
+        hi = (sh >> (2 * (7 - ib if swap_scale_bits else ib))) & 3
+        dl = d * ((lo | (hi << 4)) - 32).astype(np.float32)
+        q = a[:, 8 + 16 * ib:8 + 16 * ib + 16]
+        out[:, 32 * ib:32 * ib + 16] = dl[:, None] * cb[q & 15]
+        out[:, 32 * ib + 16:32 * ib + 32] = dl[:, None] * cb[q >> 4]
+    return out.reshape(-1)
+
+
+def np_matvec_q4k(w, x, n_rows, drop_min=False):
+    """numpy Q4_K matvec through dequant, optionally dropping the dmin*m term."""
+    a = w.reshape(n_rows, -1, 144)
+    y = np.zeros(n_rows)
+    for r in range(n_rows):
+        for b in range(a.shape[1]):
+            blk = a[r, b].copy()
+            if drop_min:
+                blk[2:4] = 0
+            y[r] += O.dequant(O.Q4_K, blk, 256).astype(np.float64) @ x[256 * b:256 * (b + 1)]
+    return y
+
+
 def test_planted_quant_mistakes_are_caught():
     k = golden("kat_quant.npz")
     g = golden("ref_vectors.npz")
@@ -323,6 +442,12 @@ def test_planted_quant_mistakes_are_caught():
     assert not bits_equal(np_q4k(g["deq12_raw"], naive_scales=True), g["deq12_out"])
     assert bits_equal(np_q6k(g["deq14_raw"]), g["deq14_out"])
     assert not bits_equal(np_q6k(g["deq14_raw"], qh_shift_off=1), g["deq14_out"])
+    assert bits_equal(np_iq4xs(g["deq23_raw"]), g["deq23_out"])
+    assert not bits_equal(np_iq4xs(g["deq23_raw"], swap_scale_bits=True), g["deq23_out"])
+    w, x = g["mv12_w"], g["mv12_x"][0].astype(np.float64)
+    n_rows = g["mv12_y"].size
+    assert scale_err(np_matvec_q4k(w, x, n_rows), g["mv12_y"]) <= 1e-6
+    assert scale_err(np_matvec_q4k(w, x, n_rows, drop_min=True), g["mv12_y"]) > 1e-3
 
 
 def test_planted_fp32_mistakes_are_caught():
