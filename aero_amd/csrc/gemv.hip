@@ -4,15 +4,16 @@
 // (:78-250), which it calls between the elementwise ops of a layer.
 //
 // One wave (a 64-thread workgroup) owns R consecutive output rows. It walks
-// the columns in chunks of U 256-value steps: the chunk's quant blocks of each
-// of its rows (contiguous in W) are loaded with coalesced 32-bit loads, all
-// issued before any is used, and staged in LDS; then in each step lane l takes
-// values 4l..4l+3 (the gather's lane layout, quant_blocks.hpp), loads one
-// float4 of x per token, and for each row expands its four weights into
-// (q[4], f, g) and accumulates f*sum(q*x) - g*sum(x) — the factoring of the
-// reference's block dots, so sum(x) is shared by all R rows and a row costs
-// four multiply-adds per lane per step. x is read once per step for R rows.
-// At the end each (row, token) sum is an xor-butterfly over the wave.
+// the columns in chunks of U 256-value steps (U*T = 8): the chunk's quant
+// blocks of each of its rows (contiguous in W) are loaded with coalesced
+// 32-bit loads and staged in LDS, and the lane's x float4 of every step of the
+// chunk is loaded into registers; the next chunk's loads are issued before the
+// current chunk is computed, so one chunk is always in flight. In each step
+// lane l takes values 4l..4l+3 (the gather's lane layout, quant_blocks.hpp)
+// and for each row expands its four weights into (q[4], f, g) and accumulates
+// f*sum(q*x) - g*sum(x) — the factoring of the reference's block dots, so
+// sum(x) is shared by all R rows and a row costs four multiply-adds per lane
+// per step. At the end each (row, token) sum is an xor-butterfly over the wave.
 //
 // HBM bytes per launch: the weight blocks once (n_rows * n_cols/bv * bb) plus
 // x and y; x is re-read from L2 by every wave. Results differ from the
@@ -39,17 +40,339 @@ struct GemvParams {
     int64_t x_stride, y_stride;
 };
 
-template <int TYPE, int R, int U, int T>
-__global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
-    using Q = QT<TYPE>;
-    constexpr int BPS = 256 / Q::BV;                           // blocks per step
-    constexpr int MAX_DW = (U * BPS * Q::BB + 3 + 3) / 4;     // + misalignment
-    constexpr int PER = (MAX_DW + 63) / 64;
-    __shared__ __align__(16) uint32_t stage[R][PER * 64];
+// ------------------------------------------------------------ lane groups
+// A super-step is 2048 consecutive columns; lane l takes the 32-value group
+// at columns 32l..32l+31 of it: group l%8 of block l/8 for the 256-value
+// types, block l for Q8_0. A lane loads only its group's words (the 8 lanes
+// of a block share the header through L1) and turns each quant byte into a
+// float with one byte-convert (unsigned forms; signed types are offset by
+// 128 or 32 and corrected through sum(x)). Its contribution is
+//     f0*sum(u*x)[0:16] + f1*sum(u*x)[16:32] - g0*sum(x)[0:16] - g1*sum(x)[16:32]
+// which is the reference's block dot for the group with q = u - offset.
+// Loading is split from expanding (RawG::load only issues loads, RawG::expand
+// is ALU), so the next super-step's words can be in flight while this one is
+// computed.
+struct Group {
+    uint32_t u[8];         // 32 unsigned bytes, value i in byte i%4 of u[i/4]
+    float f0, f1, g0, g1;
+};
 
-    const int l = threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.x * R;
-    const int steps = (p.n_cols + 255) / 256;
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+__device__ __forceinline__ uint32_t ld16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+// fp16 scale -> fp32 with the hardware conversion: exact for every finite
+// half (subnormals included: fp16 denormals are not flushed); only a
+// signalling NaN's payload could differ from the reference's bit copy.
+__device__ __forceinline__ float f16f(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+}
+
+// The (sc, m) pair of K-quant sub-block k (0..7, per lane) from the 12-byte
+// scale field (src/kernels.cpp:65-73), without branches.
+__device__ __forceinline__ void kq_scale_min_sel(uint32_t s0, uint32_t s1, uint32_t s2, int k,
+                                                 uint32_t& sc, uint32_t& mn) {
+    const bool lo = k < 4;
+    const int kk = k & 3;
+    const uint32_t a = lo ? s0 : s1;                 // byte k   (k < 4) / byte k (k >= 4)
+    const uint32_t b = lo ? s1 : s2;                 // byte k+4
+    const uint32_t bk = (a >> (8 * kk)) & 0xFFu;     // b[k]
+    const uint32_t bk4 = (b >> (8 * kk)) & 0xFFu;    // b[k+4]
+    const uint32_t bkm4 = (s0 >> (8 * kk)) & 0xFFu;  // b[k-4] (k >= 4)
+    sc = lo ? (bk & 63u) : ((bk4 & 15u) | ((bkm4 >> 6) << 4));
+    mn = lo ? (bk4 & 63u) : ((bk4 >> 4) | ((bk >> 6) << 4));
+}
+
+// Byte e of w as a float, with the byte-convert instruction (one VALU op).
+template <int E>
+__device__ __forceinline__ float cvt_ub(uint32_t w) {
+    float r;
+    if constexpr (E == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (E == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (E == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+
+// 32 bytes at a 2-byte aligned address as 9 aligned words; the 9th is read
+// only when the bytes straddle it (else the 8th again), so no load touches a
+// word that holds none of the 32 bytes.
+struct Span32 {
+    uint32_t w[9];
+    uint32_t sh;
+    __device__ __forceinline__ void load(const uint8_t* p) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        sh = (uint32_t)(a & 3u);
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(a - sh);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = q[i];
+        w[8] = q[sh ? 8 : 7];
+    }
+    __device__ __forceinline__ uint32_t word(int m) const {
+        return __builtin_amdgcn_alignbyte(w[m + 1], w[m], sh);
+    }
+};
+
+template <int TYPE> struct RawG;
+
+// Q8_0 (src/kernels.cpp:78-84): block = group (bytes 0..33: d, q[32]);
+// u = q ^ 0x80 = q + 128.
+template <> struct RawG<AERO_DTYPE_Q8_0> {
+    uint32_t d;
+    Span32 q;
+    __device__ __forceinline__ void load(const uint8_t* blk, int) {
+        d = ld16(blk);
+        q.load(blk + 2);
+    }
+    __device__ __forceinline__ Group expand(int) const {
+        Group g;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) g.u[m] = q.word(m) ^ 0x80808080u;
+        g.f0 = g.f1 = f16f(d);
+        g.g0 = g.g1 = g.f0 * 128.0f;
+        return g;
+    }
+};
+
+// Q4_K (src/kernels.cpp:123-156): group k = sub-block k; nibbles of
+// qs[32(k/2) ..], low for even k, high for odd.
+template <> struct RawG<AERO_DTYPE_Q4_K> {
+    uint32_t dd, s0, s1, s2, q[8];
+    __device__ __forceinline__ void load(const uint8_t* blk, int k) {
+        dd = ld32(blk); s0 = ld32(blk + 4); s1 = ld32(blk + 8); s2 = ld32(blk + 12);
+        const uint8_t* qs = blk + 16 + 32 * (k >> 1);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) q[m] = ld32(qs + 4 * m);
+    }
+    __device__ __forceinline__ Group expand(int k) const {
+        uint32_t sc, mn;
+        kq_scale_min_sel(s0, s1, s2, k, sc, mn);
+        const int sh = (k & 1) ? 4 : 0;
+        Group g;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) g.u[m] = (q[m] >> sh) & 0x0F0F0F0Fu;
+        g.f0 = g.f1 = f16f(dd) * (float)sc;
+        g.g0 = g.g1 = f16f(dd >> 16) * (float)mn;
+        return g;
+    }
+};
+
+// Q5_K (src/kernels.cpp:90-121): Q4_K plus bit k of qh[i] as bit 4.
+template <> struct RawG<AERO_DTYPE_Q5_K> {
+    uint32_t dd, s0, s1, s2, h[8], q[8];
+    __device__ __forceinline__ void load(const uint8_t* blk, int k) {
+        dd = ld32(blk); s0 = ld32(blk + 4); s1 = ld32(blk + 8); s2 = ld32(blk + 12);
+        const uint8_t* qs = blk + 48 + 32 * (k >> 1);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            h[m] = ld32(blk + 16 + 4 * m);
+            q[m] = ld32(qs + 4 * m);
+        }
+    }
+    __device__ __forceinline__ Group expand(int k) const {
+        uint32_t sc, mn;
+        kq_scale_min_sel(s0, s1, s2, k, sc, mn);
+        const int sh = (k & 1) ? 4 : 0;
+        Group g;
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            g.u[m] = ((q[m] >> sh) & 0x0F0F0F0Fu) | (((h[m] >> k) & 0x01010101u) << 4);
+        g.f0 = g.f1 = f16f(dd) * (float)sc;
+        g.g0 = g.g1 = f16f(dd >> 16) * (float)mn;
+        return g;
+    }
+};
+
+// Q6_K (src/kernels.cpp:170-200): group k = half h = k/4, quarter kq = k%4:
+// low (kq < 2) or high nibbles of ql[64h + 32(kq&1) ..] and bits 2kq of
+// qh[32h ..]; scale sc[8h + 2kq] for the first 16 values, sc[8h + 2kq + 1]
+// for the next; u = q + 32.
+template <> struct RawG<AERO_DTYPE_Q6_K> {
+    Span32 ql, qh;
+    uint32_t scw, d;
+    __device__ __forceinline__ void load(const uint8_t* blk, int k) {
+        const int h = k >> 2, kq = k & 3;
+        ql.load(blk + 64 * h + 32 * (kq & 1));
+        qh.load(blk + 128 + 32 * h);
+        scw = ld16(blk + 192 + 8 * h + 2 * kq);
+        d = ld16(blk + 208);
+    }
+    __device__ __forceinline__ Group expand(int k) const {
+        const int kq = k & 3;
+        const int sl = kq >= 2 ? 4 : 0, shh = 2 * kq;
+        Group g;
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            g.u[m] = ((ql.word(m) >> sl) & 0x0F0F0F0Fu) | (((qh.word(m) >> shh) & 0x03030303u) << 4);
+        const float df = f16f(d);
+        g.f0 = df * (float)(int8_t)(scw & 0xFFu);
+        g.f1 = df * (float)(int8_t)((scw >> 8) & 0xFFu);
+        g.g0 = g.f0 * 32.0f;
+        g.g1 = g.f1 * 32.0f;
+        return g;
+    }
+};
+
+// IQ4_XS (src/kernels.cpp:217-238): sub-block k; values 0..15 from the low
+// nibbles of q[16k ..], 16..31 from the high nibbles; u = codebook + 128,
+// looked up with byte permutes of the packed codebook.
+__device__ __forceinline__ uint32_t iq4_bytes(uint32_t nib) {  // 4 nibbles, one per byte
+    constexpr uint32_t C0 = 0xBFAD9881u ^ 0x80808080u, C1 = 0xF6EADDCFu ^ 0x80808080u;
+    constexpr uint32_t C2 = 0x26190D01u ^ 0x80808080u, C3 = 0x71594535u ^ 0x80808080u;
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(C1, C0, sel);  // entries 0..7
+    const uint32_t hi = __builtin_amdgcn_perm(C3, C2, sel);  // entries 8..15
+    const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+    return (lo & ~m) | (hi & m);
+}
+template <> struct RawG<AERO_DTYPE_IQ4_XS> {
+    uint32_t w0, sl, q[4];
+    __device__ __forceinline__ void load(const uint8_t* blk, int k) {
+        w0 = ld32(blk); sl = ld32(blk + 4);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) q[m] = ld32(blk + 8 + 16 * k + 4 * m);
+    }
+    __device__ __forceinline__ Group expand(int k) const {
+        const uint32_t shw = w0 >> 16;
+        const uint32_t ls = ((byte_of(sl, k >> 1) >> (4 * (k & 1))) & 15u) |
+                            (((shw >> (2 * k)) & 3u) << 4);
+        Group g;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            g.u[m] = iq4_bytes(q[m] & 0x0F0F0F0Fu);
+            g.u[m + 4] = iq4_bytes((q[m] >> 4) & 0x0F0F0F0Fu);
+        }
+        g.f0 = g.f1 = f16f(w0) * (float)((int)ls - 32);
+        g.g0 = g.g1 = g.f0 * 128.0f;
+        return g;
+    }
+};
+
+constexpr int kGemvWaves = 4;  // waves per workgroup, sharing each x slice
+
+// Lane-group coordinates of super-step ss (clamped into the row).
+template <int TYPE>
+__device__ __forceinline__ void lane_group(const GemvParams& p, int ss, int l, int& blk, int& k,
+                                           bool& live) {
+    using Q = QT<TYPE>;
+    const int col = ss * 2048 + 32 * l;
+    live = col < p.n_cols;
+    const int colc = live ? col : p.n_cols - 32;
+    blk = colc / Q::BV;
+    k = (colc % Q::BV) / 32;
+}
+
+// x of one super-step: per token 2048 floats in 128 runs of 16; a thread
+// stages XG runs (its four float4 are loaded into registers one step ahead)
+// and also stores each run's sum, so lanes read sum(x) instead of adding it.
+template <int T> struct XStage {
+    static constexpr int XG = T >= 2 ? T / 2 : 1;  // runs per thread (128*T / 256, at least 1)
+};
+
+template <int TYPE, int R, int T>
+__device__ __forceinline__ void load_step(const GemvParams& p, int ss, int l, int64_t r0,
+                                          int tid, RawG<TYPE> (&w)[R],
+                                          float4 (&xr)[XStage<T>::XG][4]) {
+    using Q = QT<TYPE>;
+    // this thread's runs of the x slice first, then the wave's weight groups
+#pragma unroll
+    for (int i = 0; i < XStage<T>::XG; ++i) {
+        const int run = min(tid + 64 * kGemvWaves * i, 128 * T - 1);  // [0, 128*T)
+        const int t = run >> 7, j = run & 127;
+        const int tt = t < p.n_tok ? t : 0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int c = min(ss * 2048 + 16 * j + 4 * m, p.n_cols - 4);
+            xr[i][m] = *reinterpret_cast<const float4*>(p.x + tt * p.x_stride + c);
+        }
+    }
+    int blk, k;
+    bool live;
+    lane_group<TYPE>(p, ss, l, blk, k, live);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = min(r0 + r, p.n_rows - 1);
+        w[r].load(p.w + row * p.rb + (int64_t)blk * Q::BB, k);
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void store_x(float4 (*xs)[512], float (*xsum)[128],
+                                        const float4 (&xr)[XStage<T>::XG][4], int tid) {
+#pragma unroll
+    for (int i = 0; i < XStage<T>::XG; ++i) {
+        const int run = tid + 64 * kGemvWaves * i;
+        if (run < 128 * T) {
+            const int t = run >> 7, j = run & 127;
+            float sum = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                xs[t][4 * j + m] = xr[i][m];
+                sum += (xr[i][m].x + xr[i][m].y) + (xr[i][m].z + xr[i][m].w);
+            }
+            xsum[t][j] = sum;
+        }
+    }
+}
+
+template <int TYPE, int R, int T>
+__device__ __forceinline__ void compute_step(const GemvParams& p, int ss, int l,
+                                             const RawG<TYPE> (&w)[R], const float4 (*xs)[512],
+                                             const float (*xsum)[128], float (&acc)[R][T]) {
+    int blk, k;
+    bool live;
+    lane_group<TYPE>(p, ss, l, blk, k, live);
+    Group g[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) g[r] = w[r].expand(k);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float4 xv[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) xv[m] = xs[t][8 * l + m];
+        const float2 sx = *reinterpret_cast<const float2*>(&xsum[t][2 * l]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float q0 = 0.0f, q1 = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                q0 = __builtin_fmaf(cvt_ub<0>(g[r].u[m]), xv[m].x, q0);
+                q0 = __builtin_fmaf(cvt_ub<1>(g[r].u[m]), xv[m].y, q0);
+                q0 = __builtin_fmaf(cvt_ub<2>(g[r].u[m]), xv[m].z, q0);
+                q0 = __builtin_fmaf(cvt_ub<3>(g[r].u[m]), xv[m].w, q0);
+                q1 = __builtin_fmaf(cvt_ub<0>(g[r].u[m + 4]), xv[m + 4].x, q1);
+                q1 = __builtin_fmaf(cvt_ub<1>(g[r].u[m + 4]), xv[m + 4].y, q1);
+                q1 = __builtin_fmaf(cvt_ub<2>(g[r].u[m + 4]), xv[m + 4].z, q1);
+                q1 = __builtin_fmaf(cvt_ub<3>(g[r].u[m + 4]), xv[m + 4].w, q1);
+            }
+            float a = acc[r][t];
+            a = __builtin_fmaf(g[r].f0, q0, a);
+            a = __builtin_fmaf(g[r].f1, q1, a);
+            a = __builtin_fmaf(-g[r].g0, sx.x, a);
+            a = __builtin_fmaf(-g[r].g1, sx.y, a);
+            acc[r][t] = live ? a : acc[r][t];
+        }
+    }
+}
+
+// A workgroup of kGemvWaves waves covers kGemvWaves*R rows; each wave owns R
+// of them. Per super-step the workgroup stages the 2048-column x slice of
+// every token in LDS (double-buffered) and each wave reads its lanes' 32
+// columns from there. Loads run one super-step ahead: the next slice of x
+// and the next weight groups are issued (x first) before the current step is
+// computed, always for super-step min(ss+1, last) so that every load is
+// unconditional and the compiler's wait counts stay exact.
+template <int TYPE, int R, int T>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvParams p) {
+    __shared__ __align__(16) float4 xs[2][T][512];
+    __shared__ __align__(16) float xsum[2][T][128];
+
+    const int tid = threadIdx.x;
+    const int l = tid & 63;
+    const int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + (tid >> 6)) * R;
+    const int n_ss = (p.n_cols + 2047) / 2048;
 
     float acc[R][T];
 #pragma unroll
@@ -57,61 +380,21 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[r][t] = 0.0f;
 
-    for (int s0 = 0; s0 < steps; s0 += U) {
-        const int nv = min(U * 256, p.n_cols - s0 * 256);  // values in this chunk
-        const int nbytes = (nv / Q::BV) * Q::BB;
-        // Each row's chunk: the 4-byte words covering it (aligned down; rows of
-        // Q8_0 / Q6_K may start 2 bytes past a word). Rows past the end re-read
-        // the last row, and lanes past the chunk its last word, so every load is
-        // unconditional and all are in flight together.
-        int off[R];
-        uint32_t wv[R][PER];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t row = min(r0 + r, p.n_rows - 1);
-            const uint8_t* g = p.w + row * p.rb + (int64_t)(s0 * 256 / Q::BV) * Q::BB;
-            off[r] = (int)(reinterpret_cast<uintptr_t>(g) & 3u);
-            const uint32_t* g4 = reinterpret_cast<const uint32_t*>(g - off[r]);
-            const int n_dw = (off[r] + nbytes + 3) >> 2;
-#pragma unroll
-            for (int i = 0; i < PER; ++i) wv[r][i] = g4[min(l + 64 * i, n_dw - 1)];
-        }
-        __syncthreads();  // the previous chunk's LDS reads are done
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int i = 0; i < PER; ++i) stage[r][l + 64 * i] = wv[r][i];
+    RawG<TYPE> wa[R], wb[R];
+    float4 xr[XStage<T>::XG][4];
+    load_step<TYPE, R, T>(p, 0, l, r0, tid, wa, xr);
+    store_x<T>(xs[0], xsum[0], xr, tid);
+    __syncthreads();
+    for (int ss = 0; ss < n_ss; ss += 2) {
+        load_step<TYPE, R, T>(p, min(ss + 1, n_ss - 1), l, r0, tid, wb, xr);
+        compute_step<TYPE, R, T>(p, ss, l, wa, xs[0], xsum[0], acc);
+        store_x<T>(xs[1], xsum[1], xr, tid);
         __syncthreads();
-
-#pragma unroll
-        for (int st = 0; st < U; ++st) {
-            const int v0 = st * 256 + 4 * l;
-            if (v0 >= nv) break;
-            float4 xv[T];
-            float sx[T];
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const int tt = t < p.n_tok ? t : 0;
-                xv[t] = *reinterpret_cast<const float4*>(p.x + tt * p.x_stride + s0 * 256 + v0);
-                sx[t] = ((xv[t].x + xv[t].y) + xv[t].z) + xv[t].w;
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                typename Q::Raw raw;
-                load_raw(reinterpret_cast<const uint8_t*>(stage[r]) + off[r] + (v0 / Q::BV) * Q::BB,
-                         l, raw);
-                const Quad w4 = expand(raw, l);
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    float qx = w4.q[0] * xv[t].x;
-                    qx = __builtin_fmaf(w4.q[1], xv[t].y, qx);
-                    qx = __builtin_fmaf(w4.q[2], xv[t].z, qx);
-                    qx = __builtin_fmaf(w4.q[3], xv[t].w, qx);
-                    acc[r][t] = __builtin_fmaf(w4.f, qx, acc[r][t]);
-                    if (HasMin<TYPE>::value) acc[r][t] = __builtin_fmaf(-w4.g, sx[t], acc[r][t]);
-                }
-            }
-        }
+        if (ss + 1 >= n_ss) break;
+        load_step<TYPE, R, T>(p, min(ss + 2, n_ss - 1), l, r0, tid, wa, xr);
+        compute_step<TYPE, R, T>(p, ss + 1, l, wb, xs[1], xsum[1], acc);
+        store_x<T>(xs[0], xsum[0], xr, tid);
+        __syncthreads();
     }
 
 #pragma unroll
@@ -125,27 +408,22 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 
 using GemvKernel = void (*)(GemvParams);
 
-template <int TYPE, int R, int U>
+template <int TYPE, int R>
 GemvKernel pick_t(int T) {
     switch (T) {
-    case 1: return gemv_kernel<TYPE, R, U, 1>;
-    case 2: return gemv_kernel<TYPE, R, U, 2>;
-    case 4: return gemv_kernel<TYPE, R, U, 4>;
-    case 8: return gemv_kernel<TYPE, R, U, 8>;
+    case 1: return gemv_kernel<TYPE, R, 1>;
+    case 2: return gemv_kernel<TYPE, R, 2>;
+    case 4: return gemv_kernel<TYPE, R, 4>;
     default: return nullptr;
     }
 }
 
-// Steps per chunk: 16 (Q8_0: 8, its blocks take 1.9x the LDS of Q4_K's).
-template <int TYPE> constexpr int chunk_steps() { return TYPE == AERO_DTYPE_Q8_0 ? 8 : 16; }
-
 template <int TYPE>
 GemvKernel pick_r(int R, int T) {
-    constexpr int U = chunk_steps<TYPE>();
     switch (R) {
-    case 1: return pick_t<TYPE, 1, U>(T);
-    case 2: return pick_t<TYPE, 2, U>(T);
-    case 4: return pick_t<TYPE, 4, U>(T);
+    case 1: return pick_t<TYPE, 1>(T);
+    case 2: return pick_t<TYPE, 2>(T);
+    case 4: return pick_t<TYPE, 4>(T);
     default: return nullptr;
     }
 }
@@ -163,7 +441,7 @@ GemvKernel pick_gemv(int dtype, int R, int T) {
 
 }  // namespace
 
-// y[t, r] for t < n_tok: tokens are taken in groups of up to 8 per launch
+// y[t, r] for t < n_tok: tokens are taken in groups of up to 4 per launch
 // (each group re-reads W; a token-tiled GEMM is the prefill path).
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
               int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s) {
@@ -194,18 +472,19 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         return false;
     }
     if (n_rows == 0 || n_tok == 0) return true;
-    // rows per wave: share each x load across more rows while the grid keeps
-    // >= 1024 waves
-    int R = n_rows >= 4 * 1024 ? 4 : (n_rows >= 2 * 1024 ? 2 : 1);
+    // rows per wave: up to 4 (2 for the 2-byte aligned Q8_0 / Q6_K blocks, whose
+    // words take two loads each) while the grid keeps >= 512 workgroups
+    int R = (dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q6_K) ? 2 : 4;
+    while (R > 1 && (n_rows + R * kGemvWaves - 1) / (R * kGemvWaves) < 512) R /= 2;
     R = tune("gemv_r", R);
-    const int64_t waves = (n_rows + R - 1) / R;
-    if (waves > 0x7fffffff) {
+    const int64_t wgs = (n_rows + (int64_t)R * kGemvWaves - 1) / ((int64_t)R * kGemvWaves);
+    if (wgs > 0x7fffffff) {
         set_error("matvec: grid too large");
         return false;
     }
-    for (int64_t t0 = 0; t0 < n_tok; t0 += 8) {
-        const int nt = (int)std::min<int64_t>(8, n_tok - t0);
-        const int T = nt == 1 ? 1 : (nt == 2 ? 2 : (nt <= 4 ? 4 : 8));
+    for (int64_t t0 = 0; t0 < n_tok; t0 += 4) {
+        const int nt = (int)std::min<int64_t>(4, n_tok - t0);
+        const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
         GemvKernel k = pick_gemv(dtype, R, T);
         if (k == nullptr) {
             set_error("matvec: no kernel for rows/wave %d", R);
@@ -213,7 +492,8 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         }
         GemvParams p{w, x + t0 * n_cols, y + t0 * n_rows, n_rows, (int)n_cols, rb, nt,
                      n_cols, n_rows};
-        if (!launch("gemv_kernel", k, dim3((unsigned)waves), dim3(64), 0, s, p)) return false;
+        if (!launch("gemv_kernel", k, dim3((unsigned)wgs), dim3(64 * kGemvWaves), 0, s, p))
+            return false;
     }
     return true;
 }

@@ -29,6 +29,7 @@ single-threaded like the reference, over a bounded sample.
     python bench.py --all-shapes        # per-op table over every layer shape
     python bench.py --all-shapes --only OP   # one op over every layer shape
     python bench.py --variants          # every op variant at the 512-token shape
+    python bench.py --gemv              # quantised GEMV (decode projections)
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
 """
@@ -67,6 +68,7 @@ def parse_args(argv=None):
     p.add_argument("--shapes", default=None, help="comma list for --all-shapes / --variants")
     p.add_argument("--variants", action="store_true",
                    help="every op variant at the Llama-3-8B 512-token geometry")
+    p.add_argument("--gemv", action="store_true", help="quantised GEMV cases")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
     p.add_argument("--copy-calibration", action="store_true")
     p.add_argument("--host-abi", action="store_true",
@@ -490,6 +492,8 @@ def main(argv=None):
         return all_shapes(a)
     if a.variants:
         return variants(a)
+    if a.gemv:
+        return gemv(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -585,6 +589,63 @@ def variants(a):
         e = op_entry(path.bytes()[op], path.rows()[op], statistics.mean(ker[op]) * 1e3, sus[op])
         print(json.dumps({"variant": name, "op": op, **e}), flush=True)
         del path
+    return 0
+
+
+GEMV_CASES = [
+    # (name, dtype, n_rows, n_cols): Llama-3-8B decode projections in Q4_K, and
+    # each block type at the 4096 x 4096 / 14336 x 4096 shapes
+    ("attn_q_4096x4096", 12, 4096, 4096), ("attn_kv_1024x4096", 12, 1024, 4096),
+    ("ffn_gate_14336x4096", 12, 14336, 4096), ("ffn_down_4096x14336", 12, 4096, 14336),
+    ("q8_0_4096x4096", 8, 4096, 4096), ("q8_0_14336x4096", 8, 14336, 4096),
+    ("q5_k_14336x4096", 13, 14336, 4096), ("q6_k_14336x4096", 14, 14336, 4096),
+    ("iq4_xs_14336x4096", 23, 14336, 4096),
+]
+
+
+def gemv(a):
+    """Quantised GEMV: sustained time per launch (back to back over a > 1 GiB
+    rotation of weight copies), weight GB/s and fraction of HBM peak, for 1, 4
+    and 8 tokens per launch."""
+    from aero_amd import ops, workloads as W
+    from aero_amd.device import DeviceArray as DA, Event, Plan, Stream
+
+    rng = np.random.default_rng(0)
+    names = a.shapes.split(",") if a.shapes else [c[0] for c in GEMV_CASES]
+    for name, t, n_rows, n_cols in GEMV_CASES:
+        if name not in names:
+            continue
+        bv, bb = W.BLOCK[t]
+        w0 = DA.from_numpy(W.make_table(t, n_rows * n_cols // bv, rng))
+        wbytes = w0.nbytes
+        n_sets = min(256, max(4, -(-SUSTAINED_ROTATION // wbytes)))
+        ws = [w0] + [w0.clone() for _ in range(n_sets - 1)]
+        res = {"case": name, "dtype": t, "n_rows": n_rows, "n_cols": n_cols,
+               "weight_bytes": wbytes}
+        for n_tok in (1, 4, 8):
+            X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
+            Y = DA.empty((n_tok, n_rows))
+            plan = Plan()
+            with plan:
+                for w in ws:
+                    ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok)
+            stream = Stream()
+            plan.launch(stream)
+            e0, e1 = Event(), Event()
+            e0.record(stream)
+            for _ in range(SUSTAINED_REPS):
+                plan.launch(stream)
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / (SUSTAINED_REPS * len(ws))
+            b = wbytes + 4 * n_tok * (n_cols + n_rows)
+            gbs = b / (us * 1e-6) / 1e9
+            res[f"t{n_tok}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            plan.destroy()
+            stream.destroy()
+        print(json.dumps(res), flush=True)
+        del ws, w0
     return 0
 
 
