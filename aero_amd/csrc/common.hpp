@@ -126,6 +126,10 @@ struct StreamOut {
                        __builtin_bit_cast(uint32_t, v.z), __builtin_bit_cast(uint32_t, v.w)};
         __builtin_amdgcn_raw_buffer_store_b128(d, rsrc, (int)byte_off, 0, kStorePolicy);
     }
+    __device__ __forceinline__ void store1(uint32_t byte_off, float v) const {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rsrc, (int)byte_off,
+                                              0, kStorePolicy);
+    }
 };
 
 // ------------------------------------------------------- device helpers

@@ -86,14 +86,126 @@ __device__ __forceinline__ void kq_scale_min_sel(uint32_t s0, uint32_t s1, uint3
 }
 
 // Byte e of w as a float, with the byte-convert instruction (one VALU op).
+#ifndef AERO_CVT_ASM
+#define AERO_CVT_ASM asm
+#endif
 template <int E>
 __device__ __forceinline__ float cvt_ub(uint32_t w) {
+#ifdef AERO_CVT_C
+    return (float)((w >> (8 * E)) & 0xFFu);
+#endif
     float r;
-    if constexpr (E == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
-    else if constexpr (E == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
-    else if constexpr (E == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+    if constexpr (E == 0) AERO_CVT_ASM("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (E == 1) AERO_CVT_ASM("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (E == 2) AERO_CVT_ASM("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+    else AERO_CVT_ASM("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
     return r;
+}
+
+// Multiply-adds of one quant word per row: al[t] += sum_e byte_e(lo) *
+// xl[e][t] and ah[t] += sum_e byte_e(hi) * xh[e][t], each byte turned into a
+// float with the byte-convert instruction right before its multiply-adds.
+// Written as one instruction group so that every convert stays next to its
+// uses (as separate operations the compiler hoists all converts of a step
+// ahead of the multiply-adds and runs out of registers).
+template <int T>
+__device__ __forceinline__ void word_fma(uint32_t lo, uint32_t hi, const float (&xl)[4][T],
+                                         const float (&xh)[4][T], float (&al)[T],
+                                         float (&ah)[T]) {
+    float t0, t1;
+    if constexpr (T == 1) {
+        asm("v_cvt_f32_ubyte0 %0, %4\n\t"
+            "v_fmac_f32 %2, %0, %6\n\t"
+            "v_cvt_f32_ubyte0 %1, %5\n\t"
+            "v_fmac_f32 %3, %1, %10\n\t"
+            "v_cvt_f32_ubyte1 %0, %4\n\t"
+            "v_fmac_f32 %2, %0, %7\n\t"
+            "v_cvt_f32_ubyte1 %1, %5\n\t"
+            "v_fmac_f32 %3, %1, %11\n\t"
+            "v_cvt_f32_ubyte2 %0, %4\n\t"
+            "v_fmac_f32 %2, %0, %8\n\t"
+            "v_cvt_f32_ubyte2 %1, %5\n\t"
+            "v_fmac_f32 %3, %1, %12\n\t"
+            "v_cvt_f32_ubyte3 %0, %4\n\t"
+            "v_fmac_f32 %2, %0, %9\n\t"
+            "v_cvt_f32_ubyte3 %1, %5\n\t"
+            "v_fmac_f32 %3, %1, %13"
+            : "=&v"(t0), "=&v"(t1), "+v"(al[0]), "+v"(ah[0])
+            : "v"(lo), "v"(hi), "v"(xl[0][0]), "v"(xl[1][0]), "v"(xl[2][0]), "v"(xl[3][0]), "v"(xh[0][0]), "v"(xh[1][0]), "v"(xh[2][0]), "v"(xh[3][0]));
+    } else if constexpr (T == 2) {
+        asm("v_cvt_f32_ubyte0 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %8\n\t"
+            "v_fmac_f32 %3, %0, %9\n\t"
+            "v_cvt_f32_ubyte0 %1, %7\n\t"
+            "v_fmac_f32 %4, %1, %16\n\t"
+            "v_fmac_f32 %5, %1, %17\n\t"
+            "v_cvt_f32_ubyte1 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %10\n\t"
+            "v_fmac_f32 %3, %0, %11\n\t"
+            "v_cvt_f32_ubyte1 %1, %7\n\t"
+            "v_fmac_f32 %4, %1, %18\n\t"
+            "v_fmac_f32 %5, %1, %19\n\t"
+            "v_cvt_f32_ubyte2 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %12\n\t"
+            "v_fmac_f32 %3, %0, %13\n\t"
+            "v_cvt_f32_ubyte2 %1, %7\n\t"
+            "v_fmac_f32 %4, %1, %20\n\t"
+            "v_fmac_f32 %5, %1, %21\n\t"
+            "v_cvt_f32_ubyte3 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %14\n\t"
+            "v_fmac_f32 %3, %0, %15\n\t"
+            "v_cvt_f32_ubyte3 %1, %7\n\t"
+            "v_fmac_f32 %4, %1, %22\n\t"
+            "v_fmac_f32 %5, %1, %23"
+            : "=&v"(t0), "=&v"(t1), "+v"(al[0]), "+v"(al[1]), "+v"(ah[0]), "+v"(ah[1])
+            : "v"(lo), "v"(hi), "v"(xl[0][0]), "v"(xl[0][1]), "v"(xl[1][0]), "v"(xl[1][1]), "v"(xl[2][0]), "v"(xl[2][1]), "v"(xl[3][0]), "v"(xl[3][1]), "v"(xh[0][0]), "v"(xh[0][1]), "v"(xh[1][0]), "v"(xh[1][1]), "v"(xh[2][0]), "v"(xh[2][1]), "v"(xh[3][0]), "v"(xh[3][1]));
+    } else {
+        static_assert(T == 4, "T is 1, 2 or 4");
+        asm("v_cvt_f32_ubyte0 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %7\n\t"
+            "v_fmac_f32 %3, %0, %8\n\t"
+            "v_fmac_f32 %4, %0, %9\n\t"
+            "v_fmac_f32 %5, %0, %10\n\t"
+            "v_cvt_f32_ubyte1 %1, %6\n\t"
+            "v_fmac_f32 %2, %1, %11\n\t"
+            "v_fmac_f32 %3, %1, %12\n\t"
+            "v_fmac_f32 %4, %1, %13\n\t"
+            "v_fmac_f32 %5, %1, %14\n\t"
+            "v_cvt_f32_ubyte2 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %15\n\t"
+            "v_fmac_f32 %3, %0, %16\n\t"
+            "v_fmac_f32 %4, %0, %17\n\t"
+            "v_fmac_f32 %5, %0, %18\n\t"
+            "v_cvt_f32_ubyte3 %1, %6\n\t"
+            "v_fmac_f32 %2, %1, %19\n\t"
+            "v_fmac_f32 %3, %1, %20\n\t"
+            "v_fmac_f32 %4, %1, %21\n\t"
+            "v_fmac_f32 %5, %1, %22"
+            : "=&v"(t0), "=&v"(t1), "+v"(al[0]), "+v"(al[1]), "+v"(al[2]), "+v"(al[3])
+            : "v"(lo), "v"(xl[0][0]), "v"(xl[0][1]), "v"(xl[0][2]), "v"(xl[0][3]), "v"(xl[1][0]), "v"(xl[1][1]), "v"(xl[1][2]), "v"(xl[1][3]), "v"(xl[2][0]), "v"(xl[2][1]), "v"(xl[2][2]), "v"(xl[2][3]), "v"(xl[3][0]), "v"(xl[3][1]), "v"(xl[3][2]), "v"(xl[3][3]));
+        asm("v_cvt_f32_ubyte0 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %7\n\t"
+            "v_fmac_f32 %3, %0, %8\n\t"
+            "v_fmac_f32 %4, %0, %9\n\t"
+            "v_fmac_f32 %5, %0, %10\n\t"
+            "v_cvt_f32_ubyte1 %1, %6\n\t"
+            "v_fmac_f32 %2, %1, %11\n\t"
+            "v_fmac_f32 %3, %1, %12\n\t"
+            "v_fmac_f32 %4, %1, %13\n\t"
+            "v_fmac_f32 %5, %1, %14\n\t"
+            "v_cvt_f32_ubyte2 %0, %6\n\t"
+            "v_fmac_f32 %2, %0, %15\n\t"
+            "v_fmac_f32 %3, %0, %16\n\t"
+            "v_fmac_f32 %4, %0, %17\n\t"
+            "v_fmac_f32 %5, %0, %18\n\t"
+            "v_cvt_f32_ubyte3 %1, %6\n\t"
+            "v_fmac_f32 %2, %1, %19\n\t"
+            "v_fmac_f32 %3, %1, %20\n\t"
+            "v_fmac_f32 %4, %1, %21\n\t"
+            "v_fmac_f32 %5, %1, %22"
+            : "=&v"(t0), "=&v"(t1), "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3])
+            : "v"(hi), "v"(xh[0][0]), "v"(xh[0][1]), "v"(xh[0][2]), "v"(xh[0][3]), "v"(xh[1][0]), "v"(xh[1][1]), "v"(xh[1][2]), "v"(xh[1][3]), "v"(xh[2][0]), "v"(xh[2][1]), "v"(xh[2][2]), "v"(xh[2][3]), "v"(xh[3][0]), "v"(xh[3][1]), "v"(xh[3][2]), "v"(xh[3][3]));
+    }
 }
 
 // 32 bytes at a 2-byte aligned address as 9 aligned words; the 9th is read
@@ -406,7 +518,265 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvParams p) {
         }
 }
 
+// ------------------------------------------------------- 64-column lanes
+// Kernel for 16-byte aligned Q4_K rows. A step is 4096 columns (16 blocks);
+// lane l owns the step's columns [64l, 64l+64): sub-block pair j = l%4 of
+// block l/4, whose 32 quant bytes are two aligned 16-byte chunks (low
+// nibbles: sub-block 2j, high: 2j+1) next to the block's 16-byte header
+// (d, dmin, scales). Every load is a 16-byte load, a wave's loads of a row
+// step cover 2304 contiguous bytes, and the scale decoding is paid once per
+// 64 weights. A workgroup of kGemvWaves waves owns kGemvWaves*R rows (R per
+// wave) and stages each step's x in LDS in lane order (float4 q of lane l at
+// [q][l], so a wave's reads are consecutive) with its 32-column sums.
+constexpr int kLaneCols = 64;
+constexpr int kStepCols = 64 * kLaneCols;
+
+template <int T>
+struct XStep {
+    float4 v[T][16][64];  // v[t][q][l] = x[t][64l + 4q .. 64l + 4q + 4)
+    float s[T][128];      // s[t][2l + h] = sum of x[t][64l + 32h .. 64l + 32h + 32)
+};
+
+// Thread tid stages columns [16 tid, 16 tid + 16) of the step for each token.
+template <int T>
+struct XStepRegs {
+    float4 v[T][4];
+};
+
+template <int T>
+__device__ __forceinline__ void xstep_load(const GemvParams& p, int st, int tid,
+                                           XStepRegs<T>& xr) {
+    const int c0 = min(st * kStepCols + 16 * tid, p.n_cols - 16);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int tt = t < p.n_tok ? t : 0;
+        const float* src = p.x + tt * p.x_stride + c0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) xr.v[t][m] = *reinterpret_cast<const float4*>(src + 4 * m);
+    }
+}
+
+// Columns past n_cols (the last step of a row that is not a whole step) hold
+// x of the row's last columns: finite and never used, those lanes are not
+// accumulated. The two halves of a sub-block sit in adjacent lanes, which add
+// their sums.
+template <int T>
+__device__ __forceinline__ void xstep_store(XStep<T>& X, const XStepRegs<T>& xr, int tid) {
+    const int sb = tid >> 1, half = tid & 1;
+    const int l = sb >> 1, q0 = 8 * (sb & 1) + 4 * half;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float s4[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            X.v[t][q0 + m][l] = xr.v[t][m];
+            s4[m] = (xr.v[t][m].x + xr.v[t][m].y) + (xr.v[t][m].z + xr.v[t][m].w);
+        }
+        float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        const float other = __shfl_xor(sum, 1, 64);
+        sum = half ? other + sum : sum + other;  // same order in both lanes
+        if (half == 0) X.s[t][sb] = sum;
+    }
+}
+
+// One row's share of a step for a lane: header chunk and the two quant chunks.
+struct Q4KLane {
+    uint4 hd, q0, q1;
+    __device__ __forceinline__ void load(const uint8_t* rowp, uint32_t off_h, uint32_t off_q) {
+        hd = *reinterpret_cast<const uint4*>(rowp + off_h);
+        q0 = *reinterpret_cast<const uint4*>(rowp + off_q);
+        q1 = *reinterpret_cast<const uint4*>(rowp + off_q + 16);
+    }
+    __device__ __forceinline__ uint32_t word(int m) const {
+        const uint4& c = m < 4 ? q0 : q1;
+        const int k = m & 3;
+        return k == 0 ? c.x : (k == 1 ? c.y : (k == 2 ? c.z : c.w));
+    }
+};
+
+template <int R, int T>
+__device__ __forceinline__ void q4k_step(const Q4KLane (&u)[R], const XStep<T>& X, int l,
+                                         bool live, float (&acc)[R][T]) {
+    float al[R][T], ah[R][T];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) al[r][t] = ah[r][t] = 0.0f;
+    float4 xl[2][T], xh[2][T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        xl[0][t] = X.v[t][0][l];
+        xh[0][t] = X.v[t][8][l];
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        if (m + 1 < 8) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                xl[(m + 1) & 1][t] = X.v[t][m + 1][l];
+                xh[(m + 1) & 1][t] = X.v[t][9 + m][l];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w = u[r].word(m);
+            const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;  // hi bytes are 16*q
+            float x4[4][T], y4[4][T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                x4[0][t] = xl[m & 1][t].x; x4[1][t] = xl[m & 1][t].y;
+                x4[2][t] = xl[m & 1][t].z; x4[3][t] = xl[m & 1][t].w;
+                y4[0][t] = xh[m & 1][t].x; y4[1][t] = xh[m & 1][t].y;
+                y4[2][t] = xh[m & 1][t].z; y4[3][t] = xh[m & 1][t].w;
+            }
+            word_fma<T>(lo, hi, x4, y4, al[r], ah[r]);
+        }
+    }
+    // (sc, m) of sub-blocks 2j, 2j+1 (src/kernels.cpp:65-73) as whole-word
+    // byte operations: bytes 0..3 of SC/MN are sub-blocks 0..3 (j < 2) or
+    // 4..7 (j >= 2); the pair is bytes 2(j%2), 2(j%2)+1.
+    const int j = l & 3;
+    const bool upper = j >= 2;
+    const uint32_t mA = upper ? 0x0F0F0F0Fu : 0x3F3F3F3Fu;
+    const uint32_t mB = upper ? 0x30303030u : 0u;
+    const int shB = upper ? 4 : 0, sel = 16 * (j & 1);
+    float2 sx[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) sx[t] = *reinterpret_cast<const float2*>(&X.s[t][2 * l]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t dd = u[r].hd.x, s0 = u[r].hd.y, s1 = u[r].hd.z, s2 = u[r].hd.w;
+        const uint32_t sc = (((upper ? s2 : s0) & mA) | ((s0 >> 2) & mB)) >> sel;
+        const uint32_t mn = ((((upper ? s2 : s1) >> shB) & mA) | ((s1 >> 2) & mB)) >> sel;
+        const float d = f16f(dd), dm = f16f(dd >> 16);
+        const float f_lo = d * cvt_ub<0>(sc), f_hi = (d * 0.0625f) * cvt_ub<1>(sc);
+        const float g_lo = dm * cvt_ub<0>(mn), g_hi = dm * cvt_ub<1>(mn);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float a = acc[r][t];
+            a = __builtin_fmaf(f_lo, al[r][t], a);
+            a = __builtin_fmaf(f_hi, ah[r][t], a);
+            a = __builtin_fmaf(-g_lo, sx[t].x, a);
+            a = __builtin_fmaf(-g_hi, sx[t].y, a);
+            acc[r][t] = live ? a : acc[r][t];
+        }
+    }
+}
+
+// Offsets of lane l's chunks in step st (its block clamped into the row, so
+// every load is in bounds; lanes past the row's end are not accumulated).
+__device__ __forceinline__ void q4k_offsets(int st, int l, int n_blk, uint32_t& off_h,
+                                            uint32_t& off_q, bool& live) {
+    const int kb = st * 16 + (l >> 2);
+    live = kb < n_blk;
+    const uint32_t kc = (uint32_t)min(kb, n_blk - 1);
+    off_h = kc * 144u;
+    off_q = off_h + 16u + 32u * (uint32_t)(l & 3);
+}
+
+
+// Stage x: 16-column run u (token t, step st, run j of the step) is loaded by
+// thread u % threads; runs past n_cols are stored as zeros. The two halves of
+// a sub-block sit in adjacent lanes, which add their sums.
+template <int R>
+__device__ __forceinline__ void q4k_load(const uint8_t* const (&rowp)[R], int st, int l,
+                                         int n_blk, Q4KLane (&u)[R], bool& live) {
+    uint32_t oh, oq;
+    q4k_offsets(st, l, n_blk, oh, oq, live);
+#pragma unroll
+    for (int r = 0; r < R; ++r) u[r].load(rowp[r], oh, oq);
+}
+
+// Each step's x is loaded before its weight chunks: loads complete in order,
+// so the wait for x before the barrier does not also wait for the weights.
+// PIPE (rows of more than one step): the next step's x and chunks are loaded
+// before the current step is computed, for step min(st+1, last) so that every
+// load is unconditional.
+template <int R, int T, bool PIPE>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_q4k_kernel(GemvParams p) {
+    __shared__ __align__(16) XStep<T> xs[PIPE ? 2 : 1];
+
+    const int tid = threadIdx.x;
+    const int l = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R;
+    const int n_blk = p.n_cols / 256;
+    const int n_st = (n_blk + 15) / 16;
+
+    const uint8_t* rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rowp[r] = p.w + min(r0 + r, p.n_rows - 1) * p.rb;
+
+    float acc[R][T];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[r][t] = 0.0f;
+
+    XStepRegs<T> xr;
+    Q4KLane ua[R];
+    bool live_a;
+    xstep_load<T>(p, 0, tid, xr);
+    q4k_load<R>(rowp, 0, l, n_blk, ua, live_a);
+    xstep_store<T>(xs[0], xr, tid);
+    __syncthreads();
+
+    if constexpr (!PIPE) {
+        q4k_step<R, T>(ua, xs[0], l, live_a, acc);  // rows of one step
+    } else {
+        Q4KLane ub[R];
+        bool live_b;
+        for (int st = 0; st < n_st; st += 2) {
+            const int s1 = min(st + 1, n_st - 1);
+            xstep_load<T>(p, s1, tid, xr);
+            q4k_load<R>(rowp, s1, l, n_blk, ub, live_b);
+            live_b = live_b && st + 1 < n_st;
+            __builtin_amdgcn_sched_barrier(0);
+            q4k_step<R, T>(ua, xs[0], l, live_a, acc);
+            xstep_store<T>(xs[1], xr, tid);
+            __syncthreads();
+            if (st + 1 >= n_st) break;
+            const int s2 = min(st + 2, n_st - 1);
+            xstep_load<T>(p, s2, tid, xr);
+            q4k_load<R>(rowp, s2, l, n_blk, ua, live_a);
+            live_a = live_a && st + 2 < n_st;
+            __builtin_amdgcn_sched_barrier(0);
+            q4k_step<R, T>(ub, xs[1], l, live_b, acc);
+            xstep_store<T>(xs[0], xr, tid);
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = group_sum<64>(acc[r][t]);
+            if (l == 0 && r0 + r < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + r0 + r] = v;
+        }
+}
+
 using GemvKernel = void (*)(GemvParams);
+
+template <int R, bool PIPE>
+GemvKernel pick_q4k_t(int T) {
+    switch (T) {
+    case 1: return gemv_q4k_kernel<R, 1, PIPE>;
+    case 2: return gemv_q4k_kernel<R, 2, PIPE>;
+    case 4: return gemv_q4k_kernel<R, 4, PIPE>;
+    default: return nullptr;
+    }
+}
+
+template <bool PIPE>
+GemvKernel pick_q4k(int R, int T) {
+    switch (R) {
+    case 1: return pick_q4k_t<1, PIPE>(T);
+    case 2: return pick_q4k_t<2, PIPE>(T);
+    case 4: return pick_q4k_t<4, PIPE>(T);
+    default: return nullptr;
+    }
+}
 
 template <int TYPE, int R>
 GemvKernel pick_t(int T) {
@@ -472,6 +842,34 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         return false;
     }
     if (n_rows == 0 || n_tok == 0) return true;
+    if (dtype == AERO_DTYPE_Q4_K && aligned16(w) && tune("gemv_lanes64", 1)) {
+        const bool pipe = n_cols > kStepCols;
+        for (int64_t t0 = 0; t0 < n_tok; t0 += 4) {
+            const int nt = (int)std::min<int64_t>(4, n_tok - t0);
+            const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
+            // rows per wave (measured on MI355X): 2 while that leaves >= 256
+            // workgroups, else 1; four tokens share the weight decoding over
+            // 4 rows when that leaves >= 512 workgroups (>= 256 for rows of
+            // several steps)
+            auto wgs_of = [&](int r) { return (n_rows + r * kGemvWaves - 1) / (r * kGemvWaves); };
+            int R = wgs_of(2) >= 256 ? 2 : 1;
+            if (T == 4 && (wgs_of(4) >= 512 || (pipe && wgs_of(4) >= 256))) R = 4;
+            R = tune("gemv_r", R);
+            const int64_t wgs =
+                (n_rows + (int64_t)R * kGemvWaves - 1) / ((int64_t)R * kGemvWaves);
+            GemvKernel k = pipe ? pick_q4k<true>(R, T) : pick_q4k<false>(R, T);
+            if (k == nullptr || wgs > 0x7fffffff) {
+                set_error("matvec: no Q4_K kernel for rows/wave %d", R);
+                return false;
+            }
+            GemvParams p{w, x + t0 * n_cols, y + t0 * n_rows, n_rows, (int)n_cols, rb, nt,
+                         n_cols, n_rows};
+            if (!launch("gemv_q4k_kernel", k, dim3((unsigned)wgs), dim3(64 * kGemvWaves), 0, s,
+                        p))
+                return false;
+        }
+        return true;
+    }
     // rows per wave: up to 4 (2 for the 2-byte aligned Q8_0 / Q6_K blocks, whose
     // words take two loads each) while the grid keeps >= 512 workgroups
     int R = (dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q6_K) ? 2 : 4;
