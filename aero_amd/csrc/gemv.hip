@@ -3,20 +3,16 @@
 // reference's matvec / matmul (src/kernels.cpp:497-538) with its block dots
 // (:78-250), which it calls between the elementwise ops of a layer.
 //
-// One wave (a 64-thread workgroup) owns R consecutive output rows. It walks
-// the columns in chunks of U 256-value steps (U*T = 8): the chunk's quant
-// blocks of each of its rows (contiguous in W) are loaded with coalesced
-// 32-bit loads and staged in LDS, and the lane's x float4 of every step of the
-// chunk is loaded into registers; the next chunk's loads are issued before the
-// current chunk is computed, so one chunk is always in flight. In each step
-// lane l takes values 4l..4l+3 (the gather's lane layout, quant_blocks.hpp)
-// and for each row expands its four weights into (q[4], f, g) and accumulates
-// f*sum(q*x) - g*sum(x) — the factoring of the reference's block dots, so
-// sum(x) is shared by all R rows and a row costs four multiply-adds per lane
-// per step. At the end each (row, token) sum is an xor-butterfly over the wave.
+// Two kernels, both workgroups of kGemvWaves waves that share x through LDS:
+//   gemv64_kernel (rows of a multiple of 16 bytes, W 16-byte aligned: every
+//     common shape): lane l of a 4096-column step owns columns 64l..64l+63
+//     and loads only its bytes of each row with 16-byte loads;
+//   gemv_kernel (any row length, W 4-byte aligned): lane l of a 2048-column
+//     step owns a 32-value group, loaded as 4-byte words.
+// Each wave owns R rows; the row sums are xor-butterflies over the wave.
 //
 // HBM bytes per launch: the weight blocks once (n_rows * n_cols/bv * bb) plus
-// x and y; x is re-read from L2 by every wave. Results differ from the
+// x and y; x is re-read from L2 by every workgroup. Results differ from the
 // reference's serial sums only in summation order.
 #include "quant_blocks.hpp"
 
@@ -519,15 +515,27 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvParams p) {
 }
 
 // ------------------------------------------------------- 64-column lanes
-// Kernel for 16-byte aligned Q4_K rows. A step is 4096 columns (16 blocks);
-// lane l owns the step's columns [64l, 64l+64): sub-block pair j = l%4 of
-// block l/4, whose 32 quant bytes are two aligned 16-byte chunks (low
-// nibbles: sub-block 2j, high: 2j+1) next to the block's 16-byte header
-// (d, dmin, scales). Every load is a 16-byte load, a wave's loads of a row
-// step cover 2304 contiguous bytes, and the scale decoding is paid once per
-// 64 weights. A workgroup of kGemvWaves waves owns kGemvWaves*R rows (R per
-// wave) and stages each step's x in LDS in lane order (float4 q of lane l at
-// [q][l], so a wave's reads are consecutive) with its 32-column sums.
+// Kernels for rows whose byte length is a multiple of 16 (16-byte aligned
+// W). A step is 4096 columns (16 blocks of 256, 128 of 32); lane l owns the
+// step's columns [64l, 64l+64) and loads only its own bytes of each row, in
+// 16-byte (8-byte for IQ4_XS) loads:
+//   Q4_K / Q5_K: sub-block pair j = l%4 of block l/4: the pair's 32 quant
+//       bytes (low nibbles sub-block 2j, high 2j+1), the 16-byte header and
+//       (Q5_K) the 32 high-bit bytes;
+//   IQ4_XS: the 32 bytes of sub-blocks 2j, 2j+1 of block l/4 and its header;
+//   Q8_0: blocks 2l, 2l+1 (68 bytes at a 4-byte aligned offset, taken from
+//       the 80 aligned bytes around them);
+//   Q6_K: ql bytes [64h+32a, +32) and qh bytes [32h, +32) of block l/4
+//       (h = j/2, a = j%2: quarters a and a+2 of half h, whose columns start
+//       in lanes l-a and l-a+1), from the 48 aligned bytes around each.
+// Quant values become unsigned bytes (signed types offset by 128 or 32,
+// corrected through sums of x), so each converts to a float with one
+// instruction; a row's share of a block dot is
+//     sum_g scale_g * (sum(u * x)_g - offset * sum(x)_g)
+// the factoring of the reference's block dots (src/kernels.cpp:78-250).
+// A workgroup of kGemvWaves waves owns kGemvWaves*R rows (R per wave) and
+// stages each step's x in LDS in lane order (float4 q of lane l at [q][l], so
+// a wave's reads are consecutive) with its 32- and 16-column sums.
 constexpr int kLaneCols = 64;
 constexpr int kStepCols = 64 * kLaneCols;
 
@@ -535,6 +543,7 @@ template <int T>
 struct XStep {
     float4 v[T][16][64];  // v[t][q][l] = x[t][64l + 4q .. 64l + 4q + 4)
     float s[T][128];      // s[t][2l + h] = sum of x[t][64l + 32h .. 64l + 32h + 32)
+    float s16[T][256];    // s16[t][i] = sum of x[t][16i .. 16i + 16)
 };
 
 // Thread tid stages columns [16 tid, 16 tid + 16) of the step for each token.
@@ -558,8 +567,8 @@ __device__ __forceinline__ void xstep_load(const GemvParams& p, int st, int tid,
 
 // Columns past n_cols (the last step of a row that is not a whole step) hold
 // x of the row's last columns: finite and never used, those lanes are not
-// accumulated. The two halves of a sub-block sit in adjacent lanes, which add
-// their sums.
+// accumulated. The two halves of a 32-column run sit in adjacent lanes, which
+// add their sums.
 template <int T>
 __device__ __forceinline__ void xstep_store(XStep<T>& X, const XStepRegs<T>& xr, int tid) {
     const int sb = tid >> 1, half = tid & 1;
@@ -573,135 +582,432 @@ __device__ __forceinline__ void xstep_store(XStep<T>& X, const XStepRegs<T>& xr,
             s4[m] = (xr.v[t][m].x + xr.v[t][m].y) + (xr.v[t][m].z + xr.v[t][m].w);
         }
         float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        X.s16[t][tid] = sum;
         const float other = __shfl_xor(sum, 1, 64);
         sum = half ? other + sum : sum + other;  // same order in both lanes
         if (half == 0) X.s[t][sb] = sum;
     }
 }
 
-// One row's share of a step for a lane: header chunk and the two quant chunks.
-struct Q4KLane {
-    uint4 hd, q0, q1;
-    __device__ __forceinline__ void load(const uint8_t* rowp, uint32_t off_h, uint32_t off_q) {
-        hd = *reinterpret_cast<const uint4*>(rowp + off_h);
-        q0 = *reinterpret_cast<const uint4*>(rowp + off_q);
-        q1 = *reinterpret_cast<const uint4*>(rowp + off_q + 16);
-    }
-    __device__ __forceinline__ uint32_t word(int m) const {
-        const uint4& c = m < 4 ? q0 : q1;
-        const int k = m & 3;
-        return k == 0 ? c.x : (k == 1 ? c.y : (k == 2 ? c.z : c.w));
-    }
-};
+__device__ __forceinline__ uint4 ld128(const uint8_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ uint2 ld64(const uint8_t* p) {
+    return *reinterpret_cast<const uint2*>(p);
+}
+template <int N>
+__device__ __forceinline__ uint32_t wd(const uint4 (&c)[N], int k) {
+    const uint4& v = c[k >> 2];
+    return (k & 3) == 0 ? v.x : ((k & 3) == 1 ? v.y : ((k & 3) == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ uint32_t rotr(uint32_t v, uint32_t s) {
+    return __builtin_amdgcn_alignbit(v, v, s);
+}
 
-template <int R, int T>
-__device__ __forceinline__ void q4k_step(const Q4KLane (&u)[R], const XStep<T>& X, int l,
-                                         bool live, float (&acc)[R][T]) {
-    float al[R][T], ah[R][T];
+// Words of the 16-byte chunks c starting at byte `ph` (even, 0..14, the same
+// for all outputs), out[i] = bytes ph+4i .. ph+4i+3: shifts by 8 and by 4
+// bytes (byte permutes of two words) and by ph & 3 (a byte align). Permutes
+// rather than selects: the compiler turns a select between two array
+// elements into a load from a selected address, which sends the array to
+// scratch memory.
+template <int N, int C>
+__device__ __forceinline__ void shifted_words(const uint4 (&c)[C], uint32_t ph,
+                                              uint32_t (&out)[N]) {
+    // words ph/4 .. ph/4 + N (the last only with a byte shift) must lie in c;
+    // reads past c are clamped (and unused when ph & 3 == 0)
+    static_assert(4 * C >= N + 3, "window too small");
+    const uint32_t sel8 = (ph & 8u) ? 0x07060504u : 0x03020100u;
+    const uint32_t sel4 = (ph & 4u) ? 0x07060504u : 0x03020100u;
+    uint32_t a[N + 2], b[N + 1];
+#pragma unroll
+    for (int i = 0; i < N + 2; ++i)
+        a[i] = __builtin_amdgcn_perm(wd(c, min(i + 2, 4 * C - 1)), wd(c, i), sel8);
+#pragma unroll
+    for (int i = 0; i < N + 1; ++i) b[i] = __builtin_amdgcn_perm(a[i + 1], a[i], sel4);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(b[i + 1], b[i], ph & 3u);
+}
+
+// x operands of word m: float4 lanes/rows chosen by the lane type.
+template <int T>
+__device__ __forceinline__ void x_words(const XStep<T>& X, int q_lo, int lane_lo, int q_hi,
+                                        int lane_hi, float (&xl)[4][T], float (&xh)[4][T]) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const float4 a = X.v[t][q_lo][lane_lo], b = X.v[t][q_hi][lane_hi];
+        xl[0][t] = a.x; xl[1][t] = a.y; xl[2][t] = a.z; xl[3][t] = a.w;
+        xh[0][t] = b.x; xh[1][t] = b.y; xh[2][t] = b.z; xh[3][t] = b.w;
+    }
+}
+
+// The word loop shared by the lane types: for m = 0..7 and each row, the lo
+// and hi unsigned-byte words wf(r, m) are multiplied with the x float4 rows
+// q_lo(m) (lane lane_lo) and q_hi(m) (lane lane_hi) and added to accumulator
+// group g(m). The next word's x is read before the current one is used.
+template <int R, int T, int G, typename WF, typename QF, typename GF>
+__device__ __forceinline__ void word_loop(const XStep<T>& X, int lane_lo, int lane_hi, WF wf,
+                                          QF qf, GF gf, float (&al)[R][G][T],
+                                          float (&ah)[R][G][T]) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int t = 0; t < T; ++t) al[r][t] = ah[r][t] = 0.0f;
-    float4 xl[2][T], xh[2][T];
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        xl[0][t] = X.v[t][0][l];
-        xh[0][t] = X.v[t][8][l];
+            for (int t = 0; t < T; ++t) al[r][g][t] = ah[r][g][t] = 0.0f;
+    float xl[2][4][T], xh[2][4][T];
+    {
+        int ql, qh;
+        qf(0, ql, qh);
+        x_words<T>(X, ql, lane_lo, qh, lane_hi, xl[0], xh[0]);
     }
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         if (m + 1 < 8) {
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                xl[(m + 1) & 1][t] = X.v[t][m + 1][l];
-                xh[(m + 1) & 1][t] = X.v[t][9 + m][l];
-            }
+            int ql, qh;
+            qf(m + 1, ql, qh);
+            x_words<T>(X, ql, lane_lo, qh, lane_hi, xl[(m + 1) & 1], xh[(m + 1) & 1]);
         }
+        const int g = gf(m);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t w = u[r].word(m);
-            const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;  // hi bytes are 16*q
-            float x4[4][T], y4[4][T];
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                x4[0][t] = xl[m & 1][t].x; x4[1][t] = xl[m & 1][t].y;
-                x4[2][t] = xl[m & 1][t].z; x4[3][t] = xl[m & 1][t].w;
-                y4[0][t] = xh[m & 1][t].x; y4[1][t] = xh[m & 1][t].y;
-                y4[2][t] = xh[m & 1][t].z; y4[3][t] = xh[m & 1][t].w;
-            }
-            word_fma<T>(lo, hi, x4, y4, al[r], ah[r]);
+            uint32_t lo, hi;
+            wf(r, m, lo, hi);
+            word_fma<T>(lo, hi, xl[m & 1], xh[m & 1], al[r][g], ah[r][g]);
         }
     }
-    // (sc, m) of sub-blocks 2j, 2j+1 (src/kernels.cpp:65-73) as whole-word
-    // byte operations: bytes 0..3 of SC/MN are sub-blocks 0..3 (j < 2) or
-    // 4..7 (j >= 2); the pair is bytes 2(j%2), 2(j%2)+1.
-    const int j = l & 3;
+}
+
+// Scale and minimum of K-quant sub-blocks 2j and 2j+1 (src/kernels.cpp:65-73)
+// as whole-word byte operations: bytes 0..3 of sc/mn hold sub-blocks 0..3
+// (j < 2) or 4..7 (j >= 2); the pair is bytes 2(j%2), 2(j%2)+1.
+__device__ __forceinline__ void kq_pair_scales(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                               float& sc_lo, float& sc_hi, float& mn_lo,
+                                               float& mn_hi) {
     const bool upper = j >= 2;
     const uint32_t mA = upper ? 0x0F0F0F0Fu : 0x3F3F3F3Fu;
     const uint32_t mB = upper ? 0x30303030u : 0u;
     const int shB = upper ? 4 : 0, sel = 16 * (j & 1);
-    float2 sx[T];
+    const uint32_t sc = (((upper ? s2 : s0) & mA) | ((s0 >> 2) & mB)) >> sel;
+    const uint32_t mn = ((((upper ? s2 : s1) >> shB) & mA) | ((s1 >> 2) & mB)) >> sel;
+    sc_lo = cvt_ub<0>(sc);
+    sc_hi = cvt_ub<1>(sc);
+    mn_lo = cvt_ub<0>(mn);
+    mn_hi = cvt_ub<1>(mn);
+}
+
+// Lambdas passed to word_loop are inlined so that their row / word
+// indices stay compile-time constants (else arrays they index go to scratch).
+#define AERO_INLINE __attribute__((always_inline))
+
+template <int TYPE> struct Lane64;
+
+// Q4_K (src/kernels.cpp:123-156). Low nibbles are masked in place; high
+// nibbles are kept as 16*q (exact), their scale carries the 1/16.
+template <> struct Lane64<AERO_DTYPE_Q4_K> {
+    uint4 hd, q[2];
+    __device__ __forceinline__ void load(const uint8_t* rowp, int st, int l, int n_blk) {
+        const uint32_t kc = (uint32_t)min(st * 16 + (l >> 2), n_blk - 1);
+        const uint32_t oh = kc * 144u, oq = oh + 16u + 32u * (uint32_t)(l & 3);
+        hd = ld128(rowp + oh);
+        q[0] = ld128(rowp + oq);
+        q[1] = ld128(rowp + oq + 16);
+    }
+    template <int R, int T>
+    static __device__ __forceinline__ void step(const Lane64 (&u)[R], const XStep<T>& X, int l,
+                                                bool live, float (&acc)[R][T]) {
+        float al[R][1][T], ah[R][1][T];
+        word_loop<R, T, 1>(
+            X, l, l,
+            [&](int r, int m, uint32_t& lo, uint32_t& hi) AERO_INLINE {
+                const uint32_t w = wd(u[r].q, m);
+                lo = w & 0x0F0F0F0Fu;
+                hi = w & 0xF0F0F0F0u;
+            },
+            [](int m, int& ql, int& qh) AERO_INLINE { ql = m; qh = 8 + m; }, [](int) AERO_INLINE { return 0; }, al, ah);
+        float2 sx[T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) sx[t] = *reinterpret_cast<const float2*>(&X.s[t][2 * l]);
+        for (int t = 0; t < T; ++t) sx[t] = *reinterpret_cast<const float2*>(&X.s[t][2 * l]);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t dd = u[r].hd.x, s0 = u[r].hd.y, s1 = u[r].hd.z, s2 = u[r].hd.w;
-        const uint32_t sc = (((upper ? s2 : s0) & mA) | ((s0 >> 2) & mB)) >> sel;
-        const uint32_t mn = ((((upper ? s2 : s1) >> shB) & mA) | ((s1 >> 2) & mB)) >> sel;
-        const float d = f16f(dd), dm = f16f(dd >> 16);
-        const float f_lo = d * cvt_ub<0>(sc), f_hi = (d * 0.0625f) * cvt_ub<1>(sc);
-        const float g_lo = dm * cvt_ub<0>(mn), g_hi = dm * cvt_ub<1>(mn);
+        for (int r = 0; r < R; ++r) {
+            float sc_lo, sc_hi, mn_lo, mn_hi;
+            kq_pair_scales(u[r].hd.y, u[r].hd.z, u[r].hd.w, l & 3, sc_lo, sc_hi, mn_lo, mn_hi);
+            const float d = f16f(u[r].hd.x), dm = f16f(u[r].hd.x >> 16);
+            const float f_lo = d * sc_lo, f_hi = (d * 0.0625f) * sc_hi;
+            const float g_lo = dm * mn_lo, g_hi = dm * mn_hi;
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            float a = acc[r][t];
-            a = __builtin_fmaf(f_lo, al[r][t], a);
-            a = __builtin_fmaf(f_hi, ah[r][t], a);
-            a = __builtin_fmaf(-g_lo, sx[t].x, a);
-            a = __builtin_fmaf(-g_hi, sx[t].y, a);
-            acc[r][t] = live ? a : acc[r][t];
+            for (int t = 0; t < T; ++t) {
+                float a = acc[r][t];
+                a = __builtin_fmaf(f_lo, al[r][0][t], a);
+                a = __builtin_fmaf(f_hi, ah[r][0][t], a);
+                a = __builtin_fmaf(-g_lo, sx[t].x, a);
+                a = __builtin_fmaf(-g_hi, sx[t].y, a);
+                acc[r][t] = live ? a : acc[r][t];
+            }
         }
     }
-}
+};
 
-// Offsets of lane l's chunks in step st (its block clamped into the row, so
-// every load is in bounds; lanes past the row's end are not accumulated).
-__device__ __forceinline__ void q4k_offsets(int st, int l, int n_blk, uint32_t& off_h,
-                                            uint32_t& off_q, bool& live) {
-    const int kb = st * 16 + (l >> 2);
-    live = kb < n_blk;
-    const uint32_t kc = (uint32_t)min(kb, n_blk - 1);
-    off_h = kc * 144u;
-    off_q = off_h + 16u + 32u * (uint32_t)(l & 3);
-}
-
-
-// Stage x: 16-column run u (token t, step st, run j of the step) is loaded by
-// thread u % threads; runs past n_cols are stored as zeros. The two halves of
-// a sub-block sit in adjacent lanes, which add their sums.
-template <int R>
-__device__ __forceinline__ void q4k_load(const uint8_t* const (&rowp)[R], int st, int l,
-                                         int n_blk, Q4KLane (&u)[R], bool& live) {
-    uint32_t oh, oq;
-    q4k_offsets(st, l, n_blk, oh, oq, live);
+// Q5_K (src/kernels.cpp:90-121): Q4_K plus bit k of qh[i] as bit 4 of value
+// i of sub-block k, moved there with a rotate of the qh word.
+template <> struct Lane64<AERO_DTYPE_Q5_K> {
+    uint4 hd, h[2], q[2];
+    __device__ __forceinline__ void load(const uint8_t* rowp, int st, int l, int n_blk) {
+        const uint32_t kc = (uint32_t)min(st * 16 + (l >> 2), n_blk - 1);
+        const uint32_t oh = kc * 176u, oq = oh + 48u + 32u * (uint32_t)(l & 3);
+        hd = ld128(rowp + oh);
+        h[0] = ld128(rowp + oh + 16);
+        h[1] = ld128(rowp + oh + 32);
+        q[0] = ld128(rowp + oq);
+        q[1] = ld128(rowp + oq + 16);
+    }
+    template <int R, int T>
+    static __device__ __forceinline__ void step(const Lane64 (&u)[R], const XStep<T>& X, int l,
+                                                bool live, float (&acc)[R][T]) {
+        const int j = l & 3;
+        const uint32_t s_lo = (uint32_t)(2 * j - 4) & 31u, s_hi = (uint32_t)(2 * j - 3) & 31u;
+        float al[R][1][T], ah[R][1][T];
+        word_loop<R, T, 1>(
+            X, l, l,
+            [&](int r, int m, uint32_t& lo, uint32_t& hi) AERO_INLINE {
+                const uint32_t w = wd(u[r].q, m), hb = wd(u[r].h, m);
+                lo = (w & 0x0F0F0F0Fu) | (rotr(hb, s_lo) & 0x10101010u);
+                hi = ((w >> 4) & 0x0F0F0F0Fu) | (rotr(hb, s_hi) & 0x10101010u);
+            },
+            [](int m, int& ql, int& qh) AERO_INLINE { ql = m; qh = 8 + m; }, [](int) AERO_INLINE { return 0; }, al, ah);
+        float2 sx[T];
 #pragma unroll
-    for (int r = 0; r < R; ++r) u[r].load(rowp[r], oh, oq);
-}
+        for (int t = 0; t < T; ++t) sx[t] = *reinterpret_cast<const float2*>(&X.s[t][2 * l]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sc_lo, sc_hi, mn_lo, mn_hi;
+            kq_pair_scales(u[r].hd.y, u[r].hd.z, u[r].hd.w, j, sc_lo, sc_hi, mn_lo, mn_hi);
+            const float d = f16f(u[r].hd.x), dm = f16f(u[r].hd.x >> 16);
+            const float f_lo = d * sc_lo, f_hi = d * sc_hi;
+            const float g_lo = dm * mn_lo, g_hi = dm * mn_hi;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float a = acc[r][t];
+                a = __builtin_fmaf(f_lo, al[r][0][t], a);
+                a = __builtin_fmaf(f_hi, ah[r][0][t], a);
+                a = __builtin_fmaf(-g_lo, sx[t].x, a);
+                a = __builtin_fmaf(-g_hi, sx[t].y, a);
+                acc[r][t] = live ? a : acc[r][t];
+            }
+        }
+    }
+};
 
-// Each step's x is loaded before its weight chunks: loads complete in order,
-// so the wait for x before the barrier does not also wait for the weights.
-// PIPE (rows of more than one step): the next step's x and chunks are loaded
-// before the current step is computed, for step min(st+1, last) so that every
-// load is unconditional.
-template <int R, int T, bool PIPE>
-__global__ __launch_bounds__(64 * kGemvWaves) void gemv_q4k_kernel(GemvParams p) {
+// IQ4_XS (src/kernels.cpp:217-238): sub-block k uses q[16k .. 16k+16):
+// values 0..15 from low nibbles, 16..31 from high; u = codebook + 128 by
+// byte permutes of the packed codebook.
+template <> struct Lane64<AERO_DTYPE_IQ4_XS> {
+    uint2 hd, q[4];
+    __device__ __forceinline__ void load(const uint8_t* rowp, int st, int l, int n_blk) {
+        const uint32_t kc = (uint32_t)min(st * 16 + (l >> 2), n_blk - 1);
+        const uint32_t oh = kc * 136u, oq = oh + 8u + 32u * (uint32_t)(l & 3);
+        hd = ld64(rowp + oh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ld64(rowp + oq + 8 * i);
+    }
+    __device__ __forceinline__ uint32_t word(int m) const {
+        return (m & 1) ? q[m >> 1].y : q[m >> 1].x;
+    }
+    template <int R, int T>
+    static __device__ __forceinline__ void step(const Lane64 (&u)[R], const XStep<T>& X, int l,
+                                                bool live, float (&acc)[R][T]) {
+        // words 0..3: sub-block 2j (columns 0..31 of the lane), 4..7: 2j+1
+        float al[R][2][T], ah[R][2][T];
+        word_loop<R, T, 2>(
+            X, l, l,
+            [&](int r, int m, uint32_t& lo, uint32_t& hi) AERO_INLINE {
+                const uint32_t w = u[r].word(m);
+                lo = iq4_bytes(w & 0x0F0F0F0Fu);
+                hi = iq4_bytes((w >> 4) & 0x0F0F0F0Fu);
+            },
+            [](int m, int& ql, int& qh) AERO_INLINE {
+                ql = (m & 3) + 8 * (m >> 2);
+                qh = ql + 4;
+            },
+            [](int m) AERO_INLINE { return m >> 2; }, al, ah);
+        const int j = l & 3;
+        float2 sx[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) sx[t] = *reinterpret_cast<const float2*>(&X.s[t][2 * l]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t shw = u[r].hd.x >> 16, slw = u[r].hd.y;
+            const uint32_t ls0 = ((slw >> (8 * j)) & 15u) | (((shw >> (4 * j)) & 3u) << 4);
+            const uint32_t ls1 = ((slw >> (8 * j + 4)) & 15u) | (((shw >> (4 * j + 2)) & 3u) << 4);
+            const float d = f16f(u[r].hd.x);
+            const float f0 = d * (float)((int)ls0 - 32), f1 = d * (float)((int)ls1 - 32);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float a = acc[r][t];
+                a = __builtin_fmaf(f0, al[r][0][t] + ah[r][0][t], a);
+                a = __builtin_fmaf(f1, al[r][1][t] + ah[r][1][t], a);
+                a = __builtin_fmaf(-128.0f * f0, sx[t].x, a);
+                a = __builtin_fmaf(-128.0f * f1, sx[t].y, a);
+                acc[r][t] = live ? a : acc[r][t];
+            }
+        }
+    }
+};
+
+// Q8_0 (src/kernels.cpp:78-84): the lane's two blocks are 68 bytes at byte
+// 68l of the step (4-byte aligned), loaded as the five aligned chunks around
+// them; u = q ^ 0x80 = q + 128.
+template <> struct Lane64<AERO_DTYPE_Q8_0> {
+    uint4 c[5];
+    uint32_t ph;  // byte offset of the blocks within c
+    __device__ __forceinline__ void load(const uint8_t* rowp, int st, int l, int n_blk) {
+        // n_blk is a multiple of 8: clamp to the last even block pair
+        const uint32_t kc = (uint32_t)min(st * 128 + 2 * l, n_blk - 2);
+        const uint32_t ob = kc * 34u;
+        ph = ob & 15u;
+        const uint8_t* base = rowp + (ob - ph);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) c[i] = ld128(base + 16 * i);
+    }
+    template <int R, int T>
+    static __device__ __forceinline__ void step(const Lane64 (&u)[R], const XStep<T>& X, int l,
+                                                bool live, float (&acc)[R][T]) {
+        uint32_t qa[R][8], qb[R][8], da[R], db[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t w[17];
+            shifted_words<17, 5>(u[r].c, u[r].ph, w);
+            da[r] = w[0];
+            db[r] = w[8] >> 16;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                qa[r][m] = __builtin_amdgcn_alignbyte(w[m + 1], w[m], 2) ^ 0x80808080u;
+                qb[r][m] = w[9 + m] ^ 0x80808080u;
+            }
+        }
+        float al[R][1][T], ah[R][1][T];
+        word_loop<R, T, 1>(
+            X, l, l,
+            [&](int r, int m, uint32_t& lo, uint32_t& hi) AERO_INLINE {
+                lo = qa[r][m];
+                hi = qb[r][m];
+            },
+            [](int m, int& ql, int& qh) AERO_INLINE { ql = m; qh = 8 + m; }, [](int) AERO_INLINE { return 0; }, al, ah);
+        float2 sx[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) sx[t] = *reinterpret_cast<const float2*>(&X.s[t][2 * l]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float fa = f16f(da[r]), fb = f16f(db[r]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float a = acc[r][t];
+                a = __builtin_fmaf(fa, al[r][0][t], a);
+                a = __builtin_fmaf(fb, ah[r][0][t], a);
+                a = __builtin_fmaf(-128.0f * fa, sx[t].x, a);
+                a = __builtin_fmaf(-128.0f * fb, sx[t].y, a);
+                acc[r][t] = live ? a : acc[r][t];
+            }
+        }
+    }
+};
+
+// Q6_K (src/kernels.cpp:170-200): lane j = 2h + a of a block takes quarters
+// a and a+2 of half h: low / high nibbles of ql[64h + 32a + i] with qh[32h + i]
+// bits 2a and 4+2a as bits 4-5; scale sc[8h + 2*quarter + i/16]; u = q + 32.
+template <> struct Lane64<AERO_DTYPE_Q6_K> {
+    uint4 l3[3], h3[3];
+    uint32_t ph, sa, sb, d;
+    __device__ __forceinline__ void load(const uint8_t* rowp, int st, int l, int n_blk) {
+        const uint32_t kc = (uint32_t)min(st * 16 + (l >> 2), n_blk - 1);
+        const uint32_t j = (uint32_t)(l & 3), h = j >> 1, a = j & 1;
+        const uint32_t ob = kc * 210u;
+        ph = ob & 15u;
+        const uint8_t* bl = rowp + (ob - ph);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            l3[i] = ld128(bl + 64 * h + 32 * a + 16 * i);
+            h3[i] = ld128(bl + 128 + 32 * h + 16 * i);
+        }
+        const uint8_t* sc = rowp + ob + 192 + 8 * h + 2 * a;
+        sa = *reinterpret_cast<const uint16_t*>(sc);
+        sb = *reinterpret_cast<const uint16_t*>(sc + 4);
+        d = *reinterpret_cast<const uint16_t*>(rowp + ob + 208);
+    }
+    template <int R, int T>
+    static __device__ __forceinline__ void step(const Lane64 (&u)[R], const XStep<T>& X, int l,
+                                                bool live, float (&acc)[R][T]) {
+        const int a = l & 1;
+        const uint32_t sl = 4 - 2 * a, sr = 2 * a;
+        uint32_t lo[R][8], hi[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t wl[8], wh[8];
+            shifted_words<8, 3>(u[r].l3, u[r].ph, wl);
+            shifted_words<8, 3>(u[r].h3, u[r].ph, wh);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                lo[r][m] = (wl[m] & 0x0F0F0F0Fu) | ((wh[m] << sl) & 0x30303030u);
+                hi[r][m] = ((wl[m] >> 4) & 0x0F0F0F0Fu) | ((wh[m] >> sr) & 0x30303030u);
+            }
+        }
+        // quarter a: columns in lane l-a, quarter a+2: lane l-a+1; x rows
+        // 8a.. of those lanes; groups: values 0..15 / 16..31 of each quarter
+        float al[R][2][T], ah[R][2][T];
+        word_loop<R, T, 2>(
+            X, l - a, l - a + 1,
+            [&](int r, int m, uint32_t& lw, uint32_t& hw) AERO_INLINE {
+                lw = lo[r][m];
+                hw = hi[r][m];
+            },
+            [a](int m, int& ql, int& qh) AERO_INLINE { ql = qh = 8 * a + m; }, [](int m) AERO_INLINE { return m >> 2; },
+            al, ah);
+        float2 sq_a[T], sq_b[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            sq_a[t] = *reinterpret_cast<const float2*>(&X.s16[t][4 * l - 2 * a]);
+            sq_b[t] = *reinterpret_cast<const float2*>(&X.s16[t][4 * l - 2 * a + 4]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float df = f16f(u[r].d);
+            const float f0 = df * (float)(int8_t)(u[r].sa & 0xFFu);
+            const float f1 = df * (float)(int8_t)((u[r].sa >> 8) & 0xFFu);
+            const float f2 = df * (float)(int8_t)(u[r].sb & 0xFFu);
+            const float f3 = df * (float)(int8_t)((u[r].sb >> 8) & 0xFFu);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float v = acc[r][t];
+                v = __builtin_fmaf(f0, al[r][0][t], v);
+                v = __builtin_fmaf(f1, al[r][1][t], v);
+                v = __builtin_fmaf(f2, ah[r][0][t], v);
+                v = __builtin_fmaf(f3, ah[r][1][t], v);
+                v = __builtin_fmaf(-32.0f * f0, sq_a[t].x, v);
+                v = __builtin_fmaf(-32.0f * f1, sq_a[t].y, v);
+                v = __builtin_fmaf(-32.0f * f2, sq_b[t].x, v);
+                v = __builtin_fmaf(-32.0f * f3, sq_b[t].y, v);
+                acc[r][t] = live ? v : acc[r][t];
+            }
+        }
+    }
+};
+
+// Each step's x is loaded before its weights: loads complete in order, so
+// the wait for x before the barrier does not also wait for the weights.
+// PIPE (rows of more than one step): the next step's x and weights are
+// loaded before the current step is computed, for step min(st+1, last) so
+// that every load is unconditional.
+template <int TYPE, int R, int T, bool PIPE>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
+    using L = Lane64<TYPE>;
+    constexpr int BV = QT<TYPE>::BV;
     __shared__ __align__(16) XStep<T> xs[PIPE ? 2 : 1];
 
     const int tid = threadIdx.x;
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R;
-    const int n_blk = p.n_cols / 256;
-    const int n_st = (n_blk + 15) / 16;
+    const int n_blk = p.n_cols / BV;
+    const int n_st = (p.n_cols + kStepCols - 1) / kStepCols;
 
     const uint8_t* rowp[R];
 #pragma unroll
@@ -714,34 +1020,37 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_q4k_kernel(GemvParams p)
         for (int t = 0; t < T; ++t) acc[r][t] = 0.0f;
 
     XStepRegs<T> xr;
-    Q4KLane ua[R];
-    bool live_a;
+    L ua[R];
     xstep_load<T>(p, 0, tid, xr);
-    q4k_load<R>(rowp, 0, l, n_blk, ua, live_a);
+#pragma unroll
+    for (int r = 0; r < R; ++r) ua[r].load(rowp[r], 0, l, n_blk);
+    bool live_a = kLaneCols * l < p.n_cols;
     xstep_store<T>(xs[0], xr, tid);
     __syncthreads();
 
     if constexpr (!PIPE) {
-        q4k_step<R, T>(ua, xs[0], l, live_a, acc);  // rows of one step
+        L::template step<R, T>(ua, xs[0], l, live_a, acc);  // rows of one step
     } else {
-        Q4KLane ub[R];
+        L ub[R];
         bool live_b;
         for (int st = 0; st < n_st; st += 2) {
             const int s1 = min(st + 1, n_st - 1);
             xstep_load<T>(p, s1, tid, xr);
-            q4k_load<R>(rowp, s1, l, n_blk, ub, live_b);
-            live_b = live_b && st + 1 < n_st;
+#pragma unroll
+            for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, l, n_blk);
+            live_b = st + 1 < n_st && s1 * kStepCols + kLaneCols * l < p.n_cols;
             __builtin_amdgcn_sched_barrier(0);
-            q4k_step<R, T>(ua, xs[0], l, live_a, acc);
+            L::template step<R, T>(ua, xs[0], l, live_a, acc);
             xstep_store<T>(xs[1], xr, tid);
             __syncthreads();
             if (st + 1 >= n_st) break;
             const int s2 = min(st + 2, n_st - 1);
             xstep_load<T>(p, s2, tid, xr);
-            q4k_load<R>(rowp, s2, l, n_blk, ua, live_a);
-            live_a = live_a && st + 2 < n_st;
+#pragma unroll
+            for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, l, n_blk);
+            live_a = st + 2 < n_st && s2 * kStepCols + kLaneCols * l < p.n_cols;
             __builtin_amdgcn_sched_barrier(0);
-            q4k_step<R, T>(ub, xs[1], l, live_b, acc);
+            L::template step<R, T>(ub, xs[1], l, live_b, acc);
             xstep_store<T>(xs[0], xr, tid);
             __syncthreads();
         }
@@ -758,22 +1067,36 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_q4k_kernel(GemvParams p)
 
 using GemvKernel = void (*)(GemvParams);
 
-template <int R, bool PIPE>
-GemvKernel pick_q4k_t(int T) {
+template <int TYPE, int R, bool PIPE>
+GemvKernel pick64_t(int T) {
     switch (T) {
-    case 1: return gemv_q4k_kernel<R, 1, PIPE>;
-    case 2: return gemv_q4k_kernel<R, 2, PIPE>;
-    case 4: return gemv_q4k_kernel<R, 4, PIPE>;
+    case 1: return gemv64_kernel<TYPE, R, 1, PIPE>;
+    case 2: return gemv64_kernel<TYPE, R, 2, PIPE>;
+    case 4:
+        if constexpr (!PIPE) return gemv64_kernel<TYPE, R, 4, PIPE>;
+        return nullptr;
+    default: return nullptr;
+    }
+}
+
+template <int TYPE, bool PIPE>
+GemvKernel pick64_r(int R, int T) {
+    switch (R) {
+    case 1: return pick64_t<TYPE, 1, PIPE>(T);
+    case 2: return pick64_t<TYPE, 2, PIPE>(T);
+    case 4: return pick64_t<TYPE, 4, PIPE>(T);
     default: return nullptr;
     }
 }
 
 template <bool PIPE>
-GemvKernel pick_q4k(int R, int T) {
-    switch (R) {
-    case 1: return pick_q4k_t<1, PIPE>(T);
-    case 2: return pick_q4k_t<2, PIPE>(T);
-    case 4: return pick_q4k_t<4, PIPE>(T);
+GemvKernel pick64(int dtype, int R, int T) {
+    switch (dtype) {
+    case AERO_DTYPE_Q8_0: return pick64_r<AERO_DTYPE_Q8_0, PIPE>(R, T);
+    case AERO_DTYPE_Q4_K: return pick64_r<AERO_DTYPE_Q4_K, PIPE>(R, T);
+    case AERO_DTYPE_Q5_K: return pick64_r<AERO_DTYPE_Q5_K, PIPE>(R, T);
+    case AERO_DTYPE_Q6_K: return pick64_r<AERO_DTYPE_Q6_K, PIPE>(R, T);
+    case AERO_DTYPE_IQ4_XS: return pick64_r<AERO_DTYPE_IQ4_XS, PIPE>(R, T);
     default: return nullptr;
     }
 }
@@ -842,10 +1165,11 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         return false;
     }
     if (n_rows == 0 || n_tok == 0) return true;
-    if (dtype == AERO_DTYPE_Q4_K && aligned16(w) && tune("gemv_lanes64", 1)) {
+    if (aligned16(w) && rb % 16 == 0 && tune("gemv_lanes64", 1)) {
         const bool pipe = n_cols > kStepCols;
-        for (int64_t t0 = 0; t0 < n_tok; t0 += 4) {
-            const int nt = (int)std::min<int64_t>(4, n_tok - t0);
+        const int t_max = pipe ? 2 : 4;  // double-buffered x of 4 tokens would fill LDS
+        for (int64_t t0 = 0; t0 < n_tok; t0 += t_max) {
+            const int nt = (int)std::min<int64_t>(t_max, n_tok - t0);
             const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
             // rows per wave (measured on MI355X): 2 while that leaves >= 256
             // workgroups, else 1; four tokens share the weight decoding over
@@ -853,19 +1177,17 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
             // several steps)
             auto wgs_of = [&](int r) { return (n_rows + r * kGemvWaves - 1) / (r * kGemvWaves); };
             int R = wgs_of(2) >= 256 ? 2 : 1;
-            if (T == 4 && (wgs_of(4) >= 512 || (pipe && wgs_of(4) >= 256))) R = 4;
+            if (T == 4 && wgs_of(4) >= 512) R = 4;
             R = tune("gemv_r", R);
-            const int64_t wgs =
-                (n_rows + (int64_t)R * kGemvWaves - 1) / ((int64_t)R * kGemvWaves);
-            GemvKernel k = pipe ? pick_q4k<true>(R, T) : pick_q4k<false>(R, T);
+            const int64_t wgs = wgs_of(R);
+            GemvKernel k = pipe ? pick64<true>(dtype, R, T) : pick64<false>(dtype, R, T);
             if (k == nullptr || wgs > 0x7fffffff) {
-                set_error("matvec: no Q4_K kernel for rows/wave %d", R);
+                set_error("matvec: no kernel for dtype %d, rows/wave %d", dtype, R);
                 return false;
             }
             GemvParams p{w, x + t0 * n_cols, y + t0 * n_rows, n_rows, (int)n_cols, rb, nt,
                          n_cols, n_rows};
-            if (!launch("gemv_q4k_kernel", k, dim3((unsigned)wgs), dim3(64 * kGemvWaves), 0, s,
-                        p))
+            if (!launch("gemv64_kernel", k, dim3((unsigned)wgs), dim3(64 * kGemvWaves), 0, s, p))
                 return false;
         }
         return true;

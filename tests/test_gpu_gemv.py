@@ -41,6 +41,7 @@ def test_matvec_golden(hip, t):
 @pytest.mark.parametrize("n_rows,n_cols,n_tok", [
     (1, 256, 1), (37, 1024, 1), (4096, 4096, 1), (1000, 14336, 1),   # decode shapes
     (4103, 4096, 2), (513, 2048, 3), (130, 4096, 8), (67, 1024, 13),  # token groups
+    (300, 14336, 5), (64, 8192, 4),  # rows of several 4096-column steps, token groups
 ])
 def test_matvec_vs_oracle(hip, oracle, t, n_rows, n_cols, n_tok):
     rng = np.random.default_rng(n_rows * 31 + n_cols + n_tok + t)
