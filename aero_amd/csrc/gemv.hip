@@ -21,6 +21,8 @@
 namespace aero {
 
 int64_t dtype_block_bytes(int t);
+bool gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
+              int64_t n_cols, int64_t rb, int64_t n_tok, hipStream_t s);
 int64_t dtype_block_values(int t);
 
 namespace {
@@ -1165,6 +1167,9 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         return false;
     }
     if (n_rows == 0 || n_tok == 0) return true;
+    // many tokens: the matrix-core GEMM reads W once per 64 tokens
+    if (n_tok >= tune("gemm_min_tokens", 32) && n_tok <= (int64_t)1 << 30)
+        return gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, s);
     if (aligned16(w) && rb % 16 == 0 && tune("gemv_lanes64", 1)) {
         const bool pipe = n_cols > kStepCols;
         const int t_max = pipe ? 2 : 4;  // double-buffered x of 4 tokens would fill LDS

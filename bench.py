@@ -69,6 +69,8 @@ def parse_args(argv=None):
     p.add_argument("--variants", action="store_true",
                    help="every op variant at the Llama-3-8B 512-token geometry")
     p.add_argument("--gemv", action="store_true", help="quantised GEMV cases")
+    p.add_argument("--gemm", action="store_true",
+                   help="quantised GEMM cases (prefill token counts)")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
     p.add_argument("--copy-calibration", action="store_true")
     p.add_argument("--host-abi", action="store_true",
@@ -494,6 +496,8 @@ def main(argv=None):
         return variants(a)
     if a.gemv:
         return gemv(a)
+    if a.gemm:
+        return gemm(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -646,6 +650,52 @@ def gemv(a):
             stream.destroy()
         print(json.dumps(res), flush=True)
         del ws, w0
+    return 0
+
+
+GEMM_CASES = [
+    # (name, dtype, n_rows, n_cols, tokens): Llama-3-8B prefill projections
+    ("attn_q_4096x4096", 12, 4096, 4096, 512), ("ffn_gate_14336x4096", 12, 14336, 4096, 512),
+    ("ffn_down_4096x14336", 12, 4096, 14336, 512), ("q8_0_14336x4096", 8, 14336, 4096, 512),
+    ("q6_k_14336x4096", 14, 14336, 4096, 512), ("ffn_gate_14336x4096_t64", 12, 14336, 4096, 64),
+]
+MFMA_FP32_PEAK_TFLOPS = 157.3
+
+
+def gemm(a):
+    """Quantised GEMM (many tokens): time per launch (events around a few
+    back-to-back launches over rotating weight copies), TFLOP/s and the
+    fraction of the fp32 matrix peak it runs at."""
+    from aero_amd import ops, workloads as W
+    from aero_amd.device import DeviceArray as DA, Event, Stream
+
+    rng = np.random.default_rng(0)
+    names = a.shapes.split(",") if a.shapes else [c[0] for c in GEMM_CASES]
+    for name, t, n_rows, n_cols, n_tok in GEMM_CASES:
+        if name not in names:
+            continue
+        bv, bb = W.BLOCK[t]
+        ws = [DA.from_numpy(W.make_table(t, n_rows * n_cols // bv, rng)) for _ in range(4)]
+        X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
+        Y = DA.empty((n_tok, n_rows))
+        stream = Stream()
+        for w in ws:
+            ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok, stream=stream)
+        reps = 5
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(reps):
+            for w in ws:
+                ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok, stream=stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * len(ws))
+        tf = 2.0 * n_rows * n_cols * n_tok / (us * 1e-6) / 1e12
+        print(json.dumps({"case": name, "dtype": t, "n_rows": n_rows, "n_cols": n_cols,
+                          "tokens": n_tok, "us": round(us, 2), "TFLOP/s": round(tf, 1),
+                          "frac_fp32_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}), flush=True)
+        stream.destroy()
+        del ws
     return 0
 
 

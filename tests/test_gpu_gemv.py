@@ -68,6 +68,36 @@ def test_matvec_rows_off_word_boundary(hip, oracle, t):
     assert rel_to_scale(gpu_matvec(t, w, X, n_rows), oracle.matmul(t, w, X, n_rows)) <= RTOL
 
 
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_rows,n_cols,n_tok", [
+    (100, 1024, 40), (130, 2048, 33), (257, 4096, 100), (64, 14336, 64),
+])
+def test_matmul_many_tokens_vs_oracle(hip, oracle, t, n_rows, n_cols, n_tok):
+    """32 or more tokens take the matrix-core GEMM (64 x 64 tiles, partial
+    row and token tiles, rows of 1 to 56 blocks)."""
+    rng = np.random.default_rng(n_rows * 17 + n_cols + n_tok + t)
+    bv, bb = W.BLOCK[t]
+    w = W.make_table(t, n_rows * n_cols // bv, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    print(f"matmul type={t} rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
+    got = gpu_matvec(t, w, X, n_rows)
+    want = oracle.matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, want) <= RTOL
+
+
+def test_matmul_prefill_size_matches_gemv(hip):
+    """At Llama-3-8B FFN size with 512 tokens (14336 x 4096 Q4_K, the prefill
+    shape), every token's GEMM row equals that token's GEMV (one-token launch)
+    to the tolerance; sampled tokens cover every 64-token tile."""
+    rng = np.random.default_rng(91)
+    n_rows, n_cols, n_tok = 14336, 4096, 512
+    w = W.make_table(W.Q4_K, n_rows * n_cols // 256, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    Y = gpu_matvec(W.Q4_K, w, X, n_rows)
+    for i in (0, 63, 64, 200, 383, 511):
+        assert rel_to_scale(Y[i], gpu_matvec(W.Q4_K, w, X[i], n_rows)[0]) <= RTOL
+
+
 def test_matvec_linearity_at_full_size(hip):
     """At Llama-3-8B FFN-down size (4096 x 14336 Q4_K): W(a*x1 + x2) equals
     a*W(x1) + W(x2) to the tolerance, and a zero x gives exactly zero."""
