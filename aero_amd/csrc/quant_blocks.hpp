@@ -224,6 +224,42 @@ __device__ __forceinline__ float4 decode(const RawIQ4& r, int l) {
     return make_float4(qv[0], qv[1], qv[2], qv[3]);
 }
 
+// 16- and 8-byte loads, and word k of an array of 16-byte chunks.
+__device__ __forceinline__ uint4 ld128(const uint8_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ uint2 ld64(const uint8_t* p) {
+    return *reinterpret_cast<const uint2*>(p);
+}
+template <int N>
+__device__ __forceinline__ uint32_t wd(const uint4 (&c)[N], int k) {
+    const uint4& v = c[k >> 2];
+    return (k & 3) == 0 ? v.x : ((k & 3) == 1 ? v.y : ((k & 3) == 2 ? v.z : v.w));
+}
+// Words of the 16-byte chunks c starting at byte `ph` (even, 0..14, the same
+// for all outputs), out[i] = bytes ph+4i .. ph+4i+3: shifts by 8 and by 4
+// bytes (byte permutes of two words) and by ph & 3 (a byte align). Permutes
+// rather than selects: the compiler turns a select between two array
+// elements into a load from a selected address, which sends the array to
+// scratch memory.
+template <int N, int C>
+__device__ __forceinline__ void shifted_words(const uint4 (&c)[C], uint32_t ph,
+                                              uint32_t (&out)[N]) {
+    // words ph/4 .. ph/4 + N (the last only with a byte shift) must lie in c;
+    // reads past c are clamped (and unused when ph & 3 == 0)
+    static_assert(4 * C >= N + 3, "window too small");
+    const uint32_t sel8 = (ph & 8u) ? 0x07060504u : 0x03020100u;
+    const uint32_t sel4 = (ph & 4u) ? 0x07060504u : 0x03020100u;
+    uint32_t a[N + 2], b[N + 1];
+#pragma unroll
+    for (int i = 0; i < N + 2; ++i)
+        a[i] = __builtin_amdgcn_perm(wd(c, min(i + 2, 4 * C - 1)), wd(c, i), sel8);
+#pragma unroll
+    for (int i = 0; i < N + 1; ++i) b[i] = __builtin_amdgcn_perm(a[i + 1], a[i], sel4);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(b[i + 1], b[i], ph & 3u);
+}
+
 template <int TYPE> struct QT;
 template <> struct QT<AERO_DTYPE_Q8_0> { static constexpr int BV = 32, BB = 34; using Raw = RawQ8; };
 template <> struct QT<AERO_DTYPE_Q4_K> { static constexpr int BV = 256, BB = 144; using Raw = RawQ4; };
