@@ -607,6 +607,31 @@ GEMV_CASES = [
 ]
 
 
+def cpu_matmul_us(t, n_rows, n_cols, n_tok, seconds=1.0):
+    """The reference's own matmul (oracle/_ref, src/kernels.cpp:497-538) or
+    else the oracle's, one thread, on a sample of rows of the same shape:
+    returns (estimated us for all rows, kind, sample description)."""
+    import time
+    from aero_amd import workloads as W
+    from oracle import cpuref, refbind
+
+    use_ref = refbind.available()
+    mm = refbind.matmul if use_ref else cpuref.matmul
+    rng = np.random.default_rng(2)
+    bv, bb = W.BLOCK[t]
+    rows = max(1, min(n_rows, (1 << 26) // max(1, n_cols * n_tok)))
+    w = W.make_table(t, rows * n_cols // bv, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    mm(t, w, X, rows)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        mm(t, w, X, rows)
+        reps += 1
+    per_row = (time.perf_counter() - t0) / (reps * rows)
+    return (per_row * n_rows * 1e6, "reference" if use_ref else "port",
+            f"{rows} of {n_rows} rows x {n_tok} tokens, {reps} calls, one thread")
+
+
 def gemv(a):
     """Quantised GEMV: sustained time per launch (back to back over a > 1 GiB
     rotation of weight copies), weight GB/s and fraction of HBM peak, for 1, 4
@@ -648,6 +673,11 @@ def gemv(a):
                                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
             plan.destroy()
             stream.destroy()
+        if not a.no_cpu:
+            cu, kind, sample = cpu_matmul_us(t, n_rows, n_cols, 1)
+            res["cpu_baseline"] = {"us_t1": round(cu, 1), "kind": kind, "cores": 1,
+                                   "sample": sample}
+            res["speedup_vs_cpu_t1"] = round(cu / res["t1"]["us"], 1)
         print(json.dumps(res), flush=True)
         del ws, w0
     return 0
@@ -691,9 +721,15 @@ def gemm(a):
         e1.synchronize()
         us = e0.elapsed_ms(e1) * 1e3 / (reps * len(ws))
         tf = 2.0 * n_rows * n_cols * n_tok / (us * 1e-6) / 1e12
-        print(json.dumps({"case": name, "dtype": t, "n_rows": n_rows, "n_cols": n_cols,
-                          "tokens": n_tok, "us": round(us, 2), "TFLOP/s": round(tf, 1),
-                          "frac_fp32_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}), flush=True)
+        res = {"case": name, "dtype": t, "n_rows": n_rows, "n_cols": n_cols, "tokens": n_tok,
+               "us": round(us, 2), "TFLOP/s": round(tf, 1),
+               "frac_fp32_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+        if not a.no_cpu:
+            cu, kind, sample = cpu_matmul_us(t, n_rows, n_cols, n_tok)
+            res["cpu_baseline"] = {"us": round(cu, 1), "kind": kind, "cores": 1,
+                                   "sample": sample}
+            res["speedup_vs_cpu"] = round(cu / us, 1)
+        print(json.dumps(res), flush=True)
         stream.destroy()
         del ws
     return 0
