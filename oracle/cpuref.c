@@ -34,6 +34,8 @@
 
 #include <math.h>
 #include <stddef.h>
+#include <stdlib.h>
+#include <string.h>
 
 /* ------------------------------------------------------------------ norms */
 
@@ -221,4 +223,190 @@ void cr_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
             xr[i1] = x0 * s[p] + x1 * c[p];
         }
     }
+}
+
+/* ------------------------------------------------------------ softmax */
+/* src/tensor.cpp:167-178: max, exp(v - max) summed serially, times 1/sum
+ * (0 when the sum is not positive). */
+static float cr_fmax_(float a, float b) { return (a < b) ? b : a; }  /* std::max */
+
+void cr_softmax(float* v, int64_t n) {
+    if (n <= 0) return;
+    float m = v[0];
+    for (int64_t i = 1; i < n; ++i) m = cr_fmax_(m, v[i]);
+    float s = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        v[i] = expf(v[i] - m);
+        s += v[i];
+    }
+    const float inv = (s > 0.0f) ? 1.0f / s : 0.0f;
+    for (int64_t i = 0; i < n; ++i) v[i] *= inv;
+}
+
+void cr_softmax_rows(float* v, int64_t n_rows, int64_t n_cols) {
+    for (int64_t r = 0; r < n_rows; ++r) cr_softmax(v + r * n_cols, n_cols);
+}
+
+/* ---------------------------------------------------------- attention */
+/* src/transformer.cpp:120-203: grouped-query attention with an online softmax
+ * over key blocks. Query t (position qpos[t] or t), head h reads kv head
+ * h / (n_head / n_head_kv); key j (position kpos[j] or j) is kept when
+ * kp <= qp and, with window > 0, qp - kp < window; its score is
+ * (sum_d q[d]*k[d]) * scale. Per block: m_new = max(m, block max), the running
+ * sum and accumulator are scaled by exp(m - m_new) (0 while m is -inf), each
+ * kept key adds p = exp(s - m_new) and p*v. out = acc / max(l, 1e-30).
+ * Returns 0 for the reference's refusals. */
+int cr_attention_tiled(const float* q, const float* k, const float* v, float* out, int64_t n_q,
+                       int64_t n_head, int64_t n_head_kv, int64_t head_dim, int64_t value_dim,
+                       float scale, const int32_t* qpos, const int32_t* kpos, int64_t n_kv,
+                       int window, int64_t block) {
+    if (n_q <= 0 || n_head <= 0 || n_head_kv <= 0 || head_dim <= 0 || value_dim <= 0 ||
+        n_kv <= 0)
+        return 0;
+    if (n_head % n_head_kv) return 0;
+    const int64_t rep = n_head / n_head_kv;
+    if (block <= 0) block = n_kv;
+    const int64_t rows = n_q * n_head;
+    float* acc = (float*)calloc((size_t)(rows * value_dim), sizeof(float));
+    float* l = (float*)calloc((size_t)rows, sizeof(float));
+    float* m = (float*)malloc((size_t)rows * sizeof(float));
+    float* sb = (float*)malloc((size_t)block * sizeof(float));
+    if (!acc || !l || !m || !sb) {
+        free(acc); free(l); free(m); free(sb);
+        return 0;
+    }
+    for (int64_t i = 0; i < rows; ++i) m[i] = -INFINITY;
+    for (int64_t b0 = 0; b0 < n_kv; b0 += block) {
+        const int64_t b1 = (b0 + block < n_kv) ? b0 + block : n_kv;
+        const int64_t nb = b1 - b0;
+        for (int64_t t = 0; t < n_q; ++t) {
+            const int64_t qp = qpos ? (int64_t)qpos[t] : t;
+            for (int64_t h = 0; h < n_head; ++h) {
+                const int64_t kh = h / rep;
+                const float* qv = q + (t * n_head + h) * head_dim;
+                float* a = acc + (t * n_head + h) * value_dim;
+                float* lp = l + t * n_head + h;
+                float* mp = m + t * n_head + h;
+                float bmax = -INFINITY;
+                for (int64_t j = 0; j < nb; ++j) {
+                    const int64_t kp = kpos ? (int64_t)kpos[b0 + j] : b0 + j;
+                    int keep = kp <= qp;
+                    if (window > 0) keep = keep && (qp - kp) < window;
+                    float sj = -INFINITY;
+                    if (keep) {
+                        const float* kj = k + ((b0 + j) * n_head_kv + kh) * head_dim;
+                        float dot = 0.0f;
+                        for (int64_t d = 0; d < head_dim; ++d) dot += qv[d] * kj[d];
+                        sj = dot * scale;
+                    }
+                    sb[j] = sj;
+                    bmax = cr_fmax_(bmax, sj);
+                }
+                const float m_new = cr_fmax_(*mp, bmax);
+                const int finite_m = isfinite(*mp);
+                const float m_safe = finite_m ? *mp : 0.0f;
+                const float mn_safe = isfinite(m_new) ? m_new : 0.0f;
+                const float alpha = finite_m ? expf(m_safe - mn_safe) : 0.0f;
+                *lp *= alpha;
+                for (int64_t d = 0; d < value_dim; ++d) a[d] *= alpha;
+                float lsum = 0.0f;
+                for (int64_t j = 0; j < nb; ++j) {
+                    const float p = isfinite(sb[j]) ? expf(sb[j] - mn_safe) : 0.0f;
+                    lsum += p;
+                    const float* vj = v + ((b0 + j) * n_head_kv + kh) * value_dim;
+                    for (int64_t d = 0; d < value_dim; ++d) a[d] += p * vj[d];
+                }
+                *lp += lsum;
+                *mp = m_new;
+            }
+        }
+    }
+    for (int64_t i = 0; i < rows; ++i) {
+        const float den = cr_fmax_(l[i], 1e-30f);
+        for (int64_t d = 0; d < value_dim; ++d) out[i * value_dim + d] = acc[i * value_dim + d] / den;
+    }
+    free(acc); free(l); free(m); free(sb);
+    return 1;
+}
+
+/* src/transformer.cpp:205-214: one query at position n_kv - 1 against keys
+ * at positions 0..n_kv-1, one block. */
+int cr_attention(const float* q, const float* k, const float* v, float* out, int64_t n_head,
+                 int64_t n_head_kv, int64_t head_dim, int64_t value_dim, float scale,
+                 int64_t n_kv, int window) {
+    if (n_kv <= 0) return 0;
+    const int32_t qp = (int32_t)(n_kv - 1);
+    int32_t* kp = (int32_t*)malloc((size_t)n_kv * sizeof(int32_t));
+    if (!kp) return 0;
+    for (int64_t j = 0; j < n_kv; ++j) kp[j] = (int32_t)j;
+    const int ok = cr_attention_tiled(q, k, v, out, 1, n_head, n_head_kv, head_dim, value_dim,
+                                      scale, &qp, kp, n_kv, window, n_kv);
+    free(kp);
+    return ok;
+}
+
+/* ------------------------------------------------------- KV quantisers */
+/* include/aero/kv.hpp:62-103: symmetric per-vector scale amax/127 (int8) or
+ * amax/7 (int4), 1 when amax is 0; q = round(x / scale) clipped; int4 packs
+ * two per byte, low nibble first, as (q & 15), sign-extended on unpack. */
+void cr_kv_quant_i8(const float* x, int64_t dim, int8_t* q, float* s) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < dim; ++i) amax = cr_fmax_(amax, fabsf(x[i]));
+    const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+    *s = sc;
+    for (int64_t i = 0; i < dim; ++i) {
+        float v = roundf(x[i] / sc);
+        if (v > 127.0f) v = 127.0f;
+        if (v < -127.0f) v = -127.0f;
+        q[i] = (int8_t)v;
+    }
+}
+
+void cr_kv_quant_i4(const float* x, int64_t dim, uint8_t* q, float* s) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < dim; ++i) amax = cr_fmax_(amax, fabsf(x[i]));
+    const float sc = amax > 0.0f ? amax / 7.0f : 1.0f;
+    *s = sc;
+    for (int64_t i = 0; i < dim; i += 2) {
+        float a = roundf(x[i] / sc), b = roundf(x[i + 1] / sc);
+        if (a > 7.0f) a = 7.0f;
+        if (a < -7.0f) a = -7.0f;
+        if (b > 7.0f) b = 7.0f;
+        if (b < -7.0f) b = -7.0f;
+        q[i / 2] = (uint8_t)(((int)a & 0x0F) | (((int)b & 0x0F) << 4));
+    }
+}
+
+/* src/kv.cpp:29-46: dequantise one vector (0 fp32 copy, 1 int8, 2 int4). */
+int cr_kv_read_vec(int dt, const void* q, const float* scale, int64_t dim, float* out) {
+    if (!q || !scale || !out || dim <= 0) return 0;
+    if (dt == 0) {
+        memcpy(out, q, (size_t)dim * sizeof(float));
+    } else if (dt == 1) {
+        const int8_t* v = (const int8_t*)q;
+        for (int64_t i = 0; i < dim; ++i) out[i] = (float)v[i] * (*scale);
+    } else if (dt == 2) {
+        if (dim % 2) return 0;
+        const uint8_t* b = (const uint8_t*)q;
+        for (int64_t i = 0; i < dim; i += 2) {
+            const int lo = b[i / 2] & 0x0F, hi = (b[i / 2] >> 4) & 0x0F;
+            out[i] = (float)(lo >= 8 ? lo - 16 : lo) * (*scale);
+            out[i + 1] = (float)(hi >= 8 ? hi - 16 : hi) * (*scale);
+        }
+    } else {
+        return 0;
+    }
+    return 1;
+}
+
+/* src/kv.cpp:13-26: quantise one vector. */
+int cr_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale) {
+    if (!x || !q || !scale || dim <= 0) return 0;
+    if (dt == 0) memcpy(q, x, (size_t)dim * sizeof(float));
+    else if (dt == 1) cr_kv_quant_i8(x, dim, (int8_t*)q, scale);
+    else if (dt == 2) {
+        if (dim % 2) return 0;
+        cr_kv_quant_i4(x, dim, (uint8_t*)q, scale);
+    } else return 0;
+    return 1;
 }

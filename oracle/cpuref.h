@@ -64,6 +64,23 @@ void    cr_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
                       const float* cos_tab, const float* sin_tab,
                       const int32_t* pos, int mode);
 
+/* softmax, GQA attention (src/tensor.cpp:167-178, src/transformer.cpp:120-214) */
+void cr_softmax(float* v, int64_t n);
+void cr_softmax_rows(float* v, int64_t n_rows, int64_t n_cols);
+int  cr_attention_tiled(const float* q, const float* k, const float* v, float* out, int64_t n_q,
+                        int64_t n_head, int64_t n_head_kv, int64_t head_dim, int64_t value_dim,
+                        float scale, const int32_t* qpos, const int32_t* kpos, int64_t n_kv,
+                        int window, int64_t block);
+int  cr_attention(const float* q, const float* k, const float* v, float* out, int64_t n_head,
+                  int64_t n_head_kv, int64_t head_dim, int64_t value_dim, float scale,
+                  int64_t n_kv, int window);
+
+/* KV cache vectors (include/aero/kv.hpp:62-103, src/kv.cpp:13-46) */
+void cr_kv_quant_i8(const float* x, int64_t dim, int8_t* q, float* s);
+void cr_kv_quant_i4(const float* x, int64_t dim, uint8_t* q, float* s);
+int  cr_kv_read_vec(int dt, const void* q, const float* scale, int64_t dim, float* out);
+int  cr_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,18 @@ def lib():
         L.cr_rope_tables.restype = c_int64
         L.cr_apply_rope.argtypes = [fp, c_int64, c_int64, c_int64, fp, fp, ip, c_int]
         L.cr_apply_rope.restype = None
+        L.cr_softmax_rows.argtypes = [fp, c_int64, c_int64]
+        L.cr_softmax_rows.restype = None
+        L.cr_attention_tiled.argtypes = [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
+                                         c_int64, c_float, ip, ip, c_int64, c_int, c_int64]
+        L.cr_attention_tiled.restype = c_int
+        L.cr_attention.argtypes = [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
+                                   c_float, c_int64, c_int]
+        L.cr_attention.restype = c_int
+        L.cr_kv_write_vec.argtypes = [c_int, fp, c_int64, ctypes.c_void_p, fp]
+        L.cr_kv_write_vec.restype = c_int
+        L.cr_kv_read_vec.argtypes = [c_int, ctypes.c_void_p, fp, c_int64, fp]
+        L.cr_kv_read_vec.restype = c_int
         _lib = L
     return _lib
 
@@ -265,3 +277,66 @@ def qk_norm_rope(x, n_tok: int, n_head: int, head_dim: int, n_rot: int, pos,
         c, s = cos_tab, sin_tab
         rowpos = np.repeat(pos, n_head)
     return apply_rope(x, c, s, rowpos, mode, n_rot=n_rot)
+
+
+# ------------------------------------------------------- softmax, attention
+def softmax(x) -> np.ndarray:
+    """src/tensor.cpp:167-178 over the last axis."""
+    out = np.array(f32(x), copy=True)
+    cols = out.shape[-1] if out.ndim else 1
+    lib().cr_softmax_rows(_f(out), out.size // max(cols, 1), cols)
+    return out
+
+
+def attention_tiled(q, k, v, scale: float, qpos=None, kpos=None, block: int = 1024,
+                    window=None) -> np.ndarray:
+    """src/transformer.cpp:120-203. q (T,H,D), k (S,HK,D), v (S,HK,DV) -> (T,H,DV)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    T, H, D = q.shape
+    S, HK, DV = k.shape[0], k.shape[1], v.shape[2]
+    out = np.zeros((T, H, DV), np.float32)
+    qp = None if qpos is None else np.ascontiguousarray(qpos, np.int32).reshape(-1)
+    kp = None if kpos is None else np.ascontiguousarray(kpos, np.int32).reshape(-1)
+    ok = lib().cr_attention_tiled(_f(q), _f(k), _f(v), _f(out), T, H, HK, D, DV, float(scale),
+                                  _i(qp), _i(kp), S, 0 if window is None else int(window),
+                                  int(block))
+    if not ok:
+        raise ValueError("attention refused")
+    return out
+
+
+def attention(q, k, v, scale: float, window=None) -> np.ndarray:
+    """src/transformer.cpp:205-214: one query at position S-1. q (H,D)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    H, D = q.shape
+    S, HK, DV = k.shape[0], k.shape[1], v.shape[2]
+    out = np.zeros((H, DV), np.float32)
+    ok = lib().cr_attention(_f(q), _f(k), _f(v), _f(out), H, HK, D, DV, float(scale), S,
+                            0 if window is None else int(window))
+    if not ok:
+        raise ValueError("attention refused")
+    return out
+
+
+KV_F32, KV_I8, KV_I4 = 0, 1, 2
+
+
+def kv_write_vec(dt: int, x):
+    """src/kv.cpp:13-26: (packed vector as uint8 bytes, scale)."""
+    x = f32(x).reshape(-1)
+    nbytes = {KV_F32: 4 * x.size, KV_I8: x.size, KV_I4: x.size // 2}[dt]
+    q = np.zeros(nbytes, np.uint8)
+    s = np.zeros(1, np.float32)
+    if not lib().cr_kv_write_vec(dt, _f(x), x.size, q.ctypes.data, _f(s)):
+        raise ValueError("kv write refused")
+    return q, float(s[0])
+
+
+def kv_read_vec(dt: int, q, scale: float, dim: int) -> np.ndarray:
+    """src/kv.cpp:29-46."""
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.array([scale], np.float32)
+    out = np.zeros(dim, np.float32)
+    if not lib().cr_kv_read_vec(dt, q.ctypes.data, _f(s), dim, _f(out)):
+        raise ValueError("kv read refused")
+    return out

@@ -19,9 +19,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REF_DIR = os.path.join(HERE, "_ref")
 KERNELS = os.path.join(REF_DIR, "libref_kernels.so")
 TRANSFORMER = os.path.join(REF_DIR, "libref_transformer.so")
+KV = os.path.join(REF_DIR, "libref_kv.so")
 
 _k = None
 _t = None
+_v = None
 
 
 def kernels():
@@ -65,8 +67,29 @@ def transformer():
         L.aero_swiglu.restype = None
         L.aero_tensor_mul.argtypes = [fp, fp, c_int64]
         L.aero_tensor_mul.restype = c_int
+        L.aero_softmax_rows.argtypes = [fp, c_int64, c_int64]
+        L.aero_softmax_rows.restype = None
+        L.aero_attention_tiled.argtypes = [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
+                                           c_int64, c_float, ip, ip, c_int64, c_int, c_int64]
+        L.aero_attention_tiled.restype = c_int
+        L.aero_attention.argtypes = [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
+                                     c_float, c_int64, c_int]
+        L.aero_attention.restype = c_int
         _t = L
     return _t
+
+
+def kv():
+    global _v
+    if _v is None and os.path.exists(KV):
+        L = ctypes.CDLL(KV)
+        fp = POINTER(c_float)
+        L.aero_kv_write_vec.argtypes = [c_int, fp, c_int64, ctypes.c_void_p, fp]
+        L.aero_kv_write_vec.restype = c_int
+        L.aero_kv_read_vec.argtypes = [c_int, ctypes.c_void_p, fp, c_int64, fp]
+        L.aero_kv_read_vec.restype = c_int
+        _v = L
+    return _v
 
 
 def available() -> bool:
@@ -186,4 +209,53 @@ def apply_rope(x, cos, sin, positions=None, mode: int = 0, n_rot=None) -> np.nda
     pos = None if positions is None else np.ascontiguousarray(positions, np.int32)
     transformer().aero_apply_rope(_f(out), out.size // head_dim, head_dim, n_rot,
                                   _f(cos), _f(sin), _i(pos), mode)
+    return out
+
+
+def softmax(x) -> np.ndarray:
+    out = np.array(np.ascontiguousarray(x, dtype=np.float32), copy=True)
+    cols = out.shape[-1]
+    transformer().aero_softmax_rows(_f(out), out.size // cols, cols)
+    return out
+
+
+def _i32(a):
+    if a is None:
+        return ctypes.cast(None, POINTER(c_int32))
+    return a.ctypes.data_as(POINTER(c_int32))
+
+
+def attention_tiled(q, k, v, scale: float, qpos=None, kpos=None, block: int = 1024,
+                    window=None) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    T, H, D = q.shape
+    S, HK, DV = k.shape[0], k.shape[1], v.shape[2]
+    out = np.zeros((T, H, DV), np.float32)
+    qp = None if qpos is None else np.ascontiguousarray(qpos, np.int32).reshape(-1)
+    kp = None if kpos is None else np.ascontiguousarray(kpos, np.int32).reshape(-1)
+    if not transformer().aero_attention_tiled(_f(q), _f(k), _f(v), _f(out), T, H, HK, D, DV,
+                                              float(scale), _i32(qp), _i32(kp), S,
+                                              0 if window is None else int(window), int(block)):
+        raise ValueError("reference attention refused")
+    return out
+
+
+def kv_write_vec(dt: int, x):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    nbytes = {0: 4 * x.size, 1: x.size, 2: x.size // 2}[dt]
+    q = np.zeros(nbytes, np.uint8)
+    s = np.zeros(1, np.float32)
+    if not kv().aero_kv_write_vec(dt, _f(x), x.size, q.ctypes.data, _f(s)):
+        raise ValueError("reference kv write refused")
+    return q, float(s[0])
+
+
+def kv_read_vec(dt: int, q, scale: float, dim: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.array([scale], np.float32)
+    out = np.zeros(dim, np.float32)
+    if not kv().aero_kv_read_vec(dt, q.ctypes.data, _f(s), dim, _f(out)):
+        raise ValueError("reference kv read refused")
     return out

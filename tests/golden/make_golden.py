@@ -18,8 +18,10 @@ where the reference tree exists):
 2. ref_vectors.npz -- inputs and outputs of the reference's own C++ (built
    into oracle/_ref/ from src/kernels.cpp, src/transformer.cpp and
    src/tensor.cpp) on small seeded inputs: row norms, activations, RoPE tables
-   and rotation, Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_XS dequant, and matvec /
-   matmul over each of those block types. These pin the oracle and the GPU
+   and rotation, Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_XS dequant, matvec /
+   matmul over each of those block types, row softmax, GQA attention (causal
+   with positions, a window, shuffled key positions) and the int8 / int4 KV
+   vector quantisers. These pin the oracle and the GPU
    path where the reference build is absent (the GPU box).
 """
 from __future__ import annotations
@@ -182,6 +184,30 @@ def ref_vectors() -> dict:
         v[f"mv{t}_w"], v[f"mv{t}_x"] = w, X
         v[f"mv{t}_y"] = R.matvec(t, w, X[0], n_rows)
         v[f"mm{t}_y"] = R.matmul(t, w, X, n_rows)
+    # softmax rows and GQA attention (src/tensor.cpp:167-178,
+    # src/transformer.cpp:120-214): prefill-style causal with positions, a
+    # window, a fully masked query (position below every key), and decode
+    sm = (rng.standard_normal((6, 37)) * 4).astype(np.float32)
+    v["softmax_x"], v["softmax_y"] = sm, R.softmax(sm)
+    T, H, HK, D, DV, S = 7, 8, 2, 64, 48, 50
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    k = rng.standard_normal((S, HK, D)).astype(np.float32)
+    vv = rng.standard_normal((S, HK, DV)).astype(np.float32)
+    qpos = np.array([0, 5, 17, 31, 49, 49, -1], np.int32)
+    v["att_q"], v["att_k"], v["att_v"], v["att_qpos"] = q, k, vv, qpos
+    v["att_out"] = R.attention_tiled(q, k, vv, 0.125, qpos=qpos, block=16)
+    v["att_out_win8"] = R.attention_tiled(q, k, vv, 0.125, qpos=qpos, block=16, window=8)
+    kpos = rng.permutation(S).astype(np.int32)
+    v["att_kpos"] = kpos
+    v["att_out_kpos"] = R.attention_tiled(q, k, vv, 0.125, qpos=qpos, kpos=kpos, block=1024)
+    # KV quantisers (src/kv.cpp:13-46)
+    kvx = (rng.standard_normal((5, 64)) * np.array([1, 1e-3, 30, 0, 7], np.float32)[:, None])
+    kvx = kvx.astype(np.float32)
+    v["kv_x"] = kvx
+    for dt in (1, 2):
+        qs, sc = zip(*(R.kv_write_vec(dt, row) for row in kvx))
+        v[f"kv{dt}_q"] = np.stack(qs)
+        v[f"kv{dt}_scale"] = np.array(sc, np.float32)
     return v
 
 

@@ -467,3 +467,127 @@ def test_planted_fp32_mistakes_are_caught():
     z = g["act_z"].astype(np.float64)
     tanh = 0.5 * z * (1 + np.tanh(math.sqrt(2 / math.pi) * (z + 0.044715 * z ** 3)))
     assert np.abs(tanh - g["gelu_out"]).max() > 1e-4
+
+
+# ------------------------------------------------------ softmax / attention
+def _attn_f64(q, k, v, scale, qpos=None, kpos=None, window=None):
+    """Definition of the reference's attention in float64: per (token, head),
+    softmax over the kept keys of (q . k) * scale, times v; zero when no key is
+    kept. GQA: head h reads kv head h // (H // HK)."""
+    T, H, D = q.shape
+    S, HK, DV = k.shape[0], k.shape[1], v.shape[2]
+    rep = H // HK
+    qp = np.arange(T) if qpos is None else np.asarray(qpos)
+    kp = np.arange(S) if kpos is None else np.asarray(kpos)
+    out = np.zeros((T, H, DV))
+    for t in range(T):
+        keep = kp <= qp[t]
+        if window:
+            keep &= (qp[t] - kp) < window
+        if not keep.any():
+            continue
+        for h in range(H):
+            s = (k[keep, h // rep].astype(np.float64) @ q[t, h].astype(np.float64)) * scale
+            p = np.exp(s - s.max())
+            out[t, h] = (p / p.sum()) @ v[keep, h // rep].astype(np.float64)
+    return out
+
+
+def test_golden_softmax_attention_kv():
+    """The reference's own softmax, attention and KV quantiser outputs."""
+    g = golden("ref_vectors.npz")
+    assert bits_equal(O.softmax(g["softmax_x"]), g["softmax_y"])
+    q, k, v, qpos = g["att_q"], g["att_k"], g["att_v"], g["att_qpos"]
+    assert bits_equal(O.attention_tiled(q, k, v, 0.125, qpos=qpos, block=16), g["att_out"])
+    assert bits_equal(O.attention_tiled(q, k, v, 0.125, qpos=qpos, block=16, window=8),
+                      g["att_out_win8"])
+    assert bits_equal(O.attention_tiled(q, k, v, 0.125, qpos=qpos, kpos=g["att_kpos"]),
+                      g["att_out_kpos"])
+    for dt in (1, 2):
+        for i, row in enumerate(g["kv_x"]):
+            qb, sc = O.kv_write_vec(dt, row)
+            assert np.array_equal(qb, g[f"kv{dt}_q"][i]) and np.float32(sc) == g[f"kv{dt}_scale"][i]
+
+
+def test_live_reference_attention():
+    """Bit-identical to the compiled reference (src/transformer.cpp) across
+    GQA ratios, block sizes, windows, positions and the decode entry."""
+    if R.transformer() is None:
+        pytest.skip("oracle/_ref not built")
+    rng = np.random.default_rng(41)
+    for (T, H, HK, D, DV, S) in ((1, 32, 8, 128, 128, 300), (9, 6, 6, 16, 24, 40),
+                                 (4, 4, 1, 32, 32, 70)):
+        q = rng.standard_normal((T, H, D)).astype(np.float32)
+        k = rng.standard_normal((S, HK, D)).astype(np.float32)
+        v = rng.standard_normal((S, HK, DV)).astype(np.float32)
+        qpos = rng.integers(-1, S + 2, T).astype(np.int32)
+        kpos = rng.permutation(S).astype(np.int32)
+        for block, window, kp in ((1024, None, None), (13, None, None), (32, 9, None),
+                                  (64, None, kpos)):
+            a = O.attention_tiled(q, k, v, 0.1, qpos=qpos, kpos=kp, block=block, window=window)
+            b = R.attention_tiled(q, k, v, 0.1, qpos=qpos, kpos=kp, block=block, window=window)
+            assert bits_equal(a, b)
+    x = (rng.standard_normal((5, 1000)) * 10).astype(np.float32)
+    assert bits_equal(O.softmax(x), R.softmax(x))
+    if R.kv() is not None:
+        for dt in (0, 1, 2):
+            xv = (rng.standard_normal(128) * 5).astype(np.float32)
+            qa, sa = O.kv_write_vec(dt, xv)
+            qb, sb = R.kv_write_vec(dt, xv)
+            assert np.array_equal(qa, qb) and sa == sb
+            assert bits_equal(O.kv_read_vec(dt, qa, sa, 128), R.kv_read_vec(dt, qb, sb, 128))
+
+
+def test_attention_definition_and_invariants():
+    """Against the float64 definition (masked softmax times V, GQA by integer
+    division of the head), plus: a fully masked query gives exactly zero, one
+    kept key returns its value row, the block size changes only rounding, and
+    a planted head mapping (h % HK) is rejected."""
+    rng = np.random.default_rng(43)
+    T, H, HK, D, DV, S = 6, 8, 2, 16, 20, 33
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    k = rng.standard_normal((S, HK, D)).astype(np.float32)
+    v = rng.standard_normal((S, HK, DV)).astype(np.float32)
+    qpos = np.array([0, 3, 10, 32, 32, -5], np.int32)
+    for window in (None, 4):
+        got = O.attention_tiled(q, k, v, 0.3, qpos=qpos, block=7, window=window)
+        want = _attn_f64(q, k, v, 0.3, qpos=qpos, window=window)
+        assert rel_to_scale(got, want) <= 1e-6
+    got = O.attention_tiled(q, k, v, 0.3, qpos=qpos)
+    assert not got[5].any()                                          # position -5: nothing kept
+    for h in range(H):                                               # position 0: key 0 only
+        assert bits_equal(got[0, h], v[0, h // (H // HK)])
+    a = O.attention_tiled(q, k, v, 0.3, qpos=qpos, block=5)
+    b = O.attention_tiled(q, k, v, 0.3, qpos=qpos, block=1024)
+    assert rel_to_scale(a, b) <= 1e-6
+    # a planted mistake: kv head h % HK instead of h // rep
+    bad = np.zeros((T, H, DV))
+    for h in range(H):
+        bad[:, h] = _attn_f64(q[:, [h]], k[:, [h % HK]], v[:, [h % HK]], 0.3, qpos=qpos)[:, 0]
+    assert rel_to_scale(O.attention_tiled(q, k, v, 0.3, qpos=qpos), bad) > 1e-3
+    # decode entry = one query at position S-1
+    dq = rng.standard_normal((H, D)).astype(np.float32)
+    assert bits_equal(O.attention(dq, k, v, 0.3),
+                      O.attention_tiled(dq[None], k, v, 0.3, qpos=[S - 1], block=S)[0])
+
+
+def test_softmax_and_kv_closed_forms():
+    """softmax rows sum to 1 and equal the float64 definition; int8 / int4
+    quantisation: scale = amax/127 (amax/7), 1 for a zero vector, every value
+    within scale/2 of x, int4 low nibble first and sign-extended on read."""
+    rng = np.random.default_rng(47)
+    x = (rng.standard_normal((4, 50)) * 6).astype(np.float32)
+    y = O.softmax(x)
+    e = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    assert np.allclose(y, e / e.sum(1, keepdims=True), rtol=1e-6, atol=1e-7)
+    for dt, qmax in ((1, 127), (2, 7)):
+        xv = (rng.standard_normal(64) * 3).astype(np.float32)
+        qb, sc = O.kv_write_vec(dt, xv)
+        assert np.float32(sc) == np.float32(np.abs(xv).max()) / np.float32(qmax)
+        back = O.kv_read_vec(dt, qb, sc, 64)
+        assert np.all(np.abs(back.astype(np.float64) - xv) <= sc / 2 * (1 + 1e-6))
+        z = O.kv_write_vec(dt, np.zeros(64, np.float32))
+        assert z[1] == 1.0 and not z[0].any()
+    qb, sc = O.kv_write_vec(2, np.array([1.0, -7.0] + [0.0] * 6, np.float32))
+    assert sc == 1.0 and qb[0] == (1 | (0x9 << 4))                  # -7 & 15 = 9, high nibble
+    assert list(O.kv_read_vec(2, qb, sc, 8)[:2]) == [1.0, -7.0]
