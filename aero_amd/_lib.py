@@ -53,6 +53,14 @@ PROTOTYPES = {
     "aero_dequant_threaded": (c_int, [c_int, u8p, c_int64, fp, c_int64, c_int]),
     "aero_matvec": (c_int, [c_int, u8p, fp, fp, c_int64, c_int64, c_int]),
     "aero_matmul": (c_int, [c_int, u8p, fp, fp, c_int64, c_int64, c_int64, c_int]),
+    "aero_tensor_softmax": (c_int, [fp, c_int64]),
+    "aero_softmax": (None, [fp, c_int64]),
+    "aero_softmax_rows": (None, [fp, c_int64, c_int64]),
+    "aero_attention_tiled": (c_int, [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
+                                     c_int64, c_float, ip, ip, c_int64, c_int, c_int64]),
+    "aero_attention": (c_int, [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64, c_float,
+                               c_int64, c_int]),
+    "aero_kv_write_vec": (c_int, [c_int, fp, c_int64, vp, fp]),
     # device-pointer fused ops
     "aero_hip_rmsnorm": (c_int, [vp, vp, vp, c_int64, c_int64, c_float, c_int, vp]),
     "aero_hip_gated_rmsnorm_silu": (c_int, [vp, vp, vp, c_int64, vp, c_int64, c_int64,
@@ -67,6 +75,14 @@ PROTOTYPES = {
                                       c_float, vp, vp, vp]),
     "aero_hip_dequant": (c_int, [c_int, vp, c_int64, vp, c_int64, vp]),
     "aero_hip_matvec": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp]),
+    "aero_hip_attention_workspace": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64,
+                                               c_int64]),
+    "aero_hip_attention": (c_int, [vp, c_int, vp, vp, vp, vp, vp, c_int64, c_int64, c_int64,
+                                   c_int64, c_int64, c_float, vp, vp, c_int64, c_int, vp,
+                                   c_int64, vp]),
+    "aero_hip_kv_write": (c_int, [c_int, vp, c_int64, c_int64, c_int64, c_int64, c_int64, vp,
+                                  vp, vp]),
+    "aero_hip_softmax_rows": (c_int, [vp, vp, c_int64, c_int64, vp]),
     "aero_hip_copy_f32": (c_int, [vp, vp, c_int64, vp]),
     # runtime
     "aero_hip_last_error": (c_char_p, []),

@@ -36,6 +36,16 @@ int64_t dtype_block_bytes(int t);
 int64_t dtype_block_values(int t);
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
               int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s);
+bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scale, const void* v,
+                   const float* v_scale, float* out, int64_t n_q, int64_t n_head,
+                   int64_t n_head_kv, int64_t head_dim, int64_t value_dim, float scale,
+                   const int32_t* qpos, const int32_t* kpos, int64_t n_kv, int window,
+                   void* workspace, int64_t ws_bytes, hipStream_t s);
+int64_t attn_workspace_bytes(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
+                             int64_t value_dim, int64_t n_kv);
+bool kv_write_dev(int dt, const float* x, int64_t n_tok, int64_t heads, int64_t dim,
+                  int64_t phys0, int64_t cap, void* q, float* scale, hipStream_t s);
+bool softmax_rows_dev(const float* x, float* y, int64_t n_rows, int64_t n_cols, hipStream_t s);
 
 namespace {
 
@@ -402,4 +412,116 @@ int aero_dequant_threaded(int t, const uint8_t* raw, int64_t raw_len, float* out
     return aero_dequant_ref(t, raw, raw_len, out, n_values);
 }
 
+
+// ------------------------------------------- src/transformer.cpp:259-284 ABI
+void aero_softmax(float* v, int64_t n) {
+    aero::clear_error();
+    if (v == nullptr || n <= 0) return;
+    aero::Staging st;
+    void* p[1];
+    const size_t bytes = (size_t)n * 4;
+    if (st.reserve({bytes}, p) && st.h2d(p[0], v, bytes) &&
+        aero::softmax_rows_dev(static_cast<float*>(p[0]), static_cast<float*>(p[0]), 1, n,
+                               st.stream()))
+        (void)(st.d2h(v, p[0], bytes) && st.finish());
+}
+
+void aero_softmax_rows(float* v, int64_t n_rows, int64_t n_cols) {
+    aero::clear_error();
+    if (v == nullptr || n_rows <= 0 || n_cols <= 0) return;
+    aero::Staging st;
+    void* p[1];
+    const size_t bytes = (size_t)(n_rows * n_cols) * 4;
+    if (st.reserve({bytes}, p) && st.h2d(p[0], v, bytes) &&
+        aero::softmax_rows_dev(static_cast<float*>(p[0]), static_cast<float*>(p[0]), n_rows,
+                               n_cols, st.stream()))
+        (void)(st.d2h(v, p[0], bytes) && st.finish());
+}
+
+// src/tensor.cpp:246-249 aero_tensor_softmax (flat vector, in place).
+int aero_tensor_softmax(float* v, int64_t n) {
+    if (v == nullptr || n <= 0) {
+        aero::clear_error();
+        set_error("aero_tensor_softmax: refused");
+        return 0;
+    }
+    aero_softmax(v, n);
+    return aero_hip_last_error()[0] == 0 ? 1 : 0;
+}
+
+// src/transformer.cpp:120-203 through :266-273. The reference's refusals
+// (non-positive sizes, n_head not a multiple of n_head_kv) return 0; `block`
+// only changes the reference's rounding and is not needed on the GPU.
+int aero_attention_tiled(const float* q, const float* k, const float* v, float* out,
+                         int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
+                         int64_t value_dim, float scale, const int32_t* qpos,
+                         const int32_t* kpos, int64_t n_kv, int window, int64_t block) {
+    (void)block;
+    aero::clear_error();
+    if (n_q <= 0 || n_head <= 0 || n_head_kv <= 0 || head_dim <= 0 || value_dim <= 0 ||
+        n_kv <= 0 || n_head % n_head_kv) {
+        set_error("aero_attention_tiled: refused sizes");
+        return 0;
+    }
+    if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) {
+        set_error("aero_attention_tiled: null pointer");
+        return 0;
+    }
+    const size_t qb = (size_t)(n_q * n_head * head_dim) * 4;
+    const size_t kb = (size_t)(n_kv * n_head_kv * head_dim) * 4;
+    const size_t vb = (size_t)(n_kv * n_head_kv * value_dim) * 4;
+    const size_t ob = (size_t)(n_q * n_head * value_dim) * 4;
+    const size_t qpb = qpos ? (size_t)n_q * 4 : 0, kpb = kpos ? (size_t)n_kv * 4 : 0;
+    const int64_t wsb = aero::attn_workspace_bytes(n_q, n_head, n_head_kv, head_dim, value_dim,
+                                                   n_kv);
+    aero::Staging st;
+    void* p[7];
+    if (!st.reserve({qb, kb, vb, ob, qpb, kpb, (size_t)wsb}, p)) return 0;
+    const bool ok =
+        st.h2d(p[0], q, qb) && st.h2d(p[1], k, kb) && st.h2d(p[2], v, vb) &&
+        (!qpos || st.h2d(p[4], qpos, qpb)) && (!kpos || st.h2d(p[5], kpos, kpb)) &&
+        aero::attention_dev(static_cast<float*>(p[0]), 0, p[1], nullptr, p[2], nullptr,
+                            static_cast<float*>(p[3]), n_q, n_head, n_head_kv, head_dim,
+                            value_dim, scale, qpos ? static_cast<int32_t*>(p[4]) : nullptr,
+                            kpos ? static_cast<int32_t*>(p[5]) : nullptr, n_kv, window,
+                            wsb > 0 ? p[6] : nullptr, wsb, st.stream()) &&
+        st.d2h(out, p[3], ob) && st.finish();
+    return ok ? 1 : 0;
+}
+
+// src/transformer.cpp:205-214: one query at position n_kv - 1; keys at
+// positions 0..n_kv-1 (the default key positions).
+int aero_attention(const float* q, const float* k, const float* v, float* out, int64_t n_head,
+                   int64_t n_head_kv, int64_t head_dim, int64_t value_dim, float scale,
+                   int64_t n_kv, int window) {
+    if (n_kv <= 0) {
+        aero::clear_error();
+        set_error("aero_attention: n_kv <= 0");
+        return 0;
+    }
+    const int32_t qp = (int32_t)(n_kv - 1);
+    return aero_attention_tiled(q, k, v, out, 1, n_head, n_head_kv, head_dim, value_dim, scale,
+                                &qp, nullptr, n_kv, window, n_kv);
+}
+
+// ---------------------------------------------------- src/kv.cpp:13-46 ABI
+// One vector through the device quantiser (dt 0 fp32, 1 int8, 2 int4).
+int aero_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale) {
+    aero::clear_error();
+    if (x == nullptr || q == nullptr || scale == nullptr || dim <= 0 || dt < 0 || dt > 2 ||
+        (dt == 2 && dim % 2)) {
+        set_error("aero_kv_write_vec: refused");
+        return 0;
+    }
+    const size_t xb = (size_t)dim * 4;
+    const size_t qb = dt == 0 ? xb : (dt == 1 ? (size_t)dim : (size_t)dim / 2);
+    aero::Staging st;
+    void* p[3];
+    if (!st.reserve({xb, qb, 4}, p)) return 0;
+    const bool ok = st.h2d(p[0], x, xb) &&
+                    aero::kv_write_dev(dt, static_cast<float*>(p[0]), 1, 1, dim, 0, 1, p[1],
+                                       static_cast<float*>(p[2]), st.stream()) &&
+                    st.d2h(q, p[1], qb) && (dt == 0 || st.d2h(scale, p[2], 4)) && st.finish();
+    return ok ? 1 : 0;
+}
 }  // extern "C"

@@ -199,6 +199,79 @@ def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: i
                                           n_cols, n_tok, _s(stream)), "matvec")
 
 
+KV_F32, KV_INT8, KV_INT4 = 0, 1, 2
+
+
+def kv_vec_bytes(dt: int, dim: int) -> int:
+    """Bytes of one (position, head) vector in a KV slot of type dt."""
+    return {KV_F32: 4 * dim, KV_INT8: dim, KV_INT4: dim // 2}[dt]
+
+
+def kv_write(dt: int, x: DeviceArray, n_tok: int, heads: int, dim: int, q: DeviceArray,
+             scale: DeviceArray | None, phys0: int, cap: int,
+             stream: Stream | None = None) -> None:
+    """Append rows (t, h) of x [n_tok, heads, dim] to a KV slot q [cap, heads, dim]
+    (fp32 / int8 / int4, with one fp32 scale per vector in `scale` for the
+    integer types) at physical positions (phys0 + t) % cap
+    (include/aero/kv.hpp:62-126)."""
+    if dt not in (KV_F32, KV_INT8, KV_INT4):
+        raise ValueError(f"kv dtype {dt}")
+    _need(x, n_tok * heads * dim, np.float32, "x")
+    if q.nbytes < cap * heads * kv_vec_bytes(dt, dim):
+        raise ValueError("kv slot too small")
+    if dt != KV_F32:
+        _need(scale, cap * heads, np.float32, "scale")
+    _lib.check(_lib.lib().aero_hip_kv_write(dt, x.ptr, n_tok, heads, dim, phys0, cap, q.ptr,
+                                            as_ptr(scale), _s(stream)), "kv_write")
+
+
+_ws_cache: dict = {}
+
+
+def attention(q: DeviceArray, k: DeviceArray, v: DeviceArray, out: DeviceArray, n_q: int,
+              n_head: int, n_head_kv: int, head_dim: int, value_dim: int, n_kv: int,
+              scale: float, qpos: DeviceArray | None = None, kpos: DeviceArray | None = None,
+              window: int = 0, kv_dt: int = KV_F32, k_scale: DeviceArray | None = None,
+              v_scale: DeviceArray | None = None, stream: Stream | None = None) -> None:
+    """GQA attention with an online softmax over a KV cache
+    (src/transformer.cpp:120-214): q [n_q, n_head, head_dim] -> out
+    [n_q, n_head, value_dim]; K / V [n_kv, n_head_kv, dim] in kv_dt. The
+    decode split's workspace is allocated once per size and reused."""
+    _need(q, n_q * n_head * head_dim, np.float32, "q")
+    _need(out, n_q * n_head * value_dim, np.float32, "out")
+    _need(qpos, n_q, np.int32, "qpos")
+    _need(kpos, n_kv, np.int32, "kpos")
+    if kv_dt == KV_F32:
+        _need(k, n_kv * n_head_kv * head_dim, np.float32, "k")
+        _need(v, n_kv * n_head_kv * value_dim, np.float32, "v")
+    else:
+        if k.nbytes < n_kv * n_head_kv * kv_vec_bytes(kv_dt, head_dim) or \
+                v.nbytes < n_kv * n_head_kv * kv_vec_bytes(kv_dt, value_dim):
+            raise ValueError("K / V cache too small")
+        _need(k_scale, n_kv * n_head_kv, np.float32, "k_scale")
+        _need(v_scale, n_kv * n_head_kv, np.float32, "v_scale")
+    L = _lib.lib()
+    wsb = int(L.aero_hip_attention_workspace(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv))
+    ws = None
+    if wsb > 0:
+        ws = _ws_cache.get(wsb)
+        if ws is None:
+            ws = _ws_cache[wsb] = DeviceArray.empty(wsb // 4, np.float32)
+    _lib.check(L.aero_hip_attention(q.ptr, kv_dt, k.ptr, as_ptr(k_scale), v.ptr,
+                                    as_ptr(v_scale), out.ptr, n_q, n_head, n_head_kv, head_dim,
+                                    value_dim, float(scale), as_ptr(qpos), as_ptr(kpos), n_kv,
+                                    int(window), as_ptr(ws), wsb, _s(stream)), "attention")
+
+
+def softmax_rows(x: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
+                 stream: Stream | None = None) -> None:
+    """y[r] = softmax(x[r]) (src/tensor.cpp:167-178); y may be x."""
+    _need(x, n_rows * n_cols, np.float32, "x")
+    _need(y, n_rows * n_cols, np.float32, "y")
+    _lib.check(_lib.lib().aero_hip_softmax_rows(x.ptr, y.ptr, n_rows, n_cols, _s(stream)),
+               "softmax_rows")
+
+
 def copy_f32(src: DeviceArray, dst: DeviceArray, n: int | None = None,
              stream: Stream | None = None) -> None:
     n = src.size if n is None else int(n)

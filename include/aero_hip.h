@@ -114,6 +114,29 @@ int aero_matvec(int t, const uint8_t* w, const float* x, float* y, int64_t n_row
 int aero_matmul(int t, const uint8_t* w, const float* X, float* Y, int64_t n_tokens,
                 int64_t n_rows, int64_t n_cols, int threads);
 
+/* src/tensor.cpp:246-249 aero_tensor_softmax (in place; 0 = refused). */
+int aero_tensor_softmax(float* v, int64_t n);
+/* src/transformer.cpp:259-263 aero_softmax / aero_softmax_rows (in place). */
+void aero_softmax(float* v, int64_t n);
+void aero_softmax_rows(float* v, int64_t n_rows, int64_t n_cols);
+/* src/transformer.cpp:266-273 aero_attention_tiled: GQA attention with an
+ * online softmax, q [n_q, n_head, head_dim], k [n_kv, n_head_kv, head_dim],
+ * v [n_kv, n_head_kv, value_dim] -> out [n_q, n_head, value_dim]; key j kept
+ * for query t when kpos[j] <= qpos[t] (and qpos - kpos < window when
+ * window > 0); null positions mean t / j. 1 = done, 0 = refused (non-positive
+ * sizes, n_head % n_head_kv). `block` is accepted and not needed. */
+int aero_attention_tiled(const float* q, const float* k, const float* v, float* out,
+                         int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
+                         int64_t value_dim, float scale, const int32_t* qpos,
+                         const int32_t* kpos, int64_t n_kv, int window, int64_t block);
+/* src/transformer.cpp:276-281 aero_attention: one query at position n_kv-1. */
+int aero_attention(const float* q, const float* k, const float* v, float* out, int64_t n_head,
+                   int64_t n_head_kv, int64_t head_dim, int64_t value_dim, float scale,
+                   int64_t n_kv, int window);
+/* src/kv.cpp:13-26 aero_kv_write_vec: quantise one vector (dt 0 fp32 copy,
+ * 1 int8 with scale amax/127, 2 int4 low-nibble-first with scale amax/7). */
+int aero_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale);
+
 /* ------------------------------------------------------------------------
  * 2. Device-pointer fused ops (HBM pointers, asynchronous on `stream`)
  * ---------------------------------------------------------------------- */
@@ -224,6 +247,31 @@ int aero_hip_dequant(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
 int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
                     float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
                     void* stream);
+
+/* Attention over a KV cache, the device form of aero_attention_tiled
+ * (src/transformer.cpp:120-214): q [n_q, n_head, head_dim] fp32; K / V
+ * [n_kv, n_head_kv, dim] in kv_dt (0 fp32, 16-byte aligned, dims a multiple
+ * of 4; 1 int8 or 2 int4 with one fp32 scale per (position, head) vector in
+ * k_scale / v_scale, read as the reference's aero_kv_read_vec); out
+ * [n_q, n_head, value_dim]. head_dim, value_dim <= 256. Decode shapes split
+ * the keys into chunks whose partial softmax states go to `workspace`
+ * (aero_hip_attention_workspace bytes; 0 when one chunk suffices). */
+int64_t aero_hip_attention_workspace(int64_t n_q, int64_t n_head, int64_t n_head_kv,
+                                     int64_t head_dim, int64_t value_dim, int64_t n_kv);
+int aero_hip_attention(const float* q, int kv_dt, const void* k, const float* k_scale,
+                       const void* v, const float* v_scale, float* out, int64_t n_q,
+                       int64_t n_head, int64_t n_head_kv, int64_t head_dim, int64_t value_dim,
+                       float scale, const int32_t* qpos, const int32_t* kpos, int64_t n_kv,
+                       int window, void* workspace, int64_t ws_bytes, void* stream);
+/* Append to a KV cache slot (include/aero/kv.hpp:62-126, src/kv.cpp:13-26):
+ * row (t, h) of x [n_tok, heads, dim] is quantised (dt 0 fp32, 1 int8, 2
+ * int4) into vector ((phys0 + t) % cap) * heads + h of the slot q (and its
+ * scale), so a ring slot wraps. */
+int aero_hip_kv_write(int dt, const float* x, int64_t n_tok, int64_t heads, int64_t dim,
+                      int64_t phys0, int64_t cap, void* q, float* scale, void* stream);
+/* Row softmax (src/tensor.cpp:167-178): y[r] = softmax(x[r]); y may alias x. */
+int aero_hip_softmax_rows(const float* x, float* y, int64_t n_rows, int64_t n_cols,
+                          void* stream);
 
 /* Plain fp32 copy kernel (dst = src, n elements): the known-size reference
  * workload used to calibrate HBM byte counters. */
