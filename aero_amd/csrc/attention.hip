@@ -3,22 +3,22 @@
 // softmax (src/tensor.cpp:167-178) and the KV cache vector quantisers
 // (include/aero/kv.hpp:62-103, src/kv.cpp:13-46).
 //
-// attn_kernel: a workgroup (4 waves) takes one kv head, QV = 4 query vectors
-// of that head's group (query vector u = token u / rep, head kh*rep + u % rep)
-// and one chunk of the keys. 16 lanes own a key at a time (lane i holds
-// elements E*i .. E*i+E-1 of the head dimension), so a wave walks 4 keys per
-// step and each K / V element is loaded once for the 4 queries. Each lane
-// group keeps an online softmax (running max m, sum l, accumulator) per
-// query; the 16 groups of the workgroup are merged through LDS at the end,
-// and with several key chunks (decode: one query, many keys) the chunks'
-// (m, l, acc) are merged by attn_combine_kernel. K / V are read in the
-// cache's format (fp32, or int8 / int4 with one fp32 scale per vector) and
-// dequantised in registers exactly as the reference's read_vec.
+// Two attention kernels share one plan. Keys are split into chunks when the
+// query tiles alone do not fill the chip (decode: one query, many keys); each
+// chunk's (max m, sum l, accumulator) is merged by attn_combine_kernel.
+//  * attn_mfma_kernel (head_dim == value_dim in {64, 128}): scores and the
+//    value sum on the fp32 matrix cores, a wave per 16-key tile, the
+//    workgroup's four waves sharing one 16-query tile.
+//  * attn_kernel (any other width up to 256): 16-lane groups own a key, the
+//    dot product is reduced with lane shuffles, four query vectors a
+//    workgroup.
+// K / V are read in the cache's format (fp32, or int8 / int4 with one fp32
+// scale per vector).
 //
 // Masking as the reference: key j (position kpos[j] or j) is kept for query
 // position qp when kp <= qp and, with window > 0, qp - kp < window; a query
 // with no kept key gives zeros. When kpos is absent, keys past the tile's
-// largest query position (or before its smallest window start) are skipped.
+// largest query position (or before its earliest window start) are skipped.
 //
 // Results differ from the reference's serial loops in summation order and in
 // the exp of the GPU's math library: <= 1e-5 relative to the output's scale.
@@ -42,14 +42,15 @@ struct AttnParams {
     const void* v;         // [n_kv, n_head_kv, value_dim] in kv_dt
     const float* v_scale;
     float* out;            // [n_q, n_head, value_dim]
-    float* part;           // [n_chunks, n_q * n_head, value_dim + 2] (several chunks)
+    float* part;           // several chunks: acc [n_chunks][n_q * n_head][value_dim],
+                           // then (m, l) [n_chunks][n_q * n_head][2]
     const int32_t* qpos;   // [n_q] or null (= t)
     const int32_t* kpos;   // [n_kv] or null (= j)
     int64_t n_q, n_head, n_head_kv, head_dim, value_dim, n_kv;
     int rep;               // n_head / n_head_kv
     int window;
     float scale;
-    int64_t chunk_len;     // keys per chunk (multiple of kKeysPerStep)
+    int64_t chunk_len;     // keys per chunk (a multiple of the kernel's keys per step)
     int n_chunks;
 };
 
@@ -213,35 +214,371 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_kernel(AttnParams p) {
         if constexpr (MERGE_OUT) {
             p.out[qrow[i] * p.value_dim + d] = at / fmaxf(lt, 1e-30f);
         } else {
-            float* pr = p.part + ((int64_t)chunk * p.n_q * p.n_head + qrow[i]) * (p.value_dim + 2);
-            pr[2 + d] = at;
+            const int64_t pi = (int64_t)chunk * p.n_q * p.n_head + qrow[i];
+            p.part[pi * p.value_dim + d] = at;
             if (d == 0) {
-                pr[0] = mt;
-                pr[1] = lt;
+                float* ml = p.part + (int64_t)p.n_chunks * p.n_q * p.n_head * p.value_dim + 2 * pi;
+                ml[0] = mt;
+                ml[1] = lt;
             }
         }
     }
 }
 
-// Merge the chunks' (m, l, acc) of every (token, head): one thread per
-// output element.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
-    const int64_t rows = p.n_q * p.n_head;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= rows * p.value_dim) return;
-    const int64_t row = idx / p.value_dim, d = idx % p.value_dim;
-    const int64_t cstride = rows * (p.value_dim + 2);
-    const float* base = p.part + row * (p.value_dim + 2);
-    float mt = -INFINITY;
-    for (int c = 0; c < p.n_chunks; ++c) mt = fmaxf(mt, base[c * cstride]);
-    float lt = 0.0f, at = 0.0f;
-    for (int c = 0; c < p.n_chunks; ++c) {
-        const float mc = base[c * cstride];
-        const float wg = (mc == -INFINITY) ? 0.0f : expf(mc - mt);
-        lt = __builtin_fmaf(base[c * cstride + 1], wg, lt);
-        at = __builtin_fmaf(base[c * cstride + 2 + d], wg, at);
+// ------------------------------------------------------------ MFMA path
+// Scores and the value sum on the fp32 matrix cores. v_mfma_f32_16x16x4f32:
+// lane l (g = l / 16, c = l % 16) supplies A[c][g] and B[g][c] and receives
+// D[4g + r][c], r = 0..3. A wave owns a tile of 16 query vectors (column c =
+// query vector) and walks the keys 16 at a time:
+//  * S^T = K . Q^T with A = K (row = key c) and B = Q^T. The head dimension is
+//    permuted (a dot product does not depend on the order of its terms): lane
+//    group g owns D/4 elements of key c and of query c, taken as 16-byte
+//    pieces that interleave with the other groups' (kdim), so the four
+//    groups' loads of one key are adjacent.
+//  * Lane l then holds the scores of query c against keys 4g + r, which is
+//    the A operand of O += P . V when the value step r takes keys
+//    {4g + r : g = 0..3}. B = V[key 4g + r][...]: lane c of the group owns
+//    DV/16 value elements, 16-byte pieces interleaved across the 16 lanes
+//    (vdim), so a row's loads are contiguous.
+//  * Output tile t, lane l: O[query 4g + r][vdim(c, t)].
+// Integer caches multiply the integer codes (exact in fp32); the key scale
+// multiplies the score and the value scale the probability.
+//
+// The four waves of a workgroup share one query tile and take every fourth
+// key tile of the chunk (balanced under a causal mask); their (m, l, acc) are
+// merged through LDS. Workgroups run the last query tiles (in causal prefill
+// the longest) first.
+template <int DT>
+constexpr int kv_bits() { return DT == 0 ? 32 : (DT == 1 ? 8 : 4); }
+
+// Loaded in place of an absent position array: the loads of positions stay
+// unconditional (a load under a branch makes the compiler wait for every
+// load in flight where the branches join) and the value is selected after.
+__device__ int32_t g_no_position = 0;
+
+__device__ __forceinline__ int32_t position_or(const int32_t* pos, int64_t i, int64_t dflt) {
+    const int32_t* a = pos ? pos + i : &g_no_position;
+    const int32_t v = *a;
+    return pos ? v : (int32_t)dflt;
+}
+
+// N bytes (4-byte multiple, or 2) at p into words.
+template <int N>
+__device__ __forceinline__ void load_words(const uint8_t* p, uint32_t* w) {
+    if constexpr (N % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 16; ++i) {
+            const uint4 x = *reinterpret_cast<const uint4*>(p + 16 * i);
+            w[4 * i] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
+        }
+    } else if constexpr (N % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) {
+            const uint2 x = *reinterpret_cast<const uint2*>(p + 8 * i);
+            w[2 * i] = x.x; w[2 * i + 1] = x.y;
+        }
+    } else if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) w[i] = reinterpret_cast<const uint32_t*>(p)[i];
+    } else {
+        static_assert(N == 2, "slice size");
+        w[0] = *reinterpret_cast<const uint16_t*>(p);
     }
-    p.out[row * p.value_dim + d] = at / fmaxf(lt, 1e-30f);
+}
+
+// element e of a slice held as words: fp32 bits, int8 or int4 (low nibble first)
+template <int DT>
+__device__ __forceinline__ float slice_elem(const uint32_t* w, int e) {
+    if constexpr (DT == 0) {
+        return __uint_as_float(w[e]);
+    } else if constexpr (DT == 1) {
+        return (float)((int32_t)(w[e >> 2] << (24 - 8 * (e & 3))) >> 24);
+    } else {
+        return (float)((int32_t)(w[e >> 3] << (28 - 4 * (e & 7))) >> 28);
+    }
+}
+
+template <int DT, int D, int DV>
+struct KvTile {
+    static constexpr int KS = D / 4, VS = DV / 16;
+    static constexpr int KB = KS * kv_bits<DT>() / 8, VB = VS * kv_bits<DT>() / 8;
+    static constexpr int KW = (KB + 3) / 4, VW = (VB + 3) / 4;
+    // bytes and elements per load, loads per lane
+    static constexpr int KLB = KB < 16 ? KB : 16, KLE = KLB * 8 / kv_bits<DT>(), KNI = KB / KLB;
+    static constexpr int VLB = VB < 16 ? VB : 16, VLE = VLB * 8 / kv_bits<DT>(), VNI = VB / VLB;
+    // head-dimension index of element j of lane group g's key / query slice
+    static __device__ __forceinline__ int kdim(int g, int j) {
+        return (j / KLE) * (4 * KLE) + g * KLE + j % KLE;
+    }
+    // value index of element t of lane c's value slice (and output column)
+    static __device__ __forceinline__ int vdim(int c, int t) {
+        return (t / VLE) * (16 * VLE) + c * VLE + t % VLE;
+    }
+    uint32_t k[KW];
+    uint32_t v[4][VW];
+    // scales (integer caches) and position of key c; lanes 4g + r hand them
+    // to the lanes that need key 4g + r
+    float ks, vs;
+    int32_t kp;
+
+    // keys kb .. kb + 15, clamped to < j1 for the loads
+    __device__ __forceinline__ void load(const AttnParams& p, int64_t kb, int64_t j1, int g,
+                                         int c, int kh) {
+        const int64_t hk = p.n_head_kv;
+        constexpr int64_t KVEC = (int64_t)D * kv_bits<DT>() / 8;
+        constexpr int64_t VVEC = (int64_t)DV * kv_bits<DT>() / 8;
+        const int64_t kk = min(kb + c, j1 - 1);
+        const uint8_t* kr = static_cast<const uint8_t*>(p.k) + (kk * hk + kh) * KVEC;
+#pragma unroll
+        for (int i = 0; i < KNI; ++i) load_words<KLB>(kr + (4 * i + g) * KLB, k + i * KLB / 4);
+        if constexpr (DT != 0) {
+            ks = p.k_scale[kk * hk + kh];
+            vs = p.v_scale[kk * hk + kh];
+        }
+        kp = position_or(p.kpos, kk, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t kv = min(kb + 4 * g + r, j1 - 1);
+            const uint8_t* vr = static_cast<const uint8_t*>(p.v) + (kv * hk + kh) * VVEC;
+#pragma unroll
+            for (int i = 0; i < VNI; ++i)
+                load_words<VLB>(vr + (16 * i + c) * VLB, v[r] + i * VLB / 4);
+        }
+    }
+};
+
+template <int DT, int D, int DV, bool MERGE_OUT>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams p) {
+    using Tile = KvTile<DT, D, DV>;
+    constexpr int KS = Tile::KS, VS = Tile::VS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int chunk = blockIdx.x, kh = blockIdx.y;
+    const int64_t n_vec = p.n_q * p.rep;
+    const int64_t tile = (int64_t)(gridDim.z - 1 - blockIdx.z);
+    constexpr int64_t istep = 4;
+
+    // this chunk's keys (every load stays below c1); the wave's first key
+    // tile is issued before the query positions, which may narrow the range,
+    // arrive: one memory round trip instead of two
+    const int64_t c0 = (int64_t)chunk * p.chunk_len;
+    const int64_t c1 = min(c0 + p.chunk_len, p.n_kv);
+    const int64_t tiles_c = (c1 - c0 + 15) / 16;
+    const int64_t i_spec = wave;
+    // integer caches: the next tile is loaded while this one is used (two
+    // tiles of int8 / int4 fit in the registers one fp32 tile takes)
+    constexpr bool PF = DT != 0;
+    Tile tl, nx;
+    tl.load(p, c0 + 16 * min(i_spec, tiles_c - 1), c1, g, c, kh);
+
+    // query vector of column c: token t, head kh * rep + u % rep
+    const int64_t u = tile * 16 + c;
+    const bool qok = u < n_vec;
+    const int64_t uc = qok ? u : n_vec - 1;
+    const int64_t tq = uc / p.rep;
+    const int64_t qrow = tq * p.n_head + (int64_t)kh * p.rep + uc % p.rep;
+    const int64_t qp = position_or(p.qpos, tq, tq);
+    float qs[KS];
+    {
+        const float* src = p.q + qrow * D;
+#pragma unroll
+        for (int e = 0; e < KS; e += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(src + Tile::kdim(g, e));
+            qs[e] = qok ? f.x : 0.0f;
+            qs[e + 1] = qok ? f.y : 0.0f;
+            qs[e + 2] = qok ? f.z : 0.0f;
+            qs[e + 3] = qok ? f.w : 0.0f;
+        }
+    }
+    int64_t qmin = qp, qmax = qp;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+        qmin = min(qmin, (int64_t)__shfl_xor(qmin, off, 16));
+        qmax = max(qmax, (int64_t)__shfl_xor(qmax, off, 16));
+    }
+
+    // key tiles [i_lo, i_hi) of the chunk can hold kept keys: without key
+    // positions, none past the tile's last query position or before its
+    // earliest window
+    int64_t i_lo = 0, i_hi = tile * 16 < n_vec ? tiles_c : 0;
+    if (p.kpos == nullptr) {
+        i_hi = min(i_hi, max<int64_t>(0, (qmax + 1 - c0 + 15) / 16));
+        if (p.window > 0) i_lo = max<int64_t>(0, (qmin - p.window + 1 - c0) / 16);
+    }
+    int64_t i = i_lo + (((wave - i_lo) % 4) + 4) % 4;
+    if (i != i_spec && i < i_hi) tl.load(p, c0 + 16 * i, c1, g, c, kh);
+
+    float m = -INFINITY, ls = 0.0f;
+    v4f acc[VS];
+#pragma unroll
+    for (int t = 0; t < VS; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    while (i < i_hi) {
+        const int64_t kb = c0 + 16 * i;
+        // (clamped to the chunk's last tile: in bounds, and no branch for the
+        // wait counters to merge)
+        if constexpr (PF) nx.load(p, c0 + 16 * min(i + istep, tiles_c - 1), c1, g, c, kh);
+        v4f s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KS; j += 2) {
+            s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(slice_elem<DT>(tl.k, j), qs[j], s0, 0,
+                                                      0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(slice_elem<DT>(tl.k, j + 1), qs[j + 1],
+                                                      s1, 0, 0, 0);
+        }
+        float sc[4];
+        float tm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t kj = kb + 4 * g + r;
+            const int64_t kp = p.kpos ? (int64_t)__shfl(tl.kp, 4 * g + r) : kj;
+            const bool keep = qok && kj < c1 && key_kept(kp, qp, p.window);
+            float y = (s0[r] + s1[r]);
+            if constexpr (DT != 0) y *= __shfl(tl.ks, 4 * g + r);
+            sc[r] = keep ? y * p.scale : -INFINITY;
+            tm = fmaxf(tm, sc[r]);
+        }
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float mn = fmaxf(m, tm);
+        const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
+        float pr[4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pr[r] = (sc[r] == -INFINITY) ? 0.0f : expf(sc[r] - mn);
+            psum += pr[r];
+            if constexpr (DT != 0) pr[r] *= __shfl(tl.vs, 4 * g + r);
+        }
+        ls = ls * alpha + psum;
+        m = mn;
+        // rescale the rows of query 4g + r by that query's alpha (lane 4g + r)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * g + r);
+#pragma unroll
+            for (int t = 0; t < VS; ++t) acc[t][r] *= ar;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < VS; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    pr[r], slice_elem<DT>(tl.v[r], t), acc[t], 0, 0, 0);
+        i += istep;
+        if (i >= i_hi) break;
+        if constexpr (PF)
+            tl = nx;
+        else
+            tl.load(p, c0 + 16 * i, c1, g, c, kh);
+    }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+
+    // merge the four waves: query vector qi of the tile, element d
+    __shared__ float sm[4][16], sl[4][16];
+    __shared__ float sacc[4][16][DV + 4];
+    if (g == 0) {
+        sm[wave][c] = m;
+        sl[wave][c] = ls;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < VS; ++t) sacc[wave][4 * g + r][Tile::vdim(c, t)] = acc[t][r];
+    __syncthreads();
+    const int64_t rows = p.n_q * p.n_head;
+    for (int w = threadIdx.x; w < 16 * DV; w += 256) {
+        const int qi = w / DV, d = w % DV;
+        const int64_t uq = tile * 16 + qi;
+        if (uq >= n_vec) break;  // w only grows
+        float mt = -INFINITY;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) mt = fmaxf(mt, sm[x][qi]);
+        float lt = 0.0f, at = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const float wg = (sm[x][qi] == -INFINITY) ? 0.0f : expf(sm[x][qi] - mt);
+            lt = __builtin_fmaf(sl[x][qi], wg, lt);
+            at = __builtin_fmaf(sacc[x][qi][d], wg, at);
+        }
+        const int64_t row = (uq / p.rep) * p.n_head + (int64_t)kh * p.rep + uq % p.rep;
+        if constexpr (MERGE_OUT) {
+            p.out[row * DV + d] = at / fmaxf(lt, 1e-30f);
+        } else {
+            const int64_t pi = (int64_t)chunk * rows + row;
+            p.part[pi * DV + d] = at;
+            if (d == 0) {
+                float* ml = p.part + (int64_t)p.n_chunks * rows * DV + 2 * pi;
+                ml[0] = mt;
+                ml[1] = lt;
+            }
+        }
+    }
+}
+
+// Merge the chunks' (m, l, acc) of one (token, head) row per workgroup. Thread
+// (part q, element d) loads (m, l, acc[d]) of chunks q, q + P, ... all at once
+// (clamped indices, no branch between the loads), merges them in registers,
+// and the parts are merged through LDS: one memory round trip.
+constexpr int kMaxChunks = 1024;
+constexpr int kCombineBatch = 16;
+__global__ __launch_bounds__(512) void attn_combine_kernel(AttnParams p) {
+    __shared__ float sm[512], sl[512], sa[512];
+    const int tid = threadIdx.x;
+    const int64_t rows = p.n_q * p.n_head;
+    const int64_t row = blockIdx.x;
+    const int64_t DV = p.value_dim;
+    const int nc = p.n_chunks;
+    const int P = (int)max<int64_t>(1, 512 / DV);
+    const float* ml = p.part + (int64_t)nc * rows * DV;
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    if (tid < P * DV) {
+        const int64_t d = tid % DV;
+        const int q = tid / (int)DV;
+        for (int c0 = q; c0 < nc; c0 += kCombineBatch * P) {
+            float mc[kCombineBatch], lc[kCombineBatch], ac[kCombineBatch];
+#pragma unroll
+            for (int i = 0; i < kCombineBatch; ++i) {
+                const int c = min(c0 + i * P, nc - 1);
+                const int64_t pi = (int64_t)c * rows + row;
+                mc[i] = ml[2 * pi];
+                lc[i] = ml[2 * pi + 1];
+                ac[i] = p.part[pi * DV + d];
+            }
+            float mb = M;
+#pragma unroll
+            for (int i = 0; i < kCombineBatch; ++i)
+                if (c0 + i * P < nc) mb = fmaxf(mb, mc[i]);
+            const float sc = (M == -INFINITY) ? 0.0f : expf(M - mb);
+            L *= sc;
+            A *= sc;
+#pragma unroll
+            for (int i = 0; i < kCombineBatch; ++i) {
+                const bool ok = c0 + i * P < nc && mc[i] != -INFINITY;
+                const float w = ok ? expf(mc[i] - mb) : 0.0f;
+                L = __builtin_fmaf(lc[i], w, L);
+                A = __builtin_fmaf(ac[i], w, A);
+            }
+            M = mb;
+        }
+    }
+    sm[tid] = M;
+    sl[tid] = L;
+    sa[tid] = A;
+    __syncthreads();
+    for (int64_t d = tid; d < DV; d += 512) {
+        float mt = -INFINITY;
+        for (int q = 0; q < P; ++q) mt = fmaxf(mt, sm[q * DV + d]);
+        float lt = 0.0f, at = 0.0f;
+        for (int q = 0; q < P; ++q) {
+            const float mq = sm[q * DV + d];
+            const float w = (mq == -INFINITY) ? 0.0f : expf(mq - mt);
+            lt = __builtin_fmaf(sl[q * DV + d], w, lt);
+            at = __builtin_fmaf(sa[q * DV + d], w, at);
+        }
+        p.out[row * DV + d] = at / fmaxf(lt, 1e-30f);
+    }
 }
 
 using AttnKernel = void (*)(AttnParams);
@@ -265,27 +602,66 @@ AttnKernel pick_attn(int dt, int E, bool merge_out) {
     }
 }
 
+template <int DT, int D>
+AttnKernel pick_mfma_d(bool merge_out) {
+    return merge_out ? attn_mfma_kernel<DT, D, D, true> : attn_mfma_kernel<DT, D, D, false>;
+}
+
+template <int DT>
+AttnKernel pick_mfma_dt(int D, bool merge_out) {
+    switch (D) {
+    case 64: return pick_mfma_d<DT, 64>(merge_out);
+    case 128: return pick_mfma_d<DT, 128>(merge_out);
+    default: return nullptr;
+    }
+}
+
+AttnKernel pick_mfma(int dt, int D, bool merge_out) {
+    switch (dt) {
+    case 0: return pick_mfma_dt<0>(D, merge_out);
+    case 1: return pick_mfma_dt<1>(D, merge_out);
+    case 2: return pick_mfma_dt<2>(D, merge_out);
+    default: return nullptr;
+    }
+}
+
 struct AttnPlan {
-    int E;
-    int64_t q_tiles, chunk_len;
+    bool mfma;
+    int E;                 // VALU kernel: elements per lane
+    int64_t grid_z;        // query tiles (4 vectors: VALU kernel, 16: MFMA kernel)
+    int64_t chunk_len;
     int n_chunks;
 };
 
+// The matrix-core kernel takes head_dim == value_dim in {64, 128} with
+// 16-byte aligned operands; other shapes take the vector kernel.
 bool attn_plan(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
-               int64_t value_dim, int64_t n_kv, AttnPlan& pl) {
+               int64_t value_dim, int64_t n_kv, bool aligned, AttnPlan& pl) {
     const int64_t width = std::max(head_dim, value_dim);
     pl.E = width <= 64 ? 4 : (width <= 128 ? 8 : (width <= 256 ? 16 : 0));
     if (pl.E == 0) return false;
     const int64_t rep = n_head / n_head_kv;
-    pl.q_tiles = (n_q * rep + kQV - 1) / kQV;
-    // enough workgroups to fill the chip: split the keys when the query
-    // tiles alone do not (decode), chunks of at least 64 keys
-    const int64_t base = n_head_kv * pl.q_tiles;
-    const int64_t target = tune("attn_wgs", 1024);
+    const int64_t n_vec = n_q * rep;
+    pl.mfma = aligned && head_dim == value_dim && (head_dim == 64 || head_dim == 128) &&
+              tune("attn_mfma", 1) != 0;
+    int64_t step;  // keys a workgroup walks per step
+    if (pl.mfma) {
+        pl.grid_z = (n_vec + 15) / 16;
+        step = 64;
+    } else {
+        pl.grid_z = (n_vec + kQV - 1) / kQV;
+        step = kKeysPerStep;
+    }
+    // enough workgroups to fill the chip: split the keys when the query tiles
+    // alone do not (decode), at least min_chunk keys a chunk
+    const int64_t base = n_head_kv * pl.grid_z;
+    const int64_t target = tune("attn_wgs", 512);
+    const int64_t min_chunk = std::max<int64_t>(step, tune("attn_min_chunk", 64));
     int64_t nc = std::max<int64_t>(1, (target + base - 1) / base);
-    nc = std::min<int64_t>(nc, std::max<int64_t>(1, (n_kv + 63) / 64));
+    nc = std::min<int64_t>(nc, std::max<int64_t>(1, (n_kv + min_chunk - 1) / min_chunk));
+    nc = std::min<int64_t>(nc, kMaxChunks);
     int64_t cl = (n_kv + nc - 1) / nc;
-    cl = (cl + kKeysPerStep - 1) / kKeysPerStep * kKeysPerStep;
+    cl = (cl + step - 1) / step * step;
     pl.chunk_len = cl;
     pl.n_chunks = (int)((n_kv + cl - 1) / cl);
     return true;
@@ -371,9 +747,13 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* x, float
 int64_t attn_workspace_bytes(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
                              int64_t value_dim, int64_t n_kv) {
     AttnPlan pl;
+    // the size for the vector kernel bounds the matrix-core kernel's
     if (n_q <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || n_kv <= 0 ||
-        !attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, pl))
+        !attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, true, pl))
         return 0;
+    AttnPlan pv;
+    attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, false, pv);
+    if (pv.n_chunks > pl.n_chunks) pl = pv;
     if (pl.n_chunks <= 1) return 0;
     return (int64_t)pl.n_chunks * n_q * n_head * (value_dim + 2) * 4;
 }
@@ -402,7 +782,9 @@ bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scal
         return false;
     }
     AttnPlan pl;
-    if (!attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, pl)) {
+    const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
+                         aligned16(workspace);
+    if (!attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, aligned, pl)) {
         set_error("attention: head_dim/value_dim %lld/%lld above 256", (long long)head_dim,
                   (long long)value_dim);
         return false;
@@ -414,24 +796,23 @@ bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scal
                   (long long)need);
         return false;
     }
-    if (pl.q_tiles > 65535 || n_head_kv > 65535) {
+    if (pl.grid_z > 65535 || n_head_kv > 65535 || n_q * n_head > 0x7fffffff) {
         set_error("attention: grid too large");
         return false;
     }
     AttnParams p{q, k, k_scale, v, v_scale, out, static_cast<float*>(workspace), qpos, kpos,
                  n_q, n_head, n_head_kv, head_dim, value_dim, n_kv,
                  (int)(n_head / n_head_kv), window, scale, pl.chunk_len, pl.n_chunks};
-    AttnKernel kern = pick_attn(kv_dt, pl.E, pl.n_chunks == 1);
-    if (!launch("attn_kernel", kern, dim3((unsigned)pl.n_chunks, (unsigned)n_head_kv,
-                                          (unsigned)pl.q_tiles),
+    const bool one = pl.n_chunks == 1;
+    AttnKernel kern = pl.mfma ? pick_mfma(kv_dt, (int)head_dim, one)
+                              : pick_attn(kv_dt, pl.E, one);
+    if (!launch(pl.mfma ? "attn_mfma_kernel" : "attn_kernel", kern,
+                dim3((unsigned)pl.n_chunks, (unsigned)n_head_kv, (unsigned)pl.grid_z),
                 dim3(64 * kAttnWaves), 0, s, p))
         return false;
-    if (pl.n_chunks > 1) {
-        const int64_t n = n_q * n_head * value_dim;
-        if (!launch("attn_combine_kernel", attn_combine_kernel, dim3((unsigned)((n + 255) / 256)),
-                    dim3(256), 0, s, p))
-            return false;
-    }
+    if (!one && !launch("attn_combine_kernel", attn_combine_kernel,
+                        dim3((unsigned)(n_q * n_head)), dim3(512), 0, s, p))
+        return false;
     return true;
 }
 

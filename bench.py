@@ -30,6 +30,8 @@ single-threaded like the reference, over a bounded sample.
     python bench.py --all-shapes --only OP   # one op over every layer shape
     python bench.py --variants          # every op variant at the 512-token shape
     python bench.py --gemv              # quantised GEMV (decode projections)
+    python bench.py --gemm              # quantised GEMM (prefill projections)
+    python bench.py --attention         # attention over a KV cache (decode, prefill)
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
 """
@@ -69,6 +71,8 @@ def parse_args(argv=None):
     p.add_argument("--variants", action="store_true",
                    help="every op variant at the Llama-3-8B 512-token geometry")
     p.add_argument("--gemv", action="store_true", help="quantised GEMV cases")
+    p.add_argument("--attention", action="store_true",
+                   help="attention over a KV cache (decode and causal prefill)")
     p.add_argument("--gemm", action="store_true",
                    help="quantised GEMM cases (prefill token counts)")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
@@ -498,6 +502,8 @@ def main(argv=None):
         return gemv(a)
     if a.gemm:
         return gemm(a)
+    if a.attention:
+        return attention_bench(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -732,6 +738,124 @@ def gemm(a):
         print(json.dumps(res), flush=True)
         stream.destroy()
         del ws
+    return 0
+
+
+ATTN_CASES = [
+    # (name, query tokens, cached keys, KV type 0 fp32 / 1 int8 / 2 int4) at
+    # Llama-3-8B heads: 32 query heads, 8 kv heads, head_dim 128
+    ("decode_s4096_f32", 1, 4096, 0), ("decode_s4096_int8", 1, 4096, 1),
+    ("decode_s4096_int4", 1, 4096, 2), ("decode_s16384_f32", 1, 16384, 0),
+    ("decode_s32768_int8", 1, 32768, 1), ("prefill_t512_causal_f32", 512, 512, 0),
+]
+
+
+def cpu_attention_us(T, S, H, HK, D, seconds):
+    """The reference's attention_tiled (oracle/_ref, src/transformer.cpp:120-203)
+    or else the oracle's, one thread, on the same shape over an fp32 cache."""
+    from oracle import cpuref, refbind
+
+    use_ref = refbind.available()
+    at = refbind.attention_tiled if use_ref else cpuref.attention_tiled
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    k = rng.standard_normal((S, HK, D)).astype(np.float32)
+    v = rng.standard_normal((S, HK, D)).astype(np.float32)
+    qpos = np.arange(S - T, S, dtype=np.int32)
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < seconds:
+        at(q, k, v, 1.0 / np.sqrt(D), qpos=qpos)
+        reps += 1
+    us = (time.perf_counter() - t0) / reps * 1e6
+    return us, "reference" if use_ref else "port", f"the full call, {reps} repeats, one thread"
+
+
+def attention_bench(a):
+    """Attention over a KV cache: mean time per call (a recorded plan of calls
+    over rotating caches of > 1 GiB together, one event pair around the
+    replays), per-kernel dispatch times (an event pair per kernel), algorithmic
+    bytes (K, V and their scales read once, q and out) and, for prefill, flops."""
+    from aero_amd import ops
+    from aero_amd.device import DeviceArray as DA, Event, Plan, Stream
+
+    H, HK, D = 32, 8, 128
+    rng = np.random.default_rng(0)
+    names = a.shapes.split(",") if a.shapes else [c[0] for c in ATTN_CASES]
+    for name, T, S, dt in ATTN_CASES:
+        if name not in names:
+            continue
+        vb = ops.kv_vec_bytes(dt, D)
+        kv_bytes = 2 * S * HK * (vb + (4 if dt else 0))
+        n_sets = min(64, max(2, -(-SUSTAINED_ROTATION // kv_bytes)))
+        src = DA.from_numpy(rng.standard_normal((S, HK, D)).astype(np.float32))
+        sets = []
+        for _ in range(n_sets):
+            if dt == 0:
+                sets.append((src.clone(), src.clone(), None, None))
+            else:
+                side = []
+                for _s in range(2):
+                    qb, sc = DA.empty(S * HK * vb, np.uint8), DA.empty(S * HK)
+                    ops.kv_write(dt, src, S, HK, D, qb, sc, 0, S)
+                    side.append((qb, sc))
+                sets.append((side[0][0], side[1][0], side[0][1], side[1][1]))
+        q = DA.from_numpy(rng.standard_normal((T, H, D)).astype(np.float32))
+        out = DA.empty((T, H, D))
+        qpos = DA.from_numpy(np.arange(S - T, S, dtype=np.int32))
+        scale = 1.0 / np.sqrt(D)
+        plan = Plan()
+        with plan:
+            for k, v, ks, vs in sets:
+                ops.attention(q, k, v, out, T, H, HK, D, D, S, scale, qpos=qpos, kv_dt=dt,
+                              k_scale=ks, v_scale=vs)
+        per_call = len(plan) // n_sets
+        stream = Stream()
+        plan.launch(stream)
+        e0, e1 = Event(), Event()
+        reps = max(2, SUSTAINED_REPS // 2)
+        e0.record(stream)
+        for _ in range(reps):
+            plan.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * n_sets)
+        starts = [Event() for _ in range(len(plan))]
+        stops = [Event() for _ in range(len(plan))]
+        ev = plan.event_arrays(starts, stops)
+        kern = [[] for _ in range(per_call)]
+        for _ in range(2):
+            plan.launch(stream, ev)
+            stream.synchronize()
+            for i, (x, y) in enumerate(zip(starts, stops)):
+                kern[i % per_call].append(x.elapsed_ms(y) * 1e3)
+        kus = [statistics.mean(x) for x in kern]
+        b = kv_bytes + 4 * T * H * 2 * D + 4 * T
+        pairs = sum(min(S, S - T + t + 1) for t in range(T))
+        flops = 2.0 * H * 2 * D * pairs
+        gbs = b / (kus[0] * 1e-6) / 1e9
+        res = {"case": name, "heads": [H, HK], "head_dim": D, "tokens": T, "keys": S,
+               "kv": ["f32", "int8", "int4"][dt], "bytes": b, "us_per_call": round(us, 3),
+               "GB/s_per_call": round(b / (us * 1e-6) / 1e9, 1),
+               "attn_kernel_us": round(kus[0], 3),
+               "roofline": {"bound": "hbm" if T == 1 else "mfma", "achieved": round(
+                   gbs if T == 1 else flops / (kus[0] * 1e-6) / 1e12, 2),
+                   "peak": HBM_PEAK_GBS if T == 1 else MFMA_FP32_PEAK_TFLOPS,
+                   "unit": "GB/s" if T == 1 else "TFLOP/s"}}
+        res["roofline"]["frac"] = round(res["roofline"]["achieved"] / res["roofline"]["peak"], 4)
+        if per_call > 1:
+            res["combine_kernel_us"] = round(kus[1], 3)
+        if T > 1:
+            res["flops"] = flops
+        if not a.no_cpu:
+            cu, kind, sample = cpu_attention_us(T, S, H, HK, D, a.cpu_seconds / len(names))
+            res["cpu_baseline"] = {"us": round(cu, 1), "kind": kind, "cores": 1,
+                                   "sample": sample + ("" if dt == 0 else
+                                                       "; fp32 cache, dequantisation not timed")}
+            res["speedup_vs_cpu"] = round(cu / us, 1)
+        print(json.dumps(res), flush=True)
+        plan.destroy()
+        stream.destroy()
+        del sets, src
     return 0
 
 

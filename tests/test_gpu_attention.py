@@ -71,6 +71,9 @@ def test_attention_golden(hip):
     (257, 8, 2, 128, 128, 257, 0),     # causal prefill
     (100, 6, 6, 80, 48, 130, 0),       # MHA, dims not a multiple of 16, value_dim < head_dim
     (33, 4, 1, 32, 32, 40, 7),         # MQA with a window
+    (200, 8, 2, 128, 128, 300, 50),    # prefill after a cached prefix, with a window
+    (3, 16, 4, 64, 64, 2500, 100),     # three tokens at once, head_dim 64, window
+    (1, 8, 8, 128, 128, 5000, 0),      # MHA decode
 ])
 def test_attention_vs_oracle(hip, oracle, T, H, HK, D, DV, S, window):
     rng = np.random.default_rng(T * 7 + H + S + D + window)
@@ -136,12 +139,12 @@ def test_kv_write_bit_exact_and_ring(hip, oracle, dt):
         assert np.array_equal(qb, wq) and np.float32(s1[0]) == np.float32(ws)
 
 
-@pytest.mark.parametrize("dt", [1, 2])
-def test_attention_over_quantised_cache(hip, oracle, dt):
+@pytest.mark.parametrize("dt,T,H,HK,D,S", [(1, 3, 32, 8, 128, 1500), (2, 3, 32, 8, 128, 1500),
+                                           (1, 40, 14, 2, 64, 700), (2, 1, 14, 2, 64, 3000)])
+def test_attention_over_quantised_cache(hip, oracle, dt, T, H, HK, D, S):
     """Attention reading an int8 / int4 cache equals the oracle's attention over
     the cache read back with the reference's aero_kv_read_vec."""
-    rng = np.random.default_rng(23 + dt)
-    T, H, HK, D, S = 3, 32, 8, 128, 1500
+    rng = np.random.default_rng(23 + dt + T)
     q, k, v = rand_qkv(rng, T, H, HK, D, D, S)
     vb = D if dt == 1 else D // 2
     kq, vq = DA.empty(S * HK * vb, np.uint8), DA.empty(S * HK * vb, np.uint8)
