@@ -74,6 +74,35 @@ PROTOTYPES = {
     "aero_hip_embed_gather": (c_int, [c_int, vp, c_int64, c_int64, c_int64, vp, c_int64,
                                       c_float, vp, vp, vp]),
     "aero_hip_dequant": (c_int, [c_int, vp, c_int64, vp, c_int64, vp]),
+    "aero_hip_tensor_rows": (c_int, [c_int, vp, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                     vp, vp]),
+    # GGUF reader
+    "aero_gguf_open": (vp, [ctypes.c_char_p]),
+    "aero_gguf_close": (None, [vp]),
+    "aero_gguf_file_size": (c_int64, [vp]),
+    "aero_gguf_version": (c_int, [vp]),
+    "aero_gguf_alignment": (c_int64, [vp]),
+    "aero_gguf_data_offset": (c_int64, [vp]),
+    "aero_gguf_arch": (ctypes.c_char_p, [vp]),
+    "aero_gguf_n_kv": (c_int64, [vp]),
+    "aero_gguf_kv_key": (ctypes.c_char_p, [vp, c_int64]),
+    "aero_gguf_kv_type": (c_int, [vp, ctypes.c_char_p]),
+    "aero_gguf_get_int": (c_int, [vp, ctypes.c_char_p, POINTER(c_int64)]),
+    "aero_gguf_get_float": (c_int, [vp, ctypes.c_char_p, POINTER(ctypes.c_double)]),
+    "aero_gguf_get_str": (vp, [vp, ctypes.c_char_p, POINTER(c_int64)]),
+    "aero_gguf_array_len": (c_int64, [vp, ctypes.c_char_p]),
+    "aero_gguf_array_ints": (c_int64, [vp, ctypes.c_char_p, POINTER(c_int64), c_int64]),
+    "aero_gguf_array_floats": (c_int64, [vp, ctypes.c_char_p, POINTER(ctypes.c_double),
+                                         c_int64]),
+    "aero_gguf_array_str": (vp, [vp, ctypes.c_char_p, c_int64, POINTER(c_int64)]),
+    "aero_gguf_kv_json": (vp, [vp, POINTER(c_int64)]),
+    "aero_gguf_n_tensors": (c_int64, [vp]),
+    "aero_gguf_tensor_name": (vp, [vp, c_int64]),
+    "aero_gguf_tensor_info": (c_int64, [vp, ctypes.c_char_p, POINTER(c_int), POINTER(c_int),
+                                        POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)]),
+    "aero_gguf_tensor_data": (vp, [vp, ctypes.c_char_p]),
+    "aero_gguf_read": (c_int, [vp, ctypes.c_char_p, c_int64, c_int64, vp]),
+    "aero_gguf_upload": (c_int, [vp, ctypes.c_char_p, c_int64, c_int64, vp, vp]),
     "aero_hip_matvec": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp]),
     "aero_hip_attention_workspace": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64,
                                                c_int64]),

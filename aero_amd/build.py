@@ -1,4 +1,4 @@
-"""Build libaero_hip.so (gfx950) in-tree from aero_amd/csrc/*.hip.
+"""Build libaero_hip.so (gfx950) in-tree from aero_amd/csrc/*.hip and *.cpp.
 
     python -m aero_amd.build          # or aero_amd.build.build()
 
@@ -40,11 +40,13 @@ CFLAGS = [
 
 
 def sources() -> list[str]:
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    """Device sources (.hip) and host-only sources (.cpp), all built by hipcc."""
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
+                  if f.endswith(".hip") or f.endswith(".cpp"))
 
 
 def _compile(src: str) -> tuple[str, str]:
-    obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
+    obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
     cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -53,7 +55,7 @@ def _compile(src: str) -> tuple[str, str]:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every .hip source for gfx950 and link libaero_hip.so. Always
+    """Compile every source for gfx950 and link libaero_hip.so. Always
     rebuilds. Returns the library path."""
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()

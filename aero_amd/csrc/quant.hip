@@ -268,9 +268,59 @@ bool embed_gather(int dtype, const uint8_t* table, int64_t table_bytes, int64_t 
     return run_gather(dtype, p, s);
 }
 
+// Rows [r0, r1) of a resident tensor of n_rows rows of n_per_row values
+// (whole blocks a row), dequantised to out [(r1 - r0) x n_per_row]: the row
+// addressing of engine/gguf.py:278-314 over HBM. Block types go through the
+// row gather (any row alignment: it loads the aligned words around a row),
+// F32 / F16 / BF16 through the element decode.
+bool tensor_rows_dev(int dtype, const uint8_t* table, int64_t table_bytes, int64_t n_rows,
+                     int64_t n_per_row, int64_t r0, int64_t r1, float* out, hipStream_t s) {
+    const bool known = dtype == AERO_DTYPE_F32 || dtype == AERO_DTYPE_F16 ||
+                       dtype == AERO_DTYPE_BF16 || is_block_quant(dtype);
+    if (!known) {
+        set_error("tensor_rows: dtype %d has no GPU dequantiser", dtype);
+        return false;
+    }
+    const int64_t bv = block_values(dtype), bb = block_bytes(dtype);
+    if (table == nullptr || out == nullptr || n_rows < 0 || n_per_row <= 0 ||
+        n_per_row % bv != 0) {
+        set_error("tensor_rows: bad arguments (n_rows=%lld n_per_row=%lld)", (long long)n_rows,
+                  (long long)n_per_row);
+        return false;
+    }
+    if (r0 < 0 || r1 < r0 || r1 > n_rows) {
+        set_error("tensor_rows: row range [%lld,%lld) outside [0,%lld)", (long long)r0,
+                  (long long)r1, (long long)n_rows);
+        return false;
+    }
+    const int64_t rb = (n_per_row / bv) * bb;
+    if (table_bytes < n_rows * rb) {
+        set_error("tensor_rows: table_bytes %lld < n_rows*row_bytes %lld",
+                  (long long)table_bytes, (long long)(n_rows * rb));
+        return false;
+    }
+    if ((reinterpret_cast<uintptr_t>(table) & 3u) || !aligned16(out)) {
+        set_error("tensor_rows: table must be 4-byte and out 16-byte aligned");
+        return false;
+    }
+    const int64_t n = r1 - r0;
+    if (n == 0) return true;
+    const uint8_t* first = table + r0 * rb;
+    if (!is_block_quant(dtype)) return dequant_dev(dtype, first, n * rb, out, n * n_per_row, s);
+    GatherParams p{first, nullptr, n, n, n_per_row / bv, rb, out, 0.0f, nullptr};
+    return run_gather(dtype, p, s);
+}
+
 }  // namespace aero
 
 extern "C" {
+
+int aero_hip_tensor_rows(int dtype, const uint8_t* table, int64_t table_bytes, int64_t n_rows,
+                         int64_t n_per_row, int64_t r0, int64_t r1, float* out, void* stream) {
+    aero::clear_error();
+    return aero::tensor_rows_dev(dtype, table, table_bytes, n_rows, n_per_row, r0, r1, out,
+                                 (hipStream_t)stream) ? 1 : 0;
+}
 
 int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
                           int64_t vocab, int64_t n_embd, const int32_t* ids,

@@ -232,6 +232,15 @@ int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
                           int64_t n_ids, float scale, float* out,
                           uint32_t* bad_count, void* stream);
 
+/* Rows [r0, r1) of a resident tensor (n_rows rows of n_per_row values, whole
+ * blocks a row, table 4-byte aligned) dequantised to out [(r1-r0) x
+ * n_per_row] (16-byte aligned): the device form of the row addressing of
+ * engine/gguf.py:278-314 (GGUFReader.tensor_rows). Types F32, F16, BF16,
+ * Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS; 0 with a reason for a range outside
+ * [0, n_rows) or a short table. */
+int aero_hip_tensor_rows(int dtype, const uint8_t* table, int64_t table_bytes, int64_t n_rows,
+                         int64_t n_per_row, int64_t r0, int64_t r1, float* out, void* stream);
+
 /* Whole-buffer dequant (the device form of aero_dequant_ref): floor(n/bv)
  * blocks of raw -> out. Types F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS. */
 int aero_hip_dequant(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
@@ -320,6 +329,67 @@ int     aero_hip_plan_destroy(void* plan);
  * aero_hip_* op records `start` when it begins and `stop` when it ends on the
  * device (hipExtLaunchKernel), then the arming is cleared. */
 int   aero_hip_time_next_kernel(void* start, void* stop);
+
+/* ---------------------------------------------------------------- GGUF
+ * A GGUF file parsed on the host (src/gguf.cpp:150-354, the reference's
+ * GgufReader; engine/gguf.py:166-233, GGUFReader._parse_index) and its tensors
+ * uploaded to HBM. The file is mapped read-only; header, metadata and tensor
+ * index are parsed with bounds checks. Handles are not thread-safe. */
+
+/* Open and parse (GgufReader::GgufReader, src/gguf.cpp:150-168). NULL with
+ * aero_hip_last_error() for a missing or unreadable file, bad magic, a
+ * version other than 2 or 3, a truncated header, metadata or index, an
+ * unknown metadata type, a general.alignment that is not a power of two,
+ * n_dims > 4, an element count that is not whole blocks, or tensor data past
+ * the end of the file (src/gguf.cpp:173-275). */
+void*       aero_gguf_open(const char* path);
+void        aero_gguf_close(void* h);                   /* GgufReader::~GgufReader */
+int64_t     aero_gguf_file_size(void* h);               /* GgufReader::file_size */
+int         aero_gguf_version(void* h);                 /* GGUFReader.version */
+int64_t     aero_gguf_alignment(void* h);               /* GGUFReader.alignment */
+int64_t     aero_gguf_data_offset(void* h);             /* GGUFReader.data_offset */
+const char* aero_gguf_arch(void* h);                    /* GgufReader::arch */
+
+/* Metadata in file order: n_kv keys; each value's GGUF type (0 u8 ... 12 f64,
+ * -1 absent). Lookups take a key verbatim or, as the reference's C++ reader,
+ * the part after its first dot unless the key starts with "tokenizer" or
+ * "general." (the first entry for a name wins; src/gguf.cpp:205-218). */
+int64_t     aero_gguf_n_kv(void* h);
+const char* aero_gguf_kv_key(void* h, int64_t i);
+int         aero_gguf_kv_type(void* h, const char* key);                  /* has :284 */
+int         aero_gguf_get_int(void* h, const char* key, int64_t* out);    /* get_int :286-294 */
+int         aero_gguf_get_float(void* h, const char* key, double* out);   /* get_float :296-304 */
+const char* aero_gguf_get_str(void* h, const char* key, int64_t* len);    /* get_str :306-310 */
+int64_t     aero_gguf_array_len(void* h, const char* key);
+int64_t     aero_gguf_array_ints(void* h, const char* key, int64_t* out, int64_t n);   /* get_int_array :312-316 */
+int64_t     aero_gguf_array_floats(void* h, const char* key, double* out, int64_t n);
+const char* aero_gguf_array_str(void* h, const char* key, int64_t i, int64_t* len); /* get_str_array :318-322 */
+/* Every metadata entry as JSON, [[key, type, value], ...] in file order (bytes
+ * >= 0x80 of strings as \u00XX, one code point per byte): the metadata dict of
+ * GGUFReader.kv (engine/gguf.py:186-198) in one call. Valid until close. */
+const char* aero_gguf_kv_json(void* h, int64_t* len);
+
+/* Tensor index (GgufReader::tensors / find, src/gguf.cpp:223-275,336-345): the
+ * tensor's ggml type, dims in GGUF order (fastest first, unused = 0), offset
+ * in the data section and size in bytes (-1 for a type whose block size is
+ * not known). Returns the tensor's index, -1 if absent. */
+int64_t     aero_gguf_n_tensors(void* h);
+const char* aero_gguf_tensor_name(void* h, int64_t i);
+int64_t     aero_gguf_tensor_info(void* h, const char* name, int* type, int* n_dims,
+                                  int64_t* dims, int64_t* offset, int64_t* nbytes);
+/* Host pointer to a tensor's bytes in the mapping (GgufReader::tensor_data,
+ * src/gguf.cpp:347-349). */
+const void* aero_gguf_tensor_data(void* h, const char* name);
+/* Copy bytes [byte0, byte0+nbytes) of a tensor to host memory
+ * (GGUFReader.tensor_bytes / _pread, engine/gguf.py:145-164,232-237). */
+int         aero_gguf_read(void* h, const char* name, int64_t byte0, int64_t nbytes, void* dst);
+/* Copy bytes [byte0, byte0+nbytes) of a tensor to device memory dst_dev on
+ * `stream`, read with pread into two pinned host buffers (allocated on the
+ * handle's first upload) overlapped with the host-to-device copies. Returns
+ * once the bytes are in HBM. No reference counterpart: the reference reads
+ * tensors into host memory only. */
+int         aero_gguf_upload(void* h, const char* name, int64_t byte0, int64_t nbytes,
+                             void* dst_dev, void* stream);
 
 #ifdef __cplusplus
 }

@@ -20,10 +20,12 @@ REF_DIR = os.path.join(HERE, "_ref")
 KERNELS = os.path.join(REF_DIR, "libref_kernels.so")
 TRANSFORMER = os.path.join(REF_DIR, "libref_transformer.so")
 KV = os.path.join(REF_DIR, "libref_kv.so")
+GGUF = os.path.join(REF_DIR, "libref_gguf.so")
 
 _k = None
 _t = None
 _v = None
+_g = None
 
 
 def kernels():
@@ -90,6 +92,32 @@ def kv():
         L.aero_kv_read_vec.restype = c_int
         _v = L
     return _v
+
+
+def gguf():
+    """The reference's GgufReader (src/gguf.cpp) through oracle/ref_gguf_shim.cpp."""
+    global _g
+    if _g is None and os.path.exists(GGUF):
+        L = ctypes.CDLL(GGUF)
+        vp, cp = ctypes.c_void_p, ctypes.c_char_p
+        for name, res, args in (
+                ("rg_open", vp, [cp, cp, c_int]), ("rg_close", None, [vp]),
+                ("rg_arch", cp, [vp]), ("rg_file_size", c_int64, [vp]),
+                ("rg_has", c_int, [vp, cp]), ("rg_get_int", c_int64, [vp, cp, c_int64]),
+                ("rg_get_float", ctypes.c_double, [vp, cp, ctypes.c_double]),
+                ("rg_get_str", c_int64, [vp, cp, cp, c_int64]),
+                ("rg_int_array", c_int64, [vp, cp, POINTER(c_int64), c_int64]),
+                ("rg_str_array_len", c_int64, [vp, cp]),
+                ("rg_str_array_item", c_int64, [vp, cp, c_int64, cp, c_int64]),
+                ("rg_n_tensors", c_int64, [vp]),
+                ("rg_tensor", c_int, [vp, cp, POINTER(c_int), POINTER(c_int), POINTER(c_int64),
+                                      POINTER(c_int64), POINTER(c_int64)]),
+                ("rg_tensor_data", vp, [vp, cp])):
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _g = L
+    return _g
 
 
 def available() -> bool:
