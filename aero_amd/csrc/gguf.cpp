@@ -15,9 +15,9 @@
 // u64 count and the elements. Scalars take their natural width (u16/i16 two
 // bytes, as the format and the reference's Python reader read them).
 //
-// Uploads read the file with pread into two pinned host buffers and copy each
-// to HBM asynchronously while the next one is read; the call returns once the
-// bytes are in HBM.
+// Uploads read the file with pread from four threads, each into two pinned
+// host buffers in turn, and queue each buffer's copy to HBM while the next
+// read runs; the call returns once the bytes are in HBM.
 #include "aero_hip.h"
 #include "common.hpp"
 
@@ -26,12 +26,15 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <atomic>
 #include <cerrno>
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -183,39 +186,55 @@ struct Tensor {
     int64_t nbytes = -1;        // -1: a type without a known block size
 };
 
-// Pinned staging for uploads, made on first use on the device current then.
+// Pinned staging for uploads, made on first use on the device current then:
+// kWorkers reader threads, each with two chunk buffers so a buffer's copy to
+// HBM overlaps the next read into the other.
 struct Staging {
-    static constexpr size_t kChunk = 16u << 20;
-    void* buf[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
-    bool used[2] = {false, false};
+    static constexpr size_t kChunk = 8u << 20;
+    static constexpr int kWorkers = 4;
+    struct Slot {
+        void* buf = nullptr;
+        hipEvent_t done = nullptr;
+        bool used = false;
+    };
+    Slot slot[kWorkers][2];
     int device = -1;
 
     bool ensure() {
         int dev = 0;
         if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return false;
-        if (buf[0] != nullptr && dev == device) return true;
+        if (slot[0][0].buf != nullptr && dev == device) return true;
         release();
-        for (int k = 0; k < 2; ++k) {
-            if (!hip_ok(hipHostMalloc(&buf[k], kChunk, hipHostMallocDefault), "hipHostMalloc") ||
-                !hip_ok(hipEventCreateWithFlags(&done[k], hipEventDisableTiming),
-                        "hipEventCreate")) {
-                release();
-                return false;
-            }
-        }
+        for (auto& w : slot)
+            for (auto& sl : w)
+                if (!hip_ok(hipHostMalloc(&sl.buf, kChunk, hipHostMallocDefault), "hipHostMalloc") ||
+                    !hip_ok(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming),
+                            "hipEventCreate")) {
+                    release();
+                    return false;
+                }
         device = dev;
         return true;
     }
+    // wait for every copy still reading from the buffers
+    bool drain() {
+        bool ok = true;
+        for (auto& w : slot)
+            for (auto& sl : w) {
+                if (sl.used && !hip_ok(hipEventSynchronize(sl.done), "hipEventSynchronize"))
+                    ok = false;
+                sl.used = false;
+            }
+        return ok;
+    }
     void release() {
-        for (int k = 0; k < 2; ++k) {
-            if (used[k] && done[k]) (void)hipEventSynchronize(done[k]);
-            if (done[k]) (void)hipEventDestroy(done[k]);
-            if (buf[k]) (void)hipHostFree(buf[k]);
-            buf[k] = nullptr;
-            done[k] = nullptr;
-            used[k] = false;
-        }
+        for (auto& w : slot)
+            for (auto& sl : w) {
+                if (sl.used && sl.done) (void)hipEventSynchronize(sl.done);
+                if (sl.done) (void)hipEventDestroy(sl.done);
+                if (sl.buf) (void)hipHostFree(sl.buf);
+                sl = Slot{};
+            }
         device = -1;
     }
 };
@@ -667,34 +686,64 @@ int aero_gguf_upload(void* h, const char* name, int64_t byte0, int64_t nbytes, v
         aero::set_error("gguf: null device destination");
         return 0;
     }
-    aero::Staging& st = f->staging_;
+    using aero::Staging;
+    Staging& st = f->staging_;
     if (!st.ensure()) return 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t file0 = f->data_offset + t->offset + byte0;
     uint8_t* dst = static_cast<uint8_t*>(dst_dev);
-    int64_t done = 0;
-    int k = 0;
-    while (done < nbytes) {
-        const size_t n = (size_t)std::min<int64_t>(aero::Staging::kChunk, nbytes - done);
-        // the buffer's previous copy must have left it before it is refilled
-        if (st.used[k] && !aero::hip_ok(hipEventSynchronize(st.done[k]), "hipEventSynchronize"))
-            return 0;
-        st.used[k] = false;
-        if (!aero::pread_all(f->fd(), st.buf[k], n, file0 + done)) return 0;
-        if (!aero::hip_ok(hipMemcpyAsync(dst + done, st.buf[k], n, hipMemcpyHostToDevice, s),
-                          "hipMemcpyAsync") ||
-            !aero::hip_ok(hipEventRecord(st.done[k], s), "hipEventRecord"))
-            return 0;
-        st.used[k] = true;
-        done += (int64_t)n;
-        k ^= 1;
+    const int64_t chunks = (nbytes + (int64_t)Staging::kChunk - 1) / (int64_t)Staging::kChunk;
+    const int nw = (int)std::min<int64_t>(Staging::kWorkers, chunks);
+    std::atomic<int64_t> next{0};
+    std::atomic<bool> ok{true};
+    std::mutex err_mu;
+    std::string err;
+    // worker w takes the next chunk index until none is left: read it into
+    // one of its two buffers (after that buffer's previous copy has left),
+    // queue the copy to HBM, record when the copy is done
+    auto work = [&](int w) {
+        const bool own_thread = nw > 1;
+        if (own_thread && !aero::hip_ok(hipSetDevice(st.device), "hipSetDevice")) ok = false;
+        int k = 0;
+        while (ok) {
+            const int64_t i = next.fetch_add(1);
+            if (i >= chunks) break;
+            Staging::Slot& sl = st.slot[w][k];
+            const int64_t off = i * (int64_t)Staging::kChunk;
+            const size_t n = (size_t)std::min<int64_t>(Staging::kChunk, nbytes - off);
+            bool good = !sl.used || aero::hip_ok(hipEventSynchronize(sl.done), "hipEventSynchronize");
+            sl.used = false;
+            good = good && aero::pread_all(f->fd(), sl.buf, n, file0 + off) &&
+                   aero::hip_ok(hipMemcpyAsync(dst + off, sl.buf, n, hipMemcpyHostToDevice, s),
+                                "hipMemcpyAsync") &&
+                   aero::hip_ok(hipEventRecord(sl.done, s), "hipEventRecord");
+            if (!good) {
+                ok = false;
+                break;
+            }
+            sl.used = true;
+            k ^= 1;
+        }
+        if (!ok && own_thread) {
+            // errors are per thread: hand this one to the caller's
+            std::lock_guard<std::mutex> g(err_mu);
+            if (err.empty()) err = aero_hip_last_error();
+        }
+    };
+    if (nw == 1) {
+        work(0);
+    } else {
+        std::vector<std::thread> threads;
+        threads.reserve((size_t)nw);
+        for (int w = 0; w < nw; ++w) threads.emplace_back(work, w);
+        for (auto& th : threads) th.join();
     }
-    for (int b = 0; b < 2; ++b) {
-        if (st.used[b] && !aero::hip_ok(hipEventSynchronize(st.done[b]), "hipEventSynchronize"))
-            return 0;
-        st.used[b] = false;
+    const bool drained = st.drain();
+    if (!ok) {
+        if (!err.empty()) aero::set_error("%s", err.c_str());
+        return 0;
     }
-    return 1;
+    return drained ? 1 : 0;
 }
 
 }  // extern "C"

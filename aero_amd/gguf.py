@@ -20,8 +20,9 @@ from __future__ import annotations
 
 import ctypes
 import json
+import struct
 from dataclasses import dataclass
-from typing import Any, Dict, Tuple
+from typing import Any, Dict, List, Tuple
 
 import numpy as np
 
@@ -50,6 +51,12 @@ TYPE_NAMES: Dict[int, str] = {
     T_Q5_0: "Q5_0", T_Q5_1: "Q5_1", T_Q8_0: "Q8_0",
     T_Q4_K: "Q4_K", T_Q5_K: "Q5_K", T_Q6_K: "Q6_K", T_IQ4_XS: "IQ4_XS",
     T_BF16: "BF16",
+}
+
+_SCALAR_FMT = {
+    GGUF_UINT8: "<B", GGUF_INT8: "<b", GGUF_UINT16: "<H", GGUF_INT16: "<h",
+    GGUF_UINT32: "<I", GGUF_INT32: "<i", GGUF_FLOAT32: "<f", GGUF_BOOL: "<?",
+    GGUF_UINT64: "<Q", GGUF_INT64: "<q", GGUF_FLOAT64: "<d",
 }
 
 # types the GPU dequantises (aero_hip_dequant / aero_hip_tensor_rows), and
@@ -373,3 +380,81 @@ class GGUFReader:
         """y = W @ x on the GPU (engine/gguf.py:387-417). Returns (y, bytes of W)."""
         Y, nb = self.matmul(name, np.asarray(x, dtype=np.float32)[None, :])
         return Y[0], nb
+
+
+class GGUFWriter:
+    """Writes a GGUF file (the interface of engine/gguf.py:448-526): version 3,
+    the metadata in the order added, the tensor index, each tensor's bytes at a
+    multiple of the alignment in the data section, the file padded to it."""
+
+    def __init__(self, arch: str, alignment: int = DEFAULT_ALIGNMENT) -> None:
+        if alignment <= 0 or alignment & (alignment - 1):
+            raise ValueError(f"bad alignment {alignment} (must be a power of two)")
+        self.arch = arch
+        self.alignment = alignment
+        self.kv: List[Tuple[str, int, Any]] = [
+            ("general.architecture", GGUF_STRING, arch),
+            ("general.alignment", GGUF_UINT32, alignment),
+        ]
+        self.tensors: List[Tuple[str, Tuple[int, ...], int, bytes]] = []
+
+    def add_kv(self, key: str, type_id: int, value: Any) -> None:
+        """value: a scalar, a str, or (element type, items) for an array."""
+        self.kv.append((key, type_id, value))
+
+    def add_scalar(self, key: str, value: Any) -> None:
+        self.add_kv(key, GGUF_UINT32 if isinstance(value, int) else GGUF_FLOAT32, value)
+
+    def add_tensor(self, name: str, shape: Tuple[int, ...], raw: bytes, type_id: int) -> None:
+        """`shape` is row-major; GGUF stores it reversed (fastest first)."""
+        self.tensors.append((name, tuple(reversed(shape)), type_id, bytes(raw)))
+
+    @staticmethod
+    def _str(s) -> bytes:
+        b = s.encode("utf-8") if isinstance(s, str) else bytes(s)
+        return struct.pack("<Q", len(b)) + b
+
+    @classmethod
+    def _value(cls, t: int, v: Any, out: List[bytes]) -> None:
+        if t == GGUF_STRING:
+            out.append(cls._str(v))
+        elif t == GGUF_ARRAY:
+            et, items = v
+            out.append(struct.pack("<IQ", et, len(items)))
+            fmt = _SCALAR_FMT.get(et)
+            if fmt is not None:                      # scalars packed in one call
+                out.append(struct.pack("<%d%s" % (len(items), fmt[1]), *items))
+            else:
+                for it in items:
+                    cls._value(et, it, out)
+        else:
+            out.append(struct.pack(_SCALAR_FMT[t], v))
+
+    def to_bytes(self) -> bytes:
+        head: List[bytes] = [MAGIC, struct.pack("<IQQ", 3, len(self.tensors), len(self.kv))]
+        for key, t, v in self.kv:
+            head.append(self._str(key) + struct.pack("<I", t))
+            self._value(t, v, head)
+        offsets, cur = [], 0
+        for _n, _d, _t, raw in self.tensors:
+            offsets.append(cur)
+            cur += len(raw)
+            cur += (-cur) % self.alignment
+        for (name, dims, t, _raw), off in zip(self.tensors, offsets):
+            head.append(self._str(name) + struct.pack("<I", len(dims)))
+            head.append(struct.pack("<%dQ" % len(dims), *dims))
+            head.append(struct.pack("<IQ", t, off))
+        out = b"".join(head)
+        out += b"\x00" * ((-len(out)) % self.alignment)
+        parts, pos = [out], 0
+        for (_n, _d, _t, raw), off in zip(self.tensors, offsets):
+            parts.append(b"\x00" * (off - pos))
+            parts.append(raw)
+            pos = off + len(raw)
+        tail = (len(out) + pos) % self.alignment
+        parts.append(b"\x00" * ((-tail) % self.alignment))
+        return b"".join(parts)
+
+    def write(self, path: str) -> None:
+        with open(path, "wb") as f:
+            f.write(self.to_bytes())

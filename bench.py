@@ -32,12 +32,14 @@ single-threaded like the reference, over a bounded sample.
     python bench.py --gemv              # quantised GEMV (decode projections)
     python bench.py --gemm              # quantised GEMM (prefill projections)
     python bench.py --attention         # attention over a KV cache (decode, prefill)
+    python bench.py --gguf              # GGUF parse, upload to HBM, device row addressing
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import re
@@ -71,6 +73,8 @@ def parse_args(argv=None):
     p.add_argument("--variants", action="store_true",
                    help="every op variant at the Llama-3-8B 512-token geometry")
     p.add_argument("--gemv", action="store_true", help="quantised GEMV cases")
+    p.add_argument("--gguf", action="store_true",
+                   help="GGUF parse, file-to-HBM upload and device row addressing")
     p.add_argument("--attention", action="store_true",
                    help="attention over a KV cache (decode and causal prefill)")
     p.add_argument("--gemm", action="store_true",
@@ -504,6 +508,8 @@ def main(argv=None):
         return gemm(a)
     if a.attention:
         return attention_bench(a)
+    if a.gguf:
+        return gguf_bench(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -856,6 +862,161 @@ def attention_bench(a):
         plan.destroy()
         stream.destroy()
         del sets, src
+    return 0
+
+
+PCIE_GEN5_X16_GBS = 64.0  # host link, one direction
+
+
+def llama3_gguf(path: str, rng) -> dict:
+    """A synthetic Llama-3-8B GGUF file: the model's metadata and tokenizer
+    sizes (128256 tokens, 280147 merges), its 291 tensor records with their
+    names, the Q4_K token embedding table at full size (128256 x 4096, 295 MB)
+    and the norms at full size; the per-layer projections carry one Q4_K block
+    each (the index is the model's, the file is not 4.9 GB)."""
+    from aero_amd import gguf as AG, workloads as W
+
+    w = AG.GGUFWriter("llama", 32)
+    for k, v in (("block_count", 32), ("context_length", 8192), ("embedding_length", 4096),
+                 ("feed_forward_length", 14336), ("attention.head_count", 32),
+                 ("attention.head_count_kv", 8), ("vocab_size", 128256)):
+        w.add_kv(f"llama.{k}", AG.GGUF_UINT32, v)
+    w.add_kv("llama.rope.freq_base", AG.GGUF_FLOAT32, 500000.0)
+    w.add_kv("llama.attention.layer_norm_rms_epsilon", AG.GGUF_FLOAT32, 1e-5)
+    w.add_kv("tokenizer.ggml.model", AG.GGUF_STRING, "gpt2")
+    w.add_kv("tokenizer.ggml.tokens", AG.GGUF_ARRAY,
+             (AG.GGUF_STRING, [f"\u0120tok{i}" for i in range(128256)]))
+    w.add_kv("tokenizer.ggml.token_type", AG.GGUF_ARRAY, (AG.GGUF_INT32, [1] * 128256))
+    w.add_kv("tokenizer.ggml.merges", AG.GGUF_ARRAY,
+             (AG.GGUF_STRING, [f"\u0120t {i}" for i in range(280147)]))
+    w.add_kv("tokenizer.ggml.bos_token_id", AG.GGUF_UINT32, 128000)
+    emb = W.make_table(12, 128256 * 16, rng).tobytes()
+    w.add_tensor("token_embd.weight", (128256, 4096), emb, 12)
+    norm = np.ones(4096, np.float32).tobytes()
+    block = W.make_table(12, 1, rng).tobytes()
+    for i in range(32):
+        w.add_tensor(f"blk.{i}.attn_norm.weight", (4096,), norm, 0)
+        w.add_tensor(f"blk.{i}.ffn_norm.weight", (4096,), norm, 0)
+        for t in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
+            w.add_tensor(f"blk.{i}.{t}.weight", (1, 256), block, 12)
+    w.add_tensor("output_norm.weight", (4096,), norm, 0)
+    w.add_tensor("output.weight", (1, 256), block, 12)
+    w.write(path)
+    return {"tensors": len(w.tensors), "file_bytes": os.path.getsize(path),
+            "table_bytes": len(emb)}
+
+
+def gguf_bench(a):
+    """GGUF on MI355X: parse time, file-to-HBM upload rate, and device row
+    addressing (tensor_rows and the id gather) over the resident table."""
+    import tempfile
+
+    from aero_amd import _lib, gguf as AG
+    from aero_amd.device import DeviceArray as DA, Event, Stream, time_next_kernel
+
+    rng = np.random.default_rng(0)
+    tmp = tempfile.mkdtemp(prefix="aero_gguf_")
+    path = os.path.join(tmp, "llama3_8b_q4k.gguf")
+    try:
+        t0 = time.perf_counter()
+        meta = llama3_gguf(path, rng)
+        write_s = time.perf_counter() - t0
+        L = _lib.load()
+        # parse: the library's C++ parse alone, and the full Python reader
+        parse_us = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            h = L.aero_gguf_open(path.encode())
+            parse_us.append((time.perf_counter() - t0) * 1e6)
+            L.aero_gguf_close(h)
+        reader_us = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            r = AG.GGUFReader(path)
+            reader_us.append((time.perf_counter() - t0) * 1e6)
+            r.close()
+        res = {"case": "parse", "workload": "Llama-3-8B GGUF index (291 tensors, 128256-token "
+               "vocabulary, 280147 merges)", "file_bytes": meta["file_bytes"],
+               "parse_us": round(statistics.median(parse_us), 1),
+               "reader_us": round(statistics.median(reader_us), 1)}
+        if not a.no_cpu:
+            from oracle import refbind
+            Lr = refbind.gguf()
+            if Lr is not None:
+                ref_us = []
+                err = ctypes.create_string_buffer(256)
+                for _ in range(5):
+                    t0 = time.perf_counter()
+                    hr = Lr.rg_open(path.encode(), err, 256)
+                    ref_us.append((time.perf_counter() - t0) * 1e6)
+                    Lr.rg_close(hr)
+                res["cpu_baseline"] = {"us": round(statistics.median(ref_us), 1),
+                                       "kind": "reference", "cores": 1,
+                                       "sample": "GgufReader constructor (src/gguf.cpp), "
+                                                 "median of 5"}
+        print(json.dumps(res), flush=True)
+
+        r = AG.GGUFReader(path)
+        info = r.tensors["token_embd.weight"]
+        up_s = []
+        for _ in range(3):
+            r.release("token_embd.weight")
+            t0 = time.perf_counter()
+            dt = r.to_device("token_embd.weight")
+            up_s.append(time.perf_counter() - t0)
+        gbs = info.nbytes / statistics.median(up_s) / 1e9
+        print(json.dumps({"case": "upload", "tensor": "token_embd.weight Q4_K 128256x4096",
+                          "bytes": info.nbytes, "s": round(statistics.median(up_s), 4),
+                          "GB/s": round(gbs, 2), "of_pcie_gen5_x16": round(gbs / PCIE_GEN5_X16_GBS, 3),
+                          "write_s": round(write_s, 2),
+                          "note": "pread from the page cache (file just written) into pinned "
+                                  "buffers, host-to-device copies overlapped"}), flush=True)
+
+        stream = Stream()
+        n = 512
+        out = DA.empty((n, 4096))
+        ids = DA.from_numpy(rng.integers(0, 128256, n).astype(np.int32))
+        row_bytes = info.nbytes // 128256
+        b = n * row_bytes + n * 4096 * 4
+        for name, run in (("tensor_rows_512", lambda: dt.rows(64000, 64000 + n, out, stream)),
+                          ("gather_512", lambda: dt.gather(ids, out, stream=stream))):
+            for _ in range(a.warmup):
+                run()
+            pairs = []
+            for _ in range(a.steps):
+                e0, e1 = Event(), Event()
+                time_next_kernel(e0, e1)
+                run()
+                pairs.append((e0, e1))
+            stream.synchronize()
+            us = statistics.mean(x.elapsed_ms(y) * 1e3 for x, y in pairs)
+            g = b / (us * 1e-6) / 1e9
+            res = {"case": name, "rows": n, "bytes": b, "kernel_us": round(us, 3),
+                   "roofline": {"bound": "hbm", "achieved": round(g, 1), "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": round(g / HBM_PEAK_GBS, 4)}}
+            if not a.no_cpu:
+                from oracle import refbind
+                raw = np.frombuffer(r.tensor_bytes(info), np.uint8)
+                rows = raw[64000 * row_bytes:(64000 + n) * row_bytes]
+                deq = refbind.dequant if refbind.kernels() is not None else None
+                if deq is not None:
+                    reps, t0 = 0, time.perf_counter()
+                    while reps == 0 or time.perf_counter() - t0 < 1.0:
+                        deq(12, rows, n * 4096)
+                        reps += 1
+                    cu = (time.perf_counter() - t0) / reps * 1e6
+                    res["cpu_baseline"] = {"us": round(cu, 1), "kind": "reference", "cores": 1,
+                                           "sample": f"aero_dequant_ref of the {n} rows' bytes "
+                                                     f"(the core of tensor_rows), {reps} calls"}
+            print(json.dumps(res), flush=True)
+        stream.destroy()
+        r.close()
+    finally:
+        try:
+            os.remove(path)
+            os.rmdir(tmp)
+        except OSError:
+            pass
     return 0
 
 

@@ -384,10 +384,11 @@ const void* aero_gguf_tensor_data(void* h, const char* name);
  * (GGUFReader.tensor_bytes / _pread, engine/gguf.py:145-164,232-237). */
 int         aero_gguf_read(void* h, const char* name, int64_t byte0, int64_t nbytes, void* dst);
 /* Copy bytes [byte0, byte0+nbytes) of a tensor to device memory dst_dev on
- * `stream`, read with pread into two pinned host buffers (allocated on the
- * handle's first upload) overlapped with the host-to-device copies. Returns
- * once the bytes are in HBM. No reference counterpart: the reference reads
- * tensors into host memory only. */
+ * `stream`: four threads pread 8 MiB chunks into pinned host buffers (two
+ * per thread, 64 MiB, allocated on the handle's first upload) and queue each
+ * chunk's host-to-device copy while reading the next. Returns once the bytes
+ * are in HBM. No reference counterpart: the reference reads tensors into host
+ * memory only. */
 int         aero_gguf_upload(void* h, const char* name, int64_t byte0, int64_t nbytes,
                              void* dst_dev, void* stream);
 

@@ -339,3 +339,23 @@ def test_library_parser_large_vocabulary(tmp_path):
     with AG.GGUFReader(path) as r:
         assert r.kv["tokenizer.ggml.tokens"] == toks
         assert r.kv["tokenizer.ggml.scores"] == scores
+
+
+def test_library_writer_matches_oracle_writer(tmp_path):
+    """aero_amd.gguf.GGUFWriter writes the same bytes as the oracle's writer
+    for the same content, and the parser reads back what was written."""
+    rng = np.random.default_rng(5)
+    kv, tensors = rich_file(rng, 64)
+    w = AG.GGUFWriter("llama", 64)
+    for key, t, v in kv[2:]:
+        w.add_kv(key, t, v)
+    for name, shape, t, raw in tensors:
+        w.add_tensor(name, shape, raw, t)
+    data = w.to_bytes()
+    assert data == G.write(kv, tensors, 64)
+    path = write(tmp_path, "w.gguf", data)
+    with AG.GGUFReader(path) as r:
+        assert r.kv == G.parse(data)["kv"]
+        for name, shape, t, raw in tensors:
+            assert r.tensors[name].shape == shape
+            assert r.tensor_bytes(r.tensors[name]) == raw
