@@ -76,6 +76,16 @@ PROTOTYPES = {
     "aero_hip_dequant": (c_int, [c_int, vp, c_int64, vp, c_int64, vp]),
     "aero_hip_tensor_rows": (c_int, [c_int, vp, c_int64, c_int64, c_int64, c_int64, c_int64,
                                      vp, vp]),
+    # gated DeltaNet
+    "aero_ssm_softplus": (c_float, [c_float]),
+    "aero_ssm_delta_step": (None, [fp] * 8 + [c_int, c_int, c_float, c_float, fp]),
+    "aero_ssm_scan": (None, [fp] * 8 + [c_int] * 4 + [c_float, c_float, fp]),
+    "aero_ssm_conv": (None, [fp, fp, fp, POINTER(c_int), fp, c_int, c_int, c_int]),
+    "aero_hip_ssm_workspace": (c_int64, [c_int64] * 4),
+    "aero_hip_ssm_scan": (c_int, [vp] * 8 + [c_int64] * 4 + [c_float, c_float, vp, vp, c_int64,
+                                                              vp]),
+    "aero_hip_ssm_conv": (c_int, [vp, vp, vp, c_int64, vp, vp, c_int64, c_int64, c_int64,
+                                  POINTER(c_int64), vp]),
     # GGUF reader
     "aero_gguf_open": (vp, [ctypes.c_char_p]),
     "aero_gguf_close": (None, [vp]),

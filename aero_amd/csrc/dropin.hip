@@ -46,6 +46,14 @@ int64_t attn_workspace_bytes(int64_t n_q, int64_t n_head, int64_t n_head_kv, int
 bool kv_write_dev(int dt, const float* x, int64_t n_tok, int64_t heads, int64_t dim,
                   int64_t phys0, int64_t cap, void* q, float* scale, hipStream_t s);
 bool softmax_rows_dev(const float* x, float* y, int64_t n_rows, int64_t n_cols, hipStream_t s);
+int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d);
+bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* alpha,
+                  const float* beta, const float* a_log, const float* dt_bias, float* state,
+                  int64_t T, int64_t n_k, int64_t n_v, int64_t d, float scale, float eps,
+                  float* outs, void* workspace, int64_t ws_bytes, hipStream_t s);
+bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tail_len,
+                  float* tail_out, float* out, int64_t T, int64_t C, int64_t K,
+                  int64_t* new_tail_len, hipStream_t s);
 
 namespace {
 
@@ -524,4 +532,82 @@ int aero_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale
                     st.d2h(q, p[1], qb) && (dt == 0 || st.d2h(scale, p[2], 4)) && st.finish();
     return ok ? 1 : 0;
 }
+// ------------------------------------------------------- gated DeltaNet
+// src/ssm.cpp:151-210. Host arrays, synchronous; the void entries report a
+// refusal through aero_hip_last_error() and leave the outputs unwritten.
+
+// softplus(x) = log1p(exp(-|x|)) + max(x, 0) (src/ssm.cpp:22-24): a scalar
+// helper of the ABI, evaluated on the host.
+float aero_ssm_softplus(float x) { return log1pf(expf(-fabsf(x))) + (x > 0.0f ? x : 0.0f); }
+
+static bool host_ssm_scan(const float* q, const float* k, const float* v, const float* alpha,
+                          const float* beta, const float* a_log, const float* dt_bias,
+                          float* state, int64_t T, int64_t n_k, int64_t n_v, int64_t d,
+                          float scale, float eps, float* outs) {
+    if (T < 0 || n_k <= 0 || n_v <= 0 || d <= 0 || n_v % n_k || !q || !k || !v || !alpha ||
+        !beta || !a_log || !dt_bias || !state || !outs) {
+        set_error("aero_ssm_scan: refused arguments");
+        return false;
+    }
+    const size_t qb = (size_t)(T * n_k * d) * 4, vb = (size_t)(T * n_v * d) * 4;
+    const size_t ab = (size_t)(T * n_v) * 4, hb = (size_t)n_v * 4;
+    const size_t sb = (size_t)(n_v * d * d) * 4;
+    const int64_t wsb = aero::ssm_workspace_bytes(T, n_k, n_v, d);
+    aero::Staging st;
+    void* p[10];
+    if (!st.reserve({qb, qb, vb, ab, ab, hb, hb, sb, vb, (size_t)wsb}, p)) return false;
+    float** f = reinterpret_cast<float**>(p);
+    return st.h2d(f[0], q, qb) && st.h2d(f[1], k, qb) && st.h2d(f[2], v, vb) &&
+           st.h2d(f[3], alpha, ab) && st.h2d(f[4], beta, ab) && st.h2d(f[5], a_log, hb) &&
+           st.h2d(f[6], dt_bias, hb) && st.h2d(f[7], state, sb) &&
+           aero::ssm_scan_dev(f[0], f[1], f[2], f[3], f[4], f[5], f[6], f[7], T, n_k, n_v, d,
+                              scale, eps, f[8], p[9], wsb, st.stream()) &&
+           st.d2h(outs, f[8], vb) && st.d2h(state, f[7], sb) && st.finish();
+}
+
+// One token with q/k already tiled to n_heads (src/ssm.cpp:153-161).
+void aero_ssm_delta_step(const float* q, const float* k, const float* v, const float* alpha,
+                         const float* beta, const float* a_log, const float* dt_bias,
+                         float* state, int n_heads, int d, float scale, float eps, float* out) {
+    aero::clear_error();
+    (void)host_ssm_scan(q, k, v, alpha, beta, a_log, dt_bias, state, 1, n_heads, n_heads, d,
+                        scale, eps, out);
+}
+
+// T tokens, v-head h reading k-head h % n_k (src/ssm.cpp:163-171).
+void aero_ssm_scan(const float* qh, const float* kh, const float* vh, const float* alpha,
+                   const float* beta, const float* a_log, const float* dt_bias, float* state,
+                   int T, int n_k, int n_v, int d, float scale, float eps, float* outs) {
+    aero::clear_error();
+    (void)host_ssm_scan(qh, kh, vh, alpha, beta, a_log, dt_bias, state, T, n_k, n_v, d, scale,
+                        eps, outs);
+}
+
+// Causal depthwise conv over [tail; x]; tail (kernel - 1 rows of room) and
+// *tail_len are updated in place (src/ssm.cpp:173-210).
+void aero_ssm_conv(const float* x, const float* w, float* tail, int* tail_len, float* out,
+                   int T, int channels, int kernel) {
+    aero::clear_error();
+    if (tail_len == nullptr || x == nullptr || w == nullptr || out == nullptr || T < 0 ||
+        channels <= 0 || kernel <= 0 || *tail_len < 0 || *tail_len > kernel - 1 ||
+        (kernel > 1 && tail == nullptr)) {
+        set_error("aero_ssm_conv: refused arguments");
+        return;
+    }
+    const int64_t tl = *tail_len;
+    const size_t xb = (size_t)T * channels * 4, wb = (size_t)channels * kernel * 4;
+    const size_t tb = (size_t)(kernel > 1 ? kernel - 1 : 0) * channels * 4;
+    aero::Staging st;
+    void* p[4];
+    if (!st.reserve({xb, wb, tb, xb}, p)) return;
+    float** f = reinterpret_cast<float**>(p);
+    int64_t keep = 0;
+    if (st.h2d(f[0], x, xb) && st.h2d(f[1], w, wb) &&
+        st.h2d(f[2], tail, (size_t)tl * channels * 4) &&
+        aero::ssm_conv_dev(f[0], f[1], f[2], tl, f[2], f[3], T, channels, kernel, &keep,
+                           st.stream()) &&
+        st.d2h(out, f[3], xb) && st.d2h(tail, f[2], (size_t)keep * channels * 4) && st.finish())
+        *tail_len = (int)keep;
+}
+
 }  // extern "C"

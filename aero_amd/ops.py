@@ -8,6 +8,8 @@ numpy wrappers live in tensor_native / transformer_native / native.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from . import _lib
@@ -270,6 +272,54 @@ def softmax_rows(x: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
     _need(y, n_rows * n_cols, np.float32, "y")
     _lib.check(_lib.lib().aero_hip_softmax_rows(x.ptr, y.ptr, n_rows, n_cols, _s(stream)),
                "softmax_rows")
+
+
+_ssm_ws: dict = {}
+
+
+def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
+             beta: DeviceArray, a_log: DeviceArray, dt_bias: DeviceArray, state: DeviceArray,
+             outs: DeviceArray, T: int, n_k: int, n_v: int, d: int, scale: float,
+             eps: float = 1e-6, stream: Stream | None = None) -> None:
+    """Gated delta-rule scan over T tokens (src/ssm.cpp:69-142): q, k
+    [T, n_k, d], v / outs [T, n_v, d], alpha / beta [T, n_v], a_log / dt_bias
+    [n_v], state [n_v, d, d] updated in place. The workspace (normalised q / k,
+    per-token decay and gate) is allocated once per size and reused."""
+    _need(q, T * n_k * d, np.float32, "q")
+    _need(k, T * n_k * d, np.float32, "k")
+    _need(v, T * n_v * d, np.float32, "v")
+    _need(outs, T * n_v * d, np.float32, "outs")
+    _need(alpha, T * n_v, np.float32, "alpha")
+    _need(beta, T * n_v, np.float32, "beta")
+    _need(a_log, n_v, np.float32, "a_log")
+    _need(dt_bias, n_v, np.float32, "dt_bias")
+    _need(state, n_v * d * d, np.float32, "state")
+    L = _lib.lib()
+    wsb = int(L.aero_hip_ssm_workspace(T, n_k, n_v, d))
+    ws = _ssm_ws.get(wsb)
+    if ws is None and wsb > 0:
+        ws = _ssm_ws[wsb] = DeviceArray.empty(wsb // 4, np.float32)
+    _lib.check(L.aero_hip_ssm_scan(q.ptr, k.ptr, v.ptr, alpha.ptr, beta.ptr, a_log.ptr,
+                                   dt_bias.ptr, state.ptr, T, n_k, n_v, d, float(scale),
+                                   float(eps), outs.ptr, as_ptr(ws), wsb, _s(stream)),
+               "ssm_scan")
+
+
+def ssm_conv(x: DeviceArray, w: DeviceArray, tail: DeviceArray | None, tail_len: int,
+             tail_out: DeviceArray | None, out: DeviceArray, T: int, channels: int,
+             kernel: int, stream: Stream | None = None) -> int:
+    """Causal depthwise conv over [tail; x] (src/ssm.cpp:173-210); the new
+    history goes to tail_out (which may be tail). Returns its length."""
+    _need(x, T * channels, np.float32, "x")
+    _need(out, T * channels, np.float32, "out")
+    _need(w, channels * kernel, np.float32, "w")
+    _need(tail, tail_len * channels, np.float32, "tail")
+    _need(tail_out, (kernel - 1) * channels, np.float32, "tail_out")
+    n = ctypes.c_int64()
+    _lib.check(_lib.lib().aero_hip_ssm_conv(x.ptr, w.ptr, as_ptr(tail), int(tail_len),
+                                            as_ptr(tail_out), out.ptr, T, channels, kernel,
+                                            ctypes.byref(n), _s(stream)), "ssm_conv")
+    return int(n.value)
 
 
 def copy_f32(src: DeviceArray, dst: DeviceArray, n: int | None = None,

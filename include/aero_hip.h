@@ -330,6 +330,48 @@ int     aero_hip_plan_destroy(void* plan);
  * device (hipExtLaunchKernel), then the arming is cleared. */
 int   aero_hip_time_next_kernel(void* start, void* stop);
 
+/* ------------------------------------------------------- gated DeltaNet
+ * The delta-rule scan and causal conv of src/ssm.cpp:17-210 (engine/ssm.py
+ * recurrence). Per token t and value head h (key head h % n_k): qn, kn =
+ * q, k / max(||.||, eps); dec = exp(min(a_log[h] * softplus(alpha + dt_bias),
+ * 0)); b = sigmoid(beta); S_h = dec S_h; v_new = (v - kn^T S_h) b;
+ * S_h += kn v_new^T; out = scale qn^T S_h. state [n_v][d][d] (row = key
+ * element) is updated in place. */
+
+/* Reference-compatible host ABI (host arrays, synchronous). The void
+ * entries leave their outputs unwritten and set aero_hip_last_error() when
+ * they refuse (sizes, null pointers, head dim not in {64, 128, 256}). */
+float aero_ssm_softplus(float x);                                   /* src/ssm.cpp:151 */
+void  aero_ssm_delta_step(const float* q, const float* k, const float* v,
+                          const float* alpha, const float* beta, const float* a_log,
+                          const float* dt_bias, float* state, int n_heads, int d,
+                          float scale, float eps, float* out);       /* src/ssm.cpp:153-161 */
+void  aero_ssm_scan(const float* qh, const float* kh, const float* vh, const float* alpha,
+                    const float* beta, const float* a_log, const float* dt_bias,
+                    float* state, int T, int n_k, int n_v, int d, float scale, float eps,
+                    float* outs);                                    /* src/ssm.cpp:163-171 */
+void  aero_ssm_conv(const float* x, const float* w, float* tail, int* tail_len, float* out,
+                    int T, int channels, int kernel);                /* src/ssm.cpp:173-210 */
+
+/* Device ABI. q, k [T][n_k][d]; v, outs [T][n_v][d]; alpha, beta [T][n_v];
+ * a_log, dt_bias [n_v]; state [n_v][d][d]; d in {64, 128, 256}; q, k, state
+ * and workspace 16-byte aligned; workspace of aero_hip_ssm_workspace bytes
+ * (normalised q / k and the per-token decay and gate). */
+int64_t aero_hip_ssm_workspace(int64_t T, int64_t n_k, int64_t n_v, int64_t d);
+int     aero_hip_ssm_scan(const float* q, const float* k, const float* v, const float* alpha,
+                          const float* beta, const float* a_log, const float* dt_bias,
+                          float* state, int64_t T, int64_t n_k, int64_t n_v, int64_t d,
+                          float scale, float eps, float* outs, void* workspace,
+                          int64_t ws_bytes, void* stream);
+/* Causal depthwise conv: x, out [T][channels], w [channels][kernel] (tap 0
+ * the oldest input), tail [tail_len][channels] of history (tail_len <
+ * kernel <= 16); the new history (the last min(kernel-1, tail_len+T) rows of
+ * [tail; x]) goes to tail_out, which may be tail, and its length to
+ * *new_tail_len (host). */
+int     aero_hip_ssm_conv(const float* x, const float* w, const float* tail, int64_t tail_len,
+                          float* tail_out, float* out, int64_t T, int64_t channels,
+                          int64_t kernel, int64_t* new_tail_len, void* stream);
+
 /* ---------------------------------------------------------------- GGUF
  * A GGUF file parsed on the host (src/gguf.cpp:150-354, the reference's
  * GgufReader; engine/gguf.py:166-233, GGUFReader._parse_index) and its tensors

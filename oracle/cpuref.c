@@ -410,3 +410,114 @@ int cr_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale) 
     } else return 0;
     return 1;
 }
+
+/* ------------------------------------------------------ gated DeltaNet */
+/* src/ssm.cpp:17-24: silu / sigmoid / softplus(x) = log1p(exp(-|x|)) +
+ * max(x, 0). */
+float cr_ssm_softplus(float x) {
+    return log1pf(expf(-fabsf(x))) + (x > 0.0f ? x : 0.0f);
+}
+
+static float cr_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* src/ssm.cpp:28-34: x / max(||x||, eps), the sum of squares serial. */
+static void cr_l2_row(const float* x, int64_t n, float eps, float* out) {
+    float ss = 0.0f;
+    for (int64_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    float nv = sqrtf(ss);
+    if (nv < eps) nv = eps;
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] / nv;
+}
+
+/* src/ssm.cpp:69-126: one token of the gated delta rule. v-head h reads
+ * k-head h % n_k; g = a_log[h] * softplus(alpha[h] + dt_bias[h]) clamped to
+ * <= 0, S *= exp(g), v_pred = kn^T S, v_new = (v - v_pred) * sigmoid(beta[h]),
+ * S += kn v_new^T, out = scale * qn^T S. state [n_v][d][d] row-major (row i =
+ * key element, column e = value element). */
+void cr_ssm_delta_step_grouped(const float* q, const float* k, const float* v,
+                               const float* alpha, const float* beta, const float* a_log,
+                               const float* dt_bias, float* state, int64_t n_k, int64_t n_v,
+                               int64_t d, float scale, float eps, float* out) {
+    float* qn = (float*)malloc(sizeof(float) * (size_t)(n_v * d));
+    float* kn = (float*)malloc(sizeof(float) * (size_t)(n_v * d));
+    float* vpred = (float*)malloc(sizeof(float) * (size_t)d);
+    float* vnew = (float*)malloc(sizeof(float) * (size_t)d);
+    for (int64_t h = 0; h < n_v; ++h) {
+        const int64_t kk = h % n_k;
+        cr_l2_row(q + kk * d, d, eps, qn + h * d);
+        cr_l2_row(k + kk * d, d, eps, kn + h * d);
+    }
+    for (int64_t h = 0; h < n_v; ++h) {
+        float g = a_log[h] * cr_ssm_softplus(alpha[h] + dt_bias[h]);
+        if (g > 0.0f) g = 0.0f;
+        const float dec = expf(g);
+        const float b = cr_sigmoid(beta[h]);
+        float* S = state + h * d * d;
+        const float* knh = kn + h * d;
+        const float* qnh = qn + h * d;
+        const float* vh = v + h * d;
+        float* oh = out + h * d;
+        for (int64_t i = 0; i < d * d; ++i) S[i] *= dec;
+        for (int64_t e = 0; e < d; ++e) {
+            float s = 0.0f;
+            for (int64_t i = 0; i < d; ++i) s += knh[i] * S[i * d + e];
+            vpred[e] = s;
+        }
+        for (int64_t e = 0; e < d; ++e) vnew[e] = (vh[e] - vpred[e]) * b;
+        for (int64_t i = 0; i < d; ++i) {
+            const float ki = knh[i];
+            for (int64_t e = 0; e < d; ++e) S[i * d + e] += ki * vnew[e];
+        }
+        for (int64_t e = 0; e < d; ++e) {
+            float s = 0.0f;
+            for (int64_t i = 0; i < d; ++i) s += qnh[i] * S[i * d + e];
+            oh[e] = scale * s;
+        }
+    }
+    free(qn);
+    free(kn);
+    free(vpred);
+    free(vnew);
+}
+
+/* src/ssm.cpp:128-142,163-171: T tokens; q, k [T][n_k][d], v [T][n_v][d],
+ * alpha, beta [T][n_v], outs [T][n_v][d]. */
+void cr_ssm_scan(const float* q, const float* k, const float* v, const float* alpha,
+                 const float* beta, const float* a_log, const float* dt_bias, float* state,
+                 int64_t T, int64_t n_k, int64_t n_v, int64_t d, float scale, float eps,
+                 float* outs) {
+    for (int64_t t = 0; t < T; ++t)
+        cr_ssm_delta_step_grouped(q + t * n_k * d, k + t * n_k * d, v + t * n_v * d,
+                                  alpha + t * n_v, beta + t * n_v, a_log, dt_bias, state, n_k,
+                                  n_v, d, scale, eps, outs + t * n_v * d);
+}
+
+/* src/ssm.cpp:173-210: causal depthwise conv over [tail; x] (tail_len rows of
+ * history), w [channels][kernel] with tap 0 on the oldest input; out [T][C];
+ * the tail becomes the last min(kernel - 1, tail_len + T) rows. */
+void cr_ssm_conv(const float* x, const float* w, float* tail, int* tail_len, float* out,
+                 int64_t T, int64_t channels, int64_t kernel) {
+    const int64_t tl = *tail_len;
+    const int64_t n = tl + T;
+    float* buf = (float*)malloc(sizeof(float) * (size_t)((n > 0 ? n : 1) * channels));
+    if (tl > 0) memcpy(buf, tail, sizeof(float) * (size_t)(tl * channels));
+    memcpy(buf + tl * channels, x, sizeof(float) * (size_t)(T * channels));
+    for (int64_t t = 0; t < T; ++t) {
+        const int64_t end = n - T + t + 1;
+        const int64_t start = end - kernel;
+        for (int64_t c = 0; c < channels; ++c) {
+            float acc = 0.0f;
+            for (int64_t j = 0; j < kernel; ++j) {
+                const int64_t idx = start + j;
+                if (idx >= 0 && idx < n) acc += buf[idx * channels + c] * w[c * kernel + j];
+            }
+            out[t * channels + c] = acc;
+        }
+    }
+    int64_t keep = kernel - 1;
+    if (keep < 0) keep = 0;
+    if (keep > n) keep = n;
+    if (keep > 0) memcpy(tail, buf + (n - keep) * channels, sizeof(float) * (size_t)(keep * channels));
+    *tail_len = (int)keep;
+    free(buf);
+}

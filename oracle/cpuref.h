@@ -81,6 +81,19 @@ void cr_kv_quant_i4(const float* x, int64_t dim, uint8_t* q, float* s);
 int  cr_kv_read_vec(int dt, const void* q, const float* scale, int64_t dim, float* out);
 int  cr_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale);
 
+/* gated DeltaNet (src/ssm.cpp:17-210) */
+float cr_ssm_softplus(float x);
+void  cr_ssm_delta_step_grouped(const float* q, const float* k, const float* v,
+                                const float* alpha, const float* beta, const float* a_log,
+                                const float* dt_bias, float* state, int64_t n_k, int64_t n_v,
+                                int64_t d, float scale, float eps, float* out);
+void  cr_ssm_scan(const float* q, const float* k, const float* v, const float* alpha,
+                  const float* beta, const float* a_log, const float* dt_bias, float* state,
+                  int64_t T, int64_t n_k, int64_t n_v, int64_t d, float scale, float eps,
+                  float* outs);
+void  cr_ssm_conv(const float* x, const float* w, float* tail, int* tail_len, float* out,
+                  int64_t T, int64_t channels, int64_t kernel);
+
 #ifdef __cplusplus
 }
 #endif

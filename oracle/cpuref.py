@@ -78,6 +78,15 @@ def lib():
         L.cr_kv_write_vec.restype = c_int
         L.cr_kv_read_vec.argtypes = [c_int, ctypes.c_void_p, fp, c_int64, fp]
         L.cr_kv_read_vec.restype = c_int
+        L.cr_ssm_softplus.argtypes = [c_float]
+        L.cr_ssm_softplus.restype = c_float
+        L.cr_ssm_delta_step_grouped.argtypes = [fp] * 8 + [c_int64] * 3 + [c_float, c_float, fp]
+        L.cr_ssm_delta_step_grouped.restype = None
+        L.cr_ssm_scan.argtypes = [fp] * 8 + [c_int64] * 4 + [c_float, c_float, fp]
+        L.cr_ssm_scan.restype = None
+        L.cr_ssm_conv.argtypes = [fp, fp, fp, POINTER(ctypes.c_int), fp, c_int64, c_int64,
+                                  c_int64]
+        L.cr_ssm_conv.restype = None
         _lib = L
     return _lib
 
@@ -340,3 +349,55 @@ def kv_read_vec(dt: int, q, scale: float, dim: int) -> np.ndarray:
     if not lib().cr_kv_read_vec(dt, q.ctypes.data, _f(s), dim, _f(out)):
         raise ValueError("kv read refused")
     return out
+
+
+# ------------------------------------------------------------ gated DeltaNet
+
+def ssm_softplus(x) -> np.ndarray:
+    """src/ssm.cpp:22-24, elementwise."""
+    x = f32(x)
+    return np.array([lib().cr_ssm_softplus(float(v)) for v in x.reshape(-1)],
+                    np.float32).reshape(x.shape)
+
+
+def ssm_delta_step(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
+    """src/ssm.cpp:69-126. q, k (n_k, d); v (n_v, d); state (n_v, d, d), not
+    mutated. Returns (out (n_v, d), new state)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    n_k, d = q.shape
+    n_v = v.shape[0]
+    st = np.array(f32(state), copy=True)
+    out = np.zeros((n_v, d), np.float32)
+    lib().cr_ssm_delta_step_grouped(_f(q), _f(k), _f(v), _f(f32(alpha)), _f(f32(beta)),
+                                    _f(f32(a_log)), _f(f32(dt_bias)), _f(st), n_k, n_v, d,
+                                    float(scale), float(eps), _f(out))
+    return out, st
+
+
+def ssm_scan(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
+    """src/ssm.cpp:128-142,163-171. q, k (T, n_k, d); v (T, n_v, d); alpha,
+    beta (T, n_v). Returns (outs (T, n_v, d), new state)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    T, n_k, d = q.shape
+    n_v = v.shape[1]
+    st = np.array(f32(state), copy=True)
+    outs = np.zeros((T, n_v, d), np.float32)
+    lib().cr_ssm_scan(_f(q), _f(k), _f(v), _f(f32(alpha)), _f(f32(beta)), _f(f32(a_log)),
+                      _f(f32(dt_bias)), _f(st), T, n_k, n_v, d, float(scale), float(eps),
+                      _f(outs))
+    return outs, st
+
+
+def ssm_conv(x, w, tail, tail_len: int):
+    """src/ssm.cpp:173-210. x (T, C); w (C, kernel); tail (>= kernel-1, C)
+    holding tail_len rows. Returns (out, new tail (kernel-1, C), new length)."""
+    x, w = f32(x), f32(w)
+    T, C = x.shape
+    kernel = w.shape[1]
+    tb = np.zeros((max(kernel - 1, 1), C), np.float32)
+    if tail_len > 0:
+        tb[:tail_len] = f32(tail)[:tail_len]
+    out = np.zeros((T, C), np.float32)
+    tl = ctypes.c_int(int(tail_len))
+    lib().cr_ssm_conv(_f(x), _f(w), _f(tb), ctypes.byref(tl), _f(out), T, C, kernel)
+    return out, tb[:max(kernel - 1, 0)], int(tl.value)

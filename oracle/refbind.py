@@ -21,11 +21,13 @@ KERNELS = os.path.join(REF_DIR, "libref_kernels.so")
 TRANSFORMER = os.path.join(REF_DIR, "libref_transformer.so")
 KV = os.path.join(REF_DIR, "libref_kv.so")
 GGUF = os.path.join(REF_DIR, "libref_gguf.so")
+SSM = os.path.join(REF_DIR, "libref_ssm.so")
 
 _k = None
 _t = None
 _v = None
 _g = None
+_s = None
 
 
 def kernels():
@@ -118,6 +120,63 @@ def gguf():
             f.argtypes = args
         _g = L
     return _g
+
+
+def ssm():
+    """The reference's gated-DeltaNet C ABI (src/ssm.cpp:151-210)."""
+    global _s
+    if _s is None and os.path.exists(SSM):
+        L = ctypes.CDLL(SSM)
+        fp = POINTER(c_float)
+        L.aero_ssm_softplus.argtypes = [c_float]
+        L.aero_ssm_softplus.restype = c_float
+        L.aero_ssm_delta_step.argtypes = [fp] * 8 + [c_int, c_int, c_float, c_float, fp]
+        L.aero_ssm_delta_step.restype = None
+        L.aero_ssm_scan.argtypes = [fp] * 8 + [c_int] * 4 + [c_float, c_float, fp]
+        L.aero_ssm_scan.restype = None
+        L.aero_ssm_conv.argtypes = [fp, fp, fp, POINTER(c_int), fp, c_int, c_int, c_int]
+        L.aero_ssm_conv.restype = None
+        _s = L
+    return _s
+
+
+def ssm_delta_step(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
+    """aero_ssm_delta_step: q, k already (n_heads, d). Returns (out, new state)."""
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    q, k, v = f(q), f(k), f(v)
+    n, d = v.shape
+    st = np.array(f(state), copy=True)
+    out = np.zeros((n, d), np.float32)
+    ssm().aero_ssm_delta_step(_f(q), _f(k), _f(v), _f(f(alpha)), _f(f(beta)), _f(f(a_log)),
+                              _f(f(dt_bias)), _f(st), n, d, float(scale), float(eps), _f(out))
+    return out, st
+
+
+def ssm_scan(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    q, k, v = f(q), f(k), f(v)
+    T, n_k, d = q.shape
+    n_v = v.shape[1]
+    st = np.array(f(state), copy=True)
+    outs = np.zeros((T, n_v, d), np.float32)
+    ssm().aero_ssm_scan(_f(q), _f(k), _f(v), _f(f(alpha)), _f(f(beta)), _f(f(a_log)),
+                        _f(f(dt_bias)), _f(st), T, n_k, n_v, d, float(scale), float(eps),
+                        _f(outs))
+    return outs, st
+
+
+def ssm_conv(x, w, tail, tail_len: int):
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    x, w = f(x), f(w)
+    T, C = x.shape
+    kernel = w.shape[1]
+    tb = np.zeros((max(kernel - 1, 1), C), np.float32)
+    if tail_len > 0:
+        tb[:tail_len] = f(tail)[:tail_len]
+    out = np.zeros((T, C), np.float32)
+    tl = c_int(int(tail_len))
+    ssm().aero_ssm_conv(_f(x), _f(w), _f(tb), ctypes.byref(tl), _f(out), T, C, kernel)
+    return out, tb[:max(kernel - 1, 0)], int(tl.value)
 
 
 def available() -> bool:

@@ -208,6 +208,27 @@ def ref_vectors() -> dict:
         qs, sc = zip(*(R.kv_write_vec(dt, row) for row in kvx))
         v[f"kv{dt}_q"] = np.stack(qs)
         v[f"kv{dt}_scale"] = np.array(sc, np.float32)
+    # gated DeltaNet scan and causal conv (src/ssm.cpp:69-210): 6 tokens,
+    # 2 k-heads, 4 v-heads, d = 32; a conv over 8 channels in two chunks
+    T, NK, NV, D = 6, 2, 4, 32
+    sq = rng.standard_normal((T, NK, D)).astype(np.float32)
+    sk = rng.standard_normal((T, NK, D)).astype(np.float32)
+    sv = rng.standard_normal((T, NV, D)).astype(np.float32)
+    sal = rng.standard_normal((T, NV)).astype(np.float32)
+    sbt = rng.standard_normal((T, NV)).astype(np.float32)
+    sa = (-np.abs(rng.standard_normal(NV)) * 0.5).astype(np.float32)
+    sdt = rng.standard_normal(NV).astype(np.float32)
+    s0 = (rng.standard_normal((NV, D, D)) * 0.1).astype(np.float32)
+    for name, arr in (("q", sq), ("k", sk), ("v", sv), ("alpha", sal), ("beta", sbt),
+                      ("a_log", sa), ("dt_bias", sdt), ("state", s0)):
+        v[f"ssm_{name}"] = arr
+    v["ssm_out"], v["ssm_state_out"] = R.ssm_scan(sq, sk, sv, sal, sbt, sa, sdt, s0, 0.125)
+    cx = rng.standard_normal((9, 8)).astype(np.float32)
+    cw = rng.standard_normal((8, 4)).astype(np.float32)
+    o1, t1, l1 = R.ssm_conv(cx[:2], cw, None, 0)
+    o2, t2, l2 = R.ssm_conv(cx[2:], cw, t1, l1)
+    v["conv_x"], v["conv_w"] = cx, cw
+    v["conv_out"], v["conv_tail"] = np.concatenate([o1, o2]), t2
     return v
 
 

@@ -591,3 +591,126 @@ def test_softmax_and_kv_closed_forms():
     qb, sc = O.kv_write_vec(2, np.array([1.0, -7.0] + [0.0] * 6, np.float32))
     assert sc == 1.0 and qb[0] == (1 | (0x9 << 4))                  # -7 & 15 = 9, high nibble
     assert list(O.kv_read_vec(2, qb, sc, 8)[:2]) == [1.0, -7.0]
+
+
+# ------------------------------------------------------------ gated DeltaNet
+
+def _ssm_inputs(rng, T, n_k, n_v, d):
+    q = rng.standard_normal((T, n_k, d)).astype(np.float32)
+    k = rng.standard_normal((T, n_k, d)).astype(np.float32)
+    v = rng.standard_normal((T, n_v, d)).astype(np.float32)
+    alpha = rng.standard_normal((T, n_v)).astype(np.float32)
+    beta = rng.standard_normal((T, n_v)).astype(np.float32)
+    a_log = (-np.abs(rng.standard_normal(n_v)) * 0.5).astype(np.float32)
+    dt_bias = rng.standard_normal(n_v).astype(np.float32)
+    state = (rng.standard_normal((n_v, d, d)) * 0.1).astype(np.float32)
+    return q, k, v, alpha, beta, a_log, dt_bias, state
+
+
+def _ssm_f64_step(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
+    """The gated delta rule in float64 from its definition (engine/ssm.py:1-20
+    recurrence; v-head h reads k-head h % n_k)."""
+    n_k, d = q.shape
+    n_v = v.shape[0]
+    S = state.astype(np.float64).copy()
+    out = np.zeros((n_v, d))
+    for h in range(n_v):
+        qn = q[h % n_k].astype(np.float64)
+        kn = k[h % n_k].astype(np.float64)
+        qn /= max(np.linalg.norm(qn), eps)
+        kn /= max(np.linalg.norm(kn), eps)
+        x = float(alpha[h]) + float(dt_bias[h])
+        g = min(float(a_log[h]) * (np.log1p(np.exp(-abs(x))) + max(x, 0.0)), 0.0)
+        b = 1.0 / (1.0 + np.exp(-float(beta[h])))
+        S[h] *= np.exp(g)
+        S[h] += np.outer(kn, (v[h] - kn @ S[h]) * b)
+        out[h] = scale * (qn @ S[h])
+    return out, S
+
+
+def test_ssm_matches_compiled_reference():
+    """Bit-identical to src/ssm.cpp built into oracle/_ref: softplus over
+    [-30, 30], the delta step (tiled heads), the grouped scan and the conv
+    with its tail, over two chunks."""
+    if R.ssm() is None:
+        pytest.skip("oracle/_ref not built")
+    L = R.ssm()
+    xs = np.linspace(-30, 30, 401).astype(np.float32)
+    assert bits_equal(O.ssm_softplus(xs), np.array([L.aero_ssm_softplus(float(x)) for x in xs],
+                                                   np.float32))
+    rng = np.random.default_rng(51)
+    q, k, v, al, bt, a_log, dt, st = _ssm_inputs(rng, 5, 2, 4, 16)
+    qe, ke = np.tile(q[0], (2, 1)), np.tile(k[0], (2, 1))
+    o1, s1 = O.ssm_delta_step(qe, ke, v[0], al[0], bt[0], a_log, dt, st, 0.25)
+    o2, s2 = R.ssm_delta_step(qe, ke, v[0], al[0], bt[0], a_log, dt, st, 0.25)
+    assert bits_equal(o1, o2) and bits_equal(s1, s2)
+    o1, s1 = O.ssm_scan(q, k, v, al, bt, a_log, dt, st, 0.25)
+    o2, s2 = R.ssm_scan(q, k, v, al, bt, a_log, dt, st, 0.25)
+    assert bits_equal(o1, o2) and bits_equal(s1, s2)
+    x = rng.standard_normal((7, 10)).astype(np.float32)
+    w = rng.standard_normal((10, 4)).astype(np.float32)
+    t0 = np.zeros((3, 10), np.float32)
+    for a, b in ((0, 2), (2, 7)):
+        r1 = O.ssm_conv(x[a:b], w, t0, 0 if a == 0 else tl)
+        r2 = R.ssm_conv(x[a:b], w, t0, 0 if a == 0 else tl)
+        assert bits_equal(r1[0], r2[0]) and r1[2] == r2[2]
+        assert bits_equal(r1[1][:r1[2]], r2[1][:r2[2]])
+        t0, tl = r1[1], r1[2]
+
+
+def test_ssm_definition_and_invariants():
+    """Against the float64 definition; the delta rule's closed form (no decay,
+    beta -> 1: the written key reads back its value, kn^T S' = v); beta -> 0
+    leaves the decayed state; the conv in two chunks equals one pass; planted
+    mistakes (h // ratio grouping, reversed conv taps) are rejected."""
+    rng = np.random.default_rng(53)
+    q, k, v, al, bt, a_log, dt, st = _ssm_inputs(rng, 3, 2, 6, 12)
+    out, S = O.ssm_delta_step(q[0], k[0], v[0], al[0], bt[0], a_log, dt, st, 0.3)
+    want, Sw = _ssm_f64_step(q[0], k[0], v[0], al[0], bt[0], a_log, dt, st, 0.3)
+    assert np.abs(out - want).max() <= 1e-5 * np.abs(want).max()
+    assert np.abs(S - Sw).max() <= 1e-5 * np.abs(Sw).max()
+    # planted: v-head h reading k-head h // (n_v / n_k) differs
+    qp, kp = np.repeat(q[0], 3, axis=0), np.repeat(k[0], 3, axis=0)
+    bad, _ = O.ssm_delta_step(qp, kp, v[0], al[0], bt[0], a_log, dt, st, 0.3)
+    assert np.abs(bad - want).max() > 1e-2
+    # no decay (a_log = 0) and beta = +40 (sigmoid = 1): kn^T S' == v
+    z = np.zeros_like(a_log)
+    _, S1 = O.ssm_delta_step(q[0], k[0], v[0], al[0], np.full(6, 40.0, np.float32), z, dt,
+                             st, 0.3)
+    for h in range(6):
+        kn = k[0][h % 2].astype(np.float64)
+        kn /= np.linalg.norm(kn)
+        assert np.abs(kn @ S1[h] - v[0][h]).max() <= 1e-5 * max(1.0, np.abs(v[0][h]).max())
+    # beta = -80 (sigmoid underflows to 0): only the decay is applied
+    _, S2 = O.ssm_delta_step(q[0], k[0], v[0], al[0], np.full(6, -80.0, np.float32), a_log,
+                             dt, st, 0.3)
+    for h in range(6):
+        x = float(al[0][h]) + float(dt[h])
+        g = min(float(a_log[h]) * (np.log1p(np.exp(-abs(x))) + max(x, 0.0)), 0.0)
+        assert np.abs(S2[h] - st[h] * np.exp(g)).max() <= 1e-6
+    # conv: two chunks == one pass; tap 0 pairs with the oldest input
+    x = rng.standard_normal((9, 5)).astype(np.float32)
+    w = rng.standard_normal((5, 4)).astype(np.float32)
+    one, t1, l1 = O.ssm_conv(x, w, None, 0)
+    a, ta, la = O.ssm_conv(x[:4], w, None, 0)
+    b, tb, lb = O.ssm_conv(x[4:], w, ta, la)
+    assert bits_equal(np.concatenate([a, b]), one) and l1 == lb == 3 and bits_equal(t1, tb)
+    f64 = np.zeros((9, 5))
+    for t in range(9):
+        for j in range(4):
+            if t - 3 + j >= 0:
+                f64[t] += x[t - 3 + j].astype(np.float64) * w[:, j]
+    assert np.abs(one - f64).max() <= 1e-5 * np.abs(f64).max()
+    rev, _, _ = O.ssm_conv(x, w[:, ::-1].copy(), None, 0)
+    assert np.abs(rev - f64).max() > 1e-2
+
+
+def test_golden_ssm():
+    """The reference's own scan and conv outputs (tests/golden/ref_vectors.npz)."""
+    g = golden("ref_vectors.npz")
+    out, st = O.ssm_scan(g["ssm_q"], g["ssm_k"], g["ssm_v"], g["ssm_alpha"], g["ssm_beta"],
+                         g["ssm_a_log"], g["ssm_dt_bias"], g["ssm_state"], 0.125)
+    assert bits_equal(out, g["ssm_out"]) and bits_equal(st, g["ssm_state_out"])
+    o1, t1, l1 = O.ssm_conv(g["conv_x"][:2], g["conv_w"], None, 0)
+    o2, t2, _ = O.ssm_conv(g["conv_x"][2:], g["conv_w"], t1, l1)
+    assert bits_equal(np.concatenate([o1, o2]), g["conv_out"]) and bits_equal(t2, g["conv_tail"])
