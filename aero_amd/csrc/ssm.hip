@@ -32,6 +32,7 @@ namespace aero {
 namespace {
 
 constexpr int kScanThreads = 256;
+constexpr int kDepth = 4;  // tokens whose operands a lane has in flight
 
 __device__ __forceinline__ float softplus_dev(float x) {
     return log1pf(expf(-fabsf(x))) + (x > 0.0f ? x : 0.0f);
@@ -72,84 +73,178 @@ __global__ __launch_bounds__(64) void ssm_prep_kernel(
     }
 }
 
-// P lanes a column, RPT = D / P rows each; lane = part * CPW + ci.
-template <int D, int P>
-__global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
-    const float* __restrict__ qn, const float* __restrict__ kn, const float* __restrict__ v,
-    const float* __restrict__ dec, const float* __restrict__ bb, float* __restrict__ state,
-    float* __restrict__ outs, int64_t T, int64_t n_k, int64_t n_v, float scale) {
-    constexpr int RPT = D / P;        // rows a lane holds
-    constexpr int CPW = 64 / P;       // columns a wave holds
-    constexpr int CW = 4 * CPW;       // columns a workgroup holds
-    static_assert(RPT % 4 == 0, "rows a lane must be whole float4s");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int part = lane / CPW, ci = lane % CPW;
-    const int64_t h = blockIdx.x;
-    const int64_t kk = h % n_k;
-    const int e = (int)blockIdx.y * CW + wave * CPW + ci;  // this lane's column
-    const int i0 = part * RPT;                              // its first row
+// Sum over each aligned group of G (8 or 16) lanes, every lane getting the
+// sum, through DPP lane moves (no LDS path): lane ^ 1, lane ^ 2 within a
+// quad, then the 8-lane and 16-lane mirrors.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(G == 8 || G == 16, "DPP groups of 8 or 16 lanes");
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    if constexpr (G == 16) v += dpp_mov<0x140>(v);  // row_mirror
+    return v;
+}
 
-    float* S = state + h * (int64_t)D * D;
+struct ScanArgs {
+    const float* q;        // [T][n_k][D]: raw (FUSED) or normalised (workspace)
+    const float* k;
+    const float* v;        // [T][n_v][D]
+    const float* alpha;    // [T][n_v]: raw alpha (FUSED) or the decay (workspace)
+    const float* beta;     // [T][n_v]: raw beta (FUSED) or the gate (workspace)
+    const float* a_log;    // [n_v] (FUSED)
+    const float* dt_bias;  // [n_v] (FUSED)
+    float* state;          // [n_v][D][D]
+    float* outs;           // [T][n_v][D]
+    int64_t T, n_k, n_v;
+    float scale, eps;
+};
+
+// One token's operands for a lane: its RPT rows of kn and qn, v of its column,
+// the head's decay and gate.
+template <int D, int RPT>
+struct TokenOps {
+    float k[RPT], q[RPT];
+    float v, dec, b;
+};
+
+// A token's loads (q / k raw when FUSED, else normalised by ssm_prep_kernel;
+// alpha / beta raw when FUSED, else the decay and gate).
+template <int D, int RPT, bool FUSED>
+__device__ __forceinline__ void load_token(const ScanArgs& a, int64_t t, int64_t h, int64_t kk,
+                                           int e, int i0, TokenOps<D, RPT>& o) {
+    const float4* k4 = reinterpret_cast<const float4*>(a.k + (t * a.n_k + kk) * D + i0);
+    const float4* q4 = reinterpret_cast<const float4*>(a.q + (t * a.n_k + kk) * D + i0);
+#pragma unroll
+    for (int j = 0; j < RPT / 4; ++j) {
+        const float4 x = k4[j], y = q4[j];
+        o.k[4 * j] = x.x; o.k[4 * j + 1] = x.y; o.k[4 * j + 2] = x.z; o.k[4 * j + 3] = x.w;
+        o.q[4 * j] = y.x; o.q[4 * j + 1] = y.y; o.q[4 * j + 2] = y.z; o.q[4 * j + 3] = y.w;
+    }
+    o.v = a.v[(t * a.n_v + h) * D + e];
+    o.dec = a.alpha[t * a.n_v + h];
+    o.b = a.beta[t * a.n_v + h];
+}
+
+// FUSED (short scans): normalise q / k (a wave reduction for each norm) and
+// compute the decay and gate, when the token is used.
+template <int D, int RPT, bool FUSED>
+__device__ __forceinline__ void finish_token(const ScanArgs& a, int64_t t, int64_t h,
+                                             int64_t kk, int lane, TokenOps<D, RPT>& o) {
+    if constexpr (FUSED) {
+        const float* kr = a.k + (t * a.n_k + kk) * D;
+        const float* qr = a.q + (t * a.n_k + kk) * D;
+        float sk = 0.0f, sq = 0.0f;
+#pragma unroll
+        for (int i = lane; i < D; i += 64) {
+            sk += kr[i] * kr[i];
+            sq += qr[i] * qr[i];
+        }
+        sk = group_sum<64>(sk);
+        sq = group_sum<64>(sq);
+        const float nk = fmaxf(sqrtf(sk), a.eps), nq = fmaxf(sqrtf(sq), a.eps);
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+            o.k[j] = o.k[j] / nk;
+            o.q[j] = o.q[j] / nq;
+        }
+        float g = a.a_log[h] * softplus_dev(o.dec + a.dt_bias[h]);
+        if (g > 0.0f) g = 0.0f;
+        o.dec = expf(g);
+        o.b = 1.0f / (1.0f + expf(-o.b));
+    }
+}
+
+// P adjacent lanes share a column (lane = ci * P + part), each holding RPT =
+// D / P consecutive rows; a wave holds CPW = 64 / P columns, the workgroup CW
+// = 4 * CPW. The state tile passes through LDS at the start and the end, so
+// its global reads and writes are row-contiguous.
+template <int D, int P, bool FUSED>
+__global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(ScanArgs a) {
+    constexpr int RPT = D / P;
+    constexpr int CPW = 64 / P;
+    constexpr int CW = 4 * CPW;
+    constexpr int LD = D + 4;  // LDS column stride (floats)
+    static_assert(RPT % 4 == 0, "rows a lane must be whole float4s");
+    __shared__ __align__(16) float tile[CW * LD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int part = lane % P, ci = lane / P;
+    const int64_t h = blockIdx.x;
+    const int64_t kk = h % a.n_k;
+    const int e0 = (int)blockIdx.y * CW;
+    const int c = wave * CPW + ci;  // this lane's column within the tile
+    const int e = e0 + c;
+    const int i0 = part * RPT;
+
+    float* S = a.state + h * (int64_t)D * D;
+    for (int f = threadIdx.x; f < D * CW; f += kScanThreads) {
+        const int i = f / CW, cc = f % CW;
+        tile[cc * LD + i] = S[(int64_t)i * D + e0 + cc];
+    }
+    __syncthreads();
     float s[RPT];
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) s[j] = S[(int64_t)(i0 + j) * D + e];
+    for (int j = 0; j < RPT; j += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(&tile[c * LD + i0 + j]);
+        s[j] = x.x; s[j + 1] = x.y; s[j + 2] = x.z; s[j + 3] = x.w;
+    }
 
-    // token t's operands; the next token's are loaded while t is computed
-    // (the last token's again at the end: in bounds, no branch)
-    float kc[RPT], qc[RPT], kx[RPT], qx[RPT];
-    float vc, dc, bc, vx, dx, bx;
-    auto load = [&](int64_t t, float (&kr)[RPT], float (&qr)[RPT], float& vr, float& dr,
-                    float& br) {
-        const float4* k4 = reinterpret_cast<const float4*>(kn + (t * n_k + kk) * D + i0);
-        const float4* q4 = reinterpret_cast<const float4*>(qn + (t * n_k + kk) * D + i0);
-#pragma unroll
-        for (int j = 0; j < RPT / 4; ++j) {
-            const float4 a = k4[j], c = q4[j];
-            kr[4 * j] = a.x; kr[4 * j + 1] = a.y; kr[4 * j + 2] = a.z; kr[4 * j + 3] = a.w;
-            qr[4 * j] = c.x; qr[4 * j + 1] = c.y; qr[4 * j + 2] = c.z; qr[4 * j + 3] = c.w;
-        }
-        vr = v[(t * n_v + h) * D + e];
-        dr = dec[t * n_v + h];
-        br = bb[t * n_v + h];
-    };
-    load(0, kc, qc, vc, dc, bc);
-    for (int64_t t = 0; t < T; ++t) {
-        load(min(t + 1, T - 1), kx, qx, vx, dx, bx);
+    // the delta-rule update of this lane's rows for one token
+    auto step = [&](TokenOps<D, RPT>& o, int64_t t) __attribute__((always_inline)) {
+        finish_token<D, RPT, FUSED>(a, t, h, kk, lane, o);
         float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < RPT; j += 2) {
-            s[j] *= dc;
-            s[j + 1] *= dc;
-            p0 = __builtin_fmaf(kc[j], s[j], p0);
-            p1 = __builtin_fmaf(kc[j + 1], s[j + 1], p1);
+            s[j] *= o.dec;
+            s[j + 1] *= o.dec;
+            p0 = __builtin_fmaf(o.k[j], s[j], p0);
+            p1 = __builtin_fmaf(o.k[j + 1], s[j + 1], p1);
         }
-        float vp = p0 + p1;
-#pragma unroll
-        for (int m = CPW; m < 64; m <<= 1) vp += __shfl_xor(vp, m);
-        const float vnew = (vc - vp) * bc;
+        const float vp = lane_group_sum<P>(p0 + p1);
+        const float vnew = (o.v - vp) * o.b;
         float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < RPT; j += 2) {
-            s[j] = __builtin_fmaf(kc[j], vnew, s[j]);
-            s[j + 1] = __builtin_fmaf(kc[j + 1], vnew, s[j + 1]);
-            o0 = __builtin_fmaf(qc[j], s[j], o0);
-            o1 = __builtin_fmaf(qc[j + 1], s[j + 1], o1);
+            s[j] = __builtin_fmaf(o.k[j], vnew, s[j]);
+            s[j + 1] = __builtin_fmaf(o.k[j + 1], vnew, s[j + 1]);
+            o0 = __builtin_fmaf(o.q[j], s[j], o0);
+            o1 = __builtin_fmaf(o.q[j + 1], s[j + 1], o1);
         }
-        float o = o0 + o1;
+        const float r = lane_group_sum<P>(o0 + o1);
+        if (part == 0) a.outs[(t * a.n_v + h) * D + e] = a.scale * r;
+    };
+    // a ring of kDepth tokens' operands in flight: slot u holds token t + u
+    // and is refilled with token t + u + kDepth once used (clamped to the last
+    // token: in bounds, no branch); slots are static in the unrolled body
+    TokenOps<D, RPT> ring[kDepth];
 #pragma unroll
-        for (int m = CPW; m < 64; m <<= 1) o += __shfl_xor(o, m);
-        if (part == 0) outs[(t * n_v + h) * D + e] = scale * o;
+    for (int u = 0; u < kDepth; ++u)
+        load_token<D, RPT, FUSED>(a, min((int64_t)u, a.T - 1), h, kk, e, i0, ring[u]);
+    int64_t t = 0;
+    for (; t + kDepth <= a.T; t += kDepth) {
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            kc[j] = kx[j];
-            qc[j] = qx[j];
+        for (int u = 0; u < kDepth; ++u) {
+            step(ring[u], t + u);
+            load_token<D, RPT, FUSED>(a, min(t + u + kDepth, a.T - 1), h, kk, e, i0, ring[u]);
         }
-        vc = vx;
-        dc = dx;
-        bc = bx;
     }
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) S[(int64_t)(i0 + j) * D + e] = s[j];
+    for (int u = 0; u < kDepth; ++u)
+        if (t + u < a.T) step(ring[u], t + u);
+
+#pragma unroll
+    for (int j = 0; j < RPT; j += 4)
+        *reinterpret_cast<float4*>(&tile[c * LD + i0 + j]) = make_float4(s[j], s[j + 1],
+                                                                           s[j + 2], s[j + 3]);
+    __syncthreads();
+    for (int f = threadIdx.x; f < D * CW; f += kScanThreads) {
+        const int i = f / CW, cc = f % CW;
+        S[(int64_t)i * D + e0 + cc] = tile[cc * LD + i];
+    }
 }
 
 // out[t, c] = sum_j buf[tl + t + 1 - K + j, c] * w[c, j] over the rows that
@@ -170,6 +265,47 @@ __global__ __launch_bounds__(256) void ssm_conv_kernel(const float* __restrict__
         acc = acc + in * w[c * K + j];
     }
     out[idx] = acc;
+}
+
+// The same conv with K fixed: a lane owns channel c for TB consecutive
+// tokens, holding its K weights and a sliding window of K inputs in
+// registers, so each input is loaded once (plus K - 1 rows of halo a block).
+// Taps before the start of the history are skipped, as above.
+template <int K, int TB>
+__global__ __launch_bounds__(256) void ssm_conv_k_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ tail,
+                                                         float* __restrict__ out, int64_t tl,
+                                                         int64_t T, int64_t C) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= C) return;
+    const int64_t t0 = (int64_t)blockIdx.y * TB;
+    float wr[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) wr[j] = w[c * K + j];
+    float win[K];
+    bool ok[K];
+    auto fetch = [&](int64_t b, float& val, bool& has) {
+        has = b >= 0;
+        val = b < 0 ? 0.0f : (b < tl ? tail[b * C + c] : x[(b - tl) * C + c]);
+    };
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) fetch(tl + t0 + 1 - K + j, win[j], ok[j]);
+    for (int tt = 0; tt < TB; ++tt) {
+        const int64_t t = t0 + tt;
+        if (t >= T) break;
+        fetch(tl + t, win[K - 1], ok[K - 1]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < K; ++j)
+            if (ok[j]) acc = acc + win[j] * wr[j];
+        out[t * C + c] = acc;
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) {
+            win[j] = win[j + 1];
+            ok[j] = ok[j + 1];
+        }
+    }
 }
 
 // The new tail: the last keep rows of buf, per channel; a lane reads all of
@@ -196,13 +332,18 @@ __global__ __launch_bounds__(256) void ssm_conv_tail_kernel(const float* __restr
     }
 }
 
-using ScanKernel = void (*)(const float*, const float*, const float*, const float*,
-                            const float*, float*, float*, int64_t, int64_t, int64_t, float);
+using ScanKernel = void (*)(ScanArgs);
 
-ScanKernel pick_scan(int64_t d, int p) {
-    if (d == 128) return p == 16 ? ssm_scan_kernel<128, 16> : ssm_scan_kernel<128, 8>;
-    if (d == 64) return p == 16 ? ssm_scan_kernel<64, 16> : ssm_scan_kernel<64, 8>;
-    if (d == 256) return ssm_scan_kernel<256, 16>;
+template <int D, int P>
+ScanKernel pick_scan_f(bool fused) {
+    return fused ? ssm_scan_kernel<D, P, true> : ssm_scan_kernel<D, P, false>;
+}
+
+// P = lanes a column: 16 (8 rows a lane) by default; 8 keeps 16 rows a lane.
+ScanKernel pick_scan(int64_t d, int p, bool fused) {
+    if (d == 128) return p == 8 ? pick_scan_f<128, 8>(fused) : pick_scan_f<128, 16>(fused);
+    if (d == 64) return p == 8 ? pick_scan_f<64, 8>(fused) : pick_scan_f<64, 16>(fused);
+    if (d == 256) return pick_scan_f<256, 16>(fused);
     return nullptr;
 }
 
@@ -228,25 +369,31 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
         set_error("ssm_scan: null pointer");
         return false;
     }
-    const int p = tune("ssm_parts", 8);
-    ScanKernel kern = pick_scan(d, p);
+    const int P = (d == 256 || tune("ssm_parts", 16) != 8) ? 16 : 8;
+    const bool fused = T <= tune("ssm_fuse_tokens", 16);
+    ScanKernel kern = pick_scan(d, P, fused);
     if (kern == nullptr) {
         set_error("ssm_scan: head dim %lld not in {64, 128, 256}", (long long)d);
         return false;
     }
-    const int P = d == 256 ? 16 : (p == 16 ? 16 : 8);
     if (!aligned16(q) || !aligned16(k) || !aligned16(state) || !aligned16(workspace)) {
         set_error("ssm_scan: q, k, state and workspace must be 16-byte aligned");
         return false;
+    }
+    if (n_v > 0x7fffffff || T * n_k > 0x7fffffff) {
+        set_error("ssm_scan: grid too large");
+        return false;
+    }
+    const int64_t cw = 4 * (64 / P);
+    const dim3 grid((unsigned)n_v, (unsigned)(d / cw));
+    if (fused) {
+        ScanArgs sa{q, k, v, alpha, beta, a_log, dt_bias, state, outs, T, n_k, n_v, scale, eps};
+        return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);
     }
     const int64_t need = ssm_workspace_bytes(T, n_k, n_v, d);
     if (workspace == nullptr || ws_bytes < need) {
         set_error("ssm_scan: workspace %lld bytes < %lld needed", (long long)ws_bytes,
                   (long long)need);
-        return false;
-    }
-    if (T * n_k > 0x7fffffff || n_v > 65535) {
-        set_error("ssm_scan: grid too large");
         return false;
     }
     const auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
@@ -258,9 +405,8 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
     if (!launch("ssm_prep_kernel", ssm_prep_kernel, dim3((unsigned)(T * n_k)), dim3(64), 0, s,
                 q, k, alpha, beta, a_log, dt_bias, qn, kn, dc, bb, n_k, n_v, d, eps))
         return false;
-    const int64_t cw = 4 * (64 / P);
-    return launch("ssm_scan_kernel", kern, dim3((unsigned)n_v, (unsigned)(d / cw)),
-                  dim3(kScanThreads), 0, s, qn, kn, v, dc, bb, state, outs, T, n_k, n_v, scale);
+    ScanArgs sa{qn, kn, v, dc, bb, nullptr, nullptr, state, outs, T, n_k, n_v, scale, eps};
+    return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);
 }
 
 bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tail_len,
@@ -283,9 +429,17 @@ bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tai
         set_error("ssm_conv: too large");
         return false;
     }
-    if (T > 0 && !launch("ssm_conv_kernel", ssm_conv_kernel, dim3((unsigned)((T * C + 255) / 256)),
-                         dim3(256), 0, s, x, w, tail, out, tail_len, T, C, (int)K))
-        return false;
+    constexpr int kTB = 32;
+    if (T > 0) {
+        const bool ok =
+            (K == 4 && (T + kTB - 1) / kTB <= 65535)
+                ? launch("ssm_conv_kernel", ssm_conv_k_kernel<4, kTB>,
+                         dim3((unsigned)((C + 255) / 256), (unsigned)((T + kTB - 1) / kTB)),
+                         dim3(256), 0, s, x, w, tail, out, tail_len, T, C)
+                : launch("ssm_conv_kernel", ssm_conv_kernel, dim3((unsigned)((T * C + 255) / 256)),
+                         dim3(256), 0, s, x, w, tail, out, tail_len, T, C, (int)K);
+        if (!ok) return false;
+    }
     if (keep > 0 && !launch("ssm_conv_tail_kernel", ssm_conv_tail_kernel,
                             dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s, x, tail,
                             tail_out, tail_len, T, C, (int)keep))

@@ -33,6 +33,7 @@ single-threaded like the reference, over a bounded sample.
     python bench.py --gemm              # quantised GEMM (prefill projections)
     python bench.py --attention         # attention over a KV cache (decode, prefill)
     python bench.py --gguf              # GGUF parse, upload to HBM, device row addressing
+    python bench.py --ssm               # gated DeltaNet scan and conv
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
 """
@@ -73,6 +74,8 @@ def parse_args(argv=None):
     p.add_argument("--variants", action="store_true",
                    help="every op variant at the Llama-3-8B 512-token geometry")
     p.add_argument("--gemv", action="store_true", help="quantised GEMV cases")
+    p.add_argument("--ssm", action="store_true",
+                   help="gated DeltaNet scan and causal conv (Qwen3-Next heads)")
     p.add_argument("--gguf", action="store_true",
                    help="GGUF parse, file-to-HBM upload and device row addressing")
     p.add_argument("--attention", action="store_true",
@@ -510,6 +513,8 @@ def main(argv=None):
         return attention_bench(a)
     if a.gguf:
         return gguf_bench(a)
+    if a.ssm:
+        return ssm_bench(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -1017,6 +1022,120 @@ def gguf_bench(a):
             os.rmdir(tmp)
         except OSError:
             pass
+    return 0
+
+
+SSM_CASES = [
+    # (name, tokens): Qwen3-Next linear-attention heads, 16 key heads, 32 value
+    # heads, d 128; qkv conv over 2*16*128 + 32*128 = 8192 channels, kernel 4
+    ("decode", 1), ("prefill_4096", 4096),
+]
+
+
+def ssm_bench(a):
+    """Gated DeltaNet: per-kernel device times (an event pair per kernel) of
+    the prep pass, the scan and the conv; decode against the HBM bytes of the
+    state it reads and writes, prefill per token; the reference's C++ on a
+    bounded sample of the same shapes beside it."""
+    from aero_amd import ops
+    from aero_amd.device import DeviceArray as DA, Event, Stream, time_next_kernel
+
+    n_k, n_v, d, C, K = 16, 32, 128, 8192, 4
+    rng = np.random.default_rng(0)
+    stream = Stream()
+    for name, T in SSM_CASES:
+        f = lambda *s: DA.from_numpy(rng.standard_normal(s).astype(np.float32))
+        q, k, v = f(T, n_k, d), f(T, n_k, d), f(T, n_v, d)
+        al, bt = f(T, n_v), f(T, n_v)
+        a_log = DA.from_numpy((-np.abs(rng.standard_normal(n_v)) * 0.5).astype(np.float32))
+        dtb = f(n_v)
+        # decode rotates over 64 layer states (> 256 MB together) so no state
+        # is still in the 256 MiB cache from its previous step
+        n_states = 64 if T == 1 else 1
+        states = [DA.from_numpy((rng.standard_normal((n_v, d, d)) * 0.1).astype(np.float32))
+                  for _ in range(n_states)]
+        outs = DA.empty((T, n_v, d))
+        x, w = f(T, C), f(C, K)
+        tail = DA.empty((K - 1) * C)
+        cout = DA.empty((T, C))
+        reps = a.steps if T == 1 else max(3, a.steps // 20)
+        times = {"prep": [], "conv": []}
+        for it in range(a.warmup + reps):
+            st = states[it % n_states]
+            pp, pc = (Event(), Event()), (Event(), Event())
+            time_next_kernel(*pp)          # the op's first kernel: the prep pass
+            ops.ssm_scan(q, k, v, al, bt, a_log, dtb, st, outs, T, n_k, n_v, d,
+                         1.0 / np.sqrt(d), stream=stream)
+            time_next_kernel(*pc)          # the conv kernel
+            ops.ssm_conv(x, w, tail, K - 1 if it else 0, tail, cout, T, C, K, stream=stream)
+            stream.synchronize()
+            if it >= a.warmup:
+                times["prep"].append(pp[0].elapsed_ms(pp[1]) * 1e3)
+                times["conv"].append(pc[0].elapsed_ms(pc[1]) * 1e3)
+        # the whole op (prep + scan) back to back; the scan is the rest
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for it in range(reps):
+            ops.ssm_scan(q, k, v, al, bt, a_log, dtb, states[it % n_states], outs, T, n_k, n_v,
+                         d, 1.0 / np.sqrt(d), stream=stream)
+        e1.record(stream)
+        e1.synchronize()
+        op_us = e0.elapsed_ms(e1) * 1e3 / reps
+        # short scans (up to 16 tokens) are one kernel, whose time the first
+        # event pair measured; longer ones a prep pass and the scan
+        fused = T <= 16
+        prep_us = 0.0 if fused else statistics.mean(times["prep"])
+        scan_us = op_us - prep_us
+        conv_us = statistics.mean(times["conv"])
+        state_bytes = 2 * n_v * d * d * 4
+        io_bytes = 4 * T * (2 * n_k * d + 2 * n_v * d + 2 * n_v)
+        conv_bytes = 4 * (2 * T * C + C * K)
+        res = {"case": name, "tokens": T, "heads": [n_k, n_v], "d": d,
+               "ssm_op_us": round(op_us, 3), "kernels": 1 if fused else 2,
+               "prep_us": round(prep_us, 3), "scan_us": round(scan_us, 3),
+               "conv_us": round(conv_us, 3),
+               "conv_GB/s": round(conv_bytes / (conv_us * 1e-6) / 1e9, 1)}
+        if T == 1:
+            g = (state_bytes + io_bytes) / (op_us * 1e-6) / 1e9
+            res["roofline"] = {"bound": "hbm", "achieved": round(g, 1), "peak": HBM_PEAK_GBS,
+                               "unit": "GB/s", "frac": round(g / HBM_PEAK_GBS, 4),
+                               "bytes": state_bytes + io_bytes,
+                               "note": "state read + written once, q/k/v/out; whole op"}
+        else:
+            res["us_per_token"] = round(op_us / T, 4)
+            g = conv_bytes / (conv_us * 1e-6) / 1e9
+            res["roofline"] = {"bound": "hbm", "achieved": round(g, 1), "peak": HBM_PEAK_GBS,
+                               "unit": "GB/s", "frac": round(g / HBM_PEAK_GBS, 4),
+                               "kernel": "ssm_conv_kernel", "bytes": conv_bytes}
+        if not a.no_cpu:
+            from oracle import refbind
+            if refbind.ssm() is not None:
+                Ts = min(T, 8)
+                hq = rng.standard_normal((Ts, n_k, d)).astype(np.float32)
+                hv = rng.standard_normal((Ts, n_v, d)).astype(np.float32)
+                ha = rng.standard_normal((Ts, n_v)).astype(np.float32)
+                hs = (rng.standard_normal((n_v, d, d)) * 0.1).astype(np.float32)
+                hl = (-np.abs(rng.standard_normal(n_v)) * 0.5).astype(np.float32)
+                reps_c, t0 = 0, time.perf_counter()
+                while reps_c == 0 or time.perf_counter() - t0 < 1.0:
+                    refbind.ssm_scan(hq, hq, hv, ha, ha, hl, hl, hs, 0.088)
+                    reps_c += 1
+                per_tok = (time.perf_counter() - t0) / (reps_c * Ts) * 1e6
+                hx = rng.standard_normal((Ts, C)).astype(np.float32)
+                hw = rng.standard_normal((C, K)).astype(np.float32)
+                reps_v, t0 = 0, time.perf_counter()
+                while reps_v == 0 or time.perf_counter() - t0 < 0.5:
+                    refbind.ssm_conv(hx, hw, None, 0)
+                    reps_v += 1
+                conv_tok = (time.perf_counter() - t0) / (reps_v * Ts) * 1e6
+                res["cpu_baseline"] = {"scan_us": round(per_tok * T, 1),
+                                       "conv_us": round(conv_tok * T, 1), "kind": "reference",
+                                       "cores": 1,
+                                       "sample": f"aero_ssm_scan / aero_ssm_conv on {Ts} tokens "
+                                                 f"({reps_c} / {reps_v} calls), per token x {T}"}
+                res["speedup_vs_cpu_scan"] = round(per_tok * T / op_us, 1)
+        print(json.dumps(res), flush=True)
+    stream.destroy()
     return 0
 
 
