@@ -114,6 +114,9 @@ PROTOTYPES = {
     "aero_gguf_read": (c_int, [vp, ctypes.c_char_p, c_int64, c_int64, vp]),
     "aero_gguf_upload": (c_int, [vp, ctypes.c_char_p, c_int64, c_int64, vp, vp]),
     "aero_hip_matvec": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp]),
+    "aero_hip_matmul_workspace": (c_int64, [c_int, c_int64, c_int64]),
+    "aero_hip_matmul": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp,
+                                c_int64, vp]),
     "aero_hip_attention_workspace": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64,
                                                c_int64]),
     "aero_hip_attention": (c_int, [vp, c_int, vp, vp, vp, vp, vp, c_int64, c_int64, c_int64,

@@ -35,7 +35,9 @@ bool dequant_dev(int dtype, const uint8_t* raw, int64_t raw_len, float* out,
 int64_t dtype_block_bytes(int t);
 int64_t dtype_block_values(int t);
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
-              int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s);
+              int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s, void* ws,
+              int64_t ws_bytes);
+int64_t split_gemm_workspace(int dtype, int64_t n_cols, int64_t n_tok);
 bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scale, const void* v,
                    const float* v_scale, float* out, int64_t n_q, int64_t n_head,
                    int64_t n_head_kv, int64_t head_dim, int64_t value_dim, float scale,
@@ -391,13 +393,17 @@ static int host_gemv(int t, const uint8_t* w, const float* X, float* Y, int64_t 
     }
     const size_t wbytes = (size_t)(n_rows * (n_cols / bv) * bb);
     const size_t xbytes = (size_t)(n_tok * n_cols) * 4, ybytes = (size_t)(n_tok * n_rows) * 4;
+    // many tokens of Q4_K / Q5_K: the split-x GEMM's workspace as a fourth buffer
+    const int64_t wsb = n_tok >= 32 ? aero::split_gemm_workspace(t, n_cols, n_tok) : 0;
     aero::Staging st;
-    void* p[3];
-    if (!st.reserve({wbytes, xbytes, ybytes}, p)) return 0;
+    void* p[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (!(wsb > 0 ? st.reserve({wbytes, xbytes, ybytes, (size_t)wsb}, p)
+                  : st.reserve({wbytes, xbytes, ybytes}, p)))
+        return 0;
     const bool ok = st.h2d(p[0], w, wbytes) && st.h2d(p[1], X, xbytes) &&
                     aero::gemv_dev(t, static_cast<uint8_t*>(p[0]), (int64_t)wbytes,
                                    static_cast<float*>(p[1]), static_cast<float*>(p[2]), n_rows,
-                                   n_cols, n_tok, st.stream()) &&
+                                   n_cols, n_tok, st.stream(), p[3], wsb) &&
                     st.d2h(Y, p[2], ybytes) && st.finish();
     return ok ? 1 : 0;
 }

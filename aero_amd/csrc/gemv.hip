@@ -23,6 +23,10 @@ namespace aero {
 int64_t dtype_block_bytes(int t);
 bool gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
               int64_t n_cols, int64_t rb, int64_t n_tok, hipStream_t s);
+int64_t split_gemm_workspace(int dtype, int64_t n_cols, int64_t n_tok);
+bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
+                    int64_t n_cols, int64_t rb, int64_t n_tok, void* ws, int64_t ws_bytes,
+                    hipStream_t s, bool* ran);
 int64_t dtype_block_values(int t);
 
 namespace {
@@ -1104,7 +1108,8 @@ GemvKernel pick_gemv(int dtype, int R, int T) {
 // y[t, r] for t < n_tok: tokens are taken in groups of up to 4 per launch
 // (each group re-reads W; a token-tiled GEMM is the prefill path).
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
-              int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s) {
+              int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s, void* ws,
+              int64_t ws_bytes) {
     const int64_t bv = dtype_block_values(dtype), bb = dtype_block_bytes(dtype);
     const bool quant = dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q4_K ||
                        dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q6_K ||
@@ -1132,9 +1137,17 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         return false;
     }
     if (n_rows == 0 || n_tok == 0) return true;
-    // many tokens: the matrix-core GEMM reads W once per 64 tokens
-    if (n_tok >= tune("gemm_min_tokens", 32) && n_tok <= (int64_t)1 << 30)
+    // many tokens: the matrix-core GEMMs (the split-x fp16 one when a
+    // workspace is given and the type has it; else fp32, W once per 64 tokens)
+    if (n_tok >= tune("gemm_min_tokens", 32) && n_tok <= (int64_t)1 << 30) {
+        if (ws != nullptr) {
+            bool ran = false;
+            if (!split_gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, ws, ws_bytes, s, &ran))
+                return false;
+            if (ran) return true;
+        }
         return gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, s);
+    }
     if (aligned16(w) && rb % 16 == 0 && tune("gemv_lanes64", 1)) {
         const bool pipe = n_cols > kStepCols;
         const int t_max = pipe ? 2 : 4;  // double-buffered x of 4 tokens would fill LDS
@@ -1195,7 +1208,18 @@ extern "C" {
 int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
                     int64_t n_rows, int64_t n_cols, int64_t n_tok, void* stream) {
     return aero::gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok,
-                          (hipStream_t)stream) ? 1 : 0;
+                          (hipStream_t)stream, nullptr, 0) ? 1 : 0;
+}
+
+int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok) {
+    return aero::split_gemm_workspace(dtype, n_cols, n_tok);
+}
+
+int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
+                    int64_t n_rows, int64_t n_cols, int64_t n_tok, void* ws, int64_t ws_bytes,
+                    void* stream) {
+    return aero::gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok, (hipStream_t)stream,
+                          ws, ws_bytes) ? 1 : 0;
 }
 
 }  // extern "C"

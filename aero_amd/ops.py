@@ -184,10 +184,16 @@ def dequant(dtype: int, raw: DeviceArray, out: DeviceArray, n_values: int,
                                            _s(stream)), "dequant")
 
 
+_gemm_ws: dict = {}
+
+
 def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: int,
-           n_cols: int, n_tok: int = 1, stream: Stream | None = None) -> None:
+           n_cols: int, n_tok: int = 1, stream: Stream | None = None,
+           split: bool = True) -> None:
     """y[t, r] = sum_c W[r, c] * x[t, c] for t < n_tok: W n_rows rows of quant
-    blocks (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS), x [n_tok, n_cols], y [n_tok, n_rows]."""
+    blocks (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS), x [n_tok, n_cols], y [n_tok, n_rows].
+    From 32 tokens, Q4_K / Q5_K run the split-x fp16 matrix-core GEMM with a
+    cached workspace (split=False: the fp32 matrix-core GEMM)."""
     if dtype not in _BLOCK or _BLOCK[dtype][0] == 1:
         raise ValueError(f"dtype {dtype} has no quantised GEMV")
     bv, bb = _BLOCK[dtype]
@@ -197,8 +203,18 @@ def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: i
         raise ValueError("weight buffer too short")
     _need(x, n_tok * n_cols, np.float32, "x")
     _need(y, n_tok * n_rows, np.float32, "y")
-    _lib.check(_lib.lib().aero_hip_matvec(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows,
-                                          n_cols, n_tok, _s(stream)), "matvec")
+    L = _lib.lib()
+    wsb = int(L.aero_hip_matmul_workspace(int(dtype), n_cols, n_tok)) if n_tok >= 32 else 0
+    if wsb and split:
+        ws = _gemm_ws.get(wsb)
+        if ws is None:
+            _gemm_ws.clear()          # one workspace at a time: the largest recent size
+            ws = _gemm_ws[wsb] = DeviceArray.empty(wsb // 4, np.float32)
+        _lib.check(L.aero_hip_matmul(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows, n_cols,
+                                     n_tok, ws.ptr, wsb, _s(stream)), "matmul")
+        return
+    _lib.check(L.aero_hip_matvec(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows,
+                                 n_cols, n_tok, _s(stream)), "matvec")
 
 
 KV_F32, KV_INT8, KV_INT4 = 0, 1, 2

@@ -707,6 +707,7 @@ GEMM_CASES = [
     ("q6_k_14336x4096", 14, 14336, 4096, 512), ("ffn_gate_14336x4096_t64", 12, 14336, 4096, 64),
 ]
 MFMA_FP32_PEAK_TFLOPS = 157.3
+MFMA_FP16_PEAK_TFLOPS = 2500.0   # dense fp16 matrix peak of MI355X
 
 
 def gemm(a):
@@ -726,27 +727,33 @@ def gemm(a):
         X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
         Y = DA.empty((n_tok, n_rows))
         stream = Stream()
-        for w in ws:
-            ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok, stream=stream)
-        reps = 5
-        e0, e1 = Event(), Event()
-        e0.record(stream)
-        for _ in range(reps):
+        # Q4_K / Q5_K: the split-x fp16 GEMM (the default), then the fp32 one
+        paths = ["split_fp16", "fp32"] if t in (W.Q4_K, W.Q5_K) else ["fp32"]
+        for path in paths:
+            split = path == "split_fp16"
             for w in ws:
-                ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok, stream=stream)
-        e1.record(stream)
-        e1.synchronize()
-        us = e0.elapsed_ms(e1) * 1e3 / (reps * len(ws))
-        tf = 2.0 * n_rows * n_cols * n_tok / (us * 1e-6) / 1e12
-        res = {"case": name, "dtype": t, "n_rows": n_rows, "n_cols": n_cols, "tokens": n_tok,
-               "us": round(us, 2), "TFLOP/s": round(tf, 1),
-               "frac_fp32_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
-        if not a.no_cpu:
-            cu, kind, sample = cpu_matmul_us(t, n_rows, n_cols, n_tok)
-            res["cpu_baseline"] = {"us": round(cu, 1), "kind": kind, "cores": 1,
-                                   "sample": sample}
-            res["speedup_vs_cpu"] = round(cu / us, 1)
-        print(json.dumps(res), flush=True)
+                ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok, stream=stream, split=split)
+            reps = 5
+            e0, e1 = Event(), Event()
+            e0.record(stream)
+            for _ in range(reps):
+                for w in ws:
+                    ops.matvec(t, w, X, Y, n_rows, n_cols, n_tok, stream=stream, split=split)
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / (reps * len(ws))
+            tf = 2.0 * n_rows * n_cols * n_tok / (us * 1e-6) / 1e12
+            res = {"case": name, "path": path, "dtype": t, "n_rows": n_rows, "n_cols": n_cols,
+                   "tokens": n_tok, "us": round(us, 2), "TFLOP/s": round(tf, 1),
+                   "frac_fp32_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+            if split:
+                res["frac_fp16_mfma_3parts"] = round(3 * tf / MFMA_FP16_PEAK_TFLOPS, 4)
+            if not a.no_cpu and path == paths[0]:
+                cu, kind, sample = cpu_matmul_us(t, n_rows, n_cols, n_tok)
+                res["cpu_baseline"] = {"us": round(cu, 1), "kind": kind, "cores": 1,
+                                       "sample": sample}
+                res["speedup_vs_cpu"] = round(cu / us, 1)
+            print(json.dumps(res), flush=True)
         stream.destroy()
         del ws
     return 0

@@ -1,0 +1,128 @@
+"""GPU parity: the split-x fp16 matrix-core GEMM (aero_hip_matmul with a
+workspace, Q4_K / Q5_K, 32 or more tokens) against the oracle's restatement of
+the reference's matmul (src/kernels.cpp:337-404,520-538) and against the exact
+product.
+
+Tolerances: 1e-5 relative to the output's scale against the oracle (the
+reference's RTOL for fp32 ops, tests/test_transformer_native.py:34-37). Each
+token's x is scaled by a power of two and split into three fp16 parts, so
+values of at least 2^-16 of the token's largest are represented exactly; the
+tests below also check that claim at extreme and mixed magnitudes, where the
+result must equal the float64 product of the dequantised weights to ~1e-6 of
+the scale (fp32 accumulation).
+"""
+import numpy as np
+import pytest
+
+from conftest import RTOL, rel_to_scale
+from aero_amd import _lib, native, ops
+from aero_amd import workloads as W
+from aero_amd.device import DeviceArray as DA
+
+pytestmark = pytest.mark.gpu
+
+KTYPES = [W.Q4_K, W.Q5_K]
+
+
+def gpu_matmul(t, w, X, n_rows, split=True):
+    X = np.ascontiguousarray(np.atleast_2d(X), np.float32)
+    T, n_cols = X.shape
+    y = DA.empty((T, n_rows))
+    ops.matvec(t, DA.from_numpy(w), DA.from_numpy(X), y, n_rows, n_cols, T, split=split)
+    return y.numpy()
+
+
+def exact(oracle, t, w, X, n_rows):
+    """float64 X @ W^T over the reference's dequantised weights."""
+    n_cols = X.shape[1]
+    Wd = oracle.dequant(t, w, n_rows * n_cols).reshape(n_rows, n_cols).astype(np.float64)
+    return X.astype(np.float64) @ Wd.T
+
+
+def test_workspace_sizes(hip):
+    L = _lib.lib()
+    for t in KTYPES:
+        assert L.aero_hip_matmul_workspace(t, 4096, 512) >= 512 * 4096 * 6
+        assert L.aero_hip_matmul_workspace(t, 4096, 33) >= 64 * 4096 * 6  # padded to 32s
+        assert L.aero_hip_matmul_workspace(t, 100, 64) == 0                # not whole blocks
+    for t in (W.Q8_0, W.Q6_K, W.IQ4_XS, W.F32):
+        assert L.aero_hip_matmul_workspace(t, 4096, 512) == 0
+
+
+@pytest.mark.parametrize("t", KTYPES)
+@pytest.mark.parametrize("n_rows,n_cols,n_tok", [
+    (100, 1024, 40), (130, 2048, 33), (257, 4096, 100), (64, 14336, 64), (1000, 256, 32),
+    (129, 512, 95),
+])
+def test_split_gemm_vs_oracle(hip, oracle, t, n_rows, n_cols, n_tok):
+    """Partial row tiles (rows not a multiple of 128), partial token tiles (33,
+    40, 95, 100 tokens), one to 56 super-blocks a row."""
+    rng = np.random.default_rng(n_rows * 31 + n_cols + n_tok + t)
+    w = W.make_table(t, n_rows * n_cols // 256, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    print(f"split gemm type={t} rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+    assert rel_to_scale(got, gpu_matmul(t, w, X, n_rows, split=False)) <= RTOL
+
+
+@pytest.mark.parametrize("t", KTYPES)
+def test_split_gemm_magnitudes(hip, oracle, t):
+    """Tokens at 1e-30 and 1e30 scale, an all-zero token, a token of one
+    outlier among small values, fp32 subnormals and values equal to 2^-16 of
+    their token's largest: all within 1e-6 of the exact product's scale (per
+    token), the zero token exactly zero."""
+    rng = np.random.default_rng(5 + t)
+    n_rows, n_cols = 96, 1024
+    w = W.make_table(t, n_rows * n_cols // 256, rng)
+    base = rng.standard_normal((8, n_cols)).astype(np.float32)
+    X = np.empty((40, n_cols), np.float32)
+    X[:] = rng.standard_normal((40, n_cols)).astype(np.float32)
+    X[0] = base[0] * np.float32(1e-30)
+    X[1] = base[1] * np.float32(1e30)
+    X[2] = 0.0
+    X[3] = base[3] * np.float32(1e-3)
+    X[3, 17] = 1e4                                      # outlier among small values
+    X[4] = base[4] * np.float32(1e-41)                  # fp32 subnormals
+    X[5] = np.float32(1.0)
+    X[5, ::3] = np.float32(2.0 ** -16)                  # the exactness threshold
+    got = gpu_matmul(t, w, X, n_rows).astype(np.float64)
+    want = exact(oracle, t, w, X, n_rows)
+    assert not got[2].any()
+    for i in range(40):
+        if i == 2:
+            continue
+        scale = np.abs(want[i]).max()
+        assert np.abs(got[i] - want[i]).max() <= 1e-6 * scale, i
+
+
+def test_split_gemm_nt4_vs_oracle(hip, oracle):
+    """8192 x 4096 Q4_K with 512 tokens: 512 workgroups of 256 rows (64 rows a
+    wave); tokens sampled from every 32-token tile against the oracle."""
+    rng = np.random.default_rng(17)
+    n_rows, n_cols, n_tok = 8192, 4096, 512
+    w = W.make_table(W.Q4_K, n_rows * n_cols // 256, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    got = gpu_matmul(W.Q4_K, w, X, n_rows)
+    idx = np.arange(5, n_tok, 32)
+    assert rel_to_scale(got[idx], oracle.matmul(W.Q4_K, w, X[idx], n_rows)) <= RTOL
+
+
+def test_split_gemm_small_workspace_and_host_abi(hip, oracle):
+    """A workspace below aero_hip_matmul_workspace takes the fp32 GEMM (same
+    results to the tolerance); the reference-compatible aero_matmul (host
+    arrays) runs the split path with its own workspace."""
+    rng = np.random.default_rng(23)
+    n_rows, n_cols, n_tok = 200, 2048, 64
+    w = W.make_table(W.Q4_K, n_rows * n_cols // 256, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    want = oracle.matmul(W.Q4_K, w, X, n_rows)
+    L = _lib.lib()
+    need = int(L.aero_hip_matmul_workspace(W.Q4_K, n_cols, n_tok))
+    ws = DA.empty(need // 8, np.float32)                 # half the bytes needed
+    dw, dx, dy = DA.from_numpy(w), DA.from_numpy(X), DA.empty((n_tok, n_rows))
+    assert L.aero_hip_matmul(W.Q4_K, dw.ptr, dw.nbytes, dx.ptr, dy.ptr, n_rows, n_cols, n_tok,
+                             ws.ptr, ws.nbytes, None) == 1
+    assert rel_to_scale(dy.numpy(), want) <= RTOL
+    Y = native.matmul(W.Q4_K, w.tobytes(), X)
+    assert rel_to_scale(Y, want) <= RTOL
