@@ -7,20 +7,21 @@
 // fp16 scales d, dmin and per-32-value 6-bit sc, m (src/kernels.cpp:337-404).
 // sc*q <= 63*31 is an integer below 2048, exact in fp16, so per super-block
 //   sum_c w_c x_c = d * sum_c (sc*q)_c x_c  -  dmin * sum_g m_g * S_g
-// with S_g the sum of x over sub-block g. Each token's x is scaled by a power
-// of two 2^(15-e) (e the exponent of its largest finite |x|, so the scaled
-// values lie below 2^15) and split into three fp16 parts hi + mid + lo: every
-// value of at least 2^-16 of the token's largest is represented exactly,
-// smaller ones to 2^-25 absolute in the scaled units (2^-39 of the largest).
-// Products of fp16 integers and fp16 parts are exact; the matrix cores add
-// them in fp32. The reference dequantises each value to fp32 and sums the
+// with S_g the sum of x over sub-block g. Each token's x is scaled, per
+// super-block, by a power of two 2^(15-e) (e the exponent of the block's
+// largest finite |x|, so the scaled values lie below 2^15) and split into
+// three fp16 parts hi + mid + lo: every value of at least 2^-16 of the
+// block's largest is represented exactly, smaller ones to 2^-25 absolute in
+// the scaled units (2^-39 of the largest). Products of fp16 integers and fp16
+// parts are exact; the matrix cores add them in fp32, and each super-block's
+// sum is scaled back (by 2^(e-15)) as it is added to the row's fp32 total. The reference dequantises each value to fp32 and sums the
 // rounded products serially; results differ from it by fp32 rounding only.
 //
 // Kernels:
-//   xscale_kernel   one workgroup a token: the per-token scale and the
-//                   sub-block sums S of the scaled x (fp32);
-//   xsplit_kernel   the fp16 parts of x in matrix-operand order, padded to
-//                   32 tokens with zeros;
+//   xsplit_kernel   one workgroup a 16-token tile and super-block: the scale,
+//                   the fp16 parts of x in matrix-operand order (padded to
+//                   32 tokens with zeros) and the sub-block sums S of the
+//                   scaled x (fp32);
 //   split_gemm_kernel  4 waves, 256 rows x 32 tokens. y^T is computed as
 //                   x^T W^T so that the weights are the B operand: lane l
 //                   holds B[k][n = l%16] for k = 8(l/16)..+7, i.e. 8 values
@@ -31,15 +32,17 @@
 //                   double-buffered per 128-column chunk, shared by the four
 //                   waves.
 //
-// Operand order. Lane group g = l/16 of a row owns qs bytes 32g..32g+31 of
-// each super-block: sub-block 2g in the low nibbles, 2g+1 in the high. At
-// step s (0..7) of the super-block it uses byte dword s, and its 8 operand
-// values are, in order, columns 64g + 4s + {0, 2, 1, 3} (low nibbles) and
-// 64g + 32 + 4s + {0, 2, 1, 3} (high): the order in which two masks of a
-// dword place nibbles in the halves of fp16 pairs. xsplit_kernel writes x in
-// the same order. A nibble pair becomes fp16 (1024 + q) by or-ing in the
-// exponent bits, and one packed fp16 FMA (1024 + q)*sc - 1024*sc gives sc*q
-// exactly (one rounding of an exactly representable result).
+// Operand order. At step s (0..3) of half h (0..1) of a super-block, lane
+// group g = l/16 of a row uses quant dword s of the 16 bytes 64h + 16g ..
+// +15 of the block's qs (one contiguous 64-byte run a row and half): the
+// bytes of sub-block pair P = 2h + g/2 (sub-block 2P in the low nibbles,
+// 2P+1 in the high) at value offset 16(g%2) + 4s. Its 8 operand values are,
+// in order, columns 64P + 16(g%2) + 4s + {0, 2, 1, 3} (low nibbles) and the
+// same + 32 (high): the order in which two masks of a dword place nibbles in
+// the halves of fp16 pairs. xsplit_kernel writes x in the same order. A
+// nibble pair becomes fp16 (1024 + q) by or-ing in the exponent bits, and
+// one packed fp16 FMA (1024 + q)*sc - 1024*sc gives sc*q exactly (one
+// rounding of an exactly representable result).
 #include "quant_blocks.hpp"
 
 #pragma clang fp contract(off)
@@ -64,57 +67,6 @@ __device__ __forceinline__ float f16_hi(uint32_t u) { return (float)as_h2(u)[1];
 __device__ __forceinline__ uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
 
 // ------------------------------------------------------------ x prepass
-// Workgroup t: e = exponent of the largest finite |x[t, :]| (frexp), the
-// scale 2^(15-e) (1 for an all-zero token), xinv[t] = its inverse, and the
-// sums of the scaled x over each 32-column sub-block. Tokens t >= n_tok (the
-// padding to 32) get scale 1 and zero sums.
-__global__ __launch_bounds__(256) void xscale_kernel(const float* __restrict__ x, int n_tok,
-                                                      int n_cols, float* __restrict__ xsum,
-                                                      float* __restrict__ xinv) {
-    __shared__ float red[4];
-    const int t = blockIdx.x;
-    const int tid = threadIdx.x;
-    const float* xr = x + (int64_t)t * n_cols;
-    float amax = 0.f;
-    if (t < n_tok) {
-        for (int c = 4 * tid; c < n_cols; c += 1024) {
-            const float4 v = *reinterpret_cast<const float4*>(xr + c);
-            const float a[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) amax = a[i] <= 3.4028235e38f ? fmaxf(amax, a[i]) : amax;
-        }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    if ((tid & 63) == 0) red[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int e = 0;
-    if (amax > 0.f) {
-        frexpf(amax, &e);
-        e = min(max(e, -111), 128);  // keeps 2^(15-e) and 2^(e-15) normal
-    } else {
-        e = kScaleMax;
-    }
-    const float scale = ldexpf(1.f, kScaleMax - e);
-    if (tid == 0) xinv[t] = ldexpf(1.f, e - kScaleMax);
-    const int n_g = n_cols >> 5;
-    for (int g = tid; g < n_g; g += 256) {
-        float s = 0.f;
-        if (t < n_tok) {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 v = *reinterpret_cast<const float4*>(xr + 32 * g + 4 * q);
-                s += v.x * scale;
-                s += v.y * scale;
-                s += v.z * scale;
-                s += v.w * scale;
-            }
-        }
-        xsum[(int64_t)t * n_g + g] = s;
-    }
-}
-
 // Parts of one scaled value: hi = fp16(v), mid = fp16(v - hi), lo =
 // fp16(v - hi - mid); both differences are exact in fp32. Non-finite values
 // keep hi = fp16(v) and zero mid / lo.
@@ -127,39 +79,95 @@ __device__ __forceinline__ void split3(float v, _Float16& hi, _Float16& mid, _Fl
     if (!(fabsf(v) <= 3.4028235e38f)) mid = lo = (_Float16)0.f;
 }
 
-// xp[((mt*nK + K)*3 + p)*64 + lane] = 8 fp16 values of part p for token
-// 16mt + lane%16, step K, lane group lane/16, in the operand order above.
-// Grid (tok_pad/16, nK/4); wave w of a workgroup writes step 4*blockIdx.y + w.
+// One workgroup a (16-token tile mt, super-block sb); grid (tok_pad/16,
+// n_cols/256). For token t of the tile: e = exponent of the largest finite
+// |x| of the super-block (frexp), scale 2^(15-e) (1 when all are zero, and
+// for the padding tokens t >= n_tok), xinv[t][sb] = 2^(e-15);
+// xp[((mt*nK + K)*3 + p)*64 + lane] = 8 fp16 values of part p of the scaled x
+// of token 16mt + lane%16 at step K = 8sb + 4h + s, lane group lane/16, in
+// the operand order above; xsum[t][8sb + k] = the sum of the scaled x over
+// sub-block k (fp32, in column order). x is read coalesced into LDS and
+// read back in operand order.
 __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x, int n_tok,
-                                                      int n_cols, const float* __restrict__ xinv,
-                                                      uint4* __restrict__ xp) {
+                                                      int n_cols, uint4* __restrict__ xp,
+                                                      float* __restrict__ xsum,
+                                                      float* __restrict__ xinv) {
+    constexpr int RowF = 256 + 4;
+    __shared__ float xl[16 * RowF];
     const int tid = threadIdx.x;
-    const int l = tid & 63;
-    const int K = 4 * blockIdx.y + (tid >> 6);
-    const int nK = n_cols >> 5;
-    const int mt = blockIdx.x;
-    const int t = 16 * mt + (l & 15), g = l >> 4;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int mt = blockIdx.x, sb = blockIdx.y;
+    const int nK = n_cols >> 5, n_sb = n_cols >> 8;
+    // token tk = tid / 16 of the tile, columns 16 (tid % 16) .. +15
+    const int tk = tid >> 4, cq = tid & 15;
+    const int t = 16 * mt + tk;
+    float4 v[4];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (t < n_tok) {
-        const float scale = 1.f / xinv[t];  // a power of two: exact
-        const float* xr = x + (int64_t)t * n_cols + 256 * (K >> 3) + 64 * g + 4 * (K & 7);
+        const float* xr = x + (int64_t)t * n_cols + 256 * sb + 16 * cq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = ld_stream(xr + 4 * i);
+            const float a[4] = {fabsf(v[i].x), fabsf(v[i].y), fabsf(v[i].z), fabsf(v[i].w)};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) amax = a[k] <= 3.4028235e38f ? fmaxf(amax, a[k]) : amax;
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    int e = kScaleMax;
+    if (amax > 0.f) {
+        frexpf(amax, &e);
+        e = min(max(e, -111), 128);  // keeps 2^(15-e) and 2^(e-15) normal
+    }
+    const float scale = ldexpf(1.f, kScaleMax - e);
+    if (cq == 0) xinv[(int64_t)t * n_sb + sb] = ldexpf(1.f, e - kScaleMax);
+    float* row = xl + tk * RowF + 16 * cq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(row + 4 * i) =
+            make_float4(v[i].x * scale, v[i].y * scale, v[i].z * scale, v[i].w * scale);
+    __syncthreads();
+
+    // operand (step 8sb + s8, lane l): thread tid makes s8 = tid/64 and tid/64 + 4
+    const int l = tid & 63, lt = l & 15, g = l >> 4;
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+        const int s8 = (tid >> 6) + 4 * rep;
+        const int c0 = 128 * (s8 >> 2) + 64 * (g >> 1) + 16 * (g & 1) + 4 * (s8 & 3);
+        const float* xr = xl + lt * RowF + c0;
         const float4 a = *reinterpret_cast<const float4*>(xr);
         const float4 b = *reinterpret_cast<const float4*>(xr + 32);
-        v[0] = a.x * scale; v[1] = a.z * scale; v[2] = a.y * scale; v[3] = a.w * scale;
-        v[4] = b.x * scale; v[5] = b.z * scale; v[6] = b.y * scale; v[7] = b.w * scale;
-    }
-    h8 parts[kParts];
+        const float w[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};
+        h8 parts[kParts];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        _Float16 hi, mid, lo;
-        split3(v[i], hi, mid, lo);
-        parts[0][i] = hi;
-        parts[1][i] = mid;
-        parts[2][i] = lo;
-    }
-    uint4* dst = xp + ((int64_t)mt * nK + K) * (kParts * 64) + l;
+        for (int i = 0; i < 8; ++i) {
+            _Float16 hi, mid, lo;
+            split3(w[i], hi, mid, lo);
+            parts[0][i] = hi;
+            parts[1][i] = mid;
+            parts[2][i] = lo;
+        }
+        uint4* dst = xp + ((int64_t)mt * nK + 8 * sb + s8) * (kParts * 64) + l;
 #pragma unroll
-    for (int p = 0; p < kParts; ++p) dst[64 * p] = __builtin_bit_cast(uint4, parts[p]);
+        for (int p = 0; p < kParts; ++p) dst[64 * p] = __builtin_bit_cast(uint4, parts[p]);
+    }
+    // sub-block sums: thread tid < 128 sums sub-block tid % 8 of token tid / 8
+    if (tid < 128) {
+        const int st = tid >> 3, k = tid & 7;
+        const float* xr = xl + st * RowF + 32 * k;
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(xr + i);
+            sum += q.x;
+            sum += q.y;
+            sum += q.z;
+            sum += q.w;
+        }
+        xsum[(int64_t)(16 * mt + st) * nK + 8 * sb + k] = sum;
+    }
 }
 
 // ---------------------------------------------------------- the GEMM
@@ -167,7 +175,7 @@ struct SplitParams {
     const uint8_t* w;     // n_rows rows of rb bytes, 16-byte aligned
     const uint4* xp;      // x parts (xsplit_kernel)
     const float* xsum;    // [tok_pad][n_cols/32] sub-block sums of the scaled x
-    const float* xinv;    // [tok_pad] inverse token scales
+    const float* xinv;    // [tok_pad][n_cols/256] inverse scales a token and super-block
     float* y;             // [n_tok][n_rows]
     int64_t n_rows;
     int n_cols;
@@ -175,26 +183,46 @@ struct SplitParams {
     int n_tok;
 };
 
-// sc*q for the 4 fp16 pairs of one dword of quants (Q5_K: with the fifth
-// bits of the matching qh dword, bits 2g / 2g+1 of each byte).
+// sc*q for the 4 fp16 pairs of one dword of quants of sub-block pair P
+// (Q5_K: with the fifth bits of the matching qh dword, bits 2P / 2P+1). The
+// masked nibbles of the dword's bytes b0..b3 are placed by byte permutes as
+// (b0, 0x64, b2, 0x64) and (b1, 0x64, b3, 0x64): fp16 pairs 1024 + q.
+// s_lo / s_hi: packed (sc, sc) of sub-blocks 2P / 2P+1, b_*: -1024 sc.
 template <bool Q5>
-__device__ __forceinline__ h8 weight_operand(uint32_t w, uint32_t h, int g, h2 s_lo, h2 b_lo,
+__device__ __forceinline__ h8 weight_operand(uint32_t w, uint32_t h, int P, h2 s_lo, h2 b_lo,
                                              h2 s_hi, h2 b_hi) {
-    constexpr uint32_t M = 0x000F000Fu, E = 0x64006400u;
-    uint32_t p0 = (w & M) | E, p1 = ((w >> 8) & M) | E;
-    uint32_t p2 = ((w >> 4) & M) | E, p3 = ((w >> 12) & M) | E;
+    constexpr uint32_t E = 0x64646464u, EVEN = 0x04020400u, ODD = 0x04030401u;
+    uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
     if (Q5) {
-        const uint32_t h0 = h >> (2 * g), h1 = h >> (2 * g + 1);
-        p0 |= (h0 & 0x00010001u) << 4;
-        p1 |= ((h0 >> 8) & 0x00010001u) << 4;
-        p2 |= (h1 & 0x00010001u) << 4;
-        p3 |= ((h1 >> 8) & 0x00010001u) << 4;
+        lo |= ((h >> (2 * P)) << 4) & 0x10101010u;
+        hi |= ((h >> (2 * P + 1)) << 4) & 0x10101010u;
     }
-    const h2 a0 = __builtin_elementwise_fma(as_h2(p0), s_lo, b_lo);
-    const h2 a1 = __builtin_elementwise_fma(as_h2(p1), s_lo, b_lo);
-    const h2 a2 = __builtin_elementwise_fma(as_h2(p2), s_hi, b_hi);
-    const h2 a3 = __builtin_elementwise_fma(as_h2(p3), s_hi, b_hi);
+    const h2 a0 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(E, lo, EVEN)), s_lo, b_lo);
+    const h2 a1 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(E, lo, ODD)), s_lo, b_lo);
+    const h2 a2 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(E, hi, EVEN)), s_hi, b_hi);
+    const h2 a3 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(E, hi, ODD)), s_hi, b_hi);
     return __builtin_bit_cast(h8, make_uint4(as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)));
+}
+
+// The two sub-block scales of pair P = 2h + G of a K-quant header as packed
+// fp16 (sc_2P, sc_2P+1), for G = 0 / 1 and half h = 0 / 1 (sub-blocks 2G,
+// 2G+1 and 4+2G, 5+2G; src/kernels.cpp:65-73): the 6-bit values unpacked two
+// bytes at a time and turned into fp16 as 1024 + sc - 1024 (exact).
+__device__ __forceinline__ h2 kq_scale_pair(uint32_t s0, uint32_t s2, int G, int h) {
+    const uint32_t u0 = s0 >> (16 * G);
+    const uint32_t sc = h == 0 ? (u0 & 0x3F3Fu)
+                               : (((s2 >> (16 * G)) & 0x0F0Fu) | ((u0 >> 2) & 0x3030u));
+    const h2 v = as_h2(__builtin_amdgcn_perm(0x64646464u, sc, 0x04010400u));
+    return v + h2{(_Float16)-1024.f, (_Float16)-1024.f};
+}
+
+// The mins m_g and m_{g+4} of a K-quant header for sub-blocks g < 4 and g + 4
+// (src/kernels.cpp:65-73).
+__device__ __forceinline__ void kq_min_pair(uint32_t s1, uint32_t s2, int g, uint32_t& m0,
+                                            uint32_t& m1) {
+    const uint32_t b1 = (s1 >> (8 * g)) & 0xFFu, b2 = (s2 >> (8 * g)) & 0xFFu;
+    m0 = b1 & 63u;
+    m1 = (b2 >> 4) | ((b1 >> 6) << 4);
 }
 
 // kq_scale_min for a sub-block index that differs between lanes: both
@@ -207,24 +235,28 @@ __device__ __forceinline__ void kq_scale_min_lanes(uint32_t s0, uint32_t s1, uin
     mn = k < 4 ? (a1 & 63u) : ((a2 >> 4) | ((a1 >> 6) << 4));
 }
 
-// The x parts and sub-block sums of one chunk on their way to LDS: thread
-// tid stages uint4 tid + 256i of the chunk, i < 3 from the first token tile,
-// i >= 3 from the second (each chunk of a token tile is 768 contiguous
-// uint4 of xp), and float4 tid of the super-block's sums.
+// The x parts, sub-block sums and inverse scales of one chunk on their way
+// to LDS: thread tid stages uint4 tid + 256i of the chunk, i < 3 from the
+// first token tile, i >= 3 from the second (each chunk of a token tile is 768
+// contiguous uint4 of xp); threads < 64 float4 tid of the super-block's sums,
+// threads 64..95 the inverse scale of token tid - 64.
 struct XStage {
     static constexpr int CSTEP = kChunkSteps * kParts * 64;
     u4 r[6];
     v4f s;
+    float iv;
     const u4* b0;
     const u4* b1;
     const v4f* sb;
+    const float* ib;
     int n_chunks;
-    __device__ __forceinline__ void init(const uint4* xp, const float* xsum, int tt, int nK,
-                                         int tid) {
+    __device__ __forceinline__ void init(const uint4* xp, const float* xsum, const float* xinv,
+                                         int tt, int nK, int tid) {
         b0 = reinterpret_cast<const u4*>(xp) + (int64_t)(2 * tt) * nK * (kParts * 64) + tid;
         b1 = b0 + (int64_t)nK * (kParts * 64);
         sb = reinterpret_cast<const v4f*>(xsum) +
              ((int64_t)(kTokTile * tt + ((tid & 63) >> 1)) * nK) / 4 + (tid & 1);
+        ib = xinv + (int64_t)(kTokTile * tt + (tid & 31)) * (nK / 8);
         n_chunks = nK / kChunkSteps;
     }
     // chunk c, clamped: past the end the last chunk is read again, unused
@@ -237,11 +269,13 @@ struct XStage {
             r[3 + i] = b1[o + 256 * i];
         }
         s = sb[2 * (c >> 1)];
+        iv = ib[c >> 1];
     }
-    __device__ __forceinline__ void store(u4* xs, v4f* ss, int tid) const {
+    __device__ __forceinline__ void store(u4* xs, v4f* ss, float* si, int tid) const {
 #pragma unroll
         for (int i = 0; i < 6; ++i) xs[tid + 256 * i] = r[i];
         if (ss != nullptr && tid < 2 * kTokTile) ss[tid] = s;
+        if (ss != nullptr && tid >= 2 * kTokTile && tid < 3 * kTokTile) si[tid - 2 * kTokTile] = iv;
     }
 };
 
@@ -261,6 +295,7 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     static_assert(MT == 2 && CHUNK == 6 * 256, "staging split");
     __shared__ u4 xs[2][CHUNK];                 // 2 x 24 KB, by chunk parity
     __shared__ v4f ss[2][kTokTile * 2];         // sub-block sums, by super-block parity
+    __shared__ __align__(16) float si[2][kTokTile];  // inverse scales, by super-block parity
 
     const int tid = threadIdx.x;
     const int l = tid & 63;
@@ -279,21 +314,20 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         woff[j] = (int)((min(row0 + 16 * j + r, p.n_rows - 1) - row0) * p.rb);
 
     XStage xst;
-    xst.init(p.xp, p.xsum, tt, nK, tid);
+    xst.init(p.xp, p.xsum, p.xinv, tt, nK, tid);
 
-    uint4 q[NT], hq[NT], hd[NT];
-    auto load_q = [&](int sb, int half, uint4 (&qq)[NT], uint4 (&hh)[NT]) {
+    // quants of both halves of a super-block (Q5_K: the qh bytes, the same for
+    // both halves) and its 16-byte header, loaded a super-block ahead
+    uint4 q[2][NT], hq[NT], hd[NT];
+    auto load_w = [&](int sb, uint4 (&qq)[2][NT], uint4 (&hh)[NT], uint4 (&dd)[NT]) {
         const uint8_t* b = wbase + (int64_t)min(sb, n_sb - 1) * BB;
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            qq[j] = ld128(b + woff[j] + QOFF + 32 * g + 16 * half);
-            if (Q5) hh[j] = ld128(b + woff[j] + 16 + 16 * half);
+            qq[0][j] = ld128(b + woff[j] + QOFF + 16 * g);
+            qq[1][j] = ld128(b + woff[j] + QOFF + 64 + 16 * g);
+            if (Q5) hh[j] = ld128(b + woff[j] + 16 + 16 * (g & 1));
+            dd[j] = ld128(b + woff[j]);
         }
-    };
-    auto load_hd = [&](int sb, uint4 (&dd)[NT]) {
-        const uint8_t* b = wbase + (int64_t)min(sb, n_sb - 1) * BB;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) dd[j] = ld128(b + woff[j]);
     };
 
     v4f acc[MT][NT], part[MT][NT];
@@ -303,21 +337,50 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         for (int j = 0; j < NT; ++j) acc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
     h2 s_lo[NT], b_lo[NT], s_hi[NT], b_hi[NT];
-    // the 4 steps of one chunk from LDS buffer xb with quants qq
-    auto run_steps = [&](const u4* xb, const uint4 (&qq)[NT], const uint4 (&hh)[NT]) {
+    // sc of the lane's sub-block pair P = 2 half + g/2 of each row tile,
+    // as packed fp16 factors (sc, sc) and offsets (-1024 sc, -1024 sc)
+    auto set_scales = [&](int half) {
 #pragma unroll
-        for (int s = 0; s < kChunkSteps; ++s) {
-            h8 B[NT], A[MT][kParts];
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-                B[j] = weight_operand<Q5>(comp(qq[j], s), Q5 ? comp(hh[j], s) : 0u, g, s_lo[j],
-                                          b_lo[j], s_hi[j], b_hi[j]);
+        for (int j = 0; j < NT; ++j) {
+            const h2 sp = kq_scale_pair(hd[j].y, hd[j].w, g >> 1, half);
+            const h2 nb = sp * h2{(_Float16)-1024.f, (_Float16)-1024.f};
+            s_lo[j] = h2{sp[0], sp[0]};
+            s_hi[j] = h2{sp[1], sp[1]};
+            b_lo[j] = h2{nb[0], nb[0]};
+            b_hi[j] = h2{nb[1], nb[1]};
+        }
+    };
+    // the 4 steps of one chunk (half `half` of a super-block) from LDS
+    // buffer xb with quants qq. Software-pipelined by one step: while the
+    // matrix steps of step s run, the weights of step s+1 are decoded (VALU)
+    // and its x operands read from LDS (two register sets of each), one matrix
+    // step, two VALU instructions and (six times) one LDS read at a time.
+    auto run_steps = [&](const u4* xb, int half, const uint4 (&qq)[NT],
+                         const uint4 (&hh)[NT]) {
+        const int P = 2 * half + (g >> 1);
+        h8 A[2][MT][kParts], B[2][NT];
+        auto read_a = [&](int s, h8 (&a)[MT][kParts]) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
 #pragma unroll
                 for (int pp = 0; pp < kParts; ++pp)
-                    A[m][pp] = __builtin_bit_cast(
+                    a[m][pp] = __builtin_bit_cast(
                         h8, xb[((m * kChunkSteps + s) * kParts + pp) * 64 + l]);
+        };
+        auto decode_b = [&](int s, h8 (&b)[NT]) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                b[j] = weight_operand<Q5>(comp(qq[j], s), Q5 ? comp(hh[j], s) : 0u, P, s_lo[j],
+                                          b_lo[j], s_hi[j], b_hi[j]);
+        };
+        read_a(0, A[0]);
+        decode_b(0, B[0]);
+#pragma unroll
+        for (int s = 0; s < kChunkSteps; ++s) {
+            if (s + 1 < kChunkSteps) {
+                read_a(s + 1, A[(s + 1) & 1]);
+                decode_b(s + 1, B[(s + 1) & 1]);
+            }
             // small parts first into each tile's super-block sum
 #pragma unroll
             for (int pp = kParts - 1; pp >= 0; --pp)
@@ -325,92 +388,82 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
                 for (int m = 0; m < MT; ++m)
 #pragma unroll
                     for (int j = 0; j < NT; ++j)
-                        part[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[m][pp], B[j],
-                                                                            part[m][j], 0, 0, 0);
-            // keeps the next step's operand reads from being hoisted here
-            // (4 steps of operands at once exceed the register file)
+                        part[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            A[s & 1][m][pp], B[s & 1][j], part[m][j], 0, 0, 0);
+            constexpr int kMfma = kParts * MT * NT, kReads = MT * kParts;
+#pragma unroll
+            for (int i = 0; i < kMfma; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix step
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+                if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     // prologue: chunk 0 (super-block 0, first half) staged, chunk 1 in flight
     xst.load(0);
-    load_q(0, 0, q, hq);
-    load_hd(0, hd);
-    xst.store(xs[0], ss[0], tid);
+    load_w(0, q, hq, hd);
+    xst.store(xs[0], ss[0], si[0], tid);
     xst.load(1);
     __syncthreads();
 
     for (int sb = 0; sb < n_sb; ++sb) {
+        uint4 qn[2][NT], hqn[NT], hdn[NT];
+        load_w(sb + 1, qn, hqn, hdn);   // the next super-block (clamped)
         // ---- first half: chunk 2sb in xs[0]
-        uint4 qn[NT], hqn[NT], hdn[NT];
-        load_q(sb, 1, qn, hqn);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            uint32_t sc0, sc1, mn;
-            kq_scale_min_lanes(hd[j].y, hd[j].z, hd[j].w, 2 * g, sc0, mn);
-            kq_scale_min_lanes(hd[j].y, hd[j].z, hd[j].w, 2 * g + 1, sc1, mn);
-            const _Float16 f0 = (_Float16)(float)sc0, f1 = (_Float16)(float)sc1;
-            const _Float16 n0 = (_Float16)(-1024.f * (float)sc0);
-            const _Float16 n1 = (_Float16)(-1024.f * (float)sc1);
-            s_lo[j] = h2{f0, f0};
-            s_hi[j] = h2{f1, f1};
-            b_lo[j] = h2{n0, n0};
-            b_hi[j] = h2{n1, n1};
-        }
+        set_scales(0);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int j = 0; j < NT; ++j) part[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        run_steps(xs[0], q, hq);
-        xst.store(xs[1], nullptr, tid);   // chunk 2sb+1 (loaded a chunk ago)
+        run_steps(xs[0], 0, q[0], hq);
+        xst.store(xs[1], nullptr, nullptr, tid);   // chunk 2sb+1 (loaded a chunk ago)
         xst.load(2 * sb + 2);
         __syncthreads();
 
         // ---- second half: chunk 2sb+1 in xs[1]
-        load_q(sb + 1, 0, q, hq);   // next super-block (clamped)
-        load_hd(sb + 1, hdn);
-        run_steps(xs[1], qn, hqn);
-        // acc += d * part - dmin * sum_k m_k S_k: the row's d, dmin and m are
-        // lane-local; a token's 8 sums are read once for all row tiles
-        const v4f* sp = ss[sb & 1];
-        float d[NT], dm[NT], mf[NT][8];
+        set_scales(1);
+        run_steps(xs[1], 1, q[1], hq);
+        // acc += inv * (d * part + mins), inv the token's inverse scale for
+        // this super-block and mins = -dmin * sum_k m_k S_k on the fp32 matrix
+        // cores: A[token][k] = S of sub-block k (k = g, then g + 4), B[k][row]
+        // = -dmin * m_k of the lane's row (lane-local), D in part's layout
+        const float* sp = reinterpret_cast<const float*>(ss[sb & 1]);
+        const float* ip = si[sb & 1];
+        float sa[MT][2];
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            d[j] = f16_lo(hd[j].x);
-            dm[j] = f16_hi(hd[j].x);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                uint32_t sc, mn;
-                kq_scale_min(hd[j].y, hd[j].z, hd[j].w, k, sc, mn);
-                mf[j][k] = (float)mn;
-            }
+        for (int m = 0; m < MT; ++m) {
+            sa[m][0] = sp[8 * (16 * m + r) + g];
+            sa[m][1] = sp[8 * (16 * m + r) + g + 4];
         }
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int j = 0; j < NT; ++j) {
+            const float d = f16_lo(hd[j].x);
+            const float ndm = -f16_hi(hd[j].x);
+            uint32_t m0, m1;
+            kq_min_pair(hd[j].z, hd[j].w, g, m0, m1);
+            const float b0 = ndm * (float)m0, b1 = ndm * (float)m1;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int tk = 16 * m + 4 * g + v;
-                const v4f s0 = sp[2 * tk], s1 = sp[2 * tk + 1];
+            for (int m = 0; m < MT; ++m) {
+                v4f mins = __builtin_amdgcn_mfma_f32_16x16x4f32(sa[m][0], b0,
+                                                                v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                mins = __builtin_amdgcn_mfma_f32_16x16x4f32(sa[m][1], b1, mins, 0, 0, 0);
+                const v4f inv = *reinterpret_cast<const v4f*>(ip + 16 * m + 4 * g);
 #pragma unroll
-                for (int j = 0; j < NT; ++j) {
-                    float ms = mf[j][0] * s0.x;
-                    ms = fmaf(mf[j][1], s0.y, ms);
-                    ms = fmaf(mf[j][2], s0.z, ms);
-                    ms = fmaf(mf[j][3], s0.w, ms);
-                    ms = fmaf(mf[j][4], s1.x, ms);
-                    ms = fmaf(mf[j][5], s1.y, ms);
-                    ms = fmaf(mf[j][6], s1.z, ms);
-                    ms = fmaf(mf[j][7], s1.w, ms);
-                    const float a = fmaf(d[j], part[m][j][v], acc[m][j][v]);
-                    acc[m][j][v] = fmaf(-dm[j], ms, a);
-                }
-                __builtin_amdgcn_sched_barrier(0);  // one token's sums at a time
+                for (int v = 0; v < 4; ++v)
+                    acc[m][j][v] = fmaf(inv[v], fmaf(d, part[m][j][v], mins[v]), acc[m][j][v]);
             }
-        xst.store(xs[0], ss[(sb + 1) & 1], tid);  // chunk 2sb+2: the next super-block
+        }
+        xst.store(xs[0], ss[(sb + 1) & 1], si[(sb + 1) & 1], tid);  // chunk 2sb+2
         xst.load(2 * sb + 3);
 #pragma unroll
-        for (int j = 0; j < NT; ++j) hd[j] = hdn[j];
+        for (int j = 0; j < NT; ++j) {
+            q[0][j] = qn[0][j];
+            q[1][j] = qn[1][j];
+            if (Q5) hq[j] = hqn[j];
+            hd[j] = hdn[j];
+        }
         __syncthreads();
     }
 
@@ -421,12 +474,11 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         for (int v = 0; v < 4; ++v) {
             const int tok = kTokTile * tt + 16 * m + 4 * g + v;
             if (tok >= p.n_tok) continue;
-            const float inv = p.xinv[tok];
             float* yp = p.y + (int64_t)tok * p.n_rows;
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 const int64_t row = row0 + 16 * j + r;
-                if (row < p.n_rows) yp[row] = acc[m][j][v] * inv;
+                if (row < p.n_rows) yp[row] = acc[m][j][v];
             }
         }
 }
@@ -437,14 +489,14 @@ inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
 // Workspace bytes of the split-x GEMM for n_tok tokens of n_cols (0 when the
 // type or shape has no split path): the x parts, the sub-block sums and the
-// token scales.
+// inverse scales.
 int64_t split_gemm_workspace(int dtype, int64_t n_cols, int64_t n_tok) {
     if ((dtype != AERO_DTYPE_Q4_K && dtype != AERO_DTYPE_Q5_K) || n_cols <= 0 ||
-        n_cols % 256 != 0 || n_cols / 128 > 65535 || n_tok <= 0)
+        n_cols % 256 != 0 || n_cols / 256 > 65535 || n_tok <= 0)
         return 0;
     const int64_t tp = (n_tok + kTokTile - 1) / kTokTile * kTokTile;
     return align256(tp * n_cols * 2 * kParts) + align256(tp * (n_cols / 32) * 4) +
-           align256(tp * 4);
+           align256(tp * (n_cols / 256) * 4);
 }
 
 // Called by the matmul entry after its argument checks; false (without an
@@ -470,11 +522,8 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
     float* xsum = reinterpret_cast<float*>(base + align256(tp * n_cols * 2 * kParts));
     float* xinv = reinterpret_cast<float*>(base + align256(tp * n_cols * 2 * kParts) +
                                            align256(tp * (n_cols / 32) * 4));
-    if (!launch("xscale_kernel", xscale_kernel, dim3((unsigned)tp), dim3(256), 0, s, x,
-                (int)n_tok, (int)n_cols, xsum, xinv))
-        return false;
-    if (!launch("xsplit_kernel", xsplit_kernel, dim3((unsigned)(tp / 16), (unsigned)(n_cols / 128)),
-                dim3(256), 0, s, x, (int)n_tok, (int)n_cols, (const float*)xinv, xp))
+    if (!launch("xsplit_kernel", xsplit_kernel, dim3((unsigned)(tp / 16), (unsigned)(n_cols / 256)),
+                dim3(256), 0, s, x, (int)n_tok, (int)n_cols, xp, xsum, xinv))
         return false;
     SplitParams p{w, xp, xsum, xinv, y, n_rows, (int)n_cols, rb, (int)n_tok};
     const bool q5 = dtype == AERO_DTYPE_Q5_K;

@@ -261,8 +261,8 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * (src/kernels.cpp:520-538). With 32 or more tokens of Q4_K or Q5_K and
  * `ws` 16-byte aligned of at least aero_hip_matmul_workspace(dtype, n_cols,
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
- * with each token's x split into three fp16 parts (exact products, fp32
- * sums; ws holds the parts); otherwise it is aero_hip_matvec. Calls sharing
+ * with x split into three fp16 parts per token and 256 columns (exact
+ * products, fp32 sums; ws holds the parts); otherwise it is aero_hip_matvec. Calls sharing
  * one workspace must be ordered on one stream. */
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok);
 int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
