@@ -507,11 +507,10 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
     *ran = false;
     const int64_t need = split_gemm_workspace(dtype, n_cols, n_tok);
     const int64_t tp = (n_tok + kTokTile - 1) / kTokTile * kTokTile;
-    // rows a wave: 64 while that leaves >= 512 workgroups, else 32
-    // (measured on MI355X)
+    // rows a wave: 32 (two waves a SIMD); 64 (AERO_HIP_TUNE gemm16_nt=4) runs
+    // one wave a SIMD and measured slower on MI355X at every prefill shape
     const int64_t tok_tiles = tp / kTokTile;
-    int nt = (n_rows + 255) / 256 * tok_tiles >= 512 ? 4 : 2;
-    nt = tune("gemm16_nt", nt) == 4 ? 4 : 2;
+    const int nt = tune("gemm16_nt", 2) == 4 ? 4 : 2;
     const int64_t row_tiles = (n_rows + 64 * nt - 1) / (64 * nt);
     if (need == 0 || ws == nullptr || ws_bytes < need || !aligned16(w) || rb % 16 != 0 ||
         !aligned16(ws) || tok_tiles > 65535 || row_tiles > 0x7fffffff || tp > 0x7fffffff ||
