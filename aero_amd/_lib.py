@@ -114,6 +114,10 @@ PROTOTYPES = {
     "aero_gguf_read": (c_int, [vp, ctypes.c_char_p, c_int64, c_int64, vp]),
     "aero_gguf_upload": (c_int, [vp, ctypes.c_char_p, c_int64, c_int64, vp, vp]),
     "aero_hip_matvec": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp]),
+    "aero_hip_norm_matvec": (c_int, [c_int, c_int, POINTER(vp), POINTER(c_int64), POINTER(c_int64),
+                                     POINTER(vp), vp, vp, c_float, c_int, c_int64, c_int64, vp]),
+    "aero_hip_norm_gate_up": (c_int, [c_int, vp, vp, c_int64, vp, vp, c_float, c_int, c_int, vp,
+                                      c_int64, c_int64, c_int64, vp]),
     "aero_hip_matmul_workspace": (c_int64, [c_int, c_int64, c_int64]),
     "aero_hip_matmul": (c_int, [c_int, vp, c_int64, vp, vp, c_int64, c_int64, c_int64, vp,
                                 c_int64, vp]),

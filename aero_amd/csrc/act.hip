@@ -11,36 +11,12 @@
 // Arithmetic follows src/tensor.cpp:47-59,104-125 with contraction off:
 // silu(g) = g * (1/(1+expf(-g))); gelu(g) = (0.5*g)*(1+erf(g*0.70710678))
 // with the A&S polynomial evaluated in the reference's order; then *up.
-#include "common.hpp"
-#include "aero_hip.h"
+#include "act_ops.hpp"
 
 #pragma clang fp contract(off)
 
 namespace aero {
 namespace {
-
-__device__ __forceinline__ float erf_as(float v) {
-    const float s = copysignf(1.0f, v);
-    const float a = fabsf(v);
-    const float t = 1.0f / (1.0f + 0.3275911f * a);
-    const float p = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t
-                      - 0.284496736f) * t + 0.254829592f) * t;
-    return s * (1.0f - p * expf(-a * a));
-}
-
-template <int KIND>
-__device__ __forceinline__ float act(float v) {
-    if constexpr (KIND == AERO_ACT_SILU) {
-        return v * (1.0f / (1.0f + expf(-v)));
-    } else if constexpr (KIND == AERO_ACT_GELU) {
-        return 0.5f * v * (1.0f + erf_as(v * 0.7071067811865476f));
-    } else if constexpr (KIND == AERO_ACT_GELU_TANH) {
-        return 0.5f * v *
-               (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
-    } else {
-        return v;
-    }
-}
 
 template <int KIND, bool UP>
 __device__ __forceinline__ float4 act4(float4 g, float4 u) {

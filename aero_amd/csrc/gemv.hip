@@ -15,6 +15,7 @@
 // x and y; x is re-read from L2 by every workgroup. Results differ from the
 // reference's serial sums only in summation order.
 #include "quant_blocks.hpp"
+#include "act_ops.hpp"
 
 #pragma clang fp contract(off)
 
@@ -1036,6 +1037,260 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
         }
 }
 
+// ------------------------------------------------ fused decode variants
+// gemv64_kernel with its neighbours of a decoder layer folded in (the
+// reference runs them as separate passes: rmsnorm_rows src/transformer.cpp:
+// 98-104, matvec src/kernels.cpp:497-518, act_mul src/tensor.cpp:104-125):
+//   * RMSNorm of x in the prologue: every workgroup sums x^2 of its tokens
+//     over the row (from L2), inv = 1/sqrtf(ss/n + eps) as the norm kernels,
+//     and stages (x*inv)*w (w, or 1+w with AERO_NORM_UNIT_OFFSET) in LDS in
+//     place of x; norm < 0: x as is;
+//   * MULTI: up to three matrices of one type and width sharing x in one
+//     launch (q, k, v): workgroups [blk[m], blk[m+1]) take matrix m;
+//   * PAIR: row i of w[0] (gate) and of w[1] (up) in the same wave, written
+//     as act(gate . x) * (up . x) (the act·mul op's arithmetic).
+// Two rows a wave, as gemv64_kernel<.., 2, ..>.
+struct GemvFuse {
+    const uint8_t* w[3];
+    float* y[3];          // y[m][t * n_rows[m] + r]; PAIR: y[0]
+    int64_t n_rows[3];    // PAIR: n_rows[0] rows of each of gate and up
+    int blk[4];           // MULTI: first workgroup of each matrix, blk[n_mat] = total
+    const float* x;       // [n_tok][n_cols]
+    const float* norm_w;  // nullable (ones)
+    float eps;
+    int norm;             // < 0: no norm; else AERO_NORM_UNIT_OFFSET or 0
+    int act;              // PAIR: AERO_ACT_*
+    int n_cols;
+    int64_t rb;
+    int n_tok;            // tokens this launch handles (<= T)
+};
+
+__device__ __forceinline__ float act_rt(int kind, float v) {
+    switch (kind) {
+    case AERO_ACT_SILU: return act<AERO_ACT_SILU>(v);
+    case AERO_ACT_GELU: return act<AERO_ACT_GELU>(v);
+    case AERO_ACT_GELU_TANH: return act<AERO_ACT_GELU_TANH>(v);
+    default: return v;
+    }
+}
+
+// R rows a wave: 4 in PAIR mode (2 of gate, the same 2 of up) and for 4
+// tokens, else 2 (as gemv64_kernel picks for these shapes). The first
+// step's weights are requested before the norm is computed (after x, which
+// the norm waits for); for rows of one step the x loaded for the norm is the
+// x staged.
+template <int TYPE, int T, bool PIPE, bool PAIR>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse f) {
+    using L = Lane64<TYPE>;
+    constexpr int R = (PAIR || T == 4) ? 4 : 2;
+    constexpr int BV = QT<TYPE>::BV;
+    __shared__ __align__(16) XStep<T> xs[PIPE ? 2 : 1];
+    __shared__ float red[kGemvWaves][T];
+
+    const int tid = threadIdx.x;
+    const int l = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n_blk = f.n_cols / BV;
+    const int n_st = (f.n_cols + kStepCols - 1) / kStepCols;
+
+    int m = 0;
+    int64_t r0;
+    const uint8_t* rowp[R];
+    if constexpr (PAIR) {
+        // rows r0 .. r0 + R/2 of gate (r < R/2) and of up (r >= R/2)
+        r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * (R / 2);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            rowp[r] = f.w[r < R / 2 ? 0 : 1] + min(r0 + r % (R / 2), f.n_rows[0] - 1) * f.rb;
+    } else {
+        const int b = blockIdx.x;
+        m = __builtin_amdgcn_readfirstlane((b >= f.blk[1]) + (b >= f.blk[2]));
+        r0 = ((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) rowp[r] = f.w[m] + min(r0 + r, f.n_rows[m] - 1) * f.rb;
+    }
+    GemvParams p{nullptr, f.x, nullptr, 0, f.n_cols, f.rb, f.n_tok, f.n_cols, 0};
+
+    float inv[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) inv[t] = 1.0f;
+    // (x * inv) * w (or 1 + w) for this thread's 16 columns of step st; the
+    // weights of a step are loaded with its x (load_w), before they are used
+    // (branch-free: a load under a branch makes the next wait a full one;
+    // without a weight every thread reads the first 64 bytes of x, unused)
+    const bool has_w = f.norm >= 0 && f.norm_w != nullptr;
+    const bool unit = has_w && (f.norm & AERO_NORM_UNIT_OFFSET);
+    const float* wsrc = has_w ? f.norm_w : f.x;
+    auto load_w = [&](int st, v4f (&wv)[4]) AERO_INLINE {
+        const int c0 = has_w ? min(st * kStepCols + 16 * tid, f.n_cols - 16) : 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wv[q] = *reinterpret_cast<const v4f*>(wsrc + c0 + 4 * q);
+    };
+    auto norm_x = [&](v4f (&wv)[4], XStepRegs<T>& xv) AERO_INLINE {
+        if (f.norm < 0) return;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const v4f one = v4f{1.0f, 1.0f, 1.0f, 1.0f};
+            wv[q] = has_w ? (unit ? one + wv[q] : wv[q]) : one;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = xv.v[t][q];
+                xv.v[t][q] = make_float4((v.x * inv[t]) * wv[q].x, (v.y * inv[t]) * wv[q].y,
+                                         (v.z * inv[t]) * wv[q].z, (v.w * inv[t]) * wv[q].w);
+            }
+    };
+
+    // x, then the norm weights, then the matrix weights: loads complete in
+    // order, so waiting for x (the norm, the staging) does not wait for W
+    XStepRegs<T> xr;
+    xstep_load<T>(p, 0, tid, xr);
+    v4f wv[4];
+    load_w(0, wv);
+    __builtin_amdgcn_sched_barrier(0);  // keeps every x load ahead of the weights
+    L ua[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) ua[r].load(rowp[r], 0, l, n_blk);
+
+    // the norm of each token's x: squares of this thread's 16 columns of
+    // each step (the last step's columns clamped to the row: counted once),
+    // a tree sum over the workgroup
+    if (f.norm >= 0) {
+        float ss[T];
+        auto add_sq = [&](int st, const XStepRegs<T>& xq) AERO_INLINE {
+            const bool own = st * kStepCols + 16 * tid < f.n_cols;  // not a clamped copy
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float a = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v = xq.v[t][q];
+                    a += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                }
+                ss[t] += own ? a : 0.0f;
+            }
+        };
+#pragma unroll
+        for (int t = 0; t < T; ++t) ss[t] = 0.0f;
+        add_sq(0, xr);
+        if constexpr (PIPE) {
+            for (int st = 1; st < n_st; ++st) {
+                XStepRegs<T> xq;
+                xstep_load<T>(p, st, tid, xq);
+                add_sq(st, xq);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            ss[t] = group_sum<64>(ss[t]);
+            if (l == 0) red[wave][t] = ss[t];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float a = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kGemvWaves; ++w) a += red[w][t];
+            inv[t] = 1.0f / sqrtf(a / (float)f.n_cols + f.eps);
+        }
+    }
+    float acc[R][T];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[r][t] = 0.0f;
+
+    norm_x(wv, xr);
+    bool live_a = kLaneCols * l < f.n_cols;
+    xstep_store<T>(xs[0], xr, tid);
+    __syncthreads();
+
+    if constexpr (!PIPE) {
+        L::template step<R, T>(ua, xs[0], l, live_a, acc);
+    } else {
+        L ub[R];
+        bool live_b;
+        for (int st = 0; st < n_st; st += 2) {
+            const int s1 = min(st + 1, n_st - 1);
+            xstep_load<T>(p, s1, tid, xr);
+            load_w(s1, wv);
+#pragma unroll
+            for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, l, n_blk);
+            live_b = st + 1 < n_st && s1 * kStepCols + kLaneCols * l < f.n_cols;
+            __builtin_amdgcn_sched_barrier(0);
+            L::template step<R, T>(ua, xs[0], l, live_a, acc);
+            norm_x(wv, xr);
+            xstep_store<T>(xs[1], xr, tid);
+            __syncthreads();
+            if (st + 1 >= n_st) break;
+            const int s2 = min(st + 2, n_st - 1);
+            xstep_load<T>(p, s2, tid, xr);
+            load_w(s2, wv);
+#pragma unroll
+            for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, l, n_blk);
+            live_a = st + 2 < n_st && s2 * kStepCols + kLaneCols * l < f.n_cols;
+            __builtin_amdgcn_sched_barrier(0);
+            L::template step<R, T>(ub, xs[1], l, live_b, acc);
+            norm_x(wv, xr);
+            xstep_store<T>(xs[0], xr, tid);
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int r = 0; r < R / 2; ++r) {
+                const float g = group_sum<64>(acc[r][t]);
+                const float u = group_sum<64>(acc[R / 2 + r][t]);
+                if (l == 0 && r0 + r < f.n_rows[0] && t < f.n_tok)
+                    f.y[0][t * f.n_rows[0] + r0 + r] = act_rt(f.act, g) * u;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float v = group_sum<64>(acc[r][t]);
+                if (l == 0 && r0 + r < f.n_rows[m] && t < f.n_tok)
+                    f.y[m][t * f.n_rows[m] + r0 + r] = v;
+            }
+        }
+    }
+}
+
+using GemvFusedKernel = void (*)(GemvFuse);
+
+template <int TYPE, bool PAIR>
+GemvFusedKernel pick_fused_t(int T, bool pipe) {
+    if (pipe) {
+        switch (T) {
+        case 1: return gemv64_fused_kernel<TYPE, 1, true, PAIR>;
+        case 2: return gemv64_fused_kernel<TYPE, 2, true, PAIR>;
+        default: return nullptr;
+        }
+    }
+    switch (T) {
+    case 1: return gemv64_fused_kernel<TYPE, 1, false, PAIR>;
+    case 2: return gemv64_fused_kernel<TYPE, 2, false, PAIR>;
+    case 4: return gemv64_fused_kernel<TYPE, 4, false, PAIR>;
+    default: return nullptr;
+    }
+}
+
+template <bool PAIR>
+GemvFusedKernel pick_fused(int dtype, int T, bool pipe) {
+    switch (dtype) {
+    case AERO_DTYPE_Q8_0: return pick_fused_t<AERO_DTYPE_Q8_0, PAIR>(T, pipe);
+    case AERO_DTYPE_Q4_K: return pick_fused_t<AERO_DTYPE_Q4_K, PAIR>(T, pipe);
+    case AERO_DTYPE_Q5_K: return pick_fused_t<AERO_DTYPE_Q5_K, PAIR>(T, pipe);
+    case AERO_DTYPE_Q6_K: return pick_fused_t<AERO_DTYPE_Q6_K, PAIR>(T, pipe);
+    case AERO_DTYPE_IQ4_XS: return pick_fused_t<AERO_DTYPE_IQ4_XS, PAIR>(T, pipe);
+    default: return nullptr;
+    }
+}
+
 using GemvKernel = void (*)(GemvParams);
 
 template <int TYPE, int R, bool PIPE>
@@ -1201,6 +1456,97 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
     return true;
 }
 
+// The fused decode GEMVs (gemv64_fused_kernel): argument checks, token
+// groups of up to 4 (2 for rows of more than one 4096-column step), one
+// launch a group. Matrices must take gemv64 (16-byte aligned, rows a
+// multiple of 16 bytes). w_bytes[m] >= n_rows[m] * row bytes.
+bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
+                    const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                    const float* x, const float* norm_w, float eps, int norm, int act,
+                    int64_t n_cols, int64_t n_tok, hipStream_t s) {
+    const char* what = pair ? "norm_gate_up" : "norm_matvec";
+    const bool quant = dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q4_K ||
+                       dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q6_K ||
+                       dtype == AERO_DTYPE_IQ4_XS;
+    if (!quant) {
+        set_error("%s: dtype %d has no quantised GEMV", what, dtype);
+        return false;
+    }
+    const int64_t bv = dtype_block_values(dtype), bb = dtype_block_bytes(dtype);
+    if (n_mat < 1 || n_mat > 3 || (pair && n_mat != 2) || w == nullptr || w_bytes == nullptr ||
+        n_rows == nullptr || y == nullptr || x == nullptr || n_cols <= 0 || n_cols % bv != 0 ||
+        n_cols > (int64_t)1 << 30 || n_tok < 0 || norm > AERO_NORM_UNIT_OFFSET || act < 0 ||
+        act > AERO_ACT_IDENTITY) {
+        set_error("%s: bad arguments (n_mat=%d n_cols=%lld n_tok=%lld norm=%d act=%d)", what,
+                  n_mat, (long long)n_cols, (long long)n_tok, norm, act);
+        return false;
+    }
+    const int64_t rb = (n_cols / bv) * bb;
+    if (rb % 16 != 0 || !aligned16(x) || (norm_w != nullptr && !aligned16(norm_w))) {
+        set_error("%s: rows must be a multiple of 16 bytes, x and the norm weight 16-byte "
+                  "aligned", what);
+        return false;
+    }
+    for (int m = 0; m < n_mat; ++m) {
+        if (w[m] == nullptr || y[pair ? 0 : m] == nullptr || n_rows[m] < 0 ||
+            n_rows[m] > (int64_t)1 << 31 || !aligned16(w[m]) || w_bytes[m] < n_rows[m] * rb ||
+            (pair && n_rows[m] != n_rows[0])) {
+            set_error("%s: matrix %d: null, misaligned (16 bytes), short, or rows differ", what,
+                      m);
+            return false;
+        }
+    }
+    if (n_tok == 0) return true;
+    GemvFuse f{};
+    // workgroups of a launch of T tokens: rows a wave as the kernel's R
+    auto grid_of = [&](int T, GemvFuse& g) -> int64_t {
+        const int R = (pair || T == 4) ? 4 : 2;
+        int64_t tot = 0;
+        if (pair) return (n_rows[0] + (int64_t)kGemvWaves * (R / 2) - 1) / (kGemvWaves * (R / 2));
+        for (int m = 0; m < 3; ++m) {
+            g.blk[m] = (int)std::min<int64_t>(tot, 0x7fffffff);
+            if (m < n_mat) tot += (n_rows[m] + (int64_t)kGemvWaves * R - 1) / (kGemvWaves * R);
+        }
+        for (int m = n_mat; m < 3; ++m) g.blk[m] = 0x7fffffff;  // never reached
+        g.blk[3] = (int)std::min<int64_t>(tot, 0x7fffffff);
+        return tot;
+    };
+    for (int m = 0; m < n_mat; ++m) {
+        f.w[m] = w[m];
+        f.n_rows[m] = n_rows[m];
+    }
+    f.norm_w = norm_w;
+    f.eps = eps;
+    f.norm = norm;
+    f.act = act;
+    f.n_cols = (int)n_cols;
+    f.rb = rb;
+    const bool pipe = n_cols > kStepCols;
+    const int t_max = pipe ? 2 : 4;
+    for (int64_t t0 = 0; t0 < n_tok; t0 += t_max) {
+        const int nt = (int)std::min<int64_t>(t_max, n_tok - t0);
+        const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
+        GemvFusedKernel k = pair ? pick_fused<true>(dtype, T, pipe) : pick_fused<false>(dtype, T, pipe);
+        if (k == nullptr) {
+            set_error("%s: no kernel for %d tokens", what, T);
+            return false;
+        }
+        f.x = x + t0 * n_cols;
+        f.n_tok = nt;
+        for (int m = 0; m < (pair ? 1 : n_mat); ++m) f.y[m] = y[m] + t0 * n_rows[m];
+        const int64_t total = grid_of(T, f);
+        if (total == 0) continue;
+        if (total > 0x7fffffff) {
+            set_error("%s: grid too large", what);
+            return false;
+        }
+        if (!launch(pair ? "gemv64_fused_kernel<pair>" : "gemv64_fused_kernel", k,
+                    dim3((unsigned)total), dim3(64 * kGemvWaves), 0, s, f))
+            return false;
+    }
+    return true;
+}
+
 }  // namespace aero
 
 extern "C" {
@@ -1209,6 +1555,26 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
                     int64_t n_rows, int64_t n_cols, int64_t n_tok, void* stream) {
     return aero::gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok,
                           (hipStream_t)stream, nullptr, 0) ? 1 : 0;
+}
+
+int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
+                         const int64_t* n_rows, float* const* y, const float* x,
+                         const float* norm_w, float eps, int norm, int64_t n_cols,
+                         int64_t n_tok, void* stream) {
+    return aero::gemv_fused_dev(dtype, false, n_mat, w, w_bytes, n_rows, y, x, norm_w, eps, norm,
+                                AERO_ACT_IDENTITY, n_cols, n_tok, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up, int64_t w_bytes,
+                          const float* x, const float* norm_w, float eps, int norm, int act,
+                          float* out, int64_t n_ff, int64_t n_cols, int64_t n_tok,
+                          void* stream) {
+    const uint8_t* w[2] = {w_gate, w_up};
+    const int64_t wb[2] = {w_bytes, w_bytes};
+    const int64_t nr[2] = {n_ff, n_ff};
+    float* y[2] = {out, out};
+    return aero::gemv_fused_dev(dtype, true, 2, w, wb, nr, y, x, norm_w, eps, norm, act, n_cols,
+                                n_tok, (hipStream_t)stream) ? 1 : 0;
 }
 
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok) {

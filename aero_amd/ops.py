@@ -217,6 +217,48 @@ def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: i
                                  n_cols, n_tok, _s(stream)), "matvec")
 
 
+def norm_matvec(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_cols: int,
+                n_tok: int = 1, norm_w: DeviceArray | None = None, eps: float = 1e-5,
+                norm: bool = True, unit_offset: bool = False,
+                stream: Stream | None = None) -> None:
+    """ys[m] = rmsnorm(x) @ W_m^T for up to 3 matrices of one type sharing x
+    (q, k, v), in one launch per 4 tokens; norm=False uses x as is."""
+    if not 1 <= len(ws) <= 3 or len(ys) != len(ws) or len(n_rows) != len(ws):
+        raise ValueError("norm_matvec: 1 to 3 matrices, with as many outputs and row counts")
+    _need(x, n_tok * n_cols, np.float32, "x")
+    _need(norm_w, n_cols, np.float32, "norm_w")
+    for y, nr in zip(ys, n_rows):
+        _need(y, n_tok * nr, np.float32, "y")
+    k = len(ws)
+    wp = (ctypes.c_void_p * k)(*[w.ptr for w in ws])
+    wb = (ctypes.c_int64 * k)(*[w.nbytes for w in ws])
+    nr = (ctypes.c_int64 * k)(*[int(n) for n in n_rows])
+    yp = (ctypes.c_void_p * k)(*[y.ptr for y in ys])
+    flag = (NORM_UNIT_OFFSET if unit_offset else 0) if norm else -1
+    _lib.check(_lib.lib().aero_hip_norm_matvec(int(dtype), k, wp, wb, nr, yp, x.ptr,
+                                               as_ptr(norm_w), float(eps), flag, n_cols, n_tok,
+                                               _s(stream)), "norm_matvec")
+
+
+def norm_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceArray,
+                 out: DeviceArray, n_ff: int, n_cols: int, n_tok: int = 1, act="silu",
+                 norm_w: DeviceArray | None = None, eps: float = 1e-5, norm: bool = True,
+                 unit_offset: bool = False, stream: Stream | None = None) -> None:
+    """out = act(rmsnorm(x) @ Wg^T) * (rmsnorm(x) @ Wu^T) in one launch per 4
+    tokens (SwiGLU / GeGLU decode); norm=False uses x as is."""
+    kind = ACTS[act] if isinstance(act, str) else int(act)
+    _need(x, n_tok * n_cols, np.float32, "x")
+    _need(out, n_tok * n_ff, np.float32, "out")
+    _need(norm_w, n_cols, np.float32, "norm_w")
+    if w_gate.nbytes != w_up.nbytes:
+        raise ValueError("norm_gate_up: gate and up must be the same size")
+    flag = (NORM_UNIT_OFFSET if unit_offset else 0) if norm else -1
+    _lib.check(_lib.lib().aero_hip_norm_gate_up(int(dtype), w_gate.ptr, w_up.ptr, w_gate.nbytes,
+                                                x.ptr, as_ptr(norm_w), float(eps), flag, kind,
+                                                out.ptr, n_ff, n_cols, n_tok, _s(stream)),
+               "norm_gate_up")
+
+
 KV_F32, KV_INT8, KV_INT4 = 0, 1, 2
 
 

@@ -31,6 +31,7 @@ single-threaded like the reference, over a bounded sample.
     python bench.py --variants          # every op variant at the 512-token shape
     python bench.py --gemv              # quantised GEMV (decode projections)
     python bench.py --gemm              # quantised GEMM (prefill projections)
+    python bench.py --fused             # fused decode GEMVs vs the launches they replace
     python bench.py --attention         # attention over a KV cache (decode, prefill)
     python bench.py --gguf              # GGUF parse, upload to HBM, device row addressing
     python bench.py --ssm               # gated DeltaNet scan and conv
@@ -80,6 +81,8 @@ def parse_args(argv=None):
                    help="GGUF parse, file-to-HBM upload and device row addressing")
     p.add_argument("--attention", action="store_true",
                    help="attention over a KV cache (decode and causal prefill)")
+    p.add_argument("--fused", action="store_true",
+                   help="fused decode GEMVs (norm + q/k/v, norm + gate/up + act) vs separate")
     p.add_argument("--gemm", action="store_true",
                    help="quantised GEMM cases (prefill token counts)")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
@@ -509,6 +512,8 @@ def main(argv=None):
         return gemv(a)
     if a.gemm:
         return gemm(a)
+    if a.fused:
+        return fused(a)
     if a.attention:
         return attention_bench(a)
     if a.gguf:
@@ -697,6 +702,85 @@ def gemv(a):
             res["speedup_vs_cpu_t1"] = round(cu / res["t1"]["us"], 1)
         print(json.dumps(res), flush=True)
         del ws, w0
+    return 0
+
+
+FUSED_CASES = [
+    # (name, kind, rows of each matrix, n_cols): Llama-3-8B decode, Q4_K
+    ("qkv_4096", "qkv", (4096, 1024, 1024), 4096),
+    ("gate_up_silu_14336", "gate_up", (14336, 14336), 4096),
+]
+
+
+def fused(a):
+    """Fused decode GEMVs against the separate launches they replace:
+    RMSNorm + q/k/v (aero_hip_norm_matvec) vs rmsnorm + three GEMVs, and
+    RMSNorm + gate/up + SiLU·mul (aero_hip_norm_gate_up) vs rmsnorm + two GEMVs
+    + act_mul. Sustained time per step (recorded plans, back to back over a
+    > 1 GiB rotation of weight sets), weight GB/s of the fused launch."""
+    from aero_amd import ops, workloads as W
+    from aero_amd.device import DeviceArray as DA, Event, Plan, Stream
+
+    t = W.Q4_K
+    rng = np.random.default_rng(0)
+    names = a.shapes.split(",") if a.shapes else [c[0] for c in FUSED_CASES]
+    for name, kind, rows, n_cols in FUSED_CASES:
+        if name not in names:
+            continue
+        w0 = [DA.from_numpy(W.make_table(t, nr * n_cols // 256, rng)) for nr in rows]
+        set_bytes = sum(w.nbytes for w in w0)
+        n_sets = min(128, max(4, -(-SUSTAINED_ROTATION // set_bytes)))
+        sets = [w0] + [[w.clone() for w in w0] for _ in range(n_sets - 1)]
+        nw = DA.from_numpy((1 + 0.1 * rng.standard_normal(n_cols)).astype(np.float32))
+        res = {"case": name, "dtype": t, "rows": list(rows), "n_cols": n_cols,
+               "weight_bytes": set_bytes}
+        for n_tok in (1, 4):
+            X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
+            H = DA.empty((n_tok, n_cols))
+            Ys = [DA.empty((n_tok, nr)) for nr in rows]
+            O = DA.empty((n_tok, rows[0]))
+            out = {}
+            for path in ("fused", "separate"):
+                plan = Plan()
+                with plan:
+                    for ws in sets:
+                        if kind == "qkv":
+                            if path == "fused":
+                                ops.norm_matvec(t, ws, X, Ys, list(rows), n_cols, n_tok,
+                                                norm_w=nw, eps=1e-5)
+                            else:
+                                ops.rmsnorm(X, nw, H, n_tok, n_cols, 1e-5)
+                                for w, y, nr in zip(ws, Ys, rows):
+                                    ops.matvec(t, w, H, y, nr, n_cols, n_tok)
+                        else:
+                            if path == "fused":
+                                ops.norm_gate_up(t, ws[0], ws[1], X, O, rows[0], n_cols, n_tok,
+                                                 act="silu", norm_w=nw, eps=1e-5)
+                            else:
+                                ops.rmsnorm(X, nw, H, n_tok, n_cols, 1e-5)
+                                ops.matvec(t, ws[0], H, Ys[0], rows[0], n_cols, n_tok)
+                                ops.matvec(t, ws[1], H, Ys[1], rows[1], n_cols, n_tok)
+                                ops.act_mul("silu", Ys[0], Ys[1], O, n_tok * rows[0])
+                stream = Stream()
+                plan.launch(stream)
+                e0, e1 = Event(), Event()
+                e0.record(stream)
+                for _ in range(SUSTAINED_REPS):
+                    plan.launch(stream)
+                e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_ms(e1) * 1e3 / (SUSTAINED_REPS * len(sets))
+                out[path] = us
+                plan.destroy()
+                stream.destroy()
+            gbs = set_bytes / (out["fused"] * 1e-6) / 1e9
+            res[f"t{n_tok}"] = {"fused_us": round(out["fused"], 3),
+                                "separate_us": round(out["separate"], 3),
+                                "speedup": round(out["separate"] / out["fused"], 3),
+                                "weight_GB/s": round(gbs, 1),
+                                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(json.dumps(res), flush=True)
+        del sets, w0
     return 0
 
 

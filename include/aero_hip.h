@@ -264,6 +264,28 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * with x split into three fp16 parts per token and 256 columns (exact
  * products, fp32 sums; ws holds the parts); otherwise it is aero_hip_matvec. Calls sharing
  * one workspace must be ordered on one stream. */
+/* Decode steps of a decoder layer in one launch each. The reference runs
+ * them as separate passes: rmsnorm_rows (src/transformer.cpp:98-104, or
+ * src/tensor.cpp:128-134), matvec (src/kernels.cpp:497-518) per matrix,
+ * act_mul (src/tensor.cpp:104-125); each result equals that composition to
+ * 1e-5 of its scale.
+ *   aero_hip_norm_matvec: y[m][t*n_rows[m] + r] = sum_c W_m[r, c] * xn[t, c]
+ *     for up to 3 matrices of one type and width sharing x (q, k, v);
+ *   aero_hip_norm_gate_up: out[t*n_ff + r] = act(Wg[r] . xn[t]) * (Wu[r] . xn[t]).
+ * xn = x normalised as aero_hip_rmsnorm with weight norm_w (nullable: ones)
+ * and flags `norm` (0 or AERO_NORM_UNIT_OFFSET); norm < 0: xn = x. act is an
+ * AERO_ACT_* kind. Weights 16-byte aligned with rows of a multiple of 16
+ * bytes (the gemv fast path), x and norm_w 16-byte aligned; tokens are taken
+ * up to 4 a launch. */
+int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w,
+                         const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                         const float* x, const float* norm_w, float eps, int norm,
+                         int64_t n_cols, int64_t n_tok, void* stream);
+int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
+                          int64_t w_bytes, const float* x, const float* norm_w, float eps,
+                          int norm, int act, float* out, int64_t n_ff, int64_t n_cols,
+                          int64_t n_tok, void* stream);
+
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok);
 int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
                     float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
