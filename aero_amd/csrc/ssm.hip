@@ -16,7 +16,9 @@
 // reductions; the state is read and written once per call.
 //
 // ssm_prep_kernel computes qn, kn, dec and b for every token first (one wave
-// a token and key head), so the serial loop only streams them.
+// a token and key head), so the serial loop only streams them. Scans of 128
+// or more tokens at head dim 128 take the chunked (WY) form instead
+// (ssm_chunk_prep_kernel + ssm_chunk_scan_kernel, below).
 //
 // Sums run in another order than the reference's serial loops, and exp /
 // log1p / sqrt are the GPU's: <= 1e-5 relative to the output's scale. The conv
@@ -39,13 +41,14 @@ __device__ __forceinline__ float softplus_dev(float x) {
 }
 
 // One wave per (token t, key head kk): qn, kn; the wave of kk == 0 also
-// writes dec and b of token t for every value head.
+// writes dec and b of token t for every value head (log_dec: the log of the
+// decay, g <= 0, in place of exp(g), for the chunked scan).
 __global__ __launch_bounds__(64) void ssm_prep_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ alpha,
     const float* __restrict__ beta, const float* __restrict__ a_log,
     const float* __restrict__ dt_bias, float* __restrict__ qn, float* __restrict__ kn,
     float* __restrict__ dec, float* __restrict__ bb, int64_t n_k, int64_t n_v, int64_t d,
-    float eps) {
+    float eps, int log_dec) {
     const int64_t row = blockIdx.x;  // t * n_k + kk
     const int64_t t = row / n_k, kk = row % n_k;
     const int lane = threadIdx.x;
@@ -67,7 +70,7 @@ __global__ __launch_bounds__(64) void ssm_prep_kernel(
         for (int64_t h = lane; h < n_v; h += 64) {
             float g = a_log[h] * softplus_dev(alpha[t * n_v + h] + dt_bias[h]);
             if (g > 0.0f) g = 0.0f;
-            dec[t * n_v + h] = expf(g);
+            dec[t * n_v + h] = log_dec ? g : expf(g);
             bb[t * n_v + h] = 1.0f / (1.0f + expf(-beta[t * n_v + h]));
         }
     }
@@ -347,12 +350,366 @@ ScanKernel pick_scan(int64_t d, int p, bool fused) {
     return nullptr;
 }
 
+// ---------------------------------------------------------- chunked scan
+// The delta rule over chunks of C = 64 tokens (the WY form of the gated
+// delta rule), algebraically the per-token recurrence above:
+//   S_t = g_t S_{t-1} + k_t d_t^T,  d_t = b_t (v_t - g_t S_{t-1}^T k_t),
+//   o_t = scale S_t^T q_t.
+// With L_t = sum_{r<=t} log g_r inside the chunk, G_t = exp(L_t) and
+// Gam_ts = exp(L_t - L_s) <= 1 (no overflow), the chunk's d rows satisfy
+//   (I + A) Dlt = diag(b) (V - diag(G) K S0),  A_ts = b_t Gam_ts (k_t . k_s) (s < t)
+// so Dlt = U - W S0 with U = (I+A)^-1 diag(b) V, W = (I+A)^-1 diag(b G) K, and
+//   O = scale (diag(G) Q S0 + P Dlt),  P_ts = Gam_ts (q_t . k_s) (s <= t),
+//   S_end = G_n S0 + sum_s exp(L_n - L_s) k_s d_s^T.
+// ssm_chunk_prep_kernel computes U, W, P and the decay factors of every
+// (chunk, value head) in parallel; ssm_chunk_scan_kernel carries the state
+// through the chunks on the fp32 matrix cores, 16 state columns a workgroup.
+// Results differ from the per-token scan by fp32 rounding (the chunked form
+// of a 512-token scan: ~6e-7 of the output's scale).
+constexpr int kChunk = 64;
+
+struct ChunkArgs {
+    const float* qn;    // [T][n_k][D] normalised
+    const float* kn;
+    const float* v;     // [T][n_v][D]
+    const float* lg;    // [T][n_v] log decay (<= 0)
+    const float* bb;    // [T][n_v] gate
+    float* U;           // [n_v][nc][C][D]
+    float* W;           // [n_v][nc][C][D]
+    float* P;           // [n_v][nc][C][C]
+    float* gam;         // [n_v][nc][C]: G_t (0 past the chunk's last token)
+    float* kfac;        // [n_v][nc][C]: exp(L_n - L_t) (0 past the last token)
+    float* gC;          // [n_v][nc]: G_n
+    float* state;       // [n_v][D][D]
+    float* outs;        // [T][n_v][D]
+    int64_t T, n_k, n_v;
+    int nc;
+    float scale;
+};
+
+// One workgroup a (chunk c, value head h).
+template <int D>
+__global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
+    constexpr int C = kChunk, KP = D + 4, AP = C + 4;
+    static_assert(2 * D == 256 && D % 32 == 0, "one X column a thread");
+    __shared__ __align__(16) float Ks[C * KP];
+    __shared__ __align__(16) float As[C * AP];
+    __shared__ float Ls[C], Bs[C];
+    const int tid = threadIdx.x, l = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = blockIdx.x;
+    const int64_t h = blockIdx.y, kk = h % a.n_k;
+    const int64_t t0 = (int64_t)c * C;
+    const int n = (int)min<int64_t>(C, a.T - t0);
+    const int64_t base = h * a.nc + c;
+
+    // the chunk's normalised keys (rows past n zero)
+#pragma unroll
+    for (int i = 0; i < C * D / 4 / 256; ++i) {
+        const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row < n) kv = *reinterpret_cast<const float4*>(a.kn + ((t0 + row) * a.n_k + kk) * D + 4 * c4);
+        *reinterpret_cast<float4*>(Ks + row * KP + 4 * c4) = kv;
+    }
+    // inclusive prefix sum of the log decays over the chunk, and the gates
+    if (wave == 0) {
+        float g = l < n ? a.lg[(t0 + l) * a.n_v + h] : 0.0f;
+        const float b = l < n ? a.bb[(t0 + l) * a.n_v + h] : 0.0f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float u = __shfl_up(g, o, 64);
+            if (l >= o) g += u;
+        }
+        Ls[l] = g;
+        Bs[l] = b;
+    }
+    __syncthreads();
+
+    // K K^T and Q K^T, 16x16 tiles on the fp32 matrix cores: wave w owns
+    // token rows 16w..16w+15 and the s tiles 0..w (the rest is above the
+    // diagonal). Lane group g supplies reduction indices 32g + j.
+    {
+        const int r = l & 15, g = l >> 4;
+        float ka[32], qa[32];
+        // query rows straight from memory (rows past n: the last row, unused)
+        const float* qrow = a.qn + ((t0 + min(16 * wave + r, n - 1)) * a.n_k + kk) * D + 32 * g;
+#pragma unroll
+        for (int j = 0; j < 32; j += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(Ks + (16 * wave + r) * KP + 32 * g + j);
+            const float4 y = *reinterpret_cast<const float4*>(qrow + j);
+            ka[j] = x.x; ka[j + 1] = x.y; ka[j + 2] = x.z; ka[j + 3] = x.w;
+            qa[j] = y.x; qa[j + 1] = y.y; qa[j + 2] = y.z; qa[j + 3] = y.w;
+        }
+        for (int sb = 0; sb < C / 16; ++sb) {
+            v4f kk4 = v4f{0.f, 0.f, 0.f, 0.f}, qk4 = kk4;
+            if (sb <= wave) {
+#pragma unroll
+                for (int j = 0; j < 32; j += 4) {
+                    const float4 x =
+                        *reinterpret_cast<const float4*>(Ks + (16 * sb + r) * KP + 32 * g + j);
+                    const float kb[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kk4 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[j + e], kb[e], kk4, 0, 0, 0);
+                        qk4 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[j + e], kb[e], qk4, 0, 0, 0);
+                    }
+                }
+            }
+            // D layout: lane holds rows 4g + v, column r of the tile
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * wave + 4 * g + vv, sidx = 16 * sb + r;
+                const float gm = (sidx <= t && t < n) ? expf(Ls[t] - Ls[sidx]) : 0.0f;
+                As[t * AP + sidx] = sidx < t ? Bs[t] * (gm * kk4[vv]) : 0.0f;
+                a.P[(base * C + t) * C + sidx] = sidx <= t ? gm * qk4[vv] : 0.0f;
+            }
+        }
+    }
+    if (tid < C) {
+        const bool live = tid < n;
+        a.gam[base * C + tid] = live ? expf(Ls[tid]) : 0.0f;
+        a.kfac[base * C + tid] = live ? expf(Ls[n - 1] - Ls[tid]) : 0.0f;
+        if (tid == 0) a.gC[base] = expf(Ls[n - 1]);
+    }
+    __syncthreads();
+
+    // forward substitution (I + A) X = [diag(b) V | diag(b G) K], one
+    // column of X a thread (registers), rows in order
+    const int j = tid;
+    float x[C];
+#pragma unroll
+    for (int t = 0; t < C; ++t) {
+        float rhs = 0.0f;
+        if (t < n)
+            rhs = j < D ? Bs[t] * a.v[((t0 + t) * a.n_v + h) * D + j]
+                        : (Bs[t] * expf(Ls[t])) * Ks[t * KP + (j - D)];
+        x[t] = rhs;
+    }
+    // row t's sum over s < t in 8 partial sums (independent products), so
+    // the dependent chain per row is t/8 FMAs rather than t
+#pragma unroll
+    for (int t = 1; t < C; ++t) {
+        float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s4 = 0; s4 < t; s4 += 4) {
+            const float4 av = *reinterpret_cast<const float4*>(As + t * AP + s4);
+            const float am[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (s4 + e < t) part[(s4 + e) & 7] += am[e] * x[s4 + e];
+        }
+        x[t] = x[t] - (((part[0] + part[1]) + (part[2] + part[3])) +
+                       ((part[4] + part[5]) + (part[6] + part[7])));
+    }
+    float* dst = (j < D ? a.U : a.W) + base * C * D + (j % D);
+#pragma unroll
+    for (int t = 0; t < C; ++t) dst[t * D] = x[t];
+}
+
+// One workgroup a (value head h, 16 CT state columns from e0); the chunks in
+// order. Wave w owns token rows 16w..16w+15 of a chunk and state rows
+// 32w..32w+31 (D = 128); its operand rows (W, Q, P, keys) serve all CT column
+// tiles. The next chunk's operands (rows of W, Q and P, U, the decay
+// factors, the keys) are loaded while the current one is computed; the keys
+// go to the other of two LDS buffers, transposed.
+template <int D, int CT>
+struct ChunkOps {
+    v4f w[8], q[8], p[4], kt[8];
+    float u[CT][4], gm[4], kf[4];
+    float gc;
+};
+
+template <int D, int CT>
+__global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
+    constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16 * CT;
+    static_assert(D == 128, "wave layout");
+    __shared__ __align__(16) float St[NC * SP];     // state block, St[col][i]
+    __shared__ __align__(16) float KT[2][D * TP];   // the chunk's keys, KT[i][s]
+    __shared__ __align__(16) float Dt[NC * TP];     // d^T: Dt[col][s]
+    __shared__ __align__(16) float Dk[NC * TP];     // (kfac d)^T
+    const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t h = blockIdx.x, kk = h % a.n_k;
+    const int e0 = NC * blockIdx.y;
+    const int trow = 16 * wave + r;
+    float* Sg = a.state + h * D * D;
+#pragma unroll
+    for (int i = 0; i < D * NC / 256; ++i) {
+        const int idx = tid + 256 * i, row = idx / NC, col = idx % NC;
+        St[col * SP + row] = Sg[(int64_t)row * D + e0 + col];
+    }
+
+    // operands of chunk c (rows past the chunk's tokens: clamped or zero)
+    auto load_ops = [&](int c, ChunkOps<D, CT>& o) __attribute__((always_inline)) {
+        const int64_t t0 = (int64_t)c * C, base = h * a.nc + c;
+        const int n = (int)min<int64_t>(C, a.T - t0);
+        const float* wr = a.W + (base * C + trow) * D + 32 * g;
+        const float* qr = a.qn + ((t0 + min(trow, n - 1)) * a.n_k + kk) * D + 32 * g;
+        const float* pr = a.P + (base * C + trow) * C + 16 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            o.w[j] = *reinterpret_cast<const v4f*>(wr + 4 * j);
+            o.q[j] = *reinterpret_cast<const v4f*>(qr + 4 * j);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 4 * j);
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv) {
+            const int t = 16 * wave + 4 * g + vv;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) o.u[ct][vv] = a.U[(base * C + t) * D + e0 + 16 * ct + r];
+            o.gm[vv] = a.gam[base * C + t];
+            o.kf[vv] = a.kfac[base * C + t];
+        }
+        o.gc = a.gC[base];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
+            const int64_t tk = t0 + min(row, n - 1);
+            const v4f kv = *reinterpret_cast<const v4f*>(a.kn + (tk * a.n_k + kk) * D + 4 * c4);
+            o.kt[i] = row < n ? kv : v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto store_kt = [&](const ChunkOps<D, CT>& o, float* K) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
+            K[(4 * c4 + 0) * TP + row] = o.kt[i].x;
+            K[(4 * c4 + 1) * TP + row] = o.kt[i].y;
+            K[(4 * c4 + 2) * TP + row] = o.kt[i].z;
+            K[(4 * c4 + 3) * TP + row] = o.kt[i].w;
+        }
+    };
+    auto chunk = [&](int c, const ChunkOps<D, CT>& o, ChunkOps<D, CT>& nx, const float* Kc,
+                     float* Kn) __attribute__((always_inline)) {
+        const int64_t t0 = (int64_t)c * C;
+        const int n = (int)min<int64_t>(C, a.T - t0);
+        load_ops(min(c + 1, a.nc - 1), nx);
+        // (a) W S0 and Q S0 for the wave's 16 tokens and each column tile
+        v4f ws[CT], qs[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) ws[ct] = qs[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const v4f sv =
+                    *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 32 * g + 4 * j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[e], ws[ct], 0, 0, 0);
+                    qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[e], qs[ct], 0, 0, 0);
+                }
+            }
+        }
+        // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * wave + 4 * g + vv;
+                const float dl = o.u[ct][vv] - ws[ct][vv];
+                Dt[(16 * ct + r) * TP + t] = dl;
+                Dk[(16 * ct + r) * TP + t] = o.kf[vv] * dl;
+            }
+        __syncthreads();
+        // (b) O = scale (G Q S0 + P d)
+        {
+            v4f pd[CT];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) pd[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const v4f dv =
+                        *reinterpret_cast<const v4f*>(Dt + (16 * ct + r) * TP + 16 * g + 4 * j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        pd[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.p[j][e], dv[e], pd[ct], 0, 0, 0);
+                }
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv) {
+                    const int t = 16 * wave + 4 * g + vv;
+                    if (t < n)
+                        a.outs[((t0 + t) * a.n_v + h) * D + e0 + 16 * ct + r] =
+                            a.scale * (o.gm[vv] * qs[ct][vv] + pd[ct][vv]);
+                }
+        }
+        // (c) S0 <- G_n S0 + K^T (kfac d) for state rows 32w..32w+31
+        {
+            v4f sd[CT][2];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) sd[ct][0] = sd[ct][1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v4f kv[2];
+#pragma unroll
+                for (int it = 0; it < 2; ++it)
+                    kv[it] = *reinterpret_cast<const v4f*>(Kc + (32 * wave + 16 * it + r) * TP +
+                                                           16 * g + 4 * j);
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const v4f dv =
+                        *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 16 * g + 4 * j);
+#pragma unroll
+                    for (int it = 0; it < 2; ++it)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[it][e], dv[e],
+                                                                              sd[ct][it], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int it = 0; it < 2; ++it)
+#pragma unroll
+                    for (int vv = 0; vv < 4; ++vv) {
+                        const int i = 32 * wave + 16 * it + 4 * g + vv;
+                        float& sv = St[(16 * ct + r) * SP + i];
+                        sv = o.gc * sv + sd[ct][it][vv];
+                    }
+        }
+        store_kt(nx, Kn);   // the next chunk's keys into the other buffer
+        __syncthreads();
+    };
+
+    ChunkOps<D, CT> oa, ob;
+    load_ops(0, oa);
+    store_kt(oa, KT[0]);
+    __syncthreads();
+    for (int c = 0; c < a.nc; c += 2) {
+        chunk(c, oa, ob, KT[0], KT[1]);
+        if (c + 1 >= a.nc) break;
+        chunk(c + 1, ob, oa, KT[1], KT[0]);
+    }
+#pragma unroll
+    for (int i = 0; i < D * NC / 256; ++i) {
+        const int idx = tid + 256 * i, row = idx / NC, col = idx % NC;
+        Sg[(int64_t)row * D + e0 + col] = St[col * SP + row];
+    }
+}
+
 }  // namespace
+
+// Long scans of head dim 128 take the chunked form (measured faster on
+// MI355X from a few chunks on).
+static bool use_chunked(int64_t T, int64_t d) {
+    return d == 128 && T >= tune("ssm_chunk_min", 128) && tune("ssm_chunk", 1) != 0;
+}
 
 int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
     if (T <= 0 || n_k <= 0 || n_v <= 0 || d <= 0) return 0;
     const auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
-    return 2 * up(T * n_k * d * 4) + 2 * up(T * n_v * 4);
+    int64_t b = 2 * up(T * n_k * d * 4) + 2 * up(T * n_v * 4);
+    if (use_chunked(T, d)) {
+        const int64_t nc = (T + kChunk - 1) / kChunk, rows = n_v * nc * kChunk;
+        b += 2 * up(rows * d * 4) + up(rows * kChunk * 4) + 2 * up(rows * 4) + up(n_v * nc * 4);
+    }
+    return b;
 }
 
 bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* alpha,
@@ -402,9 +759,55 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
     float* kn = reinterpret_cast<float*>(w + up(T * n_k * d * 4));
     float* dc = reinterpret_cast<float*>(w + 2 * up(T * n_k * d * 4));
     float* bb = reinterpret_cast<float*>(w + 2 * up(T * n_k * d * 4) + up(T * n_v * 4));
+    const bool chunked = use_chunked(T, d);
     if (!launch("ssm_prep_kernel", ssm_prep_kernel, dim3((unsigned)(T * n_k)), dim3(64), 0, s,
-                q, k, alpha, beta, a_log, dt_bias, qn, kn, dc, bb, n_k, n_v, d, eps))
+                q, k, alpha, beta, a_log, dt_bias, qn, kn, dc, bb, n_k, n_v, d, eps,
+                chunked ? 1 : 0))
         return false;
+    if (chunked) {
+        const int64_t nc = (T + kChunk - 1) / kChunk, rows = n_v * nc * kChunk;
+        if (nc > 0x7fffffff || n_v > 65535) {
+            set_error("ssm_scan: too many chunks or heads for the chunked scan");
+            return false;
+        }
+        char* cw = w + 2 * up(T * n_k * d * 4) + 2 * up(T * n_v * 4);
+        ChunkArgs ca{};
+        ca.qn = qn;
+        ca.kn = kn;
+        ca.v = v;
+        ca.lg = dc;
+        ca.bb = bb;
+        ca.U = reinterpret_cast<float*>(cw);
+        ca.W = reinterpret_cast<float*>(cw + up(rows * d * 4));
+        ca.P = reinterpret_cast<float*>(cw + 2 * up(rows * d * 4));
+        ca.gam = reinterpret_cast<float*>(cw + 2 * up(rows * d * 4) + up(rows * kChunk * 4));
+        ca.kfac = reinterpret_cast<float*>(cw + 2 * up(rows * d * 4) + up(rows * kChunk * 4) +
+                                           up(rows * 4));
+        ca.gC = reinterpret_cast<float*>(cw + 2 * up(rows * d * 4) + up(rows * kChunk * 4) +
+                                         2 * up(rows * 4));
+        ca.state = state;
+        ca.outs = outs;
+        ca.T = T;
+        ca.n_k = n_k;
+        ca.n_v = n_v;
+        ca.nc = (int)nc;
+        ca.scale = scale;
+        if (!aligned16(v) || !aligned16(outs)) {
+            set_error("ssm_scan: v and outs must be 16-byte aligned for the chunked scan");
+            return false;
+        }
+        if (!launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128>,
+                    dim3((unsigned)nc, (unsigned)n_v), dim3(256), 0, s, ca))
+            return false;
+        // one 16-column tile a workgroup (256 workgroups); two tiles sharing
+        // the operand rows (AERO_HIP_TUNE ssm_chunk_ct=2, 128 workgroups)
+        // measured 16% slower on MI355X
+        if (tune("ssm_chunk_ct", 1) == 2)
+            return launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 2>,
+                          dim3((unsigned)n_v, (unsigned)(d / 32)), dim3(256), 0, s, ca);
+        return launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 1>,
+                      dim3((unsigned)n_v, (unsigned)(d / 16)), dim3(256), 0, s, ca);
+    }
     ScanArgs sa{qn, kn, v, dc, bb, nullptr, nullptr, state, outs, T, n_k, n_v, scale, eps};
     return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);
 }

@@ -1173,8 +1173,10 @@ def ssm_bench(a):
         e1.synchronize()
         op_us = e0.elapsed_ms(e1) * 1e3 / reps
         # short scans (up to 16 tokens) are one kernel, whose time the first
-        # event pair measured; longer ones a prep pass and the scan
+        # event pair measured; longer ones a prep pass and the scan (from 128
+        # tokens the chunked scan: chunk pre-pass + state pass)
         fused = T <= 16
+        n_kern = 1 if fused else (3 if T >= 128 and os.environ.get("AERO_HIP_TUNE", "").find("ssm_chunk=0") < 0 else 2)
         prep_us = 0.0 if fused else statistics.mean(times["prep"])
         scan_us = op_us - prep_us
         conv_us = statistics.mean(times["conv"])
@@ -1182,7 +1184,7 @@ def ssm_bench(a):
         io_bytes = 4 * T * (2 * n_k * d + 2 * n_v * d + 2 * n_v)
         conv_bytes = 4 * (2 * T * C + C * K)
         res = {"case": name, "tokens": T, "heads": [n_k, n_v], "d": d,
-               "ssm_op_us": round(op_us, 3), "kernels": 1 if fused else 2,
+               "ssm_op_us": round(op_us, 3), "kernels": n_kern,
                "prep_us": round(prep_us, 3), "scan_us": round(scan_us, 3),
                "conv_us": round(conv_us, 3),
                "conv_GB/s": round(conv_bytes / (conv_us * 1e-6) / 1e9, 1)}

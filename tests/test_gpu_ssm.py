@@ -82,6 +82,47 @@ def test_scan_vs_oracle(hip, oracle, T, n_k, n_v, d):
     assert rel_to_scale(dst.numpy(), wst) <= RTOL
 
 
+@pytest.mark.parametrize("T,n_k,n_v", [
+    (128, 16, 32),     # two whole 64-token chunks at Qwen3-Next's heads
+    (300, 2, 4),       # a partial last chunk (44 tokens)
+    (1000, 3, 6),      # 16 chunks, two value heads a key head
+])
+def test_chunked_scan_vs_oracle(hip, oracle, T, n_k, n_v):
+    """Scans of 128 or more tokens at head dim 128 take the chunked (WY) form:
+    chunk pre-pass + state pass on the matrix cores; same tolerance."""
+    rng = np.random.default_rng(T + n_k)
+    args = inputs(rng, T, n_k, n_v, 128)
+    print(f"chunked ssm scan T={T} n_k={n_k} n_v={n_v}", flush=True)
+    scale = 128 ** -0.5
+    out, dst = gpu_scan(*args, scale)
+    want, wst = oracle.ssm_scan(*args, scale)
+    assert rel_to_scale(out, want) <= RTOL
+    assert rel_to_scale(dst.numpy(), wst) <= RTOL
+
+
+def test_chunked_scan_strong_decay_and_chain(hip, oracle):
+    """Decays near zero (a_log -30: exp(L) underflows inside a chunk) and near
+    one, gates near 0 and 1; two chunked calls of 200 tokens carrying the
+    state equal one of 400 and the oracle."""
+    rng = np.random.default_rng(77)
+    q, k, v, al, bt, a_log, dt, st = inputs(rng, 400, 2, 4, 128)
+    a_log = np.array([-30.0, -1e-4, -0.5, -3.0], np.float32)
+    bt[:, 0] = 20.0                                    # gate 1
+    bt[:, 1] = -20.0                                   # gate ~0
+    scale = 128 ** -0.5
+    whole, wst = gpu_scan(q, k, v, al, bt, a_log, dt, st, scale)
+    want, ost = oracle.ssm_scan(q, k, v, al, bt, a_log, dt, st, scale)
+    assert rel_to_scale(whole, want) <= RTOL and rel_to_scale(wst.numpy(), ost) <= RTOL
+    dst = DA.from_numpy(st)
+    a, _ = gpu_scan(q[:200], k[:200], v[:200], al[:200], bt[:200], a_log, dt, None, scale,
+                    dstate=dst)
+    b, _ = gpu_scan(q[200:], k[200:], v[200:], al[200:], bt[200:], a_log, dt, None, scale,
+                    dstate=dst)
+    assert rel_to_scale(np.concatenate([a, b]), want) <= RTOL
+    assert rel_to_scale(dst.numpy(), ost) <= RTOL
+    assert np.isfinite(whole).all()
+
+
 def test_scan_decode_chain_and_host_abi(hip, oracle):
     """Three one-token calls carrying the state equal one three-token call
     (the state is updated in place on the device); the host ABI's scan and
