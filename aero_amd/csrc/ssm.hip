@@ -511,7 +511,10 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
 // 32w..32w+31 (D = 128); its operand rows (W, Q, P, keys) serve all CT column
 // tiles. The next chunk's operands (rows of W, Q and P, U, the decay
 // factors, the keys) are loaded while the current one is computed; the keys
-// go to the other of two LDS buffers, transposed.
+// go to the other of two LDS buffers, row-major with a 132-float pitch, which
+// the transposed state update S^T <- G_n S^T + (kfac d)^T K reads as its B
+// operand without bank conflicts (measured: a transposed key layout spent
+// more cycles in LDS bank conflicts than in the matrix steps).
 template <int D, int CT>
 struct ChunkOps {
     v4f w[8], q[8], p[4], kt[8];
@@ -521,10 +524,10 @@ struct ChunkOps {
 
 template <int D, int CT>
 __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
-    constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16 * CT;
+    constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16 * CT, KP = D + 4;
     static_assert(D == 128, "wave layout");
     __shared__ __align__(16) float St[NC * SP];     // state block, St[col][i]
-    __shared__ __align__(16) float KT[2][D * TP];   // the chunk's keys, KT[i][s]
+    __shared__ __align__(16) float KT[2][C * KP];   // the chunk's keys, KT[s][i]
     __shared__ __align__(16) float Dt[NC * TP];     // d^T: Dt[col][s]
     __shared__ __align__(16) float Dk[NC * TP];     // (kfac d)^T
     const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
@@ -574,10 +577,7 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
-            K[(4 * c4 + 0) * TP + row] = o.kt[i].x;
-            K[(4 * c4 + 1) * TP + row] = o.kt[i].y;
-            K[(4 * c4 + 2) * TP + row] = o.kt[i].z;
-            K[(4 * c4 + 3) * TP + row] = o.kt[i].w;
+            *reinterpret_cast<v4f*>(K + row * KP + 4 * c4) = o.kt[i];
         }
     };
     auto chunk = [&](int c, const ChunkOps<D, CT>& o, ChunkOps<D, CT>& nx, const float* Kc,
@@ -602,16 +602,19 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                 }
             }
         }
-        // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d
+        // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d;
+        // the 4 rows of a lane are one 16-byte store
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
+        for (int ct = 0; ct < CT; ++ct) {
+            v4f dl, dk;
 #pragma unroll
             for (int vv = 0; vv < 4; ++vv) {
-                const int t = 16 * wave + 4 * g + vv;
-                const float dl = o.u[ct][vv] - ws[ct][vv];
-                Dt[(16 * ct + r) * TP + t] = dl;
-                Dk[(16 * ct + r) * TP + t] = o.kf[vv] * dl;
+                dl[vv] = o.u[ct][vv] - ws[ct][vv];
+                dk[vv] = o.kf[vv] * dl[vv];
             }
+            *reinterpret_cast<v4f*>(Dt + (16 * ct + r) * TP + 16 * wave + 4 * g) = dl;
+            *reinterpret_cast<v4f*>(Dk + (16 * ct + r) * TP + 16 * wave + 4 * g) = dk;
+        }
         __syncthreads();
         // (b) O = scale (G Q S0 + P d)
         {
@@ -638,27 +641,30 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                             a.scale * (o.gm[vv] * qs[ct][vv] + pd[ct][vv]);
                 }
         }
-        // (c) S0 <- G_n S0 + K^T (kfac d) for state rows 32w..32w+31
+        // (c) S0^T <- G_n S0^T + (kfac d)^T K for state rows 32w..32w+31:
+        // A[col][s] = (kfac d)[s][col] (Dk), B[s][i] = K[s][i] (row-major keys),
+        // D[col][i] lands in St's layout. Lane group g supplies the chunk
+        // rows 4g + 16j + e, so its key rows sit 4 * KP floats (16 banks)
+        // from the next group's.
         {
             v4f sd[CT][2];
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) sd[ct][0] = sd[ct][1] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                v4f kv[2];
+                v4f dv[CT];
 #pragma unroll
-                for (int it = 0; it < 2; ++it)
-                    kv[it] = *reinterpret_cast<const v4f*>(Kc + (32 * wave + 16 * it + r) * TP +
-                                                           16 * g + 4 * j);
+                for (int ct = 0; ct < CT; ++ct)
+                    dv[ct] = *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 4 * g + 16 * j);
 #pragma unroll
-                for (int ct = 0; ct < CT; ++ct) {
-                    const v4f dv =
-                        *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 16 * g + 4 * j);
+                for (int e = 0; e < 4; ++e) {
+                    const float* kr = Kc + (4 * g + 16 * j + e) * KP + 32 * wave + r;
+                    const float kb[2] = {kr[0], kr[16]};
 #pragma unroll
-                    for (int it = 0; it < 2; ++it)
+                    for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[it][e], dv[e],
+                        for (int it = 0; it < 2; ++it)
+                            sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(dv[ct][e], kb[it],
                                                                               sd[ct][it], 0, 0, 0);
                 }
             }
@@ -668,8 +674,7 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                 for (int it = 0; it < 2; ++it)
 #pragma unroll
                     for (int vv = 0; vv < 4; ++vv) {
-                        const int i = 32 * wave + 16 * it + 4 * g + vv;
-                        float& sv = St[(16 * ct + r) * SP + i];
+                        float& sv = St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r];
                         sv = o.gc * sv + sd[ct][it][vv];
                     }
         }
