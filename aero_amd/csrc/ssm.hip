@@ -387,15 +387,26 @@ struct ChunkArgs {
     float scale;
 };
 
-// One workgroup a (chunk c, value head h).
+// One workgroup a (chunk c, value head h), four waves, every product on the
+// fp32 matrix cores (16x16x4: lane (r, g) = (l % 16, l / 16) supplies A[r][g]
+// and B[g][r] and receives D[4g + v][r]):
+//  1. K K^T (strictly lower) and Q K^T (lower) in 16x16 tiles, five tile
+//     products a wave; A = diag(b) Gam (K K^T) to LDS, P = Gam (Q K^T) out.
+//  2. T = (I + A)^-1 by 16x16 blocks: the four unit lower-triangular diagonal
+//     blocks by substitution (a wave each), then
+//     T_ij = -T_ii sum_{j<=k<i} A_ik T_kj along the sub-diagonals.
+//  3. U = T diag(b) V (waves 0, 1) and W = T diag(b G) K (waves 2, 3), 64
+//     columns a wave, skipping T's zero blocks; the column scaling is folded
+//     into T's operand.
 template <int D>
 __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     constexpr int C = kChunk, KP = D + 4, AP = C + 4;
-    static_assert(2 * D == 256 && D % 32 == 0, "one X column a thread");
-    __shared__ __align__(16) float Ks[C * KP];
-    __shared__ __align__(16) float As[C * AP];
-    __shared__ float Ls[C], Bs[C];
-    const int tid = threadIdx.x, l = tid & 63;
+    static_assert(D == 128 && C == 64, "tile layout");
+    __shared__ __align__(16) float Ks[C * KP];   // keys [s][i], rows past n zero
+    __shared__ __align__(16) float As[C * AP];   // A [t][s]
+    __shared__ __align__(16) float Ts[C * AP];   // (I + A)^-1 [t][s]
+    __shared__ float Ls[C], Bs[C], Fs[C];
+    const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = blockIdx.x;
     const int64_t h = blockIdx.y, kk = h % a.n_k;
@@ -407,61 +418,64 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
     for (int i = 0; i < C * D / 4 / 256; ++i) {
         const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row < n) kv = *reinterpret_cast<const float4*>(a.kn + ((t0 + row) * a.n_k + kk) * D + 4 * c4);
-        *reinterpret_cast<float4*>(Ks + row * KP + 4 * c4) = kv;
+        v4f kv = v4f{0.f, 0.f, 0.f, 0.f};
+        if (row < n) kv = *reinterpret_cast<const v4f*>(a.kn + ((t0 + row) * a.n_k + kk) * D + 4 * c4);
+        *reinterpret_cast<v4f*>(Ks + row * KP + 4 * c4) = kv;
     }
     // inclusive prefix sum of the log decays over the chunk, and the gates
     if (wave == 0) {
-        float g = l < n ? a.lg[(t0 + l) * a.n_v + h] : 0.0f;
+        float lg = l < n ? a.lg[(t0 + l) * a.n_v + h] : 0.0f;
         const float b = l < n ? a.bb[(t0 + l) * a.n_v + h] : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const float u = __shfl_up(g, o, 64);
-            if (l >= o) g += u;
+            const float u = __shfl_up(lg, o, 64);
+            if (l >= o) lg += u;
         }
-        Ls[l] = g;
+        Ls[l] = lg;
         Bs[l] = b;
+        Fs[l] = b * expf(lg);
     }
     __syncthreads();
 
-    // K K^T and Q K^T, 16x16 tiles on the fp32 matrix cores: wave w owns
-    // token rows 16w..16w+15 and the s tiles 0..w (the rest is above the
-    // diagonal). Lane group g supplies reduction indices 32g + j.
+    // 1. wave w: row tiles {3, 0} (w < 2) or {2, 1}; K rows (even w) or Q rows
     {
-        const int r = l & 15, g = l >> 4;
-        float ka[32], qa[32];
-        // query rows straight from memory (rows past n: the last row, unused)
-        const float* qrow = a.qn + ((t0 + min(16 * wave + r, n - 1)) * a.n_k + kk) * D + 32 * g;
+        const bool isq = (wave & 1) != 0;
+        const int i_hi = wave < 2 ? 3 : 2;
 #pragma unroll
-        for (int j = 0; j < 32; j += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(Ks + (16 * wave + r) * KP + 32 * g + j);
-            const float4 y = *reinterpret_cast<const float4*>(qrow + j);
-            ka[j] = x.x; ka[j + 1] = x.y; ka[j + 2] = x.z; ka[j + 3] = x.w;
-            qa[j] = y.x; qa[j + 1] = y.y; qa[j + 2] = y.z; qa[j + 3] = y.w;
-        }
-        for (int sb = 0; sb < C / 16; ++sb) {
-            v4f kk4 = v4f{0.f, 0.f, 0.f, 0.f}, qk4 = kk4;
-            if (sb <= wave) {
+        for (int which = 0; which < 2; ++which) {
+            const int i = which ? 3 - i_hi : i_hi;
+            v4f ar[8];
+            if (isq) {
+                const float* qrow = a.qn + ((t0 + min(16 * i + r, n - 1)) * a.n_k + kk) * D + 32 * g;
 #pragma unroll
-                for (int j = 0; j < 32; j += 4) {
-                    const float4 x =
-                        *reinterpret_cast<const float4*>(Ks + (16 * sb + r) * KP + 32 * g + j);
-                    const float kb[4] = {x.x, x.y, x.z, x.w};
+                for (int jj = 0; jj < 8; ++jj) ar[jj] = *reinterpret_cast<const v4f*>(qrow + 4 * jj);
+            } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kk4 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[j + e], kb[e], kk4, 0, 0, 0);
-                        qk4 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[j + e], kb[e], qk4, 0, 0, 0);
-                    }
-                }
+                for (int jj = 0; jj < 8; ++jj)
+                    ar[jj] = *reinterpret_cast<const v4f*>(Ks + (16 * i + r) * KP + 32 * g + 4 * jj);
             }
-            // D layout: lane holds rows 4g + v, column r of the tile
+            for (int j = 0; j < C / 16; ++j) {
+                v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+                if (j <= i) {
 #pragma unroll
-            for (int vv = 0; vv < 4; ++vv) {
-                const int t = 16 * wave + 4 * g + vv, sidx = 16 * sb + r;
-                const float gm = (sidx <= t && t < n) ? expf(Ls[t] - Ls[sidx]) : 0.0f;
-                As[t * AP + sidx] = sidx < t ? Bs[t] * (gm * kk4[vv]) : 0.0f;
-                a.P[(base * C + t) * C + sidx] = sidx <= t ? gm * qk4[vv] : 0.0f;
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const v4f kb = *reinterpret_cast<const v4f*>(Ks + (16 * j + r) * KP + 32 * g + 4 * jj);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[jj][e], kb[e], acc, 0, 0, 0);
+                    }
+                } else if (!isq) {
+                    continue;   // A above the diagonal is never read
+                }
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv) {
+                    const int t = 16 * i + 4 * g + vv, sidx = 16 * j + r;
+                    const float gm = (sidx <= t && t < n) ? expf(Ls[t] - Ls[sidx]) : 0.0f;
+                    if (isq)
+                        a.P[(base * C + t) * C + sidx] = sidx <= t ? gm * acc[vv] : 0.0f;
+                    else
+                        As[t * AP + sidx] = sidx < t ? Bs[t] * (gm * acc[vv]) : 0.0f;
+                }
             }
         }
     }
@@ -473,37 +487,87 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     }
     __syncthreads();
 
-    // forward substitution (I + A) X = [diag(b) V | diag(b G) K], one
-    // column of X a thread (registers), rows in order
-    const int j = tid;
-    float x[C];
+    // 2a. diagonal block w of T: column r by substitution (rows above r zero)
+    {
+        const int b0 = 16 * wave;
+        float x[16];
 #pragma unroll
-    for (int t = 0; t < C; ++t) {
-        float rhs = 0.0f;
-        if (t < n)
-            rhs = j < D ? Bs[t] * a.v[((t0 + t) * a.n_v + h) * D + j]
-                        : (Bs[t] * expf(Ls[t])) * Ks[t * KP + (j - D)];
-        x[t] = rhs;
-    }
-    // row t's sum over s < t in 8 partial sums (independent products), so
-    // the dependent chain per row is t/8 FMAs rather than t
+        for (int t = 0; t < 16; ++t) {
+            float acc = t == r ? 1.0f : 0.0f;
 #pragma unroll
-    for (int t = 1; t < C; ++t) {
-        float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int s4 = 0; s4 < t; s4 += 4) {
+                const v4f av = *reinterpret_cast<const v4f*>(As + (b0 + t) * AP + b0 + s4);
 #pragma unroll
-        for (int s4 = 0; s4 < t; s4 += 4) {
-            const float4 av = *reinterpret_cast<const float4*>(As + t * AP + s4);
-            const float am[4] = {av.x, av.y, av.z, av.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (s4 + e < t) part[(s4 + e) & 7] += am[e] * x[s4 + e];
+                for (int e = 0; e < 4; ++e)
+                    if (s4 + e < t) acc -= av[e] * x[s4 + e];
+            }
+            x[t] = acc;
         }
-        x[t] = x[t] - (((part[0] + part[1]) + (part[2] + part[3])) +
-                       ((part[4] + part[5]) + (part[6] + part[7])));
-    }
-    float* dst = (j < D ? a.U : a.W) + base * C * D + (j % D);
+        if (g == 0) {
 #pragma unroll
-    for (int t = 0; t < C; ++t) dst[t * D] = x[t];
+            for (int t = 0; t < 16; ++t) Ts[(b0 + t) * AP + b0 + r] = x[t];
+        }
+    }
+    __syncthreads();
+    // 2b. T_ij = -T_ii X, X = sum_{j<=k<i} A_ik T_kj; X in the output layout is
+    // the B operand of the second product with T_ii's columns taken as 4g + v
+    auto off_diag = [&](int i, int j) __attribute__((always_inline)) {
+        v4f xa = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int k = j; k < i; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                xa = __builtin_amdgcn_mfma_f32_16x16x4f32(As[(16 * i + r) * AP + 16 * k + 4 * q + g],
+                                                          Ts[(16 * k + 4 * q + g) * AP + 16 * j + r],
+                                                          xa, 0, 0, 0);
+        const v4f tii = *reinterpret_cast<const v4f*>(Ts + (16 * i + r) * AP + 16 * i + 4 * g);
+        v4f y = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv)
+            y = __builtin_amdgcn_mfma_f32_16x16x4f32(tii[vv], xa[vv], y, 0, 0, 0);
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv) Ts[(16 * i + 4 * g + vv) * AP + 16 * j + r] = -y[vv];
+    };
+    if (wave < 3) off_diag(wave + 1, wave);
+    __syncthreads();
+    if (wave < 2) off_diag(wave + 2, wave);
+    __syncthreads();
+    if (wave == 0) off_diag(3, 0);
+    __syncthreads();
+
+    // 3. U = T diag(b) V, W = T diag(b G) K: lane r of column tile ct holds
+    // column c0 + 4r + ct, so each lane loads and stores 4 adjacent columns
+    {
+        const bool isw = wave >= 2;
+        const int c0 = 64 * (wave & 1);
+        v4f acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) acc[i][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+        const float* vsrc = a.v + h * D + c0 + 4 * r;
+#pragma unroll
+        for (int ks = 0; ks < C / 4; ++ks) {
+            const int sidx = 4 * ks + g;
+            // rows past n: T's column scale (b) is zero there; any finite row
+            const v4f bv = isw ? *reinterpret_cast<const v4f*>(Ks + sidx * KP + c0 + 4 * r)
+                               : *reinterpret_cast<const v4f*>(vsrc + (t0 + min(sidx, n - 1)) * a.n_v * D);
+            const float fs = isw ? Fs[sidx] : Bs[sidx];
+#pragma unroll
+            for (int i = ks / 4; i < 4; ++i) {
+                const float ta = Ts[(16 * i + r) * AP + sidx] * fs;
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+                    acc[i][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ta, bv[ct], acc[i][ct], 0, 0, 0);
+            }
+        }
+        float* dst = (isw ? a.W : a.U) + base * C * D + c0 + 4 * r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv)
+                *reinterpret_cast<v4f*>(dst + (16 * i + 4 * g + vv) * D) =
+                    v4f{acc[i][0][vv], acc[i][1][vv], acc[i][2][vv], acc[i][3][vv]};
+    }
 }
 
 // One workgroup a (value head h, 16 CT state columns from e0); the chunks in
@@ -546,16 +610,18 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
     auto load_ops = [&](int c, ChunkOps<D, CT>& o) __attribute__((always_inline)) {
         const int64_t t0 = (int64_t)c * C, base = h * a.nc + c;
         const int n = (int)min<int64_t>(C, a.T - t0);
-        const float* wr = a.W + (base * C + trow) * D + 32 * g;
-        const float* qr = a.qn + ((t0 + min(trow, n - 1)) * a.n_k + kk) * D + 32 * g;
-        const float* pr = a.P + (base * C + trow) * C + 16 * g;
+        // lane group g supplies the reduction indices 4g + 16j + e, so one
+        // load covers 64 contiguous bytes of each of the 16 rows
+        const float* wr = a.W + (base * C + trow) * D + 4 * g;
+        const float* qr = a.qn + ((t0 + min(trow, n - 1)) * a.n_k + kk) * D + 4 * g;
+        const float* pr = a.P + (base * C + trow) * C + 4 * g;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            o.w[j] = *reinterpret_cast<const v4f*>(wr + 4 * j);
-            o.q[j] = *reinterpret_cast<const v4f*>(qr + 4 * j);
+            o.w[j] = *reinterpret_cast<const v4f*>(wr + 16 * j);
+            o.q[j] = *reinterpret_cast<const v4f*>(qr + 16 * j);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 4 * j);
+        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 16 * j);
 #pragma unroll
         for (int vv = 0; vv < 4; ++vv) {
             const int t = 16 * wave + 4 * g + vv;
@@ -584,24 +650,49 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                      float* Kn) __attribute__((always_inline)) {
         const int64_t t0 = (int64_t)c * C;
         const int n = (int)min<int64_t>(C, a.T - t0);
+        // LDS operands made current by the previous chunk's last barrier, read
+        // before any matrix step so that no LDS latency sits between them: the
+        // state block (a), this chunk's keys (c), the wave's own state entries
+        // (c). Lane group g supplies the chunk rows 4g + 16j + e of (c), so its
+        // key rows sit 4 * KP floats (16 banks) from the next group's.
+        v4f sv[CT][8];
+        float kb[16][2], sold[CT][2][4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+                sv[ct][j] = *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 4 * g + 16 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float* kr = Kc + (4 * g + 16 * j + e) * KP + 32 * wave + r;
+                kb[4 * j + e][0] = kr[0];
+                kb[4 * j + e][1] = kr[16];
+            }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int it = 0; it < 2; ++it)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv)
+                    sold[ct][it][vv] = St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r];
+        __builtin_amdgcn_sched_barrier(0);
         load_ops(min(c + 1, a.nc - 1), nx);
+        __builtin_amdgcn_sched_barrier(0);
         // (a) W S0 and Q S0 for the wave's 16 tokens and each column tile
         v4f ws[CT], qs[CT];
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) ws[ct] = qs[ct] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-                const v4f sv =
-                    *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 32 * g + 4 * j);
+            for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[e], ws[ct], 0, 0, 0);
-                    qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[e], qs[ct], 0, 0, 0);
+                    ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[ct][j][e], ws[ct], 0, 0, 0);
+                    qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[ct][j][e], qs[ct], 0, 0, 0);
                 }
-            }
-        }
         // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d;
         // the 4 rows of a lane are one 16-byte store
 #pragma unroll
@@ -616,68 +707,52 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
             *reinterpret_cast<v4f*>(Dk + (16 * ct + r) * TP + 16 * wave + 4 * g) = dk;
         }
         __syncthreads();
-        // (b) O = scale (G Q S0 + P d)
-        {
-            v4f pd[CT];
+        v4f dt[CT][4], dkv[CT][4];
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct) pd[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int ct = 0; ct < CT; ++ct) {
+                dt[ct][j] = *reinterpret_cast<const v4f*>(Dt + (16 * ct + r) * TP + 4 * g + 16 * j);
+                dkv[ct][j] = *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 4 * g + 16 * j);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        // (b) P d and (c) (kfac d)^T K, independent chains interleaved.
+        // (c) computes S0^T <- G_n S0^T + (kfac d)^T K for state rows
+        // 32w..32w+31: A[col][s] = (kfac d)[s][col], B[s][i] = K[s][i]
+        // (row-major keys), D[col][i] lands in St's layout.
+        v4f pd[CT], sd[CT][2];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) pd[ct] = sd[ct][0] = sd[ct][1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
-                    const v4f dv =
-                        *reinterpret_cast<const v4f*>(Dt + (16 * ct + r) * TP + 16 * g + 4 * j);
+                    pd[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.p[j][e], dt[ct][j][e], pd[ct], 0, 0, 0);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        pd[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.p[j][e], dv[e], pd[ct], 0, 0, 0);
+                    for (int it = 0; it < 2; ++it)
+                        sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(dkv[ct][j][e], kb[4 * j + e][it],
+                                                                          sd[ct][it], 0, 0, 0);
                 }
+        // O = scale (G Q S0 + P d)
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
+        for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-                for (int vv = 0; vv < 4; ++vv) {
-                    const int t = 16 * wave + 4 * g + vv;
-                    if (t < n)
-                        a.outs[((t0 + t) * a.n_v + h) * D + e0 + 16 * ct + r] =
-                            a.scale * (o.gm[vv] * qs[ct][vv] + pd[ct][vv]);
-                }
-        }
-        // (c) S0^T <- G_n S0^T + (kfac d)^T K for state rows 32w..32w+31:
-        // A[col][s] = (kfac d)[s][col] (Dk), B[s][i] = K[s][i] (row-major keys),
-        // D[col][i] lands in St's layout. Lane group g supplies the chunk
-        // rows 4g + 16j + e, so its key rows sit 4 * KP floats (16 banks)
-        // from the next group's.
-        {
-            v4f sd[CT][2];
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) sd[ct][0] = sd[ct][1] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v4f dv[CT];
-#pragma unroll
-                for (int ct = 0; ct < CT; ++ct)
-                    dv[ct] = *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 4 * g + 16 * j);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float* kr = Kc + (4 * g + 16 * j + e) * KP + 32 * wave + r;
-                    const float kb[2] = {kr[0], kr[16]};
-#pragma unroll
-                    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-                        for (int it = 0; it < 2; ++it)
-                            sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(dv[ct][e], kb[it],
-                                                                              sd[ct][it], 0, 0, 0);
-                }
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * wave + 4 * g + vv;
+                if (t < n)
+                    a.outs[((t0 + t) * a.n_v + h) * D + e0 + 16 * ct + r] =
+                        a.scale * (o.gm[vv] * qs[ct][vv] + pd[ct][vv]);
             }
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
+        for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-                for (int it = 0; it < 2; ++it)
+            for (int it = 0; it < 2; ++it)
 #pragma unroll
-                    for (int vv = 0; vv < 4; ++vv) {
-                        float& sv = St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r];
-                        sv = o.gc * sv + sd[ct][it][vv];
-                    }
-        }
+                for (int vv = 0; vv < 4; ++vv)
+                    St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r] =
+                        o.gc * sold[ct][it][vv] + sd[ct][it][vv];
         store_kt(nx, Kn);   // the next chunk's keys into the other buffer
         __syncthreads();
     };
