@@ -375,8 +375,9 @@ struct ChunkArgs {
     const float* lg;    // [T][n_v] log decay (<= 0)
     const float* bb;    // [T][n_v] gate
     float* U;           // [n_v][nc][C][D]
-    float* W;           // [n_v][nc][C][D]
-    float* P;           // [n_v][nc][C][C]
+    float* W;           // [n_v][nc][C][D] in operand order (op_index)
+    float* P;           // [n_v][nc][C][C] in operand order
+    float* Qop;         // [n_k][nc][C][D]: normalised q in operand order
     float* gam;         // [n_v][nc][C]: G_t (0 past the chunk's last token)
     float* kfac;        // [n_v][nc][C]: exp(L_n - L_t) (0 past the last token)
     float* gC;          // [n_v][nc]: G_n
@@ -386,6 +387,14 @@ struct ChunkArgs {
     int nc;
     float scale;
 };
+
+// The scan's A operands (rows of W, Q, P) are stored in the order its waves
+// load them: element (t, k) of a chunk's C x K block (t = 16w + r, k =
+// 4g + 16j + e) at ((w * K/16 + j) * 64 + 16g + r) * 4 + e, so wave w's j-th
+// 16-byte load of lane 16g + r reads 1 KB of contiguous memory.
+__device__ __forceinline__ int op_index(int t, int k, int K) {
+    return (((t >> 4) * (K >> 4) + (k >> 4)) * 64 + ((k >> 2) & 3) * 16 + (t & 15)) * 4 + (k & 3);
+}
 
 // One workgroup a (chunk c, value head h), four waves, every product on the
 // fp32 matrix cores (16x16x4: lane (r, g) = (l % 16, l / 16) supplies A[r][g]
@@ -449,6 +458,12 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
                 const float* qrow = a.qn + ((t0 + min(16 * i + r, n - 1)) * a.n_k + kk) * D + 32 * g;
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) ar[jj] = *reinterpret_cast<const v4f*>(qrow + 4 * jj);
+                if (h < a.n_k) {   // one value head of each key head copies q
+                    float* qop = a.Qop + (kk * a.nc + c) * C * D;
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj)
+                        *reinterpret_cast<v4f*>(qop + op_index(16 * i + r, 32 * g + 4 * jj, D)) = ar[jj];
+                }
             } else {
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj)
@@ -472,7 +487,7 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
                     const int t = 16 * i + 4 * g + vv, sidx = 16 * j + r;
                     const float gm = (sidx <= t && t < n) ? expf(Ls[t] - Ls[sidx]) : 0.0f;
                     if (isq)
-                        a.P[(base * C + t) * C + sidx] = sidx <= t ? gm * acc[vv] : 0.0f;
+                        a.P[base * C * C + op_index(t, sidx, C)] = sidx <= t ? gm * acc[vv] : 0.0f;
                     else
                         As[t * AP + sidx] = sidx < t ? Bs[t] * (gm * acc[vv]) : 0.0f;
                 }
@@ -560,13 +575,16 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
                     acc[i][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ta, bv[ct], acc[i][ct], 0, 0, 0);
             }
         }
-        float* dst = (isw ? a.W : a.U) + base * C * D + c0 + 4 * r;
+        // U row-major; W in operand order (4 adjacent columns stay adjacent)
+        float* dst = (isw ? a.W : a.U) + base * C * D;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int vv = 0; vv < 4; ++vv)
-                *reinterpret_cast<v4f*>(dst + (16 * i + 4 * g + vv) * D) =
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * i + 4 * g + vv, col = c0 + 4 * r;
+                *reinterpret_cast<v4f*>(dst + (isw ? op_index(t, col, D) : t * D + col)) =
                     v4f{acc[i][0][vv], acc[i][1][vv], acc[i][2][vv], acc[i][3][vv]};
+            }
     }
 }
 
@@ -610,18 +628,18 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
     auto load_ops = [&](int c, ChunkOps<D, CT>& o) __attribute__((always_inline)) {
         const int64_t t0 = (int64_t)c * C, base = h * a.nc + c;
         const int n = (int)min<int64_t>(C, a.T - t0);
-        // lane group g supplies the reduction indices 4g + 16j + e, so one
-        // load covers 64 contiguous bytes of each of the 16 rows
-        const float* wr = a.W + (base * C + trow) * D + 4 * g;
-        const float* qr = a.qn + ((t0 + min(trow, n - 1)) * a.n_k + kk) * D + 4 * g;
-        const float* pr = a.P + (base * C + trow) * C + 4 * g;
+        // lane group g supplies the reduction indices 4g + 16j + e; the rows
+        // are stored in that order (op_index): 1 KB contiguous a load
+        const float* wr = a.W + base * C * D + (wave * (D / 16) * 64 + l) * 4;
+        const float* qr = a.Qop + (kk * a.nc + c) * C * D + (wave * (D / 16) * 64 + l) * 4;
+        const float* pr = a.P + base * C * C + (wave * (C / 16) * 64 + l) * 4;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            o.w[j] = *reinterpret_cast<const v4f*>(wr + 16 * j);
-            o.q[j] = *reinterpret_cast<const v4f*>(qr + 16 * j);
+            o.w[j] = *reinterpret_cast<const v4f*>(wr + 256 * j);
+            o.q[j] = *reinterpret_cast<const v4f*>(qr + 256 * j);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 16 * j);
+        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 256 * j);
 #pragma unroll
         for (int vv = 0; vv < 4; ++vv) {
             const int t = 16 * wave + 4 * g + vv;
@@ -787,7 +805,8 @@ int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
     int64_t b = 2 * up(T * n_k * d * 4) + 2 * up(T * n_v * 4);
     if (use_chunked(T, d)) {
         const int64_t nc = (T + kChunk - 1) / kChunk, rows = n_v * nc * kChunk;
-        b += 2 * up(rows * d * 4) + up(rows * kChunk * 4) + 2 * up(rows * 4) + up(n_v * nc * 4);
+        b += 2 * up(rows * d * 4) + up(rows * kChunk * 4) + 2 * up(rows * 4) + up(n_v * nc * 4) +
+             up(n_k * nc * kChunk * d * 4);
     }
     return b;
 }
@@ -865,6 +884,8 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
                                            up(rows * 4));
         ca.gC = reinterpret_cast<float*>(cw + 2 * up(rows * d * 4) + up(rows * kChunk * 4) +
                                          2 * up(rows * 4));
+        ca.Qop = reinterpret_cast<float*>(cw + 2 * up(rows * d * 4) + up(rows * kChunk * 4) +
+                                          2 * up(rows * 4) + up(n_v * nc * 4));
         ca.state = state;
         ca.outs = outs;
         ca.T = T;
