@@ -652,16 +652,17 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
-            const int64_t tk = t0 + min(row, n - 1);
-            const v4f kv = *reinterpret_cast<const v4f*>(a.kn + (tk * a.n_k + kk) * D + 4 * c4);
-            o.kt[i] = row < n ? kv : v4f{0.f, 0.f, 0.f, 0.f};
+            const int64_t tk = t0 + min(row, n - 1);   // rows past n: zeroed in store_kt
+            o.kt[i] = *reinterpret_cast<const v4f*>(a.kn + (tk * a.n_k + kk) * D + 4 * c4);
         }
     };
-    auto store_kt = [&](const ChunkOps<D, CT>& o, float* K) __attribute__((always_inline)) {
+    // chunk c's keys into K (rows past the chunk's tokens zero)
+    auto store_kt = [&](const ChunkOps<D, CT>& o, float* K, int c) __attribute__((always_inline)) {
+        const int n = (int)min<int64_t>(C, a.T - (int64_t)c * C);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
-            *reinterpret_cast<v4f*>(K + row * KP + 4 * c4) = o.kt[i];
+            *reinterpret_cast<v4f*>(K + row * KP + 4 * c4) = row < n ? o.kt[i] : v4f{0.f, 0.f, 0.f, 0.f};
         }
     };
     auto chunk = [&](int c, const ChunkOps<D, CT>& o, ChunkOps<D, CT>& nx, const float* Kc,
@@ -696,9 +697,11 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                 for (int vv = 0; vv < 4; ++vv)
                     sold[ct][it][vv] = St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r];
         __builtin_amdgcn_sched_barrier(0);
-        load_ops(min(c + 1, a.nc - 1), nx);
-        __builtin_amdgcn_sched_barrier(0);
-        // (a) W S0 and Q S0 for the wave's 16 tokens and each column tile
+        const int cn = min(c + 1, a.nc - 1);
+        load_ops(cn, nx);
+        // (a) W S0 and Q S0 for the wave's 16 tokens and each column tile; the
+        // next chunk's loads are issued between its matrix steps, so that
+        // their issue stalls overlap the matrix cores' work
         v4f ws[CT], qs[CT];
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) ws[ct] = qs[ct] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -711,6 +714,13 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                     ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[ct][j][e], ws[ct], 0, 0, 0);
                     qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[ct][j][e], qs[ct], 0, 0, 0);
                 }
+#pragma unroll
+        for (int i = 0; i < 41; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // a matrix step
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // a global load
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // its address arithmetic
+        }
+        __builtin_amdgcn_sched_barrier(0);
         // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d;
         // the 4 rows of a lane are one 16-byte store
 #pragma unroll
@@ -771,13 +781,13 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
                 for (int vv = 0; vv < 4; ++vv)
                     St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r] =
                         o.gc * sold[ct][it][vv] + sd[ct][it][vv];
-        store_kt(nx, Kn);   // the next chunk's keys into the other buffer
+        store_kt(nx, Kn, cn);   // the next chunk's keys into the other buffer
         __syncthreads();
     };
 
     ChunkOps<D, CT> oa, ob;
     load_ops(0, oa);
-    store_kt(oa, KT[0]);
+    store_kt(oa, KT[0], 0);
     __syncthreads();
     for (int c = 0; c < a.nc; c += 2) {
         chunk(c, oa, ob, KT[0], KT[1]);
