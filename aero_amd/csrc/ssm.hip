@@ -423,6 +423,27 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     const int n = (int)min<int64_t>(C, a.T - t0);
     const int64_t base = h * a.nc + c;
 
+    // roles: waves 0, 1 form K K^T (row tiles {3, 0} / {2, 1}) and U; waves
+    // 2, 3 form Q K^T and W. Each wave's rows from memory (V for U, Q rows
+    // for Q K^T) are loaded here, before the first barrier, with the keys.
+    const bool qw = wave >= 2;
+    const int i_hi = (wave & 1) ? 2 : 3;
+    v4f pre[16];
+    if (qw) {
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            const int i = which ? 3 - i_hi : i_hi;
+            const float* qrow = a.qn + ((t0 + min(16 * i + r, n - 1)) * a.n_k + kk) * D + 32 * g;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) pre[8 * which + jj] = *reinterpret_cast<const v4f*>(qrow + 4 * jj);
+        }
+    } else {
+        // rows past n: T's column scale (b) is zero there; any finite row
+        const float* vsrc = a.v + h * D + 64 * (wave & 1) + 4 * r;
+#pragma unroll
+        for (int ks = 0; ks < C / 4; ++ks)
+            pre[ks] = *reinterpret_cast<const v4f*>(vsrc + (t0 + min(4 * ks + g, n - 1)) * a.n_v * D);
+    }
     // the chunk's normalised keys (rows past n zero)
 #pragma unroll
     for (int i = 0; i < C * D / 4 / 256; ++i) {
@@ -446,18 +467,16 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     }
     __syncthreads();
 
-    // 1. wave w: row tiles {3, 0} (w < 2) or {2, 1}; K rows (even w) or Q rows
+    // 1. K K^T (waves 0, 1) or Q K^T (waves 2, 3) for two row tiles each
     {
-        const bool isq = (wave & 1) != 0;
-        const int i_hi = wave < 2 ? 3 : 2;
+        const bool isq = qw;
 #pragma unroll
         for (int which = 0; which < 2; ++which) {
             const int i = which ? 3 - i_hi : i_hi;
             v4f ar[8];
             if (isq) {
-                const float* qrow = a.qn + ((t0 + min(16 * i + r, n - 1)) * a.n_k + kk) * D + 32 * g;
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) ar[jj] = *reinterpret_cast<const v4f*>(qrow + 4 * jj);
+                for (int jj = 0; jj < 8; ++jj) ar[jj] = pre[8 * which + jj];
                 if (h < a.n_k) {   // one value head of each key head copies q
                     float* qop = a.Qop + (kk * a.nc + c) * C * D;
 #pragma unroll
@@ -549,23 +568,21 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     if (wave == 0) off_diag(3, 0);
     __syncthreads();
 
-    // 3. U = T diag(b) V, W = T diag(b G) K: lane r of column tile ct holds
-    // column c0 + 4r + ct, so each lane loads and stores 4 adjacent columns
+    // 3. U = T diag(b) V (waves 0, 1), W = T diag(b G) K (waves 2, 3): lane r
+    // of column tile ct holds column c0 + 4r + ct, so each lane loads and
+    // stores 4 adjacent columns
     {
-        const bool isw = wave >= 2;
+        const bool isw = qw;
         const int c0 = 64 * (wave & 1);
         v4f acc[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int ct = 0; ct < 4; ++ct) acc[i][ct] = v4f{0.f, 0.f, 0.f, 0.f};
-        const float* vsrc = a.v + h * D + c0 + 4 * r;
 #pragma unroll
         for (int ks = 0; ks < C / 4; ++ks) {
             const int sidx = 4 * ks + g;
-            // rows past n: T's column scale (b) is zero there; any finite row
-            const v4f bv = isw ? *reinterpret_cast<const v4f*>(Ks + sidx * KP + c0 + 4 * r)
-                               : *reinterpret_cast<const v4f*>(vsrc + (t0 + min(sidx, n - 1)) * a.n_v * D);
+            const v4f bv = isw ? *reinterpret_cast<const v4f*>(Ks + sidx * KP + c0 + 4 * r) : pre[ks];
             const float fs = isw ? Fs[sidx] : Bs[sidx];
 #pragma unroll
             for (int i = ks / 4; i < 4; ++i) {
