@@ -15,7 +15,7 @@
 // multiplies, three d/P-long dot/update passes and two log2(P)-step lane
 // reductions; the state is read and written once per call.
 //
-// ssm_prep_kernel computes qn, kn, dec and b for every token first (one wave
+// ssm_prep_kernel computes qn, kn, dec and b for every token first (d / 4 lanes
 // a token and key head), so the serial loop only streams them. Scans of 128
 // or more tokens at head dim 128 take the chunked (WY) form instead
 // (ssm_chunk_prep_kernel + ssm_chunk_scan_kernel, below).
@@ -40,34 +40,44 @@ __device__ __forceinline__ float softplus_dev(float x) {
     return log1pf(expf(-fabsf(x))) + (x > 0.0f ? x : 0.0f);
 }
 
-// One wave per (token t, key head kk): qn, kn; the wave of kk == 0 also
-// writes dec and b of token t for every value head (log_dec: the log of the
-// decay, g <= 0, in place of exp(g), for the chunked scan).
-__global__ __launch_bounds__(64) void ssm_prep_kernel(
+// G = d / 4 lanes per (token t, key head kk) row, each normalising 4
+// adjacent elements of q and k (one 16-byte load of each), 256 / G rows a
+// workgroup; the group of kk == 0 also writes dec and b of token t for every
+// value head (log_dec: the log of the decay, g <= 0, in place of exp(g), for
+// the chunked scan).
+template <int G>
+__global__ __launch_bounds__(256) void ssm_prep_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ alpha,
     const float* __restrict__ beta, const float* __restrict__ a_log,
     const float* __restrict__ dt_bias, float* __restrict__ qn, float* __restrict__ kn,
-    float* __restrict__ dec, float* __restrict__ bb, int64_t n_k, int64_t n_v, int64_t d,
+    float* __restrict__ dec, float* __restrict__ bb, int64_t n_rows, int64_t n_k, int64_t n_v,
     float eps, int log_dec) {
-    const int64_t row = blockIdx.x;  // t * n_k + kk
+    constexpr int D = 4 * G;
+    const int lane = threadIdx.x % G;
+    const int64_t row = (int64_t)blockIdx.x * (256 / G) + threadIdx.x / G;  // t * n_k + kk
+    if (row >= n_rows) return;   // whole groups: the sums below stay inside a group
     const int64_t t = row / n_k, kk = row % n_k;
-    const int lane = threadIdx.x;
-    const float* qr = q + row * d;
-    const float* kr = k + row * d;
+    const v4f qv = *reinterpret_cast<const v4f*>(q + row * D + 4 * lane);
+    const v4f kv = *reinterpret_cast<const v4f*>(k + row * D + 4 * lane);
     float sq = 0.0f, sk = 0.0f;
-    for (int64_t i = lane; i < d; i += 64) {
-        sq += qr[i] * qr[i];
-        sk += kr[i] * kr[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        sq += qv[e] * qv[e];
+        sk += kv[e] * kv[e];
     }
-    sq = group_sum<64>(sq);
-    sk = group_sum<64>(sk);
+    sq = group_sum<G>(sq);
+    sk = group_sum<G>(sk);
     const float nq = fmaxf(sqrtf(sq), eps), nk = fmaxf(sqrtf(sk), eps);
-    for (int64_t i = lane; i < d; i += 64) {
-        qn[row * d + i] = qr[i] / nq;
-        kn[row * d + i] = kr[i] / nk;
+    v4f qo, ko;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        qo[e] = qv[e] / nq;
+        ko[e] = kv[e] / nk;
     }
+    *reinterpret_cast<v4f*>(qn + row * D + 4 * lane) = qo;
+    *reinterpret_cast<v4f*>(kn + row * D + 4 * lane) = ko;
     if (kk == 0) {
-        for (int64_t h = lane; h < n_v; h += 64) {
+        for (int64_t h = lane; h < n_v; h += G) {
             float g = a_log[h] * softplus_dev(alpha[t * n_v + h] + dt_bias[h]);
             if (g > 0.0f) g = 0.0f;
             dec[t * n_v + h] = log_dec ? g : expf(g);
@@ -886,10 +896,19 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
     float* dc = reinterpret_cast<float*>(w + 2 * up(T * n_k * d * 4));
     float* bb = reinterpret_cast<float*>(w + 2 * up(T * n_k * d * 4) + up(T * n_v * 4));
     const bool chunked = use_chunked(T, d);
-    if (!launch("ssm_prep_kernel", ssm_prep_kernel, dim3((unsigned)(T * n_k)), dim3(64), 0, s,
-                q, k, alpha, beta, a_log, dt_bias, qn, kn, dc, bb, n_k, n_v, d, eps,
-                chunked ? 1 : 0))
-        return false;
+    {
+        const int64_t rows = T * n_k, per = 1024 / d;   // 256 threads, d / 4 a row
+        const dim3 pg((unsigned)((rows + per - 1) / per));
+        const int ld = chunked ? 1 : 0;
+        const bool ok =
+            d == 64 ? launch("ssm_prep_kernel", ssm_prep_kernel<16>, pg, dim3(256), 0, s, q, k, alpha,
+                             beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, eps, ld)
+            : d == 128 ? launch("ssm_prep_kernel", ssm_prep_kernel<32>, pg, dim3(256), 0, s, q, k,
+                                alpha, beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, eps, ld)
+                       : launch("ssm_prep_kernel", ssm_prep_kernel<64>, pg, dim3(256), 0, s, q, k,
+                                alpha, beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, eps, ld);
+        if (!ok) return false;
+    }
     if (chunked) {
         const int64_t nc = (T + kChunk - 1) / kChunk, rows = n_v * nc * kChunk;
         if (nc > 0x7fffffff || n_v > 65535) {
