@@ -321,6 +321,71 @@ __global__ __launch_bounds__(256) void ssm_conv_k_kernel(const float* __restrict
     }
 }
 
+// K = 4 with 4 adjacent channels a lane (C % 4 == 0, 16-byte aligned x, w
+// and out): a block whose taps all lie in x (t0 >= 3, the whole block inside
+// T) loads its TB + 3 rows as 16-byte loads up front, so the loads overlap;
+// other blocks take the per-channel sliding window of ssm_conv_k_kernel.
+// Same tap order, separate multiply and add from 0: bit-identical results.
+template <int TB>
+__global__ __launch_bounds__(256) void ssm_conv4_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ tail,
+                                                        float* __restrict__ out, int64_t tl,
+                                                        int64_t T, int64_t C) {
+    constexpr int K = 4;
+    const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c >= C) return;
+    const int64_t t0 = (int64_t)blockIdx.y * TB;
+    v4f wv[4];   // wv[e]: the K taps of channel c + e
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[e] = *reinterpret_cast<const v4f*>(w + (c + e) * K);
+    if (t0 >= K - 1 && t0 + TB <= T) {
+        v4f in[TB + K - 1];
+#pragma unroll
+        for (int i = 0; i < TB + K - 1; ++i)
+            in[i] = *reinterpret_cast<const v4f*>(x + (t0 - (K - 1) + i) * C + c);
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt) {
+            v4f acc;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < K; ++j) s = s + in[tt + j][e] * wv[e][j];
+                acc[e] = s;
+            }
+            *reinterpret_cast<v4f*>(out + (t0 + tt) * C + c) = acc;
+        }
+        return;
+    }
+    for (int e = 0; e < 4; ++e) {
+        const int64_t ch = c + e;
+        float win[K];
+        bool ok[K];
+        auto fetch = [&](int64_t b, float& val, bool& has) {
+            has = b >= 0;
+            val = b < 0 ? 0.0f : (b < tl ? tail[b * C + ch] : x[(b - tl) * C + ch]);
+        };
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) fetch(tl + t0 + 1 - K + j, win[j], ok[j]);
+        for (int tt = 0; tt < TB; ++tt) {
+            const int64_t t = t0 + tt;
+            if (t >= T) break;
+            fetch(tl + t, win[K - 1], ok[K - 1]);
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < K; ++j)
+                if (ok[j]) acc = acc + win[j] * wv[e][j];
+            out[t * C + ch] = acc;
+#pragma unroll
+            for (int j = 0; j < K - 1; ++j) {
+                win[j] = win[j + 1];
+                ok[j] = ok[j + 1];
+            }
+        }
+    }
+}
+
 // The new tail: the last keep rows of buf, per channel; a lane reads all of
 // its channel's rows before writing any, so tail_out may be tail.
 constexpr int kMaxConvKeep = 15;
@@ -979,8 +1044,16 @@ bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tai
         set_error("ssm_conv: too large");
         return false;
     }
-    constexpr int kTB = 32;
-    if (T > 0) {
+    constexpr int kTB = 32, kTB4 = 16;
+    // the 4-channel form from 64 tokens (short calls are all boundary blocks:
+    // the one-channel form spreads them over 4x the lanes)
+    if (T >= 4 * kTB4 && K == 4 && C % 4 == 0 && aligned16(x) && aligned16(w) &&
+        aligned16(out) && (T + kTB4 - 1) / kTB4 <= 65535) {
+        if (!launch("ssm_conv_kernel", ssm_conv4_kernel<kTB4>,
+                    dim3((unsigned)((C / 4 + 255) / 256), (unsigned)((T + kTB4 - 1) / kTB4)),
+                    dim3(256), 0, s, x, w, tail, out, tail_len, T, C))
+            return false;
+    } else if (T > 0) {
         const bool ok =
             (K == 4 && (T + kTB - 1) / kTB <= 65535)
                 ? launch("ssm_conv_kernel", ssm_conv_k_kernel<4, kTB>,

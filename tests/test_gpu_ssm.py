@@ -177,7 +177,7 @@ def test_scan_full_prefill_by_segments(hip, oracle):
 
 @pytest.mark.parametrize("T,C,K,chunks", [(7, 10, 4, [2, 5]), (1, 8192, 4, [1, 1, 1, 1]),
                                           (300, 1000, 4, [150, 150]), (5, 33, 1, [5]),
-                                          (9, 64, 6, [1, 2, 6])])
+                                          (9, 64, 6, [1, 2, 6]), (1000, 8192, 4, [500, 500])])
 def test_conv_bit_exact(hip, oracle, T, C, K, chunks):
     """Against the oracle chunk by chunk (tails shorter than kernel - 1 while
     the history fills), through the device op with the tail updated in place
