@@ -86,6 +86,7 @@ def test_scan_vs_oracle(hip, oracle, T, n_k, n_v, d):
     (128, 16, 32),     # two whole 64-token chunks at Qwen3-Next's heads
     (300, 2, 4),       # a partial last chunk (44 tokens)
     (129, 1, 2),       # a last chunk of one token
+    (256, 4, 4),       # one value head a key head
     (1000, 3, 6),      # 16 chunks, two value heads a key head
 ])
 def test_chunked_scan_vs_oracle(hip, oracle, T, n_k, n_v):
