@@ -332,7 +332,7 @@ def softmax_rows(x: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
                "softmax_rows")
 
 
-_ssm_ws: dict = {}
+_ssm_ws: dict = {}          # one workspace, grown to the largest size needed
 
 
 def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
@@ -342,7 +342,9 @@ def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
     """Gated delta-rule scan over T tokens (src/ssm.cpp:69-142): q, k
     [T, n_k, d], v / outs [T, n_v, d], alpha / beta [T, n_v], a_log / dt_bias
     [n_v], state [n_v, d, d] updated in place. The workspace (normalised q / k,
-    per-token decay and gate) is allocated once per size and reused."""
+    per-token decay and gate; the chunked form's operands from 128 tokens) is
+    one buffer, grown when a call needs more and reused by smaller calls, so
+    calls on different streams must not overlap."""
     _need(q, T * n_k * d, np.float32, "q")
     _need(k, T * n_k * d, np.float32, "k")
     _need(v, T * n_v * d, np.float32, "v")
@@ -354,12 +356,14 @@ def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
     _need(state, n_v * d * d, np.float32, "state")
     L = _lib.lib()
     wsb = int(L.aero_hip_ssm_workspace(T, n_k, n_v, d))
-    ws = _ssm_ws.get(wsb)
-    if ws is None and wsb > 0:
-        ws = _ssm_ws[wsb] = DeviceArray.empty(wsb // 4, np.float32)
+    ws = _ssm_ws.get("ws")
+    if wsb > 0 and (ws is None or ws.nbytes < wsb):
+        _ssm_ws.clear()             # the old buffer's hipFree waits for its users
+        ws = _ssm_ws["ws"] = DeviceArray.empty(-(-wsb // 4), np.float32)
     _lib.check(L.aero_hip_ssm_scan(q.ptr, k.ptr, v.ptr, alpha.ptr, beta.ptr, a_log.ptr,
                                    dt_bias.ptr, state.ptr, T, n_k, n_v, d, float(scale),
-                                   float(eps), outs.ptr, as_ptr(ws), wsb, _s(stream)),
+                                   float(eps), outs.ptr, as_ptr(ws),
+                                   ws.nbytes if ws is not None else 0, _s(stream)),
                "ssm_scan")
 
 

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from conftest import RTOL, bits_equal, golden, rel_to_scale
+from aero_amd import _lib
 from aero_amd import native_ssm as NS
 from aero_amd import ops
 from aero_amd.device import DeviceArray as DA
@@ -205,3 +206,18 @@ def test_conv_bit_exact(hip, oracle, T, C, K, chunks):
         hout, htail, htl = NS.conv(xc, w, htail, htl)
         assert bits_equal(hout, want) and htl == otl
         pos += n
+
+
+def test_workspace_grows_and_is_reused(hip, oracle):
+    """One workspace serves every size: a 300-token chunked scan, then 40
+    tokens (per-token loop, smaller workspace), then 129 (chunked again);
+    each equals the oracle and a single buffer of the largest size is kept."""
+    rng = np.random.default_rng(91)
+    scale = 128 ** -0.5
+    for T in (300, 40, 129):
+        args = inputs(rng, T, 2, 4, 128)
+        out, dst = gpu_scan(*args, scale)
+        want, wst = oracle.ssm_scan(*args, scale)
+        assert rel_to_scale(out, want) <= RTOL and rel_to_scale(dst.numpy(), wst) <= RTOL
+    assert list(ops._ssm_ws) == ["ws"]
+    assert ops._ssm_ws["ws"].nbytes >= _lib.lib().aero_hip_ssm_workspace(300, 2, 4, 128)
