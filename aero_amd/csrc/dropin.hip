@@ -74,6 +74,15 @@ Arena g_arena[kMaxDevices];
 class Staging {
 public:
     Staging() {
+        // A host-pointer call runs and copies back at once; under plan
+        // recording its kernels would be recorded instead of run, the call
+        // would copy back the unmodified input, and the plan would hold
+        // pointers into this arena, which a later larger call reallocates.
+        if (recording_plan() != nullptr) {
+            set_error("host-pointer entry points cannot be recorded into a plan; "
+                      "use the aero_hip_* device-pointer ops inside a plan");
+            return;
+        }
         int dev = 0;
         ok_ = hip_ok(hipGetDevice(&dev), "hipGetDevice");
         if (ok_ && (dev < 0 || dev >= kMaxDevices)) {
@@ -86,7 +95,7 @@ public:
             ok_ = hip_ok(hipStreamCreate(&a_->stream), "hipStreamCreate");
     }
     bool ok() const { return ok_; }
-    hipStream_t stream() const { return a_->stream; }
+    hipStream_t stream() const { return a_ ? a_->stream : nullptr; }
 
     // Reserve sizes[i] bytes for each i; pointers land in out[i].
     bool reserve(std::initializer_list<size_t> sizes, void** out) {
@@ -114,14 +123,16 @@ public:
     }
 
     bool h2d(void* d, const void* h, size_t n) {
+        if (!ok_) return false;
         return n == 0 || hip_ok(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, a_->stream),
                                 "hipMemcpyAsync H2D");
     }
     bool d2h(void* h, const void* d, size_t n) {
+        if (!ok_) return false;
         return n == 0 || hip_ok(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, a_->stream),
                                 "hipMemcpyAsync D2H");
     }
-    bool finish() { return hip_ok(hipStreamSynchronize(a_->stream), "hipStreamSynchronize"); }
+    bool finish() { return ok_ && hip_ok(hipStreamSynchronize(a_->stream), "hipStreamSynchronize"); }
 
 private:
     Arena* a_ = nullptr;

@@ -342,8 +342,12 @@ private:
                 const uint64_t dim = c.get<uint64_t>();
                 if (dim > ((uint64_t)1 << 40)) throw std::runtime_error("tensor " + t.name + ": bad dim");
                 t.dims[d] = (int64_t)dim;
+                // bound the product before forming it: n <= 2^48 and dim <= 2^40
+                // could overflow int64 (and wrap to a small count) otherwise
+                constexpr int64_t kMaxElements = (int64_t)1 << 48;
+                if (dim != 0 && n > kMaxElements / (int64_t)dim)
+                    throw std::runtime_error("tensor " + t.name + ": too large");
                 n *= (int64_t)dim;
-                if (n > ((int64_t)1 << 48)) throw std::runtime_error("tensor " + t.name + ": too large");
             }
             t.n_elements = n;
             t.type = c.get<uint32_t>();

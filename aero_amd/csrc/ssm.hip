@@ -708,7 +708,6 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t h = blockIdx.x, kk = h % a.n_k;
     const int e0 = NC * blockIdx.y;
-    const int trow = 16 * wave + r;
     float* Sg = a.state + h * D * D;
 #pragma unroll
     for (int i = 0; i < D * NC / 256; ++i) {

@@ -7,6 +7,7 @@ address passed to the aero_hip_* entry points.
 from __future__ import annotations
 
 import ctypes
+import threading
 
 import numpy as np
 
@@ -173,22 +174,33 @@ class Plan:
             ops.act_mul("silu", g, u, o)
         plan.launch(stream)              # issues the recorded kernels in order
 
-    The buffers an op was recorded with must outlive the plan; the plan keeps
-    Python references to nothing, so the caller holds them.
+    The caller's buffers an op was recorded with must outlive the plan: the
+    caller holds them. Library-owned scratch buffers (Workspace) that ops use
+    while the plan records are held by the plan itself, so a later, larger
+    call that replaces such a buffer cannot free memory the plan still
+    writes.
     """
 
     def __init__(self):
         self.handle = _lib.lib().aero_hip_plan_create()
         if not self.handle:
             raise MemoryError("plan create failed")
+        self._held: list = []
 
     def __enter__(self):
         _lib.check(_lib.lib().aero_hip_plan_begin(self.handle), "plan_begin")
+        _recording.plan = self
         return self
 
     def __exit__(self, *exc):
+        _recording.plan = None
         _lib.check(_lib.lib().aero_hip_plan_end(self.handle), "plan_end")
         return False
+
+    def hold(self, buf) -> None:
+        """Keep `buf` alive as long as this plan exists."""
+        if not any(b is buf for b in self._held):
+            self._held.append(buf)
 
     def __len__(self) -> int:
         return int(_lib.lib().aero_hip_plan_size(self.handle))
@@ -212,12 +224,46 @@ class Plan:
             if L is not None:
                 L.aero_hip_plan_destroy(self.handle)
             self.handle = None
+        self._held = []
 
     def __del__(self):
         try:
             self.destroy()
         except Exception:
             pass
+
+
+_recording = threading.local()
+
+
+def recording_plan() -> "Plan | None":
+    """The plan this thread is recording into, if any."""
+    return getattr(_recording, "plan", None)
+
+
+class Workspace:
+    """Device scratch memory for one family of ops (split GEMM, attention,
+    DeltaNet scan): one buffer, grown to the largest request seen and never
+    shrunk, so alternating sizes (a prefill layer's 4096- and 14336-column
+    GEMMs) reuse it instead of freeing and reallocating (hipFree waits for
+    the device). A buffer used while a plan records is held by that plan.
+    Calls that share a workspace must not run concurrently on different
+    streams: they would share its contents."""
+
+    def __init__(self, what: str):
+        self.what = what
+        self.buf: DeviceArray | None = None
+
+    def get(self, nbytes: int) -> "DeviceArray | None":
+        if nbytes <= 0:
+            return None
+        if self.buf is None or self.buf.nbytes < nbytes:
+            self.buf = None                    # drop ours before allocating the larger one
+            self.buf = DeviceArray.empty(-(-int(nbytes) // 4), np.float32)
+        plan = recording_plan()
+        if plan is not None:
+            plan.hold(self.buf)
+        return self.buf
 
 
 def time_next_kernel(start: Event, stop: Event) -> None:

@@ -20,9 +20,8 @@ from __future__ import annotations
 
 import ctypes
 import json
-import struct
 from dataclasses import dataclass
-from typing import Any, Dict, List, Tuple
+from typing import Any, Dict, Tuple
 
 import numpy as np
 
@@ -53,12 +52,6 @@ TYPE_NAMES: Dict[int, str] = {
     T_BF16: "BF16",
 }
 
-_SCALAR_FMT = {
-    GGUF_UINT8: "<B", GGUF_INT8: "<b", GGUF_UINT16: "<H", GGUF_INT16: "<h",
-    GGUF_UINT32: "<I", GGUF_INT32: "<i", GGUF_FLOAT32: "<f", GGUF_BOOL: "<?",
-    GGUF_UINT64: "<Q", GGUF_INT64: "<q", GGUF_FLOAT64: "<d",
-}
-
 # types the GPU dequantises (aero_hip_dequant / aero_hip_tensor_rows), and
 # those with a quantised GPU matvec (aero_hip_matvec)
 DEVICE_TYPES = frozenset({T_F32, T_F16, T_BF16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_IQ4_XS})
@@ -71,25 +64,27 @@ class GGUFUnavailable(_lib.AeroHipUnavailable):
 
 @dataclass
 class TensorInfo:
-    """One tensor of the index (engine/gguf.py:59-78)."""
+    """Where one tensor lives in the file and what it holds. `dims` are the
+    extents exactly as the file lists them, innermost first; `shape` turns
+    them round into numpy's outermost-first order. `offset` counts from the
+    start of the data section; `nbytes` is -1 for a GGML type whose block
+    geometry the library does not know. Field and property names are the
+    reference reader's interface (engine/gguf.py:59-78)."""
     name: str
-    dims: Tuple[int, ...]      # GGUF order: fastest-varying first
+    dims: Tuple[int, ...]
     type_id: int
-    offset: int                # relative to the data section
+    offset: int
     n_elements: int = 0
-    nbytes: int = -1           # bytes in the file (-1: a type of unknown block size)
+    nbytes: int = -1
 
     @property
     def shape(self) -> Tuple[int, ...]:
-        """Row-major shape (GGUF stores dims reversed)."""
-        return tuple(reversed(self.dims))
+        return self.dims[::-1]
 
     @property
     def type_name(self) -> str:
-        return TYPE_NAMES.get(self.type_id, f"type{self.type_id}")
-
-    def __str__(self) -> str:
-        return f"{self.name} {self.shape} {self.type_name}"
+        known = TYPE_NAMES.get(self.type_id)
+        return known if known is not None else f"ggml_type_{self.type_id}"
 
 
 def _text(s: str) -> str:
@@ -154,8 +149,8 @@ class DeviceTensor:
 class GGUFReader:
     """Random-access reader over a .gguf file (engine/gguf.py:105-445)."""
 
-    # tensors at or below this size are treated as constants and memoised
-    # (engine/gguf.py:274-275)
+    # tensor() keeps the host result of any tensor up to this size, as the
+    # reference reader does for norms and biases (engine/gguf.py:274-275)
     SMALL_TENSOR_BYTES = 1 << 20
 
     def __init__(self, path: str) -> None:
@@ -203,17 +198,16 @@ class GGUFReader:
 
     # ---- lifetime --------------------------------------------------------
     def summary(self) -> str:
-        """engine/gguf.py:431-443."""
-        lines = [f"{self.path}",
-                 f"  gguf v{self.version}, arch={self.arch()}, "
-                 f"{len(self.tensors)} tensors, {len(self.kv)} metadata keys"]
-        for k in ("block_count", "embedding_length", "attention.head_count",
-                  "attention.head_count_kv", "attention.key_length",
-                  "feed_forward_length", "context_length"):
-            v = self.hp(k)
-            if v is not None:
-                lines.append(f"    {k} = {v}")
-        return "\n".join(lines)
+        """A short human-readable description: the file, its format version,
+        architecture and counts, then every scalar hyperparameter stored under
+        the architecture's prefix, sorted by name."""
+        arch = self.arch()
+        head = (f"{self.path}: GGUF v{self.version}, architecture '{arch}', "
+                f"{len(self.tensors)} tensors, {len(self.kv)} metadata entries")
+        prefix = arch + "."
+        body = [f"  {k[len(prefix):]} = {v}" for k, v in sorted(self.kv.items())
+                if k.startswith(prefix) and isinstance(v, (int, float, str, bool))]
+        return "\n".join([head] + body)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -236,16 +230,19 @@ class GGUFReader:
         except Exception:
             pass
 
-    # ---- metadata helpers (engine/gguf.py:221-230) -------------------------
+    # ---- metadata (engine/gguf.py:221-230 is the interface) ---------------
     def get(self, key: str, default: Any = None) -> Any:
+        """The value stored under the full key `key`, else `default`."""
         return self.kv.get(key, default)
 
     def arch(self) -> str:
+        """general.architecture, or "unknown" when the file has none."""
         return str(self.kv.get("general.architecture", "unknown"))
 
     def hp(self, suffix: str, default: Any = None) -> Any:
-        """Architecture-scoped hyperparameter, e.g. hp('block_count')."""
-        return self.kv.get(f"{self.arch()}.{suffix}", default)
+        """The value under "<architecture>.<suffix>" (for a llama file,
+        hp("context_length") reads llama.context_length), else `default`."""
+        return self.kv.get(self.arch() + "." + suffix, default)
 
     # ---- tensor access -----------------------------------------------------
     def _cname(self, info: TensorInfo) -> bytes:
@@ -380,81 +377,3 @@ class GGUFReader:
         """y = W @ x on the GPU (engine/gguf.py:387-417). Returns (y, bytes of W)."""
         Y, nb = self.matmul(name, np.asarray(x, dtype=np.float32)[None, :])
         return Y[0], nb
-
-
-class GGUFWriter:
-    """Writes a GGUF file (the interface of engine/gguf.py:448-526): version 3,
-    the metadata in the order added, the tensor index, each tensor's bytes at a
-    multiple of the alignment in the data section, the file padded to it."""
-
-    def __init__(self, arch: str, alignment: int = DEFAULT_ALIGNMENT) -> None:
-        if alignment <= 0 or alignment & (alignment - 1):
-            raise ValueError(f"bad alignment {alignment} (must be a power of two)")
-        self.arch = arch
-        self.alignment = alignment
-        self.kv: List[Tuple[str, int, Any]] = [
-            ("general.architecture", GGUF_STRING, arch),
-            ("general.alignment", GGUF_UINT32, alignment),
-        ]
-        self.tensors: List[Tuple[str, Tuple[int, ...], int, bytes]] = []
-
-    def add_kv(self, key: str, type_id: int, value: Any) -> None:
-        """value: a scalar, a str, or (element type, items) for an array."""
-        self.kv.append((key, type_id, value))
-
-    def add_scalar(self, key: str, value: Any) -> None:
-        self.add_kv(key, GGUF_UINT32 if isinstance(value, int) else GGUF_FLOAT32, value)
-
-    def add_tensor(self, name: str, shape: Tuple[int, ...], raw: bytes, type_id: int) -> None:
-        """`shape` is row-major; GGUF stores it reversed (fastest first)."""
-        self.tensors.append((name, tuple(reversed(shape)), type_id, bytes(raw)))
-
-    @staticmethod
-    def _str(s) -> bytes:
-        b = s.encode("utf-8") if isinstance(s, str) else bytes(s)
-        return struct.pack("<Q", len(b)) + b
-
-    @classmethod
-    def _value(cls, t: int, v: Any, out: List[bytes]) -> None:
-        if t == GGUF_STRING:
-            out.append(cls._str(v))
-        elif t == GGUF_ARRAY:
-            et, items = v
-            out.append(struct.pack("<IQ", et, len(items)))
-            fmt = _SCALAR_FMT.get(et)
-            if fmt is not None:                      # scalars packed in one call
-                out.append(struct.pack("<%d%s" % (len(items), fmt[1]), *items))
-            else:
-                for it in items:
-                    cls._value(et, it, out)
-        else:
-            out.append(struct.pack(_SCALAR_FMT[t], v))
-
-    def to_bytes(self) -> bytes:
-        head: List[bytes] = [MAGIC, struct.pack("<IQQ", 3, len(self.tensors), len(self.kv))]
-        for key, t, v in self.kv:
-            head.append(self._str(key) + struct.pack("<I", t))
-            self._value(t, v, head)
-        offsets, cur = [], 0
-        for _n, _d, _t, raw in self.tensors:
-            offsets.append(cur)
-            cur += len(raw)
-            cur += (-cur) % self.alignment
-        for (name, dims, t, _raw), off in zip(self.tensors, offsets):
-            head.append(self._str(name) + struct.pack("<I", len(dims)))
-            head.append(struct.pack("<%dQ" % len(dims), *dims))
-            head.append(struct.pack("<IQ", t, off))
-        out = b"".join(head)
-        out += b"\x00" * ((-len(out)) % self.alignment)
-        parts, pos = [out], 0
-        for (_n, _d, _t, raw), off in zip(self.tensors, offsets):
-            parts.append(b"\x00" * (off - pos))
-            parts.append(raw)
-            pos = off + len(raw)
-        tail = (len(out) + pos) % self.alignment
-        parts.append(b"\x00" * ((-tail) % self.alignment))
-        return b"".join(parts)
-
-    def write(self, path: str) -> None:
-        with open(path, "wb") as f:
-            f.write(self.to_bytes())

@@ -13,7 +13,7 @@ import ctypes
 import numpy as np
 
 from . import _lib
-from .device import DeviceArray, Stream, as_ptr
+from .device import DeviceArray, Stream, Workspace, as_ptr
 
 NORM_UNIT_OFFSET = 1
 NORM_L2 = 2
@@ -184,7 +184,7 @@ def dequant(dtype: int, raw: DeviceArray, out: DeviceArray, n_values: int,
                                            _s(stream)), "dequant")
 
 
-_gemm_ws: dict = {}
+_gemm_ws = Workspace("split GEMM")
 
 
 def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: int,
@@ -207,11 +207,8 @@ def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: i
     wsb = int(L.aero_hip_matmul_workspace(int(dtype), n_cols, n_tok)) if n_tok >= 32 else 0
     if wsb and split:
         ws = _gemm_ws.get(wsb)
-        if ws is None:
-            _gemm_ws.clear()          # one workspace at a time: the largest recent size
-            ws = _gemm_ws[wsb] = DeviceArray.empty(wsb // 4, np.float32)
         _lib.check(L.aero_hip_matmul(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows, n_cols,
-                                     n_tok, ws.ptr, wsb, _s(stream)), "matmul")
+                                     n_tok, ws.ptr, ws.nbytes, _s(stream)), "matmul")
         return
     _lib.check(L.aero_hip_matvec(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows,
                                  n_cols, n_tok, _s(stream)), "matvec")
@@ -285,7 +282,7 @@ def kv_write(dt: int, x: DeviceArray, n_tok: int, heads: int, dim: int, q: Devic
                                             as_ptr(scale), _s(stream)), "kv_write")
 
 
-_ws_cache: dict = {}
+_attn_ws = Workspace("attention chunk partials")
 
 
 def attention(q: DeviceArray, k: DeviceArray, v: DeviceArray, out: DeviceArray, n_q: int,
@@ -312,15 +309,12 @@ def attention(q: DeviceArray, k: DeviceArray, v: DeviceArray, out: DeviceArray, 
         _need(v_scale, n_kv * n_head_kv, np.float32, "v_scale")
     L = _lib.lib()
     wsb = int(L.aero_hip_attention_workspace(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv))
-    ws = None
-    if wsb > 0:
-        ws = _ws_cache.get(wsb)
-        if ws is None:
-            ws = _ws_cache[wsb] = DeviceArray.empty(wsb // 4, np.float32)
+    ws = _attn_ws.get(wsb)
     _lib.check(L.aero_hip_attention(q.ptr, kv_dt, k.ptr, as_ptr(k_scale), v.ptr,
                                     as_ptr(v_scale), out.ptr, n_q, n_head, n_head_kv, head_dim,
                                     value_dim, float(scale), as_ptr(qpos), as_ptr(kpos), n_kv,
-                                    int(window), as_ptr(ws), wsb, _s(stream)), "attention")
+                                    int(window), as_ptr(ws), ws.nbytes if ws is not None else 0,
+                                    _s(stream)), "attention")
 
 
 def softmax_rows(x: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
@@ -332,7 +326,7 @@ def softmax_rows(x: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
                "softmax_rows")
 
 
-_ssm_ws: dict = {}          # one workspace, grown to the largest size needed
+_ssm_ws = Workspace("DeltaNet scan")
 
 
 def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
@@ -355,11 +349,7 @@ def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
     _need(dt_bias, n_v, np.float32, "dt_bias")
     _need(state, n_v * d * d, np.float32, "state")
     L = _lib.lib()
-    wsb = int(L.aero_hip_ssm_workspace(T, n_k, n_v, d))
-    ws = _ssm_ws.get("ws")
-    if wsb > 0 and (ws is None or ws.nbytes < wsb):
-        _ssm_ws.clear()             # the old buffer's hipFree waits for its users
-        ws = _ssm_ws["ws"] = DeviceArray.empty(-(-wsb // 4), np.float32)
+    ws = _ssm_ws.get(int(L.aero_hip_ssm_workspace(T, n_k, n_v, d)))
     _lib.check(L.aero_hip_ssm_scan(q.ptr, k.ptr, v.ptr, alpha.ptr, beta.ptr, a_log.ptr,
                                    dt_bias.ptr, state.ptr, T, n_k, n_v, d, float(scale),
                                    float(eps), outs.ptr, as_ptr(ws),

@@ -964,6 +964,61 @@ def attention_bench(a):
 PCIE_GEN5_X16_GBS = 64.0  # host link, one direction
 
 
+def gguf_image(meta, tensors, alignment: int = 32) -> bytes:
+    """The bytes of a GGUF v3 file. `meta`: (key, value type, value) in file
+    order, an array value being (element type, items); `tensors`: (name,
+    row-major shape, GGML type, raw bytes). The data section starts at the
+    first multiple of `alignment` after the index, each tensor at a multiple
+    of it within the section, and the file ends on one."""
+    import struct
+
+    from aero_amd import gguf as AG
+
+    packed = {AG.GGUF_UINT8: "B", AG.GGUF_INT8: "b", AG.GGUF_UINT16: "H", AG.GGUF_INT16: "h",
+              AG.GGUF_UINT32: "I", AG.GGUF_INT32: "i", AG.GGUF_FLOAT32: "f", AG.GGUF_BOOL: "?",
+              AG.GGUF_UINT64: "Q", AG.GGUF_INT64: "q", AG.GGUF_FLOAT64: "d"}
+    buf = bytearray()
+
+    def text(s):
+        b = s.encode("utf-8")
+        buf.extend(struct.pack("<Q", len(b)))
+        buf.extend(b)
+
+    def value(t, v):
+        if t == AG.GGUF_STRING:
+            text(v)
+        elif t == AG.GGUF_ARRAY:
+            et, items = v
+            buf.extend(struct.pack("<IQ", et, len(items)))
+            if et in packed:
+                buf.extend(struct.pack(f"<{len(items)}{packed[et]}", *items))
+            else:
+                for it in items:
+                    value(et, it)
+        else:
+            buf.extend(struct.pack("<" + packed[t], v))
+
+    def pad():
+        buf.extend(bytes(-len(buf) % alignment))
+
+    buf.extend(b"GGUF")
+    buf.extend(struct.pack("<IQQ", 3, len(tensors), len(meta)))
+    for key, t, v in meta:
+        text(key)
+        buf.extend(struct.pack("<I", t))
+        value(t, v)
+    rel = 0
+    for name, shape, t, raw in tensors:
+        text(name)
+        buf.extend(struct.pack(f"<I{len(shape)}QIQ", len(shape), *shape[::-1], t, rel))
+        rel += len(raw) + (-len(raw) % alignment)
+    pad()
+    for _name, _shape, _t, raw in tensors:
+        buf.extend(raw)
+        pad()
+    return bytes(buf)
+
+
 def llama3_gguf(path: str, rng) -> dict:
     """A synthetic Llama-3-8B GGUF file: the model's metadata and tokenizer
     sizes (128256 tokens, 280147 merges), its 291 tensor records with their
@@ -972,33 +1027,35 @@ def llama3_gguf(path: str, rng) -> dict:
     each (the index is the model's, the file is not 4.9 GB)."""
     from aero_amd import gguf as AG, workloads as W
 
-    w = AG.GGUFWriter("llama", 32)
+    meta = [("general.architecture", AG.GGUF_STRING, "llama"),
+            ("general.alignment", AG.GGUF_UINT32, 32)]
     for k, v in (("block_count", 32), ("context_length", 8192), ("embedding_length", 4096),
                  ("feed_forward_length", 14336), ("attention.head_count", 32),
                  ("attention.head_count_kv", 8), ("vocab_size", 128256)):
-        w.add_kv(f"llama.{k}", AG.GGUF_UINT32, v)
-    w.add_kv("llama.rope.freq_base", AG.GGUF_FLOAT32, 500000.0)
-    w.add_kv("llama.attention.layer_norm_rms_epsilon", AG.GGUF_FLOAT32, 1e-5)
-    w.add_kv("tokenizer.ggml.model", AG.GGUF_STRING, "gpt2")
-    w.add_kv("tokenizer.ggml.tokens", AG.GGUF_ARRAY,
-             (AG.GGUF_STRING, [f"\u0120tok{i}" for i in range(128256)]))
-    w.add_kv("tokenizer.ggml.token_type", AG.GGUF_ARRAY, (AG.GGUF_INT32, [1] * 128256))
-    w.add_kv("tokenizer.ggml.merges", AG.GGUF_ARRAY,
-             (AG.GGUF_STRING, [f"\u0120t {i}" for i in range(280147)]))
-    w.add_kv("tokenizer.ggml.bos_token_id", AG.GGUF_UINT32, 128000)
+        meta.append((f"llama.{k}", AG.GGUF_UINT32, v))
+    meta += [("llama.rope.freq_base", AG.GGUF_FLOAT32, 500000.0),
+             ("llama.attention.layer_norm_rms_epsilon", AG.GGUF_FLOAT32, 1e-5),
+             ("tokenizer.ggml.model", AG.GGUF_STRING, "gpt2"),
+             ("tokenizer.ggml.tokens", AG.GGUF_ARRAY,
+              (AG.GGUF_STRING, [f"\u0120tok{i}" for i in range(128256)])),
+             ("tokenizer.ggml.token_type", AG.GGUF_ARRAY, (AG.GGUF_INT32, [1] * 128256)),
+             ("tokenizer.ggml.merges", AG.GGUF_ARRAY,
+              (AG.GGUF_STRING, [f"\u0120t {i}" for i in range(280147)])),
+             ("tokenizer.ggml.bos_token_id", AG.GGUF_UINT32, 128000)]
     emb = W.make_table(12, 128256 * 16, rng).tobytes()
-    w.add_tensor("token_embd.weight", (128256, 4096), emb, 12)
     norm = np.ones(4096, np.float32).tobytes()
     block = W.make_table(12, 1, rng).tobytes()
+    tensors = [("token_embd.weight", (128256, 4096), 12, emb)]
     for i in range(32):
-        w.add_tensor(f"blk.{i}.attn_norm.weight", (4096,), norm, 0)
-        w.add_tensor(f"blk.{i}.ffn_norm.weight", (4096,), norm, 0)
-        for t in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
-            w.add_tensor(f"blk.{i}.{t}.weight", (1, 256), block, 12)
-    w.add_tensor("output_norm.weight", (4096,), norm, 0)
-    w.add_tensor("output.weight", (1, 256), block, 12)
-    w.write(path)
-    return {"tensors": len(w.tensors), "file_bytes": os.path.getsize(path),
+        tensors += [(f"blk.{i}.attn_norm.weight", (4096,), 0, norm),
+                    (f"blk.{i}.ffn_norm.weight", (4096,), 0, norm)]
+        tensors += [(f"blk.{i}.{t}.weight", (1, 256), 12, block)
+                    for t in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                              "ffn_down")]
+    tensors += [("output_norm.weight", (4096,), 0, norm), ("output.weight", (1, 256), 12, block)]
+    with open(path, "wb") as f:
+        f.write(gguf_image(meta, tensors, 32))
+    return {"tensors": len(tensors), "file_bytes": os.path.getsize(path),
             "table_bytes": len(emb)}
 
 

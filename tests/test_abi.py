@@ -184,13 +184,15 @@ def test_reference_python_surface():
                                      ("X", inspect._empty), ("threads", 1)]
     assert (native.DTYPE_Q8_0, native.DTYPE_Q4_K, native.DTYPE_Q6_K) == (8, 12, 14)
     assert native.NATIVE_TYPES == {8, 12, 13, 14, 23}
+    # input checks that run before the library is needed
     with pytest.raises(TypeError):
-        TN._p([1.0, 2.0])
+        TN._flat32(np.array(["a", "b"]))
+    assert TN._flat32([1, 2]).dtype == np.float32
     with pytest.raises(TypeError):
-        TN._p(np.zeros(3, np.float64))
+        native._byte_view([1, 2])
     with pytest.raises(TypeError):
-        native._u8([1, 2])
-    assert native._raw_nbytes(bytes(100), 12, 256) == 100
+        native._byte_view(np.zeros(4, np.int32))
+    assert native._byte_len(bytes(100)) == 100 and native._rows_in(bytes(288), 12, 256) == 2
 
 
 def test_workload_bytes_match_the_published_roofline_table():
@@ -226,3 +228,79 @@ def test_per_op_selector(monkeypatch):
         select.enabled("rmsnorm")
     with pytest.raises(ValueError):
         select.enabled("softmax")
+
+
+def test_native_ssm_fallback_contract():
+    """The reference's callers catch only SsmUnavailable and then run numpy
+    (engine/ssm.py:215-221, :297-304; engine/moe.py:73-77). A head dim the GPU
+    scan lacks (the reference's own tests use d = 6, tests/test_ssm_native.py:177)
+    and the routines outside the path must raise exactly that, before any
+    device work, so such a caller still gets its CPU result."""
+    from aero_amd import native_ssm as NS
+    from oracle import cpuref as O
+
+    rng = np.random.default_rng(5)
+    H, d = 3, 6
+    q, k, v = (rng.standard_normal((H, d)).astype(np.float32) for _ in range(3))
+    alpha, beta = rng.standard_normal(H).astype(np.float32), rng.standard_normal(H).astype(
+        np.float32)
+    a_log, dt_bias = rng.standard_normal(H).astype(np.float32) * 0.1, np.zeros(H, np.float32)
+    state = rng.standard_normal((H, d, d)).astype(np.float32)
+
+    def caller_step():                      # the shape of engine/ssm.py:215-221
+        try:
+            return NS.delta_step(q, k, v, alpha, beta, a_log, dt_bias, state, 0.5)
+        except NS.SsmUnavailable:
+            return O.ssm_delta_step(q, k, v, alpha, beta, a_log, dt_bias, state, 0.5)
+
+    out, st = caller_step()
+    want_out, want_st = O.ssm_delta_step(q, k, v, alpha, beta, a_log, dt_bias, state, 0.5)
+    assert np.array_equal(out, want_out) and np.array_equal(st, want_st)
+    T = 4
+    qs = rng.standard_normal((T, H, d)).astype(np.float32)
+    with pytest.raises(NS.SsmUnavailable, match="head dims"):
+        NS.scan(qs, qs, qs, np.zeros((T, H), np.float32), np.zeros((T, H), np.float32),
+                a_log, dt_bias, state, 0.5)
+    for f in (NS.forward, NS.route, NS.expert_accum, NS.ffn_block):
+        with pytest.raises(NS.SsmUnavailable):
+            f()
+
+
+def test_workspace_grows_only_and_plans_hold_what_they_recorded(monkeypatch):
+    """Host logic of ops' scratch buffers, without a GPU: one buffer per op
+    family, reallocated only when a call needs more (alternating 4096- and
+    14336-column GEMMs keep the largest), and every buffer used while a plan
+    records stays referenced by that plan after a larger call replaces it."""
+    from aero_amd import device as D
+
+    class FakeBuf:
+        def __init__(self, shape, dtype=np.float32):
+            self.nbytes = int(np.prod(shape)) * np.dtype(dtype).itemsize
+
+    monkeypatch.setattr(D.DeviceArray, "empty", classmethod(lambda cls, s, dt=np.float32:
+                                                            FakeBuf(s, dt)))
+    ws = D.Workspace("split GEMM")
+    small, big = 6 * 32 * 4096, 6 * 32 * 14336
+    a = ws.get(small)
+    b = ws.get(big)
+    c = ws.get(small)
+    assert b is c and a is not b and b.nbytes >= big
+    assert ws.get(0) is None
+
+    class FakePlan:
+        def __init__(self):
+            self._held = []
+        hold = D.Plan.hold
+
+    p = FakePlan()
+    D._recording.plan = p
+    try:
+        r1 = ws.get(small)                  # the current (largest) buffer
+        r2 = ws.get(2 * big)                # grows during recording
+        ws.get(big)
+    finally:
+        D._recording.plan = None
+    assert r1 is b and r2 is not b
+    assert p._held == [b, r2]              # each once, in first-use order
+    ws.get(4 * big)                         # outside the plan: replaces r2
+    assert ws.buf is not r2 and p._held[1] is r2

@@ -300,7 +300,8 @@ def test_library_parser_matches_compiled_reference(tmp_path):
 def test_library_parser_refusals(tmp_path):
     """Each malformed file is refused with a reason (no crash, no partial
     reader): bad magic, versions 1 and 4, unknown value type, bad alignment,
-    n_dims 5, non-whole blocks, tensor data past the end, and every
+    n_dims 5, non-whole blocks, tensor data past the end, element counts
+    past 2^48 (including ones whose product overflows int64), and every
     truncation of a valid file."""
     good = G.write([("general.architecture", G.STRING, "llama"), ("a.b", G.U32, 1)],
                    [("t", (2, 32), 8, bytes(68))])
@@ -313,6 +314,10 @@ def test_library_parser_refusals(tmp_path):
         "ndims5": G.write([], [("t", (1, 1, 1, 1, 32), 8, bytes(34))]),
         "blocks": G.write([], [("t", (1, 33), 8, bytes(68))]),
         "past_end": G.write([], [("t", (4, 32), 8, bytes(136))])[:-64],
+        # element counts whose int64 product would wrap (2^80, 2^72): refused
+        # before the multiply, not accepted as a small tensor
+        "overflow2": G.write([], [("t", (1 << 40, 1 << 40), 0, bytes(4))]),
+        "overflow3": G.write([], [("t", (1 << 24, 1 << 24, 1 << 24), 0, bytes(4))]),
     }
     for name, data in cases.items():
         path = write(tmp_path, f"bad_{name}.gguf", data)
@@ -341,18 +346,17 @@ def test_library_parser_large_vocabulary(tmp_path):
         assert r.kv["tokenizer.ggml.scores"] == scores
 
 
-def test_library_writer_matches_oracle_writer(tmp_path):
-    """aero_amd.gguf.GGUFWriter writes the same bytes as the oracle's writer
-    for the same content, and the parser reads back what was written."""
+def test_bench_gguf_image_matches_oracle_writer(tmp_path):
+    """bench.py's GGUF image builder (the synthetic Llama-3 file of
+    `bench.py --gguf`) lays out the same bytes as the oracle's writer for the
+    same content, and the library's parser reads back what was written."""
+    import bench
+
     rng = np.random.default_rng(5)
     kv, tensors = rich_file(rng, 64)
-    w = AG.GGUFWriter("llama", 64)
-    for key, t, v in kv[2:]:
-        w.add_kv(key, t, v)
-    for name, shape, t, raw in tensors:
-        w.add_tensor(name, shape, raw, t)
-    data = w.to_bytes()
-    assert data == G.write(kv, tensors, 64)
+    ascii_kv = [e for e in kv if not isinstance(e[2], bytes)]
+    data = bench.gguf_image(ascii_kv, [(n, s, t, raw) for n, s, t, raw in tensors], 64)
+    assert data == G.write(ascii_kv, tensors, 64)
     path = write(tmp_path, "w.gguf", data)
     with AG.GGUFReader(path) as r:
         assert r.kv == G.parse(data)["kv"]
