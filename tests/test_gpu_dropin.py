@@ -149,7 +149,6 @@ def f16(v: float) -> bytes:
 def test_native_dequant(hip, oracle, type_id, bb, bv):
     rng = np.random.default_rng(4)
     assert type_id in NK.NATIVE_TYPES
-    assert NK._BLOCK_BYTES[type_id] == bb and NK._BLOCK_VALUES[type_id] == bv
     assert NK.block_bytes(type_id) == bb and NK.block_values(type_id) == bv
     NB = 4
     buf = bytearray(rng.integers(0, 256, size=NB * bb, dtype=np.uint8).tobytes())
