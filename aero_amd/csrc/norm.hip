@@ -15,6 +15,8 @@
 // 128-134); L2: inv = 1/max(sqrtf(ss), eps) (src/tensor.cpp:136-154); gated:
 // out = ((x/denom)*w)*(z/(1+expf(-z))) (src/ssm.cpp:17,327-343). Only the
 // summation order of ss differs (tree instead of serial).
+#include <algorithm>
+
 #include "common.hpp"
 #include "aero_hip.h"
 
@@ -34,7 +36,11 @@ struct NormParams {
     int w_len;           // weight period
     float eps;
     int flags;
+    float* xo;           // residual form: x + z written here (may alias x or z)
 };
+
+// Kernel forms: plain / L2 norm, gated norm*silu(z), residual add then norm.
+constexpr int kPlain = 0, kGated = 1, kResid = 2;
 
 __device__ __forceinline__ float silu_div(float v) { return v / (1.0f + expf(-v)); }
 
@@ -52,9 +58,11 @@ __device__ __forceinline__ float apply_w(float v, const float* w, int idx, int f
     return v * wc;
 }
 
-template <int TPR, int V, bool GATED>
+template <int TPR, int V, int MODE>
 __global__ __launch_bounds__(TPR > 256 ? TPR : 256)
 void norm_vec_kernel(NormParams p) {
+    constexpr bool GATED = MODE == kGated;
+    constexpr bool RESID = MODE == kResid;
     constexpr int BS = TPR > 256 ? TPR : 256;
     constexpr int RPB = BS / TPR;
     const int tid = threadIdx.x;
@@ -65,7 +73,7 @@ void norm_vec_kernel(NormParams p) {
     const int nv = p.cols >> 2;
     const int64_t base = ok ? row * (int64_t)p.cols : 0;
     const float* xr = p.x + base;
-    const float* zr = GATED ? p.z + base : p.x;
+    const float* zr = (GATED || RESID) ? p.z + base : p.x;
 
     // The gated norm loads its weights here, with the row: stores count in
     // the same vector-memory counter as loads, so a load issued after the
@@ -89,9 +97,26 @@ void norm_vec_kernel(NormParams p) {
                 zv[i] = ld_stream(zr + 4 * c);
                 wv[i] = *reinterpret_cast<const float4*>(p.w + (col0 + 4 * c) % p.w_len);
             }
+            if (RESID) zv[i] = ld_stream(zr + 4 * c);
         } else {
             xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (GATED) zv[i] = xv[i];
+            if (GATED || RESID) zv[i] = xv[i];
+        }
+    }
+    if constexpr (RESID) {
+        // x + d is the new residual stream: stored at once, before the
+        // reduction, so the stores overlap the cross-wave step
+        const int64_t r0 = (int64_t)blockIdx.x * RPB;
+        const StreamOut ox(p.xo + r0 * p.cols, (p.rows - r0) * (int64_t)p.cols * 4);
+        const uint32_t xb = (uint32_t)(lr * p.cols) * 4u;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            xv[i].x = xv[i].x + zv[i].x;
+            xv[i].y = xv[i].y + zv[i].y;
+            xv[i].z = xv[i].z + zv[i].z;
+            xv[i].w = xv[i].w + zv[i].w;
+            const int c = i * TPR + t;
+            if (ok && c < nv) ox.store(xb + 16u * c, xv[i]);
         }
     }
     float ss = 0.0f;
@@ -166,14 +191,27 @@ void norm_vec_kernel(NormParams p) {
 
 // Any shape / alignment: one 256-thread block per slice, two passes over the
 // slice (the second pass hits L2). Same arithmetic as the vector kernel.
-template <bool GATED>
+template <int MODE>
 __global__ __launch_bounds__(256) void norm_scalar_kernel(NormParams p) {
+    constexpr bool GATED = MODE == kGated;
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t base = row * (int64_t)p.cols;
     const float* xr = p.x + base;
     float ss = 0.0f;
-    for (int c = tid; c < p.cols; c += 256) ss += xr[c] * xr[c];
+    if constexpr (MODE == kResid) {
+        // each thread reads back only the sums it wrote itself
+        float* xo = p.xo + base;
+        const float* dr = p.z + base;
+        for (int c = tid; c < p.cols; c += 256) {
+            const float v = xr[c] + dr[c];
+            xo[c] = v;
+            ss += v * v;
+        }
+        xr = xo;
+    } else {
+        for (int c = tid; c < p.cols; c += 256) ss += xr[c] * xr[c];
+    }
     __shared__ float part[4];
     ss = group_sum<64>(ss);
     if ((tid & 63) == 0) part[tid >> 6] = ss;
@@ -197,32 +235,32 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormParams p) {
 
 using NormKernel = void (*)(NormParams);
 
-template <bool GATED, int TPR>
+template <int MODE, int TPR>
 NormKernel pick_v(int v) {
     switch (v) {
-    case 1: return norm_vec_kernel<TPR, 1, GATED>;
-    case 2: return norm_vec_kernel<TPR, 2, GATED>;
-    case 3: return norm_vec_kernel<TPR, 3, GATED>;
-    case 4: return norm_vec_kernel<TPR, 4, GATED>;
-    case 5: return norm_vec_kernel<TPR, 5, GATED>;
-    case 6: return norm_vec_kernel<TPR, 6, GATED>;
-    case 7: return norm_vec_kernel<TPR, 7, GATED>;
-    case 8: return norm_vec_kernel<TPR, 8, GATED>;
+    case 1: return norm_vec_kernel<TPR, 1, MODE>;
+    case 2: return norm_vec_kernel<TPR, 2, MODE>;
+    case 3: return norm_vec_kernel<TPR, 3, MODE>;
+    case 4: return norm_vec_kernel<TPR, 4, MODE>;
+    case 5: return norm_vec_kernel<TPR, 5, MODE>;
+    case 6: return norm_vec_kernel<TPR, 6, MODE>;
+    case 7: return norm_vec_kernel<TPR, 7, MODE>;
+    case 8: return norm_vec_kernel<TPR, 8, MODE>;
     default: return nullptr;
     }
 }
 
-template <bool GATED>
+template <int MODE>
 NormKernel pick(int tpr, int v) {
     switch (tpr) {
-    case 8: return pick_v<GATED, 8>(v);
-    case 16: return pick_v<GATED, 16>(v);
-    case 32: return pick_v<GATED, 32>(v);
-    case 64: return pick_v<GATED, 64>(v);
-    case 128: return pick_v<GATED, 128>(v);
-    case 256: return pick_v<GATED, 256>(v);
-    case 512: return pick_v<GATED, 512>(v);
-    case 1024: return pick_v<GATED, 1024>(v);
+    case 8: return pick_v<MODE, 8>(v);
+    case 16: return pick_v<MODE, 16>(v);
+    case 32: return pick_v<MODE, 32>(v);
+    case 64: return pick_v<MODE, 64>(v);
+    case 128: return pick_v<MODE, 128>(v);
+    case 256: return pick_v<MODE, 256>(v);
+    case 512: return pick_v<MODE, 512>(v);
+    case 1024: return pick_v<MODE, 1024>(v);
     default: return nullptr;
     }
 }
@@ -238,22 +276,25 @@ void choose_shape(int nv, int* tpr, int* v) {
     *v = (nv + t - 1) / t;
 }
 
-bool run_norm(NormParams p, bool gated, hipStream_t stream) {
+bool run_norm(NormParams p, int mode, hipStream_t stream) {
     if (p.rows == 0) return true;
     const bool vec = (p.cols % 4 == 0) && aligned16(p.x) && aligned16(p.out) &&
                      (p.w == nullptr || aligned16(p.w)) &&
-                     (!gated || (aligned16(p.z) && p.w_len % 4 == 0));
+                     (mode != kGated || (aligned16(p.z) && p.w_len % 4 == 0)) &&
+                     (mode != kResid || (aligned16(p.z) && aligned16(p.xo)));
     int tpr = 0, v = 0;
     if (vec) choose_shape(p.cols / 4, &tpr, &v);
     if (vec && v <= 8) {
         const int bs = tpr > 256 ? tpr : 256;
         const int rpb = bs / tpr;
         const int64_t blocks = (p.rows + rpb - 1) / rpb;
-        NormKernel k = gated ? pick<true>(tpr, v) : pick<false>(tpr, v);
+        NormKernel k = mode == kGated ? pick<kGated>(tpr, v)
+                       : mode == kResid ? pick<kResid>(tpr, v) : pick<kPlain>(tpr, v);
         return launch("norm_vec_kernel", k, dim3((unsigned)blocks), dim3(bs), 0,
                       stream, p);
     }
-    NormKernel k = gated ? norm_scalar_kernel<true> : norm_scalar_kernel<false>;
+    NormKernel k = mode == kGated ? norm_scalar_kernel<kGated>
+                   : mode == kResid ? norm_scalar_kernel<kResid> : norm_scalar_kernel<kPlain>;
     return launch("norm_scalar_kernel", k, dim3((unsigned)p.rows), dim3(256), 0,
                   stream, p);
 }
@@ -269,8 +310,8 @@ bool norm_rows(const float* x, const float* w, float* out, int64_t rows,
                   (long long)cols);
         return false;
     }
-    NormParams p{x, nullptr, w, out, rows, (int)cols, 1, (int)cols, eps, flags};
-    return run_norm(p, false, stream);
+    NormParams p{x, nullptr, w, out, rows, (int)cols, 1, (int)cols, eps, flags, nullptr};
+    return run_norm(p, kPlain, stream);
 }
 
 }  // namespace aero
@@ -300,8 +341,25 @@ int aero_hip_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
         return 0;
     }
     aero::NormParams p{x, z, w, out, slices, (int)group, (int)(inner / group),
-                       (int)w_len, eps, 0};
-    return aero::run_norm(p, true, (hipStream_t)stream) ? 1 : 0;
+                       (int)w_len, eps, 0, nullptr};
+    return aero::run_norm(p, aero::kGated, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_add_rmsnorm(const float* x, const float* d, float* x_out, const float* w,
+                         float* h, int64_t rows, int64_t cols, float eps, int flags,
+                         void* stream) {
+    if (!x || !d || !x_out || !h || rows < 0 || cols <= 0 || cols > (int64_t)0x7fffffff ||
+        rows > (int64_t)0x7fffffff || (flags & ~AERO_NORM_UNIT_OFFSET) != 0) {
+        aero::set_error("add_rmsnorm: bad arguments (rows=%lld cols=%lld flags=%d)",
+                        (long long)rows, (long long)cols, flags);
+        return 0;
+    }
+    if (h == x || h == d || h == x_out) {
+        aero::set_error("add_rmsnorm: h must not alias x, d or x_out");
+        return 0;
+    }
+    aero::NormParams p{x, d, w, h, rows, (int)cols, 1, (int)cols, eps, flags, x_out};
+    return aero::run_norm(p, aero::kResid, (hipStream_t)stream) ? 1 : 0;
 }
 
 }  // extern "C"

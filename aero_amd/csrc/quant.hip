@@ -13,6 +13,8 @@
 // Values are the reference's dequant bit for bit (quant_blocks.hpp). The
 // optional embedding scale is a separate multiply, as the reference's second
 // pass (src/model.cpp:315-316).
+#include <algorithm>
+
 #include "quant_blocks.hpp"
 
 #pragma clang fp contract(off)
@@ -187,7 +189,197 @@ bool run_gather(int dtype, GatherParams p, hipStream_t s) {
     }
 }
 
+// ------------------------------------------------ gather + first RMSNorm
+// The model loop's first two steps in one pass (src/model.cpp:297-316, then
+// norm_row of the first block, :244-245): x = dequant(table row ids[r])
+// (* scale), h = (x * 1/sqrtf(mean(x^2)+eps)) * w. A workgroup of W waves
+// owns one row; wave wv decodes the U consecutive 256-value steps starting
+// at step wv*U (staged through its own LDS slice as in gather_rows_kernel),
+// keeps them in VGPRs, stores x at once, and after one cross-wave sum of
+// squares stores h, so the row is read from the table once and x is never
+// read back. HBM bytes per row: (n_embd/bv)*bb + 8*n_embd.
+constexpr int kEmbedNormMaxWaves = 8;
+
+struct EmbedNormParams {
+    GatherParams g;      // g.out is x
+    const float* w;      // norm weight, null = ones
+    float* h;
+    float eps;
+    int flags;           // AERO_NORM_UNIT_OFFSET
+};
+
+template <int TYPE, int U>
+__global__ __launch_bounds__(64 * kEmbedNormMaxWaves)
+void embed_norm_kernel(EmbedNormParams p) {
+    using Q = QT<TYPE>;
+    constexpr int BPS = 256 / Q::BV;
+    constexpr int MAX_DW = (U * BPS * Q::BB + 3 + 3) / 4;
+    constexpr int PER = (MAX_DW + 63) / 64;
+    __shared__ __align__(16) uint32_t stage[kEmbedNormMaxWaves][PER * 64];
+    __shared__ float part[kEmbedNormMaxWaves];
+
+    const int l = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int64_t row = blockIdx.x;
+    const int64_t n_embd = p.g.nbr * Q::BV;
+    const int64_t v_begin = (int64_t)wv * (U * 256);
+    // values this wave owns (<= 0: a wave past the row's end, which only
+    // joins the barriers)
+    const int nv = (int)max(min((int64_t)(U * 256), n_embd - v_begin), (int64_t)0);
+    const int64_t tok = p.g.ids ? (int64_t)p.g.ids[row] : row;
+    const bool good = tok >= 0 && tok < p.g.vocab;
+    if (!good && p.g.bad != nullptr && threadIdx.x == 0) atomicAdd(p.g.bad, 1u);
+
+    const int off = good ? (int)(reinterpret_cast<uintptr_t>(
+                               p.g.table + tok * p.g.rb + (v_begin / Q::BV) * Q::BB) & 3u)
+                         : 0;
+    if (good && nv > 0) {
+        const uint8_t* g = p.g.table + tok * p.g.rb + (v_begin / Q::BV) * Q::BB;
+        const uint32_t* g4 = reinterpret_cast<const uint32_t*>(g - off);
+        const int n_dw = (off + (nv / Q::BV) * Q::BB + 3) >> 2;
+        uint32_t wd[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) wd[i] = g4[min(l + 64 * i, n_dw - 1)];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) stage[wv][l + 64 * i] = wd[i];
+    }
+    __syncthreads();
+
+    const int64_t rowoff = row * n_embd + v_begin;
+    const int64_t left = (int64_t)max(nv, 0) * 4;
+    const StreamOut ox(p.g.out + rowoff, left);
+    const StreamOut oh(p.h + rowoff, left);
+    const uint8_t* run = reinterpret_cast<const uint8_t*>(stage[wv]) + off;
+    float4 xv[U];
+    float ss = 0.0f;
+#pragma unroll
+    for (int st = 0; st < U; ++st) {
+        const int v0 = st * 256 + 4 * l;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (v0 < nv) {
+            if (good) {
+                typename Q::Raw raw;
+                load_raw(run + (v0 / Q::BV) * Q::BB, l, raw);
+                v = decode(raw, l);
+                if (p.g.scale > 0.0f) {
+                    v.x = v.x * p.g.scale; v.y = v.y * p.g.scale;
+                    v.z = v.z * p.g.scale; v.w = v.w * p.g.scale;
+                }
+            }
+            ox.store((uint32_t)v0 * 4u, v);
+        }
+        xv[st] = v;
+        ss += v.x * v.x;
+        ss += v.y * v.y;
+        ss += v.z * v.z;
+        ss += v.w * v.w;
+    }
+    ss = group_sum<64>(ss);
+    if (l == 0) part[wv] = ss;
+    __syncthreads();
+    ss = part[0];
+    for (int k = 1; k < nw; ++k) ss += part[k];
+    const float inv = 1.0f / sqrtf(ss / (float)n_embd + p.eps);
+#pragma unroll
+    for (int st = 0; st < U; ++st) {
+        const int v0 = st * 256 + 4 * l;
+        if (v0 >= nv) break;
+        float4 o = make_float4(xv[st].x * inv, xv[st].y * inv, xv[st].z * inv,
+                               xv[st].w * inv);
+        if (p.w != nullptr) {
+            float4 w4 = *reinterpret_cast<const float4*>(p.w + v_begin + v0);
+            if (p.flags & AERO_NORM_UNIT_OFFSET) {
+                w4.x = 1.0f + w4.x; w4.y = 1.0f + w4.y;
+                w4.z = 1.0f + w4.z; w4.w = 1.0f + w4.w;
+            }
+            o.x = o.x * w4.x; o.y = o.y * w4.y; o.z = o.z * w4.z; o.w = o.w * w4.w;
+        }
+        oh.store((uint32_t)v0 * 4u, o);
+    }
+}
+
+// Steps a wave and waves a row: the fewest steps a wave (1, 2, 4, 8) that
+// keep the row within `maxw` waves (tunable), so short rows still spread
+// over several waves and long rows keep <= 8 float4 a lane.
+template <int TYPE>
+bool launch_embed_norm(EmbedNormParams p, hipStream_t s) {
+    const int64_t n_embd = p.g.nbr * QT<TYPE>::BV;
+    const int64_t steps = (n_embd + 255) / 256;
+    const int maxw = std::min(std::max(tune("embed_norm_waves", 8), 1), kEmbedNormMaxWaves);
+    int u = 1;
+    while (u < 8 && (steps + u - 1) / u > maxw) u *= 2;
+    u = tune("embed_norm_u", u);
+    const int64_t waves = (steps + u - 1) / u;
+    if (waves > kEmbedNormMaxWaves) {
+        set_error("embed_rmsnorm: row of %lld values needs %lld waves (max %d)",
+                  (long long)n_embd, (long long)waves, kEmbedNormMaxWaves);
+        return false;
+    }
+    if (p.g.n_rows > 0x7fffffff) {
+        set_error("embed_rmsnorm: too many rows (%lld)", (long long)p.g.n_rows);
+        return false;
+    }
+    const dim3 grid((unsigned)p.g.n_rows), block((unsigned)(64 * waves));
+    const char* name = "embed_norm_kernel";
+    switch (u) {
+    case 1: return launch(name, embed_norm_kernel<TYPE, 1>, grid, block, 0, s, p);
+    case 2: return launch(name, embed_norm_kernel<TYPE, 2>, grid, block, 0, s, p);
+    case 4: return launch(name, embed_norm_kernel<TYPE, 4>, grid, block, 0, s, p);
+    case 8: return launch(name, embed_norm_kernel<TYPE, 8>, grid, block, 0, s, p);
+    default:
+        set_error("embed_rmsnorm: steps per wave %d not in {1,2,4,8}", u);
+        return false;
+    }
+}
+
 }  // namespace
+
+bool embed_rmsnorm(int dtype, const uint8_t* table, int64_t table_bytes, int64_t vocab,
+                   int64_t n_embd, const int32_t* ids, int64_t n_ids, float scale,
+                   float* x_out, const float* norm_w, float eps, int norm_flags,
+                   float* h_out, uint32_t* bad, hipStream_t s) {
+    if (!is_block_quant(dtype)) {
+        set_error("embed_rmsnorm: dtype %d not supported (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS)",
+                  dtype);
+        return false;
+    }
+    const int64_t bv = block_values(dtype), bb = block_bytes(dtype);
+    if (table == nullptr || x_out == nullptr || h_out == nullptr ||
+        (n_ids > 0 && ids == nullptr) || vocab <= 0 || n_embd <= 0 || n_ids < 0 ||
+        n_embd % bv != 0 || (norm_flags & ~AERO_NORM_UNIT_OFFSET) != 0) {
+        set_error("embed_rmsnorm: bad arguments (vocab=%lld n_embd=%lld n_ids=%lld "
+                  "flags=%d)", (long long)vocab, (long long)n_embd, (long long)n_ids,
+                  norm_flags);
+        return false;
+    }
+    if (x_out == h_out) {
+        set_error("embed_rmsnorm: x_out and h_out must be different buffers");
+        return false;
+    }
+    const int64_t rb = (n_embd / bv) * bb;
+    if (table_bytes < vocab * rb) {
+        set_error("embed_rmsnorm: table_bytes %lld < vocab*row_bytes %lld",
+                  (long long)table_bytes, (long long)(vocab * rb));
+        return false;
+    }
+    if ((reinterpret_cast<uintptr_t>(table) & 3u) || !aligned16(x_out) || !aligned16(h_out) ||
+        (norm_w != nullptr && !aligned16(norm_w))) {
+        set_error("embed_rmsnorm: table must be 4-byte and x_out, h_out, norm_w 16-byte "
+                  "aligned");
+        return false;
+    }
+    if (n_ids == 0) return true;
+    EmbedNormParams p{{table, ids, vocab, n_ids, n_embd / bv, rb, x_out, scale, bad},
+                      norm_w, h_out, eps, norm_flags};
+    switch (dtype) {
+    case AERO_DTYPE_Q8_0: return launch_embed_norm<AERO_DTYPE_Q8_0>(p, s);
+    case AERO_DTYPE_Q4_K: return launch_embed_norm<AERO_DTYPE_Q4_K>(p, s);
+    case AERO_DTYPE_Q5_K: return launch_embed_norm<AERO_DTYPE_Q5_K>(p, s);
+    case AERO_DTYPE_Q6_K: return launch_embed_norm<AERO_DTYPE_Q6_K>(p, s);
+    default: return launch_embed_norm<AERO_DTYPE_IQ4_XS>(p, s);
+    }
+}
 
 int64_t dtype_block_bytes(int t) { return block_bytes(t); }
 int64_t dtype_block_values(int t) { return block_values(t); }
@@ -328,6 +520,16 @@ int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
                           void* stream) {
     return aero::embed_gather(dtype, table, table_bytes, vocab, n_embd, ids, n_ids,
                               scale, out, bad_count, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_embed_rmsnorm(int dtype, const uint8_t* table, int64_t table_bytes,
+                           int64_t vocab, int64_t n_embd, const int32_t* ids, int64_t n_ids,
+                           float scale, float* x_out, const float* norm_w, float eps,
+                           int norm_flags, float* h_out, uint32_t* bad_count,
+                           void* stream) {
+    return aero::embed_rmsnorm(dtype, table, table_bytes, vocab, n_embd, ids, n_ids, scale,
+                               x_out, norm_w, eps, norm_flags, h_out, bad_count,
+                               (hipStream_t)stream) ? 1 : 0;
 }
 
 int aero_hip_dequant(int dtype, const uint8_t* raw, int64_t raw_len, float* out,

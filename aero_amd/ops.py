@@ -78,6 +78,21 @@ def gated_rmsnorm_silu(x: DeviceArray, z: DeviceArray, w: DeviceArray, out: Devi
                                                       _s(stream)), "gated_rmsnorm_silu")
 
 
+def add_rmsnorm(x: DeviceArray, d: DeviceArray, w: DeviceArray | None, h: DeviceArray,
+                rows: int, cols: int, eps: float, unit_offset: bool = False,
+                x_out: DeviceArray | None = None, stream: Stream | None = None) -> None:
+    """Residual add then RMSNorm in one pass: x_out = x + d (x_out None: x
+    in place), h = rmsnorm(x_out) * (w or 1+w)."""
+    x_out = x if x_out is None else x_out
+    for a, name in ((x, "x"), (d, "d"), (x_out, "x_out"), (h, "h")):
+        _need(a, rows * cols, np.float32, name)
+    _need(w, cols, np.float32, "w")
+    _lib.check(_lib.lib().aero_hip_add_rmsnorm(x.ptr, d.ptr, x_out.ptr, as_ptr(w), h.ptr, rows,
+                                               cols, float(eps),
+                                               NORM_UNIT_OFFSET if unit_offset else 0,
+                                               _s(stream)), "add_rmsnorm")
+
+
 def act_mul(kind, gate: DeviceArray, up: DeviceArray | None, out: DeviceArray,
             n: int | None = None, stream: Stream | None = None) -> None:
     """out = act(gate) * up (up None: out = act(gate)). kind: int or name."""
@@ -172,6 +187,28 @@ def embed_gather(dtype: int, table: DeviceArray, vocab: int, n_embd: int, ids: D
     _lib.check(_lib.lib().aero_hip_embed_gather(int(dtype), table.ptr, table.nbytes, vocab,
                                                 n_embd, ids.ptr, n_ids, float(scale), out.ptr,
                                                 as_ptr(bad_count), _s(stream)), "embed_gather")
+
+
+def embed_rmsnorm(dtype: int, table: DeviceArray, vocab: int, n_embd: int, ids: DeviceArray,
+                  x_out: DeviceArray, h_out: DeviceArray, norm_w: DeviceArray | None,
+                  eps: float, scale: float = 0.0, unit_offset: bool = False,
+                  bad_count: DeviceArray | None = None, n_ids: int | None = None,
+                  stream: Stream | None = None) -> None:
+    """Embedding gather and the first RMSNorm in one pass: x_out as
+    embed_gather, h_out = rmsnorm(x_out) * (norm_w or 1+norm_w)."""
+    n_ids = ids.size if n_ids is None else int(n_ids)
+    rb = row_bytes(dtype, n_embd)
+    if table.nbytes < vocab * rb:
+        raise ValueError(f"table holds {table.nbytes} B, needs {vocab * rb}")
+    _need(ids, n_ids, np.int32, "ids")
+    _need(x_out, n_ids * n_embd, np.float32, "x_out")
+    _need(h_out, n_ids * n_embd, np.float32, "h_out")
+    _need(norm_w, n_embd, np.float32, "norm_w")
+    _need(bad_count, 1, np.uint32, "bad_count")
+    _lib.check(_lib.lib().aero_hip_embed_rmsnorm(
+        int(dtype), table.ptr, table.nbytes, vocab, n_embd, ids.ptr, n_ids, float(scale),
+        x_out.ptr, as_ptr(norm_w), float(eps), NORM_UNIT_OFFSET if unit_offset else 0,
+        h_out.ptr, as_ptr(bad_count), _s(stream)), "embed_rmsnorm")
 
 
 def dequant(dtype: int, raw: DeviceArray, out: DeviceArray, n_values: int,

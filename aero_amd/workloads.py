@@ -251,3 +251,14 @@ def bytes_act(R: int, F: int) -> int:
 def bytes_embed(R: int, N: int, t: int) -> int:
     bv, bb = BLOCK[t]
     return R * (N // bv) * bb + 4 * R * N + 4 * R
+
+
+def bytes_embed_rmsnorm(R: int, N: int, t: int) -> int:
+    """Fused gather + first RMSNorm: table rows and ids read, x and h written,
+    the norm weight once."""
+    return bytes_embed(R, N, t) + 4 * R * N + 4 * N
+
+
+def bytes_add_rmsnorm(R: int, N: int) -> int:
+    """Residual add + RMSNorm: x and d read, x + d and h written, the weight once."""
+    return 16 * R * N + 4 * N

@@ -1,29 +1,34 @@
 """Benchmark of the fused per-layer elementwise path on one MI355X.
 
 A step is one pass of the path over one batch at the Llama-3-8B 512-token
-prefill shape: Q4_K token-embedding gather (512 rows of 4096), RMSNorm
-(512 x 4096), NeoX RoPE on q (512 x 32 x 128) and k (512 x 8 x 128) at
-positions 0..511, and SwiGLU on gate/up (512 x 14336). Inputs are synthetic
-(seeded), resident in HBM before timing starts, and rotated over --sets
-buffer sets (> 1 GiB together) so no launch reads data the 256 MiB Infinity
-Cache still holds from the previous use of its set.
+prefill shape, as a model loop runs it: the Q4_K token-embedding gather with
+the first RMSNorm in one kernel (512 rows of 4096: x and h written), NeoX
+RoPE on q (512 x 32 x 128) and k (512 x 8 x 128) at positions 0..511, the
+residual add with the next RMSNorm in one kernel (512 x 4096), and SwiGLU on
+gate/up (512 x 14336). Inputs are synthetic (seeded), resident in HBM before
+timing starts, and rotated over --sets buffer sets (> 1 GiB together) so no
+launch reads data the 256 MiB Infinity Cache still holds from the previous
+use of its set.
 
 A step replays a recorded plan (aero_hip_plan_launch: the four kernels
 issued from C, one host call per step). `value` is the whole step's
 algorithmic HBM bytes / wall time per step over the timed region (GB/s).
-Each entry of `ops` gives two device timings of the op: per dispatch
-(`kernel_us`, `frac`: a second region of the same run replays the same plans
-with an event pair recorded by each kernel's own dispatch, hipExtLaunchKernel;
-events per kernel serialise the host side, so that region times kernels, not
-steps) and sustained (`sustained_us`, `sustained_frac`: the op alone, launched
-back to back on one stream over its own > 1 GiB rotation of buffers, with one
-HIP event pair on that stream around the whole region; mean duration =
-region / launches). `roofline` is the dominant kernel (SwiGLU, 88 MB per
-launch): algorithmic bytes / its sustained mean launch duration (the
-per-dispatch figure is kept beside it; a rare slow dispatch moves that mean
-by several percent). `cpu_baseline` is the same step on the host: the reference's own C++
-(built into oracle/_ref) when present, else the oracle's restatement,
-single-threaded like the reference, over a bounded sample.
+`ops` also reports the unfused gather and RMSNorm the two fused kernels
+replace. Each entry of `ops` gives two device timings of the op: per
+dispatch (`kernel_us`, `frac`: a second region of the same run replays plans
+of the ops with an event pair recorded by each kernel's own dispatch,
+hipExtLaunchKernel; events per kernel serialise the host side, so that
+region times kernels, not steps) and sustained (`sustained_us`,
+`sustained_frac`: the op alone, launched back to back on one stream over its
+own > 1 GiB rotation of buffers, with one HIP event pair on that stream
+around the whole region; mean duration = region / launches). `roofline` is
+the dominant kernel (SwiGLU, 88 MB per launch): algorithmic bytes / its mean
+per-dispatch duration, the figure a rocprofv3 kernel trace of the same
+command reproduces (the sustained figure is kept beside it). `cpu_baseline`
+is the same step on the host: the reference's own C++ (built into
+oracle/_ref) when present, else the oracle's restatement, single-threaded
+like the reference, over a bounded sample, with the reference's threaded
+dequant over the same rows beside it.
 
     python bench.py [--steps K] [--warmup W] [--sets S] [--cpu-seconds T]
     python bench.py --all-shapes        # per-op table over every layer shape
@@ -37,6 +42,7 @@ single-threaded like the reference, over a bounded sample.
     python bench.py --ssm               # gated DeltaNet scan and conv
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
+    python bench.py --copy-sweep        # plain copies from 2 MiB to 1 GiB
 """
 from __future__ import annotations
 
@@ -58,7 +64,14 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 SUSTAINED_ROTATION = 5 << 28  # bytes one rotation of buffer sets moves (1.25 GiB)
 SUSTAINED_REPS = 8            # rotations timed per op
 METRIC = "fused-op HBM GB/s (% of MI355X peak) + rows/s vs CPU ref, Llama-3-8B shapes"
-OPS = ("embed_gather", "rmsnorm", "rope_qk", "swiglu")
+# the ops of the path as separate kernels, and the data-flow fusions that
+# replace the gather and the norms in a model loop
+UNFUSED_OPS = ("embed_gather", "rmsnorm", "rope_qk", "swiglu")
+FUSED_OPS = ("embed_rmsnorm", "add_rmsnorm")
+OPS = UNFUSED_OPS + FUSED_OPS
+# one layer's elementwise path as a model loop runs it: gather + first norm,
+# RoPE on q/k, residual add + norm, act-mul
+STEP_OPS = ("embed_rmsnorm", "rope_qk", "add_rmsnorm", "swiglu")
 
 
 def parse_args(argv=None):
@@ -87,6 +100,8 @@ def parse_args(argv=None):
                    help="quantised GEMM cases (prefill token counts)")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
     p.add_argument("--copy-calibration", action="store_true")
+    p.add_argument("--copy-sweep", action="store_true",
+                   help="plain copy at 2 MiB .. 1 GiB: the streaming ceiling per size")
     p.add_argument("--host-abi", action="store_true",
                    help="PCIe-inclusive rate of the reference-compatible host ABI")
     p.add_argument("--launch-floor", action="store_true",
@@ -115,6 +130,14 @@ class StepBuffers:
         if want("rmsnorm"):
             self.x = normal(R, s.hidden)
             self.h = DA.empty((R, s.hidden))
+        if want("embed_rmsnorm"):
+            self.eids = DA.from_numpy(rng.integers(0, s.vocab, R).astype(np.int32))
+            self.ex = DA.empty((R, s.hidden))
+            self.eh = DA.empty((R, s.hidden))
+        if want("add_rmsnorm"):
+            self.rx = normal(R, s.hidden)
+            self.rd = normal(R, s.hidden)
+            self.rh = DA.empty((R, s.hidden))
         if want("rope_qk"):
             self.q = normal(R, s.hq, s.head_dim)
             self.k = normal(R, s.hk, s.head_dim)
@@ -130,6 +153,7 @@ class StepBuffers:
         self.table = d_table
 
     INPUTS = {"embed_gather": (("ids",), ("emb_out",)), "rmsnorm": (("x",), ("h",)),
+              "embed_rmsnorm": (("eids",), ("ex", "eh")), "add_rmsnorm": (("rx", "rd"), ("rh",)),
               "rope_qk": (("q", "k"), ()), "swiglu": (("gate", "up"), ("act_out",)),
               "gated_norm": (("gx", "gz"), ("gout",))}
 
@@ -145,7 +169,7 @@ class StepBuffers:
         for n in ins:
             a = getattr(src, n)
             setattr(b, n, DA.from_numpy(rng.integers(0, vocab, a.shape).astype(np.int32))
-                    if n == "ids" else a.clone())
+                    if n in ("ids", "eids") else a.clone())
         for n in outs:
             setattr(b, n, DA.empty(getattr(src, n).shape))
         b.table = src.table
@@ -167,7 +191,7 @@ class Path:
         rng = np.random.default_rng(seed)
         bv, bb = W.BLOCK[s.emb_type]
         self.table = self.table_host = None
-        if only in (None, "embed_gather"):
+        if only in (None, "embed_gather", "embed_rmsnorm"):
             self.table_host = W.make_table(s.emb_type, s.vocab * (s.hidden // bv), rng)
             self.table = DA.from_numpy(self.table_host)
         w = rng.standard_normal(s.hidden, dtype=np.float32) * np.float32(0.1)
@@ -203,6 +227,8 @@ class Path:
                                     True, bool(s.rope_table)) + (4 * s.head_dim if s.qk_norm
                                                                  else 0),
             "swiglu": W.bytes_act(s.n_tok, s.ffn),
+            "embed_rmsnorm": W.bytes_embed_rmsnorm(s.n_tok, s.hidden, s.emb_type),
+            "add_rmsnorm": W.bytes_add_rmsnorm(s.n_tok, s.hidden),
         }
         if s.gated:
             b["gated_norm"] = W.bytes_gated(s.n_tok, s.gated[0] * s.gated[1], s.gated[1])
@@ -211,7 +237,7 @@ class Path:
     def rows(self):
         s = self.s
         r = {"embed_gather": s.n_tok, "rmsnorm": s.n_tok, "rope_qk": s.n_tok * (s.hq + s.hk),
-             "swiglu": s.n_tok}
+             "swiglu": s.n_tok, "embed_rmsnorm": s.n_tok, "add_rmsnorm": s.n_tok}
         if s.gated:
             r["gated_norm"] = s.n_tok
         return r
@@ -234,6 +260,13 @@ class Path:
                              stream=stream, **kw)
         elif op == "swiglu":
             ops.act_mul(s.act, b.gate, b.up, b.act_out, stream=stream)
+        elif op == "embed_rmsnorm":
+            ops.embed_rmsnorm(s.emb_type, b.table, s.vocab, s.hidden, b.eids, b.ex, b.eh,
+                              self.w, s.eps, scale=self.scale, unit_offset=s.unit_offset,
+                              stream=stream)
+        elif op == "add_rmsnorm":
+            ops.add_rmsnorm(b.rx, b.rd, self.w, b.rh, s.n_tok, s.hidden, s.eps,
+                            unit_offset=s.unit_offset, stream=stream)
         elif op == "gated_norm":
             ops.gated_rmsnorm_silu(b.gx, b.gz, self.gw, b.gout, s.n_tok,
                                    s.gated[0] * s.gated[1], s.eps, stream=stream)
@@ -241,16 +274,22 @@ class Path:
             raise ValueError(op)
 
     def step_ops(self):
+        """The kernels a model loop runs for one layer's elementwise path."""
         if self.only:
             return [self.only]
-        return list(OPS) + (["gated_norm"] if self.s.gated else [])
+        return list(STEP_OPS) + (["gated_norm"] if self.s.gated else [])
+
+    def report_ops(self):
+        """The step's kernels and the unfused ops they replace."""
+        if self.only:
+            return [self.only]
+        return self.step_ops() + [op for op in UNFUSED_OPS if op not in STEP_OPS]
 
 
-def build_plans(path, only=None):
-    """One recorded plan per buffer set: the step's ops in order."""
+def build_plans(path, ops_list):
+    """One recorded plan per buffer set: the given ops in order."""
     from aero_amd.device import Plan
 
-    ops_list = [only] if only else path.step_ops()
     plans = []
     for i in range(len(path.sets)):
         p = Plan()
@@ -275,14 +314,14 @@ def kernel_kinds(path, ops_list):
     return kinds
 
 
-def timed_steps(path, steps, warmup, only=None):
+def timed_steps(path, steps, warmup):
     """The timed region: `warmup` untimed step replays, then exactly `steps`
     replays (one plan launch, one C call each) bracketed by a stream
     synchronize on both sides. Returns wall ms per step."""
     from aero_amd.device import Stream
 
     stream = Stream()
-    plans, _ = build_plans(path, only)
+    plans, _ = build_plans(path, path.step_ops())
     for i in range(warmup):
         plans[i % len(plans)].launch(stream)
     stream.synchronize()
@@ -297,7 +336,7 @@ def timed_steps(path, steps, warmup, only=None):
     return wall
 
 
-def kernel_times(path, steps, warmup, only=None):
+def kernel_times(path, steps, warmup, ops_list):
     """The kernel-timing region: the same replays with every kernel recording
     its own device begin/end (hipExtLaunchKernel events on the stream it runs
     on). Recording events per kernel serialises the host side, so this region
@@ -305,7 +344,7 @@ def kernel_times(path, steps, warmup, only=None):
     from aero_amd.device import Event, Stream, synchronize
 
     stream = Stream()
-    plans, ops_list = build_plans(path, only)
+    plans, ops_list = build_plans(path, ops_list)
     kinds = kernel_kinds(path, ops_list)
     n_k = len(plans[0])
     assert len(kinds) == n_k
@@ -460,19 +499,60 @@ def cpu_baseline(path, seconds):
         else:
             C.cr_act_mul(0, fp(g), fp(up), fp(g), g.size)
 
+    # the residual add of src/model.cpp:279 (an elementwise loop there; numpy
+    # here), then the norm of the sum
+    rx0 = rng.standard_normal((R, s.hidden), dtype=np.float32)
+    rd = rng.standard_normal((R, s.hidden), dtype=np.float32)
+
+    def add_norm(rx):
+        np.add(rx, rd, out=rx)
+        if use_ref:
+            T.aero_rmsnorm_rows(fp(rx), fp(w), fp(h), R, s.hidden, s.eps)
+        else:
+            C.cr_rmsnorm_rows(fp(rx), fp(w), fp(h), R, s.hidden, s.eps, 0)
+
+    def embed_norm():
+        embed()
+        if use_ref:
+            T.aero_rmsnorm_rows(fp(emb), fp(w), fp(h), R, s.hidden, s.eps)
+        else:
+            C.cr_rmsnorm_rows(fp(emb), fp(w), fp(h), R, s.hidden, s.eps, 0)
+
     times = {op: [] for op in OPS}
     t_end = time.perf_counter() + seconds
     reps = 0
     while reps < 3 or time.perf_counter() < t_end:
-        q, k, g = q0.copy(), k0.copy(), g0.copy()   # fresh inputs, outside the timing
+        q, k, g, rx = q0.copy(), k0.copy(), g0.copy(), rx0.copy()  # outside the timing
         for op, fn in (("embed_gather", embed), ("rmsnorm", norm),
-                       ("rope_qk", lambda: rope(q, k)), ("swiglu", lambda: swiglu(g))):
+                       ("rope_qk", lambda: rope(q, k)), ("swiglu", lambda: swiglu(g)),
+                       ("embed_rmsnorm", embed_norm), ("add_rmsnorm", lambda: add_norm(rx))):
             t0 = time.perf_counter_ns()
             fn()
             times[op].append((time.perf_counter_ns() - t0) * 1e-6)
         reps += 1
     med = {op: statistics.median(v) for op, v in times.items()}
-    return med, reps, ("reference" if use_ref else "port")
+
+    # the threaded dequant row (src/kernels.cpp:463-494 at min(hw, 8) threads,
+    # src/kernels.cpp:541-548): the same rows' blocks, copied into one
+    # contiguous buffer outside the timing, dequantised by the reference's
+    # aero_dequant_threaded (or the oracle's restatement of it)
+    threads = min(os.cpu_count() or 1, 8)
+    raw = np.concatenate([table[int(t) * rb:(int(t) + 1) * rb] for t in ids])
+    flat = np.empty(R * s.hidden, np.float32)
+    rawp = raw.ctypes.data_as(POINTER(c_uint8))
+    thr = []
+    t_end = time.perf_counter() + min(seconds, 3.0)
+    while len(thr) < 5 or time.perf_counter() < t_end:
+        t0 = time.perf_counter_ns()
+        ok = (K.aero_dequant_threaded if use_ref else C.cr_dequant_threaded)(
+            s.emb_type, rawp, raw.size, fp(flat), flat.size, threads)
+        thr.append((time.perf_counter_ns() - t0) * 1e-6)
+        assert ok
+    assert np.array_equal(flat.reshape(R, s.hidden).view(np.uint32), emb.view(np.uint32))
+    threaded = {"ms": round(statistics.median(thr), 3), "threads": threads,
+                "reps": len(thr), "entry": "aero_dequant_threaded" if use_ref
+                else "cr_dequant_threaded"}
+    return med, reps, ("reference" if use_ref else "port"), threaded
 
 
 # ---------------------------------------------------------------- reports
@@ -500,6 +580,8 @@ def main(argv=None):
         return 1
     if a.copy_calibration:
         return copy_calibration(a)
+    if a.copy_sweep:
+        return copy_sweep(a)
     if a.host_abi:
         return host_abi(a)
     if a.launch_floor:
@@ -524,32 +606,34 @@ def main(argv=None):
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
     if a.only:
-        ker = kernel_times(path, a.steps, a.warmup, a.only)
+        ker = kernel_times(path, a.steps, a.warmup, [a.only])
         b = path.bytes()[a.only]
         mean = statistics.mean(ker[a.only])
         print(json.dumps({"op": a.only, "shape": name, "kernel_us": round(mean * 1e3, 3),
                           "GB/s": round(b / (mean * 1e-3) / 1e9, 1), "bytes": b}))
         return 0
     wall = timed_steps(path, a.steps, a.warmup)
-    ker = kernel_times(path, a.steps, a.warmup)
-    sus = sustained_times(path, path.step_ops(), SUSTAINED_REPS)
+    ker = kernel_times(path, a.steps, a.warmup, path.report_ops())
+    sus = sustained_times(path, path.report_ops(), SUSTAINED_REPS)
     bts = path.bytes()
     rows = path.rows()
     total = sum(bts[op] for op in path.step_ops())
     value = total / (wall * 1e-3) / 1e9
     per_op = {}
-    for op in path.step_ops():
+    for op in path.report_ops():
         per_op[op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3, sus[op])
         per_op[op]["kernel_us_median"] = round(statistics.median(ker[op]) * 1e3, 3)
     dom = "swiglu"
-    ach = per_op[dom]["sustained_GB/s"]
+    ach = per_op[dom]["GB/s"]
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(wall, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"{name}: Q4_K embedding gather + RMSNorm + NeoX RoPE (q, k) "
-                               f"+ SwiGLU, one layer's elementwise path",
+        "config": {"workload": f"{name}: one layer's elementwise path as the model loop "
+                               f"runs it: Q4_K embedding gather + first RMSNorm (one kernel), "
+                               f"NeoX RoPE on q and k, residual add + RMSNorm (one kernel), "
+                               f"SwiGLU",
                    "tokens": path.s.n_tok, "hidden": path.s.hidden, "heads": [path.s.hq,
                                                                               path.s.hk],
                    "head_dim": path.s.head_dim, "ffn": path.s.ffn, "buffer_sets": a.sets},
@@ -557,21 +641,27 @@ def main(argv=None):
         "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                      "kernel": "act_vec_kernel<silu> (SwiGLU 512x14336)",
-                     "bytes_per_launch": bts[dom], "launch_us": per_op[dom]["sustained_us"],
-                     "per_dispatch_GB/s": per_op[dom]["GB/s"]},
+                     "bytes_per_launch": bts[dom], "launch_us": per_op[dom]["kernel_us"],
+                     "sustained_GB/s": per_op[dom]["sustained_GB/s"],
+                     "sustained_frac": per_op[dom]["sustained_frac"]},
         "ops": per_op,
     }
     if not a.no_cpu:
-        med, reps, kind = cpu_baseline(path, a.cpu_seconds)
-        cpu_ms = sum(med.values())
+        med, reps, kind, threaded = cpu_baseline(path, a.cpu_seconds)
+        cpu_ms = sum(med[op] for op in path.step_ops())
+        emb_b = bts["embed_gather"]
         out["cpu_baseline"] = {
             "value": round(total / (cpu_ms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": kind, "rows_per_s": round(path.s.n_tok / (cpu_ms * 1e-3), 1),
             "ms_per_step": round(cpu_ms, 3),
             "ops_ms": {k: round(v, 3) for k, v in med.items()},
-            "sample": f"the full step ({path.s.n_tok} tokens) repeated {reps} times "
-                      f"(~{a.cpu_seconds:.0f} s), median per op, single thread, "
-                      f"os.cpu_count()={os.cpu_count()}"}
+            "threaded_dequant": {**threaded, "GB/s": round(emb_b / (threaded["ms"] * 1e-3)
+                                                          / 1e9, 3),
+                                 "single_thread_ms": round(med["embed_gather"], 3)},
+            "sample": f"the full step ({path.s.n_tok} tokens) and the unfused ops, repeated "
+                      f"{reps} times (~{a.cpu_seconds:.0f} s), median per op, single thread "
+                      f"(the threaded dequant row: {threaded['threads']} threads over the "
+                      f"same {path.s.n_tok} rows' blocks), os.cpu_count()={os.cpu_count()}"}
         out["speedup_vs_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
     print(json.dumps(out))
     return 0
@@ -586,10 +676,10 @@ def all_shapes(a):
     for name in names:
         sets = a.sets if W.SHAPES[name].n_tok <= 4096 else 2
         path = Path(name, sets)
-        ops_list = [a.only] if a.only else path.step_ops()
+        ops_list = [a.only] if a.only else path.report_ops()
         if a.only == "gated_norm" and not path.s.gated:
             continue
-        ker = kernel_times(path, max(20, a.steps // 4), 5, a.only)
+        ker = kernel_times(path, max(20, a.steps // 4), 5, ops_list)
         sus = sustained_times(path, ops_list, SUSTAINED_REPS)
         bts, rows = path.bytes(), path.rows()
         res[name] = {}
@@ -610,7 +700,7 @@ def variants(a):
     for name in names:
         shape, op = W.VARIANTS[name]
         path = Path(name, a.sets, shape=shape, only=op)
-        ker = kernel_times(path, max(20, a.steps // 4), 5, op)
+        ker = kernel_times(path, max(20, a.steps // 4), 5, [op])
         sus = sustained_times(path, [op], SUSTAINED_REPS)
         e = op_entry(path.bytes()[op], path.rows()[op], statistics.mean(ker[op]) * 1e3, sus[op])
         print(json.dumps({"variant": name, "op": op, **e}), flush=True)
@@ -1309,6 +1399,38 @@ def copy_calibration(a):
     print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n,
                       "kernel_us": round(m * 1e3, 2),
                       "GB/s": round(8 * n / (m * 1e-3) / 1e9, 1)}))
+    return 0
+
+
+def copy_sweep(a):
+    """The streaming ceiling at each op's size: a plain fp32 copy (the act
+    kernel's access pattern, one read and one write per element) of total
+    traffic 2 MiB .. 1 GiB, rotated over buffers of > 1 GiB together, timed
+    per dispatch. One JSON line per size."""
+    from aero_amd import ops
+    from aero_amd.device import DeviceArray as DA, Event, synchronize, time_next_kernel
+
+    for mib in (2, 4, 8, 16, 32, 64, 128, 256, 512, 1024):
+        n = mib * (1 << 20) // 8                 # floats per buffer (read + write = mib)
+        k = max(2, -(-(3 << 29) // (8 * n)))     # buffer pairs over 1.5 GiB
+        bufs = [(DA.empty(n), DA.empty(n)) for _ in range(k)]
+        ts = []
+        for i in range(a.warmup + a.steps):
+            src, dst = bufs[i % k]
+            e0, e1 = Event(), Event()
+            time_next_kernel(e0, e1)
+            ops.copy_f32(src, dst)
+            if i >= a.warmup:
+                ts.append((e0, e1))
+        synchronize()
+        us = [x.elapsed_ms(y) * 1e3 for x, y in ts]
+        m = statistics.mean(us)
+        print(json.dumps({"copy_bytes": 8 * n, "kernel_us": round(m, 3),
+                          "kernel_us_median": round(statistics.median(us), 3),
+                          "GB/s": round(8 * n / (m * 1e-6) / 1e9, 1),
+                          "frac": round(8 * n / (m * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}),
+              flush=True)
+        del bufs, ts
     return 0
 
 

@@ -160,6 +160,17 @@ int aero_hip_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
                                 int64_t inner, int64_t group, float eps,
                                 void* stream);
 
+/* Residual add + RMSNorm in one pass: x_out = x + d (the residual stream),
+ * h = rmsnorm(x_out) * w as aero_hip_rmsnorm (flags 0 or
+ * AERO_NORM_UNIT_OFFSET; w NULL = ones). Replaces the reference block's
+ * `x_[i] += o_[i]` followed by norm_row(x_, w, h_) (src/model.cpp:279-282),
+ * and the end of a block (`x_ += d_`, :284) followed by the next block's
+ * first norm_row (:244-245). x_out may alias x or d (x_out == x: in place,
+ * as the reference); h must be a different buffer. [rows, cols] fp32. */
+int aero_hip_add_rmsnorm(const float* x, const float* d, float* x_out, const float* w,
+                         float* h, int64_t rows, int64_t cols, float eps, int flags,
+                         void* stream);
+
 #define AERO_ACT_SILU      0 /* g*sigmoid(g)           src/tensor.cpp:104-106,120-125 */
 #define AERO_ACT_GELU      1 /* erf GELU, A&S 7.1.26   src/tensor.cpp:52-59,108-114   */
 #define AERO_ACT_GELU_TANH 2 /* tanh-approximate GELU (no reference function)        */
@@ -231,6 +242,21 @@ int aero_hip_embed_gather(int dtype, const uint8_t* table, int64_t table_bytes,
                           int64_t vocab, int64_t n_embd, const int32_t* ids,
                           int64_t n_ids, float scale, float* out,
                           uint32_t* bad_count, void* stream);
+
+/* Embedding gather + the first block's RMSNorm in one pass: x_out[i] =
+ * dequant(table row ids[i]) (* scale when scale > 0), exactly as
+ * aero_hip_embed_gather, and h_out[i] = rmsnorm(x_out[i]) * norm_w as
+ * aero_hip_rmsnorm (norm_flags 0 or AERO_NORM_UNIT_OFFSET; norm_w NULL =
+ * ones). Replaces the reference's embedding loop and scale pass
+ * (src/model.cpp:297-316) followed by norm_row(x_, attn_norm, h_)
+ * (src/model.cpp:244-245). x_out, h_out, norm_w 16-byte aligned; x_out !=
+ * h_out; n_embd <= 8*8*256 values. Out-of-range ids as embed_gather (zero
+ * x and h rows, *bad_count += 1). */
+int aero_hip_embed_rmsnorm(int dtype, const uint8_t* table, int64_t table_bytes,
+                           int64_t vocab, int64_t n_embd, const int32_t* ids, int64_t n_ids,
+                           float scale, float* x_out, const float* norm_w, float eps,
+                           int norm_flags, float* h_out, uint32_t* bad_count,
+                           void* stream);
 
 /* Rows [r0, r1) of a resident tensor (n_rows rows of n_per_row values, whole
  * blocks a row, table 4-byte aligned) dequantised to out [(r1-r0) x
