@@ -43,6 +43,8 @@
 // nibble pair becomes fp16 (1024 + q) by or-ing in the exponent bits, and
 // one packed fp16 FMA (1024 + q)*sc - 1024*sc gives sc*q exactly (one
 // rounding of an exactly representable result).
+#include <mutex>
+
 #include "quant_blocks.hpp"
 
 #pragma clang fp contract(off)
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     const int r = l & 15, g = l >> 4;
     const int64_t row0 = (int64_t)blockIdx.x * (4 * kRowsWave) + wave * kRowsWave;
     const int tt = blockIdx.y;
-    const int nK = p.n_cols >> 5, n_g = nK;
+    const int nK = p.n_cols >> 5;
     const int n_chunks = nK / kChunkSteps, n_sb = n_chunks / 2;
 
     // rows past n_rows read the last row (their results are not stored)
@@ -535,4 +537,79 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
     return true;
 }
 
+// the quantised GEMV / GEMM dispatch (gemv.hip)
+bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
+              int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s, void* ws,
+              int64_t ws_bytes);
+
+// ------------------------------------------------ allocation-free matmul
+// The split GEMM's workspace in a file-scope device array, for callers that
+// cannot allocate (code under HIP graph capture, serving loops, harnesses
+// that forbid hipMalloc). Each GPU the library runs on holds its own copy
+// of kScratchBytes until the process ends. The array's name is a host-side
+// stand-in; its device address on the current GPU comes from
+// hipGetSymbolAddress, taken once per device and kept.
+constexpr int64_t kScratchBytes = 32ll << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// The current device's scratch address, looked up on its first use.
+void* scratch_ptr() {
+    int dev = -1;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= kScratchDevices) {
+        set_error("matmul_noalloc: device %d outside the %d the scratch table holds", dev,
+                  kScratchDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+            return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+int64_t matmul_scratch_bytes() { return kScratchBytes; }
+
+bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
+                    int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s) {
+    const int64_t need = split_gemm_workspace(dtype, n_cols, n_tok);
+    if (need > kScratchBytes) {
+        set_error("matmul_noalloc: %lld tokens of %lld columns need %lld bytes of scratch, "
+                  "more than the %lld the library holds a device; use aero_hip_matmul with a "
+                  "workspace", (long long)n_tok, (long long)n_cols, (long long)need,
+                  (long long)kScratchBytes);
+        return false;
+    }
+    void* ws = nullptr;
+    if (need > 0) {
+        ws = scratch_ptr();
+        if (ws == nullptr) return false;
+    }
+    return gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok, s, ws, need);
+}
+
 }  // namespace aero
+
+extern "C" {
+
+int aero_hip_matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
+                            float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
+                            void* stream) {
+    return aero::matmul_noalloc(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok,
+                                (hipStream_t)stream) ? 1 : 0;
+}
+
+int64_t aero_hip_matmul_noalloc_max_bytes(void) { return aero::matmul_scratch_bytes(); }
+
+}  // extern "C"

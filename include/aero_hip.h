@@ -317,6 +317,23 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
                     float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
                     void* ws, int64_t ws_bytes, void* stream);
 
+/* aero_hip_matmul without a workspace argument and without allocating: the
+ * split-x GEMM's workspace is a device array inside the library, of
+ * aero_hip_matmul_noalloc_max_bytes() (32 MiB) a GPU, held by each GPU the
+ * library runs on until the process ends. No counterpart in the reference:
+ * it is for callers that cannot call hipMalloc (code under HIP graph
+ * capture, serving loops, harnesses that forbid allocation). Results equal
+ * aero_hip_matmul's with a workspace bit for bit. Returns 0 with a reason
+ * when the call would need more scratch than the maximum (n_tok * n_cols *
+ * 6 bytes and a little more for Q4_K / Q5_K at 32 or more tokens). Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other host threads) race; calls ordered on one stream do
+ * not. Nothing in the array needs clearing between calls. */
+int aero_hip_matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
+                            float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
+                            void* stream);
+int64_t aero_hip_matmul_noalloc_max_bytes(void);
+
 /* Attention over a KV cache, the device form of aero_attention_tiled
  * (src/transformer.cpp:120-214): q [n_q, n_head, head_dim] fp32; K / V
  * [n_kv, n_head_kv, dim] in kv_dt (0 fp32, 16-byte aligned, dims a multiple
