@@ -45,6 +45,7 @@
 // rounding of an exactly representable result).
 #include <mutex>
 
+#include "act_ops.hpp"
 #include "quant_blocks.hpp"
 
 #pragma clang fp contract(off)
@@ -90,41 +91,103 @@ __device__ __forceinline__ void split3(float v, _Float16& hi, _Float16& mid, _Fl
 // the operand order above; xsum[t][8sb + k] = the sum of the scaled x over
 // sub-block k (fp32, in column order). x is read coalesced into LDS and
 // read back in operand order.
-__global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x, int n_tok,
-                                                      int n_cols, uint4* __restrict__ xp,
-                                                      float* __restrict__ xsum,
-                                                      float* __restrict__ xinv) {
+//
+// Folded steps of the model loop (the reference runs them as separate
+// passes before its matmul, src/model.cpp:244-245,279-282):
+//   RESID: x = x + d, and the sum is stored to x_out (the residual stream);
+//   NORM:  ssq[t][sb] = the sum of x^2 over the super-block, and x is
+//          multiplied by the norm weight w (or 1 + w) before the split. The
+//          GEMM multiplies each token's sums by 1/sqrtf(sum_sb ssq/n + eps),
+//          so y = W (x*inv*w) without the normalised x ever reaching HBM.
+struct XsplitArgs {
+    const float* x;
+    const float* d;       // RESID
+    float* x_out;         // RESID
+    const float* w;       // NORM (null: ones)
+    float* ssq;           // NORM: [tok_pad][n_cols/256]
+    int unit_offset;      // NORM: w applied as 1 + w
+    int n_tok;
+    int n_cols;
+    uint4* xp;
+    float* xsum;
+    float* xinv;
+};
+
+template <bool NORM, bool RESID>
+__global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
     constexpr int RowF = 256 + 4;
     __shared__ float xl[16 * RowF];
     const int tid = threadIdx.x;
     const int mt = blockIdx.x, sb = blockIdx.y;
+    const int n_cols = a.n_cols;
     const int nK = n_cols >> 5, n_sb = n_cols >> 8;
+    uint4* __restrict__ xp = a.xp;
+    float* __restrict__ xsum = a.xsum;
     // token tk = tid / 16 of the tile, columns 16 (tid % 16) .. +15
     const int tk = tid >> 4, cq = tid & 15;
     const int t = 16 * mt + tk;
     float4 v[4];
-    float amax = 0.f;
+    float amax = 0.f, ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < n_tok) {
-        const float* xr = x + (int64_t)t * n_cols + 256 * sb + 16 * cq;
+    if (t < a.n_tok) {
+        const int64_t off = (int64_t)t * n_cols + 256 * sb + 16 * cq;
+        const float* xr = a.x + off;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ld_stream(xr + 4 * i);
+        if constexpr (RESID) {
+            const float* dr = a.d + off;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 dv = ld_stream(dr + 4 * i);
+                v[i].x = v[i].x + dv.x; v[i].y = v[i].y + dv.y;
+                v[i].z = v[i].z + dv.z; v[i].w = v[i].w + dv.w;
+                __builtin_nontemporal_store(v4f{v[i].x, v[i].y, v[i].z, v[i].w},
+                                            reinterpret_cast<v4f*>(a.x_out + off + 4 * i));
+            }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ss += v[i].x * v[i].x;
+                ss += v[i].y * v[i].y;
+                ss += v[i].z * v[i].z;
+                ss += v[i].w * v[i].w;
+            }
+            if (a.w != nullptr) {
+                const float* wr = a.w + 256 * sb + 16 * cq;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float4 w4 = *reinterpret_cast<const float4*>(wr + 4 * i);
+                    if (a.unit_offset) {
+                        w4.x = 1.0f + w4.x; w4.y = 1.0f + w4.y;
+                        w4.z = 1.0f + w4.z; w4.w = 1.0f + w4.w;
+                    }
+                    v[i].x = v[i].x * w4.x; v[i].y = v[i].y * w4.y;
+                    v[i].z = v[i].z * w4.z; v[i].w = v[i].w * w4.w;
+                }
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            v[i] = ld_stream(xr + 4 * i);
-            const float a[4] = {fabsf(v[i].x), fabsf(v[i].y), fabsf(v[i].z), fabsf(v[i].w)};
+            const float q[4] = {fabsf(v[i].x), fabsf(v[i].y), fabsf(v[i].z), fabsf(v[i].w)};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) amax = a[k] <= 3.4028235e38f ? fmaxf(amax, a[k]) : amax;
+            for (int k = 0; k < 4; ++k) amax = q[k] <= 3.4028235e38f ? fmaxf(amax, q[k]) : amax;
         }
     }
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if constexpr (NORM) {
+        ss = group_sum<16>(ss);
+        if (cq == 0) a.ssq[(int64_t)t * n_sb + sb] = ss;
+    }
     int e = kScaleMax;
     if (amax > 0.f) {
         frexpf(amax, &e);
         e = min(max(e, -111), 128);  // keeps 2^(15-e) and 2^(e-15) normal
     }
     const float scale = ldexpf(1.f, kScaleMax - e);
-    if (cq == 0) xinv[(int64_t)t * n_sb + sb] = ldexpf(1.f, e - kScaleMax);
+    if (cq == 0) a.xinv[(int64_t)t * n_sb + sb] = ldexpf(1.f, e - kScaleMax);
     float* row = xl + tk * RowF + 16 * cq;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -139,9 +202,9 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
         const int s8 = (tid >> 6) + 4 * rep;
         const int c0 = 128 * (s8 >> 2) + 64 * (g >> 1) + 16 * (g & 1) + 4 * (s8 & 3);
         const float* xr = xl + lt * RowF + c0;
-        const float4 a = *reinterpret_cast<const float4*>(xr);
-        const float4 b = *reinterpret_cast<const float4*>(xr + 32);
-        const float w[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};
+        const float4 va = *reinterpret_cast<const float4*>(xr);
+        const float4 vb = *reinterpret_cast<const float4*>(xr + 32);
+        const float w[8] = {va.x, va.z, va.y, va.w, vb.x, vb.z, vb.y, vb.w};
         h8 parts[kParts];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -183,7 +246,14 @@ struct SplitParams {
     int n_cols;
     int64_t rb;
     int n_tok;
+    const uint8_t* w2;    // gate/up form: the up matrix (w is the gate)
+    const float* ssq;     // folded norm: [tok_pad][n_cols/256] sums of x^2, else null
+    float eps;
 };
+
+// Epilogue forms: y = acc (kEpiPlain), or the gate/up form: out =
+// act(gate) * up with act an AERO_ACT_* kind (src/tensor.cpp:104-125).
+constexpr int kEpiPlain = -1;
 
 // sc*q for the 4 fp16 pairs of one dword of quants of sub-block pair P
 // (Q5_K: with the fifth bits of the matching qh dword, bits 2P / 2P+1). The
@@ -285,13 +355,19 @@ __device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// NT matrix tiles of 16 rows a wave; a workgroup covers 4 x 16NT rows.
-template <int TYPE, int NT>
+// NT matrix tiles of 16 rows a wave; a workgroup covers 4 x 16NT rows. In
+// the gate/up form (EPI >= 0, NT = 2) tile 0 holds 16 rows of the gate
+// matrix and tile 1 the same 16 rows of the up matrix, so each lane ends
+// with gate and up of the same (token, row) and writes act(gate) * up: a
+// workgroup covers 4 x 16 output rows.
+template <int TYPE, int NT, int EPI>
 __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     constexpr bool Q5 = TYPE == AERO_DTYPE_Q5_K;
+    constexpr bool GU = EPI != kEpiPlain;
+    static_assert(!GU || NT == 2, "gate/up pairs one gate and one up tile");
     constexpr int BB = Q5 ? 176 : 144;          // bytes a super-block
     constexpr int QOFF = Q5 ? 48 : 16;          // quants within the block
-    constexpr int kRowsWave = 16 * NT;
+    constexpr int kRowsWave = GU ? 16 : 16 * NT;
     constexpr int MT = kTokTile / 16;           // matrix tiles over tokens (2)
     constexpr int CHUNK = MT * XStage::CSTEP;   // uint4 a chunk (1536)
     static_assert(MT == 2 && CHUNK == 6 * 256, "staging split");
@@ -309,11 +385,14 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     const int n_chunks = nK / kChunkSteps, n_sb = n_chunks / 2;
 
     // rows past n_rows read the last row (their results are not stored)
-    const uint8_t* wbase = p.w + row0 * p.rb;
+    const uint8_t* wbase[NT];
     int woff[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
-        woff[j] = (int)((min(row0 + 16 * j + r, p.n_rows - 1) - row0) * p.rb);
+    for (int j = 0; j < NT; ++j) {
+        wbase[j] = (GU && j == 1 ? p.w2 : p.w) + row0 * p.rb;
+        const int64_t rj = GU ? row0 + r : row0 + 16 * j + r;
+        woff[j] = (int)((min(rj, p.n_rows - 1) - row0) * p.rb);
+    }
 
     XStage xst;
     xst.init(p.xp, p.xsum, p.xinv, tt, nK, tid);
@@ -322,9 +401,10 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     // both halves) and its 16-byte header, loaded a super-block ahead
     uint4 q[2][NT], hq[NT], hd[NT];
     auto load_w = [&](int sb, uint4 (&qq)[2][NT], uint4 (&hh)[NT], uint4 (&dd)[NT]) {
-        const uint8_t* b = wbase + (int64_t)min(sb, n_sb - 1) * BB;
+        const int64_t sbo = (int64_t)min(sb, n_sb - 1) * BB;
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
+            const uint8_t* b = wbase[j] + sbo;
             qq[0][j] = ld128(b + woff[j] + QOFF + 16 * g);
             qq[1][j] = ld128(b + woff[j] + QOFF + 64 + 16 * g);
             if (Q5) hh[j] = ld128(b + woff[j] + 16 + 16 * (g & 1));
@@ -469,23 +549,172 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         __syncthreads();
     }
 
-    // acc[m][j][v]: token 32tt + 16m + 4g + v, row row0 + 16j + r
+    // folded norm: each token's sums times 1/sqrtf(sum of x^2 / n + eps),
+    // the sum of its super-block partials (8 lanes a token, in a fixed order)
+    __shared__ float tinv[kTokTile];
+    if (p.ssq != nullptr) {
+        const int k = tid >> 3, part = tid & 7;
+        const float* sp = p.ssq + (int64_t)(kTokTile * tt + k) * n_sb;
+        float sum = 0.f;
+        for (int i = part; i < n_sb; i += 8) sum += sp[i];
+        sum = group_sum<8>(sum);
+        if (part == 0) tinv[k] = 1.0f / sqrtf(sum / (float)p.n_cols + p.eps);
+        __syncthreads();
+    }
+
+    // acc[m][j][v]: token 32tt + 16m + 4g + v, row row0 + 16j + r (gate/up:
+    // row row0 + r of the gate (j = 0) and the up (j = 1) matrix)
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int tok = kTokTile * tt + 16 * m + 4 * g + v;
+            const int tk = 16 * m + 4 * g + v;
+            const int tok = kTokTile * tt + tk;
             if (tok >= p.n_tok) continue;
+            const float inv = p.ssq != nullptr ? tinv[tk] : 1.0f;
             float* yp = p.y + (int64_t)tok * p.n_rows;
+            if constexpr (GU) {
+                const int64_t row = row0 + r;
+                float gv = acc[m][0][v], uv = acc[m][1][v];
+                if (p.ssq != nullptr) {
+                    gv = gv * inv;
+                    uv = uv * inv;
+                }
+                if (row < p.n_rows) yp[row] = act<GU ? EPI : 0>(gv) * uv;
+            } else {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                const int64_t row = row0 + 16 * j + r;
-                if (row < p.n_rows) yp[row] = acc[m][j][v];
+                for (int j = 0; j < NT; ++j) {
+                    const int64_t row = row0 + 16 * j + r;
+                    const float y = p.ssq != nullptr ? acc[m][j][v] * inv : acc[m][j][v];
+                    if (row < p.n_rows) yp[row] = y;
+                }
             }
         }
 }
 
 inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+// Workspace layout of the split-x GEMM for tp (padded) tokens of n_cols:
+// the x parts, the sub-block sums, the inverse scales and, with a folded
+// norm, the per-super-block sums of x^2.
+struct SplitWs {
+    uint4* xp;
+    float* xsum;
+    float* xinv;
+    float* ssq;
+};
+
+int64_t split_ws_bytes(int64_t tp, int64_t n_cols, bool norm) {
+    return align256(tp * n_cols * 2 * kParts) + align256(tp * (n_cols / 32) * 4) +
+           align256(tp * (n_cols / 256) * 4) + (norm ? align256(tp * (n_cols / 256) * 4) : 0);
+}
+
+SplitWs split_ws(void* ws, int64_t tp, int64_t n_cols) {
+    uint8_t* b = static_cast<uint8_t*>(ws);
+    SplitWs w;
+    w.xp = reinterpret_cast<uint4*>(b);
+    b += align256(tp * n_cols * 2 * kParts);
+    w.xsum = reinterpret_cast<float*>(b);
+    b += align256(tp * (n_cols / 32) * 4);
+    w.xinv = reinterpret_cast<float*>(b);
+    b += align256(tp * (n_cols / 256) * 4);
+    w.ssq = reinterpret_cast<float*>(b);
+    return w;
+}
+
+int64_t pad_tokens(int64_t n_tok) { return (n_tok + kTokTile - 1) / kTokTile * kTokTile; }
+
+// The shape part of whether the split path applies (types with it, whole
+// super-blocks a row, grid limits); alignment is checked at the call.
+bool split_shape_ok(int dtype, int64_t n_cols, int64_t n_tok) {
+    return (dtype == AERO_DTYPE_Q4_K || dtype == AERO_DTYPE_Q5_K) && n_cols > 0 &&
+           n_cols % 256 == 0 && n_cols / 256 <= 65535 && n_tok > 0 &&
+           pad_tokens(n_tok) / kTokTile <= 65535 && pad_tokens(n_tok) <= 0x7fffffff;
+}
+
+// One folded pre-pass, then the GEMM launches: n_mat plain products
+// y[m] = W_m x', or (w_up != null) one gate/up launch out = act(W x') * (U x').
+struct SplitJob {
+    int dtype;
+    const float* x;
+    const float* d;        // residual input (x' = x + d, stored to x_out) or null
+    float* x_out;
+    const float* norm_w;   // folded RMSNorm weight (null: ones)
+    int norm;              // < 0: no norm; else 0 / AERO_NORM_UNIT_OFFSET
+    float eps;
+    int n_mat;
+    const uint8_t* const* w;
+    const uint8_t* w_up;   // gate/up form when non-null (w[0] is the gate)
+    int act;
+    const int64_t* n_rows;
+    float* const* y;
+    int64_t n_cols;
+    int64_t rb;
+    int64_t n_tok;
+    void* ws;
+};
+
+template <bool NORM, bool RESID>
+bool launch_xsplit(const XsplitArgs& a, int64_t tp, hipStream_t s) {
+    return launch("xsplit_kernel", xsplit_kernel<NORM, RESID>,
+                  dim3((unsigned)(tp / 16), (unsigned)(a.n_cols / 256)), dim3(256), 0, s, a);
+}
+
+template <int TYPE>
+void* pick_split_gemm(int nt, int epi) {
+    switch (epi) {
+    case kEpiPlain:
+        return nt == 4 ? (void*)split_gemm_kernel<TYPE, 4, kEpiPlain>
+                       : (void*)split_gemm_kernel<TYPE, 2, kEpiPlain>;
+    case AERO_ACT_SILU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_SILU>;
+    case AERO_ACT_GELU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_GELU>;
+    case AERO_ACT_GELU_TANH: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_GELU_TANH>;
+    case AERO_ACT_IDENTITY: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_IDENTITY>;
+    default: return nullptr;
+    }
+}
+
+bool split_run(const SplitJob& j, hipStream_t s) {
+    const int64_t tp = pad_tokens(j.n_tok);
+    const bool norm = j.norm >= 0;
+    const SplitWs w = split_ws(j.ws, tp, j.n_cols);
+    XsplitArgs a{j.x, j.d, j.x_out, j.norm_w, w.ssq, norm && (j.norm & AERO_NORM_UNIT_OFFSET),
+                 (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv};
+    const bool ok = norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
+                                : launch_xsplit<true, false>(a, tp, s))
+                         : (j.d ? launch_xsplit<false, true>(a, tp, s)
+                                : launch_xsplit<false, false>(a, tp, s));
+    if (!ok) return false;
+    const bool gu = j.w_up != nullptr;
+    // rows a wave: 32 (two waves a SIMD); 64 (AERO_HIP_TUNE gemm16_nt=4) runs
+    // one wave a SIMD and measured slower on MI355X at every prefill shape
+    const int nt = gu ? 2 : (tune("gemm16_nt", 2) == 4 ? 4 : 2);
+    const int rows_wg = gu ? 64 : 64 * nt;
+    const bool q5 = j.dtype == AERO_DTYPE_Q5_K;
+    const int epi = gu ? j.act : kEpiPlain;
+    void* kp = q5 ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi)
+                  : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi);
+    if (kp == nullptr) {
+        set_error("split GEMM: unknown activation %d", j.act);
+        return false;
+    }
+    auto k = reinterpret_cast<void (*)(SplitParams)>(kp);
+    const int n_launch = gu ? 1 : j.n_mat;
+    for (int m = 0; m < n_launch; ++m) {
+        const int64_t row_tiles = (j.n_rows[m] + rows_wg - 1) / rows_wg;
+        if (row_tiles > 0x7fffffff) {
+            set_error("split GEMM: too many rows (%lld)", (long long)j.n_rows[m]);
+            return false;
+        }
+        if (row_tiles == 0) continue;
+        SplitParams p{j.w[m], w.xp, w.xsum, w.xinv, j.y[m], j.n_rows[m], (int)j.n_cols, j.rb,
+                      (int)j.n_tok, gu ? j.w_up : nullptr, norm ? w.ssq : nullptr, j.eps};
+        if (!launch("split_gemm_kernel", k, dim3((unsigned)row_tiles, (unsigned)(tp / kTokTile)),
+                    dim3(256), 0, s, p))
+            return false;
+    }
+    return true;
+}
 
 }  // namespace
 
@@ -493,12 +722,8 @@ inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 // type or shape has no split path): the x parts, the sub-block sums and the
 // inverse scales.
 int64_t split_gemm_workspace(int dtype, int64_t n_cols, int64_t n_tok) {
-    if ((dtype != AERO_DTYPE_Q4_K && dtype != AERO_DTYPE_Q5_K) || n_cols <= 0 ||
-        n_cols % 256 != 0 || n_cols / 256 > 65535 || n_tok <= 0)
-        return 0;
-    const int64_t tp = (n_tok + kTokTile - 1) / kTokTile * kTokTile;
-    return align256(tp * n_cols * 2 * kParts) + align256(tp * (n_cols / 32) * 4) +
-           align256(tp * (n_cols / 256) * 4);
+    if (!split_shape_ok(dtype, n_cols, n_tok)) return 0;
+    return split_ws_bytes(pad_tokens(n_tok), n_cols, false);
 }
 
 // Called by the matmul entry after its argument checks; false (without an
@@ -508,34 +733,19 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
                     hipStream_t s, bool* ran) {
     *ran = false;
     const int64_t need = split_gemm_workspace(dtype, n_cols, n_tok);
-    const int64_t tp = (n_tok + kTokTile - 1) / kTokTile * kTokTile;
-    // rows a wave: 32 (two waves a SIMD); 64 (AERO_HIP_TUNE gemm16_nt=4) runs
-    // one wave a SIMD and measured slower on MI355X at every prefill shape
-    const int64_t tok_tiles = tp / kTokTile;
-    const int nt = tune("gemm16_nt", 2) == 4 ? 4 : 2;
-    const int64_t row_tiles = (n_rows + 64 * nt - 1) / (64 * nt);
     if (need == 0 || ws == nullptr || ws_bytes < need || !aligned16(w) || rb % 16 != 0 ||
-        !aligned16(ws) || tok_tiles > 65535 || row_tiles > 0x7fffffff || tp > 0x7fffffff ||
-        !tune("gemm16", 1))
+        !aligned16(ws) || !tune("gemm16", 1))
         return true;
-    uint8_t* base = static_cast<uint8_t*>(ws);
-    uint4* xp = reinterpret_cast<uint4*>(base);
-    float* xsum = reinterpret_cast<float*>(base + align256(tp * n_cols * 2 * kParts));
-    float* xinv = reinterpret_cast<float*>(base + align256(tp * n_cols * 2 * kParts) +
-                                           align256(tp * (n_cols / 32) * 4));
-    if (!launch("xsplit_kernel", xsplit_kernel, dim3((unsigned)(tp / 16), (unsigned)(n_cols / 256)),
-                dim3(256), 0, s, x, (int)n_tok, (int)n_cols, xp, xsum, xinv))
-        return false;
-    SplitParams p{w, xp, xsum, xinv, y, n_rows, (int)n_cols, rb, (int)n_tok};
-    const bool q5 = dtype == AERO_DTYPE_Q5_K;
-    auto k = nt == 4 ? (q5 ? split_gemm_kernel<AERO_DTYPE_Q5_K, 4> : split_gemm_kernel<AERO_DTYPE_Q4_K, 4>)
-                     : (q5 ? split_gemm_kernel<AERO_DTYPE_Q5_K, 2> : split_gemm_kernel<AERO_DTYPE_Q4_K, 2>);
-    if (!launch("split_gemm_kernel", k, dim3((unsigned)row_tiles, (unsigned)tok_tiles), dim3(256),
-                0, s, p))
-        return false;
+    SplitJob j{dtype, x, nullptr, nullptr, nullptr, -1, 0.f, 1, &w, nullptr, 0, &n_rows, &y,
+               n_cols, rb, n_tok, ws};
+    if (!split_run(j, s)) return false;
     *ran = true;
     return true;
 }
+
+// block sizes of the ggml types (quant.hip)
+int64_t dtype_block_bytes(int t);
+int64_t dtype_block_values(int t);
 
 // the quantised GEMV / GEMM dispatch (gemv.hip)
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
@@ -599,9 +809,128 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
     return gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok, s, ws, need);
 }
 
+// ------------------------------------ norm (and residual) folded into GEMMs
+// The prefill forms of the model loop's "norm -> projections" and "norm ->
+// gate/up -> act" steps (src/model.cpp:166-178,244-245,279-282): the split
+// path folds the residual add and the RMSNorm into the x pre-pass and the
+// act-mul into the GEMM epilogue; other types and shapes run the same steps
+// as separate launches (add+norm into the workspace, the library GEMM, the
+// act-mul), so every type and token count is accepted.
+int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok) {
+    if (n_cols <= 0 || n_tok <= 0 || n_ff < 0) return 0;
+    if (split_shape_ok(dtype, n_cols, n_tok) && n_tok >= tune("gemm_min_tokens", 32))
+        return split_ws_bytes(pad_tokens(n_tok), n_cols, true);
+    return align256(n_tok * n_cols * 4) + (n_ff > 0 ? align256(n_tok * n_ff * 4) : 0);
+}
+
+namespace {
+
+bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t ws_bytes,
+                     hipStream_t s) {
+    const int64_t bv = dtype_block_values(j.dtype), bb = dtype_block_bytes(j.dtype);
+    const bool gu = j.w_up != nullptr;
+    if (bv <= 0 || j.x == nullptr || j.n_cols <= 0 || j.n_tok < 0 || j.n_cols % bv != 0 ||
+        j.n_cols > (int64_t)1 << 30 || j.n_tok > 0x7fffffff || (j.d && !j.x_out) ||
+        j.norm > AERO_NORM_UNIT_OFFSET || j.n_mat < 1 || j.n_mat > 4 ||
+        (j.norm_w && !aligned16(j.norm_w)) || !aligned16(j.x) || (j.d && !aligned16(j.d)) ||
+        (j.x_out && !aligned16(j.x_out))) {
+        set_error("norm_matmul: bad arguments (n_cols=%lld n_tok=%lld n_mat=%d norm=%d; x, d, "
+                  "x_out, norm_w 16-byte aligned, n_cols a multiple of %lld, d needs x_out)",
+                  (long long)j.n_cols, (long long)j.n_tok, j.n_mat, j.norm, (long long)bv);
+        return false;
+    }
+    j.rb = (j.n_cols / bv) * bb;
+    for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) {
+        if (j.w[m] == nullptr || j.y[m] == nullptr || j.n_rows[m] < 0 ||
+            w_bytes[m] < j.n_rows[m] * j.rb) {
+            set_error("norm_matmul: matrix %d: null, or w_bytes %lld < n_rows*row_bytes %lld", m,
+                      (long long)w_bytes[m], (long long)(j.n_rows[m] * j.rb));
+            return false;
+        }
+    }
+    if (j.n_tok == 0) return true;
+    const int64_t need = norm_matmul_workspace(j.dtype, j.n_cols, gu ? n_ff : 0, j.n_tok);
+    if (j.ws == nullptr || ws_bytes < need || !aligned16(j.ws)) {
+        set_error("norm_matmul: workspace of %lld bytes (16-byte aligned) needed, %lld given",
+                  (long long)need, (long long)ws_bytes);
+        return false;
+    }
+    bool split = split_shape_ok(j.dtype, j.n_cols, j.n_tok) &&
+                 j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
+    for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
+    if (gu) split = split && aligned16(j.w_up);
+    if (split) return split_run(j, s);
+
+    // separate launches: x' (= x + d) and h = rmsnorm(x') in the workspace
+    const float* h = j.d ? j.x_out : j.x;
+    float* hb = static_cast<float*>(j.ws);
+    if (j.norm >= 0) {
+        const int ok = j.d ? aero_hip_add_rmsnorm(j.x, j.d, j.x_out, j.norm_w, hb, j.n_tok,
+                                                  j.n_cols, j.eps, j.norm, s)
+                           : aero_hip_rmsnorm(j.x, j.norm_w, hb, j.n_tok, j.n_cols, j.eps,
+                                              j.norm, s);
+        if (!ok) return false;
+        h = hb;
+    } else if (j.d) {
+        if (!aero_hip_act_mul(AERO_ACT_IDENTITY, j.x, j.d, j.x_out, j.n_tok * j.n_cols, s))
+            return false;
+    }
+    if (!gu) {
+        for (int m = 0; m < j.n_mat; ++m)
+            if (!gemv_dev(j.dtype, j.w[m], w_bytes[m], h, j.y[m], j.n_rows[m], j.n_cols,
+                          j.n_tok, s, nullptr, 0))
+                return false;
+        return true;
+    }
+    float* ub = reinterpret_cast<float*>(static_cast<uint8_t*>(j.ws) +
+                                         align256(j.n_tok * j.n_cols * 4));
+    return gemv_dev(j.dtype, j.w[0], w_bytes[0], h, j.y[0], n_ff, j.n_cols, j.n_tok, s,
+                    nullptr, 0) &&
+           gemv_dev(j.dtype, j.w_up, w_bytes[0], h, ub, n_ff, j.n_cols, j.n_tok, s, nullptr,
+                    0) &&
+           aero_hip_act_mul(j.act, j.y[0], ub, j.y[0], j.n_tok * n_ff, s) == 1;
+}
+
+}  // namespace
+
 }  // namespace aero
 
 extern "C" {
+
+int64_t aero_hip_norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok) {
+    return aero::norm_matmul_workspace(dtype, n_cols, n_ff, n_tok);
+}
+
+int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
+                         const int64_t* n_rows, float* const* y, const float* x, const float* d,
+                         float* x_out, const float* norm_w, float eps, int norm, int64_t n_cols,
+                         int64_t n_tok, void* ws, int64_t ws_bytes, void* stream) {
+    if (w == nullptr || w_bytes == nullptr || n_rows == nullptr || y == nullptr) {
+        aero::set_error("norm_matmul: null matrix arrays");
+        return 0;
+    }
+    aero::SplitJob j{dtype, x, d, x_out, norm_w, norm, eps, n_mat, w, nullptr, 0, n_rows, y,
+                     n_cols, 0, n_tok, ws};
+    return aero::norm_matmul_run(j, w_bytes, 0, ws_bytes, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
+                                 int64_t w_bytes, const float* x, const float* d, float* x_out,
+                                 const float* norm_w, float eps, int norm, int act, float* out,
+                                 int64_t n_ff, int64_t n_cols, int64_t n_tok, void* ws,
+                                 int64_t ws_bytes, void* stream) {
+    if (w_up == nullptr || act < AERO_ACT_SILU || act > AERO_ACT_IDENTITY) {
+        aero::set_error("norm_matmul_gate_up: null up matrix or unknown activation %d", act);
+        return 0;
+    }
+    const uint8_t* const ws_g[1] = {w_gate};
+    const int64_t wb[1] = {w_bytes};
+    const int64_t nr[1] = {n_ff};
+    float* const ys[1] = {out};
+    aero::SplitJob j{dtype, x, d, x_out, norm_w, norm, eps, 1, ws_g, w_up, act, nr, ys,
+                     n_cols, 0, n_tok, ws};
+    return aero::norm_matmul_run(j, wb, n_ff, ws_bytes, (hipStream_t)stream) ? 1 : 0;
+}
 
 int aero_hip_matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
                             float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,

@@ -293,6 +293,73 @@ def norm_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceAr
                "norm_gate_up")
 
 
+_norm_mm_ws = Workspace("norm GEMM")
+
+
+def _norm_flag(norm: bool, unit_offset: bool) -> int:
+    return (NORM_UNIT_OFFSET if unit_offset else 0) if norm else -1
+
+
+def norm_matmul(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_cols: int,
+                n_tok: int, norm_w: DeviceArray | None = None, eps: float = 1e-5,
+                norm: bool = True, unit_offset: bool = False, d: DeviceArray | None = None,
+                x_out: DeviceArray | None = None, stream: Stream | None = None) -> None:
+    """ys[m] = rmsnorm(x') @ W_m^T for up to 4 matrices of one type sharing x'
+    (q, k, v), any token count; x' = x + d (stored to x_out, default x) when
+    d is given, else x. The split GEMM folds the add and the norm into its
+    x pre-pass (Q4_K / Q5_K, 32+ tokens)."""
+    if not 1 <= len(ws) <= 4 or len(ys) != len(ws) or len(n_rows) != len(ws):
+        raise ValueError("norm_matmul: 1 to 4 matrices, with as many outputs and row counts")
+    if d is not None and x_out is None:
+        x_out = x
+    for a, name in ((x, "x"), (d, "d"), (x_out, "x_out")):
+        _need(a, n_tok * n_cols, np.float32, name)
+    _need(norm_w, n_cols, np.float32, "norm_w")
+    for y, nr in zip(ys, n_rows):
+        _need(y, n_tok * nr, np.float32, "y")
+    k = len(ws)
+    wp = (ctypes.c_void_p * k)(*[w.ptr for w in ws])
+    wb = (ctypes.c_int64 * k)(*[w.nbytes for w in ws])
+    nr = (ctypes.c_int64 * k)(*[int(n) for n in n_rows])
+    yp = (ctypes.c_void_p * k)(*[y.ptr for y in ys])
+    L = _lib.lib()
+    wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, 0, n_tok)
+    buf = _norm_mm_ws.get(wsb)
+    _lib.check(L.aero_hip_norm_matmul(int(dtype), k, wp, wb, nr, yp, x.ptr, as_ptr(d),
+                                      as_ptr(x_out), as_ptr(norm_w), float(eps),
+                                      _norm_flag(norm, unit_offset), n_cols, n_tok, as_ptr(buf),
+                                      0 if buf is None else buf.nbytes, _s(stream)),
+               "norm_matmul")
+
+
+def norm_matmul_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceArray,
+                        out: DeviceArray, n_ff: int, n_cols: int, n_tok: int, act="silu",
+                        norm_w: DeviceArray | None = None, eps: float = 1e-5,
+                        norm: bool = True, unit_offset: bool = False,
+                        d: DeviceArray | None = None, x_out: DeviceArray | None = None,
+                        stream: Stream | None = None) -> None:
+    """out = act(rmsnorm(x') @ Wg^T) * (rmsnorm(x') @ Wu^T), any token count,
+    x' as norm_matmul. The split GEMM forms act(gate)*up in its epilogue."""
+    kind = ACTS[act] if isinstance(act, str) else int(act)
+    if w_gate.nbytes != w_up.nbytes:
+        raise ValueError("norm_matmul_gate_up: gate and up must be the same size")
+    if d is not None and x_out is None:
+        x_out = x
+    for a, name in ((x, "x"), (d, "d"), (x_out, "x_out")):
+        _need(a, n_tok * n_cols, np.float32, name)
+    _need(out, n_tok * n_ff, np.float32, "out")
+    _need(norm_w, n_cols, np.float32, "norm_w")
+    L = _lib.lib()
+    wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, n_ff, n_tok)
+    buf = _norm_mm_ws.get(wsb)
+    _lib.check(L.aero_hip_norm_matmul_gate_up(int(dtype), w_gate.ptr, w_up.ptr, w_gate.nbytes,
+                                              x.ptr, as_ptr(d), as_ptr(x_out), as_ptr(norm_w),
+                                              float(eps), _norm_flag(norm, unit_offset), kind,
+                                              out.ptr, n_ff, n_cols, n_tok, as_ptr(buf),
+                                              0 if buf is None else buf.nbytes, _s(stream)),
+               "norm_matmul_gate_up")
+
+
 KV_F32, KV_INT8, KV_INT4 = 0, 1, 2
 
 

@@ -37,6 +37,7 @@ dequant over the same rows beside it.
     python bench.py --gemv              # quantised GEMV (decode projections)
     python bench.py --gemm              # quantised GEMM (prefill projections)
     python bench.py --fused             # fused decode GEMVs vs the launches they replace
+    python bench.py --layer-gemm        # prefill add+norm folded into the GEMMs vs unfused
     python bench.py --attention         # attention over a KV cache (decode, prefill)
     python bench.py --gguf              # GGUF parse, upload to HBM, device row addressing
     python bench.py --ssm               # gated DeltaNet scan and conv
@@ -96,6 +97,8 @@ def parse_args(argv=None):
                    help="attention over a KV cache (decode and causal prefill)")
     p.add_argument("--fused", action="store_true",
                    help="fused decode GEMVs (norm + q/k/v, norm + gate/up + act) vs separate")
+    p.add_argument("--layer-gemm", action="store_true",
+                   help="norm -> projections, unfused vs folded into the GEMM (512 tokens)")
     p.add_argument("--gemm", action="store_true",
                    help="quantised GEMM cases (prefill token counts)")
     p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
@@ -594,6 +597,8 @@ def main(argv=None):
         return gemv(a)
     if a.gemm:
         return gemm(a)
+    if a.layer_gemm:
+        return layer_gemm(a)
     if a.fused:
         return fused(a)
     if a.attention:
@@ -930,6 +935,83 @@ def gemm(a):
             print(json.dumps(res), flush=True)
         stream.destroy()
         del ws
+    return 0
+
+
+def layer_gemm(a):
+    """The prefill layer's two norm -> projection steps at the Llama-3-8B
+    512-token shape over Q4_K weights, unfused (add + RMSNorm kernel, then
+    the split GEMM per matrix, then act-mul) against the folded forms
+    (aero_hip_norm_matmul, aero_hip_norm_matmul_gate_up). Each form is a
+    recorded plan replayed back to back over 4 weight sets (> 256 MiB
+    together); mean µs per call between one event pair."""
+    from aero_amd import ops, workloads as W
+    from aero_amd.device import DeviceArray as DA, Event, Plan, Stream
+
+    s = W.SHAPES[W.HEADLINE]
+    T, N, F = s.n_tok, s.hidden, s.ffn
+    rng = np.random.default_rng(0)
+    t = W.Q4_K
+    rows = [s.hq * s.head_dim, s.hk * s.head_dim, s.hk * s.head_dim]
+
+    def mat(r):
+        return DA.from_numpy(W.make_table(t, r * N // 256, rng))
+
+    sets = [{"qkv": [mat(r) for r in rows], "g": mat(F), "u": mat(F)} for _ in range(4)]
+    x = DA.from_numpy(rng.standard_normal((T, N), dtype=np.float32))
+    d = DA.from_numpy(rng.standard_normal((T, N), dtype=np.float32))
+    w = DA.from_numpy(np.float32(1) + rng.standard_normal(N, dtype=np.float32) * np.float32(0.1))
+    h = DA.empty((T, N))
+    ys = [DA.empty((T, r)) for r in rows]
+    g, u = DA.empty((T, F)), DA.empty((T, F))
+
+    def attn_unfused(m):
+        ops.add_rmsnorm(x, d, w, h, T, N, s.eps)
+        for wm, y, r in zip(m["qkv"], ys, rows):
+            ops.matvec(t, wm, h, y, r, N, T)
+
+    def attn_fused(m):
+        ops.norm_matmul(t, m["qkv"], x, ys, rows, N, T, norm_w=w, eps=s.eps, d=d)
+
+    def ffn_unfused(m):
+        ops.add_rmsnorm(x, d, w, h, T, N, s.eps)
+        ops.matvec(t, m["g"], h, g, F, N, T)
+        ops.matvec(t, m["u"], h, u, F, N, T)
+        ops.act_mul("silu", g, u, g)
+
+    def ffn_fused(m):
+        ops.norm_matmul_gate_up(t, m["g"], m["u"], x, g, F, N, T, act="silu", norm_w=w,
+                                eps=s.eps, d=d)
+
+    flops = {"attn": 2.0 * T * N * sum(rows), "ffn": 2.0 * T * N * 2 * F}
+    res = {}
+    for name, fn in (("attn_unfused", attn_unfused), ("attn_fused", attn_fused),
+                     ("ffn_unfused", ffn_unfused), ("ffn_fused", ffn_fused)):
+        plan = Plan()
+        with plan:
+            for m in sets:
+                fn(m)
+        stream = Stream()
+        plan.launch(stream)
+        reps = max(5, a.steps // 20)
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(reps):
+            plan.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * len(sets))
+        kinds = len(plan) // len(sets)
+        res[name] = us
+        tf = flops[name.split("_")[0]] / (us * 1e-6) / 1e12
+        print(json.dumps({"case": name, "us": round(us, 2), "launches": kinds,
+                          "TFLOP/s": round(tf, 1), "shape": f"{T}x{N} Q4_K"}), flush=True)
+        plan.destroy()
+        stream.destroy()
+    print(json.dumps({"attn_speedup": round(res["attn_unfused"] / res["attn_fused"], 3),
+                      "ffn_speedup": round(res["ffn_unfused"] / res["ffn_fused"], 3),
+                      "saved_us": round(res["attn_unfused"] - res["attn_fused"] +
+                                        res["ffn_unfused"] - res["ffn_fused"], 2)}), flush=True)
     return 0
 
 

@@ -317,6 +317,39 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
                     float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
                     void* ws, int64_t ws_bytes, void* stream);
 
+/* Prefill forms of the decode steps above, any token count: one pass that
+ * folds the residual add and the RMSNorm into the GEMM's x pre-pass, then
+ * the projections. The reference runs these as separate passes: `x_ +=
+ * o_`, norm_row (src/model.cpp:244-245,279-282), matmul per matrix
+ * (src/kernels.cpp:520-538) and act-mul (src/model.cpp:172-175). x is
+ * [n_tok, n_cols] fp32; with d != NULL, x' = x + d is the residual stream
+ * and is stored to x_out (may alias x or d), else x' = x. h = x' normalised
+ * as aero_hip_rmsnorm (weight norm_w, NULL = ones; flags `norm` 0 or
+ * AERO_NORM_UNIT_OFFSET; norm < 0: h = x').
+ *   aero_hip_norm_matmul: y[m][t*n_rows[m] + r] = W_m[r] . h[t] for up to 4
+ *     matrices of one type and width (q, k, v);
+ *   aero_hip_norm_matmul_gate_up: out[t*n_ff + r] = act(Wg[r] . h[t]) *
+ *     (Wu[r] . h[t]), act an AERO_ACT_* kind.
+ * Q4_K / Q5_K with 32 or more tokens (weights 16-byte aligned) run the
+ * split-x fp16 GEMM with h never written: each token's sums are scaled by
+ * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
+ * epilogue. Other types and shapes run add+norm into the workspace, the
+ * library GEMM per matrix and the act-mul. Each result equals that
+ * composition to 1e-5 of its scale. ws (16-byte aligned) of at least
+ * aero_hip_norm_matmul_workspace(dtype, n_cols, n_ff (0 for the plain
+ * form), n_tok) bytes; x, d, x_out, norm_w 16-byte aligned; h, y and out
+ * must not overlap x, d or x_out. */
+int64_t aero_hip_norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok);
+int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
+                         const int64_t* n_rows, float* const* y, const float* x, const float* d,
+                         float* x_out, const float* norm_w, float eps, int norm, int64_t n_cols,
+                         int64_t n_tok, void* ws, int64_t ws_bytes, void* stream);
+int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
+                                 int64_t w_bytes, const float* x, const float* d, float* x_out,
+                                 const float* norm_w, float eps, int norm, int act, float* out,
+                                 int64_t n_ff, int64_t n_cols, int64_t n_tok, void* ws,
+                                 int64_t ws_bytes, void* stream);
+
 /* aero_hip_matmul without a workspace argument and without allocating: the
  * split-x GEMM's workspace is a device array inside the library, of
  * aero_hip_matmul_noalloc_max_bytes() (32 MiB) a GPU, held by each GPU the

@@ -1,0 +1,168 @@
+"""GPU parity: the prefill norm -> projection forms (aero_hip_norm_matmul,
+aero_hip_norm_matmul_gate_up) against the oracle's composition of the passes
+they replace: the residual add `x_ += o_` and norm_row (src/model.cpp:244-245,
+279-282), matmul (src/kernels.cpp:520-538) and act_mul (src/model.cpp:172-175).
+
+Q4_K / Q5_K with 32+ tokens take the split-x GEMM with the add and the norm
+folded into its pre-pass and act(gate)*up in its epilogue; other types and
+token counts take separate launches. Tolerance: 1e-5 of the output's scale
+(the reference's RTOL, tests/test_transformer_native.py:34-37); the residual
+stream x + d is bit-exact (one IEEE add).
+"""
+import numpy as np
+import pytest
+
+from conftest import RTOL, bits_equal, rel_to_scale
+from aero_amd import _lib, ops
+from aero_amd import workloads as W
+from aero_amd.device import DeviceArray as DA
+
+pytestmark = pytest.mark.gpu
+
+ACT = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
+
+
+def weights(t, n_rows, n_cols, rng):
+    return W.make_table(t, n_rows * n_cols // W.BLOCK[t][0], rng)
+
+
+def oracle_h(oracle, x, d, w, eps, unit_offset, norm=True):
+    xs = x + d if d is not None else x
+    return xs, (oracle.rmsnorm_rows(xs, w, eps, unit_offset) if norm else xs)
+
+
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q5_K, W.Q6_K, W.Q8_0])
+@pytest.mark.parametrize("n_tok,n_cols,rows", [
+    (64, 1024, (256, 64, 64)), (33, 2048, (130,)), (100, 512, (96, 40)), (7, 1024, (64, 64, 64)),
+])
+@pytest.mark.parametrize("form", ["norm", "resid_norm", "unit_offset", "no_norm"])
+def test_norm_matmul_vs_oracle(hip, oracle, t, n_tok, n_cols, rows, form):
+    rng = np.random.default_rng(n_tok * 7 + n_cols + len(rows) + t)
+    x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+    d = rng.standard_normal((n_tok, n_cols), dtype=np.float32) if form == "resid_norm" else None
+    uo = form == "unit_offset"
+    w = (rng.standard_normal(n_cols, dtype=np.float32) * np.float32(0.1) + (0 if uo else 1)
+         ).astype(np.float32)
+    mats = [weights(t, r, n_cols, rng) for r in rows]
+    print(f"norm_matmul type={t} tok={n_tok} cols={n_cols} rows={rows} form={form}", flush=True)
+    dx, dw = DA.from_numpy(x), DA.from_numpy(w)
+    dd = None if d is None else DA.from_numpy(d)
+    ys = [DA.empty((n_tok, r)) for r in rows]
+    ops.norm_matmul(t, [DA.from_numpy(m) for m in mats], dx, ys, list(rows), n_cols, n_tok,
+                    norm_w=dw, eps=1e-5, norm=form != "no_norm", unit_offset=uo, d=dd)
+    xs, h = oracle_h(oracle, x, d, w, 1e-5, uo, norm=form != "no_norm")
+    if d is not None:
+        assert bits_equal(dx.numpy(), xs)          # the residual stream, in place
+    for y, m, r in zip(ys, mats, rows):
+        assert rel_to_scale(y.numpy(), oracle.matmul(t, m, h, r)) <= RTOL
+
+
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q5_K, W.Q6_K])
+@pytest.mark.parametrize("act", list(ACT))
+@pytest.mark.parametrize("n_tok,n_cols,n_ff", [(64, 1024, 320), (45, 512, 100), (5, 512, 64)])
+def test_gate_up_vs_oracle(hip, oracle, t, act, n_tok, n_cols, n_ff):
+    rng = np.random.default_rng(n_tok + n_cols + n_ff + t + ACT[act])
+    x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+    d = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+    w = (np.float32(1) + rng.standard_normal(n_cols, dtype=np.float32) * np.float32(0.1))
+    wg, wu = weights(t, n_ff, n_cols, rng), weights(t, n_ff, n_cols, rng)
+    print(f"gate_up type={t} act={act} tok={n_tok} cols={n_cols} ff={n_ff}", flush=True)
+    dx, dd = DA.from_numpy(x), DA.from_numpy(d)
+    xo = DA.empty(x.shape)
+    out = DA.empty((n_tok, n_ff))
+    ops.norm_matmul_gate_up(t, DA.from_numpy(wg), DA.from_numpy(wu), dx, out, n_ff, n_cols,
+                            n_tok, act=act, norm_w=DA.from_numpy(w), eps=1e-6, d=dd, x_out=xo)
+    xs, h = oracle_h(oracle, x, d, w, 1e-6, False)
+    assert bits_equal(xo.numpy(), xs)
+    assert bits_equal(dx.numpy(), x)                # x untouched when x_out is separate
+    g = oracle.matmul(t, wg, h, n_ff)
+    u = oracle.matmul(t, wu, h, n_ff)
+    assert rel_to_scale(out.numpy(), oracle.act_mul(ACT[act], g, u)) <= RTOL
+
+
+def exact_rows(oracle, t, mat, n_cols, rows, h):
+    """float64 h @ W[rows]^T over the oracle's dequantised rows."""
+    bv, bb = W.BLOCK[t]
+    rb = n_cols // bv * bb
+    Wd = np.stack([oracle.dequant(t, mat[r * rb:(r + 1) * rb], n_cols) for r in rows])
+    return h.astype(np.float64) @ Wd.astype(np.float64).T
+
+
+def test_llama3_8b_prefill_layer_shapes(hip, oracle):
+    """512 tokens of 4096: q/k/v (4096, 1024, 1024 rows) after add+norm, and
+    gate/up (14336) + SwiGLU. Every output against the unfused GPU passes
+    (add_rmsnorm, the split GEMM, act_mul), and 256 sampled rows of each
+    against the float64 product of the oracle's dequantised weights."""
+    s = W.SHAPES["llama3_8b_prefill"]
+    T, N, F = s.n_tok, s.hidden, s.ffn
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((T, N), dtype=np.float32)
+    d = rng.standard_normal((T, N), dtype=np.float32)
+    w = np.float32(1) + rng.standard_normal(N, dtype=np.float32) * np.float32(0.1)
+    dw = DA.from_numpy(w)
+    xs, h = oracle_h(oracle, x, d, w, s.eps, False)
+    # q/k/v
+    rows = (s.hq * s.head_dim, s.hk * s.head_dim, s.hk * s.head_dim)
+    mats = [weights(W.Q4_K, r, N, rng) for r in rows]
+    dmats = [DA.from_numpy(m) for m in mats]
+    dx, dd = DA.from_numpy(x), DA.from_numpy(d)
+    ys = [DA.empty((T, r)) for r in rows]
+    print("llama3 qkv", flush=True)
+    ops.norm_matmul(W.Q4_K, dmats, dx, ys, list(rows), N, T, norm_w=dw, eps=s.eps, d=dd)
+    assert bits_equal(dx.numpy(), xs)
+    hb = DA.empty((T, N))
+    ops.rmsnorm(DA.from_numpy(xs), dw, hb, T, N, s.eps)
+    for y, dm, m, r in zip(ys, dmats, mats, rows):
+        ref = DA.empty((T, r))
+        ops.matvec(W.Q4_K, dm, hb, ref, r, N, T)
+        got = y.numpy()
+        assert rel_to_scale(got, ref.numpy()) <= RTOL
+        pick = np.sort(rng.choice(r, 256, replace=False))
+        assert rel_to_scale(got[:, pick], exact_rows(oracle, W.Q4_K, m, N, pick, h)) <= RTOL
+    # gate/up + SwiGLU
+    print("llama3 gate/up", flush=True)
+    wg, wu = weights(W.Q4_K, F, N, rng), weights(W.Q4_K, F, N, rng)
+    dg, du = DA.from_numpy(wg), DA.from_numpy(wu)
+    out = DA.empty((T, F))
+    dx2 = DA.from_numpy(x)
+    ops.norm_matmul_gate_up(W.Q4_K, dg, du, dx2, out, F, N, T, act="silu", norm_w=dw,
+                            eps=s.eps, d=dd)
+    assert bits_equal(dx2.numpy(), xs)
+    g, u = DA.empty((T, F)), DA.empty((T, F))
+    ops.matvec(W.Q4_K, dg, hb, g, F, N, T)
+    ops.matvec(W.Q4_K, du, hb, u, F, N, T)
+    ops.act_mul("silu", g, u, g)
+    got = out.numpy()
+    assert rel_to_scale(got, g.numpy()) <= RTOL
+    pick = np.sort(rng.choice(F, 256, replace=False))
+    gx = exact_rows(oracle, W.Q4_K, wg, N, pick, h)
+    ux = exact_rows(oracle, W.Q4_K, wu, N, pick, h)
+    with np.errstate(over="ignore"):          # exp(-g) -> inf: silu(g) -> 0
+        want = (gx / (1.0 + np.exp(-gx))) * ux
+    assert rel_to_scale(got[:, pick], want) <= RTOL
+
+
+def test_norm_matmul_refusals(hip):
+    """Refused on the host before any launch: no or too small a workspace,
+    d without x_out, a misaligned x."""
+    L = _lib.lib()
+    n_tok, n_cols, n_rows = 64, 512, 64
+    need = L.aero_hip_norm_matmul_workspace(W.Q4_K, n_cols, 0, n_tok)
+    assert need > 0
+    x = DA.empty((n_tok, n_cols))
+    y = DA.empty((n_tok, n_rows))
+    m = DA.empty((n_rows * n_cols // 256 * 144,), np.uint8)
+    import ctypes
+    wp = (ctypes.c_void_p * 1)(m.ptr)
+    wb = (ctypes.c_int64 * 1)(m.nbytes)
+    nr = (ctypes.c_int64 * 1)(n_rows)
+    yp = (ctypes.c_void_p * 1)(y.ptr)
+    ws = DA.empty((need,), np.uint8)
+    args = lambda xp, d, xo, wsp, wsb: (W.Q4_K, 1, wp, wb, nr, yp, xp, d, xo, None, 1e-5, 0,  # noqa: E731
+                                        n_cols, n_tok, wsp, wsb, None)
+    assert L.aero_hip_norm_matmul(*args(x.ptr, None, None, None, 0)) == 0
+    assert "workspace" in _lib.last_error()
+    assert L.aero_hip_norm_matmul(*args(x.ptr, None, None, ws.ptr, need - 256)) == 0
+    assert L.aero_hip_norm_matmul(*args(x.ptr, x.ptr, None, ws.ptr, need)) == 0
+    assert L.aero_hip_norm_matmul(*args(x.ptr + 4, None, None, ws.ptr, need)) == 0
+    assert L.aero_hip_norm_matmul(*args(x.ptr, None, None, ws.ptr, need)) == 1
