@@ -1,0 +1,292 @@
+"""A device-resident decoder block: the model-loop counterpart of the fused ops.
+
+One Qwen-style block of the reference (src/model.cpp:234-287, with the
+attention hook of src/attention_layer.cpp:60-240 and the FFN of
+src/model.cpp:166-178) over quantised weights resident in HBM, every
+activation kept on the device:
+
+    x = embed(ids) (* scale)                      src/model.cpp:297-316
+    h = rmsnorm(x, attn_norm)                     :244-245
+    q, k, v = h Wq, h Wk, h Wv                    attention_layer.cpp
+    q, k = qk_norm(q, k); rope(q, k)              :89-156
+    k, v -> KV cache rows kv_len .. kv_len+T-1    :158-200
+    a = attention(q, K, V), causal                :202-225
+    x += a Wo                                     src/model.cpp:279
+    h = rmsnorm(x, ffn_norm)                      :280-282
+    x += (act(h Wg) * (h Wu)) Wd                  :166-178, 284
+    h_out = rmsnorm(x, out_norm)                  :329
+
+Each elementwise site asks aero_amd.select whether its op runs on the GPU
+(AERO_GPU_OPS; unset means every op, for this device-resident loop) and which
+fusions apply (AERO_GPU_FUSE; unset means all): the gather with the first
+norm (embed_norm), norms and residual adds folded into the projections that
+consume them (norm_gemm), the act-mul folded into the gate/up projection
+(act_gemm). An op off the GPU runs the caller's host hook for it, as the
+reference's model loop keeps its own code for the ops it does not hand to a
+library; with no hook the block raises select.HostPathRequired, since the
+library has no CPU path. With every op on the GPU, `forward` can be recorded
+as a Plan and replayed with one call a step.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import ops, select
+from . import workloads as W
+from .device import DeviceArray as DA, Stream
+
+_SPLIT_TYPES = (W.Q4_K, W.Q5_K)
+
+
+@dataclass(frozen=True)
+class BlockConfig:
+    hidden: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    ffn: int
+    eps: float
+    theta: float
+    n_rot: int
+    act: str            # "silu" | "gelu" | "gelu_tanh"
+    wtype: int          # projection weights' ggml type
+    emb_type: int
+    vocab: int
+    qk_norm: bool = False
+    unit_offset: bool = False
+    emb_scale: bool = False
+
+    @classmethod
+    def from_shape(cls, s: W.Shape, wtype: int, vocab: int | None = None) -> "BlockConfig":
+        return cls(s.hidden, s.hq, s.hk, s.head_dim, s.ffn, s.eps, s.theta, s.n_rot, s.act,
+                   wtype, s.emb_type, s.vocab if vocab is None else vocab, s.qk_norm,
+                   s.unit_offset, s.emb_scale)
+
+
+class BlockWeights:
+    """Synthetic weights of one block (seeded): quantised projections of
+    trained-like scale (values of rms ~1/sqrt(columns)), the embedding table,
+    fp32 norm weights; kept on the host (`host`) and in HBM."""
+
+    MATS = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
+
+    def __init__(self, cfg: BlockConfig, seed: int = 0):
+        rng = np.random.default_rng(seed)
+        N, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
+        HD, KD = cfg.n_head * D, cfg.n_head_kv * D
+        bv = W.BLOCK[cfg.wtype][0]
+        shapes = {"wq": (HD, N), "wk": (KD, N), "wv": (KD, N), "wo": (N, HD), "wg": (F, N),
+                  "wu": (F, N), "wd": (N, F)}
+        h = {}
+        for name in self.MATS:
+            r, c = shapes[name]
+            if c % bv:
+                raise ValueError(f"{name}: {c} columns are not whole {bv}-value blocks")
+            h[name] = W.weight_table(cfg.wtype, r, c, rng)
+        self.shapes = shapes
+        h["emb"] = W.make_table(cfg.emb_type, cfg.vocab * (N // W.BLOCK[cfg.emb_type][0]), rng)
+
+        def norm_w(n):
+            w = rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)
+            return w if cfg.unit_offset else (np.float32(1) + w).astype(np.float32)
+
+        for name in ("attn_norm", "ffn_norm", "out_norm"):
+            h[name] = norm_w(N)
+        if cfg.qk_norm:
+            h["q_norm"], h["k_norm"] = norm_w(D), norm_w(D)
+        self.host = h
+        self.dev = {k: DA.from_numpy(v) for k, v in h.items()}
+
+
+class LayerStep:
+    """Embedding, one block and the output norm over device buffers sized for
+    `max_tokens` tokens a step and a KV cache of `kv_cap` positions (fp32).
+
+        step = LayerStep(cfg, BlockWeights(cfg), max_tokens=512, kv_cap=4096)
+        step.prepare(ids, kv_len)          # token ids and positions to HBM
+        step.forward(len(ids), kv_len)     # or record it: with plan: ...
+        x, h_out = step.x, step.h_out      # [T, hidden] each, in HBM
+    """
+
+    def __init__(self, cfg: BlockConfig, weights: BlockWeights, max_tokens: int,
+                 kv_cap: int, gpu_ops: dict | None = None, fusions: dict | None = None,
+                 hooks: dict | None = None):
+        self.cfg, self.w = cfg, weights
+        self.gpu_ops, self.fusions, self.hooks = gpu_ops or {}, fusions or {}, hooks or {}
+        N, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
+        T = max_tokens
+        self.max_tokens, self.kv_cap = T, kv_cap
+        HD, KD = cfg.n_head * D, cfg.n_head_kv * D
+        self.x, self.h, self.h_out = DA.empty((T, N)), DA.empty((T, N)), DA.empty((T, N))
+        self.q, self.att = DA.empty((T, HD)), DA.empty((T, HD))
+        self.o, self.dn = DA.empty((T, N)), DA.empty((T, N))
+        self.g, self.u = DA.empty((T, F)), DA.empty((T, F))
+        self.ids, self.pos = DA.empty((T,), np.int32), DA.empty((T,), np.int32)
+        self.K, self.V = DA.empty((kv_cap, KD)), DA.empty((kv_cap, KD))
+        n_rot, inv = ops.rope_inv_freq(D, cfg.n_rot, cfg.theta)
+        self.n_rot, self.inv = n_rot, DA.from_numpy(inv)
+        self.scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
+        rb = (N // W.BLOCK[cfg.wtype][0]) * W.BLOCK[cfg.wtype][1]
+        self.rows16 = rb % 16 == 0        # rows fit the fused decode GEMVs
+
+    # ------------------------------------------------------------ selection
+    def gpu(self, op: str) -> bool:
+        if select.enabled(op, self.gpu_ops.get(op), default=True):
+            return True
+        if op in self.hooks:
+            return False
+        raise select.HostPathRequired(
+            f"op {op!r} is off the GPU ({select.ENV}) and no host hook was given for it")
+
+    def fuse(self, name: str) -> bool:
+        return select.fusion_enabled(name, self.fusions.get(name))
+
+    def uses_host(self) -> bool:
+        """True when some op runs a host hook (the step then cannot be recorded)."""
+        return any(not self.gpu(op) for op in ("embed", "rmsnorm", "rope", "act") +
+                   (("qk_norm",) if self.cfg.qk_norm else ()))
+
+    # ------------------------------------------------------------ host side
+    def prepare(self, ids, kv_len: int, positions=None) -> None:
+        """Token ids and their positions (default kv_len ..) to HBM."""
+        ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
+        T = ids.size
+        if not 0 < T <= self.max_tokens or kv_len < 0 or kv_len + T > self.kv_cap:
+            raise ValueError(f"{T} tokens at kv_len {kv_len}: outside max_tokens "
+                             f"{self.max_tokens} / kv_cap {self.kv_cap}")
+        pos = (np.arange(kv_len, kv_len + T, dtype=np.int32) if positions is None
+               else np.ascontiguousarray(positions, np.int32).reshape(-1))
+        self.ids.view((T,)).copy_from(ids)
+        self.pos.view((T,)).copy_from(pos)
+
+    def _host(self, a: DA, shape):
+        return a.view(shape).numpy()
+
+    def _put(self, a: DA, v) -> None:
+        a.view(np.shape(v)).copy_from(np.ascontiguousarray(v, np.float32))
+
+    # ------------------------------------------------------------ the block
+    def forward(self, T: int, kv_len: int, stream: Stream | None = None) -> None:
+        c, d = self.cfg, self.w.dev
+        N, H, HK, D, F = c.hidden, c.n_head, c.n_head_kv, c.head_dim, c.ffn
+        if not 0 < T <= self.max_tokens or kv_len + T > self.kv_cap:
+            raise ValueError("forward: tokens or KV span outside the buffers")
+        s = stream
+        x, h = self.x.view((T, N)), self.h.view((T, N))
+        kv0 = kv_len * HK * D * 4
+        kq = self.K.view((T, HK * D), offset_bytes=kv0)
+        vq = self.V.view((T, HK * D), offset_bytes=kv0)
+        q = self.q.view((T, H * D))
+
+        # embedding (+ the attention norm when the projections need h)
+        fold_a = self._folds_norm(T, None)
+        h_ready = False
+        if self.gpu("embed"):
+            if not fold_a and self.fuse("embed_norm") and self.gpu("rmsnorm"):
+                ops.embed_rmsnorm(c.emb_type, d["emb"], c.vocab, N, self.ids, x, h,
+                                  d["attn_norm"], c.eps, scale=self.scale,
+                                  unit_offset=c.unit_offset, n_ids=T, stream=s)
+                h_ready = True
+            else:
+                ops.embed_gather(c.emb_type, d["emb"], c.vocab, N, self.ids, x,
+                                 scale=self.scale, n_ids=T, stream=s)
+        else:
+            self._put(x, self.hooks["embed"](self._host(self.ids, (T,))))
+
+        # q, k, v (k and v straight into the cache rows of these positions)
+        self._project(x, None, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
+                      [H * D, HK * D, HK * D], T, h_ready, s)
+
+        # per-head norms and RoPE, in place (the cache rows of k included)
+        if self.gpu("rope") and (not c.qk_norm or self.gpu("qk_norm")):
+            ops.qk_norm_rope(q, H, T, D, self.n_rot, k=kq, n_k_heads=HK,
+                             q_norm_w=d.get("q_norm"), k_norm_w=d.get("k_norm"), eps=c.eps,
+                             unit_offset=c.unit_offset, pos=self.pos, inv_freq=self.inv,
+                             stream=s)
+        else:
+            qh, kh = self.hooks["rope"](self._host(q, (T, H, D)), self._host(kq, (T, HK, D)),
+                                        self._host(self.pos, (T,)))
+            self._put(q, qh)
+            self._put(kq, kh)
+
+        # causal attention over the cache, then the output projection
+        att = self.att.view((T, H * D))
+        ops.attention(q, self.K, self.V, att, T, H, HK, D, D, kv_len + T, 1.0 / math.sqrt(D),
+                      qpos=self.pos, stream=s)
+        o = self.o.view((T, N))
+        ops.matvec(c.wtype, d["wo"], att, o, N, H * D, T, stream=s)
+
+        # x += o; h = rmsnorm(x); g = act(h Wg) * (h Wu)
+        g = self.g.view((T, F))
+        if self._folds_norm(T, o) and self.fuse("act_gemm") and self.gpu("act"):
+            ops.norm_matmul_gate_up(c.wtype, d["wg"], d["wu"], x, g, F, N, T, act=c.act,
+                                    norm_w=d["ffn_norm"], eps=c.eps, unit_offset=c.unit_offset,
+                                    d=o, stream=s)
+        else:
+            self._norm(x, o, "ffn_norm", h, T, s)
+            if self.gpu("act") and self.fuse("act_gemm") and T < 32 and self.rows16:
+                ops.norm_gate_up(c.wtype, d["wg"], d["wu"], h, g, F, N, T, act=c.act,
+                                 norm=False, stream=s)
+            else:
+                u = self.u.view((T, F))
+                ops.matvec(c.wtype, d["wg"], h, g, F, N, T, stream=s)
+                ops.matvec(c.wtype, d["wu"], h, u, F, N, T, stream=s)
+                if self.gpu("act"):
+                    ops.act_mul(c.act, g, u, g, stream=s)
+                else:
+                    self._put(g, self.hooks["act"](self._host(g, (T, F)), self._host(u, (T, F))))
+
+        # down projection; x += down and the output norm
+        dn = self.dn.view((T, N))
+        ops.matvec(c.wtype, d["wd"], g, dn, N, F, T, stream=s)
+        self._norm(x, dn, "out_norm", self.h_out.view((T, N)), T, s)
+
+    def _folds_norm(self, T: int, resid) -> bool:
+        """True when the norm (and residual add) before a projection folds into
+        it: the split GEMM's pre-pass at 32+ tokens, or (no residual) the fused
+        decode GEMV below that."""
+        if not (self.fuse("norm_gemm") and self.gpu("rmsnorm")):
+            return False
+        if T >= 32:
+            return self.cfg.wtype in _SPLIT_TYPES
+        return resid is None and self.rows16
+
+    def _norm(self, x, resid, wname, h, T, s) -> None:
+        """x += resid (when given); h = rmsnorm(x) * the norm weight `wname`."""
+        c = self.cfg
+        w = self.w.dev[wname]
+        if self.gpu("rmsnorm"):
+            if resid is not None:
+                ops.add_rmsnorm(x, resid, w, h, T, c.hidden, c.eps, c.unit_offset, stream=s)
+            else:
+                ops.rmsnorm(x, w, h, T, c.hidden, c.eps, c.unit_offset, stream=s)
+            return
+        xn, hn = self.hooks["rmsnorm"](self._host(x, (T, c.hidden)),
+                                       None if resid is None else self._host(resid, (T, c.hidden)),
+                                       self.w.host[wname], c.eps, c.unit_offset)
+        self._put(x, xn)
+        self._put(h, hn)
+
+    def _project(self, x, resid, wname, mats, ys, rows, T, h_ready, s) -> None:
+        """ys[m] = rmsnorm(x (+ resid)) W_m^T, the norm folded when it can be."""
+        c = self.cfg
+        norm_w = self.w.dev[wname]
+        if not h_ready and self._folds_norm(T, resid):
+            if T >= 32:
+                ops.norm_matmul(c.wtype, mats, x, ys, rows, c.hidden, T, norm_w=norm_w,
+                                eps=c.eps, unit_offset=c.unit_offset, d=resid, stream=s)
+            else:
+                ops.norm_matvec(c.wtype, mats, x, ys, rows, c.hidden, T, norm_w=norm_w,
+                                eps=c.eps, unit_offset=c.unit_offset, stream=s)
+            return
+        h = self.h.view((T, c.hidden))
+        if not h_ready:
+            self._norm(x, resid, wname, h, T, s)
+        if self.fuse("norm_gemm") and T < 32 and self.rows16 and len(mats) <= 3:
+            ops.norm_matvec(c.wtype, mats, h, ys, rows, c.hidden, T, norm=False, stream=s)
+        else:
+            for m, y, r in zip(mats, ys, rows):
+                ops.matvec(c.wtype, m, h, y, r, c.hidden, T, stream=s)

@@ -22,31 +22,59 @@ import os
 OPS = ("rmsnorm", "qk_norm", "gated_norm", "rope", "act", "embed", "dequant")
 ENV = "AERO_GPU_OPS"
 
+# Fusions a device-resident loop may use when every op they join is on the
+# GPU: the embedding gather with the first norm, the norms (and residual
+# adds) folded into the projections that consume them, the act-mul folded
+# into the gate/up projection. AERO_GPU_FUSE=none turns them off (the same
+# ops then run as separate kernels); unset means all on.
+FUSIONS = ("embed_norm", "norm_gemm", "act_gemm")
+FUSE_ENV = "AERO_GPU_FUSE"
 
-def parse(spec: str | None) -> frozenset:
+
+class HostPathRequired(RuntimeError):
+    """An op is off the GPU (AERO_GPU_OPS) and the caller gave no host code
+    for it: a device-resident loop has no CPU path of its own."""
+
+
+def parse(spec: str | None, names: tuple = OPS, env: str = ENV) -> frozenset:
     if spec is None:
         return frozenset()
     spec = spec.strip().lower()
     if spec in ("", "none", "0", "off"):
         return frozenset()
     if spec in ("all", "1", "on"):
-        return frozenset(OPS)
-    names = {s.strip() for s in spec.split(",") if s.strip()}
-    unknown = names - set(OPS)
+        return frozenset(names)
+    got = {s.strip() for s in spec.split(",") if s.strip()}
+    unknown = got - set(names)
     if unknown:
-        raise ValueError(f"{ENV}: unknown op(s) {sorted(unknown)}; choose from {OPS}")
-    return frozenset(names)
+        raise ValueError(f"{env}: unknown name(s) {sorted(unknown)}; choose from {names}")
+    return frozenset(got)
 
 
 def enabled_ops() -> frozenset:
     return parse(os.environ.get(ENV))
 
 
-def enabled(op: str, override: bool | None = None) -> bool:
+def enabled(op: str, override: bool | None = None, default: bool = False) -> bool:
     """True when `op` should run on the GPU: the call-site override if given,
-    else AERO_GPU_OPS."""
+    else AERO_GPU_OPS, else `default` when AERO_GPU_OPS is unset."""
     if op not in OPS:
         raise ValueError(f"unknown op {op!r}; choose from {OPS}")
     if override is not None:
         return bool(override)
+    if os.environ.get(ENV) is None:
+        return bool(default)
     return op in enabled_ops()
+
+
+def fusion_enabled(name: str, override: bool | None = None) -> bool:
+    """True when fusion `name` may be used: the override if given, else
+    AERO_GPU_FUSE (unset: every fusion)."""
+    if name not in FUSIONS:
+        raise ValueError(f"unknown fusion {name!r}; choose from {FUSIONS}")
+    if override is not None:
+        return bool(override)
+    spec = os.environ.get(FUSE_ENV)
+    if spec is None:
+        return True
+    return name in parse(spec, FUSIONS, FUSE_ENV)

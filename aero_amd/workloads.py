@@ -170,39 +170,59 @@ def _f16_bytes(v: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(-1, 2)
 
 
-def make_table(t: int, n_blocks: int, rng) -> np.ndarray:
-    """n_blocks GGML blocks of type t as a flat uint8 array."""
+# Root mean square of a dequantised value per unit of the random block scale
+# (d, and dmin alike) make_table draws, from the distributions below: Q8_0
+# rms(q) over U{-127..127}; the K-quants rms(sc*q) with 6-bit sc and 4-, 5-
+# or 6-bit q (the min term is an order of magnitude smaller); IQ4_XS the
+# codebook times its 6-bit signed scales. Used to draw weights of a chosen
+# scale (weight_table).
+_RMS_PER_D = {Q8_0: 73.3 * 0.02 / 127, Q4_K: 323.0 * 0.01, Q5_K: 659.0 * 0.01,
+              Q6_K: 1365.0 * 0.01, IQ4_XS: 1080.0 * 0.001}
+
+
+def weight_table(t: int, n_rows: int, n_cols: int, rng) -> np.ndarray:
+    """A synthetic weight matrix of type t whose values have an rms of about
+    1/sqrt(n_cols), as trained projections do, so that activations stay of
+    unit scale through a block (attention scores of order one)."""
+    return make_table(t, n_rows * n_cols // BLOCK[t][0], rng,
+                      d_scale=1.0 / (_RMS_PER_D[t] * math.sqrt(n_cols)))
+
+
+def make_table(t: int, n_blocks: int, rng, d_scale: float = 1.0) -> np.ndarray:
+    """n_blocks GGML blocks of type t as a flat uint8 array (block scales
+    drawn as below, times d_scale)."""
     bv, bb = BLOCK[t]
+    ds = np.float32(d_scale)
     if t == Q8_0:
         # int8 quants U{-127..127}; d = fp16(|N(0, 0.02)| / 127)
         blk = np.empty((n_blocks, bb), dtype=np.uint8)
         q = rng.integers(-127, 128, size=(n_blocks, 32), dtype=np.int8)
-        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.02)) / np.float32(127)
+        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.02)) / np.float32(127) * ds
         blk[:, 0:2] = _f16_bytes(d)
         blk[:, 2:] = q.view(np.uint8)
         return blk.reshape(-1)
     if t == Q4_K:
         # every byte random, then d, dmin = fp16(|N(0, 0.01)|)
         blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
-        dd = np.abs(rng.standard_normal((n_blocks, 2), dtype=np.float32) * np.float32(0.01))
+        dd = np.abs(rng.standard_normal((n_blocks, 2), dtype=np.float32) * np.float32(0.01)) * ds
         blk[:, 0:4] = np.ascontiguousarray(dd.astype(np.float16)).view(np.uint8).reshape(-1, 4)
         return blk.reshape(-1)
     if t == Q6_K:
         # ql/qh random bytes, int8 scales U{-128..127}, d = fp16(|N(0, 0.01)|)
         blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
-        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.01))
+        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.01)) * ds
         blk[:, 208:210] = _f16_bytes(d)
         return blk.reshape(-1)
     if t == Q5_K:
         # as Q4_K: random bytes (scales, qh, qs), d, dmin = fp16(|N(0, 0.01)|)
         blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
-        dd = np.abs(rng.standard_normal((n_blocks, 2), dtype=np.float32) * np.float32(0.01))
+        dd = np.abs(rng.standard_normal((n_blocks, 2), dtype=np.float32) * np.float32(0.01)) * ds
         blk[:, 0:4] = np.ascontiguousarray(dd.astype(np.float16)).view(np.uint8).reshape(-1, 4)
         return blk.reshape(-1)
     if t == IQ4_XS:
         # random scale and quant bytes, d = fp16(|N(0, 0.001)|) (x codebook up to 127)
         blk = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
-        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.001))
+        d = np.abs(rng.standard_normal(n_blocks, dtype=np.float32) * np.float32(0.001)) * ds
         blk[:, 0:2] = _f16_bytes(d)
         return blk.reshape(-1)
     raise ValueError(t)

@@ -38,6 +38,7 @@ dequant over the same rows beside it.
     python bench.py --gemm              # quantised GEMM (prefill projections)
     python bench.py --fused             # fused decode GEMVs vs the launches they replace
     python bench.py --layer-gemm        # prefill add+norm folded into the GEMMs vs unfused
+    python bench.py --layer             # one decoder block, all fusions on / off
     python bench.py --attention         # attention over a KV cache (decode, prefill)
     python bench.py --gguf              # GGUF parse, upload to HBM, device row addressing
     python bench.py --ssm               # gated DeltaNet scan and conv
@@ -97,6 +98,8 @@ def parse_args(argv=None):
                    help="attention over a KV cache (decode and causal prefill)")
     p.add_argument("--fused", action="store_true",
                    help="fused decode GEMVs (norm + q/k/v, norm + gate/up + act) vs separate")
+    p.add_argument("--layer", action="store_true",
+                   help="one decoder block, fused and unfused (decode and 512-token prefill)")
     p.add_argument("--layer-gemm", action="store_true",
                    help="norm -> projections, unfused vs folded into the GEMM (512 tokens)")
     p.add_argument("--gemm", action="store_true",
@@ -599,6 +602,8 @@ def main(argv=None):
         return gemm(a)
     if a.layer_gemm:
         return layer_gemm(a)
+    if a.layer:
+        return layer_bench(a)
     if a.fused:
         return fused(a)
     if a.attention:
@@ -1012,6 +1017,70 @@ def layer_gemm(a):
                       "ffn_speedup": round(res["ffn_unfused"] / res["ffn_fused"], 3),
                       "saved_us": round(res["attn_unfused"] - res["attn_fused"] +
                                         res["ffn_unfused"] - res["ffn_fused"], 2)}), flush=True)
+    return 0
+
+
+LAYER_CASES = [
+    # (shape, weight type, tokens, earlier cache positions)
+    ("qwen2_0p5b_decode", 8, 1, 37),
+    ("llama3_8b_prefill", 12, 512, 0),
+]
+
+
+def layer_bench(a):
+    """One decoder block (aero_amd.layer.LayerStep: embedding, q/k/v, QK-norm +
+    RoPE, attention, o, residual + norm, gate/up + act, down, output norm)
+    at the Qwen2-0.5B decode and Llama-3-8B 512-token prefill shapes, with
+    every fusion on and with every fusion off. Four blocks with their own
+    weights (rotated, so weights come from HBM as in a deep model), each
+    recorded as a plan; µs per block = region / blocks run, between one
+    event pair on the stream."""
+    from aero_amd import layer, select, workloads as W
+    from aero_amd.device import Event, Plan, Stream
+
+    names = a.shapes.split(",") if a.shapes else [c[0] for c in LAYER_CASES]
+    for shape, wtype, T, kv_len in LAYER_CASES:
+        if shape not in names:
+            continue
+        cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype)
+        weights = [layer.BlockWeights(cfg, seed=i) for i in range(4)]
+        rng = np.random.default_rng(5)
+        ids = rng.integers(0, cfg.vocab, T).astype(np.int32)
+        res = {}
+        for mode in ("fused", "unfused"):
+            fus = None if mode == "fused" else {f: False for f in select.FUSIONS}
+            steps = [layer.LayerStep(cfg, w, T, kv_len + T, fusions=fus) for w in weights]
+            plans = []
+            for st in steps:
+                st.prepare(ids, kv_len)
+                p = Plan()
+                with p:
+                    st.forward(T, kv_len)
+                plans.append(p)
+            stream = Stream()
+            for p in plans:
+                p.launch(stream)
+            reps = max(3, a.steps // 10)
+            e0, e1 = Event(), Event()
+            e0.record(stream)
+            for _ in range(reps):
+                for p in plans:
+                    p.launch(stream)
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / (reps * len(plans))
+            res[mode] = us
+            print(json.dumps({"layer": shape, "mode": mode, "weight_type": wtype,
+                              "tokens": T, "kv_len": kv_len, "us_per_block": round(us, 2),
+                              "launches": len(plans[0]),
+                              "tokens_per_s_per_block": round(T / (us * 1e-6), 1)}),
+                  flush=True)
+            for p in plans:
+                p.destroy()
+            stream.destroy()
+            del steps
+        print(json.dumps({"layer": shape, "fused_speedup": round(res["unfused"] / res["fused"],
+                                                                 3)}), flush=True)
     return 0
 
 

@@ -223,11 +223,30 @@ def test_per_op_selector(monkeypatch):
     assert not any(select.enabled(op) for op in select.OPS)
     monkeypatch.delenv("AERO_GPU_OPS")
     assert not select.enabled("embed")
+    assert select.enabled("embed", default=True)        # a device-resident loop's default
+    monkeypatch.setenv("AERO_GPU_OPS", "none")
+    assert not select.enabled("embed", default=True)    # an explicit setting wins
     monkeypatch.setenv("AERO_GPU_OPS", "rmsnrom")
     with pytest.raises(ValueError):
         select.enabled("rmsnorm")
     with pytest.raises(ValueError):
         select.enabled("softmax")
+
+
+def test_fusion_selector(monkeypatch):
+    from aero_amd import select
+    monkeypatch.delenv("AERO_GPU_FUSE", raising=False)
+    assert all(select.fusion_enabled(f) for f in select.FUSIONS)
+    monkeypatch.setenv("AERO_GPU_FUSE", "none")
+    assert not any(select.fusion_enabled(f) for f in select.FUSIONS)
+    assert select.fusion_enabled("act_gemm", override=True)
+    monkeypatch.setenv("AERO_GPU_FUSE", "norm_gemm")
+    assert select.fusion_enabled("norm_gemm") and not select.fusion_enabled("embed_norm")
+    monkeypatch.setenv("AERO_GPU_FUSE", "norm_gem")
+    with pytest.raises(ValueError):
+        select.fusion_enabled("norm_gemm")
+    with pytest.raises(ValueError):
+        select.fusion_enabled("softmax")
 
 
 def test_native_ssm_fallback_contract():

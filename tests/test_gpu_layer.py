@@ -1,0 +1,153 @@
+"""GPU parity: the device-resident block (aero_amd.layer.LayerStep) against the
+oracle's composition of the same block (src/model.cpp:234-287,297-316,329 with
+the attention hook of src/attention_layer.cpp:89-225): the oracle's embedding
+gather, rmsnorm_rows, qk_norm_rope, attention_tiled and act_mul, and float64
+products over the oracle's dequantised weights for the projections (the
+oracle's matmul equals that product to ~1e-6 of scale, tests/test_gpu_gemm16.py).
+
+Checked at the Qwen2-0.5B decode shape (one token at position 37 over a
+cache of 37 earlier positions; Q8_0 weights, whose 896-value rows take the
+separate-launch paths) and the Llama-3-8B 512-token prefill (Q4_K weights:
+the split GEMM with the norms folded), with every fusion on and with every
+fusion off, and with host hooks standing in for ops taken off the GPU.
+Tolerance 1e-5 of each output's scale; x is the residual stream after the
+block, h_out its output norm.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import RTOL, rel_to_scale
+from aero_amd import layer, select
+from aero_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+ACT = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
+
+CASES = {
+    # name: (shape, weight type, vocab, tokens, earlier cache positions)
+    "qwen2_0p5b_decode": ("qwen2_0p5b_decode", W.Q8_0, 4096, 1, 37),
+    "llama3_8b_prefill": ("llama3_8b_prefill", W.Q4_K, 4096, 512, 0),
+    "gemma_like_prefill": ("gemma3_4b_prefill", W.Q4_K, 2048, 64, 0),
+}
+
+
+def dq(oracle, t, raw, rows, cols):
+    return oracle.dequant(t, raw, rows * cols).reshape(rows, cols).astype(np.float64)
+
+
+def oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0):
+    h_ = wts.host
+    N, H, HK, D = cfg.hidden, cfg.n_head, cfg.n_head_kv, cfg.head_dim
+    T = ids.size
+    pos = np.arange(kv_len, kv_len + T, dtype=np.int32)
+    mats = {k: dq(oracle, cfg.wtype, h_[k], *wts.shapes[k]) for k in wts.MATS}
+
+    def mm(name, a):
+        return (a.astype(np.float64) @ mats[name].T).astype(np.float32)
+
+    scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
+    x = oracle.embed_gather(cfg.emb_type, h_["emb"], cfg.vocab, N, ids, scale)
+    h = oracle.rmsnorm_rows(x, h_["attn_norm"], cfg.eps, cfg.unit_offset)
+    q, k, v = mm("wq", h), mm("wk", h), mm("wv", h)
+    q = oracle.qk_norm_rope(q, T, H, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("q_norm"), cfg.eps,
+                            cfg.unit_offset)
+    k = oracle.qk_norm_rope(k, T, HK, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("k_norm"), cfg.eps,
+                            cfg.unit_offset)
+    Kc = np.concatenate([K0[:kv_len], k.reshape(T, HK * D)]).reshape(-1, HK, D)
+    Vc = np.concatenate([V0[:kv_len], v.reshape(T, HK * D)]).reshape(-1, HK, D)
+    att = oracle.attention_tiled(q.reshape(T, H, D), Kc, Vc, 1.0 / math.sqrt(D), qpos=pos,
+                                 kpos=np.arange(kv_len + T, dtype=np.int32))
+    x = x + mm("wo", att.reshape(T, H * D))
+    h = oracle.rmsnorm_rows(x, h_["ffn_norm"], cfg.eps, cfg.unit_offset)
+    g = oracle.act_mul(ACT[cfg.act], mm("wg", h), mm("wu", h))
+    x = x + mm("wd", g)
+    return x, oracle.rmsnorm_rows(x, h_["out_norm"], cfg.eps, cfg.unit_offset)
+
+
+def setup(name, seed=0, **kw):
+    shape, wtype, vocab, T, kv_len = CASES[name]
+    cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype, vocab=vocab)
+    wts = layer.BlockWeights(cfg, seed=seed)
+    step = layer.LayerStep(cfg, wts, max_tokens=T, kv_cap=kv_len + T, **kw)
+    rng = np.random.default_rng(seed + 1)
+    ids = rng.integers(0, vocab, T).astype(np.int32)
+    KD = cfg.n_head_kv * cfg.head_dim
+    K0 = rng.standard_normal((kv_len + T, KD), dtype=np.float32)
+    V0 = rng.standard_normal((kv_len + T, KD), dtype=np.float32)
+    step.K.copy_from(K0)
+    step.V.copy_from(V0)
+    return cfg, wts, step, ids, kv_len, K0, V0
+
+
+def run_and_check(oracle, name, **kw):
+    cfg, wts, step, ids, kv_len, K0, V0 = setup(name, **kw)
+    T = ids.size
+    print(f"layer {name} tokens={T} kv_len={kv_len} wtype={cfg.wtype} {kw}", flush=True)
+    step.prepare(ids, kv_len)
+    step.forward(T, kv_len)
+    want_x, want_h = oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0)
+    got_x = step.x.view((T, cfg.hidden)).numpy()
+    got_h = step.h_out.view((T, cfg.hidden)).numpy()
+    ex, eh = rel_to_scale(got_x, want_x), rel_to_scale(got_h, want_h)
+    print(f"  rel x {ex:.2e} h_out {eh:.2e}", flush=True)
+    assert ex <= RTOL and eh <= RTOL
+    return step
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("fused", [True, False])
+def test_layer_vs_oracle(hip, oracle, name, fused):
+    fus = None if fused else {f: False for f in select.FUSIONS}
+    run_and_check(oracle, name, fusions=fus)
+
+
+def test_layer_plan_replay(hip, oracle):
+    """The step recorded as a plan and replayed twice gives the eager result
+    (the second replay starts from the first one's residual stream, so x is
+    reset between them)."""
+    from aero_amd.device import Plan, Stream, synchronize
+
+    cfg, wts, step, ids, kv_len, K0, V0 = setup("llama3_8b_prefill")
+    T = ids.size
+    step.prepare(ids, kv_len)
+    plan = Plan()
+    with plan:
+        step.forward(T, kv_len)
+    want_x, want_h = oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0)
+    stream = Stream()
+    for _ in range(2):
+        plan.launch(stream)
+        stream.synchronize()
+        synchronize()
+        assert rel_to_scale(step.h_out.view((T, cfg.hidden)).numpy(), want_h) <= RTOL
+        assert rel_to_scale(step.x.view((T, cfg.hidden)).numpy(), want_x) <= RTOL
+    plan.destroy()
+    stream.destroy()
+
+
+def test_layer_host_hooks(hip, oracle):
+    """rope and act taken off the GPU: the caller's host code (here the
+    oracle's) runs at those sites, the rest stays on the GPU."""
+    cfg = layer.BlockConfig.from_shape(W.SHAPES["qwen2_0p5b_decode"], W.Q8_0, vocab=4096)
+
+    def rope(q, k, pos):
+        T, H, D = q.shape
+        qo = oracle.qk_norm_rope(q, T, H, D, cfg.n_rot, pos, cfg.theta)
+        ko = oracle.qk_norm_rope(k, T, k.shape[1], D, cfg.n_rot, pos, cfg.theta)
+        return qo, ko
+
+    def act(g, u):
+        return oracle.act_mul(ACT[cfg.act], g, u)
+
+    run_and_check(oracle, "qwen2_0p5b_decode", gpu_ops={"rope": False, "act": False},
+                  hooks={"rope": rope, "act": act})
+
+
+def test_layer_refuses_without_host_path(hip):
+    cfg, wts, step, ids, kv_len, _, _ = setup("qwen2_0p5b_decode", gpu_ops={"rmsnorm": False})
+    step.prepare(ids, kv_len)
+    with pytest.raises(select.HostPathRequired):
+        step.forward(ids.size, kv_len)

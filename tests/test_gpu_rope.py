@@ -83,15 +83,17 @@ def test_rope_layer_shapes_table(hip, oracle, name):
     cos, sin = oracle.rope_tables(s.head_dim, np.arange(s.rope_table, dtype=np.int32), s.theta)
     print(f"rope-table {name} q{d['q'].shape} table {cos.shape}", flush=True)
     gq, gk = gpu_rope(d["q"], d["pos"], s.head_dim, s.n_rot, k=d["k"], table=(cos, sin))
-    rows = slice(0, min(s.n_tok, 2048))  # the oracle checks the first 2048 tokens
-    wq = oracle_rope(oracle, d["q"][rows], d["pos"][rows], s.head_dim, s.n_rot,
-                     table=(cos, sin))
-    wk = oracle_rope(oracle, d["k"][rows], d["pos"][rows], s.head_dim, s.n_rot,
-                     table=(cos, sin))
-    # same table, same operation order: bit-exact
-    assert bits_equal(gq[rows], wq)
-    assert bits_equal(gk[rows], wk)
-    # every token rotated: norm of each head row is preserved
+    # every token against the oracle, in slices of 2048 tokens; same table,
+    # same operation order: bit-exact
+    for t0 in range(0, s.n_tok, 2048):
+        rows = slice(t0, min(s.n_tok, t0 + 2048))
+        wq = oracle_rope(oracle, d["q"][rows], d["pos"][rows], s.head_dim, s.n_rot,
+                         table=(cos, sin))
+        wk = oracle_rope(oracle, d["k"][rows], d["pos"][rows], s.head_dim, s.n_rot,
+                         table=(cos, sin))
+        assert bits_equal(gq[rows], wq), f"q tokens {rows}"
+        assert bits_equal(gk[rows], wk), f"k tokens {rows}"
+    # and every head row's norm is preserved
     nq = np.linalg.norm(gq.astype(np.float64), axis=-1)
     n0 = np.linalg.norm(d["q"].astype(np.float64), axis=-1)
     assert np.abs(nq - n0).max() / n0.max() < 1e-5
