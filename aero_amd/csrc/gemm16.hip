@@ -1,4 +1,4 @@
-// Quantised GEMM on the fp16 matrix cores with x split into three fp16 parts
+// Quantised GEMM on the fp16 matrix cores with x split into fp16 parts
 // (prefill): y[t, r] = sum_c W[r, c] * x[t, c], W in Q4_K / Q5_K blocks, x and
 // y fp32 — the reference's matmul (src/kernels.cpp:520-538) over its block
 // dots (:78-250), at fp32-grade accuracy on the fp16 matrix rate.
@@ -10,12 +10,17 @@
 // with S_g the sum of x over sub-block g. Each token's x is scaled, per
 // super-block, by a power of two 2^(15-e) (e the exponent of the block's
 // largest finite |x|, so the scaled values lie below 2^15) and split into
-// three fp16 parts hi + mid + lo: every value of at least 2^-16 of the
-// block's largest is represented exactly, smaller ones to 2^-25 absolute in
-// the scaled units (2^-39 of the largest). Products of fp16 integers and fp16
-// parts are exact; the matrix cores add them in fp32, and each super-block's
-// sum is scaled back (by 2^(e-15)) as it is added to the row's fp32 total. The reference dequantises each value to fp32 and sums the
-// rounded products serially; results differ from it by fp32 rounding only.
+// two fp16 parts hi + lo: 22 significant bits of each value (relative error
+// at most 2^-22; fp32 holds 24), and values below 2^-3 in the scaled units
+// to 2^-25 absolute (2^-39 of the block's largest). A build with
+// -DAERO_SPLIT_PARTS=3 adds a third part (hi + mid + lo): every value of at
+// least 2^-16 of the block's largest is then exact, for half again the
+// matrix work. Products of fp16 integers and fp16 parts are exact; the
+// matrix cores add them in fp32, and each super-block's sum is scaled back
+// (by 2^(e-15)) as it is added to the row's fp32 total. The reference
+// dequantises each value to fp32 and sums the rounded products serially; on
+// the layer shapes both differ from the exact product by 2-5e-7 of the
+// output's scale (measured), the reference's own fp32 rounding level.
 //
 // Kernels:
 //   xsplit_kernel   one workgroup a 16-token tile and super-block: the scale,
@@ -58,7 +63,11 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));  // 16 bytes, kept in registers
 
-constexpr int kParts = 3;          // fp16 parts of x
+#ifndef AERO_SPLIT_PARTS
+#define AERO_SPLIT_PARTS 2
+#endif
+constexpr int kParts = AERO_SPLIT_PARTS;  // fp16 parts of x (2 or 3)
+static_assert(kParts == 2 || kParts == 3, "x is split into two or three fp16 parts");
 constexpr int kTokTile = 32;       // tokens a workgroup
 constexpr int kChunkSteps = 4;     // 32-column steps a staged chunk
 constexpr int kScaleMax = 15;      // scaled |x| < 2^15
@@ -72,7 +81,7 @@ __device__ __forceinline__ uint32_t as_u32(h2 h) { return __builtin_bit_cast(uin
 // ------------------------------------------------------------ x prepass
 // Parts of one scaled value: hi = fp16(v), mid = fp16(v - hi), lo =
 // fp16(v - hi - mid); both differences are exact in fp32. Non-finite values
-// keep hi = fp16(v) and zero mid / lo.
+// keep hi = fp16(v) and zero mid / lo. The two-part split keeps hi and mid.
 __device__ __forceinline__ void split3(float v, _Float16& hi, _Float16& mid, _Float16& lo) {
     hi = (_Float16)v;
     const float r1 = v - (float)hi;
@@ -86,7 +95,7 @@ __device__ __forceinline__ void split3(float v, _Float16& hi, _Float16& mid, _Fl
 // n_cols/256). For token t of the tile: e = exponent of the largest finite
 // |x| of the super-block (frexp), scale 2^(15-e) (1 when all are zero, and
 // for the padding tokens t >= n_tok), xinv[t][sb] = 2^(e-15);
-// xp[((mt*nK + K)*3 + p)*64 + lane] = 8 fp16 values of part p of the scaled x
+// xp[((mt*nK + K)*kParts + p)*64 + lane] = 8 fp16 values of part p of the scaled x
 // of token 16mt + lane%16 at step K = 8sb + 4h + s, lane group lane/16, in
 // the operand order above; xsum[t][8sb + k] = the sum of the scaled x over
 // sub-block k (fp32, in column order). x is read coalesced into LDS and
@@ -212,7 +221,7 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
             split3(w[i], hi, mid, lo);
             parts[0][i] = hi;
             parts[1][i] = mid;
-            parts[2][i] = lo;
+            if constexpr (kParts == 3) parts[2][i] = lo;
         }
         uint4* dst = xp + ((int64_t)mt * nK + 8 * sb + s8) * (kParts * 64) + l;
 #pragma unroll
@@ -236,17 +245,25 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
 }
 
 // ---------------------------------------------------------- the GEMM
+// Up to kMaxMats matrices of one type and width sharing x (q, k, v) run in
+// one launch: the row tiles of matrix m are workgroups tile0[m] ..
+// tile0[m+1]-1 along x, so small matrices (k, v) fill the GPU together with
+// the large one.
+constexpr int kMaxMats = 4;
+
 struct SplitParams {
-    const uint8_t* w;     // n_rows rows of rb bytes, 16-byte aligned
+    const uint8_t* w[kMaxMats];   // n_rows[m] rows of rb bytes, 16-byte aligned
+    float* y[kMaxMats];           // [n_tok][n_rows[m]]
+    int64_t n_rows[kMaxMats];
+    int tile0[kMaxMats + 1];      // first row tile of each matrix; tile0[n_mat] = all
+    int n_mat;
     const uint4* xp;      // x parts (xsplit_kernel)
     const float* xsum;    // [tok_pad][n_cols/32] sub-block sums of the scaled x
     const float* xinv;    // [tok_pad][n_cols/256] inverse scales a token and super-block
-    float* y;             // [n_tok][n_rows]
-    int64_t n_rows;
     int n_cols;
     int64_t rb;
     int n_tok;
-    const uint8_t* w2;    // gate/up form: the up matrix (w is the gate)
+    const uint8_t* w2;    // gate/up form: the up matrix (w[0] is the gate)
     const float* ssq;     // folded norm: [tok_pad][n_cols/256] sums of x^2, else null
     float eps;
 };
@@ -308,13 +325,14 @@ __device__ __forceinline__ void kq_scale_min_lanes(uint32_t s0, uint32_t s1, uin
 }
 
 // The x parts, sub-block sums and inverse scales of one chunk on their way
-// to LDS: thread tid stages uint4 tid + 256i of the chunk, i < 3 from the
-// first token tile, i >= 3 from the second (each chunk of a token tile is 768
-// contiguous uint4 of xp); threads < 64 float4 tid of the super-block's sums,
+// to LDS: thread tid stages uint4 tid + 256i of the chunk, i < kParts from
+// the first token tile, the rest from the second (each chunk of a token tile
+// is 256 * kParts contiguous uint4 of xp); threads < 64 float4 tid of the
+// super-block's sums,
 // threads 64..95 the inverse scale of token tid - 64.
 struct XStage {
     static constexpr int CSTEP = kChunkSteps * kParts * 64;
-    u4 r[6];
+    u4 r[2 * kParts];
     v4f s;
     float iv;
     const u4* b0;
@@ -336,16 +354,16 @@ struct XStage {
         c = min(c, n_chunks - 1);
         const int64_t o = (int64_t)c * CSTEP;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
+        for (int i = 0; i < kParts; ++i) {
             r[i] = b0[o + 256 * i];
-            r[3 + i] = b1[o + 256 * i];
+            r[kParts + i] = b1[o + 256 * i];
         }
         s = sb[2 * (c >> 1)];
         iv = ib[c >> 1];
     }
     __device__ __forceinline__ void store(u4* xs, v4f* ss, float* si, int tid) const {
 #pragma unroll
-        for (int i = 0; i < 6; ++i) xs[tid + 256 * i] = r[i];
+        for (int i = 0; i < 2 * kParts; ++i) xs[tid + 256 * i] = r[i];
         if (ss != nullptr && tid < 2 * kTokTile) ss[tid] = s;
         if (ss != nullptr && tid >= 2 * kTokTile && tid < 3 * kTokTile) si[tid - 2 * kTokTile] = iv;
     }
@@ -370,7 +388,7 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     constexpr int kRowsWave = GU ? 16 : 16 * NT;
     constexpr int MT = kTokTile / 16;           // matrix tiles over tokens (2)
     constexpr int CHUNK = MT * XStage::CSTEP;   // uint4 a chunk (1536)
-    static_assert(MT == 2 && CHUNK == 6 * 256, "staging split");
+    static_assert(MT == 2 && CHUNK == 2 * kParts * 256, "staging split");
     __shared__ u4 xs[2][CHUNK];                 // 2 x 24 KB, by chunk parity
     __shared__ v4f ss[2][kTokTile * 2];         // sub-block sums, by super-block parity
     __shared__ __align__(16) float si[2][kTokTile];  // inverse scales, by super-block parity
@@ -379,7 +397,15 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = l & 15, g = l >> 4;
-    const int64_t row0 = (int64_t)blockIdx.x * (4 * kRowsWave) + wave * kRowsWave;
+    // this workgroup's matrix and its row tile within it (uniform)
+    int mi = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxMats; ++k) mi += (k < p.n_mat && (int)blockIdx.x >= p.tile0[k]);
+    const uint8_t* const W = p.w[mi];
+    float* const Y = p.y[mi];
+    const int64_t n_rows = p.n_rows[mi];
+    const int64_t row0 = (int64_t)((int)blockIdx.x - p.tile0[mi]) * (4 * kRowsWave) +
+                         wave * kRowsWave;
     const int tt = blockIdx.y;
     const int nK = p.n_cols >> 5;
     const int n_chunks = nK / kChunkSteps, n_sb = n_chunks / 2;
@@ -389,9 +415,9 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     int woff[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        wbase[j] = (GU && j == 1 ? p.w2 : p.w) + row0 * p.rb;
+        wbase[j] = (GU && j == 1 ? p.w2 : W) + row0 * p.rb;
         const int64_t rj = GU ? row0 + r : row0 + 16 * j + r;
-        woff[j] = (int)((min(rj, p.n_rows - 1) - row0) * p.rb);
+        woff[j] = (int)((min(rj, n_rows - 1) - row0) * p.rb);
     }
 
     XStage xst;
@@ -572,7 +598,7 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
             const int tok = kTokTile * tt + tk;
             if (tok >= p.n_tok) continue;
             const float inv = p.ssq != nullptr ? tinv[tk] : 1.0f;
-            float* yp = p.y + (int64_t)tok * p.n_rows;
+            float* yp = Y + (int64_t)tok * n_rows;
             if constexpr (GU) {
                 const int64_t row = row0 + r;
                 float gv = acc[m][0][v], uv = acc[m][1][v];
@@ -580,13 +606,13 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
                     gv = gv * inv;
                     uv = uv * inv;
                 }
-                if (row < p.n_rows) yp[row] = act<GU ? EPI : 0>(gv) * uv;
+                if (row < n_rows) yp[row] = act<GU ? EPI : 0>(gv) * uv;
             } else {
 #pragma unroll
                 for (int j = 0; j < NT; ++j) {
                     const int64_t row = row0 + 16 * j + r;
                     const float y = p.ssq != nullptr ? acc[m][j][v] * inv : acc[m][j][v];
-                    if (row < p.n_rows) yp[row] = y;
+                    if (row < n_rows) yp[row] = y;
                 }
             }
         }
@@ -699,20 +725,36 @@ bool split_run(const SplitJob& j, hipStream_t s) {
         return false;
     }
     auto k = reinterpret_cast<void (*)(SplitParams)>(kp);
-    const int n_launch = gu ? 1 : j.n_mat;
-    for (int m = 0; m < n_launch; ++m) {
-        const int64_t row_tiles = (j.n_rows[m] + rows_wg - 1) / rows_wg;
-        if (row_tiles > 0x7fffffff) {
-            set_error("split GEMM: too many rows (%lld)", (long long)j.n_rows[m]);
+    // one launch for every matrix: row tiles of matrix m follow those of m-1
+    SplitParams p{};
+    const int n_mat = gu ? 1 : j.n_mat;
+    p.n_mat = n_mat;
+    int64_t tiles = 0;
+    for (int m = 0; m < n_mat; ++m) {
+        p.w[m] = j.w[m];
+        p.y[m] = j.y[m];
+        p.n_rows[m] = j.n_rows[m];
+        p.tile0[m] = (int)tiles;
+        tiles += (j.n_rows[m] + rows_wg - 1) / rows_wg;
+        if (tiles > 0x7fffffff) {
+            set_error("split GEMM: too many rows");
             return false;
         }
-        if (row_tiles == 0) continue;
-        SplitParams p{j.w[m], w.xp, w.xsum, w.xinv, j.y[m], j.n_rows[m], (int)j.n_cols, j.rb,
-                      (int)j.n_tok, gu ? j.w_up : nullptr, norm ? w.ssq : nullptr, j.eps};
-        if (!launch("split_gemm_kernel", k, dim3((unsigned)row_tiles, (unsigned)(tp / kTokTile)),
-                    dim3(256), 0, s, p))
-            return false;
     }
+    for (int m = n_mat; m <= kMaxMats; ++m) p.tile0[m] = (int)tiles;
+    if (tiles == 0) return true;
+    p.xp = w.xp;
+    p.xsum = w.xsum;
+    p.xinv = w.xinv;
+    p.n_cols = (int)j.n_cols;
+    p.rb = j.rb;
+    p.n_tok = (int)j.n_tok;
+    p.w2 = gu ? j.w_up : nullptr;
+    p.ssq = norm ? w.ssq : nullptr;
+    p.eps = j.eps;
+    if (!launch("split_gemm_kernel", k, dim3((unsigned)tiles, (unsigned)(tp / kTokTile)),
+                dim3(256), 0, s, p))
+        return false;
     return true;
 }
 

@@ -894,6 +894,14 @@ MFMA_FP32_PEAK_TFLOPS = 157.3
 MFMA_FP16_PEAK_TFLOPS = 2500.0   # dense fp16 matrix peak of MI355X
 
 
+def split_parts():
+    """fp16 parts the library's split GEMM cuts x into (2, or 3 in a build with
+    -DAERO_SPLIT_PARTS=3), read off its workspace size for 32 tokens of 256
+    columns: 32*256*2 bytes a part plus 1280 bytes of sums and scales."""
+    from aero_amd import _lib
+    return (int(_lib.lib().aero_hip_matmul_workspace(12, 256, 32)) - 1280) // (32 * 256 * 2)
+
+
 def gemm(a):
     """Quantised GEMM (many tokens): time per launch (events around a few
     back-to-back launches over rotating weight copies), TFLOP/s and the
@@ -931,7 +939,9 @@ def gemm(a):
                    "tokens": n_tok, "us": round(us, 2), "TFLOP/s": round(tf, 1),
                    "frac_fp32_mfma": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
             if split:
-                res["frac_fp16_mfma_3parts"] = round(3 * tf / MFMA_FP16_PEAK_TFLOPS, 4)
+                parts = split_parts()
+                res["x_parts"] = parts
+                res["frac_fp16_mfma_parts"] = round(parts * tf / MFMA_FP16_PEAK_TFLOPS, 4)
             if not a.no_cpu and path == paths[0]:
                 cu, kind, sample = cpu_matmul_us(t, n_rows, n_cols, n_tok)
                 res["cpu_baseline"] = {"us": round(cu, 1), "kind": kind, "cores": 1,

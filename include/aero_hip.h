@@ -287,9 +287,10 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * (src/kernels.cpp:520-538). With 32 or more tokens of Q4_K or Q5_K and
  * `ws` 16-byte aligned of at least aero_hip_matmul_workspace(dtype, n_cols,
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
- * with x split into three fp16 parts per token and 256 columns (exact
- * products, fp32 sums; ws holds the parts); otherwise it is aero_hip_matvec. Calls sharing
- * one workspace must be ordered on one stream. */
+ * with x split into two fp16 parts per token and 256 columns (22
+ * significant bits of x, exact products, fp32 sums; ws holds the parts);
+ * otherwise it is aero_hip_matvec. Calls sharing one workspace must be
+ * ordered on one stream. */
 /* Decode steps of a decoder layer in one launch each. The reference runs
  * them as separate passes: rmsnorm_rows (src/transformer.cpp:98-104, or
  * src/tensor.cpp:128-134), matvec (src/kernels.cpp:497-518) per matrix,
@@ -358,7 +359,7 @@ int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t
  * capture, serving loops, harnesses that forbid allocation). Results equal
  * aero_hip_matmul's with a workspace bit for bit. Returns 0 with a reason
  * when the call would need more scratch than the maximum (n_tok * n_cols *
- * 6 bytes and a little more for Q4_K / Q5_K at 32 or more tokens). Every
+ * 4 bytes and a little more for Q4_K / Q5_K at 32 or more tokens). Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other host threads) race; calls ordered on one stream do
  * not. Nothing in the array needs clearing between calls. */

@@ -77,7 +77,7 @@ def test_noalloc_other_paths_and_refusal(hip, oracle):
         synchronize()
         assert bits_equal(got, y.numpy())
         assert rel_to_scale(got, oracle.matmul(t, w, X, 96)) <= RTOL
-    n_cols, n_tok = 14336, 512
+    n_cols, n_tok = 14336, 1024
     assert L.aero_hip_matmul_workspace(W.Q4_K, n_cols, n_tok) > 32 << 20
     dx = DA.empty((n_tok, n_cols))
     dw = DA.empty((8 * (n_cols // 256) * 144,), np.uint8)
