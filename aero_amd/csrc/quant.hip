@@ -300,13 +300,17 @@ void embed_norm_kernel(EmbedNormParams p) {
 }
 
 // Steps a wave and waves a row: the fewest steps a wave (1, 2, 4, 8) that
-// keep the row within `maxw` waves (tunable), so short rows still spread
-// over several waves and long rows keep <= 8 float4 a lane.
+// keep the row within `maxw` waves, so short rows still spread over several
+// waves and long rows keep <= 8 float4 a lane. maxw is 8 up to 1024 rows
+// and 4 beyond (sweep on MI355X: 512 x 4096 Q4_K 5.1 us at 8, 5.7 at 4;
+// 2048 x 2560 Q6_K 8.8 us at 4, 10.3 at 8; 4096 x 2048 Q8_0 13.2 at 4, 17.2
+// at 8; 16384 x 8192 Q4_K within 3% either way).
 template <int TYPE>
 bool launch_embed_norm(EmbedNormParams p, hipStream_t s) {
     const int64_t n_embd = p.g.nbr * QT<TYPE>::BV;
     const int64_t steps = (n_embd + 255) / 256;
-    const int maxw = std::min(std::max(tune("embed_norm_waves", 8), 1), kEmbedNormMaxWaves);
+    const int maxw = std::min(std::max(tune("embed_norm_waves", p.g.n_rows <= 1024 ? 8 : 4), 1),
+                              kEmbedNormMaxWaves);
     int u = 1;
     while (u < 8 && (steps + u - 1) / u > maxw) u *= 2;
     u = tune("embed_norm_u", u);
