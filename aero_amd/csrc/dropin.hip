@@ -7,7 +7,14 @@
 // demand, reused across calls, freed at exit), the same device kernels as
 // the aero_hip_* entry points run on a library-owned stream, and the result
 // is copied back before returning. Calls from several threads serialise on
-// the arena lock. Bad arguments are refused before any device work. The
+// the arena lock.
+//
+// Host buffers are pageable (numpy arrays), and a DMA from pageable memory
+// goes through the driver's own single-threaded staging (6-7 GB/s measured).
+// Large transfers instead move in 4 MiB chunks through two pinned buffers
+// per device: a pool of host threads copies chunk i between the caller's
+// memory and one pinned buffer while the DMA engine moves chunk i-1 from or
+// to the other, each buffer guarded by an event of its last DMA. Bad arguments are refused before any device work. The
 // `void` entry points clear the error string on entry; after a refusal or a
 // HIP error they return with aero_hip_last_error() saying why, so a caller
 // detects failure by a non-empty error string.
@@ -15,7 +22,9 @@
 #include "aero_hip.h"
 
 #include <algorithm>
+#include <condition_variable>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -59,11 +68,97 @@ bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tai
 
 namespace {
 
+// ------------------------------------------------------ host copy pool
+// A fixed pool of host threads for large memcpys between pageable and
+// pinned memory: copy(dst, src, n) splits n into one part a worker (plus the
+// caller) and returns when every part is done. Workers start on first use
+// and are joined at exit.
+class CopyPool {
+public:
+    static CopyPool& get() {
+        static CopyPool pool;
+        return pool;
+    }
+    void copy(void* dst, const void* src, size_t n) {
+        std::lock_guard<std::mutex> call(call_mu_);   // one copy at a time
+        const int parts = (int)std::min<size_t>(workers_.size() + 1, std::max<size_t>(1, n >> 19));
+        if (parts <= 1) {
+            std::memcpy(dst, src, n);
+            return;
+        }
+        const size_t per = ((n + parts - 1) / parts + 63) & ~size_t(63);
+        char* d = static_cast<char*>(dst);
+        const char* sp = static_cast<const char*>(src);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            pending_ = 0;
+            for (int i = 1; i < parts; ++i) {
+                const size_t o = (size_t)i * per;
+                if (o >= n) break;
+                jobs_.push_back({d + o, sp + o, std::min(per, n - o)});
+                ++pending_;
+            }
+        }
+        cv_.notify_all();
+        std::memcpy(d, sp, std::min(per, n));
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [&] { return pending_ == 0; });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto& t : workers_) t.join();
+    }
+
+private:
+    struct Job {
+        char* d;
+        const char* s;
+        size_t n;
+    };
+    CopyPool() {
+        const unsigned hc = std::thread::hardware_concurrency();
+        const int n = (int)std::min(hc == 0 ? 1u : hc, 8u) - 1;
+        for (int i = 0; i < n; ++i) workers_.emplace_back([this] { run(); });
+    }
+    void run() {
+        for (;;) {
+            Job j;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || !jobs_.empty(); });
+                if (stop_ && jobs_.empty()) return;
+                j = jobs_.back();
+                jobs_.pop_back();
+            }
+            std::memcpy(j.d, j.s, j.n);
+            std::lock_guard<std::mutex> lk(mu_);
+            if (--pending_ == 0) done_.notify_all();
+        }
+    }
+    std::vector<std::thread> workers_;
+    std::vector<Job> jobs_;
+    std::mutex call_mu_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    int pending_ = 0;
+    bool stop_ = false;
+};
+
+constexpr size_t kChunk = 4u << 20;      // bytes a pinned transfer chunk
+constexpr size_t kDirect = 1u << 20;     // below this, plain async copies
+
 struct Arena {
     std::mutex mu;
     void* buf = nullptr;
     size_t cap = 0;
     hipStream_t stream = nullptr;
+    void* pinned[2] = {nullptr, nullptr};    // kChunk bytes each
+    hipEvent_t done[2] = {nullptr, nullptr}; // the last DMA of each buffer
+    bool busy[2] = {false, false};           // an event is recorded on it
 };
 
 constexpr int kMaxDevices = 64;
@@ -122,19 +217,90 @@ public:
         return true;
     }
 
+    // host -> device: returns once every chunk is in a pinned buffer and its
+    // DMA queued on the stream
     bool h2d(void* d, const void* h, size_t n) {
         if (!ok_) return false;
-        return n == 0 || hip_ok(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, a_->stream),
-                                "hipMemcpyAsync H2D");
+        if (n < kDirect || !pinned())
+            return n == 0 || hip_ok(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, a_->stream),
+                                    "hipMemcpyAsync H2D");
+        for (size_t o = 0, i = 0; o < n; o += kChunk, ++i) {
+            const int b = (int)(i & 1);
+            const size_t len = std::min(kChunk, n - o);
+            if (!wait(b)) return false;
+            CopyPool::get().copy(a_->pinned[b], static_cast<const char*>(h) + o, len);
+            if (!hip_ok(hipMemcpyAsync(static_cast<char*>(d) + o, a_->pinned[b], len,
+                                       hipMemcpyHostToDevice, a_->stream), "hipMemcpyAsync H2D") ||
+                !record(b))
+                return false;
+        }
+        return true;
     }
+    // device -> host, after the work queued before it: returns with the data
+    // in host memory
     bool d2h(void* h, const void* d, size_t n) {
         if (!ok_) return false;
-        return n == 0 || hip_ok(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, a_->stream),
-                                "hipMemcpyAsync D2H");
+        if (n < kDirect || !pinned())
+            return n == 0 || hip_ok(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, a_->stream),
+                                    "hipMemcpyAsync D2H");
+        const size_t nc = (n + kChunk - 1) / kChunk;
+        auto issue = [&](size_t i) {
+            const int b = (int)(i & 1);
+            const size_t o = i * kChunk, len = std::min(kChunk, n - o);
+            return wait(b) &&
+                   hip_ok(hipMemcpyAsync(a_->pinned[b], static_cast<const char*>(d) + o, len,
+                                         hipMemcpyDeviceToHost, a_->stream),
+                          "hipMemcpyAsync D2H") &&
+                   record(b);
+        };
+        if (!issue(0)) return false;
+        for (size_t i = 0; i < nc; ++i) {
+            const int b = (int)(i & 1);
+            // the next chunk's DMA runs while this one is copied out
+            if (i + 1 < nc) {
+                // the other buffer's last DMA must land before it is reused:
+                // its contents (chunk i-1) were copied out in the previous turn
+                if (!issue(i + 1)) return false;
+            }
+            if (!wait(b)) return false;
+            const size_t o = i * kChunk, len = std::min(kChunk, n - o);
+            CopyPool::get().copy(static_cast<char*>(h) + o, a_->pinned[b], len);
+        }
+        return true;
     }
     bool finish() { return ok_ && hip_ok(hipStreamSynchronize(a_->stream), "hipStreamSynchronize"); }
 
 private:
+    // the two pinned chunk buffers and their events, made on first use
+    bool pinned() {
+        if (a_->pinned[0] != nullptr) return true;
+        for (int b = 0; b < 2; ++b) {
+            if (!hip_ok(hipHostMalloc(&a_->pinned[b], kChunk, hipHostMallocDefault),
+                        "hipHostMalloc(staging)") ||
+                !hip_ok(hipEventCreateWithFlags(&a_->done[b], hipEventDisableTiming),
+                        "hipEventCreate")) {
+                for (int c = 0; c < 2; ++c) {
+                    if (a_->pinned[c] != nullptr) (void)hipHostFree(a_->pinned[c]);
+                    if (a_->done[c] != nullptr) (void)hipEventDestroy(a_->done[c]);
+                    a_->pinned[c] = nullptr;
+                    a_->done[c] = nullptr;
+                }
+                clear_error();   // fall back to the driver's pageable copies
+                return false;
+            }
+        }
+        return true;
+    }
+    bool wait(int b) {
+        if (!a_->busy[b]) return true;
+        a_->busy[b] = false;
+        return hip_ok(hipEventSynchronize(a_->done[b]), "hipEventSynchronize");
+    }
+    bool record(int b) {
+        a_->busy[b] = true;
+        return hip_ok(hipEventRecord(a_->done[b], a_->stream), "hipEventRecord");
+    }
+
     Arena* a_ = nullptr;
     std::unique_lock<std::mutex> lock_;
     bool ok_ = false;

@@ -1597,9 +1597,13 @@ def copy_sweep(a):
 
 def host_abi(a):
     """The reference-compatible host-pointer entry points at the 512-token
-    shape: algorithmic bytes / wall time of the whole call, PCIe included."""
+    shape: algorithmic bytes / wall time of the whole call, PCIe both ways
+    included, beside the reference's own C++ (oracle/_ref, one thread) on the
+    same arrays. Inputs an op modifies in place are fresh copies made outside
+    the timing."""
     from aero_amd import native as NK, tensor_native as TN, transformer_native as N
     from aero_amd import workloads as W
+    from oracle import refbind
 
     s = W.SHAPES[W.HEADLINE]
     rng = np.random.default_rng(0)
@@ -1611,26 +1615,44 @@ def host_abi(a):
     c, si = N.rope_tables(s.head_dim, np.arange(s.n_tok), s.theta)
     qpos = np.repeat(np.arange(s.n_tok), s.hq).astype(np.int32)
     raw = W.make_table(s.emb_type, s.n_tok * (s.hidden // 256), rng).tobytes()
+    raw_np = np.frombuffer(raw, np.uint8)
+    use_ref = refbind.available()
+    reps = max(3, a.steps // 20)
     cases = [
-        ("transformer_native.rmsnorm_rows", lambda: N.rmsnorm_rows(x, w, s.eps),
+        ("transformer_native.rmsnorm_rows", lambda _: N.rmsnorm_rows(x, w, s.eps),
+         (lambda _: refbind.rmsnorm_rows(x, w, s.eps)) if use_ref else None, None,
          W.bytes_rmsnorm(s.n_tok, s.hidden)),
-        ("tensor_native.swiglu", lambda: TN.swiglu(g.copy(), u), W.bytes_act(s.n_tok, s.ffn)),
-        ("transformer_native.apply_rope(q)", lambda: N.apply_rope(q, c, si, qpos),
+        ("tensor_native.swiglu", lambda gi: TN.swiglu(gi, u),
+         (lambda gi: refbind.swiglu(gi, u)) if use_ref else None, g, W.bytes_act(s.n_tok, s.ffn)),
+        ("transformer_native.apply_rope(q)", lambda _: N.apply_rope(q, c, si, qpos),
+         (lambda _: refbind.apply_rope(q, c, si, qpos)) if use_ref else None, None,
          8 * q.size),
-        ("native.dequant(Q4_K, 512 rows)", lambda: NK.dequant(s.emb_type, raw, (s.n_tok, s.hidden)),
-         W.bytes_embed(s.n_tok, s.hidden, s.emb_type)),
+        ("native.dequant(Q4_K, 512 rows)",
+         lambda _: NK.dequant(s.emb_type, raw, (s.n_tok, s.hidden)),
+         (lambda _: refbind.dequant(s.emb_type, raw_np, s.n_tok * s.hidden)) if use_ref
+         else None, None, W.bytes_embed(s.n_tok, s.hidden, s.emb_type)),
     ]
-    out = {}
-    for name, fn, b in cases:
-        fn()
+
+    def timed(fn, fresh):
+        fn(None if fresh is None else fresh.copy())
         ts = []
-        for _ in range(max(3, a.steps // 20)):
+        for _ in range(reps):
+            arg = None if fresh is None else fresh.copy()
             t0 = time.perf_counter()
-            fn()
+            fn(arg)
             ts.append(time.perf_counter() - t0)
-        m = statistics.median(ts)
-        out[name] = {"ms": round(m * 1e3, 3), "GB/s_incl_pcie": round(b / m / 1e9, 2)}
-    print(json.dumps({"host_abi_llama3_8b_prefill": out}))
+        return statistics.median(ts)
+
+    out = {}
+    for name, fn, ref, fresh, b in cases:
+        m = timed(fn, fresh)
+        e = {"ms": round(m * 1e3, 3), "GB/s_incl_pcie": round(b / m / 1e9, 2)}
+        if ref is not None:
+            r = timed(ref, fresh)
+            e.update({"reference_cpu_ms": round(r * 1e3, 3), "speedup_vs_cpu": round(r / m, 2)})
+        out[name] = e
+    print(json.dumps({"host_abi_llama3_8b_prefill": out, "reps": reps,
+                      "cpu": "reference C++ (oracle/_ref), one thread" if use_ref else None}))
     return 0
 
 
