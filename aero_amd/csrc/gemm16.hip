@@ -903,19 +903,20 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     if (gu) split = split && aligned16(j.w_up);
     if (split) return split_run(j, s);
 
-    // separate launches: x' (= x + d) and h = rmsnorm(x') in the workspace
+    // separate launches: x' (= x + d) and h = rmsnorm(x') in the workspace;
+    // without a norm the add still runs through the add + norm kernel (its h
+    // is left unused) and h is x'
     const float* h = j.d ? j.x_out : j.x;
     float* hb = static_cast<float*>(j.ws);
-    if (j.norm >= 0) {
-        const int ok = j.d ? aero_hip_add_rmsnorm(j.x, j.d, j.x_out, j.norm_w, hb, j.n_tok,
-                                                  j.n_cols, j.eps, j.norm, s)
-                           : aero_hip_rmsnorm(j.x, j.norm_w, hb, j.n_tok, j.n_cols, j.eps,
-                                              j.norm, s);
-        if (!ok) return false;
-        h = hb;
-    } else if (j.d) {
-        if (!aero_hip_act_mul(AERO_ACT_IDENTITY, j.x, j.d, j.x_out, j.n_tok * j.n_cols, s))
+    if (j.d) {
+        if (!aero_hip_add_rmsnorm(j.x, j.d, j.x_out, j.norm_w, hb, j.n_tok, j.n_cols, j.eps,
+                                  j.norm >= 0 ? j.norm : 0, s))
             return false;
+        if (j.norm >= 0) h = hb;
+    } else if (j.norm >= 0) {
+        if (!aero_hip_rmsnorm(j.x, j.norm_w, hb, j.n_tok, j.n_cols, j.eps, j.norm, s))
+            return false;
+        h = hb;
     }
     if (!gu) {
         for (int m = 0; m < j.n_mat; ++m)

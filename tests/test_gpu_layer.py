@@ -101,13 +101,14 @@ def run_and_check(oracle, name, **kw):
 @pytest.mark.parametrize("fused", [True, False])
 def test_layer_vs_oracle(hip, oracle, name, fused):
     fus = None if fused else {f: False for f in select.FUSIONS}
-    run_and_check(oracle, name, fusions=fus)
+    step = run_and_check(oracle, name, fusions=fus)
+    assert not step.uses_host()
 
 
 def test_layer_plan_replay(hip, oracle):
-    """The step recorded as a plan and replayed twice gives the eager result
-    (the second replay starts from the first one's residual stream, so x is
-    reset between them)."""
+    """The step recorded as a plan and replayed twice gives the oracle's
+    result both times (a replay starts from the embedding gather and writes
+    the same KV cache rows, so nothing carries over between replays)."""
     from aero_amd.device import Plan, Stream, synchronize
 
     cfg, wts, step, ids, kv_len, K0, V0 = setup("llama3_8b_prefill")
@@ -142,8 +143,9 @@ def test_layer_host_hooks(hip, oracle):
     def act(g, u):
         return oracle.act_mul(ACT[cfg.act], g, u)
 
-    run_and_check(oracle, "qwen2_0p5b_decode", gpu_ops={"rope": False, "act": False},
-                  hooks={"rope": rope, "act": act})
+    step = run_and_check(oracle, "qwen2_0p5b_decode", gpu_ops={"rope": False, "act": False},
+                         hooks={"rope": rope, "act": act})
+    assert step.uses_host()
 
 
 def test_layer_refuses_without_host_path(hip):

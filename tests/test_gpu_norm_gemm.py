@@ -35,11 +35,13 @@ def oracle_h(oracle, x, d, w, eps, unit_offset, norm=True):
 @pytest.mark.parametrize("n_tok,n_cols,rows", [
     (64, 1024, (256, 64, 64)), (33, 2048, (130,)), (100, 512, (96, 40)), (7, 1024, (64, 64, 64)),
 ])
-@pytest.mark.parametrize("form", ["norm", "resid_norm", "unit_offset", "no_norm"])
+@pytest.mark.parametrize("form", ["norm", "resid_norm", "unit_offset", "no_norm",
+                                  "resid_no_norm"])
 def test_norm_matmul_vs_oracle(hip, oracle, t, n_tok, n_cols, rows, form):
     rng = np.random.default_rng(n_tok * 7 + n_cols + len(rows) + t)
     x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
-    d = rng.standard_normal((n_tok, n_cols), dtype=np.float32) if form == "resid_norm" else None
+    d = (rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+         if form.startswith("resid") else None)
     uo = form == "unit_offset"
     w = (rng.standard_normal(n_cols, dtype=np.float32) * np.float32(0.1) + (0 if uo else 1)
          ).astype(np.float32)
@@ -48,9 +50,10 @@ def test_norm_matmul_vs_oracle(hip, oracle, t, n_tok, n_cols, rows, form):
     dx, dw = DA.from_numpy(x), DA.from_numpy(w)
     dd = None if d is None else DA.from_numpy(d)
     ys = [DA.empty((n_tok, r)) for r in rows]
+    norm = not form.endswith("no_norm")
     ops.norm_matmul(t, [DA.from_numpy(m) for m in mats], dx, ys, list(rows), n_cols, n_tok,
-                    norm_w=dw, eps=1e-5, norm=form != "no_norm", unit_offset=uo, d=dd)
-    xs, h = oracle_h(oracle, x, d, w, 1e-5, uo, norm=form != "no_norm")
+                    norm_w=dw, eps=1e-5, norm=norm, unit_offset=uo, d=dd)
+    xs, h = oracle_h(oracle, x, d, w, 1e-5, uo, norm=norm)
     if d is not None:
         assert bits_equal(dx.numpy(), xs)          # the residual stream, in place
     for y, m, r in zip(ys, mats, rows):
