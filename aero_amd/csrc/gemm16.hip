@@ -858,6 +858,10 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 // act-mul into the GEMM epilogue; other types and shapes run the same steps
 // as separate launches (add+norm into the workspace, the library GEMM, the
 // act-mul), so every type and token count is accepted.
+// Sized for the path the shape takes with 16-byte aligned weights (as the
+// GGUF loader and the ops allocate them); a call whose weights are not
+// aligned takes the separate launches and refuses, with the size it needs,
+// a workspace too small for them.
 int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok) {
     if (n_cols <= 0 || n_tok <= 0 || n_ff < 0) return 0;
     if (split_shape_ok(dtype, n_cols, n_tok) && n_tok >= tune("gemm_min_tokens", 32))
@@ -891,16 +895,20 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
         }
     }
     if (j.n_tok == 0) return true;
-    const int64_t need = norm_matmul_workspace(j.dtype, j.n_cols, gu ? n_ff : 0, j.n_tok);
+    // the path decides the workspace: the split GEMM's parts, or the separate
+    // launches' h (and up) buffers
+    bool split = split_shape_ok(j.dtype, j.n_cols, j.n_tok) &&
+                 j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
+    for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
+    if (gu) split = split && aligned16(j.w_up);
+    const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)
+                               : align256(j.n_tok * j.n_cols * 4) +
+                                     (gu ? align256(j.n_tok * n_ff * 4) : 0);
     if (j.ws == nullptr || ws_bytes < need || !aligned16(j.ws)) {
         set_error("norm_matmul: workspace of %lld bytes (16-byte aligned) needed, %lld given",
                   (long long)need, (long long)ws_bytes);
         return false;
     }
-    bool split = split_shape_ok(j.dtype, j.n_cols, j.n_tok) &&
-                 j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
-    for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
-    if (gu) split = split && aligned16(j.w_up);
     if (split) return split_run(j, s);
 
     // separate launches: x' (= x + d) and h = rmsnorm(x') in the workspace;

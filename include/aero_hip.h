@@ -338,8 +338,10 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * library GEMM per matrix and the act-mul. Each result equals that
  * composition to 1e-5 of its scale. ws (16-byte aligned) of at least
  * aero_hip_norm_matmul_workspace(dtype, n_cols, n_ff (0 for the plain
- * form), n_tok) bytes; x, d, x_out, norm_w 16-byte aligned; h, y and out
- * must not overlap x, d or x_out. */
+ * form), n_tok) bytes, sized for 16-byte aligned weights (weights that are
+ * not take the separate launches, and a call whose workspace is too small
+ * for them is refused with the size needed); x, d, x_out, norm_w 16-byte
+ * aligned; h, y and out must not overlap x, d or x_out. */
 int64_t aero_hip_norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok);
 int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
                          const int64_t* n_rows, float* const* y, const float* x, const float* d,

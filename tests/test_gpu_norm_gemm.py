@@ -169,3 +169,15 @@ def test_norm_matmul_refusals(hip):
     assert L.aero_hip_norm_matmul(*args(x.ptr, x.ptr, None, ws.ptr, need)) == 0
     assert L.aero_hip_norm_matmul(*args(x.ptr + 4, None, None, ws.ptr, need)) == 0
     assert L.aero_hip_norm_matmul(*args(x.ptr, None, None, ws.ptr, need)) == 1
+    # gate/up weights off a 16-byte boundary take the separate launches,
+    # whose h and up buffers this split-sized workspace cannot hold
+    n_ff = 64
+    need_gu = L.aero_hip_norm_matmul_workspace(W.Q4_K, n_cols, n_ff, n_tok)
+    assert need_gu < n_tok * (n_cols + n_ff) * 4
+    ws_gu = DA.empty((need_gu,), np.uint8)
+    m2 = DA.empty((2 * m.nbytes + 16,), np.uint8)
+    out = DA.empty((n_tok, n_ff))
+    assert L.aero_hip_norm_matmul_gate_up(W.Q4_K, m2.ptr + 4, m2.ptr + 4 + m.nbytes, m.nbytes,
+                                          x.ptr, None, None, None, 1e-5, 0, 0, out.ptr, n_ff,
+                                          n_cols, n_tok, ws_gu.ptr, need_gu, None) == 0
+    assert "workspace" in _lib.last_error()
