@@ -1034,13 +1034,15 @@ LAYER_CASES = [
     # (shape, weight type, tokens, earlier cache positions)
     ("qwen2_0p5b_decode", 8, 1, 37),
     ("llama3_8b_prefill", 12, 512, 0),
+    ("llama3_8b_decode", 12, 1, 4095),     # the prefill geometry, one token at 4095
 ]
 
 
 def layer_bench(a):
     """One decoder block (aero_amd.layer.LayerStep: embedding, q/k/v, QK-norm +
     RoPE, attention, o, residual + norm, gate/up + act, down, output norm)
-    at the Qwen2-0.5B decode and Llama-3-8B 512-token prefill shapes, with
+    at the Qwen2-0.5B decode, Llama-3-8B 512-token prefill and Llama-3-8B
+    one-token decode (4095 cached positions) shapes, with
     every fusion on and with every fusion off. Four blocks with their own
     weights (rotated, so weights come from HBM as in a deep model), each
     recorded as a plan; µs per block = region / blocks run, between one
@@ -1052,7 +1054,9 @@ def layer_bench(a):
     for shape, wtype, T, kv_len in LAYER_CASES:
         if shape not in names:
             continue
-        cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype)
+        cfg = layer.BlockConfig.from_shape(W.SHAPES[shape.replace("decode", "prefill")
+                                                     if shape == "llama3_8b_decode" else shape],
+                                           wtype)
         weights = [layer.BlockWeights(cfg, seed=i) for i in range(4)]
         rng = np.random.default_rng(5)
         ids = rng.integers(0, cfg.vocab, T).astype(np.int32)

@@ -7,9 +7,12 @@ oracle's matmul equals that product to ~1e-6 of scale, tests/test_gpu_gemm16.py)
 
 Checked at the Qwen2-0.5B decode shape (one token at position 37 over a
 cache of 37 earlier positions; Q8_0 weights, whose 896-value rows take the
-separate-launch paths) and the Llama-3-8B 512-token prefill (Q4_K weights:
-the split GEMM with the norms folded), with every fusion on and with every
-fusion off, and with host hooks standing in for ops taken off the GPU.
+separate-launch paths), the Llama-3-8B 512-token prefill (Q4_K weights: the
+split GEMM with the norms folded), a Llama-3-8B one-token decode over 1023
+cached positions (the fused decode GEMVs, chunked attention) and a
+Gemma-style 64-token prefill (QK-norm, (1+w) norms, GeGLU tanh, scaled
+embedding), with every fusion on and with every fusion off, and with host
+hooks standing in for ops taken off the GPU.
 Tolerance 1e-5 of each output's scale; x is the residual stream after the
 block, h_out its output norm.
 """
@@ -31,6 +34,9 @@ CASES = {
     "qwen2_0p5b_decode": ("qwen2_0p5b_decode", W.Q8_0, 4096, 1, 37),
     "llama3_8b_prefill": ("llama3_8b_prefill", W.Q4_K, 4096, 512, 0),
     "gemma_like_prefill": ("gemma3_4b_prefill", W.Q4_K, 2048, 64, 0),
+    # one token over 1023 cached positions at the Llama-3-8B geometry: the
+    # fused decode GEMVs (16-byte Q4_K rows) and the chunked attention
+    "llama3_8b_decode": ("llama3_8b_prefill", W.Q4_K, 4096, 1, 1023),
 }
 
 
