@@ -102,8 +102,10 @@ class BlockWeights:
 
 
 class LayerStep:
-    """Embedding, one block and the output norm over device buffers sized for
-    `max_tokens` tokens a step and a KV cache of `kv_cap` positions (fp32).
+    """Embedding, one block or a stack of them (`weights` a BlockWeights or a
+    list, one a layer, each with its own KV cache) and the output norm, over
+    device buffers sized for `max_tokens` tokens a step and KV caches of
+    `kv_cap` positions (fp32).
 
         step = LayerStep(cfg, BlockWeights(cfg), max_tokens=512, kv_cap=4096)
         step.prepare(ids, kv_len)          # token ids and positions to HBM
@@ -111,10 +113,14 @@ class LayerStep:
         x, h_out = step.x, step.h_out      # [T, hidden] each, in HBM
     """
 
-    def __init__(self, cfg: BlockConfig, weights: BlockWeights, max_tokens: int,
+    def __init__(self, cfg: BlockConfig, weights, max_tokens: int,
                  kv_cap: int, gpu_ops: dict | None = None, fusions: dict | None = None,
                  hooks: dict | None = None):
-        self.cfg, self.w = cfg, weights
+        self.layers = list(weights) if isinstance(weights, (list, tuple)) else [weights]
+        if not self.layers:
+            raise ValueError("LayerStep needs the weights of at least one block")
+        self.cfg = cfg
+        self.w = self.layers[0]
         self.gpu_ops, self.fusions, self.hooks = gpu_ops or {}, fusions or {}, hooks or {}
         N, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
         T = max_tokens
@@ -122,10 +128,13 @@ class LayerStep:
         HD, KD = cfg.n_head * D, cfg.n_head_kv * D
         self.x, self.h, self.h_out = DA.empty((T, N)), DA.empty((T, N)), DA.empty((T, N))
         self.q, self.att = DA.empty((T, HD)), DA.empty((T, HD))
-        self.o, self.dn = DA.empty((T, N)), DA.empty((T, N))
+        self.o = DA.empty((T, N))
+        self.dn = DA.empty((T, N))
         self.g, self.u = DA.empty((T, F)), DA.empty((T, F))
         self.ids, self.pos = DA.empty((T,), np.int32), DA.empty((T,), np.int32)
-        self.K, self.V = DA.empty((kv_cap, KD)), DA.empty((kv_cap, KD))
+        # one KV cache a layer; K, V are the first layer's
+        self.kv = [(DA.empty((kv_cap, KD)), DA.empty((kv_cap, KD))) for _ in self.layers]
+        self.K, self.V = self.kv[0]
         n_rot, inv = ops.rope_inv_freq(D, cfg.n_rot, cfg.theta)
         self.n_rot, self.inv = n_rot, DA.from_numpy(inv)
         self.scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
@@ -168,36 +177,58 @@ class LayerStep:
     def _put(self, a: DA, v) -> None:
         a.view(np.shape(v)).copy_from(np.ascontiguousarray(v, np.float32))
 
-    # ------------------------------------------------------------ the block
+    # ------------------------------------------------------------ the blocks
     def forward(self, T: int, kv_len: int, stream: Stream | None = None) -> None:
-        c, d = self.cfg, self.w.dev
-        N, H, HK, D, F = c.hidden, c.n_head, c.n_head_kv, c.head_dim, c.ffn
+        """Embedding, every block, the output norm. A block's FFN output is not
+        added to x at its end: the next block's first norm takes it as the
+        residual input (folded into its q/k/v pre-pass where it can be), and
+        after the last block the output norm does (src/model.cpp:284,
+        244-245, 329)."""
+        c = self.cfg
+        N = c.hidden
         if not 0 < T <= self.max_tokens or kv_len + T > self.kv_cap:
             raise ValueError("forward: tokens or KV span outside the buffers")
         s = stream
         x, h = self.x.view((T, N)), self.h.view((T, N))
-        kv0 = kv_len * HK * D * 4
-        kq = self.K.view((T, HK * D), offset_bytes=kv0)
-        vq = self.V.view((T, HK * D), offset_bytes=kv0)
-        q = self.q.view((T, H * D))
+        w0 = self.layers[0]
 
-        # embedding (+ the attention norm when the projections need h)
-        fold_a = self._folds_norm(T, None)
+        # embedding (+ the first block's attention norm when its projections
+        # need h)
         h_ready = False
         if self.gpu("embed"):
-            if not fold_a and self.fuse("embed_norm") and self.gpu("rmsnorm"):
-                ops.embed_rmsnorm(c.emb_type, d["emb"], c.vocab, N, self.ids, x, h,
-                                  d["attn_norm"], c.eps, scale=self.scale,
+            if not self._folds_norm(T, None) and self.fuse("embed_norm") and self.gpu("rmsnorm"):
+                ops.embed_rmsnorm(c.emb_type, w0.dev["emb"], c.vocab, N, self.ids, x, h,
+                                  w0.dev["attn_norm"], c.eps, scale=self.scale,
                                   unit_offset=c.unit_offset, n_ids=T, stream=s)
                 h_ready = True
             else:
-                ops.embed_gather(c.emb_type, d["emb"], c.vocab, N, self.ids, x,
+                ops.embed_gather(c.emb_type, w0.dev["emb"], c.vocab, N, self.ids, x,
                                  scale=self.scale, n_ids=T, stream=s)
         else:
             self._put(x, self.hooks["embed"](self._host(self.ids, (T,))))
 
-        # q, k, v (k and v straight into the cache rows of these positions)
-        self._project(x, None, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
+        resid = None
+        for li, w in enumerate(self.layers):
+            resid = self._block(w, li, T, kv_len, resid, h_ready, s)
+            h_ready = False
+        self._norm(self.layers[-1], x, resid, "out_norm", self.h_out.view((T, N)), T, s)
+
+    def _block(self, w: BlockWeights, li: int, T: int, kv_len: int, resid, h_ready: bool,
+               s) -> DA:
+        """One block on x (+ resid, the previous block's FFN output). Returns
+        this block's FFN output, to be added by the next norm."""
+        c, d = self.cfg, w.dev
+        N, H, HK, D, F = c.hidden, c.n_head, c.n_head_kv, c.head_dim, c.ffn
+        x = self.x.view((T, N))
+        Kc, Vc = self.kv[li]
+        kv0 = kv_len * HK * D * 4
+        kq = Kc.view((T, HK * D), offset_bytes=kv0)
+        vq = Vc.view((T, HK * D), offset_bytes=kv0)
+        q = self.q.view((T, H * D))
+
+        # x += resid; q, k, v (k and v straight into the cache rows of these
+        # positions)
+        self._project(w, x, resid, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
                       [H * D, HK * D, HK * D], T, h_ready, s)
 
         # per-head norms and RoPE, in place (the cache rows of k included)
@@ -214,7 +245,7 @@ class LayerStep:
 
         # causal attention over the cache, then the output projection
         att = self.att.view((T, H * D))
-        ops.attention(q, self.K, self.V, att, T, H, HK, D, D, kv_len + T, 1.0 / math.sqrt(D),
+        ops.attention(q, Kc, Vc, att, T, H, HK, D, D, kv_len + T, 1.0 / math.sqrt(D),
                       qpos=self.pos, stream=s)
         o = self.o.view((T, N))
         ops.matvec(c.wtype, d["wo"], att, o, N, H * D, T, stream=s)
@@ -226,7 +257,8 @@ class LayerStep:
                                     norm_w=d["ffn_norm"], eps=c.eps, unit_offset=c.unit_offset,
                                     d=o, stream=s)
         else:
-            self._norm(x, o, "ffn_norm", h, T, s)
+            h = self.h.view((T, N))
+            self._norm(w, x, o, "ffn_norm", h, T, s)
             if self.gpu("act") and self.fuse("act_gemm") and T < 32 and self.rows16:
                 ops.norm_gate_up(c.wtype, d["wg"], d["wu"], h, g, F, N, T, act=c.act,
                                  norm=False, stream=s)
@@ -239,10 +271,11 @@ class LayerStep:
                 else:
                     self._put(g, self.hooks["act"](self._host(g, (T, F)), self._host(u, (T, F))))
 
-        # down projection; x += down and the output norm
+        # the down projection (the next norm adds it to x; this block's own
+        # residual input in dn was consumed by its first norm)
         dn = self.dn.view((T, N))
         ops.matvec(c.wtype, d["wd"], g, dn, N, F, T, stream=s)
-        self._norm(x, dn, "out_norm", self.h_out.view((T, N)), T, s)
+        return dn
 
     def _folds_norm(self, T: int, resid) -> bool:
         """True when the norm (and residual add) before a projection folds into
@@ -254,10 +287,10 @@ class LayerStep:
             return self.cfg.wtype in _SPLIT_TYPES
         return resid is None and self.rows16
 
-    def _norm(self, x, resid, wname, h, T, s) -> None:
+    def _norm(self, wts: BlockWeights, x, resid, wname, h, T, s) -> None:
         """x += resid (when given); h = rmsnorm(x) * the norm weight `wname`."""
         c = self.cfg
-        w = self.w.dev[wname]
+        w = wts.dev[wname]
         if self.gpu("rmsnorm"):
             if resid is not None:
                 ops.add_rmsnorm(x, resid, w, h, T, c.hidden, c.eps, c.unit_offset, stream=s)
@@ -266,14 +299,15 @@ class LayerStep:
             return
         xn, hn = self.hooks["rmsnorm"](self._host(x, (T, c.hidden)),
                                        None if resid is None else self._host(resid, (T, c.hidden)),
-                                       self.w.host[wname], c.eps, c.unit_offset)
+                                       wts.host[wname], c.eps, c.unit_offset)
         self._put(x, xn)
         self._put(h, hn)
 
-    def _project(self, x, resid, wname, mats, ys, rows, T, h_ready, s) -> None:
+    def _project(self, wts: BlockWeights, x, resid, wname, mats, ys, rows, T, h_ready,
+                 s) -> None:
         """ys[m] = rmsnorm(x (+ resid)) W_m^T, the norm folded when it can be."""
         c = self.cfg
-        norm_w = self.w.dev[wname]
+        norm_w = wts.dev[wname]
         if not h_ready and self._folds_norm(T, resid):
             if T >= 32:
                 ops.norm_matmul(c.wtype, mats, x, ys, rows, c.hidden, T, norm_w=norm_w,
@@ -284,7 +318,7 @@ class LayerStep:
             return
         h = self.h.view((T, c.hidden))
         if not h_ready:
-            self._norm(x, resid, wname, h, T, s)
+            self._norm(wts, x, resid, wname, h, T, s)
         if self.fuse("norm_gemm") and T < 32 and self.rows16 and len(mats) <= 3:
             ops.norm_matvec(c.wtype, mats, h, ys, rows, c.hidden, T, norm=False, stream=s)
         else:

@@ -1046,7 +1046,9 @@ def layer_bench(a):
     every fusion on and with every fusion off. Four blocks with their own
     weights (rotated, so weights come from HBM as in a deep model), each
     recorded as a plan; µs per block = region / blocks run, between one
-    event pair on the stream."""
+    event pair on the stream. Then the same four blocks as one 4-layer stack
+    (one plan; a block's residual add folded into the next block's first
+    norm): µs per layer."""
     from aero_amd import layer, select, workloads as W
     from aero_amd.device import Event, Plan, Stream
 
@@ -1095,6 +1097,30 @@ def layer_bench(a):
             del steps
         print(json.dumps({"layer": shape, "fused_speedup": round(res["unfused"] / res["fused"],
                                                                  3)}), flush=True)
+        # the four blocks as one 4-layer stack: one embedding and one output
+        # norm, each block's FFN output added by the next block's first norm
+        st = layer.LayerStep(cfg, weights, T, kv_len + T)
+        st.prepare(ids, kv_len)
+        p = Plan()
+        with p:
+            st.forward(T, kv_len)
+        stream = Stream()
+        p.launch(stream)
+        reps = max(3, a.steps // 10)
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(reps):
+            p.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * len(weights))
+        print(json.dumps({"layer": shape, "mode": "stack", "layers": len(weights),
+                          "weight_type": wtype, "tokens": T, "kv_len": kv_len,
+                          "us_per_layer": round(us, 2), "launches": len(p),
+                          "tokens_per_s_per_layer": round(T / (us * 1e-6), 1)}), flush=True)
+        p.destroy()
+        stream.destroy()
+        del st
     return 0
 
 

@@ -13,8 +13,10 @@ cached positions (the fused decode GEMVs, chunked attention) and a
 Gemma-style 64-token prefill (QK-norm, (1+w) norms, GeGLU tanh, scaled
 embedding), with every fusion on and with every fusion off, and with host
 hooks standing in for ops taken off the GPU.
+Stacks of 2-3 blocks (each with its own weights and KV cache) are checked
+at the same shapes against the oracle's blocks in turn.
 Tolerance 1e-5 of each output's scale; x is the residual stream after the
-block, h_out its output norm.
+last block, h_out its output norm.
 """
 import math
 
@@ -45,56 +47,75 @@ def dq(oracle, t, raw, rows, cols):
 
 
 def oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0):
-    h_ = wts.host
+    return oracle_stack(oracle, cfg, [wts], ids, kv_len, [K0], [V0])
+
+
+def oracle_stack(oracle, cfg, layers, ids, kv_len, K0s, V0s):
+    """The blocks in turn on the embedded tokens, then the last block's output
+    norm; layer i attends over its own cache K0s[i], V0s[i]."""
     N, H, HK, D = cfg.hidden, cfg.n_head, cfg.n_head_kv, cfg.head_dim
     T = ids.size
     pos = np.arange(kv_len, kv_len + T, dtype=np.int32)
-    mats = {k: dq(oracle, cfg.wtype, h_[k], *wts.shapes[k]) for k in wts.MATS}
-
-    def mm(name, a):
-        return (a.astype(np.float64) @ mats[name].T).astype(np.float32)
-
     scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
-    x = oracle.embed_gather(cfg.emb_type, h_["emb"], cfg.vocab, N, ids, scale)
-    h = oracle.rmsnorm_rows(x, h_["attn_norm"], cfg.eps, cfg.unit_offset)
-    q, k, v = mm("wq", h), mm("wk", h), mm("wv", h)
-    q = oracle.qk_norm_rope(q, T, H, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("q_norm"), cfg.eps,
-                            cfg.unit_offset)
-    k = oracle.qk_norm_rope(k, T, HK, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("k_norm"), cfg.eps,
-                            cfg.unit_offset)
-    Kc = np.concatenate([K0[:kv_len], k.reshape(T, HK * D)]).reshape(-1, HK, D)
-    Vc = np.concatenate([V0[:kv_len], v.reshape(T, HK * D)]).reshape(-1, HK, D)
-    att = oracle.attention_tiled(q.reshape(T, H, D), Kc, Vc, 1.0 / math.sqrt(D), qpos=pos,
-                                 kpos=np.arange(kv_len + T, dtype=np.int32))
-    x = x + mm("wo", att.reshape(T, H * D))
-    h = oracle.rmsnorm_rows(x, h_["ffn_norm"], cfg.eps, cfg.unit_offset)
-    g = oracle.act_mul(ACT[cfg.act], mm("wg", h), mm("wu", h))
-    x = x + mm("wd", g)
-    return x, oracle.rmsnorm_rows(x, h_["out_norm"], cfg.eps, cfg.unit_offset)
+    h0 = layers[0].host
+    x = oracle.embed_gather(cfg.emb_type, h0["emb"], cfg.vocab, N, ids, scale)
+    for wts, K0, V0 in zip(layers, K0s, V0s):
+        h_ = wts.host
+        mats = {k: dq(oracle, cfg.wtype, h_[k], *wts.shapes[k]) for k in wts.MATS}
+
+        def mm(name, a):
+            return (a.astype(np.float64) @ mats[name].T).astype(np.float32)
+
+        h = oracle.rmsnorm_rows(x, h_["attn_norm"], cfg.eps, cfg.unit_offset)
+        q, k, v = mm("wq", h), mm("wk", h), mm("wv", h)
+        q = oracle.qk_norm_rope(q, T, H, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("q_norm"),
+                                cfg.eps, cfg.unit_offset)
+        k = oracle.qk_norm_rope(k, T, HK, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("k_norm"),
+                                cfg.eps, cfg.unit_offset)
+        Kc = np.concatenate([K0[:kv_len], k.reshape(T, HK * D)]).reshape(-1, HK, D)
+        Vc = np.concatenate([V0[:kv_len], v.reshape(T, HK * D)]).reshape(-1, HK, D)
+        att = oracle.attention_tiled(q.reshape(T, H, D), Kc, Vc, 1.0 / math.sqrt(D), qpos=pos,
+                                     kpos=np.arange(kv_len + T, dtype=np.int32))
+        x = x + mm("wo", att.reshape(T, H * D))
+        h = oracle.rmsnorm_rows(x, h_["ffn_norm"], cfg.eps, cfg.unit_offset)
+        g = oracle.act_mul(ACT[cfg.act], mm("wg", h), mm("wu", h))
+        x = x + mm("wd", g)
+    return x, oracle.rmsnorm_rows(x, layers[-1].host["out_norm"], cfg.eps, cfg.unit_offset)
 
 
-def setup(name, seed=0, **kw):
+def setup(name, seed=0, n_layers=1, **kw):
     shape, wtype, vocab, T, kv_len = CASES[name]
     cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype, vocab=vocab)
-    wts = layer.BlockWeights(cfg, seed=seed)
-    step = layer.LayerStep(cfg, wts, max_tokens=T, kv_cap=kv_len + T, **kw)
+    layers = [layer.BlockWeights(cfg, seed=seed + 17 * i) for i in range(n_layers)]
+    step = layer.LayerStep(cfg, layers if n_layers > 1 else layers[0], max_tokens=T,
+                           kv_cap=kv_len + T, **kw)
     rng = np.random.default_rng(seed + 1)
     ids = rng.integers(0, vocab, T).astype(np.int32)
     KD = cfg.n_head_kv * cfg.head_dim
-    K0 = rng.standard_normal((kv_len + T, KD), dtype=np.float32)
-    V0 = rng.standard_normal((kv_len + T, KD), dtype=np.float32)
-    step.K.copy_from(K0)
-    step.V.copy_from(V0)
-    return cfg, wts, step, ids, kv_len, K0, V0
+    K0s, V0s = [], []
+    for Kd, Vd in step.kv:
+        K0 = rng.standard_normal((kv_len + T, KD), dtype=np.float32)
+        V0 = rng.standard_normal((kv_len + T, KD), dtype=np.float32)
+        Kd.copy_from(K0)
+        Vd.copy_from(V0)
+        K0s.append(K0)
+        V0s.append(V0)
+    if n_layers == 1:
+        return cfg, layers[0], step, ids, kv_len, K0s[0], V0s[0]
+    return cfg, layers, step, ids, kv_len, K0s, V0s
 
 
-def run_and_check(oracle, name, **kw):
-    cfg, wts, step, ids, kv_len, K0, V0 = setup(name, **kw)
+def run_and_check(oracle, name, n_layers=1, **kw):
+    cfg, wts, step, ids, kv_len, K0, V0 = setup(name, n_layers=n_layers, **kw)
     T = ids.size
-    print(f"layer {name} tokens={T} kv_len={kv_len} wtype={cfg.wtype} {kw}", flush=True)
+    print(f"layer {name} layers={n_layers} tokens={T} kv_len={kv_len} wtype={cfg.wtype} {kw}",
+          flush=True)
     step.prepare(ids, kv_len)
     step.forward(T, kv_len)
-    want_x, want_h = oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0)
+    if n_layers == 1:
+        want_x, want_h = oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0)
+    else:
+        want_x, want_h = oracle_stack(oracle, cfg, wts, ids, kv_len, K0, V0)
     got_x = step.x.view((T, cfg.hidden)).numpy()
     got_h = step.h_out.view((T, cfg.hidden)).numpy()
     ex, eh = rel_to_scale(got_x, want_x), rel_to_scale(got_h, want_h)
@@ -108,6 +129,18 @@ def run_and_check(oracle, name, **kw):
 def test_layer_vs_oracle(hip, oracle, name, fused):
     fus = None if fused else {f: False for f in select.FUSIONS}
     step = run_and_check(oracle, name, fusions=fus)
+    assert not step.uses_host()
+
+
+@pytest.mark.parametrize("name,n_layers", [("qwen2_0p5b_decode", 3), ("llama3_8b_prefill", 2),
+                                           ("llama3_8b_decode", 2), ("gemma_like_prefill", 2)])
+@pytest.mark.parametrize("fused", [True, False])
+def test_layer_stack_vs_oracle(hip, oracle, name, n_layers, fused):
+    """A stack of blocks, each with its own weights and KV cache: a block's
+    FFN output is added to x by the next block's attention norm (at 32+ tokens
+    in the q/k/v GEMMs' pre-pass), and by the output norm after the last."""
+    fus = None if fused else {f: False for f in select.FUSIONS}
+    step = run_and_check(oracle, name, n_layers=n_layers, fusions=fus)
     assert not step.uses_host()
 
 
