@@ -789,10 +789,14 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
 int64_t dtype_block_bytes(int t);
 int64_t dtype_block_values(int t);
 
-// the quantised GEMV / GEMM dispatch (gemv.hip)
+// the quantised GEMV / GEMM dispatch and the fused decode GEMVs (gemv.hip)
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
               int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s, void* ws,
               int64_t ws_bytes);
+bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
+                    const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                    const float* x, const float* norm_w, float eps, int norm, int act,
+                    int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d, float* xo);
 
 // ------------------------------------------------ allocation-free matmul
 // The split GEMM's workspace in a file-scope device array, for callers that
@@ -855,9 +859,12 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 // The prefill forms of the model loop's "norm -> projections" and "norm ->
 // gate/up -> act" steps (src/model.cpp:166-178,244-245,279-282): the split
 // path folds the residual add and the RMSNorm into the x pre-pass and the
-// act-mul into the GEMM epilogue; other types and shapes run the same steps
-// as separate launches (add+norm into the workspace, the library GEMM, the
-// act-mul), so every type and token count is accepted.
+// act-mul into the GEMM epilogue. Below 32 tokens, rows of whole 16 bytes
+// take the fused decode GEMVs: the norm and the residual add (x_out apart
+// from x and d) in their prologue, the act-mul in their epilogue, no
+// workspace. Other types and shapes run the same steps as separate launches
+// (add+norm into the workspace, the library GEMM, the act-mul), so every
+// type and token count is accepted.
 // Sized for the path the shape takes with 16-byte aligned weights (as the
 // GGUF loader and the ops allocate them); a call whose weights are not
 // aligned takes the separate launches and refuses, with the size it needs,
@@ -870,6 +877,26 @@ int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n
 }
 
 namespace {
+
+// The fused decode GEMV takes the call: few tokens, 16-byte aligned rows of
+// whole 16 bytes, at most 3 matrices (or the gate/up pair), and a residual
+// add only with a norm and an x_out apart from x and d (one workgroup stores
+// x + d while the others read x and d).
+bool fused_gemv_ok(const SplitJob& j, bool gu) {
+    if (j.n_tok >= tune("gemm_min_tokens", 32) || j.rb % 16 != 0 || (!gu && j.n_mat > 3) ||
+        !tune("gemv_lanes64", 1) || !tune("fused_gemv", 1))
+        return false;
+    for (int m = 0; m < (gu ? 1 : j.n_mat); ++m)
+        if (!aligned16(j.w[m])) return false;
+    if (gu && !aligned16(j.w_up)) return false;
+    if (j.d == nullptr) return true;
+    const uintptr_t nb = (uintptr_t)(j.n_tok * j.n_cols * 4);
+    auto apart = [nb](const void* a, const void* b) {
+        const uintptr_t ua = reinterpret_cast<uintptr_t>(a), ub = reinterpret_cast<uintptr_t>(b);
+        return ua + nb <= ub || ub + nb <= ua;
+    };
+    return j.norm >= 0 && apart(j.x_out, j.x) && apart(j.x_out, j.d);
+}
 
 bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t ws_bytes,
                      hipStream_t s) {
@@ -901,6 +928,22 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
                  j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
+    if (!split && fused_gemv_ok(j, gu)) {
+        const uint8_t* w[3] = {j.w[0], gu ? j.w_up : nullptr, nullptr};
+        int64_t wb[3] = {w_bytes[0], w_bytes[0], 0}, nr[3] = {j.n_rows[0], j.n_rows[0], 0};
+        float* y[3] = {j.y[0], j.y[0], nullptr};
+        if (!gu) {
+            for (int m = 1; m < j.n_mat; ++m) {
+                w[m] = j.w[m];
+                wb[m] = w_bytes[m];
+                nr[m] = j.n_rows[m];
+                y[m] = j.y[m];
+            }
+        }
+        return gemv_fused_dev(j.dtype, gu, gu ? 2 : j.n_mat, w, wb, nr, y, j.x, j.norm_w, j.eps,
+                              j.norm, gu ? j.act : AERO_ACT_IDENTITY, j.n_cols, j.n_tok, s, j.d,
+                              j.d ? j.x_out : nullptr);
+    }
     const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)
                                : align256(j.n_tok * j.n_cols * 4) +
                                      (gu ? align256(j.n_tok * n_ff * 4) : 0);

@@ -1048,7 +1048,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
 //   * MULTI: up to three matrices of one type and width sharing x in one
 //     launch (q, k, v): workgroups [blk[m], blk[m+1]) take matrix m;
 //   * PAIR: row i of w[0] (gate) and of w[1] (up) in the same wave, written
-//     as act(gate . x) * (up . x) (the act·mul op's arithmetic).
+//     as act(gate . x) * (up . x) (the act·mul op's arithmetic);
+//   * RESID: the residual add before the norm (src/model.cpp:244-245, 284):
+//     every x load also loads d and uses x + d (one fp32 add, as add_rmsnorm),
+//     and workgroup 0 stores x + d to xo, which overlaps neither x nor d (the
+//     other workgroups still read them).
 // Two rows a wave, as gemv64_kernel<.., 2, ..>.
 struct GemvFuse {
     const uint8_t* w[3];
@@ -1057,6 +1061,8 @@ struct GemvFuse {
     int blk[4];           // MULTI: first workgroup of each matrix, blk[n_mat] = total
     const float* x;       // [n_tok][n_cols]
     const float* norm_w;  // nullable (ones)
+    const float* d;       // RESID: [n_tok][n_cols], added to x
+    float* xo;            // RESID: x + d, written by workgroup 0
     float eps;
     int norm;             // < 0: no norm; else AERO_NORM_UNIT_OFFSET or 0
     int act;              // PAIR: AERO_ACT_*
@@ -1079,7 +1085,7 @@ __device__ __forceinline__ float act_rt(int kind, float v) {
 // step's weights are requested before the norm is computed (after x, which
 // the norm waits for); for rows of one step the x loaded for the norm is the
 // x staged.
-template <int TYPE, int T, bool PIPE, bool PAIR>
+template <int TYPE, int T, bool PIPE, bool PAIR, bool RESID>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse f) {
     using L = Lane64<TYPE>;
     constexpr int R = (PAIR || T == 4) ? 4 : 2;
@@ -1110,6 +1116,38 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         for (int r = 0; r < R; ++r) rowp[r] = f.w[m] + min(r0 + r, f.n_rows[m] - 1) * f.rb;
     }
     GemvParams p{nullptr, f.x, nullptr, 0, f.n_cols, f.rb, f.n_tok, f.n_cols, 0};
+    GemvParams pd = p;
+    pd.x = f.d;
+    // this thread's 16 columns of step st for each token: x, or x + d
+    auto load_x = [&](int st, XStepRegs<T>& xq) AERO_INLINE {
+        xstep_load<T>(p, st, tid, xq);
+        if constexpr (RESID) {
+            XStepRegs<T> dv;
+            xstep_load<T>(pd, st, tid, dv);
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 a = xq.v[t][q], b = dv.v[t][q];
+                    xq.v[t][q] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                }
+        }
+    };
+    // RESID: workgroup 0 stores x + d of its columns (the last step's clamped
+    // copies and the padding tokens are not stored)
+    auto store_x = [&](int st, const XStepRegs<T>& xq) AERO_INLINE {
+        if constexpr (RESID) {
+            const int c = st * kStepCols + 16 * tid;
+            if (blockIdx.x != 0 || c >= f.n_cols) return;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                if (t >= f.n_tok) break;
+                float* dst = f.xo + (int64_t)t * f.n_cols + c;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(dst + 4 * q) = xq.v[t][q];
+            }
+        }
+    };
 
     float inv[T];
 #pragma unroll
@@ -1146,7 +1184,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     // x, then the norm weights, then the matrix weights: loads complete in
     // order, so waiting for x (the norm, the staging) does not wait for W
     XStepRegs<T> xr;
-    xstep_load<T>(p, 0, tid, xr);
+    load_x(0, xr);
     v4f wv[4];
     load_w(0, wv);
     __builtin_amdgcn_sched_barrier(0);  // keeps every x load ahead of the weights
@@ -1175,11 +1213,13 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
 #pragma unroll
         for (int t = 0; t < T; ++t) ss[t] = 0.0f;
         add_sq(0, xr);
+        store_x(0, xr);
         if constexpr (PIPE) {
             for (int st = 1; st < n_st; ++st) {
                 XStepRegs<T> xq;
-                xstep_load<T>(p, st, tid, xq);
+                load_x(st, xq);
                 add_sq(st, xq);
+                store_x(st, xq);
             }
         }
 #pragma unroll
@@ -1214,7 +1254,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         bool live_b;
         for (int st = 0; st < n_st; st += 2) {
             const int s1 = min(st + 1, n_st - 1);
-            xstep_load<T>(p, s1, tid, xr);
+            load_x(s1, xr);
             load_w(s1, wv);
 #pragma unroll
             for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, l, n_blk);
@@ -1226,7 +1266,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             __syncthreads();
             if (st + 1 >= n_st) break;
             const int s2 = min(st + 2, n_st - 1);
-            xstep_load<T>(p, s2, tid, xr);
+            load_x(s2, xr);
             load_w(s2, wv);
 #pragma unroll
             for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, l, n_blk);
@@ -1262,33 +1302,41 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
 
 using GemvFusedKernel = void (*)(GemvFuse);
 
-template <int TYPE, bool PAIR>
+template <int TYPE, bool PAIR, bool RESID>
 GemvFusedKernel pick_fused_t(int T, bool pipe) {
     if (pipe) {
         switch (T) {
-        case 1: return gemv64_fused_kernel<TYPE, 1, true, PAIR>;
-        case 2: return gemv64_fused_kernel<TYPE, 2, true, PAIR>;
+        case 1: return gemv64_fused_kernel<TYPE, 1, true, PAIR, RESID>;
+        case 2: return gemv64_fused_kernel<TYPE, 2, true, PAIR, RESID>;
         default: return nullptr;
         }
     }
     switch (T) {
-    case 1: return gemv64_fused_kernel<TYPE, 1, false, PAIR>;
-    case 2: return gemv64_fused_kernel<TYPE, 2, false, PAIR>;
-    case 4: return gemv64_fused_kernel<TYPE, 4, false, PAIR>;
+    case 1: return gemv64_fused_kernel<TYPE, 1, false, PAIR, RESID>;
+    case 2: return gemv64_fused_kernel<TYPE, 2, false, PAIR, RESID>;
+    case 4: return gemv64_fused_kernel<TYPE, 4, false, PAIR, RESID>;
     default: return nullptr;
     }
 }
 
-template <bool PAIR>
-GemvFusedKernel pick_fused(int dtype, int T, bool pipe) {
+template <bool PAIR, bool RESID>
+GemvFusedKernel pick_fused_r(int dtype, int T, bool pipe) {
     switch (dtype) {
-    case AERO_DTYPE_Q8_0: return pick_fused_t<AERO_DTYPE_Q8_0, PAIR>(T, pipe);
-    case AERO_DTYPE_Q4_K: return pick_fused_t<AERO_DTYPE_Q4_K, PAIR>(T, pipe);
-    case AERO_DTYPE_Q5_K: return pick_fused_t<AERO_DTYPE_Q5_K, PAIR>(T, pipe);
-    case AERO_DTYPE_Q6_K: return pick_fused_t<AERO_DTYPE_Q6_K, PAIR>(T, pipe);
-    case AERO_DTYPE_IQ4_XS: return pick_fused_t<AERO_DTYPE_IQ4_XS, PAIR>(T, pipe);
+    case AERO_DTYPE_Q8_0: return pick_fused_t<AERO_DTYPE_Q8_0, PAIR, RESID>(T, pipe);
+    case AERO_DTYPE_Q4_K: return pick_fused_t<AERO_DTYPE_Q4_K, PAIR, RESID>(T, pipe);
+    case AERO_DTYPE_Q5_K: return pick_fused_t<AERO_DTYPE_Q5_K, PAIR, RESID>(T, pipe);
+    case AERO_DTYPE_Q6_K: return pick_fused_t<AERO_DTYPE_Q6_K, PAIR, RESID>(T, pipe);
+    case AERO_DTYPE_IQ4_XS: return pick_fused_t<AERO_DTYPE_IQ4_XS, PAIR, RESID>(T, pipe);
     default: return nullptr;
     }
+}
+
+GemvFusedKernel pick_fused(bool pair, bool resid, int dtype, int T, bool pipe) {
+    if (pair)
+        return resid ? pick_fused_r<true, true>(dtype, T, pipe)
+                     : pick_fused_r<true, false>(dtype, T, pipe);
+    return resid ? pick_fused_r<false, true>(dtype, T, pipe)
+                 : pick_fused_r<false, false>(dtype, T, pipe);
 }
 
 using GemvKernel = void (*)(GemvParams);
@@ -1463,7 +1511,8 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
 bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                     const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                     const float* x, const float* norm_w, float eps, int norm, int act,
-                    int64_t n_cols, int64_t n_tok, hipStream_t s) {
+                    int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d,
+                    float* xo) {
     const char* what = pair ? "norm_gate_up" : "norm_matvec";
     const bool quant = dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q4_K ||
                        dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q6_K ||
@@ -1486,6 +1535,20 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
         set_error("%s: rows must be a multiple of 16 bytes, x and the norm weight 16-byte "
                   "aligned", what);
         return false;
+    }
+    if (d != nullptr) {
+        // x + d is stored by one workgroup while the others read x and d
+        const int64_t nb = n_tok * n_cols * 4;
+        auto apart = [nb](const void* a, const void* b) {
+            const uintptr_t ua = reinterpret_cast<uintptr_t>(a), ub = reinterpret_cast<uintptr_t>(b);
+            return ua + nb <= ub || ub + nb <= ua;
+        };
+        if (xo == nullptr || norm < 0 || !aligned16(d) || !aligned16(xo) || !apart(xo, x) ||
+            !apart(xo, d)) {
+            set_error("%s: the residual add needs a norm and x_out 16-byte aligned, overlapping "
+                      "neither x nor d", what);
+            return false;
+        }
     }
     for (int m = 0; m < n_mat; ++m) {
         if (w[m] == nullptr || y[pair ? 0 : m] == nullptr || n_rows[m] < 0 ||
@@ -1526,12 +1589,14 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
     for (int64_t t0 = 0; t0 < n_tok; t0 += t_max) {
         const int nt = (int)std::min<int64_t>(t_max, n_tok - t0);
         const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
-        GemvFusedKernel k = pair ? pick_fused<true>(dtype, T, pipe) : pick_fused<false>(dtype, T, pipe);
+        GemvFusedKernel k = pick_fused(pair, d != nullptr, dtype, T, pipe);
         if (k == nullptr) {
             set_error("%s: no kernel for %d tokens", what, T);
             return false;
         }
         f.x = x + t0 * n_cols;
+        f.d = d ? d + t0 * n_cols : nullptr;
+        f.xo = d ? xo + t0 * n_cols : nullptr;
         f.n_tok = nt;
         for (int m = 0; m < (pair ? 1 : n_mat); ++m) f.y[m] = y[m] + t0 * n_rows[m];
         const int64_t total = grid_of(T, f);
@@ -1562,7 +1627,8 @@ int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w, const in
                          const float* norm_w, float eps, int norm, int64_t n_cols,
                          int64_t n_tok, void* stream) {
     return aero::gemv_fused_dev(dtype, false, n_mat, w, w_bytes, n_rows, y, x, norm_w, eps, norm,
-                                AERO_ACT_IDENTITY, n_cols, n_tok, (hipStream_t)stream) ? 1 : 0;
+                                AERO_ACT_IDENTITY, n_cols, n_tok, (hipStream_t)stream, nullptr,
+                                nullptr) ? 1 : 0;
 }
 
 int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up, int64_t w_bytes,
@@ -1574,7 +1640,7 @@ int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
     const int64_t nr[2] = {n_ff, n_ff};
     float* y[2] = {out, out};
     return aero::gemv_fused_dev(dtype, true, 2, w, wb, nr, y, x, norm_w, eps, norm, act, n_cols,
-                                n_tok, (hipStream_t)stream) ? 1 : 0;
+                                n_tok, (hipStream_t)stream, nullptr, nullptr) ? 1 : 0;
 }
 
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok) {

@@ -1,9 +1,9 @@
-"""A device-resident decoder block: the model-loop counterpart of the fused ops.
+"""Device-resident decoder blocks: the model-loop counterpart of the fused ops.
 
-One Qwen-style block of the reference (src/model.cpp:234-287, with the
+Qwen-style blocks of the reference (src/model.cpp:234-287, with the
 attention hook of src/attention_layer.cpp:60-240 and the FFN of
-src/model.cpp:166-178) over quantised weights resident in HBM, every
-activation kept on the device:
+src/model.cpp:166-178), one or a stack, over quantised weights resident in
+HBM, every activation kept on the device. Per block:
 
     x = embed(ids) (* scale)                      src/model.cpp:297-316
     h = rmsnorm(x, attn_norm)                     :244-245
@@ -15,6 +15,10 @@ activation kept on the device:
     h = rmsnorm(x, ffn_norm)                      :280-282
     x += (act(h Wg) * (h Wu)) Wd                  :166-178, 284
     h_out = rmsnorm(x, out_norm)                  :329
+
+In a stack the FFN output of a block is added to x by the next block's
+attention norm (and after the last block by the output norm), so that add
+folds into the next projections like the o-projection's does.
 
 Each elementwise site asks aero_amd.select whether its op runs on the GPU
 (AERO_GPU_OPS; unset means every op, for this device-resident loop) and which
@@ -127,6 +131,11 @@ class LayerStep:
         self.max_tokens, self.kv_cap = T, kv_cap
         HD, KD = cfg.n_head * D, cfg.n_head_kv * D
         self.x, self.h, self.h_out = DA.empty((T, N)), DA.empty((T, N)), DA.empty((T, N))
+        # x and a second residual buffer: below 32 tokens a projection that
+        # folds the residual add stores x + d into the other one (its
+        # workgroups still read x); the output norm leaves x in self.x
+        self.xs = (self.x, DA.empty((T, N)))
+        self._cur = 0
         self.q, self.att = DA.empty((T, HD)), DA.empty((T, HD))
         self.o = DA.empty((T, N))
         self.dn = DA.empty((T, N))
@@ -190,13 +199,14 @@ class LayerStep:
             raise ValueError("forward: tokens or KV span outside the buffers")
         s = stream
         x, h = self.x.view((T, N)), self.h.view((T, N))
+        self._cur = 0
         w0 = self.layers[0]
 
         # embedding (+ the first block's attention norm when its projections
         # need h)
         h_ready = False
         if self.gpu("embed"):
-            if not self._folds_norm(T, None) and self.fuse("embed_norm") and self.gpu("rmsnorm"):
+            if not self._folds_norm(T) and self.fuse("embed_norm") and self.gpu("rmsnorm"):
                 ops.embed_rmsnorm(c.emb_type, w0.dev["emb"], c.vocab, N, self.ids, x, h,
                                   w0.dev["attn_norm"], c.eps, scale=self.scale,
                                   unit_offset=c.unit_offset, n_ids=T, stream=s)
@@ -211,7 +221,8 @@ class LayerStep:
         for li, w in enumerate(self.layers):
             resid = self._block(w, li, T, kv_len, resid, h_ready, s)
             h_ready = False
-        self._norm(self.layers[-1], x, resid, "out_norm", self.h_out.view((T, N)), T, s)
+        self._norm(self.layers[-1], self._x(T), resid, "out_norm", self.h_out.view((T, N)), T,
+                   s, x_out=x)
 
     def _block(self, w: BlockWeights, li: int, T: int, kv_len: int, resid, h_ready: bool,
                s) -> DA:
@@ -219,7 +230,6 @@ class LayerStep:
         this block's FFN output, to be added by the next norm."""
         c, d = self.cfg, w.dev
         N, H, HK, D, F = c.hidden, c.n_head, c.n_head_kv, c.head_dim, c.ffn
-        x = self.x.view((T, N))
         Kc, Vc = self.kv[li]
         kv0 = kv_len * HK * D * 4
         kq = Kc.view((T, HK * D), offset_bytes=kv0)
@@ -228,7 +238,7 @@ class LayerStep:
 
         # x += resid; q, k, v (k and v straight into the cache rows of these
         # positions)
-        self._project(w, x, resid, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
+        self._project(w, resid, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
                       [H * D, HK * D, HK * D], T, h_ready, s)
 
         # per-head norms and RoPE, in place (the cache rows of k included)
@@ -252,13 +262,14 @@ class LayerStep:
 
         # x += o; h = rmsnorm(x); g = act(h Wg) * (h Wu)
         g = self.g.view((T, F))
-        if self._folds_norm(T, o) and self.fuse("act_gemm") and self.gpu("act"):
-            ops.norm_matmul_gate_up(c.wtype, d["wg"], d["wu"], x, g, F, N, T, act=c.act,
+        if self._folds_norm(T) and self.fuse("act_gemm") and self.gpu("act"):
+            xi, xo = self._advance(T, o)
+            ops.norm_matmul_gate_up(c.wtype, d["wg"], d["wu"], xi, g, F, N, T, act=c.act,
                                     norm_w=d["ffn_norm"], eps=c.eps, unit_offset=c.unit_offset,
-                                    d=o, stream=s)
+                                    d=o, x_out=xo, stream=s)
         else:
             h = self.h.view((T, N))
-            self._norm(w, x, o, "ffn_norm", h, T, s)
+            self._norm(w, self._x(T), o, "ffn_norm", h, T, s)
             if self.gpu("act") and self.fuse("act_gemm") and T < 32 and self.rows16:
                 ops.norm_gate_up(c.wtype, d["wg"], d["wu"], h, g, F, N, T, act=c.act,
                                  norm=False, stream=s)
@@ -277,48 +288,63 @@ class LayerStep:
         ops.matvec(c.wtype, d["wd"], g, dn, N, F, T, stream=s)
         return dn
 
-    def _folds_norm(self, T: int, resid) -> bool:
+    def _folds_norm(self, T: int) -> bool:
         """True when the norm (and residual add) before a projection folds into
-        it: the split GEMM's pre-pass at 32+ tokens, or (no residual) the fused
-        decode GEMV below that."""
+        it: the split GEMM's pre-pass at 32+ tokens, the fused decode GEMV's
+        prologue below that."""
         if not (self.fuse("norm_gemm") and self.gpu("rmsnorm")):
             return False
         if T >= 32:
             return self.cfg.wtype in _SPLIT_TYPES
-        return resid is None and self.rows16
+        return self.rows16
 
-    def _norm(self, wts: BlockWeights, x, resid, wname, h, T, s) -> None:
-        """x += resid (when given); h = rmsnorm(x) * the norm weight `wname`."""
+    def _x(self, T: int) -> DA:
+        """The residual stream x as it stands (one of the two x buffers)."""
+        return self.xs[self._cur].view((T, self.cfg.hidden))
+
+    def _advance(self, T: int, resid):
+        """(x, x_out) for a projection folding x += resid: in place at 32+
+        tokens (the split GEMM's pre-pass owns each token's row), else into
+        the other x buffer, which then holds x."""
+        xi = self._x(T)
+        if resid is None or T >= 32:
+            return xi, xi
+        self._cur ^= 1
+        return xi, self._x(T)
+
+    def _norm(self, wts: BlockWeights, x, resid, wname, h, T, s, x_out=None) -> None:
+        """x_out = x + resid (resid given; x_out None: x in place); h =
+        rmsnorm of that (or of x) * the norm weight `wname`."""
         c = self.cfg
         w = wts.dev[wname]
+        if resid is None and x_out is not None and x_out.ptr != x.ptr:
+            raise ValueError("_norm: x_out without a residual input")
         if self.gpu("rmsnorm"):
             if resid is not None:
-                ops.add_rmsnorm(x, resid, w, h, T, c.hidden, c.eps, c.unit_offset, stream=s)
+                ops.add_rmsnorm(x, resid, w, h, T, c.hidden, c.eps, c.unit_offset, x_out=x_out,
+                                stream=s)
             else:
                 ops.rmsnorm(x, w, h, T, c.hidden, c.eps, c.unit_offset, stream=s)
             return
         xn, hn = self.hooks["rmsnorm"](self._host(x, (T, c.hidden)),
                                        None if resid is None else self._host(resid, (T, c.hidden)),
                                        wts.host[wname], c.eps, c.unit_offset)
-        self._put(x, xn)
+        self._put(x if x_out is None else x_out, xn)
         self._put(h, hn)
 
-    def _project(self, wts: BlockWeights, x, resid, wname, mats, ys, rows, T, h_ready,
+    def _project(self, wts: BlockWeights, resid, wname, mats, ys, rows, T, h_ready,
                  s) -> None:
         """ys[m] = rmsnorm(x (+ resid)) W_m^T, the norm folded when it can be."""
         c = self.cfg
         norm_w = wts.dev[wname]
-        if not h_ready and self._folds_norm(T, resid):
-            if T >= 32:
-                ops.norm_matmul(c.wtype, mats, x, ys, rows, c.hidden, T, norm_w=norm_w,
-                                eps=c.eps, unit_offset=c.unit_offset, d=resid, stream=s)
-            else:
-                ops.norm_matvec(c.wtype, mats, x, ys, rows, c.hidden, T, norm_w=norm_w,
-                                eps=c.eps, unit_offset=c.unit_offset, stream=s)
+        if not h_ready and self._folds_norm(T):
+            xi, xo = self._advance(T, resid)
+            ops.norm_matmul(c.wtype, mats, xi, ys, rows, c.hidden, T, norm_w=norm_w,
+                            eps=c.eps, unit_offset=c.unit_offset, d=resid, x_out=xo, stream=s)
             return
         h = self.h.view((T, c.hidden))
         if not h_ready:
-            self._norm(wts, x, resid, wname, h, T, s)
+            self._norm(wts, self._x(T), resid, wname, h, T, s)
         if self.fuse("norm_gemm") and T < 32 and self.rows16 and len(mats) <= 3:
             ops.norm_matvec(c.wtype, mats, h, ys, rows, c.hidden, T, norm=False, stream=s)
         else:

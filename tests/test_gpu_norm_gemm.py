@@ -4,8 +4,10 @@ they replace: the residual add `x_ += o_` and norm_row (src/model.cpp:244-245,
 279-282), matmul (src/kernels.cpp:520-538) and act_mul (src/model.cpp:172-175).
 
 Q4_K / Q5_K with 32+ tokens take the split-x GEMM with the add and the norm
-folded into its pre-pass and act(gate)*up in its epilogue; other types and
-token counts take separate launches. Tolerance: 1e-5 of the output's scale
+folded into its pre-pass and act(gate)*up in its epilogue; below 32 tokens
+rows of whole 16 bytes take the fused decode GEMV (the add and the norm in its
+prologue, act(gate)*up in its epilogue); other types and token counts take
+separate launches. Tolerance: 1e-5 of the output's scale
 (the reference's RTOL, tests/test_transformer_native.py:34-37); the residual
 stream x + d is bit-exact (one IEEE add).
 """
@@ -60,9 +62,42 @@ def test_norm_matmul_vs_oracle(hip, oracle, t, n_tok, n_cols, rows, form):
         assert rel_to_scale(y.numpy(), oracle.matmul(t, m, h, r)) <= RTOL
 
 
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q8_0, W.Q5_K, W.Q6_K, W.IQ4_XS])
+@pytest.mark.parametrize("n_tok,n_cols,rows", [
+    (1, 4096, (512, 128, 128)), (3, 1024, (64, 96)), (5, 8192, (96,)), (2, 5120, (64, 32, 64)),
+    (31, 512, (64,)),
+])
+@pytest.mark.parametrize("apart", [True, False])
+def test_norm_matmul_resid_few_tokens(hip, oracle, t, n_tok, n_cols, rows, apart):
+    """Below 32 tokens with x_out apart from x and d, rows of whole 16 bytes
+    take the fused decode GEMV with the add and the norm in its prologue
+    (one workgroup stores x + d); x_out = x, or rows of other sizes (Q6_K
+    here at 1024 and 5120 columns), take add + norm then the GEMVs. Both
+    match the oracle, and x_out is x + d bit for bit."""
+    rng = np.random.default_rng(n_tok * 13 + n_cols + len(rows) + t)
+    x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+    d = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+    w = (rng.standard_normal(n_cols, dtype=np.float32) * np.float32(0.1) + 1).astype(np.float32)
+    mats = [weights(t, r, n_cols, rng) for r in rows]
+    print(f"norm_matmul few tokens type={t} tok={n_tok} cols={n_cols} rows={rows} "
+          f"apart={apart}", flush=True)
+    dx, dd, dw = DA.from_numpy(x), DA.from_numpy(d), DA.from_numpy(w)
+    xo = DA.empty(x.shape) if apart else dx
+    ys = [DA.empty((n_tok, r)) for r in rows]
+    ops.norm_matmul(t, [DA.from_numpy(m) for m in mats], dx, ys, list(rows), n_cols, n_tok,
+                    norm_w=dw, eps=1e-5, d=dd, x_out=xo)
+    xs, h = oracle_h(oracle, x, d, w, 1e-5, False)
+    assert bits_equal(xo.numpy(), xs)
+    if apart:
+        assert bits_equal(dx.numpy(), x)
+    for y, m, r in zip(ys, mats, rows):
+        assert rel_to_scale(y.numpy(), oracle.matmul(t, m, h, r)) <= RTOL
+
+
 @pytest.mark.parametrize("t", [W.Q4_K, W.Q5_K, W.Q6_K])
 @pytest.mark.parametrize("act", list(ACT))
-@pytest.mark.parametrize("n_tok,n_cols,n_ff", [(64, 1024, 320), (45, 512, 100), (5, 512, 64)])
+@pytest.mark.parametrize("n_tok,n_cols,n_ff", [(64, 1024, 320), (45, 512, 100), (5, 512, 64),
+                                              (1, 5120, 96), (3, 8192, 64)])
 def test_gate_up_vs_oracle(hip, oracle, t, act, n_tok, n_cols, n_ff):
     rng = np.random.default_rng(n_tok + n_cols + n_ff + t + ACT[act])
     x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
