@@ -860,11 +860,12 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 // gate/up -> act" steps (src/model.cpp:166-178,244-245,279-282): the split
 // path folds the residual add and the RMSNorm into the x pre-pass and the
 // act-mul into the GEMM epilogue. Below 32 tokens, rows of whole 16 bytes
-// take the fused decode GEMVs: the norm and the residual add (x_out apart
-// from x and d) in their prologue, the act-mul in their epilogue, no
-// workspace. Other types and shapes run the same steps as separate launches
-// (add+norm into the workspace, the library GEMM, the act-mul), so every
-// type and token count is accepted.
+// take the fused decode GEMVs (every matrix, or gate/up with the act-mul in
+// the epilogue, in one launch): at one token (two without a residual) with
+// the norm and the residual add (x_out apart from x and d) in their
+// prologue, else after an add + norm pass into the workspace. Other types and shapes run the same
+// steps as separate launches (add+norm into the workspace, the library
+// GEMM, the act-mul), so every type and token count is accepted.
 // Sized for the path the shape takes with 16-byte aligned weights (as the
 // GGUF loader and the ops allocate them); a call whose weights are not
 // aligned takes the separate launches and refuses, with the size it needs,
@@ -878,17 +879,27 @@ int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n
 
 namespace {
 
-// The fused decode GEMV takes the call: few tokens, 16-byte aligned rows of
-// whole 16 bytes, at most 3 matrices (or the gate/up pair), and a residual
-// add only with a norm and an x_out apart from x and d (one workgroup stores
-// x + d while the others read x and d).
-bool fused_gemv_ok(const SplitJob& j, bool gu) {
+// The fused decode GEMVs take the call's matrices in one launch (a group of
+// up to 4 tokens): few tokens, 16-byte aligned rows of whole 16 bytes, at
+// most 3 matrices (or the gate/up pair).
+bool fused_gemv_rows_ok(const SplitJob& j, bool gu) {
     if (j.n_tok >= tune("gemm_min_tokens", 32) || j.rb % 16 != 0 || (!gu && j.n_mat > 3) ||
         !tune("gemv_lanes64", 1) || !tune("fused_gemv", 1))
         return false;
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m)
         if (!aligned16(j.w[m])) return false;
-    if (gu && !aligned16(j.w_up)) return false;
+    return !gu || aligned16(j.w_up);
+}
+
+// ... and also the norm (and residual add) in their prologue: every
+// workgroup sums x^2 of its tokens over the row (and loads d), which pays
+// at few tokens a launch. Measured on MI355X at the Llama-3-8B decode
+// shapes: the norm alone up to 2 tokens, the add + norm at 1; beyond that
+// the add + norm pass plus the GEMV on h is as fast or faster. A residual
+// add only with a norm and an x_out apart from x and d (one workgroup
+// stores x + d while the others read x and d).
+bool fused_prologue_ok(const SplitJob& j) {
+    if (j.n_tok > tune("fused_norm_max_tokens", j.d ? 1 : 2)) return false;
     if (j.d == nullptr) return true;
     const uintptr_t nb = (uintptr_t)(j.n_tok * j.n_cols * 4);
     auto apart = [nb](const void* a, const void* b) {
@@ -896,6 +907,26 @@ bool fused_gemv_ok(const SplitJob& j, bool gu) {
         return ua + nb <= ub || ub + nb <= ua;
     };
     return j.norm >= 0 && apart(j.x_out, j.x) && apart(j.x_out, j.d);
+}
+
+// One fused-GEMV launch per token group over x (norm / residual per the
+// arguments) for the call's matrices, or its gate/up pair with the act-mul.
+bool fused_gemv_run(const SplitJob& j, bool gu, const int64_t* w_bytes, const float* x,
+                    int norm, const float* d, hipStream_t s) {
+    const uint8_t* w[3] = {j.w[0], gu ? j.w_up : nullptr, nullptr};
+    int64_t wb[3] = {w_bytes[0], w_bytes[0], 0}, nr[3] = {j.n_rows[0], j.n_rows[0], 0};
+    float* y[3] = {j.y[0], j.y[0], nullptr};
+    if (!gu) {
+        for (int m = 1; m < j.n_mat; ++m) {
+            w[m] = j.w[m];
+            wb[m] = w_bytes[m];
+            nr[m] = j.n_rows[m];
+            y[m] = j.y[m];
+        }
+    }
+    return gemv_fused_dev(j.dtype, gu, gu ? 2 : j.n_mat, w, wb, nr, y, x, j.norm_w, j.eps, norm,
+                          gu ? j.act : AERO_ACT_IDENTITY, j.n_cols, j.n_tok, s, d,
+                          d ? j.x_out : nullptr);
 }
 
 bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t ws_bytes,
@@ -928,25 +959,11 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
                  j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
-    if (!split && fused_gemv_ok(j, gu)) {
-        const uint8_t* w[3] = {j.w[0], gu ? j.w_up : nullptr, nullptr};
-        int64_t wb[3] = {w_bytes[0], w_bytes[0], 0}, nr[3] = {j.n_rows[0], j.n_rows[0], 0};
-        float* y[3] = {j.y[0], j.y[0], nullptr};
-        if (!gu) {
-            for (int m = 1; m < j.n_mat; ++m) {
-                w[m] = j.w[m];
-                wb[m] = w_bytes[m];
-                nr[m] = j.n_rows[m];
-                y[m] = j.y[m];
-            }
-        }
-        return gemv_fused_dev(j.dtype, gu, gu ? 2 : j.n_mat, w, wb, nr, y, j.x, j.norm_w, j.eps,
-                              j.norm, gu ? j.act : AERO_ACT_IDENTITY, j.n_cols, j.n_tok, s, j.d,
-                              j.d ? j.x_out : nullptr);
-    }
+    const bool fused = !split && fused_gemv_rows_ok(j, gu);
+    if (fused && fused_prologue_ok(j)) return fused_gemv_run(j, gu, w_bytes, j.x, j.norm, j.d, s);
     const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)
                                : align256(j.n_tok * j.n_cols * 4) +
-                                     (gu ? align256(j.n_tok * n_ff * 4) : 0);
+                                     (gu && !fused ? align256(j.n_tok * n_ff * 4) : 0);
     if (j.ws == nullptr || ws_bytes < need || !aligned16(j.ws)) {
         set_error("norm_matmul: workspace of %lld bytes (16-byte aligned) needed, %lld given",
                   (long long)need, (long long)ws_bytes);
@@ -969,6 +986,9 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
             return false;
         h = hb;
     }
+    // the matrices (or the gate/up pair with its act-mul) in one fused launch
+    // on h when their rows allow it
+    if (fused) return fused_gemv_run(j, gu, w_bytes, h, -1, nullptr, s);
     if (!gu) {
         for (int m = 0; m < j.n_mat; ++m)
             if (!gemv_dev(j.dtype, j.w[m], w_bytes[m], h, j.y[m], j.n_rows[m], j.n_cols,

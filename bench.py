@@ -816,8 +816,11 @@ def fused(a):
     """Fused decode GEMVs against the separate launches they replace:
     RMSNorm + q/k/v (aero_hip_norm_matvec) vs rmsnorm + three GEMVs, and
     RMSNorm + gate/up + SiLU·mul (aero_hip_norm_gate_up) vs rmsnorm + two GEMVs
-    + act_mul. Sustained time per step (recorded plans, back to back over a
-    > 1 GiB rotation of weight sets), weight GB/s of the fused launch."""
+    + act_mul; and with a residual input, the same launches with the add in
+    their prologue (norm_matmul / norm_matmul_gate_up below 32 tokens) vs
+    add_rmsnorm + the fused GEMV without a norm. Sustained time per step
+    (recorded plans, back to back over a > 1 GiB rotation of weight sets),
+    weight GB/s of the fused launch."""
     from aero_amd import ops, workloads as W
     from aero_amd.device import DeviceArray as DA, Event, Plan, Stream
 
@@ -834,17 +837,38 @@ def fused(a):
         nw = DA.from_numpy((1 + 0.1 * rng.standard_normal(n_cols)).astype(np.float32))
         res = {"case": name, "dtype": t, "rows": list(rows), "n_cols": n_cols,
                "weight_bytes": set_bytes}
-        for n_tok in (1, 4):
+        for n_tok in (1, 2, 4):
             X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
             H = DA.empty((n_tok, n_cols))
             Ys = [DA.empty((n_tok, nr)) for nr in rows]
             O = DA.empty((n_tok, rows[0]))
+            D = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
+            XO = DA.empty((n_tok, n_cols))
             out = {}
-            for path in ("fused", "separate"):
+            for path in ("fused", "separate", "resid_fused", "resid_separate"):
                 plan = Plan()
                 with plan:
                     for ws in sets:
-                        if kind == "qkv":
+                        if path == "resid_fused":
+                            # x_out = x + d, then the same launch with the add
+                            # in its prologue (norm_matmul below 32 tokens)
+                            if kind == "qkv":
+                                ops.norm_matmul(t, ws, X, Ys, list(rows), n_cols, n_tok,
+                                                norm_w=nw, eps=1e-5, d=D, x_out=XO)
+                            else:
+                                ops.norm_matmul_gate_up(t, ws[0], ws[1], X, O, rows[0], n_cols,
+                                                        n_tok, act="silu", norm_w=nw, eps=1e-5,
+                                                        d=D, x_out=XO)
+                        elif path == "resid_separate":
+                            # add + norm, then the fused GEMV on h without a norm
+                            ops.add_rmsnorm(X, D, nw, H, n_tok, n_cols, 1e-5, x_out=XO)
+                            if kind == "qkv":
+                                ops.norm_matvec(t, ws, H, Ys, list(rows), n_cols, n_tok,
+                                                norm=False)
+                            else:
+                                ops.norm_gate_up(t, ws[0], ws[1], H, O, rows[0], n_cols, n_tok,
+                                                 act="silu", norm=False)
+                        elif kind == "qkv":
                             if path == "fused":
                                 ops.norm_matvec(t, ws, X, Ys, list(rows), n_cols, n_tok,
                                                 norm_w=nw, eps=1e-5)
@@ -878,7 +902,11 @@ def fused(a):
                                 "separate_us": round(out["separate"], 3),
                                 "speedup": round(out["separate"] / out["fused"], 3),
                                 "weight_GB/s": round(gbs, 1),
-                                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                "resid_fused_us": round(out["resid_fused"], 3),
+                                "resid_separate_us": round(out["resid_separate"], 3),
+                                "resid_speedup": round(out["resid_separate"] /
+                                                       out["resid_fused"], 3)}
         print(json.dumps(res), flush=True)
         del sets, w0
     return 0
@@ -1074,9 +1102,10 @@ def layer_bench(a):
                     st.forward(T, kv_len)
                 plans.append(p)
             stream = Stream()
-            for p in plans:
-                p.launch(stream)
             reps = max(3, a.steps // 10)
+            for _ in range(reps):          # warm-up as long as the timed region
+                for p in plans:
+                    p.launch(stream)
             e0, e1 = Event(), Event()
             e0.record(stream)
             for _ in range(reps):
@@ -1105,8 +1134,9 @@ def layer_bench(a):
         with p:
             st.forward(T, kv_len)
         stream = Stream()
-        p.launch(stream)
         reps = max(3, a.steps // 10)
+        for _ in range(reps):
+            p.launch(stream)
         e0, e1 = Event(), Event()
         e0.record(stream)
         for _ in range(reps):

@@ -36,6 +36,7 @@ def oracle_h(oracle, x, d, w, eps, unit_offset, norm=True):
 @pytest.mark.parametrize("t", [W.Q4_K, W.Q5_K, W.Q6_K, W.Q8_0])
 @pytest.mark.parametrize("n_tok,n_cols,rows", [
     (64, 1024, (256, 64, 64)), (33, 2048, (130,)), (100, 512, (96, 40)), (7, 1024, (64, 64, 64)),
+    (2, 1024, (64, 64, 64)), (1, 5120, (96, 32)),
 ])
 @pytest.mark.parametrize("form", ["norm", "resid_norm", "unit_offset", "no_norm",
                                   "resid_no_norm"])
@@ -65,15 +66,15 @@ def test_norm_matmul_vs_oracle(hip, oracle, t, n_tok, n_cols, rows, form):
 @pytest.mark.parametrize("t", [W.Q4_K, W.Q8_0, W.Q5_K, W.Q6_K, W.IQ4_XS])
 @pytest.mark.parametrize("n_tok,n_cols,rows", [
     (1, 4096, (512, 128, 128)), (3, 1024, (64, 96)), (5, 8192, (96,)), (2, 5120, (64, 32, 64)),
-    (31, 512, (64,)),
+    (31, 512, (64,)), (1, 5120, (64, 32, 64)), (1, 8192, (96,)),
 ])
 @pytest.mark.parametrize("apart", [True, False])
 def test_norm_matmul_resid_few_tokens(hip, oracle, t, n_tok, n_cols, rows, apart):
-    """Below 32 tokens with x_out apart from x and d, rows of whole 16 bytes
-    take the fused decode GEMV with the add and the norm in its prologue
-    (one workgroup stores x + d); x_out = x, or rows of other sizes (Q6_K
-    here at 1024 and 5120 columns), take add + norm then the GEMVs. Both
-    match the oracle, and x_out is x + d bit for bit."""
+    """Below 32 tokens, rows of whole 16 bytes take the fused decode GEMV: at
+    one token with x_out apart from x and d, with the add and the norm in its
+    prologue (one workgroup stores x + d); else after an add + norm pass.
+    Rows of other sizes (Q6_K here at 1024 and 5120 columns) take add + norm
+    then the GEMVs. All match the oracle, and x_out is x + d bit for bit."""
     rng = np.random.default_rng(n_tok * 13 + n_cols + len(rows) + t)
     x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
     d = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
