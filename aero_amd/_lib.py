@@ -127,6 +127,10 @@ PROTOTYPES = {
     "aero_hip_norm_matmul": (c_int, [c_int, c_int, POINTER(vp), POINTER(c_int64), POINTER(c_int64),
                                      POINTER(vp), vp, vp, vp, vp, c_float, c_int, c_int64,
                                      c_int64, vp, c_int64, vp]),
+    "aero_hip_norm_matmul_rope": (c_int, [c_int, c_int, POINTER(vp), POINTER(c_int64),
+                                          POINTER(c_int64), POINTER(vp), vp, vp, vp, vp, c_float,
+                                          c_int, c_int64, c_int64, c_int, c_int64, c_int, vp, vp,
+                                          vp, c_int64, vp]),
     "aero_hip_norm_matmul_gate_up": (c_int, [c_int, vp, vp, c_int64, vp, vp, vp, vp, c_float,
                                              c_int, c_int, vp, c_int64, c_int64, c_int64, vp,
                                              c_int64, vp]),

@@ -87,6 +87,18 @@ inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// RoPE folded into the fused decode GEMV's epilogue (gemv.hip): the outputs
+// of matrices 0 .. mats-1 are heads of D rows, every channel rotated at the
+// token's position, angle (float)pos * inv[p].
+struct RopeFold {
+    int mats;             // 0: none
+    int D;
+    int mode;             // AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED
+    const int32_t* pos;   // [n_tok]
+    const float* inv;     // [D / 2]
+};
+bool rope_fold_ok(const RopeFold& rope, bool pair, int n_mat, const int64_t* n_rows);
+
 // ------------------------------------------------- streaming loads/stores
 // Data read once or written once (activations) moves with the nontemporal
 // hint, so it streams through the caches without evicting what is reused

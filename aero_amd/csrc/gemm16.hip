@@ -678,6 +678,7 @@ struct SplitJob {
     int64_t rb;
     int64_t n_tok;
     void* ws;
+    RopeFold rope;         // RoPE on the first rope.mats outputs (norm_matmul_rope)
 };
 
 template <bool NORM, bool RESID>
@@ -779,7 +780,7 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
         !aligned16(ws) || !tune("gemm16", 1))
         return true;
     SplitJob j{dtype, x, nullptr, nullptr, nullptr, -1, 0.f, 1, &w, nullptr, 0, &n_rows, &y,
-               n_cols, rb, n_tok, ws};
+               n_cols, rb, n_tok, ws, {}};
     if (!split_run(j, s)) return false;
     *ran = true;
     return true;
@@ -796,7 +797,8 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
 bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                     const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                     const float* x, const float* norm_w, float eps, int norm, int act,
-                    int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d, float* xo);
+                    int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d, float* xo,
+                    const RopeFold* rope);
 
 // ------------------------------------------------ allocation-free matmul
 // The split GEMM's workspace in a file-scope device array, for callers that
@@ -910,9 +912,10 @@ bool fused_prologue_ok(const SplitJob& j) {
 }
 
 // One fused-GEMV launch per token group over x (norm / residual per the
-// arguments) for the call's matrices, or its gate/up pair with the act-mul.
+// arguments) for the call's matrices, or its gate/up pair with the act-mul;
+// the RoPE of j.rope in its epilogue when that folds (*rope_done).
 bool fused_gemv_run(const SplitJob& j, bool gu, const int64_t* w_bytes, const float* x,
-                    int norm, const float* d, hipStream_t s) {
+                    int norm, const float* d, hipStream_t s, bool* rope_done) {
     const uint8_t* w[3] = {j.w[0], gu ? j.w_up : nullptr, nullptr};
     int64_t wb[3] = {w_bytes[0], w_bytes[0], 0}, nr[3] = {j.n_rows[0], j.n_rows[0], 0};
     float* y[3] = {j.y[0], j.y[0], nullptr};
@@ -924,13 +927,18 @@ bool fused_gemv_run(const SplitJob& j, bool gu, const int64_t* w_bytes, const fl
             y[m] = j.y[m];
         }
     }
-    return gemv_fused_dev(j.dtype, gu, gu ? 2 : j.n_mat, w, wb, nr, y, x, j.norm_w, j.eps, norm,
-                          gu ? j.act : AERO_ACT_IDENTITY, j.n_cols, j.n_tok, s, d,
-                          d ? j.x_out : nullptr);
+    const bool fold = j.rope.mats > 0 && rope_fold_ok(j.rope, gu, j.n_mat, j.n_rows);
+    if (!gemv_fused_dev(j.dtype, gu, gu ? 2 : j.n_mat, w, wb, nr, y, x, j.norm_w, j.eps, norm,
+                        gu ? j.act : AERO_ACT_IDENTITY, j.n_cols, j.n_tok, s, d,
+                        d ? j.x_out : nullptr, fold ? &j.rope : nullptr))
+        return false;
+    *rope_done = fold;
+    return true;
 }
 
 bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t ws_bytes,
-                     hipStream_t s) {
+                     hipStream_t s, bool* rope_done) {
+    *rope_done = false;
     const int64_t bv = dtype_block_values(j.dtype), bb = dtype_block_bytes(j.dtype);
     const bool gu = j.w_up != nullptr;
     if (bv <= 0 || j.x == nullptr || j.n_cols <= 0 || j.n_tok < 0 || j.n_cols % bv != 0 ||
@@ -960,7 +968,8 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
     const bool fused = !split && fused_gemv_rows_ok(j, gu);
-    if (fused && fused_prologue_ok(j)) return fused_gemv_run(j, gu, w_bytes, j.x, j.norm, j.d, s);
+    if (fused && fused_prologue_ok(j))
+        return fused_gemv_run(j, gu, w_bytes, j.x, j.norm, j.d, s, rope_done);
     const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)
                                : align256(j.n_tok * j.n_cols * 4) +
                                      (gu && !fused ? align256(j.n_tok * n_ff * 4) : 0);
@@ -988,7 +997,7 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     }
     // the matrices (or the gate/up pair with its act-mul) in one fused launch
     // on h when their rows allow it
-    if (fused) return fused_gemv_run(j, gu, w_bytes, h, -1, nullptr, s);
+    if (fused) return fused_gemv_run(j, gu, w_bytes, h, -1, nullptr, s, rope_done);
     if (!gu) {
         for (int m = 0; m < j.n_mat; ++m)
             if (!gemv_dev(j.dtype, j.w[m], w_bytes[m], h, j.y[m], j.n_rows[m], j.n_cols,
@@ -1024,8 +1033,49 @@ int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const in
         return 0;
     }
     aero::SplitJob j{dtype, x, d, x_out, norm_w, norm, eps, n_mat, w, nullptr, 0, n_rows, y,
-                     n_cols, 0, n_tok, ws};
-    return aero::norm_matmul_run(j, w_bytes, 0, ws_bytes, (hipStream_t)stream) ? 1 : 0;
+                     n_cols, 0, n_tok, ws, {}};
+    bool rope_done;
+    return aero::norm_matmul_run(j, w_bytes, 0, ws_bytes, (hipStream_t)stream, &rope_done) ? 1
+                                                                                           : 0;
+}
+
+int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
+                              const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                              const float* x, const float* d, float* x_out, const float* norm_w,
+                              float eps, int norm, int64_t n_cols, int64_t n_tok, int n_rope,
+                              int64_t head_dim, int rope_mode, const int32_t* pos,
+                              const float* inv_freq, void* ws, int64_t ws_bytes, void* stream) {
+    if (w == nullptr || w_bytes == nullptr || n_rows == nullptr || y == nullptr) {
+        aero::set_error("norm_matmul_rope: null matrix arrays");
+        return 0;
+    }
+    if (n_rope < 1 || n_rope > 2 || n_rope > n_mat || head_dim < 2 || head_dim % 2 ||
+        head_dim > 512 || pos == nullptr || inv_freq == nullptr ||
+        (rope_mode != AERO_ROPE_NEOX && rope_mode != AERO_ROPE_INTERLEAVED)) {
+        aero::set_error("norm_matmul_rope: bad RoPE arguments (n_rope=%d of %d matrices, "
+                        "head_dim=%lld, mode=%d, pos and inv_freq required)", n_rope, n_mat,
+                        (long long)head_dim, rope_mode);
+        return 0;
+    }
+    for (int m = 0; m < n_rope; ++m) {
+        if (n_rows[m] % head_dim) {
+            aero::set_error("norm_matmul_rope: matrix %d has %lld rows, not whole heads of %lld",
+                            m, (long long)n_rows[m], (long long)head_dim);
+            return 0;
+        }
+    }
+    aero::SplitJob j{dtype, x, d, x_out, norm_w, norm, eps, n_mat, w, nullptr, 0, n_rows, y,
+                     n_cols, 0, n_tok, ws,
+                     {n_rope, (int)head_dim, rope_mode, pos, inv_freq}};
+    bool rope_done = false;
+    if (!aero::norm_matmul_run(j, w_bytes, 0, ws_bytes, (hipStream_t)stream, &rope_done))
+        return 0;
+    if (rope_done || n_tok == 0) return 1;
+    // the path taken has no RoPE epilogue: the RoPE pass on q (and k)
+    return aero_hip_qk_norm_rope(y[0], nullptr, n_rows[0] / head_dim, n_rope > 1 ? y[1] : nullptr,
+                                 nullptr, n_rope > 1 ? n_rows[1] / head_dim : 0, nullptr,
+                                 nullptr, 0.f, 0, n_tok, head_dim, head_dim, rope_mode, pos,
+                                 inv_freq, nullptr, nullptr, 0, stream);
 }
 
 int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
@@ -1042,8 +1092,10 @@ int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t
     const int64_t nr[1] = {n_ff};
     float* const ys[1] = {out};
     aero::SplitJob j{dtype, x, d, x_out, norm_w, norm, eps, 1, ws_g, w_up, act, nr, ys,
-                     n_cols, 0, n_tok, ws};
-    return aero::norm_matmul_run(j, wb, n_ff, ws_bytes, (hipStream_t)stream) ? 1 : 0;
+                     n_cols, 0, n_tok, ws, {}};
+    bool rope_done;
+    return aero::norm_matmul_run(j, wb, n_ff, ws_bytes, (hipStream_t)stream, &rope_done) ? 1
+                                                                                         : 0;
 }
 
 int aero_hip_matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,

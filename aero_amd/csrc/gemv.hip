@@ -1052,7 +1052,14 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
 //   * RESID: the residual add before the norm (src/model.cpp:244-245, 284):
 //     every x load also loads d and uses x + d (one fp32 add, as add_rmsnorm),
 //     and workgroup 0 stores x + d to xo, which overlaps neither x nor d (the
-//     other workgroups still read them).
+//     other workgroups still read them);
+//   * RoPE on the outputs of matrices m < rope_mats (q, k; the rotation of
+//     src/attention_layer.cpp:120-156 over every channel of heads of
+//     rope_D rows, angle (float)pos * inv[p] as the RoPE kernel): NeoX
+//     pairs (i, i + D/2) are 64 or 32 rows apart, so a workgroup of such a
+//     matrix owns 2R rows of a head's first half (waves 0, 1) and the same
+//     2R rows of its second half (waves 2, 3), and the partners' sums meet
+//     in LDS; interleaved pairs (2i, 2i+1) are two rows of one wave.
 // Two rows a wave, as gemv64_kernel<.., 2, ..>.
 struct GemvFuse {
     const uint8_t* w[3];
@@ -1069,6 +1076,11 @@ struct GemvFuse {
     int n_cols;
     int64_t rb;
     int n_tok;            // tokens this launch handles (<= T)
+    int rope_mats;        // matrices 0 .. rope_mats-1 rotate their outputs (0: none)
+    int rope_D;           // rows a head (every channel rotates)
+    int rope_mode;        // AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED
+    const int32_t* pos;   // [n_tok] positions of this launch's tokens
+    const float* inv;     // [rope_D / 2] inverse frequencies
 };
 
 __device__ __forceinline__ float act_rt(int kind, float v) {
@@ -1092,6 +1104,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     constexpr int BV = QT<TYPE>::BV;
     __shared__ __align__(16) XStep<T> xs[PIPE ? 2 : 1];
     __shared__ float red[kGemvWaves][T];
+    __shared__ float rot[kGemvWaves][R][T];   // RoPE: each wave's row sums
 
     const int tid = threadIdx.x;
     const int l = tid & 63;
@@ -1101,6 +1114,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
 
     int m = 0;
     int64_t r0;
+    int pair0 = 0;  // NeoX RoPE: the pair index (within the head) of the wave's first row
     const uint8_t* rowp[R];
     if constexpr (PAIR) {
         // rows r0 .. r0 + R/2 of gate (r < R/2) and of up (r >= R/2)
@@ -1111,7 +1125,17 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     } else {
         const int b = blockIdx.x;
         m = __builtin_amdgcn_readfirstlane((b >= f.blk[1]) + (b >= f.blk[2]));
-        r0 = ((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R;
+        if (m < f.rope_mats && f.rope_mode == AERO_ROPE_NEOX) {
+            // 2R pairs a workgroup: rows p0 .. p0+2R-1 of the head's first
+            // half (waves 0, 1) and of its second half (waves 2, 3)
+            const int P = f.rope_D / 2, per_head = P / (2 * R);
+            const int bl = b - f.blk[m];
+            const int h = bl / per_head;
+            pair0 = (bl % per_head) * (2 * R) + (wave & 1) * R;
+            r0 = (int64_t)h * f.rope_D + (wave >= 2 ? P : 0) + pair0;
+        } else {
+            r0 = ((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R;
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) rowp[r] = f.w[m] + min(r0 + r, f.n_rows[m] - 1) * f.rb;
     }
@@ -1289,12 +1313,57 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
                 if (l == 0 && r0 + r < f.n_rows[0] && t < f.n_tok)
                     f.y[0][t * f.n_rows[0] + r0 + r] = act_rt(f.act, g) * u;
             }
-        } else {
+        } else if (m >= f.rope_mats) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float v = group_sum<64>(acc[r][t]);
                 if (l == 0 && r0 + r < f.n_rows[m] && t < f.n_tok)
                     f.y[m][t * f.n_rows[m] + r0 + r] = v;
+            }
+        }
+    }
+    if constexpr (!PAIR) {
+        if (m < f.rope_mats) {  // uniform: the workgroup's matrix
+            float v[R][T];
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int r = 0; r < R; ++r) v[r][t] = group_sum<64>(acc[r][t]);
+            const bool neox = f.rope_mode == AERO_ROPE_NEOX;
+            if (neox) {
+                if (l == 0) {
+#pragma unroll
+                    for (int t = 0; t < T; ++t)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) rot[wave][r][t] = v[r][t];
+                }
+                __syncthreads();
+            }
+            if (l == 0) {
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    if (t >= f.n_tok) break;
+                    const float pt = (float)f.pos[t];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float o;
+                        if (neox) {
+                            // x'[i] = x[i] c - x[i+P] s; x'[i+P] = x[i+P] c + x[i] s
+                            float sn, c;
+                            sincosf(pt * f.inv[pair0 + r], &sn, &c);
+                            const float other = rot[wave ^ 2][r][t];
+                            o = wave < 2 ? v[r][t] * c - other * sn : v[r][t] * c + other * sn;
+                        } else {
+                            // x'[2i] = x[2i] c - x[2i+1] s; x'[2i+1] = x[2i] s + x[2i+1] c
+                            const int rr = r & ~1;
+                            float sn, c;
+                            sincosf(pt * f.inv[(int)((r0 + rr) % f.rope_D) / 2], &sn, &c);
+                            o = (r & 1) == 0 ? v[rr][t] * c - v[rr + 1][t] * sn
+                                             : v[rr][t] * sn + v[rr + 1][t] * c;
+                        }
+                        if (r0 + r < f.n_rows[m]) f.y[m][t * f.n_rows[m] + r0 + r] = o;
+                    }
+                }
             }
         }
     }
@@ -1504,6 +1573,21 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
     return true;
 }
 
+// Whether RoPE on the outputs of matrices 0 .. rope.mats-1 folds into the
+// fused GEMV: plain (not gate/up) matrices whose rows are whole heads of D
+// rows, D even; NeoX needs D a multiple of 16 (a workgroup takes 2R of a
+// head's pairs, R up to 4); positions and inverse frequencies given.
+bool rope_fold_ok(const RopeFold& rope, bool pair, int n_mat, const int64_t* n_rows) {
+    if (pair || rope.mats < 1 || rope.mats > n_mat || rope.pos == nullptr ||
+        rope.inv == nullptr || rope.D < 2 || rope.D % 2 || rope.D > 1024 ||
+        (rope.mode != AERO_ROPE_NEOX && rope.mode != AERO_ROPE_INTERLEAVED) ||
+        (rope.mode == AERO_ROPE_NEOX && rope.D % 16))
+        return false;
+    for (int m = 0; m < rope.mats; ++m)
+        if (n_rows[m] % rope.D) return false;
+    return true;
+}
+
 // The fused decode GEMVs (gemv64_fused_kernel): argument checks, token
 // groups of up to 4 (2 for rows of more than one 4096-column step), one
 // launch a group. Matrices must take gemv64 (16-byte aligned, rows a
@@ -1512,7 +1596,7 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                     const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                     const float* x, const float* norm_w, float eps, int norm, int act,
                     int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d,
-                    float* xo) {
+                    float* xo, const RopeFold* rope) {
     const char* what = pair ? "norm_gate_up" : "norm_matvec";
     const bool quant = dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q4_K ||
                        dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q6_K ||
@@ -1559,8 +1643,19 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
             return false;
         }
     }
+    if (rope != nullptr && rope->mats > 0 && !rope_fold_ok(*rope, pair, n_mat, n_rows)) {
+        set_error("%s: RoPE on %d matrices of heads of %d rows (mode %d) cannot fold", what,
+                  rope->mats, rope->D, rope->mode);
+        return false;
+    }
     if (n_tok == 0) return true;
     GemvFuse f{};
+    if (rope != nullptr && rope->mats > 0) {
+        f.rope_mats = rope->mats;
+        f.rope_D = rope->D;
+        f.rope_mode = rope->mode;
+        f.inv = rope->inv;
+    }
     // workgroups of a launch of T tokens: rows a wave as the kernel's R
     auto grid_of = [&](int T, GemvFuse& g) -> int64_t {
         const int R = (pair || T == 4) ? 4 : 2;
@@ -1595,6 +1690,7 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
             return false;
         }
         f.x = x + t0 * n_cols;
+        f.pos = f.rope_mats > 0 ? rope->pos + t0 : nullptr;
         f.d = d ? d + t0 * n_cols : nullptr;
         f.xo = d ? xo + t0 * n_cols : nullptr;
         f.n_tok = nt;
@@ -1628,7 +1724,7 @@ int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w, const in
                          int64_t n_tok, void* stream) {
     return aero::gemv_fused_dev(dtype, false, n_mat, w, w_bytes, n_rows, y, x, norm_w, eps, norm,
                                 AERO_ACT_IDENTITY, n_cols, n_tok, (hipStream_t)stream, nullptr,
-                                nullptr) ? 1 : 0;
+                                nullptr, nullptr) ? 1 : 0;
 }
 
 int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up, int64_t w_bytes,
@@ -1640,7 +1736,7 @@ int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
     const int64_t nr[2] = {n_ff, n_ff};
     float* y[2] = {out, out};
     return aero::gemv_fused_dev(dtype, true, 2, w, wb, nr, y, x, norm_w, eps, norm, act, n_cols,
-                                n_tok, (hipStream_t)stream, nullptr, nullptr) ? 1 : 0;
+                                n_tok, (hipStream_t)stream, nullptr, nullptr, nullptr) ? 1 : 0;
 }
 
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok) {

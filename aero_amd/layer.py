@@ -25,7 +25,8 @@ Each elementwise site asks aero_amd.select whether its op runs on the GPU
 fusions apply (AERO_GPU_FUSE; unset means all): the gather with the first
 norm (embed_norm), norms and residual adds folded into the projections that
 consume them (norm_gemm), the act-mul folded into the gate/up projection
-(act_gemm). An op off the GPU runs the caller's host hook for it, as the
+(act_gemm), RoPE in the epilogue of the few-token q/k projection
+(rope_gemm). An op off the GPU runs the caller's host hook for it, as the
 reference's model loop keeps its own code for the ops it does not hand to a
 library; with no hook the block raises select.HostPathRequired, since the
 library has no CPU path. With every op on the GPU, `forward` can be recorded
@@ -237,21 +238,28 @@ class LayerStep:
         q = self.q.view((T, H * D))
 
         # x += resid; q, k, v (k and v straight into the cache rows of these
-        # positions)
+        # positions), with RoPE on q and k in the projection's epilogue when
+        # that folds
+        rope = None
+        if self._folds_rope(T, h_ready):
+            rope = {"n": 2, "head_dim": D, "mode": ops.ROPE_NEOX, "pos": self.pos,
+                    "inv_freq": self.inv}
         self._project(w, resid, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
-                      [H * D, HK * D, HK * D], T, h_ready, s)
+                      [H * D, HK * D, HK * D], T, h_ready, s, rope=rope)
 
-        # per-head norms and RoPE, in place (the cache rows of k included)
-        if self.gpu("rope") and (not c.qk_norm or self.gpu("qk_norm")):
-            ops.qk_norm_rope(q, H, T, D, self.n_rot, k=kq, n_k_heads=HK,
-                             q_norm_w=d.get("q_norm"), k_norm_w=d.get("k_norm"), eps=c.eps,
-                             unit_offset=c.unit_offset, pos=self.pos, inv_freq=self.inv,
-                             stream=s)
-        else:
-            qh, kh = self.hooks["rope"](self._host(q, (T, H, D)), self._host(kq, (T, HK, D)),
-                                        self._host(self.pos, (T,)))
-            self._put(q, qh)
-            self._put(kq, kh)
+        # per-head norms and RoPE, in place (the cache rows of k included),
+        # unless the projection's epilogue rotated q and k
+        if rope is None:
+            if self.gpu("rope") and (not c.qk_norm or self.gpu("qk_norm")):
+                ops.qk_norm_rope(q, H, T, D, self.n_rot, k=kq, n_k_heads=HK,
+                                 q_norm_w=d.get("q_norm"), k_norm_w=d.get("k_norm"), eps=c.eps,
+                                 unit_offset=c.unit_offset, pos=self.pos, inv_freq=self.inv,
+                                 stream=s)
+            else:
+                qh, kh = self.hooks["rope"](self._host(q, (T, H, D)),
+                                            self._host(kq, (T, HK, D)), self._host(self.pos, (T,)))
+                self._put(q, qh)
+                self._put(kq, kh)
 
         # causal attention over the cache, then the output projection
         att = self.att.view((T, H * D))
@@ -298,6 +306,15 @@ class LayerStep:
             return self.cfg.wtype in _SPLIT_TYPES
         return self.rows16
 
+    def _folds_rope(self, T: int, h_ready: bool) -> bool:
+        """True when RoPE on q and k runs in the epilogue of the few-token
+        q/k/v projection: the norm folds there (fused decode GEMV), every
+        channel rotates and no per-head norm comes between."""
+        c = self.cfg
+        return (T < 32 and not h_ready and self._folds_norm(T) and self.fuse("rope_gemm") and
+                self.gpu("rope") and not c.qk_norm and self.n_rot == c.head_dim and
+                c.head_dim % 16 == 0)
+
     def _x(self, T: int) -> DA:
         """The residual stream x as it stands (one of the two x buffers)."""
         return self.xs[self._cur].view((T, self.cfg.hidden))
@@ -333,15 +350,19 @@ class LayerStep:
         self._put(h, hn)
 
     def _project(self, wts: BlockWeights, resid, wname, mats, ys, rows, T, h_ready,
-                 s) -> None:
-        """ys[m] = rmsnorm(x (+ resid)) W_m^T, the norm folded when it can be."""
+                 s, rope=None) -> None:
+        """ys[m] = rmsnorm(x (+ resid)) W_m^T, the norm folded when it can be
+        (and the RoPE of `rope` on the first outputs, which needs that path)."""
         c = self.cfg
         norm_w = wts.dev[wname]
         if not h_ready and self._folds_norm(T):
             xi, xo = self._advance(T, resid)
             ops.norm_matmul(c.wtype, mats, xi, ys, rows, c.hidden, T, norm_w=norm_w,
-                            eps=c.eps, unit_offset=c.unit_offset, d=resid, x_out=xo, stream=s)
+                            eps=c.eps, unit_offset=c.unit_offset, d=resid, x_out=xo, rope=rope,
+                            stream=s)
             return
+        if rope is not None:
+            raise ValueError("_project: RoPE folds only into the folded-norm projection")
         h = self.h.view((T, c.hidden))
         if not h_ready:
             self._norm(wts, self._x(T), resid, wname, h, T, s)

@@ -303,11 +303,18 @@ def _norm_flag(norm: bool, unit_offset: bool) -> int:
 def norm_matmul(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_cols: int,
                 n_tok: int, norm_w: DeviceArray | None = None, eps: float = 1e-5,
                 norm: bool = True, unit_offset: bool = False, d: DeviceArray | None = None,
-                x_out: DeviceArray | None = None, stream: Stream | None = None) -> None:
+                x_out: DeviceArray | None = None, rope: dict | None = None,
+                stream: Stream | None = None) -> None:
     """ys[m] = rmsnorm(x') @ W_m^T for up to 4 matrices of one type sharing x'
     (q, k, v), any token count; x' = x + d (stored to x_out, default x) when
     d is given, else x. The split GEMM folds the add and the norm into its
-    x pre-pass (Q4_K / Q5_K, 32+ tokens)."""
+    x pre-pass (Q4_K / Q5_K, 32+ tokens); below 32 tokens the fused decode
+    GEMV takes them in its prologue.
+
+    rope = {"n": 1 or 2, "head_dim": D, "mode": ROPE_NEOX / ROPE_INTERLEAVED,
+    "pos": int32 [n_tok], "inv_freq": [D/2]} also rotates the first n outputs
+    (q, k) over every channel: in the fused GEMV's epilogue when it takes
+    the call, else by the RoPE pass after the projections."""
     if not 1 <= len(ws) <= 4 or len(ys) != len(ws) or len(n_rows) != len(ws):
         raise ValueError("norm_matmul: 1 to 4 matrices, with as many outputs and row counts")
     if d is not None and x_out is None:
@@ -325,11 +332,23 @@ def norm_matmul(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_
     L = _lib.lib()
     wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, 0, n_tok)
     buf = _norm_mm_ws.get(wsb)
-    _lib.check(L.aero_hip_norm_matmul(int(dtype), k, wp, wb, nr, yp, x.ptr, as_ptr(d),
-                                      as_ptr(x_out), as_ptr(norm_w), float(eps),
-                                      _norm_flag(norm, unit_offset), n_cols, n_tok, as_ptr(buf),
-                                      0 if buf is None else buf.nbytes, _s(stream)),
-               "norm_matmul")
+    if rope is None:
+        _lib.check(L.aero_hip_norm_matmul(int(dtype), k, wp, wb, nr, yp, x.ptr, as_ptr(d),
+                                          as_ptr(x_out), as_ptr(norm_w), float(eps),
+                                          _norm_flag(norm, unit_offset), n_cols, n_tok,
+                                          as_ptr(buf), 0 if buf is None else buf.nbytes,
+                                          _s(stream)), "norm_matmul")
+        return
+    D = int(rope["head_dim"])
+    _need(rope["pos"], n_tok, np.int32, "rope pos")
+    _need(rope["inv_freq"], D // 2, np.float32, "rope inv_freq")
+    _lib.check(L.aero_hip_norm_matmul_rope(int(dtype), k, wp, wb, nr, yp, x.ptr, as_ptr(d),
+                                           as_ptr(x_out), as_ptr(norm_w), float(eps),
+                                           _norm_flag(norm, unit_offset), n_cols, n_tok,
+                                           int(rope["n"]), D, int(rope.get("mode", ROPE_NEOX)),
+                                           rope["pos"].ptr, rope["inv_freq"].ptr, as_ptr(buf),
+                                           0 if buf is None else buf.nbytes, _s(stream)),
+               "norm_matmul_rope")
 
 
 def norm_matmul_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceArray,

@@ -334,7 +334,11 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * Q4_K / Q5_K with 32 or more tokens (weights 16-byte aligned) run the
  * split-x fp16 GEMM with h never written: each token's sums are scaled by
  * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
- * epilogue. Other types and shapes run add+norm into the workspace, the
+ * epilogue. Below 32 tokens, rows of a multiple of 16 bytes run the fused
+ * decode GEMVs, every matrix (or gate/up with the act-mul) in one launch: at
+ * one token (two without d) with the add and the norm in their prologue
+ * (x_out then must overlap neither x nor d; otherwise the add + norm pass
+ * runs first). Other types and shapes run add+norm into the workspace, the
  * library GEMM per matrix and the act-mul. Each result equals that
  * composition to 1e-5 of its scale. ws (16-byte aligned) of at least
  * aero_hip_norm_matmul_workspace(dtype, n_cols, n_ff (0 for the plain
@@ -352,6 +356,24 @@ int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t
                                  const float* norm_w, float eps, int norm, int act, float* out,
                                  int64_t n_ff, int64_t n_cols, int64_t n_tok, void* ws,
                                  int64_t ws_bytes, void* stream);
+
+/* aero_hip_norm_matmul, then RoPE on the outputs of its first n_rope (1 or
+ * 2) matrices, q [n_tok, n_rows[0]] and k [n_tok, n_rows[1]] as heads of
+ * head_dim rows: every channel rotated (n_rot = head_dim) at positions pos
+ * [n_tok] with inv_freq [head_dim/2], mode AERO_ROPE_NEOX or
+ * AERO_ROPE_INTERLEAVED. That is the projection and rotation of
+ * src/attention_layer.cpp:60-156 without the per-head norms, and equals
+ * aero_hip_norm_matmul followed by aero_hip_qk_norm_rope (no norm weights,
+ * n_rot = head_dim). When the call takes the fused decode GEMV (below 32
+ * tokens; NeoX heads a multiple of 16 rows) the rotation runs in its
+ * epilogue: the partner rows of a pair are computed by the same workgroup
+ * and meet in LDS. Otherwise the RoPE pass follows the projections. */
+int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
+                              const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                              const float* x, const float* d, float* x_out, const float* norm_w,
+                              float eps, int norm, int64_t n_cols, int64_t n_tok, int n_rope,
+                              int64_t head_dim, int rope_mode, const int32_t* pos,
+                              const float* inv_freq, void* ws, int64_t ws_bytes, void* stream);
 
 /* aero_hip_matmul without a workspace argument and without allocating: the
  * split-x GEMM's workspace is a device array inside the library, of

@@ -192,3 +192,21 @@ def test_layer_refuses_without_host_path(hip):
     step.prepare(ids, kv_len)
     with pytest.raises(select.HostPathRequired):
         step.forward(ids.size, kv_len)
+
+
+def test_layer_decode_rope_fold(hip, oracle):
+    """At one token the q/k/v GEMV rotates q and k in its epilogue: the
+    Llama-3-8B decode block records one launch fewer than with rope_gemm
+    off, and both match the oracle."""
+    from aero_amd.device import Plan
+
+    counts = {}
+    for fold in (True, False):
+        step = run_and_check(oracle, "llama3_8b_decode", fusions={"rope_gemm": fold})
+        cfg = step.cfg
+        plan = Plan()
+        with plan:
+            step.forward(1, CASES["llama3_8b_decode"][4])
+        counts[fold] = len(plan)
+        plan.destroy()
+    assert counts[True] == counts[False] - 1, counts

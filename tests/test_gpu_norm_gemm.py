@@ -217,3 +217,99 @@ def test_norm_matmul_refusals(hip):
                                           x.ptr, None, None, None, 1e-5, 0, 0, out.ptr, n_ff,
                                           n_cols, n_tok, ws_gu.ptr, need_gu, None) == 0
     assert "workspace" in _lib.last_error()
+
+
+@pytest.mark.parametrize("t,n_tok,n_cols,head_dim,n_heads,mode,resid,n_rope", [
+    # one token: the fused GEMV's prologue (add + norm) and RoPE epilogue
+    (W.Q4_K, 1, 4096, 128, (4, 2, 2), 0, True, 2),
+    (W.Q4_K, 1, 4096, 128, (4, 2, 2), 1, False, 2),
+    (W.Q8_0, 1, 1024, 64, (4, 2, 2), 0, True, 1),
+    (W.Q4_K, 1, 5120, 128, (2, 1), 0, True, 2),          # two-step rows
+    (W.IQ4_XS, 2, 1024, 64, (3, 1, 1), 0, False, 2),     # two tokens, norm in the prologue
+    (W.Q5_K, 3, 2048, 128, (2, 1, 1), 0, True, 2),       # add + norm pass, RoPE epilogue
+    (W.Q4_K, 4, 1024, 64, (4, 2, 2), 1, True, 2),        # four tokens: 4 rows a wave
+    (W.Q4_K, 5, 8192, 128, (2, 1, 1), 0, False, 2),
+    (W.Q4_K, 1, 1024, 48, (4, 2, 2), 0, True, 2),        # heads of 48 rows, 6 workgroups a head
+    (W.Q4_K, 1, 1024, 40, (4, 2, 2), 0, True, 2),        # NeoX heads of 40 rows: RoPE pass
+    (W.Q6_K, 2, 1024, 64, (2, 1, 1), 0, True, 2),        # 840-byte rows: separate launches
+    (W.Q4_K, 40, 1024, 128, (2, 1, 1), 0, True, 2),      # split GEMM, then the RoPE pass
+])
+def test_norm_matmul_rope_vs_oracle(hip, oracle, t, n_tok, n_cols, head_dim, n_heads, mode,
+                                    resid, n_rope):
+    """aero_hip_norm_matmul_rope: the projections of the norm (and residual
+    add), then RoPE over every channel of the first n_rope outputs (q, k)
+    at the tokens' positions, against the oracle's rmsnorm -> matmul ->
+    qk_norm_rope (src/attention_layer.cpp:60-156 without the head norms).
+    The fused decode GEMV rotates in its epilogue (NeoX partners 64 rows
+    apart meet in LDS); other paths run the RoPE pass; both to 1e-5."""
+    rng = np.random.default_rng(n_tok * 31 + n_cols + head_dim + mode + t)
+    rows = tuple(h * head_dim for h in n_heads)
+    x = rng.standard_normal((n_tok, n_cols), dtype=np.float32)
+    d = rng.standard_normal((n_tok, n_cols), dtype=np.float32) if resid else None
+    w = (rng.standard_normal(n_cols, dtype=np.float32) * np.float32(0.1) + 1).astype(np.float32)
+    mats = [weights(t, r, n_cols, rng) for r in rows]
+    pos = rng.integers(0, 16384, n_tok).astype(np.int32)
+    theta = 500000.0
+    n_rot, inv = ops.rope_inv_freq(head_dim, None, theta)
+    assert n_rot == head_dim
+    print(f"norm_matmul_rope type={t} tok={n_tok} cols={n_cols} D={head_dim} heads={n_heads} "
+          f"mode={mode} resid={resid} n_rope={n_rope}", flush=True)
+    dx, dw = DA.from_numpy(x), DA.from_numpy(w)
+    dd = None if d is None else DA.from_numpy(d)
+    xo = DA.empty(x.shape) if resid else None
+    ys = [DA.empty((n_tok, r)) for r in rows]
+    rope = {"n": n_rope, "head_dim": head_dim, "mode": mode, "pos": DA.from_numpy(pos),
+            "inv_freq": DA.from_numpy(inv)}
+    ops.norm_matmul(t, [DA.from_numpy(m) for m in mats], dx, ys, list(rows), n_cols, n_tok,
+                    norm_w=dw, eps=1e-5, d=dd, x_out=xo, rope=rope)
+    xs, h = oracle_h(oracle, x, d, w, 1e-5, False)
+    if resid:
+        assert bits_equal(xo.numpy(), xs)
+    # the fold adds no launch; the RoPE pass adds one
+    from aero_amd.device import Plan
+    rb = n_cols // W.BLOCK[t][0] * W.BLOCK[t][1]
+    folds = n_tok < 32 and rb % 16 == 0 and (mode == 1 or head_dim % 16 == 0)
+    dmats = [DA.from_numpy(mm) for mm in mats]
+    counts = []
+    for rp in (None, rope):
+        plan = Plan()
+        with plan:
+            ops.norm_matmul(t, dmats, dx, [DA.empty((n_tok, r)) for r in rows], list(rows),
+                            n_cols, n_tok, norm_w=dw, eps=1e-5, d=dd, x_out=xo, rope=rp)
+        counts.append(len(plan))
+        plan.destroy()
+    assert counts[1] == counts[0] + (0 if folds else 1), counts
+    for m, (y, mat, r) in enumerate(zip(ys, mats, rows)):
+        want = oracle.matmul(t, mat, h, r)
+        if m < n_rope:
+            want = oracle.qk_norm_rope(want, n_tok, r // head_dim, head_dim, head_dim, pos, theta,
+                                       mode).reshape(n_tok, r)
+        assert rel_to_scale(y.numpy(), want) <= RTOL, f"matrix {m}"
+
+
+def test_norm_matmul_rope_refusals(hip):
+    """Refused before any launch: rows that are not whole heads, an odd head
+    size, no positions, more rotated matrices than given."""
+    import ctypes
+    L = _lib.lib()
+    n_cols, D = 1024, 64
+    x = DA.empty((1, n_cols))
+    m = DA.empty((96 * n_cols // 256 * 144,), np.uint8)
+    y = DA.empty((1, 96))
+    pos = DA.from_numpy(np.zeros(1, np.int32))
+    inv = DA.from_numpy(np.ones(D // 2, np.float32))
+    ws = DA.empty((1 << 20,), np.uint8)
+
+    def call(rows, D, n_rope, pos_ptr):
+        wp = (ctypes.c_void_p * 1)(m.ptr)
+        wb = (ctypes.c_int64 * 1)(m.nbytes)
+        nr = (ctypes.c_int64 * 1)(rows)
+        yp = (ctypes.c_void_p * 1)(y.ptr)
+        return L.aero_hip_norm_matmul_rope(W.Q4_K, 1, wp, wb, nr, yp, x.ptr, None, None, None,
+                                           1e-5, 0, n_cols, 1, n_rope, D, 0, pos_ptr, inv.ptr,
+                                           ws.ptr, ws.nbytes, None)
+    assert call(96, 64, 1, pos.ptr) == 0 and "whole heads" in _lib.last_error()
+    assert call(96, 33, 1, pos.ptr) == 0
+    assert call(64, 64, 1, None) == 0
+    assert call(64, 64, 2, pos.ptr) == 0
+    assert call(64, 64, 1, pos.ptr) == 1
