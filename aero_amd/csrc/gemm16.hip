@@ -794,6 +794,7 @@ int64_t dtype_block_values(int t);
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
               int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s, void* ws,
               int64_t ws_bytes);
+bool lanes64_ok(int dtype, const uint8_t* w, int64_t rb, int64_t n_rows, int64_t w_bytes);
 bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                     const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                     const float* x, const float* norm_w, float eps, int norm, int act,
@@ -882,15 +883,16 @@ int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n
 namespace {
 
 // The fused decode GEMVs take the call's matrices in one launch (a group of
-// up to 4 tokens): few tokens, 16-byte aligned rows of whole 16 bytes, at
+// up to 4 tokens): few tokens, matrices the 64-column lane kernels take
+// (lanes64_ok: 16-byte aligned rows of whole 16 bytes, Q8_0 also of 8), at
 // most 3 matrices (or the gate/up pair).
-bool fused_gemv_rows_ok(const SplitJob& j, bool gu) {
-    if (j.n_tok >= tune("gemm_min_tokens", 32) || j.rb % 16 != 0 || (!gu && j.n_mat > 3) ||
+bool fused_gemv_rows_ok(const SplitJob& j, bool gu, const int64_t* w_bytes) {
+    if (j.n_tok >= tune("gemm_min_tokens", 32) || (!gu && j.n_mat > 3) ||
         !tune("gemv_lanes64", 1) || !tune("fused_gemv", 1))
         return false;
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m)
-        if (!aligned16(j.w[m])) return false;
-    return !gu || aligned16(j.w_up);
+        if (!lanes64_ok(j.dtype, j.w[m], j.rb, j.n_rows[m], w_bytes[m])) return false;
+    return !gu || lanes64_ok(j.dtype, j.w_up, j.rb, j.n_rows[0], w_bytes[0]);
 }
 
 // ... and also the norm (and residual add) in their prologue: every
@@ -967,7 +969,7 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
                  j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
-    const bool fused = !split && fused_gemv_rows_ok(j, gu);
+    const bool fused = !split && fused_gemv_rows_ok(j, gu, w_bytes);
     if (fused && fused_prologue_ok(j))
         return fused_gemv_run(j, gu, w_bytes, j.x, j.norm, j.d, s, rope_done);
     const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)

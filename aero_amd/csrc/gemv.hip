@@ -4,9 +4,10 @@
 // (:78-250), which it calls between the elementwise ops of a layer.
 //
 // Two kernels, both workgroups of kGemvWaves waves that share x through LDS:
-//   gemv64_kernel (rows of a multiple of 16 bytes, W 16-byte aligned: every
-//     common shape): lane l of a 4096-column step owns columns 64l..64l+63
-//     and loads only its bytes of each row with 16-byte loads;
+//   gemv64_kernel (rows of a multiple of 16 bytes, Q8_0 rows also of 8, W
+//     16-byte aligned: every common shape): lane l of a 4096-column step
+//     owns columns 64l..64l+63 and loads only its bytes of each row with
+//     16-byte loads;
 //   gemv_kernel (any row length, W 4-byte aligned): lane l of a 2048-column
 //     step owns a 32-value group, loaded as 4-byte words.
 // Each wave owns R rows; the row sums are xor-butterflies over the wave.
@@ -826,17 +827,23 @@ template <> struct Lane64<AERO_DTYPE_IQ4_XS> {
 };
 
 // Q8_0 (src/kernels.cpp:78-84): the lane's two blocks are 68 bytes at byte
-// 68l of the step (4-byte aligned), loaded as the five aligned chunks around
-// them; u = q ^ 0x80 = q + 128.
+// 68l of the step, loaded as the five 16-byte-aligned chunks around them;
+// u = q ^ 0x80 = q + 128. Rows start on 8-byte boundaries at least (the
+// 896-column rows of 952 bytes alternate between 16- and 8-byte aligned),
+// so the blocks' absolute address is 4-byte aligned and ph in {0,4,8,12}.
 template <> struct Lane64<AERO_DTYPE_Q8_0> {
     uint4 c[5];
     uint32_t ph;  // byte offset of the blocks within c
     __device__ __forceinline__ void load(const uint8_t* rowp, int st, int l, int n_blk) {
-        // n_blk is a multiple of 8: clamp to the last even block pair
+        // n_blk is a multiple of 4: clamp to the last even block pair
         const uint32_t kc = (uint32_t)min(st * 128 + 2 * l, n_blk - 2);
         const uint32_t ob = kc * 34u;
-        ph = ob & 15u;
-        const uint8_t* base = rowp + (ob - ph);
+        // the 16-byte boundary at or below the blocks' absolute address (ph
+        // may exceed ob on a row that starts 8 bytes past a boundary, so the
+        // base is not formed as rowp + (ob - ph) in 32-bit arithmetic)
+        const uintptr_t a = reinterpret_cast<uintptr_t>(rowp) + ob;
+        ph = (uint32_t)(a & 15u);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(a - ph);
 #pragma unroll
         for (int i = 0; i < 5; ++i) c[i] = ld128(base + 16 * i);
     }
@@ -1479,6 +1486,20 @@ GemvKernel pick_gemv(int dtype, int R, int T) {
 
 // y[t, r] for t < n_tok: tokens are taken in groups of up to 4 per launch
 // (each group re-reads W; a token-tiled GEMM is the prefill path).
+// Whether a matrix takes the 64-column lane kernels (gemv64_kernel and the
+// fused decode GEMVs): W 16-byte aligned with rows of whole 16 bytes, or a
+// Q8_0 matrix with rows of whole 8 bytes whose lane windows are placed from
+// the absolute address. The window of the last row's final block pair ends
+// at the first 16-byte boundary at or past that row (up to 8 bytes beyond
+// it), which must lie inside w_bytes.
+bool lanes64_ok(int dtype, const uint8_t* w, int64_t rb, int64_t n_rows, int64_t w_bytes) {
+    if (!aligned16(w)) return false;
+    if (rb % 16 == 0) return true;
+    if (dtype != AERO_DTYPE_Q8_0 || rb % 8 != 0 || n_rows <= 0) return false;
+    const int64_t end = n_rows * rb;
+    return w_bytes >= end + ((16 - (end & 15)) & 15);
+}
+
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
               int64_t n_rows, int64_t n_cols, int64_t n_tok, hipStream_t s, void* ws,
               int64_t ws_bytes) {
@@ -1520,7 +1541,7 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         }
         return gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, s);
     }
-    if (aligned16(w) && rb % 16 == 0 && tune("gemv_lanes64", 1)) {
+    if (lanes64_ok(dtype, w, rb, n_rows, w_bytes) && tune("gemv_lanes64", 1)) {
         const bool pipe = n_cols > kStepCols;
         const int t_max = pipe ? 2 : 4;  // double-buffered x of 4 tokens would fill LDS
         for (int64_t t0 = 0; t0 < n_tok; t0 += t_max) {
@@ -1615,9 +1636,8 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
         return false;
     }
     const int64_t rb = (n_cols / bv) * bb;
-    if (rb % 16 != 0 || !aligned16(x) || (norm_w != nullptr && !aligned16(norm_w))) {
-        set_error("%s: rows must be a multiple of 16 bytes, x and the norm weight 16-byte "
-                  "aligned", what);
+    if (!aligned16(x) || (norm_w != nullptr && !aligned16(norm_w))) {
+        set_error("%s: x and the norm weight must be 16-byte aligned", what);
         return false;
     }
     if (d != nullptr) {
@@ -1636,10 +1656,12 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
     }
     for (int m = 0; m < n_mat; ++m) {
         if (w[m] == nullptr || y[pair ? 0 : m] == nullptr || n_rows[m] < 0 ||
-            n_rows[m] > (int64_t)1 << 31 || !aligned16(w[m]) || w_bytes[m] < n_rows[m] * rb ||
+            n_rows[m] > (int64_t)1 << 31 || w_bytes[m] < n_rows[m] * rb ||
+            !lanes64_ok(dtype, w[m], rb, n_rows[m], w_bytes[m]) ||
             (pair && n_rows[m] != n_rows[0])) {
-            set_error("%s: matrix %d: null, misaligned (16 bytes), short, or rows differ", what,
-                      m);
+            set_error("%s: matrix %d: null, short, rows differ, or not 16-byte aligned with rows "
+                      "of whole 16 bytes (Q8_0: 8, with the last row's 16-byte window inside "
+                      "w_bytes)", what, m);
             return false;
         }
     }

@@ -149,7 +149,12 @@ class LayerStep:
         self.n_rot, self.inv = n_rot, DA.from_numpy(inv)
         self.scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
         rb = (N // W.BLOCK[cfg.wtype][0]) * W.BLOCK[cfg.wtype][1]
-        self.rows16 = rb % 16 == 0        # rows fit the fused decode GEMVs
+        # rows fit the fused decode GEMVs: whole 16 bytes, or Q8_0 rows of
+        # whole 8 bytes in matrices (allocated to size) ending on a 16-byte
+        # boundary
+        rows_n = (cfg.n_head * D, cfg.n_head_kv * D, F)
+        self.rows16 = rb % 16 == 0 or (cfg.wtype == W.Q8_0 and rb % 8 == 0 and
+                                       all(n * rb % 16 == 0 for n in rows_n))
 
     # ------------------------------------------------------------ selection
     def gpu(self, op: str) -> bool:

@@ -302,8 +302,10 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * xn = x normalised as aero_hip_rmsnorm with weight norm_w (nullable: ones)
  * and flags `norm` (0 or AERO_NORM_UNIT_OFFSET); norm < 0: xn = x. act is an
  * AERO_ACT_* kind. Weights 16-byte aligned with rows of a multiple of 16
- * bytes (the gemv fast path), x and norm_w 16-byte aligned; tokens are taken
- * up to 4 a launch. */
+ * bytes (the gemv fast path; Q8_0 rows of a multiple of 8 bytes too, such
+ * as the 952-byte rows of 896 columns, when w_bytes also covers the 16-byte
+ * boundary at or after the last row's end), x and norm_w 16-byte aligned;
+ * tokens are taken up to 4 a launch. */
 int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w,
                          const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                          const float* x, const float* norm_w, float eps, int norm,
@@ -334,7 +336,7 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * Q4_K / Q5_K with 32 or more tokens (weights 16-byte aligned) run the
  * split-x fp16 GEMM with h never written: each token's sums are scaled by
  * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
- * epilogue. Below 32 tokens, rows of a multiple of 16 bytes run the fused
+ * epilogue. Below 32 tokens, rows the fused decode GEMVs take (above) run the fused
  * decode GEMVs, every matrix (or gate/up with the act-mul) in one launch: at
  * one token (two without d) with the add and the norm in their prologue
  * (x_out then must overlap neither x nor d; otherwise the add + norm pass

@@ -142,8 +142,9 @@ def test_norm_gate_up_llama_decode(hip, oracle):
 
 def test_fused_refusals(hip):
     """Four matrices, a type without a GEMV, misaligned weights, rows not a
-    multiple of 16 bytes (Q6_K at 1024 columns: 840 bytes) and gate/up of
-    different sizes are refused with an error, nothing launched."""
+    multiple of 16 bytes (Q6_K at 1024 columns: 840 bytes; Q8_0 rows of 952
+    bytes in an odd number) and gate/up of different sizes are refused with
+    an error, nothing launched."""
     rng = np.random.default_rng(51)
     w = DA.from_numpy(table(W.Q4_K, 64, 1024, rng))
     x = DA.from_numpy(rng.standard_normal((1, 1024)).astype(np.float32))
@@ -153,8 +154,14 @@ def test_fused_refusals(hip):
     with pytest.raises(_lib.AeroHipError):
         ops.norm_matvec(W.F32, [w], x, ys[:1], [64], 1024)
     w6 = DA.from_numpy(table(W.Q6_K, 64, 1024, rng))
-    with pytest.raises(_lib.AeroHipError, match="multiple of 16"):
+    with pytest.raises(_lib.AeroHipError, match="whole 16 bytes"):
         ops.norm_matvec(W.Q6_K, [w6], x, ys[:1], [64], 1024)
+    # Q8_0 rows of 952 bytes: an odd row count ends 8 bytes short of a
+    # 16-byte boundary, which the last lane window would read past the weights
+    w8 = DA.from_numpy(table(W.Q8_0, 127, 896, rng))
+    x8 = DA.from_numpy(rng.standard_normal((1, 896)).astype(np.float32))
+    with pytest.raises(_lib.AeroHipError, match="window"):
+        ops.norm_matvec(W.Q8_0, [w8], x8, [DA.empty((1, 127))], [127], 896)
     L = _lib.lib()
     wp = (ctypes.c_void_p * 1)(w.ptr + 4)                    # 4-byte aligned only
     wb = (ctypes.c_int64 * 1)(w.nbytes - 4)
@@ -168,3 +175,32 @@ def test_fused_refusals(hip):
         ops.norm_gate_up(W.Q4_K, w, w2, x, DA.empty((1, 64)), 64, 1024)
     with pytest.raises(_lib.AeroHipError):                    # 64 rows need 64 * 576 bytes
         ops.norm_gate_up(W.Q4_K, w2, w2, x, DA.empty((1, 64)), 64, 1024)
+
+
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_fused_q8_0_qwen2_0p5b_rows(hip, oracle, n_tok):
+    """Qwen2-0.5B's decode projections in Q8_0 (896 columns: 952-byte rows,
+    every other one 8 bytes off a 16-byte boundary): RMSNorm + q/k/v (896,
+    128, 128 rows) and RMSNorm + gate/up (4864) + SiLU·mul in one launch
+    each, against the oracle's rmsnorm -> matmul (-> act_mul)."""
+    rng = np.random.default_rng(91 + n_tok)
+    N, F = 896, 4864
+    x = rng.standard_normal((n_tok, N)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    rows = (896, 128, 128)
+    mats = [table(W.Q8_0, r, N, rng) for r in rows]
+    dx, dw = DA.from_numpy(x), DA.from_numpy(nw)
+    ys = [DA.empty((n_tok, r)) for r in rows]
+    print(f"fused Q8_0 896 tokens={n_tok}", flush=True)
+    ops.norm_matvec(W.Q8_0, [DA.from_numpy(m) for m in mats], dx, ys, list(rows), N, n_tok,
+                    norm_w=dw, eps=1e-6)
+    xn = oracle.rmsnorm_rows(x, nw, 1e-6)
+    for y, m, r in zip(ys, mats, rows):
+        assert rel_to_scale(y.numpy(), want_proj(oracle, W.Q8_0, m, xn, r)) <= RTOL
+    wg, wu = table(W.Q8_0, F, N, rng), table(W.Q8_0, F, N, rng)
+    out = DA.empty((n_tok, F))
+    ops.norm_gate_up(W.Q8_0, DA.from_numpy(wg), DA.from_numpy(wu), dx, out, F, N, n_tok,
+                     act="silu", norm_w=dw, eps=1e-6)
+    want = oracle.act_mul(SILU, oracle.matmul(W.Q8_0, wg, xn, F),
+                          oracle.matmul(W.Q8_0, wu, xn, F))
+    assert rel_to_scale(out.numpy(), want) <= RTOL

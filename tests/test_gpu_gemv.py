@@ -54,6 +54,24 @@ def test_matvec_vs_oracle(hip, oracle, t, n_rows, n_cols, n_tok):
     assert rel_to_scale(got, want) <= RTOL
 
 
+@pytest.mark.parametrize("n_rows,n_cols,n_tok", [
+    (896, 896, 1), (128, 896, 3), (4864, 896, 1), (127, 896, 2), (64, 640, 5),
+])
+def test_matvec_q8_0_rows_of_8_bytes(hip, oracle, n_rows, n_cols, n_tok):
+    """Q8_0 rows of a multiple of 8 bytes but not of 16 (896 columns: 952
+    bytes, Qwen2-0.5B; 640: 680) alternate between 16- and 8-byte aligned
+    starts: the 64-column lane kernel places each lane's 16-byte window from
+    the absolute address. With an odd row count the last row ends 8 bytes
+    short of a 16-byte boundary, past the weights: that matrix takes the
+    word kernel. Both match the oracle."""
+    t = W.Q8_0
+    rng = np.random.default_rng(n_rows + n_cols + n_tok)
+    w = W.make_table(t, n_rows * n_cols // 32, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    print(f"matvec Q8_0 rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
+    assert rel_to_scale(gpu_matvec(t, w, X, n_rows), oracle.matmul(t, w, X, n_rows)) <= RTOL
+
+
 @pytest.mark.parametrize("t", [W.Q8_0, W.Q6_K])
 def test_matvec_rows_off_word_boundary(hip, oracle, t):
     """Row sizes that are not a multiple of 4 bytes (Q8_0 with 45 blocks per row,

@@ -233,6 +233,7 @@ def test_norm_matmul_refusals(hip):
     (W.Q4_K, 1, 1024, 40, (4, 2, 2), 0, True, 2),        # NeoX heads of 40 rows: RoPE pass
     (W.Q6_K, 2, 1024, 64, (2, 1, 1), 0, True, 2),        # 840-byte rows: separate launches
     (W.Q4_K, 40, 1024, 128, (2, 1, 1), 0, True, 2),      # split GEMM, then the RoPE pass
+    (W.Q8_0, 1, 896, 64, (14, 2, 2), 0, True, 2),        # Qwen2-0.5B: 952-byte rows
 ])
 def test_norm_matmul_rope_vs_oracle(hip, oracle, t, n_tok, n_cols, head_dim, n_heads, mode,
                                     resid, n_rope):
@@ -268,7 +269,9 @@ def test_norm_matmul_rope_vs_oracle(hip, oracle, t, n_tok, n_cols, head_dim, n_h
     # the fold adds no launch; the RoPE pass adds one
     from aero_amd.device import Plan
     rb = n_cols // W.BLOCK[t][0] * W.BLOCK[t][1]
-    folds = n_tok < 32 and rb % 16 == 0 and (mode == 1 or head_dim % 16 == 0)
+    lanes = rb % 16 == 0 or (t == W.Q8_0 and rb % 8 == 0 and
+                             all(r * rb % 16 == 0 for r in rows))
+    folds = n_tok < 32 and lanes and (mode == 1 or head_dim % 16 == 0)
     dmats = [DA.from_numpy(mm) for mm in mats]
     counts = []
     for rp in (None, rope):
