@@ -575,8 +575,8 @@ def traffic_from_profiles(kernel_tag):
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
-              "(every op is row-independent: see DESIGN.md for how it shards).",
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported "
+              "(every op of the path is row-independent, so N GPUs each take 1/N of the rows).",
               file=sys.stderr)
         return 2
     from aero_amd import _lib, workloads as W

@@ -1,7 +1,7 @@
 /* oracle/cpuref.c -- fp32 part of the CPU restatement (norms, activations,
  * RoPE, gated norm).
  *
- * TEST INFRASTRUCTURE: the checker for the HIP path, and the "port" CPU
+ * TEST INFRASTRUCTURE: the oracle of the HIP path, and the "port" CPU
  * baseline. Built with gcc -O2 -ffp-contract=off and no -ffast-math, as the
  * reference builds its fp32 libraries (Makefile:74-76,144-154), so every
  * multiply and add rounds separately and summation is serial in fp32.
@@ -87,7 +87,7 @@ static float silu_div(float v) { return v / (1.0f + expf(-v)); }
  * 346-348). For each `group`-long slice of a row: ss over the slice,
  * denom = sqrt(ss/group + eps), out = ((x/denom) * w[col % w_len]) * silu(z),
  * where col is the column inside the `inner`-long row. group = inner is the
- * reference (whole-row RMS, F4 in the survey); a smaller group that divides
+ * reference (whole-row RMS over the inner dimension); a smaller group that divides
  * inner is the per-head reading. */
 void cr_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
                            int64_t w_len, float* out, int64_t rows,

@@ -1,6 +1,6 @@
 /* oracle/cpuref.h -- CPU restatement of Aero's fused per-layer elementwise path.
  *
- * TEST INFRASTRUCTURE. This library is the checker, never the product: only
+ * TEST INFRASTRUCTURE. This library checks the product and is never part of it: only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
  * The GPU path in aero_amd/ never calls it and has no CPU fallback.
  *

@@ -1,6 +1,6 @@
 /* oracle/cpuref_quant.c -- GGUF block dequant and embedding row gather.
  *
- * TEST INFRASTRUCTURE: the checker for the HIP gather/dequant kernels and the
+ * TEST INFRASTRUCTURE: the oracle of the HIP gather/dequant kernels and the
  * "port" CPU baseline. Built with -O2 -ffast-math -fno-math-errno -pthread as
  * the reference builds src/kernels.cpp (Makefile:29), plus -ffp-contract=off
  * so d*q and f*q - g round as separate IEEE operations.

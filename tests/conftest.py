@@ -48,7 +48,7 @@ def bits_equal(a, b) -> bool:
 
 @pytest.fixture(scope="session")
 def hip():
-    """The HIP library on a GPU box. Fails (never skips) when it is missing, so
+    """The HIP library, on a machine with a GPU. Fails (never skips) when it is missing, so
     a GPU run cannot pass on a silent fallback."""
     from aero_amd import _lib
 

@@ -22,7 +22,7 @@ where the reference tree exists):
    matmul over each of those block types, row softmax, GQA attention (causal
    with positions, a window, shuffled key positions) and the int8 / int4 KV
    vector quantisers. These pin the oracle and the GPU
-   path where the reference build is absent (the GPU box).
+   path on machines where the reference build is absent.
 """
 from __future__ import annotations
 

@@ -1,4 +1,4 @@
-"""CPU: pin the oracle (oracle/cpuref*.c) before trusting it as the checker.
+"""CPU: pin the oracle (oracle/cpuref*.c) before trusting it to check the GPU path.
 
 Every function is checked against at least one of: the reference's own C++
 outputs (golden vectors from oracle/_ref, committed, and the live build when
