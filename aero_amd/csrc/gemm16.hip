@@ -761,6 +761,22 @@ bool split_run(const SplitJob& j, hipStream_t s) {
 
 }  // namespace
 
+// Whether n_tok tokens over n_rows rows (every matrix of the call) take the
+// split GEMM rather than the GEMV (the shape and a workspace permitting). The
+// GEMV converts and multiply-adds each weight once per token; the split
+// GEMM decodes it once per 32 tokens and runs the products on the matrix
+// cores, but below 32 tokens it fills fewer workgroups. Measured on MI355X
+// at the Llama-3-8B shapes (Q4_K, split / GEMV, µs): 14336 rows at 8 tokens
+// 36.8 / 46.1, at 16 tokens 37.5 / 92.6, at 24 tokens 38.2 / 137.6; 4096
+// rows x 14336 columns at 16 tokens 110.4 / 124.7; 4096 x 4096 at 16
+// tokens 36.3 / 34.9. AERO_HIP_TUNE gemm_split_min_tokens=N sets one
+// threshold instead.
+bool split_tokens_ok(int64_t n_tok, int64_t n_rows) {
+    const int fixed = tune("gemm_split_min_tokens", 0);
+    if (fixed > 0) return n_tok >= fixed;
+    return n_tok >= 16 || (n_tok >= 8 && n_rows >= 8192);
+}
+
 // Workspace bytes of the split-x GEMM for n_tok tokens of n_cols (0 when the
 // type or shape has no split path): the x parts, the sub-block sums and the
 // inverse scales.
@@ -862,8 +878,9 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 // The prefill forms of the model loop's "norm -> projections" and "norm ->
 // gate/up -> act" steps (src/model.cpp:166-178,244-245,279-282): the split
 // path folds the residual add and the RMSNorm into the x pre-pass and the
-// act-mul into the GEMM epilogue. Below 32 tokens, rows of whole 16 bytes
-// take the fused decode GEMVs (every matrix, or gate/up with the act-mul in
+// act-mul into the GEMM epilogue (from the token counts split_tokens_ok
+// gives). With fewer tokens, rows the lane GEMVs take go to the fused
+// decode GEMVs (every matrix, or gate/up with the act-mul in
 // the epilogue, in one launch): at one token (two without a residual) with
 // the norm and the residual add (x_out apart from x and d) in their
 // prologue, else after an add + norm pass into the workspace. Other types and shapes run the same
@@ -875,9 +892,11 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 // a workspace too small for them.
 int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok) {
     if (n_cols <= 0 || n_tok <= 0 || n_ff < 0) return 0;
-    if (split_shape_ok(dtype, n_cols, n_tok) && n_tok >= tune("gemm_min_tokens", 32))
-        return split_ws_bytes(pad_tokens(n_tok), n_cols, true);
-    return align256(n_tok * n_cols * 4) + (n_ff > 0 ? align256(n_tok * n_ff * 4) : 0);
+    const int64_t sep = align256(n_tok * n_cols * 4) + (n_ff > 0 ? align256(n_tok * n_ff * 4) : 0);
+    if (!split_shape_ok(dtype, n_cols, n_tok) || !split_tokens_ok(n_tok, INT64_MAX)) return sep;
+    const int64_t spl = split_ws_bytes(pad_tokens(n_tok), n_cols, true);
+    // below the all-shapes threshold the rows decide the path: room for both
+    return split_tokens_ok(n_tok, 0) ? spl : std::max(spl, sep);
 }
 
 namespace {
@@ -965,8 +984,10 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     if (j.n_tok == 0) return true;
     // the path decides the workspace: the split GEMM's parts, or the separate
     // launches' h (and up) buffers
+    int64_t all_rows = gu ? 2 * n_ff : 0;
+    for (int m = 0; m < (gu ? 0 : j.n_mat); ++m) all_rows += j.n_rows[m];
     bool split = split_shape_ok(j.dtype, j.n_cols, j.n_tok) &&
-                 j.n_tok >= tune("gemm_min_tokens", 32) && j.rb % 16 == 0 && tune("gemm16", 1);
+                 split_tokens_ok(j.n_tok, all_rows) && j.rb % 16 == 0 && tune("gemm16", 1);
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
     const bool fused = !split && fused_gemv_rows_ok(j, gu, w_bytes);

@@ -26,6 +26,7 @@ int64_t dtype_block_bytes(int t);
 bool gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
               int64_t n_cols, int64_t rb, int64_t n_tok, hipStream_t s);
 int64_t split_gemm_workspace(int dtype, int64_t n_cols, int64_t n_tok);
+bool split_tokens_ok(int64_t n_tok, int64_t n_rows);
 bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
                     int64_t n_cols, int64_t rb, int64_t n_tok, void* ws, int64_t ws_bytes,
                     hipStream_t s, bool* ran);
@@ -1530,17 +1531,17 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
         return false;
     }
     if (n_rows == 0 || n_tok == 0) return true;
-    // many tokens: the matrix-core GEMMs (the split-x fp16 one when a
-    // workspace is given and the type has it; else fp32, W once per 64 tokens)
-    if (n_tok >= tune("gemm_min_tokens", 32) && n_tok <= (int64_t)1 << 30) {
-        if (ws != nullptr) {
-            bool ran = false;
-            if (!split_gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, ws, ws_bytes, s, &ran))
-                return false;
-            if (ran) return true;
-        }
-        return gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, s);
+    // several tokens: the matrix-core GEMMs. The split-x fp16 one when a
+    // workspace is given and the type has it (from 8-16 tokens,
+    // split_tokens_ok), else the fp32 one from 32 tokens (W once per 64).
+    if (ws != nullptr && n_tok <= (int64_t)1 << 30 && split_tokens_ok(n_tok, n_rows)) {
+        bool ran = false;
+        if (!split_gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, ws, ws_bytes, s, &ran))
+            return false;
+        if (ran) return true;
     }
+    if (n_tok >= tune("gemm_min_tokens", 32) && n_tok <= (int64_t)1 << 30)
+        return gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, s);
     if (lanes64_ok(dtype, w, rb, n_rows, w_bytes) && tune("gemv_lanes64", 1)) {
         const bool pipe = n_cols > kStepCols;
         const int t_max = pipe ? 2 : 4;  // double-buffered x of 4 tokens would fill LDS

@@ -917,6 +917,11 @@ GEMM_CASES = [
     ("attn_q_4096x4096", 12, 4096, 4096, 512), ("ffn_gate_14336x4096", 12, 14336, 4096, 512),
     ("ffn_down_4096x14336", 12, 4096, 14336, 512), ("q8_0_14336x4096", 8, 14336, 4096, 512),
     ("q6_k_14336x4096", 14, 14336, 4096, 512), ("ffn_gate_14336x4096_t64", 12, 14336, 4096, 64),
+    # few tokens (speculative decoding, small batches): the GEMV below the
+    # split GEMM's token threshold
+    ("ffn_gate_14336x4096_t8", 12, 14336, 4096, 8), ("ffn_gate_14336x4096_t16", 12, 14336, 4096, 16),
+    ("ffn_gate_14336x4096_t24", 12, 14336, 4096, 24), ("attn_q_4096x4096_t16", 12, 4096, 4096, 16),
+    ("ffn_down_4096x14336_t16", 12, 4096, 14336, 16),
 ]
 MFMA_FP32_PEAK_TFLOPS = 157.3
 MFMA_FP16_PEAK_TFLOPS = 2500.0   # dense fp16 matrix peak of MI355X
@@ -947,8 +952,10 @@ def gemm(a):
         X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
         Y = DA.empty((n_tok, n_rows))
         stream = Stream()
-        # Q4_K / Q5_K: the split-x fp16 GEMM (the default), then the fp32 one
-        paths = ["split_fp16", "fp32"] if t in (W.Q4_K, W.Q5_K) else ["fp32"]
+        # Q4_K / Q5_K: the split-x fp16 GEMM (the default), then the call
+        # without a workspace: the fp32 GEMM from 32 tokens, the GEMV below
+        plain = "fp32" if n_tok >= 32 else "gemv"
+        paths = ["split_fp16", plain] if t in (W.Q4_K, W.Q5_K) else [plain]
         for path in paths:
             split = path == "split_fp16"
             for w in ws:
@@ -1059,18 +1066,20 @@ def layer_gemm(a):
 
 
 LAYER_CASES = [
-    # (shape, weight type, tokens, earlier cache positions)
-    ("qwen2_0p5b_decode", 8, 1, 37),
-    ("llama3_8b_prefill", 12, 512, 0),
-    ("llama3_8b_decode", 12, 1, 4095),     # the prefill geometry, one token at 4095
+    # (name, layer geometry, weight type, tokens, earlier cache positions)
+    ("qwen2_0p5b_decode", "qwen2_0p5b_decode", 8, 1, 37),
+    ("llama3_8b_prefill", "llama3_8b_prefill", 12, 512, 0),
+    ("llama3_8b_decode", "llama3_8b_prefill", 12, 1, 4095),    # one token at 4095
+    ("llama3_8b_t16", "llama3_8b_prefill", 12, 16, 4080),      # 16 tokens (speculative step)
 ]
 
 
 def layer_bench(a):
     """One decoder block (aero_amd.layer.LayerStep: embedding, q/k/v, QK-norm +
     RoPE, attention, o, residual + norm, gate/up + act, down, output norm)
-    at the Qwen2-0.5B decode, Llama-3-8B 512-token prefill and Llama-3-8B
-    one-token decode (4095 cached positions) shapes, with
+    at the Qwen2-0.5B decode, Llama-3-8B 512-token prefill, Llama-3-8B
+    one-token decode (4095 cached positions) and Llama-3-8B 16-token
+    (4080 cached positions) shapes, with
     every fusion on and with every fusion off. Four blocks with their own
     weights (rotated, so weights come from HBM as in a deep model), each
     recorded as a plan; µs per block = region / blocks run, between one
@@ -1081,12 +1090,10 @@ def layer_bench(a):
     from aero_amd.device import Event, Plan, Stream
 
     names = a.shapes.split(",") if a.shapes else [c[0] for c in LAYER_CASES]
-    for shape, wtype, T, kv_len in LAYER_CASES:
+    for shape, geom, wtype, T, kv_len in LAYER_CASES:
         if shape not in names:
             continue
-        cfg = layer.BlockConfig.from_shape(W.SHAPES[shape.replace("decode", "prefill")
-                                                     if shape == "llama3_8b_decode" else shape],
-                                           wtype)
+        cfg = layer.BlockConfig.from_shape(W.SHAPES[geom], wtype)
         weights = [layer.BlockWeights(cfg, seed=i) for i in range(4)]
         rng = np.random.default_rng(5)
         ids = rng.integers(0, cfg.vocab, T).astype(np.int32)

@@ -284,7 +284,8 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
                     void* stream);
 
 /* aero_hip_matvec with a workspace, the same call as the reference's matmul
- * (src/kernels.cpp:520-538). With 32 or more tokens of Q4_K or Q5_K and
+ * (src/kernels.cpp:520-538). With 16 or more tokens of Q4_K or Q5_K (8 or
+ * more when the matrix has 8192+ rows, where that is measured faster) and
  * `ws` 16-byte aligned of at least aero_hip_matmul_workspace(dtype, n_cols,
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
  * with x split into two fp16 parts per token and 256 columns (22
@@ -333,10 +334,11 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  *     matrices of one type and width (q, k, v);
  *   aero_hip_norm_matmul_gate_up: out[t*n_ff + r] = act(Wg[r] . h[t]) *
  *     (Wu[r] . h[t]), act an AERO_ACT_* kind.
- * Q4_K / Q5_K with 32 or more tokens (weights 16-byte aligned) run the
+ * Q4_K / Q5_K with 16 or more tokens (8 or more when the call's matrices
+ * have 8192+ rows together; weights 16-byte aligned) run the
  * split-x fp16 GEMM with h never written: each token's sums are scaled by
  * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
- * epilogue. Below 32 tokens, rows the fused decode GEMVs take (above) run the fused
+ * epilogue. Fewer tokens, with rows the fused decode GEMVs take (above), run the fused
  * decode GEMVs, every matrix (or gate/up with the act-mul) in one launch: at
  * one token (two without d) with the add and the norm in their prologue
  * (x_out then must overlap neither x nor d; otherwise the add + norm pass
@@ -385,7 +387,7 @@ int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
  * capture, serving loops, harnesses that forbid allocation). Results equal
  * aero_hip_matmul's with a workspace bit for bit. Returns 0 with a reason
  * when the call would need more scratch than the maximum (n_tok * n_cols *
- * 4 bytes and a little more for Q4_K / Q5_K at 32 or more tokens). Every
+ * 4 bytes and a little more for Q4_K / Q5_K on the split path). Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other host threads) race; calls ordered on one stream do
  * not. Nothing in the array needs clearing between calls. */

@@ -6,13 +6,15 @@ products over the oracle's dequantised weights for the projections (the
 oracle's matmul equals that product to ~1e-6 of scale, tests/test_gpu_gemm16.py).
 
 Checked at the Qwen2-0.5B decode shape (one token at position 37 over a
-cache of 37 earlier positions; Q8_0 weights, whose 896-value rows take the
-separate-launch paths), the Llama-3-8B 512-token prefill (Q4_K weights: the
-split GEMM with the norms folded), a Llama-3-8B one-token decode over 1023
-cached positions (the fused decode GEMVs, chunked attention) and a
-Gemma-style 64-token prefill (QK-norm, (1+w) norms, GeGLU tanh, scaled
-embedding), with every fusion on and with every fusion off, and with host
-hooks standing in for ops taken off the GPU.
+cache of 37 earlier positions; Q8_0 weights, whose 952-byte rows of 896
+values take the fused decode GEMVs), the Llama-3-8B 512-token prefill (Q4_K
+weights: the split GEMM with the norms folded), a Llama-3-8B one-token
+decode over 1023 cached positions (the fused decode GEMVs with RoPE in the
+epilogue, chunked attention), 16 Llama-3-8B tokens over 100 cached
+positions (the split GEMMs below 32 tokens) and a Gemma-style 64-token
+prefill (QK-norm, (1+w) norms, GeGLU tanh, scaled embedding), with every
+fusion on and with every fusion off, and with host hooks standing in for
+ops taken off the GPU.
 Stacks of 2-3 blocks (each with its own weights and KV cache) are checked
 at the same shapes against the oracle's blocks in turn.
 Tolerance 1e-5 of each output's scale; x is the residual stream after the
@@ -39,6 +41,9 @@ CASES = {
     # one token over 1023 cached positions at the Llama-3-8B geometry: the
     # fused decode GEMVs (16-byte Q4_K rows) and the chunked attention
     "llama3_8b_decode": ("llama3_8b_prefill", W.Q4_K, 4096, 1, 1023),
+    # 16 tokens over 100 cached positions (a speculative-decoding step): the
+    # projections take the split GEMM with the norms folded below 32 tokens
+    "llama3_8b_t16": ("llama3_8b_prefill", W.Q4_K, 4096, 16, 100),
 }
 
 
