@@ -266,6 +266,14 @@ struct SplitParams {
     const uint8_t* w2;    // gate/up form: the up matrix (w[0] is the gate)
     const float* ssq;     // folded norm: [tok_pad][n_cols/256] sums of x^2, else null
     float eps;
+    // split over columns (ksplit > 1): workgroup z of the grid's third
+    // dimension takes super-blocks [z, z+1) * n_sb/ksplit and writes its raw
+    // sums to part[z][token][roff[m] + row] (gate/up: gate rows, then up
+    // rows), which split_reduce_kernel adds up
+    int ksplit;
+    float* part;
+    int64_t roff[kMaxMats];
+    int64_t r_all;        // partial rows a token
 };
 
 // Epilogue forms: y = acc (kEpiPlain), or the gate/up form: out =
@@ -409,6 +417,9 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
     const int tt = blockIdx.y;
     const int nK = p.n_cols >> 5;
     const int n_chunks = nK / kChunkSteps, n_sb = n_chunks / 2;
+    // this workgroup's super-blocks (all of them unless split over columns)
+    const int sb_per = n_sb / p.ksplit;
+    const int sb0 = (int)blockIdx.z * sb_per, sb1 = sb0 + sb_per;
 
     // rows past n_rows read the last row (their results are not stored)
     const uint8_t* wbase[NT];
@@ -509,14 +520,15 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         }
     };
 
-    // prologue: chunk 0 (super-block 0, first half) staged, chunk 1 in flight
-    xst.load(0);
-    load_w(0, q, hq, hd);
-    xst.store(xs[0], ss[0], si[0], tid);
-    xst.load(1);
+    // prologue: chunk 2 sb0 (super-block sb0, first half) staged, the next in
+    // flight
+    xst.load(2 * sb0);
+    load_w(sb0, q, hq, hd);
+    xst.store(xs[0], ss[sb0 & 1], si[sb0 & 1], tid);
+    xst.load(2 * sb0 + 1);
     __syncthreads();
 
-    for (int sb = 0; sb < n_sb; ++sb) {
+    for (int sb = sb0; sb < sb1; ++sb) {
         uint4 qn[2][NT], hqn[NT], hdn[NT];
         load_w(sb + 1, qn, hqn, hdn);   // the next super-block (clamped)
         // ---- first half: chunk 2sb in xs[0]
@@ -575,6 +587,34 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         __syncthreads();
     }
 
+    // split over columns: the raw sums go to the partials (the norm's scale
+    // and the gate/up act follow the reduction)
+    if (p.ksplit > 1) {
+        float* P = p.part + (int64_t)blockIdx.z * p.n_tok * p.r_all;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int tok = kTokTile * tt + 16 * m + 4 * g + v;
+                if (tok >= p.n_tok) continue;
+                float* pp = P + (int64_t)tok * p.r_all;
+                if constexpr (GU) {
+                    const int64_t row = row0 + r;
+                    if (row < n_rows) {
+                        pp[row] = acc[m][0][v];
+                        pp[n_rows + row] = acc[m][1][v];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) {
+                        const int64_t row = row0 + 16 * j + r;
+                        if (row < n_rows) pp[p.roff[mi] + row] = acc[m][j][v];
+                    }
+                }
+            }
+        return;
+    }
+
     // folded norm: each token's sums times 1/sqrtf(sum of x^2 / n + eps),
     // the sum of its super-block partials (8 lanes a token, in a fixed order)
     __shared__ float tinv[kTokTile];
@@ -616,6 +656,73 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
                 }
             }
         }
+}
+
+// Sum of the column splits' partials of split_gemm_kernel, in split order,
+// then the epilogue the unsplit kernel applies: each token's sums times its
+// 1/sqrtf(sum of x^2 / n + eps) (folded norm; the super-block partials
+// summed by 8 lanes in the kernel's order), and y = sum, or (gate/up) out =
+// act(gate) * up. Workgroup (x, token) covers 1024 partial rows.
+struct ReduceArgs {
+    const float* part;    // [ksplit][n_tok][r_all]
+    int ksplit;
+    int n_tok;
+    int64_t r_all;
+    const float* ssq;     // [tok_pad][n_sb] or null
+    int n_sb;
+    int n_cols;
+    float eps;
+    int n_mat;            // plain form
+    float* y[kMaxMats];
+    int64_t n_rows[kMaxMats];
+    int64_t roff[kMaxMats + 1];
+};
+
+template <int EPI>
+__global__ __launch_bounds__(256) void split_reduce_kernel(ReduceArgs a) {
+    constexpr bool GU = EPI != kEpiPlain;
+    const int tid = threadIdx.x;
+    const int tok = blockIdx.y;
+    __shared__ float tinv;
+    if (tid < 8) {
+        float sum = 0.f;
+        if (a.ssq != nullptr) {
+            const float* sp = a.ssq + (int64_t)tok * a.n_sb;
+            for (int i = tid; i < a.n_sb; i += 8) sum += sp[i];
+        }
+        sum = group_sum<8>(sum);
+        if (tid == 0) tinv = a.ssq != nullptr ? 1.0f / sqrtf(sum / (float)a.n_cols + a.eps) : 1.f;
+    }
+    __syncthreads();
+    const float inv = tinv;
+    const int64_t stride = (int64_t)a.n_tok * a.r_all;
+    const float* pt = a.part + (int64_t)tok * a.r_all;
+    const int64_t n_out = GU ? a.r_all / 2 : a.r_all;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t o = (int64_t)blockIdx.x * 1024 + 256 * k + tid;
+        if (o >= n_out) break;
+        if constexpr (GU) {
+            float gv = 0.f, uv = 0.f;
+            for (int z = 0; z < a.ksplit; ++z) {
+                gv += pt[z * stride + o];
+                uv += pt[z * stride + n_out + o];
+            }
+            if (a.ssq != nullptr) {
+                gv = gv * inv;
+                uv = uv * inv;
+            }
+            a.y[0][(int64_t)tok * n_out + o] = act<GU ? EPI : 0>(gv) * uv;
+        } else {
+            float v = 0.f;
+            for (int z = 0; z < a.ksplit; ++z) v += pt[z * stride + o];
+            if (a.ssq != nullptr) v = v * inv;
+            int m = 0;
+#pragma unroll
+            for (int i = 1; i < kMaxMats; ++i) m += (i < a.n_mat && o >= a.roff[i]);
+            a.y[m][(int64_t)tok * a.n_rows[m] + (o - a.roff[m])] = v;
+        }
+    }
 }
 
 inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
@@ -679,6 +786,7 @@ struct SplitJob {
     int64_t n_tok;
     void* ws;
     RopeFold rope;         // RoPE on the first rope.mats outputs (norm_matmul_rope)
+    int64_t ws_bytes;      // room beyond split_ws_bytes lets few tokens split the columns
 };
 
 template <bool NORM, bool RESID>
@@ -699,6 +807,39 @@ void* pick_split_gemm(int nt, int epi) {
     case AERO_ACT_IDENTITY: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_IDENTITY>;
     default: return nullptr;
     }
+}
+
+// Column splits for a launch of base_wgs workgroups over n_sb super-blocks:
+// for launches of fewer than 128 workgroups (half the CUs; the reduction is
+// a launch more, which a launch of 224 workgroups measured not to repay),
+// the largest divisor d of n_sb (at most 16) that keeps d * base_wgs within
+// 512 workgroups and two super-blocks a split, when room holds the d
+// partials of part_bytes each; 1 otherwise. Measured on MI355X, Q4_K, 16
+// tokens: 4096 x 14336 108.6 -> 40.1 us (14 splits), 4096 x 4096 35.5 ->
+// 23.8 (8), 14336 x 4096 36.8 -> 29.9 (4). AERO_HIP_TUNE gemm16_ksplit=N
+// caps it (1: never split).
+int pick_ksplit(int64_t base_wgs, int n_sb, int64_t part_bytes, int64_t room) {
+    const int cap = std::min(16, tune("gemm16_ksplit", 16));
+    int ks = 1;
+    if (base_wgs >= 128) return 1;
+    for (int d = 2; d <= cap; ++d) {
+        if (n_sb % d || n_sb / d < 2 || base_wgs * d > 512) continue;
+        if (room < (int64_t)d * part_bytes) break;
+        ks = d;
+    }
+    return ks;
+}
+
+// Bytes of the column-split partials beyond split_ws_bytes for a call over
+// n_rows rows in all (gate/up: both matrices) of n_cols columns and n_tok
+// tokens: the most pick_ksplit can use (0 when the call never splits).
+int64_t split_partials_bytes(int64_t n_rows, int64_t n_cols, int64_t n_tok) {
+    if (n_rows <= 0 || n_cols % 256 || n_tok <= 0) return 0;
+    const int n_sb = (int)(n_cols / 256);
+    // the fewest workgroups such a call can have (128 rows each), so the most splits
+    const int64_t base = (n_rows + 127) / 128 * ((pad_tokens(n_tok) + kTokTile - 1) / kTokTile);
+    const int ks = pick_ksplit(base, n_sb, 1, INT64_MAX);
+    return ks > 1 ? (int64_t)ks * n_tok * n_rows * 4 : 0;
 }
 
 bool split_run(const SplitJob& j, hipStream_t s) {
@@ -753,10 +894,60 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     p.w2 = gu ? j.w_up : nullptr;
     p.ssq = norm ? w.ssq : nullptr;
     p.eps = j.eps;
-    if (!launch("split_gemm_kernel", k, dim3((unsigned)tiles, (unsigned)(tp / kTokTile)),
-                dim3(256), 0, s, p))
+    // few tokens leave workgroups idle: split the columns when the
+    // workspace holds the partials
+    int64_t r_all = 0;
+    for (int m = 0; m < n_mat; ++m) {
+        p.roff[m] = r_all;
+        r_all += j.n_rows[m];
+    }
+    if (gu) r_all = 2 * j.n_rows[0];
+    const int64_t base_wgs = tiles * (tp / kTokTile);
+    const int n_sb = (int)(j.n_cols / 256);
+    const int64_t part_off = split_ws_bytes(tp, j.n_cols, norm);
+    const int ks = pick_ksplit(base_wgs, n_sb, j.n_tok * r_all * 4, j.ws_bytes - part_off);
+    p.ksplit = ks;
+    p.r_all = r_all;
+    p.part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(j.ws) + part_off) : nullptr;
+    if (!launch("split_gemm_kernel", k,
+                dim3((unsigned)tiles, (unsigned)(tp / kTokTile), (unsigned)ks), dim3(256), 0, s,
+                p))
         return false;
-    return true;
+    if (ks == 1) return true;
+    ReduceArgs ra{};
+    ra.part = p.part;
+    ra.ksplit = ks;
+    ra.n_tok = (int)j.n_tok;
+    ra.r_all = r_all;
+    ra.ssq = p.ssq;
+    ra.n_sb = n_sb;
+    ra.n_cols = (int)j.n_cols;
+    ra.eps = j.eps;
+    ra.n_mat = n_mat;
+    for (int m = 0; m < n_mat; ++m) {
+        ra.y[m] = j.y[m];
+        ra.n_rows[m] = j.n_rows[m];
+        ra.roff[m] = p.roff[m];
+    }
+    for (int m = n_mat; m <= kMaxMats; ++m) ra.roff[m] = r_all;
+    const int64_t n_out = gu ? r_all / 2 : r_all;
+    const dim3 rg((unsigned)((n_out + 1023) / 1024), (unsigned)j.n_tok);
+    switch (epi) {
+    case kEpiPlain:
+        return launch("split_reduce_kernel", split_reduce_kernel<kEpiPlain>, rg, dim3(256), 0, s, ra);
+    case AERO_ACT_SILU:
+        return launch("split_reduce_kernel", split_reduce_kernel<AERO_ACT_SILU>, rg, dim3(256), 0, s,
+                      ra);
+    case AERO_ACT_GELU:
+        return launch("split_reduce_kernel", split_reduce_kernel<AERO_ACT_GELU>, rg, dim3(256), 0, s,
+                      ra);
+    case AERO_ACT_GELU_TANH:
+        return launch("split_reduce_kernel", split_reduce_kernel<AERO_ACT_GELU_TANH>, rg, dim3(256),
+                      0, s, ra);
+    default:
+        return launch("split_reduce_kernel", split_reduce_kernel<AERO_ACT_IDENTITY>, rg, dim3(256),
+                      0, s, ra);
+    }
 }
 
 }  // namespace
@@ -796,7 +987,7 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
         !aligned16(ws) || !tune("gemm16", 1))
         return true;
     SplitJob j{dtype, x, nullptr, nullptr, nullptr, -1, 0.f, 1, &w, nullptr, 0, &n_rows, &y,
-               n_cols, rb, n_tok, ws, {}};
+               n_cols, rb, n_tok, ws, {}, ws_bytes};
     if (!split_run(j, s)) return false;
     *ran = true;
     return true;
@@ -960,6 +1151,7 @@ bool fused_gemv_run(const SplitJob& j, bool gu, const int64_t* w_bytes, const fl
 bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t ws_bytes,
                      hipStream_t s, bool* rope_done) {
     *rope_done = false;
+    j.ws_bytes = ws_bytes;
     const int64_t bv = dtype_block_values(j.dtype), bb = dtype_block_bytes(j.dtype);
     const bool gu = j.w_up != nullptr;
     if (bv <= 0 || j.x == nullptr || j.n_cols <= 0 || j.n_tok < 0 || j.n_cols % bv != 0 ||
@@ -1042,6 +1234,10 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
 }  // namespace aero
 
 extern "C" {
+
+int64_t aero_hip_split_partials_bytes(int64_t n_rows, int64_t n_cols, int64_t n_tok) {
+    return aero::split_partials_bytes(n_rows, n_cols, n_tok);
+}
 
 int64_t aero_hip_norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok) {
     return aero::norm_matmul_workspace(dtype, n_cols, n_ff, n_tok);

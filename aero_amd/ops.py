@@ -242,6 +242,8 @@ def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: i
     _need(y, n_tok * n_rows, np.float32, "y")
     L = _lib.lib()
     wsb = int(L.aero_hip_matmul_workspace(int(dtype), n_cols, n_tok)) if n_tok > 1 else 0
+    if wsb:      # room for column-split partials (few tokens)
+        wsb += int(L.aero_hip_split_partials_bytes(n_rows, n_cols, n_tok))
     if wsb and split:
         ws = _gemm_ws.get(wsb)
         _lib.check(L.aero_hip_matmul(int(dtype), w.ptr, w.nbytes, x.ptr, y.ptr, n_rows, n_cols,
@@ -331,6 +333,7 @@ def norm_matmul(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_
     yp = (ctypes.c_void_p * k)(*[y.ptr for y in ys])
     L = _lib.lib()
     wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, 0, n_tok)
+    wsb += L.aero_hip_split_partials_bytes(int(sum(int(r) for r in n_rows)), n_cols, n_tok)
     buf = _norm_mm_ws.get(wsb)
     if rope is None:
         _lib.check(L.aero_hip_norm_matmul(int(dtype), k, wp, wb, nr, yp, x.ptr, as_ptr(d),
@@ -370,6 +373,7 @@ def norm_matmul_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: D
     _need(norm_w, n_cols, np.float32, "norm_w")
     L = _lib.lib()
     wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, n_ff, n_tok)
+    wsb += L.aero_hip_split_partials_bytes(2 * n_ff, n_cols, n_tok)
     buf = _norm_mm_ws.get(wsb)
     _lib.check(L.aero_hip_norm_matmul_gate_up(int(dtype), w_gate.ptr, w_up.ptr, w_gate.nbytes,
                                               x.ptr, as_ptr(d), as_ptr(x_out), as_ptr(norm_w),

@@ -351,6 +351,16 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * for them is refused with the size needed); x, d, x_out, norm_w 16-byte
  * aligned; h, y and out must not overlap x, d or x_out. */
 int64_t aero_hip_norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok);
+
+/* Extra workspace bytes that let a split-path call of few tokens split its
+ * columns over more workgroups: n_rows is the call's rows in all (every
+ * matrix; gate/up: both), n_cols its columns. A workspace of
+ * aero_hip_matmul_workspace / aero_hip_norm_matmul_workspace plus this
+ * many bytes lets the call write each split's partial sums there and add
+ * them in a second launch (in split order: deterministic); with less it
+ * runs unsplit. 0 when the call would not split. No counterpart in the
+ * reference, whose matmul runs on the CPU. */
+int64_t aero_hip_split_partials_bytes(int64_t n_rows, int64_t n_cols, int64_t n_tok);
 int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
                          const int64_t* n_rows, float* const* y, const float* x, const float* d,
                          float* x_out, const float* norm_w, float eps, int norm, int64_t n_cols,
