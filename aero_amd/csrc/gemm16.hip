@@ -952,20 +952,26 @@ bool split_run(const SplitJob& j, hipStream_t s) {
 
 }  // namespace
 
-// Whether n_tok tokens over n_rows rows (every matrix of the call) take the
-// split GEMM rather than the GEMV (the shape and a workspace permitting). The
-// GEMV converts and multiply-adds each weight once per token; the split
-// GEMM decodes it once per 32 tokens and runs the products on the matrix
-// cores, but below 32 tokens it fills fewer workgroups. Measured on MI355X
-// at the Llama-3-8B shapes (Q4_K, split / GEMV, µs): 14336 rows at 8 tokens
-// 36.8 / 46.1, at 16 tokens 37.5 / 92.6, at 24 tokens 38.2 / 137.6; 4096
-// rows x 14336 columns at 16 tokens 110.4 / 124.7; 4096 x 4096 at 16
-// tokens 36.3 / 34.9. AERO_HIP_TUNE gemm_split_min_tokens=N sets one
-// threshold instead.
-bool split_tokens_ok(int64_t n_tok, int64_t n_rows) {
+// The fewest tokens with which a call over n_rows rows (every matrix of the
+// call) of n_cols columns takes the split GEMM rather than the GEMV (the
+// shape and a workspace permitting). The GEMV converts and multiply-adds
+// each weight once per token and streams the matrix once per 4 tokens; the
+// split GEMM decodes each weight once per 32 tokens and runs the products
+// on the matrix cores (small grids split over columns). Measured on MI355X,
+// Q4_K, split / GEMV, µs: 14336 x 4096 at 4 tokens 29.2 / 23.2, 5: 28.7 /
+// 30.8, 6: 29.2 / 35.2, 8: 29.5 / 46.1; 4096 x 14336 at 8 tokens 40.5 /
+// 62.3; 4096 x 4096 at 8 tokens 23.7 / 17.5, 12: 24.2 / 26.3. So: 5
+// tokens from 32M weights, 12 from 8M, 16 below. AERO_HIP_TUNE
+// gemm_split_min_tokens=N sets one threshold instead.
+int split_min_tokens(int64_t n_rows, int64_t n_cols) {
     const int fixed = tune("gemm_split_min_tokens", 0);
-    if (fixed > 0) return n_tok >= fixed;
-    return n_tok >= 16 || (n_tok >= 8 && n_rows >= 8192);
+    if (fixed > 0) return fixed;
+    const int64_t weights = n_rows * n_cols;
+    return weights >= ((int64_t)32 << 20) ? 5 : (weights >= ((int64_t)8 << 20) ? 12 : 16);
+}
+
+bool split_tokens_ok(int64_t n_tok, int64_t n_rows, int64_t n_cols) {
+    return n_tok >= split_min_tokens(n_rows, n_cols);
 }
 
 // Workspace bytes of the split-x GEMM for n_tok tokens of n_cols (0 when the
@@ -1084,10 +1090,13 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 int64_t norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, int64_t n_tok) {
     if (n_cols <= 0 || n_tok <= 0 || n_ff < 0) return 0;
     const int64_t sep = align256(n_tok * n_cols * 4) + (n_ff > 0 ? align256(n_tok * n_ff * 4) : 0);
-    if (!split_shape_ok(dtype, n_cols, n_tok) || !split_tokens_ok(n_tok, INT64_MAX)) return sep;
+    // the rows (unknown here) decide the path between the largest and the
+    // smallest threshold: room for both
+    if (!split_shape_ok(dtype, n_cols, n_tok) ||
+        n_tok < split_min_tokens((int64_t)1 << 40, 1 << 20))
+        return sep;
     const int64_t spl = split_ws_bytes(pad_tokens(n_tok), n_cols, true);
-    // below the all-shapes threshold the rows decide the path: room for both
-    return split_tokens_ok(n_tok, 0) ? spl : std::max(spl, sep);
+    return n_tok >= split_min_tokens(1, 1) ? spl : std::max(spl, sep);
 }
 
 namespace {
@@ -1179,7 +1188,8 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     int64_t all_rows = gu ? 2 * n_ff : 0;
     for (int m = 0; m < (gu ? 0 : j.n_mat); ++m) all_rows += j.n_rows[m];
     bool split = split_shape_ok(j.dtype, j.n_cols, j.n_tok) &&
-                 split_tokens_ok(j.n_tok, all_rows) && j.rb % 16 == 0 && tune("gemm16", 1);
+                 split_tokens_ok(j.n_tok, all_rows, j.n_cols) && j.rb % 16 == 0 &&
+                 tune("gemm16", 1);
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
     const bool fused = !split && fused_gemv_rows_ok(j, gu, w_bytes);

@@ -26,7 +26,7 @@ int64_t dtype_block_bytes(int t);
 bool gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
               int64_t n_cols, int64_t rb, int64_t n_tok, hipStream_t s);
 int64_t split_gemm_workspace(int dtype, int64_t n_cols, int64_t n_tok);
-bool split_tokens_ok(int64_t n_tok, int64_t n_rows);
+bool split_tokens_ok(int64_t n_tok, int64_t n_rows, int64_t n_cols);
 bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64_t n_rows,
                     int64_t n_cols, int64_t rb, int64_t n_tok, void* ws, int64_t ws_bytes,
                     hipStream_t s, bool* ran);
@@ -1532,9 +1532,10 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
     }
     if (n_rows == 0 || n_tok == 0) return true;
     // several tokens: the matrix-core GEMMs. The split-x fp16 one when a
-    // workspace is given and the type has it (from 8-16 tokens,
-    // split_tokens_ok), else the fp32 one from 32 tokens (W once per 64).
-    if (ws != nullptr && n_tok <= (int64_t)1 << 30 && split_tokens_ok(n_tok, n_rows)) {
+    // workspace is given and the type has it (from 5-16 tokens by the
+    // matrix size, split_tokens_ok), else the fp32 one from 32 tokens (W
+    // once per 64).
+    if (ws != nullptr && n_tok <= (int64_t)1 << 30 && split_tokens_ok(n_tok, n_rows, n_cols)) {
         bool ran = false;
         if (!split_gemm_dev(dtype, w, x, y, n_rows, n_cols, rb, n_tok, ws, ws_bytes, s, &ran))
             return false;

@@ -304,7 +304,7 @@ class LayerStep:
     def _folds_norm(self, T: int) -> bool:
         """True when the norm (and residual add) before a projection folds into
         it: the split GEMM's pre-pass at 32+ tokens (the call itself takes it
-        from 8-16 tokens where it is faster), the fused decode GEMV's
+        from 5-16 tokens where it is faster), the fused decode GEMV's
         prologue below that."""
         if not (self.fuse("norm_gemm") and self.gpu("rmsnorm")):
             return False

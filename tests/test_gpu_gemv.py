@@ -42,9 +42,9 @@ def test_matvec_golden(hip, t):
     (1, 256, 1), (37, 1024, 1), (4096, 4096, 1), (1000, 14336, 1),   # decode shapes
     (4103, 4096, 2), (513, 2048, 3), (130, 4096, 8), (67, 1024, 13),  # token groups
     (300, 14336, 5), (64, 8192, 4),  # rows of several 4096-column steps, token groups
-    # 8-24 tokens: Q4_K / Q5_K take the split GEMM (16+ tokens, or 8+ with
-    # 8192+ rows), the other types the GEMV
-    (8200, 1024, 8), (100, 2048, 16), (33, 512, 24),
+    # 5-24 tokens: Q4_K / Q5_K take the split GEMM (5+ tokens from 32M
+    # weights, 12+ from 8M, else 16+), the other types the GEMV
+    (8200, 1024, 8), (100, 2048, 16), (33, 512, 24), (8192, 4096, 5),
 ])
 def test_matvec_vs_oracle(hip, oracle, t, n_rows, n_cols, n_tok):
     rng = np.random.default_rng(n_rows * 31 + n_cols + n_tok + t)
