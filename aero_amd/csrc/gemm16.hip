@@ -662,7 +662,9 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
 // then the epilogue the unsplit kernel applies: each token's sums times its
 // 1/sqrtf(sum of x^2 / n + eps) (folded norm; the super-block partials
 // summed by 8 lanes in the kernel's order), and y = sum, or (gate/up) out =
-// act(gate) * up. Workgroup (x, token) covers 1024 partial rows.
+// act(gate) * up. Thread (x, token) owns one output: every partial load is
+// issued at once (clamped, at most kMaxSplits), then added in order.
+constexpr int kMaxSplits = 16;
 struct ReduceArgs {
     const float* part;    // [ksplit][n_tok][r_all]
     int ksplit;
@@ -693,35 +695,40 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceArgs a) {
         sum = group_sum<8>(sum);
         if (tid == 0) tinv = a.ssq != nullptr ? 1.0f / sqrtf(sum / (float)a.n_cols + a.eps) : 1.f;
     }
+    const int64_t n_out = GU ? a.r_all / 2 : a.r_all;
+    const int64_t o = (int64_t)blockIdx.x * 256 + tid;
+    const int64_t oc = o < n_out ? o : n_out - 1;
+    const int64_t stride = (int64_t)a.n_tok * a.r_all;
+    const float* pt = a.part + (int64_t)tok * a.r_all + oc;
+    float pg[kMaxSplits], pu[GU ? kMaxSplits : 1];
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z) {
+        const int64_t zo = (int64_t)min(z, a.ksplit - 1) * stride;
+        pg[z] = pt[zo];
+        if constexpr (GU) pu[z] = pt[zo + n_out];
+    }
     __syncthreads();
     const float inv = tinv;
-    const int64_t stride = (int64_t)a.n_tok * a.r_all;
-    const float* pt = a.part + (int64_t)tok * a.r_all;
-    const int64_t n_out = GU ? a.r_all / 2 : a.r_all;
+    if (o >= n_out) return;
+    float gv = 0.f, uv = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int64_t o = (int64_t)blockIdx.x * 1024 + 256 * k + tid;
-        if (o >= n_out) break;
-        if constexpr (GU) {
-            float gv = 0.f, uv = 0.f;
-            for (int z = 0; z < a.ksplit; ++z) {
-                gv += pt[z * stride + o];
-                uv += pt[z * stride + n_out + o];
-            }
-            if (a.ssq != nullptr) {
-                gv = gv * inv;
-                uv = uv * inv;
-            }
-            a.y[0][(int64_t)tok * n_out + o] = act<GU ? EPI : 0>(gv) * uv;
-        } else {
-            float v = 0.f;
-            for (int z = 0; z < a.ksplit; ++z) v += pt[z * stride + o];
-            if (a.ssq != nullptr) v = v * inv;
-            int m = 0;
-#pragma unroll
-            for (int i = 1; i < kMaxMats; ++i) m += (i < a.n_mat && o >= a.roff[i]);
-            a.y[m][(int64_t)tok * a.n_rows[m] + (o - a.roff[m])] = v;
+    for (int z = 0; z < kMaxSplits; ++z) {
+        if (z < a.ksplit) {
+            gv += pg[z];
+            if constexpr (GU) uv += pu[z];
         }
+    }
+    if (a.ssq != nullptr) {
+        gv = gv * inv;
+        if constexpr (GU) uv = uv * inv;
+    }
+    if constexpr (GU) {
+        a.y[0][(int64_t)tok * n_out + o] = act<GU ? EPI : 0>(gv) * uv;
+    } else {
+        int m = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxMats; ++i) m += (i < a.n_mat && o >= a.roff[i]);
+        a.y[m][(int64_t)tok * a.n_rows[m] + (o - a.roff[m])] = gv;
     }
 }
 
@@ -819,7 +826,7 @@ void* pick_split_gemm(int nt, int epi) {
 // 23.8 (8), 14336 x 4096 36.8 -> 29.9 (4). AERO_HIP_TUNE gemm16_ksplit=N
 // caps it (1: never split).
 int pick_ksplit(int64_t base_wgs, int n_sb, int64_t part_bytes, int64_t room) {
-    const int cap = std::min(16, tune("gemm16_ksplit", 16));
+    const int cap = std::min(kMaxSplits, tune("gemm16_ksplit", kMaxSplits));
     int ks = 1;
     if (base_wgs >= 128) return 1;
     for (int d = 2; d <= cap; ++d) {
@@ -931,7 +938,7 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     }
     for (int m = n_mat; m <= kMaxMats; ++m) ra.roff[m] = r_all;
     const int64_t n_out = gu ? r_all / 2 : r_all;
-    const dim3 rg((unsigned)((n_out + 1023) / 1024), (unsigned)j.n_tok);
+    const dim3 rg((unsigned)((n_out + 255) / 256), (unsigned)j.n_tok);
     switch (epi) {
     case kEpiPlain:
         return launch("split_reduce_kernel", split_reduce_kernel<kEpiPlain>, rg, dim3(256), 0, s, ra);
@@ -958,16 +965,18 @@ bool split_run(const SplitJob& j, hipStream_t s) {
 // each weight once per token and streams the matrix once per 4 tokens; the
 // split GEMM decodes each weight once per 32 tokens and runs the products
 // on the matrix cores (small grids split over columns). Measured on MI355X,
-// Q4_K, split / GEMV, µs: 14336 x 4096 at 4 tokens 29.2 / 23.2, 5: 28.7 /
-// 30.8, 6: 29.2 / 35.2, 8: 29.5 / 46.1; 4096 x 14336 at 8 tokens 40.5 /
-// 62.3; 4096 x 4096 at 8 tokens 23.7 / 17.5, 12: 24.2 / 26.3. So: 5
-// tokens from 32M weights, 12 from 8M, 16 below. AERO_HIP_TUNE
+// Q4_K, split / GEMV, µs: 14336 x 4096 at 4 tokens 24.9 / 23.2, 5: 25.1 /
+// 31.0; 4096 x 4096 at 6 tokens 14.5 / 14.2, 8: 14.6 / 17.6; 1024 x 4096
+// at 8 tokens 13.3 / 10.6, 12: 13.4 / 15.8. So: 5 tokens from 32M
+// weights, 7 from 8M, 10 from 2M, 16 below. AERO_HIP_TUNE
 // gemm_split_min_tokens=N sets one threshold instead.
 int split_min_tokens(int64_t n_rows, int64_t n_cols) {
     const int fixed = tune("gemm_split_min_tokens", 0);
     if (fixed > 0) return fixed;
     const int64_t weights = n_rows * n_cols;
-    return weights >= ((int64_t)32 << 20) ? 5 : (weights >= ((int64_t)8 << 20) ? 12 : 16);
+    return weights >= ((int64_t)32 << 20) ? 5
+                                          : weights >= ((int64_t)8 << 20) ? 7
+                                                                          : weights >= ((int64_t)2 << 20) ? 10 : 16;
 }
 
 bool split_tokens_ok(int64_t n_tok, int64_t n_rows, int64_t n_cols) {

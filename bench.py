@@ -925,6 +925,8 @@ GEMM_CASES = [
     ("ffn_gate_14336x4096_t4", 12, 14336, 4096, 4), ("ffn_gate_14336x4096_t5", 12, 14336, 4096, 5),
     ("ffn_gate_14336x4096_t6", 12, 14336, 4096, 6), ("ffn_down_4096x14336_t8", 12, 4096, 14336, 8),
     ("attn_q_4096x4096_t8", 12, 4096, 4096, 8), ("attn_q_4096x4096_t12", 12, 4096, 4096, 12),
+    ("attn_q_4096x4096_t6", 12, 4096, 4096, 6), ("attn_kv_1024x4096_t8", 12, 1024, 4096, 8),
+    ("attn_kv_1024x4096_t12", 12, 1024, 4096, 12), ("attn_kv_1024x4096_t16", 12, 1024, 4096, 16),
 ]
 MFMA_FP32_PEAK_TFLOPS = 157.3
 MFMA_FP16_PEAK_TFLOPS = 2500.0   # dense fp16 matrix peak of MI355X

@@ -285,7 +285,8 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 
 /* aero_hip_matvec with a workspace, the same call as the reference's matmul
  * (src/kernels.cpp:520-538). With enough tokens of Q4_K or Q5_K (5 for
- * matrices of 32M+ weights, 12 for 8M+, else 16: where measured faster)
+ * matrices of 32M+ weights, 7 for 8M+, 10 for 2M+, else 16: where measured
+ * faster)
  * and
  * `ws` 16-byte aligned of at least aero_hip_matmul_workspace(dtype, n_cols,
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
@@ -336,7 +337,8 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  *   aero_hip_norm_matmul_gate_up: out[t*n_ff + r] = act(Wg[r] . h[t]) *
  *     (Wu[r] . h[t]), act an AERO_ACT_* kind.
  * Q4_K / Q5_K with enough tokens (5 when the call's matrices hold 32M+
- * weights together, 12 for 8M+, else 16; weights 16-byte aligned) run the
+ * weights together, 7 for 8M+, 10 for 2M+, else 16; weights 16-byte
+ * aligned) run the
  * split-x fp16 GEMM with h never written: each token's sums are scaled by
  * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
  * epilogue. Fewer tokens, with rows the fused decode GEMVs take (above), run the fused
