@@ -818,7 +818,9 @@ void* pick_split_gemm(int nt, int epi) {
 
 // Column splits for a launch of base_wgs workgroups over n_sb super-blocks:
 // for launches of fewer than 128 workgroups (half the CUs; the reduction is
-// a launch more, which a launch of 224 workgroups measured not to repay),
+// a launch more, which a launch of 224 workgroups does not repay: gate
+// 14336 x 4096 at 64 tokens 40.4 us unsplit, 44.9 in two; AERO_HIP_TUNE
+// gemm16_ksplit_below=N moves the limit),
 // the largest divisor d of n_sb (at most 16) that keeps d * base_wgs within
 // 512 workgroups and two super-blocks a split, when room holds the d
 // partials of part_bytes each; 1 otherwise. Measured on MI355X, Q4_K, 16
@@ -828,7 +830,7 @@ void* pick_split_gemm(int nt, int epi) {
 int pick_ksplit(int64_t base_wgs, int n_sb, int64_t part_bytes, int64_t room) {
     const int cap = std::min(kMaxSplits, tune("gemm16_ksplit", kMaxSplits));
     int ks = 1;
-    if (base_wgs >= 128) return 1;
+    if (base_wgs >= tune("gemm16_ksplit_below", 128)) return 1;
     for (int d = 2; d <= cap; ++d) {
         if (n_sb % d || n_sb / d < 2 || base_wgs * d > 512) continue;
         if (room < (int64_t)d * part_bytes) break;
