@@ -824,9 +824,9 @@ void* pick_split_gemm(int nt, int epi) {
 // the largest divisor d of n_sb (at most 16) that keeps d * base_wgs within
 // 512 workgroups and two super-blocks a split, when room holds the d
 // partials of part_bytes each; 1 otherwise. Measured on MI355X, Q4_K, 16
-// tokens: 4096 x 14336 108.6 -> 40.1 us (14 splits), 4096 x 4096 35.5 ->
-// 23.8 (8), 14336 x 4096 36.8 -> 29.9 (4). AERO_HIP_TUNE gemm16_ksplit=N
-// caps it (1: never split).
+// tokens, with the reduction: 4096 x 14336 108.6 -> 27.1 us (14 splits),
+// 4096 x 4096 35.5 -> 15.5 (8), 14336 x 4096 37.6 -> 26.9 (4).
+// AERO_HIP_TUNE gemm16_ksplit=N caps it (1: never split).
 int pick_ksplit(int64_t base_wgs, int n_sb, int64_t part_bytes, int64_t room) {
     const int cap = std::min(kMaxSplits, tune("gemm16_ksplit", kMaxSplits));
     int ks = 1;
