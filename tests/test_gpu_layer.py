@@ -215,3 +215,72 @@ def test_layer_decode_rope_fold(hip, oracle):
         counts[fold] = len(plan)
         plan.destroy()
     assert counts[True] == counts[False] - 1, counts
+
+
+def test_stack_prefill_then_decode(hip, oracle):
+    """A 2-layer Llama-3-8B stack run as a model runs it: 16 prompt tokens at
+    positions 0-15 (the split GEMMs with the norms folded), then 3 decode
+    tokens at positions 16, 17, 18 (the fused decode GEMVs with RoPE in the
+    epilogue), each step attending over the K/V rows the earlier steps wrote.
+    The oracle keeps its own K/V cache from its own projections; every
+    step's x and h_out match it to 1e-5 of scale."""
+    shape, wtype, vocab = "llama3_8b_prefill", W.Q4_K, 4096
+    cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype, vocab=vocab)
+    layers = [layer.BlockWeights(cfg, seed=40 + i) for i in range(2)]
+    n_prompt, n_dec = 16, 3
+    cap = n_prompt + n_dec
+    step = layer.LayerStep(cfg, layers, max_tokens=n_prompt, kv_cap=cap)
+    KD = cfg.n_head_kv * cfg.head_dim
+    Ks = [np.zeros((cap, KD), np.float32) for _ in layers]
+    Vs = [np.zeros((cap, KD), np.float32) for _ in layers]
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, vocab, n_prompt).astype(np.int32)
+    N, H, HK, D = cfg.hidden, cfg.n_head, cfg.n_head_kv, cfg.head_dim
+
+    def oracle_step(ids, kv_len):
+        """The stack on ids at positions kv_len.., extending Ks / Vs."""
+        T = ids.size
+        pos = np.arange(kv_len, kv_len + T, dtype=np.int32)
+        x = oracle.embed_gather(cfg.emb_type, layers[0].host["emb"], cfg.vocab, N, ids, 0.0)
+        for li, wts in enumerate(layers):
+            h_ = wts.host
+            mats = {k: dq(oracle, cfg.wtype, h_[k], *wts.shapes[k]) for k in wts.MATS}
+
+            def mm(name, a):
+                return (a.astype(np.float64) @ mats[name].T).astype(np.float32)
+
+            h = oracle.rmsnorm_rows(x, h_["attn_norm"], cfg.eps, cfg.unit_offset)
+            q, k, v = mm("wq", h), mm("wk", h), mm("wv", h)
+            q = oracle.qk_norm_rope(q, T, H, D, cfg.n_rot, pos, cfg.theta, 0)
+            k = oracle.qk_norm_rope(k, T, HK, D, cfg.n_rot, pos, cfg.theta, 0)
+            Ks[li][kv_len:kv_len + T] = k.reshape(T, KD)
+            Vs[li][kv_len:kv_len + T] = v.reshape(T, KD)
+            S = kv_len + T
+            att = oracle.attention_tiled(q.reshape(T, H, D), Ks[li][:S].reshape(S, HK, D),
+                                         Vs[li][:S].reshape(S, HK, D), 1.0 / math.sqrt(D),
+                                         qpos=pos, kpos=np.arange(S, dtype=np.int32))
+            x = x + mm("wo", att.reshape(T, H * D))
+            h = oracle.rmsnorm_rows(x, h_["ffn_norm"], cfg.eps, cfg.unit_offset)
+            x = x + mm("wd", oracle.act_mul(ACT[cfg.act], mm("wg", h), mm("wu", h)))
+        return x, oracle.rmsnorm_rows(x, layers[-1].host["out_norm"], cfg.eps, cfg.unit_offset)
+
+    def check(T, kv_len, ids, what):
+        step.prepare(ids, kv_len)
+        step.forward(T, kv_len)
+        want_x, want_h = oracle_step(ids, kv_len)
+        ex = rel_to_scale(step.x.view((T, N)).numpy(), want_x)
+        eh = rel_to_scale(step.h_out.view((T, N)).numpy(), want_h)
+        print(f"  {what}: rel x {ex:.2e} h_out {eh:.2e}", flush=True)
+        assert ex <= RTOL and eh <= RTOL, what
+        return want_h
+
+    print("stack prefill 16 then decode 3", flush=True)
+    check(n_prompt, 0, prompt, "prompt")
+    for i in range(n_dec):
+        tok = np.array([rng.integers(0, vocab)], np.int32)
+        check(1, n_prompt + i, tok, f"decode {i}")
+    # the caches the GPU steps wrote hold the oracle's rows
+    for li in range(len(layers)):
+        Kd, Vd = step.kv[li]
+        assert rel_to_scale(Kd.numpy(), Ks[li]) <= RTOL
+        assert rel_to_scale(Vd.numpy(), Vs[li]) <= RTOL
