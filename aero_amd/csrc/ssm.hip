@@ -453,6 +453,7 @@ struct ChunkArgs {
     float* W;           // [n_v][nc][C][D] in operand order (op_index)
     float* P;           // [n_v][nc][C][C] in operand order
     float* Qop;         // [n_k][nc][C][D]: normalised q in operand order
+    float* Kop;         // [n_k][nc][C][D]: keys in the lean pass's order (kop_index)
     float* gam;         // [n_v][nc][C]: G_t (0 past the chunk's last token)
     float* kfac;        // [n_v][nc][C]: exp(L_n - L_t) (0 past the last token)
     float* gC;          // [n_v][nc]: G_n
@@ -476,20 +477,31 @@ __device__ __forceinline__ int op_index(int t, int k, int K) {
 // and B[g][r] and receives D[4g + v][r]):
 //  1. K K^T (strictly lower) and Q K^T (lower) in 16x16 tiles, five tile
 //     products a wave; A = diag(b) Gam (K K^T) to LDS, P = Gam (Q K^T) out.
+//     Lane group g supplies the reduction indices (D/4) g + 4 jj + e.
 //  2. T = (I + A)^-1 by 16x16 blocks: the four unit lower-triangular diagonal
 //     blocks by substitution (a wave each), then
 //     T_ij = -T_ii sum_{j<=k<i} A_ik T_kj along the sub-diagonals.
-//  3. U = T diag(b) V (waves 0, 1) and W = T diag(b G) K (waves 2, 3), 64
-//     columns a wave, skipping T's zero blocks; the column scaling is folded
-//     into T's operand.
-template <int D>
+//  3. U = T diag(b) V (waves 0, 1) and W = T diag(b G) K (waves 2, 3), skipping
+//     T's zero blocks; the column scaling is folded into T's operand. From
+//     D = 128 the two waves of a product split its columns (D / 2 each, in
+//     groups of 64); at D = 64 they split its row tiles ({3, 0} and {2, 1},
+//     equal work under the triangle).
+// KOP: also store the keys in the order the lean state pass loads them, from
+// one value head of each key head: entry ((((w * D/64 + it) * 4 + j) * 64 +
+// 16g + r) * 4 + e) holds K[16j + 4g + e][(D/4) w + 16 it + r].
+template <int D, bool KOP>
 __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     constexpr int C = kChunk, KP = D + 4, AP = C + 4;
-    static_assert(D == 128 && C == 64, "tile layout");
+    constexpr int NJ = D / 16;                  // 16-byte loads a lane a 16-row tile
+    constexpr int NG = D >= 128 ? D / 128 : 1;  // 64-column groups a wave in step 3
+    constexpr int NT = D >= 128 ? 4 : 2;        // row tiles a wave in step 3
+    constexpr int NPRE = 2 * NJ > 16 * NG ? 2 * NJ : 16 * NG;
+    static_assert((D == 64 || D == 128 || D == 256) && C == 64, "tile layout");
     __shared__ __align__(16) float Ks[C * KP];   // keys [s][i], rows past n zero
     __shared__ __align__(16) float As[C * AP];   // A [t][s]
     __shared__ __align__(16) float Ts[C * AP];   // (I + A)^-1 [t][s]
-    __shared__ float Ls[C], Bs[C], Fs[C];
+    __shared__ double Ls[C];
+    __shared__ float Bs[C], Fs[C];
     const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = blockIdx.x;
@@ -503,21 +515,25 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     // for Q K^T) are loaded here, before the first barrier, with the keys.
     const bool qw = wave >= 2;
     const int i_hi = (wave & 1) ? 2 : 3;
-    v4f pre[16];
+    v4f pre[NPRE];
     if (qw) {
 #pragma unroll
         for (int which = 0; which < 2; ++which) {
             const int i = which ? 3 - i_hi : i_hi;
-            const float* qrow = a.qn + ((t0 + min(16 * i + r, n - 1)) * a.n_k + kk) * D + 32 * g;
+            const float* qrow = a.qn + ((t0 + min(16 * i + r, n - 1)) * a.n_k + kk) * D + (D / 4) * g;
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) pre[8 * which + jj] = *reinterpret_cast<const v4f*>(qrow + 4 * jj);
+            for (int jj = 0; jj < NJ; ++jj) pre[NJ * which + jj] = *reinterpret_cast<const v4f*>(qrow + 4 * jj);
         }
     } else {
         // rows past n: T's column scale (b) is zero there; any finite row
-        const float* vsrc = a.v + h * D + 64 * (wave & 1) + 4 * r;
 #pragma unroll
-        for (int ks = 0; ks < C / 4; ++ks)
-            pre[ks] = *reinterpret_cast<const v4f*>(vsrc + (t0 + min(4 * ks + g, n - 1)) * a.n_v * D);
+        for (int cg = 0; cg < NG; ++cg) {
+            const int c0 = D >= 128 ? (D / 2) * (wave & 1) + 64 * cg : 0;
+            const float* vsrc = a.v + h * D + c0 + 4 * r;
+#pragma unroll
+            for (int ks = 0; ks < C / 4; ++ks)
+                pre[16 * cg + ks] = *reinterpret_cast<const v4f*>(vsrc + (t0 + min(4 * ks + g, n - 1)) * a.n_v * D);
+        }
     }
     // the chunk's normalised keys (rows past n zero)
 #pragma unroll
@@ -527,20 +543,39 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
         if (row < n) kv = *reinterpret_cast<const v4f*>(a.kn + ((t0 + row) * a.n_k + kk) * D + 4 * c4);
         *reinterpret_cast<v4f*>(Ks + row * KP + 4 * c4) = kv;
     }
-    // inclusive prefix sum of the log decays over the chunk, and the gates
+    // inclusive prefix sum of the log decays over the chunk, and the gates.
+    // In float64: under strong decay L reaches -1e3 within a chunk, where a
+    // float32 sum resolves 6e-5, and every factor below is exp of a
+    // difference L_t - L_s of nearby tokens.
     if (wave == 0) {
-        float lg = l < n ? a.lg[(t0 + l) * a.n_v + h] : 0.0f;
+        double lg = l < n ? (double)a.lg[(t0 + l) * a.n_v + h] : 0.0;
         const float b = l < n ? a.bb[(t0 + l) * a.n_v + h] : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const float u = __shfl_up(lg, o, 64);
+            const double u = __shfl_up(lg, o, 64);
             if (l >= o) lg += u;
         }
         Ls[l] = lg;
         Bs[l] = b;
-        Fs[l] = b * expf(lg);
+        Fs[l] = b * expf((float)lg);
     }
     __syncthreads();
+
+    if constexpr (KOP) {
+        if (h < a.n_k) {   // one value head of each key head copies the keys
+            float* kop = a.Kop + (kk * a.nc + c) * C * D;
+#pragma unroll
+            for (int m = 0; m < C * D / 4 / 256; ++m) {
+                // entry idx holds K[s][i] for e = 0..3 (kop_index's inverse)
+                const int idx = tid + 256 * m, lane = idx & 63, rest = idx >> 6;
+                const int j = rest & 3, wit = rest >> 2;
+                const int i = (wit / (D / 64)) * (D / 4) + (wit % (D / 64)) * 16 + (lane & 15);
+                const int s0 = 16 * j + 4 * (lane >> 4);
+                *reinterpret_cast<v4f*>(kop + 4 * idx) =
+                    v4f{Ks[s0 * KP + i], Ks[(s0 + 1) * KP + i], Ks[(s0 + 2) * KP + i], Ks[(s0 + 3) * KP + i]};
+            }
+        }
+    }
 
     // 1. K K^T (waves 0, 1) or Q K^T (waves 2, 3) for two row tiles each
     {
@@ -548,27 +583,27 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
         for (int which = 0; which < 2; ++which) {
             const int i = which ? 3 - i_hi : i_hi;
-            v4f ar[8];
+            v4f ar[NJ];
             if (isq) {
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) ar[jj] = pre[8 * which + jj];
+                for (int jj = 0; jj < NJ; ++jj) ar[jj] = pre[NJ * which + jj];
                 if (h < a.n_k) {   // one value head of each key head copies q
                     float* qop = a.Qop + (kk * a.nc + c) * C * D;
 #pragma unroll
-                    for (int jj = 0; jj < 8; ++jj)
-                        *reinterpret_cast<v4f*>(qop + op_index(16 * i + r, 32 * g + 4 * jj, D)) = ar[jj];
+                    for (int jj = 0; jj < NJ; ++jj)
+                        *reinterpret_cast<v4f*>(qop + op_index(16 * i + r, (D / 4) * g + 4 * jj, D)) = ar[jj];
                 }
             } else {
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj)
-                    ar[jj] = *reinterpret_cast<const v4f*>(Ks + (16 * i + r) * KP + 32 * g + 4 * jj);
+                for (int jj = 0; jj < NJ; ++jj)
+                    ar[jj] = *reinterpret_cast<const v4f*>(Ks + (16 * i + r) * KP + (D / 4) * g + 4 * jj);
             }
             for (int j = 0; j < C / 16; ++j) {
                 v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
                 if (j <= i) {
 #pragma unroll
-                    for (int jj = 0; jj < 8; ++jj) {
-                        const v4f kb = *reinterpret_cast<const v4f*>(Ks + (16 * j + r) * KP + 32 * g + 4 * jj);
+                    for (int jj = 0; jj < NJ; ++jj) {
+                        const v4f kb = *reinterpret_cast<const v4f*>(Ks + (16 * j + r) * KP + (D / 4) * g + 4 * jj);
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[jj][e], kb[e], acc, 0, 0, 0);
@@ -579,7 +614,7 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
                 for (int vv = 0; vv < 4; ++vv) {
                     const int t = 16 * i + 4 * g + vv, sidx = 16 * j + r;
-                    const float gm = (sidx <= t && t < n) ? expf(Ls[t] - Ls[sidx]) : 0.0f;
+                    const float gm = (sidx <= t && t < n) ? expf((float)(Ls[t] - Ls[sidx])) : 0.0f;
                     if (isq)
                         a.P[base * C * C + op_index(t, sidx, C)] = sidx <= t ? gm * acc[vv] : 0.0f;
                     else
@@ -590,9 +625,9 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     }
     if (tid < C) {
         const bool live = tid < n;
-        a.gam[base * C + tid] = live ? expf(Ls[tid]) : 0.0f;
-        a.kfac[base * C + tid] = live ? expf(Ls[n - 1] - Ls[tid]) : 0.0f;
-        if (tid == 0) a.gC[base] = expf(Ls[n - 1]);
+        a.gam[base * C + tid] = live ? expf((float)Ls[tid]) : 0.0f;
+        a.kfac[base * C + tid] = live ? expf((float)(Ls[n - 1] - Ls[tid])) : 0.0f;
+        if (tid == 0) a.gC[base] = expf((float)Ls[n - 1]);
     }
     __syncthreads();
 
@@ -646,36 +681,40 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     // 3. U = T diag(b) V (waves 0, 1), W = T diag(b G) K (waves 2, 3): lane r
     // of column tile ct holds column c0 + 4r + ct, so each lane loads and
     // stores 4 adjacent columns
-    {
-        const bool isw = qw;
-        const int c0 = 64 * (wave & 1);
-        v4f acc[4][4];
+    const bool isw = qw;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+    for (int cg = 0; cg < NG; ++cg) {
+        const int c0 = D >= 128 ? (D / 2) * (wave & 1) + 64 * cg : 0;
+        v4f acc[NT][4];
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) acc[i][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ti = 0; ti < NT; ++ti)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) acc[ti][ct] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < C / 4; ++ks) {
             const int sidx = 4 * ks + g;
-            const v4f bv = isw ? *reinterpret_cast<const v4f*>(Ks + sidx * KP + c0 + 4 * r) : pre[ks];
+            const v4f bv = isw ? *reinterpret_cast<const v4f*>(Ks + sidx * KP + c0 + 4 * r) : pre[16 * cg + ks];
             const float fs = isw ? Fs[sidx] : Bs[sidx];
 #pragma unroll
-            for (int i = ks / 4; i < 4; ++i) {
+            for (int ti = 0; ti < NT; ++ti) {
+                const int i = NT == 4 ? ti : (ti ? 3 - i_hi : i_hi);
+                if (NT == 4 ? ks / 4 > ti : ks / 4 > i) continue;   // T is lower triangular
                 const float ta = Ts[(16 * i + r) * AP + sidx] * fs;
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct)
-                    acc[i][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ta, bv[ct], acc[i][ct], 0, 0, 0);
+                    acc[ti][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ta, bv[ct], acc[ti][ct], 0, 0, 0);
             }
         }
         // U row-major; W in operand order (4 adjacent columns stay adjacent)
         float* dst = (isw ? a.W : a.U) + base * C * D;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int ti = 0; ti < NT; ++ti)
 #pragma unroll
             for (int vv = 0; vv < 4; ++vv) {
+                const int i = NT == 4 ? ti : (ti ? 3 - i_hi : i_hi);
                 const int t = 16 * i + 4 * g + vv, col = c0 + 4 * r;
                 *reinterpret_cast<v4f*>(dst + (isw ? op_index(t, col, D) : t * D + col)) =
-                    v4f{acc[i][0][vv], acc[i][1][vv], acc[i][2][vv], acc[i][3][vv]};
+                    v4f{acc[ti][0][vv], acc[ti][1][vv], acc[ti][2][vv], acc[ti][3][vv]};
             }
     }
 }
@@ -892,13 +931,238 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
     }
 }
 
+// The lean state pass, for head dims 64, 128 and 256: the three products of
+// ssm_chunk_scan_kernel in the same order and layout, with the registers a
+// chunk holds cut to what head dim 256 allows (512 a lane):
+// - the keys come from Kop, already in the order (c) consumes them, so no key
+//   buffer sits in LDS (at D = 256 two would take 133 KB);
+// - the state tile streams from LDS into (a), 16 bytes a step;
+// - the next chunk's rows of W and Q are loaded right after (a), when this
+//   chunk's are dead, and land during (b) and (c); its rows of P and the keys
+//   after (c), landing during the next (a); U and the decay factors at the
+//   chunk's start. At D = 256 (QLATE) a chunk's Q rows load at its own start,
+//   behind W S0, so that two chunks' Q rows are never held at once.
+// Wave w owns token rows 16w..16w+15 of a chunk and state rows
+// (D/4) w..(D/4)(w+1)-1 (D/64 tiles of 16).
+template <int D>
+struct LeanWQ {
+    v4f w[D / 16], q[D / 16];
+};
+template <int D, int CT>
+struct LeanOps {
+    v4f p[4], kb[D / 16];
+    float u[CT][4], gm[4], kf[4];
+    float gc;
+};
+
+template <int D, int CT>
+__global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
+    constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16 * CT, NJ = D / 16, IT = D / 64;
+    constexpr bool QLATE = D == 256;
+    static_assert((D == 64 || D == 128 || D == 256) && C == 64, "wave layout");
+    __shared__ __align__(16) float St[NC * SP];   // state block, St[col][i]
+    __shared__ __align__(16) float Dt[NC * TP];   // d^T: Dt[col][s]
+    __shared__ __align__(16) float Dk[NC * TP];   // (kfac d)^T
+    const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t h = blockIdx.x, kk = h % a.n_k;
+    const int e0 = NC * blockIdx.y;
+    float* Sg = a.state + h * D * D;
+#pragma unroll
+    for (int i = 0; i < D * NC / 256; ++i) {
+        const int idx = tid + 256 * i, row = idx / NC, col = idx % NC;
+        St[col * SP + row] = Sg[(int64_t)row * D + e0 + col];
+    }
+
+    // rows of W and Q in operand order (op_index): 1 KB contiguous a load
+    auto load_w = [&](int c, LeanWQ<D>& o) __attribute__((always_inline)) {
+        const float* wr = a.W + (h * a.nc + c) * C * D + (wave * NJ * 64 + l) * 4;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) o.w[j] = *reinterpret_cast<const v4f*>(wr + 256 * j);
+    };
+    auto load_q = [&](int c, LeanWQ<D>& o) __attribute__((always_inline)) {
+        const float* qr = a.Qop + (kk * a.nc + c) * C * D + (wave * NJ * 64 + l) * 4;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) o.q[j] = *reinterpret_cast<const v4f*>(qr + 256 * j);
+    };
+    // rows of P and the keys, used by (b) and (c)
+    auto load_pk = [&](int c, LeanOps<D, CT>& o) __attribute__((always_inline)) {
+        const int64_t base = h * a.nc + c;
+        const float* pr = a.P + base * C * C + (wave * (C / 16) * 64 + l) * 4;
+        const float* kr = a.Kop + (kk * a.nc + c) * C * D + (wave * IT * 4 * 64 + l) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 256 * j);
+#pragma unroll
+        for (int m = 0; m < NJ; ++m) o.kb[m] = *reinterpret_cast<const v4f*>(kr + 256 * m);
+    };
+    // U and the per-token factors
+    auto load_ops = [&](int c, LeanOps<D, CT>& o) __attribute__((always_inline)) {
+        const int64_t base = h * a.nc + c;
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv) {
+            const int t = 16 * wave + 4 * g + vv;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) o.u[ct][vv] = a.U[(base * C + t) * D + e0 + 16 * ct + r];
+            o.gm[vv] = a.gam[base * C + t];
+            o.kf[vv] = a.kfac[base * C + t];
+        }
+        o.gc = a.gC[base];
+    };
+    auto chunk = [&](int c, LeanWQ<D>& o, LeanWQ<D>& nwq, const LeanOps<D, CT>& op,
+                     LeanOps<D, CT>& nop) __attribute__((always_inline)) {
+        const int64_t t0 = (int64_t)c * C;
+        const int n = (int)min<int64_t>(C, a.T - t0);
+        const int cn = min(c + 1, a.nc - 1);
+        load_ops(cn, nop);
+        // (a) W S0 and Q S0 for the wave's 16 tokens and each column tile:
+        // B[i][col] = S0[i][e0 + 16 ct + r], i = 4g + 16j + e. With QLATE the
+        // chunk's Q rows load here and W S0 runs first, over their latency.
+        v4f ws[CT], qs[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) ws[ct] = qs[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+        if constexpr (QLATE) {
+            load_q(c, o);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const v4f sv = *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 4 * g + 16 * j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[e], ws[ct], 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(cn, nwq);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const v4f sv = *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 4 * g + 16 * j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[e], qs[ct], 0, 0, 0);
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const v4f sv = *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 4 * g + 16 * j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[e], ws[ct], 0, 0, 0);
+                        qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[e], qs[ct], 0, 0, 0);
+                    }
+                }
+        }
+        // the wave's own state entries, for the update after the barrier
+        float sold[CT][IT][4];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int it = 0; it < IT; ++it)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv)
+                    sold[ct][it][vv] = St[(16 * ct + 4 * g + vv) * SP + (D / 4) * wave + 16 * it + r];
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!QLATE) {
+            load_w(cn, nwq);
+            load_q(cn, nwq);
+        }
+        // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            v4f dl, dk;
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                dl[vv] = op.u[ct][vv] - ws[ct][vv];
+                dk[vv] = op.kf[vv] * dl[vv];
+            }
+            *reinterpret_cast<v4f*>(Dt + (16 * ct + r) * TP + 16 * wave + 4 * g) = dl;
+            *reinterpret_cast<v4f*>(Dk + (16 * ct + r) * TP + 16 * wave + 4 * g) = dk;
+        }
+        __syncthreads();
+        v4f dt[CT][4], dkv[CT][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                dt[ct][j] = *reinterpret_cast<const v4f*>(Dt + (16 * ct + r) * TP + 4 * g + 16 * j);
+                dkv[ct][j] = *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 4 * g + 16 * j);
+            }
+        // (b) P d and (c) S0^T <- G_n S0^T + (kfac d)^T K for the wave's state
+        // rows: A[col][s] = (kfac d)[s][col], B[s][i] = K[s][i] from kb
+        v4f pd[CT], sd[CT][IT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            pd[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int it = 0; it < IT; ++it) sd[ct][it] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    pd[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(op.p[j][e], dt[ct][j][e], pd[ct], 0, 0, 0);
+#pragma unroll
+                    for (int it = 0; it < IT; ++it)
+                        sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(dkv[ct][j][e], op.kb[4 * it + j][e],
+                                                                          sd[ct][it], 0, 0, 0);
+                }
+        // O = scale (G Q S0 + P d)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * wave + 4 * g + vv;
+                if (t < n)
+                    a.outs[((t0 + t) * a.n_v + h) * D + e0 + 16 * ct + r] =
+                        a.scale * (op.gm[vv] * qs[ct][vv] + pd[ct][vv]);
+            }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int it = 0; it < IT; ++it)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv)
+                    St[(16 * ct + 4 * g + vv) * SP + (D / 4) * wave + 16 * it + r] =
+                        op.gc * sold[ct][it][vv] + sd[ct][it][vv];
+        __builtin_amdgcn_sched_barrier(0);
+        load_pk(cn, nop);
+        __syncthreads();
+    };
+
+    LeanWQ<D> wa, wb;
+    LeanOps<D, CT> oa, ob;
+    load_w(0, wa);
+    if constexpr (!QLATE) load_q(0, wa);
+    load_ops(0, oa);
+    load_pk(0, oa);
+    __syncthreads();
+    for (int c = 0; c < a.nc; c += 2) {
+        chunk(c, wa, wb, oa, ob);
+        if (c + 1 >= a.nc) break;
+        chunk(c + 1, wb, wa, ob, oa);
+    }
+#pragma unroll
+    for (int i = 0; i < D * NC / 256; ++i) {
+        const int idx = tid + 256 * i, row = idx / NC, col = idx % NC;
+        Sg[(int64_t)row * D + e0 + col] = St[col * SP + row];
+    }
+}
+
 }  // namespace
 
-// Long scans of head dim 128 take the chunked form (measured faster on
-// MI355X from a few chunks on).
+// Long scans take the chunked form (measured faster on MI355X from a few
+// chunks on). Head dim 128 runs ssm_chunk_scan_kernel, 64 and 256 the lean
+// state pass (AERO_HIP_TUNE ssm_lean=1 sends 128 there too).
 static bool use_chunked(int64_t T, int64_t d) {
-    return d == 128 && T >= tune("ssm_chunk_min", 128) && tune("ssm_chunk", 1) != 0;
+    return (d == 64 || d == 128 || d == 256) && T >= tune("ssm_chunk_min", 128) &&
+           tune("ssm_chunk", 1) != 0;
 }
+static bool use_lean(int64_t d) { return d != 128 || tune("ssm_lean", 0) != 0; }
 
 int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
     if (T <= 0 || n_k <= 0 || n_v <= 0 || d <= 0) return 0;
@@ -908,6 +1172,7 @@ int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
         const int64_t nc = (T + kChunk - 1) / kChunk, rows = n_v * nc * kChunk;
         b += 2 * up(rows * d * 4) + up(rows * kChunk * 4) + 2 * up(rows * 4) + up(n_v * nc * 4) +
              up(n_k * nc * kChunk * d * 4);
+        if (use_lean(d)) b += up(n_k * nc * kChunk * d * 4);   // Kop
     }
     return b;
 }
@@ -1007,8 +1272,20 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
             set_error("ssm_scan: v and outs must be 16-byte aligned for the chunked scan");
             return false;
         }
-        if (!launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128>,
-                    dim3((unsigned)nc, (unsigned)n_v), dim3(256), 0, s, ca))
+        const dim3 pgrid((unsigned)nc, (unsigned)n_v);
+        if (use_lean(d)) {
+            ca.Kop = reinterpret_cast<float*>(reinterpret_cast<char*>(ca.Qop) + up(n_k * nc * kChunk * d * 4));
+            const dim3 sgrid((unsigned)n_v, (unsigned)(d / 16));
+            if (d == 64)
+                return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<64, true>, pgrid, dim3(256), 0, s, ca) &&
+                       launch("ssm_chunk_lean_kernel", ssm_chunk_lean_kernel<64, 1>, sgrid, dim3(256), 0, s, ca);
+            if (d == 256)
+                return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<256, true>, pgrid, dim3(256), 0, s, ca) &&
+                       launch("ssm_chunk_lean_kernel", ssm_chunk_lean_kernel<256, 1>, sgrid, dim3(256), 0, s, ca);
+            return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128, true>, pgrid, dim3(256), 0, s, ca) &&
+                   launch("ssm_chunk_lean_kernel", ssm_chunk_lean_kernel<128, 1>, sgrid, dim3(256), 0, s, ca);
+        }
+        if (!launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128, false>, pgrid, dim3(256), 0, s, ca))
             return false;
         // one 16-column tile a workgroup (256 workgroups); two tiles sharing
         // the operand rows (AERO_HIP_TUNE ssm_chunk_ct=2, 128 workgroups)

@@ -508,9 +508,10 @@ void  aero_ssm_conv(const float* x, const float* w, float* tail, int* tail_len, 
 /* Device ABI. q, k [T][n_k][d]; v, outs [T][n_v][d]; alpha, beta [T][n_v];
  * a_log, dt_bias [n_v]; state [n_v][d][d]; d in {64, 128, 256}; q, k, state
  * and workspace 16-byte aligned; workspace of aero_hip_ssm_workspace bytes
- * (normalised q / k and the per-token decay and gate; from 128 tokens at
- * d = 128 also the chunked form's per-chunk operands, about
- * (2 n_v + n_k) T d + n_v T 64 floats; v and outs then 16-byte aligned too). */
+ * (normalised q / k and the per-token decay and gate; from 128 tokens also
+ * the chunked form's per-chunk operands, about (2 n_v + n_k) T d + n_v T 64
+ * floats, plus n_k T d at d = 64 and 256; v and outs then 16-byte aligned
+ * too). */
 int64_t aero_hip_ssm_workspace(int64_t T, int64_t n_k, int64_t n_v, int64_t d);
 int     aero_hip_ssm_scan(const float* q, const float* k, const float* v, const float* alpha,
                           const float* beta, const float* a_log, const float* dt_bias,

@@ -83,36 +83,47 @@ def test_scan_vs_oracle(hip, oracle, T, n_k, n_v, d):
     assert rel_to_scale(dst.numpy(), wst) <= RTOL
 
 
-@pytest.mark.parametrize("T,n_k,n_v", [
-    (128, 16, 32),     # two whole 64-token chunks at Qwen3-Next's heads
-    (300, 2, 4),       # a partial last chunk (44 tokens)
-    (129, 1, 2),       # a last chunk of one token
-    (256, 4, 4),       # one value head a key head
-    (1000, 3, 6),      # 16 chunks, two value heads a key head
+@pytest.mark.parametrize("T,n_k,n_v,d", [
+    (128, 16, 32, 128),    # two whole 64-token chunks at Qwen3-Next's heads
+    (300, 2, 4, 128),      # a partial last chunk (44 tokens)
+    (129, 1, 2, 128),      # a last chunk of one token
+    (256, 4, 4, 128),      # one value head a key head
+    (1000, 3, 6, 128),     # 16 chunks, two value heads a key head
+    # head dims 64 and 256: the lean state pass
+    (128, 4, 8, 64),
+    (300, 2, 4, 64),
+    (129, 1, 2, 64),
+    (1000, 3, 6, 64),
+    (128, 2, 4, 256),
+    (300, 1, 2, 256),
+    (129, 2, 2, 256),
+    (700, 1, 3, 256),
 ])
-def test_chunked_scan_vs_oracle(hip, oracle, T, n_k, n_v):
-    """Scans of 128 or more tokens at head dim 128 take the chunked (WY) form:
-    chunk pre-pass + state pass on the matrix cores; same tolerance."""
-    rng = np.random.default_rng(T + n_k)
-    args = inputs(rng, T, n_k, n_v, 128)
-    print(f"chunked ssm scan T={T} n_k={n_k} n_v={n_v}", flush=True)
-    scale = 128 ** -0.5
+def test_chunked_scan_vs_oracle(hip, oracle, T, n_k, n_v, d):
+    """Scans of 128 or more tokens take the chunked (WY) form: chunk pre-pass +
+    state pass on the matrix cores; same tolerance."""
+    rng = np.random.default_rng(T + n_k + d)
+    args = inputs(rng, T, n_k, n_v, d)
+    print(f"chunked ssm scan T={T} n_k={n_k} n_v={n_v} d={d}", flush=True)
+    scale = d ** -0.5
     out, dst = gpu_scan(*args, scale)
     want, wst = oracle.ssm_scan(*args, scale)
     assert rel_to_scale(out, want) <= RTOL
     assert rel_to_scale(dst.numpy(), wst) <= RTOL
 
 
-def test_chunked_scan_strong_decay_and_chain(hip, oracle):
+@pytest.mark.parametrize("d", [128, 64, 256])
+def test_chunked_scan_strong_decay_and_chain(hip, oracle, d):
     """Decays near zero (a_log -30: exp(L) underflows inside a chunk) and near
     one, gates near 0 and 1; two chunked calls of 200 tokens carrying the
     state equal one of 400 and the oracle."""
-    rng = np.random.default_rng(77)
-    q, k, v, al, bt, a_log, dt, st = inputs(rng, 400, 2, 4, 128)
+    rng = np.random.default_rng(77 + d)
+    print(f"chunked ssm scan chain d={d}", flush=True)
+    q, k, v, al, bt, a_log, dt, st = inputs(rng, 400, 2, 4, d)
     a_log = np.array([-30.0, -1e-4, -0.5, -3.0], np.float32)
     bt[:, 0] = 20.0                                    # gate 1
     bt[:, 1] = -20.0                                   # gate ~0
-    scale = 128 ** -0.5
+    scale = d ** -0.5
     whole, wst = gpu_scan(q, k, v, al, bt, a_log, dt, st, scale)
     want, ost = oracle.ssm_scan(q, k, v, al, bt, a_log, dt, st, scale)
     assert rel_to_scale(whole, want) <= RTOL and rel_to_scale(wst.numpy(), ost) <= RTOL
