@@ -17,8 +17,8 @@
 //
 // ssm_prep_kernel computes qn, kn, dec and b for every token first (d / 4 lanes
 // a token and key head), so the serial loop only streams them. Scans of 128
-// or more tokens at head dim 128 take the chunked (WY) form instead
-// (ssm_chunk_prep_kernel + ssm_chunk_scan_kernel, below).
+// or more tokens take the chunked (WY) form instead (ssm_chunk_prep_kernel +
+// ssm_chunk_scan_kernel, below).
 //
 // Sums run in another order than the reference's serial loops, and exp /
 // log1p / sqrt are the GPU's: <= 1e-5 relative to the output's scale. The conv
@@ -453,7 +453,7 @@ struct ChunkArgs {
     float* W;           // [n_v][nc][C][D] in operand order (op_index)
     float* P;           // [n_v][nc][C][C] in operand order
     float* Qop;         // [n_k][nc][C][D]: normalised q in operand order
-    float* Kop;         // [n_k][nc][C][D]: keys in the lean pass's order (kop_index)
+    float* Kop;         // [n_k][nc][C][D]: keys in the state pass's operand order
     float* gam;         // [n_v][nc][C]: G_t (0 past the chunk's last token)
     float* kfac;        // [n_v][nc][C]: exp(L_n - L_t) (0 past the last token)
     float* gC;          // [n_v][nc]: G_n
@@ -486,10 +486,10 @@ __device__ __forceinline__ int op_index(int t, int k, int K) {
 //     D = 128 the two waves of a product split its columns (D / 2 each, in
 //     groups of 64); at D = 64 they split its row tiles ({3, 0} and {2, 1},
 //     equal work under the triangle).
-// KOP: also store the keys in the order the lean state pass loads them, from
-// one value head of each key head: entry ((((w * D/64 + it) * 4 + j) * 64 +
+// The keys are also stored in the order the state pass loads them, from one
+// value head of each key head: entry ((((w * D/64 + it) * 4 + j) * 64 +
 // 16g + r) * 4 + e) holds K[16j + 4g + e][(D/4) w + 16 it + r].
-template <int D, bool KOP>
+template <int D>
 __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     constexpr int C = kChunk, KP = D + 4, AP = C + 4;
     constexpr int NJ = D / 16;                  // 16-byte loads a lane a 16-row tile
@@ -561,19 +561,17 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     }
     __syncthreads();
 
-    if constexpr (KOP) {
-        if (h < a.n_k) {   // one value head of each key head copies the keys
-            float* kop = a.Kop + (kk * a.nc + c) * C * D;
+    if (h < a.n_k) {   // one value head of each key head copies the keys
+        float* kop = a.Kop + (kk * a.nc + c) * C * D;
 #pragma unroll
-            for (int m = 0; m < C * D / 4 / 256; ++m) {
-                // entry idx holds K[s][i] for e = 0..3 (kop_index's inverse)
-                const int idx = tid + 256 * m, lane = idx & 63, rest = idx >> 6;
-                const int j = rest & 3, wit = rest >> 2;
-                const int i = (wit / (D / 64)) * (D / 4) + (wit % (D / 64)) * 16 + (lane & 15);
-                const int s0 = 16 * j + 4 * (lane >> 4);
-                *reinterpret_cast<v4f*>(kop + 4 * idx) =
-                    v4f{Ks[s0 * KP + i], Ks[(s0 + 1) * KP + i], Ks[(s0 + 2) * KP + i], Ks[(s0 + 3) * KP + i]};
-            }
+        for (int m = 0; m < C * D / 4 / 256; ++m) {
+            // entry idx holds K[s][i] for e = 0..3
+            const int idx = tid + 256 * m, lane = idx & 63, rest = idx >> 6;
+            const int j = rest & 3, wit = rest >> 2;
+            const int i = (wit / (D / 64)) * (D / 4) + (wit % (D / 64)) * 16 + (lane & 15);
+            const int s0 = 16 * j + 4 * (lane >> 4);
+            *reinterpret_cast<v4f*>(kop + 4 * idx) =
+                v4f{Ks[s0 * KP + i], Ks[(s0 + 1) * KP + i], Ks[(s0 + 2) * KP + i], Ks[(s0 + 3) * KP + i]};
         }
     }
 
@@ -719,221 +717,16 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
     }
 }
 
-// One workgroup a (value head h, 16 CT state columns from e0); the chunks in
-// order. Wave w owns token rows 16w..16w+15 of a chunk and state rows
-// 32w..32w+31 (D = 128); its operand rows (W, Q, P, keys) serve all CT column
-// tiles. The next chunk's operands (rows of W, Q and P, U, the decay
-// factors, the keys) are loaded while the current one is computed; the keys
-// go to the other of two LDS buffers, row-major with a 132-float pitch, which
-// the transposed state update S^T <- G_n S^T + (kfac d)^T K reads as its B
-// operand without bank conflicts (measured: a transposed key layout spent
-// more cycles in LDS bank conflicts than in the matrix steps).
-template <int D, int CT>
-struct ChunkOps {
-    v4f w[8], q[8], p[4], kt[8];
-    float u[CT][4], gm[4], kf[4];
-    float gc;
-};
-
-template <int D, int CT>
-__global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
-    constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16 * CT, KP = D + 4;
-    static_assert(D == 128, "wave layout");
-    __shared__ __align__(16) float St[NC * SP];     // state block, St[col][i]
-    __shared__ __align__(16) float KT[2][C * KP];   // the chunk's keys, KT[s][i]
-    __shared__ __align__(16) float Dt[NC * TP];     // d^T: Dt[col][s]
-    __shared__ __align__(16) float Dk[NC * TP];     // (kfac d)^T
-    const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t h = blockIdx.x, kk = h % a.n_k;
-    const int e0 = NC * blockIdx.y;
-    float* Sg = a.state + h * D * D;
-#pragma unroll
-    for (int i = 0; i < D * NC / 256; ++i) {
-        const int idx = tid + 256 * i, row = idx / NC, col = idx % NC;
-        St[col * SP + row] = Sg[(int64_t)row * D + e0 + col];
-    }
-
-    // operands of chunk c (rows past the chunk's tokens: clamped or zero)
-    auto load_ops = [&](int c, ChunkOps<D, CT>& o) __attribute__((always_inline)) {
-        const int64_t t0 = (int64_t)c * C, base = h * a.nc + c;
-        const int n = (int)min<int64_t>(C, a.T - t0);
-        // lane group g supplies the reduction indices 4g + 16j + e; the rows
-        // are stored in that order (op_index): 1 KB contiguous a load
-        const float* wr = a.W + base * C * D + (wave * (D / 16) * 64 + l) * 4;
-        const float* qr = a.Qop + (kk * a.nc + c) * C * D + (wave * (D / 16) * 64 + l) * 4;
-        const float* pr = a.P + base * C * C + (wave * (C / 16) * 64 + l) * 4;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            o.w[j] = *reinterpret_cast<const v4f*>(wr + 256 * j);
-            o.q[j] = *reinterpret_cast<const v4f*>(qr + 256 * j);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 256 * j);
-#pragma unroll
-        for (int vv = 0; vv < 4; ++vv) {
-            const int t = 16 * wave + 4 * g + vv;
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) o.u[ct][vv] = a.U[(base * C + t) * D + e0 + 16 * ct + r];
-            o.gm[vv] = a.gam[base * C + t];
-            o.kf[vv] = a.kfac[base * C + t];
-        }
-        o.gc = a.gC[base];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
-            const int64_t tk = t0 + min(row, n - 1);   // rows past n: zeroed in store_kt
-            o.kt[i] = *reinterpret_cast<const v4f*>(a.kn + (tk * a.n_k + kk) * D + 4 * c4);
-        }
-    };
-    // chunk c's keys into K (rows past the chunk's tokens zero)
-    auto store_kt = [&](const ChunkOps<D, CT>& o, float* K, int c) __attribute__((always_inline)) {
-        const int n = (int)min<int64_t>(C, a.T - (int64_t)c * C);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + 256 * i, row = idx / (D / 4), c4 = idx % (D / 4);
-            *reinterpret_cast<v4f*>(K + row * KP + 4 * c4) = row < n ? o.kt[i] : v4f{0.f, 0.f, 0.f, 0.f};
-        }
-    };
-    auto chunk = [&](int c, const ChunkOps<D, CT>& o, ChunkOps<D, CT>& nx, const float* Kc,
-                     float* Kn) __attribute__((always_inline)) {
-        const int64_t t0 = (int64_t)c * C;
-        const int n = (int)min<int64_t>(C, a.T - t0);
-        // LDS operands made current by the previous chunk's last barrier, read
-        // before any matrix step so that no LDS latency sits between them: the
-        // state block (a), this chunk's keys (c), the wave's own state entries
-        // (c). Lane group g supplies the chunk rows 4g + 16j + e of (c), so its
-        // key rows sit 4 * KP floats (16 banks) from the next group's.
-        v4f sv[CT][8];
-        float kb[16][2], sold[CT][2][4];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
-                sv[ct][j] = *reinterpret_cast<const v4f*>(St + (16 * ct + r) * SP + 4 * g + 16 * j);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float* kr = Kc + (4 * g + 16 * j + e) * KP + 32 * wave + r;
-                kb[4 * j + e][0] = kr[0];
-                kb[4 * j + e][1] = kr[16];
-            }
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int it = 0; it < 2; ++it)
-#pragma unroll
-                for (int vv = 0; vv < 4; ++vv)
-                    sold[ct][it][vv] = St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r];
-        __builtin_amdgcn_sched_barrier(0);
-        const int cn = min(c + 1, a.nc - 1);
-        load_ops(cn, nx);
-        // (a) W S0 and Q S0 for the wave's 16 tokens and each column tile; the
-        // next chunk's loads are issued between its matrix steps, so that
-        // their issue stalls overlap the matrix cores' work
-        v4f ws[CT], qs[CT];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) ws[ct] = qs[ct] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    ws[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[j][e], sv[ct][j][e], ws[ct], 0, 0, 0);
-                    qs[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.q[j][e], sv[ct][j][e], qs[ct], 0, 0, 0);
-                }
-#pragma unroll
-        for (int i = 0; i < 41; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // a matrix step
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // a global load
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // its address arithmetic
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // d = U - W S0 (rows 16w + 4g + v, column r of each tile); kfac d;
-        // the 4 rows of a lane are one 16-byte store
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-            v4f dl, dk;
-#pragma unroll
-            for (int vv = 0; vv < 4; ++vv) {
-                dl[vv] = o.u[ct][vv] - ws[ct][vv];
-                dk[vv] = o.kf[vv] * dl[vv];
-            }
-            *reinterpret_cast<v4f*>(Dt + (16 * ct + r) * TP + 16 * wave + 4 * g) = dl;
-            *reinterpret_cast<v4f*>(Dk + (16 * ct + r) * TP + 16 * wave + 4 * g) = dk;
-        }
-        __syncthreads();
-        v4f dt[CT][4], dkv[CT][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-                dt[ct][j] = *reinterpret_cast<const v4f*>(Dt + (16 * ct + r) * TP + 4 * g + 16 * j);
-                dkv[ct][j] = *reinterpret_cast<const v4f*>(Dk + (16 * ct + r) * TP + 4 * g + 16 * j);
-            }
-        __builtin_amdgcn_sched_barrier(0);
-        // (b) P d and (c) (kfac d)^T K, independent chains interleaved.
-        // (c) computes S0^T <- G_n S0^T + (kfac d)^T K for state rows
-        // 32w..32w+31: A[col][s] = (kfac d)[s][col], B[s][i] = K[s][i]
-        // (row-major keys), D[col][i] lands in St's layout.
-        v4f pd[CT], sd[CT][2];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) pd[ct] = sd[ct][0] = sd[ct][1] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int ct = 0; ct < CT; ++ct) {
-                    pd[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.p[j][e], dt[ct][j][e], pd[ct], 0, 0, 0);
-#pragma unroll
-                    for (int it = 0; it < 2; ++it)
-                        sd[ct][it] = __builtin_amdgcn_mfma_f32_16x16x4f32(dkv[ct][j][e], kb[4 * j + e][it],
-                                                                          sd[ct][it], 0, 0, 0);
-                }
-        // O = scale (G Q S0 + P d)
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int vv = 0; vv < 4; ++vv) {
-                const int t = 16 * wave + 4 * g + vv;
-                if (t < n)
-                    a.outs[((t0 + t) * a.n_v + h) * D + e0 + 16 * ct + r] =
-                        a.scale * (o.gm[vv] * qs[ct][vv] + pd[ct][vv]);
-            }
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int it = 0; it < 2; ++it)
-#pragma unroll
-                for (int vv = 0; vv < 4; ++vv)
-                    St[(16 * ct + 4 * g + vv) * SP + 32 * wave + 16 * it + r] =
-                        o.gc * sold[ct][it][vv] + sd[ct][it][vv];
-        store_kt(nx, Kn, cn);   // the next chunk's keys into the other buffer
-        __syncthreads();
-    };
-
-    ChunkOps<D, CT> oa, ob;
-    load_ops(0, oa);
-    store_kt(oa, KT[0], 0);
-    __syncthreads();
-    for (int c = 0; c < a.nc; c += 2) {
-        chunk(c, oa, ob, KT[0], KT[1]);
-        if (c + 1 >= a.nc) break;
-        chunk(c + 1, ob, oa, KT[1], KT[0]);
-    }
-#pragma unroll
-    for (int i = 0; i < D * NC / 256; ++i) {
-        const int idx = tid + 256 * i, row = idx / NC, col = idx % NC;
-        Sg[(int64_t)row * D + e0 + col] = St[col * SP + row];
-    }
-}
-
-// The lean state pass, for head dims 64, 128 and 256: the three products of
-// ssm_chunk_scan_kernel in the same order and layout, with the registers a
-// chunk holds cut to what head dim 256 allows (512 a lane):
+// The state pass, for head dims 64, 128 and 256. One workgroup a (value head
+// h, 16 CT state columns from e0) carries that block of the state in LDS
+// through the chunks in order. Per chunk, on the fp32 matrix cores:
+//  (a) W S0 and Q S0 for each wave's 16 tokens;
+//  then d = U - W S0 and kfac d go to LDS (one barrier), and
+//  (b) P d, giving O = scale (diag(G) Q S0 + P d);
+//  (c) the state update, computed transposed, S0^T <- G_n S0^T + (kfac d)^T K,
+//      so the keys are its B operand.
+// The registers a chunk holds are cut to what head dim 256 allows (512 a
+// lane):
 // - the keys come from Kop, already in the order (c) consumes them, so no key
 //   buffer sits in LDS (at D = 256 two would take 133 KB);
 // - the state tile streams from LDS into (a), 16 bytes a step;
@@ -945,18 +738,18 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
 // Wave w owns token rows 16w..16w+15 of a chunk and state rows
 // (D/4) w..(D/4)(w+1)-1 (D/64 tiles of 16).
 template <int D>
-struct LeanWQ {
+struct ChunkWQ {
     v4f w[D / 16], q[D / 16];
 };
 template <int D, int CT>
-struct LeanOps {
+struct ChunkOps {
     v4f p[4], kb[D / 16];
     float u[CT][4], gm[4], kf[4];
     float gc;
 };
 
 template <int D, int CT>
-__global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
+__global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
     constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16 * CT, NJ = D / 16, IT = D / 64;
     constexpr bool QLATE = D == 256;
     static_assert((D == 64 || D == 128 || D == 256) && C == 64, "wave layout");
@@ -975,18 +768,18 @@ __global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
     }
 
     // rows of W and Q in operand order (op_index): 1 KB contiguous a load
-    auto load_w = [&](int c, LeanWQ<D>& o) __attribute__((always_inline)) {
+    auto load_w = [&](int c, ChunkWQ<D>& o) __attribute__((always_inline)) {
         const float* wr = a.W + (h * a.nc + c) * C * D + (wave * NJ * 64 + l) * 4;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) o.w[j] = *reinterpret_cast<const v4f*>(wr + 256 * j);
     };
-    auto load_q = [&](int c, LeanWQ<D>& o) __attribute__((always_inline)) {
+    auto load_q = [&](int c, ChunkWQ<D>& o) __attribute__((always_inline)) {
         const float* qr = a.Qop + (kk * a.nc + c) * C * D + (wave * NJ * 64 + l) * 4;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) o.q[j] = *reinterpret_cast<const v4f*>(qr + 256 * j);
     };
     // rows of P and the keys, used by (b) and (c)
-    auto load_pk = [&](int c, LeanOps<D, CT>& o) __attribute__((always_inline)) {
+    auto load_pk = [&](int c, ChunkOps<D, CT>& o) __attribute__((always_inline)) {
         const int64_t base = h * a.nc + c;
         const float* pr = a.P + base * C * C + (wave * (C / 16) * 64 + l) * 4;
         const float* kr = a.Kop + (kk * a.nc + c) * C * D + (wave * IT * 4 * 64 + l) * 4;
@@ -996,7 +789,7 @@ __global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
         for (int m = 0; m < NJ; ++m) o.kb[m] = *reinterpret_cast<const v4f*>(kr + 256 * m);
     };
     // U and the per-token factors
-    auto load_ops = [&](int c, LeanOps<D, CT>& o) __attribute__((always_inline)) {
+    auto load_ops = [&](int c, ChunkOps<D, CT>& o) __attribute__((always_inline)) {
         const int64_t base = h * a.nc + c;
 #pragma unroll
         for (int vv = 0; vv < 4; ++vv) {
@@ -1008,8 +801,8 @@ __global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
         }
         o.gc = a.gC[base];
     };
-    auto chunk = [&](int c, LeanWQ<D>& o, LeanWQ<D>& nwq, const LeanOps<D, CT>& op,
-                     LeanOps<D, CT>& nop) __attribute__((always_inline)) {
+    auto chunk = [&](int c, ChunkWQ<D>& o, ChunkWQ<D>& nwq, const ChunkOps<D, CT>& op,
+                     ChunkOps<D, CT>& nop) __attribute__((always_inline)) {
         const int64_t t0 = (int64_t)c * C;
         const int n = (int)min<int64_t>(C, a.T - t0);
         const int cn = min(c + 1, a.nc - 1);
@@ -1134,8 +927,8 @@ __global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
         __syncthreads();
     };
 
-    LeanWQ<D> wa, wb;
-    LeanOps<D, CT> oa, ob;
+    ChunkWQ<D> wa, wb;
+    ChunkOps<D, CT> oa, ob;
     load_w(0, wa);
     if constexpr (!QLATE) load_q(0, wa);
     load_ops(0, oa);
@@ -1156,13 +949,11 @@ __global__ __launch_bounds__(256) void ssm_chunk_lean_kernel(ChunkArgs a) {
 }  // namespace
 
 // Long scans take the chunked form (measured faster on MI355X from a few
-// chunks on). Head dim 128 runs ssm_chunk_scan_kernel, 64 and 256 the lean
-// state pass (AERO_HIP_TUNE ssm_lean=1 sends 128 there too).
+// chunks on).
 static bool use_chunked(int64_t T, int64_t d) {
     return (d == 64 || d == 128 || d == 256) && T >= tune("ssm_chunk_min", 128) &&
            tune("ssm_chunk", 1) != 0;
 }
-static bool use_lean(int64_t d) { return d != 128 || tune("ssm_lean", 0) != 0; }
 
 int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
     if (T <= 0 || n_k <= 0 || n_v <= 0 || d <= 0) return 0;
@@ -1171,8 +962,7 @@ int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
     if (use_chunked(T, d)) {
         const int64_t nc = (T + kChunk - 1) / kChunk, rows = n_v * nc * kChunk;
         b += 2 * up(rows * d * 4) + up(rows * kChunk * 4) + 2 * up(rows * 4) + up(n_v * nc * 4) +
-             up(n_k * nc * kChunk * d * 4);
-        if (use_lean(d)) b += up(n_k * nc * kChunk * d * 4);   // Kop
+             2 * up(n_k * nc * kChunk * d * 4);
     }
     return b;
 }
@@ -1272,29 +1062,18 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
             set_error("ssm_scan: v and outs must be 16-byte aligned for the chunked scan");
             return false;
         }
-        const dim3 pgrid((unsigned)nc, (unsigned)n_v);
-        if (use_lean(d)) {
-            ca.Kop = reinterpret_cast<float*>(reinterpret_cast<char*>(ca.Qop) + up(n_k * nc * kChunk * d * 4));
-            const dim3 sgrid((unsigned)n_v, (unsigned)(d / 16));
-            if (d == 64)
-                return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<64, true>, pgrid, dim3(256), 0, s, ca) &&
-                       launch("ssm_chunk_lean_kernel", ssm_chunk_lean_kernel<64, 1>, sgrid, dim3(256), 0, s, ca);
-            if (d == 256)
-                return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<256, true>, pgrid, dim3(256), 0, s, ca) &&
-                       launch("ssm_chunk_lean_kernel", ssm_chunk_lean_kernel<256, 1>, sgrid, dim3(256), 0, s, ca);
-            return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128, true>, pgrid, dim3(256), 0, s, ca) &&
-                   launch("ssm_chunk_lean_kernel", ssm_chunk_lean_kernel<128, 1>, sgrid, dim3(256), 0, s, ca);
-        }
-        if (!launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128, false>, pgrid, dim3(256), 0, s, ca))
-            return false;
-        // one 16-column tile a workgroup (256 workgroups); two tiles sharing
-        // the operand rows (AERO_HIP_TUNE ssm_chunk_ct=2, 128 workgroups)
-        // measured 16% slower on MI355X
-        if (tune("ssm_chunk_ct", 1) == 2)
-            return launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 2>,
-                          dim3((unsigned)n_v, (unsigned)(d / 32)), dim3(256), 0, s, ca);
-        return launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 1>,
-                      dim3((unsigned)n_v, (unsigned)(d / 16)), dim3(256), 0, s, ca);
+        ca.Kop = reinterpret_cast<float*>(reinterpret_cast<char*>(ca.Qop) + up(n_k * nc * kChunk * d * 4));
+        // chunk pre-pass: one workgroup a (chunk, value head); state pass: one
+        // a (value head, 16 state columns), 256 at Qwen3-Next's 32 heads of 128
+        const dim3 pgrid((unsigned)nc, (unsigned)n_v), sgrid((unsigned)n_v, (unsigned)(d / 16));
+        if (d == 64)
+            return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<64>, pgrid, dim3(256), 0, s, ca) &&
+                   launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<64, 1>, sgrid, dim3(256), 0, s, ca);
+        if (d == 256)
+            return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<256>, pgrid, dim3(256), 0, s, ca) &&
+                   launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<256, 1>, sgrid, dim3(256), 0, s, ca);
+        return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128>, pgrid, dim3(256), 0, s, ca) &&
+               launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 1>, sgrid, dim3(256), 0, s, ca);
     }
     ScanArgs sa{qn, kn, v, dc, bb, nullptr, nullptr, state, outs, T, n_k, n_v, scale, eps};
     return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);

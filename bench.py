@@ -1497,9 +1497,12 @@ def gguf_bench(a):
 
 
 SSM_CASES = [
-    # (name, tokens): Qwen3-Next linear-attention heads, 16 key heads, 32 value
-    # heads, d 128; qkv conv over 2*16*128 + 32*128 = 8192 channels, kernel 4
-    ("decode", 1), ("prefill_4096", 4096),
+    # (name, tokens, key heads, value heads, head dim): Qwen3-Next's linear
+    # attention is 16 key heads, 32 value heads, d 128; the same prefill at
+    # head dims 64 and 256. The qkv conv (8192 channels, kernel 4) is timed
+    # beside each.
+    ("decode", 1, 16, 32, 128), ("prefill_4096", 4096, 16, 32, 128),
+    ("prefill_4096_d64", 4096, 16, 32, 64), ("prefill_4096_d256", 4096, 8, 16, 256),
 ]
 
 
@@ -1511,10 +1514,10 @@ def ssm_bench(a):
     from aero_amd import ops
     from aero_amd.device import DeviceArray as DA, Event, Stream, time_next_kernel
 
-    n_k, n_v, d, C, K = 16, 32, 128, 8192, 4
+    C, K = 8192, 4
     rng = np.random.default_rng(0)
     stream = Stream()
-    for name, T in SSM_CASES:
+    for name, T, n_k, n_v, d in SSM_CASES:
         f = lambda *s: DA.from_numpy(rng.standard_normal(s).astype(np.float32))
         q, k, v = f(T, n_k, d), f(T, n_k, d), f(T, n_v, d)
         al, bt = f(T, n_v), f(T, n_v)
@@ -1556,7 +1559,8 @@ def ssm_bench(a):
         # event pair measured; longer ones a prep pass and the scan (from 128
         # tokens the chunked scan: chunk pre-pass + state pass)
         fused = T <= 16
-        n_kern = 1 if fused else (3 if T >= 128 and os.environ.get("AERO_HIP_TUNE", "").find("ssm_chunk=0") < 0 else 2)
+        chunked = T >= 128 and os.environ.get("AERO_HIP_TUNE", "").find("ssm_chunk=0") < 0
+        n_kern = 1 if fused else (3 if chunked else 2)
         prep_us = 0.0 if fused else statistics.mean(times["prep"])
         scan_us = op_us - prep_us
         conv_us = statistics.mean(times["conv"])
@@ -1564,6 +1568,7 @@ def ssm_bench(a):
         io_bytes = 4 * T * (2 * n_k * d + 2 * n_v * d + 2 * n_v)
         conv_bytes = 4 * (2 * T * C + C * K)
         res = {"case": name, "tokens": T, "heads": [n_k, n_v], "d": d,
+               "form": "fused" if fused else ("chunked" if chunked else "per-token"),
                "ssm_op_us": round(op_us, 3), "kernels": n_kern,
                "prep_us": round(prep_us, 3), "scan_us": round(scan_us, 3),
                "conv_us": round(conv_us, 3),
