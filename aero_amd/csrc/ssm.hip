@@ -437,7 +437,8 @@ ScanKernel pick_scan(int64_t d, int p, bool fused) {
 //   O = scale (diag(G) Q S0 + P Dlt),  P_ts = Gam_ts (q_t . k_s) (s <= t),
 //   S_end = G_n S0 + sum_s exp(L_n - L_s) k_s d_s^T.
 // ssm_chunk_prep_kernel computes U, W, P and the decay factors of every
-// (chunk, value head) in parallel; ssm_chunk_scan_kernel carries the state
+// (chunk, value head) in parallel; the state pass (ssm_chunk_split_kernel at
+// head dims 64 and 128, ssm_chunk_scan_kernel at 256) carries the state
 // through the chunks on the fp32 matrix cores, 16 state columns a workgroup.
 // Results differ from the per-token scan by fp32 rounding (the chunked form
 // of a 512-token scan: ~6e-7 of the output's scale).
@@ -946,6 +947,172 @@ __global__ __launch_bounds__(256) void ssm_chunk_scan_kernel(ChunkArgs a) {
     }
 }
 
+// The state pass with two waves a SIMD (head dims 64 and 128): the four
+// state waves carry the chain W S0 -> d -> state update, and four output
+// waves take Q S0 and P d off it. Per chunk:
+//   state wave w:  W S0 (its 16 tokens) | d, kfac d -> LDS | barrier |
+//                  (c) on its D/4 state rows | barrier
+//   output wave w: Q S0 (its 16 tokens) |                  | barrier |
+//                  P d, the outputs      | barrier
+// St is read by every wave before the first barrier and written by the
+// state waves after it; Dt / Dk written before it and read after. Each
+// wave's operands for the next chunk load at the chunk's start.
+template <int D>
+struct SplitStateOps {
+    v4f w[D / 16], kb[D / 16];
+    float u[4], kf[4];
+    float gc;
+};
+template <int D>
+struct SplitOutOps {
+    v4f q[D / 16], p[4];
+    float gm[4];
+};
+
+template <int D>
+__global__ __launch_bounds__(512) void ssm_chunk_split_kernel(ChunkArgs a) {
+    constexpr int C = kChunk, SP = D + 4, TP = C + 4, NC = 16, NJ = D / 16, IT = D / 64;
+    static_assert((D == 64 || D == 128) && C == 64, "wave layout");
+    __shared__ __align__(16) float St[NC * SP];   // state block, St[col][i]
+    __shared__ __align__(16) float Dt[NC * TP];   // d^T: Dt[col][s]
+    __shared__ __align__(16) float Dk[NC * TP];   // (kfac d)^T
+    const int tid = threadIdx.x, l = tid & 63, r = l & 15, g = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wq = wave & 3;
+    const int64_t h = blockIdx.x, kk = h % a.n_k;
+    const int e0 = NC * blockIdx.y;
+    float* Sg = a.state + h * D * D;
+#pragma unroll
+    for (int i = 0; i < D * NC / 512; ++i) {
+        const int idx = tid + 512 * i, row = idx / NC, col = idx % NC;
+        St[col * SP + row] = Sg[(int64_t)row * D + e0 + col];
+    }
+    // B[i][col] = S0[i][e0 + r], i = 4g + 16j + e, against A rows x[j]
+    auto s0_product = [&](const v4f* x) __attribute__((always_inline)) {
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const v4f sv = *reinterpret_cast<const v4f*>(St + r * SP + 4 * g + 16 * j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[j][e], sv[e], acc, 0, 0, 0);
+        }
+        return acc;
+    };
+
+    if (wave < 4) {
+        auto load = [&](int c, SplitStateOps<D>& o) __attribute__((always_inline)) {
+            const int64_t base = h * a.nc + c;
+            const float* wr = a.W + base * C * D + (wq * NJ * 64 + l) * 4;
+            const float* kr = a.Kop + (kk * a.nc + c) * C * D + (wq * IT * 4 * 64 + l) * 4;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                o.w[j] = *reinterpret_cast<const v4f*>(wr + 256 * j);
+                o.kb[j] = *reinterpret_cast<const v4f*>(kr + 256 * j);
+            }
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * wq + 4 * g + vv;
+                o.u[vv] = a.U[(base * C + t) * D + e0 + r];
+                o.kf[vv] = a.kfac[base * C + t];
+            }
+            o.gc = a.gC[base];
+        };
+        auto chunk = [&](int c, const SplitStateOps<D>& o, SplitStateOps<D>& nx) __attribute__((always_inline)) {
+            load(min(c + 1, a.nc - 1), nx);
+            const v4f ws = s0_product(o.w);
+            float sold[IT][4];
+#pragma unroll
+            for (int it = 0; it < IT; ++it)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv) sold[it][vv] = St[(4 * g + vv) * SP + (D / 4) * wq + 16 * it + r];
+            v4f dl, dk;
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                dl[vv] = o.u[vv] - ws[vv];
+                dk[vv] = o.kf[vv] * dl[vv];
+            }
+            *reinterpret_cast<v4f*>(Dt + r * TP + 16 * wq + 4 * g) = dl;
+            *reinterpret_cast<v4f*>(Dk + r * TP + 16 * wq + 4 * g) = dk;
+            __syncthreads();
+            v4f dkv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dkv[j] = *reinterpret_cast<const v4f*>(Dk + r * TP + 4 * g + 16 * j);
+            // (c) S0^T <- G_n S0^T + (kfac d)^T K on state rows (D/4) wq + 16 it + r
+            v4f sd[IT];
+#pragma unroll
+            for (int it = 0; it < IT; ++it) sd[it] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int it = 0; it < IT; ++it)
+                        sd[it] = __builtin_amdgcn_mfma_f32_16x16x4f32(dkv[j][e], o.kb[4 * it + j][e], sd[it], 0, 0, 0);
+#pragma unroll
+            for (int it = 0; it < IT; ++it)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv)
+                    St[(4 * g + vv) * SP + (D / 4) * wq + 16 * it + r] = o.gc * sold[it][vv] + sd[it][vv];
+            __syncthreads();
+        };
+        SplitStateOps<D> oa, ob;
+        load(0, oa);
+        __syncthreads();
+        for (int c = 0; c < a.nc; c += 2) {
+            chunk(c, oa, ob);
+            if (c + 1 >= a.nc) break;
+            chunk(c + 1, ob, oa);
+        }
+    } else {
+        auto load = [&](int c, SplitOutOps<D>& o) __attribute__((always_inline)) {
+            const int64_t base = h * a.nc + c;
+            const float* qr = a.Qop + (kk * a.nc + c) * C * D + (wq * NJ * 64 + l) * 4;
+            const float* pr = a.P + base * C * C + (wq * (C / 16) * 64 + l) * 4;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) o.q[j] = *reinterpret_cast<const v4f*>(qr + 256 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o.p[j] = *reinterpret_cast<const v4f*>(pr + 256 * j);
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) o.gm[vv] = a.gam[base * C + 16 * wq + 4 * g + vv];
+        };
+        auto chunk = [&](int c, const SplitOutOps<D>& o, SplitOutOps<D>& nx) __attribute__((always_inline)) {
+            const int64_t t0 = (int64_t)c * C;
+            const int n = (int)min<int64_t>(C, a.T - t0);
+            load(min(c + 1, a.nc - 1), nx);
+            const v4f qs = s0_product(o.q);
+            __syncthreads();
+            v4f dt[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dt[j] = *reinterpret_cast<const v4f*>(Dt + r * TP + 4 * g + 16 * j);
+            v4f pd = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pd = __builtin_amdgcn_mfma_f32_16x16x4f32(o.p[j][e], dt[j][e], pd, 0, 0, 0);
+            // O = scale (G Q S0 + P d)
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int t = 16 * wq + 4 * g + vv;
+                if (t < n)
+                    a.outs[((t0 + t) * a.n_v + h) * D + e0 + r] = a.scale * (o.gm[vv] * qs[vv] + pd[vv]);
+            }
+            __syncthreads();
+        };
+        SplitOutOps<D> oa, ob;
+        load(0, oa);
+        __syncthreads();
+        for (int c = 0; c < a.nc; c += 2) {
+            chunk(c, oa, ob);
+            if (c + 1 >= a.nc) break;
+            chunk(c + 1, ob, oa);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < D * NC / 512; ++i) {
+        const int idx = tid + 512 * i, row = idx / NC, col = idx % NC;
+        Sg[(int64_t)row * D + e0 + col] = St[col * SP + row];
+    }
+}
+
 }  // namespace
 
 // Long scans take the chunked form (measured faster on MI355X from a few
@@ -1066,14 +1233,19 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
         // chunk pre-pass: one workgroup a (chunk, value head); state pass: one
         // a (value head, 16 state columns), 256 at Qwen3-Next's 32 heads of 128
         const dim3 pgrid((unsigned)nc, (unsigned)n_v), sgrid((unsigned)n_v, (unsigned)(d / 16));
+        // head dims 64 and 128: two waves a SIMD (AERO_HIP_TUNE ssm_split=0:
+        // the one-wave form, measured 3-7% slower on MI355X)
+        const bool split = tune("ssm_split", 1) != 0;
         if (d == 64)
             return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<64>, pgrid, dim3(256), 0, s, ca) &&
-                   launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<64, 1>, sgrid, dim3(256), 0, s, ca);
+                   (split ? launch("ssm_chunk_split_kernel", ssm_chunk_split_kernel<64>, sgrid, dim3(512), 0, s, ca)
+                          : launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<64, 1>, sgrid, dim3(256), 0, s, ca));
         if (d == 256)
             return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<256>, pgrid, dim3(256), 0, s, ca) &&
                    launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<256, 1>, sgrid, dim3(256), 0, s, ca);
         return launch("ssm_chunk_prep_kernel", ssm_chunk_prep_kernel<128>, pgrid, dim3(256), 0, s, ca) &&
-               launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 1>, sgrid, dim3(256), 0, s, ca);
+               (split ? launch("ssm_chunk_split_kernel", ssm_chunk_split_kernel<128>, sgrid, dim3(512), 0, s, ca)
+                      : launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 1>, sgrid, dim3(256), 0, s, ca));
     }
     ScanArgs sa{qn, kn, v, dc, bb, nullptr, nullptr, state, outs, T, n_k, n_v, scale, eps};
     return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);
