@@ -90,6 +90,10 @@ PROTOTYPES = {
                                                               vp]),
     "aero_hip_ssm_conv": (c_int, [vp, vp, vp, c_int64, vp, vp, c_int64, c_int64, c_int64,
                                   POINTER(c_int64), vp]),
+    "aero_hip_ssm_scan_strided": (c_int, [vp, c_int64, vp, c_int64, vp, c_int64] + [vp] * 5
+                                  + [c_int64] * 4 + [c_float, c_float, vp, vp, c_int64, vp]),
+    "aero_hip_ssm_conv_silu": (c_int, [vp, vp, vp, c_int64, vp, vp, c_int64, c_int64, c_int64,
+                                       POINTER(c_int64), vp]),
     # GGUF reader
     "aero_gguf_open": (vp, [ctypes.c_char_p]),
     "aero_gguf_close": (None, [vp]),
@@ -122,6 +126,8 @@ PROTOTYPES = {
                                      POINTER(vp), vp, vp, c_float, c_int, c_int64, c_int64, vp]),
     "aero_hip_norm_gate_up": (c_int, [c_int, vp, vp, c_int64, vp, vp, c_float, c_int, c_int, vp,
                                       c_int64, c_int64, c_int64, vp]),
+    "aero_hip_gated_norm_matvec": (c_int, [c_int, vp, c_int64, c_int64, vp, vp, vp, vp, c_int64,
+                                           c_float, c_int64, c_int64, vp]),
     "aero_hip_matmul_workspace": (c_int64, [c_int, c_int64, c_int64]),
     "aero_hip_norm_matmul_workspace": (c_int64, [c_int, c_int64, c_int64, c_int64]),
     "aero_hip_split_partials_bytes": (c_int64, [c_int64, c_int64, c_int64]),

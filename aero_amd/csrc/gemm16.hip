@@ -1117,7 +1117,7 @@ namespace {
 // (lanes64_ok: 16-byte aligned rows of whole 16 bytes, Q8_0 also of 8), at
 // most 3 matrices (or the gate/up pair).
 bool fused_gemv_rows_ok(const SplitJob& j, bool gu, const int64_t* w_bytes) {
-    if (j.n_tok >= tune("gemm_min_tokens", 32) || (!gu && j.n_mat > 3) ||
+    if (j.n_tok >= tune("gemm_min_tokens", 32) || (!gu && j.n_mat > 4) ||
         !tune("gemv_lanes64", 1) || !tune("fused_gemv", 1))
         return false;
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m)

@@ -1053,14 +1053,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
 //     over the row (from L2), inv = 1/sqrtf(ss/n + eps) as the norm kernels,
 //     and stages (x*inv)*w (w, or 1+w with AERO_NORM_UNIT_OFFSET) in LDS in
 //     place of x; norm < 0: x as is;
-//   * MULTI: up to three matrices of one type and width sharing x in one
-//     launch (q, k, v): workgroups [blk[m], blk[m+1]) take matrix m;
+//   * MULTI: up to four matrices of one type and width sharing x in one
+//     launch (q, k, v; a DeltaNet layer's qkv, gate, alpha, beta):
+//     workgroups [blk[m], blk[m+1]) take matrix m;
 //   * PAIR: row i of w[0] (gate) and of w[1] (up) in the same wave, written
 //     as act(gate . x) * (up . x) (the act·mul op's arithmetic);
 //   * RESID: the residual add before the norm (src/model.cpp:244-245, 284):
 //     every x load also loads d and uses x + d (one fp32 add, as add_rmsnorm),
 //     and workgroup 0 stores x + d to xo, which overlaps neither x nor d (the
 //     other workgroups still read them);
+//   * GATED: the gated-DeltaNet norm in place of the RMSNorm (src/ssm.cpp:
+//     322-340): x / sqrt(mean(x^2) + eps) * norm_w[c % w_len] * silu(z[c]),
+//     the row's sum of squares as the RMSNorm's, z loaded with x;
 //   * RoPE on the outputs of matrices m < rope_mats (q, k; the rotation of
 //     src/attention_layer.cpp:120-156 over every channel of heads of
 //     rope_D rows, angle (float)pos * inv[p] as the RoPE kernel): NeoX
@@ -1070,14 +1074,16 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
 //     in LDS; interleaved pairs (2i, 2i+1) are two rows of one wave.
 // Two rows a wave, as gemv64_kernel<.., 2, ..>.
 struct GemvFuse {
-    const uint8_t* w[3];
-    float* y[3];          // y[m][t * n_rows[m] + r]; PAIR: y[0]
-    int64_t n_rows[3];    // PAIR: n_rows[0] rows of each of gate and up
-    int blk[4];           // MULTI: first workgroup of each matrix, blk[n_mat] = total
+    const uint8_t* w[4];
+    float* y[4];          // y[m][t * n_rows[m] + r]; PAIR: y[0]
+    int64_t n_rows[4];    // PAIR: n_rows[0] rows of each of gate and up
+    int blk[5];           // MULTI: first workgroup of each matrix, blk[4] = total
     const float* x;       // [n_tok][n_cols]
     const float* norm_w;  // nullable (ones)
     const float* d;       // RESID: [n_tok][n_cols], added to x
     float* xo;            // RESID: x + d, written by workgroup 0
+    const float* z;       // GATED: [n_tok][n_cols], the gate
+    int w_len;            // GATED: norm_w's length, tiled over the row
     float eps;
     int norm;             // < 0: no norm; else AERO_NORM_UNIT_OFFSET or 0
     int act;              // PAIR: AERO_ACT_*
@@ -1105,7 +1111,9 @@ __device__ __forceinline__ float act_rt(int kind, float v) {
 // step's weights are requested before the norm is computed (after x, which
 // the norm waits for); for rows of one step the x loaded for the norm is the
 // x staged.
-template <int TYPE, int T, bool PIPE, bool PAIR, bool RESID>
+__device__ __forceinline__ float gate_silu(float v) { return v / (1.0f + expf(-v)); }
+
+template <int TYPE, int T, bool PIPE, bool PAIR, bool RESID, bool GATED = false>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse f) {
     using L = Lane64<TYPE>;
     constexpr int R = (PAIR || T == 4) ? 4 : 2;
@@ -1132,7 +1140,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             rowp[r] = f.w[r < R / 2 ? 0 : 1] + min(r0 + r % (R / 2), f.n_rows[0] - 1) * f.rb;
     } else {
         const int b = blockIdx.x;
-        m = __builtin_amdgcn_readfirstlane((b >= f.blk[1]) + (b >= f.blk[2]));
+        m = __builtin_amdgcn_readfirstlane((b >= f.blk[1]) + (b >= f.blk[2]) + (b >= f.blk[3]));
         if (m < f.rope_mats && f.rope_mode == AERO_ROPE_NEOX) {
             // 2R pairs a workgroup: rows p0 .. p0+2R-1 of the head's first
             // half (waves 0, 1) and of its second half (waves 2, 3)
@@ -1150,6 +1158,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     GemvParams p{nullptr, f.x, nullptr, 0, f.n_cols, f.rb, f.n_tok, f.n_cols, 0};
     GemvParams pd = p;
     pd.x = f.d;
+    GemvParams pz = p;
+    pz.x = f.z;
+    XStepRegs<T> zr;   // GATED: the gate of the step held in xr
+    auto load_z = [&](int st) AERO_INLINE {
+        if constexpr (GATED) xstep_load<T>(pz, st, tid, zr);
+    };
     // this thread's 16 columns of step st for each token: x, or x + d
     auto load_x = [&](int st, XStepRegs<T>& xq) AERO_INLINE {
         xstep_load<T>(p, st, tid, xq);
@@ -1181,9 +1195,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         }
     };
 
-    float inv[T];
+    float inv[T], den[T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) inv[t] = 1.0f;
+    for (int t = 0; t < T; ++t) inv[t] = den[t] = 1.0f;
     // (x * inv) * w (or 1 + w) for this thread's 16 columns of step st; the
     // weights of a step are loaded with its x (load_w), before they are used
     // (branch-free: a load under a branch makes the next wait a full one;
@@ -1192,11 +1206,25 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     const bool unit = has_w && (f.norm & AERO_NORM_UNIT_OFFSET);
     const float* wsrc = has_w ? f.norm_w : f.x;
     auto load_w = [&](int st, v4f (&wv)[4]) AERO_INLINE {
-        const int c0 = has_w ? min(st * kStepCols + 16 * tid, f.n_cols - 16) : 0;
+        int c0 = has_w ? min(st * kStepCols + 16 * tid, f.n_cols - 16) : 0;
+        if constexpr (GATED) c0 %= f.w_len;   // 16 columns inside one period
 #pragma unroll
         for (int q = 0; q < 4; ++q) wv[q] = *reinterpret_cast<const v4f*>(wsrc + c0 + 4 * q);
     };
     auto norm_x = [&](v4f (&wv)[4], XStepRegs<T>& xv) AERO_INLINE {
+        if constexpr (GATED) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v = xv.v[t][q], z = zr.v[t][q];
+                    xv.v[t][q] = make_float4(((v.x / den[t]) * wv[q].x) * gate_silu(z.x),
+                                             ((v.y / den[t]) * wv[q].y) * gate_silu(z.y),
+                                             ((v.z / den[t]) * wv[q].z) * gate_silu(z.z),
+                                             ((v.w / den[t]) * wv[q].w) * gate_silu(z.w));
+                }
+            return;
+        }
         if (f.norm < 0) return;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1217,6 +1245,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     // order, so waiting for x (the norm, the staging) does not wait for W
     XStepRegs<T> xr;
     load_x(0, xr);
+    load_z(0);
     v4f wv[4];
     load_w(0, wv);
     __builtin_amdgcn_sched_barrier(0);  // keeps every x load ahead of the weights
@@ -1265,7 +1294,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             float a = 0.0f;
 #pragma unroll
             for (int w = 0; w < kGemvWaves; ++w) a += red[w][t];
-            inv[t] = 1.0f / sqrtf(a / (float)f.n_cols + f.eps);
+            den[t] = sqrtf(a / (float)f.n_cols + f.eps);
+            inv[t] = 1.0f / den[t];
         }
     }
     float acc[R][T];
@@ -1287,6 +1317,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         for (int st = 0; st < n_st; st += 2) {
             const int s1 = min(st + 1, n_st - 1);
             load_x(s1, xr);
+            load_z(s1);
             load_w(s1, wv);
 #pragma unroll
             for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, l, n_blk);
@@ -1299,6 +1330,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             if (st + 1 >= n_st) break;
             const int s2 = min(st + 2, n_st - 1);
             load_x(s2, xr);
+            load_z(s2);
             load_w(s2, wv);
 #pragma unroll
             for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, l, n_blk);
@@ -1404,6 +1436,26 @@ GemvFusedKernel pick_fused_r(int dtype, int T, bool pipe) {
     case AERO_DTYPE_Q5_K: return pick_fused_t<AERO_DTYPE_Q5_K, PAIR, RESID>(T, pipe);
     case AERO_DTYPE_Q6_K: return pick_fused_t<AERO_DTYPE_Q6_K, PAIR, RESID>(T, pipe);
     case AERO_DTYPE_IQ4_XS: return pick_fused_t<AERO_DTYPE_IQ4_XS, PAIR, RESID>(T, pipe);
+    default: return nullptr;
+    }
+}
+
+template <int TYPE>
+GemvFusedKernel pick_gated_t(int T, bool pipe) {
+    if (T == 1) return pipe ? gemv64_fused_kernel<TYPE, 1, true, false, false, true>
+                            : gemv64_fused_kernel<TYPE, 1, false, false, false, true>;
+    if (T == 2) return pipe ? gemv64_fused_kernel<TYPE, 2, true, false, false, true>
+                            : gemv64_fused_kernel<TYPE, 2, false, false, false, true>;
+    return nullptr;
+}
+
+GemvFusedKernel pick_gated(int dtype, int T, bool pipe) {
+    switch (dtype) {
+    case AERO_DTYPE_Q8_0: return pick_gated_t<AERO_DTYPE_Q8_0>(T, pipe);
+    case AERO_DTYPE_Q4_K: return pick_gated_t<AERO_DTYPE_Q4_K>(T, pipe);
+    case AERO_DTYPE_Q5_K: return pick_gated_t<AERO_DTYPE_Q5_K>(T, pipe);
+    case AERO_DTYPE_Q6_K: return pick_gated_t<AERO_DTYPE_Q6_K>(T, pipe);
+    case AERO_DTYPE_IQ4_XS: return pick_gated_t<AERO_DTYPE_IQ4_XS>(T, pipe);
     default: return nullptr;
     }
 }
@@ -1615,12 +1667,19 @@ bool rope_fold_ok(const RopeFold& rope, bool pair, int n_mat, const int64_t* n_r
 // groups of up to 4 (2 for rows of more than one 4096-column step), one
 // launch a group. Matrices must take gemv64 (16-byte aligned, rows a
 // multiple of 16 bytes). w_bytes[m] >= n_rows[m] * row bytes.
-bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
-                    const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
-                    const float* x, const float* norm_w, float eps, int norm, int act,
-                    int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d,
-                    float* xo, const RopeFold* rope) {
-    const char* what = pair ? "norm_gate_up" : "norm_matvec";
+// The gated-DeltaNet norm as the prologue (GATED): the gate z [n_tok][n_cols]
+// and the length of the tiled norm weight.
+struct GatedIn {
+    const float* z;
+    int64_t w_len;
+};
+
+static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* const* w,
+                            const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                            const float* x, const float* norm_w, float eps, int norm, int act,
+                            int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d,
+                            float* xo, const RopeFold* rope, const GatedIn* gated) {
+    const char* what = gated ? "gated_norm_matvec" : (pair ? "norm_gate_up" : "norm_matvec");
     const bool quant = dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q4_K ||
                        dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q6_K ||
                        dtype == AERO_DTYPE_IQ4_XS;
@@ -1629,7 +1688,7 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
         return false;
     }
     const int64_t bv = dtype_block_values(dtype), bb = dtype_block_bytes(dtype);
-    if (n_mat < 1 || n_mat > 3 || (pair && n_mat != 2) || w == nullptr || w_bytes == nullptr ||
+    if (n_mat < 1 || n_mat > 4 || (pair && n_mat != 2) || w == nullptr || w_bytes == nullptr ||
         n_rows == nullptr || y == nullptr || x == nullptr || n_cols <= 0 || n_cols % bv != 0 ||
         n_cols > (int64_t)1 << 30 || n_tok < 0 || norm > AERO_NORM_UNIT_OFFSET || act < 0 ||
         act > AERO_ACT_IDENTITY) {
@@ -1672,8 +1731,18 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                   rope->mats, rope->D, rope->mode);
         return false;
     }
+    if (gated != nullptr &&
+        (pair || d != nullptr || (rope != nullptr && rope->mats > 0) || norm != 0 ||
+         norm_w == nullptr || gated->z == nullptr || !aligned16(gated->z) ||
+         gated->w_len < 16 || gated->w_len % 16 || n_cols % gated->w_len || n_tok > 2)) {
+        set_error("%s: the gated norm takes a 16-byte aligned gate, a norm weight whose length "
+                  "is a multiple of 16 dividing the row, and at most 2 tokens (n_tok=%lld)",
+                  what, (long long)n_tok);
+        return false;
+    }
     if (n_tok == 0) return true;
     GemvFuse f{};
+    if (gated != nullptr) f.w_len = (int)gated->w_len;
     if (rope != nullptr && rope->mats > 0) {
         f.rope_mats = rope->mats;
         f.rope_D = rope->D;
@@ -1685,12 +1754,12 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
         const int R = (pair || T == 4) ? 4 : 2;
         int64_t tot = 0;
         if (pair) return (n_rows[0] + (int64_t)kGemvWaves * (R / 2) - 1) / (kGemvWaves * (R / 2));
-        for (int m = 0; m < 3; ++m) {
+        for (int m = 0; m < 4; ++m) {
             g.blk[m] = (int)std::min<int64_t>(tot, 0x7fffffff);
             if (m < n_mat) tot += (n_rows[m] + (int64_t)kGemvWaves * R - 1) / (kGemvWaves * R);
         }
-        for (int m = n_mat; m < 3; ++m) g.blk[m] = 0x7fffffff;  // never reached
-        g.blk[3] = (int)std::min<int64_t>(tot, 0x7fffffff);
+        for (int m = n_mat; m < 4; ++m) g.blk[m] = 0x7fffffff;  // never reached
+        g.blk[4] = (int)std::min<int64_t>(tot, 0x7fffffff);
         return tot;
     };
     for (int m = 0; m < n_mat; ++m) {
@@ -1708,7 +1777,8 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
     for (int64_t t0 = 0; t0 < n_tok; t0 += t_max) {
         const int nt = (int)std::min<int64_t>(t_max, n_tok - t0);
         const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
-        GemvFusedKernel k = pick_fused(pair, d != nullptr, dtype, T, pipe);
+        GemvFusedKernel k = gated ? pick_gated(dtype, T, pipe)
+                              : pick_fused(pair, d != nullptr, dtype, T, pipe);
         if (k == nullptr) {
             set_error("%s: no kernel for %d tokens", what, T);
             return false;
@@ -1717,6 +1787,7 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
         f.pos = f.rope_mats > 0 ? rope->pos + t0 : nullptr;
         f.d = d ? d + t0 * n_cols : nullptr;
         f.xo = d ? xo + t0 * n_cols : nullptr;
+        f.z = gated ? gated->z + t0 * n_cols : nullptr;
         f.n_tok = nt;
         for (int m = 0; m < (pair ? 1 : n_mat); ++m) f.y[m] = y[m] + t0 * n_rows[m];
         const int64_t total = grid_of(T, f);
@@ -1730,6 +1801,23 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
             return false;
     }
     return true;
+}
+
+bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
+                    const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
+                    const float* x, const float* norm_w, float eps, int norm, int act,
+                    int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d,
+                    float* xo, const RopeFold* rope) {
+    return gemv_fused_impl(dtype, pair, n_mat, w, w_bytes, n_rows, y, x, norm_w, eps, norm, act,
+                           n_cols, n_tok, s, d, xo, rope, nullptr);
+}
+
+bool gemv_gated_dev(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows, float* y,
+                    const float* x, const float* z, const float* norm_w, int64_t w_len,
+                    float eps, int64_t n_cols, int64_t n_tok, hipStream_t s) {
+    const GatedIn g{z, w_len};
+    return gemv_fused_impl(dtype, false, 1, &w, &w_bytes, &n_rows, &y, x, norm_w, eps, 0,
+                           AERO_ACT_IDENTITY, n_cols, n_tok, s, nullptr, nullptr, nullptr, &g);
 }
 
 }  // namespace aero
@@ -1749,6 +1837,15 @@ int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w, const in
     return aero::gemv_fused_dev(dtype, false, n_mat, w, w_bytes, n_rows, y, x, norm_w, eps, norm,
                                 AERO_ACT_IDENTITY, n_cols, n_tok, (hipStream_t)stream, nullptr,
                                 nullptr, nullptr) ? 1 : 0;
+}
+
+int aero_hip_gated_norm_matvec(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows,
+                               float* y, const float* x, const float* z, const float* norm_w,
+                               int64_t w_len, float eps, int64_t n_cols, int64_t n_tok,
+                               void* stream) {
+    aero::clear_error();
+    return aero::gemv_gated_dev(dtype, w, w_bytes, n_rows, y, x, z, norm_w, w_len, eps, n_cols,
+                                n_tok, (hipStream_t)stream) ? 1 : 0;
 }
 
 int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up, int64_t w_bytes,

@@ -41,8 +41,9 @@ __device__ __forceinline__ float softplus_dev(float x) {
 }
 
 // G = d / 4 lanes per (token t, key head kk) row, each normalising 4
-// adjacent elements of q and k (one 16-byte load of each), 256 / G rows a
-// workgroup; the group of kk == 0 also writes dec and b of token t for every
+// adjacent elements of q and k (one 16-byte load of each; token rows
+// q_stride / k_stride floats apart), 256 / G rows a workgroup; qn and kn are
+// written contiguous [T][n_k][d]; the group of kk == 0 also writes dec and b of token t for every
 // value head (log_dec: the log of the decay, g <= 0, in place of exp(g), for
 // the chunked scan).
 template <int G>
@@ -51,14 +52,14 @@ __global__ __launch_bounds__(256) void ssm_prep_kernel(
     const float* __restrict__ beta, const float* __restrict__ a_log,
     const float* __restrict__ dt_bias, float* __restrict__ qn, float* __restrict__ kn,
     float* __restrict__ dec, float* __restrict__ bb, int64_t n_rows, int64_t n_k, int64_t n_v,
-    float eps, int log_dec) {
+    int64_t q_stride, int64_t k_stride, float eps, int log_dec) {
     constexpr int D = 4 * G;
     const int lane = threadIdx.x % G;
     const int64_t row = (int64_t)blockIdx.x * (256 / G) + threadIdx.x / G;  // t * n_k + kk
     if (row >= n_rows) return;   // whole groups: the sums below stay inside a group
     const int64_t t = row / n_k, kk = row % n_k;
-    const v4f qv = *reinterpret_cast<const v4f*>(q + row * D + 4 * lane);
-    const v4f kv = *reinterpret_cast<const v4f*>(k + row * D + 4 * lane);
+    const v4f qv = *reinterpret_cast<const v4f*>(q + t * q_stride + kk * D + 4 * lane);
+    const v4f kv = *reinterpret_cast<const v4f*>(k + t * k_stride + kk * D + 4 * lane);
     float sq = 0.0f, sk = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -107,6 +108,7 @@ struct ScanArgs {
     const float* q;        // [T][n_k][D]: raw (FUSED) or normalised (workspace)
     const float* k;
     const float* v;        // [T][n_v][D]
+    int64_t qs, ks, vs;    // floats from one token's q / k / v row to the next
     const float* alpha;    // [T][n_v]: raw alpha (FUSED) or the decay (workspace)
     const float* beta;     // [T][n_v]: raw beta (FUSED) or the gate (workspace)
     const float* a_log;    // [n_v] (FUSED)
@@ -130,15 +132,15 @@ struct TokenOps {
 template <int D, int RPT, bool FUSED>
 __device__ __forceinline__ void load_token(const ScanArgs& a, int64_t t, int64_t h, int64_t kk,
                                            int e, int i0, TokenOps<D, RPT>& o) {
-    const float4* k4 = reinterpret_cast<const float4*>(a.k + (t * a.n_k + kk) * D + i0);
-    const float4* q4 = reinterpret_cast<const float4*>(a.q + (t * a.n_k + kk) * D + i0);
+    const float4* k4 = reinterpret_cast<const float4*>(a.k + t * a.ks + kk * D + i0);
+    const float4* q4 = reinterpret_cast<const float4*>(a.q + t * a.qs + kk * D + i0);
 #pragma unroll
     for (int j = 0; j < RPT / 4; ++j) {
         const float4 x = k4[j], y = q4[j];
         o.k[4 * j] = x.x; o.k[4 * j + 1] = x.y; o.k[4 * j + 2] = x.z; o.k[4 * j + 3] = x.w;
         o.q[4 * j] = y.x; o.q[4 * j + 1] = y.y; o.q[4 * j + 2] = y.z; o.q[4 * j + 3] = y.w;
     }
-    o.v = a.v[(t * a.n_v + h) * D + e];
+    o.v = a.v[t * a.vs + h * D + e];
     o.dec = a.alpha[t * a.n_v + h];
     o.b = a.beta[t * a.n_v + h];
 }
@@ -149,8 +151,8 @@ template <int D, int RPT, bool FUSED>
 __device__ __forceinline__ void finish_token(const ScanArgs& a, int64_t t, int64_t h,
                                              int64_t kk, int lane, TokenOps<D, RPT>& o) {
     if constexpr (FUSED) {
-        const float* kr = a.k + (t * a.n_k + kk) * D;
-        const float* qr = a.q + (t * a.n_k + kk) * D;
+        const float* kr = a.k + t * a.ks + kk * D;
+        const float* qr = a.q + t * a.qs + kk * D;
         float sk = 0.0f, sq = 0.0f;
 #pragma unroll
         for (int i = lane; i < D; i += 64) {
@@ -260,8 +262,17 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(ScanArgs a) {
     }
 }
 
+// silu in the reference's division form (src/ssm.cpp:17), applied to the
+// conv's outputs when the SSM layer asks for it (src/ssm.cpp:298-301)
+template <bool SILU>
+__device__ __forceinline__ float conv_out(float v) {
+    if constexpr (SILU) return v / (1.0f + expf(-v));
+    return v;
+}
+
 // out[t, c] = sum_j buf[tl + t + 1 - K + j, c] * w[c, j] over the rows that
 // exist, buf = [tail (tl rows); x], taps in order, tap 0 the oldest.
+template <bool SILU>
 __global__ __launch_bounds__(256) void ssm_conv_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
                                                        const float* __restrict__ tail,
@@ -277,19 +288,22 @@ __global__ __launch_bounds__(256) void ssm_conv_kernel(const float* __restrict__
         const float in = b < tl ? tail[b * C + c] : x[(b - tl) * C + c];
         acc = acc + in * w[c * K + j];
     }
-    out[idx] = acc;
+    out[idx] = conv_out<SILU>(acc);
 }
 
 // The same conv with K fixed: a lane owns channel c for TB consecutive
 // tokens, holding its K weights and a sliding window of K inputs in
 // registers, so each input is loaded once (plus K - 1 rows of halo a block).
-// Taps before the start of the history are skipped, as above.
-template <int K, int TB>
-__global__ __launch_bounds__(256) void ssm_conv_k_kernel(const float* __restrict__ x,
-                                                         const float* __restrict__ w,
-                                                         const float* __restrict__ tail,
-                                                         float* __restrict__ out, int64_t tl,
-                                                         int64_t T, int64_t C) {
+// Taps before the start of the history are skipped, as above. With one
+// block of tokens (T <= TB) and tail_out given, the lane also writes its
+// channel's new history, the last keep rows of [tail; x], from the window
+// after its last token: it has read every history row of the channel by
+// then, so tail_out may be tail.
+template <int K, int TB, bool SILU>
+__global__ __launch_bounds__(256) void ssm_conv_k_kernel(const float* x, const float* __restrict__ w,
+                                                         const float* tail, float* __restrict__ out,
+                                                         int64_t tl, int64_t T, int64_t C,
+                                                         float* tail_out, int keep) {
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (c >= C) return;
     const int64_t t0 = (int64_t)blockIdx.y * TB;
@@ -312,12 +326,18 @@ __global__ __launch_bounds__(256) void ssm_conv_k_kernel(const float* __restrict
 #pragma unroll
         for (int j = 0; j < K; ++j)
             if (ok[j]) acc = acc + win[j] * wr[j];
-        out[t * C + c] = acc;
+        out[t * C + c] = conv_out<SILU>(acc);
 #pragma unroll
         for (int j = 0; j < K - 1; ++j) {
             win[j] = win[j + 1];
             ok[j] = ok[j + 1];
         }
+    }
+    // the window now holds rows tl + T - (K - 1) .. tl + T - 1 of [tail; x]
+    if (tail_out != nullptr) {
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i)
+            if (i < keep) tail_out[(int64_t)i * C + c] = win[K - 1 - keep + i];
     }
 }
 
@@ -326,7 +346,7 @@ __global__ __launch_bounds__(256) void ssm_conv_k_kernel(const float* __restrict
 // T) loads its TB + 3 rows as 16-byte loads up front, so the loads overlap;
 // other blocks take the per-channel sliding window of ssm_conv_k_kernel.
 // Same tap order, separate multiply and add from 0: bit-identical results.
-template <int TB>
+template <int TB, bool SILU>
 __global__ __launch_bounds__(256) void ssm_conv4_kernel(const float* __restrict__ x,
                                                         const float* __restrict__ w,
                                                         const float* __restrict__ tail,
@@ -352,7 +372,7 @@ __global__ __launch_bounds__(256) void ssm_conv4_kernel(const float* __restrict_
                 float s = 0.0f;
 #pragma unroll
                 for (int j = 0; j < K; ++j) s = s + in[tt + j][e] * wv[e][j];
-                acc[e] = s;
+                acc[e] = conv_out<SILU>(s);
             }
             *reinterpret_cast<v4f*>(out + (t0 + tt) * C + c) = acc;
         }
@@ -376,7 +396,7 @@ __global__ __launch_bounds__(256) void ssm_conv4_kernel(const float* __restrict_
 #pragma unroll
             for (int j = 0; j < K; ++j)
                 if (ok[j]) acc = acc + win[j] * wv[e][j];
-            out[t * C + ch] = acc;
+            out[t * C + ch] = conv_out<SILU>(acc);
 #pragma unroll
             for (int j = 0; j < K - 1; ++j) {
                 win[j] = win[j + 1];
@@ -447,7 +467,8 @@ constexpr int kChunk = 64;
 struct ChunkArgs {
     const float* qn;    // [T][n_k][D] normalised
     const float* kn;
-    const float* v;     // [T][n_v][D]
+    const float* v;     // [T][n_v][D], token rows vs floats apart
+    int64_t vs;
     const float* lg;    // [T][n_v] log decay (<= 0)
     const float* bb;    // [T][n_v] gate
     float* U;           // [n_v][nc][C][D]
@@ -533,7 +554,7 @@ __global__ __launch_bounds__(256) void ssm_chunk_prep_kernel(ChunkArgs a) {
             const float* vsrc = a.v + h * D + c0 + 4 * r;
 #pragma unroll
             for (int ks = 0; ks < C / 4; ++ks)
-                pre[16 * cg + ks] = *reinterpret_cast<const v4f*>(vsrc + (t0 + min(4 * ks + g, n - 1)) * a.n_v * D);
+                pre[16 * cg + ks] = *reinterpret_cast<const v4f*>(vsrc + (t0 + min(4 * ks + g, n - 1)) * a.vs);
         }
     }
     // the chunk's normalised keys (rows past n zero)
@@ -1134,13 +1155,22 @@ int64_t ssm_workspace_bytes(int64_t T, int64_t n_k, int64_t n_v, int64_t d) {
     return b;
 }
 
-bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* alpha,
-                  const float* beta, const float* a_log, const float* dt_bias, float* state,
-                  int64_t T, int64_t n_k, int64_t n_v, int64_t d, float scale, float eps,
-                  float* outs, void* workspace, int64_t ws_bytes, hipStream_t s) {
+// q, k and v token rows qs, ks, vs floats apart (the reference's
+// scan_strided, src/ssm.cpp:128-142: the SSM layer scans slices of its packed
+// qkv rows); outs contiguous [T][n_v][d].
+bool ssm_scan_strided_dev(const float* q, int64_t qs, const float* k, int64_t ks, const float* v,
+                          int64_t vs, const float* alpha, const float* beta, const float* a_log,
+                          const float* dt_bias, float* state, int64_t T, int64_t n_k, int64_t n_v,
+                          int64_t d, float scale, float eps, float* outs, void* workspace,
+                          int64_t ws_bytes, hipStream_t s) {
     if (T < 0 || n_k <= 0 || n_v <= 0 || n_v % n_k || d <= 0) {
         set_error("ssm_scan: bad sizes (T=%lld n_k=%lld n_v=%lld d=%lld)", (long long)T,
                   (long long)n_k, (long long)n_v, (long long)d);
+        return false;
+    }
+    if (qs < n_k * d || ks < n_k * d || vs < n_v * d || qs % 4 || ks % 4 || vs % 4) {
+        set_error("ssm_scan: row strides (q %lld, k %lld, v %lld) must cover a token's heads "
+                  "and be multiples of 4 floats", (long long)qs, (long long)ks, (long long)vs);
         return false;
     }
     if (T == 0) return true;
@@ -1166,7 +1196,8 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
     const int64_t cw = 4 * (64 / P);
     const dim3 grid((unsigned)n_v, (unsigned)(d / cw));
     if (fused) {
-        ScanArgs sa{q, k, v, alpha, beta, a_log, dt_bias, state, outs, T, n_k, n_v, scale, eps};
+        ScanArgs sa{q, k, v, qs, ks, vs, alpha, beta, a_log, dt_bias, state, outs, T, n_k, n_v,
+                    scale, eps};
         return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);
     }
     const int64_t need = ssm_workspace_bytes(T, n_k, n_v, d);
@@ -1188,11 +1219,13 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
         const int ld = chunked ? 1 : 0;
         const bool ok =
             d == 64 ? launch("ssm_prep_kernel", ssm_prep_kernel<16>, pg, dim3(256), 0, s, q, k, alpha,
-                             beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, eps, ld)
+                             beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, qs, ks, eps, ld)
             : d == 128 ? launch("ssm_prep_kernel", ssm_prep_kernel<32>, pg, dim3(256), 0, s, q, k,
-                                alpha, beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, eps, ld)
+                                alpha, beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, qs, ks,
+                                eps, ld)
                        : launch("ssm_prep_kernel", ssm_prep_kernel<64>, pg, dim3(256), 0, s, q, k,
-                                alpha, beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, eps, ld);
+                                alpha, beta, a_log, dt_bias, qn, kn, dc, bb, rows, n_k, n_v, qs, ks,
+                                eps, ld);
         if (!ok) return false;
     }
     if (chunked) {
@@ -1206,6 +1239,7 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
         ca.qn = qn;
         ca.kn = kn;
         ca.v = v;
+        ca.vs = vs;
         ca.lg = dc;
         ca.bb = bb;
         ca.U = reinterpret_cast<float*>(cw);
@@ -1247,13 +1281,23 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
                (split ? launch("ssm_chunk_split_kernel", ssm_chunk_split_kernel<128>, sgrid, dim3(512), 0, s, ca)
                       : launch("ssm_chunk_scan_kernel", ssm_chunk_scan_kernel<128, 1>, sgrid, dim3(256), 0, s, ca));
     }
-    ScanArgs sa{qn, kn, v, dc, bb, nullptr, nullptr, state, outs, T, n_k, n_v, scale, eps};
+    ScanArgs sa{qn, kn, v, n_k * d, n_k * d, vs, dc, bb, nullptr, nullptr, state, outs, T, n_k,
+                n_v, scale, eps};
     return launch("ssm_scan_kernel", kern, grid, dim3(kScanThreads), 0, s, sa);
 }
 
-bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tail_len,
-                  float* tail_out, float* out, int64_t T, int64_t C, int64_t K,
-                  int64_t* new_tail_len, hipStream_t s) {
+bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* alpha,
+                  const float* beta, const float* a_log, const float* dt_bias, float* state,
+                  int64_t T, int64_t n_k, int64_t n_v, int64_t d, float scale, float eps,
+                  float* outs, void* workspace, int64_t ws_bytes, hipStream_t s) {
+    return ssm_scan_strided_dev(q, n_k * d, k, n_k * d, v, n_v * d, alpha, beta, a_log, dt_bias,
+                                state, T, n_k, n_v, d, scale, eps, outs, workspace, ws_bytes, s);
+}
+
+// silu: out = silu(conv) (the SSM layer's order, src/ssm.cpp:298-301)
+bool ssm_conv_act_dev(const float* x, const float* w, const float* tail, int64_t tail_len,
+                      float* tail_out, float* out, int64_t T, int64_t C, int64_t K, bool silu,
+                      int64_t* new_tail_len, hipStream_t s) {
     if (T < 0 || C <= 0 || K <= 0 || K - 1 > kMaxConvKeep || tail_len < 0 ||
         tail_len > K - 1 || (T > 0 && (x == nullptr || out == nullptr)) || w == nullptr ||
         (tail_len > 0 && tail == nullptr)) {
@@ -1272,30 +1316,41 @@ bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tai
         return false;
     }
     constexpr int kTB = 32, kTB4 = 16;
+    bool tail_done = false;
     // the 4-channel form from 64 tokens (short calls are all boundary blocks:
     // the one-channel form spreads them over 4x the lanes)
     if (T >= 4 * kTB4 && K == 4 && C % 4 == 0 && aligned16(x) && aligned16(w) &&
         aligned16(out) && (T + kTB4 - 1) / kTB4 <= 65535) {
-        if (!launch("ssm_conv_kernel", ssm_conv4_kernel<kTB4>,
-                    dim3((unsigned)((C / 4 + 255) / 256), (unsigned)((T + kTB4 - 1) / kTB4)),
-                    dim3(256), 0, s, x, w, tail, out, tail_len, T, C))
+        const dim3 grid((unsigned)((C / 4 + 255) / 256), (unsigned)((T + kTB4 - 1) / kTB4));
+        if (!launch("ssm_conv_kernel", silu ? ssm_conv4_kernel<kTB4, true> : ssm_conv4_kernel<kTB4, false>,
+                    grid, dim3(256), 0, s, x, w, tail, out, tail_len, T, C))
             return false;
     } else if (T > 0) {
+        const dim3 gk((unsigned)((C + 255) / 256), (unsigned)((T + kTB - 1) / kTB));
+        const dim3 g1((unsigned)((T * C + 255) / 256));
+        // one block of tokens: the conv kernel writes the new history itself
+        tail_done = K == 4 && T <= kTB;
+        float* to = tail_done ? tail_out : nullptr;
         const bool ok =
             (K == 4 && (T + kTB - 1) / kTB <= 65535)
-                ? launch("ssm_conv_kernel", ssm_conv_k_kernel<4, kTB>,
-                         dim3((unsigned)((C + 255) / 256), (unsigned)((T + kTB - 1) / kTB)),
-                         dim3(256), 0, s, x, w, tail, out, tail_len, T, C)
-                : launch("ssm_conv_kernel", ssm_conv_kernel, dim3((unsigned)((T * C + 255) / 256)),
+                ? launch("ssm_conv_kernel", silu ? ssm_conv_k_kernel<4, kTB, true> : ssm_conv_k_kernel<4, kTB, false>,
+                         gk, dim3(256), 0, s, x, w, tail, out, tail_len, T, C, to, (int)keep)
+                : launch("ssm_conv_kernel", silu ? ssm_conv_kernel<true> : ssm_conv_kernel<false>, g1,
                          dim3(256), 0, s, x, w, tail, out, tail_len, T, C, (int)K);
         if (!ok) return false;
     }
-    if (keep > 0 && !launch("ssm_conv_tail_kernel", ssm_conv_tail_kernel,
+    if (keep > 0 && !tail_done && !launch("ssm_conv_tail_kernel", ssm_conv_tail_kernel,
                             dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s, x, tail,
                             tail_out, tail_len, T, C, (int)keep))
         return false;
     if (new_tail_len) *new_tail_len = keep;
     return true;
+}
+
+bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tail_len,
+                  float* tail_out, float* out, int64_t T, int64_t C, int64_t K,
+                  int64_t* new_tail_len, hipStream_t s) {
+    return ssm_conv_act_dev(x, w, tail, tail_len, tail_out, out, T, C, K, false, new_tail_len, s);
 }
 
 }  // namespace aero
@@ -1321,6 +1376,26 @@ int aero_hip_ssm_conv(const float* x, const float* w, const float* tail, int64_t
     aero::clear_error();
     return aero::ssm_conv_dev(x, w, tail, tail_len, tail_out, out, T, channels, kernel,
                               new_tail_len, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_ssm_scan_strided(const float* q, int64_t q_stride, const float* k, int64_t k_stride,
+                              const float* v, int64_t v_stride, const float* alpha,
+                              const float* beta, const float* a_log, const float* dt_bias,
+                              float* state, int64_t T, int64_t n_k, int64_t n_v, int64_t d,
+                              float scale, float eps, float* outs, void* workspace,
+                              int64_t ws_bytes, void* stream) {
+    aero::clear_error();
+    return aero::ssm_scan_strided_dev(q, q_stride, k, k_stride, v, v_stride, alpha, beta, a_log,
+                                      dt_bias, state, T, n_k, n_v, d, scale, eps, outs, workspace,
+                                      ws_bytes, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_ssm_conv_silu(const float* x, const float* w, const float* tail, int64_t tail_len,
+                           float* tail_out, float* out, int64_t T, int64_t channels,
+                           int64_t kernel, int64_t* new_tail_len, void* stream) {
+    aero::clear_error();
+    return aero::ssm_conv_act_dev(x, w, tail, tail_len, tail_out, out, T, channels, kernel, true,
+                                  new_tail_len, (hipStream_t)stream) ? 1 : 0;
 }
 
 }  // extern "C"

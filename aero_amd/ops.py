@@ -257,10 +257,10 @@ def norm_matvec(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_
                 n_tok: int = 1, norm_w: DeviceArray | None = None, eps: float = 1e-5,
                 norm: bool = True, unit_offset: bool = False,
                 stream: Stream | None = None) -> None:
-    """ys[m] = rmsnorm(x) @ W_m^T for up to 3 matrices of one type sharing x
+    """ys[m] = rmsnorm(x) @ W_m^T for up to 4 matrices of one type sharing x
     (q, k, v), in one launch per 4 tokens; norm=False uses x as is."""
-    if not 1 <= len(ws) <= 3 or len(ys) != len(ws) or len(n_rows) != len(ws):
-        raise ValueError("norm_matvec: 1 to 3 matrices, with as many outputs and row counts")
+    if not 1 <= len(ws) <= 4 or len(ys) != len(ws) or len(n_rows) != len(ws):
+        raise ValueError("norm_matvec: 1 to 4 matrices, with as many outputs and row counts")
     _need(x, n_tok * n_cols, np.float32, "x")
     _need(norm_w, n_cols, np.float32, "norm_w")
     for y, nr in zip(ys, n_rows):
@@ -296,6 +296,22 @@ def norm_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceAr
 
 
 _norm_mm_ws = Workspace("norm GEMM")
+
+
+def gated_norm_matvec(dtype: int, w: DeviceArray, x: DeviceArray, z: DeviceArray,
+                      norm_w: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
+                      n_tok: int, eps: float, stream: Stream | None = None) -> None:
+    """y = gated_rmsnorm_silu(x, z, tile(norm_w)) @ W^T over whole rows, the
+    norm in the GEMV's prologue (src/ssm.cpp:322-348, a DeltaNet layer's
+    gated norm and output projection); up to 2 tokens."""
+    _need(x, n_tok * n_cols, np.float32, "x")
+    _need(z, n_tok * n_cols, np.float32, "z")
+    _need(y, n_tok * n_rows, np.float32, "y")
+    _need(norm_w, 1, np.float32, "norm_w")
+    _lib.check(_lib.lib().aero_hip_gated_norm_matvec(int(dtype), w.ptr, w.nbytes, n_rows, y.ptr,
+                                                     x.ptr, z.ptr, norm_w.ptr, norm_w.size,
+                                                     float(eps), n_cols, n_tok, _s(stream)),
+               "gated_norm_matvec")
 
 
 def _norm_flag(norm: bool, unit_offset: bool) -> int:
@@ -459,16 +475,22 @@ _ssm_ws = Workspace("DeltaNet scan")
 def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
              beta: DeviceArray, a_log: DeviceArray, dt_bias: DeviceArray, state: DeviceArray,
              outs: DeviceArray, T: int, n_k: int, n_v: int, d: int, scale: float,
-             eps: float = 1e-6, stream: Stream | None = None) -> None:
+             eps: float = 1e-6, strides: tuple | None = None, q_off: int = 0, k_off: int = 0,
+             v_off: int = 0, stream: Stream | None = None) -> None:
     """Gated delta-rule scan over T tokens (src/ssm.cpp:69-142): q, k
     [T, n_k, d], v / outs [T, n_v, d], alpha / beta [T, n_v], a_log / dt_bias
-    [n_v], state [n_v, d, d] updated in place. The workspace (normalised q / k,
+    [n_v], state [n_v, d, d] updated in place. strides = (q, k, v) floats
+    between token rows, with q / k / v starting q_off / k_off / v_off floats
+    into their arrays: slices of one packed qkv buffer, as scan_strided
+    (src/ssm.cpp:128-142) reads them. The workspace (normalised q / k,
     per-token decay and gate; the chunked form's operands from 128 tokens) is
     one buffer, grown when a call needs more and reused by smaller calls, so
     calls on different streams must not overlap."""
-    _need(q, T * n_k * d, np.float32, "q")
-    _need(k, T * n_k * d, np.float32, "k")
-    _need(v, T * n_v * d, np.float32, "v")
+    qs, ks, vs = strides if strides is not None else (n_k * d, n_k * d, n_v * d)
+    span = lambda stride, off, w: off + (T - 1) * stride + w if T > 0 else 0
+    _need(q, span(qs, q_off, n_k * d), np.float32, "q")
+    _need(k, span(ks, k_off, n_k * d), np.float32, "k")
+    _need(v, span(vs, v_off, n_v * d), np.float32, "v")
     _need(outs, T * n_v * d, np.float32, "outs")
     _need(alpha, T * n_v, np.float32, "alpha")
     _need(beta, T * n_v, np.float32, "beta")
@@ -477,27 +499,39 @@ def ssm_scan(q: DeviceArray, k: DeviceArray, v: DeviceArray, alpha: DeviceArray,
     _need(state, n_v * d * d, np.float32, "state")
     L = _lib.lib()
     ws = _ssm_ws.get(int(L.aero_hip_ssm_workspace(T, n_k, n_v, d)))
-    _lib.check(L.aero_hip_ssm_scan(q.ptr, k.ptr, v.ptr, alpha.ptr, beta.ptr, a_log.ptr,
-                                   dt_bias.ptr, state.ptr, T, n_k, n_v, d, float(scale),
-                                   float(eps), outs.ptr, as_ptr(ws),
-                                   ws.nbytes if ws is not None else 0, _s(stream)),
-               "ssm_scan")
+    if strides is None and q_off == k_off == v_off == 0:
+        _lib.check(L.aero_hip_ssm_scan(q.ptr, k.ptr, v.ptr, alpha.ptr, beta.ptr, a_log.ptr,
+                                       dt_bias.ptr, state.ptr, T, n_k, n_v, d, float(scale),
+                                       float(eps), outs.ptr, as_ptr(ws),
+                                       ws.nbytes if ws is not None else 0, _s(stream)),
+                   "ssm_scan")
+        return
+    _lib.check(L.aero_hip_ssm_scan_strided(q.ptr + 4 * q_off, qs, k.ptr + 4 * k_off, ks,
+                                           v.ptr + 4 * v_off, vs, alpha.ptr, beta.ptr,
+                                           a_log.ptr, dt_bias.ptr, state.ptr, T, n_k, n_v, d,
+                                           float(scale), float(eps), outs.ptr, as_ptr(ws),
+                                           ws.nbytes if ws is not None else 0, _s(stream)),
+               "ssm_scan_strided")
 
 
 def ssm_conv(x: DeviceArray, w: DeviceArray, tail: DeviceArray | None, tail_len: int,
              tail_out: DeviceArray | None, out: DeviceArray, T: int, channels: int,
-             kernel: int, stream: Stream | None = None) -> int:
+             kernel: int, silu: bool = False, stream: Stream | None = None) -> int:
     """Causal depthwise conv over [tail; x] (src/ssm.cpp:173-210); the new
-    history goes to tail_out (which may be tail). Returns its length."""
+    history goes to tail_out (which may be tail). Returns its length. silu:
+    out = silu(conv), the SSM layer's next step (src/ssm.cpp:298-301), in the
+    same pass."""
     _need(x, T * channels, np.float32, "x")
     _need(out, T * channels, np.float32, "out")
     _need(w, channels * kernel, np.float32, "w")
     _need(tail, tail_len * channels, np.float32, "tail")
     _need(tail_out, (kernel - 1) * channels, np.float32, "tail_out")
     n = ctypes.c_int64()
-    _lib.check(_lib.lib().aero_hip_ssm_conv(x.ptr, w.ptr, as_ptr(tail), int(tail_len),
-                                            as_ptr(tail_out), out.ptr, T, channels, kernel,
-                                            ctypes.byref(n), _s(stream)), "ssm_conv")
+    L = _lib.lib()
+    fn = L.aero_hip_ssm_conv_silu if silu else L.aero_hip_ssm_conv
+    _lib.check(fn(x.ptr, w.ptr, as_ptr(tail), int(tail_len), as_ptr(tail_out), out.ptr, T,
+                  channels, kernel, ctypes.byref(n), _s(stream)),
+               "ssm_conv_silu" if silu else "ssm_conv")
     return int(n.value)
 
 

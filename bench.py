@@ -42,6 +42,7 @@ dequant over the same rows beside it.
     python bench.py --attention         # attention over a KV cache (decode, prefill)
     python bench.py --gguf              # GGUF parse, upload to HBM, device row addressing
     python bench.py --ssm               # gated DeltaNet scan and conv
+    python bench.py --ssm-layer         # one gated-DeltaNet layer (projections .. out)
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
     python bench.py --copy-sweep        # plain copies from 2 MiB to 1 GiB
@@ -92,6 +93,8 @@ def parse_args(argv=None):
     p.add_argument("--gemv", action="store_true", help="quantised GEMV cases")
     p.add_argument("--ssm", action="store_true",
                    help="gated DeltaNet scan and causal conv (Qwen3-Next heads)")
+    p.add_argument("--ssm-layer", action="store_true",
+                   help="one gated-DeltaNet layer at Qwen3-Next's size (prefill and decode)")
     p.add_argument("--gguf", action="store_true",
                    help="GGUF parse, file-to-HBM upload and device row addressing")
     p.add_argument("--attention", action="store_true",
@@ -612,6 +615,8 @@ def main(argv=None):
         return gguf_bench(a)
     if a.ssm:
         return ssm_bench(a)
+    if a.ssm_layer:
+        return ssm_layer_bench(a)
 
     name = a.shape or W.HEADLINE
     path = Path(name, a.sets)
@@ -1614,6 +1619,89 @@ def ssm_bench(a):
                 res["speedup_vs_cpu_scan"] = round(per_tok * T / op_us, 1)
         print(json.dumps(res), flush=True)
     stream.destroy()
+    return 0
+
+
+SSM_LAYER_CASES = [
+    # (name, tokens): Qwen3-Next's linear-attention layer, hidden 2048, 16 key
+    # and 32 value heads of 128, conv kernel 4, Q4_K projections
+    ("prefill_4096", 4096), ("decode", 1),
+]
+
+
+def ssm_layer_bench(a):
+    """One gated-DeltaNet layer (aero_amd.ssm_layer, aero_ssm_forward_q of
+    src/ssm.cpp:262-352) recorded as a plan: mean time per layer over plan
+    replays, per-launch device times (an event pair a launch), the weight
+    bytes a call streams; the reference's aero_ssm_forward_q on a bounded
+    sample of tokens on one host core beside it."""
+    from aero_amd import ssm_layer as S
+    from aero_amd import workloads as W
+    from aero_amd.device import Event, Plan, Stream
+
+    cfg = S.SsmConfig(2048, 16, 32, 128, 4, (W.Q4_K,) * 5)
+    wts = S.SsmWeights(cfg, seed=0)
+    w_bytes = sum(wts.host[n].nbytes for n in S.PROJ)
+    rng = np.random.default_rng(0)
+    for name, T in SSM_LAYER_CASES:
+        step = S.SsmStep(cfg, wts, max_tokens=T)
+        step.x.view((T, cfg.hidden)).copy_from(rng.standard_normal((T, cfg.hidden),
+                                                                   dtype=np.float32))
+        step.forward(T)            # conv history at kernel - 1 rows from here on
+        stream = Stream()
+        plan = Plan()
+        with plan:
+            step.forward(T, stream=stream)
+        n = len(plan)
+        reps = a.steps if T == 1 else max(5, a.steps // 10)
+        for _ in range(a.warmup):
+            plan.launch(stream)
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(reps):
+            plan.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+        starts, stops = [Event() for _ in range(n)], [Event() for _ in range(n)]
+        ev = plan.event_arrays(starts, stops)
+        kern = [[] for _ in range(n)]
+        for _ in range(3):
+            plan.launch(stream, ev)
+            stream.synchronize()
+            for i, (x, y) in enumerate(zip(starts, stops)):
+                kern[i].append(x.elapsed_ms(y) * 1e3)
+        res = {"case": name, "tokens": T, "hidden": cfg.hidden, "heads": [cfg.n_k, cfg.n_v],
+               "d": cfg.head_dim, "weights": "Q4_K", "launches": n,
+               "us_per_layer": round(us, 2), "us_per_token": round(us / T, 4),
+               "launch_us": [round(statistics.mean(k), 2) for k in kern],
+               "weight_bytes": w_bytes,
+               "weight_GB/s": round(w_bytes / (us * 1e-6) / 1e9, 1)}
+        if not a.no_cpu:
+            from oracle import refbind
+            if refbind.ssm() is not None:
+                h = wts.host
+                Ts = min(T, 2)
+                case = dict(dts=list(cfg.wtypes), weights=[h[k] for k in S.PROJ],
+                            a_log=h["a_log"], dt_bias=h["dt_bias"], conv1d=h["conv1d"],
+                            norm=h["norm"], n_k=cfg.n_k, d=cfg.head_dim, inner=cfg.inner,
+                            eps=cfg.eps, norm_eps=cfg.norm_eps)
+                x = rng.standard_normal((Ts, cfg.hidden)).astype(np.float32)
+                tail = np.zeros((cfg.conv_kernel - 1, cfg.qkv), np.float32)
+                st = np.zeros((cfg.n_v, cfg.head_dim, cfg.head_dim), np.float32)
+                calls, t0 = 0, time.perf_counter()
+                while calls == 0 or time.perf_counter() - t0 < min(a.cpu_seconds, 5.0):
+                    refbind.ssm_forward(x, tail=tail, tail_len=0, state=st, threads=1, **case)
+                    calls += 1
+                per_tok = (time.perf_counter() - t0) / (calls * Ts) * 1e6
+                res["cpu_baseline"] = {"us": round(per_tok * T, 1), "kind": "reference",
+                                       "cores": 1,
+                                       "sample": f"aero_ssm_forward_q on {Ts} tokens ({calls} "
+                                                 f"calls), per token x {T}"}
+                res["speedup_vs_cpu"] = round(per_tok * T / us, 1)
+        print(json.dumps(res), flush=True)
+        plan.destroy()
+        stream.destroy()
     return 0
 
 

@@ -300,7 +300,8 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * act_mul (src/tensor.cpp:104-125); each result equals that composition to
  * 1e-5 of its scale.
  *   aero_hip_norm_matvec: y[m][t*n_rows[m] + r] = sum_c W_m[r, c] * xn[t, c]
- *     for up to 3 matrices of one type and width sharing x (q, k, v);
+ *     for up to 4 matrices of one type and width sharing x (q, k, v; a
+ *     DeltaNet layer's qkv, gate, alpha, beta);
  *   aero_hip_norm_gate_up: out[t*n_ff + r] = act(Wg[r] . xn[t]) * (Wu[r] . xn[t]).
  * xn = x normalised as aero_hip_rmsnorm with weight norm_w (nullable: ones)
  * and flags `norm` (0 or AERO_NORM_UNIT_OFFSET); norm < 0: xn = x. act is an
@@ -317,6 +318,18 @@ int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
                           int64_t w_bytes, const float* x, const float* norm_w, float eps,
                           int norm, int act, float* out, int64_t n_ff, int64_t n_cols,
                           int64_t n_tok, void* stream);
+/* The gated-DeltaNet norm folded into the next projection's GEMV:
+ * y[t*n_rows + r] = sum_c W[r, c] * on[t, c], with
+ * on[t, c] = x[t, c] / sqrt(mean_c x[t]^2 + eps) * norm_w[c % w_len] * silu(z[t, c])
+ * over the whole row, as aero_hip_gated_rmsnorm_silu with group = n_cols. It
+ * replaces the gated norm (src/ssm.cpp:322-340) and the output projection
+ * (:343-348) of aero_ssm_forward_q for up to 2 tokens (decode); w_len a
+ * multiple of 16 that divides n_cols; x, z, norm_w 16-byte aligned; weights as
+ * aero_hip_norm_matvec. Equals that composition to 1e-5 of scale. */
+int aero_hip_gated_norm_matvec(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows,
+                               float* y, const float* x, const float* z, const float* norm_w,
+                               int64_t w_len, float eps, int64_t n_cols, int64_t n_tok,
+                               void* stream);
 
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok);
 int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
@@ -526,6 +539,23 @@ int     aero_hip_ssm_scan(const float* q, const float* k, const float* v, const 
 int     aero_hip_ssm_conv(const float* x, const float* w, const float* tail, int64_t tail_len,
                           float* tail_out, float* out, int64_t T, int64_t channels,
                           int64_t kernel, int64_t* new_tail_len, void* stream);
+/* The scan over q, k, v token rows q_stride, k_stride, v_stride floats apart
+ * (each a multiple of 4, at least the token's heads): slices of one packed
+ * [T][qkv] buffer, as the SSM layer scans them. Replaces scan_strided
+ * (src/ssm.cpp:128-142) as aero_ssm_forward_q calls it (:316-320); same
+ * workspace and alignment as aero_hip_ssm_scan. */
+int     aero_hip_ssm_scan_strided(const float* q, int64_t q_stride, const float* k,
+                                  int64_t k_stride, const float* v, int64_t v_stride,
+                                  const float* alpha, const float* beta, const float* a_log,
+                                  const float* dt_bias, float* state, int64_t T, int64_t n_k,
+                                  int64_t n_v, int64_t d, float scale, float eps, float* outs,
+                                  void* workspace, int64_t ws_bytes, void* stream);
+/* aero_hip_ssm_conv with silu(x) = x / (1 + exp(-x)) applied to every output:
+ * the conv then silu of aero_ssm_forward_q (src/ssm.cpp:298-301) in one pass. */
+int     aero_hip_ssm_conv_silu(const float* x, const float* w, const float* tail,
+                               int64_t tail_len, float* tail_out, float* out, int64_t T,
+                               int64_t channels, int64_t kernel, int64_t* new_tail_len,
+                               void* stream);
 
 /* ---------------------------------------------------------------- GGUF
  * A GGUF file parsed on the host (src/gguf.cpp:150-354, the reference's

@@ -388,6 +388,52 @@ def ssm_scan(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
     return outs, st
 
 
+def ssm_forward(x, dts, weights, a_log, dt_bias, conv1d, norm, n_k: int, d: int, inner: int,
+                eps: float, norm_eps: float, tail, tail_len: int, state):
+    """One gated-DeltaNet layer, aero_ssm_forward_q (src/ssm.cpp:262-352),
+    composed from the oracle's restatements. x [T, n_embd] is the layer's
+    (already normed) input; dts / weights list the (qkv, gate, alpha, beta,
+    out) projections (:224-225), each [n_out, n_in]: dtype 0 a float32 array,
+    else raw GGUF blocks; conv1d [qkv, K] with qkv = 2 n_k d + inner; norm [d]
+    tiled over the n_v = inner / d heads; tail [K-1, qkv] holds tail_len rows
+    of conv history; state [n_v, d, d]. Returns (out [T, n_embd], tail,
+    tail_len, state), the inputs untouched.
+    - :289-296 the qkv projection per token, then (:297) the causal conv over
+      [tail; qkv] and (:298-301) silu = x / (1 + exp(-x)) on every element;
+    - :303-315 alpha, beta (n_v each) and gate (inner) from x;
+    - :316-320 the scan over the q / k / v slices of each qkv row, scale
+      1/sqrt(d), the l2 eps eps;
+    - :322-340 the gated RMSNorm over the whole row (group = inner), norm eps
+      norm_eps, w[c % d];
+    - :343-348 the output projection.
+    float32 projections are evaluated in float64 and rounded (the reference
+    sums them serially in float32: matvec_fp32, :37-44)."""
+    x = f32(x)
+    T, n_embd = x.shape
+    n_v = inner // d
+    qkv_w = 2 * n_k * d + inner
+
+    def proj(i, X, n_out):
+        if dts[i] == F32:
+            W = np.asarray(weights[i], np.float32).reshape(n_out, X.shape[1])
+            return (X.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32)
+        return matmul(dts[i], weights[i], X, n_out)
+
+    qkv = proj(0, x, qkv_w)
+    conv, tail2, tl2 = ssm_conv(qkv, conv1d, tail, tail_len)
+    conv = conv / (np.float32(1.0) + np.exp(-conv))
+    alpha = proj(2, x, n_v)
+    beta = proj(3, x, n_v)
+    gate = proj(1, x, inner)
+    q = conv[:, :n_k * d].reshape(T, n_k, d)
+    k = conv[:, n_k * d:2 * n_k * d].reshape(T, n_k, d)
+    v = conv[:, 2 * n_k * d:].reshape(T, n_v, d)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    outs, st = ssm_scan(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps)
+    o = gated_rmsnorm_silu(outs.reshape(T, inner), gate, norm, norm_eps, group=inner)
+    return proj(4, o, n_embd), tail2, tl2, st
+
+
 def ssm_conv(x, w, tail, tail_len: int):
     """src/ssm.cpp:173-210. x (T, C); w (C, kernel); tail (>= kernel-1, C)
     holding tail_len rows. Returns (out, new tail (kernel-1, C), new length)."""

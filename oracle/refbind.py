@@ -136,6 +136,12 @@ def ssm():
         L.aero_ssm_scan.restype = None
         L.aero_ssm_conv.argtypes = [fp, fp, fp, POINTER(c_int), fp, c_int, c_int, c_int]
         L.aero_ssm_conv.restype = None
+        vp = ctypes.c_void_p
+        L.aero_ssm_forward_q.argtypes = ([fp, POINTER(c_int), POINTER(vp), POINTER(c_int64)]
+                                         + [fp] * 4 + [c_int] * 7 + [c_float, c_float, fp,
+                                                                     POINTER(c_int), fp, fp,
+                                                                     c_int])
+        L.aero_ssm_forward_q.restype = c_int
         _s = L
     return _s
 
@@ -163,6 +169,36 @@ def ssm_scan(q, k, v, alpha, beta, a_log, dt_bias, state, scale, eps=1e-6):
                         _f(f(dt_bias)), _f(st), T, n_k, n_v, d, float(scale), float(eps),
                         _f(outs))
     return outs, st
+
+
+def ssm_forward(x, dts, weights, a_log, dt_bias, conv1d, norm, n_k: int, d: int, inner: int,
+                eps: float, norm_eps: float, tail, tail_len: int, state, threads: int = 1):
+    """aero_ssm_forward_q (src/ssm.cpp:262-352) on the same arguments as the
+    oracle's cpuref.ssm_forward. Returns (out, tail, tail_len, state)."""
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    x = f(x)
+    T, n_embd = x.shape
+    n_v = inner // d
+    qkv_w = 2 * n_k * d + inner
+    K = conv1d.shape[1]
+    keep = [f(w) if dt == 0 else np.ascontiguousarray(w, np.uint8).reshape(-1)
+            for dt, w in zip(dts, weights)]
+    wp = (ctypes.c_void_p * 5)(*[w.ctypes.data for w in keep])
+    wl = (c_int64 * 5)(*[0 if dt == 0 else w.size for dt, w in zip(dts, keep)])
+    dt = (c_int * 5)(*[int(t) for t in dts])
+    tb = np.zeros((max(K - 1, 1), qkv_w), np.float32)
+    if tail_len > 0:
+        tb[:tail_len] = f(tail)[:tail_len]
+    tl = c_int(int(tail_len))
+    st = np.array(f(state), copy=True)
+    out = np.zeros((T, n_embd), np.float32)
+    rc = ssm().aero_ssm_forward_q(_f(x), dt, wp, wl, _f(f(a_log)), _f(f(dt_bias)), _f(f(conv1d)),
+                                  _f(f(norm)), T, n_embd, inner, d, n_k, K, n_v, float(eps),
+                                  float(norm_eps), _f(tb), ctypes.byref(tl), _f(st), _f(out),
+                                  int(threads))
+    if rc != 0:
+        raise ValueError(f"aero_ssm_forward_q refused ({rc})")
+    return out, tb[:max(K - 1, 0)], int(tl.value), st
 
 
 def ssm_conv(x, w, tail, tail_len: int):

@@ -1,5 +1,5 @@
 """GPU parity: the fused decode GEMVs (aero_hip_norm_matvec: RMSNorm + up to
-three projections sharing x; aero_hip_norm_gate_up: RMSNorm + gate/up
+four projections sharing x; aero_hip_norm_gate_up: RMSNorm + gate/up
 projections + act·mul) against the oracle's composition of the reference's
 separate passes: rmsnorm_rows (src/transformer.cpp:98-104), matvec / matmul
 (src/kernels.cpp:497-538) and act_mul (src/tensor.cpp:104-125).
@@ -50,6 +50,59 @@ def test_norm_matvec_qkv_vs_oracle(hip, oracle, t, n_tok):
     xn = oracle.rmsnorm_rows(x, nw, 1e-5)
     for w, nr, y in zip(ws, rows, ys):
         assert rel_to_scale(y.numpy(), want_proj(oracle, t, w, xn, nr)) <= RTOL
+
+
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q8_0, W.Q6_K])
+@pytest.mark.parametrize("n_tok,norm", [(1, False), (2, True), (4, False)])
+def test_norm_matvec_four_matrices(hip, oracle, t, n_tok, norm):
+    """Four matrices in one launch, as a DeltaNet layer's projections of x
+    (qkv 1536, gate 512, alpha and beta 8 rows: the small ones one workgroup
+    each) of 2048 columns; without the norm (the layer's x is already
+    normed) and with it."""
+    rng = np.random.default_rng(7 * t + n_tok)
+    n_cols, rows = 2048, [1536, 512, 8, 8]
+    ws = [table(t, nr, n_cols, rng) for nr in rows]
+    x = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(n_cols)).astype(np.float32)
+    ys = [DA.empty((n_tok, nr)) for nr in rows]
+    print(f"norm_matvec 4 matrices type={t} tokens={n_tok} norm={norm}", flush=True)
+    ops.norm_matvec(t, [DA.from_numpy(w) for w in ws], DA.from_numpy(x), ys, rows, n_cols,
+                    n_tok, norm_w=DA.from_numpy(nw) if norm else None, eps=1e-5, norm=norm)
+    xn = oracle.rmsnorm_rows(x, nw, 1e-5) if norm else x
+    for w, nr, y in zip(ws, rows, ys):
+        assert rel_to_scale(y.numpy(), want_proj(oracle, t, w, xn, nr)) <= RTOL
+
+
+@pytest.mark.parametrize("t,n_cols,w_len", [(W.Q4_K, 4096, 128), (W.Q8_0, 1024, 64),
+                                             (W.Q6_K, 2048, 256), (W.IQ4_XS, 512, 128)])
+@pytest.mark.parametrize("n_tok", [1, 2])
+def test_gated_norm_matvec_vs_oracle(hip, oracle, t, n_cols, w_len, n_tok):
+    """The gated-DeltaNet norm (whole-row RMS, tiled weight, silu gate) in the
+    GEMV prologue against the oracle's gated_rmsnorm_silu then matmul; one
+    step of columns (512, 1024) and several (2048, 4096)."""
+    rng = np.random.default_rng(n_cols + w_len + n_tok)
+    n_rows = 384
+    w = table(t, n_rows, n_cols, rng)
+    x = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    z = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(w_len)).astype(np.float32)
+    y = DA.empty((n_tok, n_rows))
+    print(f"gated_norm_matvec type={t} cols={n_cols} w_len={w_len} tokens={n_tok}", flush=True)
+    ops.gated_norm_matvec(t, DA.from_numpy(w), DA.from_numpy(x), DA.from_numpy(z),
+                          DA.from_numpy(nw), y, n_rows, n_cols, n_tok, 1e-6)
+    on = oracle.gated_rmsnorm_silu(x, z, nw, 1e-6)
+    assert rel_to_scale(y.numpy(), want_proj(oracle, t, w, on, n_rows)) <= RTOL
+
+
+def test_gated_norm_matvec_refusals(hip):
+    rng = np.random.default_rng(5)
+    w = DA.from_numpy(table(W.Q4_K, 64, 1024, rng))
+    x = DA.from_numpy(rng.standard_normal((3, 1024)).astype(np.float32))
+    y = DA.empty((3, 64))
+    for n_tok, wl in ((3, 128), (1, 24), (1, 384)):   # 3 tokens; 24 not 16k; 384 not dividing
+        nw = DA.from_numpy(np.ones(wl, np.float32))
+        with pytest.raises(_lib.AeroHipError, match="gated norm"):
+            ops.gated_norm_matvec(W.Q4_K, w, x, x, nw, y, 64, 1024, n_tok, 1e-6)
 
 
 def test_norm_matvec_llama_decode_and_variants(hip, oracle):
@@ -141,16 +194,24 @@ def test_norm_gate_up_llama_decode(hip, oracle):
 
 
 def test_fused_refusals(hip):
-    """Four matrices, a type without a GEMV, misaligned weights, rows not a
+    """Five matrices, a type without a GEMV, misaligned weights, rows not a
     multiple of 16 bytes (Q6_K at 1024 columns: 840 bytes; Q8_0 rows of 952
     bytes in an odd number) and gate/up of different sizes are refused with
     an error, nothing launched."""
     rng = np.random.default_rng(51)
     w = DA.from_numpy(table(W.Q4_K, 64, 1024, rng))
     x = DA.from_numpy(rng.standard_normal((1, 1024)).astype(np.float32))
-    ys = [DA.empty((1, 64)) for _ in range(4)]
+    ys = [DA.empty((1, 64)) for _ in range(5)]
     with pytest.raises(ValueError):
-        ops.norm_matvec(W.Q4_K, [w] * 4, x, ys, [64] * 4, 1024)
+        ops.norm_matvec(W.Q4_K, [w] * 5, x, ys, [64] * 5, 1024)
+    L = _lib.lib()
+    p5 = (ctypes.c_void_p * 5)(*[w.ptr] * 5)
+    b5 = (ctypes.c_int64 * 5)(*[w.nbytes] * 5)
+    r5 = (ctypes.c_int64 * 5)(*[64] * 5)
+    y5 = (ctypes.c_void_p * 5)(*[y.ptr for y in ys])
+    assert L.aero_hip_norm_matvec(W.Q4_K, 5, p5, b5, r5, y5, x.ptr, None, 1e-5, 0, 1024, 1,
+                                  None) == 0
+    assert "n_mat=5" in _lib.last_error()
     with pytest.raises(_lib.AeroHipError):
         ops.norm_matvec(W.F32, [w], x, ys[:1], [64], 1024)
     w6 = DA.from_numpy(table(W.Q6_K, 64, 1024, rng))

@@ -1,0 +1,121 @@
+"""GPU parity: the device-resident gated-DeltaNet layer (aero_amd.ssm_layer,
+aero_ssm_forward_q of src/ssm.cpp:262-352) against the oracle's composition
+of the same layer (oracle.cpuref.ssm_forward, itself checked against the
+compiled reference in test_oracle.py).
+
+Calls run in sequence on one SsmStep, carrying the recurrent state and the
+conv history: a prompt (the chunked scan from 128 tokens), then decode calls.
+Every call's output and the state after it: <= 1e-5 of scale (the GPU sums
+its dots in another order, and the chunked scan re-associates the delta rule).
+"""
+import numpy as np
+import pytest
+
+from conftest import RTOL, rel_to_scale
+from aero_amd import ssm_layer as S
+from aero_amd import workloads as W
+from aero_amd.device import Plan, Stream
+
+pytestmark = pytest.mark.gpu
+
+
+def run_chain(oracle, cfg, seed, calls):
+    wts = S.SsmWeights(cfg, seed=seed)
+    step = S.SsmStep(cfg, wts, max_tokens=max(calls))
+    h = wts.host
+    case = dict(dts=list(cfg.wtypes), weights=[h[n] for n in S.PROJ], a_log=h["a_log"],
+                dt_bias=h["dt_bias"], conv1d=h["conv1d"], norm=h["norm"], n_k=cfg.n_k,
+                d=cfg.head_dim, inner=cfg.inner, eps=cfg.eps, norm_eps=cfg.norm_eps)
+    K = cfg.conv_kernel
+    tail, tl = np.zeros((K - 1, cfg.qkv), np.float32), 0
+    st = np.zeros((cfg.n_v, cfg.head_dim, cfg.head_dim), np.float32)
+    rng = np.random.default_rng(seed + 1)
+    for i, T in enumerate(calls):
+        x = rng.standard_normal((T, cfg.hidden)).astype(np.float32)
+        print(f"  call {i}: {T} tokens", flush=True)
+        step.x.view((T, cfg.hidden)).copy_from(x)
+        step.forward(T)
+        want, tail, tl, st = oracle.ssm_forward(x, tail=tail, tail_len=tl, state=st, **case)
+        got = step.out.view((T, cfg.hidden)).numpy()
+        e_out, e_st = rel_to_scale(got, want), rel_to_scale(step.state.numpy(), st)
+        print(f"    out {e_out:.2e} state {e_st:.2e}", flush=True)
+        assert e_out <= RTOL and e_st <= RTOL, (i, T, e_out, e_st)
+        assert step.tail_len == tl
+
+
+@pytest.mark.parametrize("name,cfg,calls", [
+    # Qwen3-Next's heads (16 key, 32 value, d 128) at a narrower hidden size
+    ("qwen3next_heads_q4k", S.SsmConfig(512, 16, 32, 128, 4, (W.Q4_K,) * 5), (200, 1, 1, 3)),
+    # mixed types: Q4_K projections with Q8_0 gate inputs (two launches for x)
+    ("mixed_q4k_q8_0", S.SsmConfig(1024, 4, 8, 128, 4, (W.Q4_K, W.Q4_K, W.Q8_0, W.Q8_0, W.Q4_K)),
+     (130, 2, 1)),
+    ("d64_q8_0", S.SsmConfig(256, 2, 4, 64, 4, (W.Q8_0,) * 5), (1, 140, 1, 17)),
+    ("d256_q6k", S.SsmConfig(256, 1, 2, 256, 4, (W.Q6_K, W.Q6_K, W.Q8_0, W.Q8_0, W.Q6_K)),
+     (129, 1)),
+    ("kernel3_short", S.SsmConfig(256, 2, 2, 128, 3, (W.Q8_0,) * 5), (1, 1, 5, 40)),
+])
+def test_ssm_layer_vs_oracle(hip, oracle, name, cfg, calls):
+    print(f"ssm layer {name}", flush=True)
+    run_chain(oracle, cfg, 5 + len(name), calls)
+
+
+def test_ssm_layer_plan_replay(hip, oracle):
+    """The decode call recorded once as a plan and replayed three times, each
+    replay a new token against the state the previous one left; every replay
+    equals the oracle's chain."""
+    cfg = S.SsmConfig(512, 4, 8, 128, 4, (W.Q4_K,) * 5)
+    wts = S.SsmWeights(cfg, seed=3)
+    step = S.SsmStep(cfg, wts, max_tokens=64)
+    h = wts.host
+    case = dict(dts=list(cfg.wtypes), weights=[h[n] for n in S.PROJ], a_log=h["a_log"],
+                dt_bias=h["dt_bias"], conv1d=h["conv1d"], norm=h["norm"], n_k=cfg.n_k,
+                d=cfg.head_dim, inner=cfg.inner, eps=cfg.eps, norm_eps=cfg.norm_eps)
+    rng = np.random.default_rng(9)
+    tail, tl = np.zeros((3, cfg.qkv), np.float32), 0
+    st = np.zeros((cfg.n_v, cfg.head_dim, cfg.head_dim), np.float32)
+    x = rng.standard_normal((40, cfg.hidden)).astype(np.float32)
+    step.x.view((40, cfg.hidden)).copy_from(x)
+    step.forward(40)       # a prompt: the history is kernel - 1 rows from here on
+    _, tail, tl, st = oracle.ssm_forward(x, tail=tail, tail_len=tl, state=st, **case)
+    stream = Stream()
+    plan = Plan()
+    with plan:
+        step.forward(1, stream=stream)
+    for i in range(3):
+        x = rng.standard_normal((1, cfg.hidden)).astype(np.float32)
+        step.x.view((1, cfg.hidden)).copy_from(x)
+        plan.launch(stream)
+        stream.synchronize()
+        want, tail, tl, st = oracle.ssm_forward(x, tail=tail, tail_len=tl, state=st, **case)
+        e = rel_to_scale(step.out.view((1, cfg.hidden)).numpy(), want)
+        print(f"  replay {i}: out {e:.2e}", flush=True)
+        assert e <= RTOL
+        assert rel_to_scale(step.state.numpy(), st) <= RTOL
+    plan.destroy()
+    stream.destroy()
+
+
+def test_ssm_layer_decode_launches(hip):
+    """Decode is four launches (projections of x, the conv writing its own
+    history, scan, gated norm in the output projection's GEMV), five with the
+    norm_gemm fusion off (the gated norm its own launch)."""
+    cfg = S.SsmConfig(512, 4, 8, 128, 4, (W.Q4_K,) * 5)
+    wts = S.SsmWeights(cfg, seed=1)
+    for fuse, want in ((True, 4), (False, 5)):
+        step = S.SsmStep(cfg, wts, max_tokens=8, fusions={"norm_gemm": fuse})
+        step.forward(4)
+        plan = Plan()
+        with plan:
+            step.forward(1)
+        assert len(plan) == want, (fuse, len(plan))
+        plan.destroy()
+
+
+def test_ssm_layer_refusals(hip):
+    with pytest.raises(ValueError, match="head dim"):
+        S.SsmStep(S.SsmConfig(256, 1, 1, 32, 4, (W.Q8_0,) * 5),
+                  S.SsmWeights(S.SsmConfig(256, 1, 1, 32, 4, (W.Q8_0,) * 5)), 8)
+    cfg = S.SsmConfig(256, 2, 2, 64, 4, (W.Q8_0,) * 5)
+    step = S.SsmStep(cfg, S.SsmWeights(cfg), max_tokens=8)
+    with pytest.raises(ValueError, match="tokens"):
+        step.forward(9)

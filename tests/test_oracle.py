@@ -714,3 +714,48 @@ def test_golden_ssm():
     o1, t1, l1 = O.ssm_conv(g["conv_x"][:2], g["conv_w"], None, 0)
     o2, t2, _ = O.ssm_conv(g["conv_x"][2:], g["conv_w"], t1, l1)
     assert bits_equal(np.concatenate([o1, o2]), g["conv_out"]) and bits_equal(t2, g["conv_tail"])
+
+
+def _ssm_layer_case(rng, dts, n_embd, n_k, n_v, d, K):
+    from aero_amd import workloads as W
+    inner, qkv = n_v * d, 2 * n_k * d + n_v * d
+    shapes = [(qkv, n_embd), (inner, n_embd), (n_v, n_embd), (n_v, n_embd), (n_embd, inner)]
+    ws = [(rng.standard_normal((r, c)) / np.sqrt(c)).astype(np.float32) if t == 0
+          else W.weight_table(t, r, c, rng) for t, (r, c) in zip(dts, shapes)]
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    return dict(dts=list(dts), weights=ws, a_log=(-np.abs(f(n_v)) * 0.5).astype(np.float32),
+                dt_bias=f(n_v), conv1d=(f(qkv, K) * 0.5).astype(np.float32),
+                norm=(1 + f(d) * 0.1).astype(np.float32), n_k=n_k, d=d, inner=inner,
+                eps=1e-6, norm_eps=1e-6)
+
+
+@pytest.mark.parametrize("dts,n_embd,n_k,n_v,d,K", [
+    ((0, 0, 0, 0, 0), 48, 2, 4, 16, 4),            # every projection fp32 (aero_ssm_forward)
+    ((8, 8, 8, 8, 8), 64, 1, 2, 32, 4),            # Q8_0
+    ((12, 12, 8, 8, 12), 256, 2, 4, 64, 3),        # Q4_K with Q8_0 gates, kernel 3
+    ((14, 0, 0, 0, 14), 256, 1, 2, 128, 4),        # Q6_K with fp32 gate / alpha / beta
+])
+def test_ssm_forward_matches_compiled_reference(dts, n_embd, n_k, n_v, d, K):
+    """The oracle's composition of one gated-DeltaNet layer (cpuref.ssm_forward)
+    against aero_ssm_forward_q compiled from src/ssm.cpp: two calls of 5 and
+    3 tokens carrying the conv history and the state, <= 1e-5 of scale (the
+    reference sums its fp32 projections and the gated norm in float32, its
+    quantised dots with -ffast-math)."""
+    if R.ssm() is None:
+        pytest.skip("oracle/_ref not built")
+    rng = np.random.default_rng(n_embd + d + K)
+    case = _ssm_layer_case(rng, dts, n_embd, n_k, n_v, d, K)
+    qkv = 2 * n_k * d + n_v * d
+    tail, tl = np.zeros((K - 1, qkv), np.float32), 0
+    rtail, rtl = tail, 0
+    st = (rng.standard_normal((n_v, d, d)) * 0.1).astype(np.float32)
+    rst = st
+    for T in (5, 3):
+        x = rng.standard_normal((T, n_embd)).astype(np.float32)
+        out, tail, tl, st = O.ssm_forward(x, tail=tail, tail_len=tl, state=st, **case)
+        rout, rtail, rtl, rst = R.ssm_forward(x, tail=rtail, tail_len=rtl, state=rst, **case)
+        assert tl == rtl == min(K - 1, 8 if T == 3 else 5)
+        assert rel_to_scale(out, rout) <= 1e-5, (T, rel_to_scale(out, rout))
+        assert rel_to_scale(st, rst) <= 1e-5
+        # the history holds raw projections: equal to their summation order
+        assert rel_to_scale(tail[:tl], rtail[:rtl]) <= 1e-5
