@@ -138,15 +138,18 @@ def conv(x, w, tail, tail_len):
     return out, carried, int(n_tail.value)
 
 
-def _outside(name: str):
+def _outside(name: str, why: str = "use the caller's own implementation"):
     def f(*args, **kwargs):
-        raise SsmUnavailable(f"native_ssm.{name} is outside the GPU path; use the "
-                             "caller's own implementation")
+        raise SsmUnavailable(f"native_ssm.{name} is outside the GPU path; {why}")
     f.__name__ = name
     return f
 
 
-forward = _outside("forward")
+# the SSM layer runs device-resident (aero_amd.ssm_layer.SsmStep: weights, state
+# and conv history kept in HBM); a host-pointer entry would upload every
+# weight on each call, slower than the caller's own CPU path
+forward = _outside("forward", "run the layer device-resident with aero_amd.ssm_layer.SsmStep "
+                              "(weights, state and conv history in HBM)")
 route = _outside("route")
 expert_accum = _outside("expert_accum")
 ffn_block = _outside("ffn_block")

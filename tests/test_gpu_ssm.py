@@ -231,3 +231,64 @@ def test_workspace_grows_and_is_reused(hip, oracle):
         want, wst = oracle.ssm_scan(*args, scale)
         assert rel_to_scale(out, want) <= RTOL and rel_to_scale(dst.numpy(), wst) <= RTOL
     assert ops._ssm_ws.buf.nbytes >= _lib.lib().aero_hip_ssm_workspace(300, 2, 4, 128)
+
+
+@pytest.mark.parametrize("T", [5, 40, 200])
+def test_scan_strided_equals_contiguous(hip, T):
+    """q, k, v as slices of packed rows (with 8 floats of padding a row) give
+    the contiguous scan's outputs and state bit for bit, on the fused (5
+    tokens), per-token (40) and chunked (200) paths."""
+    rng = np.random.default_rng(T)
+    n_k, n_v, d = 2, 4, 128
+    q, k, v, al, bt, a_log, dt, st = inputs(rng, T, n_k, n_v, d)
+    W_ = 2 * n_k * d + n_v * d + 8
+    packed = np.zeros((T, W_), np.float32)
+    packed[:, :n_k * d] = q.reshape(T, -1)
+    packed[:, n_k * d:2 * n_k * d] = k.reshape(T, -1)
+    packed[:, 2 * n_k * d:2 * n_k * d + n_v * d] = v.reshape(T, -1)
+    print(f"strided scan T={T}", flush=True)
+    want, wst = gpu_scan(q, k, v, al, bt, a_log, dt, st, d ** -0.5)
+    dp, sdev, outs = DA.from_numpy(packed), DA.from_numpy(st), DA.empty((T, n_v, d))
+    ops.ssm_scan(dp, dp, dp, DA.from_numpy(al), DA.from_numpy(bt), DA.from_numpy(a_log),
+                 DA.from_numpy(dt), sdev, outs, T, n_k, n_v, d, d ** -0.5,
+                 strides=(W_, W_, W_), q_off=0, k_off=n_k * d, v_off=2 * n_k * d)
+    assert bits_equal(outs.numpy(), want) and bits_equal(sdev.numpy(), wst.numpy())
+
+
+def test_scan_strided_refusals(hip):
+    rng = np.random.default_rng(3)
+    T, n_k, n_v, d = 4, 1, 2, 64
+    q, k, v, al, bt, a_log, dt, st = inputs(rng, T, n_k, n_v, d)
+    L = _lib.lib()
+    dq, dv, da = DA.from_numpy(q), DA.from_numpy(v), DA.from_numpy(al)
+    ds, do = DA.from_numpy(st), DA.empty((T, n_v, d))
+    ws = DA.empty((L.aero_hip_ssm_workspace(T, n_k, n_v, d) // 4 + 64,))
+    for qs, vs in ((n_k * d - 4, n_v * d), (n_k * d + 2, n_v * d), (n_k * d, n_v * d - 64)):
+        assert L.aero_hip_ssm_scan_strided(dq.ptr, qs, dq.ptr, qs, dv.ptr, vs, da.ptr, da.ptr,
+                                           da.ptr, da.ptr, ds.ptr, T, n_k, n_v, d, 0.1, 1e-6,
+                                           do.ptr, ws.ptr, ws.nbytes, None) == 0
+        assert "strides" in _lib.last_error()
+
+
+@pytest.mark.parametrize("T,C,K,chunks", [(40, 1000, 4, [1, 2, 37]), (300, 1024, 4, [3, 297]),
+                                          (9, 64, 6, [4, 5])])
+def test_conv_silu(hip, oracle, T, C, K, chunks):
+    """The conv with silu in its store equals the oracle's conv then
+    x / (1 + exp(-x)) (1e-6 of scale: the GPU's exp), and its history
+    (written by the one-block kernel below 33 tokens) is the plain conv's, bit
+    for bit, over chunks carrying it."""
+    rng = np.random.default_rng(T + C)
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    w = rng.standard_normal((C, K)).astype(np.float32)
+    tail = DA.empty((K - 1, C))
+    tl, otail, otl, a = 0, np.zeros((K - 1, C), np.float32), 0, 0
+    for n in chunks:
+        print(f"conv silu chunk {a}:{a + n} of C={C} K={K}", flush=True)
+        out = DA.empty((n, C))
+        tl = ops.ssm_conv(DA.from_numpy(x[a:a + n]), DA.from_numpy(w), tail, tl, tail, out, n, C,
+                          K, silu=True)
+        want, otail, otl = oracle.ssm_conv(x[a:a + n], w, otail, otl)
+        want = want / (np.float32(1) + np.exp(-want))
+        assert rel_to_scale(out.numpy(), want) <= 1e-6
+        assert tl == otl and bits_equal(tail.numpy()[:tl], otail[:otl])
+        a += n
