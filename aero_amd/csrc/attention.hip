@@ -347,6 +347,58 @@ struct KvTile {
     }
 };
 
+// The four waves' (m, l, acc) of one 16-query tile merged through LDS, then
+// the output (one chunk) or the chunk's partials written: query vector qi of
+// the tile, element d a thread.
+template <typename Tile, int DV, bool MERGE_OUT>
+__device__ __forceinline__ void merge_tile(const AttnParams& p, float m, float ls,
+                                           const v4f (&acc)[DV / 16], int64_t tile,
+                                           int64_t n_vec, int chunk, int kh, int wave, int g,
+                                           int c) {
+    constexpr int VS = DV / 16;
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    __shared__ float sm[4][16], sl[4][16];
+    __shared__ float sacc[4][16][DV + 4];
+    if (g == 0) {
+        sm[wave][c] = m;
+        sl[wave][c] = ls;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < VS; ++t) sacc[wave][4 * g + r][Tile::vdim(c, t)] = acc[t][r];
+    __syncthreads();
+    const int64_t rows = p.n_q * p.n_head;
+    for (int w = threadIdx.x; w < 16 * DV; w += 256) {
+        const int qi = w / DV, d = w % DV;
+        const int64_t uq = tile * 16 + qi;
+        if (uq >= n_vec) break;  // w only grows
+        float mt = -INFINITY;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) mt = fmaxf(mt, sm[x][qi]);
+        float lt = 0.0f, at = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const float wg = (sm[x][qi] == -INFINITY) ? 0.0f : expf(sm[x][qi] - mt);
+            lt = __builtin_fmaf(sl[x][qi], wg, lt);
+            at = __builtin_fmaf(sacc[x][qi][d], wg, at);
+        }
+        const int64_t row = (uq / p.rep) * p.n_head + (int64_t)kh * p.rep + uq % p.rep;
+        if constexpr (MERGE_OUT) {
+            p.out[row * DV + d] = at / fmaxf(lt, 1e-30f);
+        } else {
+            const int64_t pi = (int64_t)chunk * rows + row;
+            p.part[pi * DV + d] = at;
+            if (d == 0) {
+                float* ml = p.part + (int64_t)p.n_chunks * rows * DV + 2 * pi;
+                ml[0] = mt;
+                ml[1] = lt;
+            }
+        }
+    }
+}
+
 template <int DT, int D, int DV, bool MERGE_OUT>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams p) {
     using Tile = KvTile<DT, D, DV>;
@@ -472,49 +524,255 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams p) {
         else
             tl.load(p, c0 + 16 * i, c1, g, c, kh);
     }
-    ls += __shfl_xor(ls, 16);
-    ls += __shfl_xor(ls, 32);
+    merge_tile<Tile, DV, MERGE_OUT>(p, m, ls, acc, tile, n_vec, chunk, kh, wave, g, c);
+}
 
-    // merge the four waves: query vector qi of the tile, element d
-    __shared__ float sm[4][16], sl[4][16];
-    __shared__ float sacc[4][16][DV + 4];
-    if (g == 0) {
-        sm[wave][c] = m;
-        sl[wave][c] = ls;
+// ---------------------------------------------------- integer caches, fp16
+// Integer caches on the fp16 matrix cores (v_mfma_f32_16x16x32_f16: lane
+// (r, g) supplies A[r][8g..8g+7] and B[8g..8g+7][r], receives D[4g+v][r]).
+// The codes are exact in fp16: a code c becomes the fp16 bits 0x6400 | u of
+// 1024 + u, u = c + 128 (int8) or c + 8 (int4), minus 1152 or 1032. q, scaled
+// by 2^(14-e) per query (|q| < 2^15), and each tile's probabilities times the
+// value scales, scaled by 2^(14-e) of the tile's largest value scale, are
+// split into two fp16 parts (hi = fp16(v), lo = fp16(v - hi)): every product
+// is exact and the fp32 sums carry about 22 bits of each operand. A wave
+// takes 32 keys a step, two halves of 16 loaded as attn_mfma_kernel's tiles:
+//  * scores: D[key][query] over K = 32 dimensions a matrix step; lane group
+//    g's 8 values of a step are elements 8s..8s+7 of its key slice (the
+//    order of int4 nibbles within a dword: 0, 4, 2, 6, 1, 5, 3, 7);
+//  * value sum: D[query][value dim] over the 32 keys in one matrix step a
+//    value tile, lane group g's k-slots being keys 4g..4g+3 of each half:
+//    the probabilities the lane holds after the scores, and the codes of
+//    those keys' value rows it loaded.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2 u32_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t h2_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// the 8 codes of key-slice step s as fp16, in the order described above
+template <int DT>
+__device__ __forceinline__ h8 key_codes(const uint32_t* k, int s) {
+    constexpr uint32_t E = 0x64646464u;
+    if constexpr (DT == 1) {
+        const h2 off = h2{(_Float16)-1152.f, (_Float16)-1152.f};
+        const uint32_t u0 = k[2 * s] ^ 0x80808080u, u1 = k[2 * s + 1] ^ 0x80808080u;
+        const h2 a0 = u32_h2(__builtin_amdgcn_perm(E, u0, 0x04010400u)) + off;
+        const h2 a1 = u32_h2(__builtin_amdgcn_perm(E, u0, 0x04030402u)) + off;
+        const h2 a2 = u32_h2(__builtin_amdgcn_perm(E, u1, 0x04010400u)) + off;
+        const h2 a3 = u32_h2(__builtin_amdgcn_perm(E, u1, 0x04030402u)) + off;
+        return __builtin_bit_cast(h8, make_uint4(h2_u32(a0), h2_u32(a1), h2_u32(a2), h2_u32(a3)));
+    } else {
+        const h2 off = h2{(_Float16)-1032.f, (_Float16)-1032.f};
+        const uint32_t u = k[s] ^ 0x88888888u;
+        const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+        const h2 a0 = u32_h2(__builtin_amdgcn_perm(E, lo, 0x04020400u)) + off;  // 0, 4
+        const h2 a1 = u32_h2(__builtin_amdgcn_perm(E, lo, 0x04030401u)) + off;  // 2, 6
+        const h2 a2 = u32_h2(__builtin_amdgcn_perm(E, hi, 0x04020400u)) + off;  // 1, 5
+        const h2 a3 = u32_h2(__builtin_amdgcn_perm(E, hi, 0x04030401u)) + off;  // 3, 7
+        return __builtin_bit_cast(h8, make_uint4(h2_u32(a0), h2_u32(a1), h2_u32(a2), h2_u32(a3)));
     }
+}
+
+// element i of a key-slice operand is slice element 8s + key_order(i)
+template <int DT>
+__device__ __forceinline__ constexpr int key_order(int i) {
+    return DT == 1 ? i : ((i & 1) ? 4 : 0) + ((i >> 1) & 1) * 2 + (i >> 2);
+}
+
+// codes of element t of two value rows (words a, b of those rows) as fp16
+// (code_a, code_b)
+template <int DT>
+__device__ __forceinline__ uint32_t value_pair(const uint32_t* a, const uint32_t* b, int t) {
+    if constexpr (DT == 1) {
+        const uint32_t byte = (uint32_t)(t & 3);
+        const uint32_t sel = 0x0C000C00u | ((4u + byte) << 16) | byte;
+        const uint32_t x = __builtin_amdgcn_perm(b[t >> 2], a[t >> 2], sel) ^ 0x64806480u;
+        return h2_u32(u32_h2(x) + h2{(_Float16)-1152.f, (_Float16)-1152.f});
+    } else {
+        const uint32_t byte = (uint32_t)((t >> 1) & 3);
+        const uint32_t sel = 0x0C000C00u | ((4u + byte) << 16) | byte;
+        uint32_t x = __builtin_amdgcn_perm(b[t >> 3], a[t >> 3], sel);
+        x = ((t & 1) ? (x >> 4) : x) & 0x000F000Fu;
+        return h2_u32(u32_h2(x ^ 0x64086408u) + h2{(_Float16)-1032.f, (_Float16)-1032.f});
+    }
+}
+
+// v = 2^scale-shifted value split into fp16 hi and lo
+__device__ __forceinline__ void split2(float v, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
+}
+
+template <int DT, int D, bool MERGE_OUT>
+__global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
+    static_assert(DT == 1 || DT == 2, "integer caches");
+    using Tile = KvTile<DT, D, D>;
+    constexpr int KS = Tile::KS, VS = Tile::VS, NS = KS / 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int chunk = blockIdx.x, kh = blockIdx.y;
+    const int64_t n_vec = p.n_q * p.rep;
+    const int64_t tile = (int64_t)(gridDim.z - 1 - blockIdx.z);
+    constexpr int64_t istep = 4;
+
+    // this chunk's keys in 32-key steps; the wave's first step is issued
+    // before the query positions, which may narrow the range, arrive
+    const int64_t c0 = (int64_t)chunk * p.chunk_len;
+    const int64_t c1 = min(c0 + p.chunk_len, p.n_kv);
+    const int64_t tiles_c = (c1 - c0 + 31) / 32;
+    const int64_t i_spec = wave;
+    Tile ta, tb, na, nb;
+    {
+        const int64_t kb = c0 + 32 * min(i_spec, tiles_c - 1);
+        ta.load(p, kb, c1, g, c, kh);
+        tb.load(p, kb + 16, c1, g, c, kh);
+    }
+
+    // query vector of column c, scaled by 2^(14 - e) and split
+    const int64_t u = tile * 16 + c;
+    const bool qok = u < n_vec;
+    const int64_t uc = qok ? u : n_vec - 1;
+    const int64_t tq = uc / p.rep;
+    const int64_t qrow = tq * p.n_head + (int64_t)kh * p.rep + uc % p.rep;
+    const int64_t qp = position_or(p.qpos, tq, tq);
+    float qs[KS];
+    float qmax = 0.0f;
+    {
+        const float* src = p.q + qrow * D;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int t = 0; t < VS; ++t) sacc[wave][4 * g + r][Tile::vdim(c, t)] = acc[t][r];
-    __syncthreads();
-    const int64_t rows = p.n_q * p.n_head;
-    for (int w = threadIdx.x; w < 16 * DV; w += 256) {
-        const int qi = w / DV, d = w % DV;
-        const int64_t uq = tile * 16 + qi;
-        if (uq >= n_vec) break;  // w only grows
-        float mt = -INFINITY;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) mt = fmaxf(mt, sm[x][qi]);
-        float lt = 0.0f, at = 0.0f;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            const float wg = (sm[x][qi] == -INFINITY) ? 0.0f : expf(sm[x][qi] - mt);
-            lt = __builtin_fmaf(sl[x][qi], wg, lt);
-            at = __builtin_fmaf(sacc[x][qi][d], wg, at);
+        for (int e = 0; e < KS; e += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(src + Tile::kdim(g, e));
+            qs[e] = qok ? f.x : 0.0f;
+            qs[e + 1] = qok ? f.y : 0.0f;
+            qs[e + 2] = qok ? f.z : 0.0f;
+            qs[e + 3] = qok ? f.w : 0.0f;
         }
-        const int64_t row = (uq / p.rep) * p.n_head + (int64_t)kh * p.rep + uq % p.rep;
-        if constexpr (MERGE_OUT) {
-            p.out[row * DV + d] = at / fmaxf(lt, 1e-30f);
-        } else {
-            const int64_t pi = (int64_t)chunk * rows + row;
-            p.part[pi * DV + d] = at;
-            if (d == 0) {
-                float* ml = p.part + (int64_t)p.n_chunks * rows * DV + 2 * pi;
-                ml[0] = mt;
-                ml[1] = lt;
+#pragma unroll
+        for (int e = 0; e < KS; ++e) qmax = fmaxf(qmax, fabsf(qs[e]));
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    int eq = 0;
+    if (qmax > 0.0f && qmax <= 3.4028235e38f) frexpf(qmax, &eq);
+    const float qsc = ldexpf(1.0f, 14 - eq), qinv = ldexpf(1.0f, eq - 14);
+    h8 qhi[NS], qlo[NS];
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 hi, lo;
+            split2(qs[8 * st + key_order<DT>(i)] * qsc, hi, lo);
+            qhi[st][i] = hi;
+            qlo[st][i] = lo;
+        }
+    int64_t qmin = qp, qmx = qp;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+        qmin = min(qmin, (int64_t)__shfl_xor(qmin, off, 16));
+        qmx = max(qmx, (int64_t)__shfl_xor(qmx, off, 16));
+    }
+
+    // 32-key steps [i_lo, i_hi) of the chunk can hold kept keys (as
+    // attn_mfma_kernel's 16-key tiles)
+    int64_t i_lo = 0, i_hi = tile * 16 < n_vec ? tiles_c : 0;
+    if (p.kpos == nullptr) {
+        i_hi = min(i_hi, max<int64_t>(0, (qmx + 1 - c0 + 31) / 32));
+        if (p.window > 0) i_lo = max<int64_t>(0, (qmin - p.window + 1 - c0) / 32);
+    }
+    int64_t i = i_lo + (((wave - i_lo) % 4) + 4) % 4;
+    if (i != i_spec && i < i_hi) {
+        ta.load(p, c0 + 32 * i, c1, g, c, kh);
+        tb.load(p, c0 + 32 * i + 16, c1, g, c, kh);
+    }
+
+    float m = -INFINITY, ls = 0.0f;
+    v4f acc[VS];
+#pragma unroll
+    for (int t = 0; t < VS; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    while (i < i_hi) {
+        const int64_t kb = c0 + 32 * i;
+        {
+            const int64_t kn = c0 + 32 * min(i + istep, tiles_c - 1);
+            na.load(p, kn, c1, g, c, kh);
+            nb.load(p, kn + 16, c1, g, c, kh);
+        }
+        // scores of keys kb + 16 h + 4g + r for query c, h = 0, 1
+        v4f sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const h8 ka = key_codes<DT>(ta.k, st), kbv = key_codes<DT>(tb.k, st);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[st], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qlo[st], sb, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[st], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qhi[st], sb, 0, 0, 0);
+        }
+        float sc[8];
+        float tm = -INFINITY;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const Tile& th = h ? tb : ta;
+                const int64_t kj = kb + 16 * h + 4 * g + r;
+                const int64_t kp = p.kpos ? (int64_t)__shfl(th.kp, 4 * g + r) : kj;
+                const bool keep = qok && kj < c1 && key_kept(kp, qp, p.window);
+                const float y = (h ? sb[r] : sa[r]) * (qinv * __shfl(th.ks, 4 * g + r));
+                sc[4 * h + r] = keep ? y * p.scale : -INFINITY;
+                tm = fmaxf(tm, sc[4 * h + r]);
             }
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float mn = fmaxf(m, tm);
+        const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
+        // the step's largest value scale (every lane group holds the scales
+        // of keys c of both halves)
+        float vmax = fmaxf(ta.vs, tb.vs);
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
+        int ev = 0;
+        if (vmax > 0.0f && vmax <= 3.4028235e38f) frexpf(vmax, &ev);
+        const float psc = ldexpf(1.0f, 14 - ev), pinv = ldexpf(1.0f, ev - 14);
+        h8 phi, plo;
+        float psum = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pr = (sc[4 * h + r] == -INFINITY) ? 0.0f : expf(sc[4 * h + r] - mn);
+                psum += pr;
+                _Float16 hi, lo;
+                split2(pr * __shfl((h ? tb : ta).vs, 4 * g + r) * psc, hi, lo);
+                phi[4 * h + r] = hi;
+                plo[4 * h + r] = lo;
+            }
+        ls = ls * alpha + psum;
+        m = mn;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * g + r);
+#pragma unroll
+            for (int t = 0; t < VS; ++t) acc[t][r] *= ar;
         }
+        // value sum: B = codes of element vdim(c, t) of the 8 keys' rows
+#pragma unroll
+        for (int t = 0; t < VS; ++t) {
+            const h8 vb = __builtin_bit_cast(
+                h8, make_uint4(value_pair<DT>(ta.v[0], ta.v[1], t), value_pair<DT>(ta.v[2], ta.v[3], t),
+                               value_pair<DT>(tb.v[0], tb.v[1], t), value_pair<DT>(tb.v[2], tb.v[3], t)));
+            v4f pv = {0.f, 0.f, 0.f, 0.f};
+            pv = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, vb, pv, 0, 0, 0);
+            pv = __builtin_amdgcn_mfma_f32_16x16x32_f16(phi, vb, pv, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(pv[r], pinv, acc[t][r]);
+        }
+        i += istep;
+        if (i >= i_hi) break;
+        ta = na;
+        tb = nb;
     }
+    merge_tile<Tile, D, MERGE_OUT>(p, m, ls, acc, tile, n_vec, chunk, kh, wave, g, c);
 }
 
 // Merge the chunks' (m, l, acc) of one (token, head) row per workgroup. Thread
@@ -625,8 +883,20 @@ AttnKernel pick_mfma(int dt, int D, bool merge_out) {
     }
 }
 
+template <int DT>
+AttnKernel pick_f16_dt(int D, bool merge_out) {
+    if (D == 64) return merge_out ? attn_f16_kernel<DT, 64, true> : attn_f16_kernel<DT, 64, false>;
+    if (D == 128) return merge_out ? attn_f16_kernel<DT, 128, true> : attn_f16_kernel<DT, 128, false>;
+    return nullptr;
+}
+
+AttnKernel pick_f16(int dt, int D, bool merge_out) {
+    return dt == 1 ? pick_f16_dt<1>(D, merge_out) : (dt == 2 ? pick_f16_dt<2>(D, merge_out) : nullptr);
+}
+
 struct AttnPlan {
     bool mfma;
+    bool f16;              // integer caches on the fp16 matrix cores (attn_f16_kernel)
     int E;                 // VALU kernel: elements per lane
     int64_t grid_z;        // query tiles (4 vectors: VALU kernel, 16: MFMA kernel)
     int64_t chunk_len;
@@ -636,7 +906,7 @@ struct AttnPlan {
 // The matrix-core kernel takes head_dim == value_dim in {64, 128} with
 // 16-byte aligned operands; other shapes take the vector kernel.
 bool attn_plan(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
-               int64_t value_dim, int64_t n_kv, bool aligned, AttnPlan& pl) {
+               int64_t value_dim, int64_t n_kv, bool aligned, int kv_dt, AttnPlan& pl) {
     const int64_t width = std::max(head_dim, value_dim);
     pl.E = width <= 64 ? 4 : (width <= 128 ? 8 : (width <= 256 ? 16 : 0));
     if (pl.E == 0) return false;
@@ -644,10 +914,12 @@ bool attn_plan(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
     const int64_t n_vec = n_q * rep;
     pl.mfma = aligned && head_dim == value_dim && (head_dim == 64 || head_dim == 128) &&
               tune("attn_mfma", 1) != 0;
+    // integer caches: 32-key steps a wave on the fp16 matrix cores
+    pl.f16 = pl.mfma && kv_dt != 0 && tune("attn_f16", 1) != 0;
     int64_t step;  // keys a workgroup walks per step
     if (pl.mfma) {
         pl.grid_z = (n_vec + 15) / 16;
-        step = 64;
+        step = pl.f16 ? 128 : 64;
     } else {
         pl.grid_z = (n_vec + kQV - 1) / kQV;
         step = kKeysPerStep;
@@ -749,10 +1021,10 @@ int64_t attn_workspace_bytes(int64_t n_q, int64_t n_head, int64_t n_head_kv, int
     AttnPlan pl;
     // the size for the vector kernel bounds the matrix-core kernel's
     if (n_q <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || n_kv <= 0 ||
-        !attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, true, pl))
+        !attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, true, 0, pl))
         return 0;
-    AttnPlan pv;
-    attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, false, pv);
+    AttnPlan pv;   // (the fp16 plan's 128-key steps give no more chunks)
+    attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, false, 0, pv);
     if (pv.n_chunks > pl.n_chunks) pl = pv;
     if (pl.n_chunks <= 1) return 0;
     return (int64_t)pl.n_chunks * n_q * n_head * (value_dim + 2) * 4;
@@ -784,7 +1056,7 @@ bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scal
     AttnPlan pl;
     const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
                          aligned16(workspace);
-    if (!attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, aligned, pl)) {
+    if (!attn_plan(n_q, n_head, n_head_kv, head_dim, value_dim, n_kv, aligned, kv_dt, pl)) {
         set_error("attention: head_dim/value_dim %lld/%lld above 256", (long long)head_dim,
                   (long long)value_dim);
         return false;
@@ -804,9 +1076,10 @@ bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scal
                  n_q, n_head, n_head_kv, head_dim, value_dim, n_kv,
                  (int)(n_head / n_head_kv), window, scale, pl.chunk_len, pl.n_chunks};
     const bool one = pl.n_chunks == 1;
-    AttnKernel kern = pl.mfma ? pick_mfma(kv_dt, (int)head_dim, one)
-                              : pick_attn(kv_dt, pl.E, one);
-    if (!launch(pl.mfma ? "attn_mfma_kernel" : "attn_kernel", kern,
+    AttnKernel kern = pl.f16 ? pick_f16(kv_dt, (int)head_dim, one)
+                      : pl.mfma ? pick_mfma(kv_dt, (int)head_dim, one)
+                                : pick_attn(kv_dt, pl.E, one);
+    if (!launch(pl.f16 ? "attn_f16_kernel" : (pl.mfma ? "attn_mfma_kernel" : "attn_kernel"), kern,
                 dim3((unsigned)pl.n_chunks, (unsigned)n_head_kv, (unsigned)pl.grid_z),
                 dim3(64 * kAttnWaves), 0, s, p))
         return false;
