@@ -140,11 +140,17 @@ def test_kv_write_bit_exact_and_ring(hip, oracle, dt):
 
 
 @pytest.mark.parametrize("dt,T,H,HK,D,S", [(1, 3, 32, 8, 128, 1500), (2, 3, 32, 8, 128, 1500),
-                                           (1, 40, 14, 2, 64, 700), (2, 1, 14, 2, 64, 3000)])
+                                           (1, 40, 14, 2, 64, 700), (2, 1, 14, 2, 64, 3000),
+                                           # several 32-key steps a wave (4 a chunk of 512),
+                                           # a partial last chunk
+                                           (1, 64, 32, 8, 128, 2048), (2, 64, 32, 8, 128, 2048),
+                                           (1, 1, 32, 8, 128, 32768), (2, 1, 32, 8, 64, 20000)])
 def test_attention_over_quantised_cache(hip, oracle, dt, T, H, HK, D, S):
-    """Attention reading an int8 / int4 cache equals the oracle's attention over
-    the cache read back with the reference's aero_kv_read_vec."""
+    """Attention reading an int8 / int4 cache (the fp16 matrix-core kernel at
+    head dims 64 and 128) equals the oracle's attention over the cache read
+    back with the reference's aero_kv_read_vec."""
     rng = np.random.default_rng(23 + dt + T)
+    print(f"quantised-cache attention dt={dt} T={T} H={H}/{HK} D={D} S={S}", flush=True)
     q, k, v = rand_qkv(rng, T, H, HK, D, D, S)
     vb = D if dt == 1 else D // 2
     kq, vq = DA.empty(S * HK * vb, np.uint8), DA.empty(S * HK * vb, np.uint8)
