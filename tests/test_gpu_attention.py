@@ -170,6 +170,41 @@ def test_attention_over_quantised_cache(hip, oracle, dt, T, H, HK, D, S):
     assert rel_to_scale(out.numpy(), want) <= RTOL
 
 
+@pytest.mark.parametrize("dt,D,H,HK,S", [(1, 64, 8, 2, 700), (2, 64, 8, 2, 700),
+                                          (1, 128, 32, 8, 6000), (2, 128, 32, 8, 6000)])
+def test_quantised_cache_positions_and_masks(hip, oracle, dt, D, H, HK, S):
+    """The integer-cache kernel (fp16 matrix steps) under arbitrary positions:
+    a shuffled cache (700 keys: one 32-key step a wave; 6000 keys: chunks of
+    384, three steps a wave), a query before every key (exact zeros),
+    positions past the cache, then the same with a window of 37."""
+    rng = np.random.default_rng(11 * dt + D)
+    T = 9
+    print(f"quantised-cache positions dt={dt} D={D} S={S}", flush=True)
+    q, k, v = rand_qkv(rng, T, H, HK, D, D, S)
+    vb = D if dt == 1 else D // 2
+    kq, vq = DA.empty(S * HK * vb, np.uint8), DA.empty(S * HK * vb, np.uint8)
+    ks, vs = DA.empty(S * HK), DA.empty(S * HK)
+    ops.kv_write(dt, DA.from_numpy(k), S, HK, D, kq, ks, 0, S)
+    ops.kv_write(dt, DA.from_numpy(v), S, HK, D, vq, vs, 0, S)
+    kqh, vqh = kq.numpy().reshape(S * HK, vb), vq.numpy().reshape(S * HK, vb)
+    ksh, vsh = ks.numpy(), vs.numpy()
+    kd = np.stack([oracle.kv_read_vec(dt, kqh[i], ksh[i], D) for i in range(S * HK)])
+    vd = np.stack([oracle.kv_read_vec(dt, vqh[i], vsh[i], D) for i in range(S * HK)])
+    kd, vd = kd.reshape(S, HK, D), vd.reshape(S, HK, D)
+    qpos = np.array([-3, 0, 5, S - 1, 120, 400, 401, S + 300, 2], np.int32)
+    kpos = rng.permutation(S).astype(np.int32)
+    for window in (0, 37):
+        out = DA.empty((T, H, D))
+        ops.attention(DA.from_numpy(q), kq, vq, out, T, H, HK, D, D, S, 0.11,
+                      qpos=DA.from_numpy(qpos), kpos=DA.from_numpy(kpos), window=window,
+                      kv_dt=dt, k_scale=ks, v_scale=vs)
+        want = oracle.attention_tiled(q, kd, vd, 0.11, qpos=qpos, kpos=kpos,
+                                      window=window or None)
+        got = out.numpy()
+        assert rel_to_scale(got, want) <= RTOL, window
+        assert not got[0].any()
+
+
 def test_softmax_rows(hip, oracle):
     """Rows of 1..100k values, large and tiny ranges; the flat-vector host ABI."""
     rng = np.random.default_rng(31)
