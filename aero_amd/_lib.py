@@ -128,6 +128,8 @@ PROTOTYPES = {
                                       c_int64, c_int64, c_int64, vp]),
     "aero_hip_gated_norm_matvec": (c_int, [c_int, vp, c_int64, c_int64, vp, vp, vp, vp, c_int64,
                                            c_float, c_int64, c_int64, vp]),
+    "aero_hip_gated_norm_matmul": (c_int, [c_int, vp, c_int64, c_int64, vp, vp, vp, vp, c_int64,
+                                           c_float, c_int64, c_int64, vp, c_int64, vp]),
     "aero_hip_matmul_workspace": (c_int64, [c_int, c_int64, c_int64]),
     "aero_hip_norm_matmul_workspace": (c_int64, [c_int, c_int64, c_int64, c_int64]),
     "aero_hip_split_partials_bytes": (c_int64, [c_int64, c_int64, c_int64]),

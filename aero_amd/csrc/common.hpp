@@ -99,6 +99,14 @@ struct RopeFold {
 };
 bool rope_fold_ok(const RopeFold& rope, bool pair, int n_mat, const int64_t* n_rows);
 
+// silu(v) = v / (1 + exp(-v)) with the hardware exp and reciprocal (about 1
+// ulp each), where silu sits in a pass that is limited by its instructions
+// (the conv's store, the split GEMM's x pre-pass, the gated GEMV prologue);
+// -inf gives NaN, as the division form does.
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+}
+
 // ------------------------------------------------- streaming loads/stores
 // Data read once or written once (activations) moves with the nontemporal
 // hint, so it streams through the caches without evicting what is reused

@@ -120,6 +120,8 @@ struct XsplitArgs {
     uint4* xp;
     float* xsum;
     float* xinv;
+    const float* z;       // NORM, gated (src/ssm.cpp:322-340): x * w[c % w_len] * silu(z)
+    int w_len;
 };
 
 template <bool NORM, bool RESID>
@@ -164,7 +166,8 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
                 ss += v[i].w * v[i].w;
             }
             if (a.w != nullptr) {
-                const float* wr = a.w + 256 * sb + 16 * cq;
+                const int wc = 256 * sb + 16 * cq;
+                const float* wr = a.w + (a.z != nullptr ? wc % a.w_len : wc);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float4 w4 = *reinterpret_cast<const float4*>(wr + 4 * i);
@@ -174,6 +177,17 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
                     }
                     v[i].x = v[i].x * w4.x; v[i].y = v[i].y * w4.y;
                     v[i].z = v[i].z * w4.z; v[i].w = v[i].w * w4.w;
+                }
+            }
+            if (a.z != nullptr) {   // gated: silu of the gate
+                const float* zr = a.z + off;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 z4 = ld_stream(zr + 4 * i);
+                    v[i].x = v[i].x * silu_fast(z4.x);
+                    v[i].y = v[i].y * silu_fast(z4.y);
+                    v[i].z = v[i].z * silu_fast(z4.z);
+                    v[i].w = v[i].w * silu_fast(z4.w);
                 }
             }
         }
@@ -794,6 +808,8 @@ struct SplitJob {
     void* ws;
     RopeFold rope;         // RoPE on the first rope.mats outputs (norm_matmul_rope)
     int64_t ws_bytes;      // room beyond split_ws_bytes lets few tokens split the columns
+    const float* z;        // gated norm (gated_norm_matmul): the gate, norm_w tiled
+    int64_t w_len;         //   with period w_len
 };
 
 template <bool NORM, bool RESID>
@@ -856,7 +872,7 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     const bool norm = j.norm >= 0;
     const SplitWs w = split_ws(j.ws, tp, j.n_cols);
     XsplitArgs a{j.x, j.d, j.x_out, j.norm_w, w.ssq, norm && (j.norm & AERO_NORM_UNIT_OFFSET),
-                 (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv};
+                 (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv, j.z, (int)j.w_len};
     const bool ok = norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
                                 : launch_xsplit<true, false>(a, tp, s))
                          : (j.d ? launch_xsplit<false, true>(a, tp, s)
@@ -1024,6 +1040,9 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                     const float* x, const float* norm_w, float eps, int norm, int act,
                     int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d, float* xo,
                     const RopeFold* rope);
+bool gemv_gated_dev(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows, float* y,
+                    const float* x, const float* z, const float* norm_w, int64_t w_len,
+                    float eps, int64_t n_cols, int64_t n_tok, hipStream_t s);
 
 // ------------------------------------------------ allocation-free matmul
 // The split GEMM's workspace in a file-scope device array, for callers that
@@ -1184,6 +1203,14 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
                   (long long)j.n_cols, (long long)j.n_tok, j.n_mat, j.norm, (long long)bv);
         return false;
     }
+    if (j.z != nullptr &&
+        (gu || j.n_mat != 1 || j.d != nullptr || j.norm != 0 || j.norm_w == nullptr ||
+         !aligned16(j.z) || j.w_len < 16 || j.w_len % 16 || j.n_cols % j.w_len)) {
+        set_error("gated_norm_matmul: one matrix, a 16-byte aligned gate and a norm weight whose "
+                  "length is a multiple of 16 dividing the row (w_len=%lld, n_cols=%lld)",
+                  (long long)j.w_len, (long long)j.n_cols);
+        return false;
+    }
     j.rb = (j.n_cols / bv) * bb;
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) {
         if (j.w[m] == nullptr || j.y[m] == nullptr || j.n_rows[m] < 0 ||
@@ -1204,7 +1231,10 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
     const bool fused = !split && fused_gemv_rows_ok(j, gu, w_bytes);
-    if (fused && fused_prologue_ok(j))
+    if (fused && j.z != nullptr && j.n_tok <= 2)   // the gated norm in the GEMV's prologue
+        return gemv_gated_dev(j.dtype, j.w[0], w_bytes[0], j.n_rows[0], j.y[0], j.x, j.z,
+                              j.norm_w, j.w_len, j.eps, j.n_cols, j.n_tok, s);
+    if (fused && j.z == nullptr && fused_prologue_ok(j))
         return fused_gemv_run(j, gu, w_bytes, j.x, j.norm, j.d, s, rope_done);
     const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)
                                : align256(j.n_tok * j.n_cols * 4) +
@@ -1221,7 +1251,12 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     // is left unused) and h is x'
     const float* h = j.d ? j.x_out : j.x;
     float* hb = static_cast<float*>(j.ws);
-    if (j.d) {
+    if (j.z != nullptr) {
+        if (!aero_hip_gated_rmsnorm_silu(j.x, j.z, j.norm_w, j.w_len, hb, j.n_tok, j.n_cols,
+                                         j.n_cols, j.eps, s))
+            return false;
+        h = hb;
+    } else if (j.d) {
         if (!aero_hip_add_rmsnorm(j.x, j.d, j.x_out, j.norm_w, hb, j.n_tok, j.n_cols, j.eps,
                                   j.norm >= 0 ? j.norm : 0, s))
             return false;
@@ -1277,6 +1312,24 @@ int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const in
     bool rope_done;
     return aero::norm_matmul_run(j, w_bytes, 0, ws_bytes, (hipStream_t)stream, &rope_done) ? 1
                                                                                            : 0;
+}
+
+int aero_hip_gated_norm_matmul(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows,
+                               float* y, const float* x, const float* z, const float* norm_w,
+                               int64_t w_len, float eps, int64_t n_cols, int64_t n_tok,
+                               void* ws, int64_t ws_bytes, void* stream) {
+    aero::clear_error();
+    aero::SplitJob j{dtype, x, nullptr, nullptr, norm_w, 0, eps, 1, &w, nullptr, 0, &n_rows, &y,
+                     n_cols, 0, n_tok, ws, {}};
+    j.z = z;
+    j.w_len = w_len;
+    if (z == nullptr) {
+        aero::set_error("gated_norm_matmul: null gate");
+        return 0;
+    }
+    bool rope_done;
+    return aero::norm_matmul_run(j, &w_bytes, 0, ws_bytes, (hipStream_t)stream, &rope_done) ? 1
+                                                                                            : 0;
 }
 
 int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,

@@ -1111,8 +1111,6 @@ __device__ __forceinline__ float act_rt(int kind, float v) {
 // step's weights are requested before the norm is computed (after x, which
 // the norm waits for); for rows of one step the x loaded for the norm is the
 // x staged.
-__device__ __forceinline__ float gate_silu(float v) { return v / (1.0f + expf(-v)); }
-
 template <int TYPE, int T, bool PIPE, bool PAIR, bool RESID, bool GATED = false>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse f) {
     using L = Lane64<TYPE>;
@@ -1218,10 +1216,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float4 v = xv.v[t][q], z = zr.v[t][q];
-                    xv.v[t][q] = make_float4(((v.x / den[t]) * wv[q].x) * gate_silu(z.x),
-                                             ((v.y / den[t]) * wv[q].y) * gate_silu(z.y),
-                                             ((v.z / den[t]) * wv[q].z) * gate_silu(z.z),
-                                             ((v.w / den[t]) * wv[q].w) * gate_silu(z.w));
+                    xv.v[t][q] = make_float4(((v.x / den[t]) * wv[q].x) * silu_fast(z.x),
+                                             ((v.y / den[t]) * wv[q].y) * silu_fast(z.y),
+                                             ((v.z / den[t]) * wv[q].z) * silu_fast(z.z),
+                                             ((v.w / den[t]) * wv[q].w) * silu_fast(z.w));
                 }
             return;
         }

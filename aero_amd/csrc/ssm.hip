@@ -262,11 +262,11 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(ScanArgs a) {
     }
 }
 
-// silu in the reference's division form (src/ssm.cpp:17), applied to the
-// conv's outputs when the SSM layer asks for it (src/ssm.cpp:298-301)
+// silu (src/ssm.cpp:17), applied to the conv's outputs when the SSM layer
+// asks for it (src/ssm.cpp:298-301)
 template <bool SILU>
 __device__ __forceinline__ float conv_out(float v) {
-    if constexpr (SILU) return v / (1.0f + expf(-v));
+    if constexpr (SILU) return silu_fast(v);
     return v;
 }
 

@@ -314,6 +314,27 @@ def gated_norm_matvec(dtype: int, w: DeviceArray, x: DeviceArray, z: DeviceArray
                "gated_norm_matvec")
 
 
+def gated_norm_matmul(dtype: int, w: DeviceArray, x: DeviceArray, z: DeviceArray,
+                      norm_w: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
+                      n_tok: int, eps: float, stream: Stream | None = None) -> None:
+    """y = gated_rmsnorm_silu(x, z, tile(norm_w)) @ W^T over whole rows, any
+    token count (src/ssm.cpp:322-348): the norm in the fused GEMV's prologue
+    up to 2 tokens, in the split GEMM's x pre-pass on its path, else a gated
+    norm pass into the workspace before the projection."""
+    _need(x, n_tok * n_cols, np.float32, "x")
+    _need(z, n_tok * n_cols, np.float32, "z")
+    _need(y, n_tok * n_rows, np.float32, "y")
+    _need(norm_w, 1, np.float32, "norm_w")
+    L = _lib.lib()
+    wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, 0, n_tok)
+    wsb += L.aero_hip_split_partials_bytes(int(n_rows), n_cols, n_tok)
+    buf = _norm_mm_ws.get(wsb)
+    _lib.check(L.aero_hip_gated_norm_matmul(int(dtype), w.ptr, w.nbytes, n_rows, y.ptr, x.ptr,
+                                            z.ptr, norm_w.ptr, norm_w.size, float(eps), n_cols,
+                                            n_tok, as_ptr(buf), 0 if buf is None else buf.nbytes,
+                                            _s(stream)), "gated_norm_matmul")
+
+
 def _norm_flag(norm: bool, unit_offset: bool) -> int:
     return (NORM_UNIT_OFFSET if unit_offset else 0) if norm else -1
 

@@ -15,9 +15,10 @@ Projections of one weight type that read x go to the GPU in one launch (up
 to four matrices); the silu runs in the conv's store, and the scan reads q,
 k and v as strided slices of the conv output (scan_strided, :128-142), so
 five launches carry the layer (the scan adds its prep pass and, from 128
-tokens, the chunk pre-pass). At one or two tokens the conv also writes its
-history, and the gated norm runs in the output projection's GEMV prologue
-(fusion "norm_gemm"): four launches. The gated norm site consults aero_amd.select
+tokens, the chunk pre-pass). The gated norm runs inside the output
+projection (fusion "norm_gemm"): in its GEMV prologue at one or two tokens,
+in the split GEMM's x pre-pass on that path. At one or two tokens the conv
+also writes its history: four launches. The gated norm site consults aero_amd.select
 (op "gated_norm") like the decoder block's sites; the projections, conv and
 scan have no host path. With every op on the GPU, `forward` can be recorded
 as a Plan: the recording keeps the conv history length of its first call,
@@ -121,12 +122,6 @@ class SsmStep:
         for name, t in zip(PROJ[:4], cfg.wtypes[:4]):
             groups.setdefault(t, []).append(name)
         self.groups = [(t, names, [outs[n] for n in names]) for t, names in groups.items()]
-        # the output projection's rows fit the fused decode GEMV (whole 16
-        # bytes, or Q8_0 rows of whole 8 bytes in a matrix ending on a 16-byte
-        # boundary): the gated norm can run in its prologue
-        t4 = cfg.wtypes[4]
-        rb = (I // W.BLOCK[t4][0]) * W.BLOCK[t4][1]
-        self.out_rows16 = rb % 16 == 0 or (t4 == W.Q8_0 and rb % 8 == 0 and N * rb % 16 == 0)
         self.reset()
 
     def reset(self) -> None:
@@ -160,10 +155,12 @@ class SsmStep:
                      dev["dt_bias"], self.state, self.o, T, cfg.n_k, cfg.n_v, cfg.head_dim,
                      self.scale, cfg.eps, strides=(cfg.qkv, cfg.qkv, cfg.qkv), q_off=0,
                      k_off=nk_d, v_off=2 * nk_d, stream=stream)
-        if T <= 2 and self.out_rows16 and self.gpu("gated_norm") and select.fusion_enabled(
-                "norm_gemm", self.fusions.get("norm_gemm")):
-            # decode: the gated norm in the output projection's GEMV prologue
-            ops.gated_norm_matvec(cfg.wtypes[4], dev["out"], self.o, self.gate, dev["norm"],
+        if self.gpu("gated_norm") and select.fusion_enabled("norm_gemm",
+                                                            self.fusions.get("norm_gemm")):
+            # the gated norm in the output projection: its GEMV prologue at
+            # decode, its x pre-pass on the split GEMM's path, else a gated
+            # norm pass into the projection's workspace
+            ops.gated_norm_matmul(cfg.wtypes[4], dev["out"], self.o, self.gate, dev["norm"],
                                   self.out, cfg.hidden, cfg.inner, T, cfg.norm_eps,
                                   stream=stream)
             return

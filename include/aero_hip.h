@@ -330,6 +330,16 @@ int aero_hip_gated_norm_matvec(int dtype, const uint8_t* w, int64_t w_bytes, int
                                float* y, const float* x, const float* z, const float* norm_w,
                                int64_t w_len, float eps, int64_t n_cols, int64_t n_tok,
                                void* stream);
+/* The same for any token count, with the workspace of aero_hip_norm_matmul
+ * (aero_hip_norm_matmul_workspace(dtype, n_cols, 0, n_tok) plus
+ * aero_hip_split_partials_bytes(n_rows, n_cols, n_tok)): up to 2 tokens the
+ * fused GEMV above; on the split GEMM's path (Q4_K / Q5_K, from 5-16 tokens by
+ * matrix size) the gated norm in its x pre-pass, the inverse RMS in its
+ * epilogue; otherwise the gated norm into the workspace, then the projection. */
+int aero_hip_gated_norm_matmul(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows,
+                               float* y, const float* x, const float* z, const float* norm_w,
+                               int64_t w_len, float eps, int64_t n_cols, int64_t n_tok,
+                               void* ws, int64_t ws_bytes, void* stream);
 
 int64_t aero_hip_matmul_workspace(int dtype, int64_t n_cols, int64_t n_tok);
 int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,

@@ -316,3 +316,26 @@ def test_norm_matmul_rope_refusals(hip):
     assert call(64, 64, 1, None) == 0
     assert call(64, 64, 2, pos.ptr) == 0
     assert call(64, 64, 1, pos.ptr) == 1
+
+
+@pytest.mark.parametrize("t,n_cols,w_len", [(W.Q4_K, 1024, 128), (W.Q8_0, 512, 64),
+                                             (W.Q6_K, 1024, 256)])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 16, 40, 100])
+def test_gated_norm_matmul_vs_oracle(hip, oracle, t, n_cols, w_len, n_tok):
+    """The gated-DeltaNet norm folded into the projection after it, any token
+    count: the fused GEMV's prologue (1-2 tokens), a gated norm pass then the
+    GEMV (3-16; Q6_K rows of 840 bytes always), the split GEMM's x pre-pass
+    (Q4_K from 16 tokens at this size), the fp32 GEMM on the normed rows (Q8_0
+    from 32); against the oracle's gated_rmsnorm_silu then matmul."""
+    rng = np.random.default_rng(n_cols + w_len + n_tok)
+    n_rows = 512
+    w = W.weight_table(t, n_rows, n_cols, rng)
+    x = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    z = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(w_len)).astype(np.float32)
+    y = DA.empty((n_tok, n_rows))
+    print(f"gated_norm_matmul type={t} cols={n_cols} w_len={w_len} tokens={n_tok}", flush=True)
+    ops.gated_norm_matmul(t, DA.from_numpy(w), DA.from_numpy(x), DA.from_numpy(z),
+                          DA.from_numpy(nw), y, n_rows, n_cols, n_tok, 1e-6)
+    want = oracle.matmul(t, w, oracle.gated_rmsnorm_silu(x, z, nw, 1e-6), n_rows)
+    assert rel_to_scale(y.numpy(), want) <= RTOL
