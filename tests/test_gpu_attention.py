@@ -234,3 +234,53 @@ def test_attention_decode_full_size(hip, oracle):
     q, k, v = rand_qkv(rng, 512, 32, 8, 128, 128, 512)
     got = gpu_attention(q, k, v, 1 / np.sqrt(128))
     assert rel_to_scale(got, oracle.attention_tiled(q, k, v, 1 / np.sqrt(128))) <= RTOL
+
+
+def _random_attention_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        dt = int(rng.integers(0, 3))
+        D = int(rng.choice([64, 128]))
+        HK = int(rng.choice([1, 2, 4, 8]))
+        H = HK * int(rng.choice([1, 2, 4, 7, 8]))
+        T = int(rng.integers(1, 71))
+        S = int(rng.integers(T, 3001))
+        window = int(rng.choice([0, 0, int(rng.integers(1, S + 1))]))
+        cases.append((i, dt, T, H, HK, D, S, window))
+    return cases
+
+
+@pytest.mark.parametrize("i,dt,T,H,HK,D,S,window", _random_attention_cases(24, 2026))
+def test_attention_random_shapes(hip, oracle, i, dt, T, H, HK, D, S, window):
+    """Seeded random shapes over every cache type and both matrix-core kernels:
+    1-70 queries at the last positions of 1-3000 keys, 1-8 query heads a kv
+    head, head dims 64 / 128, with and without a window."""
+    rng = np.random.default_rng(100 + i)
+    print(f"random attention {i}: dt={dt} T={T} H={H}/{HK} D={D} S={S} window={window}",
+          flush=True)
+    q, k, v = rand_qkv(rng, T, H, HK, D, D, S)
+    qpos = np.arange(S - T, S, dtype=np.int32)
+    scale = 1.0 / np.sqrt(D)
+    if dt == 0:
+        got = gpu_attention(q, k, v, scale, qpos=qpos, window=window)
+        want = oracle.attention_tiled(q, k, v, scale, qpos=qpos, window=window or None)
+    else:
+        vb = D if dt == 1 else D // 2
+        kq, vq = DA.empty(S * HK * vb, np.uint8), DA.empty(S * HK * vb, np.uint8)
+        ks, vs = DA.empty(S * HK), DA.empty(S * HK)
+        ops.kv_write(dt, DA.from_numpy(k), S, HK, D, kq, ks, 0, S)
+        ops.kv_write(dt, DA.from_numpy(v), S, HK, D, vq, vs, 0, S)
+        kqh, vqh = kq.numpy().reshape(S * HK, vb), vq.numpy().reshape(S * HK, vb)
+        ksh, vsh = ks.numpy(), vs.numpy()
+        kd = np.stack([oracle.kv_read_vec(dt, kqh[j], ksh[j], D)
+                       for j in range(S * HK)]).reshape(S, HK, D)
+        vd = np.stack([oracle.kv_read_vec(dt, vqh[j], vsh[j], D)
+                       for j in range(S * HK)]).reshape(S, HK, D)
+        out = DA.empty((T, H, D))
+        ops.attention(DA.from_numpy(q), kq, vq, out, T, H, HK, D, D, S, scale,
+                      qpos=DA.from_numpy(qpos), window=window, kv_dt=dt, k_scale=ks,
+                      v_scale=vs)
+        got = out.numpy()
+        want = oracle.attention_tiled(q, kd, vd, scale, qpos=qpos, window=window or None)
+    assert rel_to_scale(got, want) <= RTOL
