@@ -122,6 +122,7 @@ struct XsplitArgs {
     float* xinv;
     const float* z;       // NORM, gated (src/ssm.cpp:322-340): x * w[c % w_len] * silu(z)
     int w_len;
+    int q8;               // Q8_0 operand order (else the K-quant order)
 };
 
 template <bool NORM, bool RESID>
@@ -223,11 +224,21 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
 #pragma unroll
     for (int rep = 0; rep < 2; ++rep) {
         const int s8 = (tid >> 6) + 4 * rep;
-        const int c0 = 128 * (s8 >> 2) + 64 * (g >> 1) + 16 * (g & 1) + 4 * (s8 & 3);
-        const float* xr = xl + lt * RowF + c0;
-        const float4 va = *reinterpret_cast<const float4*>(xr);
-        const float4 vb = *reinterpret_cast<const float4*>(xr + 32);
-        const float w[8] = {va.x, va.z, va.y, va.w, vb.x, vb.z, vb.y, vb.w};
+        float w[8];
+        if (a.q8) {
+            // Q8_0 block s8: values (2 + 8g + i) % 32 of even blocks, 8g + i of odd
+            const float* xr = xl + lt * RowF + 32 * s8;
+            const int o = (s8 & 1) ? 8 * g : 2 + 8 * g;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = xr[(o + i) & 31];
+        } else {
+            const int c0 = 128 * (s8 >> 2) + 64 * (g >> 1) + 16 * (g & 1) + 4 * (s8 & 3);
+            const float* xr = xl + lt * RowF + c0;
+            const float4 va = *reinterpret_cast<const float4*>(xr);
+            const float4 vb = *reinterpret_cast<const float4*>(xr + 32);
+            w[0] = va.x; w[1] = va.z; w[2] = va.y; w[3] = va.w;
+            w[4] = vb.x; w[5] = vb.z; w[6] = vb.y; w[7] = vb.w;
+        }
         h8 parts[kParts];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -395,17 +406,51 @@ __device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
+// Q8_0 (src/kernels.cpp:364-373): 34-byte blocks of an fp16 scale d and 32
+// int8 quants, value d*q. Here a super-block is 8 blocks (272 bytes) and
+// step s of half h is block 4h + s. A block pair (68 bytes: d0 q0[32] d1
+// q1[32]) starts 4-byte aligned, so lane group g takes, as dwords:
+//   even block: q0[2+8g .. 9+8g] at pair bytes 4+8g (g = 3: q0[26..29], and
+//               q0[30], q0[31], q0[0], q0[1] from the dwords at 32 and 0),
+//   odd block:  q1[8g .. 8g+7] at pair bytes 36+8g,
+// and every lane d0 (dword 0) and d1 (dword 32, high half): six dwords a
+// pair. xsplit_kernel writes x in this order. q is exact in fp16 and so is
+// each product with an x part; d scales each block's sum (fp32) after its
+// matrix steps, lane-locally since an accumulator lane holds one row.
+__device__ __forceinline__ uint32_t ld_w1(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+__device__ __forceinline__ uint2 ld_w2(const uint8_t* p) {   // 4-byte aligned
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return make_uint2(q[0], q[1]);
+}
+// 8 int8 quants (bytes of w0, then w1) as fp16: each byte offset by 128 and
+// placed under the exponent bits of 1024 by a byte permute, then 1152
+// subtracted (exact).
+__device__ __forceinline__ h8 q8_operand(uint32_t w0, uint32_t w1) {
+    constexpr uint32_t E = 0x64646464u, LO = 0x04010400u, HI = 0x04030402u;
+    const h2 off{(_Float16)-1152.f, (_Float16)-1152.f};
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+    const h2 a0 = as_h2(__builtin_amdgcn_perm(E, u0, LO)) + off;
+    const h2 a1 = as_h2(__builtin_amdgcn_perm(E, u0, HI)) + off;
+    const h2 a2 = as_h2(__builtin_amdgcn_perm(E, u1, LO)) + off;
+    const h2 a3 = as_h2(__builtin_amdgcn_perm(E, u1, HI)) + off;
+    return __builtin_bit_cast(h8, make_uint4(as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)));
+}
+
 // NT matrix tiles of 16 rows a wave; a workgroup covers 4 x 16NT rows. In
 // the gate/up form (EPI >= 0, NT = 2) tile 0 holds 16 rows of the gate
 // matrix and tile 1 the same 16 rows of the up matrix, so each lane ends
 // with gate and up of the same (token, row) and writes act(gate) * up: a
 // workgroup covers 4 x 16 output rows.
 template <int TYPE, int NT, int EPI>
-__global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 4 ? 1 : 2)))
+void split_gemm_kernel(SplitParams p) {
     constexpr bool Q5 = TYPE == AERO_DTYPE_Q5_K;
+    constexpr bool Q8 = TYPE == AERO_DTYPE_Q8_0;
     constexpr bool GU = EPI != kEpiPlain;
     static_assert(!GU || NT == 2, "gate/up pairs one gate and one up tile");
-    constexpr int BB = Q5 ? 176 : 144;          // bytes a super-block
+    constexpr int BB = Q8 ? 272 : (Q5 ? 176 : 144);   // bytes a super-block
     constexpr int QOFF = Q5 ? 48 : 16;          // quants within the block
     constexpr int kRowsWave = GU ? 16 : 16 * NT;
     constexpr int MT = kTokTile / 16;           // matrix tiles over tokens (2)
@@ -534,6 +579,130 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
         }
     };
 
+    // Q8_0: the six dwords of each block pair of half `half` of super-block sb
+    auto load_w8 = [&](int sb, int half, uint32_t (&dst)[NT][12]) {
+        const int64_t o = (int64_t)min(sb, n_sb - 1) * BB + 136 * half;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const uint8_t* e = wbase[j] + woff[j] + o + 68 * pr;
+                const uint2 l0 = ld_w2(e + 4 + 8 * g), l2 = ld_w2(e + 36 + 8 * g);
+                dst[j][6 * pr + 0] = l0.x;
+                dst[j][6 * pr + 1] = l0.y;
+                dst[j][6 * pr + 2] = ld_w1(e);
+                dst[j][6 * pr + 3] = l2.x;
+                dst[j][6 * pr + 4] = l2.y;
+                dst[j][6 * pr + 5] = ld_w1(e + 32);
+            }
+    };
+    // the 4 blocks of one half from LDS buffer xb: each block's matrix steps
+    // into P from zero, then sacc += d * P a step later (pipelined as
+    // run_steps, with the block's d conversion and scaling among the VALU)
+    v4f sacc[MT][NT];
+    auto run_q8 = [&](const u4* xb, const uint32_t (&wq)[NT][12]) {
+        h8 A[2][MT][kParts], B[2][NT];
+        float dsc[kChunkSteps][NT];
+        v4f P[2][MT][NT];
+        auto read_a = [&](int s, h8 (&a)[MT][kParts]) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int pp = 0; pp < kParts; ++pp)
+                    a[m][pp] = __builtin_bit_cast(
+                        h8, xb[((m * kChunkSteps + s) * kParts + pp) * 64 + l]);
+        };
+        auto decode = [&](int s, h8 (&b)[NT]) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const uint32_t* w = wq[j] + 6 * (s >> 1);
+                if (s & 1) {
+                    b[j] = q8_operand(w[3], w[4]);
+                    dsc[s][j] = f16_hi(w[5]);
+                } else {
+                    const uint32_t w1 = g == 3 ? __builtin_amdgcn_perm(w[5], w[2], 0x03020504u)
+                                               : w[1];
+                    b[j] = q8_operand(w[0], w1);
+                    dsc[s][j] = f16_lo(w[2]);
+                }
+            }
+        };
+        auto scale_in = [&](int s) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        sacc[m][j][v] = fmaf(dsc[s][j], P[s & 1][m][j][v], sacc[m][j][v]);
+        };
+        read_a(0, A[0]);
+        decode(0, B[0]);
+#pragma unroll
+        for (int s = 0; s < kChunkSteps; ++s) {
+            if (s + 1 < kChunkSteps) {
+                read_a(s + 1, A[(s + 1) & 1]);
+                decode(s + 1, B[(s + 1) & 1]);
+            }
+#pragma unroll
+            for (int pp = kParts - 1; pp >= 0; --pp)
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j)
+                        P[s & 1][m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            A[s & 1][m][pp], B[s & 1][j],
+                            pp == kParts - 1 ? v4f{0.f, 0.f, 0.f, 0.f} : P[s & 1][m][j], 0, 0,
+                            0);
+            if (s > 0) scale_in(s - 1);
+            constexpr int kMfma = kParts * MT * NT, kReads = MT * kParts;
+#pragma unroll
+            for (int i = 0; i < kMfma; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix step
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+                if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        scale_in(kChunkSteps - 1);
+    };
+
+    if constexpr (Q8) {
+        uint32_t wa[NT][12];
+        xst.load(2 * sb0);
+        load_w8(sb0, 0, wa);
+        xst.store(xs[0], ss[sb0 & 1], si[sb0 & 1], tid);
+        xst.load(2 * sb0 + 1);
+        __syncthreads();
+        for (int sb = sb0; sb < sb1; ++sb) {
+            uint32_t wb[NT][12];
+            load_w8(sb, 1, wb);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int j = 0; j < NT; ++j) sacc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            run_q8(xs[0], wa);
+            xst.store(xs[1], nullptr, nullptr, tid);
+            xst.load(2 * sb + 2);
+            __syncthreads();
+            load_w8(sb + 1, 0, wa);   // the next super-block's first half (clamped)
+            run_q8(xs[1], wb);
+            // acc += inv * sacc, inv the token's inverse scale of this super-block
+            const float* ip = si[sb & 1];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const v4f inv = *reinterpret_cast<const v4f*>(ip + 16 * m + 4 * g);
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[m][j][v] = fmaf(inv[v], sacc[m][j][v], acc[m][j][v]);
+            }
+            xst.store(xs[0], ss[(sb + 1) & 1], si[(sb + 1) & 1], tid);
+            xst.load(2 * sb + 3);
+            __syncthreads();
+        }
+    } else {
     // prologue: chunk 2 sb0 (super-block sb0, first half) staged, the next in
     // flight
     xst.load(2 * sb0);
@@ -599,6 +768,7 @@ __global__ __launch_bounds__(256) void split_gemm_kernel(SplitParams p) {
             hd[j] = hdn[j];
         }
         __syncthreads();
+    }
     }
 
     // split over columns: the raw sums go to the partials (the norm's scale
@@ -781,7 +951,8 @@ int64_t pad_tokens(int64_t n_tok) { return (n_tok + kTokTile - 1) / kTokTile * k
 // The shape part of whether the split path applies (types with it, whole
 // super-blocks a row, grid limits); alignment is checked at the call.
 bool split_shape_ok(int dtype, int64_t n_cols, int64_t n_tok) {
-    return (dtype == AERO_DTYPE_Q4_K || dtype == AERO_DTYPE_Q5_K) && n_cols > 0 &&
+    return (dtype == AERO_DTYPE_Q4_K || dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q8_0) &&
+           n_cols > 0 &&
            n_cols % 256 == 0 && n_cols / 256 <= 65535 && n_tok > 0 &&
            pad_tokens(n_tok) / kTokTile <= 65535 && pad_tokens(n_tok) <= 0x7fffffff;
 }
@@ -872,7 +1043,8 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     const bool norm = j.norm >= 0;
     const SplitWs w = split_ws(j.ws, tp, j.n_cols);
     XsplitArgs a{j.x, j.d, j.x_out, j.norm_w, w.ssq, norm && (j.norm & AERO_NORM_UNIT_OFFSET),
-                 (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv, j.z, (int)j.w_len};
+                 (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv, j.z, (int)j.w_len,
+                 j.dtype == AERO_DTYPE_Q8_0};
     const bool ok = norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
                                 : launch_xsplit<true, false>(a, tp, s))
                          : (j.d ? launch_xsplit<false, true>(a, tp, s)
@@ -883,10 +1055,10 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     // one wave a SIMD and measured slower on MI355X at every prefill shape
     const int nt = gu ? 2 : (tune("gemm16_nt", 2) == 4 ? 4 : 2);
     const int rows_wg = gu ? 64 : 64 * nt;
-    const bool q5 = j.dtype == AERO_DTYPE_Q5_K;
     const int epi = gu ? j.act : kEpiPlain;
-    void* kp = q5 ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi)
-                  : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi);
+    void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi)
+               : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi)
+                                            : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi);
     if (kp == nullptr) {
         set_error("split GEMM: unknown activation %d", j.act);
         return false;

@@ -1,7 +1,7 @@
 """GPU parity: the split-x fp16 matrix-core GEMM (aero_hip_matmul with a
-workspace, Q4_K / Q5_K, 32 or more tokens) against the oracle's restatement of
-the reference's matmul (src/kernels.cpp:337-404,520-538) and against the exact
-product.
+workspace, Q4_K / Q5_K / Q8_0, 32 or more tokens) against the oracle's
+restatement of the reference's matmul (src/kernels.cpp:337-404,364-373,520-538)
+and against the exact product.
 
 Tolerances: 1e-5 relative to the output's scale against the oracle (the
 reference's RTOL for fp32 ops, tests/test_transformer_native.py:34-37). Each
@@ -21,7 +21,11 @@ from aero_amd.device import DeviceArray as DA
 
 pytestmark = pytest.mark.gpu
 
-KTYPES = [W.Q4_K, W.Q5_K]
+KTYPES = [W.Q4_K, W.Q5_K, W.Q8_0]
+
+
+def table(t, n_rows, n_cols, rng):
+    return W.make_table(t, n_rows * n_cols // W.BLOCK[t][0], rng)
 
 
 def gpu_matmul(t, w, X, n_rows, split=True):
@@ -45,7 +49,7 @@ def test_workspace_sizes(hip):
         assert L.aero_hip_matmul_workspace(t, 4096, 512) >= 512 * 4096 * 4   # 2 fp16 parts
         assert L.aero_hip_matmul_workspace(t, 4096, 33) >= 64 * 4096 * 4  # padded to 32s
         assert L.aero_hip_matmul_workspace(t, 100, 64) == 0                # not whole blocks
-    for t in (W.Q8_0, W.Q6_K, W.IQ4_XS, W.F32):
+    for t in (W.Q6_K, W.IQ4_XS, W.F32):
         assert L.aero_hip_matmul_workspace(t, 4096, 512) == 0
 
 
@@ -58,7 +62,7 @@ def test_split_gemm_vs_oracle(hip, oracle, t, n_rows, n_cols, n_tok):
     """Partial row tiles (rows not a multiple of 128), partial token tiles (33,
     40, 95, 100 tokens), one to 56 super-blocks a row."""
     rng = np.random.default_rng(n_rows * 31 + n_cols + n_tok + t)
-    w = W.make_table(t, n_rows * n_cols // 256, rng)
+    w = table(t, n_rows, n_cols, rng)
     X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
     print(f"split gemm type={t} rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
     got = gpu_matmul(t, w, X, n_rows)
@@ -71,10 +75,13 @@ def test_split_gemm_magnitudes(hip, oracle, t):
     """Tokens at 1e-30 and 1e30 scale, an all-zero token, a token of one
     outlier among small values, fp32 subnormals and values equal to 2^-16 of
     their token's largest: all within 1e-6 of the exact product's scale (per
-    token), the zero token exactly zero."""
+    token), the zero token exactly zero. The subnormal token's outputs are
+    themselves subnormal (~13 significant bits): there each super-block's
+    scaled-back sum is rounded once to the fp32 grid (2^-149) as it is added,
+    so the bound gains one grid step a super-block."""
     rng = np.random.default_rng(5 + t)
     n_rows, n_cols = 96, 1024
-    w = W.make_table(t, n_rows * n_cols // 256, rng)
+    w = table(t, n_rows, n_cols, rng)
     base = rng.standard_normal((8, n_cols)).astype(np.float32)
     X = np.empty((40, n_cols), np.float32)
     X[:] = rng.standard_normal((40, n_cols)).astype(np.float32)
@@ -93,7 +100,7 @@ def test_split_gemm_magnitudes(hip, oracle, t):
         if i == 2:
             continue
         scale = np.abs(want[i]).max()
-        assert np.abs(got[i] - want[i]).max() <= 1e-6 * scale, i
+        assert np.abs(got[i] - want[i]).max() <= 1e-6 * scale + (n_cols // 256) * 2.0 ** -149, i
 
 
 def test_split_gemm_per_value_bound(hip, oracle):
@@ -136,6 +143,59 @@ def test_split_gemm_per_value_bound(hip, oracle):
     assert np.array_equal(got[1], want[1])            # 22 or fewer bits: exact
     # the scaled block's largest is in [2^14, 2^15): 2^-25 absolute there
     assert np.abs(got[2, ::2] - want[2, ::2]).max() <= 1000.0 * 2.0 ** -39
+
+
+def q8_blocks(q, d):
+    """Q8_0 rows from int8 quants q [rows, cols] and fp16 scales d [rows, cols/32]."""
+    rows, cols = q.shape
+    blk = np.empty((rows, cols // 32, 34), np.uint8)
+    blk[:, :, 0:2] = np.ascontiguousarray(d.astype(np.float16)).view(np.uint8).reshape(
+        rows, cols // 32, 2)
+    blk[:, :, 2:] = q.astype(np.int8).view(np.uint8).reshape(rows, cols // 32, 32)
+    return blk.reshape(-1)
+
+
+def test_split_gemm_q8_identity(hip, oracle):
+    """Q8_0 rows that pick one column each (d = 1, q = 1 there, 0 elsewhere),
+    every column of 1024 once: y equals x value for value, for x of 22
+    significant bits within 2^7 of their super-block's largest (the two fp16
+    parts then hold them exactly). Each column
+    position of the even and odd blocks of a pair comes from a different lane
+    and dword of the weight rows, so a wrong operand order shows."""
+    t, n = W.Q8_0, 1024
+    rng = np.random.default_rng(41)
+    perm = rng.permutation(n)
+    q = np.zeros((n, n), np.int8)
+    q[np.arange(n), perm] = 1
+    w = q8_blocks(q, np.ones((n, n // 32), np.float32))
+    Wd = oracle.dequant(t, w, n * n).reshape(n, n)
+    assert np.array_equal(np.argmax(Wd, axis=1), perm) and Wd.sum() == n
+    X = (rng.uniform(0.05, 4.0, (48, n)) * rng.choice([-1, 1], (48, n))).astype(np.float32)
+    X = (X.view(np.uint32) & np.uint32(0xFFFFFFFC)).view(np.float32)   # 22 bits
+    got = gpu_matmul(t, w, X, n)
+    assert np.array_equal(got, X[:, perm])
+
+
+def test_split_gemm_q8_full_range(hip, oracle):
+    """Q8_0 with every int8 quant (-128 included), negative, subnormal and
+    large fp16 scales, against the oracle and the exact product."""
+    t, n_rows, n_cols, T = W.Q8_0, 160, 2048, 70
+    rng = np.random.default_rng(43)
+    q = rng.integers(-128, 128, size=(n_rows, n_cols)).astype(np.int8)
+    q[0, :256] = -128
+    q[1, :256] = 127
+    d = (rng.standard_normal((n_rows, n_cols // 32)) * 0.01).astype(np.float32)
+    d[2] = np.float32(3e-7)     # fp16 subnormals
+    d[3] = np.float32(-60000.0)
+    d[4, ::2] = 0.0
+    w = q8_blocks(q, d)
+    X = rng.standard_normal((T, n_cols)).astype(np.float32)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+    want = exact(oracle, t, w, X, n_rows)
+    for r in range(5):
+        scale = np.abs(want[:, r]).max()
+        assert np.abs(got[:, r] - want[:, r]).max() <= 1e-6 * scale, r
 
 
 def test_split_gemm_nt4_vs_oracle(hip, oracle):
