@@ -226,9 +226,11 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
         const int s8 = (tid >> 6) + 4 * rep;
         float w[8];
         if (a.q8) {
-            // Q8_0 block s8: values (2 + 8g + i) % 32 of even blocks, 8g + i of odd
+            // Q8_0 block s8: values (2 + 8s + i) % 32 of even blocks, 8s + i of
+            // odd, s = 2(g&1) + g/2
             const float* xr = xl + lt * RowF + 32 * s8;
-            const int o = (s8 & 1) ? 8 * g : 2 + 8 * g;
+            const int sg = ((g & 1) << 1) | (g >> 1);
+            const int o = (s8 & 1) ? 8 * sg : 2 + 8 * sg;
 #pragma unroll
             for (int i = 0; i < 8; ++i) w[i] = xr[(o + i) & 31];
         } else {
@@ -409,20 +411,24 @@ __device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
 // Q8_0 (src/kernels.cpp:364-373): 34-byte blocks of an fp16 scale d and 32
 // int8 quants, value d*q. Here a super-block is 8 blocks (272 bytes) and
 // step s of half h is block 4h + s. A block pair (68 bytes: d0 q0[32] d1
-// q1[32]) starts 4-byte aligned, so lane group g takes, as dwords:
-//   even block: q0[2+8g .. 9+8g] at pair bytes 4+8g (g = 3: q0[26..29], and
-//               q0[30], q0[31], q0[0], q0[1] from the dwords at 32 and 0),
-//   odd block:  q1[8g .. 8g+7] at pair bytes 36+8g,
-// and every lane d0 (dword 0) and d1 (dword 32, high half): six dwords a
-// pair. xsplit_kernel writes x in this order. q is exact in fp16 and so is
-// each product with an x part; d scales each block's sum (fp32) after its
-// matrix steps, lane-locally since an accumulator lane holds one row.
+// q1[32]; dword k = bytes 4k..4k+3) starts 4-byte aligned. Lane group g
+// loads dwords 4g+1 .. 4g+4 of each pair (16 bytes: the pair's bytes 4..67
+// over the four groups) and one dword of the half's scale dwords (0 and 8
+// of both pairs). Two lane swaps between the halves of the wave leave each
+// group two dwords of each block: group g, s(g) = 2(g&1) + g/2, holds
+//   even block: q0[2+8s .. 9+8s] (s = 3: q0[26..29], and q0[30], q0[31],
+//               q0[0], q0[1] from dwords 8 and 0),
+//   odd block:  q1[8s .. 8s+7],
+// and three more swaps give every lane the four scale dwords. xsplit_kernel
+// writes x in this order. q is exact in fp16 and so is each product with an
+// x part; d scales each block's sum (fp32) after its matrix steps,
+// lane-locally since an accumulator lane holds one row.
 __device__ __forceinline__ uint32_t ld_w1(const uint8_t* p) {
     return *reinterpret_cast<const uint32_t*>(p);
 }
-__device__ __forceinline__ uint2 ld_w2(const uint8_t* p) {   // 4-byte aligned
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    return make_uint2(q[0], q[1]);
+typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ u4a ld_w4(const uint8_t* p) {   // 4-byte aligned
+    return *reinterpret_cast<const u4a*>(p);
 }
 // 8 int8 quants (bytes of w0, then w1) as fp16: each byte offset by 128 and
 // placed under the exponent bits of 1024 by a byte permute, then 1152
@@ -579,30 +585,56 @@ void split_gemm_kernel(SplitParams p) {
         }
     };
 
-    // Q8_0: the six dwords of each block pair of half `half` of super-block sb
+    // Q8_0: half `half` of super-block sb as loaded (dwords 4g+1 .. 4g+4 of
+    // each pair, then the scale dword g); arranged by arrange_w8 before use
     auto load_w8 = [&](int sb, int half, uint32_t (&dst)[NT][12]) {
         const int64_t o = (int64_t)min(sb, n_sb - 1) * BB + 136 * half;
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
+        for (int j = 0; j < NT; ++j) {
+            const uint8_t* e = wbase[j] + woff[j] + o;
 #pragma unroll
             for (int pr = 0; pr < 2; ++pr) {
-                const uint8_t* e = wbase[j] + woff[j] + o + 68 * pr;
-                const uint2 l0 = ld_w2(e + 4 + 8 * g), l2 = ld_w2(e + 36 + 8 * g);
-                dst[j][6 * pr + 0] = l0.x;
-                dst[j][6 * pr + 1] = l0.y;
-                dst[j][6 * pr + 2] = ld_w1(e);
-                dst[j][6 * pr + 3] = l2.x;
-                dst[j][6 * pr + 4] = l2.y;
-                dst[j][6 * pr + 5] = ld_w1(e + 32);
+                const u4a v = ld_w4(e + 68 * pr + 4 + 16 * g);
+                dst[j][4 * pr + 0] = v[0];
+                dst[j][4 * pr + 1] = v[1];
+                dst[j][4 * pr + 2] = v[2];
+                dst[j][4 * pr + 3] = v[3];
             }
+            dst[j][8] = ld_w1(e + 68 * (g >> 1) + 32 * (g & 1));
+        }
+    };
+    // in place: per pair, dwords 0-1 the even block's operand words, 2-3 the
+    // odd block's; 8-11 the scale dwords 0 and 8 of pair 0, then of pair 1
+    auto arrange_w8 = [&](uint32_t (&w)[NT][12]) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                uint32_t* v = w[j] + 4 * pr;
+                const auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+                const auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+                v[0] = a[0];
+                v[2] = a[1];
+                v[1] = b[0];
+                v[3] = b[1];
+            }
+            const uint32_t x = w[j][8];
+            const auto c = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+            const auto e = __builtin_amdgcn_permlane32_swap(c[0], c[0], false, false);
+            const auto f = __builtin_amdgcn_permlane32_swap(c[1], c[1], false, false);
+            w[j][8] = e[0];
+            w[j][9] = f[0];
+            w[j][10] = e[1];
+            w[j][11] = f[1];
+        }
     };
     // the 4 blocks of one half from LDS buffer xb: each block's matrix steps
     // into P from zero, then sacc += d * P a step later (pipelined as
     // run_steps, with the block's d conversion and scaling among the VALU)
     v4f sacc[MT][NT];
-    auto run_q8 = [&](const u4* xb, const uint32_t (&wq)[NT][12]) {
+    auto run_q8 = [&](const u4* xb, uint32_t (&wq)[NT][12]) {
+        arrange_w8(wq);
         h8 A[2][MT][kParts], B[2][NT];
-        float dsc[kChunkSteps][NT];
         v4f P[2][MT][NT];
         auto read_a = [&](int s, h8 (&a)[MT][kParts]) {
 #pragma unroll
@@ -615,26 +647,27 @@ void split_gemm_kernel(SplitParams p) {
         auto decode = [&](int s, h8 (&b)[NT]) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
-                const uint32_t* w = wq[j] + 6 * (s >> 1);
+                const uint32_t* w = wq[j] + 4 * (s >> 1);
+                const uint32_t d0 = wq[j][8 + 2 * (s >> 1)], d8 = wq[j][9 + 2 * (s >> 1)];
                 if (s & 1) {
-                    b[j] = q8_operand(w[3], w[4]);
-                    dsc[s][j] = f16_hi(w[5]);
+                    b[j] = q8_operand(w[2], w[3]);
                 } else {
-                    const uint32_t w1 = g == 3 ? __builtin_amdgcn_perm(w[5], w[2], 0x03020504u)
-                                               : w[1];
+                    const uint32_t w1 = g == 3 ? __builtin_amdgcn_perm(d8, d0, 0x03020504u) : w[1];
                     b[j] = q8_operand(w[0], w1);
-                    dsc[s][j] = f16_lo(w[2]);
                 }
             }
         };
         auto scale_in = [&](int s) {
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
+            for (int j = 0; j < NT; ++j) {
+                const uint32_t dw = wq[j][8 + 2 * (s >> 1) + (s & 1)];
+                const float d = (s & 1) ? f16_hi(dw) : f16_lo(dw);
 #pragma unroll
-                for (int j = 0; j < NT; ++j)
+                for (int m = 0; m < MT; ++m)
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        sacc[m][j][v] = fmaf(dsc[s][j], P[s & 1][m][j][v], sacc[m][j][v]);
+                        sacc[m][j][v] = fmaf(d, P[s & 1][m][j][v], sacc[m][j][v]);
+            }
         };
         read_a(0, A[0]);
         decode(0, B[0]);
