@@ -122,7 +122,7 @@ struct XsplitArgs {
     float* xinv;
     const float* z;       // NORM, gated (src/ssm.cpp:322-340): x * w[c % w_len] * silu(z)
     int w_len;
-    int q8;               // Q8_0 operand order (else the K-quant order)
+    int order;            // operand order: 0 Q4_K / Q5_K, 1 Q8_0, 2 Q6_K
 };
 
 template <bool NORM, bool RESID>
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
     for (int rep = 0; rep < 2; ++rep) {
         const int s8 = (tid >> 6) + 4 * rep;
         float w[8];
-        if (a.q8) {
+        if (a.order == 1) {
             // Q8_0 block s8: values (2 + 8s + i) % 32 of even blocks, 8s + i of
             // odd, s = 2(g&1) + g/2
             const float* xr = xl + lt * RowF + 32 * s8;
@@ -233,6 +233,14 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
             const int o = (s8 & 1) ? 8 * sg : 2 + 8 * sg;
 #pragma unroll
             for (int i = 0; i < 8; ++i) w[i] = xr[(o + i) & 31];
+        } else if (a.order == 2) {
+            // Q6_K quarter s8 % 4 of half s8 / 4: values 8t .. 8t+7, t = (1, 3, 0, 2)[g]
+            const int t6 = (0x2031 >> (4 * g)) & 3;
+            const float* xr = xl + lt * RowF + 32 * s8 + 8 * t6;
+            const float4 va = *reinterpret_cast<const float4*>(xr);
+            const float4 vb = *reinterpret_cast<const float4*>(xr + 4);
+            w[0] = va.x; w[1] = va.y; w[2] = va.z; w[3] = va.w;
+            w[4] = vb.x; w[5] = vb.y; w[6] = vb.z; w[7] = vb.w;
         } else {
             const int c0 = 128 * (s8 >> 2) + 64 * (g >> 1) + 16 * (g & 1) + 4 * (s8 & 3);
             const float* xr = xl + lt * RowF + c0;
@@ -444,6 +452,34 @@ __device__ __forceinline__ h8 q8_operand(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(h8, make_uint4(as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)));
 }
 
+// Q6_K (src/kernels.cpp:427-458): 210-byte blocks of ql[128] (low 4 bits),
+// qh[64] (high 2 bits), 16 int8 scales and an fp16 d; value d*sc*(q - 32)
+// with sc per 16 values. Step s of half h is quarter s: values
+// 128h + 32s + l, l < 32, from ql[64h + l + 32(s&1)] (low nibble for s < 2,
+// high for s >= 2), bits 2s..2s+1 of qh[32h + l], scale sc[8h + 2s + l/16].
+// Lane group g takes l = 8t .. 8t+7, t = (1, 3, 0, 2)[g]: it loads 16 bytes
+// of the half's ql (ql[64h + 16g ..]), which two lane swaps across the wave's
+// halves turn into ql[64h + 8t ..] and ql[64h + 32 + 8t ..]; 8 bytes of qh
+// and the half's 8 scales. Blocks of odd index start 2 bytes past a 4-byte
+// boundary: their words are loaded from 2 bytes earlier and funnel-shifted.
+// sc*(q-32) reaches 4096, beyond fp16's exact integers (2048): it is split
+// as w_hi = fp16(sc*(q-32)) (rounded) and w_lo = sc*(q-32) - w_hi (exact,
+// |w_lo| <= 1), and each x part meets w_hi, the largest part w_lo as well.
+// 8 quants of one quarter: low nibbles (ns = 0) or high (ns = 4) of the ql
+// words, bits 2s..2s+1 of the qh words as bits 4-5, then q - 32 as fp16
+// pairs (exponent bits of 1024 placed by byte permutes, 1056 subtracted).
+__device__ __forceinline__ void q6_quants(uint32_t l0, uint32_t l1, uint32_t h0, uint32_t h1,
+                                          int ns, int s, h2 (&q)[4]) {
+    constexpr uint32_t E = 0x64646464u, LO = 0x04010400u, HI = 0x04030402u;
+    const h2 off{(_Float16)-1056.f, (_Float16)-1056.f};
+    const uint32_t u0 = ((l0 >> ns) & 0x0F0F0F0Fu) | (((h0 >> (2 * s)) << 4) & 0x30303030u);
+    const uint32_t u1 = ((l1 >> ns) & 0x0F0F0F0Fu) | (((h1 >> (2 * s)) << 4) & 0x30303030u);
+    q[0] = as_h2(__builtin_amdgcn_perm(E, u0, LO)) + off;
+    q[1] = as_h2(__builtin_amdgcn_perm(E, u0, HI)) + off;
+    q[2] = as_h2(__builtin_amdgcn_perm(E, u1, LO)) + off;
+    q[3] = as_h2(__builtin_amdgcn_perm(E, u1, HI)) + off;
+}
+
 // NT matrix tiles of 16 rows a wave; a workgroup covers 4 x 16NT rows. In
 // the gate/up form (EPI >= 0, NT = 2) tile 0 holds 16 rows of the gate
 // matrix and tile 1 the same 16 rows of the up matrix, so each lane ends
@@ -454,9 +490,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 4 ? 1
 void split_gemm_kernel(SplitParams p) {
     constexpr bool Q5 = TYPE == AERO_DTYPE_Q5_K;
     constexpr bool Q8 = TYPE == AERO_DTYPE_Q8_0;
+    constexpr bool Q6 = TYPE == AERO_DTYPE_Q6_K;
     constexpr bool GU = EPI != kEpiPlain;
     static_assert(!GU || NT == 2, "gate/up pairs one gate and one up tile");
-    constexpr int BB = Q8 ? 272 : (Q5 ? 176 : 144);   // bytes a super-block
+    constexpr int BB = Q8 ? 272 : (Q6 ? 210 : (Q5 ? 176 : 144));   // bytes a super-block
     constexpr int QOFF = Q5 ? 48 : 16;          // quants within the block
     constexpr int kRowsWave = GU ? 16 : 16 * NT;
     constexpr int MT = kTokTile / 16;           // matrix tiles over tokens (2)
@@ -700,7 +737,167 @@ void split_gemm_kernel(SplitParams p) {
         scale_in(kChunkSteps - 1);
     };
 
-    if constexpr (Q8) {
+    // Q6_K: half `half` of super-block sb as loaded: 4-byte aligned words from
+    // sh = 2 (odd blocks) or 0 bytes before each field: ql 16 bytes (5 words),
+    // qh 8 (3 words), the half's 8 scales (3 words)
+    typedef uint32_t u3a __attribute__((ext_vector_type(3), aligned(4)));
+    auto load_w6 = [&](int sb, int half, uint32_t (&dst)[NT][11]) {
+        const int sbc = min(sb, n_sb - 1);
+        const int64_t o = (int64_t)sbc * BB - 2 * (sbc & 1);
+        const int t6 = (0x2031 >> (4 * g)) & 3;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const uint8_t* e = wbase[j] + woff[j] + o;
+            const u4a v = ld_w4(e + 64 * half + 16 * g);
+            const u3a h = *reinterpret_cast<const u3a*>(e + 128 + 32 * half + 8 * t6);
+            const u3a c = *reinterpret_cast<const u3a*>(e + 192 + 8 * half);
+            dst[j][0] = v[0];
+            dst[j][1] = v[1];
+            dst[j][2] = v[2];
+            dst[j][3] = v[3];
+            dst[j][4] = ld_w1(e + 64 * half + 16 * g + 16);
+            dst[j][5] = h[0];
+            dst[j][6] = h[1];
+            dst[j][7] = h[2];
+            dst[j][8] = c[0];
+            dst[j][9] = c[1];
+            dst[j][10] = c[2];
+        }
+    };
+    // the 4 quarters of one half from LDS buffer xb into part (raw words wq
+    // of a block starting sh bytes past a 4-byte boundary); pipelined as
+    // run_steps, three matrix steps a tile and quarter
+    auto run_q6 = [&](const u4* xb, const uint32_t (&wq)[NT][11], int sh) {
+        // ql: (lq[2], lq[3]) = ql[.. + 8t ..], (lq[0], lq[1]) = ql[.. + 32 + 8t ..]
+        uint32_t lq[NT][4], hq6[NT][2], sq[NT][2];
+        const int t6 = (0x2031 >> (4 * g)) & 3;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            uint32_t f[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) f[i] = __builtin_amdgcn_alignbyte(wq[j][i + 1], wq[j][i], sh);
+            const auto a = __builtin_amdgcn_permlane32_swap(f[2], f[0], false, false);
+            const auto b = __builtin_amdgcn_permlane32_swap(f[3], f[1], false, false);
+            lq[j][2] = a[0];
+            lq[j][0] = a[1];
+            lq[j][3] = b[0];
+            lq[j][1] = b[1];
+            hq6[j][0] = __builtin_amdgcn_alignbyte(wq[j][6], wq[j][5], sh);
+            hq6[j][1] = __builtin_amdgcn_alignbyte(wq[j][7], wq[j][6], sh);
+            sq[j][0] = __builtin_amdgcn_alignbyte(wq[j][9], wq[j][8], sh) ^ 0x80808080u;
+            sq[j][1] = __builtin_amdgcn_alignbyte(wq[j][10], wq[j][9], sh) ^ 0x80808080u;
+        }
+        h8 A[2][MT][kParts], Bh[2][NT], Bl[2][NT];
+        auto read_a = [&](int s, h8 (&a)[MT][kParts]) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int pp = 0; pp < kParts; ++pp)
+                    a[m][pp] = __builtin_bit_cast(
+                        h8, xb[((m * kChunkSteps + s) * kParts + pp) * 64 + l]);
+        };
+        auto decode = [&](int s, h8 (&bh)[NT], h8 (&bl)[NT]) {
+            // the lane's scale sc[8h + 2s + t/2] as a packed fp16 pair
+            const uint32_t k = 2 * (s & 1) + (t6 >> 1);
+            const uint32_t sel = k | (4u << 8) | (k << 16) | (4u << 24);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                h2 q[4];
+                q6_quants(lq[j][(s & 1) ? 0 : 2], lq[j][(s & 1) ? 1 : 3], hq6[j][0], hq6[j][1],
+                          (s >> 1) * 4, s, q);
+                const h2 sc = as_h2(__builtin_amdgcn_perm(0x64646464u, sq[j][s >> 1], sel)) +
+                              h2{(_Float16)-1152.f, (_Float16)-1152.f};
+                h2 hi[4], lo[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    hi[i] = q[i] * sc;
+                    lo[i] = __builtin_elementwise_fma(q[i], sc, -hi[i]);
+                }
+                bh[j] = __builtin_bit_cast(h8, make_uint4(as_u32(hi[0]), as_u32(hi[1]),
+                                                          as_u32(hi[2]), as_u32(hi[3])));
+                bl[j] = __builtin_bit_cast(h8, make_uint4(as_u32(lo[0]), as_u32(lo[1]),
+                                                          as_u32(lo[2]), as_u32(lo[3])));
+            }
+        };
+        read_a(0, A[0]);
+        decode(0, Bh[0], Bl[0]);
+#pragma unroll
+        for (int s = 0; s < kChunkSteps; ++s) {
+            if (s + 1 < kChunkSteps) {
+                read_a(s + 1, A[(s + 1) & 1]);
+                decode(s + 1, Bh[(s + 1) & 1], Bl[(s + 1) & 1]);
+            }
+            // small parts first: x's lower parts with w_hi, x's largest with
+            // w_lo, then with w_hi
+#pragma unroll
+            for (int pp = kParts - 1; pp >= 1; --pp)
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j)
+                        part[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            A[s & 1][m][pp], Bh[s & 1][j], part[m][j], 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    part[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        A[s & 1][m][0], Bl[s & 1][j], part[m][j], 0, 0, 0);
+                    part[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        A[s & 1][m][0], Bh[s & 1][j], part[m][j], 0, 0, 0);
+                }
+            constexpr int kMfma = (kParts + 1) * MT * NT, kReads = MT * kParts;
+#pragma unroll
+            for (int i = 0; i < kMfma; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix step
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+                if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    if constexpr (Q6) {
+        uint32_t wa[NT][11];
+        xst.load(2 * sb0);
+        load_w6(sb0, 0, wa);
+        xst.store(xs[0], ss[sb0 & 1], si[sb0 & 1], tid);
+        xst.load(2 * sb0 + 1);
+        __syncthreads();
+        for (int sb = sb0; sb < sb1; ++sb) {
+            uint32_t wb[NT][11];
+            load_w6(sb, 1, wb);
+            const int sh = 2 * (sb & 1);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int j = 0; j < NT; ++j) part[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            run_q6(xs[0], wa, sh);
+            xst.store(xs[1], nullptr, nullptr, tid);
+            xst.load(2 * sb + 2);
+            __syncthreads();
+            load_w6(sb + 1, 0, wa);   // the next super-block's first half (clamped)
+            run_q6(xs[1], wb, sh);
+            // acc += inv * d * part: d in the second half's scale words (block
+            // bytes 208-209: the low half of the last word, or its high half
+            // when the words start 2 bytes early)
+            const float* ip = si[sb & 1];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const float d = sh ? f16_hi(wb[j][10]) : f16_lo(wb[j][10]);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const v4f inv = *reinterpret_cast<const v4f*>(ip + 16 * m + 4 * g);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[m][j][v] = fmaf(inv[v], d * part[m][j][v], acc[m][j][v]);
+                }
+            }
+            xst.store(xs[0], ss[(sb + 1) & 1], si[(sb + 1) & 1], tid);
+            xst.load(2 * sb + 3);
+            __syncthreads();
+        }
+    } else if constexpr (Q8) {
         uint32_t wa[NT][12];
         xst.load(2 * sb0);
         load_w8(sb0, 0, wa);
@@ -984,7 +1181,9 @@ int64_t pad_tokens(int64_t n_tok) { return (n_tok + kTokTile - 1) / kTokTile * k
 // The shape part of whether the split path applies (types with it, whole
 // super-blocks a row, grid limits); alignment is checked at the call.
 bool split_shape_ok(int dtype, int64_t n_cols, int64_t n_tok) {
-    return (dtype == AERO_DTYPE_Q4_K || dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q8_0) &&
+    // Q6_K: 210-byte blocks, rows 16-byte aligned from 8 blocks
+    return (dtype == AERO_DTYPE_Q4_K || dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q8_0 ||
+            (dtype == AERO_DTYPE_Q6_K && n_cols % 2048 == 0)) &&
            n_cols > 0 &&
            n_cols % 256 == 0 && n_cols / 256 <= 65535 && n_tok > 0 &&
            pad_tokens(n_tok) / kTokTile <= 65535 && pad_tokens(n_tok) <= 0x7fffffff;
@@ -1077,7 +1276,7 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     const SplitWs w = split_ws(j.ws, tp, j.n_cols);
     XsplitArgs a{j.x, j.d, j.x_out, j.norm_w, w.ssq, norm && (j.norm & AERO_NORM_UNIT_OFFSET),
                  (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv, j.z, (int)j.w_len,
-                 j.dtype == AERO_DTYPE_Q8_0};
+                 j.dtype == AERO_DTYPE_Q8_0 ? 1 : (j.dtype == AERO_DTYPE_Q6_K ? 2 : 0)};
     const bool ok = norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
                                 : launch_xsplit<true, false>(a, tp, s))
                          : (j.d ? launch_xsplit<false, true>(a, tp, s)
@@ -1091,6 +1290,7 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     const int epi = gu ? j.act : kEpiPlain;
     void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi)
                : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi)
+               : j.dtype == AERO_DTYPE_Q6_K ? pick_split_gemm<AERO_DTYPE_Q6_K>(nt, epi)
                                             : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi);
     if (kp == nullptr) {
         set_error("split GEMM: unknown activation %d", j.act);

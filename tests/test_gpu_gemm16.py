@@ -1,7 +1,7 @@
 """GPU parity: the split-x fp16 matrix-core GEMM (aero_hip_matmul with a
-workspace, Q4_K / Q5_K / Q8_0, 32 or more tokens) against the oracle's
-restatement of the reference's matmul (src/kernels.cpp:337-404,364-373,520-538)
-and against the exact product.
+workspace, Q4_K / Q5_K / Q8_0 / Q6_K, 32 or more tokens) against the oracle's
+restatement of the reference's matmul (src/kernels.cpp:337-404,364-373,427-458,
+520-538) and against the exact product.
 
 Tolerances: 1e-5 relative to the output's scale against the oracle (the
 reference's RTOL for fp32 ops, tests/test_transformer_native.py:34-37). Each
@@ -49,7 +49,9 @@ def test_workspace_sizes(hip):
         assert L.aero_hip_matmul_workspace(t, 4096, 512) >= 512 * 4096 * 4   # 2 fp16 parts
         assert L.aero_hip_matmul_workspace(t, 4096, 33) >= 64 * 4096 * 4  # padded to 32s
         assert L.aero_hip_matmul_workspace(t, 100, 64) == 0                # not whole blocks
-    for t in (W.Q6_K, W.IQ4_XS, W.F32):
+    assert L.aero_hip_matmul_workspace(W.Q6_K, 4096, 512) >= 512 * 4096 * 4
+    assert L.aero_hip_matmul_workspace(W.Q6_K, 5120, 512) == 0   # rows not 16-byte aligned
+    for t in (W.IQ4_XS, W.F32):
         assert L.aero_hip_matmul_workspace(t, 4096, 512) == 0
 
 
@@ -196,6 +198,87 @@ def test_split_gemm_q8_full_range(hip, oracle):
     for r in range(5):
         scale = np.abs(want[:, r]).max()
         assert np.abs(got[:, r] - want[:, r]).max() <= 1e-6 * scale, r
+
+
+@pytest.mark.parametrize("n_rows,n_cols,n_tok", [
+    (100, 2048, 40), (257, 4096, 100), (64, 14336, 64), (130, 6144, 33),
+])
+def test_split_gemm_q6k_vs_oracle(hip, oracle, n_rows, n_cols, n_tok):
+    """Q6_K rows of 8 or more blocks (16-byte aligned): blocks at odd indices
+    start 2 bytes past a 4-byte boundary."""
+    t = W.Q6_K
+    rng = np.random.default_rng(n_rows + n_cols + n_tok)
+    w = table(t, n_rows, n_cols, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    print(f"split gemm Q6_K rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+    assert rel_to_scale(got, gpu_matmul(t, w, X, n_rows, split=False)) <= RTOL
+
+
+def q6k_blocks(q, sc, d):
+    """Q6_K rows from 6-bit quants q [rows, cols] (0..63), int8 scales sc
+    [rows, cols/16] and fp16 d [rows, cols/256], in the layout of
+    src/kernels.cpp:427-458."""
+    rows, cols = q.shape
+    nb = cols // 256
+    blk = np.zeros((rows, nb, 210), np.uint8)
+    v = np.arange(256)
+    n, r = v // 128, v % 128
+    Q, l = r // 32, r % 32
+    qli = 64 * n + l + 32 * (Q & 1)
+    qhi = 128 + 32 * n + l
+    qb = q.reshape(rows, nb, 256).astype(np.uint8)
+    for i in range(256):
+        lo = qb[:, :, i] & 15
+        blk[:, :, qli[i]] |= (lo << (4 * (Q[i] >> 1))).astype(np.uint8)
+        blk[:, :, qhi[i]] |= ((qb[:, :, i] >> 4) << (2 * Q[i])).astype(np.uint8)
+    blk[:, :, 192:208] = sc.astype(np.int8).view(np.uint8).reshape(rows, nb, 16)
+    blk[:, :, 208:210] = np.ascontiguousarray(d.astype(np.float16)).view(np.uint8).reshape(
+        rows, nb, 2)
+    return blk.reshape(-1)
+
+
+def test_split_gemm_q6k_identity(hip, oracle):
+    """Q6_K rows that pick one column each (d = 1, scales 1, q - 32 = 1
+    there, 0 elsewhere), every column of 2048 once: y equals x value for
+    value (x of 22 significant bits within 2^7 of their super-block's
+    largest). Each quarter, lane group and block parity reads other words."""
+    t, n = W.Q6_K, 2048
+    rng = np.random.default_rng(47)
+    perm = rng.permutation(n)
+    q = np.full((n, n), 32, np.int64)
+    q[np.arange(n), perm] = 33
+    w = q6k_blocks(q, np.ones((n, n // 16)), np.ones((n, n // 256), np.float32))
+    Wd = oracle.dequant(t, w, n * n).reshape(n, n)
+    assert np.array_equal(np.argmax(Wd, axis=1), perm) and Wd.sum() == n
+    X = (rng.uniform(0.05, 4.0, (40, n)) * rng.choice([-1, 1], (40, n))).astype(np.float32)
+    X = (X.view(np.uint32) & np.uint32(0xFFFFFFFC)).view(np.float32)
+    got = gpu_matmul(t, w, X, n)
+    assert np.array_equal(got, X[:, perm])
+
+
+def test_split_gemm_q6k_full_range(hip, oracle):
+    """Q6_K with every 6-bit quant and scales -128..127 (sc*(q-32) up to
+    4096, beyond fp16's exact integers), large, subnormal and negative d,
+    against the oracle and the exact product."""
+    t, n_rows, n_cols, T = W.Q6_K, 96, 4096, 48
+    rng = np.random.default_rng(53)
+    q = rng.integers(0, 64, size=(n_rows, n_cols))
+    sc = rng.integers(-128, 128, size=(n_rows, n_cols // 16))
+    q[0], sc[0] = 0, -128            # (q - 32) * sc = 4096
+    q[1], sc[1] = 63, -127           # -3937: odd beyond 2048
+    d = (rng.standard_normal((n_rows, n_cols // 256)) * 0.01).astype(np.float32)
+    d[2] = np.float32(3e-7)
+    d[3] = np.float32(-30000.0)
+    w = q6k_blocks(q, sc, d)
+    X = rng.standard_normal((T, n_cols)).astype(np.float32)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+    want = exact(oracle, t, w, X, n_rows)
+    for r in range(n_rows):
+        scale = np.abs(want[:, r]).max()
+        assert np.abs(got[:, r] - want[:, r]).max() <= 2e-6 * scale, r
 
 
 def test_split_gemm_nt4_vs_oracle(hip, oracle):
