@@ -122,7 +122,7 @@ struct XsplitArgs {
     float* xinv;
     const float* z;       // NORM, gated (src/ssm.cpp:322-340): x * w[c % w_len] * silu(z)
     int w_len;
-    int order;            // operand order: 0 Q4_K / Q5_K, 1 Q8_0, 2 Q6_K
+    int order;            // operand order: 0 Q4_K / Q5_K, 1 Q8_0, 2 Q6_K, 3 IQ4_XS
 };
 
 template <bool NORM, bool RESID>
@@ -233,6 +233,13 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
             const int o = (s8 & 1) ? 8 * sg : 2 + 8 * sg;
 #pragma unroll
             for (int i = 0; i < 8; ++i) w[i] = xr[(o + i) & 31];
+        } else if (a.order == 3) {
+            // IQ4_XS sub-block s8: values 4k + i and 16 + 4k + i, k = 3 - g
+            const float* xr = xl + lt * RowF + 32 * s8 + 4 * (3 - g);
+            const float4 va = *reinterpret_cast<const float4*>(xr);
+            const float4 vb = *reinterpret_cast<const float4*>(xr + 16);
+            w[0] = va.x; w[1] = va.y; w[2] = va.z; w[3] = va.w;
+            w[4] = vb.x; w[5] = vb.y; w[6] = vb.z; w[7] = vb.w;
         } else if (a.order == 2) {
             // Q6_K quarter s8 % 4 of half s8 / 4: values 8t .. 8t+7, t = (1, 3, 0, 2)[g]
             const int t6 = (0x2031 >> (4 * g)) & 3;
@@ -480,6 +487,39 @@ __device__ __forceinline__ void q6_quants(uint32_t l0, uint32_t l1, uint32_t h0,
     q[3] = as_h2(__builtin_amdgcn_perm(E, u1, HI)) + off;
 }
 
+// IQ4_XS (src/kernels.cpp:405-425): 136-byte blocks of an fp16 d, 2+6 bits
+// of scale ls a 32-value sub-block (scales_h, scales_l) and 128 quant bytes,
+// value d*(ls - 32)*codebook[q]. A step is one sub-block; lane group g takes
+// quant dword k = 3 - g of it: values 4k .. 4k+3 (low nibbles) and 16 + 4k ..
+// +3 (high). Each lane loads 16 bytes (a whole sub-block) and a 4 x 4
+// transpose by lane swaps hands it its dword of each. The codebook (int8,
+// offset by 128) is looked up by byte permutes from two 8-entry halves,
+// then made fp16 as for Q8_0; d*(ls - 32) scales each sub-block's sums.
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t u) {   // 4 nibbles in bytes
+    constexpr uint32_t T0 = 0xBFAD9881u ^ 0x80808080u, T1 = 0xF6EADDCFu ^ 0x80808080u;
+    constexpr uint32_t T2 = 0x26190D01u ^ 0x80808080u, T3 = 0x71594535u ^ 0x80808080u;
+    const uint32_t sel = u & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    const uint32_t m = ((u >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+__device__ __forceinline__ h8 iq4_operand(uint32_t w) {
+    constexpr uint32_t E = 0x64646464u, LO = 0x04010400u, HI = 0x04030402u;
+    const h2 off{(_Float16)-1152.f, (_Float16)-1152.f};
+    const uint32_t a = iq4_lookup(w & 0x0F0F0F0Fu), b = iq4_lookup((w >> 4) & 0x0F0F0F0Fu);
+    const h2 a0 = as_h2(__builtin_amdgcn_perm(E, a, LO)) + off;
+    const h2 a1 = as_h2(__builtin_amdgcn_perm(E, a, HI)) + off;
+    const h2 a2 = as_h2(__builtin_amdgcn_perm(E, b, LO)) + off;
+    const h2 a3 = as_h2(__builtin_amdgcn_perm(E, b, HI)) + off;
+    return __builtin_bit_cast(h8, make_uint4(as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)));
+}
+// d*(ls - 32) of sub-block ib from the header words h0 (d, scales_h) and h1
+// (scales_l), as the reference forms dl (src/kernels.cpp:413-415)
+__device__ __forceinline__ float iq4_scale(uint32_t h0, uint32_t h1, int ib) {
+    const int ls = (int)(((h1 >> (4 * ib)) & 0xFu) | (((h0 >> (16 + 2 * ib)) & 3u) << 4));
+    return f16_lo(h0) * (float)(ls - 32);
+}
+
 // NT matrix tiles of 16 rows a wave; a workgroup covers 4 x 16NT rows. In
 // the gate/up form (EPI >= 0, NT = 2) tile 0 holds 16 rows of the gate
 // matrix and tile 1 the same 16 rows of the up matrix, so each lane ends
@@ -491,9 +531,10 @@ void split_gemm_kernel(SplitParams p) {
     constexpr bool Q5 = TYPE == AERO_DTYPE_Q5_K;
     constexpr bool Q8 = TYPE == AERO_DTYPE_Q8_0;
     constexpr bool Q6 = TYPE == AERO_DTYPE_Q6_K;
+    constexpr bool IQ4 = TYPE == AERO_DTYPE_IQ4_XS;
     constexpr bool GU = EPI != kEpiPlain;
     static_assert(!GU || NT == 2, "gate/up pairs one gate and one up tile");
-    constexpr int BB = Q8 ? 272 : (Q6 ? 210 : (Q5 ? 176 : 144));   // bytes a super-block
+    constexpr int BB = Q8 ? 272 : (Q6 ? 210 : (Q5 ? 176 : (IQ4 ? 136 : 144)));   // bytes a super-block
     constexpr int QOFF = Q5 ? 48 : 16;          // quants within the block
     constexpr int kRowsWave = GU ? 16 : 16 * NT;
     constexpr int MT = kTokTile / 16;           // matrix tiles over tokens (2)
@@ -665,12 +706,50 @@ void split_gemm_kernel(SplitParams p) {
             w[j][11] = f[1];
         }
     };
+    // IQ4_XS: half `half` of super-block sb: dwords 0-3 the 16 quant bytes
+    // 64 half + 16 g of the block's qs (sub-block 4 half + g), 4-5 its header
+    auto load_iq4 = [&](int sb, int half, uint32_t (&dst)[NT][12]) {
+        const int64_t o = (int64_t)min(sb, n_sb - 1) * BB;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const uint8_t* e = wbase[j] + woff[j] + o;
+            const u4a v = ld_w4(e + 8 + 64 * half + 16 * g);
+            const uint2 h = ld64(e);
+            dst[j][0] = v[0];
+            dst[j][1] = v[1];
+            dst[j][2] = v[2];
+            dst[j][3] = v[3];
+            dst[j][4] = h.x;
+            dst[j][5] = h.y;
+        }
+    };
+    auto load_wb = [&](int sb, int half, uint32_t (&dst)[NT][12]) {
+        if constexpr (IQ4) load_iq4(sb, half, dst);
+        else load_w8(sb, half, dst);
+    };
+    // in place, a 4 x 4 transpose over the lane groups: dword 3 - s becomes
+    // quant dword 3 - g of sub-block 4 half + s
+    auto arrange_iq4 = [&](uint32_t (&w)[NT][12]) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            uint32_t* v = w[j];
+            const auto a = __builtin_amdgcn_permlane32_swap(v[2], v[0], false, false);
+            const auto b = __builtin_amdgcn_permlane32_swap(v[3], v[1], false, false);
+            const auto c = __builtin_amdgcn_permlane16_swap(b[1], a[1], false, false);
+            const auto e = __builtin_amdgcn_permlane16_swap(b[0], a[0], false, false);
+            v[1] = c[0];
+            v[0] = c[1];
+            v[3] = e[0];
+            v[2] = e[1];
+        }
+    };
     // the 4 blocks of one half from LDS buffer xb: each block's matrix steps
     // into P from zero, then sacc += d * P a step later (pipelined as
     // run_steps, with the block's d conversion and scaling among the VALU)
     v4f sacc[MT][NT];
-    auto run_q8 = [&](const u4* xb, uint32_t (&wq)[NT][12]) {
-        arrange_w8(wq);
+    auto run_q8 = [&](const u4* xb, uint32_t (&wq)[NT][12], int half) {
+        if constexpr (IQ4) arrange_iq4(wq);
+        else arrange_w8(wq);
         h8 A[2][MT][kParts], B[2][NT];
         v4f P[2][MT][NT];
         auto read_a = [&](int s, h8 (&a)[MT][kParts]) {
@@ -684,6 +763,10 @@ void split_gemm_kernel(SplitParams p) {
         auto decode = [&](int s, h8 (&b)[NT]) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
+                if constexpr (IQ4) {
+                    b[j] = iq4_operand(wq[j][3 - s]);
+                    continue;
+                }
                 const uint32_t* w = wq[j] + 4 * (s >> 1);
                 const uint32_t d0 = wq[j][8 + 2 * (s >> 1)], d8 = wq[j][9 + 2 * (s >> 1)];
                 if (s & 1) {
@@ -697,8 +780,13 @@ void split_gemm_kernel(SplitParams p) {
         auto scale_in = [&](int s) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
-                const uint32_t dw = wq[j][8 + 2 * (s >> 1) + (s & 1)];
-                const float d = (s & 1) ? f16_hi(dw) : f16_lo(dw);
+                float d;
+                if constexpr (IQ4) {
+                    d = iq4_scale(wq[j][4], wq[j][5], 4 * half + s);
+                } else {
+                    const uint32_t dw = wq[j][8 + 2 * (s >> 1) + (s & 1)];
+                    d = (s & 1) ? f16_hi(dw) : f16_lo(dw);
+                }
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -897,26 +985,26 @@ void split_gemm_kernel(SplitParams p) {
             xst.load(2 * sb + 3);
             __syncthreads();
         }
-    } else if constexpr (Q8) {
+    } else if constexpr (Q8 || IQ4) {
         uint32_t wa[NT][12];
         xst.load(2 * sb0);
-        load_w8(sb0, 0, wa);
+        load_wb(sb0, 0, wa);
         xst.store(xs[0], ss[sb0 & 1], si[sb0 & 1], tid);
         xst.load(2 * sb0 + 1);
         __syncthreads();
         for (int sb = sb0; sb < sb1; ++sb) {
             uint32_t wb[NT][12];
-            load_w8(sb, 1, wb);
+            load_wb(sb, 1, wb);
 #pragma unroll
             for (int m = 0; m < MT; ++m)
 #pragma unroll
                 for (int j = 0; j < NT; ++j) sacc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
-            run_q8(xs[0], wa);
+            run_q8(xs[0], wa, 0);
             xst.store(xs[1], nullptr, nullptr, tid);
             xst.load(2 * sb + 2);
             __syncthreads();
-            load_w8(sb + 1, 0, wa);   // the next super-block's first half (clamped)
-            run_q8(xs[1], wb);
+            load_wb(sb + 1, 0, wa);   // the next super-block's first half (clamped)
+            run_q8(xs[1], wb, 1);
             // acc += inv * sacc, inv the token's inverse scale of this super-block
             const float* ip = si[sb & 1];
 #pragma unroll
@@ -1181,9 +1269,11 @@ int64_t pad_tokens(int64_t n_tok) { return (n_tok + kTokTile - 1) / kTokTile * k
 // The shape part of whether the split path applies (types with it, whole
 // super-blocks a row, grid limits); alignment is checked at the call.
 bool split_shape_ok(int dtype, int64_t n_cols, int64_t n_tok) {
-    // Q6_K: 210-byte blocks, rows 16-byte aligned from 8 blocks
+    // Q6_K: 210-byte blocks, rows 16-byte aligned from 8 blocks; IQ4_XS: 136
+    // bytes, from 2
     return (dtype == AERO_DTYPE_Q4_K || dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q8_0 ||
-            (dtype == AERO_DTYPE_Q6_K && n_cols % 2048 == 0)) &&
+            (dtype == AERO_DTYPE_Q6_K && n_cols % 2048 == 0) ||
+            (dtype == AERO_DTYPE_IQ4_XS && n_cols % 512 == 0)) &&
            n_cols > 0 &&
            n_cols % 256 == 0 && n_cols / 256 <= 65535 && n_tok > 0 &&
            pad_tokens(n_tok) / kTokTile <= 65535 && pad_tokens(n_tok) <= 0x7fffffff;
@@ -1276,7 +1366,9 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     const SplitWs w = split_ws(j.ws, tp, j.n_cols);
     XsplitArgs a{j.x, j.d, j.x_out, j.norm_w, w.ssq, norm && (j.norm & AERO_NORM_UNIT_OFFSET),
                  (int)j.n_tok, (int)j.n_cols, w.xp, w.xsum, w.xinv, j.z, (int)j.w_len,
-                 j.dtype == AERO_DTYPE_Q8_0 ? 1 : (j.dtype == AERO_DTYPE_Q6_K ? 2 : 0)};
+                 j.dtype == AERO_DTYPE_Q8_0   ? 1
+                 : j.dtype == AERO_DTYPE_Q6_K ? 2
+                 : j.dtype == AERO_DTYPE_IQ4_XS ? 3 : 0};
     const bool ok = norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
                                 : launch_xsplit<true, false>(a, tp, s))
                          : (j.d ? launch_xsplit<false, true>(a, tp, s)
@@ -1291,6 +1383,7 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi)
                : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi)
                : j.dtype == AERO_DTYPE_Q6_K ? pick_split_gemm<AERO_DTYPE_Q6_K>(nt, epi)
+               : j.dtype == AERO_DTYPE_IQ4_XS ? pick_split_gemm<AERO_DTYPE_IQ4_XS>(nt, epi)
                                             : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi);
     if (kp == nullptr) {
         set_error("split GEMM: unknown activation %d", j.act);

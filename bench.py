@@ -922,6 +922,7 @@ GEMM_CASES = [
     ("attn_q_4096x4096", 12, 4096, 4096, 512), ("ffn_gate_14336x4096", 12, 14336, 4096, 512),
     ("ffn_down_4096x14336", 12, 4096, 14336, 512), ("q8_0_14336x4096", 8, 14336, 4096, 512),
     ("q6_k_14336x4096", 14, 14336, 4096, 512), ("q6_k_4096x14336", 14, 4096, 14336, 512),
+    ("iq4_xs_14336x4096", 23, 14336, 4096, 512),
     ("ffn_gate_14336x4096_t64", 12, 14336, 4096, 64),
     ("q8_0_4096x4096", 8, 4096, 4096, 512), ("q8_0_4096x14336", 8, 4096, 14336, 512),
     ("q8_0_14336x4096_t8", 8, 14336, 4096, 8), ("q8_0_14336x4096_t16", 8, 14336, 4096, 16),
@@ -966,10 +967,10 @@ def gemm(a):
         X = DA.from_numpy(rng.standard_normal((n_tok, n_cols)).astype(np.float32))
         Y = DA.empty((n_tok, n_rows))
         stream = Stream()
-        # Q4_K / Q5_K / Q8_0 / Q6_K: the split-x fp16 GEMM (the default), then the call
+        # Q4_K / Q5_K / Q8_0 / Q6_K / IQ4_XS: the split-x fp16 GEMM (the default), then the call
         # without a workspace: the fp32 GEMM from 32 tokens, the GEMV below
         plain = "fp32" if n_tok >= 32 else "gemv"
-        paths = ["split_fp16", plain] if t in (W.Q4_K, W.Q5_K, W.Q8_0, W.Q6_K) else [plain]
+        paths = ["split_fp16", plain] if t in (W.Q4_K, W.Q5_K, W.Q8_0, W.Q6_K, W.IQ4_XS) else [plain]
         for path in paths:
             split = path == "split_fp16"
             for w in ws:

@@ -1,7 +1,7 @@
 """GPU parity: the split-x fp16 matrix-core GEMM (aero_hip_matmul with a
-workspace, Q4_K / Q5_K / Q8_0 / Q6_K, 32 or more tokens) against the oracle's
-restatement of the reference's matmul (src/kernels.cpp:337-404,364-373,427-458,
-520-538) and against the exact product.
+workspace, Q4_K / Q5_K / Q8_0 / Q6_K / IQ4_XS, 32 or more tokens) against the
+oracle's restatement of the reference's matmul (src/kernels.cpp:337-458,520-538)
+and against the exact product.
 
 Tolerances: 1e-5 relative to the output's scale against the oracle (the
 reference's RTOL for fp32 ops, tests/test_transformer_native.py:34-37). Each
@@ -51,8 +51,9 @@ def test_workspace_sizes(hip):
         assert L.aero_hip_matmul_workspace(t, 100, 64) == 0                # not whole blocks
     assert L.aero_hip_matmul_workspace(W.Q6_K, 4096, 512) >= 512 * 4096 * 4
     assert L.aero_hip_matmul_workspace(W.Q6_K, 5120, 512) == 0   # rows not 16-byte aligned
-    for t in (W.IQ4_XS, W.F32):
-        assert L.aero_hip_matmul_workspace(t, 4096, 512) == 0
+    assert L.aero_hip_matmul_workspace(W.IQ4_XS, 4096, 512) >= 512 * 4096 * 4
+    assert L.aero_hip_matmul_workspace(W.IQ4_XS, 768, 512) == 0   # odd block count
+    assert L.aero_hip_matmul_workspace(W.F32, 4096, 512) == 0
 
 
 @pytest.mark.parametrize("t", KTYPES)
@@ -279,6 +280,47 @@ def test_split_gemm_q6k_full_range(hip, oracle):
     for r in range(n_rows):
         scale = np.abs(want[:, r]).max()
         assert np.abs(got[:, r] - want[:, r]).max() <= 2e-6 * scale, r
+
+
+@pytest.mark.parametrize("n_rows,n_cols,n_tok", [
+    (100, 512, 40), (257, 4096, 100), (64, 14336, 64), (130, 1536, 33),
+])
+def test_split_gemm_iq4xs_vs_oracle(hip, oracle, n_rows, n_cols, n_tok):
+    """IQ4_XS rows of an even block count (16-byte aligned)."""
+    t = W.IQ4_XS
+    rng = np.random.default_rng(3 * n_rows + n_cols + n_tok)
+    w = table(t, n_rows, n_cols, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    print(f"split gemm IQ4_XS rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+    assert rel_to_scale(got, gpu_matmul(t, w, X, n_rows, split=False)) <= RTOL
+
+
+def test_split_gemm_iq4xs_full_range(hip, oracle):
+    """IQ4_XS with every codebook entry and every 6-bit scale (ls - 32 from
+    -32 to 31, zero included), large, subnormal and negative d, against the
+    oracle and the exact product; one row of codebook entry 8 (value 1)
+    but for column 5 of each block (113)."""
+    t, n_rows, n_cols, T = W.IQ4_XS, 96, 2048, 40
+    rng = np.random.default_rng(59)
+    blk = rng.integers(0, 256, size=(n_rows, n_cols // 256, 136), dtype=np.uint8)
+    d = (rng.standard_normal((n_rows, n_cols // 256)) * 0.001).astype(np.float32)
+    d[0] = np.float32(3e-7)
+    d[1] = np.float32(-20.0)
+    d[2] = np.float32(100.0)
+    blk[:, :, 0:2] = np.ascontiguousarray(d.astype(np.float16)).view(np.uint8).reshape(
+        n_rows, -1, 2)
+    blk[3, :, 8:] = 0x88              # codebook entry 8 (value 1) everywhere
+    blk[3, :, 8 + 5] = 0x8F           # value 113 at column 5 of each block
+    w = blk.reshape(-1)
+    X = rng.standard_normal((T, n_cols)).astype(np.float32)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+    want = exact(oracle, t, w, X, n_rows)
+    for r in range(n_rows):
+        scale = np.abs(want[:, r]).max()
+        assert np.abs(got[:, r] - want[:, r]).max() <= 1e-6 * scale, r
 
 
 def test_split_gemm_nt4_vs_oracle(hip, oracle):

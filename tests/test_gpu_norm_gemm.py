@@ -95,7 +95,7 @@ def test_norm_matmul_resid_few_tokens(hip, oracle, t, n_tok, n_cols, rows, apart
         assert rel_to_scale(y.numpy(), oracle.matmul(t, m, h, r)) <= RTOL
 
 
-@pytest.mark.parametrize("t", [W.Q4_K, W.Q5_K, W.Q6_K, W.Q8_0])
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q5_K, W.Q6_K, W.Q8_0, W.IQ4_XS])
 @pytest.mark.parametrize("act", list(ACT))
 @pytest.mark.parametrize("n_tok,n_cols,n_ff", [(64, 1024, 320), (45, 512, 100), (5, 512, 64),
                                               (1, 5120, 96), (3, 8192, 64), (40, 2048, 96)])
