@@ -229,7 +229,8 @@ def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: i
            split: bool = True) -> None:
     """y[t, r] = sum_c W[r, c] * x[t, c] for t < n_tok: W n_rows rows of quant
     blocks (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS), x [n_tok, n_cols], y [n_tok, n_rows].
-    From 5-16 tokens (by matrix size), Q4_K / Q5_K run the split-x fp16 matrix-core GEMM with a
+    From 5-16 tokens (by matrix size), Q4_K, Q5_K, Q8_0, Q6_K (rows of 2048k
+    columns) and IQ4_XS (512k) run the split-x fp16 matrix-core GEMM with a
     cached workspace (split=False: the fp32 matrix-core GEMM)."""
     if dtype not in _BLOCK or _BLOCK[dtype][0] == 1:
         raise ValueError(f"dtype {dtype} has no quantised GEMV")
@@ -347,8 +348,8 @@ def norm_matmul(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_
     """ys[m] = rmsnorm(x') @ W_m^T for up to 4 matrices of one type sharing x'
     (q, k, v), any token count; x' = x + d (stored to x_out, default x) when
     d is given, else x. The split GEMM folds the add and the norm into its
-    x pre-pass (Q4_K / Q5_K, from 5-16 tokens by matrix size); with fewer tokens the fused decode
-    GEMV takes them in its prologue.
+    x pre-pass (the split GEMM's types, from 5-16 tokens by matrix size); with
+    fewer tokens the fused decode GEMV takes them in its prologue.
 
     rope = {"n": 1 or 2, "head_dim": D, "mode": ROPE_NEOX / ROPE_INTERLEAVED,
     "pos": int32 [n_tok], "inv_freq": [D/2]} also rotates the first n outputs

@@ -284,9 +284,9 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
                     void* stream);
 
 /* aero_hip_matvec with a workspace, the same call as the reference's matmul
- * (src/kernels.cpp:520-538). With enough tokens of Q4_K or Q5_K (5 for
- * matrices of 32M+ weights, 7 for 8M+, 10 for 2M+, else 16: where measured
- * faster)
+ * (src/kernels.cpp:520-538). With enough tokens of Q4_K, Q5_K, Q8_0,
+ * Q6_K (rows a multiple of 2048 columns) or IQ4_XS (of 512) (5 for matrices
+ * of 32M+ weights, 7 for 8M+, 10 for 2M+, else 16: where measured faster)
  * and
  * `ws` 16-byte aligned of at least aero_hip_matmul_workspace(dtype, n_cols,
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
@@ -333,7 +333,7 @@ int aero_hip_gated_norm_matvec(int dtype, const uint8_t* w, int64_t w_bytes, int
 /* The same for any token count, with the workspace of aero_hip_norm_matmul
  * (aero_hip_norm_matmul_workspace(dtype, n_cols, 0, n_tok) plus
  * aero_hip_split_partials_bytes(n_rows, n_cols, n_tok)): up to 2 tokens the
- * fused GEMV above; on the split GEMM's path (Q4_K / Q5_K, from 5-16 tokens by
+ * fused GEMV above; on the split GEMM's path (aero_hip_matmul's types, from 5-16 tokens by
  * matrix size) the gated norm in its x pre-pass, the inverse RMS in its
  * epilogue; otherwise the gated norm into the workspace, then the projection. */
 int aero_hip_gated_norm_matmul(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows,
@@ -359,8 +359,8 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  *     matrices of one type and width (q, k, v);
  *   aero_hip_norm_matmul_gate_up: out[t*n_ff + r] = act(Wg[r] . h[t]) *
  *     (Wu[r] . h[t]), act an AERO_ACT_* kind.
- * Q4_K / Q5_K with enough tokens (5 when the call's matrices hold 32M+
- * weights together, 7 for 8M+, 10 for 2M+, else 16; weights 16-byte
+ * The split GEMM's types (aero_hip_matmul) with enough tokens (5 when the
+ * call's matrices hold 32M+ weights together, 7 for 8M+, 10 for 2M+, else 16; weights 16-byte
  * aligned) run the
  * split-x fp16 GEMM with h never written: each token's sums are scaled by
  * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
@@ -423,7 +423,7 @@ int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
  * capture, serving loops, harnesses that forbid allocation). Results equal
  * aero_hip_matmul's with a workspace bit for bit. Returns 0 with a reason
  * when the call would need more scratch than the maximum (n_tok * n_cols *
- * 4 bytes and a little more for Q4_K / Q5_K on the split path). Every
+ * 4 bytes and a little more for the split path's types). Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other host threads) race; calls ordered on one stream do
  * not. Nothing in the array needs clearing between calls. */
