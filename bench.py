@@ -923,6 +923,10 @@ GEMM_CASES = [
     ("ffn_down_4096x14336", 12, 4096, 14336, 512), ("q8_0_14336x4096", 8, 14336, 4096, 512),
     ("q6_k_14336x4096", 14, 14336, 4096, 512), ("q6_k_4096x14336", 14, 4096, 14336, 512),
     ("iq4_xs_14336x4096", 23, 14336, 4096, 512),
+    ("q6_k_14336x4096_t5", 14, 14336, 4096, 5), ("q6_k_14336x4096_t8", 14, 14336, 4096, 8),
+    ("q6_k_14336x4096_t16", 14, 14336, 4096, 16), ("q8_0_14336x4096_t5", 8, 14336, 4096, 5),
+    ("iq4_xs_14336x4096_t5", 23, 14336, 4096, 5), ("iq4_xs_14336x4096_t8", 23, 14336, 4096, 8),
+    ("q6_k_4096x4096_t8", 14, 4096, 4096, 8), ("q8_0_4096x4096_t8", 8, 4096, 4096, 8),
     ("ffn_gate_14336x4096_t64", 12, 14336, 4096, 64),
     ("q8_0_4096x4096", 8, 4096, 4096, 512), ("q8_0_4096x14336", 8, 4096, 14336, 512),
     ("q8_0_14336x4096_t8", 8, 14336, 4096, 8), ("q8_0_14336x4096_t16", 8, 14336, 4096, 16),
