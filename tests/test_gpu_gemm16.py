@@ -353,3 +353,29 @@ def test_split_gemm_small_workspace_and_host_abi(hip, oracle):
     assert rel_to_scale(dy.numpy(), want) <= RTOL
     Y = native.matmul(W.Q4_K, w.tobytes(), X)
     assert rel_to_scale(Y, want) <= RTOL
+
+
+def _random_split_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    unit = {W.Q4_K: 256, W.Q5_K: 256, W.Q8_0: 256, W.Q6_K: 2048, W.IQ4_XS: 512}
+    types = list(unit)
+    cases = []
+    for i in range(n):
+        t = types[i % len(types)]
+        n_cols = unit[t] * int(rng.integers(1, 9 if unit[t] < 2048 else 4))
+        cases.append((i, t, int(rng.integers(1, 700)), n_cols, int(rng.integers(5, 150))))
+    return cases
+
+
+@pytest.mark.parametrize("i,t,n_rows,n_cols,n_tok", _random_split_cases(25, 7))
+def test_split_gemm_random_shapes(hip, oracle, i, t, n_rows, n_cols, n_tok):
+    """Seeded random shapes of every split-path type: 1-700 rows, 5-150
+    tokens (partial tiles, column splits at the low counts), the smallest
+    row widths each type takes and up to 8 of them."""
+    rng = np.random.default_rng(1000 + i)
+    w = table(t, n_rows, n_cols, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    print(f"random split gemm {i}: type={t} rows={n_rows} cols={n_cols} tokens={n_tok}",
+          flush=True)
+    got = gpu_matmul(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
