@@ -43,6 +43,7 @@ struct GemvParams {
     int64_t rb;
     int n_tok;         // tokens this launch handles (<= T)
     int64_t x_stride, y_stride;
+    int half;          // gemv64_kernel: rows of <= 2048 columns, a row a half-wave
 };
 
 // ------------------------------------------------------------ lane groups
@@ -985,13 +986,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
     const int tid = threadIdx.x;
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R;
+    // p.half: each half-wave takes a row (2R rows a wave); lc is the lane's
+    // 64-column slot within its row
+    const bool half = p.half;
+    const int lc = half ? (l & 31) : l;
+    const int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R * (half ? 2 : 1);
     const int n_blk = p.n_cols / BV;
     const int n_st = (p.n_cols + kStepCols - 1) / kStepCols;
 
     const uint8_t* rowp[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rowp[r] = p.w + min(r0 + r, p.n_rows - 1) * p.rb;
+    for (int r = 0; r < R; ++r)
+        rowp[r] = p.w + min(r0 + (half ? 2 * r + (l >> 5) : r), p.n_rows - 1) * p.rb;
 
     float acc[R][T];
 #pragma unroll
@@ -1003,13 +1009,13 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
     L ua[R];
     xstep_load<T>(p, 0, tid, xr);
 #pragma unroll
-    for (int r = 0; r < R; ++r) ua[r].load(rowp[r], 0, l, n_blk);
-    bool live_a = kLaneCols * l < p.n_cols;
+    for (int r = 0; r < R; ++r) ua[r].load(rowp[r], 0, lc, n_blk);
+    bool live_a = kLaneCols * lc < p.n_cols;
     xstep_store<T>(xs[0], xr, tid);
     __syncthreads();
 
     if constexpr (!PIPE) {
-        L::template step<R, T>(ua, xs[0], l, live_a, acc);  // rows of one step
+        L::template step<R, T>(ua, xs[0], lc, live_a, acc);  // rows of one step
     } else {
         L ub[R];
         bool live_b;
@@ -1017,20 +1023,20 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
             const int s1 = min(st + 1, n_st - 1);
             xstep_load<T>(p, s1, tid, xr);
 #pragma unroll
-            for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, l, n_blk);
-            live_b = st + 1 < n_st && s1 * kStepCols + kLaneCols * l < p.n_cols;
+            for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, lc, n_blk);
+            live_b = st + 1 < n_st && s1 * kStepCols + kLaneCols * lc < p.n_cols;
             __builtin_amdgcn_sched_barrier(0);
-            L::template step<R, T>(ua, xs[0], l, live_a, acc);
+            L::template step<R, T>(ua, xs[0], lc, live_a, acc);
             xstep_store<T>(xs[1], xr, tid);
             __syncthreads();
             if (st + 1 >= n_st) break;
             const int s2 = min(st + 2, n_st - 1);
             xstep_load<T>(p, s2, tid, xr);
 #pragma unroll
-            for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, l, n_blk);
-            live_a = st + 2 < n_st && s2 * kStepCols + kLaneCols * l < p.n_cols;
+            for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, lc, n_blk);
+            live_a = st + 2 < n_st && s2 * kStepCols + kLaneCols * lc < p.n_cols;
             __builtin_amdgcn_sched_barrier(0);
-            L::template step<R, T>(ub, xs[1], l, live_b, acc);
+            L::template step<R, T>(ub, xs[1], lc, live_b, acc);
             xstep_store<T>(xs[0], xr, tid);
             __syncthreads();
         }
@@ -1040,8 +1046,14 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const float v = group_sum<64>(acc[r][t]);
-            if (l == 0 && r0 + r < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + r0 + r] = v;
+            if (half) {
+                const float v = group_sum<32>(acc[r][t]);
+                const int64_t row = r0 + 2 * r + (l >> 5);
+                if (lc == 0 && row < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + row] = v;
+            } else {
+                const float v = group_sum<64>(acc[r][t]);
+                if (l == 0 && r0 + r < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + r0 + r] = v;
+            }
         }
 }
 
@@ -1095,6 +1107,7 @@ struct GemvFuse {
     int rope_mode;        // AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED
     const int32_t* pos;   // [n_tok] positions of this launch's tokens
     const float* inv;     // [rope_D / 2] inverse frequencies
+    int half;             // rows of <= 2048 columns, no PAIR / RoPE: a row a half-wave
 };
 
 __device__ __forceinline__ float act_rt(int kind, float v) {
@@ -1123,6 +1136,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     const int tid = threadIdx.x;
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // rows of at most 2048 columns (f.half): each half-wave takes a row, so a
+    // wave covers 2R rows; lc is the lane's 64-column slot within its row
+    const bool half = !PAIR && f.half;
+    const int lc = half ? (l & 31) : l;
     const int n_blk = f.n_cols / BV;
     const int n_st = (f.n_cols + kStepCols - 1) / kStepCols;
 
@@ -1148,10 +1165,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             pair0 = (bl % per_head) * (2 * R) + (wave & 1) * R;
             r0 = (int64_t)h * f.rope_D + (wave >= 2 ? P : 0) + pair0;
         } else {
-            r0 = ((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R;
+            r0 = ((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R * (half ? 2 : 1);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) rowp[r] = f.w[m] + min(r0 + r, f.n_rows[m] - 1) * f.rb;
+        for (int r = 0; r < R; ++r)
+            rowp[r] = f.w[m] + min(r0 + (half ? 2 * r + (l >> 5) : r), f.n_rows[m] - 1) * f.rb;
     }
     GemvParams p{nullptr, f.x, nullptr, 0, f.n_cols, f.rb, f.n_tok, f.n_cols, 0};
     GemvParams pd = p;
@@ -1249,7 +1267,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     __builtin_amdgcn_sched_barrier(0);  // keeps every x load ahead of the weights
     L ua[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) ua[r].load(rowp[r], 0, l, n_blk);
+    for (int r = 0; r < R; ++r) ua[r].load(rowp[r], 0, lc, n_blk);
 
     // the norm of each token's x: squares of this thread's 16 columns of
     // each step (the last step's columns clamped to the row: counted once),
@@ -1303,12 +1321,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         for (int t = 0; t < T; ++t) acc[r][t] = 0.0f;
 
     norm_x(wv, xr);
-    bool live_a = kLaneCols * l < f.n_cols;
+    bool live_a = kLaneCols * lc < f.n_cols;
     xstep_store<T>(xs[0], xr, tid);
     __syncthreads();
 
     if constexpr (!PIPE) {
-        L::template step<R, T>(ua, xs[0], l, live_a, acc);
+        L::template step<R, T>(ua, xs[0], lc, live_a, acc);
     } else {
         L ub[R];
         bool live_b;
@@ -1318,10 +1336,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             load_z(s1);
             load_w(s1, wv);
 #pragma unroll
-            for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, l, n_blk);
-            live_b = st + 1 < n_st && s1 * kStepCols + kLaneCols * l < f.n_cols;
+            for (int r = 0; r < R; ++r) ub[r].load(rowp[r], s1, lc, n_blk);
+            live_b = st + 1 < n_st && s1 * kStepCols + kLaneCols * lc < f.n_cols;
             __builtin_amdgcn_sched_barrier(0);
-            L::template step<R, T>(ua, xs[0], l, live_a, acc);
+            L::template step<R, T>(ua, xs[0], lc, live_a, acc);
             norm_x(wv, xr);
             xstep_store<T>(xs[1], xr, tid);
             __syncthreads();
@@ -1331,10 +1349,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             load_z(s2);
             load_w(s2, wv);
 #pragma unroll
-            for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, l, n_blk);
-            live_a = st + 2 < n_st && s2 * kStepCols + kLaneCols * l < f.n_cols;
+            for (int r = 0; r < R; ++r) ua[r].load(rowp[r], s2, lc, n_blk);
+            live_a = st + 2 < n_st && s2 * kStepCols + kLaneCols * lc < f.n_cols;
             __builtin_amdgcn_sched_barrier(0);
-            L::template step<R, T>(ub, xs[1], l, live_b, acc);
+            L::template step<R, T>(ub, xs[1], lc, live_b, acc);
             norm_x(wv, xr);
             xstep_store<T>(xs[0], xr, tid);
             __syncthreads();
@@ -1354,9 +1372,16 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         } else if (m >= f.rope_mats) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float v = group_sum<64>(acc[r][t]);
-                if (l == 0 && r0 + r < f.n_rows[m] && t < f.n_tok)
-                    f.y[m][t * f.n_rows[m] + r0 + r] = v;
+                if (half) {
+                    const float v = group_sum<32>(acc[r][t]);
+                    const int64_t row = r0 + 2 * r + (l >> 5);
+                    if (lc == 0 && row < f.n_rows[m] && t < f.n_tok)
+                        f.y[m][t * f.n_rows[m] + row] = v;
+                } else {
+                    const float v = group_sum<64>(acc[r][t]);
+                    if (l == 0 && r0 + r < f.n_rows[m] && t < f.n_tok)
+                        f.y[m][t * f.n_rows[m] + r0 + r] = v;
+                }
             }
         }
     }
@@ -1603,7 +1628,12 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
             // workgroups, else 1; four tokens share the weight decoding over
             // 4 rows when that leaves >= 512 workgroups (>= 256 for rows of
             // several steps)
-            auto wgs_of = [&](int r) { return (n_rows + r * kGemvWaves - 1) / (r * kGemvWaves); };
+            // rows of at most 2048 columns fill half a wave's lanes: each
+            // half-wave then takes a row (twice the rows a workgroup)
+            const int hf = n_cols <= kStepCols / 2 && tune("gemv_half", 1) ? 2 : 1;
+            auto wgs_of = [&](int r) {
+                return (n_rows + r * hf * kGemvWaves - 1) / (r * hf * kGemvWaves);
+            };
             int R = wgs_of(2) >= 256 ? 2 : 1;
             if (T == 4 && wgs_of(4) >= 512) R = 4;
             R = tune("gemv_r", R);
@@ -1614,7 +1644,7 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
                 return false;
             }
             GemvParams p{w, x + t0 * n_cols, y + t0 * n_rows, n_rows, (int)n_cols, rb, nt,
-                         n_cols, n_rows};
+                         n_cols, n_rows, hf == 2};
             if (!launch("gemv64_kernel", k, dim3((unsigned)wgs), dim3(64 * kGemvWaves), 0, s, p))
                 return false;
         }
@@ -1747,9 +1777,13 @@ static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* cons
         f.rope_mode = rope->mode;
         f.inv = rope->inv;
     }
+    // rows of at most 2048 columns fill only half a wave's 64-column lanes:
+    // each half-wave then takes a row of its own (not with RoPE or the pair)
+    f.half = !pair && f.rope_mats == 0 && n_cols <= kStepCols / 2 && tune("gemv_half", 1);
     // workgroups of a launch of T tokens: rows a wave as the kernel's R
+    // (twice that with half-wave rows)
     auto grid_of = [&](int T, GemvFuse& g) -> int64_t {
-        const int R = (pair || T == 4) ? 4 : 2;
+        const int R = ((pair || T == 4) ? 4 : 2) * (f.half ? 2 : 1);
         int64_t tot = 0;
         if (pair) return (n_rows[0] + (int64_t)kGemvWaves * (R / 2) - 1) / (kGemvWaves * (R / 2));
         for (int m = 0; m < 4; ++m) {

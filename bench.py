@@ -731,6 +731,9 @@ GEMV_CASES = [
     ("q8_0_4096x4096", 8, 4096, 4096), ("q8_0_14336x4096", 8, 14336, 4096),
     ("q5_k_14336x4096", 13, 14336, 4096), ("q6_k_14336x4096", 14, 14336, 4096),
     ("iq4_xs_14336x4096", 23, 14336, 4096),
+    # hidden 2048 (Qwen3-Next, Llama-3.2-1B): rows of half a 4096-column step
+    ("q4_k_8192x2048", 12, 8192, 2048), ("q4_k_2048x8192", 12, 2048, 8192),
+    ("q8_0_8192x2048", 8, 8192, 2048),
 ]
 
 
