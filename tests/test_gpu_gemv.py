@@ -153,3 +153,34 @@ def test_host_abi_matvec_matmul(hip, oracle):
         native.matvec(W.F32, bytes(64), np.zeros(16, np.float32))
     with pytest.raises(ValueError):
         native.matvec(W.Q4_K, bytes(144 * 4), np.zeros(255, np.float32))
+
+
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q8_0, W.Q6_K, W.IQ4_XS, W.Q5_K])
+@pytest.mark.parametrize("n_rows,n_cols", [(1, 2048), (3, 1024), (37, 2048), (129, 512)])
+@pytest.mark.parametrize("n_tok", [1, 2, 4])
+def test_matvec_half_wave_rows(hip, oracle, t, n_rows, n_cols, n_tok):
+    """Rows of at most 2048 columns, one a half-wave: odd row counts leave the
+    last wave's upper half on a clamped row whose sum is not stored, and rows
+    of 512 columns use 8 of a half-wave's 32 column slots."""
+    rng = np.random.default_rng(n_rows * 7 + n_cols + n_tok + t)
+    w = W.make_table(t, n_rows * n_cols // W.BLOCK[t][0], rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    got = gpu_matvec(t, w, X, n_rows)
+    assert rel_to_scale(got, oracle.matmul(t, w, X, n_rows)) <= RTOL
+
+
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_norm_matvec_half_wave_odd_rows(hip, oracle, n_tok):
+    """The fused decode GEMV over three matrices of odd row counts and 2048
+    columns (a row a half-wave), with the RMSNorm in its prologue."""
+    t, n_cols, rows = W.Q4_K, 2048, [37, 5, 1]
+    rng = np.random.default_rng(61 + n_tok)
+    ws = [W.make_table(t, r * n_cols // 256, rng) for r in rows]
+    x = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(n_cols)).astype(np.float32)
+    ys = [DA.empty((n_tok, r)) for r in rows]
+    ops.norm_matvec(t, [DA.from_numpy(w) for w in ws], DA.from_numpy(x), ys, rows, n_cols,
+                    n_tok, norm_w=DA.from_numpy(nw), eps=1e-5)
+    h = oracle.rmsnorm_rows(x, nw, 1e-5)
+    for w, r, y in zip(ws, rows, ys):
+        assert rel_to_scale(y.numpy(), oracle.matmul(t, w, h, r)) <= RTOL
