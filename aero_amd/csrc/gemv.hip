@@ -43,7 +43,7 @@ struct GemvParams {
     int64_t rb;
     int n_tok;         // tokens this launch handles (<= T)
     int64_t x_stride, y_stride;
-    int half;          // gemv64_kernel: rows of <= 2048 columns, a row a half-wave
+    int sub;           // gemv64_kernel: rows of <= 2048 (1) / 1024 (2) columns, a row a 64 >> sub lanes
 };
 
 // ------------------------------------------------------------ lane groups
@@ -977,7 +977,20 @@ template <> struct Lane64<AERO_DTYPE_Q6_K> {
 // PIPE (rows of more than one step): the next step's x and weights are
 // loaded before the current step is computed, for step min(st+1, last) so
 // that every load is unconditional.
-template <int TYPE, int R, int T, bool PIPE>
+// Rows of at most 1024 / 2048 columns fill only 16 / 32 of a wave's lanes:
+// with sub = 2 / 1 each group of 64 >> sub lanes takes a row of its own (lane
+// l: row slot l >> (6 - sub), column slot l & ((64 >> sub) - 1)); a row's sum
+// is a butterfly over its group.
+__device__ __forceinline__ float sub_sum(float v, int sub) {
+    return sub == 0 ? group_sum<64>(v) : (sub == 1 ? group_sum<32>(v) : group_sum<16>(v));
+}
+// the width of rows a wave's sub-groups take whole (0: one row a wave)
+inline int gemv_sub(int64_t n_cols) {
+    if (!tune("gemv_half", 1)) return 0;
+    return n_cols <= kStepCols / 4 ? 2 : (n_cols <= kStepCols / 2 ? 1 : 0);
+}
+
+template <int TYPE, int R, int T, bool PIPE, bool SUBR = false>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
     using L = Lane64<TYPE>;
     constexpr int BV = QT<TYPE>::BV;
@@ -986,18 +999,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
     const int tid = threadIdx.x;
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // p.half: each half-wave takes a row (2R rows a wave); lc is the lane's
-    // 64-column slot within its row
-    const bool half = p.half;
-    const int lc = half ? (l & 31) : l;
-    const int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R * (half ? 2 : 1);
+    // p.sub: each group of 64 >> sub lanes takes a row (R << sub rows a
+    // wave); lc is the lane's 64-column slot within its row
+    const int sub = SUBR && !PIPE ? p.sub : 0;   // SUBR: rows of one step or less
+    const int lc = l & ((64 >> sub) - 1), lrow = l >> (6 - sub);
+    const int64_t r0 = (((int64_t)blockIdx.x * kGemvWaves + wave) * R) << sub;
     const int n_blk = p.n_cols / BV;
     const int n_st = (p.n_cols + kStepCols - 1) / kStepCols;
 
     const uint8_t* rowp[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        rowp[r] = p.w + min(r0 + (half ? 2 * r + (l >> 5) : r), p.n_rows - 1) * p.rb;
+        rowp[r] = p.w + min(r0 + (r << sub) + lrow, p.n_rows - 1) * p.rb;
 
     float acc[R][T];
 #pragma unroll
@@ -1046,14 +1059,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_kernel(GemvParams p) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            if (half) {
-                const float v = group_sum<32>(acc[r][t]);
-                const int64_t row = r0 + 2 * r + (l >> 5);
-                if (lc == 0 && row < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + row] = v;
-            } else {
-                const float v = group_sum<64>(acc[r][t]);
-                if (l == 0 && r0 + r < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + r0 + r] = v;
-            }
+            const float v = sub_sum(acc[r][t], sub);
+            const int64_t row = r0 + (r << sub) + lrow;
+            if (lc == 0 && row < p.n_rows && t < p.n_tok) p.y[t * p.y_stride + row] = v;
         }
 }
 
@@ -1107,7 +1115,7 @@ struct GemvFuse {
     int rope_mode;        // AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED
     const int32_t* pos;   // [n_tok] positions of this launch's tokens
     const float* inv;     // [rope_D / 2] inverse frequencies
-    int half;             // rows of <= 2048 columns, no PAIR / RoPE: a row a half-wave
+    int sub;              // rows of <= 2048 (1) / 1024 (2) columns, no RoPE: a row a 64 >> sub lanes
 };
 
 __device__ __forceinline__ float act_rt(int kind, float v) {
@@ -1124,7 +1132,8 @@ __device__ __forceinline__ float act_rt(int kind, float v) {
 // step's weights are requested before the norm is computed (after x, which
 // the norm waits for); for rows of one step the x loaded for the norm is the
 // x staged.
-template <int TYPE, int T, bool PIPE, bool PAIR, bool RESID, bool GATED = false>
+template <int TYPE, int T, bool PIPE, bool PAIR, bool RESID, bool GATED = false,
+          bool SUBR = false>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse f) {
     using L = Lane64<TYPE>;
     constexpr int R = (PAIR || T == 4) ? 4 : 2;
@@ -1136,10 +1145,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     const int tid = threadIdx.x;
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // rows of at most 2048 columns (f.half): each half-wave takes a row, so a
-    // wave covers 2R rows; lc is the lane's 64-column slot within its row
-    const bool half = !PAIR && f.half;
-    const int lc = half ? (l & 31) : l;
+    // f.sub: each group of 64 >> sub lanes takes a row, so a wave covers
+    // R << sub rows; lc is the lane's 64-column slot within its row
+    const int sub = SUBR && !PIPE ? f.sub : 0;   // SUBR: rows of one step or less
+    const int lc = l & ((64 >> sub) - 1), lrow = l >> (6 - sub);
     const int n_blk = f.n_cols / BV;
     const int n_st = (f.n_cols + kStepCols - 1) / kStepCols;
 
@@ -1149,10 +1158,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
     const uint8_t* rowp[R];
     if constexpr (PAIR) {
         // rows r0 .. r0 + R/2 of gate (r < R/2) and of up (r >= R/2)
-        r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * (R / 2);
+        r0 = (((int64_t)blockIdx.x * kGemvWaves + wave) * (R / 2)) << sub;
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            rowp[r] = f.w[r < R / 2 ? 0 : 1] + min(r0 + r % (R / 2), f.n_rows[0] - 1) * f.rb;
+            rowp[r] = f.w[r < R / 2 ? 0 : 1] +
+                      min(r0 + ((r % (R / 2)) << sub) + lrow, f.n_rows[0] - 1) * f.rb;
     } else {
         const int b = blockIdx.x;
         m = __builtin_amdgcn_readfirstlane((b >= f.blk[1]) + (b >= f.blk[2]) + (b >= f.blk[3]));
@@ -1165,11 +1175,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             pair0 = (bl % per_head) * (2 * R) + (wave & 1) * R;
             r0 = (int64_t)h * f.rope_D + (wave >= 2 ? P : 0) + pair0;
         } else {
-            r0 = ((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R * (half ? 2 : 1);
+            r0 = (((int64_t)(b - f.blk[m]) * kGemvWaves + wave) * R) << sub;
         }
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            rowp[r] = f.w[m] + min(r0 + (half ? 2 * r + (l >> 5) : r), f.n_rows[m] - 1) * f.rb;
+            rowp[r] = f.w[m] + min(r0 + (r << sub) + lrow, f.n_rows[m] - 1) * f.rb;
     }
     GemvParams p{nullptr, f.x, nullptr, 0, f.n_cols, f.rb, f.n_tok, f.n_cols, 0};
     GemvParams pd = p;
@@ -1364,24 +1374,19 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
         if constexpr (PAIR) {
 #pragma unroll
             for (int r = 0; r < R / 2; ++r) {
-                const float g = group_sum<64>(acc[r][t]);
-                const float u = group_sum<64>(acc[R / 2 + r][t]);
-                if (l == 0 && r0 + r < f.n_rows[0] && t < f.n_tok)
-                    f.y[0][t * f.n_rows[0] + r0 + r] = act_rt(f.act, g) * u;
+                const float g = sub_sum(acc[r][t], sub);
+                const float u = sub_sum(acc[R / 2 + r][t], sub);
+                const int64_t row = r0 + (r << sub) + lrow;
+                if (lc == 0 && row < f.n_rows[0] && t < f.n_tok)
+                    f.y[0][t * f.n_rows[0] + row] = act_rt(f.act, g) * u;
             }
         } else if (m >= f.rope_mats) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (half) {
-                    const float v = group_sum<32>(acc[r][t]);
-                    const int64_t row = r0 + 2 * r + (l >> 5);
-                    if (lc == 0 && row < f.n_rows[m] && t < f.n_tok)
-                        f.y[m][t * f.n_rows[m] + row] = v;
-                } else {
-                    const float v = group_sum<64>(acc[r][t]);
-                    if (l == 0 && r0 + r < f.n_rows[m] && t < f.n_tok)
-                        f.y[m][t * f.n_rows[m] + r0 + r] = v;
-                }
+                const float v = sub_sum(acc[r][t], sub);
+                const int64_t row = r0 + (r << sub) + lrow;
+                if (lc == 0 && row < f.n_rows[m] && t < f.n_tok)
+                    f.y[m][t * f.n_rows[m] + row] = v;
             }
         }
     }
@@ -1435,7 +1440,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
 using GemvFusedKernel = void (*)(GemvFuse);
 
 template <int TYPE, bool PAIR, bool RESID>
-GemvFusedKernel pick_fused_t(int T, bool pipe) {
+GemvFusedKernel pick_fused_t(int T, bool pipe, bool subr) {
     if (pipe) {
         switch (T) {
         case 1: return gemv64_fused_kernel<TYPE, 1, true, PAIR, RESID>;
@@ -1444,21 +1449,24 @@ GemvFusedKernel pick_fused_t(int T, bool pipe) {
         }
     }
     switch (T) {
-    case 1: return gemv64_fused_kernel<TYPE, 1, false, PAIR, RESID>;
-    case 2: return gemv64_fused_kernel<TYPE, 2, false, PAIR, RESID>;
-    case 4: return gemv64_fused_kernel<TYPE, 4, false, PAIR, RESID>;
+    case 1: return subr ? gemv64_fused_kernel<TYPE, 1, false, PAIR, RESID, false, true>
+                        : gemv64_fused_kernel<TYPE, 1, false, PAIR, RESID>;
+    case 2: return subr ? gemv64_fused_kernel<TYPE, 2, false, PAIR, RESID, false, true>
+                        : gemv64_fused_kernel<TYPE, 2, false, PAIR, RESID>;
+    case 4: return subr ? gemv64_fused_kernel<TYPE, 4, false, PAIR, RESID, false, true>
+                        : gemv64_fused_kernel<TYPE, 4, false, PAIR, RESID>;
     default: return nullptr;
     }
 }
 
 template <bool PAIR, bool RESID>
-GemvFusedKernel pick_fused_r(int dtype, int T, bool pipe) {
+GemvFusedKernel pick_fused_r(int dtype, int T, bool pipe, bool subr) {
     switch (dtype) {
-    case AERO_DTYPE_Q8_0: return pick_fused_t<AERO_DTYPE_Q8_0, PAIR, RESID>(T, pipe);
-    case AERO_DTYPE_Q4_K: return pick_fused_t<AERO_DTYPE_Q4_K, PAIR, RESID>(T, pipe);
-    case AERO_DTYPE_Q5_K: return pick_fused_t<AERO_DTYPE_Q5_K, PAIR, RESID>(T, pipe);
-    case AERO_DTYPE_Q6_K: return pick_fused_t<AERO_DTYPE_Q6_K, PAIR, RESID>(T, pipe);
-    case AERO_DTYPE_IQ4_XS: return pick_fused_t<AERO_DTYPE_IQ4_XS, PAIR, RESID>(T, pipe);
+    case AERO_DTYPE_Q8_0: return pick_fused_t<AERO_DTYPE_Q8_0, PAIR, RESID>(T, pipe, subr);
+    case AERO_DTYPE_Q4_K: return pick_fused_t<AERO_DTYPE_Q4_K, PAIR, RESID>(T, pipe, subr);
+    case AERO_DTYPE_Q5_K: return pick_fused_t<AERO_DTYPE_Q5_K, PAIR, RESID>(T, pipe, subr);
+    case AERO_DTYPE_Q6_K: return pick_fused_t<AERO_DTYPE_Q6_K, PAIR, RESID>(T, pipe, subr);
+    case AERO_DTYPE_IQ4_XS: return pick_fused_t<AERO_DTYPE_IQ4_XS, PAIR, RESID>(T, pipe, subr);
     default: return nullptr;
     }
 }
@@ -1483,46 +1491,47 @@ GemvFusedKernel pick_gated(int dtype, int T, bool pipe) {
     }
 }
 
-GemvFusedKernel pick_fused(bool pair, bool resid, int dtype, int T, bool pipe) {
+GemvFusedKernel pick_fused(bool pair, bool resid, int dtype, int T, bool pipe, bool subr) {
     if (pair)
-        return resid ? pick_fused_r<true, true>(dtype, T, pipe)
-                     : pick_fused_r<true, false>(dtype, T, pipe);
-    return resid ? pick_fused_r<false, true>(dtype, T, pipe)
-                 : pick_fused_r<false, false>(dtype, T, pipe);
+        return resid ? pick_fused_r<true, true>(dtype, T, pipe, subr)
+                     : pick_fused_r<true, false>(dtype, T, pipe, subr);
+    return resid ? pick_fused_r<false, true>(dtype, T, pipe, subr)
+                 : pick_fused_r<false, false>(dtype, T, pipe, subr);
 }
 
 using GemvKernel = void (*)(GemvParams);
 
-template <int TYPE, int R, bool PIPE>
+template <int TYPE, int R, bool PIPE, bool SUBR>
 GemvKernel pick64_t(int T) {
     switch (T) {
-    case 1: return gemv64_kernel<TYPE, R, 1, PIPE>;
-    case 2: return gemv64_kernel<TYPE, R, 2, PIPE>;
+    case 1: return gemv64_kernel<TYPE, R, 1, PIPE, SUBR>;
+    case 2: return gemv64_kernel<TYPE, R, 2, PIPE, SUBR>;
     case 4:
-        if constexpr (!PIPE) return gemv64_kernel<TYPE, R, 4, PIPE>;
+        if constexpr (!PIPE) return gemv64_kernel<TYPE, R, 4, PIPE, SUBR>;
         return nullptr;
     default: return nullptr;
     }
 }
 
-template <int TYPE, bool PIPE>
+template <int TYPE, bool PIPE, bool SUBR>
 GemvKernel pick64_r(int R, int T) {
     switch (R) {
-    case 1: return pick64_t<TYPE, 1, PIPE>(T);
-    case 2: return pick64_t<TYPE, 2, PIPE>(T);
-    case 4: return pick64_t<TYPE, 4, PIPE>(T);
+    case 1: return pick64_t<TYPE, 1, PIPE, SUBR>(T);
+    case 2: return pick64_t<TYPE, 2, PIPE, SUBR>(T);
+    case 4: return pick64_t<TYPE, 4, PIPE, SUBR>(T);
     default: return nullptr;
     }
 }
 
-template <bool PIPE>
+// SUBR: the sub-wave row layout (rows of one step or less, GemvParams::sub)
+template <bool PIPE, bool SUBR = false>
 GemvKernel pick64(int dtype, int R, int T) {
     switch (dtype) {
-    case AERO_DTYPE_Q8_0: return pick64_r<AERO_DTYPE_Q8_0, PIPE>(R, T);
-    case AERO_DTYPE_Q4_K: return pick64_r<AERO_DTYPE_Q4_K, PIPE>(R, T);
-    case AERO_DTYPE_Q5_K: return pick64_r<AERO_DTYPE_Q5_K, PIPE>(R, T);
-    case AERO_DTYPE_Q6_K: return pick64_r<AERO_DTYPE_Q6_K, PIPE>(R, T);
-    case AERO_DTYPE_IQ4_XS: return pick64_r<AERO_DTYPE_IQ4_XS, PIPE>(R, T);
+    case AERO_DTYPE_Q8_0: return pick64_r<AERO_DTYPE_Q8_0, PIPE, SUBR>(R, T);
+    case AERO_DTYPE_Q4_K: return pick64_r<AERO_DTYPE_Q4_K, PIPE, SUBR>(R, T);
+    case AERO_DTYPE_Q5_K: return pick64_r<AERO_DTYPE_Q5_K, PIPE, SUBR>(R, T);
+    case AERO_DTYPE_Q6_K: return pick64_r<AERO_DTYPE_Q6_K, PIPE, SUBR>(R, T);
+    case AERO_DTYPE_IQ4_XS: return pick64_r<AERO_DTYPE_IQ4_XS, PIPE, SUBR>(R, T);
     default: return nullptr;
     }
 }
@@ -1628,9 +1637,8 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
             // workgroups, else 1; four tokens share the weight decoding over
             // 4 rows when that leaves >= 512 workgroups (>= 256 for rows of
             // several steps)
-            // rows of at most 2048 columns fill half a wave's lanes: each
-            // half-wave then takes a row (twice the rows a workgroup)
-            const int hf = n_cols <= kStepCols / 2 && tune("gemv_half", 1) ? 2 : 1;
+            // rows of at most 2048 / 1024 columns: a row a half / quarter wave
+            const int hf = 1 << gemv_sub(n_cols);
             auto wgs_of = [&](int r) {
                 return (n_rows + r * hf * kGemvWaves - 1) / (r * hf * kGemvWaves);
             };
@@ -1638,13 +1646,15 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
             if (T == 4 && wgs_of(4) >= 512) R = 4;
             R = tune("gemv_r", R);
             const int64_t wgs = wgs_of(R);
-            GemvKernel k = pipe ? pick64<true>(dtype, R, T) : pick64<false>(dtype, R, T);
+            GemvKernel k = pipe ? pick64<true>(dtype, R, T)
+                                : (hf > 1 ? pick64<false, true>(dtype, R, T)
+                                          : pick64<false>(dtype, R, T));
             if (k == nullptr || wgs > 0x7fffffff) {
                 set_error("matvec: no kernel for dtype %d, rows/wave %d", dtype, R);
                 return false;
             }
             GemvParams p{w, x + t0 * n_cols, y + t0 * n_rows, n_rows, (int)n_cols, rb, nt,
-                         n_cols, n_rows, hf == 2};
+                         n_cols, n_rows, gemv_sub(n_cols)};
             if (!launch("gemv64_kernel", k, dim3((unsigned)wgs), dim3(64 * kGemvWaves), 0, s, p))
                 return false;
         }
@@ -1777,13 +1787,14 @@ static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* cons
         f.rope_mode = rope->mode;
         f.inv = rope->inv;
     }
-    // rows of at most 2048 columns fill only half a wave's 64-column lanes:
-    // each half-wave then takes a row of its own (not with RoPE or the pair)
-    f.half = !pair && f.rope_mats == 0 && n_cols <= kStepCols / 2 && tune("gemv_half", 1);
-    // workgroups of a launch of T tokens: rows a wave as the kernel's R
-    // (twice that with half-wave rows)
+    // rows of at most 2048 / 1024 columns fill only half / a quarter of a
+    // wave's 64-column lanes: each half / quarter wave then takes a row of its
+    // own (not with RoPE, whose row pairs follow the one-row-a-wave layout)
+    f.sub = f.rope_mats == 0 && gated == nullptr ? gemv_sub(n_cols) : 0;
+    // workgroups of a launch of T tokens: rows a wave as the kernel's R, times
+    // 2^sub
     auto grid_of = [&](int T, GemvFuse& g) -> int64_t {
-        const int R = ((pair || T == 4) ? 4 : 2) * (f.half ? 2 : 1);
+        const int R = ((pair || T == 4) ? 4 : 2) << f.sub;
         int64_t tot = 0;
         if (pair) return (n_rows[0] + (int64_t)kGemvWaves * (R / 2) - 1) / (kGemvWaves * (R / 2));
         for (int m = 0; m < 4; ++m) {
@@ -1810,7 +1821,7 @@ static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* cons
         const int nt = (int)std::min<int64_t>(t_max, n_tok - t0);
         const int T = nt == 1 ? 1 : (nt == 2 ? 2 : 4);
         GemvFusedKernel k = gated ? pick_gated(dtype, T, pipe)
-                              : pick_fused(pair, d != nullptr, dtype, T, pipe);
+                              : pick_fused(pair, d != nullptr, dtype, T, pipe, f.sub > 0);
         if (k == nullptr) {
             set_error("%s: no kernel for %d tokens", what, T);
             return false;
