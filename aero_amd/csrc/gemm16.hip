@@ -1484,12 +1484,16 @@ bool split_run(const SplitJob& j, hipStream_t s) {
 // Q4_K, split / GEMV, µs: 14336 x 4096 at 4 tokens 24.9 / 23.2, 5: 25.1 /
 // 31.0; 4096 x 4096 at 6 tokens 14.5 / 14.2, 8: 14.6 / 17.6; 1024 x 4096
 // at 8 tokens 13.3 / 10.6, 12: 13.4 / 15.8. So: 5 tokens from 32M
-// weights, 7 from 8M, 10 from 2M, 16 below. AERO_HIP_TUNE
-// gemm_split_min_tokens=N sets one threshold instead.
+// weights, 7 from 8M, 10 from 2M, 16 below. Rows longer than one 4096-column
+// GEMV step run as GEMV launches of two tokens at most, so there 4 tokens
+// from 32M weights: 4096 x 14336 at 4 tokens 25.9 / 31.6 (Q8_0 33.3 /
+// 39.7), at 3 25.7 / 26.1. AERO_HIP_TUNE gemm_split_min_tokens=N sets one
+// threshold instead.
 int split_min_tokens(int64_t n_rows, int64_t n_cols) {
     const int fixed = tune("gemm_split_min_tokens", 0);
     if (fixed > 0) return fixed;
     const int64_t weights = n_rows * n_cols;
+    if (n_cols > 4096 && weights >= ((int64_t)32 << 20)) return 4;
     return weights >= ((int64_t)32 << 20) ? 5
                                           : weights >= ((int64_t)8 << 20) ? 7
                                                                           : weights >= ((int64_t)2 << 20) ? 10 : 16;

@@ -930,6 +930,8 @@ GEMM_CASES = [
     ("q6_k_14336x4096_t16", 14, 14336, 4096, 16), ("q8_0_14336x4096_t5", 8, 14336, 4096, 5),
     ("iq4_xs_14336x4096_t5", 23, 14336, 4096, 5), ("iq4_xs_14336x4096_t8", 23, 14336, 4096, 8),
     ("q6_k_4096x4096_t8", 14, 4096, 4096, 8), ("q8_0_4096x4096_t8", 8, 4096, 4096, 8),
+    ("ffn_down_4096x14336_t3", 12, 4096, 14336, 3), ("ffn_down_4096x14336_t4", 12, 4096, 14336, 4),
+    ("q8_0_4096x14336_t4", 8, 4096, 14336, 4), ("attn_o_4096x8192_t4", 12, 4096, 8192, 4),
     ("ffn_gate_14336x4096_t64", 12, 14336, 4096, 64),
     ("q8_0_4096x4096", 8, 4096, 4096, 512), ("q8_0_4096x14336", 8, 4096, 14336, 512),
     ("q8_0_14336x4096_t8", 8, 14336, 4096, 8), ("q8_0_14336x4096_t16", 8, 14336, 4096, 16),

@@ -286,7 +286,8 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
 /* aero_hip_matvec with a workspace, the same call as the reference's matmul
  * (src/kernels.cpp:520-538). With enough tokens of Q4_K, Q5_K, Q8_0,
  * Q6_K (rows a multiple of 2048 columns) or IQ4_XS (of 512) (5 for matrices
- * of 32M+ weights, 7 for 8M+, 10 for 2M+, else 16: where measured faster)
+ * of 32M+ weights, 4 when their rows are longer than 4096 columns, 7 for 8M+,
+ * 10 for 2M+, else 16: where measured faster)
  * and
  * `ws` 16-byte aligned of at least aero_hip_matmul_workspace(dtype, n_cols,
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
@@ -360,7 +361,8 @@ int aero_hip_matmul(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  *   aero_hip_norm_matmul_gate_up: out[t*n_ff + r] = act(Wg[r] . h[t]) *
  *     (Wu[r] . h[t]), act an AERO_ACT_* kind.
  * The split GEMM's types (aero_hip_matmul) with enough tokens (5 when the
- * call's matrices hold 32M+ weights together, 7 for 8M+, 10 for 2M+, else 16; weights 16-byte
+ * call's matrices hold 32M+ weights together (4 for rows of more than 4096
+ * columns), 7 for 8M+, 10 for 2M+, else 16; weights 16-byte
  * aligned) run the
  * split-x fp16 GEMM with h never written: each token's sums are scaled by
  * its 1/sqrt(mean(x'^2)+eps) and act(gate)*up is formed in the GEMM
