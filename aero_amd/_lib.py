@@ -126,6 +126,8 @@ PROTOTYPES = {
                                      POINTER(vp), vp, vp, c_float, c_int, c_int64, c_int64, vp]),
     "aero_hip_norm_gate_up": (c_int, [c_int, vp, vp, c_int64, vp, vp, c_float, c_int, c_int, vp,
                                       c_int64, c_int64, c_int64, vp]),
+    "aero_hip_ssm_proj_conv": (c_int, [c_int, c_int, POINTER(vp), POINTER(c_int64), POINTER(c_int64),
+                                       POINTER(vp), vp, c_int64, vp, vp, c_int64, vp, vp]),
     "aero_hip_gated_norm_matvec": (c_int, [c_int, vp, c_int64, c_int64, vp, vp, vp, vp, c_int64,
                                            c_float, c_int64, c_int64, vp]),
     "aero_hip_gated_norm_matmul": (c_int, [c_int, vp, c_int64, c_int64, vp, vp, vp, vp, c_int64,

@@ -1116,7 +1116,35 @@ struct GemvFuse {
     const int32_t* pos;   // [n_tok] positions of this launch's tokens
     const float* inv;     // [rope_D / 2] inverse frequencies
     int sub;              // rows of <= 2048 (1) / 1024 (2) columns, no RoPE: a row a 64 >> sub lanes
+    // one token, matrix 0 = a DeltaNet layer's qkv projection: its rows go
+    // through the causal conv (kernel 4) and silu instead of to y[0]
+    const float* conv_w;  // [n_rows[0]][4] taps, or null
+    float* conv_tail;     // [3][n_rows[0]] history, conv_tl rows valid; updated
+    float* conv_out;      // [n_rows[0]]
+    int64_t conv_tl;
 };
+
+// Channel c of a DeltaNet layer's causal depthwise conv (kernel 4) over
+// [history; v] for one new token v, silu in the store, and the channel's
+// history moved on by one: the arithmetic of ssm_conv_k_kernel (ssm.hip) at
+// T = 1 (src/ssm.cpp:297-301), the history read before it is written.
+__device__ __forceinline__ void conv_fold(const GemvFuse& f, int64_t c, float v) {
+    constexpr int K = 4;
+    const int64_t C = f.n_rows[0], tl = f.conv_tl;
+    float win[K];
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const int64_t b = tl + 1 - K + j;
+        win[j] = j == K - 1 ? v : (b < 0 ? 0.0f : f.conv_tail[b * C + c]);
+        if (b >= 0) acc = acc + win[j] * f.conv_w[c * K + j];
+    }
+    f.conv_out[c] = silu_fast(acc);
+    const int keep = (int)(tl + 1 < K - 1 ? tl + 1 : K - 1);
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i)
+        if (i < keep) f.conv_tail[i * C + c] = win[K - keep + i];
+}
 
 __device__ __forceinline__ float act_rt(int kind, float v) {
     switch (kind) {
@@ -1385,8 +1413,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv64_fused_kernel(GemvFuse 
             for (int r = 0; r < R; ++r) {
                 const float v = sub_sum(acc[r][t], sub);
                 const int64_t row = r0 + (r << sub) + lrow;
-                if (lc == 0 && row < f.n_rows[m] && t < f.n_tok)
-                    f.y[m][t * f.n_rows[m] + row] = v;
+                if (lc == 0 && row < f.n_rows[m] && t < f.n_tok) {
+                    if (!PAIR && !GATED && T == 1 && m == 0 && f.conv_w != nullptr)
+                        conv_fold(f, row, v);
+                    else
+                        f.y[m][t * f.n_rows[m] + row] = v;
+                }
             }
         }
     }
@@ -1712,11 +1744,20 @@ struct GatedIn {
     int64_t w_len;
 };
 
+// a DeltaNet layer's conv (kernel 4) on matrix 0's rows (one token)
+struct ConvIn {
+    const float* w;
+    float* tail;
+    int64_t tail_len;
+    float* out;
+};
+
 static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                             const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                             const float* x, const float* norm_w, float eps, int norm, int act,
                             int64_t n_cols, int64_t n_tok, hipStream_t s, const float* d,
-                            float* xo, const RopeFold* rope, const GatedIn* gated) {
+                            float* xo, const RopeFold* rope, const GatedIn* gated,
+                            const ConvIn* conv = nullptr) {
     const char* what = gated ? "gated_norm_matvec" : (pair ? "norm_gate_up" : "norm_matvec");
     const bool quant = dtype == AERO_DTYPE_Q8_0 || dtype == AERO_DTYPE_Q4_K ||
                        dtype == AERO_DTYPE_Q5_K || dtype == AERO_DTYPE_Q6_K ||
@@ -1778,9 +1819,23 @@ static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* cons
                   what, (long long)n_tok);
         return false;
     }
+    if (conv != nullptr &&
+        (pair || d != nullptr || gated != nullptr || (rope != nullptr && rope->mats > 0) ||
+         n_tok != 1 || conv->w == nullptr || conv->tail == nullptr || conv->out == nullptr ||
+         conv->tail_len < 0 || conv->tail_len > 3)) {
+        set_error("%s: the conv fold takes one token, no residual, RoPE or gated norm, and a "
+                  "history of 0-3 rows (tail_len=%lld)", what, (long long)conv->tail_len);
+        return false;
+    }
     if (n_tok == 0) return true;
     GemvFuse f{};
     if (gated != nullptr) f.w_len = (int)gated->w_len;
+    if (conv != nullptr) {
+        f.conv_w = conv->w;
+        f.conv_tail = conv->tail;
+        f.conv_out = conv->out;
+        f.conv_tl = conv->tail_len;
+    }
     if (rope != nullptr && rope->mats > 0) {
         f.rope_mats = rope->mats;
         f.rope_D = rope->D;
@@ -1855,6 +1910,16 @@ bool gemv_fused_dev(int dtype, bool pair, int n_mat, const uint8_t* const* w,
                            n_cols, n_tok, s, d, xo, rope, nullptr);
 }
 
+bool gemv_conv_dev(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
+                   const int64_t* n_rows, float* const* y, const float* x, int64_t n_cols,
+                   const float* conv_w, float* tail, int64_t tail_len, float* conv_out,
+                   hipStream_t s) {
+    const ConvIn c{conv_w, tail, tail_len, conv_out};
+    return gemv_fused_impl(dtype, false, n_mat, w, w_bytes, n_rows, y, x, nullptr, 0.f, -1,
+                           AERO_ACT_IDENTITY, n_cols, 1, s, nullptr, nullptr, nullptr, nullptr,
+                           &c);
+}
+
 bool gemv_gated_dev(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows, float* y,
                     const float* x, const float* z, const float* norm_w, int64_t w_len,
                     float eps, int64_t n_cols, int64_t n_tok, hipStream_t s) {
@@ -1880,6 +1945,20 @@ int aero_hip_norm_matvec(int dtype, int n_mat, const uint8_t* const* w, const in
     return aero::gemv_fused_dev(dtype, false, n_mat, w, w_bytes, n_rows, y, x, norm_w, eps, norm,
                                 AERO_ACT_IDENTITY, n_cols, n_tok, (hipStream_t)stream, nullptr,
                                 nullptr, nullptr) ? 1 : 0;
+}
+
+int aero_hip_ssm_proj_conv(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
+                           const int64_t* n_rows, float* const* y, const float* x,
+                           int64_t n_cols, const float* conv_w, float* tail, int64_t tail_len,
+                           float* conv_out, void* stream) {
+    aero::clear_error();
+    if (w == nullptr || w_bytes == nullptr || n_rows == nullptr || y == nullptr || n_mat < 1 ||
+        n_mat > 4) {
+        aero::set_error("ssm_proj_conv: 1-4 matrices with their sizes and outputs");
+        return 0;
+    }
+    return aero::gemv_conv_dev(dtype, n_mat, w, w_bytes, n_rows, y, x, n_cols, conv_w, tail,
+                               tail_len, conv_out, (hipStream_t)stream) ? 1 : 0;
 }
 
 int aero_hip_gated_norm_matvec(int dtype, const uint8_t* w, int64_t w_bytes, int64_t n_rows,

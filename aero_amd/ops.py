@@ -299,6 +299,34 @@ def norm_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceAr
 _norm_mm_ws = Workspace("norm GEMM")
 
 
+def ssm_proj_conv(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_cols: int,
+                  conv_w: DeviceArray, tail: DeviceArray, tail_len: int, conv_out: DeviceArray,
+                  stream: Stream | None = None) -> int:
+    """One token of a DeltaNet layer's input projections (up to 4 matrices of
+    one type sharing x) with matrix 0's rows (qkv) through the causal conv of
+    kernel 4 and silu into conv_out, the history tail [3, n_rows[0]] moved on
+    in place (src/ssm.cpp:289-315,297-301); ys[0] is not written. Returns the
+    history's new length."""
+    k = len(ws)
+    if not 1 <= k <= 4 or len(ys) != k or len(n_rows) != k:
+        raise ValueError("ssm_proj_conv: 1-4 matrices, one output and row count each")
+    C = int(n_rows[0])
+    _need(x, n_cols, np.float32, "x")
+    _need(conv_w, 4 * C, np.float32, "conv_w")
+    _need(tail, 3 * C, np.float32, "tail")
+    _need(conv_out, C, np.float32, "conv_out")
+    for y, n in zip(ys, n_rows):
+        _need(y, int(n), np.float32, "y")
+    wp = (ctypes.c_void_p * k)(*[w.ptr for w in ws])
+    wb = (ctypes.c_int64 * k)(*[w.nbytes for w in ws])
+    nr = (ctypes.c_int64 * k)(*[int(n) for n in n_rows])
+    yp = (ctypes.c_void_p * k)(*[y.ptr for y in ys])
+    _lib.check(_lib.lib().aero_hip_ssm_proj_conv(int(dtype), k, wp, wb, nr, yp, x.ptr, n_cols,
+                                                 conv_w.ptr, tail.ptr, int(tail_len),
+                                                 conv_out.ptr, _s(stream)), "ssm_proj_conv")
+    return min(3, int(tail_len) + 1)
+
+
 def gated_norm_matvec(dtype: int, w: DeviceArray, x: DeviceArray, z: DeviceArray,
                       norm_w: DeviceArray, y: DeviceArray, n_rows: int, n_cols: int,
                       n_tok: int, eps: float, stream: Stream | None = None) -> None:

@@ -26,9 +26,10 @@ ENV = "AERO_GPU_OPS"
 # GPU: the embedding gather with the first norm, the norms (and residual
 # adds) folded into the projections that consume them, the act-mul folded
 # into the gate/up projection, RoPE folded into the q/k projection's
-# epilogue. AERO_GPU_FUSE=none turns them off (the same ops then run as
+# epilogue, a DeltaNet layer's conv folded into its input projections'
+# epilogue at one token. AERO_GPU_FUSE=none turns them off (the same ops then run as
 # separate kernels); unset means all on.
-FUSIONS = ("embed_norm", "norm_gemm", "act_gemm", "rope_gemm")
+FUSIONS = ("embed_norm", "norm_gemm", "act_gemm", "rope_gemm", "conv_gemm")
 FUSE_ENV = "AERO_GPU_FUSE"
 
 

@@ -12,13 +12,15 @@ recurrent state and conv history kept on the device between calls:
 
 x is the layer's input, already normed (the reference's caller passes it so).
 Projections of one weight type that read x go to the GPU in one launch (up
-to four matrices); the silu runs in the conv's store, and the scan reads q,
-k and v as strided slices of the conv output (scan_strided, :128-142), so
-five launches carry the layer (the scan adds its prep pass and, from 128
+to four matrices); the silu runs in the conv's store, and the scan reads
+q, k and v as strided slices of the conv output (scan_strided, :128-142),
+so five launches carry the layer (the scan adds its prep pass and, from 128
 tokens, the chunk pre-pass). The gated norm runs inside the output
 projection (fusion "norm_gemm"): in its GEMV prologue at one or two tokens,
 in the split GEMM's x pre-pass on that path. At one or two tokens the conv
-also writes its history: four launches. The gated norm site consults aero_amd.select
+also writes its history, and at one token (fusion "conv_gemm": one weight
+type for the four input projections) the conv and silu run on the qkv rows
+in the projections' GEMV epilogue: three launches. The gated norm site consults aero_amd.select
 (op "gated_norm") like the decoder block's sites; the projections, conv and
 scan have no host path. With every op on the GPU, `forward` can be recorded
 as a Plan: the recording keeps the conv history length of its first call,
@@ -122,6 +124,11 @@ class SsmStep:
         for name, t in zip(PROJ[:4], cfg.wtypes[:4]):
             groups.setdefault(t, []).append(name)
         self.groups = [(t, names, [outs[n] for n in names]) for t, names in groups.items()]
+        # decode folds the conv into the projections' GEMV: one weight type for
+        # the four, kernel 4, rows of whole 16 bytes (the 64-column lane GEMV)
+        bv, bb = W.BLOCK[cfg.wtypes[0]]
+        self.conv_fold = (len(self.groups) == 1 and cfg.conv_kernel == 4 and
+                          cfg.hidden % bv == 0 and (cfg.hidden // bv * bb) % 16 == 0)
         self.reset()
 
     def reset(self) -> None:
@@ -144,12 +151,23 @@ class SsmStep:
             raise ValueError(f"{T} tokens: outside 1..{self.max_tokens}")
         shapes = cfg.shapes()
         x = self.x.view((T, cfg.hidden))
-        for t, names, ys in self.groups:
-            ops.norm_matmul(t, [dev[n] for n in names], x, ys, [shapes[n][0] for n in names],
-                            cfg.hidden, T, norm=False, stream=stream)
-        self.tail_len = ops.ssm_conv(self.qkv, dev["conv1d"], self.tail, self.tail_len,
-                                     self.tail, self.conv, T, cfg.qkv, cfg.conv_kernel,
-                                     silu=True, stream=stream)
+        if T == 1 and self.conv_fold and select.fusion_enabled("conv_gemm",
+                                                               self.fusions.get("conv_gemm")):
+            # one token: the conv and silu on the qkv rows in the projections'
+            # GEMV epilogue, the history moved on there too
+            (t, names, ys), = self.groups
+            self.tail_len = ops.ssm_proj_conv(t, [dev[n] for n in names], x, ys,
+                                              [shapes[n][0] for n in names], cfg.hidden,
+                                              dev["conv1d"], self.tail, self.tail_len, self.conv,
+                                              stream=stream)
+        else:
+            for t, names, ys in self.groups:
+                ops.norm_matmul(t, [dev[n] for n in names], x, ys,
+                                [shapes[n][0] for n in names], cfg.hidden, T, norm=False,
+                                stream=stream)
+            self.tail_len = ops.ssm_conv(self.qkv, dev["conv1d"], self.tail, self.tail_len,
+                                         self.tail, self.conv, T, cfg.qkv, cfg.conv_kernel,
+                                         silu=True, stream=stream)
         nk_d = cfg.n_k * cfg.head_dim
         ops.ssm_scan(self.conv, self.conv, self.conv, self.alpha, self.beta, dev["a_log"],
                      dev["dt_bias"], self.state, self.o, T, cfg.n_k, cfg.n_v, cfg.head_dim,

@@ -319,6 +319,22 @@ int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
                           int64_t w_bytes, const float* x, const float* norm_w, float eps,
                           int norm, int act, float* out, int64_t n_ff, int64_t n_cols,
                           int64_t n_tok, void* stream);
+/* A gated-DeltaNet layer's input projections and its causal conv for one
+ * token (decode), in one launch: matrices 0 .. n_mat-1 (1-4, one type and
+ * width, weights as aero_hip_norm_matvec) times x as aero_hip_norm_matvec with
+ * no norm, except that matrix 0's rows (the qkv projection, n_rows[0]
+ * channels) go through the conv of kernel 4 over the channel's history and
+ * silu: conv_out[c] = silu(sum_j conv_w[c*4 + j] * [tail; row][tail_len - 3
+ * + j]) (rows before the history count as absent), and the history tail
+ * [3][n_rows[0]] (tail_len rows valid) is moved on by one row in place
+ * (min(3, tail_len + 1) rows valid after). It replaces the projections
+ * (src/ssm.cpp:289-315) and the conv (:297-301) of aero_ssm_forward_q, as
+ * aero_hip_norm_matvec followed by aero_hip_ssm_conv_silu; y[0] is not
+ * written. */
+int aero_hip_ssm_proj_conv(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
+                           const int64_t* n_rows, float* const* y, const float* x,
+                           int64_t n_cols, const float* conv_w, float* tail, int64_t tail_len,
+                           float* conv_out, void* stream);
 /* The gated-DeltaNet norm folded into the next projection's GEMV:
  * y[t*n_rows + r] = sum_c W[r, c] * on[t, c], with
  * on[t, c] = x[t, c] / sqrt(mean_c x[t]^2 + eps) * norm_w[c % w_len] * silu(z[t, c])

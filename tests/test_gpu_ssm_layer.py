@@ -19,9 +19,9 @@ from aero_amd.device import Plan, Stream
 pytestmark = pytest.mark.gpu
 
 
-def run_chain(oracle, cfg, seed, calls):
+def run_chain(oracle, cfg, seed, calls, fusions=None):
     wts = S.SsmWeights(cfg, seed=seed)
-    step = S.SsmStep(cfg, wts, max_tokens=max(calls))
+    step = S.SsmStep(cfg, wts, max_tokens=max(calls), fusions=fusions)
     h = wts.host
     case = dict(dts=list(cfg.wtypes), weights=[h[n] for n in S.PROJ], a_log=h["a_log"],
                 dt_bias=h["dt_bias"], conv1d=h["conv1d"], norm=h["norm"], n_k=cfg.n_k,
@@ -57,6 +57,12 @@ def run_chain(oracle, cfg, seed, calls):
 def test_ssm_layer_vs_oracle(hip, oracle, name, cfg, calls):
     print(f"ssm layer {name}", flush=True)
     run_chain(oracle, cfg, 5 + len(name), calls)
+
+
+def test_ssm_layer_decode_conv_unfolded(hip, oracle):
+    """The same chain with the conv as its own launch at one token."""
+    cfg = S.SsmConfig(512, 4, 8, 128, 4, (W.Q4_K,) * 5)
+    run_chain(oracle, cfg, 17, (1, 1, 40, 1, 1), fusions={"conv_gemm": False})
 
 
 def test_ssm_layer_plan_replay(hip, oracle):
@@ -96,18 +102,20 @@ def test_ssm_layer_plan_replay(hip, oracle):
 
 
 def test_ssm_layer_decode_launches(hip):
-    """Decode is four launches (projections of x, the conv writing its own
-    history, scan, gated norm in the output projection's GEMV), five with the
-    norm_gemm fusion off (the gated norm its own launch)."""
+    """Decode is three launches (projections of x with the conv and silu on
+    the qkv rows in their epilogue, scan, gated norm in the output
+    projection's GEMV); four with the conv_gemm fusion off (the conv writing
+    its own history) or with norm_gemm off (the gated norm its own launch)."""
     cfg = S.SsmConfig(512, 4, 8, 128, 4, (W.Q4_K,) * 5)
     wts = S.SsmWeights(cfg, seed=1)
-    for fuse, want in ((True, 4), (False, 5)):
-        step = S.SsmStep(cfg, wts, max_tokens=8, fusions={"norm_gemm": fuse})
+    for fus, want in (({}, 3), ({"conv_gemm": False}, 4), ({"norm_gemm": False}, 4),
+                      ({"conv_gemm": False, "norm_gemm": False}, 5)):
+        step = S.SsmStep(cfg, wts, max_tokens=8, fusions=fus)
         step.forward(4)
         plan = Plan()
         with plan:
             step.forward(1)
-        assert len(plan) == want, (fuse, len(plan))
+        assert len(plan) == want, (fus, len(plan))
         plan.destroy()
 
 
