@@ -127,3 +127,41 @@ def test_ssm_layer_refusals(hip):
     step = S.SsmStep(cfg, S.SsmWeights(cfg), max_tokens=8)
     with pytest.raises(ValueError, match="tokens"):
         step.forward(9)
+
+
+@pytest.mark.parametrize("hidden", [1024, 2048])
+@pytest.mark.parametrize("tail_len", [0, 1, 2, 3])
+def test_ssm_proj_conv_equals_separate_launches(hip, hidden, tail_len):
+    """aero_hip_ssm_proj_conv against the same projections (norm_matmul with
+    no norm) followed by the conv with silu, at every history length: the
+    conv output and the moved history bit for bit (the same arithmetic in
+    the same order), the other projections likewise."""
+    from aero_amd import ops
+    from aero_amd.device import DeviceArray as DA
+    cfg = S.SsmConfig(hidden, 2, 4, 64, 4, (W.Q4_K,) * 5)
+    wts = S.SsmWeights(cfg, seed=tail_len)
+    h, d = wts.host, wts.dev
+    rng = np.random.default_rng(71 + tail_len)
+    x = DA.from_numpy(rng.standard_normal((1, hidden)).astype(np.float32))
+    tail0 = rng.standard_normal((3, cfg.qkv)).astype(np.float32)
+    names = S.PROJ[:4]
+    rows = [cfg.shapes()[n][0] for n in names]
+    ws = [d[n] for n in names]
+    # separate launches
+    ys_a = [DA.empty((1, r)) for r in rows]
+    ops.norm_matmul(W.Q4_K, ws, x, ys_a, rows, hidden, 1, norm=False)
+    tail_a, conv_a = DA.from_numpy(tail0), DA.empty((1, cfg.qkv))
+    tl_a = ops.ssm_conv(ys_a[0], d["conv1d"], tail_a, tail_len, tail_a, conv_a, 1, cfg.qkv, 4,
+                        silu=True)
+    # one launch
+    ys_b = [DA.empty((1, r)) for r in rows]
+    tail_b, conv_b = DA.from_numpy(tail0), DA.empty((1, cfg.qkv))
+    tl_b = ops.ssm_proj_conv(W.Q4_K, ws, x, ys_b, rows, hidden, d["conv1d"], tail_b, tail_len,
+                             conv_b)
+    assert tl_a == tl_b == min(3, tail_len + 1)
+    assert np.array_equal(conv_a.numpy(), conv_b.numpy())
+    assert np.array_equal(tail_a.numpy()[:tl_a], tail_b.numpy()[:tl_b])
+    for ya, yb in zip(ys_a[1:], ys_b[1:]):
+        assert np.array_equal(ya.numpy(), yb.numpy())
+    with pytest.raises(Exception, match="history"):
+        ops.ssm_proj_conv(W.Q4_K, ws, x, ys_b, rows, hidden, d["conv1d"], tail_b, 4, conv_b)
