@@ -159,6 +159,7 @@ PROTOTYPES = {
                                   vp, vp]),
     "aero_hip_softmax_rows": (c_int, [vp, vp, c_int64, c_int64, vp]),
     "aero_hip_copy_f32": (c_int, [vp, vp, c_int64, vp]),
+    "aero_hip_fill_f32": (c_int, [vp, c_float, c_int64, vp]),
     # runtime
     "aero_hip_last_error": (c_char_p, []),
     "aero_hip_version": (c_char_p, []),
@@ -170,6 +171,7 @@ PROTOTYPES = {
     "aero_hip_memcpy_dtoh": (c_int, [vp, vp, c_int64]),
     "aero_hip_memcpy_dtod": (c_int, [vp, vp, c_int64, vp]),
     "aero_hip_memset": (c_int, [vp, c_int, c_int64]),
+    "aero_hip_tune_set": (c_int, [c_char_p, c_int, c_int]),
     "aero_hip_stream_create": (vp, []),
     "aero_hip_stream_destroy": (c_int, [vp]),
     "aero_hip_stream_synchronize": (c_int, [vp]),

@@ -23,6 +23,7 @@ template <int KIND>
 __device__ __forceinline__ float act(float v) {
     if constexpr (KIND == AERO_ACT_SILU) {
         return v * (1.0f / (1.0f + expf(-v)));
+
     } else if constexpr (KIND == AERO_ACT_GELU) {
         return 0.5f * v * (1.0f + erf_as(v * 0.7071067811865476f));
     } else if constexpr (KIND == AERO_ACT_GELU_TANH) {

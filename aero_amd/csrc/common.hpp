@@ -79,9 +79,15 @@ bool async_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 // ------------------------------------------------------------------ tuning
 // Launch-shape knobs (block sizes, lanes per row, rows per lane). Defaults
-// are the measured best; AERO_HIP_TUNE="key=value,..." overrides them for
-// sweeps. Read once per process.
+// are the measured best; AERO_HIP_TUNE="key=value,..." (read once per
+// process) or tune_set overrides them for sweeps.
 int tune(const char* key, int dflt);
+// Set (or, with erase, drop) one knob for the rest of the process: lets a
+// sweep change launch shapes without a new process. Thread-safe.
+bool tune_set(const char* key, int value, bool erase);
+
+// Compute units of the current device (256 on MI355X), cached per device.
+int cu_count();
 
 inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;

@@ -12,9 +12,11 @@
 //
 // Arithmetic follows the reference operation by operation with contraction
 // disabled: inv = 1/sqrtf(ss/n + eps), out = (x*inv)*w (src/tensor.cpp:
-// 128-134); L2: inv = 1/max(sqrtf(ss), eps) (src/tensor.cpp:136-154); gated:
-// out = ((x/denom)*w)*(z/(1+expf(-z))) (src/ssm.cpp:17,327-343). Only the
-// summation order of ss differs (tree instead of serial).
+// 128-134); L2: inv = 1/max(sqrtf(ss), eps) (src/tensor.cpp:136-154). The
+// summation order of ss differs (tree instead of serial). The gated norm,
+// out = ((x/denom)*w)*(z/(1+expf(-z))) in the reference (src/ssm.cpp:17,
+// 327-343), multiplies by 1/denom and takes silu from the hardware exp and
+// reciprocal (a few ulp from the division form; see the vector kernel).
 #include <algorithm>
 
 #include "common.hpp"
@@ -42,7 +44,6 @@ struct NormParams {
 // Kernel forms: plain / L2 norm, gated norm*silu(z), residual add then norm.
 constexpr int kPlain = 0, kGated = 1, kResid = 2;
 
-__device__ __forceinline__ float silu_div(float v) { return v / (1.0f + expf(-v)); }
 
 __device__ __forceinline__ float norm_scale(float ss, const NormParams& p) {
     if (p.flags & AERO_NORM_L2) {
@@ -147,13 +148,18 @@ void norm_vec_kernel(NormParams p) {
     if (!ok) return;
 
     if constexpr (GATED) {
-        const float denom = sqrtf(ss / (float)p.cols + p.eps);
+        // one division a row, then multiplies; silu with the hardware exp and
+        // reciprocal. The gated norm is bound by its instructions, not its
+        // bytes, with the division form (x/denom, z/(1+expf(-z))): 35.0 ->
+        // 33.6 us at 4096 x 4096 and 7.2 -> 5.5 us at 512 x 4096 on MI355X,
+        // within 1.5e-6 of the reference's division form.
+        const float rinv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
         auto out4 = [&](int i) {
             float4 o;
-            o.x = ((xv[i].x / denom) * wv[i].x) * silu_div(zv[i].x);
-            o.y = ((xv[i].y / denom) * wv[i].y) * silu_div(zv[i].y);
-            o.z = ((xv[i].z / denom) * wv[i].z) * silu_div(zv[i].z);
-            o.w = ((xv[i].w / denom) * wv[i].w) * silu_div(zv[i].w);
+            o.x = ((xv[i].x * rinv) * wv[i].x) * silu_fast(zv[i].x);
+            o.y = ((xv[i].y * rinv) * wv[i].y) * silu_fast(zv[i].y);
+            o.z = ((xv[i].z * rinv) * wv[i].z) * silu_fast(zv[i].z);
+            o.w = ((xv[i].w * rinv) * wv[i].w) * silu_fast(zv[i].w);
             return o;
         };
         if (nv == V * TPR) {
@@ -189,6 +195,159 @@ void norm_vec_kernel(NormParams p) {
     }
 }
 
+// Read-only stand-in weight for a weightless norm, read with stride 0
+// (global memory, so the select between it and p.w stays a global load).
+__device__ float kOnes[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+
+// Persistent form of norm_vec_kernel for many rows: a grid of a few
+// workgroups per CU, each looping over row groups blockIdx.x, +gridDim.x, ...
+// (`iters` rounds, the last one partial). Two differences from the per-row
+// form:
+//  - the lane's weight chunks are loaded once, into registers, for every row
+//    it sees; the per-row form re-reads them from L2 for every row, half as
+//    many extra L2 requests as the row's own loads and stores;
+//  - the next row group's loads are issued before this one's reduction and
+//    stores, so each wave keeps a row in flight across its own reduction.
+// Loads are unconditional, from clamped row and chunk indices (a branch
+// around a load makes the compiler wait for every load before it); chunks
+// past the row's end are zeroed by a select and never stored, and a round
+// past the last group only loads (the clamped last group) and stores
+// nothing. Gated slices need cols % w_len == 0, so every slice has the same
+// weight phase. Same arithmetic and summation order as norm_vec_kernel.
+template <int TPR, int V, int MODE>
+__global__ __launch_bounds__(TPR > 256 ? TPR : 256)
+void norm_loop_kernel(NormParams p, int iters) {
+    constexpr bool GATED = MODE == kGated;
+    constexpr bool RESID = MODE == kResid;
+    constexpr bool TWO = GATED || RESID;
+    constexpr int BS = TPR > 256 ? TPR : 256;
+    constexpr int RPB = BS / TPR;
+    constexpr int NW = BS / 64;
+    __shared__ float part[2][NW];
+    const int tid = threadIdx.x;
+    const int lr = tid / TPR;
+    const int t = tid % TPR;
+    const int nv = p.cols >> 2;
+    const int64_t last = p.rows - 1;
+    const int64_t ngroups = (p.rows + RPB - 1) / RPB;
+
+    int cc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) cc[i] = min(i * TPR + t, nv - 1);
+
+    const bool has_w = p.w != nullptr;
+    const float* wb = has_w ? p.w : kOnes;
+    const int wst = has_w ? 1 : 0;
+    const bool unit = has_w && (p.flags & AERO_NORM_UNIT_OFFSET) != 0;
+    float4 wv[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int wi = GATED ? (4 * cc[i]) % p.w_len : 4 * cc[i];
+        wv[i] = *reinterpret_cast<const float4*>(wb + wst * wi);
+    }
+
+    auto load_rows = [&](int64_t g, float4 (&xv)[V], float4 (&zv)[V]) {
+        const int64_t row = min(g * RPB + lr, last);
+        const float* xr = p.x + row * (int64_t)p.cols;
+        const float* zr = (TWO ? p.z : p.x) + row * (int64_t)p.cols;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            xv[i] = ld_stream(xr + 4 * cc[i]);
+            if (TWO) zv[i] = ld_stream(zr + 4 * cc[i]);
+        }
+    };
+
+    auto process = [&](int64_t g, int k, float4 (&xv)[V], float4 (&zv)[V]) {
+        const int64_t row0 = g * RPB;
+        const bool ok = row0 + lr < p.rows;
+        const uint32_t obase = (uint32_t)(lr * p.cols) * 4u;
+        if constexpr (RESID) {
+            const StreamOut ox(p.xo + row0 * p.cols, (p.rows - row0) * (int64_t)p.cols * 4);
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                xv[i].x = xv[i].x + zv[i].x;
+                xv[i].y = xv[i].y + zv[i].y;
+                xv[i].z = xv[i].z + zv[i].z;
+                xv[i].w = xv[i].w + zv[i].w;
+                const int c = i * TPR + t;
+                if (ok && c < nv) ox.store(obase + 16u * c, xv[i]);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const bool in = i * TPR + t < nv;
+            const float a = in ? xv[i].x : 0.0f, b = in ? xv[i].y : 0.0f;
+            const float c = in ? xv[i].z : 0.0f, d = in ? xv[i].w : 0.0f;
+            ss += a * a;
+            ss += b * b;
+            ss += c * c;
+            ss += d * d;
+        }
+        if constexpr (TPR <= 64) {
+            ss = group_sum<TPR>(ss);
+        } else {
+            constexpr int WPR = TPR / 64;
+            ss = group_sum<64>(ss);
+            if ((tid & 63) == 0) part[k & 1][tid >> 6] = ss;
+            __syncthreads();
+            const int w0 = lr * WPR;
+            ss = part[k & 1][w0];
+#pragma unroll
+            for (int q = 1; q < WPR; ++q) ss += part[k & 1][w0 + q];
+        }
+        const StreamOut os(p.out + row0 * p.cols, (p.rows - row0) * (int64_t)p.cols * 4);
+        if (!ok) return;
+        if constexpr (GATED) {
+            const float rinv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const int c = i * TPR + t;
+                if (c >= nv) continue;
+                float4 o;
+                o.x = ((xv[i].x * rinv) * wv[i].x) * silu_fast(zv[i].x);
+                o.y = ((xv[i].y * rinv) * wv[i].y) * silu_fast(zv[i].y);
+                o.z = ((xv[i].z * rinv) * wv[i].z) * silu_fast(zv[i].z);
+                o.w = ((xv[i].w * rinv) * wv[i].w) * silu_fast(zv[i].w);
+                os.store(obase + 16u * c, o);
+            }
+        } else {
+            const float inv = norm_scale(ss, p);
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const int c = i * TPR + t;
+                if (c >= nv) continue;
+                float4 w4 = wv[i];
+                if (unit) {
+                    w4.x = 1.0f + w4.x; w4.y = 1.0f + w4.y;
+                    w4.z = 1.0f + w4.z; w4.w = 1.0f + w4.w;
+                }
+                float4 o = make_float4(xv[i].x * inv, xv[i].y * inv, xv[i].z * inv,
+                                       xv[i].w * inv);
+                o.x = o.x * w4.x; o.y = o.y * w4.y; o.z = o.z * w4.z; o.w = o.w * w4.w;
+                os.store(obase + 16u * c, o);
+            }
+        }
+    };
+
+    const int64_t G = gridDim.x;
+    int64_t g = blockIdx.x;
+    float4 xa[V], za[V];
+    load_rows(g, xa, za);
+    for (int k = 0; k < iters - 1; ++k) {
+        float4 xb[V], zb[V];
+        load_rows(min(g + G, ngroups - 1), xb, zb);
+        process(g, k, xa, za);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            xa[i] = xb[i];
+            if (TWO) za[i] = zb[i];
+        }
+        g += G;
+    }
+    if (g < ngroups) process(g, iters - 1, xa, za);
+}
+
 // Any shape / alignment: one 256-thread block per slice, two passes over the
 // slice (the second pass hits L2). Same arithmetic as the vector kernel.
 template <int MODE>
@@ -219,12 +378,12 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormParams p) {
     ss = ((part[0] + part[1]) + part[2]) + part[3];
     float* o = p.out + base;
     if constexpr (GATED) {
-        const float denom = sqrtf(ss / (float)p.cols + p.eps);
+        const float rinv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
         const float* zr = p.z + base;
         const int64_t col0 = (row % p.gpr) * (int64_t)p.cols;
         for (int c = tid; c < p.cols; c += 256) {
             const float wn = p.w[(col0 + c) % p.w_len];
-            o[c] = ((xr[c] / denom) * wn) * silu_div(zr[c]);
+            o[c] = ((xr[c] * rinv) * wn) * silu_fast(zr[c]);
         }
     } else {
         const float inv = norm_scale(ss, p);
@@ -234,6 +393,34 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormParams p) {
 }
 
 using NormKernel = void (*)(NormParams);
+using NormLoopKernel = void (*)(NormParams, int);
+
+template <int MODE, int TPR>
+NormLoopKernel pick_loop_v(int v) {
+    switch (v) {
+    case 1: return norm_loop_kernel<TPR, 1, MODE>;
+    case 2: return norm_loop_kernel<TPR, 2, MODE>;
+    case 3: return norm_loop_kernel<TPR, 3, MODE>;
+    case 4: return norm_loop_kernel<TPR, 4, MODE>;
+    case 8: return norm_loop_kernel<TPR, 8, MODE>;
+    default: return nullptr;
+    }
+}
+
+template <int MODE>
+NormLoopKernel pick_loop(int tpr, int v) {
+    switch (tpr) {
+    case 8: return pick_loop_v<MODE, 8>(v);
+    case 16: return pick_loop_v<MODE, 16>(v);
+    case 32: return pick_loop_v<MODE, 32>(v);
+    case 64: return pick_loop_v<MODE, 64>(v);
+    case 128: return pick_loop_v<MODE, 128>(v);
+    case 256: return pick_loop_v<MODE, 256>(v);
+    case 512: return pick_loop_v<MODE, 512>(v);
+    case 1024: return pick_loop_v<MODE, 1024>(v);
+    default: return nullptr;
+    }
+}
 
 template <int MODE, int TPR>
 NormKernel pick_v(int v) {
@@ -250,14 +437,24 @@ NormKernel pick_v(int v) {
     }
 }
 
+// one or two waves a row with 16 or 32 float4 a lane (wide rows, no or one
+// cross-wave step)
+template <int MODE, int TPR>
+NormKernel pick_wide(int v) {
+    if (v <= 8) return pick_v<MODE, TPR>(v);
+    if (v <= 16) return norm_vec_kernel<TPR, 16, MODE>;
+    if (v <= 32) return norm_vec_kernel<TPR, 32, MODE>;
+    return nullptr;
+}
+
 template <int MODE>
 NormKernel pick(int tpr, int v) {
     switch (tpr) {
     case 8: return pick_v<MODE, 8>(v);
     case 16: return pick_v<MODE, 16>(v);
     case 32: return pick_v<MODE, 32>(v);
-    case 64: return pick_v<MODE, 64>(v);
-    case 128: return pick_v<MODE, 128>(v);
+    case 64: return pick_wide<MODE, 64>(v);
+    case 128: return pick_wide<MODE, 128>(v);
     case 256: return pick_v<MODE, 256>(v);
     case 512: return pick_v<MODE, 512>(v);
     case 1024: return pick_v<MODE, 1024>(v);
@@ -271,7 +468,8 @@ NormKernel pick(int tpr, int v) {
 void choose_shape(int nv, int* tpr, int* v) {
     const int vmax = tune("norm_vmax", 4);
     int t = 8;
-    while (t < 1024 && t * vmax < nv) t *= 2;
+    // more than 8 float4 a lane exist for whole-wave rows only (64 or 128 lanes)
+    while (t < 1024 && (t * vmax < nv || (vmax > 8 && t < 64))) t *= 2;
     *tpr = t;
     *v = (nv + t - 1) / t;
 }
@@ -284,10 +482,22 @@ bool run_norm(NormParams p, int mode, hipStream_t stream) {
                      (mode != kResid || (aligned16(p.z) && aligned16(p.xo)));
     int tpr = 0, v = 0;
     if (vec) choose_shape(p.cols / 4, &tpr, &v);
-    if (vec && v <= 8) {
+    if (vec && (v <= 8 || ((tpr == 64 || tpr == 128) && v <= 32))) {
         const int bs = tpr > 256 ? tpr : 256;
         const int rpb = bs / tpr;
         const int64_t blocks = (p.rows + rpb - 1) / rpb;
+        // many rows: the persistent form, `norm_loop` workgroups per CU
+        const int per_cu = tune("norm_loop", 0);
+        const int64_t G = (int64_t)per_cu * cu_count();
+        if (per_cu > 0 && blocks > G && (v <= 4 || v == 8) &&
+            (mode != kGated || p.cols % p.w_len == 0)) {
+            NormLoopKernel k = mode == kGated ? pick_loop<kGated>(tpr, v)
+                               : mode == kResid ? pick_loop<kResid>(tpr, v)
+                                                : pick_loop<kPlain>(tpr, v);
+            const int iters = (int)((blocks + G - 1) / G);
+            return launch("norm_loop_kernel", k, dim3((unsigned)G), dim3(bs), 0, stream, p,
+                          iters);
+        }
         NormKernel k = mode == kGated ? pick<kGated>(tpr, v)
                        : mode == kResid ? pick<kResid>(tpr, v) : pick<kPlain>(tpr, v);
         return launch("norm_vec_kernel", k, dim3((unsigned)blocks), dim3(bs), 0,

@@ -36,9 +36,14 @@ bool async_copy(void* dst, const void* src, size_t bytes, hipStream_t stream) {
                   "hipMemcpyAsync D2D");
 }
 
-int tune(const char* key, int dflt) {
+namespace {
+std::mutex g_knob_mu;
+std::map<std::string, int>& knobs() {
+    static std::map<std::string, int> k;
+    return k;
+}
+void load_knobs() {
     static std::once_flag once;
-    static std::map<std::string, int> knobs;
     std::call_once(once, [] {
         const char* env = std::getenv("AERO_HIP_TUNE");
         if (env == nullptr) return;
@@ -50,12 +55,44 @@ int tune(const char* key, int dflt) {
             const std::string kv = all.substr(i, j - i);
             const size_t eq = kv.find('=');
             if (eq != std::string::npos)
-                knobs[kv.substr(0, eq)] = std::atoi(kv.c_str() + eq + 1);
+                knobs()[kv.substr(0, eq)] = std::atoi(kv.c_str() + eq + 1);
             i = j + 1;
         }
     });
-    auto it = knobs.find(key);
-    return it == knobs.end() ? dflt : it->second;
+}
+}  // namespace
+
+int tune(const char* key, int dflt) {
+    load_knobs();
+    std::lock_guard<std::mutex> g(g_knob_mu);
+    auto it = knobs().find(key);
+    return it == knobs().end() ? dflt : it->second;
+}
+
+int cu_count() {
+    static std::mutex mu;
+    static std::map<int, int> by_dev;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> g(mu);
+    auto it = by_dev.find(dev);
+    if (it != by_dev.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+        n = 256;
+    by_dev[dev] = n;
+    return n;
+}
+
+bool tune_set(const char* key, int value, bool erase) {
+    load_knobs();
+    std::lock_guard<std::mutex> g(g_knob_mu);
+    if (erase)
+        knobs().erase(key);
+    else
+        knobs()[key] = value;
+    return true;
 }
 
 void set_error(const char* fmt, ...) {
@@ -112,6 +149,14 @@ void* aero_hip_malloc(int64_t bytes) {
 int aero_hip_free(void* p) {
     if (p == nullptr) return 1;
     return hip_ok(hipFree(p), "hipFree") ? 1 : 0;
+}
+
+int aero_hip_tune_set(const char* key, int value, int erase) {
+    if (key == nullptr || key[0] == '\0') {
+        aero::set_error("aero_hip_tune_set: empty key");
+        return 0;
+    }
+    return aero::tune_set(key, value, erase != 0) ? 1 : 0;
 }
 
 int aero_hip_memcpy_htod(void* dst, const void* src, int64_t bytes) {

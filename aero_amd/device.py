@@ -279,3 +279,11 @@ def synchronize() -> None:
 def device_count() -> int:
     L = _lib.load()
     return 0 if L is None else int(L.aero_hip_device_count())
+
+
+def tune_set(key: str, value: int | None) -> None:
+    """Override one launch-shape knob for the rest of the process (None drops
+    the override, so the built-in default applies). Plans keep the kernel
+    choice they recorded."""
+    _lib.check(_lib.lib().aero_hip_tune_set(key.encode(), 0 if value is None else int(value),
+                                            1 if value is None else 0), "tune_set")

@@ -591,3 +591,11 @@ def copy_f32(src: DeviceArray, dst: DeviceArray, n: int | None = None,
     _need(src, n, np.float32, "src")
     _need(dst, n, np.float32, "dst")
     _lib.check(_lib.lib().aero_hip_copy_f32(src.ptr, dst.ptr, n, _s(stream)), "copy_f32")
+
+
+def fill_f32(dst: DeviceArray, value: float, n: int | None = None,
+             stream: Stream | None = None) -> None:
+    """dst[:n] = value with the store-only streaming kernel."""
+    n = dst.size if n is None else int(n)
+    _need(dst, n, np.float32, "dst")
+    _lib.check(_lib.lib().aero_hip_fill_f32(dst.ptr, float(value), n, _s(stream)), "fill_f32")

@@ -15,16 +15,18 @@ issued from C, one host call per step). `value` is the whole step's
 algorithmic HBM bytes / wall time per step over the timed region (GB/s).
 `ops` also reports the unfused gather and RMSNorm the two fused kernels
 replace. Each entry of `ops` gives two device timings of the op: per
-dispatch (`kernel_us`, `frac`: a second region of the same run replays plans
-of the ops with an event pair recorded by each kernel's own dispatch,
-hipExtLaunchKernel; events per kernel serialise the host side, so that
-region times kernels, not steps) and sustained (`sustained_us`,
+dispatch (`kernel_us`, `frac`: the median dispatch, the mean beside it; a
+second region of the same run replays plans of the ops with an event pair
+recorded by each kernel's own dispatch, hipExtLaunchKernel; events per
+kernel serialise the host side, so that region times kernels, not steps)
+and sustained (`sustained_us`,
 `sustained_frac`: the op alone, launched back to back on one stream over its
 own > 1 GiB rotation of buffers, with one HIP event pair on that stream
 around the whole region; mean duration = region / launches). `roofline` is
-the dominant kernel (SwiGLU, 88 MB per launch): algorithmic bytes / its mean
-per-dispatch duration, the figure a rocprofv3 kernel trace of the same
-command reproduces (the sustained figure is kept beside it). `cpu_baseline`
+the dominant kernel (SwiGLU, 88 MB per launch): algorithmic bytes / its
+median per-dispatch duration, the figure a rocprofv3 kernel trace of the
+same command reproduces (the mean and the sustained figure are kept beside
+it). `cpu_baseline`
 is the same step on the host: the reference's own C++ (built into
 oracle/_ref) when present, else the oracle's restatement, single-threaded
 like the reference, over a bounded sample, with the reference's threaded
@@ -45,7 +47,8 @@ dequant over the same rows beside it.
     python bench.py --ssm-layer         # one gated-DeltaNet layer (projections .. out)
     python bench.py --only OP --steps K # one kernel only (for counter runs)
     python bench.py --copy-calibration  # a plain copy of known size
-    python bench.py --copy-sweep        # plain copies from 2 MiB to 1 GiB
+    python bench.py --copy-sweep        # copy kernel, runtime copy, fill: 2 MiB to 1 GiB
+    python bench.py --sweep             # streaming ops under alternative launch shapes
 """
 from __future__ import annotations
 
@@ -113,6 +116,8 @@ def parse_args(argv=None):
                    help="plain copy at 2 MiB .. 1 GiB: the streaming ceiling per size")
     p.add_argument("--host-abi", action="store_true",
                    help="PCIe-inclusive rate of the reference-compatible host ABI")
+    p.add_argument("--sweep", action="store_true",
+                   help="the streaming ops under every alternative launch shape (tuning knobs)")
     p.add_argument("--launch-floor", action="store_true",
                    help="device duration of a one-block launch")
     return p.parse_args(argv)
@@ -418,13 +423,18 @@ def sustained_times(path, ops_list, reps):
     return out
 
 
-def op_entry(b, rows, us_event, us_sustained):
-    """Per-op figures: per-dispatch (events on each kernel) and sustained
-    (back-to-back launches)."""
-    e = {"kernel_us": round(us_event, 3), "bytes": b,
-         "GB/s": round(b / (us_event * 1e-6) / 1e9, 1),
-         "frac": round(b / (us_event * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-         "rows_per_s": round(rows / (us_event * 1e-6), 1)}
+def op_entry(b, rows, ms_per_dispatch, us_sustained):
+    """Per-op figures: per dispatch (events on each kernel; `kernel_us` and
+    `frac` from the median dispatch, the mean beside them: a few slow
+    dispatches pull the mean) and sustained (back-to-back launches)."""
+    us = statistics.median(ms_per_dispatch) * 1e3
+    mean = statistics.mean(ms_per_dispatch) * 1e3
+    e = {"kernel_us": round(us, 3), "bytes": b,
+         "GB/s": round(b / (us * 1e-6) / 1e9, 1),
+         "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+         "kernel_us_mean": round(mean, 3),
+         "frac_mean": round(b / (mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+         "rows_per_s": round(rows / (us * 1e-6), 1)}
     if us_sustained is not None:
         g = b / (us_sustained * 1e-6) / 1e9
         e.update({"sustained_us": round(us_sustained, 3), "sustained_GB/s": round(g, 1),
@@ -595,6 +605,8 @@ def main(argv=None):
         return host_abi(a)
     if a.launch_floor:
         return launch_floor(a)
+    if a.sweep:
+        return shape_sweep(a)
     if a.all_shapes:
         return all_shapes(a)
     if a.variants:
@@ -623,9 +635,10 @@ def main(argv=None):
     if a.only:
         ker = kernel_times(path, a.steps, a.warmup, [a.only])
         b = path.bytes()[a.only]
-        mean = statistics.mean(ker[a.only])
-        print(json.dumps({"op": a.only, "shape": name, "kernel_us": round(mean * 1e3, 3),
-                          "GB/s": round(b / (mean * 1e-3) / 1e9, 1), "bytes": b}))
+        med = statistics.median(ker[a.only])
+        print(json.dumps({"op": a.only, "shape": name, "kernel_us": round(med * 1e3, 3),
+                          "kernel_us_mean": round(statistics.mean(ker[a.only]) * 1e3, 3),
+                          "GB/s": round(b / (med * 1e-3) / 1e9, 1), "bytes": b}))
         return 0
     wall = timed_steps(path, a.steps, a.warmup)
     ker = kernel_times(path, a.steps, a.warmup, path.report_ops())
@@ -636,8 +649,7 @@ def main(argv=None):
     value = total / (wall * 1e-3) / 1e9
     per_op = {}
     for op in path.report_ops():
-        per_op[op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3, sus[op])
-        per_op[op]["kernel_us_median"] = round(statistics.median(ker[op]) * 1e3, 3)
+        per_op[op] = op_entry(bts[op], rows[op], ker[op], sus[op])
     dom = "swiglu"
     ach = per_op[dom]["GB/s"]
     out = {
@@ -657,6 +669,8 @@ def main(argv=None):
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                      "kernel": "act_vec_kernel<silu> (SwiGLU 512x14336)",
                      "bytes_per_launch": bts[dom], "launch_us": per_op[dom]["kernel_us"],
+                     "launch_us_mean": per_op[dom]["kernel_us_mean"],
+                     "frac_mean": per_op[dom]["frac_mean"], "duration": "median dispatch",
                      "sustained_GB/s": per_op[dom]["sustained_GB/s"],
                      "sustained_frac": per_op[dom]["sustained_frac"]},
         "ops": per_op,
@@ -699,10 +713,64 @@ def all_shapes(a):
         bts, rows = path.bytes(), path.rows()
         res[name] = {}
         for op in ops_list:
-            res[name][op] = op_entry(bts[op], rows[op], statistics.mean(ker[op]) * 1e3,
-                                     sus[op])
+            res[name][op] = op_entry(bts[op], rows[op], ker[op], sus[op])
         print(json.dumps({"shape": name, "ops": res[name]}), flush=True)
         del path
+    return 0
+
+
+# The alternative launch shapes of the streaming kernels (AERO_HIP_TUNE keys):
+# norm_loop = a persistent grid of that many workgroups per CU (weights in
+# registers, next row's loads before this row's stores); norm_vmax = float4 a
+# lane before another lane is added to a row (16, 32: one or two waves a row
+# at 4096-8192 columns); act_grid = a persistent act grid of that many
+# workgroups per CU; act_bs / act_u = lanes per workgroup / float4 per lane.
+SWEEP_SHAPES = ("llama3_8b_prefill", "gemma3_4b_prefill", "qwen3next_hybrid",
+                "llama3_70b_prefill16k")
+SWEEP = (
+    (("rmsnorm", "add_rmsnorm", "gated_norm"),
+     ({}, {"norm_loop": 1}, {"norm_loop": 2}, {"norm_loop": 4}, {"norm_vmax": 8},
+      {"norm_vmax": 16}, {"norm_vmax": 32})),
+    (("swiglu",),
+     ({}, {"act_grid": 4}, {"act_grid": 16}, {"act_bs": 256}, {"act_bs": 256, "act_grid": 4},
+      {"act_u": 2})),
+)
+
+
+def shape_sweep(a):
+    """Each streaming op at each large shape under every alternative launch
+    shape of SWEEP, set in-process (aero_hip_tune_set) and dropped again:
+    median per-dispatch and sustained time, one JSON line per case, the
+    default shape first."""
+    from aero_amd import workloads as W
+    from aero_amd.device import tune_set
+
+    names = a.shapes.split(",") if a.shapes else list(SWEEP_SHAPES)
+    for name in names:
+        s = W.SHAPES[name]
+        for ops_list, knob_sets in SWEEP:
+            for op in ops_list:
+                if op == "gated_norm" and not s.gated:
+                    continue
+                path = Path(name, 2 if s.n_tok > 4096 else 4, only=op)
+                b = path.bytes()[op]
+                for kn in knob_sets:
+                    for k, v in kn.items():
+                        tune_set(k, v)
+                    try:
+                        ker = kernel_times(path, 30, 5, [op])[op]
+                        sus = sustained_times(path, [op], 4)[op]
+                    finally:
+                        for k in kn:
+                            tune_set(k, None)
+                    med = statistics.median(ker) * 1e3
+                    print(json.dumps({"shape": name, "op": op, "knobs": kn, "bytes": b,
+                                      "kernel_us": round(med, 3),
+                                      "frac": round(b / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "sustained_us": round(sus, 3),
+                                      "sustained_frac": round(b / (sus * 1e-6) / 1e9
+                                                              / HBM_PEAK_GBS, 4)}), flush=True)
+                del path
     return 0
 
 
@@ -717,7 +785,7 @@ def variants(a):
         path = Path(name, a.sets, shape=shape, only=op)
         ker = kernel_times(path, max(20, a.steps // 4), 5, [op])
         sus = sustained_times(path, [op], SUSTAINED_REPS)
-        e = op_entry(path.bytes()[op], path.rows()[op], statistics.mean(ker[op]) * 1e3, sus[op])
+        e = op_entry(path.bytes()[op], path.rows()[op], ker[op], sus[op])
         print(json.dumps({"variant": name, "op": op, **e}), flush=True)
         del path
     return 0
@@ -1743,34 +1811,57 @@ def copy_calibration(a):
 
 
 def copy_sweep(a):
-    """The streaming ceiling at each op's size: a plain fp32 copy (the act
-    kernel's access pattern, one read and one write per element) of total
-    traffic 2 MiB .. 1 GiB, rotated over buffers of > 1 GiB together, timed
-    per dispatch. One JSON line per size."""
-    from aero_amd import ops
-    from aero_amd.device import DeviceArray as DA, Event, synchronize, time_next_kernel
+    """The streaming ceiling at each launch size, three ways: this library's
+    plain fp32 copy kernel (`aero_hip_copy_f32`, the act kernel's access
+    pattern: one read and one write per element), the HIP runtime's own
+    device-to-device copy (`hipMemcpyAsync`, which runs the runtime's blit
+    kernel), and a store-only fill (`aero_hip_fill_f32`, the ceiling of a
+    kernel whose bytes are nearly all writes, like the embedding gathers),
+    each of total traffic 2 MiB .. 1 GiB, rotated over buffers of > 1.5 GiB
+    together. The kernels are timed per dispatch by their own events; the
+    runtime copy by an event pair on its stream around each call (a
+    rocprofv3 kernel trace of the same command times all three alike). One
+    JSON line per size and copy."""
+    from aero_amd import _lib, ops
+    from aero_amd.device import DeviceArray as DA, Event, Stream, synchronize, time_next_kernel
 
+    L = _lib.lib()
+    stream = Stream()
     for mib in (2, 4, 8, 16, 32, 64, 128, 256, 512, 1024):
         n = mib * (1 << 20) // 8                 # floats per buffer (read + write = mib)
         k = max(2, -(-(3 << 29) // (8 * n)))     # buffer pairs over 1.5 GiB
         bufs = [(DA.empty(n), DA.empty(n)) for _ in range(k)]
-        ts = []
-        for i in range(a.warmup + a.steps):
-            src, dst = bufs[i % k]
-            e0, e1 = Event(), Event()
-            time_next_kernel(e0, e1)
-            ops.copy_f32(src, dst)
-            if i >= a.warmup:
-                ts.append((e0, e1))
-        synchronize()
-        us = [x.elapsed_ms(y) * 1e3 for x, y in ts]
-        m = statistics.mean(us)
-        print(json.dumps({"copy_bytes": 8 * n, "kernel_us": round(m, 3),
-                          "kernel_us_median": round(statistics.median(us), 3),
-                          "GB/s": round(8 * n / (m * 1e-6) / 1e9, 1),
-                          "frac": round(8 * n / (m * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}),
-              flush=True)
-        del bufs, ts
+        fills = [DA.empty(2 * n) for _ in range(k)]
+        for how in ("kernel", "hipMemcpyAsync", "fill"):
+            ts = []
+            for i in range(a.warmup + a.steps):
+                src, dst = bufs[i % k]
+                e0, e1 = Event(), Event()
+                if how == "kernel":
+                    time_next_kernel(e0, e1)
+                    ops.copy_f32(src, dst, stream=stream)
+                elif how == "fill":
+                    # write-only, the same byte count as the copy's read + write
+                    time_next_kernel(e0, e1)
+                    ops.fill_f32(fills[i % k], 1.0, stream=stream)
+                else:
+                    e0.record(stream)
+                    _lib.check(L.aero_hip_memcpy_dtod(dst.ptr, src.ptr, 4 * n, stream.handle),
+                               "memcpy D2D")
+                    e1.record(stream)
+                if i >= a.warmup:
+                    ts.append((e0, e1))
+            synchronize()
+            us = [x.elapsed_ms(y) * 1e3 for x, y in ts]
+            m = statistics.mean(us)
+            med = statistics.median(us)
+            print(json.dumps({"copy": how, "copy_bytes": 8 * n, "kernel_us": round(m, 3),
+                              "kernel_us_median": round(med, 3),
+                              "GB/s": round(8 * n / (m * 1e-6) / 1e9, 1),
+                              "frac_median": round(8 * n / (med * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                                   4)}), flush=True)
+        del bufs, fills, ts
+    stream.destroy()
     return 0
 
 

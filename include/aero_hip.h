@@ -478,6 +478,10 @@ int aero_hip_softmax_rows(const float* x, float* y, int64_t n_rows, int64_t n_co
 /* Plain fp32 copy kernel (dst = src, n elements): the known-size reference
  * workload used to calibrate HBM byte counters. */
 int aero_hip_copy_f32(const float* src, float* dst, int64_t n, void* stream);
+/* Store-only fill (dst[i] = value, n % 4 == 0, 16-byte aligned): the
+ * write-only streaming ceiling, beside the copy's read + write one. No
+ * counterpart in the reference (measurement only). */
+int aero_hip_fill_f32(float* dst, float value, int64_t n, void* stream);
 
 /* ------------------------------------------------------------------------
  * 3. Runtime helpers
@@ -493,6 +497,11 @@ int   aero_hip_memcpy_dtoh(void* dst, const void* src, int64_t bytes);
 int   aero_hip_memcpy_dtod(void* dst, const void* src, int64_t bytes,
                            void* stream);
 int   aero_hip_memset(void* dst, int value, int64_t bytes);  /* synchronous */
+/* Launch-shape knob override for sweeps (the AERO_HIP_TUNE keys, e.g.
+ * "norm_loop", "act_bs"): sets `key` to `value`, or drops it when `erase` is
+ * nonzero so the built-in default applies again. Plans keep the kernel
+ * choice they recorded. No counterpart in the reference (tuning only). */
+int   aero_hip_tune_set(const char* key, int value, int erase);
 void* aero_hip_stream_create(void);     /* default priority                 */
 int   aero_hip_stream_destroy(void* stream);
 int   aero_hip_stream_synchronize(void* stream);
