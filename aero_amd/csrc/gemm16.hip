@@ -1360,6 +1360,16 @@ int64_t split_partials_bytes(int64_t n_rows, int64_t n_cols, int64_t n_tok) {
     return ks > 1 ? (int64_t)ks * n_tok * n_rows * 4 : 0;
 }
 
+// Below 16 tokens the split GEMM beats the GEMV only with its columns split
+// over more workgroups (MI355X, Q4_K, 4096 x 14336: 108.6 us unsplit at 16
+// tokens or fewer, 27.1 split 14 ways; the GEMV 31.6 us at 4 tokens, 62.2 at
+// 8): such a call takes the split path only when `room` (the workspace
+// beyond the split GEMM's own) holds every partial it would write.
+bool split_room_ok(int64_t n_rows, int64_t n_cols, int64_t n_tok, int64_t room) {
+    if (n_tok >= 16) return true;
+    return room >= split_partials_bytes(n_rows, n_cols, n_tok);
+}
+
 bool split_run(const SplitJob& j, hipStream_t s) {
     const int64_t tp = pad_tokens(j.n_tok);
     const bool norm = j.norm >= 0;
@@ -1521,6 +1531,7 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
     if (need == 0 || ws == nullptr || ws_bytes < need || !aligned16(w) || rb % 16 != 0 ||
         !aligned16(ws) || !tune("gemm16", 1))
         return true;
+    if (!split_room_ok(n_rows, n_cols, n_tok, ws_bytes - need)) return true;
     SplitJob j{dtype, x, nullptr, nullptr, nullptr, -1, 0.f, 1, &w, nullptr, 0, &n_rows, &y,
                n_cols, rb, n_tok, ws, {}, ws_bytes};
     if (!split_run(j, s)) return false;
@@ -1561,6 +1572,15 @@ namespace {
 
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kScratchDevices] = {};
+// The last call's stream on each device and an event recorded after it, so
+// a call on another stream while that one may still run is refused rather
+// than left to race on the shared array.
+struct ScratchUse {
+    hipEvent_t done = nullptr;
+    hipStream_t stream = nullptr;
+    bool used = false;
+};
+ScratchUse g_scratch_use[kScratchDevices];
 
 // The current device's scratch address, looked up on its first use.
 void* scratch_ptr() {
@@ -1600,7 +1620,43 @@ bool matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
         ws = scratch_ptr();
         if (ws == nullptr) return false;
     }
-    return gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok, s, ws, need);
+    if (need == 0)
+        return gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok, s, nullptr, 0);
+    // Overlap check (eager calls only: a call recorded into a plan or a HIP
+    // graph runs later, so there is nothing to compare it with now): a call
+    // on a stream other than the last call's, while that call may still
+    // run, is refused.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const bool eager = recording_plan() == nullptr &&
+                       hipStreamIsCapturing(s, &cap) == hipSuccess &&
+                       cap == hipStreamCaptureStatusNone;
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return false;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ScratchUse& u = g_scratch_use[dev];
+    if (eager && u.used && u.stream != s) {
+        const hipError_t q = hipEventQuery(u.done);
+        if (q == hipErrorNotReady) {
+            set_error("matmul_noalloc: the previous call on this GPU (another stream) may still "
+                      "be using its scratch; order the calls on one stream or wait for it");
+            return false;
+        }
+        if (!hip_ok(q, "hipEventQuery")) return false;
+    }
+    // the whole array is the call's room: a few-token call writes its
+    // column splits' partials there too (they are far smaller than the
+    // array: 14 x 16 tokens x 4096 rows x 4 bytes = 3.7 MB at most)
+    if (!gemv_dev(dtype, w, w_bytes, x, y, n_rows, n_cols, n_tok, s, ws, kScratchBytes))
+        return false;
+    if (eager) {
+        if (u.done == nullptr &&
+            !hip_ok(hipEventCreateWithFlags(&u.done, hipEventDisableTiming), "hipEventCreate"))
+            return false;
+        if (!hip_ok(hipEventRecord(u.done, s), "hipEventRecord")) return false;
+        u.stream = s;
+        u.used = true;
+    }
+    return true;
 }
 
 // ------------------------------------ norm (and residual) folded into GEMMs
@@ -1729,7 +1785,9 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     for (int m = 0; m < (gu ? 0 : j.n_mat); ++m) all_rows += j.n_rows[m];
     bool split = split_shape_ok(j.dtype, j.n_cols, j.n_tok) &&
                  split_tokens_ok(j.n_tok, all_rows, j.n_cols) && j.rb % 16 == 0 &&
-                 tune("gemm16", 1);
+                 tune("gemm16", 1) &&
+                 split_room_ok(all_rows, j.n_cols, j.n_tok,
+                               ws_bytes - split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true));
     for (int m = 0; m < (gu ? 1 : j.n_mat); ++m) split = split && aligned16(j.w[m]);
     if (gu) split = split && aligned16(j.w_up);
     const bool fused = !split && fused_gemv_rows_ok(j, gu, w_bytes);
@@ -1792,6 +1850,15 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
 }  // namespace aero
 
 extern "C" {
+
+int aero_hip_split_ok(int dtype, int64_t n_cols, int64_t n_rows, int64_t n_tok) {
+    const int64_t bv = aero::dtype_block_values(dtype), bb = aero::dtype_block_bytes(dtype);
+    if (bv <= 1 || n_cols <= 0 || n_rows <= 0 || n_tok <= 0 || n_cols % bv != 0) return 0;
+    const int64_t rb = (n_cols / bv) * bb;
+    return aero::split_shape_ok(dtype, n_cols, n_tok) && rb % 16 == 0 &&
+                   aero::split_tokens_ok(n_tok, n_rows, n_cols) && aero::tune("gemm16", 1)
+               ? 1 : 0;
+}
 
 int64_t aero_hip_split_partials_bytes(int64_t n_rows, int64_t n_cols, int64_t n_tok) {
     return aero::split_partials_bytes(n_rows, n_cols, n_tok);

@@ -26,9 +26,14 @@ def case(t, n_rows, n_cols, n_tok, seed):
     return w, X
 
 
-def with_workspace(L, t, dw, dx, n_rows, n_cols, n_tok):
+def with_workspace(L, t, dw, dx, n_rows, n_cols, n_tok, partials=True):
+    """aero_hip_matmul with a caller workspace: the split GEMM's own bytes and,
+    with `partials`, room for its column splits' partials (the room the
+    allocation-free entry has in its array)."""
     ws_bytes = L.aero_hip_matmul_workspace(t, n_cols, n_tok)
     assert ws_bytes > 0
+    if partials:
+        ws_bytes += L.aero_hip_split_partials_bytes(n_rows, n_cols, n_tok)
     ws = DA.empty((ws_bytes,), np.uint8)
     y = DA.empty((n_tok, n_rows))
     assert L.aero_hip_matmul(t, dw.ptr, dw.nbytes, dx.ptr, y.ptr, n_rows, n_cols, n_tok, ws.ptr,
@@ -49,8 +54,10 @@ def no_alloc(L, t, dw, dx, n_rows, n_cols, n_tok):
 def test_noalloc_matches_workspace_entry(hip, oracle, t):
     L = _lib.lib()
     assert L.aero_hip_matmul_noalloc_max_bytes() == 32 << 20
-    # the larger call first, then a smaller one over the array it left behind
-    for n_rows, n_cols, n_tok, seed in ((1024, 4096, 512, 1), (130, 2048, 33, 2)):
+    # the larger call first, then smaller ones over the array it left behind;
+    # 33 and 4 tokens split their columns (partials in the array too)
+    for n_rows, n_cols, n_tok, seed in ((1024, 4096, 512, 1), (130, 2048, 33, 2),
+                                        (4096, 14336, 4, 3)):
         print(f"noalloc type={t} rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
         assert L.aero_hip_matmul_workspace(t, n_cols, n_tok) <= 32 << 20
         w, X = case(t, n_rows, n_cols, n_tok, seed + t)
@@ -85,3 +92,57 @@ def test_noalloc_other_paths_and_refusal(hip, oracle):
     assert L.aero_hip_matmul_noalloc(W.Q4_K, dw.ptr, dw.nbytes, dx.ptr, y.ptr, 8, n_cols, n_tok,
                                      None) == 0
     assert "scratch" in _lib.last_error()
+
+
+def test_few_tokens_without_partials_room_take_the_gemv(hip, oracle):
+    """A few-token call given only the split GEMM's own workspace (no room for
+    its column splits' partials) runs the GEMV rather than the unsplit split
+    GEMM, which is slower there: bit-identical to the same call with no
+    workspace at all."""
+    L = _lib.lib()
+    t, n_rows, n_cols, n_tok = W.Q4_K, 4096, 14336, 4
+    assert L.aero_hip_split_partials_bytes(n_rows, n_cols, n_tok) > 0
+    w, X = case(t, n_rows, n_cols, n_tok, 11)
+    dw, dx = DA.from_numpy(w), DA.from_numpy(X)
+    print(f"few-token split room rows={n_rows} cols={n_cols} tokens={n_tok}", flush=True)
+    short = with_workspace(L, t, dw, dx, n_rows, n_cols, n_tok, partials=False)
+    y = DA.empty((n_tok, n_rows))
+    assert L.aero_hip_matmul(t, dw.ptr, dw.nbytes, dx.ptr, y.ptr, n_rows, n_cols, n_tok, None, 0,
+                             None) == 1
+    synchronize()
+    assert bits_equal(short, y.numpy())
+    assert rel_to_scale(short, oracle.matmul(t, w, X, n_rows)) <= RTOL
+
+
+def test_overlapping_calls_on_two_streams_are_refused(hip):
+    """A call on a second stream while the first stream's call may still be
+    using the array is refused with a reason (not left to race); once the
+    first stream is done, the second stream's call runs and gives the same
+    bits. The first call is held behind ~2 ms of copies on its stream, so
+    it is still queued when the second call is made."""
+    from aero_amd import ops
+    from aero_amd.device import Stream
+
+    L = _lib.lib()
+    t, n_rows, n_cols, n_tok = W.Q4_K, 1024, 4096, 64
+    w, X = case(t, n_rows, n_cols, n_tok, 21)
+    dw, dx = DA.from_numpy(w), DA.from_numpy(X)
+    s1, s2 = Stream(), Stream()
+    big = [(DA.empty(1 << 27), DA.empty(1 << 27)) for _ in range(2)]   # 2 x 512 MiB pairs
+    y1, y2 = DA.empty((n_tok, n_rows)), DA.empty((n_tok, n_rows))
+    print("noalloc overlap: copies then a call on stream 1, a call on stream 2", flush=True)
+    for _ in range(4):
+        for a, b in big:
+            ops.copy_f32(a, b, stream=s1)
+    assert L.aero_hip_matmul_noalloc(t, dw.ptr, dw.nbytes, dx.ptr, y1.ptr, n_rows, n_cols,
+                                     n_tok, s1.handle) == 1, _lib.last_error()
+    r = L.aero_hip_matmul_noalloc(t, dw.ptr, dw.nbytes, dx.ptr, y2.ptr, n_rows, n_cols, n_tok,
+                                  s2.handle)
+    assert r == 0 and "another stream" in _lib.last_error()
+    s1.synchronize()
+    assert L.aero_hip_matmul_noalloc(t, dw.ptr, dw.nbytes, dx.ptr, y2.ptr, n_rows, n_cols, n_tok,
+                                     s2.handle) == 1, _lib.last_error()
+    s2.synchronize()
+    assert bits_equal(y1.numpy(), y2.numpy())
+    s1.destroy()
+    s2.destroy()
