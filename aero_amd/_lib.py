@@ -135,6 +135,7 @@ PROTOTYPES = {
     "aero_hip_matmul_workspace": (c_int64, [c_int, c_int64, c_int64]),
     "aero_hip_norm_matmul_workspace": (c_int64, [c_int, c_int64, c_int64, c_int64]),
     "aero_hip_split_partials_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "aero_hip_split_ok": (c_int, [c_int, c_int64, c_int64, c_int64]),
     "aero_hip_norm_matmul": (c_int, [c_int, c_int, POINTER(vp), POINTER(c_int64), POINTER(c_int64),
                                      POINTER(vp), vp, vp, vp, vp, c_float, c_int, c_int64,
                                      c_int64, vp, c_int64, vp]),

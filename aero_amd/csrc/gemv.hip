@@ -1827,6 +1827,40 @@ static bool gemv_fused_impl(int dtype, bool pair, int n_mat, const uint8_t* cons
                   "history of 0-3 rows (tail_len=%lld)", what, (long long)conv->tail_len);
         return false;
     }
+    if (conv != nullptr) {
+        // every workgroup reads x, the weights and the conv weights while
+        // single lanes write conv_out[c] and the history rows: those two
+        // must be apart from each other and from everything read or written
+        // by the other workgroups
+        const int64_t C = n_rows[0];
+        struct Span {
+            const void* p;
+            int64_t bytes;
+        };
+        auto meets = [](Span a, Span b) {
+            const uintptr_t ua = reinterpret_cast<uintptr_t>(a.p);
+            const uintptr_t ub = reinterpret_cast<uintptr_t>(b.p);
+            return a.bytes > 0 && b.bytes > 0 && ua < ub + (uintptr_t)b.bytes &&
+                   ub < ua + (uintptr_t)a.bytes;
+        };
+        const Span out{conv->out, C * 4}, hist{conv->tail, 3 * C * 4};
+        bool clash = meets(out, hist) || meets(out, {x, n_cols * 4}) ||
+                     meets(hist, {x, n_cols * 4}) || meets(out, {conv->w, C * 16}) ||
+                     meets(hist, {conv->w, C * 16});
+        for (int m = 0; m < n_mat && !clash; ++m) {
+            const Span wm{w[m], w_bytes[m]};
+            clash = meets(out, wm) || meets(hist, wm);
+            if (m > 0) {
+                const Span ym{y[m], n_rows[m] * 4};
+                clash = clash || meets(out, ym) || meets(hist, ym);
+            }
+        }
+        if (clash) {
+            set_error("%s: conv_out and the history tail must overlap neither each other nor x, "
+                      "the weights, the conv weights or the other outputs", what);
+            return false;
+        }
+    }
     if (n_tok == 0) return true;
     GemvFuse f{};
     if (gated != nullptr) f.w_len = (int)gated->w_len;

@@ -43,9 +43,6 @@ from . import ops, select
 from . import workloads as W
 from .device import DeviceArray as DA, Stream
 
-_SPLIT_TYPES = (W.Q4_K, W.Q5_K)
-
-
 @dataclass(frozen=True)
 class BlockConfig:
     hidden: int
@@ -303,13 +300,15 @@ class LayerStep:
 
     def _folds_norm(self, T: int) -> bool:
         """True when the norm (and residual add) before a projection folds into
-        it: the split GEMM's pre-pass at 32+ tokens (the call itself takes it
-        from 5-16 tokens where it is faster), the fused decode GEMV's
-        prologue below that."""
+        it: the split GEMM's pre-pass at 32+ tokens, when the library's own
+        rule (ops.split_ok) gives the split path to this type and shape (the
+        call itself takes it from 5-16 tokens where it is faster), the fused
+        decode GEMV's prologue below that."""
         if not (self.fuse("norm_gemm") and self.gpu("rmsnorm")):
             return False
         if T >= 32:
-            return self.cfg.wtype in _SPLIT_TYPES
+            c = self.cfg
+            return ops.split_ok(c.wtype, c.hidden, (c.n_head + 2 * c.n_head_kv) * c.head_dim, T)
         return self.rows16
 
     def _folds_rope(self, T: int, h_ready: bool) -> bool:

@@ -224,6 +224,15 @@ def dequant(dtype: int, raw: DeviceArray, out: DeviceArray, n_values: int,
 _gemm_ws = Workspace("split GEMM")
 
 
+def split_ok(dtype: int, n_cols: int, n_rows: int, n_tok: int) -> bool:
+    """True when a (norm_)matmul of this shape takes the split-x GEMM, the
+    path whose pre-pass folds a residual add and an RMSNorm."""
+    L = _lib.load()
+    if L is None:
+        raise _lib.AeroHipUnavailable(_lib.unavailable_reason())
+    return bool(L.aero_hip_split_ok(int(dtype), int(n_cols), int(n_rows), int(n_tok)))
+
+
 def matvec(dtype: int, w: DeviceArray, x: DeviceArray, y: DeviceArray, n_rows: int,
            n_cols: int, n_tok: int = 1, stream: Stream | None = None,
            split: bool = True) -> None:

@@ -23,8 +23,9 @@ type for the four input projections) the conv and silu run on the qkv rows
 in the projections' GEMV epilogue: three launches. The gated norm site consults aero_amd.select
 (op "gated_norm") like the decoder block's sites; the projections, conv and
 scan have no host path. With every op on the GPU, `forward` can be recorded
-as a Plan: the recording keeps the conv history length of its first call,
-which is kernel - 1 from the second call on.
+as a Plan once the conv history is full (kernel - 1 rows, from the second
+call on): the history length is a launch argument, so a recording refuses
+a shorter one rather than replay it.
 """
 from __future__ import annotations
 
@@ -34,7 +35,7 @@ import numpy as np
 
 from . import ops, select
 from . import workloads as W
-from .device import DeviceArray as DA, Stream
+from .device import DeviceArray as DA, Stream, recording_plan
 
 # projection order of aero_ssm_forward_q's weight descriptors (src/ssm.cpp:224-225)
 PROJ = ("qkv", "gate", "alpha", "beta", "out")
@@ -149,6 +150,12 @@ class SsmStep:
         cfg, dev = self.cfg, self.w.dev
         if not 0 < T <= self.max_tokens:
             raise ValueError(f"{T} tokens: outside 1..{self.max_tokens}")
+        if recording_plan() is not None and self.tail_len < cfg.conv_kernel - 1:
+            # the history length is a launch argument: a recording made now
+            # would replay this short history on every later step
+            raise ValueError(f"forward: recording a plan with {self.tail_len} rows of conv "
+                             f"history (fewer than {cfg.conv_kernel - 1}); record it once "
+                             f"the history is full")
         shapes = cfg.shapes()
         x = self.x.view((T, cfg.hidden))
         if T == 1 and self.conv_fold and select.fusion_enabled("conv_gemm",

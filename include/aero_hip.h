@@ -293,8 +293,10 @@ int aero_hip_matvec(int dtype, const uint8_t* w, int64_t w_bytes, const float* x
  * n_tok) bytes (W 16-byte aligned), the GEMM runs on the fp16 matrix cores
  * with x split into two fp16 parts per token and 256 columns (22
  * significant bits of x, exact products, fp32 sums; ws holds the parts);
- * otherwise it is aero_hip_matvec. Calls sharing one workspace must be
- * ordered on one stream. */
+ * otherwise it is aero_hip_matvec. Below 16 tokens the split GEMM is taken
+ * only when ws also holds aero_hip_split_partials_bytes for its column
+ * splits (unsplit it is slower than the GEMV there). Calls sharing one
+ * workspace must be ordered on one stream. */
 /* Decode steps of a decoder layer in one launch each. The reference runs
  * them as separate passes: rmsnorm_rows (src/transformer.cpp:98-104, or
  * src/tensor.cpp:128-134), matvec (src/kernels.cpp:497-518) per matrix,
@@ -330,7 +332,8 @@ int aero_hip_norm_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,
  * (min(3, tail_len + 1) rows valid after). It replaces the projections
  * (src/ssm.cpp:289-315) and the conv (:297-301) of aero_ssm_forward_q, as
  * aero_hip_norm_matvec followed by aero_hip_ssm_conv_silu; y[0] is not
- * written. */
+ * written. conv_out and tail must overlap neither each other nor x, the
+ * weights, conv_w or y[1..] (refused otherwise). */
 int aero_hip_ssm_proj_conv(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
                            const int64_t* n_rows, float* const* y, const float* x,
                            int64_t n_cols, const float* conv_w, float* tail, int64_t tail_len,
@@ -405,6 +408,13 @@ int64_t aero_hip_norm_matmul_workspace(int dtype, int64_t n_cols, int64_t n_ff, 
  * runs unsplit. 0 when the call would not split. No counterpart in the
  * reference, whose matmul runs on the CPU. */
 int64_t aero_hip_split_partials_bytes(int64_t n_rows, int64_t n_cols, int64_t n_tok);
+/* 1 when a matmul (or norm_matmul) of n_tok tokens over n_rows rows (all
+ * matrices together) of n_cols columns of `dtype` takes the split-x fp16
+ * GEMM, whose pre-pass folds a residual add and an RMSNorm, given 16-byte
+ * aligned pointers and the workspace; 0 when it runs as separate launches.
+ * Lets a model loop decide whether to fold its norm into the projection
+ * from the library's own rule. No counterpart in the reference. */
+int aero_hip_split_ok(int dtype, int64_t n_cols, int64_t n_rows, int64_t n_tok);
 int aero_hip_norm_matmul(int dtype, int n_mat, const uint8_t* const* w, const int64_t* w_bytes,
                          const int64_t* n_rows, float* const* y, const float* x, const float* d,
                          float* x_out, const float* norm_w, float eps, int norm, int64_t n_cols,
@@ -439,12 +449,16 @@ int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
  * library runs on until the process ends. No counterpart in the reference:
  * it is for callers that cannot call hipMalloc (code under HIP graph
  * capture, serving loops, harnesses that forbid allocation). Results equal
- * aero_hip_matmul's with a workspace bit for bit. Returns 0 with a reason
- * when the call would need more scratch than the maximum (n_tok * n_cols *
- * 4 bytes and a little more for the split path's types). Every
- * call on one GPU shares that GPU's array: calls that overlap on one GPU
- * (other streams, other host threads) race; calls ordered on one stream do
- * not. Nothing in the array needs clearing between calls. */
+ * aero_hip_matmul's with a workspace of aero_hip_matmul_workspace +
+ * aero_hip_split_partials_bytes bytes bit for bit (the array is the call's
+ * room, column-split partials included). Returns 0 with a reason when the
+ * call would need more scratch than the maximum (n_tok * n_cols * 4 bytes
+ * and a little more for the split path's types). Every call on one GPU
+ * shares that GPU's array: calls ordered on one stream are safe; an eager
+ * call on another stream while the last call may still run is refused
+ * (0, "another stream"); calls recorded into a plan or captured into a HIP
+ * graph are not checked, and such calls that overlap on one GPU race.
+ * Nothing in the array needs clearing between calls. */
 int aero_hip_matmul_noalloc(int dtype, const uint8_t* w, int64_t w_bytes, const float* x,
                             float* y, int64_t n_rows, int64_t n_cols, int64_t n_tok,
                             void* stream);

@@ -323,3 +323,23 @@ def test_workspace_grows_only_and_plans_hold_what_they_recorded(monkeypatch):
     assert p._held == [b, r2]              # each once, in first-use order
     ws.get(4 * big)                         # outside the plan: replaces r2
     assert ws.buf is not r2 and p._held[1] is r2
+
+
+def test_split_ok_follows_the_split_rule():
+    """aero_hip_split_ok is host arithmetic over the split path's shape rule:
+    Q4_K/Q5_K/Q8_0 rows of whole 16 bytes, Q6_K of whole 2048-value groups,
+    IQ4_XS of whole 512, from a token count that depends on the matrix size."""
+    from aero_amd import ops, workloads as W
+
+    assert ops.split_ok(W.Q4_K, 4096, 6144, 512)
+    assert ops.split_ok(W.Q5_K, 4096, 6144, 512)
+    assert ops.split_ok(W.Q8_0, 4096, 6144, 512)
+    assert ops.split_ok(W.Q6_K, 4096, 6144, 512)
+    assert ops.split_ok(W.Q6_K, 14336, 4096, 512)
+    assert ops.split_ok(W.IQ4_XS, 4096, 6144, 512)
+    assert not ops.split_ok(W.Q6_K, 2560, 4096, 512)     # 2560 % 2048
+    assert not ops.split_ok(W.Q8_0, 896, 1152, 512)      # 952-byte rows
+    assert not ops.split_ok(W.F32, 4096, 4096, 512)
+    assert not ops.split_ok(W.Q4_K, 4096, 6144, 2)       # below the token threshold
+    assert ops.split_ok(W.Q4_K, 4096, 14336, 5) and not ops.split_ok(W.Q4_K, 4096, 14336, 4)
+    assert not ops.split_ok(W.Q4_K, 4000, 4096, 512)     # not whole super-blocks

@@ -44,6 +44,11 @@ CASES = {
     # 16 tokens over 100 cached positions (a speculative-decoding step): the
     # projections take the split GEMM with the norms folded below 32 tokens
     "llama3_8b_t16": ("llama3_8b_prefill", W.Q4_K, 4096, 16, 100),
+    # the 512-token prefill in the other split-GEMM types: the norms and
+    # residual adds fold into the pre-pass for these too (Q6_K: rows of 4096
+    # and 14336 columns are whole 2048-value groups)
+    "llama3_8b_prefill_q8_0": ("llama3_8b_prefill", W.Q8_0, 4096, 512, 0),
+    "llama3_8b_prefill_q6_k": ("llama3_8b_prefill", W.Q6_K, 4096, 512, 0),
 }
 
 
@@ -135,6 +140,9 @@ def test_layer_vs_oracle(hip, oracle, name, fused):
     fus = None if fused else {f: False for f in select.FUSIONS}
     step = run_and_check(oracle, name, fusions=fus)
     assert not step.uses_host()
+    if fused and CASES[name][3] >= 32:
+        # the fold decision follows the library's split rule for every type
+        assert step._folds_norm(CASES[name][3])
 
 
 @pytest.mark.parametrize("name,n_layers", [("qwen2_0p5b_decode", 3), ("llama3_8b_prefill", 2),

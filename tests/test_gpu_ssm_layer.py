@@ -129,16 +129,30 @@ def test_ssm_layer_refusals(hip):
         step.forward(9)
 
 
-@pytest.mark.parametrize("hidden", [1024, 2048])
-@pytest.mark.parametrize("tail_len", [0, 1, 2, 3])
-def test_ssm_proj_conv_equals_separate_launches(hip, hidden, tail_len):
+def _conv_fold_admits(t, hidden):
+    bv, bb = W.BLOCK[t]
+    return hidden % bv == 0 and (hidden // bv * bb) % 16 == 0
+
+
+PROJ_CONV_CASES = [(W.Q4_K, h, tl) for h in (1024, 2048) for tl in (0, 1, 2, 3)] + [
+    (t, h, tl) for t in (W.Q4_K, W.Q8_0, W.Q5_K, W.Q6_K, W.IQ4_XS)
+    for h in (1024, 2048, 4096, 5120) for tl in (0, 3)
+    if _conv_fold_admits(t, h) and not (t == W.Q4_K and h <= 2048)]
+
+
+@pytest.mark.parametrize("t,hidden,tail_len", PROJ_CONV_CASES)
+def test_ssm_proj_conv_equals_separate_launches(hip, t, hidden, tail_len):
     """aero_hip_ssm_proj_conv against the same projections (norm_matmul with
-    no norm) followed by the conv with silu, at every history length: the
-    conv output and the moved history bit for bit (the same arithmetic in
-    the same order), the other projections likewise."""
+    no norm) followed by the conv with silu, at every history length, for
+    every type the layer's conv fold admits and for rows that take each
+    GEMV form (quarter and half wave up to 2048 columns, a whole wave up to
+    4096, the pipelined form beyond): the conv output and the moved history
+    bit for bit (the same arithmetic in the same order), the other
+    projections likewise."""
     from aero_amd import ops
     from aero_amd.device import DeviceArray as DA
-    cfg = S.SsmConfig(hidden, 2, 4, 64, 4, (W.Q4_K,) * 5)
+    print(f"proj_conv type={t} hidden={hidden} tail_len={tail_len}", flush=True)
+    cfg = S.SsmConfig(hidden, 2, 4, 64, 4, (t,) * 5)
     wts = S.SsmWeights(cfg, seed=tail_len)
     h, d = wts.host, wts.dev
     rng = np.random.default_rng(71 + tail_len)
@@ -149,14 +163,14 @@ def test_ssm_proj_conv_equals_separate_launches(hip, hidden, tail_len):
     ws = [d[n] for n in names]
     # separate launches
     ys_a = [DA.empty((1, r)) for r in rows]
-    ops.norm_matmul(W.Q4_K, ws, x, ys_a, rows, hidden, 1, norm=False)
+    ops.norm_matmul(t, ws, x, ys_a, rows, hidden, 1, norm=False)
     tail_a, conv_a = DA.from_numpy(tail0), DA.empty((1, cfg.qkv))
     tl_a = ops.ssm_conv(ys_a[0], d["conv1d"], tail_a, tail_len, tail_a, conv_a, 1, cfg.qkv, 4,
                         silu=True)
     # one launch
     ys_b = [DA.empty((1, r)) for r in rows]
     tail_b, conv_b = DA.from_numpy(tail0), DA.empty((1, cfg.qkv))
-    tl_b = ops.ssm_proj_conv(W.Q4_K, ws, x, ys_b, rows, hidden, d["conv1d"], tail_b, tail_len,
+    tl_b = ops.ssm_proj_conv(t, ws, x, ys_b, rows, hidden, d["conv1d"], tail_b, tail_len,
                              conv_b)
     assert tl_a == tl_b == min(3, tail_len + 1)
     assert np.array_equal(conv_a.numpy(), conv_b.numpy())
@@ -164,4 +178,55 @@ def test_ssm_proj_conv_equals_separate_launches(hip, hidden, tail_len):
     for ya, yb in zip(ys_a[1:], ys_b[1:]):
         assert np.array_equal(ya.numpy(), yb.numpy())
     with pytest.raises(Exception, match="history"):
-        ops.ssm_proj_conv(W.Q4_K, ws, x, ys_b, rows, hidden, d["conv1d"], tail_b, 4, conv_b)
+        ops.ssm_proj_conv(t, ws, x, ys_b, rows, hidden, d["conv1d"], tail_b, 4, conv_b)
+
+
+def test_ssm_proj_conv_refuses_overlaps(hip):
+    """conv_out and the history tail are written by single lanes while every
+    workgroup reads x: overlapping x, each other or another output is
+    refused on the host, before any launch."""
+    from aero_amd import _lib, ops
+    from aero_amd.device import DeviceArray as DA
+    cfg = S.SsmConfig(1024, 2, 4, 64, 4, (W.Q4_K,) * 5)
+    wts = S.SsmWeights(cfg, seed=5)
+    d = wts.dev
+    names = S.PROJ[:4]
+    rows = [cfg.shapes()[n][0] for n in names]
+    C = rows[0]
+    ws = [d[n] for n in names]
+    x = DA.from_numpy(np.ones((1, 1024), np.float32))
+    tail, conv = DA.empty((3, C)), DA.empty((1, C))
+    big = DA.empty((4 * C,))
+    shared = DA.empty((max(C, rows[1]),))
+    ys = [DA.empty((1, r)) for r in rows]
+    ys_shared = [ys[0], shared.view((1, rows[1]))] + ys[2:]
+    cases = {
+        "conv_out inside the tail": (ys, tail, tail.view((1, C), offset_bytes=8)),
+        "tail over conv_out": (ys, big, big.view((1, C), offset_bytes=4 * C)),
+        "conv_out over x": (ys, tail, x.view((1, C))),
+        "conv_out over y[1]": (ys_shared, tail, shared.view((1, C))),
+    }
+    for what, (yy, tl, cv) in cases.items():
+        print(f"proj_conv overlap refusal: {what}", flush=True)
+        with pytest.raises(_lib.AeroHipError, match="overlap"):
+            ops.ssm_proj_conv(W.Q4_K, ws, x, yy, rows, 1024, d["conv1d"], tl, 0, cv)
+    # apart: accepted (returns the history's new length)
+    assert ops.ssm_proj_conv(W.Q4_K, ws, x, ys, rows, 1024, d["conv1d"], tail, 0, conv) == 1
+
+
+def test_ssm_layer_plan_refuses_short_history(hip):
+    """A plan recorded before the conv history is full would replay the short
+    history length forever: forward refuses to record then."""
+    cfg = S.SsmConfig(512, 4, 8, 128, 4, (W.Q4_K,) * 5)
+    step = S.SsmStep(cfg, S.SsmWeights(cfg, seed=2), max_tokens=8)
+    plan = Plan()
+    with pytest.raises(ValueError, match="history"):
+        with plan:
+            step.forward(1)
+    plan.destroy()
+    step.forward(3)          # three rows of history now
+    plan = Plan()
+    with plan:
+        step.forward(1)
+    assert len(plan) > 0
+    plan.destroy()
