@@ -31,6 +31,10 @@ vp = c_void_p
 # name -> (restype, argtypes), exactly the prototypes of include/aero_hip.h
 PROTOTYPES = {
     # reference-compatible host ABI
+    "aero_tensor_threads": (c_int, []),
+    "aero_tensor_matvec": (c_int, [fp, fp, fp, c_int64, c_int64, c_int]),
+    "aero_tensor_matmul": (c_int, [fp, fp, fp, c_int64, c_int64, c_int64, c_int]),
+    "aero_tensor_argmax": (c_int, [fp, c_int64]),
     "aero_tensor_silu": (c_int, [fp, c_int64]),
     "aero_tensor_gelu": (c_int, [fp, c_int64]),
     "aero_tensor_mul": (c_int, [fp, fp, c_int64]),
@@ -61,6 +65,18 @@ PROTOTYPES = {
     "aero_attention": (c_int, [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64, c_float,
                                c_int64, c_int]),
     "aero_kv_write_vec": (c_int, [c_int, fp, c_int64, vp, fp]),
+    "aero_kv_read_vec": (c_int, [c_int, vp, fp, c_int64, fp]),
+    "aero_kv_ring_indices": (c_int, [c_int64, c_int64, POINTER(c_int64)]),
+    "aero_kv_ring_rotate": (c_int, [c_int64, c_int64, c_int64, POINTER(c_int64)]),
+    "aero_kv_span_error": (c_int, [c_int, vp, fp, c_int64, fp, fp]),
+    "aero_kv_slot_new": (vp, [c_int64, c_int64, c_int64, c_int, c_int]),
+    "aero_kv_slot_free": (None, [vp]),
+    "aero_kv_slot_bytes": (c_int64, [vp]),
+    "aero_kv_slot_write": (c_int, [vp, c_int64, c_int64, fp]),
+    "aero_kv_slot_read": (c_int, [vp, c_int64, c_int64, fp]),
+    "aero_hip_kv_slot_view": (c_int, [vp, POINTER(vp), POINTER(fp), POINTER(c_int64),
+                                      POINTER(c_int64), POINTER(c_int64), POINTER(c_int),
+                                      POINTER(c_int)]),
     # device-pointer fused ops
     "aero_hip_rmsnorm": (c_int, [vp, vp, vp, c_int64, c_int64, c_float, c_int, vp]),
     "aero_hip_gated_rmsnorm_silu": (c_int, [vp, vp, vp, c_int64, vp, c_int64, c_int64,

@@ -26,6 +26,7 @@
 #include <cstring>
 #include <functional>
 #include <mutex>
+#include <new>
 #include <thread>
 #include <vector>
 
@@ -65,6 +66,29 @@ bool ssm_scan_dev(const float* q, const float* k, const float* v, const float* a
 bool ssm_conv_dev(const float* x, const float* w, const float* tail, int64_t tail_len,
                   float* tail_out, float* out, int64_t T, int64_t C, int64_t K,
                   int64_t* new_tail_len, hipStream_t s);
+bool dense_matmul_dev(const float* w, const float* x, float* y, int64_t n_rows, int64_t n_cols,
+                      int64_t n_tok, hipStream_t s);
+bool argmax_dev(const float* v, int64_t n, int32_t* out, hipStream_t s);
+bool kv_read_dev(int dt, const void* q, const float* scale, int64_t n_vec, int64_t dim,
+                 float* out, hipStream_t s);
+bool kv_span_error_dev(int dt, const void* q, const float* scale, int64_t dim, const float* x,
+                       float* out, hipStream_t s);
+
+// A KV slot (src/kv.cpp:92-133, include/aero/kv.hpp:35-60) resident in HBM:
+// codes [cap, heads, dim] (fp32, int8, or int4 two a byte) and one fp32
+// scale a (position, head) for int8/int4, zeroed at creation, on the device
+// that was current then. aero_hip_kv_slot_view hands the device pointers to
+// the attention entry point.
+struct KvSlotDev {
+    int64_t cap, heads, dim;
+    int dt;
+    int ring;
+    int device;
+    void* q;
+    float* scale;
+    int64_t vec_bytes() const { return dt == 2 ? dim / 2 : (dt == 1 ? dim : dim * 4); }
+    int64_t bytes() const { return cap * heads * vec_bytes() + (dt != 0 ? cap * heads * 4 : 0); }
+};
 
 namespace {
 
@@ -318,6 +342,22 @@ bool host_act(int kind, float* g, const float* u, int64_t n) {
            act_mul(kind, dg, du, dg, n, st.stream()) && st.d2h(g, dg, bytes) && st.finish();
 }
 
+// Y = X W^T for host W [n_rows, n_cols] and X [n_tok, n_cols] (fp32).
+bool host_dense(const float* w, const float* x, float* y, int64_t n_tok, int64_t n_rows,
+                int64_t n_cols) {
+    Staging st;
+    void* p[3];
+    const size_t wb = (size_t)(n_rows * n_cols) * 4, xb = (size_t)(n_tok * n_cols) * 4,
+                 yb = (size_t)(n_tok * n_rows) * 4;
+    if (!st.reserve({wb, xb, yb}, p)) return false;
+    float* dw = static_cast<float*>(p[0]);
+    float* dx = static_cast<float*>(p[1]);
+    float* dy = static_cast<float*>(p[2]);
+    return st.h2d(dw, w, wb) && st.h2d(dx, x, xb) &&
+           dense_matmul_dev(dw, dx, dy, n_rows, n_cols, n_tok, st.stream()) &&
+           st.d2h(y, dy, yb) && st.finish();
+}
+
 bool host_norm(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
                float eps, int flags) {
     Staging st;
@@ -395,6 +435,60 @@ int aero_tensor_rmsnorm_rows(float* t, int64_t rows, int64_t cols, float eps) {
         return 0;
     }
     return aero::host_norm(t, nullptr, t, rows, cols, eps, 0) ? 1 : 0;
+}
+
+// src/tensor.cpp:207 aero_tensor_threads: the thread count the reference's
+// native layer would pick (hardware threads, at most 8). The GPU entry
+// points below take and ignore a `threads` argument.
+int aero_tensor_threads(void) {
+    const unsigned hc = std::thread::hardware_concurrency();
+    return (int)std::min(hc == 0 ? 1u : hc, 8u);
+}
+
+// src/tensor.cpp:209-218 aero_tensor_matvec: y[r] = dot(W.row(r), x), fp32,
+// summed in the reference's order (bit-identical for any `threads`).
+int aero_tensor_matvec(const float* w, const float* x, float* y, int64_t n_rows, int64_t n_cols,
+                       int threads) {
+    (void)threads;
+    aero::clear_error();
+    if (!w || !x || !y || n_rows <= 0 || n_cols <= 0) {
+        set_error("aero_tensor_matvec: null or non-positive dims");
+        return 0;
+    }
+    return aero::host_dense(w, x, y, 1, n_rows, n_cols) ? 1 : 0;
+}
+
+// src/tensor.cpp:220-231 aero_tensor_matmul: Y[t][r] = dot(W.row(r),
+// X.row(t)); one token is the matvec.
+int aero_tensor_matmul(const float* w, const float* X, float* Y, int64_t n_tokens,
+                       int64_t n_rows, int64_t n_cols, int threads) {
+    (void)threads;
+    aero::clear_error();
+    if (!w || !X || !Y || n_tokens <= 0 || n_rows <= 0 || n_cols <= 0) {
+        set_error("aero_tensor_matmul: null or non-positive dims");
+        return 0;
+    }
+    return aero::host_dense(w, X, Y, n_tokens, n_rows, n_cols) ? 1 : 0;
+}
+
+// src/tensor.cpp:298-302 aero_tensor_argmax: index of the first largest
+// value (NaN never chosen; 0 when v[0] is NaN); -1 when refused.
+int aero_tensor_argmax(const float* v, int64_t n) {
+    aero::clear_error();
+    if (!v || n <= 0) {
+        set_error("aero_tensor_argmax: null or n <= 0");
+        return -1;
+    }
+    aero::Staging st;
+    void* p[2];
+    const size_t vb = (size_t)n * 4;
+    int32_t best = -1;
+    if (!st.reserve({vb, 4}, p) || !st.h2d(p[0], v, vb) ||
+        !aero::argmax_dev(static_cast<const float*>(p[0]), n, static_cast<int32_t*>(p[1]),
+                          st.stream()) ||
+        !st.d2h(&best, p[1], 4) || !st.finish())
+        return -1;
+    return best;
 }
 
 // ------------------------------------------------- src/transformer.cpp ABI
@@ -715,6 +809,193 @@ int aero_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale
                     st.d2h(q, p[1], qb) && (dt == 0 || st.d2h(scale, p[2], 4)) && st.finish();
     return ok ? 1 : 0;
 }
+// src/kv.cpp:28-46 aero_kv_read_vec: one vector back to fp32 (code * scale).
+int aero_kv_read_vec(int dt, const void* q, const float* scale, int64_t dim, float* out) {
+    aero::clear_error();
+    if (q == nullptr || scale == nullptr || out == nullptr || dim <= 0 || dt < 0 || dt > 2 ||
+        (dt == 2 && dim % 2)) {
+        set_error("aero_kv_read_vec: refused");
+        return 0;
+    }
+    const size_t ob = (size_t)dim * 4;
+    const size_t qb = dt == 0 ? ob : (dt == 1 ? (size_t)dim : (size_t)dim / 2);
+    aero::Staging st;
+    void* p[3];
+    if (!st.reserve({qb, 4, ob}, p)) return 0;
+    const bool ok = st.h2d(p[0], q, qb) && (dt == 0 || st.h2d(p[1], scale, 4)) &&
+                    aero::kv_read_dev(dt, p[0], static_cast<float*>(p[1]), 1, dim,
+                                      static_cast<float*>(p[2]), st.stream()) &&
+                    st.d2h(out, p[2], ob) && st.finish();
+    return ok ? 1 : 0;
+}
+
+// src/kv.cpp:48-56 aero_kv_ring_indices: 0 .. n-1 (a ring that has not
+// wrapped); index bookkeeping on the host.
+int aero_kv_ring_indices(int64_t cap, int64_t n, int64_t* out) {
+    if (cap <= 0 || n < 0 || out == nullptr || n > cap) return 0;
+    for (int64_t i = 0; i < n; ++i) out[i] = i;
+    return 1;
+}
+
+// src/kv.cpp:58-64 aero_kv_ring_rotate: the physical indices of the first n
+// positions in chronological order, (start + i) % cap.
+int aero_kv_ring_rotate(int64_t cap, int64_t start, int64_t n, int64_t* out) {
+    if (cap <= 0 || n < 0 || out == nullptr || start < 0 || start >= cap || n > cap) return 0;
+    for (int64_t i = 0; i < n; ++i) out[i] = (start + i) % cap;
+    return 1;
+}
+
+// src/kv.cpp:66-82 aero_kv_span_error: max|x - read(q)| / max|x| (1e-9 for
+// an all-zero x) of one written vector.
+int aero_kv_span_error(int dt, const void* q, const float* scale, int64_t dim, const float* x,
+                       float* out) {
+    aero::clear_error();
+    if (q == nullptr || scale == nullptr || x == nullptr || out == nullptr || dim <= 0 ||
+        dt < 0 || dt > 2 || (dt == 2 && dim % 2)) {
+        set_error("aero_kv_span_error: refused");
+        return 0;
+    }
+    const size_t xb = (size_t)dim * 4;
+    const size_t qb = dt == 0 ? xb : (dt == 1 ? (size_t)dim : (size_t)dim / 2);
+    aero::Staging st;
+    void* p[4];
+    if (!st.reserve({qb, 4, xb, 4}, p)) return 0;
+    const bool ok = st.h2d(p[0], q, qb) && (dt == 0 || st.h2d(p[1], scale, 4)) &&
+                    st.h2d(p[2], x, xb) &&
+                    aero::kv_span_error_dev(dt, p[0], static_cast<float*>(p[1]), dim,
+                                            static_cast<float*>(p[2]),
+                                            static_cast<float*>(p[3]), st.stream()) &&
+                    st.d2h(out, p[3], 4) && st.finish();
+    return ok ? 1 : 0;
+}
+
+// src/kv.cpp:92-108 aero_kv_slot_new: a slot in HBM on the current device
+// (NULL when refused or out of memory).
+void* aero_kv_slot_new(int64_t cap, int64_t heads, int64_t dim, int dt, int ring) {
+    aero::clear_error();
+    if (cap <= 0 || heads <= 0 || dim <= 0 || dt < 0 || dt > 2 || (dt == 2 && dim % 2)) {
+        set_error("aero_kv_slot_new: refused (cap=%lld heads=%lld dim=%lld dt=%d)",
+                  (long long)cap, (long long)heads, (long long)dim, dt);
+        return nullptr;
+    }
+    auto* sl = new (std::nothrow) aero::KvSlotDev{cap, heads, dim, dt, ring != 0, 0, nullptr,
+                                                 nullptr};
+    if (sl == nullptr) return nullptr;
+    const size_t qb = (size_t)(cap * heads * sl->vec_bytes());
+    const size_t sb = dt != 0 ? (size_t)(cap * heads) * 4 : 0;
+    bool ok = aero::hip_ok(hipGetDevice(&sl->device), "hipGetDevice") &&
+              aero::hip_ok(hipMalloc(&sl->q, qb), "hipMalloc(kv slot)") &&
+              aero::hip_ok(hipMemset(sl->q, 0, qb), "hipMemset(kv slot)");
+    if (ok && sb) {
+        void* sp = nullptr;
+        ok = aero::hip_ok(hipMalloc(&sp, sb), "hipMalloc(kv slot scales)") &&
+             aero::hip_ok(hipMemset(sp, 0, sb), "hipMemset(kv slot scales)");
+        sl->scale = static_cast<float*>(sp);
+    }
+    if (!ok) {
+        if (sl->q) (void)hipFree(sl->q);
+        if (sl->scale) (void)hipFree(sl->scale);
+        delete sl;
+        return nullptr;
+    }
+    return sl;
+}
+
+// src/kv.cpp:110 aero_kv_slot_free (NULL is ignored).
+void aero_kv_slot_free(void* s) {
+    auto* sl = static_cast<aero::KvSlotDev*>(s);
+    if (sl == nullptr) return;
+    (void)hipDeviceSynchronize();
+    if (sl->q) (void)hipFree(sl->q);
+    if (sl->scale) (void)hipFree(sl->scale);
+    delete sl;
+}
+
+// src/kv.cpp:112-115 aero_kv_slot_bytes: the reference's KvSlot::bytes()
+// (codes plus int8/int4 scales); -1 for NULL.
+int64_t aero_kv_slot_bytes(void* s) {
+    auto* sl = static_cast<aero::KvSlotDev*>(s);
+    return sl ? sl->bytes() : -1;
+}
+
+// src/kv.cpp:117-124 aero_kv_slot_write: quantise host x into the slot's
+// (phys, head) vector; the head is checked too (the reference checks phys
+// only).
+int aero_kv_slot_write(void* s, int64_t phys, int64_t head, const float* x) {
+    auto* sl = static_cast<aero::KvSlotDev*>(s);
+    aero::clear_error();
+    if (sl == nullptr || x == nullptr || phys < 0 || phys >= sl->cap || head < 0 ||
+        head >= sl->heads) {
+        set_error("aero_kv_slot_write: refused");
+        return 0;
+    }
+    int dev = -1;
+    if (!aero::hip_ok(hipGetDevice(&dev), "hipGetDevice")) return 0;
+    if (dev != sl->device) {
+        set_error("aero_kv_slot_write: the slot lives on device %d, device %d is current", sl->device,
+                  dev);
+        return 0;
+    }
+    const int64_t vec = phys * sl->heads + head;
+    const size_t xb = (size_t)sl->dim * 4;
+    aero::Staging st;
+    void* p[1];
+    if (!st.reserve({xb}, p)) return 0;
+    void* qv = static_cast<uint8_t*>(sl->q) + vec * sl->vec_bytes();
+    const bool ok = st.h2d(p[0], x, xb) &&
+                    aero::kv_write_dev(sl->dt, static_cast<float*>(p[0]), 1, 1, sl->dim, 0, 1,
+                                       qv, sl->scale ? sl->scale + vec : nullptr, st.stream()) &&
+                    st.finish();
+    return ok ? 1 : 0;
+}
+
+// src/kv.cpp:126-131 aero_kv_slot_read: the slot's (phys, head) vector as
+// fp32 into host out.
+int aero_kv_slot_read(void* s, int64_t phys, int64_t head, float* out) {
+    auto* sl = static_cast<aero::KvSlotDev*>(s);
+    aero::clear_error();
+    if (sl == nullptr || out == nullptr || phys < 0 || phys >= sl->cap || head < 0 ||
+        head >= sl->heads) {
+        set_error("aero_kv_slot_read: refused");
+        return 0;
+    }
+    int dev = -1;
+    if (!aero::hip_ok(hipGetDevice(&dev), "hipGetDevice")) return 0;
+    if (dev != sl->device) {
+        set_error("aero_kv_slot_read: the slot lives on device %d, device %d is current", sl->device,
+                  dev);
+        return 0;
+    }
+    const int64_t vec = phys * sl->heads + head;
+    const size_t ob = (size_t)sl->dim * 4;
+    aero::Staging st;
+    void* p[1];
+    if (!st.reserve({ob}, p)) return 0;
+    const void* qv = static_cast<const uint8_t*>(sl->q) + vec * sl->vec_bytes();
+    const bool ok = aero::kv_read_dev(sl->dt, qv, sl->scale ? sl->scale + vec : nullptr, 1,
+                                      sl->dim, static_cast<float*>(p[0]), st.stream()) &&
+                    st.d2h(out, p[0], ob) && st.finish();
+    return ok ? 1 : 0;
+}
+
+int aero_hip_kv_slot_view(void* s, void** q, float** scale, int64_t* cap, int64_t* heads,
+                          int64_t* dim, int* dt, int* ring) {
+    auto* sl = static_cast<aero::KvSlotDev*>(s);
+    aero::clear_error();
+    if (sl == nullptr) {
+        set_error("aero_hip_kv_slot_view: NULL slot");
+        return 0;
+    }
+    if (q) *q = sl->q;
+    if (scale) *scale = sl->scale;
+    if (cap) *cap = sl->cap;
+    if (heads) *heads = sl->heads;
+    if (dim) *dim = sl->dim;
+    if (dt) *dt = sl->dt;
+    if (ring) *ring = sl->ring;
+    return 1;
+}
+
 // ------------------------------------------------------- gated DeltaNet
 // src/ssm.cpp:151-210. Host arrays, synchronous; the void entries report a
 // refusal through aero_hip_last_error() and leave the outputs unwritten.

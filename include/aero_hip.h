@@ -40,6 +40,23 @@ extern "C" {
  * 1. Reference-compatible host-pointer ABI
  * ---------------------------------------------------------------------- */
 
+/* src/tensor.cpp:207 aero_tensor_threads: the default thread count of the
+ * reference's native layer (hardware threads, at most 8); the GPU entry
+ * points take and ignore `threads`. */
+int aero_tensor_threads(void);
+/* src/tensor.cpp:209-218 aero_tensor_matvec: y[r] = dot(W.row(r), x), W
+ * [n_rows, n_cols] fp32, summed in the reference's order (four products at
+ * a time): bit-identical. 1 = ok, 0 = refused (null or dims <= 0). */
+int aero_tensor_matvec(const float* w, const float* x, float* y, int64_t n_rows,
+                       int64_t n_cols, int threads);
+/* src/tensor.cpp:220-231 aero_tensor_matmul: Y[t][r] = dot(W.row(r), X.row(t)),
+ * X [n_tokens, n_cols], Y [n_tokens, n_rows]; one token is the matvec,
+ * several sum one product at a time as the reference: bit-identical. */
+int aero_tensor_matmul(const float* w, const float* X, float* Y, int64_t n_tokens,
+                       int64_t n_rows, int64_t n_cols, int threads);
+/* src/tensor.cpp:298-302 aero_tensor_argmax: index of the first largest
+ * value (NaN never chosen; 0 when v[0] is NaN), -1 = refused. */
+int aero_tensor_argmax(const float* v, int64_t n);
 /* src/tensor.cpp:234-238 aero_tensor_silu: v[i] *= sigmoid(v[i]), in place.
  * 1 = ok, 0 = refused (null or n <= 0). */
 int aero_tensor_silu(float* v, int64_t n);
@@ -136,6 +153,35 @@ int aero_attention(const float* q, const float* k, const float* v, float* out, i
 /* src/kv.cpp:13-26 aero_kv_write_vec: quantise one vector (dt 0 fp32 copy,
  * 1 int8 with scale amax/127, 2 int4 low-nibble-first with scale amax/7). */
 int aero_kv_write_vec(int dt, const float* x, int64_t dim, void* q, float* scale);
+/* src/kv.cpp:28-46 aero_kv_read_vec: one vector back to fp32, code * scale
+ * (bit-exact). 0 = refused. */
+int aero_kv_read_vec(int dt, const void* q, const float* scale, int64_t dim, float* out);
+/* src/kv.cpp:48-56 aero_kv_ring_indices: out[i] = i for i < n <= cap. */
+int aero_kv_ring_indices(int64_t cap, int64_t n, int64_t* out);
+/* src/kv.cpp:58-64 aero_kv_ring_rotate: out[i] = (start + i) % cap, the
+ * chronological physical order of a wrapped ring. */
+int aero_kv_ring_rotate(int64_t cap, int64_t start, int64_t n, int64_t* out);
+/* src/kv.cpp:66-82 aero_kv_span_error: *out = max|x - read(q)| / max|x|
+ * (1e-9 for an all-zero x), bit-exact. */
+int aero_kv_span_error(int dt, const void* q, const float* scale, int64_t dim, const float* x,
+                       float* out);
+/* src/kv.cpp:92-133 the KV slot, here resident in HBM on the device current
+ * at creation: codes [cap, heads, dim] (dt 0 fp32, 1 int8, 2 int4) plus one
+ * fp32 scale a vector for int8/int4, zeroed. new returns NULL when refused;
+ * bytes is the reference's KvSlot::bytes() (-1 for NULL); write quantises a
+ * host vector into (phys, head), read returns it as fp32; both refuse a phys
+ * or head out of range (the reference checks phys only) and another current
+ * device. A ring slot's wrap is the caller's, as in the reference. */
+void*   aero_kv_slot_new(int64_t cap, int64_t heads, int64_t dim, int dt, int ring);
+void    aero_kv_slot_free(void* slot);
+int64_t aero_kv_slot_bytes(void* slot);
+int     aero_kv_slot_write(void* slot, int64_t phys, int64_t head, const float* x);
+int     aero_kv_slot_read(void* slot, int64_t phys, int64_t head, float* out);
+/* The device side of a slot: its codes and scales in HBM (the k / v and
+ * k_scale / v_scale arguments of aero_hip_attention, vector (phys, head) at
+ * phys * heads + head) and its shape. No counterpart in the reference. */
+int aero_hip_kv_slot_view(void* slot, void** q, float** scale, int64_t* cap, int64_t* heads,
+                          int64_t* dim, int* dt, int* ring);
 
 /* ------------------------------------------------------------------------
  * 2. Device-pointer fused ops (HBM pointers, asynchronous on `stream`)

@@ -26,6 +26,14 @@
  *                      spot values of tests/test_tensor_native.py:118-132;
  *                      compiled reference (bit-exact for silu/gelu/swiglu/mul).
  *                      gelu_tanh has no reference function: closed form only.
+ *   cr_dense_matvec / cr_dense_matmul  compiled reference src/tensor.cpp
+ *                      (bit-exact, 1-5 tokens, ragged widths); float64 product
+ *                      to 5e-6 of scale; a planted regrouping of the sum (one
+ *                      product at a time in the matvec) is caught by the
+ *                      bit-exact check.
+ *   cr_argmax          compiled reference (bit-exact) on ties, NaN at 0 and
+ *                      elsewhere, signed zeros, infinities; np.argmax on
+ *                      NaN-free input.
  *   cr_rope_*          compiled reference (bit-exact); relative-position
  *                      invariance, norm preservation, tail pass-through and
  *                      freq_factor 1e30 => cos 1, sin 0
@@ -247,6 +255,56 @@ void cr_softmax(float* v, int64_t n) {
 
 void cr_softmax_rows(float* v, int64_t n_rows, int64_t n_cols) {
     for (int64_t r = 0; r < n_rows; ++r) cr_softmax(v + r * n_cols, n_cols);
+}
+
+/* ------------------------------------------------------ dense fp32 */
+/* src/tensor.cpp:65-81 matvec: per row, four products summed left to right
+ * and added to acc at a time, then the tail one product at a time. */
+void cr_dense_matvec(const float* w, const float* x, float* y, int64_t n_rows,
+                     int64_t n_cols) {
+    for (int64_t r = 0; r < n_rows; ++r) {
+        const float* wr = w + r * n_cols;
+        float acc = 0.0f;
+        int64_t c = 0;
+        for (; c + 4 <= n_cols; c += 4) {
+            float g = wr[c] * x[c];
+            g = g + wr[c + 1] * x[c + 1];
+            g = g + wr[c + 2] * x[c + 2];
+            g = g + wr[c + 3] * x[c + 3];
+            acc = acc + g;
+        }
+        for (; c < n_cols; ++c) acc = acc + wr[c] * x[c];
+        y[r] = acc;
+    }
+}
+
+/* src/tensor.cpp:83-92 matmul: one token is the matvec; several sum each
+ * row's products one at a time. Y is [n_tok, n_rows]. */
+void cr_dense_matmul(const float* w, const float* x, float* y, int64_t n_tok, int64_t n_rows,
+                     int64_t n_cols) {
+    if (n_tok == 1) {
+        cr_dense_matvec(w, x, y, n_rows, n_cols);
+        return;
+    }
+    for (int64_t r = 0; r < n_rows; ++r)
+        for (int64_t t = 0; t < n_tok; ++t) {
+            float acc = 0.0f;
+            for (int64_t c = 0; c < n_cols; ++c) acc = acc + w[r * n_cols + c] * x[t * n_cols + c];
+            y[t * n_rows + r] = acc;
+        }
+}
+
+/* src/tensor.cpp:180-186 argmax: start at v[0], move on only to a strictly
+ * larger value (so the first of equal maxima wins and NaN is never taken). */
+int cr_argmax(const float* v, int64_t n) {
+    int best = 0;
+    float bv = v[0];
+    for (int64_t i = 1; i < n; ++i)
+        if (v[i] > bv) {
+            bv = v[i];
+            best = (int)i;
+        }
+    return best;
 }
 
 /* ---------------------------------------------------------- attention */

@@ -65,6 +65,10 @@ void    cr_apply_rope(float* x, int64_t n_rows, int64_t head_dim, int64_t n_rot,
                       const int32_t* pos, int mode);
 
 /* softmax, GQA attention (src/tensor.cpp:167-178, src/transformer.cpp:120-214) */
+void cr_dense_matvec(const float* w, const float* x, float* y, int64_t n_rows, int64_t n_cols);
+void cr_dense_matmul(const float* w, const float* x, float* y, int64_t n_tok, int64_t n_rows,
+                     int64_t n_cols);
+int cr_argmax(const float* v, int64_t n);
 void cr_softmax(float* v, int64_t n);
 void cr_softmax_rows(float* v, int64_t n_rows, int64_t n_cols);
 int  cr_attention_tiled(const float* q, const float* k, const float* v, float* out, int64_t n_q,

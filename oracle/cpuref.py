@@ -66,6 +66,12 @@ def lib():
         L.cr_rope_tables.restype = c_int64
         L.cr_apply_rope.argtypes = [fp, c_int64, c_int64, c_int64, fp, fp, ip, c_int]
         L.cr_apply_rope.restype = None
+        L.cr_dense_matvec.argtypes = [fp, fp, fp, c_int64, c_int64]
+        L.cr_dense_matvec.restype = None
+        L.cr_dense_matmul.argtypes = [fp, fp, fp, c_int64, c_int64, c_int64]
+        L.cr_dense_matmul.restype = None
+        L.cr_argmax.argtypes = [fp, c_int64]
+        L.cr_argmax.restype = ctypes.c_int
         L.cr_softmax_rows.argtypes = [fp, c_int64, c_int64]
         L.cr_softmax_rows.restype = None
         L.cr_attention_tiled.argtypes = [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
@@ -289,6 +295,31 @@ def qk_norm_rope(x, n_tok: int, n_head: int, head_dim: int, n_rot: int, pos,
 
 
 # ------------------------------------------------------- softmax, attention
+def dense_matvec(w, x) -> np.ndarray:
+    """src/tensor.cpp:65-81: y = W x, fp32, four products at a time."""
+    w = f32(w)
+    x = f32(x).reshape(-1)
+    y = np.empty(w.shape[0], np.float32)
+    lib().cr_dense_matvec(_f(w), _f(x), _f(y), w.shape[0], w.shape[1])
+    return y
+
+
+def dense_matmul(w, X) -> np.ndarray:
+    """src/tensor.cpp:83-92: Y = X W^T, fp32."""
+    w = f32(w)
+    X = np.atleast_2d(f32(X))
+    Y = np.empty((X.shape[0], w.shape[0]), np.float32)
+    lib().cr_dense_matmul(_f(w), _f(X), _f(Y), X.shape[0], w.shape[0], w.shape[1])
+    return Y
+
+
+def argmax(v) -> int:
+    """src/tensor.cpp:180-186: first index of the largest value (strict '>'
+    scan from v[0])."""
+    v = f32(v).reshape(-1)
+    return int(lib().cr_argmax(_f(v), v.size))
+
+
 def softmax(x) -> np.ndarray:
     """src/tensor.cpp:167-178 over the last axis."""
     out = np.array(f32(x), copy=True)

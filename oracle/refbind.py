@@ -73,6 +73,14 @@ def transformer():
         L.aero_tensor_mul.restype = c_int
         L.aero_softmax_rows.argtypes = [fp, c_int64, c_int64]
         L.aero_softmax_rows.restype = None
+        L.aero_tensor_matvec.argtypes = [fp, fp, fp, c_int64, c_int64, c_int]
+        L.aero_tensor_matvec.restype = c_int
+        L.aero_tensor_matmul.argtypes = [fp, fp, fp, c_int64, c_int64, c_int64, c_int]
+        L.aero_tensor_matmul.restype = c_int
+        L.aero_tensor_argmax.argtypes = [fp, c_int64]
+        L.aero_tensor_argmax.restype = c_int
+        L.aero_tensor_threads.argtypes = []
+        L.aero_tensor_threads.restype = c_int
         L.aero_attention_tiled.argtypes = [fp, fp, fp, fp, c_int64, c_int64, c_int64, c_int64,
                                            c_int64, c_float, ip, ip, c_int64, c_int, c_int64]
         L.aero_attention_tiled.restype = c_int
@@ -92,6 +100,23 @@ def kv():
         L.aero_kv_write_vec.restype = c_int
         L.aero_kv_read_vec.argtypes = [c_int, ctypes.c_void_p, fp, c_int64, fp]
         L.aero_kv_read_vec.restype = c_int
+        i64p, vp = POINTER(c_int64), ctypes.c_void_p
+        L.aero_kv_ring_indices.argtypes = [c_int64, c_int64, i64p]
+        L.aero_kv_ring_indices.restype = c_int
+        L.aero_kv_ring_rotate.argtypes = [c_int64, c_int64, c_int64, i64p]
+        L.aero_kv_ring_rotate.restype = c_int
+        L.aero_kv_span_error.argtypes = [c_int, vp, fp, c_int64, fp, fp]
+        L.aero_kv_span_error.restype = c_int
+        L.aero_kv_slot_new.argtypes = [c_int64, c_int64, c_int64, c_int, c_int]
+        L.aero_kv_slot_new.restype = vp
+        L.aero_kv_slot_free.argtypes = [vp]
+        L.aero_kv_slot_free.restype = None
+        L.aero_kv_slot_bytes.argtypes = [vp]
+        L.aero_kv_slot_bytes.restype = c_int64
+        L.aero_kv_slot_write.argtypes = [vp, c_int64, c_int64, fp]
+        L.aero_kv_slot_write.restype = c_int
+        L.aero_kv_slot_read.argtypes = [vp, c_int64, c_int64, fp]
+        L.aero_kv_slot_read.restype = c_int
         _v = L
     return _v
 
@@ -335,6 +360,26 @@ def apply_rope(x, cos, sin, positions=None, mode: int = 0, n_rot=None) -> np.nda
     return out
 
 
+def dense_matmul(w, X, threads: int = 1) -> np.ndarray:
+    """The reference's aero_tensor_matvec (one token) / aero_tensor_matmul."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    X = np.atleast_2d(np.ascontiguousarray(X, dtype=np.float32))
+    Y = np.empty((X.shape[0], w.shape[0]), np.float32)
+    L = transformer()
+    if X.shape[0] == 1:
+        ok = L.aero_tensor_matvec(_f(w), _f(X), _f(Y), w.shape[0], w.shape[1], threads)
+    else:
+        ok = L.aero_tensor_matmul(_f(w), _f(X), _f(Y), X.shape[0], w.shape[0], w.shape[1],
+                                  threads)
+    assert ok
+    return Y
+
+
+def argmax(v) -> int:
+    v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+    return int(transformer().aero_tensor_argmax(_f(v), v.size))
+
+
 def softmax(x) -> np.ndarray:
     out = np.array(np.ascontiguousarray(x, dtype=np.float32), copy=True)
     cols = out.shape[-1]
@@ -373,6 +418,41 @@ def kv_write_vec(dt: int, x):
     if not kv().aero_kv_write_vec(dt, _f(x), x.size, q.ctypes.data, _f(s)):
         raise ValueError("reference kv write refused")
     return q, float(s[0])
+
+
+def kv_span_error(dt: int, q, scale: float, x) -> float:
+    q = np.ascontiguousarray(q, np.uint8)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    s = np.array([scale], np.float32)
+    out = np.zeros(1, np.float32)
+    if not kv().aero_kv_span_error(dt, q.ctypes.data, _f(s), x.size, _f(x), _f(out)):
+        raise ValueError("reference kv span error refused")
+    return float(out[0])
+
+
+def kv_ring_rotate(cap: int, start: int, n: int):
+    out = np.zeros(max(n, 1), np.int64)
+    ok = kv().aero_kv_ring_rotate(cap, start, n, out.ctypes.data_as(POINTER(c_int64)))
+    return ok, out[:n]
+
+
+def kv_slot_roundtrip(cap: int, heads: int, dim: int, dt: int, writes):
+    """The reference's KvSlot: write each (phys, head, x) of `writes`, then
+    read every vector back; returns (bytes, [cap, heads, dim] fp32)."""
+    L = kv()
+    sl = L.aero_kv_slot_new(cap, heads, dim, dt, 0)
+    assert sl
+    try:
+        for phys, head, x in writes:
+            x = np.ascontiguousarray(x, np.float32)
+            assert L.aero_kv_slot_write(sl, phys, head, _f(x))
+        out = np.zeros((cap, heads, dim), np.float32)
+        for p in range(cap):
+            for h in range(heads):
+                assert L.aero_kv_slot_read(sl, p, h, _f(out[p, h]))
+        return int(L.aero_kv_slot_bytes(sl)), out
+    finally:
+        L.aero_kv_slot_free(sl)
 
 
 def kv_read_vec(dt: int, q, scale: float, dim: int) -> np.ndarray:

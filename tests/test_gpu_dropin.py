@@ -6,6 +6,7 @@ tests/test_quant_native_extra.py, with the oracle standing where those suites
 use the numpy module.
 """
 import math
+import os
 import struct
 
 import numpy as np
@@ -137,6 +138,85 @@ def test_tensor_native_refusals(hip):
         TN.rmsnorm_rows(np.zeros(4, np.float32), 1e-6)
     r64 = TN.silu(np.arange(8, dtype=np.float64))
     assert r64.dtype == np.float32
+
+
+def test_tensor_native_dense_and_argmax(hip, oracle):
+    """matvec / matmul / argmax (src/tensor.cpp:65-92,180-186): bit-identical to
+    the oracle's restatement of the reference's sums, and to the reference's
+    own compiled functions where oracle/_ref is built."""
+    from oracle import refbind
+    rng = np.random.default_rng(41)
+    for n_tok, n_rows, n_cols in ((1, 1, 1), (1, 7, 5), (1, 896, 896), (1, 300, 4099),
+                                  (3, 33, 130), (5, 257, 4096), (2, 9, 1027)):
+        w = rng.standard_normal((n_rows, n_cols)).astype(np.float32)
+        X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+        print(f"tensor_native dense tokens={n_tok} rows={n_rows} cols={n_cols}", flush=True)
+        want = oracle.dense_matmul(w, X)
+        got = TN.matvec(w, X[0]) if n_tok == 1 else TN.matmul(w, X, threads=3)
+        assert bits_equal(got.reshape(want.shape), want)
+        if n_tok == 1:
+            assert bits_equal(TN.matmul(w, X), want)
+        if refbind.available():
+            assert bits_equal(want, refbind.dense_matmul(w, X))
+    nan, inf = float("nan"), float("inf")
+    cases = [np.array(c, np.float32) for c in
+             ([3, 1, 3, 2], [nan, 5, 7], [1, nan, 0.5, nan, 2], [-0.0, 0.0, -0.0],
+              [-inf, -inf], [-inf, inf, inf], [2.5])]
+    cases += [rng.standard_normal(n).astype(np.float32) for n in (2, 1025, 151936)]
+    cases.append(rng.integers(0, 8, 100000).astype(np.float32))
+    for v in cases:
+        assert TN.argmax(v) == oracle.argmax(v), v[:6]
+        if refbind.available():
+            assert oracle.argmax(v) == refbind.argmax(v)
+    assert TN.threads() == min(os.cpu_count() or 1, 8)
+    with pytest.raises(ValueError):
+        TN.matvec(np.zeros((3, 4), np.float32), np.zeros(5, np.float32))
+    with pytest.raises(ValueError):
+        TN.argmax(np.zeros(0, np.float32))
+
+
+def test_reference_loader_binds_the_library(hip):
+    """The reference's loader (engine/tensor_native.py:41-71) sets these
+    argtypes on every symbol and treats a missing one as an unusable library;
+    bound the same way, libaero_hip.so has every symbol and they compute."""
+    import ctypes
+    from ctypes import POINTER, c_float, c_int, c_int64
+
+    from aero_amd import _lib
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    cp = POINTER(c_float)
+    lib.aero_tensor_matvec.argtypes = [cp, cp, cp, c_int64, c_int64, c_int]
+    lib.aero_tensor_matvec.restype = c_int
+    lib.aero_tensor_matmul.argtypes = [cp, cp, cp, c_int64, c_int64, c_int64, c_int]
+    lib.aero_tensor_matmul.restype = c_int
+    for name in ("silu", "gelu", "softmax"):
+        f = getattr(lib, "aero_tensor_" + name)
+        f.argtypes = [cp, c_int64]
+        f.restype = c_int
+    lib.aero_tensor_mul.argtypes = [cp, cp, c_int64]
+    lib.aero_tensor_mul.restype = c_int
+    lib.aero_tensor_swiglu.argtypes = [cp, cp, c_int64]
+    lib.aero_tensor_swiglu.restype = c_int
+    lib.aero_tensor_rmsnorm.argtypes = [cp, cp, cp, c_int64, c_float]
+    lib.aero_tensor_rmsnorm.restype = c_int
+    lib.aero_tensor_l2norm.argtypes = [cp, cp, cp, c_int64, c_float, c_int]
+    lib.aero_tensor_l2norm.restype = c_int
+    lib.aero_tensor_rmsnorm_rows.argtypes = [cp, c_int64, c_int64, c_float]
+    lib.aero_tensor_rmsnorm_rows.restype = c_int
+    lib.aero_tensor_argmax.argtypes = [cp, c_int64]
+    lib.aero_tensor_argmax.restype = c_int
+    lib.aero_tensor_threads.argtypes = []
+    lib.aero_tensor_threads.restype = c_int
+    w = np.arange(12, dtype=np.float32).reshape(3, 4)
+    x = np.ones(4, np.float32)
+    y = np.empty(3, np.float32)
+    p = lambda a: a.ctypes.data_as(cp)  # noqa: E731
+    assert lib.aero_tensor_matvec(p(w), p(x), p(y), 3, 4, 0) == 1
+    assert y.tolist() == [6.0, 22.0, 38.0]
+    assert lib.aero_tensor_argmax(p(y), 3) == 2
+    assert lib.aero_tensor_argmax(p(y), 0) == -1
+    assert lib.aero_tensor_matvec(p(w), p(x), p(y), 0, 4, 0) == 0
+    assert lib.aero_tensor_threads() >= 1
 
 
 # ---------------------------------------------- tests/test_quant_native_extra.py

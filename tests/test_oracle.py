@@ -759,3 +759,79 @@ def test_ssm_forward_matches_compiled_reference(dts, n_embd, n_k, n_v, d, K):
         assert rel_to_scale(st, rst) <= 1e-5
         # the history holds raw projections: equal to their summation order
         assert rel_to_scale(tail[:tl], rtail[:rtl]) <= 1e-5
+
+
+# ------------------------------------------------- dense fp32 and argmax
+DENSE_SHAPES = ((1, 1, 1), (1, 7, 5), (1, 64, 896), (3, 33, 130), (5, 17, 4096), (2, 9, 4099))
+
+
+@ref_built
+def test_dense_matvec_matmul_match_compiled_reference():
+    """cr_dense_matvec / cr_dense_matmul equal the reference's aero_tensor_matvec
+    / aero_tensor_matmul (src/tensor.cpp:65-92,209-231) bit for bit, for one
+    and several tokens and ragged widths, whatever the reference's thread
+    count."""
+    rng = np.random.default_rng(31)
+    for n_tok, n_rows, n_cols in DENSE_SHAPES:
+        w = rng.standard_normal((n_rows, n_cols)).astype(np.float32)
+        X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+        want = R.dense_matmul(w, X, threads=1)
+        assert bits_equal(O.dense_matmul(w, X), want), (n_tok, n_rows, n_cols)
+        assert bits_equal(R.dense_matmul(w, X, threads=4), want)
+        if n_tok == 1:
+            assert bits_equal(O.dense_matvec(w, X[0]), want[0])
+
+
+def test_dense_matmul_is_the_product():
+    """The fp32 sums are the float64 product to 5e-6 of scale; a planted
+    regrouping (one product at a time in the one-token matvec) differs in
+    the last bits somewhere, so the bit-exact checks above would catch it."""
+    rng = np.random.default_rng(32)
+    for n_tok, n_rows, n_cols in DENSE_SHAPES:
+        w = rng.standard_normal((n_rows, n_cols)).astype(np.float32)
+        X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+        exact = X.astype(np.float64) @ w.astype(np.float64).T
+        assert rel_to_scale(O.dense_matmul(w, X), exact) <= 5e-6
+    w = rng.standard_normal((256, 4096)).astype(np.float32)
+    x = rng.standard_normal((1, 4096)).astype(np.float32)
+    serial = np.empty(256, np.float32)
+    for r in range(256):
+        acc = np.float32(0)
+        for p in (w[r] * x[0]):
+            acc = np.float32(acc + p)
+        serial[r] = acc
+    assert not bits_equal(serial, O.dense_matvec(w, x[0]))
+
+
+ARGMAX_CASES = [
+    [3.0, 1.0, 3.0, 2.0],                         # first of equal maxima
+    [float("nan"), 5.0, 7.0],                      # NaN at 0: index 0
+    [1.0, float("nan"), 0.5, float("nan"), 2.0],   # NaN elsewhere never taken
+    [-0.0, 0.0, -0.0],                             # signed zeros are equal
+    [-np.inf, -np.inf, -np.inf],
+    [-np.inf, np.inf, np.inf],
+    [2.5],
+]
+
+
+@ref_built
+def test_argmax_matches_compiled_reference():
+    rng = np.random.default_rng(33)
+    cases = [np.array(c, np.float32) for c in ARGMAX_CASES]
+    cases += [rng.standard_normal(n).astype(np.float32) for n in (2, 1000, 151936)]
+    t = rng.integers(0, 8, 5000).astype(np.float32)          # many ties
+    cases.append(t)
+    for v in cases:
+        assert O.argmax(v) == R.argmax(v), v[:8]
+
+
+def test_argmax_closed_forms():
+    """First index of the largest value (np.argmax) on NaN-free input; 0 when
+    v[0] is NaN; NaN elsewhere skipped."""
+    rng = np.random.default_rng(34)
+    for n in (1, 2, 77, 5000):
+        v = rng.integers(-3, 4, n).astype(np.float32)
+        assert O.argmax(v) == int(np.argmax(v))
+    assert O.argmax(np.array(ARGMAX_CASES[1], np.float32)) == 0
+    assert O.argmax(np.array(ARGMAX_CASES[2], np.float32)) == 4
+    assert O.argmax(np.array(ARGMAX_CASES[3], np.float32)) == 0
