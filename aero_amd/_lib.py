@@ -84,6 +84,8 @@ PROTOTYPES = {
     "aero_hip_act_mul": (c_int, [c_int, vp, vp, vp, c_int64, vp]),
     "aero_hip_add_rmsnorm": (c_int, [vp, vp, vp, vp, vp, c_int64, c_int64, c_float, c_int,
                                      vp]),
+    "aero_hip_post_norm_add": (c_int, [vp, vp, vp, vp, c_float, c_float, vp, vp, c_int64,
+                                       c_int64, c_float, c_int, vp]),
     "aero_hip_rope_inv_freq": (c_int64, [c_int64, c_int64, c_float, fp, c_int64, fp]),
     "aero_hip_rope_tables": (c_int, [vp, c_int64, vp, c_int64, vp, vp, vp]),
     "aero_hip_qk_norm_rope": (c_int, [vp, vp, c_int64, vp, vp, c_int64, vp, vp, c_float,

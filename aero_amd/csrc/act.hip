@@ -202,6 +202,7 @@ bool act_mul(int kind, const float* g, const float* u, float* out, int64_t n,
     case AERO_ACT_SILU: return run_act_kind<AERO_ACT_SILU>(g, u, out, n, s);
     case AERO_ACT_GELU: return run_act_kind<AERO_ACT_GELU>(g, u, out, n, s);
     case AERO_ACT_GELU_TANH: return run_act_kind<AERO_ACT_GELU_TANH>(g, u, out, n, s);
+    case AERO_ACT_SIGMOID: return run_act_kind<AERO_ACT_SIGMOID>(g, u, out, n, s);
     case AERO_ACT_IDENTITY:
         if (u == nullptr) {
             set_error("act_mul: identity needs `up`");

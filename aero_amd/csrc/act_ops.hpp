@@ -1,7 +1,9 @@
 // Activation functions of the act·mul ops, shared by act.hip and the GEMV's
 // fused gate/up epilogue so both compute the same values: SiLU g*sigmoid(g)
 // (src/tensor.cpp:104-106,120-125), erf GELU with the Abramowitz & Stegun
-// 7.1.26 erf (src/tensor.cpp:52-59,108-114), tanh-approximate GELU, identity.
+// 7.1.26 erf (src/tensor.cpp:52-59,108-114), tanh-approximate GELU, identity,
+// and the sigmoid of the attention output gate (src/attention_layer.cpp:
+// 262-263: att * (1/(1+exp(-g))), the same product as sigmoid(g) * att).
 #pragma once
 #include "common.hpp"
 #include "aero_hip.h"
@@ -26,6 +28,8 @@ __device__ __forceinline__ float act(float v) {
 
     } else if constexpr (KIND == AERO_ACT_GELU) {
         return 0.5f * v * (1.0f + erf_as(v * 0.7071067811865476f));
+    } else if constexpr (KIND == AERO_ACT_SIGMOID) {
+        return 1.0f / (1.0f + expf(-v));
     } else if constexpr (KIND == AERO_ACT_GELU_TANH) {
         return 0.5f * v *
                (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));

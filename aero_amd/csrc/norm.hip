@@ -392,6 +392,191 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormParams p) {
     }
 }
 
+// ---------------------------------------------- Gemma sandwich-norm sites
+// After a Gemma block's attention and after its FFN (src/model.cpp:213-215,
+// 224-231), the sublayer output y is normalised with its post-norm weight,
+// scaled by ds, added to the residual stream x, the sum scaled by ss (1 at
+// the attention site), and the next norm taken of the result:
+//   a = (y * inv(y)) * w1,  x' = (x + ds * a) * ss,  h = (x' * inv(x')) * w2
+// with inv(v) = 1/sqrtf(mean(v^2) + eps) and (1+w) weights under
+// AERO_NORM_UNIT_OFFSET. One pass reads y and x and writes x' and h, the
+// four streams of add + norm, where the reference makes four passes (norm,
+// add, norm, and the output-scale pass). Lanes own row chunks as
+// norm_vec_kernel; two cross-wave sums.
+struct PostParams {
+    const float* y;
+    const float* x;
+    const float* w1;     // post-norm weight (null: ones)
+    const float* w2;     // next norm's weight (null: ones)
+    float* xo;           // x' (may alias x)
+    float* h;
+    int64_t rows;
+    int cols;
+    float eps, ds, ss;
+    int flags;
+};
+
+__device__ __forceinline__ float4 w4_at(const float* w, int c, int flags) {
+    if (w == nullptr) return make_float4(1.f, 1.f, 1.f, 1.f);
+    float4 v = reinterpret_cast<const float4*>(w)[c];
+    if (flags & AERO_NORM_UNIT_OFFSET) {
+        v.x = 1.0f + v.x; v.y = 1.0f + v.y; v.z = 1.0f + v.z; v.w = 1.0f + v.w;
+    }
+    return v;
+}
+
+template <int TPR>
+__device__ __forceinline__ float row_sum(float ss, float* part, int tid, int lr) {
+    if constexpr (TPR <= 64) {
+        return group_sum<TPR>(ss);
+    } else {
+        constexpr int WPR = TPR / 64;
+        ss = group_sum<64>(ss);
+        if ((tid & 63) == 0) part[tid >> 6] = ss;
+        __syncthreads();
+        const int w0 = lr * WPR;
+        ss = part[w0];
+#pragma unroll
+        for (int k = 1; k < WPR; ++k) ss += part[w0 + k];
+        return ss;
+    }
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(TPR > 256 ? TPR : 256)
+void post_norm_add_kernel(PostParams p) {
+    constexpr int BS = TPR > 256 ? TPR : 256;
+    constexpr int RPB = BS / TPR;
+    __shared__ float part1[BS / 64], part2[BS / 64];
+    const int tid = threadIdx.x;
+    const int lr = tid / TPR;
+    const int t = tid % TPR;
+    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
+    const bool ok = row < p.rows;
+    const int nv = p.cols >> 2;
+    const int64_t base = ok ? row * (int64_t)p.cols : 0;
+    float4 yv[V], xv[V], w1[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = i * TPR + t;
+        if (ok && c < nv) {
+            yv[i] = ld_stream(p.y + base + 4 * c);
+            xv[i] = ld_stream(p.x + base + 4 * c);
+            w1[i] = w4_at(p.w1, c, p.flags);
+        } else {
+            yv[i] = xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            w1[i] = make_float4(1.f, 1.f, 1.f, 1.f);
+        }
+    }
+    float s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        s1 += yv[i].x * yv[i].x;
+        s1 += yv[i].y * yv[i].y;
+        s1 += yv[i].z * yv[i].z;
+        s1 += yv[i].w * yv[i].w;
+    }
+    s1 = row_sum<TPR>(s1, part1, tid, lr);
+    const float inv1 = 1.0f / sqrtf(s1 / (float)p.cols + p.eps);
+    const int64_t r0 = (int64_t)blockIdx.x * RPB;
+    const StreamOut ox(p.xo + r0 * p.cols, (p.rows - r0) * (int64_t)p.cols * 4);
+    const uint32_t ob = (uint32_t)(lr * p.cols) * 4u;
+    auto step = [&](float y, float w, float x) {
+        const float a = (y * inv1) * w;
+        return (x + p.ds * a) * p.ss;
+    };
+    float s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        xv[i].x = step(yv[i].x, w1[i].x, xv[i].x);
+        xv[i].y = step(yv[i].y, w1[i].y, xv[i].y);
+        xv[i].z = step(yv[i].z, w1[i].z, xv[i].z);
+        xv[i].w = step(yv[i].w, w1[i].w, xv[i].w);
+        const int c = i * TPR + t;
+        if (ok && c < nv) ox.store(ob + 16u * c, xv[i]);
+        else xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        s2 += xv[i].x * xv[i].x;
+        s2 += xv[i].y * xv[i].y;
+        s2 += xv[i].z * xv[i].z;
+        s2 += xv[i].w * xv[i].w;
+    }
+    s2 = row_sum<TPR>(s2, part2, tid, lr);
+    const float inv2 = 1.0f / sqrtf(s2 / (float)p.cols + p.eps);
+    const StreamOut oh(p.h + r0 * p.cols, (p.rows - r0) * (int64_t)p.cols * 4);
+    if (!ok) return;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = i * TPR + t;
+        if (c >= nv) continue;
+        const float4 w = w4_at(p.w2, c, p.flags);
+        const float4 o = make_float4((xv[i].x * inv2) * w.x, (xv[i].y * inv2) * w.y,
+                                     (xv[i].z * inv2) * w.z, (xv[i].w * inv2) * w.w);
+        oh.store(ob + 16u * c, o);
+    }
+}
+
+// Any shape / alignment: one 256-lane workgroup a row, the same arithmetic;
+// x' is read back only by the lane that wrote it.
+__global__ __launch_bounds__(256) void post_norm_add_scalar_kernel(PostParams p) {
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t base = row * (int64_t)p.cols;
+    __shared__ float part[4];
+    auto wv = [&](const float* w, int c) {
+        if (w == nullptr) return 1.0f;
+        return (p.flags & AERO_NORM_UNIT_OFFSET) ? 1.0f + w[c] : w[c];
+    };
+    float s1 = 0.0f;
+    for (int c = tid; c < p.cols; c += 256) s1 += p.y[base + c] * p.y[base + c];
+    s1 = group_sum<64>(s1);
+    if ((tid & 63) == 0) part[tid >> 6] = s1;
+    __syncthreads();
+    s1 = ((part[0] + part[1]) + part[2]) + part[3];
+    __syncthreads();
+    const float inv1 = 1.0f / sqrtf(s1 / (float)p.cols + p.eps);
+    float s2 = 0.0f;
+    for (int c = tid; c < p.cols; c += 256) {
+        const float a = (p.y[base + c] * inv1) * wv(p.w1, c);
+        const float v = (p.x[base + c] + p.ds * a) * p.ss;
+        p.xo[base + c] = v;
+        s2 += v * v;
+    }
+    s2 = group_sum<64>(s2);
+    if ((tid & 63) == 0) part[tid >> 6] = s2;
+    __syncthreads();
+    s2 = ((part[0] + part[1]) + part[2]) + part[3];
+    const float inv2 = 1.0f / sqrtf(s2 / (float)p.cols + p.eps);
+    for (int c = tid; c < p.cols; c += 256)
+        p.h[base + c] = (p.xo[base + c] * inv2) * wv(p.w2, c);
+}
+
+using PostKernel = void (*)(PostParams);
+
+template <int TPR>
+PostKernel pick_post_v(int v) {
+    switch (v) {
+    case 1: return post_norm_add_kernel<TPR, 1>;
+    case 2: return post_norm_add_kernel<TPR, 2>;
+    case 3: return post_norm_add_kernel<TPR, 3>;
+    case 4: return post_norm_add_kernel<TPR, 4>;
+    default: return nullptr;
+    }
+}
+
+PostKernel pick_post(int tpr, int v) {
+    switch (tpr) {
+    case 8: return pick_post_v<8>(v);
+    case 16: return pick_post_v<16>(v);
+    case 32: return pick_post_v<32>(v);
+    case 64: return pick_post_v<64>(v);
+    case 128: return pick_post_v<128>(v);
+    case 256: return pick_post_v<256>(v);
+    case 512: return pick_post_v<512>(v);
+    case 1024: return pick_post_v<1024>(v);
+    default: return nullptr;
+    }
+}
+
 using NormKernel = void (*)(NormParams);
 using NormLoopKernel = void (*)(NormParams, int);
 
@@ -509,6 +694,29 @@ bool run_norm(NormParams p, int mode, hipStream_t stream) {
                   stream, p);
 }
 
+bool run_post_norm_add(const PostParams& p, hipStream_t stream) {
+    if (p.rows == 0) return true;
+    const bool vec = (p.cols % 4 == 0) && aligned16(p.y) && aligned16(p.x) && aligned16(p.xo) &&
+                     aligned16(p.h) && (p.w1 == nullptr || aligned16(p.w1)) &&
+                     (p.w2 == nullptr || aligned16(p.w2));
+    int tpr = 0, v = 0;
+    if (vec) {
+        // at most 4 float4 a lane (the default norm shape)
+        int t = 8;
+        while (t < 1024 && t * 4 < p.cols / 4) t *= 2;
+        tpr = t;
+        v = (p.cols / 4 + t - 1) / t;
+    }
+    if (vec && v <= 4) {
+        const int bs = tpr > 256 ? tpr : 256;
+        const int64_t blocks = (p.rows + bs / tpr - 1) / (bs / tpr);
+        return launch("post_norm_add_kernel", pick_post(tpr, v), dim3((unsigned)blocks), dim3(bs),
+                      0, stream, p);
+    }
+    return launch("post_norm_add_scalar_kernel", post_norm_add_scalar_kernel,
+                  dim3((unsigned)p.rows), dim3(256), 0, stream, p);
+}
+
 }  // namespace
 
 // Used by the host-pointer ABI (dropin.hip).
@@ -570,6 +778,23 @@ int aero_hip_add_rmsnorm(const float* x, const float* d, float* x_out, const flo
     }
     aero::NormParams p{x, d, w, h, rows, (int)cols, 1, (int)cols, eps, flags, x_out};
     return aero::run_norm(p, aero::kResid, (hipStream_t)stream) ? 1 : 0;
+}
+
+int aero_hip_post_norm_add(const float* y, const float* x, float* x_out, const float* w_post,
+                           float ds, float ss, const float* w_next, float* h, int64_t rows,
+                           int64_t cols, float eps, int flags, void* stream) {
+    if (!y || !x || !x_out || !h || rows < 0 || cols <= 0 || cols > (int64_t)0x7fffffff ||
+        rows > (int64_t)0x7fffffff || (flags & ~AERO_NORM_UNIT_OFFSET) != 0) {
+        aero::set_error("post_norm_add: bad arguments (rows=%lld cols=%lld flags=%d)",
+                        (long long)rows, (long long)cols, flags);
+        return 0;
+    }
+    if (h == y || h == x || h == x_out || y == x_out) {
+        aero::set_error("post_norm_add: h must not alias y, x or x_out, nor x_out y");
+        return 0;
+    }
+    aero::PostParams p{y, x, w_post, w_next, x_out, h, rows, (int)cols, eps, ds, ss, flags};
+    return aero::run_post_norm_add(p, (hipStream_t)stream) ? 1 : 0;
 }
 
 }  // extern "C"

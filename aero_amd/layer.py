@@ -60,12 +60,26 @@ class BlockConfig:
     qk_norm: bool = False
     unit_offset: bool = False
     emb_scale: bool = False
+    # Gemma blocks (src/model.cpp:181-232): a post-norm on the attention and
+    # on the FFN output before each residual add, and the layer output scale
+    # applied to the deltas (out_scale_mode 1) or to the whole sum (2)
+    post_norms: bool = False
+    out_scale_mode: int = 0
+    # the attention layer's options (src/attention_layer.cpp:60-156,262-263):
+    # q rows interleaved per head with a gate [q_h | gate_h] and a sigmoid
+    # output gate; a weightless per-head V norm; V := K (no V projection);
+    # RoPE frequency factors
+    attn_gate: bool = False
+    v_norm: bool = False
+    v_from_k: bool = False
+    freq_factors: tuple | None = None
 
     @classmethod
-    def from_shape(cls, s: W.Shape, wtype: int, vocab: int | None = None) -> "BlockConfig":
+    def from_shape(cls, s: W.Shape, wtype: int, vocab: int | None = None,
+                   **options) -> "BlockConfig":
         return cls(s.hidden, s.hq, s.hk, s.head_dim, s.ffn, s.eps, s.theta, s.n_rot, s.act,
                    wtype, s.emb_type, s.vocab if vocab is None else vocab, s.qk_norm,
-                   s.unit_offset, s.emb_scale)
+                   s.unit_offset, s.emb_scale, **options)
 
 
 class BlockWeights:
@@ -73,15 +87,17 @@ class BlockWeights:
     trained-like scale (values of rms ~1/sqrt(columns)), the embedding table,
     fp32 norm weights; kept on the host (`host`) and in HBM."""
 
-    MATS = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
-
     def __init__(self, cfg: BlockConfig, seed: int = 0):
         rng = np.random.default_rng(seed)
         N, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
         HD, KD = cfg.n_head * D, cfg.n_head_kv * D
-        bv = W.BLOCK[cfg.wtype][0]
-        shapes = {"wq": (HD, N), "wk": (KD, N), "wv": (KD, N), "wo": (N, HD), "wg": (F, N),
-                  "wu": (F, N), "wd": (N, F)}
+        bv, bb = W.BLOCK[cfg.wtype]
+        # with the output gate, wq holds 2*HD rows, [q_h | gate_h] per head,
+        # as the reference's file stores it
+        shapes = {"wq": (2 * HD if cfg.attn_gate else HD, N), "wk": (KD, N), "wv": (KD, N),
+                  "wo": (N, HD), "wg": (F, N), "wu": (F, N), "wd": (N, F)}
+        self.MATS = tuple(m for m in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
+                          if not (m == "wv" and cfg.v_from_k))
         h = {}
         for name in self.MATS:
             r, c = shapes[name]
@@ -95,12 +111,25 @@ class BlockWeights:
             w = rng.standard_normal(n, dtype=np.float32) * np.float32(0.1)
             return w if cfg.unit_offset else (np.float32(1) + w).astype(np.float32)
 
-        for name in ("attn_norm", "ffn_norm", "out_norm"):
+        for name in ("attn_norm", "ffn_norm", "out_norm") + (
+                ("post_attn_norm", "post_ffw_norm") if cfg.post_norms else ()):
             h[name] = norm_w(N)
         if cfg.qk_norm:
             h["q_norm"], h["k_norm"] = norm_w(D), norm_w(D)
+        # the layer output scale (a per-layer scalar of the file)
+        self.out_scale = float(np.float32(rng.uniform(0.5, 1.5))) if cfg.out_scale_mode else 1.0
         self.host = h
-        self.dev = {k: DA.from_numpy(v) for k, v in h.items()}
+        dev = {k: DA.from_numpy(v) for k, v in h.items() if k != "wq" or not cfg.attn_gate}
+        if cfg.attn_gate:
+            # the q and the gate rows of each head, regrouped once at upload
+            # into two matrices (row bytes are whole blocks, so this moves
+            # bytes only), so the projection writes q and the gate to their
+            # own buffers and no split pass runs per step
+            rb = (N // bv) * bb
+            rows = h["wq"].reshape(cfg.n_head, 2, D, rb)
+            dev["wq"] = DA.from_numpy(np.ascontiguousarray(rows[:, 0]).reshape(-1))
+            dev["wq_gate"] = DA.from_numpy(np.ascontiguousarray(rows[:, 1]).reshape(-1))
+        self.dev = dev
 
 
 class LayerStep:
@@ -135,6 +164,10 @@ class LayerStep:
         self.xs = (self.x, DA.empty((T, N)))
         self._cur = 0
         self.q, self.att = DA.empty((T, HD)), DA.empty((T, HD))
+        self.qgate = DA.empty((T, HD)) if cfg.attn_gate else None
+        # the pending post-norm of a Gemma block's FFN output, applied by the
+        # next norm site: (post_ffw_norm weight, ds, ss)
+        self._post = None
         self.o = DA.empty((T, N))
         self.dn = DA.empty((T, N))
         self.g, self.u = DA.empty((T, F)), DA.empty((T, F))
@@ -142,7 +175,9 @@ class LayerStep:
         # one KV cache a layer; K, V are the first layer's
         self.kv = [(DA.empty((kv_cap, KD)), DA.empty((kv_cap, KD))) for _ in self.layers]
         self.K, self.V = self.kv[0]
-        n_rot, inv = ops.rope_inv_freq(D, cfg.n_rot, cfg.theta)
+        n_rot, inv = ops.rope_inv_freq(D, cfg.n_rot, cfg.theta,
+                                       None if cfg.freq_factors is None
+                                       else np.asarray(cfg.freq_factors, np.float32))
         self.n_rot, self.inv = n_rot, DA.from_numpy(inv)
         self.scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
         rb = (N // W.BLOCK[cfg.wtype][0]) * W.BLOCK[cfg.wtype][1]
@@ -203,6 +238,7 @@ class LayerStep:
         s = stream
         x, h = self.x.view((T, N)), self.h.view((T, N))
         self._cur = 0
+        self._post = None
         w0 = self.layers[0]
 
         # embedding (+ the first block's attention norm when its projections
@@ -246,8 +282,27 @@ class LayerStep:
         if self._folds_rope(T, h_ready):
             rope = {"n": 2, "head_dim": D, "mode": ops.ROPE_NEOX, "pos": self.pos,
                     "inv_freq": self.inv}
-        self._project(w, resid, "attn_norm", [d["wq"], d["wk"], d["wv"]], [q, kq, vq],
-                      [H * D, HK * D, HK * D], T, h_ready, s, rope=rope)
+        # V := K projects K's matrix again into the V cache rows (the raw
+        # projection, before the k norm and RoPE, as src/attention_layer.cpp:
+        # 67-69 copies it); with the output gate a fourth matrix writes the
+        # gate rows
+        mats = [d["wq"], d["wk"], d["wk"] if c.v_from_k else d["wv"]]
+        ys, rows = [q, kq, vq], [H * D, HK * D, HK * D]
+        if c.attn_gate:
+            mats.append(d["wq_gate"])
+            ys.append(self.qgate.view((T, H * D)))
+            rows.append(H * D)
+        self._project(w, resid, "attn_norm", mats, ys, rows, T, h_ready, s, rope=rope)
+
+        # the weightless per-head V norm (src/attention_layer.cpp:109-114; not
+        # on a V taken from K), in the cache rows
+        if c.v_norm and not c.v_from_k:
+            if self.gpu("rmsnorm"):
+                ops.rmsnorm(vq, None, vq, T * HK, D, c.eps, stream=s)
+            else:
+                _, vn = self.hooks["rmsnorm"](self._host(vq, (T * HK, D)), None,
+                                              np.ones(D, np.float32), c.eps, False)
+                self._put(vq, vn)
 
         # per-head norms and RoPE, in place (the cache rows of k included),
         # unless the projection's epilogue rotated q and k
@@ -267,12 +322,22 @@ class LayerStep:
         att = self.att.view((T, H * D))
         ops.attention(q, Kc, Vc, att, T, H, HK, D, D, kv_len + T, 1.0 / math.sqrt(D),
                       qpos=self.pos, stream=s)
+        if c.attn_gate:
+            # att *= sigmoid(gate) (src/attention_layer.cpp:262-263)
+            ops.act_mul("sigmoid", self.qgate.view((T, H * D)), att, att, stream=s)
         o = self.o.view((T, N))
         ops.matvec(c.wtype, d["wo"], att, o, N, H * D, T, stream=s)
 
-        # x += o; h = rmsnorm(x); g = act(h Wg) * (h Wu)
+        # x += o; h = rmsnorm(x); g = act(h Wg) * (h Wu). Gemma: x += ds *
+        # post_attn_norm(o) before that norm (src/model.cpp:213-219)
         g = self.g.view((T, F))
-        if self._folds_norm(T) and self.fuse("act_gemm") and self.gpu("act"):
+        if c.post_norms:
+            h = self.h.view((T, N))
+            ds = w.out_scale if c.out_scale_mode == 1 else 1.0
+            self._norm(w, self._x(T), o, "ffn_norm", h, T, s,
+                       post=(d["post_attn_norm"], ds, 1.0))
+            self._gate_up(w, h, g, T, s)
+        elif self._folds_norm(T) and self.fuse("act_gemm") and self.gpu("act"):
             xi, xo = self._advance(T, o)
             ops.norm_matmul_gate_up(c.wtype, d["wg"], d["wu"], xi, g, F, N, T, act=c.act,
                                     norm_w=d["ffn_norm"], eps=c.eps, unit_offset=c.unit_offset,
@@ -296,7 +361,30 @@ class LayerStep:
         # residual input in dn was consumed by its first norm)
         dn = self.dn.view((T, N))
         ops.matvec(c.wtype, d["wd"], g, dn, N, F, T, stream=s)
+        if c.post_norms:
+            # the next norm site adds (x + ds * post_ffw_norm(dn)) * ss
+            # (src/model.cpp:228-231)
+            self._post = (d["post_ffw_norm"],
+                          w.out_scale if c.out_scale_mode == 1 else 1.0,
+                          w.out_scale if c.out_scale_mode == 2 else 1.0)
         return dn
+
+    def _gate_up(self, w: BlockWeights, h, g, T: int, s) -> None:
+        """g = act(h Wg) * (h Wu) for a normalised h: one launch (the split
+        GEMM's act epilogue, or the fused decode GEMV) when act-mul folds."""
+        c, d = self.cfg, w.dev
+        F, N = c.ffn, c.hidden
+        if self.gpu("act") and self.fuse("act_gemm"):
+            ops.norm_matmul_gate_up(c.wtype, d["wg"], d["wu"], h, g, F, N, T, act=c.act,
+                                    norm=False, stream=s)
+            return
+        u = self.u.view((T, F))
+        ops.matvec(c.wtype, d["wg"], h, g, F, N, T, stream=s)
+        ops.matvec(c.wtype, d["wu"], h, u, F, N, T, stream=s)
+        if self.gpu("act"):
+            ops.act_mul(c.act, g, u, g, stream=s)
+        else:
+            self._put(g, self.hooks["act"](self._host(g, (T, F)), self._host(u, (T, F))))
 
     def _folds_norm(self, T: int) -> bool:
         """True when the norm (and residual add) before a projection folds into
@@ -304,11 +392,15 @@ class LayerStep:
         rule (ops.split_ok) gives the split path to this type and shape (the
         call itself takes it from 5-16 tokens where it is faster), the fused
         decode GEMV's prologue below that."""
-        if not (self.fuse("norm_gemm") and self.gpu("rmsnorm")):
+        c = self.cfg
+        if not (self.fuse("norm_gemm") and self.gpu("rmsnorm")) or c.post_norms:
+            # Gemma's sites take a second norm of the sublayer output first:
+            # their own kernel (post_norm_add), then the projection on h
             return False
         if T >= 32:
-            c = self.cfg
-            return ops.split_ok(c.wtype, c.hidden, (c.n_head + 2 * c.n_head_kv) * c.head_dim, T)
+            return ops.split_ok(c.wtype, c.hidden,
+                                ((2 if c.attn_gate else 1) * c.n_head + 2 * c.n_head_kv)
+                                * c.head_dim, T)
         return self.rows16
 
     def _folds_rope(self, T: int, h_ready: bool) -> bool:
@@ -334,13 +426,23 @@ class LayerStep:
         self._cur ^= 1
         return xi, self._x(T)
 
-    def _norm(self, wts: BlockWeights, x, resid, wname, h, T, s, x_out=None) -> None:
+    def _norm(self, wts: BlockWeights, x, resid, wname, h, T, s, x_out=None,
+              post=None) -> None:
         """x_out = x + resid (resid given; x_out None: x in place); h =
-        rmsnorm of that (or of x) * the norm weight `wname`."""
+        rmsnorm of that (or of x) * the norm weight `wname`. Gemma blocks:
+        x_out = (x + ds * rmsnorm(resid) * w_post) * ss with (w_post, ds, ss)
+        = `post`, or the pending post-norm of the previous block's FFN."""
         c = self.cfg
         w = wts.dev[wname]
         if resid is None and x_out is not None and x_out.ptr != x.ptr:
             raise ValueError("_norm: x_out without a residual input")
+        if resid is not None and c.post_norms:
+            post = post if post is not None else self._post
+            if not self.gpu("rmsnorm"):
+                raise select.HostPathRequired("the Gemma post-norm sites run on the GPU only")
+            ops.post_norm_add(resid, x, post[0], w, h, T, c.hidden, c.eps, ds=post[1],
+                              ss=post[2], unit_offset=c.unit_offset, x_out=x_out, stream=s)
+            return
         if self.gpu("rmsnorm"):
             if resid is not None:
                 ops.add_rmsnorm(x, resid, w, h, T, c.hidden, c.eps, c.unit_offset, x_out=x_out,
@@ -373,6 +475,10 @@ class LayerStep:
             self._norm(wts, self._x(T), resid, wname, h, T, s)
         if self.fuse("norm_gemm") and T < 32 and self.rows16 and len(mats) <= 3:
             ops.norm_matvec(c.wtype, mats, h, ys, rows, c.hidden, T, norm=False, stream=s)
+        elif self.fuse("norm_gemm"):
+            # every matrix in one launch where the shape allows (split GEMM,
+            # fused GEMV), with x as is
+            ops.norm_matmul(c.wtype, mats, h, ys, rows, c.hidden, T, norm=False, stream=s)
         else:
             for m, y, r in zip(mats, ys, rows):
                 ops.matvec(c.wtype, m, h, y, r, c.hidden, T, stream=s)

@@ -22,9 +22,10 @@ ACT_SILU = 0
 ACT_GELU = 1
 ACT_GELU_TANH = 2
 ACT_IDENTITY = 3
+ACT_SIGMOID = 4
 ACTS = {"silu": ACT_SILU, "swiglu": ACT_SILU, "gelu": ACT_GELU, "geglu": ACT_GELU,
         "gelu_erf": ACT_GELU, "gelu_tanh": ACT_GELU_TANH, "geglu_tanh": ACT_GELU_TANH,
-        "identity": ACT_IDENTITY, "mul": ACT_IDENTITY}
+        "identity": ACT_IDENTITY, "mul": ACT_IDENTITY, "sigmoid": ACT_SIGMOID}
 
 ROPE_NEOX = 0
 ROPE_INTERLEAVED = 1
@@ -76,6 +77,23 @@ def gated_rmsnorm_silu(x: DeviceArray, z: DeviceArray, w: DeviceArray, out: Devi
     _lib.check(_lib.lib().aero_hip_gated_rmsnorm_silu(x.ptr, z.ptr, w.ptr, w.size, out.ptr,
                                                       rows, inner, group, float(eps),
                                                       _s(stream)), "gated_rmsnorm_silu")
+
+
+def post_norm_add(y: DeviceArray, x: DeviceArray, w_post: DeviceArray | None,
+                  w_next: DeviceArray | None, h: DeviceArray, rows: int, cols: int, eps: float,
+                  ds: float = 1.0, ss: float = 1.0, unit_offset: bool = False,
+                  x_out: DeviceArray | None = None, stream: Stream | None = None) -> None:
+    """A Gemma sandwich-norm site in one pass: x_out = (x + ds * rmsnorm(y) *
+    w_post) * ss (x_out None: x in place), h = rmsnorm(x_out) * w_next."""
+    x_out = x if x_out is None else x_out
+    for a, name in ((y, "y"), (x, "x"), (x_out, "x_out"), (h, "h")):
+        _need(a, rows * cols, np.float32, name)
+    _need(w_post, cols, np.float32, "w_post")
+    _need(w_next, cols, np.float32, "w_next")
+    _lib.check(_lib.lib().aero_hip_post_norm_add(
+        y.ptr, x.ptr, x_out.ptr, as_ptr(w_post), float(ds), float(ss), as_ptr(w_next), h.ptr,
+        rows, cols, float(eps), NORM_UNIT_OFFSET if unit_offset else 0, _s(stream)),
+        "post_norm_add")
 
 
 def add_rmsnorm(x: DeviceArray, d: DeviceArray, w: DeviceArray | None, h: DeviceArray,

@@ -206,6 +206,21 @@ int aero_hip_gated_rmsnorm_silu(const float* x, const float* z, const float* w,
                                 int64_t inner, int64_t group, float eps,
                                 void* stream);
 
+/* A Gemma block's sandwich-norm site in one pass (src/model.cpp:213-215,
+ * 224-231): the sublayer output y is normalised with its post-norm weight,
+ * scaled by ds and added to the residual stream, the sum scaled by ss, and
+ * the next norm taken of it:
+ *   a = rmsnorm(y) * w_post;  x_out = (x + ds * a) * ss;
+ *   h = rmsnorm(x_out) * w_next
+ * rmsnorm as aero_hip_rmsnorm (same eps; flags 0 or AERO_NORM_UNIT_OFFSET
+ * for both weights; NULL weights are ones). After attention ss = 1 and
+ * w_next is the FFN norm; after the FFN, ss is the layer output scale and
+ * w_next the next block's attention norm (or the output norm). x_out may
+ * alias x; h must not alias y, x or x_out, nor x_out y. [rows, cols] fp32. */
+int aero_hip_post_norm_add(const float* y, const float* x, float* x_out, const float* w_post,
+                           float ds, float ss, const float* w_next, float* h, int64_t rows,
+                           int64_t cols, float eps, int flags, void* stream);
+
 /* Residual add + RMSNorm in one pass: x_out = x + d (the residual stream),
  * h = rmsnorm(x_out) * w as aero_hip_rmsnorm (flags 0 or
  * AERO_NORM_UNIT_OFFSET; w NULL = ones). Replaces the reference block's
@@ -221,6 +236,8 @@ int aero_hip_add_rmsnorm(const float* x, const float* d, float* x_out, const flo
 #define AERO_ACT_GELU      1 /* erf GELU, A&S 7.1.26   src/tensor.cpp:52-59,108-114   */
 #define AERO_ACT_GELU_TANH 2 /* tanh-approximate GELU (no reference function)        */
 #define AERO_ACT_IDENTITY  3 /* plain product (mul_)   src/tensor.cpp:116-118         */
+#define AERO_ACT_SIGMOID   4 /* sigmoid(g), the attention output gate
+                                src/attention_layer.cpp:262-263 (act-mul only)      */
 
 /* out[i] = act(gate[i]) * up[i] (up == NULL: out = act(gate)). n elements.
  * out may alias gate or up. Replaces swiglu_ / gelu_+mul_ / silu_ / mul_. */

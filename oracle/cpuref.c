@@ -26,6 +26,9 @@
  *                      spot values of tests/test_tensor_native.py:118-132;
  *                      compiled reference (bit-exact for silu/gelu/swiglu/mul).
  *                      gelu_tanh has no reference function: closed form only.
+ *                      sigmoid (kind 4, the attention output gate): float64
+ *                      closed form, and v * sigmoid(v) is the compiled
+ *                      reference's silu bit for bit.
  *   cr_dense_matvec / cr_dense_matmul  compiled reference src/tensor.cpp
  *                      (bit-exact, 1-5 tokens, ragged widths); float64 product
  *                      to 5e-6 of scale; a planted regrouping of the sum (one
@@ -146,6 +149,8 @@ static float act1(int kind, float v) {
     case 2: /* tanh-approximate GELU: no reference function; closed form */
         return 0.5f * v *
                (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+    case 4: /* src/attention_layer.cpp:262-263: the output gate 1/(1+exp(-g)) */
+        return sigmoid_recip(v);
     default:
         return v;
     }

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libaero_cpuref.so")
 
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, BF16 = 0, 1, 8, 12, 13, 14, 23, 30
-ACT_SILU, ACT_GELU, ACT_GELU_TANH, ACT_IDENTITY = 0, 1, 2, 3
+ACT_SILU, ACT_GELU, ACT_GELU_TANH, ACT_IDENTITY, ACT_SIGMOID = 0, 1, 2, 3, 4
 ROPE_NEOX, ROPE_INTERLEAVED = 0, 1
 
 _lib = None

@@ -165,3 +165,56 @@ def test_add_rmsnorm_refuses_aliased_h(hip):
                                       None) == 0
     assert L.aero_hip_add_rmsnorm(x.ptr, d.ptr, x.ptr, None, d.ptr, 2, 64, 1e-6,
                                   ops.NORM_L2, None) == 0
+
+
+# ------------------------------------------------------------ post_norm_add
+def post_norm_ref(oracle, y, x, w1, w2, eps, ds, ss, unit):
+    """The reference's gemma_block site (src/model.cpp:213-219, 228-231):
+    a = norm_row(y, w1); x' = (x + ds*a) * ss; h = norm_row(x', w2)."""
+    a = oracle.rmsnorm_rows(y, w1, eps, unit)
+    xn = ((x + np.float32(ds) * a) * np.float32(ss)).astype(np.float32)
+    return xn, oracle.rmsnorm_rows(xn, w2, eps, unit)
+
+
+@pytest.mark.parametrize("rows,cols", [(2048, 2560), (64, 2560), (1, 2560), (512, 4096),
+                                       (7, 8192), (33, 1000), (5, 130)])
+@pytest.mark.parametrize("ds,ss", [(1.0, 1.0), (0.7, 1.0), (1.0, 1.3), (0.5, 0.9)])
+@pytest.mark.parametrize("unit", [False, True])
+def test_post_norm_add_vs_oracle(hip, oracle, rows, cols, ds, ss, unit):
+    """x' within one rounding of every step (the post-norm's 1e-5 carried
+    through the add) and h within 1e-5 of scale of the oracle's composition;
+    the Gemma-3-4B-style config-3 shape (2048 x 2560) among them."""
+    rng = np.random.default_rng(rows * cols)
+    y = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(3)
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    w1 = (rng.standard_normal(cols) * 0.1 + (0 if unit else 1)).astype(np.float32)
+    w2 = (rng.standard_normal(cols) * 0.1 + (0 if unit else 1)).astype(np.float32)
+    print(f"post_norm_add {rows}x{cols} ds={ds} ss={ss} unit={unit}", flush=True)
+    dy, dx = DA.from_numpy(y), DA.from_numpy(x)
+    h = DA.empty((rows, cols))
+    ops.post_norm_add(dy, dx, DA.from_numpy(w1), DA.from_numpy(w2), h, rows, cols, 1e-6,
+                      ds=ds, ss=ss, unit_offset=unit)
+    want_x, want_h = post_norm_ref(oracle, y, x, w1, w2, 1e-6, ds, ss, unit)
+    assert rel_to_scale(dx.numpy(), want_x) <= RTOL
+    assert rel_to_scale(h.numpy(), want_h) <= RTOL
+
+
+def test_post_norm_add_out_of_place_and_weightless(hip, oracle):
+    rng = np.random.default_rng(3)
+    y = rng.standard_normal((40, 2560), dtype=np.float32)
+    x = rng.standard_normal((40, 2560), dtype=np.float32)
+    dy, dx, xo, h = DA.from_numpy(y), DA.from_numpy(x), DA.empty((40, 2560)), DA.empty((40, 2560))
+    ops.post_norm_add(dy, dx, None, None, h, 40, 2560, 1e-6, ds=0.8, x_out=xo)
+    want_x, want_h = post_norm_ref(oracle, y, x, None, None, 1e-6, 0.8, 1.0, False)
+    assert bits_equal(dx.numpy(), x)                      # x untouched
+    assert rel_to_scale(xo.numpy(), want_x) <= RTOL
+    assert rel_to_scale(h.numpy(), want_h) <= RTOL
+
+
+def test_post_norm_add_refusals(hip):
+    a, b, c = DA.empty((4, 64)), DA.empty((4, 64)), DA.empty((4, 64))
+    for args in ((a, b, None, None, a), (a, b, None, None, b)):
+        with pytest.raises(_lib.AeroHipError, match="alias"):
+            ops.post_norm_add(*args, 4, 64, 1e-6)
+    with pytest.raises(_lib.AeroHipError, match="alias"):
+        ops.post_norm_add(a, b, None, None, c, 4, 64, 1e-6, x_out=a)

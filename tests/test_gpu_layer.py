@@ -51,6 +51,28 @@ CASES = {
     "llama3_8b_prefill_q6_k": ("llama3_8b_prefill", W.Q6_K, 4096, 512, 0),
 }
 
+# Blocks with the options of src/model.cpp:181-232 (Gemma's sandwich norms
+# and layer output scale) and src/attention_layer.cpp:60-156,262-263 (the
+# per-head output gate, the weightless V norm, V := K, RoPE frequency
+# factors), at the config-3 (Gemma-3-4B-style) and config-4 (Qwen3-Next
+# attention) layer geometries: (CASES entry, BlockConfig options)
+OPTION_CASES = {
+    "gemma_sandwich_prefill": (("gemma3_4b_prefill", W.Q4_K, 2048, 64, 0),
+                               {"post_norms": True, "out_scale_mode": 1}),
+    "gemma_sandwich_decode": (("gemma3_4b_prefill", W.Q4_K, 2048, 1, 40),
+                              {"post_norms": True, "out_scale_mode": 2}),
+    "gemma_v_from_k_prefill": (("gemma3_4b_prefill", W.Q8_0, 2048, 48, 16),
+                               {"post_norms": True, "v_from_k": True}),
+    # Q8_0 (zero-mean weights): with the Q4_K tables' non-zero row means the
+    # stacked residual stream of this geometry grows to ~1e4 on some tokens
+    # and near-cancelling rows make the output norm ill-conditioned
+    "qwen3next_gated_attn_prefill": (("qwen3next_hybrid", W.Q8_0, 2048, 64, 0),
+                                     {"attn_gate": True, "v_norm": True,
+                                      "freq_factors": "random"}),
+    "qwen3next_gated_attn_decode": (("qwen3next_hybrid", W.Q8_0, 2048, 1, 33),
+                                    {"attn_gate": True, "v_norm": True}),
+}
+
 
 def dq(oracle, t, raw, rows, cols):
     return oracle.dequant(t, raw, rows * cols).reshape(rows, cols).astype(np.float64)
@@ -62,40 +84,80 @@ def oracle_block(oracle, cfg, wts, ids, kv_len, K0, V0):
 
 def oracle_stack(oracle, cfg, layers, ids, kv_len, K0s, V0s):
     """The blocks in turn on the embedded tokens, then the last block's output
-    norm; layer i attends over its own cache K0s[i], V0s[i]."""
+    norm; layer i attends over its own cache K0s[i], V0s[i]. The block is the
+    reference's qwen_block (src/model.cpp:234-287) or, with post_norms, its
+    gemma_block (:181-232), around its attention layer (src/attention_layer.
+    cpp:60-263): q/gate split per head, V := K, the weightless V norm, q/k
+    norms, RoPE with frequency factors, the sigmoid output gate."""
     N, H, HK, D = cfg.hidden, cfg.n_head, cfg.n_head_kv, cfg.head_dim
     T = ids.size
     pos = np.arange(kv_len, kv_len + T, dtype=np.int32)
     scale = float(np.float32(math.sqrt(N))) if cfg.emb_scale else 0.0
+    ff = None if cfg.freq_factors is None else np.asarray(cfg.freq_factors, np.float32)
     h0 = layers[0].host
     x = oracle.embed_gather(cfg.emb_type, h0["emb"], cfg.vocab, N, ids, scale)
     for wts, K0, V0 in zip(layers, K0s, V0s):
         h_ = wts.host
         mats = {k: dq(oracle, cfg.wtype, h_[k], *wts.shapes[k]) for k in wts.MATS}
+        ds = np.float32(wts.out_scale if cfg.out_scale_mode == 1 else 1.0)
+        ss = np.float32(wts.out_scale if cfg.out_scale_mode == 2 else 1.0)
 
         def mm(name, a):
             return (a.astype(np.float64) @ mats[name].T).astype(np.float32)
 
-        h = oracle.rmsnorm_rows(x, h_["attn_norm"], cfg.eps, cfg.unit_offset)
-        q, k, v = mm("wq", h), mm("wk", h), mm("wv", h)
+        def norm(a, name):
+            return oracle.rmsnorm_rows(a, h_[name], cfg.eps, cfg.unit_offset)
+
+        h = norm(x, "attn_norm")
+        q, k = mm("wq", h), mm("wk", h)
+        v = k.copy() if cfg.v_from_k else mm("wv", h)
+        gate = None
+        if cfg.attn_gate:
+            qg = q.reshape(T, H, 2, D)
+            q, gate = np.ascontiguousarray(qg[:, :, 0]), np.ascontiguousarray(qg[:, :, 1])
+        if cfg.v_norm and not cfg.v_from_k:
+            v = oracle.rmsnorm_rows(v.reshape(T * HK, D), None, cfg.eps)
         q = oracle.qk_norm_rope(q, T, H, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("q_norm"),
-                                cfg.eps, cfg.unit_offset)
+                                cfg.eps, cfg.unit_offset, ff=ff)
         k = oracle.qk_norm_rope(k, T, HK, D, cfg.n_rot, pos, cfg.theta, 0, h_.get("k_norm"),
-                                cfg.eps, cfg.unit_offset)
+                                cfg.eps, cfg.unit_offset, ff=ff)
         Kc = np.concatenate([K0[:kv_len], k.reshape(T, HK * D)]).reshape(-1, HK, D)
         Vc = np.concatenate([V0[:kv_len], v.reshape(T, HK * D)]).reshape(-1, HK, D)
         att = oracle.attention_tiled(q.reshape(T, H, D), Kc, Vc, 1.0 / math.sqrt(D), qpos=pos,
                                      kpos=np.arange(kv_len + T, dtype=np.int32))
-        x = x + mm("wo", att.reshape(T, H * D))
-        h = oracle.rmsnorm_rows(x, h_["ffn_norm"], cfg.eps, cfg.unit_offset)
+        att = att.reshape(T, H * D)
+        if gate is not None:
+            att = oracle.act_mul(oracle.ACT_SIGMOID, gate.reshape(T, H * D), att)
+        o = mm("wo", att)
+        if cfg.post_norms:
+            x = x + ds * norm(o, "post_attn_norm")
+        else:
+            x = x + o
+        h = norm(x, "ffn_norm")
         g = oracle.act_mul(ACT[cfg.act], mm("wg", h), mm("wu", h))
-        x = x + mm("wd", g)
+        dn = mm("wd", g)
+        if cfg.post_norms:
+            x = (x + ds * norm(dn, "post_ffw_norm")) * ss
+        else:
+            x = x + dn
     return x, oracle.rmsnorm_rows(x, layers[-1].host["out_norm"], cfg.eps, cfg.unit_offset)
 
 
+def block_options(name):
+    if name not in OPTION_CASES:
+        return CASES[name], {}
+    case, opts = OPTION_CASES[name]
+    opts = dict(opts)
+    if opts.get("freq_factors") == "random":
+        n_rot = W.SHAPES[case[0]].n_rot
+        ff = np.random.default_rng(5).uniform(0.5, 4.0, n_rot // 2).astype(np.float32)
+        opts["freq_factors"] = tuple(float(f) for f in ff)
+    return case, opts
+
+
 def setup(name, seed=0, n_layers=1, **kw):
-    shape, wtype, vocab, T, kv_len = CASES[name]
-    cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype, vocab=vocab)
+    (shape, wtype, vocab, T, kv_len), opts = block_options(name)
+    cfg = layer.BlockConfig.from_shape(W.SHAPES[shape], wtype, vocab=vocab, **opts)
     layers = [layer.BlockWeights(cfg, seed=seed + 17 * i) for i in range(n_layers)]
     step = layer.LayerStep(cfg, layers if n_layers > 1 else layers[0], max_tokens=T,
                            kv_cap=kv_len + T, **kw)
@@ -132,6 +194,20 @@ def run_and_check(oracle, name, n_layers=1, **kw):
     print(f"  rel x {ex:.2e} h_out {eh:.2e}", flush=True)
     assert ex <= RTOL and eh <= RTOL
     return step
+
+
+@pytest.mark.parametrize("name", list(OPTION_CASES))
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("n_layers", [1, 2])
+def test_block_options_vs_oracle(hip, oracle, name, fused, n_layers):
+    """Gemma sandwich norms with the layer output scale on the deltas or the
+    whole sum, V := K, the gated attention with the V norm and frequency
+    factors: one block and a 2-block stack (the post-norm of a block's FFN
+    output applied at the next block's first norm) against the oracle's
+    composition, with every fusion on and off."""
+    fus = None if fused else {f: False for f in select.FUSIONS}
+    step = run_and_check(oracle, name, n_layers=n_layers, fusions=fus)
+    assert not step.uses_host()
 
 
 @pytest.mark.parametrize("name", list(CASES))

@@ -835,3 +835,18 @@ def test_argmax_closed_forms():
     assert O.argmax(np.array(ARGMAX_CASES[1], np.float32)) == 0
     assert O.argmax(np.array(ARGMAX_CASES[2], np.float32)) == 4
     assert O.argmax(np.array(ARGMAX_CASES[3], np.float32)) == 0
+
+
+def test_sigmoid_gate_closed_form_and_silu_relation():
+    """The attention output gate 1/(1+exp(-g)) (src/attention_layer.cpp:
+    262-263): float64 closed form, and v * sigmoid(v) equals the oracle's silu
+    (itself the compiled reference's bit for bit) exactly."""
+    rng = np.random.default_rng(35)
+    v = (rng.standard_normal(5000) * 8).astype(np.float32)
+    s = O.act(O.ACT_SIGMOID, v)
+    exact = 1.0 / (1.0 + np.exp(-v.astype(np.float64)))
+    assert np.abs(s - exact).max() <= 2e-7
+    assert bits_equal((v * s).astype(np.float32), O.act(O.ACT_SILU, v))
+    # the gate multiplies the attention output: sigmoid(g) * a, in either order
+    a = rng.standard_normal(5000).astype(np.float32)
+    assert bits_equal(O.act_mul(O.ACT_SIGMOID, v, a), (a * s).astype(np.float32))
