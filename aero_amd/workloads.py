@@ -282,3 +282,8 @@ def bytes_embed_rmsnorm(R: int, N: int, t: int) -> int:
 def bytes_add_rmsnorm(R: int, N: int) -> int:
     """Residual add + RMSNorm: x and d read, x + d and h written, the weight once."""
     return 16 * R * N + 4 * N
+
+
+def bytes_post_norm_add(R: int, N: int) -> int:
+    """Gemma's sandwich-norm site: y and x read, x' and h written, both weights once."""
+    return 16 * R * N + 8 * N

@@ -110,7 +110,7 @@ def parse_args(argv=None):
                    help="norm -> projections, unfused vs folded into the GEMM (512 tokens)")
     p.add_argument("--gemm", action="store_true",
                    help="quantised GEMM cases (prefill token counts)")
-    p.add_argument("--only", choices=OPS + ("gated_norm",), default=None)
+    p.add_argument("--only", choices=OPS + ("gated_norm", "post_norm_add"), default=None)
     p.add_argument("--copy-calibration", action="store_true")
     p.add_argument("--copy-sweep", action="store_true",
                    help="plain copy at 2 MiB .. 1 GiB: the streaming ceiling per size")
@@ -159,6 +159,10 @@ class StepBuffers:
             self.gate = normal(R, s.ffn)
             self.up = normal(R, s.ffn)
             self.act_out = DA.empty((R, s.ffn))
+        if s.unit_offset and want("post_norm_add"):
+            self.py = normal(R, s.hidden)
+            self.px = normal(R, s.hidden)
+            self.ph = DA.empty((R, s.hidden))
         if s.gated and want("gated_norm"):
             n_v, dd = s.gated
             self.gx = normal(R, n_v * dd)
@@ -169,7 +173,8 @@ class StepBuffers:
     INPUTS = {"embed_gather": (("ids",), ("emb_out",)), "rmsnorm": (("x",), ("h",)),
               "embed_rmsnorm": (("eids",), ("ex", "eh")), "add_rmsnorm": (("rx", "rd"), ("rh",)),
               "rope_qk": (("q", "k"), ()), "swiglu": (("gate", "up"), ("act_out",)),
-              "gated_norm": (("gx", "gz"), ("gout",))}
+              "gated_norm": (("gx", "gz"), ("gout",)),
+              "post_norm_add": (("py", "px"), ("ph",))}
 
     @classmethod
     def copy_for(cls, src, op, rng, vocab):
@@ -246,6 +251,8 @@ class Path:
         }
         if s.gated:
             b["gated_norm"] = W.bytes_gated(s.n_tok, s.gated[0] * s.gated[1], s.gated[1])
+        if s.unit_offset:
+            b["post_norm_add"] = W.bytes_post_norm_add(s.n_tok, s.hidden)
         return b
 
     def rows(self):
@@ -254,6 +261,8 @@ class Path:
              "swiglu": s.n_tok, "embed_rmsnorm": s.n_tok, "add_rmsnorm": s.n_tok}
         if s.gated:
             r["gated_norm"] = s.n_tok
+        if s.unit_offset:
+            r["post_norm_add"] = s.n_tok
         return r
 
     def run(self, op, i, stream=None):
@@ -281,6 +290,9 @@ class Path:
         elif op == "add_rmsnorm":
             ops.add_rmsnorm(b.rx, b.rd, self.w, b.rh, s.n_tok, s.hidden, s.eps,
                             unit_offset=s.unit_offset, stream=stream)
+        elif op == "post_norm_add":
+            ops.post_norm_add(b.py, b.px, self.w, self.w, b.ph, s.n_tok, s.hidden, s.eps,
+                              ds=0.5, unit_offset=s.unit_offset, stream=stream)
         elif op == "gated_norm":
             ops.gated_rmsnorm_silu(b.gx, b.gz, self.gw, b.gout, s.n_tok,
                                    s.gated[0] * s.gated[1], s.eps, stream=stream)
@@ -291,7 +303,8 @@ class Path:
         """The kernels a model loop runs for one layer's elementwise path."""
         if self.only:
             return [self.only]
-        return list(STEP_OPS) + (["gated_norm"] if self.s.gated else [])
+        return list(STEP_OPS) + (["gated_norm"] if self.s.gated else []) + (
+            ["post_norm_add"] if self.s.unit_offset else [])
 
     def report_ops(self):
         """The step's kernels and the unfused ops they replace."""
@@ -631,7 +644,11 @@ def main(argv=None):
         return ssm_layer_bench(a)
 
     name = a.shape or W.HEADLINE
-    path = Path(name, a.sets)
+    if a.only:
+        # only that op's buffers (two sets beyond 4096 tokens)
+        path = Path(name, a.sets if W.SHAPES[name].n_tok <= 4096 else 2, only=a.only)
+    else:
+        path = Path(name, a.sets)
     if a.only:
         ker = kernel_times(path, a.steps, a.warmup, [a.only])
         b = path.bytes()[a.only]
@@ -706,7 +723,8 @@ def all_shapes(a):
         sets = a.sets if W.SHAPES[name].n_tok <= 4096 else 2
         path = Path(name, sets)
         ops_list = [a.only] if a.only else path.report_ops()
-        if a.only == "gated_norm" and not path.s.gated:
+        if (a.only == "gated_norm" and not path.s.gated) or (
+                a.only == "post_norm_add" and not path.s.unit_offset):
             continue
         ker = kernel_times(path, max(20, a.steps // 4), 5, ops_list)
         sus = sustained_times(path, ops_list, SUSTAINED_REPS)
@@ -1163,6 +1181,19 @@ LAYER_CASES = [
     ("llama3_8b_prefill", "llama3_8b_prefill", 12, 512, 0),
     ("llama3_8b_decode", "llama3_8b_prefill", 12, 1, 4095),    # one token at 4095
     ("llama3_8b_t16", "llama3_8b_prefill", 12, 16, 4080),      # 16 tokens (speculative step)
+    # the 512-token prefill in the other split-GEMM types
+    ("llama3_8b_prefill_q8_0", "llama3_8b_prefill", 8, 512, 0),
+    ("llama3_8b_prefill_q6_k", "llama3_8b_prefill", 14, 512, 0),
+    # Gemma blocks (sandwich norms, layer output scale on the deltas) at the
+    # Gemma-3-4B-style geometry, 2048-token prefill and one-token decode; a
+    # 65536-row embedding table (the gather reads T rows of it)
+    ("gemma3_4b_sandwich_prefill", "gemma3_4b_prefill", 12, 2048, 0,
+     {"post_norms": True, "out_scale_mode": 1, "vocab": 65536}),
+    ("gemma3_4b_sandwich_decode", "gemma3_4b_prefill", 12, 1, 4095,
+     {"post_norms": True, "out_scale_mode": 1, "vocab": 65536}),
+    # the Qwen3-Next attention layer (output gate, V norm) at 512 tokens
+    ("qwen3next_gated_attn_t512", "qwen3next_hybrid", 8, 512, 0,
+     {"attn_gate": True, "v_norm": True, "vocab": 65536}),
 ]
 
 
@@ -1171,7 +1202,9 @@ def layer_bench(a):
     RoPE, attention, o, residual + norm, gate/up + act, down, output norm)
     at the Qwen2-0.5B decode, Llama-3-8B 512-token prefill, Llama-3-8B
     one-token decode (4095 cached positions) and Llama-3-8B 16-token
-    (4080 cached positions) shapes, with
+    (4080 cached positions) shapes, Gemma blocks (sandwich norms) at the
+    Gemma-3-4B-style 2048-token prefill and one-token decode, and the
+    Qwen3-Next gated attention block at 512 tokens, with
     every fusion on and with every fusion off. Four blocks with their own
     weights (rotated, so weights come from HBM as in a deep model), each
     recorded as a plan; µs per block = region / blocks run, between one
@@ -1182,10 +1215,13 @@ def layer_bench(a):
     from aero_amd.device import Event, Plan, Stream
 
     names = a.shapes.split(",") if a.shapes else [c[0] for c in LAYER_CASES]
-    for shape, geom, wtype, T, kv_len in LAYER_CASES:
+    for case in LAYER_CASES:
+        shape, geom, wtype, T, kv_len = case[:5]
+        opts = dict(case[5]) if len(case) > 5 else {}
         if shape not in names:
             continue
-        cfg = layer.BlockConfig.from_shape(W.SHAPES[geom], wtype)
+        vocab = opts.pop("vocab", None)
+        cfg = layer.BlockConfig.from_shape(W.SHAPES[geom], wtype, vocab=vocab, **opts)
         weights = [layer.BlockWeights(cfg, seed=i) for i in range(4)]
         rng = np.random.default_rng(5)
         ids = rng.integers(0, cfg.vocab, T).astype(np.int32)
