@@ -28,6 +28,20 @@ ip = POINTER(c_int32)
 u8p = POINTER(c_uint8)
 vp = c_void_p
 
+
+
+class AttnInput(ctypes.Structure):
+    """aero_attn_input_t of include/aero_hip.h, field for field."""
+    _fields_ = [("dtype", c_int), ("n_mat", c_int), ("w", POINTER(vp)),
+                ("w_bytes", POINTER(c_int64)), ("n_rows", POINTER(c_int64)), ("y", POINTER(vp)),
+                ("n_cols", c_int64), ("n_tok", c_int64), ("x", vp), ("d", vp), ("x_out", vp),
+                ("emb_type", c_int), ("emb", vp), ("emb_bytes", c_int64), ("vocab", c_int64),
+                ("ids", vp), ("emb_scale", c_float), ("norm_w", vp), ("eps", c_float),
+                ("norm", c_int), ("n_rope", c_int), ("head_dim", c_int64), ("n_rot", c_int64),
+                ("rope_mode", c_int), ("pos", vp), ("inv_freq", vp), ("q_norm_w", vp),
+                ("k_norm_w", vp), ("qk_eps", c_float), ("qk_flags", c_int)]
+
+
 # name -> (restype, argtypes), exactly the prototypes of include/aero_hip.h
 PROTOTYPES = {
     # reference-compatible host ABI
@@ -161,6 +175,7 @@ PROTOTYPES = {
                                           POINTER(c_int64), POINTER(vp), vp, vp, vp, vp, c_float,
                                           c_int, c_int64, c_int64, c_int, c_int64, c_int, vp, vp,
                                           vp, c_int64, vp]),
+    "aero_hip_attn_input": (c_int, [POINTER(AttnInput), vp, c_int64, vp]),
     "aero_hip_norm_matmul_gate_up": (c_int, [c_int, vp, vp, c_int64, vp, vp, vp, vp, c_float,
                                              c_int, c_int, vp, c_int64, c_int64, c_int64, vp,
                                              c_int64, vp]),

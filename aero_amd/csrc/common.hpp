@@ -93,15 +93,24 @@ inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
-// RoPE folded into the fused decode GEMV's epilogue (gemv.hip): the outputs
-// of matrices 0 .. mats-1 are heads of D rows, every channel rotated at the
-// token's position, angle (float)pos * inv[p].
+// RoPE folded into a projection's epilogue (the fused decode GEMV's,
+// gemv.hip, or the split GEMM's, gemm16.hip): the outputs of matrices
+// 0 .. mats-1 are heads of D rows, channels rotated at the token's position,
+// angle (float)pos * inv[p]. The split GEMM also takes a per-head RMSNorm
+// before the rotation (qk_w) and a partial rotation (n_rot < D); the GEMV
+// fold takes neither.
 struct RopeFold {
     int mats;             // 0: none
     int D;
     int mode;             // AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED
     const int32_t* pos;   // [n_tok]
-    const float* inv;     // [D / 2]
+    const float* inv;     // [n_rot / 2]
+    int n_rot = 0;        // rotated channels (0: all D)
+    const float* qk_w[2] = {nullptr, nullptr};  // per-head norm weights of matrices 0, 1 [D]
+    float qk_eps = 0.f;
+    int qk_flags = 0;     // 0 or AERO_NORM_UNIT_OFFSET
+    bool qk_norm() const { return qk_w[0] != nullptr || qk_w[1] != nullptr; }
+    int rot() const { return n_rot > 0 ? n_rot : D; }
 };
 bool rope_fold_ok(const RopeFold& rope, bool pair, int n_mat, const int64_t* n_rows);
 

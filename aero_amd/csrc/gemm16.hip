@@ -57,6 +57,10 @@
 
 namespace aero {
 
+// block sizes of the ggml types (quant.hip)
+int64_t dtype_block_bytes(int t);
+int64_t dtype_block_values(int t);
+
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -104,6 +108,10 @@ __device__ __forceinline__ void split3(float v, _Float16& hi, _Float16& mid, _Fl
 // Folded steps of the model loop (the reference runs them as separate
 // passes before its matmul, src/model.cpp:244-245,279-282):
 //   RESID: x = x + d, and the sum is stored to x_out (the residual stream);
+//   EMB:   x = the embedding rows of the token ids (a ggml type EMB, times
+//          emb_scale when that is > 0, src/model.cpp:297-316), stored to
+//          x_out; dequantised as the gather does (bit for bit), an id
+//          outside the vocabulary giving a zero row;
 //   NORM:  ssq[t][sb] = the sum of x^2 over the super-block, and x is
 //          multiplied by the norm weight w (or 1 + w) before the split. The
 //          GEMM multiplies each token's sums by 1/sqrtf(sum_sb ssq/n + eps),
@@ -123,9 +131,14 @@ struct XsplitArgs {
     const float* z;       // NORM, gated (src/ssm.cpp:322-340): x * w[c % w_len] * silu(z)
     int w_len;
     int order;            // operand order: 0 Q4_K / Q5_K, 1 Q8_0, 2 Q6_K, 3 IQ4_XS
+    const uint8_t* emb;   // EMB: the table, rows of emb_rb bytes
+    const int32_t* ids;   // EMB: [n_tok]
+    int64_t vocab;
+    int64_t emb_rb;
+    float emb_scale;
 };
 
-template <bool NORM, bool RESID>
+template <bool NORM, bool RESID, int EMB>
 __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
     constexpr int RowF = 256 + 4;
     __shared__ float xl[16 * RowF];
@@ -144,9 +157,34 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
     for (int i = 0; i < 4; ++i) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (t < a.n_tok) {
         const int64_t off = (int64_t)t * n_cols + 256 * sb + 16 * cq;
-        const float* xr = a.x + off;
+        if constexpr (EMB != 0) {
+            // values 16 cq .. +15 of the row's super-block sb: the gather's
+            // lanes 4 cq .. 4 cq + 3 of that 256-value step
+            using Q = QT<EMB>;
+            const int64_t id = a.ids[t];
+            if (id >= 0 && id < a.vocab) {
+                const uint8_t* rowp = a.emb + id * a.emb_rb;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = ld_stream(xr + 4 * i);
+                for (int i = 0; i < 4; ++i) {
+                    const int vl = 4 * cq + i;
+                    typename Q::Raw raw;
+                    load_raw(rowp + ((256 * sb + 4 * vl) / Q::BV) * Q::BB, vl, raw);
+                    v[i] = decode(raw, vl);
+                    if (a.emb_scale > 0.0f) {
+                        v[i].x = v[i].x * a.emb_scale; v[i].y = v[i].y * a.emb_scale;
+                        v[i].z = v[i].z * a.emb_scale; v[i].w = v[i].w * a.emb_scale;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __builtin_nontemporal_store(v4f{v[i].x, v[i].y, v[i].z, v[i].w},
+                                            reinterpret_cast<v4f*>(a.x_out + off + 4 * i));
+        } else {
+            const float* xr = a.x + off;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = ld_stream(xr + 4 * i);
+        }
         if constexpr (RESID) {
             const float* dr = a.d + off;
 #pragma unroll
@@ -316,6 +354,17 @@ struct SplitParams {
     float* part;
     int64_t roff[kMaxMats];
     int64_t r_all;        // partial rows a token
+    // per-head RMSNorm and RoPE on the outputs of matrices 0 .. rope_mats-1
+    // (heads of rope_D rows, whole heads a workgroup), in the epilogue
+    int rope_mats;
+    int rope_D;
+    int rope_rot;         // rotated channels
+    int rope_mode;        // AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED
+    const int32_t* pos;   // [n_tok]
+    const float* rinv;    // [rope_rot / 2] inverse frequencies
+    const float* qk_w[2]; // per-head norm weights of matrices 0 and 1, or null
+    float qk_eps;
+    int qk_flags;
 };
 
 // Epilogue forms: y = acc (kEpiPlain), or the gate/up form: out =
@@ -1130,6 +1179,96 @@ void split_gemm_kernel(SplitParams p) {
         __syncthreads();
     }
 
+    // q / k heads: the per-head norm and RoPE on the workgroup's whole heads
+    // (src/attention_layer.cpp:89-156). The tile goes through LDS (the x
+    // staging buffers, free after the loop's last barrier) so that each
+    // thread holds SLOTS channel pairs of one (token, head): NeoX pairs
+    // (i, i + rot/2) for i < rot/2, then the unrotated channels two at a
+    // time; interleaved pairs (2i, 2i + 1). Threads of one (token, head)
+    // are TPU adjacent lanes; the norm's sum of squares is theirs.
+    if constexpr (!GU) {
+        if (mi < p.rope_mats) {   // uniform: the workgroup's matrix
+            constexpr int RW = 4 * kRowsWave;            // rows a workgroup
+            constexpr int LD = NT == 2 ? RW + 4 : RW;    // tile row stride (floats)
+            constexpr int SLOTS = RW / 16;               // pairs a thread
+            static_assert(kTokTile * LD * 4 <= (int)sizeof(xs), "rope tile fits the staging");
+            float* tile = reinterpret_cast<float*>(&xs[0][0]);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int tk = 16 * m + 4 * g + v;
+                    const float inv = p.ssq != nullptr ? tinv[tk] : 1.0f;
+#pragma unroll
+                    for (int j = 0; j < NT; ++j)
+                        tile[tk * LD + wave * kRowsWave + 16 * j + r] =
+                            p.ssq != nullptr ? acc[m][j][v] * inv : acc[m][j][v];
+                }
+            __syncthreads();
+            const int D = p.rope_D, half = p.rope_rot / 2;
+            const int tpu = D / (2 * SLOTS);             // threads a (token, head)
+            const int hpw = RW / D;                      // heads a workgroup
+            const int u = tid / tpu, k = tid - u * tpu;
+            const int tk = u / hpw, hl = u - tk * hpw;
+            const int tok = kTokTile * tt + tk;
+            const int64_t hrow = (int64_t)((int)blockIdx.x - p.tile0[mi]) * RW + hl * D;
+            const bool neox = p.rope_mode == AERO_ROPE_NEOX;
+            float a[SLOTS], b[SLOTS];
+            int c0[SLOTS], c1[SLOTS];
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) {
+                const int qi = k * SLOTS + i;
+                if (neox) {
+                    c0[i] = qi < half ? qi : p.rope_rot + 2 * (qi - half);
+                    c1[i] = qi < half ? qi + half : c0[i] + 1;
+                } else {
+                    c0[i] = 2 * qi;
+                    c1[i] = 2 * qi + 1;
+                }
+                a[i] = tile[tk * LD + hl * D + c0[i]];
+                b[i] = tile[tk * LD + hl * D + c1[i]];
+            }
+            const float* qw = p.qk_w[mi < 2 ? mi : 0];
+            if (qw != nullptr) {   // uniform
+                float ss = 0.f;
+#pragma unroll
+                for (int i = 0; i < SLOTS; ++i) {
+                    ss += a[i] * a[i];
+                    ss += b[i] * b[i];
+                }
+                for (int o = 1; o < tpu; o <<= 1) ss += __shfl_xor(ss, o);
+                const float ninv = 1.0f / sqrtf(ss / (float)D + p.qk_eps);
+                const bool uo = (p.qk_flags & AERO_NORM_UNIT_OFFSET) != 0;
+#pragma unroll
+                for (int i = 0; i < SLOTS; ++i) {
+                    const float w0 = uo ? 1.0f + qw[c0[i]] : qw[c0[i]];
+                    const float w1 = uo ? 1.0f + qw[c1[i]] : qw[c1[i]];
+                    a[i] = (a[i] * ninv) * w0;
+                    b[i] = (b[i] * ninv) * w1;
+                }
+            }
+            if (tok < p.n_tok && hrow < n_rows) {
+                const float pt = (float)p.pos[tok];
+                float* yp = Y + (int64_t)tok * n_rows + hrow;
+#pragma unroll
+                for (int i = 0; i < SLOTS; ++i) {
+                    const int qi = k * SLOTS + i;
+                    float o0 = a[i], o1 = b[i];
+                    if (qi < half) {
+                        // x0 c - x1 s, x0 s + x1 c (src/transformer.cpp:77-93)
+                        float sn, c;
+                        sincosf(pt * p.rinv[qi], &sn, &c);
+                        o0 = a[i] * c - b[i] * sn;
+                        o1 = a[i] * sn + b[i] * c;
+                    }
+                    yp[c0[i]] = o0;
+                    yp[c1[i]] = o1;
+                }
+            }
+            return;
+        }
+    }
+
     // acc[m][j][v]: token 32tt + 16m + 4g + v, row row0 + 16j + r (gate/up:
     // row row0 + r of the gate (j = 0) and the up (j = 1) matrix)
 #pragma unroll
@@ -1303,12 +1442,34 @@ struct SplitJob {
     int64_t ws_bytes;      // room beyond split_ws_bytes lets few tokens split the columns
     const float* z;        // gated norm (gated_norm_matmul): the gate, norm_w tiled
     int64_t w_len;         //   with period w_len
+    // x from the embedding rows of ids (attn_input): x is unused and x_out
+    // receives the rows
+    const uint8_t* emb;
+    int emb_type;
+    int64_t emb_bytes;
+    int64_t vocab;
+    const int32_t* ids;
+    float emb_scale;
 };
 
-template <bool NORM, bool RESID>
+template <bool NORM, bool RESID, int EMB = 0>
 bool launch_xsplit(const XsplitArgs& a, int64_t tp, hipStream_t s) {
-    return launch("xsplit_kernel", xsplit_kernel<NORM, RESID>,
+    return launch("xsplit_kernel", xsplit_kernel<NORM, RESID, EMB>,
                   dim3((unsigned)(tp / 16), (unsigned)(a.n_cols / 256)), dim3(256), 0, s, a);
+}
+
+// The pre-pass reading x from the embedding rows (with the norm).
+bool launch_xsplit_emb(int emb_type, const XsplitArgs& a, int64_t tp, hipStream_t s) {
+    switch (emb_type) {
+    case AERO_DTYPE_Q8_0: return launch_xsplit<true, false, AERO_DTYPE_Q8_0>(a, tp, s);
+    case AERO_DTYPE_Q4_K: return launch_xsplit<true, false, AERO_DTYPE_Q4_K>(a, tp, s);
+    case AERO_DTYPE_Q5_K: return launch_xsplit<true, false, AERO_DTYPE_Q5_K>(a, tp, s);
+    case AERO_DTYPE_Q6_K: return launch_xsplit<true, false, AERO_DTYPE_Q6_K>(a, tp, s);
+    case AERO_DTYPE_IQ4_XS: return launch_xsplit<true, false, AERO_DTYPE_IQ4_XS>(a, tp, s);
+    default:
+        set_error("split pre-pass: embedding type %d has no device dequant here", emb_type);
+        return false;
+    }
 }
 
 template <int TYPE>
@@ -1370,7 +1531,25 @@ bool split_room_ok(int64_t n_rows, int64_t n_cols, int64_t n_tok, int64_t room) 
     return room >= split_partials_bytes(n_rows, n_cols, n_tok);
 }
 
-bool split_run(const SplitJob& j, hipStream_t s) {
+// Whether the per-head norm and RoPE of j.rope run in the split GEMM's
+// epilogue: plain matrices of whole heads, each workgroup's rows (rows_wg)
+// whole heads of D rows with D / (rows_wg / 8) lanes a head, an even rotated
+// width, positions and inverse frequencies given, no column split.
+bool split_rope_ok(const SplitJob& j, int rows_wg, int ks) {
+    const RopeFold& r = j.rope;
+    const int D = r.D, pairs = rows_wg / 16;
+    if (r.mats < 1 || j.w_up != nullptr || ks != 1 || r.mats > j.n_mat || r.mats > 2 ||
+        r.pos == nullptr || r.inv == nullptr || D < 2 * pairs || D > rows_wg ||
+        rows_wg % D || D % (2 * pairs) || r.rot() < 2 || r.rot() > D || r.rot() % 2 ||
+        (r.mode != AERO_ROPE_NEOX && r.mode != AERO_ROPE_INTERLEAVED))
+        return false;
+    for (int m = 0; m < r.mats; ++m)
+        if (j.n_rows[m] % D) return false;
+    return true;
+}
+
+bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
+    if (rope_done != nullptr) *rope_done = false;
     const int64_t tp = pad_tokens(j.n_tok);
     const bool norm = j.norm >= 0;
     const SplitWs w = split_ws(j.ws, tp, j.n_cols);
@@ -1379,10 +1558,18 @@ bool split_run(const SplitJob& j, hipStream_t s) {
                  j.dtype == AERO_DTYPE_Q8_0   ? 1
                  : j.dtype == AERO_DTYPE_Q6_K ? 2
                  : j.dtype == AERO_DTYPE_IQ4_XS ? 3 : 0};
-    const bool ok = norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
-                                : launch_xsplit<true, false>(a, tp, s))
-                         : (j.d ? launch_xsplit<false, true>(a, tp, s)
-                                : launch_xsplit<false, false>(a, tp, s));
+    if (j.emb != nullptr) {
+        a.emb = j.emb;
+        a.ids = j.ids;
+        a.vocab = j.vocab;
+        a.emb_rb = j.n_cols / dtype_block_values(j.emb_type) * dtype_block_bytes(j.emb_type);
+        a.emb_scale = j.emb_scale;
+    }
+    const bool ok = j.emb != nullptr ? launch_xsplit_emb(j.emb_type, a, tp, s)
+                    : norm ? (j.d ? launch_xsplit<true, true>(a, tp, s)
+                                  : launch_xsplit<true, false>(a, tp, s))
+                           : (j.d ? launch_xsplit<false, true>(a, tp, s)
+                                  : launch_xsplit<false, false>(a, tp, s));
     if (!ok) return false;
     const bool gu = j.w_up != nullptr;
     // rows a wave: 32 (two waves a SIMD); 64 (AERO_HIP_TUNE gemm16_nt=4) runs
@@ -1442,6 +1629,19 @@ bool split_run(const SplitJob& j, hipStream_t s) {
     p.ksplit = ks;
     p.r_all = r_all;
     p.part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(j.ws) + part_off) : nullptr;
+    if (split_rope_ok(j, rows_wg, ks)) {
+        p.rope_mats = j.rope.mats;
+        p.rope_D = j.rope.D;
+        p.rope_rot = j.rope.rot();
+        p.rope_mode = j.rope.mode;
+        p.pos = j.rope.pos;
+        p.rinv = j.rope.inv;
+        p.qk_w[0] = j.rope.qk_w[0];
+        p.qk_w[1] = j.rope.qk_w[1];
+        p.qk_eps = j.rope.qk_eps;
+        p.qk_flags = j.rope.qk_flags;
+        if (rope_done != nullptr) *rope_done = true;
+    }
     if (!launch("split_gemm_kernel", k,
                 dim3((unsigned)tiles, (unsigned)(tp / kTokTile), (unsigned)ks), dim3(256), 0, s,
                 p))
@@ -1538,10 +1738,6 @@ bool split_gemm_dev(int dtype, const uint8_t* w, const float* x, float* y, int64
     *ran = true;
     return true;
 }
-
-// block sizes of the ggml types (quant.hip)
-int64_t dtype_block_bytes(int t);
-int64_t dtype_block_values(int t);
 
 // the quantised GEMV / GEMM dispatch and the fused decode GEMVs (gemv.hip)
 bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, float* y,
@@ -1745,16 +1941,47 @@ bool fused_gemv_run(const SplitJob& j, bool gu, const int64_t* w_bytes, const fl
     return true;
 }
 
+// The embedding rows as x: checks, and the gather into x_out first where
+// the split pre-pass or the gather + norm pass cannot read the table
+// themselves (no norm, a type without their dequant, rows beyond 16384
+// values); j then reads x from x_out.
+bool emb_input(SplitJob& j, hipStream_t s) {
+    const int64_t ebv = dtype_block_values(j.emb_type), ebb = dtype_block_bytes(j.emb_type);
+    if (ebv <= 0 || j.ids == nullptr || j.x_out == nullptr || j.d != nullptr ||
+        j.z != nullptr || j.vocab <= 0 || j.n_cols <= 0 || j.n_cols % ebv != 0 ||
+        j.emb_bytes < j.vocab * (j.n_cols / ebv) * ebb || !aligned16(j.x_out)) {
+        set_error("attn_input: bad embedding arguments (type %d, vocab %lld, %lld bytes for "
+                  "%lld columns; ids and a 16-byte aligned x_out needed, no residual input)",
+                  j.emb_type, (long long)j.vocab, (long long)j.emb_bytes, (long long)j.n_cols);
+        return false;
+    }
+    const bool direct = j.norm >= 0 && j.n_cols <= 8 * 8 * 256 &&
+                        (j.emb_type == AERO_DTYPE_Q8_0 || j.emb_type == AERO_DTYPE_Q4_K ||
+                         j.emb_type == AERO_DTYPE_Q5_K || j.emb_type == AERO_DTYPE_Q6_K ||
+                         j.emb_type == AERO_DTYPE_IQ4_XS);
+    if (direct || j.n_tok == 0) return true;
+    if (!aero_hip_embed_gather(j.emb_type, j.emb, j.emb_bytes, j.vocab, j.n_cols, j.ids,
+                               j.n_tok, j.emb_scale, j.x_out, nullptr, s))
+        return false;
+    j.x = j.x_out;
+    j.emb = nullptr;
+    return true;
+}
+
 bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t ws_bytes,
                      hipStream_t s, bool* rope_done) {
     *rope_done = false;
     j.ws_bytes = ws_bytes;
     const int64_t bv = dtype_block_values(j.dtype), bb = dtype_block_bytes(j.dtype);
     const bool gu = j.w_up != nullptr;
-    if (bv <= 0 || j.x == nullptr || j.n_cols <= 0 || j.n_tok < 0 || j.n_cols % bv != 0 ||
+    if (j.emb != nullptr && !emb_input(j, s)) return false;
+    const bool emb = j.emb != nullptr;   // x from the table (the split pre-pass or gather + norm)
+    if (bv <= 0 || (j.x == nullptr && !emb) || j.n_cols <= 0 || j.n_tok < 0 ||
+        j.n_cols % bv != 0 ||
         j.n_cols > (int64_t)1 << 30 || j.n_tok > 0x7fffffff || (j.d && !j.x_out) ||
         j.norm > AERO_NORM_UNIT_OFFSET || j.n_mat < 1 || j.n_mat > 4 ||
-        (j.norm_w && !aligned16(j.norm_w)) || !aligned16(j.x) || (j.d && !aligned16(j.d)) ||
+        (j.norm_w && !aligned16(j.norm_w)) || (!emb && !aligned16(j.x)) ||
+        (j.d && !aligned16(j.d)) ||
         (j.x_out && !aligned16(j.x_out))) {
         set_error("norm_matmul: bad arguments (n_cols=%lld n_tok=%lld n_mat=%d norm=%d; x, d, "
                   "x_out, norm_w 16-byte aligned, n_cols a multiple of %lld, d needs x_out)",
@@ -1794,7 +2021,7 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
     if (fused && j.z != nullptr && j.n_tok <= 2)   // the gated norm in the GEMV's prologue
         return gemv_gated_dev(j.dtype, j.w[0], w_bytes[0], j.n_rows[0], j.y[0], j.x, j.z,
                               j.norm_w, j.w_len, j.eps, j.n_cols, j.n_tok, s);
-    if (fused && j.z == nullptr && fused_prologue_ok(j))
+    if (fused && j.z == nullptr && !emb && fused_prologue_ok(j))
         return fused_gemv_run(j, gu, w_bytes, j.x, j.norm, j.d, s, rope_done);
     const int64_t need = split ? split_ws_bytes(pad_tokens(j.n_tok), j.n_cols, true)
                                : align256(j.n_tok * j.n_cols * 4) +
@@ -1804,14 +2031,21 @@ bool norm_matmul_run(SplitJob j, const int64_t* w_bytes, int64_t n_ff, int64_t w
                   (long long)need, (long long)ws_bytes);
         return false;
     }
-    if (split) return split_run(j, s);
+    if (split) return split_run(j, s, rope_done);
 
-    // separate launches: x' (= x + d) and h = rmsnorm(x') in the workspace;
+    // separate launches: x' (= x + d, or the embedding rows) and h =
+    // rmsnorm(x') in the workspace;
     // without a norm the add still runs through the add + norm kernel (its h
     // is left unused) and h is x'
     const float* h = j.d ? j.x_out : j.x;
     float* hb = static_cast<float*>(j.ws);
-    if (j.z != nullptr) {
+    if (emb) {   // with a norm (emb_input gathered the other cases)
+        if (!aero_hip_embed_rmsnorm(j.emb_type, j.emb, j.emb_bytes, j.vocab, j.n_cols, j.ids,
+                                    j.n_tok, j.emb_scale, j.x_out, j.norm_w, j.eps, j.norm, hb,
+                                    nullptr, s))
+            return false;
+        h = hb;
+    } else if (j.z != nullptr) {
         if (!aero_hip_gated_rmsnorm_silu(j.x, j.z, j.norm_w, j.w_len, hb, j.n_tok, j.n_cols,
                                          j.n_cols, j.eps, s))
             return false;
@@ -1938,6 +2172,61 @@ int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
                                  nullptr, n_rope > 1 ? n_rows[1] / head_dim : 0, nullptr,
                                  nullptr, 0.f, 0, n_tok, head_dim, head_dim, rope_mode, pos,
                                  inv_freq, nullptr, nullptr, 0, stream);
+}
+
+int aero_hip_attn_input(const aero_attn_input_t* a, void* ws, int64_t ws_bytes, void* stream) {
+    if (a == nullptr || a->w == nullptr || a->w_bytes == nullptr || a->n_rows == nullptr ||
+        a->y == nullptr) {
+        aero::set_error("attn_input: null arguments or matrix arrays");
+        return 0;
+    }
+    const bool rope = a->n_rope > 0;
+    if (a->n_rope < 0 || a->n_rope > 2 || a->n_rope > a->n_mat ||
+        (rope && (a->head_dim < 2 || a->head_dim % 2 || a->head_dim > 512 || a->n_rot < 0 ||
+                  a->n_rot > a->head_dim || a->n_rot % 2 || a->pos == nullptr ||
+                  (a->n_rot > 0 && a->inv_freq == nullptr) ||
+                  (a->rope_mode != AERO_ROPE_NEOX && a->rope_mode != AERO_ROPE_INTERLEAVED) ||
+                  (a->qk_flags & ~AERO_NORM_UNIT_OFFSET) != 0))) {
+        aero::set_error("attn_input: bad RoPE arguments (n_rope=%d of %d matrices, head_dim=%lld, "
+                        "n_rot=%lld, mode=%d; pos and inv_freq required)", a->n_rope, a->n_mat,
+                        (long long)a->head_dim, (long long)a->n_rot, a->rope_mode);
+        return 0;
+    }
+    for (int m = 0; m < a->n_rope; ++m) {
+        if (a->n_rows[m] % a->head_dim) {
+            aero::set_error("attn_input: matrix %d has %lld rows, not whole heads of %lld", m,
+                            (long long)a->n_rows[m], (long long)a->head_dim);
+            return 0;
+        }
+    }
+    aero::SplitJob j{a->dtype, a->x, a->d, a->x_out, a->norm_w, a->norm, a->eps, a->n_mat, a->w,
+                     nullptr, 0, a->n_rows, a->y, a->n_cols, 0, a->n_tok, ws, {}};
+    if (rope && a->n_rot > 0) {
+        j.rope = aero::RopeFold{a->n_rope, (int)a->head_dim, a->rope_mode, a->pos, a->inv_freq};
+        j.rope.n_rot = (int)a->n_rot;
+        j.rope.qk_w[0] = a->q_norm_w;
+        j.rope.qk_w[1] = a->n_rope > 1 ? a->k_norm_w : nullptr;
+        j.rope.qk_eps = a->qk_eps;
+        j.rope.qk_flags = a->qk_flags;
+    }
+    j.emb = a->emb;
+    j.emb_type = a->emb_type;
+    j.emb_bytes = a->emb_bytes;
+    j.vocab = a->vocab;
+    j.ids = a->ids;
+    j.emb_scale = a->emb_scale;
+    bool rope_done = false;
+    if (!aero::norm_matmul_run(j, a->w_bytes, 0, ws_bytes, (hipStream_t)stream, &rope_done))
+        return 0;
+    const bool norms = a->q_norm_w != nullptr || (a->n_rope > 1 && a->k_norm_w != nullptr);
+    if (rope_done || a->n_tok == 0 || !rope || (a->n_rot == 0 && !norms)) return 1;
+    // the path taken has no such epilogue: the per-head norm + RoPE pass
+    return aero_hip_qk_norm_rope(
+        a->y[0], nullptr, a->n_rows[0] / a->head_dim, a->n_rope > 1 ? a->y[1] : nullptr, nullptr,
+        a->n_rope > 1 ? a->n_rows[1] / a->head_dim : 0, a->q_norm_w,
+        a->n_rope > 1 ? a->k_norm_w : nullptr, a->qk_eps, a->qk_flags, a->n_tok, a->head_dim,
+        a->n_rot, a->rope_mode, a->pos, a->n_rot > 0 ? a->inv_freq : nullptr, nullptr, nullptr,
+        0, stream);
 }
 
 int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t* w_up,

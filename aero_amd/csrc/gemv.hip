@@ -1721,10 +1721,12 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
 // Whether RoPE on the outputs of matrices 0 .. rope.mats-1 folds into the
 // fused GEMV: plain (not gate/up) matrices whose rows are whole heads of D
 // rows, D even; NeoX needs D a multiple of 16 (a workgroup takes 2R of a
-// head's pairs, R up to 4); positions and inverse frequencies given.
+// head's pairs, R up to 4); positions and inverse frequencies given; every
+// channel rotates and no per-head norm comes first.
 bool rope_fold_ok(const RopeFold& rope, bool pair, int n_mat, const int64_t* n_rows) {
     if (pair || rope.mats < 1 || rope.mats > n_mat || rope.pos == nullptr ||
         rope.inv == nullptr || rope.D < 2 || rope.D % 2 || rope.D > 1024 ||
+        rope.rot() != rope.D || rope.qk_norm() ||
         (rope.mode != AERO_ROPE_NEOX && rope.mode != AERO_ROPE_INTERLEAVED) ||
         (rope.mode == AERO_ROPE_NEOX && rope.D % 16))
         return false;

@@ -25,8 +25,12 @@ Each elementwise site asks aero_amd.select whether its op runs on the GPU
 fusions apply (AERO_GPU_FUSE; unset means all): the gather with the first
 norm (embed_norm), norms and residual adds folded into the projections that
 consume them (norm_gemm), the act-mul folded into the gate/up projection
-(act_gemm), RoPE in the epilogue of the few-token q/k projection
-(rope_gemm). An op off the GPU runs the caller's host hook for it, as the
+(act_gemm), the per-head norms and RoPE in the epilogue of the q/k
+projection (rope_gemm), the embedding rows read by the first q/k/v
+projection's pre-pass (embed_gemm). At 512 Llama-3-8B tokens a block is then
+10 launches: pre-pass + q/k/v GEMM (with the gather, norm, RoPE), attention,
+and a pre-pass + GEMM each for o, gate/up (+ act) and down, and the output
+norm. An op off the GPU runs the caller's host hook for it, as the
 reference's model loop keeps its own code for the ops it does not hand to a
 library; with no hook the block raises select.HostPathRequired, since the
 library has no CPU path. With every op on the GPU, `forward` can be recorded
@@ -242,9 +246,12 @@ class LayerStep:
         w0 = self.layers[0]
 
         # embedding (+ the first block's attention norm when its projections
-        # need h)
+        # need h); or read by the first q/k/v projection's pre-pass
         h_ready = False
-        if self.gpu("embed"):
+        emb_fold = self._folds_emb(T)
+        if emb_fold:
+            pass
+        elif self.gpu("embed"):
             if not self._folds_norm(T) and self.fuse("embed_norm") and self.gpu("rmsnorm"):
                 ops.embed_rmsnorm(c.emb_type, w0.dev["emb"], c.vocab, N, self.ids, x, h,
                                   w0.dev["attn_norm"], c.eps, scale=self.scale,
@@ -258,14 +265,15 @@ class LayerStep:
 
         resid = None
         for li, w in enumerate(self.layers):
-            resid = self._block(w, li, T, kv_len, resid, h_ready, s)
+            resid = self._block(w, li, T, kv_len, resid, h_ready, s, emb=emb_fold and li == 0)
             h_ready = False
         self._norm(self.layers[-1], self._x(T), resid, "out_norm", self.h_out.view((T, N)), T,
                    s, x_out=x)
 
     def _block(self, w: BlockWeights, li: int, T: int, kv_len: int, resid, h_ready: bool,
-               s) -> DA:
-        """One block on x (+ resid, the previous block's FFN output). Returns
+               s, emb: bool = False) -> DA:
+        """One block on x (+ resid, the previous block's FFN output; emb: x is
+        the embedding rows, read by the q/k/v projection's pre-pass). Returns
         this block's FFN output, to be added by the next norm."""
         c, d = self.cfg, w.dev
         N, H, HK, D, F = c.hidden, c.n_head, c.n_head_kv, c.head_dim, c.ffn
@@ -275,13 +283,9 @@ class LayerStep:
         vq = Vc.view((T, HK * D), offset_bytes=kv0)
         q = self.q.view((T, H * D))
 
-        # x += resid; q, k, v (k and v straight into the cache rows of these
-        # positions), with RoPE on q and k in the projection's epilogue when
-        # that folds
-        rope = None
-        if self._folds_rope(T, h_ready):
-            rope = {"n": 2, "head_dim": D, "mode": ops.ROPE_NEOX, "pos": self.pos,
-                    "inv_freq": self.inv}
+        # x += resid (or x = the embedding rows); q, k, v (k and v straight
+        # into the cache rows of these positions), with the per-head norms and
+        # RoPE on q and k in the projection's epilogue where that folds
         # V := K projects K's matrix again into the V cache rows (the raw
         # projection, before the k norm and RoPE, as src/attention_layer.cpp:
         # 67-69 copies it); with the output gate a fourth matrix writes the
@@ -292,7 +296,19 @@ class LayerStep:
             mats.append(d["wq_gate"])
             ys.append(self.qgate.view((T, H * D)))
             rows.append(H * D)
-        self._project(w, resid, "attn_norm", mats, ys, rows, T, h_ready, s, rope=rope)
+        rope = None
+        if not h_ready and self._folds_norm(T):
+            rope = self._rope_args(w)
+            xi, xo = self._advance(T, resid)
+            first = self.layers[0].dev
+            ops.attn_input(c.wtype, mats, ys, rows, N, T, x_out=xo, x=None if emb else xi,
+                           d=resid,
+                           emb={"type": c.emb_type, "table": first["emb"], "vocab": c.vocab,
+                                "ids": self.ids, "scale": self.scale} if emb else None,
+                           norm_w=d["attn_norm"], eps=c.eps, unit_offset=c.unit_offset,
+                           rope=rope, stream=s)
+        else:
+            self._project(w, resid, "attn_norm", mats, ys, rows, T, h_ready, s)
 
         # the weightless per-head V norm (src/attention_layer.cpp:109-114; not
         # on a V taken from K), in the cache rows
@@ -403,14 +419,28 @@ class LayerStep:
                                 * c.head_dim, T)
         return self.rows16
 
-    def _folds_rope(self, T: int, h_ready: bool) -> bool:
-        """True when RoPE on q and k runs in the epilogue of the few-token
-        q/k/v projection: the norm folds there (fused decode GEMV), every
-        channel rotates and no per-head norm comes between."""
+    def _rope_args(self, w: BlockWeights) -> dict | None:
+        """The per-head norms and RoPE of q and k for the folded q/k/v
+        projection (ops.attn_input), or None when they run apart: their ops
+        on the GPU and the rope_gemm fusion on. The library folds them into
+        the projection's epilogue where the path taken allows (the split
+        GEMM: heads of up to 128 rows; the fused decode GEMV: every channel
+        rotated, no per-head norm) and runs the per-head pass otherwise."""
+        c, d = self.cfg, w.dev
+        if not (self.fuse("rope_gemm") and self.gpu("rope") and
+                (not c.qk_norm or self.gpu("qk_norm"))):
+            return None
+        return {"n": 2, "head_dim": c.head_dim, "n_rot": self.n_rot, "mode": ops.ROPE_NEOX,
+                "pos": self.pos, "inv_freq": self.inv, "q_norm_w": d.get("q_norm"),
+                "k_norm_w": d.get("k_norm"), "eps": c.eps, "unit_offset": c.unit_offset}
+
+    def _folds_emb(self, T: int) -> bool:
+        """True when the first block's q/k/v pre-pass reads the embedding
+        rows itself (the split GEMM at 32+ tokens, a table type its pre-pass
+        dequantises), so no embedding launch runs."""
         c = self.cfg
-        return (T < 32 and not h_ready and self._folds_norm(T) and self.fuse("rope_gemm") and
-                self.gpu("rope") and not c.qk_norm and self.n_rot == c.head_dim and
-                c.head_dim % 16 == 0)
+        return (T >= 32 and self.gpu("embed") and self.fuse("embed_gemm") and
+                self._folds_norm(T) and c.emb_type in (W.Q8_0, W.Q4_K, W.Q5_K, W.Q6_K, W.IQ4_XS))
 
     def _x(self, T: int) -> DA:
         """The residual stream x as it stands (one of the two x buffers)."""
@@ -457,19 +487,10 @@ class LayerStep:
         self._put(h, hn)
 
     def _project(self, wts: BlockWeights, resid, wname, mats, ys, rows, T, h_ready,
-                 s, rope=None) -> None:
-        """ys[m] = rmsnorm(x (+ resid)) W_m^T, the norm folded when it can be
-        (and the RoPE of `rope` on the first outputs, which needs that path)."""
+                 s) -> None:
+        """ys[m] = rmsnorm(x (+ resid)) W_m^T with the norm as its own pass
+        (or h already normed): the sites whose norm does not fold."""
         c = self.cfg
-        norm_w = wts.dev[wname]
-        if not h_ready and self._folds_norm(T):
-            xi, xo = self._advance(T, resid)
-            ops.norm_matmul(c.wtype, mats, xi, ys, rows, c.hidden, T, norm_w=norm_w,
-                            eps=c.eps, unit_offset=c.unit_offset, d=resid, x_out=xo, rope=rope,
-                            stream=s)
-            return
-        if rope is not None:
-            raise ValueError("_project: RoPE folds only into the folded-norm projection")
         h = self.h.view((T, c.hidden))
         if not h_ready:
             self._norm(wts, self._x(T), resid, wname, h, T, s)

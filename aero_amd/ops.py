@@ -447,6 +447,76 @@ def norm_matmul(dtype: int, ws: list, x: DeviceArray, ys: list, n_rows: list, n_
                "norm_matmul_rope")
 
 
+def attn_input(dtype: int, ws: list, ys: list, n_rows: list, n_cols: int, n_tok: int,
+               x_out: DeviceArray, x: DeviceArray | None = None, d: DeviceArray | None = None,
+               emb: dict | None = None, norm_w: DeviceArray | None = None, eps: float = 1e-5,
+               norm: bool = True, unit_offset: bool = False, rope: dict | None = None,
+               stream: Stream | None = None) -> None:
+    """The attention sublayer's input (aero_hip_attn_input): x' = the
+    embedding rows (emb) or x + d (d None: x), stored to x_out; ys[m] =
+    rmsnorm(x') @ W_m^T for 1-4 matrices; then the per-head norm and RoPE of
+    the first rope["n"] outputs (q, k).
+
+    emb = {"type": ggml type, "table": DeviceArray, "vocab": V, "ids": int32
+    [n_tok], "scale": s (applied when > 0)}.
+    rope = {"n": 1 or 2, "head_dim": D, "n_rot": rotated channels (default
+    D; 0: none), "mode": ROPE_NEOX / ROPE_INTERLEAVED, "pos": int32 [n_tok],
+    "inv_freq": [n_rot/2], "q_norm_w" / "k_norm_w": [D] or None, "eps",
+    "unit_offset": bool}.
+
+    With the split GEMM the embedding rows are read by its pre-pass and the
+    per-head norm + RoPE run in its epilogue (heads of up to 128 rows); other
+    paths run the same steps as separate passes."""
+    if not 1 <= len(ws) <= 4 or len(ys) != len(ws) or len(n_rows) != len(ws):
+        raise ValueError("attn_input: 1 to 4 matrices, with as many outputs and row counts")
+    if emb is None and x is None:
+        raise ValueError("attn_input: x or emb is needed")
+    if emb is not None and d is not None:
+        raise ValueError("attn_input: the embedding rows take no residual input")
+    for a, name in ((x, "x"), (d, "d"), (x_out, "x_out")):
+        _need(a, n_tok * n_cols, np.float32, name)
+    _need(norm_w, n_cols, np.float32, "norm_w")
+    for y, nr in zip(ys, n_rows):
+        _need(y, n_tok * nr, np.float32, "y")
+    k = len(ws)
+    wp = (ctypes.c_void_p * k)(*[w.ptr for w in ws])
+    wb = (ctypes.c_int64 * k)(*[w.nbytes for w in ws])
+    nr = (ctypes.c_int64 * k)(*[int(n) for n in n_rows])
+    yp = (ctypes.c_void_p * k)(*[y.ptr for y in ys])
+    a = _lib.AttnInput()
+    a.dtype, a.n_mat, a.w, a.w_bytes, a.n_rows, a.y = int(dtype), k, wp, wb, nr, yp
+    a.n_cols, a.n_tok = int(n_cols), int(n_tok)
+    a.x, a.d, a.x_out = as_ptr(x), as_ptr(d), x_out.ptr
+    if emb is not None:
+        _need(emb["ids"], n_tok, np.int32, "emb ids")
+        a.emb_type, a.emb, a.emb_bytes = int(emb["type"]), emb["table"].ptr, emb["table"].nbytes
+        a.vocab, a.ids = int(emb["vocab"]), emb["ids"].ptr
+        a.emb_scale = float(emb.get("scale", 0.0))
+    a.norm_w, a.eps, a.norm = as_ptr(norm_w), float(eps), _norm_flag(norm, unit_offset)
+    if rope is not None:
+        D = int(rope["head_dim"])
+        n_rot = int(rope.get("n_rot", D))
+        _need(rope["pos"], n_tok, np.int32, "rope pos")
+        if n_rot > 0:
+            _need(rope["inv_freq"], n_rot // 2, np.float32, "rope inv_freq")
+        for key in ("q_norm_w", "k_norm_w"):
+            _need(rope.get(key), D, np.float32, key)
+        a.n_rope, a.head_dim, a.n_rot = int(rope["n"]), D, n_rot
+        a.rope_mode = int(rope.get("mode", ROPE_NEOX))
+        a.pos = rope["pos"].ptr
+        a.inv_freq = as_ptr(rope.get("inv_freq") if n_rot > 0 else None)
+        a.q_norm_w, a.k_norm_w = as_ptr(rope.get("q_norm_w")), as_ptr(rope.get("k_norm_w"))
+        a.qk_eps = float(rope.get("eps", eps))
+        a.qk_flags = NORM_UNIT_OFFSET if rope.get("unit_offset") else 0
+    L = _lib.lib()
+    wsb = L.aero_hip_norm_matmul_workspace(int(dtype), n_cols, 0, n_tok)
+    wsb += L.aero_hip_split_partials_bytes(int(sum(int(r) for r in n_rows)), n_cols, n_tok)
+    buf = _norm_mm_ws.get(wsb)
+    _lib.check(L.aero_hip_attn_input(ctypes.byref(a), as_ptr(buf),
+                                     0 if buf is None else buf.nbytes, _s(stream)),
+               "attn_input")
+
+
 def norm_matmul_gate_up(dtype: int, w_gate: DeviceArray, w_up: DeviceArray, x: DeviceArray,
                         out: DeviceArray, n_ff: int, n_cols: int, n_tok: int, act="silu",
                         norm_w: DeviceArray | None = None, eps: float = 1e-5,

@@ -25,11 +25,12 @@ ENV = "AERO_GPU_OPS"
 # Fusions a device-resident loop may use when every op they join is on the
 # GPU: the embedding gather with the first norm, the norms (and residual
 # adds) folded into the projections that consume them, the act-mul folded
-# into the gate/up projection, RoPE folded into the q/k projection's
-# epilogue, a DeltaNet layer's conv folded into its input projections'
-# epilogue at one token. AERO_GPU_FUSE=none turns them off (the same ops then run as
-# separate kernels); unset means all on.
-FUSIONS = ("embed_norm", "norm_gemm", "act_gemm", "rope_gemm", "conv_gemm")
+# into the gate/up projection, RoPE (and the per-head norm) folded into the
+# q/k projection's epilogue, the embedding rows read by the first q/k/v
+# projection's pre-pass, a DeltaNet layer's conv folded into its input
+# projections' epilogue at one token. AERO_GPU_FUSE=none turns them off (the
+# same ops then run as separate kernels); unset means all on.
+FUSIONS = ("embed_norm", "norm_gemm", "act_gemm", "rope_gemm", "conv_gemm", "embed_gemm")
 FUSE_ENV = "AERO_GPU_FUSE"
 
 

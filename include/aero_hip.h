@@ -498,13 +498,71 @@ int aero_hip_norm_matmul_gate_up(int dtype, const uint8_t* w_gate, const uint8_t
  * n_rot = head_dim). When the call takes the fused decode GEMV (below 32
  * tokens; NeoX heads a multiple of 16 rows) the rotation runs in its
  * epilogue: the partner rows of a pair are computed by the same workgroup
- * and meet in LDS. Otherwise the RoPE pass follows the projections. */
+ * and meet in LDS. When it takes the split GEMM with workgroups of whole
+ * heads (head_dim 16-128) the rotation runs in that GEMM's epilogue.
+ * Otherwise the RoPE pass follows the projections. */
 int aero_hip_norm_matmul_rope(int dtype, int n_mat, const uint8_t* const* w,
                               const int64_t* w_bytes, const int64_t* n_rows, float* const* y,
                               const float* x, const float* d, float* x_out, const float* norm_w,
                               float eps, int norm, int64_t n_cols, int64_t n_tok, int n_rope,
                               int64_t head_dim, int rope_mode, const int32_t* pos,
                               const float* inv_freq, void* ws, int64_t ws_bytes, void* stream);
+
+/* The attention sublayer's input in one call, the steps of
+ * src/model.cpp:244-245,297-316 and src/attention_layer.cpp:60-156:
+ *   1. x' = the embedding rows of ids (ggml type emb_type, emb_bytes of
+ *      table, times emb_scale when > 0) when emb is set, else x + d (d NULL:
+ *      x); x' is stored to x_out (required with emb or d);
+ *   2. h = rmsnorm(x') * norm_w (norm: -1 none, else 0 / AERO_NORM_UNIT_OFFSET);
+ *   3. y[m] = h W_m^T for the n_mat (1-4) matrices of one type sharing h;
+ *   4. on the first n_rope (0-2) outputs, q and k as heads of head_dim rows:
+ *      the per-head RMSNorm (q_norm_w / k_norm_w [head_dim], NULL: none;
+ *      qk_eps, qk_flags 0 / AERO_NORM_UNIT_OFFSET), then RoPE on the first
+ *      n_rot channels (0: none) at positions pos [n_tok], inv_freq
+ *      [n_rot/2], mode AERO_ROPE_NEOX / AERO_ROPE_INTERLEAVED.
+ * Results equal aero_hip_embed_rmsnorm (or aero_hip_add_rmsnorm), the
+ * projections and aero_hip_qk_norm_rope to fp32 re-association. With the
+ * split GEMM (aero_hip_split_ok) the embedding rows are dequantised in its
+ * x pre-pass (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS tables; bit-identical to the
+ * gather; an id outside the vocabulary gives a zero row) and, for
+ * workgroups of whole heads (head_dim 16-128), step 4 runs in the GEMM's
+ * epilogue: one pre-pass and one GEMM launch for all four steps. Otherwise
+ * the steps take the gather + norm pass, the projections and the per-head
+ * pass. Workspace: as aero_hip_norm_matmul. Plain C struct, no padding
+ * assumptions beyond the platform ABI. */
+typedef struct aero_attn_input {
+    int dtype;
+    int n_mat;
+    const uint8_t* const* w;
+    const int64_t* w_bytes;
+    const int64_t* n_rows;
+    float* const* y;
+    int64_t n_cols;
+    int64_t n_tok;
+    const float* x;
+    const float* d;
+    float* x_out;
+    int emb_type;
+    const uint8_t* emb;
+    int64_t emb_bytes;
+    int64_t vocab;
+    const int32_t* ids;
+    float emb_scale;
+    const float* norm_w;
+    float eps;
+    int norm;
+    int n_rope;
+    int64_t head_dim;
+    int64_t n_rot;
+    int rope_mode;
+    const int32_t* pos;
+    const float* inv_freq;
+    const float* q_norm_w;
+    const float* k_norm_w;
+    float qk_eps;
+    int qk_flags;
+} aero_attn_input_t;
+int aero_hip_attn_input(const aero_attn_input_t* a, void* ws, int64_t ws_bytes, void* stream);
 
 /* aero_hip_matmul without a workspace argument and without allocating: the
  * split-x GEMM's workspace is a device array inside the library, of

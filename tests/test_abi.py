@@ -343,3 +343,27 @@ def test_split_ok_follows_the_split_rule():
     assert not ops.split_ok(W.Q4_K, 4096, 6144, 2)       # below the token threshold
     assert ops.split_ok(W.Q4_K, 4096, 14336, 5) and not ops.split_ok(W.Q4_K, 4096, 14336, 4)
     assert not ops.split_ok(W.Q4_K, 4000, 4096, 512)     # not whole super-blocks
+
+
+def test_attn_input_struct_layout(tmp_path):
+    """aero_attn_input_t as the C compiler lays it out (gcc on the header)
+    equals the ctypes mirror field for field: offsets and size."""
+    fields = [f for f, _ in _lib.AttnInput._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "aero_hip.h"\n'
+                   "int main(void) {\n"
+                   + "".join(f'  printf("%zu\\n", offsetof(aero_attn_input_t, {f}));\n'
+                             for f in fields)
+                   + '  printf("%zu\\n", sizeof(aero_attn_input_t));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    want = [getattr(_lib.AttnInput, f).offset for f in fields] + [ctypes_sizeof()]
+    assert got == want
+
+
+def ctypes_sizeof():
+    import ctypes
+    return ctypes.sizeof(_lib.AttnInput)

@@ -301,6 +301,24 @@ def test_layer_decode_rope_fold(hip, oracle):
     assert counts[True] == counts[False] - 1, counts
 
 
+def test_layer_prefill_ten_launches(hip, oracle):
+    """At 512 Llama-3-8B tokens the q/k/v pre-pass reads the embedding rows
+    and the q/k/v GEMM's epilogue runs RoPE: the block records 10 launches,
+    12 with embed_gemm and rope_gemm off, and both match the oracle."""
+    from aero_amd.device import Plan
+
+    counts = {}
+    for fold in (True, False):
+        step = run_and_check(oracle, "llama3_8b_prefill",
+                             fusions={"rope_gemm": fold, "embed_gemm": fold})
+        plan = Plan()
+        with plan:
+            step.forward(512, 0)
+        counts[fold] = len(plan)
+        plan.destroy()
+    assert counts == {True: 10, False: 12}, counts
+
+
 def test_stack_prefill_then_decode(hip, oracle):
     """A 2-layer Llama-3-8B stack run as a model runs it: 16 prompt tokens at
     positions 0-15 (the split GEMMs with the norms folded), then 3 decode
