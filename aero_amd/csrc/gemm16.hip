@@ -372,13 +372,30 @@ struct SplitParams {
 constexpr int kEpiPlain = -1;
 
 // sc*q for the 4 fp16 pairs of one dword of quants of sub-block pair P
-// (Q5_K: with the fifth bits of the matching qh dword, bits 2P / 2P+1). The
-// masked nibbles of the dword's bytes b0..b3 are placed by byte permutes as
-// (b0, 0x64, b2, 0x64) and (b1, 0x64, b3, 0x64): fp16 pairs 1024 + q.
-// s_lo / s_hi: packed (sc, sc) of sub-blocks 2P / 2P+1, b_*: -1024 sc.
+// (Q5_K: with the fifth bits of the matching qh dword, bits 2P / 2P+1), in
+// the pair order (b0, b2), (b1, b3) of the dword's bytes b0..b3, low nibbles
+// then high. Q4_K: the low nibbles of b0 and b2 sit at bits 0-3 and 16-19,
+// so or-ing in 0x6400 makes fp16 1024 + q; the high nibbles sit at bits 4-7
+// and 20-23, mantissa bits worth 1 under the exponent of 64, so or-ing in
+// 0x5400 makes 64 + q (b1, b3 the same after a shift by 8): one and-or a
+// pair. Q5_K: the nibbles with their fifth bit placed by byte permutes as
+// (b0, 0x64, b2, 0x64) and (b1, 0x64, b3, 0x64), fp16 pairs 1024 + q.
+// s_lo / s_hi: packed (sc, sc) of sub-blocks 2P / 2P+1; b_lo: -1024 sc,
+// b_hi: -64 sc (Q4_K) or -1024 sc (Q5_K). One packed fp16 FMA a pair gives
+// sc*q exactly (one rounding of an exactly representable result).
+// e_lo / e_hi: 0x64006400 / 0x54005400 held in VGPRs (one and-or a pair:
+// the mask is its one scalar operand).
 template <bool Q5>
 __device__ __forceinline__ h8 weight_operand(uint32_t w, uint32_t h, int P, h2 s_lo, h2 b_lo,
-                                             h2 s_hi, h2 b_hi) {
+                                             h2 s_hi, h2 b_hi, uint32_t e_lo, uint32_t e_hi) {
+    if constexpr (!Q5) {
+        const uint32_t w8 = w >> 8;
+        const h2 a0 = __builtin_elementwise_fma(as_h2((w & 0x000F000Fu) | e_lo), s_lo, b_lo);
+        const h2 a1 = __builtin_elementwise_fma(as_h2((w8 & 0x000F000Fu) | e_lo), s_lo, b_lo);
+        const h2 a2 = __builtin_elementwise_fma(as_h2((w & 0x00F000F0u) | e_hi), s_hi, b_hi);
+        const h2 a3 = __builtin_elementwise_fma(as_h2((w8 & 0x00F000F0u) | e_hi), s_hi, b_hi);
+        return __builtin_bit_cast(h8, make_uint4(as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)));
+    }
     constexpr uint32_t E = 0x64646464u, EVEN = 0x04020400u, ODD = 0x04030401u;
     uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
     if (Q5) {
@@ -423,29 +440,32 @@ __device__ __forceinline__ void kq_scale_min_lanes(uint32_t s0, uint32_t s1, uin
     mn = k < 4 ? (a1 & 63u) : ((a2 >> 4) | ((a1 >> 6) << 4));
 }
 
-// The x parts, sub-block sums and inverse scales of one chunk on their way
-// to LDS: thread tid stages uint4 tid + 256i of the chunk, i < kParts from
-// the first token tile, the rest from the second (each chunk of a token tile
-// is 256 * kParts contiguous uint4 of xp); threads < 64 float4 tid of the
-// super-block's sums,
-// threads 64..95 the inverse scale of token tid - 64.
+// The x parts, sub-block sums and inverse scales of one chunk of MT
+// 16-token tiles (TT tokens) on their way to LDS: thread tid stages uint4
+// tid + 256i of the chunk, kParts of them from each tile (each chunk of a
+// token tile is 256 * kParts contiguous uint4 of xp); threads < 2TT float4
+// tid of the super-block's sums, threads 2TT .. 3TT-1 the inverse scale of
+// token tid - 2TT.
+template <int MT>
 struct XStage {
-    static constexpr int CSTEP = kChunkSteps * kParts * 64;
-    u4 r[2 * kParts];
+    static constexpr int TT = 16 * MT;
+    static constexpr int CSTEP = kChunkSteps * kParts * 64;   // uint4 a tile's chunk
+    static_assert(CSTEP == 256 * kParts && 3 * TT <= 256, "staging split");
+    u4 r[MT * kParts];
     v4f s;
     float iv;
-    const u4* b0;
-    const u4* b1;
+    const u4* b;          // tile 0; tile m at + m * tstride
+    int64_t tstride;
     const v4f* sb;
     const float* ib;
     int n_chunks;
     __device__ __forceinline__ void init(const uint4* xp, const float* xsum, const float* xinv,
                                          int tt, int nK, int tid) {
-        b0 = reinterpret_cast<const u4*>(xp) + (int64_t)(2 * tt) * nK * (kParts * 64) + tid;
-        b1 = b0 + (int64_t)nK * (kParts * 64);
+        tstride = (int64_t)nK * (kParts * 64);
+        b = reinterpret_cast<const u4*>(xp) + (int64_t)(MT * tt) * tstride + tid;
         sb = reinterpret_cast<const v4f*>(xsum) +
-             ((int64_t)(kTokTile * tt + ((tid & 63) >> 1)) * nK) / 4 + (tid & 1);
-        ib = xinv + (int64_t)(kTokTile * tt + (tid & 31)) * (nK / 8);
+             ((int64_t)(TT * tt + ((tid & (2 * TT - 1)) >> 1)) * nK) / 4 + (tid & 1);
+        ib = xinv + (int64_t)(TT * tt + (tid & (TT - 1))) * (nK / 8);
         n_chunks = nK / kChunkSteps;
     }
     // chunk c, clamped: past the end the last chunk is read again, unused
@@ -453,18 +473,17 @@ struct XStage {
         c = min(c, n_chunks - 1);
         const int64_t o = (int64_t)c * CSTEP;
 #pragma unroll
-        for (int i = 0; i < kParts; ++i) {
-            r[i] = b0[o + 256 * i];
-            r[kParts + i] = b1[o + 256 * i];
-        }
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < kParts; ++i) r[m * kParts + i] = b[m * tstride + o + 256 * i];
         s = sb[2 * (c >> 1)];
         iv = ib[c >> 1];
     }
     __device__ __forceinline__ void store(u4* xs, v4f* ss, float* si, int tid) const {
 #pragma unroll
-        for (int i = 0; i < 2 * kParts; ++i) xs[tid + 256 * i] = r[i];
-        if (ss != nullptr && tid < 2 * kTokTile) ss[tid] = s;
-        if (ss != nullptr && tid >= 2 * kTokTile && tid < 3 * kTokTile) si[tid - 2 * kTokTile] = iv;
+        for (int i = 0; i < MT * kParts; ++i) xs[tid + 256 * i] = r[i];
+        if (ss != nullptr && tid < 2 * TT) ss[tid] = s;
+        if (ss != nullptr && tid >= 2 * TT && tid < 3 * TT) si[tid - 2 * TT] = iv;
     }
 };
 
@@ -574,7 +593,7 @@ __device__ __forceinline__ float iq4_scale(uint32_t h0, uint32_t h1, int ib) {
 // matrix and tile 1 the same 16 rows of the up matrix, so each lane ends
 // with gate and up of the same (token, row) and writes act(gate) * up: a
 // workgroup covers 4 x 16 output rows.
-template <int TYPE, int NT, int EPI>
+template <int TYPE, int NT, int EPI, int MT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 4 ? 1 : 2)))
 void split_gemm_kernel(SplitParams p) {
     constexpr bool Q5 = TYPE == AERO_DTYPE_Q5_K;
@@ -586,17 +605,21 @@ void split_gemm_kernel(SplitParams p) {
     constexpr int BB = Q8 ? 272 : (Q6 ? 210 : (Q5 ? 176 : (IQ4 ? 136 : 144)));   // bytes a super-block
     constexpr int QOFF = Q5 ? 48 : 16;          // quants within the block
     constexpr int kRowsWave = GU ? 16 : 16 * NT;
-    constexpr int MT = kTokTile / 16;           // matrix tiles over tokens (2)
-    constexpr int CHUNK = MT * XStage::CSTEP;   // uint4 a chunk (1536)
-    static_assert(MT == 2 && CHUNK == 2 * kParts * 256, "staging split");
-    __shared__ u4 xs[2][CHUNK];                 // 2 x 24 KB, by chunk parity
-    __shared__ v4f ss[2][kTokTile * 2];         // sub-block sums, by super-block parity
-    __shared__ __align__(16) float si[2][kTokTile];  // inverse scales, by super-block parity
+    constexpr int TT = 16 * MT;                 // tokens a workgroup (MT matrix tiles)
+    constexpr int CHUNK = MT * XStage<MT>::CSTEP;   // uint4 a chunk
+    __shared__ u4 xs[2][CHUNK];                 // 2 x 16 KB (MT = 2), by chunk parity
+    __shared__ v4f ss[2][TT * 2];               // sub-block sums, by super-block parity
+    __shared__ __align__(16) float si[2][TT];   // inverse scales, by super-block parity
 
     const int tid = threadIdx.x;
     const int l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = l & 15, g = l >> 4;
+    // the exponent bits of the Q4_K operand decode, kept in VGPRs (a VALU
+    // instruction here takes one scalar or literal operand, the mask)
+    uint32_t e_lo, e_hi;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(e_lo));
+    asm("v_mov_b32 %0, 0x54005400" : "=v"(e_hi));
     // this workgroup's matrix and its row tile within it (uniform)
     int mi = 0;
 #pragma unroll
@@ -623,7 +646,7 @@ void split_gemm_kernel(SplitParams p) {
         woff[j] = (int)((min(rj, n_rows - 1) - row0) * p.rb);
     }
 
-    XStage xst;
+    XStage<MT> xst;
     xst.init(p.xp, p.xsum, p.xinv, tt, nK, tid);
 
     // quants of both halves of a super-block (Q5_K: the qh bytes, the same for
@@ -648,13 +671,14 @@ void split_gemm_kernel(SplitParams p) {
         for (int j = 0; j < NT; ++j) acc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
     h2 s_lo[NT], b_lo[NT], s_hi[NT], b_hi[NT];
-    // sc of the lane's sub-block pair P = 2 half + g/2 of each row tile,
-    // as packed fp16 factors (sc, sc) and offsets (-1024 sc, -1024 sc)
-    auto set_scales = [&](int half) {
+    // sc of the lane's sub-block pair P = 2 half + g/2 of each row tile
+    // (headers hh), as packed fp16 factors (sc, sc) and offsets (-1024 sc
+    // for the low nibbles, -64 sc or Q5_K's -1024 sc for the high)
+    auto set_scales = [&](int half, const uint4 (&hh)[NT]) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            const h2 sp = kq_scale_pair(hd[j].y, hd[j].w, g >> 1, half);
-            const h2 nb = sp * h2{(_Float16)-1024.f, (_Float16)-1024.f};
+            const h2 sp = kq_scale_pair(hh[j].y, hh[j].w, g >> 1, half);
+            const h2 nb = sp * h2{(_Float16)-1024.f, (_Float16)(Q5 ? -1024.f : -64.f)};
             s_lo[j] = h2{sp[0], sp[0]};
             s_hi[j] = h2{sp[1], sp[1]};
             b_lo[j] = h2{nb[0], nb[0]};
@@ -669,7 +693,6 @@ void split_gemm_kernel(SplitParams p) {
     auto run_steps = [&](const u4* xb, int half, const uint4 (&qq)[NT],
                          const uint4 (&hh)[NT]) {
         const int P = 2 * half + (g >> 1);
-        h8 A[2][MT][kParts], B[2][NT];
         auto read_a = [&](int s, h8 (&a)[MT][kParts]) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
@@ -682,8 +705,45 @@ void split_gemm_kernel(SplitParams p) {
 #pragma unroll
             for (int j = 0; j < NT; ++j)
                 b[j] = weight_operand<Q5>(comp(qq[j], s), Q5 ? comp(hh[j], s) : 0u, P, s_lo[j],
-                                          b_lo[j], s_hi[j], b_hi[j]);
+                                          b_lo[j], s_hi[j], b_hi[j], e_lo, e_hi);
         };
+        if constexpr (MT == 4) {
+            // 64 tokens: one register set of x operands, each tile's refilled
+            // for the next step as soon as its matrix steps are issued
+            h8 A[MT][kParts], B[2][NT];
+            read_a(0, A);
+            decode_b(0, B[0]);
+#pragma unroll
+            for (int s = 0; s < kChunkSteps; ++s) {
+                if (s + 1 < kChunkSteps) decode_b(s + 1, B[(s + 1) & 1]);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    // small parts first into each tile's super-block sum
+#pragma unroll
+                    for (int pp = kParts - 1; pp >= 0; --pp)
+#pragma unroll
+                        for (int j = 0; j < NT; ++j)
+                            part[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                A[m][pp], B[s & 1][j], part[m][j], 0, 0, 0);
+                    if (s + 1 < kChunkSteps) {
+#pragma unroll
+                        for (int pp = 0; pp < kParts; ++pp)
+                            A[m][pp] = __builtin_bit_cast(
+                                h8, xb[((m * kChunkSteps + s + 1) * kParts + pp) * 64 + l]);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < kParts * MT * NT; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix step
+                    __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // one VALU
+                    if (i % (kParts * NT) == kParts * NT - 1)
+                        __builtin_amdgcn_sched_group_barrier(0x100, kParts, 0);  // LDS reads
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return;
+        }
+        h8 A[2][MT][kParts], B[2][NT];
         read_a(0, A[0]);
         decode_b(0, B[0]);
 #pragma unroll
@@ -1078,23 +1138,26 @@ void split_gemm_kernel(SplitParams p) {
     xst.load(2 * sb0 + 1);
     __syncthreads();
 
-    for (int sb = sb0; sb < sb1; ++sb) {
-        uint4 qn[2][NT], hqn[NT], hdn[NT];
+    // one super-block with its weights in (qc, hqc, hdc) while the next one's
+    // load into (qn, hqn, hdn); the loop alternates the two register sets
+    auto sb_body = [&](int sb, const uint4 (&qc)[2][NT], const uint4 (&hqc)[NT],
+                       const uint4 (&hdc)[NT], uint4 (&qn)[2][NT], uint4 (&hqn)[NT],
+                       uint4 (&hdn)[NT]) {
         load_w(sb + 1, qn, hqn, hdn);   // the next super-block (clamped)
         // ---- first half: chunk 2sb in xs[0]
-        set_scales(0);
+        set_scales(0, hdc);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int j = 0; j < NT; ++j) part[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        run_steps(xs[0], 0, q[0], hq);
+        run_steps(xs[0], 0, qc[0], hqc);
         xst.store(xs[1], nullptr, nullptr, tid);   // chunk 2sb+1 (loaded a chunk ago)
         xst.load(2 * sb + 2);
         __syncthreads();
 
         // ---- second half: chunk 2sb+1 in xs[1]
-        set_scales(1);
-        run_steps(xs[1], 1, q[1], hq);
+        set_scales(1, hdc);
+        run_steps(xs[1], 1, qc[1], hqc);
         // acc += inv * (d * part + mins), inv the token's inverse scale for
         // this super-block and mins = -dmin * sum_k m_k S_k on the fp32 matrix
         // cores: A[token][k] = S of sub-block k (k = g, then g + 4), B[k][row]
@@ -1109,10 +1172,10 @@ void split_gemm_kernel(SplitParams p) {
         }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            const float d = f16_lo(hd[j].x);
-            const float ndm = -f16_hi(hd[j].x);
+            const float d = f16_lo(hdc[j].x);
+            const float ndm = -f16_hi(hdc[j].x);
             uint32_t m0, m1;
-            kq_min_pair(hd[j].z, hd[j].w, g, m0, m1);
+            kq_min_pair(hdc[j].z, hdc[j].w, g, m0, m1);
             const float b0 = ndm * (float)m0, b1 = ndm * (float)m1;
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
@@ -1127,14 +1190,12 @@ void split_gemm_kernel(SplitParams p) {
         }
         xst.store(xs[0], ss[(sb + 1) & 1], si[(sb + 1) & 1], tid);  // chunk 2sb+2
         xst.load(2 * sb + 3);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            q[0][j] = qn[0][j];
-            q[1][j] = qn[1][j];
-            if (Q5) hq[j] = hqn[j];
-            hd[j] = hdn[j];
-        }
         __syncthreads();
+    };
+    uint4 q2[2][NT], hq2[NT], hd2[NT];
+    for (int sb = sb0; sb < sb1; sb += 2) {
+        sb_body(sb, q, hq, hd, q2, hq2, hd2);
+        if (sb + 1 < sb1) sb_body(sb + 1, q2, hq2, hd2, q, hq, hd);
     }
     }
 
@@ -1146,7 +1207,7 @@ void split_gemm_kernel(SplitParams p) {
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int tok = kTokTile * tt + 16 * m + 4 * g + v;
+                const int tok = TT * tt + 16 * m + 4 * g + v;
                 if (tok >= p.n_tok) continue;
                 float* pp = P + (int64_t)tok * p.r_all;
                 if constexpr (GU) {
@@ -1167,15 +1228,19 @@ void split_gemm_kernel(SplitParams p) {
     }
 
     // folded norm: each token's sums times 1/sqrtf(sum of x^2 / n + eps),
-    // the sum of its super-block partials (8 lanes a token, in a fixed order)
-    __shared__ float tinv[kTokTile];
+    // the sum of its super-block partials (8 lanes a token, in a fixed order;
+    // 64-token tiles take two rounds)
+    __shared__ float tinv[TT];
     if (p.ssq != nullptr) {
-        const int k = tid >> 3, part = tid & 7;
-        const float* sp = p.ssq + (int64_t)(kTokTile * tt + k) * n_sb;
-        float sum = 0.f;
-        for (int i = part; i < n_sb; i += 8) sum += sp[i];
-        sum = group_sum<8>(sum);
-        if (part == 0) tinv[k] = 1.0f / sqrtf(sum / (float)p.n_cols + p.eps);
+#pragma unroll
+        for (int h = 0; h < MT / 2; ++h) {
+            const int k = 32 * h + (tid >> 3), part = tid & 7;
+            const float* sp = p.ssq + (int64_t)(TT * tt + k) * n_sb;
+            float sum = 0.f;
+            for (int i = part; i < n_sb; i += 8) sum += sp[i];
+            sum = group_sum<8>(sum);
+            if (part == 0) tinv[k] = 1.0f / sqrtf(sum / (float)p.n_cols + p.eps);
+        }
         __syncthreads();
     }
 
@@ -1190,8 +1255,8 @@ void split_gemm_kernel(SplitParams p) {
         if (mi < p.rope_mats) {   // uniform: the workgroup's matrix
             constexpr int RW = 4 * kRowsWave;            // rows a workgroup
             constexpr int LD = NT == 2 ? RW + 4 : RW;    // tile row stride (floats)
-            constexpr int SLOTS = RW / 16;               // pairs a thread
-            static_assert(kTokTile * LD * 4 <= (int)sizeof(xs), "rope tile fits the staging");
+            constexpr int SLOTS = TT * RW / 512;         // pairs a thread
+            static_assert(TT * LD * 4 <= (int)sizeof(xs), "rope tile fits the staging");
             float* tile = reinterpret_cast<float*>(&xs[0][0]);
 #pragma unroll
             for (int m = 0; m < MT; ++m)
@@ -1210,7 +1275,7 @@ void split_gemm_kernel(SplitParams p) {
             const int hpw = RW / D;                      // heads a workgroup
             const int u = tid / tpu, k = tid - u * tpu;
             const int tk = u / hpw, hl = u - tk * hpw;
-            const int tok = kTokTile * tt + tk;
+            const int tok = TT * tt + tk;
             const int64_t hrow = (int64_t)((int)blockIdx.x - p.tile0[mi]) * RW + hl * D;
             const bool neox = p.rope_mode == AERO_ROPE_NEOX;
             float a[SLOTS], b[SLOTS];
@@ -1269,14 +1334,14 @@ void split_gemm_kernel(SplitParams p) {
         }
     }
 
-    // acc[m][j][v]: token 32tt + 16m + 4g + v, row row0 + 16j + r (gate/up:
+    // acc[m][j][v]: token TT tt + 16m + 4g + v, row row0 + 16j + r (gate/up:
     // row row0 + r of the gate (j = 0) and the up (j = 1) matrix)
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int tk = 16 * m + 4 * g + v;
-            const int tok = kTokTile * tt + tk;
+            const int tok = TT * tt + tk;
             if (tok >= p.n_tok) continue;
             const float inv = p.ssq != nullptr ? tinv[tk] : 1.0f;
             float* yp = Y + (int64_t)tok * n_rows;
@@ -1472,18 +1537,25 @@ bool launch_xsplit_emb(int emb_type, const XsplitArgs& a, int64_t tp, hipStream_
     }
 }
 
-template <int TYPE>
-void* pick_split_gemm(int nt, int epi) {
+template <int TYPE, int MT>
+void* pick_split_gemm_mt(int nt, int epi) {
     switch (epi) {
     case kEpiPlain:
-        return nt == 4 ? (void*)split_gemm_kernel<TYPE, 4, kEpiPlain>
-                       : (void*)split_gemm_kernel<TYPE, 2, kEpiPlain>;
-    case AERO_ACT_SILU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_SILU>;
-    case AERO_ACT_GELU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_GELU>;
-    case AERO_ACT_GELU_TANH: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_GELU_TANH>;
-    case AERO_ACT_IDENTITY: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_IDENTITY>;
+        return nt == 4 && MT == 2 ? (void*)split_gemm_kernel<TYPE, 4, kEpiPlain, 2>
+                                  : (void*)split_gemm_kernel<TYPE, 2, kEpiPlain, MT>;
+    case AERO_ACT_SILU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_SILU, MT>;
+    case AERO_ACT_GELU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_GELU, MT>;
+    case AERO_ACT_GELU_TANH: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_GELU_TANH, MT>;
+    case AERO_ACT_IDENTITY: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_IDENTITY, MT>;
     default: return nullptr;
     }
+}
+
+template <int TYPE>
+void* pick_split_gemm(int nt, int epi, int mt) {
+    if constexpr (TYPE == AERO_DTYPE_Q4_K || TYPE == AERO_DTYPE_Q6_K)
+        if (mt == 4) return pick_split_gemm_mt<TYPE, 4>(nt, epi);
+    return pick_split_gemm_mt<TYPE, 2>(nt, epi);
 }
 
 // Column splits for a launch of base_wgs workgroups over n_sb super-blocks:
@@ -1535,9 +1607,9 @@ bool split_room_ok(int64_t n_rows, int64_t n_cols, int64_t n_tok, int64_t room) 
 // epilogue: plain matrices of whole heads, each workgroup's rows (rows_wg)
 // whole heads of D rows with D / (rows_wg / 8) lanes a head, an even rotated
 // width, positions and inverse frequencies given, no column split.
-bool split_rope_ok(const SplitJob& j, int rows_wg, int ks) {
+bool split_rope_ok(const SplitJob& j, int rows_wg, int ks, int mt) {
     const RopeFold& r = j.rope;
-    const int D = r.D, pairs = rows_wg / 16;
+    const int D = r.D, pairs = mt * rows_wg / 32;   // channel pairs a thread
     if (r.mats < 1 || j.w_up != nullptr || ks != 1 || r.mats > j.n_mat || r.mats > 2 ||
         r.pos == nullptr || r.inv == nullptr || D < 2 * pairs || D > rows_wg ||
         rows_wg % D || D % (2 * pairs) || r.rot() < 2 || r.rot() > D || r.rot() % 2 ||
@@ -1577,16 +1649,6 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
     const int nt = gu ? 2 : (tune("gemm16_nt", 2) == 4 ? 4 : 2);
     const int rows_wg = gu ? 64 : 64 * nt;
     const int epi = gu ? j.act : kEpiPlain;
-    void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi)
-               : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi)
-               : j.dtype == AERO_DTYPE_Q6_K ? pick_split_gemm<AERO_DTYPE_Q6_K>(nt, epi)
-               : j.dtype == AERO_DTYPE_IQ4_XS ? pick_split_gemm<AERO_DTYPE_IQ4_XS>(nt, epi)
-                                            : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi);
-    if (kp == nullptr) {
-        set_error("split GEMM: unknown activation %d", j.act);
-        return false;
-    }
-    auto k = reinterpret_cast<void (*)(SplitParams)>(kp);
     // one launch for every matrix: row tiles of matrix m follow those of m-1
     SplitParams p{};
     const int n_mat = gu ? 1 : j.n_mat;
@@ -1629,7 +1691,28 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
     p.ksplit = ks;
     p.r_all = r_all;
     p.part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(j.ws) + part_off) : nullptr;
-    if (split_rope_ok(j, rows_wg, ks)) {
+    // 64 tokens a workgroup (each decoded weight serving twice the matrix
+    // steps) for Q4_K and Q6_K (the others would spill registers) where the
+    // launch still has two workgroups a CU:
+    // 512 tokens of gate/up or of a 14336-row matrix, not q/k/v, o or down at
+    // 4096 rows. AERO_HIP_TUNE gemm16_mt=2 keeps 32, gemm16_mt=4 takes 64
+    // wherever the shape allows.
+    const bool kq = j.dtype == AERO_DTYPE_Q4_K || j.dtype == AERO_DTYPE_Q6_K;
+    const int mt_knob = tune("gemm16_mt", 0);
+    const int mt = kq && nt == 2 && ks == 1 && tp % 64 == 0 && mt_knob != 2 &&
+                           (mt_knob == 4 || tiles * (tp / 64) >= 2 * cu_count())
+                       ? 4 : 2;
+    void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi, mt)
+               : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi, mt)
+               : j.dtype == AERO_DTYPE_Q6_K ? pick_split_gemm<AERO_DTYPE_Q6_K>(nt, epi, mt)
+               : j.dtype == AERO_DTYPE_IQ4_XS ? pick_split_gemm<AERO_DTYPE_IQ4_XS>(nt, epi, mt)
+                                            : pick_split_gemm<AERO_DTYPE_Q4_K>(nt, epi, mt);
+    if (kp == nullptr) {
+        set_error("split GEMM: unknown activation %d", j.act);
+        return false;
+    }
+    auto k = reinterpret_cast<void (*)(SplitParams)>(kp);
+    if (split_rope_ok(j, rows_wg, ks, mt)) {
         p.rope_mats = j.rope.mats;
         p.rope_D = j.rope.D;
         p.rope_rot = j.rope.rot();
@@ -1643,7 +1726,7 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
         if (rope_done != nullptr) *rope_done = true;
     }
     if (!launch("split_gemm_kernel", k,
-                dim3((unsigned)tiles, (unsigned)(tp / kTokTile), (unsigned)ks), dim3(256), 0, s,
+                dim3((unsigned)tiles, (unsigned)(tp / (16 * mt)), (unsigned)ks), dim3(256), 0, s,
                 p))
         return false;
     if (ks == 1) return true;

@@ -335,6 +335,47 @@ def test_split_gemm_nt4_vs_oracle(hip, oracle):
     assert rel_to_scale(got[idx], oracle.matmul(W.Q4_K, w, X[idx], n_rows)) <= RTOL
 
 
+@pytest.mark.parametrize("t", [W.Q4_K, W.Q6_K])
+@pytest.mark.parametrize("n_rows,n_cols,n_tok", [
+    (257, 4096, 100), (1000, 2048, 64), (130, 6144, 128), (64, 14336, 192)])
+def test_split_gemm_64_token_tiles(hip, oracle, t, n_rows, n_cols, n_tok):
+    """Workgroups of 64 tokens (AERO_HIP_TUNE gemm16_mt=4; taken by itself at
+    512 tokens of gate/up or 14336-row matrices): bit-identical to the
+    32-token workgroups (every accumulator sums the same products in the
+    same order) and within 1e-5 of the oracle, plain and with the folded
+    add + norm and the gate/up epilogue."""
+    from aero_amd import device
+    rng = np.random.default_rng(n_rows + n_cols + n_tok + t)
+    w = table(t, n_rows, n_cols, rng)
+    u = table(t, n_rows, n_cols, rng)
+    X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    D = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
+    nw = (rng.standard_normal(n_cols) * 0.1 + 1).astype(np.float32)
+    print(f"split gemm 64-token tiles type={t} rows={n_rows} cols={n_cols} tokens={n_tok}",
+          flush=True)
+    got = {}
+    device.tune_set("gemm16_ksplit", 1)   # one workgroup a tile, as at the model's sizes
+    try:
+        for mt in (2, 4):
+            device.tune_set("gemm16_mt", mt)
+            plain = gpu_matmul(t, w, X, n_rows)
+            out = DA.empty((n_tok, n_rows))
+            xo = DA.empty((n_tok, n_cols))
+            ops.norm_matmul_gate_up(t, DA.from_numpy(w), DA.from_numpy(u), DA.from_numpy(X), out,
+                                    n_rows, n_cols, n_tok, act="silu", norm_w=DA.from_numpy(nw),
+                                    eps=1e-5, d=DA.from_numpy(D), x_out=xo)
+            got[mt] = (plain, out.numpy(), xo.numpy())
+    finally:
+        device.tune_set("gemm16_mt", None)
+        device.tune_set("gemm16_ksplit", None)
+    for a, b in zip(got[2], got[4]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert rel_to_scale(got[4][0], oracle.matmul(t, w, X, n_rows)) <= RTOL
+    h = oracle.rmsnorm_rows(X + D, nw, 1e-5)
+    want = oracle.act_mul(0, oracle.matmul(t, w, h, n_rows), oracle.matmul(t, u, h, n_rows))
+    assert rel_to_scale(got[4][1], want) <= RTOL
+
+
 def test_split_gemm_small_workspace_and_host_abi(hip, oracle):
     """A workspace below aero_hip_matmul_workspace takes the fp32 GEMM (same
     results to the tolerance); the reference-compatible aero_matmul (host
