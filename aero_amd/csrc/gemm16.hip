@@ -1541,6 +1541,7 @@ template <int TYPE, int MT>
 void* pick_split_gemm_mt(int nt, int epi) {
     switch (epi) {
     case kEpiPlain:
+        if (nt == 1 && MT == 4) return (void*)split_gemm_kernel<TYPE, 1, kEpiPlain, 4>;
         return nt == 4 && MT == 2 ? (void*)split_gemm_kernel<TYPE, 4, kEpiPlain, 2>
                                   : (void*)split_gemm_kernel<TYPE, 2, kEpiPlain, MT>;
     case AERO_ACT_SILU: return (void*)split_gemm_kernel<TYPE, 2, AERO_ACT_SILU, MT>;
@@ -1646,23 +1647,49 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
     const bool gu = j.w_up != nullptr;
     // rows a wave: 32 (two waves a SIMD); 64 (AERO_HIP_TUNE gemm16_nt=4) runs
     // one wave a SIMD and measured slower on MI355X at every prefill shape
-    const int nt = gu ? 2 : (tune("gemm16_nt", 2) == 4 ? 4 : 2);
-    const int rows_wg = gu ? 64 : 64 * nt;
+    int nt = gu ? 2 : (tune("gemm16_nt", 2) == 4 ? 4 : 2);
     const int epi = gu ? j.act : kEpiPlain;
     // one launch for every matrix: row tiles of matrix m follow those of m-1
     SplitParams p{};
     const int n_mat = gu ? 1 : j.n_mat;
     p.n_mat = n_mat;
-    int64_t tiles = 0;
-    for (int m = 0; m < n_mat; ++m) {
-        p.w[m] = j.w[m];
-        p.y[m] = j.y[m];
-        p.n_rows[m] = j.n_rows[m];
-        p.tile0[m] = (int)tiles;
-        tiles += (j.n_rows[m] + rows_wg - 1) / rows_wg;
-        if (tiles > 0x7fffffff) {
-            set_error("split GEMM: too many rows");
-            return false;
+    auto count_tiles = [&](int rows_wg) {
+        int64_t t = 0;
+        for (int m = 0; m < n_mat; ++m) t += (j.n_rows[m] + rows_wg - 1) / rows_wg;
+        return t;
+    };
+    int rows_wg = gu ? 64 : 64 * nt;
+    int64_t tiles = count_tiles(rows_wg);
+    // 16 rows a wave and 64 tokens a workgroup for plain Q6_K launches that
+    // have two such workgroups a CU but not two of 32-row waves (4096-row
+    // matrices at 512 tokens): Q6_K's decode (two operand halves a weight) is
+    // then shared by twice the tokens. Measured on MI355X at 512 tokens,
+    // 4096 x 14336: Q6_K 325.8 -> 286.3 us; Q4_K 228.6 -> 255.2 (its x reads
+    // from LDS, twice as many a matrix step, cost more than the decode saved),
+    // so Q4_K keeps 32 rows (AERO_HIP_TUNE gemm16_nt1=1 / 0 forces / forbids).
+    const bool kq = j.dtype == AERO_DTYPE_Q4_K || j.dtype == AERO_DTYPE_Q6_K;
+    const int nt1 = tune("gemm16_nt1", j.dtype == AERO_DTYPE_Q6_K ? 1 : 0);
+    // (not where it would lose a per-head epilogue the 32-row waves take)
+    const bool keeps_rope = j.rope.mats == 0 || split_rope_ok(j, 64, 1, 4) ||
+                            !split_rope_ok(j, 128, 1, 2);
+    if (!gu && nt == 2 && kq && tp % 64 == 0 && nt1 == 1 && keeps_rope &&
+        tiles * (tp / 64) < 2 * cu_count() && count_tiles(64) * (tp / 64) >= 2 * cu_count()) {
+        nt = 1;
+        rows_wg = 64;
+        tiles = count_tiles(64);
+    }
+    if (tiles > 0x7fffffff) {
+        set_error("split GEMM: too many rows");
+        return false;
+    }
+    {
+        int64_t t0 = 0;
+        for (int m = 0; m < n_mat; ++m) {
+            p.w[m] = j.w[m];
+            p.y[m] = j.y[m];
+            p.n_rows[m] = j.n_rows[m];
+            p.tile0[m] = (int)t0;
+            t0 += (j.n_rows[m] + rows_wg - 1) / rows_wg;
         }
     }
     for (int m = n_mat; m <= kMaxMats; ++m) p.tile0[m] = (int)tiles;
@@ -1697,10 +1724,9 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
     // 512 tokens of gate/up or of a 14336-row matrix, not q/k/v, o or down at
     // 4096 rows. AERO_HIP_TUNE gemm16_mt=2 keeps 32, gemm16_mt=4 takes 64
     // wherever the shape allows.
-    const bool kq = j.dtype == AERO_DTYPE_Q4_K || j.dtype == AERO_DTYPE_Q6_K;
     const int mt_knob = tune("gemm16_mt", 0);
-    const int mt = kq && nt == 2 && ks == 1 && tp % 64 == 0 && mt_knob != 2 &&
-                           (mt_knob == 4 || tiles * (tp / 64) >= 2 * cu_count())
+    const int mt = nt == 1 || (kq && nt == 2 && ks == 1 && tp % 64 == 0 && mt_knob != 2 &&
+                               (mt_knob == 4 || tiles * (tp / 64) >= 2 * cu_count()))
                        ? 4 : 2;
     void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi, mt)
                : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi, mt)
