@@ -1676,6 +1676,12 @@ bool gemv_dev(int dtype, const uint8_t* w, int64_t w_bytes, const float* x, floa
             };
             int R = wgs_of(2) >= 256 ? 2 : 1;
             if (T == 4 && wgs_of(4) >= 512) R = 4;
+            // one Q8_0 token of one-step rows: a row a wave (its 80-byte
+            // windows leave the wave's loads fewer; twice the workgroups keep
+            // more in flight): 4096 x 4096 7.72 -> 6.29 us, 14336 x 4096
+            // 17.80 -> 15.67 us on MI355X (Q4_K, Q5_K, Q6_K, IQ4_XS: equal or
+            // slower)
+            if (dtype == AERO_DTYPE_Q8_0 && T == 1 && !pipe && hf == 1) R = 1;
             R = tune("gemv_r", R);
             const int64_t wgs = wgs_of(R);
             GemvKernel k = pipe ? pick64<true>(dtype, R, T)

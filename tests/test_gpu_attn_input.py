@@ -124,6 +124,31 @@ def test_attn_input_vs_oracle(hip, oracle, case):
         assert n == 3, n               # pre-pass + GEMM + the per-head pass
 
 
+@pytest.mark.parametrize("case", [c for c in CASES if c[11] and c[2] % 64 == 0 and c[0] in
+                                  (W.Q4_K, W.Q6_K)],
+                         ids=lambda c: f"{c[0]}-{c[1]}-T{c[2]}-D{c[4]}-{c[10]}")
+def test_attn_input_64_token_workgroups(hip, oracle, case):
+    """The per-head epilogue in 64-token workgroups (AERO_HIP_TUNE
+    gemm16_mt=4; taken by itself when q/k/v has enough rows and tokens, e.g.
+    2048 tokens at the Llama-3-8B shape): 16 channel pairs a thread, against
+    the oracle; still one pre-pass and one GEMM launch."""
+    wt, et, T, N, D, heads, n_rot, mode, qk, uo, src, fold = case
+    device.tune_set("gemm16_ksplit", 1)
+    device.tune_set("gemm16_mt", 4)
+    try:
+        dmats, rows, kw_args, ys = run_case(oracle, wt, et, T, N, D, heads, n_rot, mode, qk, uo,
+                                            src, seed=T * 17 + N + D + wt)
+        plan = Plan()
+        with plan:
+            ops.attn_input(wt, dmats, [DA.empty(y.shape) for y in ys], rows, N, T, **kw_args)
+        n = len(plan)
+        plan.destroy()
+    finally:
+        device.tune_set("gemm16_mt", None)
+        device.tune_set("gemm16_ksplit", None)
+    assert n == 2, n
+
+
 def test_attn_input_llama3_8b_512_tokens(hip, oracle):
     """The Llama-3-8B block's attention input at 512 tokens (hidden 4096,
     32/8 heads of 128, Q4_K weights and table): two launches, checked on a
