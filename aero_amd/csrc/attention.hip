@@ -348,8 +348,9 @@ struct KvTile {
 };
 
 // The four waves' (m, l, acc) of one 16-query tile merged through LDS, then
-// the output (one chunk) or the chunk's partials written: query vector qi of
-// the tile, element d a thread.
+// the output (one chunk) or the chunk's partials written. The 16 queries'
+// merge weights, sums and output rows are computed once (64 threads: wave x,
+// query qi), then each thread writes elements d of query vectors qi.
 template <typename Tile, int DV, bool MERGE_OUT>
 __device__ __forceinline__ void merge_tile(const AttnParams& p, float m, float ls,
                                            const v4f (&acc)[DV / 16], int64_t tile,
@@ -358,7 +359,8 @@ __device__ __forceinline__ void merge_tile(const AttnParams& p, float m, float l
     constexpr int VS = DV / 16;
     ls += __shfl_xor(ls, 16);
     ls += __shfl_xor(ls, 32);
-    __shared__ float sm[4][16], sl[4][16];
+    __shared__ float sm[4][16], sl[4][16], sw[4][16], smt[16], slt[16];
+    __shared__ int32_t srow[16];
     __shared__ float sacc[4][16][DV + 4];
     if (g == 0) {
         sm[wave][c] = m;
@@ -369,30 +371,44 @@ __device__ __forceinline__ void merge_tile(const AttnParams& p, float m, float l
 #pragma unroll
         for (int t = 0; t < VS; ++t) sacc[wave][4 * g + r][Tile::vdim(c, t)] = acc[t][r];
     __syncthreads();
-    const int64_t rows = p.n_q * p.n_head;
-    for (int w = threadIdx.x; w < 16 * DV; w += 256) {
-        const int qi = w / DV, d = w % DV;
-        const int64_t uq = tile * 16 + qi;
-        if (uq >= n_vec) break;  // w only grows
-        float mt = -INFINITY;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) mt = fmaxf(mt, sm[x][qi]);
-        float lt = 0.0f, at = 0.0f;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            const float wg = (sm[x][qi] == -INFINITY) ? 0.0f : expf(sm[x][qi] - mt);
-            lt = __builtin_fmaf(sl[x][qi], wg, lt);
-            at = __builtin_fmaf(sacc[x][qi][d], wg, at);
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const int x = tid >> 4, qi = tid & 15;
+        const float mt = fmaxf(fmaxf(sm[0][qi], sm[1][qi]), fmaxf(sm[2][qi], sm[3][qi]));
+        const float wg = (sm[x][qi] == -INFINITY) ? 0.0f : expf(sm[x][qi] - mt);
+        sw[x][qi] = wg;
+        float lw = sl[x][qi] * wg;
+        lw += __shfl_xor(lw, 16);
+        lw += __shfl_xor(lw, 32);
+        if (x == 0) {
+            smt[qi] = mt;
+            slt[qi] = lw;
+            const int64_t uq = tile * 16 + qi;
+            srow[qi] = uq < n_vec ? (int32_t)((uq / p.rep) * p.n_head + (int64_t)kh * p.rep +
+                                              uq % p.rep)
+                                  : -1;
         }
-        const int64_t row = (uq / p.rep) * p.n_head + (int64_t)kh * p.rep + uq % p.rep;
+    }
+    __syncthreads();
+    const int64_t rows = p.n_q * p.n_head;
+#pragma unroll
+    for (int w0 = 0; w0 < 16 * DV; w0 += 256) {
+        const int w = w0 + tid;
+        const int qi = w / DV, d = w % DV;
+        const int32_t row = srow[qi];
+        if (row < 0) break;  // rows past the last vector: qi only grows
+        float at = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) at = __builtin_fmaf(sacc[x][qi][d], sw[x][qi], at);
+        const float lt = slt[qi];
         if constexpr (MERGE_OUT) {
-            p.out[row * DV + d] = at / fmaxf(lt, 1e-30f);
+            p.out[(int64_t)row * DV + d] = at / fmaxf(lt, 1e-30f);
         } else {
             const int64_t pi = (int64_t)chunk * rows + row;
             p.part[pi * DV + d] = at;
             if (d == 0) {
                 float* ml = p.part + (int64_t)p.n_chunks * rows * DV + 2 * pi;
-                ml[0] = mt;
+                ml[0] = smt[qi];
                 ml[1] = lt;
             }
         }
@@ -546,6 +562,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams p) {
 //    those keys' value rows it loaded.
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ h2 u32_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ uint32_t h2_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -604,58 +621,197 @@ __device__ __forceinline__ void split2(float v, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(v - (float)hi);
 }
 
-template <int DT, int D, bool MERGE_OUT>
-__global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
+// One kv head's keys [c0, c0 + n) of an integer cache, read through buffer
+// descriptors. A 16-key tile's descriptors start at its first key and end at
+// the chunk's last one, so a lane's byte offsets within a tile are fixed (no
+// per-step address arithmetic: the tile's place is wave-uniform), and a key
+// at or past the chunk's end reads as zero codes, scales and positions (the
+// hardware's range check) instead of being clamped to the last key. Lane
+// (g, c) loads key c's slice (the scores' operand), the value rows of keys
+// 4g + r (the value sum's operand), and those keys' scales and positions.
+// The host keeps a chunk's bytes below 2^31.
+template <int DT, int D, bool KPOS>
+struct IntKv {
+    using Tile = KvTile<DT, D, D>;
+    static constexpr int KVEC = D * kv_bits<DT>() / 8;  // bytes of a key or value vector
+    static constexpr int KW = Tile::KW, VW = Tile::VW, KLB = Tile::KLB, KNI = Tile::KNI;
+    static constexpr int VLB = Tile::VLB, VNI = Tile::VNI;
+    struct T {
+        uint32_t k[KW];
+        uint32_t v[4][VW];
+        float ks[4], vs[4];
+        int32_t kp[4];
+    };
+    const uint8_t* kb;
+    const uint8_t* vb;
+    const uint8_t* ksb;
+    const uint8_t* vsb;
+    const uint8_t* kpb;
+    uint32_t kstride, sstride;   // bytes from one key to the next: n_head_kv * KVEC, * 4
+    int32_t n;                   // keys in the chunk
+    uint32_t ko, vo[4], so[4], po[4];
+
+    __device__ __forceinline__ IntKv(const AttnParams& p, int64_t c0, int64_t c1, int kh, int g,
+                                     int c) {
+        const int64_t hk = p.n_head_kv;
+        kb = static_cast<const uint8_t*>(p.k) + (c0 * hk + kh) * KVEC;
+        vb = static_cast<const uint8_t*>(p.v) + (c0 * hk + kh) * KVEC;
+        ksb = reinterpret_cast<const uint8_t*>(p.k_scale + c0 * hk + kh);
+        vsb = reinterpret_cast<const uint8_t*>(p.v_scale + c0 * hk + kh);
+        kpb = KPOS ? reinterpret_cast<const uint8_t*>(p.kpos + c0) : nullptr;
+        kstride = (uint32_t)(hk * KVEC);
+        sstride = (uint32_t)(hk * 4);
+        n = (int32_t)(c1 - c0);
+        ko = (uint32_t)c * kstride + (uint32_t)(g * KLB);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            vo[r] = (uint32_t)(4 * g + r) * kstride + (uint32_t)(c * VLB);
+            so[r] = (uint32_t)(4 * g + r) * sstride;
+            po[r] = (uint32_t)(4 * g + r) * 4u;
+        }
+    }
+
+    // descriptor over [base + j0 * stride, the end of the chunk's last vector)
+    static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint8_t* base, int32_t j0,
+                                                                   int32_t n, uint32_t stride,
+                                                                   uint32_t vec) {
+        const int32_t left = n - j0;
+        const uint32_t bytes = left > 0 ? (uint32_t)(left - 1) * stride + vec : 0u;
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(base) + (int64_t)j0 * stride, 0, (int)bytes, kBufferDword3);
+    }
+
+    template <int N>
+    static __device__ __forceinline__ void words(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                                 uint32_t* w) {
+        if constexpr (N == 16) {
+            const v4u x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+            w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+        } else if constexpr (N == 8) {
+            const v2u x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+            w[0] = x.x; w[1] = x.y;
+        } else if constexpr (N == 4) {
+            w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+        } else {
+            static_assert(N == 2, "slice size");
+            w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+        }
+    }
+
+    static __device__ __forceinline__ float word_f(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+    }
+
+    // keys c0 + j0 .. c0 + j0 + 15 (j0 wave-uniform)
+    __device__ __forceinline__ void load(T& t, int32_t j0) const {
+        const __amdgpu_buffer_rsrc_t rk = rsrc(kb, j0, n, kstride, KVEC);
+        const __amdgpu_buffer_rsrc_t rv = rsrc(vb, j0, n, kstride, KVEC);
+        const __amdgpu_buffer_rsrc_t rks = rsrc(ksb, j0, n, sstride, 4);
+        const __amdgpu_buffer_rsrc_t rvs = rsrc(vsb, j0, n, sstride, 4);
+#pragma unroll
+        for (int i = 0; i < KNI; ++i)
+            words<KLB>(rk, ko + (uint32_t)(4 * i * KLB), t.k + i * KLB / 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < VNI; ++i)
+                words<VLB>(rv, vo[r] + (uint32_t)(16 * i * VLB), t.v[r] + i * VLB / 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            t.ks[r] = word_f(rks, so[r]);
+            t.vs[r] = word_f(rvs, so[r]);
+        }
+        if constexpr (KPOS) {
+            const __amdgpu_buffer_rsrc_t rp = rsrc(kpb, j0, n, 4, 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                t.kp[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (int)po[r], 0, 0);
+        }
+    }
+};
+
+// 2^e as a float, e in [-126, 127]
+__device__ __forceinline__ float pow2i(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Per 32-key step:
+//  * the scores are kept in log2 units (the softmax scale times log2(e)
+//    folded into the query's scale) and exponentiated with the hardware's
+//    exp2; m is returned in natural units for the merges;
+//  * a step whose 32 keys are all inside the chunk and kept for every query
+//    of the tile (no key positions, past the window's start, before the
+//    tile's earliest query) skips the per-key masks (a wave-uniform branch);
+//    a query column past the tile's last vector holds a real query's copy
+//    (finite scores) and is never written out;
+//  * the value sum accumulates in the matrix cores' accumulator in units of
+//    2^(e - 6), and the probabilities are taken against a reference max m
+//    that may sit up to 8 (log2 units) below the running max: p <= 2^8, so
+//    p * value scale * 2^(6 - e) < 2^14 while e is at least the exponent of
+//    the step's largest value scale. The reference max and e move (and the
+//    sums are rescaled by 2^(m_old - m_new) * 2^(e_old - e_new)) only when
+//    some query's max passes m + 8, a value scale passes 2^e, or the step's
+//    largest value scale falls 2^8 below it (then e follows it as far as the
+//    rescaled sums stay below 2^100): most steps of a long decode rescale
+//    nothing;
+//  * the tiles alternate between two register sets (the loop body twice),
+//    so the next step's loads land without copies.
+template <int DT, int D, bool MERGE_OUT, bool KPOS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_f16_kernel(AttnParams p) {
     static_assert(DT == 1 || DT == 2, "integer caches");
     using Tile = KvTile<DT, D, D>;
+    using Kv = IntKv<DT, D, KPOS>;
+    using KT = typename Kv::T;
     constexpr int KS = Tile::KS, VS = Tile::VS, NS = KS / 8;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, c = lane & 15;
     const int chunk = blockIdx.x, kh = blockIdx.y;
     const int64_t n_vec = p.n_q * p.rep;
     const int64_t tile = (int64_t)(gridDim.z - 1 - blockIdx.z);
-    constexpr int64_t istep = 4;
+    constexpr int istep = 4;
 
-    // this chunk's keys in 32-key steps; the wave's first step is issued
-    // before the query positions, which may narrow the range, arrive
+    // this chunk's keys in 32-key steps
     const int64_t c0 = (int64_t)chunk * p.chunk_len;
     const int64_t c1 = min(c0 + p.chunk_len, p.n_kv);
-    const int64_t tiles_c = (c1 - c0 + 31) / 32;
-    const int64_t i_spec = wave;
-    Tile ta, tb, na, nb;
-    {
-        const int64_t kb = c0 + 32 * min(i_spec, tiles_c - 1);
-        ta.load(p, kb, c1, g, c, kh);
-        tb.load(p, kb + 16, c1, g, c, kh);
-    }
-
-    // query vector of column c, scaled by 2^(14 - e) and split
+    const int tiles_c = (int)((c1 - c0 + 31) / 32);
+    const Kv kv(p, c0, c1, kh, g, c);
+    KT ta, tb, na, nb;
+    const int i_spec = min(wave, tiles_c - 1);
     const int64_t u = tile * 16 + c;
-    const bool qok = u < n_vec;
-    const int64_t uc = qok ? u : n_vec - 1;
+    const int64_t uc = u < n_vec ? u : n_vec - 1;
     const int64_t tq = uc / p.rep;
     const int64_t qrow = tq * p.n_head + (int64_t)kh * p.rep + uc % p.rep;
-    const int64_t qp = position_or(p.qpos, tq, tq);
     float qs[KS];
-    float qmax = 0.0f;
     {
         const float* src = p.q + qrow * D;
 #pragma unroll
         for (int e = 0; e < KS; e += 4) {
             const float4 f = *reinterpret_cast<const float4*>(src + Tile::kdim(g, e));
-            qs[e] = qok ? f.x : 0.0f;
-            qs[e + 1] = qok ? f.y : 0.0f;
-            qs[e + 2] = qok ? f.z : 0.0f;
-            qs[e + 3] = qok ? f.w : 0.0f;
+            qs[e] = f.x; qs[e + 1] = f.y; qs[e + 2] = f.z; qs[e + 3] = f.w;
         }
-#pragma unroll
-        for (int e = 0; e < KS; ++e) qmax = fmaxf(qmax, fabsf(qs[e]));
     }
+    // the wave's first step is issued after the query (loads complete in
+    // order: the split waits for q only) and before the query position
+    // (which may narrow the range and is only used after the split)
+    __builtin_amdgcn_sched_barrier(0);
+    kv.load(ta, 32 * i_spec);
+    kv.load(tb, 32 * i_spec + 16);
+    // (a buffer load: a flat one would make every wait a full one)
+    const __amdgpu_buffer_rsrc_t rqp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(p.qpos), 0, p.qpos ? 0x7fffffff : 0, kBufferDword3);
+    const int32_t qp_raw = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rqp, (int)(tq * 4), 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    float qmax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < KS; ++e) qmax = fmaxf(qmax, fabsf(qs[e]));
     qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
     qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
     int eq = 0;
     if (qmax > 0.0f && qmax <= 3.4028235e38f) frexpf(qmax, &eq);
-    const float qsc = ldexpf(1.0f, 14 - eq), qinv = ldexpf(1.0f, eq - 14);
+    const float qsc = ldexpf(1.0f, 14 - eq);
+    const float qsl = ldexpf(p.scale * kLog2e, eq - 14);
     h8 qhi[NS], qlo[NS];
 #pragma unroll
     for (int st = 0; st < NS; ++st)
@@ -666,112 +822,179 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
             qhi[st][i] = hi;
             qlo[st][i] = lo;
         }
+    // (the split stays here, ahead of the wait for the query position and
+    // the first step, rather than being sunk into the loop's preheader)
+#pragma unroll
+    for (int st = 0; st < NS; ++st) asm volatile("" : "+v"(qhi[st]), "+v"(qlo[st]));
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t qp = p.qpos ? (int64_t)qp_raw : tq;
     int64_t qmin = qp, qmx = qp;
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) {
         qmin = min(qmin, (int64_t)__shfl_xor(qmin, off, 16));
         qmx = max(qmx, (int64_t)__shfl_xor(qmx, off, 16));
     }
+    // (every lane group holds the 16 columns' positions: wave-uniform)
+    qmin = (int64_t)__builtin_amdgcn_readfirstlane((uint32_t)qmin) |
+           ((int64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)qmin >> 32)) << 32);
+    qmx = (int64_t)__builtin_amdgcn_readfirstlane((uint32_t)qmx) |
+          ((int64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)qmx >> 32)) << 32);
 
     // 32-key steps [i_lo, i_hi) of the chunk can hold kept keys (as
     // attn_mfma_kernel's 16-key tiles)
     int64_t i_lo = 0, i_hi = tile * 16 < n_vec ? tiles_c : 0;
-    if (p.kpos == nullptr) {
+    if constexpr (!KPOS) {
         i_hi = min(i_hi, max<int64_t>(0, (qmx + 1 - c0 + 31) / 32));
         if (p.window > 0) i_lo = max<int64_t>(0, (qmin - p.window + 1 - c0) / 32);
     }
-    int64_t i = i_lo + (((wave - i_lo) % 4) + 4) % 4;
+    int i = (int)(i_lo + (((wave - i_lo) % 4) + 4) % 4);
     if (i != i_spec && i < i_hi) {
-        ta.load(p, c0 + 32 * i, c1, g, c, kh);
-        tb.load(p, c0 + 32 * i + 16, c1, g, c, kh);
+        kv.load(ta, 32 * i);
+        kv.load(tb, 32 * i + 16);
     }
 
-    float m = -INFINITY, ls = 0.0f;
+    float m = -INFINITY, ls = 0.0f;   // reference max (log2 units), sum of p
+    int e_acc = -1000;                 // the sums' exponent (none yet)
     v4f acc[VS];
 #pragma unroll
     for (int t = 0; t < VS; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    while (i < i_hi) {
-        const int64_t kb = c0 + 32 * i;
-        {
-            const int64_t kn = c0 + 32 * min(i + istep, tiles_c - 1);
-            na.load(p, kn, c1, g, c, kh);
-            nb.load(p, kn + 16, c1, g, c, kh);
-        }
+    auto body = [&](const KT& A, const KT& B, int64_t kb) __attribute__((always_inline)) {
         // scores of keys kb + 16 h + 4g + r for query c, h = 0, 1
         v4f sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const h8 ka = key_codes<DT>(ta.k, st), kbv = key_codes<DT>(tb.k, st);
+            const h8 ka = key_codes<DT>(A.k, st), kbv = key_codes<DT>(B.k, st);
             sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[st], sa, 0, 0, 0);
             sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qlo[st], sb, 0, 0, 0);
             sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[st], sa, 0, 0, 0);
             sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qhi[st], sb, 0, 0, 0);
         }
         float sc[8];
-        float tm = -INFINITY;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int r = 0; r < 4; ++r) {
+            sc[r] = sa[r] * (qsl * A.ks[r]);
+            sc[4 + r] = sb[r] * (qsl * B.ks[r]);
+        }
+        const bool full = !KPOS && kb + 32 <= c1 && kb + 31 <= qmin &&
+                          (p.window <= 0 || qmx - kb < p.window);
+        if (!full) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const Tile& th = h ? tb : ta;
-                const int64_t kj = kb + 16 * h + 4 * g + r;
-                const int64_t kp = p.kpos ? (int64_t)__shfl(th.kp, 4 * g + r) : kj;
-                const bool keep = qok && kj < c1 && key_kept(kp, qp, p.window);
-                const float y = (h ? sb[r] : sa[r]) * (qinv * __shfl(th.ks, 4 * g + r));
-                sc[4 * h + r] = keep ? y * p.scale : -INFINITY;
-                tm = fmaxf(tm, sc[4 * h + r]);
-            }
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t kj = kb + 16 * h + 4 * g + r;
+                    const int64_t kp = KPOS ? (int64_t)(h ? B.kp[r] : A.kp[r]) : kj;
+                    const bool keep = kj < c1 && key_kept(kp, qp, p.window);
+                    sc[4 * h + r] = keep ? sc[4 * h + r] : -INFINITY;
+                }
+        }
+        float tm = sc[0];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) tm = fmaxf(tm, sc[k]);
         tm = fmaxf(tm, __shfl_xor(tm, 16));
         tm = fmaxf(tm, __shfl_xor(tm, 32));
-        const float mn = fmaxf(m, tm);
-        const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
-        // the step's largest value scale (every lane group holds the scales
-        // of keys c of both halves)
-        float vmax = fmaxf(ta.vs, tb.vs);
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
+        // the step's largest value scale (lane group g holds the scales of
+        // keys 4g .. 4g + 3 of both halves)
+        float vmax = fmaxf(fmaxf(fmaxf(A.vs[0], A.vs[1]), fmaxf(A.vs[2], A.vs[3])),
+                           fmaxf(fmaxf(B.vs[0], B.vs[1]), fmaxf(B.vs[2], B.vs[3])));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
         int ev = 0;
         if (vmax > 0.0f && vmax <= 3.4028235e38f) frexpf(vmax, &ev);
-        const float psc = ldexpf(1.0f, 14 - ev), pinv = ldexpf(1.0f, ev - 14);
+        ev = __builtin_amdgcn_readfirstlane(ev);
+        int e_new = e_acc;
+        if (ev > e_acc) {
+            e_new = ev;
+        } else if (ev < e_acc - 8) {
+            // down to ev, as far as the sums (times 2^(e_acc - e_new)) stay
+            // below 2^100 (the later steps add < 2^53 to them)
+            float amax = 0.0f;
+#pragma unroll
+            for (int t = 0; t < VS; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(acc[t][r]));
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+            int ea = -1000;
+            if (amax > 0.0f) frexpf(amax, &ea);
+            ea = __builtin_amdgcn_readfirstlane(ea);
+            e_new = max(ev, e_acc - (100 - ea));
+        }
+        e_new = min(max(e_new, -120), 128);   // 2^(6 - e) and 2^(e - 6) normal
+        if (__any(tm > m + 8.0f) || e_new != e_acc) {
+            const float mn = fmaxf(m, tm);
+            const float alpha = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+            ls = ls * alpha;
+            // rescale the rows of query 4g + r by that query's alpha (lane
+            // 4g + r), then all by 2^(e_acc - e_new)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float ar = __shfl(alpha, 4 * g + r);
+#pragma unroll
+                for (int t = 0; t < VS; ++t) acc[t][r] *= ar;
+            }
+            const int d = e_acc - e_new;
+            if (d != 0) {
+#pragma unroll
+                for (int t = 0; t < VS; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[t][r] = ldexpf(acc[t][r], d);
+            }
+            m = mn;
+            e_acc = e_new;
+        }
+        const float msafe = (m == -INFINITY) ? 0.0f : m;   // p = 0 for a masked key
+        const float psc = pow2i(6 - e_acc);
         h8 phi, plo;
         float psum = 0.0f;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float pr = (sc[4 * h + r] == -INFINITY) ? 0.0f : expf(sc[4 * h + r] - mn);
+                const float pr = __builtin_amdgcn_exp2f(sc[4 * h + r] - msafe);
                 psum += pr;
                 _Float16 hi, lo;
-                split2(pr * __shfl((h ? tb : ta).vs, 4 * g + r) * psc, hi, lo);
+                split2(pr * (h ? B.vs[r] : A.vs[r]) * psc, hi, lo);
                 phi[4 * h + r] = hi;
                 plo[4 * h + r] = lo;
             }
-        ls = ls * alpha + psum;
-        m = mn;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float ar = __shfl(alpha, 4 * g + r);
-#pragma unroll
-            for (int t = 0; t < VS; ++t) acc[t][r] *= ar;
-        }
+        ls = ls + psum;
         // value sum: B = codes of element vdim(c, t) of the 8 keys' rows
 #pragma unroll
         for (int t = 0; t < VS; ++t) {
-            const h8 vb = __builtin_bit_cast(
-                h8, make_uint4(value_pair<DT>(ta.v[0], ta.v[1], t), value_pair<DT>(ta.v[2], ta.v[3], t),
-                               value_pair<DT>(tb.v[0], tb.v[1], t), value_pair<DT>(tb.v[2], tb.v[3], t)));
-            v4f pv = {0.f, 0.f, 0.f, 0.f};
-            pv = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, vb, pv, 0, 0, 0);
-            pv = __builtin_amdgcn_mfma_f32_16x16x32_f16(phi, vb, pv, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(pv[r], pinv, acc[t][r]);
+            const h8 vbv = __builtin_bit_cast(
+                h8, make_uint4(value_pair<DT>(A.v[0], A.v[1], t), value_pair<DT>(A.v[2], A.v[3], t),
+                               value_pair<DT>(B.v[0], B.v[1], t), value_pair<DT>(B.v[2], B.v[3], t)));
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, vbv, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(phi, vbv, acc[t], 0, 0, 0);
         }
+    };
+
+    // steps i, i + 4, ...: ta/tb hold step i, na/nb receive the next (a
+    // wave-uniform branch: the last step loads nothing)
+    while (i < (int)i_hi) {
+        if (i + istep < (int)i_hi) {
+            kv.load(na, 32 * (i + istep));
+            kv.load(nb, 32 * (i + istep) + 16);
+        }
+        body(ta, tb, c0 + 32 * (int64_t)i);
         i += istep;
-        if (i >= i_hi) break;
-        ta = na;
-        tb = nb;
+        if (i >= (int)i_hi) break;
+        if (i + istep < (int)i_hi) {
+            kv.load(ta, 32 * (i + istep));
+            kv.load(tb, 32 * (i + istep) + 16);
+        }
+        body(na, nb, c0 + 32 * (int64_t)i);
+        i += istep;
     }
+    // back to natural units: the sums times 2^(e - 6), m times ln 2
+    const float back = e_acc < -120 ? 0.0f : pow2i(e_acc - 6);
+#pragma unroll
+    for (int t = 0; t < VS; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] *= back;
+    m = m * kLn2;
     merge_tile<Tile, D, MERGE_OUT>(p, m, ls, acc, tile, n_vec, chunk, kh, wave, g, c);
 }
 
@@ -883,15 +1106,22 @@ AttnKernel pick_mfma(int dt, int D, bool merge_out) {
     }
 }
 
+template <int DT, int D>
+AttnKernel pick_f16_d(bool merge_out, bool kpos) {
+    if (kpos) return merge_out ? attn_f16_kernel<DT, D, true, true> : attn_f16_kernel<DT, D, false, true>;
+    return merge_out ? attn_f16_kernel<DT, D, true, false> : attn_f16_kernel<DT, D, false, false>;
+}
+
 template <int DT>
-AttnKernel pick_f16_dt(int D, bool merge_out) {
-    if (D == 64) return merge_out ? attn_f16_kernel<DT, 64, true> : attn_f16_kernel<DT, 64, false>;
-    if (D == 128) return merge_out ? attn_f16_kernel<DT, 128, true> : attn_f16_kernel<DT, 128, false>;
+AttnKernel pick_f16_dt(int D, bool merge_out, bool kpos) {
+    if (D == 64) return pick_f16_d<DT, 64>(merge_out, kpos);
+    if (D == 128) return pick_f16_d<DT, 128>(merge_out, kpos);
     return nullptr;
 }
 
-AttnKernel pick_f16(int dt, int D, bool merge_out) {
-    return dt == 1 ? pick_f16_dt<1>(D, merge_out) : (dt == 2 ? pick_f16_dt<2>(D, merge_out) : nullptr);
+AttnKernel pick_f16(int dt, int D, bool merge_out, bool kpos) {
+    return dt == 1 ? pick_f16_dt<1>(D, merge_out, kpos)
+                   : (dt == 2 ? pick_f16_dt<2>(D, merge_out, kpos) : nullptr);
 }
 
 struct AttnPlan {
@@ -936,6 +1166,9 @@ bool attn_plan(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
     cl = (cl + step - 1) / step * step;
     pl.chunk_len = cl;
     pl.n_chunks = (int)((n_kv + cl - 1) / cl);
+    // the fp16 kernel addresses a chunk of one kv head with 32-bit offsets
+    const int64_t vec_bytes = head_dim * (kv_dt == 1 ? 8 : 4) / 8;
+    if (pl.f16 && cl * n_head_kv * vec_bytes >= (int64_t(1) << 31)) pl.f16 = false;
     return true;
 }
 
@@ -1076,7 +1309,7 @@ bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scal
                  n_q, n_head, n_head_kv, head_dim, value_dim, n_kv,
                  (int)(n_head / n_head_kv), window, scale, pl.chunk_len, pl.n_chunks};
     const bool one = pl.n_chunks == 1;
-    AttnKernel kern = pl.f16 ? pick_f16(kv_dt, (int)head_dim, one)
+    AttnKernel kern = pl.f16 ? pick_f16(kv_dt, (int)head_dim, one, kpos != nullptr)
                       : pl.mfma ? pick_mfma(kv_dt, (int)head_dim, one)
                                 : pick_attn(kv_dt, pl.E, one);
     if (!launch(pl.f16 ? "attn_f16_kernel" : (pl.mfma ? "attn_mfma_kernel" : "attn_kernel"), kern,

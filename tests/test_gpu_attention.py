@@ -205,6 +205,68 @@ def test_quantised_cache_positions_and_masks(hip, oracle, dt, D, H, HK, S):
         assert not got[0].any()
 
 
+@pytest.mark.parametrize("dt", [1, 2])
+@pytest.mark.parametrize("case", ["late_jump", "tiny_block"])
+@pytest.mark.parametrize("one_chunk", [False, True])
+def test_quantised_cache_scale_ranges(hip, oracle, dt, case, one_chunk):
+    """Value vectors in blocks of 1e-30, 1e24, 1, 1e-20 and 3 along the cache
+    (value scales 2^-100 .. 2^80), keys of the 1e24 block (and, for
+    tiny_block, of every block but 1e-20) pointing away from the queries so
+    their weights vanish, and a late key whose score jumps far above the
+    running max (late_jump) or an output carried by the 1e-20 block alone
+    (tiny_block). The integer-cache kernel keeps its value sums in units of a
+    per-step power of two and its probabilities against a reference max that
+    moves only on large changes; with one chunk every wave walks ~23 steps in
+    one pass and meets each change. Against the oracle's attention over the
+    read-back cache."""
+    from aero_amd.device import tune_set
+    rng = np.random.default_rng(91 + dt + 2 * one_chunk)
+    T, H, HK, D, S = 1, 8, 2, 128, 3000
+    q, k, v = rand_qkv(rng, T, H, HK, D, D, S)
+    mags = np.ones(S, np.float32)
+    mags[0:400], mags[400:800], mags[1600:2400], mags[2400:] = 1e-30, 1e24, 1e-20, 3.0
+    v = (v * mags[:, None, None]).astype(np.float32)
+    qdir = q[0].reshape(HK, H // HK, D).sum(1)
+    qdir = qdir / np.linalg.norm(qdir, axis=-1, keepdims=True)
+    away = list(range(400, 800)) if case == "late_jump" else \
+        list(range(400, 1600)) + list(range(2400, S))
+    k[away] = -qdir[None] * 4000.0
+    if case == "late_jump":
+        k[2990] = qdir * 30.0
+    else:
+        k[1600:2400] = k[1600:2400] * 0.2 + qdir[None] * 10.0
+    vb = D if dt == 1 else D // 2
+    kq, vq = DA.empty(S * HK * vb, np.uint8), DA.empty(S * HK * vb, np.uint8)
+    ks, vs = DA.empty(S * HK), DA.empty(S * HK)
+    ops.kv_write(dt, DA.from_numpy(k.astype(np.float32)), S, HK, D, kq, ks, 0, S)
+    ops.kv_write(dt, DA.from_numpy(v), S, HK, D, vq, vs, 0, S)
+    kqh, vqh = kq.numpy().reshape(S * HK, vb), vq.numpy().reshape(S * HK, vb)
+    ksh, vsh = ks.numpy(), vs.numpy()
+    kd = np.stack([oracle.kv_read_vec(dt, kqh[i], ksh[i], D) for i in range(S * HK)])
+    vd = np.stack([oracle.kv_read_vec(dt, vqh[i], vsh[i], D) for i in range(S * HK)])
+    kd, vd = kd.reshape(S, HK, D), vd.reshape(S, HK, D)
+    qpos = np.array([S - 1], np.int32)
+    want = oracle.attention_tiled(q, kd, vd, 0.09, qpos=qpos)
+    scale = np.abs(want).max()
+    if case == "tiny_block":
+        assert 1e-24 < scale < 1e-16   # carried by the 1e-20 block
+    else:
+        assert 0.5 < scale < 20.0      # carried by the late key (3.0 block)
+    print(f"scale ranges dt={dt} {case} one_chunk={one_chunk}", flush=True)
+    out = DA.empty((T, H, D))
+    if one_chunk:
+        tune_set("attn_wgs", 1)
+    try:
+        ops.attention(DA.from_numpy(q), kq, vq, out, T, H, HK, D, D, S, 0.09,
+                      qpos=DA.from_numpy(qpos), kv_dt=dt, k_scale=ks, v_scale=vs)
+        got = out.numpy()
+    finally:
+        if one_chunk:
+            tune_set("attn_wgs", None)
+    assert np.isfinite(got).all()
+    assert rel_to_scale(got, want) <= RTOL
+
+
 def test_softmax_rows(hip, oracle):
     """Rows of 1..100k values, large and tiny ranges; the flat-vector host ABI."""
     rng = np.random.default_rng(31)
