@@ -176,6 +176,8 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
                     }
                 }
             }
+            // (stored at once: measured faster here than after the norm's
+            // weight loads)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 __builtin_nontemporal_store(v4f{v[i].x, v[i].y, v[i].z, v[i].w},
@@ -185,13 +187,34 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = ld_stream(xr + 4 * i);
         }
+        // the residual, the norm's weights and the gate are loaded before x + d
+        // is stored: stores count in the same vector-memory counter as loads,
+        // so a load issued after a store waits for that store too (the
+        // residual pre-pass at 512 x 4096: 16.7 -> 10.5 us on MI355X)
+        float4 dv[4], w4[4], z4[4];
         if constexpr (RESID) {
             const float* dr = a.d + off;
 #pragma unroll
+            for (int i = 0; i < 4; ++i) dv[i] = ld_stream(dr + 4 * i);
+        }
+        const int wc = 256 * sb + 16 * cq;
+        const bool has_w = NORM && a.w != nullptr, has_z = NORM && a.z != nullptr;
+        if (has_w) {
+            const float* wr = a.w + (a.z != nullptr ? wc % a.w_len : wc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w4[i] = *reinterpret_cast<const float4*>(wr + 4 * i);
+        }
+        if (has_z) {
+            const float* zr = a.z + off;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) z4[i] = ld_stream(zr + 4 * i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (RESID) {
+#pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float4 dv = ld_stream(dr + 4 * i);
-                v[i].x = v[i].x + dv.x; v[i].y = v[i].y + dv.y;
-                v[i].z = v[i].z + dv.z; v[i].w = v[i].w + dv.w;
+                v[i].x = v[i].x + dv[i].x; v[i].y = v[i].y + dv[i].y;
+                v[i].z = v[i].z + dv[i].z; v[i].w = v[i].w + dv[i].w;
                 __builtin_nontemporal_store(v4f{v[i].x, v[i].y, v[i].z, v[i].w},
                                             reinterpret_cast<v4f*>(a.x_out + off + 4 * i));
             }
@@ -204,29 +227,25 @@ __global__ __launch_bounds__(256) void xsplit_kernel(XsplitArgs a) {
                 ss += v[i].z * v[i].z;
                 ss += v[i].w * v[i].w;
             }
-            if (a.w != nullptr) {
-                const int wc = 256 * sb + 16 * cq;
-                const float* wr = a.w + (a.z != nullptr ? wc % a.w_len : wc);
+            if (has_w) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float4 w4 = *reinterpret_cast<const float4*>(wr + 4 * i);
+                    float4 wv = w4[i];
                     if (a.unit_offset) {
-                        w4.x = 1.0f + w4.x; w4.y = 1.0f + w4.y;
-                        w4.z = 1.0f + w4.z; w4.w = 1.0f + w4.w;
+                        wv.x = 1.0f + wv.x; wv.y = 1.0f + wv.y;
+                        wv.z = 1.0f + wv.z; wv.w = 1.0f + wv.w;
                     }
-                    v[i].x = v[i].x * w4.x; v[i].y = v[i].y * w4.y;
-                    v[i].z = v[i].z * w4.z; v[i].w = v[i].w * w4.w;
+                    v[i].x = v[i].x * wv.x; v[i].y = v[i].y * wv.y;
+                    v[i].z = v[i].z * wv.z; v[i].w = v[i].w * wv.w;
                 }
             }
-            if (a.z != nullptr) {   // gated: silu of the gate
-                const float* zr = a.z + off;
+            if (has_z) {   // gated: silu of the gate
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float4 z4 = ld_stream(zr + 4 * i);
-                    v[i].x = v[i].x * silu_fast(z4.x);
-                    v[i].y = v[i].y * silu_fast(z4.y);
-                    v[i].z = v[i].z * silu_fast(z4.z);
-                    v[i].w = v[i].w * silu_fast(z4.w);
+                    v[i].x = v[i].x * silu_fast(z4[i].x);
+                    v[i].y = v[i].y * silu_fast(z4[i].y);
+                    v[i].z = v[i].z * silu_fast(z4[i].z);
+                    v[i].w = v[i].w * silu_fast(z4[i].w);
                 }
             }
         }

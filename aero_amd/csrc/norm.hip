@@ -79,11 +79,15 @@ void norm_vec_kernel(NormParams p) {
     // The gated norm loads its weights here, with the row: stores count in
     // the same vector-memory counter as loads, so a load issued after the
     // first store waits for every store before it (measured: 40.1 -> 36.4 us
-    // at 4096 x 4096). The plain norm keeps its weight load beside each store:
-    // moving it here, or after the reduction, made 2048 x 2560 and
-    // 4096 x 2048 ~20% slower on MI355X (7.7 -> 9.5 us, 11.0 -> 13.3 us) and
-    // gained 2-4% elsewhere; an explicit wait after each store did not
-    // recover it.
+    // at 4096 x 4096). So does the residual form, which stores x + d before
+    // its reduction, at up to 4 float4 a lane (512 x 4096: 6.3 -> 5.9 us,
+    // 16384 x 8192: 364.5 -> 351.8 us on MI355X; at 5 a lane the extra
+    // registers cost a wave a SIMD: 2048 x 2560 14.3 -> 15.1 us). The plain
+    // norm keeps its weight load beside each store: moving it here, or after
+    // the reduction, made 2048 x 2560 and 4096 x 2048 ~20% slower on MI355X
+    // (7.7 -> 9.5 us, 11.0 -> 13.3 us) and gained 2-4% elsewhere; an explicit
+    // wait after each store did not recover it.
+    constexpr bool W_EARLY = RESID && V <= 4;
     float4 xv[V];
     float4 zv[V];
     float4 wv[V];
@@ -99,6 +103,7 @@ void norm_vec_kernel(NormParams p) {
                 wv[i] = *reinterpret_cast<const float4*>(p.w + (col0 + 4 * c) % p.w_len);
             }
             if (RESID) zv[i] = ld_stream(zr + 4 * c);
+            if (W_EARLY && p.w != nullptr) wv[i] = *reinterpret_cast<const float4*>(p.w + 4 * c);
         } else {
             xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (GATED || RESID) zv[i] = xv[i];
@@ -183,7 +188,7 @@ void norm_vec_kernel(NormParams p) {
             float4 o = make_float4(xv[i].x * inv, xv[i].y * inv, xv[i].z * inv,
                                    xv[i].w * inv);
             if (p.w != nullptr) {
-                float4 w4 = reinterpret_cast<const float4*>(p.w)[c];
+                float4 w4 = W_EARLY ? wv[i] : reinterpret_cast<const float4*>(p.w)[c];
                 if (p.flags & AERO_NORM_UNIT_OFFSET) {
                     w4.x = 1.0f + w4.x; w4.y = 1.0f + w4.y;
                     w4.z = 1.0f + w4.z; w4.w = 1.0f + w4.w;
