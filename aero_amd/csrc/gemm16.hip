@@ -1575,6 +1575,11 @@ template <int TYPE>
 void* pick_split_gemm(int nt, int epi, int mt) {
     if constexpr (TYPE == AERO_DTYPE_Q4_K || TYPE == AERO_DTYPE_Q6_K)
         if (mt == 4) return pick_split_gemm_mt<TYPE, 4>(nt, epi);
+    // Q8_0: 64-token workgroups only with 16-row waves (32-row waves would
+    // spill)
+    if constexpr (TYPE == AERO_DTYPE_Q8_0)
+        if (mt == 4 && nt == 1 && epi == kEpiPlain)
+            return (void*)split_gemm_kernel<TYPE, 1, kEpiPlain, 4>;
     return pick_split_gemm_mt<TYPE, 2>(nt, epi);
 }
 
@@ -1679,19 +1684,21 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
     };
     int rows_wg = gu ? 64 : 64 * nt;
     int64_t tiles = count_tiles(rows_wg);
-    // 16 rows a wave and 64 tokens a workgroup for plain Q6_K launches that
-    // have two such workgroups a CU but not two of 32-row waves (4096-row
-    // matrices at 512 tokens): Q6_K's decode (two operand halves a weight) is
-    // then shared by twice the tokens. Measured on MI355X at 512 tokens,
-    // 4096 x 14336: Q6_K 325.8 -> 286.3 us; Q4_K 228.6 -> 255.2 (its x reads
-    // from LDS, twice as many a matrix step, cost more than the decode saved),
-    // so Q4_K keeps 32 rows (AERO_HIP_TUNE gemm16_nt1=1 / 0 forces / forbids).
+    // 16 rows a wave and 64 tokens a workgroup for plain Q6_K and Q8_0
+    // launches that have two such workgroups a CU but not two of 32-row waves
+    // (4096-row matrices at 512 tokens): the decode of a weight is then shared
+    // by twice the tokens. Measured on MI355X at 512 tokens, 4096 x 14336:
+    // Q6_K 325.8 -> 286.3 us, Q8_0 280.7 -> 270.2 (4096 x 4096 82.4 -> 77.5);
+    // Q4_K 228.6 -> 255.2 (its x reads from LDS, twice as many a matrix step,
+    // cost more than the decode saved), so Q4_K keeps 32 rows (AERO_HIP_TUNE
+    // gemm16_nt1=1 / 0 forces / forbids).
     const bool kq = j.dtype == AERO_DTYPE_Q4_K || j.dtype == AERO_DTYPE_Q6_K;
-    const int nt1 = tune("gemm16_nt1", j.dtype == AERO_DTYPE_Q6_K ? 1 : 0);
+    const bool nt1_ok = kq || j.dtype == AERO_DTYPE_Q8_0;
+    const int nt1 = tune("gemm16_nt1", j.dtype == AERO_DTYPE_Q4_K ? 0 : 1);
     // (not where it would lose a per-head epilogue the 32-row waves take)
     const bool keeps_rope = j.rope.mats == 0 || split_rope_ok(j, 64, 1, 4) ||
                             !split_rope_ok(j, 128, 1, 2);
-    if (!gu && nt == 2 && kq && tp % 64 == 0 && nt1 == 1 && keeps_rope &&
+    if (!gu && nt == 2 && nt1_ok && tp % 64 == 0 && nt1 == 1 && keeps_rope &&
         tiles * (tp / 64) < 2 * cu_count() && count_tiles(64) * (tp / 64) >= 2 * cu_count()) {
         nt = 1;
         rows_wg = 64;

@@ -376,27 +376,29 @@ def test_split_gemm_64_token_tiles(hip, oracle, t, n_rows, n_cols, n_tok):
     assert rel_to_scale(got[4][1], want) <= RTOL
 
 
-def test_split_gemm_q6k_16_row_waves(hip, oracle):
-    """Q6_K 4096 x 4096 at 512 tokens takes waves of 16 rows with 64-token
-    workgroups (512 of them): bit-identical to 32-row waves of 32 tokens
-    (AERO_HIP_TUNE gemm16_nt1=0, gemm16_mt=2) and, on tokens from every
-    64-token tile, within 1e-5 of the oracle."""
+@pytest.mark.parametrize("t", [W.Q6_K, W.Q8_0])
+def test_split_gemm_16_row_waves(hip, oracle, t):
+    """Q6_K and Q8_0 4096 x 4096 at 512 tokens take waves of 16 rows with
+    64-token workgroups (512 of them): bit-identical to 32-row waves of 32
+    tokens (AERO_HIP_TUNE gemm16_nt1=0, gemm16_mt=2) and, on tokens from
+    every 64-token tile, within 1e-5 of the oracle."""
     from aero_amd import device
-    rng = np.random.default_rng(29)
+    rng = np.random.default_rng(29 + t)
     n_rows, n_cols, n_tok = 4096, 4096, 512
-    w = W.make_table(W.Q6_K, n_rows * n_cols // 256, rng)
+    bv, _ = W.BLOCK[t]
+    w = W.make_table(t, n_rows * n_cols // bv, rng)
     X = rng.standard_normal((n_tok, n_cols)).astype(np.float32)
-    got = gpu_matmul(W.Q6_K, w, X, n_rows)
+    got = gpu_matmul(t, w, X, n_rows)
     try:
         device.tune_set("gemm16_nt1", 0)
         device.tune_set("gemm16_mt", 2)
-        ref = gpu_matmul(W.Q6_K, w, X, n_rows)
+        ref = gpu_matmul(t, w, X, n_rows)
     finally:
         device.tune_set("gemm16_nt1", None)
         device.tune_set("gemm16_mt", None)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
     idx = np.arange(7, n_tok, 64)
-    assert rel_to_scale(got[idx], oracle.matmul(W.Q6_K, w, X[idx], n_rows)) <= RTOL
+    assert rel_to_scale(got[idx], oracle.matmul(t, w, X[idx], n_rows)) <= RTOL
 
 
 def test_split_gemm_small_workspace_and_host_abi(hip, oracle):
