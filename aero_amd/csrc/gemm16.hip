@@ -1746,13 +1746,17 @@ bool split_run(const SplitJob& j, hipStream_t s, bool* rope_done = nullptr) {
     p.part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(j.ws) + part_off) : nullptr;
     // 64 tokens a workgroup (each decoded weight serving twice the matrix
     // steps) for Q4_K and Q6_K (the others would spill registers) where the
-    // launch still has two workgroups a CU:
-    // 512 tokens of gate/up or of a 14336-row matrix, not q/k/v, o or down at
-    // 4096 rows. AERO_HIP_TUNE gemm16_mt=2 keeps 32, gemm16_mt=4 takes 64
-    // wherever the shape allows.
+    // launch still has two workgroups a CU (512 tokens of gate/up or of a
+    // 14336-row matrix), or one on (nearly) every CU instead of two (o and
+    // down at 4096 rows and 512 tokens: Q4_K 4096 x 4096 68.0 -> 66.4 us,
+    // 4096 x 14336 232.5 -> 220.9 us on MI355X); not where one CU in two
+    // would hold a second (q/k/v, 6144 rows: 86.9 -> 90.1 us). AERO_HIP_TUNE
+    // gemm16_mt=2 keeps 32, gemm16_mt=4 takes 64 wherever the shape allows.
     const int mt_knob = tune("gemm16_mt", 0);
+    const int64_t w64 = tiles * (tp / 64), cus = cu_count();
     const int mt = nt == 1 || (kq && nt == 2 && ks == 1 && tp % 64 == 0 && mt_knob != 2 &&
-                               (mt_knob == 4 || tiles * (tp / 64) >= 2 * cu_count()))
+                               (mt_knob == 4 || w64 >= 2 * cus ||
+                                (w64 <= cus && w64 >= cus - cus / 8)))
                        ? 4 : 2;
     void* kp = j.dtype == AERO_DTYPE_Q5_K   ? pick_split_gemm<AERO_DTYPE_Q5_K>(nt, epi, mt)
                : j.dtype == AERO_DTYPE_Q8_0 ? pick_split_gemm<AERO_DTYPE_Q8_0>(nt, epi, mt)
