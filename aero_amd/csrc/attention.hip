@@ -1062,6 +1062,84 @@ __global__ __launch_bounds__(512) void attn_combine_kernel(AttnParams p) {
     }
 }
 
+// The same merge for value widths that are a multiple of 4 (16-byte aligned
+// partials and output): lane d4 of lane group grp (DV / 4 lanes a group,
+// G = 512 / (DV / 4) groups) loads elements 4 d4 .. 4 d4 + 3 of chunks grp,
+// grp + G, ... as one float4 each and the chunk's (m, l) as one float2, a
+// batch of chunks at once: an eighth of the load instructions of
+// attn_combine_kernel. Each group then scales its (l, acc) by its weight
+// against the groups' max (one LDS pass), and DV / 4 threads add the
+// groups' scaled sums.
+constexpr int kCombineBatch4 = 8;
+__global__ __launch_bounds__(512) void attn_combine4_kernel(AttnParams p) {
+    __shared__ float sm[512], sl[512];
+    __shared__ float4 sa[512];
+    const int tid = threadIdx.x;
+    const int64_t rows = p.n_q * p.n_head;
+    const int64_t row = blockIdx.x;
+    const int DV = (int)p.value_dim;
+    const int lpr = DV / 4;
+    const int G = 512 / lpr;
+    const int nc = p.n_chunks;
+    const float2* ml = reinterpret_cast<const float2*>(p.part + (int64_t)nc * rows * DV);
+    const int d4 = tid % lpr, grp = tid / lpr;
+    float M = -INFINITY, L = 0.0f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (grp < G) {
+        for (int c0 = grp; c0 < nc; c0 += kCombineBatch4 * G) {
+            float2 mc[kCombineBatch4];
+            float4 ac[kCombineBatch4];
+#pragma unroll
+            for (int i = 0; i < kCombineBatch4; ++i) {
+                const int c = min(c0 + i * G, nc - 1);
+                const int64_t pi = (int64_t)c * rows + row;
+                mc[i] = ml[pi];
+                ac[i] = *reinterpret_cast<const float4*>(p.part + pi * DV + 4 * d4);
+            }
+            float mb = M;
+#pragma unroll
+            for (int i = 0; i < kCombineBatch4; ++i)
+                if (c0 + i * G < nc) mb = fmaxf(mb, mc[i].x);
+            const float sc = (M == -INFINITY) ? 0.0f : expf(M - mb);
+            L *= sc;
+            A.x *= sc; A.y *= sc; A.z *= sc; A.w *= sc;
+#pragma unroll
+            for (int i = 0; i < kCombineBatch4; ++i) {
+                const bool ok = c0 + i * G < nc && mc[i].x != -INFINITY;
+                const float w = ok ? expf(mc[i].x - mb) : 0.0f;
+                L = __builtin_fmaf(mc[i].y, w, L);
+                A.x = __builtin_fmaf(ac[i].x, w, A.x);
+                A.y = __builtin_fmaf(ac[i].y, w, A.y);
+                A.z = __builtin_fmaf(ac[i].z, w, A.z);
+                A.w = __builtin_fmaf(ac[i].w, w, A.w);
+            }
+            M = mb;
+        }
+        if (d4 == 0) sm[grp] = M;
+    }
+    __syncthreads();
+    if (grp < G) {
+        float mt = -INFINITY;
+        for (int k = 0; k < G; ++k) mt = fmaxf(mt, sm[k]);
+        const float w = (M == -INFINITY) ? 0.0f : expf(M - mt);
+        sa[tid] = make_float4(A.x * w, A.y * w, A.z * w, A.w * w);
+        if (d4 == 0) sl[grp] = L * w;
+    }
+    __syncthreads();
+    if (tid < lpr) {
+        float lt = 0.0f;
+        float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < G; ++k) {
+            const float4 a = sa[k * lpr + tid];
+            lt += sl[k];
+            at.x += a.x; at.y += a.y; at.z += a.z; at.w += a.w;
+        }
+        const float r = 1.0f / fmaxf(lt, 1e-30f);
+        *reinterpret_cast<float4*>(p.out + row * DV + 4 * tid) =
+            make_float4(at.x * r, at.y * r, at.z * r, at.w * r);
+    }
+}
+
 using AttnKernel = void (*)(AttnParams);
 
 template <int DT, bool MERGE_OUT>
@@ -1316,7 +1394,11 @@ bool attention_dev(const float* q, int kv_dt, const void* k, const float* k_scal
                 dim3((unsigned)pl.n_chunks, (unsigned)n_head_kv, (unsigned)pl.grid_z),
                 dim3(64 * kAttnWaves), 0, s, p))
         return false;
-    if (!one && !launch("attn_combine_kernel", attn_combine_kernel,
+    // (value widths of a multiple of 4 up to 256 here: DV / 4 <= 512 lanes)
+    const bool c4 = value_dim % 4 == 0 && aligned16(workspace) && aligned16(out) &&
+                    tune("attn_combine4", 1) != 0;
+    if (!one && !launch(c4 ? "attn_combine4_kernel" : "attn_combine_kernel",
+                        c4 ? attn_combine4_kernel : attn_combine_kernel,
                         dim3((unsigned)(n_q * n_head)), dim3(512), 0, s, p))
         return false;
     return true;

@@ -267,6 +267,47 @@ def test_quantised_cache_scale_ranges(hip, oracle, dt, case, one_chunk):
     assert rel_to_scale(got, want) <= RTOL
 
 
+@pytest.mark.parametrize("combine4", [1, 0])
+@pytest.mark.parametrize("dt,H,HK,D,DV,S", [(0, 32, 8, 128, 128, 4096), (0, 16, 2, 256, 256, 3000),
+                                             (0, 14, 2, 64, 48, 2500), (1, 8, 2, 42, 42, 3000),
+                                             (1, 32, 8, 128, 128, 9000)])
+def test_chunk_merge_kernels(hip, oracle, combine4, dt, H, HK, D, DV, S):
+    """Decode over many key chunks: the chunk merge with float4 lanes (value
+    widths of a multiple of 4) and the scalar one (attn_combine4=0, and the
+    42-wide int8 value rows, which always take it) both equal the oracle."""
+    from aero_amd.device import tune_set
+    rng = np.random.default_rng(31 + D + S)
+    q, k, v = rand_qkv(rng, 1, H, HK, D, DV, S)
+    qpos = np.array([S - 1], np.int32)
+    print(f"chunk merge combine4={combine4} dt={dt} H={H}/{HK} D={D} DV={DV} S={S}", flush=True)
+    if dt == 0:
+        kd, vd, args = k, v, {}
+    else:
+        kq, vq = DA.empty(S * HK * D, np.uint8), DA.empty(S * HK * DV, np.uint8)
+        ks, vs = DA.empty(S * HK), DA.empty(S * HK)
+        ops.kv_write(dt, DA.from_numpy(k), S, HK, D, kq, ks, 0, S)
+        ops.kv_write(dt, DA.from_numpy(v), S, HK, DV, vq, vs, 0, S)
+        kqh, vqh = kq.numpy().reshape(S * HK, D), vq.numpy().reshape(S * HK, DV)
+        ksh, vsh = ks.numpy(), vs.numpy()
+        kd = np.stack([oracle.kv_read_vec(dt, kqh[i], ksh[i], D)
+                       for i in range(S * HK)]).reshape(S, HK, D)
+        vd = np.stack([oracle.kv_read_vec(dt, vqh[i], vsh[i], DV)
+                       for i in range(S * HK)]).reshape(S, HK, DV)
+        args = dict(kv_dt=dt, k_scale=ks, v_scale=vs)
+    out = DA.empty((1, H, DV))
+    dk = DA.from_numpy(k) if dt == 0 else kq
+    dv = DA.from_numpy(v) if dt == 0 else vq
+    tune_set("attn_combine4", combine4)
+    try:
+        ops.attention(DA.from_numpy(q), dk, dv, out, 1, H, HK, D, DV, S, 0.11,
+                      qpos=DA.from_numpy(qpos), **args)
+        got = out.numpy()
+    finally:
+        tune_set("attn_combine4", None)
+    want = oracle.attention_tiled(q, kd, vd, 0.11, qpos=qpos)
+    assert rel_to_scale(got, want) <= RTOL
+
+
 def test_softmax_rows(hip, oracle):
     """Rows of 1..100k values, large and tiny ranges; the flat-vector host ABI."""
     rng = np.random.default_rng(31)
