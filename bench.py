@@ -1290,11 +1290,17 @@ def layer_bench(a):
 
 
 ATTN_CASES = [
-    # (name, query tokens, cached keys, KV type 0 fp32 / 1 int8 / 2 int4) at
-    # Llama-3-8B heads: 32 query heads, 8 kv heads, head_dim 128
+    # (name, query tokens, cached keys, KV type 0 fp32 / 1 int8 / 2 int4[,
+    # (query heads, kv heads, head_dim)]); Llama-3-8B heads by default: 32 query
+    # heads, 8 kv heads, head_dim 128
     ("decode_s4096_f32", 1, 4096, 0), ("decode_s4096_int8", 1, 4096, 1),
     ("decode_s4096_int4", 1, 4096, 2), ("decode_s16384_f32", 1, 16384, 0),
     ("decode_s32768_int8", 1, 32768, 1), ("prefill_t512_causal_f32", 512, 512, 0),
+    # Gemma-3-4B heads (8 / 4, head_dim 256) and Qwen3-Next's attention heads
+    # (16 / 2, head_dim 256)
+    ("prefill_t2048_causal_f32_gemma3", 2048, 2048, 0, (8, 4, 256)),
+    ("prefill_t512_causal_f32_qwen3next", 512, 512, 0, (16, 2, 256)),
+    ("decode_s4096_f32_gemma3", 1, 4096, 0, (8, 4, 256)),
 ]
 
 
@@ -1326,12 +1332,12 @@ def attention_bench(a):
     from aero_amd import ops
     from aero_amd.device import DeviceArray as DA, Event, Plan, Stream
 
-    H, HK, D = 32, 8, 128
     rng = np.random.default_rng(0)
     names = a.shapes.split(",") if a.shapes else [c[0] for c in ATTN_CASES]
-    for name, T, S, dt in ATTN_CASES:
+    for name, T, S, dt, *heads in ATTN_CASES:
         if name not in names:
             continue
+        H, HK, D = heads[0] if heads else (32, 8, 128)
         vb = ops.kv_vec_bytes(dt, D)
         kv_bytes = 2 * S * HK * (vb + (4 if dt else 0))
         n_sets = min(64, max(2, -(-SUSTAINED_ROTATION // kv_bytes)))
