@@ -433,9 +433,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams p) {
     const int64_t c1 = min(c0 + p.chunk_len, p.n_kv);
     const int64_t tiles_c = (c1 - c0 + 15) / 16;
     const int64_t i_spec = wave;
-    // integer caches: the next tile is loaded while this one is used (two
-    // tiles of int8 / int4 fit in the registers one fp32 tile takes)
-    constexpr bool PF = DT != 0;
+    // the next tile is loaded while this one is used: integer caches (two
+    // tiles of int8 / int4 fit in the registers one fp32 tile takes) and
+    // single-chunk calls (prefill) at head dim 256, which runs one wave a SIMD
+    // either way (2048-token Gemma-3 prefill 288 -> 253 us on MI355X). Not at
+    // head dim 128, where an fp32 prefetch would cost the second wave a SIMD
+    // (512-token prefill 43.8 -> 54.4 us), nor for decode chunks, whose waves
+    // take one tile and would load it again (the next tile is clamped to the
+    // chunk's last). The next tile is copied into this one's registers: at
+    // head dim 256 two alternating register sets would not fit without spills.
+    constexpr bool PF = DT != 0 || (D == 256 && MERGE_OUT);
     Tile tl, nx;
     tl.load(p, c0 + 16 * min(i_spec, tiles_c - 1), c1, g, c, kh);
 
