@@ -74,6 +74,9 @@ def test_attention_golden(hip):
     (200, 8, 2, 128, 128, 300, 50),    # prefill after a cached prefix, with a window
     (3, 16, 4, 64, 64, 2500, 100),     # three tokens at once, head_dim 64, window
     (1, 8, 8, 128, 128, 5000, 0),      # MHA decode
+    (100, 8, 4, 256, 256, 300, 0),     # head_dim 256 prefill after a cached prefix (matrix cores)
+    (77, 16, 2, 256, 256, 77, 40),     # head_dim 256, 8 query heads a kv head, a window
+    (1024, 8, 4, 256, 256, 1024, 0),   # Gemma-3-4B heads, 1024-token causal prefill
 ])
 def test_attention_vs_oracle(hip, oracle, T, H, HK, D, DV, S, window):
     rng = np.random.default_rng(T * 7 + H + S + D + window)
