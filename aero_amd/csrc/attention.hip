@@ -6,9 +6,9 @@
 // Two attention kernels share one plan. Keys are split into chunks when the
 // query tiles alone do not fill the chip (decode: one query, many keys); each
 // chunk's (max m, sum l, accumulator) is merged by attn_combine_kernel.
-//  * attn_mfma_kernel (head_dim == value_dim in {64, 128}, and 256 over fp32
-//    caches): scores and the value sum on the fp32 matrix cores, a wave per
-//    16-key tile, the workgroup's four waves sharing one 16-query tile.
+//  * attn_mfma_kernel (head_dim == value_dim in {64, 128, 256}): scores and
+//    the value sum on the fp32 matrix cores, a wave per 16-key tile, the
+//    workgroup's four waves sharing one 16-query tile.
 //  * attn_kernel (any other width up to 256): 16-lane groups own a key, the
 //    dot product is reduced with lane shuffles, four query vectors a
 //    workgroup.
@@ -1178,7 +1178,7 @@ AttnKernel pick_mfma_dt(int D, bool merge_out) {
     switch (D) {
     case 64: return pick_mfma_d<DT, 64>(merge_out);
     case 128: return pick_mfma_d<DT, 128>(merge_out);
-    case 256: return DT == 0 ? pick_mfma_d<0, 256>(merge_out) : nullptr;
+    case 256: return pick_mfma_d<DT, 256>(merge_out);
     default: return nullptr;
     }
 }
@@ -1228,12 +1228,13 @@ bool attn_plan(int64_t n_q, int64_t n_head, int64_t n_head_kv, int64_t head_dim,
     if (pl.E == 0) return false;
     const int64_t rep = n_head / n_head_kv;
     const int64_t n_vec = n_q * rep;
-    // (head dim 256: fp32 caches, one wave a SIMD at 383 registers)
+    // (head dim 256: one wave a SIMD, 320-481 registers by cache type)
     pl.mfma = aligned && head_dim == value_dim &&
-              (head_dim == 64 || head_dim == 128 || (head_dim == 256 && kv_dt == 0)) &&
+              (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
               tune("attn_mfma", 1) != 0;
-    // integer caches: 32-key steps a wave on the fp16 matrix cores
-    pl.f16 = pl.mfma && kv_dt != 0 && tune("attn_f16", 1) != 0;
+    // integer caches at head dims 64 and 128: 32-key steps a wave on the fp16
+    // matrix cores (at 256 the fp32 matrix-core kernel reads their codes)
+    pl.f16 = pl.mfma && kv_dt != 0 && head_dim != 256 && tune("attn_f16", 1) != 0;
     int64_t step;  // keys a workgroup walks per step
     if (pl.mfma) {
         pl.grid_z = (n_vec + 15) / 16;

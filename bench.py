@@ -1301,6 +1301,7 @@ ATTN_CASES = [
     ("prefill_t2048_causal_f32_gemma3", 2048, 2048, 0, (8, 4, 256)),
     ("prefill_t512_causal_f32_qwen3next", 512, 512, 0, (16, 2, 256)),
     ("decode_s4096_f32_gemma3", 1, 4096, 0, (8, 4, 256)),
+    ("decode_s4096_int8_gemma3", 1, 4096, 1, (8, 4, 256)),
 ]
 
 

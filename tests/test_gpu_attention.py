@@ -147,7 +147,11 @@ def test_kv_write_bit_exact_and_ring(hip, oracle, dt):
                                            # several 32-key steps a wave (4 a chunk of 512),
                                            # a partial last chunk
                                            (1, 64, 32, 8, 128, 2048), (2, 64, 32, 8, 128, 2048),
-                                           (1, 1, 32, 8, 128, 32768), (2, 1, 32, 8, 64, 20000)])
+                                           (1, 1, 32, 8, 128, 32768), (2, 1, 32, 8, 64, 20000),
+                                           # head_dim 256 (the fp32 matrix-core kernel
+                                           # reading the codes): decode and prefill
+                                           (1, 1, 8, 4, 256, 3000), (2, 1, 8, 4, 256, 3000),
+                                           (1, 70, 16, 2, 256, 300), (2, 70, 16, 2, 256, 300)])
 def test_attention_over_quantised_cache(hip, oracle, dt, T, H, HK, D, S):
     """Attention reading an int8 / int4 cache (the fp16 matrix-core kernel at
     head dims 64 and 128) equals the oracle's attention over the cache read
