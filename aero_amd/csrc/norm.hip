@@ -86,8 +86,11 @@ void norm_vec_kernel(NormParams p) {
     // norm keeps its weight load beside each store: moving it here, or after
     // the reduction, made 2048 x 2560 and 4096 x 2048 ~20% slower on MI355X
     // (7.7 -> 9.5 us, 11.0 -> 13.3 us) and gained 2-4% elsewhere; an explicit
-    // wait after each store did not recover it.
-    constexpr bool W_EARLY = RESID && V <= 4;
+    // wait after each store did not recover it. Rows of 512 lanes (8192
+    // columns and more) take it: 16384 x 8192 182.5 -> 177.0 us a dispatch
+    // (at 256 lanes, 512 x 4096, per-dispatch and back-to-back times moved in
+    // opposite directions by 2-4%).
+    constexpr bool W_EARLY = V <= 4 && (RESID || (!GATED && TPR >= 512));
     float4 xv[V];
     float4 zv[V];
     float4 wv[V];
