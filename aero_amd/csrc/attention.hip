@@ -437,8 +437,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnParams p) {
     // tiles of int8 / int4 fit in the registers one fp32 tile takes) and
     // single-chunk calls (prefill) at head dim 256, which runs one wave a SIMD
     // either way (2048-token Gemma-3 prefill 288 -> 253 us on MI355X). Not at
-    // head dim 128, where an fp32 prefetch would cost the second wave a SIMD
-    // (512-token prefill 43.8 -> 54.4 us), nor for decode chunks, whose waves
+    // head dim 128, where an fp32 prefetch costs the second wave a SIMD (the
+    // 512-token prefill measured slower), nor for decode chunks, whose waves
     // take one tile and would load it again (the next tile is clamped to the
     // chunk's last). The next tile is copied into this one's registers: at
     // head dim 256 two alternating register sets would not fit without spills.
