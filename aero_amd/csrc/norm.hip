@@ -89,7 +89,7 @@ void norm_vec_kernel(NormParams p) {
     // wait after each store did not recover it. Rows of 512 lanes (8192
     // columns and more) take it: 16384 x 8192 182.5 -> 177.0 us a dispatch
     // (at 256 lanes, 512 x 4096, per-dispatch and back-to-back times moved in
-    // opposite directions by 2-4%).
+    // opposite directions).
     constexpr bool W_EARLY = V <= 4 && (RESID || (!GATED && TPR >= 512));
     float4 xv[V];
     float4 zv[V];
