@@ -89,11 +89,13 @@ def test_attention_vs_oracle(hip, oracle, T, H, HK, D, DV, S, window):
     assert rel_to_scale(got, want) <= RTOL
 
 
-def test_attention_positions_and_masks(hip, oracle):
+@pytest.mark.parametrize("D", [64, 256])
+def test_attention_positions_and_masks(hip, oracle, D):
     """Arbitrary query / key positions (a shuffled cache), a query before every
-    key (exact zeros), and the decode entry of the host ABI."""
-    rng = np.random.default_rng(5)
-    T, H, HK, D, S = 9, 8, 4, 64, 70
+    key (exact zeros), and the decode entry of the host ABI; head dims 64 and
+    256 (both on the fp32 matrix-core kernel)."""
+    rng = np.random.default_rng(5 + D)
+    T, H, HK, S = 9, 8, 4, 70
     q, k, v = rand_qkv(rng, T, H, HK, D, D, S)
     qpos = np.array([-3, 0, 5, 69, 12, 40, 41, 100, 2], np.int32)
     kpos = rng.permutation(S).astype(np.int32)
@@ -178,12 +180,14 @@ def test_attention_over_quantised_cache(hip, oracle, dt, T, H, HK, D, S):
 
 
 @pytest.mark.parametrize("dt,D,H,HK,S", [(1, 64, 8, 2, 700), (2, 64, 8, 2, 700),
-                                          (1, 128, 32, 8, 6000), (2, 128, 32, 8, 6000)])
+                                          (1, 128, 32, 8, 6000), (2, 128, 32, 8, 6000),
+                                          (1, 256, 8, 4, 700), (2, 256, 8, 4, 700)])
 def test_quantised_cache_positions_and_masks(hip, oracle, dt, D, H, HK, S):
-    """The integer-cache kernel (fp16 matrix steps) under arbitrary positions:
-    a shuffled cache (700 keys: one 32-key step a wave; 6000 keys: chunks of
-    384, three steps a wave), a query before every key (exact zeros),
-    positions past the cache, then the same with a window of 37."""
+    """The integer-cache kernels (fp16 matrix steps at head dims 64 and 128,
+    the fp32 matrix-core kernel reading the codes at 256) under arbitrary
+    positions: a shuffled cache (700 keys: one 32-key step a wave; 6000 keys:
+    chunks of 384, three steps a wave), a query before every key (exact
+    zeros), positions past the cache, then the same with a window of 37."""
     rng = np.random.default_rng(11 * dt + D)
     T = 9
     print(f"quantised-cache positions dt={dt} D={D} S={S}", flush=True)
