@@ -931,22 +931,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         e_new = min(max(e_new, -120), 128);   // 2^(6 - e) and 2^(e - 6) normal
         if (__any(tm > m + 8.0f) || e_new != e_acc) {
             const float mn = fmaxf(m, tm);
-            const float alpha = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-            ls = ls * alpha;
-            // rescale the rows of query 4g + r by that query's alpha (lane
-            // 4g + r), then all by 2^(e_acc - e_new)
+            // (before the first step's sums (e_acc -1000, wave-uniform) the
+            // sums and l are zero: nothing to rescale)
+            if (e_acc != -1000) {
+                const float alpha = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+                ls = ls * alpha;
+                // rescale the rows of query 4g + r by that query's alpha
+                // (lane 4g + r), then all by 2^(e_acc - e_new)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float ar = __shfl(alpha, 4 * g + r);
+                for (int r = 0; r < 4; ++r) {
+                    const float ar = __shfl(alpha, 4 * g + r);
 #pragma unroll
-                for (int t = 0; t < VS; ++t) acc[t][r] *= ar;
-            }
-            const int d = e_acc - e_new;
-            if (d != 0) {
+                    for (int t = 0; t < VS; ++t) acc[t][r] *= ar;
+                }
+                const int d = e_acc - e_new;
+                if (d != 0) {
 #pragma unroll
-                for (int t = 0; t < VS; ++t)
+                    for (int t = 0; t < VS; ++t)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[t][r] = ldexpf(acc[t][r], d);
+                        for (int r = 0; r < 4; ++r) acc[t][r] = ldexpf(acc[t][r], d);
+                }
             }
             m = mn;
             e_acc = e_new;
