@@ -1772,7 +1772,10 @@ def ssm_layer_bench(a):
         step = S.SsmStep(cfg, wts, max_tokens=T)
         step.x.view((T, cfg.hidden)).copy_from(rng.standard_normal((T, cfg.hidden),
                                                                    dtype=np.float32))
-        step.forward(T)            # conv history at kernel - 1 rows from here on
+        # eager steps until the conv history holds kernel - 1 rows (a plan
+        # records the history length it was made with)
+        while step.tail_len < cfg.conv_kernel - 1:
+            step.forward(T)
         stream = Stream()
         plan = Plan()
         with plan:
