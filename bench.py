@@ -798,6 +798,11 @@ def variants(a):
     from aero_amd import workloads as W
 
     names = a.shapes.split(",") if a.shapes else list(W.VARIANTS)
+    unknown = [n for n in names if n not in W.VARIANTS]
+    if unknown:
+        print(f"--variants: unknown variant(s) {unknown}; one of {list(W.VARIANTS)}",
+              file=sys.stderr)
+        return 2
     for name in names:
         shape, op = W.VARIANTS[name]
         path = Path(name, a.sets, shape=shape, only=op)
